@@ -1,0 +1,308 @@
+/*
+ * sejong_hip.h -- C ABI of the MI355X (gfx950) kernels for Sejong's byte /
+ * NativeValue Transformer training step.
+ *
+ * This library replaces the Triton launcher behind crates/sejong-gpu's
+ * `Engine` (crates/sejong-gpu/src/lib.rs:366-487): each `Engine` op method
+ * that today calls `self.launch("<triton op>", ...)` calls the function
+ * declared here instead.  The citation above each declaration names the
+ * reference method (and Triton kernel) it replaces.
+ *
+ * Conventions
+ *  - Every function returns an int status: SJ_OK (0) or one of SJ_ERR_*.
+ *    sj_last_error() returns the message of the last failure on the calling
+ *    thread (the reference's Error::Message / Error::Capacity text).
+ *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *    All launches are asynchronous on it; nothing here synchronises unless
+ *    its comment says so (the model calls that read results back).
+ *  - All pointers are caller-owned device pointers, row-major 2-D with an
+ *    explicit leading dimension (`ld*`, in elements).  No call allocates
+ *    device memory except sj_model_create.  Calls that need scratch take a
+ *    `workspace` pointer sized by the matching *_workspace_bytes query.
+ *  - dtypes use the reference's DType order (crates/sejong-core/src/lib.rs:
+ *    34-41) plus bf16: SJ_F32=0, SJ_F64=1, SJ_F16=2, SJ_I32=3, SJ_BF16=4.
+ *    The kernels compute in fp32 (FP64 for norms and loss sums, as the
+ *    reference does) and accept SJ_F32 or SJ_BF16 storage.
+ *  - Calls on one stream are not re-entrant (the reference Engine is a
+ *    single-thread, single-stream object: hip.rs:114-124).
+ */
+#ifndef SEJONG_HIP_H
+#define SEJONG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SJ_OK 0
+#define SJ_ERR_INVALID 1     /* shape / argument error (Error::Message)     */
+#define SJ_ERR_CAPACITY 2    /* memory or shared-memory budget (Error::Capacity) */
+#define SJ_ERR_HIP 3         /* HIP runtime error (hip.rs:47-57)             */
+#define SJ_ERR_UNSUPPORTED 4 /* dtype / layout combination not implemented  */
+#define SJ_ERR_NONFINITE 5   /* non-finite clipping gradient (train lib.rs:210) */
+
+#define SJ_F32 0
+#define SJ_F64 1
+#define SJ_F16 2
+#define SJ_I32 3
+#define SJ_BF16 4
+
+const char *sj_status_string(int status);
+const char *sj_last_error(void);
+/* Library / device identification: writes the gfx arch name (e.g. "gfx950")
+ * and CU count of the current device. */
+int sj_device_info(char *arch, size_t arch_len, int *compute_units);
+
+/* ---------------------------------------------------------- elementwise */
+
+/* Engine::full, crates/sejong-gpu/src/lib.rs:544-553 (kernel `fill`,
+ * python/sejong_kernels/ops/kernels.py:6-9). */
+int sj_fill(void *stream, void *y, int dtype, long n, float value);
+/* Engine::cast / copy_into, lib.rs:554-571 (kernel `copy`, kernels.py:11-14). */
+int sj_cast(void *stream, const void *x, int x_dtype, void *y, int y_dtype, long n);
+/* Engine::add / add_into, lib.rs:572-593 (kernel `add`, kernels.py:16-21):
+ * y = x + alpha*z computed in fp32, stored in y_dtype. */
+int sj_add(void *stream, const void *x, int x_dtype, const void *z, int z_dtype,
+           void *y, int y_dtype, long n, float alpha);
+
+/* Engine::embedding, lib.rs:650-666 (kernels.py:41-45): Y[i] = W[ids[i]]. */
+int sj_embedding_fwd(void *stream, const void *w, int w_dtype, const int32_t *ids,
+                     void *y, int y_dtype, long n, long d);
+/* Engine::embedding_backward, lib.rs:667-687 (kernels.py:47-52):
+ * dW[v] = sum_{i: ids[i]=v} dY[i], written (not accumulated) over all V rows.
+ * Deterministic: rows are summed in token order (the reference uses fp32
+ * atomics).  Needs sj_embedding_bwd_workspace_bytes of scratch. */
+size_t sj_embedding_bwd_workspace_bytes(long n, long vocab);
+int sj_embedding_bwd(void *stream, const float *dy, const int32_t *ids, float *dw,
+                     long n, long d, long vocab, void *workspace, size_t workspace_bytes);
+
+/* Engine::rope, lib.rs:734-758 (kernels.py:103-113): interleaved pairs,
+ * pos = (row / heads) mod t + offset (rows of width heads*head_dim, so row =
+ * token index), inverse != 0 negates the sine (backward, graph.rs:879-882). */
+int sj_rope(void *stream, const void *x, void *y, int dtype, long rows, long ld,
+            long t, long heads, long head_dim, long offset, float theta, int inverse);
+/* cos/sin table [t][head_dim/2] (interleaved cos, sin; angles formed in
+ * double) consumed by the fused RoPE epilogues of sj_qkv_fwd and
+ * sj_attention_bwd. */
+int sj_rope_table(void *stream, float *table, long t, long head_dim, float theta);
+
+/* Engine::swiglu / swiglu_backward, lib.rs:700-733 (kernels.py:90-101). */
+int sj_swiglu_fwd(void *stream, const void *g, const void *u, void *h, int dtype, long n);
+int sj_swiglu_bwd(void *stream, const void *g, const void *u, int gu_dtype,
+                  const float *dy, float *dg, float *du, long n);
+
+/* -------------------------------------------------------------- RMSNorm */
+
+/* Engine::norm, lib.rs:688-699 (kernel `rmsnorm`, kernels.py:54-61):
+ * y = x * (1/sqrt(mean x^2 + eps)) * w, stored in x's dtype. */
+int sj_rmsnorm_fwd(void *stream, const void *x, int x_dtype, const void *w, int w_dtype,
+                   void *y, long rows, long d, float eps);
+/* Engine::norm_backward, crates/sejong-gpu/src/norm_ops.rs:14-71 (kernels
+ * rmsnorm_backward_partial / _reduce, kernels.py:63-87):
+ * dx = s*(dy*w - x*mean(dy*w*x)*s^2) [+ dx_acc], dw = sum_rows dy*x*s with
+ * s = rsqrt(mean x^2 + eps).  dx_acc (nullable) fuses the tape's fp32
+ * gradient accumulation (graph.rs:503-513).  dw is written, reduced
+ * deterministically through `workspace` (sj_rmsnorm_bwd_workspace_bytes). */
+size_t sj_rmsnorm_bwd_workspace_bytes(long rows, long d);
+int sj_rmsnorm_bwd(void *stream, const void *x, int x_dtype, const void *w, int w_dtype,
+                   const float *dy, const float *dx_acc, float *dx, float *dw,
+                   long rows, long d, float eps, void *workspace, size_t workspace_bytes);
+
+/* ----------------------------------------------------------------- GEMM */
+
+/* Engine::matmul, lib.rs:594-649 (kernel `matmul`, kernels.py:23-39):
+ * C[M,N] (+)= op(A)[M,K] * op(B)[K,N].  ta: A stored [K,M]; tb: B stored
+ * [N,K].  A/B in SJ_F32 or SJ_BF16, C in SJ_F32 or SJ_BF16, fp32
+ * accumulation on bf16 MFMA.  fp32 operands are fed as hi+lo bf16 pairs
+ * (error ~2^-16 relative, the reference's fp32 "ieee" dot for dY operands).
+ * accumulate != 0 adds into C (fp32 C only).  workspace: split-K partials,
+ * sized by sj_gemm_workspace_bytes (0 is valid: no split-K). */
+size_t sj_gemm_workspace_bytes(long M, long N, long K);
+int sj_gemm(void *stream, int ta, int tb, long M, long N, long K,
+            const void *a, int a_dtype, long lda, const void *b, int b_dtype, long ldb,
+            void *c, int c_dtype, long ldc, int accumulate,
+            void *workspace, size_t workspace_bytes);
+
+/* Engine::project_qkv, crates/sejong-gpu/src/projection_ops.rs:6-43 (kernel
+ * projection_qkv, python/sejong_kernels/ops/projection.py:6-44): one launch
+ * computes Q = X Wq [M,N], K = X Wk and V = X Wv [M,KV], stored in x dtype.
+ * With rope_table non-null (sj_rope_table of rope_t positions) the RoPE of
+ * Engine::rope (rounded value in, fp32 math, stored again) is applied to the
+ * head_dim-wide heads of Q and K in the epilogue, replacing the two rope
+ * launches of Block::apply (crates/sejong-model/src/architecture.rs:215-216).
+ * N and KV must be multiples of 64. */
+int sj_qkv_fwd(void *stream, const void *x, long ldx, long M, long D,
+               const void *wq, long ldwq, const void *wk, long ldwk, const void *wv, long ldwv,
+               long N, long KV, void *q, long ldq, void *k, long ldk, void *v, long ldv,
+               int dtype, const float *rope_table, long rope_t, long head_dim);
+
+/* Engine::gate_up, projection_ops.rs:45-79 (kernel projection_gate_up,
+ * projection.py:47-73): G = X Wg, U = X Wu rounded to the storage dtype,
+ * H = g*sigmoid(g)*u from the rounded values. */
+int sj_gate_up_fwd(void *stream, const void *x, long ldx, long M, long D,
+                   const void *wg, long ldwg, const void *wu, long ldwu, long F,
+                   void *g, void *u, void *h, long ldo, int dtype);
+
+/* Residual projection: Y = R + round(X W), the `matmul` + `add` pair of
+ * Block::apply (architecture.rs:226-227 and :245) fused in one epilogue
+ * with the reference's two roundings (matmul output, then the sum). */
+int sj_linear_residual_fwd(void *stream, const void *x, long ldx, long M, long K,
+                           const void *w, long ldw, long N, const void *r, long ldr,
+                           void *y, long ldy, int dtype);
+
+/* dX of the gate/up pair fused with Engine::swiglu_backward (lib.rs:711-733):
+ * dH = dY W_down^T (fp32) is never stored; the epilogue writes
+ * dG = dH*u*s*(1+g(1-s)), dU = dH*g*s (s = sigmoid(g)) into dgu[:, 0:F] and
+ * dgu[:, F:2F]. */
+int sj_down_bwd_swiglu(void *stream, const float *dy, long lddy, long M, long D,
+                       const void *w_down, long ldw, long F, const void *g, const void *u,
+                       long ldgu_in, int gu_dtype, float *dgu, long lddgu);
+
+/* ------------------------------------------------------------ Attention */
+
+/* Engine::attention_grouped, crates/sejong-gpu/src/hierarchy_ops.rs:10-72
+ * (kernel hierarchy_attention, python/sejong_kernels/ops/hierarchy.py:7-39):
+ * causal GQA attention (kv head = h / (HQ/HK)), scale head_dim^-1/2,
+ * window 0 = full causal.  O stored in the q dtype, LSE fp32 [B*T*HQ].
+ * Training shape (tq = tk = t, offset 0). */
+int sj_attention_fwd(void *stream, const void *q, long ldq, const void *k, long ldk,
+                     const void *v, long ldv, void *o, long ldo, float *lse, int dtype,
+                     long batch, long t, long hq, long hk, long head_dim, long window);
+/* Engine::attention_grouped_backward, hierarchy_ops.rs:74-147 (kernels
+ * hierarchy_attention_dq, which writes Delta = sum dO*O, and
+ * hierarchy_attention_dkv, which reads it and loops the group's query
+ * heads: hierarchy.py:42-104).  dQ/dK/dV fp32.  With rope_table non-null
+ * (sj_rope_table) the inverse RoPE (rope backward, graph.rs:879-882) is
+ * applied to dQ and dK before they are stored.  delta: fp32 [B*T*HQ]
+ * scratch/output (Delta of each query row). */
+int sj_attention_bwd(void *stream, const void *q, long ldq, const void *k, long ldk,
+                     const void *v, long ldv, const void *o, long ldo, const float *lse,
+                     const float *dout, long lddo, float *dq, long lddq, float *dk, long lddk,
+                     float *dv, long lddv, float *delta, int dtype, long batch, long t,
+                     long hq, long hk, long head_dim, long window, const float *rope_table);
+
+/* -------------------------------------------------------- Cross entropy */
+
+/* Engine::cross_entropy + cross_entropy_backward, lib.rs:881-913 (kernels
+ * cross_entropy / cross_entropy_backward, kernels.py:176-191) in one pass:
+ * loss[r] = logsumexp(x_r) - x_r[t_r]; dx = (softmax - onehot) * dy_r with
+ * dy_r = dy ? dy[r] : dy_scalar (the mean-CE seed scale/count of
+ * Graph::backward, graph.rs:539-549).  dx may be NULL (forward only). */
+int sj_cross_entropy(void *stream, const float *x, long ldx, const int32_t *targets,
+                     float *loss, float *dx, long lddx, long rows, long vocab,
+                     const float *dy, float dy_scalar);
+/* Engine::loss_summary, lib.rs:524-543 (kernels.py:254-262): out[slot] =
+ * (sum_i loss[i] in FP64) * weight / n. */
+int sj_loss_summary(void *stream, const float *loss, long n, double *out, long slot, float weight);
+
+/* ------------------------------------------------------------ Optimizer */
+
+/* Engine::gradient_norm, lib.rs:494-523 (kernel gradient_norm, kernels.py:
+ * 265-287): out_sumsq[0] = sum g^2 in FP64, deterministic two-stage
+ * reduction, result left on the device (no host sync). */
+size_t sj_sum_squares_workspace_bytes(long n);
+int sj_sum_squares(void *stream, const float *g, long n, double *out_sumsq,
+                   void *workspace, size_t workspace_bytes);
+/* Engine::adamw, lib.rs:925-957 (kernel adamw, kernels.py:193-202), one
+ * tensor, host-computed scalars exactly as the reference passes them. */
+int sj_adamw(void *stream, float *w, const float *g, float *m, float *v, long n,
+             float lr, float beta1, float beta2, float eps, float decay,
+             float inv_b1, float inv_b2, float scale);
+
+/* Device-resident step scalars for the multi-tensor AdamW (no host sync:
+ * the clip factor of Adam::update, crates/sejong-train/src/lib.rs:199-238,
+ * is formed on the device from the FP64 squared norm). */
+typedef struct {
+  float lr, beta1, beta2, eps, weight_decay, inv_b1, inv_b2, clip_norm, loss_scale;
+  int32_t clip_enabled;
+} sj_adam_step;
+/* Adam::update over one flat parameter arena: elements [0, n_nodecay) are
+ * 1-D tensors (no decay), the rest decay (`p.value.shape.len() > 1`,
+ * train lib.rs:234).  scale = clip/loss_scale with clip = clip_norm/norm
+ * when clip_enabled and norm > clip_norm, norm = sqrt(*sumsq)/loss_scale.
+ * A non-finite norm sets *status_flag = 1 and leaves w, m, v untouched.
+ * w_mirror (nullable, bf16) receives the compute-precision copy of the
+ * updated w (the next step's Model::bind cast, model lib.rs:214-219). */
+int sj_adamw_multi(void *stream, float *w, const float *g, float *m, float *v,
+                   uint16_t *w_mirror, long n, long n_nodecay, const sj_adam_step *step,
+                   const double *sumsq, int32_t *status_flag);
+
+/* ---------------------------------------------------------------- Model
+ *
+ * Step driver for the dense byte Transformer (cfg1 / cfg2 family): the
+ * per-step op sequence of train_configured (crates/sejong-train/src/lib.rs:
+ * 387-453) -- Model::bind / logits (model lib.rs:206-340, Block::apply
+ * architecture.rs:200-247), cross_entropy, Graph::backward (graph.rs:
+ * 533-913), Adam::update -- issued on one stream over a preallocated
+ * activation-retention arena, optionally replayed as a hipGraph.
+ * Parameters are exchanged in the reference layout (architecture.rs:63-137,
+ * names from sj_model_param_info); the device keeps fused internal copies.
+ */
+typedef struct sj_model sj_model;
+typedef struct {
+  long vocab;      /* 257 (core lib.rs:305)                 */
+  long width;      /* d_model                                */
+  long layers;
+  long heads;      /* query heads                            */
+  long kv_heads;
+  long ffn_width;
+  long sequence;   /* T                                      */
+  long batch;      /* B                                      */
+  float norm_epsilon;
+  float rope_theta;
+  int precision;   /* SJ_F32 or SJ_BF16 compute/storage dtype */
+} sj_model_config;
+typedef struct {
+  float beta1, beta2, epsilon, weight_decay, clip_norm, loss_scale;
+  int clip_enabled;
+} sj_adam_config;
+
+int sj_model_create(const sj_model_config *cfg, const sj_adam_config *adam, void *stream,
+                    sj_model **out);
+int sj_model_destroy(sj_model *m);
+/* Number of parameter tensors / total elements in the reference layout. */
+long sj_model_param_tensors(const sj_model *m);
+long sj_model_param_count(const sj_model *m);
+/* name, shape and element offset (reference layout order) of tensor i. */
+int sj_model_param_info(const sj_model *m, long i, const char **name, long *rows, long *cols,
+                        long *offset);
+/* Host <-> device exchange in the reference layout (synchronous). */
+int sj_model_set_params(sj_model *m, const float *host);
+int sj_model_get_params(sj_model *m, float *host);
+int sj_model_get_grads(sj_model *m, float *host);
+int sj_model_get_adam_state(sj_model *m, float *m_host, float *v_host, long *step);
+int sj_model_set_adam_state(sj_model *m, const float *m_host, const float *v_host, long step);
+/* Batch input: host arrays (synchronous copy) or device arrays (async D2D
+ * on the model stream).  ids/targets int32 [batch*sequence]. */
+int sj_model_set_batch(sj_model *m, const int32_t *ids, const int32_t *targets, int on_device);
+/* Forward + backward only (gradients left in the model's gradient arena). */
+int sj_model_forward_backward(sj_model *m);
+/* One full training step: forward, backward, FP64 grad norm, clip, AdamW
+ * with learning rate lr (Adam::update increments the step first). */
+int sj_model_train_step(sj_model *m, float lr);
+/* Capture the step as a hipGraph on the next sj_model_train_step and replay
+ * it afterwards (on != 0), or run eagerly (on == 0). */
+int sj_model_use_graph(sj_model *m, int on);
+/* Reads the last step's mean loss and gradient norm (synchronises the
+ * model stream).  Returns SJ_ERR_NONFINITE if the last update saw a
+ * non-finite norm. */
+int sj_model_read_loss(sj_model *m, double *loss, double *grad_norm);
+/* Per-op timing (the reference's kernel-profile feature, crates/sejong-gpu/
+ * src/lib.rs:451-482 and counters.rs:33-56): with profiling on, steps run
+ * eagerly and every op is bracketed by a HIP event pair on the model stream.
+ * sj_model_profile_collect synchronises, aggregates the ops recorded since
+ * its last call by op name and returns the number of names (or -1);
+ * sj_model_profile_entry reads one aggregate. */
+int sj_model_profile(sj_model *m, int on);
+long sj_model_profile_collect(sj_model *m);
+int sj_model_profile_entry(sj_model *m, long i, const char **name, double *total_ms, long *calls);
+/* Device pointers of internal buffers for callers that time or inspect
+ * kernels directly (what: "logits", "loss_rows", "ids", "targets"). */
+int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SEJONG_HIP_H */

@@ -1,0 +1,148 @@
+"""ctypes binding of libsejong_hip.so (the C ABI in include/sejong_hip.h).
+
+The library is the only compute path: importing this module on a machine
+without the built library raises immediately; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsejong_hip.so")
+
+SJ_F32, SJ_F64, SJ_F16, SJ_I32, SJ_BF16 = 0, 1, 2, 3, 4
+
+_P = ctypes.c_void_p
+_L = ctypes.c_long
+_I = ctypes.c_int
+_F = ctypes.c_float
+_S = ctypes.c_size_t
+
+
+class SejongError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [("vocab", _L), ("width", _L), ("layers", _L), ("heads", _L), ("kv_heads", _L),
+                ("ffn_width", _L), ("sequence", _L), ("batch", _L), ("norm_epsilon", _F),
+                ("rope_theta", _F), ("precision", _I)]
+
+
+class AdamConfig(ctypes.Structure):
+    _fields_ = [("beta1", _F), ("beta2", _F), ("epsilon", _F), ("weight_decay", _F),
+                ("clip_norm", _F), ("loss_scale", _F), ("clip_enabled", _I)]
+
+
+class AdamStep(ctypes.Structure):
+    _fields_ = [("lr", _F), ("beta1", _F), ("beta2", _F), ("eps", _F), ("weight_decay", _F),
+                ("inv_b1", _F), ("inv_b2", _F), ("clip_norm", _F), ("loss_scale", _F),
+                ("clip_enabled", ctypes.c_int32)]
+
+
+# name -> (restype, argtypes); int-returning functions are status-checked
+SIGNATURES = {
+    "sj_status_string": (ctypes.c_char_p, [_I]),
+    "sj_last_error": (ctypes.c_char_p, []),
+    "sj_device_info": (_I, [ctypes.c_char_p, _S, ctypes.POINTER(_I)]),
+    "sj_fill": (_I, [_P, _P, _I, _L, _F]),
+    "sj_cast": (_I, [_P, _P, _I, _P, _I, _L]),
+    "sj_add": (_I, [_P, _P, _I, _P, _I, _P, _I, _L, _F]),
+    "sj_embedding_fwd": (_I, [_P, _P, _I, _P, _P, _I, _L, _L]),
+    "sj_embedding_bwd_workspace_bytes": (_S, [_L, _L]),
+    "sj_embedding_bwd": (_I, [_P, _P, _P, _P, _L, _L, _L, _P, _S]),
+    "sj_rope": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _F, _I]),
+    "sj_rope_table": (_I, [_P, _P, _L, _L, _F]),
+    "sj_swiglu_fwd": (_I, [_P, _P, _P, _P, _I, _L]),
+    "sj_swiglu_bwd": (_I, [_P, _P, _P, _I, _P, _P, _P, _L]),
+    "sj_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _I, _P, _L, _L, _F]),
+    "sj_rmsnorm_bwd_workspace_bytes": (_S, [_L, _L]),
+    "sj_rmsnorm_bwd": (_I, [_P, _P, _I, _P, _I, _P, _P, _P, _P, _L, _L, _F, _P, _S]),
+    "sj_gemm_workspace_bytes": (_S, [_L, _L, _L]),
+    "sj_gemm": (_I, [_P, _I, _I, _L, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _I, _P, _S]),
+    "sj_qkv_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _I,
+                        _P, _L, _L]),
+    "sj_gate_up_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _L, _P, _P, _P, _L, _I]),
+    "sj_linear_residual_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _L, _I]),
+    "sj_down_bwd_swiglu": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _P, _L, _I, _P, _L]),
+    "sj_attention_fwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _I, _L, _L, _L, _L, _L, _L]),
+    "sj_attention_bwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _L, _P,
+                              _I, _L, _L, _L, _L, _L, _L, _P]),
+    "sj_cross_entropy": (_I, [_P, _P, _L, _P, _P, _P, _L, _L, _L, _P, _F]),
+    "sj_loss_summary": (_I, [_P, _P, _L, _P, _L, _F]),
+    "sj_sum_squares_workspace_bytes": (_S, [_L]),
+    "sj_sum_squares": (_I, [_P, _P, _L, _P, _P, _S]),
+    "sj_adamw": (_I, [_P, _P, _P, _P, _P, _L, _F, _F, _F, _F, _F, _F, _F, _F]),
+    "sj_adamw_multi": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
+    "sj_model_destroy": (_I, [_P]),
+    "sj_model_param_tensors": (_L, [_P]),
+    "sj_model_param_count": (_L, [_P]),
+    "sj_model_param_info": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_L),
+                                 ctypes.POINTER(_L), ctypes.POINTER(_L)]),
+    "sj_model_set_params": (_I, [_P, _P]),
+    "sj_model_get_params": (_I, [_P, _P]),
+    "sj_model_get_grads": (_I, [_P, _P]),
+    "sj_model_get_adam_state": (_I, [_P, _P, _P, ctypes.POINTER(_L)]),
+    "sj_model_set_adam_state": (_I, [_P, _P, _P, _L]),
+    "sj_model_set_batch": (_I, [_P, _P, _P, _I]),
+    "sj_model_forward_backward": (_I, [_P]),
+    "sj_model_train_step": (_I, [_P, _F]),
+    "sj_model_use_graph": (_I, [_P, _I]),
+    "sj_model_read_loss": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "sj_model_profile": (_I, [_P, _I]),
+    "sj_model_profile_collect": (_L, [_P]),
+    "sj_model_profile_entry": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(_L)]),
+    "sj_model_buffer": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_L)]),
+}
+
+STATUS_FUNCS = {n for n, (r, _) in SIGNATURES.items() if r is _I and n not in ("sj_status_string",)}
+
+_lib = None
+
+
+def load(path: str | None = None):
+    """Load the library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -m sejong_amd.build` "
+                          "(there is no CPU fallback for the HIP path)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().sj_last_error().decode()
+
+
+def check(status: int):
+    if status != 0:
+        raise SejongError(status, last_error())
+
+
+class _Checked:
+    """lib.<name>(...) raising SejongError on a non-zero status."""
+
+    def __getattr__(self, name):
+        fn = getattr(load(), name)
+        if name not in STATUS_FUNCS:
+            return fn
+
+        def call(*args):
+            check(fn(*args))
+        return call
+
+
+api = _Checked()

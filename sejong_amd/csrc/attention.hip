@@ -1,0 +1,702 @@
+// GQA causal attention, forward and backward, for gfx950.
+//
+// Forward  (hierarchy.py:7-39):  one workgroup per (64-query block, query
+//   head, batch); 4 waves x 16 queries.  S^T = K Q^T on MFMA so that each
+//   lane holds 16 scores of ONE query -- the softmax statistics need only
+//   xor-16/32 shuffles and the P fragment for O += P V is already in the
+//   lane's registers (the key order inside the MFMA k-slots is permuted,
+//   and V^T is read from LDS in the same permuted order).
+// Backward (hierarchy.py:42-104), deterministic and atomic-free like the
+//   reference: k_attn_dq (per query block; writes Delta = sum dO*O) then
+//   k_attn_dkv (per key block of one KV head, looping the HQ/HK query heads
+//   of its group).  Optional inverse RoPE on dQ/dK in the epilogue.
+// P, dS and dO are fp32 values multiplied on bf16 MFMA as hi+lo pairs
+// (error ~2^-16 relative); a single bf16 rounding of them costs ~1.6e-3
+// normwise, more than the 1e-3 gradient tolerance.
+//
+// The MFMA kernels handle bf16 storage, head_dim 64 and full causal masks;
+// fp32 storage, other head widths and sliding windows use the wavefront-
+// per-row kernels at the end of this file (same formulas, fp32 FMA).
+#include <math.h>
+
+#include "common.h"
+
+using namespace sj;
+
+namespace {
+
+constexpr int DH = 64;
+constexpr int QB = 64;   // queries / keys per block
+constexpr int LS = DH + 8;  // LDS row stride (bf16)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+__device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8 bf16 from two 4-element LDS runs (permuted key order of the k-slots)
+__device__ __forceinline__ bf16x8 ld_perm(const bf16_t* row, int a, int b) {
+  u32x2 x = *(const u32x2*)(row + a);
+  u32x2 y = *(const u32x2*)(row + b);
+  return as_bf8(u32x4{x.x, x.y, y.x, y.y});
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float* v) {
+  return as_bf8(u32x4{pack2(f2bf(v[0]), f2bf(v[1])), pack2(f2bf(v[2]), f2bf(v[3])), pack2(f2bf(v[4]), f2bf(v[5])),
+                      pack2(f2bf(v[6]), f2bf(v[7]))});
+}
+// hi/lo split of 8 floats
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+  bf16_t h[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) split_bf(v[i], h[i], l[i]);
+  hi = as_bf8(u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])});
+  lo = as_bf8(u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])});
+}
+
+// Stage rows [row0, row0+64) x cols [col0, col0+64) of a bf16 matrix.
+// normal: dst[r][c]; transposed: dst[c][r].  Rows >= nrows read as zero.
+__device__ __forceinline__ void stage_bf16(bf16_t* dst, const bf16_t* src, long ld, long row0, long nrows, long col0) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    int ch = t + p * 256;
+    int r = ch >> 3, cc = ch & 7;
+    long row = row0 + r;
+    u32x4 v = u32x4{0, 0, 0, 0};
+    if (row < nrows) v = *(const u32x4*)(src + row * ld + col0 + cc * 8);
+    *(u32x4*)(dst + r * LS + cc * 8) = v;
+  }
+}
+__device__ __forceinline__ void stage_bf16_t(bf16_t* dst, const bf16_t* src, long ld, long row0, long nrows,
+                                             long col0) {
+  const int t = threadIdx.x;
+  const int rg = t >> 5, cp = t & 31;  // 8 row groups x 32 column pairs
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    long row = row0 + rg * 8 + i;
+    w[i] = row < nrows ? *(const uint32_t*)(src + row * ld + col0 + 2 * cp) : 0u;
+  }
+  bf16_t* d0 = dst + (2 * cp) * LS + rg * 8;
+  *(u32x4*)d0 = u32x4{(w[0] & 0xffffu) | (w[1] << 16), (w[2] & 0xffffu) | (w[3] << 16),
+                      (w[4] & 0xffffu) | (w[5] << 16), (w[6] & 0xffffu) | (w[7] << 16)};
+  *(u32x4*)(d0 + LS) = u32x4{(w[0] >> 16) | (w[1] & 0xffff0000u), (w[2] >> 16) | (w[3] & 0xffff0000u),
+                             (w[4] >> 16) | (w[5] & 0xffff0000u), (w[6] >> 16) | (w[7] & 0xffff0000u)};
+}
+// fp32 source -> hi/lo planes, normal and transposed
+__device__ __forceinline__ void stage_f32_split(bf16_t* hi, bf16_t* lo, bf16_t* hit, bf16_t* lot, const float* src,
+                                                long ld, long row0, long nrows, long col0) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    int ch = t + p * 256;
+    int r = ch >> 3, cc = ch & 7;
+    long row = row0 + r;
+    float v[8];
+    if (row < nrows) {
+      float4 a = *(const float4*)(src + row * ld + col0 + cc * 8);
+      float4 b = *(const float4*)(src + row * ld + col0 + cc * 8 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.f;
+    }
+    bf16x8 h, l;
+    split8(v, h, l);
+    *(bf16x8*)(hi + r * LS + cc * 8) = h;
+    *(bf16x8*)(lo + r * LS + cc * 8) = l;
+  }
+  const int rg = t >> 5, cp = t & 31;
+  bf16_t h0[8], l0[8], h1[8], l1[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    long row = row0 + rg * 8 + i;
+    float2 v = row < nrows ? *(const float2*)(src + row * ld + col0 + 2 * cp) : make_float2(0.f, 0.f);
+    split_bf(v.x, h0[i], l0[i]);
+    split_bf(v.y, h1[i], l1[i]);
+  }
+  bf16_t* d = hit + (2 * cp) * LS + rg * 8;
+  *(u32x4*)d = u32x4{pack2(h0[0], h0[1]), pack2(h0[2], h0[3]), pack2(h0[4], h0[5]), pack2(h0[6], h0[7])};
+  *(u32x4*)(d + LS) = u32x4{pack2(h1[0], h1[1]), pack2(h1[2], h1[3]), pack2(h1[4], h1[5]), pack2(h1[6], h1[7])};
+  d = lot + (2 * cp) * LS + rg * 8;
+  *(u32x4*)d = u32x4{pack2(l0[0], l0[1]), pack2(l0[2], l0[3]), pack2(l0[4], l0[5]), pack2(l0[6], l0[7])};
+  *(u32x4*)(d + LS) = u32x4{pack2(l1[0], l1[1]), pack2(l1[2], l1[3]), pack2(l1[4], l1[5]), pack2(l1[6], l1[7])};
+}
+
+struct AttnArgs {
+  const bf16_t *q, *k, *v, *o;
+  long ldq, ldk, ldv, ldo;
+  bf16_t* out;
+  float* lse;
+  const float* dout;
+  long lddo;
+  float *dq, *dk, *dv, *delta;
+  long lddq, lddk, lddv;
+  long T, HQ, HK;
+  const float* rope;  // inverse-rope table (cos, sin) [T][DH/2] or null
+};
+
+// ------------------------------------------------------------------ forward
+__global__ __launch_bounds__(256) void k_attn_fwd(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t sK[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sVt[DH * LS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const long qb = (long)gridDim.x - 1 - blockIdx.x;  // longest blocks first
+  const long h = blockIdx.y, b = blockIdx.z;
+  const long kvh = h / (a.HQ / a.HK);
+  const long T = a.T;
+  const long qrow0 = qb * QB + wave * 16;  // first query (position) of this wave
+  const long myq = qrow0 + j;              // query whose stats this lane holds
+  const float sc = 0.125f * LOG2E;         // DH^-1/2 * log2(e)
+
+  bf16x8 qf[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    u32x4 v = u32x4{0, 0, 0, 0};
+    if (myq < T) v = *(const u32x4*)(a.q + (b * T + myq) * a.ldq + h * DH + 32 * c + 8 * g);
+    qf[c] = as_bf8(v);
+  }
+  f32x4 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -INFINITY, lrow = 0.f;
+
+  const bf16_t* kbase = a.k + b * T * a.ldk + kvh * DH;
+  const bf16_t* vbase = a.v + b * T * a.ldv + kvh * DH;
+  for (long kb = 0; kb <= qb; kb++) {
+    __syncthreads();
+    stage_bf16(sK, kbase, a.ldk, kb * QB, T, 0);
+    stage_bf16_t(sVt, vbase, a.ldv, kb * QB, T, 0);
+    __syncthreads();
+    float s[4][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; c++) acc = mfma(as_bf8(*(const u32x4*)(sK + (sb * 16 + j) * LS + 32 * c + 8 * g)), qf[c], acc);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        long key = kb * QB + sb * 16 + 4 * g + r;
+        s[sb][r] = (key <= myq && key < T) ? acc[r] * sc : -INFINITY;
+      }
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) bm = fmaxf(bm, s[sb][r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mnew = fmaxf(mrow, bm);
+    const float alpha = exp2f(mrow - mnew);  // 0 on the first block
+    float ps = 0.f;
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s[sb][r] = exp2f(s[sb][r] - mnew);
+        ps += s[sb][r];
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    lrow = lrow * alpha + ps;
+    mrow = mnew;
+    // rescale O rows (queries 4g + r) by their alpha
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float al = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+      for (int d = 0; d < 4; d++) o[d][r] *= al;
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      float pv[8] = {s[2 * c][0], s[2 * c][1], s[2 * c][2], s[2 * c][3],
+                     s[2 * c + 1][0], s[2 * c + 1][1], s[2 * c + 1][2], s[2 * c + 1][3]};
+      bf16x8 ph, pl;
+      split8(pv, ph, pl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        bf16x8 vf = ld_perm(sVt + (16 * d + j) * LS, 32 * c + 4 * g, 32 * c + 16 + 4 * g);
+        o[d] = mfma(ph, vf, o[d]);
+        o[d] = mfma(pl, vf, o[d]);
+      }
+    }
+  }
+  // normalise and store
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    float l = __shfl(lrow, 4 * g + r, 64);
+    long qpos = qrow0 + 4 * g + r;
+    if (qpos < T) {
+      bf16_t* orow = a.out + (b * T + qpos) * a.ldo + h * DH;
+#pragma unroll
+      for (int d = 0; d < 4; d++) orow[16 * d + j] = f2bf(o[d][r] / l);
+    }
+  }
+  if (g == 0 && myq < T) a.lse[(b * T + myq) * a.HQ + h] = (mrow + log2f(lrow)) * LN2;
+}
+
+// ------------------------------------------------------------- backward dQ
+__global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t sK[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sKt[DH * LS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const long qb = (long)gridDim.x - 1 - blockIdx.x;
+  const long h = blockIdx.y, b = blockIdx.z;
+  const long kvh = h / (a.HQ / a.HK);
+  const long T = a.T;
+  const long qrow0 = qb * QB + wave * 16;
+  const long myq = qrow0 + j;
+  const float sc = 0.125f * LOG2E;
+
+  bf16x8 qf[2], dh[2], dl[2];
+  float delta_part = 0.f;
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    u32x4 qv = u32x4{0, 0, 0, 0};
+    float dov[8], ov[8];
+    if (myq < T) {
+      qv = *(const u32x4*)(a.q + (b * T + myq) * a.ldq + h * DH + 32 * c + 8 * g);
+      const float* dp = a.dout + (b * T + myq) * a.lddo + h * DH + 32 * c + 8 * g;
+      float4 x0 = *(const float4*)dp, x1 = *(const float4*)(dp + 4);
+      dov[0] = x0.x; dov[1] = x0.y; dov[2] = x0.z; dov[3] = x0.w; dov[4] = x1.x; dov[5] = x1.y; dov[6] = x1.z; dov[7] = x1.w;
+      u32x4 ow = *(const u32x4*)(a.o + (b * T + myq) * a.ldo + h * DH + 32 * c + 8 * g);
+      uint32_t w4[4] = {ow.x, ow.y, ow.z, ow.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        ov[2 * i] = bf2f((bf16_t)(w4[i] & 0xffff));
+        ov[2 * i + 1] = bf2f((bf16_t)(w4[i] >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) dov[i] = ov[i] = 0.f;
+    }
+    qf[c] = as_bf8(qv);
+    split8(dov, dh[c], dl[c]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) delta_part += dov[i] * ov[i];
+  }
+  delta_part += __shfl_xor(delta_part, 16, 64);
+  delta_part += __shfl_xor(delta_part, 32, 64);
+  const float delta = delta_part;
+  float lse2 = 0.f;
+  if (myq < T) {
+    lse2 = a.lse[(b * T + myq) * a.HQ + h] * LOG2E;
+    if (g == 0) a.delta[(b * T + myq) * a.HQ + h] = delta;
+  }
+
+  f32x4 dq[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const bf16_t* kbase = a.k + b * T * a.ldk + kvh * DH;
+  const bf16_t* vbase = a.v + b * T * a.ldv + kvh * DH;
+  for (long kb = 0; kb <= qb; kb++) {
+    __syncthreads();
+    stage_bf16(sK, kbase, a.ldk, kb * QB, T, 0);
+    stage_bf16(sV, vbase, a.ldv, kb * QB, T, 0);
+    stage_bf16_t(sKt, kbase, a.ldk, kb * QB, T, 0);
+    __syncthreads();
+    float ds[4][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        st = mfma(as_bf8(*(const u32x4*)(sK + (sb * 16 + j) * LS + 32 * c + 8 * g)), qf[c], st);
+        bf16x8 vf = as_bf8(*(const u32x4*)(sV + (sb * 16 + j) * LS + 32 * c + 8 * g));
+        dp = mfma(vf, dh[c], dp);
+        dp = mfma(vf, dl[c], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        long key = kb * QB + sb * 16 + 4 * g + r;
+        float p = (key <= myq && key < T) ? exp2f(st[r] * sc - lse2) : 0.f;
+        ds[sb][r] = p * (dp[r] - delta) * 0.125f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      float dv8[8] = {ds[2 * c][0], ds[2 * c][1], ds[2 * c][2], ds[2 * c][3],
+                      ds[2 * c + 1][0], ds[2 * c + 1][1], ds[2 * c + 1][2], ds[2 * c + 1][3]};
+      bf16x8 sh, sl;
+      split8(dv8, sh, sl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        bf16x8 kf = ld_perm(sKt + (16 * d + j) * LS, 32 * c + 4 * g, 32 * c + 16 + 4 * g);
+        dq[d] = mfma(sh, kf, dq[d]);
+        dq[d] = mfma(sl, kf, dq[d]);
+      }
+    }
+  }
+  // epilogue: optional inverse RoPE, pair (2i, 2i+1) in lanes (l, l^1)
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    long qpos = qrow0 + 4 * g + r;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      float x = dq[d][r];
+      float y = __shfl_xor(x, 1, 64);
+      long col = 16 * d + j;
+      if (a.rope && qpos < T) {
+        float2 cs = *(const float2*)(a.rope + 2 * (qpos * (DH / 2) + (col >> 1)));
+        x = (j & 1) ? (x * cs.x - y * cs.y) : (x * cs.x + y * cs.y);
+      }
+      if (qpos < T) a.dq[(b * T + qpos) * a.lddq + h * DH + col] = x;
+    }
+  }
+}
+
+// ------------------------------------------------------------ backward dKV
+__global__ __launch_bounds__(256) void k_attn_dkv(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16_t sQ[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sQt[DH * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sDh[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sDl[QB * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sDth[DH * LS];
+  __shared__ __attribute__((aligned(16))) bf16_t sDtl[DH * LS];
+  __shared__ float sL[QB], sD[QB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const long kb = blockIdx.x;
+  const long kvh = blockIdx.y, b = blockIdx.z;
+  const long T = a.T;
+  const long group = a.HQ / a.HK;
+  const long krow0 = kb * QB + wave * 16;
+  const long myk = krow0 + j;  // key whose fragments this lane supplies
+  const float sc = 0.125f * LOG2E;
+
+  bf16x8 kf[2], vf[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    u32x4 kv = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
+    if (myk < T) {
+      kv = *(const u32x4*)(a.k + (b * T + myk) * a.ldk + kvh * DH + 32 * c + 8 * g);
+      vv = *(const u32x4*)(a.v + (b * T + myk) * a.ldv + kvh * DH + 32 * c + 8 * g);
+    }
+    kf[c] = as_bf8(kv);
+    vf[c] = as_bf8(vv);
+  }
+  f32x4 dk[4], dv[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const long nqb = (T + QB - 1) / QB;
+  for (long gi = 0; gi < group; gi++) {
+    const long h = kvh * group + gi;
+    for (long qb = kb; qb < nqb; qb++) {
+      __syncthreads();
+      const bf16_t* qbase = a.q + b * T * a.ldq + h * DH;
+      stage_bf16(sQ, qbase, a.ldq, qb * QB, T, 0);
+      stage_bf16_t(sQt, qbase, a.ldq, qb * QB, T, 0);
+      stage_f32_split(sDh, sDl, sDth, sDtl, a.dout + b * T * a.lddo + h * DH, a.lddo, qb * QB, T, 0);
+      if (threadIdx.x < QB) {
+        long q = qb * QB + threadIdx.x;
+        sL[threadIdx.x] = q < T ? a.lse[(b * T + q) * a.HQ + h] * LOG2E : 0.f;
+        sD[threadIdx.x] = q < T ? a.delta[(b * T + q) * a.HQ + h] : 0.f;
+      }
+      __syncthreads();
+      float pp[4][4], ds[4][4];
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++) {
+        f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          st = mfma(as_bf8(*(const u32x4*)(sQ + (sb * 16 + j) * LS + 32 * c + 8 * g)), kf[c], st);
+          dp = mfma(as_bf8(*(const u32x4*)(sDh + (sb * 16 + j) * LS + 32 * c + 8 * g)), vf[c], dp);
+          dp = mfma(as_bf8(*(const u32x4*)(sDl + (sb * 16 + j) * LS + 32 * c + 8 * g)), vf[c], dp);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          int ql = sb * 16 + 4 * g + r;
+          long q = qb * QB + ql;
+          float p = (q >= myk && q < T && myk < T) ? exp2f(st[r] * sc - sL[ql]) : 0.f;
+          pp[sb][r] = p;
+          ds[sb][r] = p * (dp[r] - sD[ql]) * 0.125f;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        float p8[8] = {pp[2 * c][0], pp[2 * c][1], pp[2 * c][2], pp[2 * c][3],
+                       pp[2 * c + 1][0], pp[2 * c + 1][1], pp[2 * c + 1][2], pp[2 * c + 1][3]};
+        float s8[8] = {ds[2 * c][0], ds[2 * c][1], ds[2 * c][2], ds[2 * c][3],
+                       ds[2 * c + 1][0], ds[2 * c + 1][1], ds[2 * c + 1][2], ds[2 * c + 1][3]};
+        bf16x8 ph, pl, sh, sl;
+        split8(p8, ph, pl);
+        split8(s8, sh, sl);
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          const int ra = 32 * c + 4 * g, rb = 32 * c + 16 + 4 * g;
+          bf16x8 doh = ld_perm(sDth + (16 * d + j) * LS, ra, rb);
+          bf16x8 dol = ld_perm(sDtl + (16 * d + j) * LS, ra, rb);
+          bf16x8 qt = ld_perm(sQt + (16 * d + j) * LS, ra, rb);
+          dv[d] = mfma(ph, doh, dv[d]);
+          dv[d] = mfma(ph, dol, dv[d]);
+          dv[d] = mfma(pl, doh, dv[d]);
+          dk[d] = mfma(sh, qt, dk[d]);
+          dk[d] = mfma(sl, qt, dk[d]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    long kpos = krow0 + 4 * g + r;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      float x = dk[d][r];
+      float y = __shfl_xor(x, 1, 64);
+      long col = 16 * d + j;
+      if (a.rope && kpos < T) {
+        float2 cs = *(const float2*)(a.rope + 2 * (kpos * (DH / 2) + (col >> 1)));
+        x = (j & 1) ? (x * cs.x - y * cs.y) : (x * cs.x + y * cs.y);
+      }
+      if (kpos < T) {
+        a.dk[(b * T + kpos) * a.lddk + kvh * DH + col] = x;
+        a.dv[(b * T + kpos) * a.lddv + kvh * DH + col] = dv[d][r];
+      }
+    }
+  }
+}
+
+// ----------------------------------------------- wavefront-per-row kernels
+// Any storage dtype, head width <= 128, optional window (hierarchy.py:24,
+// 60, 87).  Lanes span the head dimension; keys are walked in order.
+struct RowArgs {
+  const void *q, *k, *v, *o;
+  long ldq, ldk, ldv, ldo;
+  void* out;
+  float* lse;
+  const float* dout;
+  long lddo;
+  float *dq, *dk, *dv, *delta;
+  long lddq, lddk, lddv;
+  int dt;
+  long B, T, HQ, HK, D, window;
+  const float* rope;
+};
+
+__global__ __launch_bounds__(256) void k_attn_fwd_rows(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long row = blockIdx.x * 4L + (threadIdx.x >> 6);  // (b*T + pos)*HQ + h
+  if (row >= a.B * a.T * a.HQ) return;
+  const long h = row % a.HQ, bt = row / a.HQ, pos = bt % a.T, b = bt / a.T;
+  const long kvh = h / (a.HQ / a.HK);
+  const float scale = 1.f / sqrtf((float)a.D);
+  float q[2], acc[2] = {0.f, 0.f};
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    q[i] = d < a.D ? load_as_f32(a.q, a.dt, bt * a.ldq + h * a.D + d) : 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  long first = a.window > 0 ? (pos + 1 - a.window > 0 ? pos + 1 - a.window : 0) : 0;
+  for (long p = first; p <= pos; p++) {
+    long kr = (b * a.T + p);
+    float s = 0.f;
+    for (int i = 0; i < 2; i++) {
+      long d = lane + 64 * i;
+      if (d < a.D) s += q[i] * load_as_f32(a.k, a.dt, kr * a.ldk + kvh * a.D + d);
+    }
+    s = wave_sum(s) * scale;
+    float mn = fmaxf(m, s);
+    float al = expf(m - mn), pr = expf(s - mn);
+    for (int i = 0; i < 2; i++) {
+      long d = lane + 64 * i;
+      float vv = d < a.D ? load_as_f32(a.v, a.dt, kr * a.ldv + kvh * a.D + d) : 0.f;
+      acc[i] = acc[i] * al + pr * vv;
+    }
+    l = l * al + pr;
+    m = mn;
+  }
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    if (d < a.D) store_from_f32(a.out, a.dt, bt * a.ldo + h * a.D + d, acc[i] / l);
+  }
+  if (lane == 0) a.lse[row] = m + logf(l);
+}
+
+__device__ __forceinline__ void inv_rope_store(float* dst, const float* rope, long pos, long D, int lane, float x0,
+                                               float x1) {
+  // lanes hold consecutive columns; pair partner is lane ^ 1 (D even)
+  float y0 = __shfl_xor(x0, 1, 64), y1 = __shfl_xor(x1, 1, 64);
+  float xs[2] = {x0, x1}, ys[2] = {y0, y1};
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    if (d < D) {
+      float x = xs[i];
+      if (rope) {
+        float2 cs = *(const float2*)(rope + 2 * (pos * (D / 2) + (d >> 1)));
+        x = (d & 1) ? (x * cs.x - ys[i] * cs.y) : (x * cs.x + ys[i] * cs.y);
+      }
+      dst[d] = x;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_attn_dq_rows(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long row = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (row >= a.B * a.T * a.HQ) return;
+  const long h = row % a.HQ, bt = row / a.HQ, pos = bt % a.T, b = bt / a.T;
+  const long kvh = h / (a.HQ / a.HK);
+  const float scale = 1.f / sqrtf((float)a.D);
+  float q[2], dy[2], acc[2] = {0.f, 0.f};
+  float dl = 0.f;
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    q[i] = d < a.D ? load_as_f32(a.q, a.dt, bt * a.ldq + h * a.D + d) : 0.f;
+    dy[i] = d < a.D ? a.dout[bt * a.lddo + h * a.D + d] : 0.f;
+    float ov = d < a.D ? load_as_f32(a.o, a.dt, bt * a.ldo + h * a.D + d) : 0.f;
+    dl += dy[i] * ov;
+  }
+  dl = wave_sum(dl);
+  if (lane == 0) a.delta[row] = dl;
+  const float lse = a.lse[row];
+  long first = a.window > 0 ? (pos + 1 - a.window > 0 ? pos + 1 - a.window : 0) : 0;
+  for (long p = first; p <= pos; p++) {
+    long kr = b * a.T + p;
+    float s = 0.f, dp = 0.f, kv[2];
+    for (int i = 0; i < 2; i++) {
+      long d = lane + 64 * i;
+      kv[i] = d < a.D ? load_as_f32(a.k, a.dt, kr * a.ldk + kvh * a.D + d) : 0.f;
+      float vv = d < a.D ? load_as_f32(a.v, a.dt, kr * a.ldv + kvh * a.D + d) : 0.f;
+      s += q[i] * kv[i];
+      dp += dy[i] * vv;
+    }
+    s = wave_sum(s);
+    dp = wave_sum(dp);
+    float pr = expf(s * scale - lse);
+    float ds = pr * (dp - dl) * scale;
+    for (int i = 0; i < 2; i++) acc[i] += ds * kv[i];
+  }
+  inv_rope_store(a.dq + bt * a.lddq + h * a.D, a.rope, pos, a.D, lane, acc[0], acc[1]);
+}
+
+__global__ __launch_bounds__(256) void k_attn_dkv_rows(RowArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long row = blockIdx.x * 4L + (threadIdx.x >> 6);  // (b*T + pos)*HK + kvh
+  if (row >= a.B * a.T * a.HK) return;
+  const long kvh = row % a.HK, bt = row / a.HK, pos = bt % a.T, b = bt / a.T;
+  const long group = a.HQ / a.HK;
+  const float scale = 1.f / sqrtf((float)a.D);
+  float k[2], v[2], ak[2] = {0.f, 0.f}, av[2] = {0.f, 0.f};
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    k[i] = d < a.D ? load_as_f32(a.k, a.dt, bt * a.ldk + kvh * a.D + d) : 0.f;
+    v[i] = d < a.D ? load_as_f32(a.v, a.dt, bt * a.ldv + kvh * a.D + d) : 0.f;
+  }
+  long end = a.window > 0 ? (pos + a.window < a.T ? pos + a.window : a.T) : a.T;
+  for (long gi = 0; gi < group; gi++) {
+    long h = kvh * group + gi;
+    for (long qp = pos; qp < end; qp++) {
+      long qr = (b * a.T + qp);
+      float s = 0.f, dp = 0.f, qv[2], dy[2];
+      for (int i = 0; i < 2; i++) {
+        long d = lane + 64 * i;
+        qv[i] = d < a.D ? load_as_f32(a.q, a.dt, qr * a.ldq + h * a.D + d) : 0.f;
+        dy[i] = d < a.D ? a.dout[qr * a.lddo + h * a.D + d] : 0.f;
+        s += qv[i] * k[i];
+        dp += dy[i] * v[i];
+      }
+      s = wave_sum(s);
+      dp = wave_sum(dp);
+      long qrow = qr * a.HQ + h;
+      float pr = expf(s * scale - a.lse[qrow]);
+      float ds = pr * (dp - a.delta[qrow]) * scale;
+      for (int i = 0; i < 2; i++) {
+        ak[i] += ds * qv[i];
+        av[i] += pr * dy[i];
+      }
+    }
+  }
+  inv_rope_store(a.dk + bt * a.lddk + kvh * a.D, a.rope, pos, a.D, lane, ak[0], ak[1]);
+  for (int i = 0; i < 2; i++) {
+    long d = lane + 64 * i;
+    if (d < a.D) a.dv[bt * a.lddv + kvh * a.D + d] = av[i];
+  }
+}
+
+bool use_mfma(int dtype, long head_dim, long window, long t, long ldq, long ldk, long ldv, long ldo,
+              const void* q, const void* k, const void* v, const void* o) {
+  if (dtype != SJ_BF16 || head_dim != DH) return false;
+  if (window > 0 && window < t) return false;
+  if ((ldq | ldk | ldv | ldo) % 8) return false;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int sj_attention_fwd(void* stream, const void* q, long ldq, const void* k, long ldk, const void* v, long ldv,
+                                void* o, long ldo, float* lse, int dtype, long batch, long t, long hq, long hk,
+                                long head_dim, long window) {
+  SJ_REQUIRE(dtype == SJ_F32 || dtype == SJ_BF16, "grouped attention dtype %d", dtype);
+  SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim > 0 && head_dim <= 128 &&
+                 head_dim % 2 == 0 && window >= 0,
+             "grouped attention sequence/head dimensions");
+  SJ_REQUIRE(ldq >= hq * head_dim && ldo >= hq * head_dim && ldk >= hk * head_dim && ldv >= hk * head_dim,
+             "grouped attention head width/dtype mismatch");
+  hipStream_t s = (hipStream_t)stream;
+  if (use_mfma(dtype, head_dim, window, t, ldq, ldk, ldv, ldo, q, k, v, o)) {
+    AttnArgs a = {};
+    a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+    a.out = (bf16_t*)o; a.lse = lse; a.T = t; a.HQ = hq; a.HK = hk;
+    hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch), dim3(256), 0, s,
+                       a);
+  } else {
+    RowArgs a = {};
+    a.q = q; a.k = k; a.v = v; a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+    a.out = o; a.lse = lse; a.dt = dtype; a.B = batch; a.T = t; a.HQ = hq; a.HK = hk; a.D = head_dim;
+    a.window = window;
+    long rows = batch * t * hq;
+    hipLaunchKernelGGL(k_attn_fwd_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+  }
+  SJ_LAUNCH_CHECK("hierarchy_attention");
+  return SJ_OK;
+}
+
+extern "C" int sj_attention_bwd(void* stream, const void* q, long ldq, const void* k, long ldk, const void* v,
+                                long ldv, const void* o, long ldo, const float* lse, const float* dout, long lddo,
+                                float* dq, long lddq, float* dk, long lddk, float* dv, long lddv, float* delta,
+                                int dtype, long batch, long t, long hq, long hk, long head_dim, long window,
+                                const float* rope_table) {
+  SJ_REQUIRE(dtype == SJ_F32 || dtype == SJ_BF16, "grouped attention backward dtype %d", dtype);
+  SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim > 0 && head_dim <= 128 &&
+                 head_dim % 2 == 0 && window >= 0,
+             "grouped attention backward dimensions");
+  SJ_REQUIRE(ldq >= hq * head_dim && ldo >= hq * head_dim && lddo >= hq * head_dim && lddq >= hq * head_dim &&
+                 ldk >= hk * head_dim && ldv >= hk * head_dim && lddk >= hk * head_dim && lddv >= hk * head_dim,
+             "grouped attention backward head/LSE dimensions");
+  hipStream_t s = (hipStream_t)stream;
+  bool fast = use_mfma(dtype, head_dim, window, t, ldq, ldk, ldv, ldo, q, k, v, o) && lddo % 4 == 0 &&
+              ((uintptr_t)dout % 16) == 0;
+  if (fast) {
+    AttnArgs a = {};
+    a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.o = (const bf16_t*)o;
+    a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+    a.lse = (float*)lse; a.dout = dout; a.lddo = lddo;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.delta = delta; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.T = t; a.HQ = hq; a.HK = hk; a.rope = rope_table;
+    unsigned nb = (unsigned)((t + QB - 1) / QB);
+    hipLaunchKernelGGL(k_attn_dq, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_dkv, dim3(nb, (unsigned)hk, (unsigned)batch), dim3(256), 0, s, a);
+  } else {
+    RowArgs a = {};
+    a.q = q; a.k = k; a.v = v; a.o = o; a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+    a.lse = (float*)lse; a.dout = dout; a.lddo = lddo;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.delta = delta; a.lddq = lddq; a.lddk = lddk; a.lddv = lddv;
+    a.dt = dtype; a.B = batch; a.T = t; a.HQ = hq; a.HK = hk; a.D = head_dim; a.window = window;
+    a.rope = rope_table;
+    long rows = batch * t * hq;
+    hipLaunchKernelGGL(k_attn_dq_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+    long krows = batch * t * hk;
+    hipLaunchKernelGGL(k_attn_dkv_rows, dim3((unsigned)((krows + 3) / 4)), dim3(256), 0, s, a);
+  }
+  SJ_LAUNCH_CHECK("hierarchy_attention_backward");
+  return SJ_OK;
+}

@@ -1,0 +1,51 @@
+// Status strings, last-error message and device identification.
+// Error text follows the reference's Error::Message / Error::Capacity /
+// "HIP {code}: {str}" forms (crates/sejong-core/src/lib.rs:8-24,
+// crates/sejong-gpu/src/hip.rs:47-57).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+static thread_local char g_last_error[1024] = "";
+
+namespace sjh {
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+int hip_check(hipError_t e, const char* what) {
+  return fail(SJ_ERR_HIP, "%s: HIP %d: %s", what, (int)e, hipGetErrorString(e));
+}
+}  // namespace sjh
+
+extern "C" const char* sj_status_string(int status) {
+  switch (status) {
+    case SJ_OK: return "ok";
+    case SJ_ERR_INVALID: return "invalid argument or shape";
+    case SJ_ERR_CAPACITY: return "capacity exceeded";
+    case SJ_ERR_HIP: return "HIP runtime error";
+    case SJ_ERR_UNSUPPORTED: return "unsupported dtype or layout";
+    case SJ_ERR_NONFINITE: return "nonfinite clipping gradient";
+    default: return "unknown status";
+  }
+}
+
+extern "C" const char* sj_last_error(void) { return g_last_error; }
+
+extern "C" int sj_device_info(char* arch, size_t arch_len, int* compute_units) {
+  int dev = 0;
+  SJ_HIP(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  SJ_HIP(hipGetDeviceProperties(&prop, dev));
+  if (arch && arch_len) {
+    strncpy(arch, prop.gcnArchName, arch_len - 1);
+    arch[arch_len - 1] = 0;
+  }
+  if (compute_units) *compute_units = prop.multiProcessorCount;
+  return SJ_OK;
+}

@@ -1,0 +1,108 @@
+// Shared device/host helpers for the gfx950 kernels of the Sejong training
+// step.  Wave64 throughout; bf16 values are carried as raw 16-bit words in
+// memory and converted with the hardware v_cvt_pk_bf16_f32 (round to nearest
+// even) through the __bf16 type.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/sejong_hip.h"
+
+namespace sj {
+
+typedef uint16_t bf16_t;  // raw bf16 bits in memory
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ bf16_t f2bf(float x) {
+  __bf16 b = (__bf16)x;
+  return __builtin_bit_cast(bf16_t, b);
+}
+
+// Round-to-nearest-even float -> bf16 value, returned as float.
+__device__ __forceinline__ float round_bf(float x) { return bf2f(f2bf(x)); }
+
+// Split an fp32 value into hi + lo bf16 words with x ~= hi + lo to ~2^-16
+// relative: hi = RNE(x), lo = RNE(x - hi).  Used so fp32 gradient operands
+// can feed bf16 MFMA without the ~1e-3 error of a single bf16 rounding.
+__device__ __forceinline__ void split_bf(float x, bf16_t& hi, bf16_t& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+
+__device__ __forceinline__ uint32_t pack2(bf16_t a, bf16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
+
+// Load a value of dtype `dt` (SJ_F32 or SJ_BF16) at index i as float.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, long i) {
+  return dt == SJ_BF16 ? bf2f(((const bf16_t*)p)[i]) : ((const float*)p)[i];
+}
+__device__ __forceinline__ void store_from_f32(void* p, int dt, long i, float v) {
+  if (dt == SJ_BF16)
+    ((bf16_t*)p)[i] = f2bf(v);
+  else
+    ((float*)p)[i] = v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    T u = __shfl_xor(v, o, WAVE);
+    v = u > v ? u : v;
+  }
+  return v;
+}
+
+// Block-wide sum for blockDim.x = NT (multiple of 64); `red` holds NT/64 T.
+template <typename T, int NT>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  T s = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; i++) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+}  // namespace sj
+
+// ------------------------------------------------------------- host side
+namespace sjh {
+// Record a failure message for sj_last_error() and return the status.
+int fail(int status, const char* fmt, ...);
+int hip_check(hipError_t e, const char* what);
+}  // namespace sjh
+
+#define SJ_REQUIRE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return sjh::fail(SJ_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define SJ_HIP(call)                                          \
+  do {                                                        \
+    hipError_t _e = (call);                                   \
+    if (_e != hipSuccess) return sjh::hip_check(_e, #call);   \
+  } while (0)
+
+#define SJ_LAUNCH_CHECK(what)                                 \
+  do {                                                        \
+    hipError_t _e = hipGetLastError();                        \
+    if (_e != hipSuccess) return sjh::hip_check(_e, what);    \
+  } while (0)

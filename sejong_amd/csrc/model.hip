@@ -1,0 +1,656 @@
+// Step driver for the dense byte Transformer: the per-step call sequence of
+// train_configured (crates/sejong-train/src/lib.rs:387-453) restated for one
+// stream and a preallocated arena:
+//   Model::bind cast        -> fused into AdamW (bf16 mirror of the masters)
+//   Model::logits           -> Block::apply per layer (architecture.rs:200-247)
+//                              + final norm + fp32 head (model lib.rs:336-340)
+//   cross_entropy + seed    -> one fused CE kernel (graph.rs:539-549)
+//   Graph::backward         -> the reverse rules of graph.rs:567-911 in the
+//                              fixed order of one block, gradients written
+//                              straight into a gradient arena
+//   Adam::update            -> FP64 norm on device + one multi-tensor AdamW
+//                              with the clip factor formed on device
+// so the whole step has no host synchronisation and can be captured once
+// as a hipGraph and replayed.
+//
+// Internal parameter layout (all fp32 masters, 256-byte aligned tensors):
+//   [no decay]  per layer attention_norm, ffn_norm; final_norm
+//   [decay]     embedding [V][d]; per layer W_qkv [d][d+2J] (query|key|value
+//               column blocks), attention_output [d][d], W_gu [d][2F]
+//               (gate|up), down [F][d]; output [d][Vp] (Vp = V rounded up
+//               to 8, padding columns stay zero)
+// Exchange with the host uses the reference layout (architecture.rs:63-137).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+extern "C" int sj_rope_table(void* stream, float* table, long t, long head_dim, float theta);
+
+namespace {
+
+long align64(long x) { return (x + 63) / 64 * 64; }
+
+struct RefTensor {
+  std::string name;
+  long rows, cols;  // reference shape ([n] 1-D tensors have rows = 1)
+  long ref_offset;  // offset in the reference-layout flat vector
+  long int_offset;  // offset of element (0,0) in the internal arena
+  long int_ld;      // internal row stride
+};
+
+struct Layer {
+  long an, fn, qkv, wo, gu, down;  // internal offsets
+};
+
+}  // namespace
+
+struct sj_model {
+  sj_model_config c;
+  sj_adam_config adam;
+  hipStream_t stream;
+  long V, Vp, d, L, HQ, HK, Dh, J, F, T, B, M, NQKV;
+  int dt;
+  size_t esz;  // bytes per activation element
+  // parameter arenas
+  long n_params;   // internal arena elements
+  long n_nodecay;  // [0, n_nodecay) not decayed
+  long ref_count;  // reference layout elements
+  std::vector<RefTensor> tensors;
+  std::vector<Layer> layers;
+  long emb, final_norm, out;
+  float *w = nullptr, *g = nullptr, *m = nullptr, *v = nullptr;
+  uint16_t* mirror = nullptr;  // bf16 compute copy (dt == bf16)
+  // activations
+  std::vector<void*> x;  // L+1 residual stream tensors
+  std::vector<void*> z, qkv, o, x1, z2, gg, uu, hh;
+  std::vector<float*> lse;
+  void* hn = nullptr;
+  float *logits = nullptr, *dlogits = nullptr, *loss_rows = nullptr;
+  // backward scratch
+  float *dres[2] = {nullptr, nullptr}, *dx1 = nullptr, *dO = nullptr, *dqkv = nullptr, *dgu = nullptr, *dz = nullptr,
+        *delta = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  float* rope = nullptr;
+  int32_t *ids = nullptr, *targets = nullptr;
+  double *loss = nullptr, *sumsq = nullptr;
+  int32_t* status = nullptr;
+  sj_adam_step* step_dev = nullptr;
+  // pinned ring of host step records: slot k is reused only after the copy
+  // issued from it RING steps earlier has completed (its event)
+  static constexpr int RING = 64;
+  sj_adam_step* step_host = nullptr;
+  hipEvent_t step_done[RING] = {};
+  long step = 0;
+  bool own_stream = false;
+  // per-op HIP-event profile (eager steps only)
+  bool profiling = false;
+  std::vector<hipEvent_t> prof_events;
+  std::vector<const char*> prof_names;  // one per recorded op
+  std::vector<std::string> agg_names;
+  std::vector<double> agg_ms;
+  std::vector<long> agg_calls;
+  // graph
+  bool use_graph = false;
+  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph = nullptr;
+  std::vector<void*> allocations;
+};
+
+namespace {
+
+int dalloc(sj_model* m, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) {
+    size_t fr = 0, tot = 0;
+    hipMemGetInfo(&fr, &tot);
+    return sjh::fail(SJ_ERR_CAPACITY, "model allocation: required %zu bytes, available %zu bytes", bytes, fr);
+  }
+  m->allocations.push_back(*p);
+  return SJ_OK;
+}
+
+#define TRY(x)              \
+  do {                      \
+    int _s = (x);           \
+    if (_s) return _s;      \
+  } while (0)
+
+// Run one op; when profiling, bracket it with a pair of events on the model
+// stream (the kernel-profile feature of the reference, lib.rs:451-482).
+int prof_mark(sj_model* m, const char* name) {
+  size_t k = m->prof_names.size();
+  if (2 * k + 2 > m->prof_events.size()) {
+    for (int i = 0; i < 64; i++) {
+      hipEvent_t e;
+      SJ_HIP(hipEventCreate(&e));
+      m->prof_events.push_back(e);
+    }
+  }
+  m->prof_names.push_back(name);
+  SJ_HIP(hipEventRecord(m->prof_events[2 * k], m->stream));
+  return SJ_OK;
+}
+int prof_end(sj_model* m) {
+  size_t k = m->prof_names.size() - 1;
+  SJ_HIP(hipEventRecord(m->prof_events[2 * k + 1], m->stream));
+  return SJ_OK;
+}
+#define OP(name, call)                         \
+  do {                                         \
+    if (m->profiling) TRY(prof_mark(m, name)); \
+    TRY(call);                                 \
+    if (m->profiling) TRY(prof_end(m));        \
+  } while (0)
+
+// Build reference-layout tensor list and the internal arena layout.
+void build_layout(sj_model* m) {
+  const long d = m->d, J = m->J, F = m->F, V = m->V;
+  long off = 0;
+  m->layers.resize(m->L);
+  for (long l = 0; l < m->L; l++) {
+    m->layers[l].an = off; off = align64(off + d);
+    m->layers[l].fn = off; off = align64(off + d);
+  }
+  m->final_norm = off; off = align64(off + d);
+  m->n_nodecay = off;
+  m->emb = off; off = align64(off + V * d);
+  for (long l = 0; l < m->L; l++) {
+    m->layers[l].qkv = off; off = align64(off + d * m->NQKV);
+    m->layers[l].wo = off; off = align64(off + d * d);
+    m->layers[l].gu = off; off = align64(off + d * 2 * F);
+    m->layers[l].down = off; off = align64(off + F * d);
+  }
+  m->out = off; off = align64(off + d * m->Vp);
+  m->n_params = off;
+
+  long ro = 0;
+  auto add = [&](const std::string& name, long rows, long cols, long ioff, long ild) {
+    m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild});
+    ro += rows * cols;
+  };
+  add("embedding", V, d, m->emb, d);
+  for (long l = 0; l < m->L; l++) {
+    std::string p = "layers." + std::to_string(l) + ".";
+    const Layer& y = m->layers[l];
+    add(p + "attention_norm", 1, d, y.an, d);
+    add(p + "ffn_norm", 1, d, y.fn, d);
+    add(p + "query", d, d, y.qkv, m->NQKV);
+    add(p + "key", d, J, y.qkv + d, m->NQKV);
+    add(p + "value", d, J, y.qkv + d + J, m->NQKV);
+    add(p + "attention_output", d, d, y.wo, d);
+    add(p + "gate", d, F, y.gu, 2 * F);
+    add(p + "up", d, F, y.gu + F, 2 * F);
+    add(p + "down", F, d, y.down, d);
+  }
+  add("final_norm", 1, d, m->final_norm, d);
+  add("output", d, V, m->out, m->Vp);
+  m->ref_count = ro;
+}
+
+// reference <-> internal host conversion
+void ref_to_internal(const sj_model* m, const float* ref, float* in) {
+  for (const auto& t : m->tensors)
+    for (long r = 0; r < t.rows; r++)
+      memcpy(in + t.int_offset + r * t.int_ld, ref + t.ref_offset + r * t.cols, sizeof(float) * t.cols);
+}
+void internal_to_ref(const sj_model* m, const float* in, float* ref) {
+  for (const auto& t : m->tensors)
+    for (long r = 0; r < t.rows; r++)
+      memcpy(ref + t.ref_offset + r * t.cols, in + t.int_offset + r * t.int_ld, sizeof(float) * t.cols);
+}
+
+// compute-precision view of a parameter (bf16 mirror or the fp32 master)
+const void* wc(const sj_model* m, long off) {
+  return m->dt == SJ_BF16 ? (const void*)(m->mirror + off) : (const void*)(m->w + off);
+}
+
+int refresh_mirror(sj_model* m) {
+  if (m->dt != SJ_BF16) return SJ_OK;
+  return sj_cast(m->stream, m->w, SJ_F32, m->mirror, SJ_BF16, m->n_params);
+}
+
+// ---------------------------------------------------------------- forward
+int forward(sj_model* m) {
+  hipStream_t s = m->stream;
+  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
+  const int dt = m->dt;
+  const float eps = m->c.norm_epsilon;
+  OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, M, d));
+  for (long l = 0; l < m->L; l++) {
+    const Layer& y = m->layers[l];
+    char* qkv = (char*)m->qkv[l];
+    OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[l], dt, wc(m, y.an), dt, m->z[l], M, d, eps));
+    const char* wq = (const char*)wc(m, y.qkv);
+    OP("qkv_rope", sj_qkv_fwd(s, m->z[l], d, M, d, wq, NQ, wq + d * m->esz, NQ, wq + (d + J) * m->esz, NQ, d, J, qkv, NQ,
+                   qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, dt, m->rope, m->T, m->Dh));
+    OP("attention_fwd", sj_attention_fwd(s, qkv, NQ, qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, m->o[l], d, m->lse[l], dt, m->B,
+                         m->T, m->HQ, m->HK, m->Dh, 0));
+    OP("attn_out_residual", sj_linear_residual_fwd(s, m->o[l], d, M, d, wc(m, y.wo), d, d, m->x[l], d, m->x1[l], d, dt));
+    OP("rmsnorm", sj_rmsnorm_fwd(s, m->x1[l], dt, wc(m, y.fn), dt, m->z2[l], M, d, eps));
+    const char* wg = (const char*)wc(m, y.gu);
+    OP("gate_up_swiglu", sj_gate_up_fwd(s, m->z2[l], d, M, d, wg, 2 * F, wg + F * m->esz, 2 * F, F, m->gg[l], m->uu[l], m->hh[l], F, dt));
+    OP("down_residual", sj_linear_residual_fwd(s, m->hh[l], F, M, F, wc(m, y.down), d, d, m->x1[l], d, m->x[l + 1], d, dt));
+  }
+  OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->hn, M, d, eps));
+  // fp32 head on the fp32 master (architecture.rs:160-167); hn's values are
+  // exact in fp32 (Graph::cast to F32), so it is read in its storage dtype.
+  OP("head_fwd", sj_gemm(s, 0, 0, M, m->V, d, m->hn, dt, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp, 0, m->ws,
+              m->ws_bytes));
+  const float seed = 1.0f / (float)M;  // scale / count, graph.rs:546
+  OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlogits, m->Vp, M, m->V, nullptr, seed));
+  OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, 0, 1.0f));
+  return SJ_OK;
+}
+
+// --------------------------------------------------------------- backward
+int backward(sj_model* m) {
+  hipStream_t s = m->stream;
+  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
+  const int dt = m->dt;
+  const float eps = m->c.norm_epsilon;
+  float* G = m->g;
+  // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
+  OP("head_dx", sj_gemm(s, 0, 1, M, d, m->V, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d, 0, m->ws,
+              m->ws_bytes));
+  OP("head_dw", sj_gemm(s, 1, 0, d, m->V, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0, m->ws,
+              m->ws_bytes));
+  int cur = 0;
+  OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->dz, nullptr, m->dres[cur], G + m->final_norm, M,
+                     d, eps, m->ws, m->ws_bytes));
+  for (long l = m->L - 1; l >= 0; l--) {
+    const Layer& y = m->layers[l];
+    float* dres = m->dres[cur];
+    // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
+    OP("down_dx_swiglu", sj_down_bwd_swiglu(s, dres, d, M, d, wc(m, y.down), d, F, m->gg[l], m->uu[l], F, dt, m->dgu, 2 * F));
+    OP("down_dw", sj_gemm(s, 1, 0, F, d, M, m->hh[l], dt, F, dres, SJ_F32, d, G + y.down, SJ_F32, d, 0, m->ws, m->ws_bytes));
+    OP("gate_up_dx", sj_gemm(s, 0, 1, M, d, 2 * F, m->dgu, SJ_F32, 2 * F, wc(m, y.gu), dt, 2 * F, m->dz, SJ_F32, d, 0, m->ws,
+                m->ws_bytes));
+    OP("gate_up_dw", sj_gemm(s, 1, 0, d, 2 * F, M, m->z2[l], dt, d, m->dgu, SJ_F32, 2 * F, G + y.gu, SJ_F32, 2 * F, 0, m->ws,
+                m->ws_bytes));
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x1[l], dt, wc(m, y.fn), dt, m->dz, dres, m->dx1, G + y.fn, M, d, eps, m->ws, m->ws_bytes));
+    // x1 = x + attention_output(o)
+    OP("attn_out_dx", sj_gemm(s, 0, 1, M, d, d, m->dx1, SJ_F32, d, wc(m, y.wo), dt, d, m->dO, SJ_F32, d, 0, m->ws, m->ws_bytes));
+    OP("attn_out_dw", sj_gemm(s, 1, 0, d, d, M, m->o[l], dt, d, m->dx1, SJ_F32, d, G + y.wo, SJ_F32, d, 0, m->ws, m->ws_bytes));
+    char* qkv = (char*)m->qkv[l];
+    OP("attention_bwd", sj_attention_bwd(s, qkv, NQ, qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, m->o[l], d, m->lse[l], m->dO, d,
+                         m->dqkv, NQ, m->dqkv + d, NQ, m->dqkv + d + J, NQ, m->delta, dt, m->B, m->T, m->HQ, m->HK,
+                         m->Dh, 0, m->rope));
+    OP("qkv_dx", sj_gemm(s, 0, 1, M, d, NQ, m->dqkv, SJ_F32, NQ, wc(m, y.qkv), dt, NQ, m->dz, SJ_F32, d, 0, m->ws, m->ws_bytes));
+    OP("qkv_dw", sj_gemm(s, 1, 0, d, NQ, M, m->z[l], dt, d, m->dqkv, SJ_F32, NQ, G + y.qkv, SJ_F32, NQ, 0, m->ws, m->ws_bytes));
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[l], dt, wc(m, y.an), dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d, eps, m->ws,
+                       m->ws_bytes));
+    cur ^= 1;
+  }
+  OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, M, d, m->V, nullptr, 0));
+  return SJ_OK;
+}
+
+int update(sj_model* m) {
+  OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
+  OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
+                     m->n_nodecay, m->step_dev, m->sumsq, m->status));
+  return SJ_OK;
+}
+
+int whole_step(sj_model* m) {
+  TRY(forward(m));
+  TRY(backward(m));
+  TRY(update(m));
+  return SJ_OK;
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config* adam, void* stream,
+                               sj_model** out) {
+  SJ_REQUIRE(cfg && adam && out, "model: null argument");
+  const sj_model_config& c = *cfg;
+  SJ_REQUIRE(c.vocab > 0 && c.width > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.ffn_width > 0 &&
+                 c.sequence > 0 && c.batch > 0,
+             "layers, ffn_width and context must be positive");
+  SJ_REQUIRE(c.width % c.heads == 0, "width must be divisible by heads");
+  SJ_REQUIRE((c.width / c.heads) % 2 == 0, "RoPE requires an even head width");
+  SJ_REQUIRE(c.heads % c.kv_heads == 0, "heads must be divisible by kv_heads");
+  SJ_REQUIRE(c.precision == SJ_F32 || c.precision == SJ_BF16, "precision must be f32 or bf16");
+  sj_model* m = new sj_model();
+  m->c = c;
+  m->adam = *adam;
+  m->stream = (hipStream_t)stream;
+  if (!m->stream) {
+    // graph capture needs a stream other than the null stream
+    if (hipStreamCreate(&m->stream) != hipSuccess) {
+      delete m;
+      return sjh::fail(SJ_ERR_HIP, "model: stream creation");
+    }
+    m->own_stream = true;
+  }
+  m->V = c.vocab;
+  m->Vp = (c.vocab + 7) / 8 * 8;
+  m->d = c.width;
+  m->L = c.layers;
+  m->HQ = c.heads;
+  m->HK = c.kv_heads;
+  m->Dh = c.width / c.heads;
+  m->J = m->Dh * c.kv_heads;
+  m->F = c.ffn_width;
+  m->T = c.sequence;
+  m->B = c.batch;
+  m->M = c.sequence * c.batch;
+  m->NQKV = m->d + 2 * m->J;
+  m->dt = c.precision;
+  m->esz = m->dt == SJ_BF16 ? 2 : 4;
+  build_layout(m);
+  int st = SJ_OK;
+  auto fail_cleanup = [&](int s) {
+    sj_model_destroy(m);
+    return s;
+  };
+#define ALLOC(ptr, bytes)                                    \
+  do {                                                       \
+    void* _p = nullptr;                                      \
+    st = dalloc(m, &_p, (size_t)(bytes));                    \
+    if (st) return fail_cleanup(st);                         \
+    ptr = (decltype(ptr))_p;                                 \
+  } while (0)
+  const size_t P = (size_t)m->n_params;
+  ALLOC(m->w, P * 4);
+  ALLOC(m->g, P * 4);
+  ALLOC(m->m, P * 4);
+  ALLOC(m->v, P * 4);
+  if (m->dt == SJ_BF16) ALLOC(m->mirror, P * 2);
+  const size_t M = (size_t)m->M, d = (size_t)m->d, F = (size_t)m->F, es = m->esz;
+  m->x.resize(m->L + 1);
+  for (long l = 0; l <= m->L; l++) ALLOC(m->x[l], M * d * es);
+  m->z.resize(m->L); m->qkv.resize(m->L); m->o.resize(m->L); m->x1.resize(m->L); m->z2.resize(m->L);
+  m->gg.resize(m->L); m->uu.resize(m->L); m->hh.resize(m->L); m->lse.resize(m->L);
+  for (long l = 0; l < m->L; l++) {
+    ALLOC(m->z[l], M * d * es);
+    ALLOC(m->qkv[l], M * (size_t)m->NQKV * es);
+    ALLOC(m->o[l], M * d * es);
+    ALLOC(m->lse[l], M * (size_t)m->HQ * 4);
+    ALLOC(m->x1[l], M * d * es);
+    ALLOC(m->z2[l], M * d * es);
+    ALLOC(m->gg[l], M * F * es);
+    ALLOC(m->uu[l], M * F * es);
+    ALLOC(m->hh[l], M * F * es);
+  }
+  ALLOC(m->hn, M * d * es);
+  ALLOC(m->logits, M * (size_t)m->Vp * 4);
+  ALLOC(m->dlogits, M * (size_t)m->Vp * 4);
+  ALLOC(m->loss_rows, M * 4);
+  ALLOC(m->dres[0], M * d * 4);
+  ALLOC(m->dres[1], M * d * 4);
+  ALLOC(m->dx1, M * d * 4);
+  ALLOC(m->dO, M * d * 4);
+  ALLOC(m->dz, M * d * 4);
+  ALLOC(m->dqkv, M * (size_t)m->NQKV * 4);
+  ALLOC(m->dgu, M * 2 * F * 4);
+  ALLOC(m->delta, M * (size_t)m->HQ * 4);
+  ALLOC(m->rope, (size_t)m->T * (size_t)m->Dh * 4);
+  ALLOC(m->ids, M * 4);
+  ALLOC(m->targets, M * 4);
+  ALLOC(m->loss, 64);
+  ALLOC(m->sumsq, 64);
+  ALLOC(m->status, 64);
+  ALLOC(m->step_dev, sizeof(sj_adam_step));
+  // workspace: max over the step's calls
+  size_t ws = 0;
+  auto upd = [&](size_t b) { ws = b > ws ? b : ws; };
+  const long Mi = m->M;
+  upd(sj_rmsnorm_bwd_workspace_bytes(Mi, m->d));
+  upd(sj_sum_squares_workspace_bytes(m->n_params));
+  upd(sj_gemm_workspace_bytes(Mi, m->d, m->V));
+  upd(sj_gemm_workspace_bytes(m->d, m->V, Mi));
+  upd(sj_gemm_workspace_bytes(m->F, m->d, Mi));
+  upd(sj_gemm_workspace_bytes(m->d, 2 * m->F, Mi));
+  upd(sj_gemm_workspace_bytes(m->d, m->d, Mi));
+  upd(sj_gemm_workspace_bytes(m->d, m->NQKV, Mi));
+  upd(sj_gemm_workspace_bytes(Mi, m->d, 2 * m->F));
+  upd(sj_gemm_workspace_bytes(Mi, m->d, m->NQKV));
+  m->ws_bytes = ws;
+  ALLOC(m->ws, ws);
+#undef ALLOC
+  if (hipHostMalloc((void**)&m->step_host, sizeof(sj_adam_step) * sj_model::RING, 0) != hipSuccess)
+    return fail_cleanup(sjh::fail(SJ_ERR_CAPACITY, "model: pinned step buffer"));
+  for (int i = 0; i < sj_model::RING; i++)
+    if (hipEventCreateWithFlags(&m->step_done[i], hipEventDisableTiming) != hipSuccess)
+      return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: event creation"));
+  // zero state, rope table
+  hipStream_t s = m->stream;
+  hipError_t e = hipSuccess;
+  for (void* p : {(void*)m->w, (void*)m->g, (void*)m->m, (void*)m->v})
+    if (e == hipSuccess) e = hipMemsetAsync(p, 0, P * 4, s);
+  if (e == hipSuccess && m->mirror) e = hipMemsetAsync(m->mirror, 0, P * 2, s);
+  if (e == hipSuccess) e = hipMemsetAsync(m->status, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, 64, s);
+  if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: clear arenas"));
+  st = sj_rope_table(s, m->rope, m->T, m->Dh, c.rope_theta);
+  if (st) return fail_cleanup(st);
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: init sync"));
+  *out = m;
+  return SJ_OK;
+}
+
+extern "C" int sj_model_destroy(sj_model* m) {
+  if (!m) return SJ_OK;
+  if (m->stream) hipStreamSynchronize(m->stream);
+  if (m->exec) hipGraphExecDestroy(m->exec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  for (void* p : m->allocations) hipFree(p);
+  for (hipEvent_t e : m->prof_events) hipEventDestroy(e);
+  if (m->step_host) hipHostFree(m->step_host);
+  for (int i = 0; i < sj_model::RING; i++)
+    if (m->step_done[i]) hipEventDestroy(m->step_done[i]);
+  if (m->own_stream) hipStreamDestroy(m->stream);
+  delete m;
+  return SJ_OK;
+}
+
+extern "C" long sj_model_param_tensors(const sj_model* m) { return m ? (long)m->tensors.size() : 0; }
+extern "C" long sj_model_param_count(const sj_model* m) { return m ? m->ref_count : 0; }
+
+extern "C" int sj_model_param_info(const sj_model* m, long i, const char** name, long* rows, long* cols,
+                                   long* offset) {
+  SJ_REQUIRE(m && i >= 0 && i < (long)m->tensors.size(), "param_info: index %ld", i);
+  const RefTensor& t = m->tensors[i];
+  if (name) *name = t.name.c_str();
+  if (rows) *rows = t.rows;
+  if (cols) *cols = t.cols;
+  if (offset) *offset = t.ref_offset;
+  return SJ_OK;
+}
+
+static int copy_arena_in(sj_model* m, const float* host, float* dev) {
+  std::vector<float> in((size_t)m->n_params, 0.f);
+  ref_to_internal(m, host, in.data());
+  SJ_HIP(hipMemcpyAsync(dev, in.data(), sizeof(float) * in.size(), hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  return SJ_OK;
+}
+static int copy_arena_out(sj_model* m, const float* dev, float* host) {
+  std::vector<float> in((size_t)m->n_params);
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  SJ_HIP(hipMemcpy(in.data(), dev, sizeof(float) * in.size(), hipMemcpyDeviceToHost));
+  internal_to_ref(m, in.data(), host);
+  return SJ_OK;
+}
+
+extern "C" int sj_model_set_params(sj_model* m, const float* host) {
+  SJ_REQUIRE(m && host, "set_params: null");
+  TRY(copy_arena_in(m, host, m->w));
+  TRY(refresh_mirror(m));
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  return SJ_OK;
+}
+extern "C" int sj_model_get_params(sj_model* m, float* host) {
+  SJ_REQUIRE(m && host, "get_params: null");
+  return copy_arena_out(m, m->w, host);
+}
+extern "C" int sj_model_get_grads(sj_model* m, float* host) {
+  SJ_REQUIRE(m && host, "get_grads: null");
+  return copy_arena_out(m, m->g, host);
+}
+extern "C" int sj_model_get_adam_state(sj_model* m, float* mh, float* vh, long* step) {
+  SJ_REQUIRE(m, "get_adam_state: null");
+  if (mh) TRY(copy_arena_out(m, m->m, mh));
+  if (vh) TRY(copy_arena_out(m, m->v, vh));
+  if (step) *step = m->step;
+  return SJ_OK;
+}
+extern "C" int sj_model_set_adam_state(sj_model* m, const float* mh, const float* vh, long step) {
+  SJ_REQUIRE(m && mh && vh && step >= 0, "set_adam_state: arguments");
+  TRY(copy_arena_in(m, mh, m->m));
+  TRY(copy_arena_in(m, vh, m->v));
+  m->step = step;
+  return SJ_OK;
+}
+
+extern "C" int sj_model_set_batch(sj_model* m, const int32_t* ids, const int32_t* targets, int on_device) {
+  SJ_REQUIRE(m && ids && targets, "set_batch: null");
+  size_t bytes = sizeof(int32_t) * (size_t)m->M;
+  if (on_device) {
+    SJ_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyDeviceToDevice, m->stream));
+    SJ_HIP(hipMemcpyAsync(m->targets, targets, bytes, hipMemcpyDeviceToDevice, m->stream));
+  } else {
+    for (long i = 0; i < m->M; i++)
+      SJ_REQUIRE(ids[i] >= 0 && ids[i] < m->V && targets[i] >= 0 && targets[i] < m->V,
+                 "batch token %ld out of vocabulary", i);
+    SJ_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyHostToDevice, m->stream));
+    SJ_HIP(hipMemcpyAsync(m->targets, targets, bytes, hipMemcpyHostToDevice, m->stream));
+    SJ_HIP(hipStreamSynchronize(m->stream));
+  }
+  return SJ_OK;
+}
+
+extern "C" int sj_model_forward_backward(sj_model* m) {
+  SJ_REQUIRE(m, "forward_backward: null");
+  TRY(forward(m));
+  TRY(backward(m));
+  return SJ_OK;
+}
+
+extern "C" int sj_model_use_graph(sj_model* m, int on) {
+  SJ_REQUIRE(m, "use_graph: null");
+  m->use_graph = on != 0;
+  return SJ_OK;
+}
+
+extern "C" int sj_model_train_step(sj_model* m, float lr) {
+  SJ_REQUIRE(m, "train_step: null");
+  // Adam::update increments the step and forms 1/(1-beta^step) on the host
+  // in f32 (crates/sejong-gpu/src/lib.rs:950-951).
+  m->step += 1;
+  const int slot = (int)(m->step % sj_model::RING);
+  sj_adam_step* h = m->step_host + slot;
+  SJ_HIP(hipEventSynchronize(m->step_done[slot]));  // copy from RING steps ago
+  h->lr = lr;
+  h->beta1 = m->adam.beta1;
+  h->beta2 = m->adam.beta2;
+  h->eps = m->adam.epsilon;
+  h->weight_decay = m->adam.weight_decay;
+  h->inv_b1 = 1.f / (1.f - powf(m->adam.beta1, (float)m->step));
+  h->inv_b2 = 1.f / (1.f - powf(m->adam.beta2, (float)m->step));
+  h->clip_norm = m->adam.clip_norm;
+  h->loss_scale = m->adam.loss_scale;
+  h->clip_enabled = m->adam.clip_enabled;
+  SJ_HIP(hipMemcpyAsync(m->step_dev, h, sizeof(sj_adam_step), hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipEventRecord(m->step_done[slot], m->stream));
+  if (!m->use_graph || m->profiling) return whole_step(m);
+  if (!m->exec) {
+    SJ_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int st = whole_step(m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (st) {
+      if (g) hipGraphDestroy(g);
+      return st;
+    }
+    SJ_HIP(e);
+    m->graph = g;
+    SJ_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+  }
+  SJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  return SJ_OK;
+}
+
+extern "C" int sj_model_profile(sj_model* m, int on) {
+  SJ_REQUIRE(m, "profile: null");
+  m->profiling = on != 0;
+  return SJ_OK;
+}
+
+// Aggregates the events of the ops recorded since the last call (syncs).
+extern "C" long sj_model_profile_collect(sj_model* m) {
+  if (!m) return -1;
+  if (hipStreamSynchronize(m->stream) != hipSuccess) return -1;
+  m->agg_names.clear();
+  m->agg_ms.clear();
+  m->agg_calls.clear();
+  for (size_t k = 0; k < m->prof_names.size(); k++) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, m->prof_events[2 * k], m->prof_events[2 * k + 1]) != hipSuccess) return -1;
+    std::string nm(m->prof_names[k]);
+    size_t j = 0;
+    while (j < m->agg_names.size() && m->agg_names[j] != nm) j++;
+    if (j == m->agg_names.size()) {
+      m->agg_names.push_back(nm);
+      m->agg_ms.push_back(0.0);
+      m->agg_calls.push_back(0);
+    }
+    m->agg_ms[j] += ms;
+    m->agg_calls[j] += 1;
+  }
+  m->prof_names.clear();
+  return (long)m->agg_names.size();
+}
+
+extern "C" int sj_model_profile_entry(sj_model* m, long i, const char** name, double* total_ms, long* calls) {
+  SJ_REQUIRE(m && i >= 0 && i < (long)m->agg_names.size(), "profile_entry: index %ld", i);
+  if (name) *name = m->agg_names[i].c_str();
+  if (total_ms) *total_ms = m->agg_ms[i];
+  if (calls) *calls = m->agg_calls[i];
+  return SJ_OK;
+}
+
+extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) {
+  SJ_REQUIRE(m, "read_loss: null");
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  double l = 0, ss = 0;
+  int32_t flag = 0;
+  SJ_HIP(hipMemcpy(&l, m->loss, sizeof(double), hipMemcpyDeviceToHost));
+  SJ_HIP(hipMemcpy(&ss, m->sumsq, sizeof(double), hipMemcpyDeviceToHost));
+  SJ_HIP(hipMemcpy(&flag, m->status, sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (loss) *loss = l;
+  if (grad_norm) *grad_norm = sqrt(ss) / (double)m->adam.loss_scale;
+  if (flag) return sjh::fail(SJ_ERR_NONFINITE, "nonfinite clipping gradient");
+  return SJ_OK;
+}
+
+extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* elements) {
+  SJ_REQUIRE(m && what && ptr, "buffer: null");
+  std::string w(what);
+  long n = 0;
+  if (w == "logits") { *ptr = m->logits; n = m->M * m->Vp; }
+  else if (w == "dlogits") { *ptr = m->dlogits; n = m->M * m->Vp; }
+  else if (w == "loss_rows") { *ptr = m->loss_rows; n = m->M; }
+  else if (w == "ids") { *ptr = m->ids; n = m->M; }
+  else if (w == "targets") { *ptr = m->targets; n = m->M; }
+  else if (w == "params") { *ptr = m->w; n = m->n_params; }
+  else if (w == "grads") { *ptr = m->g; n = m->n_params; }
+  else if (w == "mirror") { *ptr = m->mirror; n = m->mirror ? m->n_params : 0; }
+  else if (w == "workspace") { *ptr = m->ws; n = (long)m->ws_bytes; }
+  else if (w == "stream") { *ptr = (void*)m->stream; n = 0; }
+  else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);
+  if (elements) *elements = n;
+  return SJ_OK;
+}

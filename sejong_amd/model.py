@@ -1,0 +1,248 @@
+"""Host side of the byte Transformer step: configuration, reference
+parameter layout and initialisation, synthetic byte batches, and a Model /
+Adam pair that drives the native step driver (sj_model_* in the C ABI).
+
+Mirrors crates/sejong-core (ModelConfig / TrainConfig defaults, lib.rs:
+60-434), crates/sejong-model (layout architecture.rs:63-137, Model::
+initialize lib.rs:56-133) and crates/sejong-train (Adam lib.rs:111-247,
+Corpus::batch lib.rs:72-88).  All compute runs in libsejong_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _native as N
+from .rng import Rng
+
+VOCAB = 257  # core lib.rs:305
+EOS = 256
+F32_EPSILON = float(np.finfo(np.float32).eps)
+
+
+@dataclass
+class ModelConfig:
+    """crates/sejong-core/src/lib.rs:60-111 (dense subset used by this path)."""
+    width: int = 512
+    layers: int = 8
+    heads: int = 8
+    kv_heads: int | None = None
+    ffn_width: int = 1536
+    context: int = 2048
+    rope_theta: float = 10000.0
+    norm_epsilon: float = F32_EPSILON
+    precision: str = "bf16"  # "f32" | "bf16"
+    seed: int = 42
+
+    @property
+    def kv(self) -> int:
+        return self.kv_heads or self.heads
+
+    @property
+    def head_dim(self) -> int:
+        return self.width // self.heads
+
+    def validate(self):
+        if not (self.width > 0 and self.heads > 0 and self.width % self.heads == 0):
+            raise ValueError("width must be divisible by heads")
+        if self.head_dim % 2:
+            raise ValueError("RoPE requires an even head width")
+        if not (self.layers > 0 and self.ffn_width > 0 and self.context > 0):
+            raise ValueError("layers, ffn_width and context must be positive")
+        if self.heads % self.kv:
+            raise ValueError("heads must be divisible by kv_heads")
+        if self.precision not in ("f32", "bf16"):
+            raise ValueError("precision must be f32 or bf16")
+
+
+@dataclass
+class TrainConfig:
+    """crates/sejong-core/src/lib.rs:308-362 defaults (AdamW subset)."""
+    sequence: int = 512
+    batch: int = 1
+    learning_rate: float = 3e-4
+    beta1: float = 0.9
+    beta2: float = 0.95
+    epsilon: float = 0.0
+    weight_decay: float = 0.1
+    clip_norm: float = 1.0
+    clip_enabled: bool = True
+    loss_scale: float = 1.0
+    seed: int = 123
+
+
+# BASELINE configurations of this path
+def config(name: str) -> tuple[ModelConfig, TrainConfig]:
+    if name == "cfg1":  # single pre-norm block, fp32
+        return (ModelConfig(width=128, layers=1, heads=4, kv_heads=2, ffn_width=384, context=128,
+                            norm_epsilon=1e-6, precision="f32"),
+                TrainConfig(sequence=128, batch=2))
+    if name == "cfg2":  # 6-layer byte Transformer, bf16, AdamW lr 3e-4 wd 0.01
+        return (ModelConfig(width=384, layers=6, heads=6, kv_heads=2, ffn_width=1024, context=512,
+                            precision="bf16"),
+                TrainConfig(sequence=512, batch=8, learning_rate=3e-4, weight_decay=0.01))
+    raise KeyError(name)
+
+
+def layout(c: ModelConfig) -> list[tuple[str, tuple[int, ...], bool]]:
+    """(name, shape, is_norm) in the reference order (architecture.rs:63-137,
+    dense global stage)."""
+    d, kv = c.width, c.width // c.heads * c.kv
+    out = [("embedding", (VOCAB, d), False)]
+    for i in range(c.layers):
+        p = f"layers.{i}"
+        out += [(f"{p}.attention_norm", (d,), True), (f"{p}.ffn_norm", (d,), True),
+                (f"{p}.query", (d, d), False), (f"{p}.key", (d, kv), False), (f"{p}.value", (d, kv), False),
+                (f"{p}.attention_output", (d, d), False),
+                (f"{p}.gate", (d, c.ffn_width), False), (f"{p}.up", (d, c.ffn_width), False),
+                (f"{p}.down", (c.ffn_width, d), False)]
+    out += [("final_norm", (d,), True), ("output", (d, VOCAB), False)]
+    return out
+
+
+def param_count(c: ModelConfig) -> int:
+    return sum(math.prod(s) for _, s, _ in layout(c))
+
+
+def init_params(c: ModelConfig, std: float | None = 0.02, seed: int | None = None) -> np.ndarray:
+    """Flat fp32 masters in the reference layout.  std=None restates
+    Model::initialize (model lib.rs:83-115): N(0, 1/sqrt(fan_in)), /sqrt(2
+    depth) for down / attention_output, embedding 1/sqrt(d); otherwise every
+    matrix is N(0, std) (the BASELINE weights).  Norm weights are 1."""
+    rng = Rng(c.seed if seed is None else seed)
+    parts = []
+    for name, shape, norm in layout(c):
+        n = math.prod(shape)
+        if norm:
+            parts.append(np.ones(n))
+            continue
+        if std is None:
+            s = 1.0 / math.sqrt(shape[1] if name == "embedding" else shape[0])
+            if name.endswith(".down") or name.endswith(".attention_output"):
+                s /= math.sqrt(2.0 * c.layers)
+        else:
+            s = std
+        parts.append(rng.normal(n, s))
+    return np.concatenate(parts).astype(np.float32)
+
+
+def byte_batch(rng: Rng, batch: int, sequence: int) -> tuple[np.ndarray, np.ndarray]:
+    """Synthetic uniform-byte batch: each row is sequence+1 bytes drawn with
+    index(256); inputs are [0:T], targets [1:T+1] (the Corpus::batch shift,
+    train lib.rs:72-88)."""
+    raw = rng.indices(256, batch * (sequence + 1)).reshape(batch, sequence + 1).astype(np.int32)
+    return raw[:, :-1].reshape(-1).copy(), raw[:, 1:].reshape(-1).copy()
+
+
+def _np_ptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class Model:
+    """One byte Transformer resident on the GPU with its AdamW state."""
+
+    def __init__(self, mc: ModelConfig, tc: TrainConfig, stream: int | None = None):
+        mc.validate()
+        if tc.sequence > mc.context:
+            raise ValueError("training requires sequence within context")
+        self.mc, self.tc = mc, tc
+        cfg = N.ModelConfig(vocab=VOCAB, width=mc.width, layers=mc.layers, heads=mc.heads, kv_heads=mc.kv,
+                            ffn_width=mc.ffn_width, sequence=tc.sequence, batch=tc.batch,
+                            norm_epsilon=mc.norm_epsilon, rope_theta=mc.rope_theta,
+                            precision=N.SJ_BF16 if mc.precision == "bf16" else N.SJ_F32)
+        adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
+                            clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
+        handle = ctypes.c_void_p()
+        N.api.sj_model_create(ctypes.byref(cfg), ctypes.byref(adam), ctypes.c_void_p(stream or 0),
+                              ctypes.byref(handle))
+        self.h = handle
+        self.count = N.load().sj_model_param_count(self.h)
+        assert self.count == param_count(mc), (self.count, param_count(mc))
+
+    def close(self):
+        if self.h:
+            N.api.sj_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def param_info(self):
+        out = []
+        for i in range(N.load().sj_model_param_tensors(self.h)):
+            name, r, c, o = ctypes.c_char_p(), ctypes.c_long(), ctypes.c_long(), ctypes.c_long()
+            N.api.sj_model_param_info(self.h, i, ctypes.byref(name), ctypes.byref(r), ctypes.byref(c), ctypes.byref(o))
+            out.append((name.value.decode(), (r.value, c.value), o.value))
+        return out
+
+    def set_params(self, flat: np.ndarray):
+        a = np.ascontiguousarray(flat, dtype=np.float32)
+        assert a.size == self.count
+        N.api.sj_model_set_params(self.h, _np_ptr(a))
+
+    def get_params(self) -> np.ndarray:
+        a = np.empty(self.count, np.float32)
+        N.api.sj_model_get_params(self.h, _np_ptr(a))
+        return a
+
+    def get_grads(self) -> np.ndarray:
+        a = np.empty(self.count, np.float32)
+        N.api.sj_model_get_grads(self.h, _np_ptr(a))
+        return a
+
+    def get_adam_state(self):
+        m = np.empty(self.count, np.float32); v = np.empty(self.count, np.float32); st = ctypes.c_long()
+        N.api.sj_model_get_adam_state(self.h, _np_ptr(m), _np_ptr(v), ctypes.byref(st))
+        return m, v, st.value
+
+    def set_batch(self, ids: np.ndarray, targets: np.ndarray):
+        ids = np.ascontiguousarray(ids, dtype=np.int32); tg = np.ascontiguousarray(targets, dtype=np.int32)
+        assert ids.size == self.tc.batch * self.tc.sequence == tg.size
+        N.api.sj_model_set_batch(self.h, _np_ptr(ids), _np_ptr(tg), 0)
+
+    def set_batch_device(self, ids_ptr: int, targets_ptr: int):
+        N.api.sj_model_set_batch(self.h, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(targets_ptr), 1)
+
+    def forward_backward(self):
+        N.api.sj_model_forward_backward(self.h)
+
+    def use_graph(self, on: bool = True):
+        N.api.sj_model_use_graph(self.h, int(on))
+
+    def train_step(self, lr: float | None = None):
+        N.api.sj_model_train_step(self.h, ctypes.c_float(self.tc.learning_rate if lr is None else lr))
+
+    def read_loss(self) -> tuple[float, float]:
+        loss, norm = ctypes.c_double(), ctypes.c_double()
+        N.api.sj_model_read_loss(self.h, ctypes.byref(loss), ctypes.byref(norm))
+        return loss.value, norm.value
+
+    def profile(self, on: bool = True):
+        N.api.sj_model_profile(self.h, int(on))
+
+    def profile_collect(self) -> dict[str, tuple[float, int]]:
+        """{op name: (total ms, calls)} for the ops run since the last collect."""
+        n = N.load().sj_model_profile_collect(self.h)
+        if n < 0:
+            raise N.SejongError(3, "profile collection failed")
+        out = {}
+        for i in range(n):
+            name, ms, calls = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_long()
+            N.api.sj_model_profile_entry(self.h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(calls))
+            out[name.value.decode()] = (ms.value, calls.value)
+        return out
+
+    def buffer(self, what: str) -> tuple[int, int]:
+        p, n = ctypes.c_void_p(), ctypes.c_long()
+        N.api.sj_model_buffer(self.h, what.encode(), ctypes.byref(p), ctypes.byref(n))
+        return p.value or 0, n.value
+
+    @property
+    def stream(self) -> int:
+        return self.buffer("stream")[0]

@@ -1,0 +1,365 @@
+"""Pins the FP64 oracle before anything is checked against it.
+
+Each test checks one oracle function against something that does not share
+its code: published test vectors, the reference's own check programs
+(restated from their text), closed forms, invariants, finite differences and
+brute force.  A plausible slip in the oracle (dropped term, wrong sign or
+index, transposed operand) fails at least one of them.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def values(n, offset):
+    """Closed-form inputs of crates/sejong-gpu/examples/hierarchy_check.rs:11-15."""
+    return np.array([((i * 17 + offset) % 41 - 20.0) / 31.0 for i in range(n)], dtype=np.float32).astype(np.float64)
+
+
+# ------------------------------------------------------------------ RNG
+def test_splitmix64_published_vectors():
+    # SplitMix64 reference outputs (Vigna's splitmix64.c / Java SplittableRandom).
+    r = O.Rng(1234567)
+    assert [r.next_u64() for _ in range(5)] == [
+        6457827717110365317, 3203168211198807973, 9817491932198370423,
+        4593380528125082431, 16408922859458223821]
+    assert O.Rng(0).next_u64() == 0xE220A8397B1DCDAF
+
+
+def test_rng_index_rejection_threshold():
+    # index(n) rejects draws below (2^64 - n) mod n (core lib.rs:610-619);
+    # for powers of two the threshold is 0 so index == next_u64 % n.
+    a, b = O.Rng(7), O.Rng(7)
+    for _ in range(100):
+        assert a.index(256) == b.next_u64() % 256
+    # n = 3: threshold = 2^64 mod 3 = 1; brute-force the accept rule
+    a, b = O.Rng(11), O.Rng(11)
+    thr = (2 ** 64) % 3
+    for _ in range(50):
+        got = a.index(3)
+        while True:
+            x = b.next_u64()
+            if x >= thr:
+                break
+        assert got == x % 3
+
+
+def test_rng_uniform_and_normal_moments():
+    r = O.Rng(42)
+    u = np.array([r.uniform() for _ in range(20000)])
+    assert 0 < u.min() and u.max() < 1 and abs(u.mean() - 0.5) < 0.01
+    z = O.Rng(42).normal_fill(200000, 0.02)
+    assert abs(z.mean()) < 2e-4 and abs(z.std() - 0.02) < 2e-4
+
+
+# ------------------------------------------------------------ rounding
+def _bf16_bits(x32):
+    b = x32.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def test_round_bf16_matches_bit_trick():
+    rng = np.random.default_rng(0)
+    x = rng.normal(0, 1, 100000).astype(np.float32) * np.float32(2.0) ** rng.integers(-60, 60, 100000).astype(np.float32)
+    # exact ties: low 16 bits == 0x8000 (odd and even upper halves)
+    ties = (rng.integers(0, 2 ** 31, 1000).astype(np.uint32) & 0xFFFF0000 | 0x8000).view(np.float32)
+    x = np.concatenate([x, ties, np.array([1e-40, -3e-39, 0.0], np.float32)])
+    np.testing.assert_array_equal(O.round_to(x.astype(np.float64), "bf16"), _bf16_bits(x))
+
+
+def test_round_f32():
+    x = np.random.default_rng(1).normal(size=1000)
+    np.testing.assert_array_equal(O.round_to(x, "f32"), x.astype(np.float32).astype(np.float64))
+
+
+# --------------------------------------------------------------- matmul
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_matmul_vs_numpy(ta, tb):
+    rng = np.random.default_rng(2)
+    M, N, K = 13, 7, 29
+    A = rng.normal(size=(K, M) if ta else (M, K))
+    B = rng.normal(size=(N, K) if tb else (K, N))
+    ref = (A.T if ta else A) @ (B.T if tb else B)
+    np.testing.assert_allclose(O.matmul(A, B, ta, tb), ref, rtol=1e-12, atol=1e-12)
+
+
+# -------------------------------------------------------------- RMSNorm
+def test_rmsnorm_closed_form_and_scale_invariance():
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(5, 16)); w = rng.normal(size=16)
+    y = O.rmsnorm_fwd(x, w, 0.0)
+    np.testing.assert_allclose(y, O.rmsnorm_fwd(7.5 * x, w, 0.0), rtol=1e-13)
+    # unit weights: every row has unit RMS
+    np.testing.assert_allclose(np.sqrt((O.rmsnorm_fwd(x, np.ones(16), 0.0) ** 2).mean(1)), 1.0, rtol=1e-13)
+
+
+def _fd_vjp(f, x, dy, eps=1e-6, ndir=3, seed=0):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(ndir):
+        e = rng.normal(size=x.shape)
+        out.append((e, ((f(x + eps * e) - f(x - eps * e)) * dy).sum() / (2 * eps)))
+    return out
+
+
+def test_rmsnorm_backward_finite_difference():
+    rng = np.random.default_rng(4)
+    R, D, eps = 6, 24, 1e-6
+    x = rng.normal(size=(R, D)); w = rng.normal(size=D); dy = rng.normal(size=(R, D))
+    acc = rng.normal(size=(R, D))
+    dx, dw = O.rmsnorm_bwd(x, w, dy, eps, dx_acc=acc)
+    for e, fd in _fd_vjp(lambda xx: O.rmsnorm_fwd(xx, w, eps), x, dy):
+        assert abs(((dx - acc) * e).sum() - fd) < 1e-7 * max(1, abs(fd))
+    for e, fd in _fd_vjp(lambda ww: O.rmsnorm_fwd(x, ww, eps), w, dy):
+        assert abs((dw * e).sum() - fd) < 1e-7 * max(1, abs(fd))
+    # eps = 0: y is scale invariant in x, so sum(dx * x) = 0 per row
+    dx0, _ = O.rmsnorm_bwd(x, w, dy, 0.0)
+    np.testing.assert_allclose((dx0 * x).sum(1), 0.0, atol=1e-12)
+
+
+# ----------------------------------------------------------------- RoPE
+def test_rope_closed_form_inverse_and_norm():
+    rng = np.random.default_rng(5)
+    T, H, D = 7, 3, 8
+    x = rng.normal(size=(2 * T, H * D))
+    y = O.rope(x, T, H, D)
+    # position 0 is the identity
+    np.testing.assert_allclose(y[0], x[0], rtol=0, atol=0)
+    # position 1, pair 0: angle = 1 rad
+    a, b = x[1, 0], x[1, 1]
+    np.testing.assert_allclose(y[1, :2], [a * math.cos(1) - b * math.sin(1), a * math.sin(1) + b * math.cos(1)], rtol=1e-14)
+    # position 3, pair 2: angle = 3 * 10000^(-4/8)
+    ang = 3 * 10000.0 ** (-4 / 8)
+    a, b = x[3, D + 4], x[3, D + 5]
+    np.testing.assert_allclose(y[3, D + 4:D + 6], [a * math.cos(ang) - b * math.sin(ang), a * math.sin(ang) + b * math.cos(ang)], rtol=1e-13)
+    # rotation: pair norms preserved, inverse undoes
+    np.testing.assert_allclose((y.reshape(-1, 2) ** 2).sum(1), (x.reshape(-1, 2) ** 2).sum(1), rtol=1e-13)
+    np.testing.assert_allclose(O.rope(y, T, H, D, inverse=True), x, atol=1e-13)
+    # second batch row-block restarts positions (pos = row mod T)
+    np.testing.assert_allclose(y[T], x[T])
+
+
+# ------------------------------------------------------------ Attention
+def _attention_reference_check(q, k, v, dy, t, h, kh, d, window):
+    """Text restatement of attention_reference, gpu/examples/hierarchy_check.rs:16-77."""
+    out = np.zeros(q.size); dq = np.zeros(q.size); dk = np.zeros(k.size); dv = np.zeros(k.size)
+    for pos in range(t):
+        for head in range(h):
+            qr = (pos * h + head) * d
+            kvh = head // (h // kh)
+            first = 0 if window == 0 else max(pos + 1 - window, 0)
+            ps = list(range(first, pos + 1))
+            scores = [sum(q[qr + j] * k[(p * kh + kvh) * d + j] for j in range(d)) / math.sqrt(d) for p in ps]
+            m = max(scores)
+            z = sum(math.exp(s - m) for s in scores)
+            probs = [math.exp(s - m) / z for s in scores]
+            dp = [sum(dy[qr + j] * v[(p * kh + kvh) * d + j] for j in range(d)) for p in ps]
+            delta = sum(a * b for a, b in zip(probs, dp))
+            for j, p in enumerate(ps):
+                kr = (p * kh + kvh) * d
+                ds = probs[j] * (dp[j] - delta) / math.sqrt(d)
+                for col in range(d):
+                    out[qr + col] += probs[j] * v[kr + col]
+                    dq[qr + col] += ds * k[kr + col]
+                    dk[kr + col] += ds * q[qr + col]
+                    dv[kr + col] += probs[j] * dy[qr + col]
+    return out, dq, dk, dv
+
+
+@pytest.mark.parametrize("window", [0, 3])
+def test_attention_matches_reference_check(window):
+    t, h, kh, d = 5, 4, 2, 4
+    q = values(t * h * d, 0); k = values(t * kh * d, 3); v = values(t * kh * d, 9); dy = values(t * h * d, 12)
+    ref = _attention_reference_check(q, k, v, dy, t, h, kh, d, window)
+    o, lse = O.attention_fwd(q.reshape(t, h * d), k.reshape(t, kh * d), v.reshape(t, kh * d), 1, t, h, kh, d, window)
+    dq, dk, dv, _ = O.attention_bwd(q.reshape(t, h * d), k.reshape(t, kh * d), v.reshape(t, kh * d), o, lse,
+                                    dy.reshape(t, h * d), 1, t, h, kh, d, window)
+    for got, exp in zip((o, dq, dk, dv), ref):
+        np.testing.assert_allclose(got.ravel(), exp, rtol=1e-12, atol=1e-14)
+
+
+def test_attention_gqa_equals_repeated_mha_and_fd():
+    rng = np.random.default_rng(6)
+    B, T, HQ, HK, D = 2, 9, 6, 2, 4
+    q = rng.normal(size=(B * T, HQ * D)); k = rng.normal(size=(B * T, HK * D)); v = rng.normal(size=(B * T, HK * D))
+    do = rng.normal(size=(B * T, HQ * D))
+    o, lse = O.attention_fwd(q, k, v, B, T, HQ, HK, D)
+    rep = HQ // HK
+    kr = np.repeat(k.reshape(B * T, HK, D), rep, axis=1).reshape(B * T, HQ * D)
+    vr = np.repeat(v.reshape(B * T, HK, D), rep, axis=1).reshape(B * T, HQ * D)
+    o2, lse2 = O.attention_fwd(q, kr, vr, B, T, HQ, HQ, D)
+    np.testing.assert_allclose(o, o2, rtol=1e-13); np.testing.assert_allclose(lse, lse2, rtol=1e-13)
+    # first position attends only to itself: o = v, lse = q.k/sqrt(D)
+    np.testing.assert_allclose(o.reshape(B * T, HQ, D)[0, 0], v.reshape(B * T, HK, D)[0, 0], rtol=1e-13)
+    dq, dk, dv, delta = O.attention_bwd(q, k, v, o, lse, do, B, T, HQ, HK, D)
+    np.testing.assert_allclose(delta, (do * o).reshape(-1, D).sum(1), rtol=1e-12)
+    f = lambda qq, kk, vv: O.attention_fwd(qq, kk, vv, B, T, HQ, HK, D)[0]
+    for e, fd in _fd_vjp(lambda qq: f(qq, k, v), q, do):
+        assert abs((dq * e).sum() - fd) < 1e-6 * max(1, abs(fd))
+    for e, fd in _fd_vjp(lambda kk: f(q, kk, v), k, do):
+        assert abs((dk * e).sum() - fd) < 1e-6 * max(1, abs(fd))
+    for e, fd in _fd_vjp(lambda vv: f(q, k, vv), v, do):
+        assert abs((dv * e).sum() - fd) < 1e-6 * max(1, abs(fd))
+
+
+def test_attention_window_covering_sequence_is_causal():
+    rng = np.random.default_rng(7)
+    B, T, H, D = 1, 6, 2, 4
+    q, k, v = (rng.normal(size=(T, H * D)) for _ in range(3))
+    a = O.attention_fwd(q, k, v, B, T, H, H, D, 0)
+    b = O.attention_fwd(q, k, v, B, T, H, H, D, T)
+    np.testing.assert_allclose(a[0], b[0]); np.testing.assert_allclose(a[1], b[1])
+
+
+# --------------------------------------------------------------- SwiGLU
+def test_swiglu_fd():
+    rng = np.random.default_rng(8)
+    g, u, dy = (rng.normal(size=50) * 3 for _ in range(3))
+    dg, du = O.swiglu_bwd(g, u, dy)
+    h = O.swiglu_fwd(g, u)
+    np.testing.assert_allclose(h, g * u / (1 + np.exp(-g)), rtol=1e-14)
+    eps = 1e-6
+    np.testing.assert_allclose(dg, dy * (O.swiglu_fwd(g + eps, u) - O.swiglu_fwd(g - eps, u)) / (2 * eps), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(du, dy * (O.swiglu_fwd(g, u + eps) - O.swiglu_fwd(g, u - eps)) / (2 * eps), rtol=1e-6, atol=1e-9)
+
+
+# ------------------------------------------------------ CE / embedding
+def test_cross_entropy_closed_form_and_fd():
+    rng = np.random.default_rng(9)
+    x = rng.normal(size=(5, O.VOCAB)) * 3; t = rng.integers(0, 256, 5).astype(np.int32)
+    loss, dx = O.cross_entropy(x, t, 0.25)
+    m = x.max(1, keepdims=True)
+    np.testing.assert_allclose(loss, (m[:, 0] + np.log(np.exp(x - m).sum(1))) - x[np.arange(5), t], rtol=1e-13)
+    np.testing.assert_allclose(dx.sum(1), 0.0, atol=1e-14)
+    eps = 1e-6
+    e = rng.normal(size=x.shape)
+    fd = (O.cross_entropy(x + eps * e, t)[0].sum() - O.cross_entropy(x - eps * e, t)[0].sum()) / (2 * eps) * 0.25
+    assert abs((dx * e).sum() - fd) < 1e-7
+
+
+def test_embedding_roundtrip():
+    rng = np.random.default_rng(10)
+    W = rng.normal(size=(O.VOCAB, 6)); ids = np.array([3, 256, 3, 0], np.int32)
+    y = O.embedding_fwd(W, ids)
+    np.testing.assert_array_equal(y, W[ids])
+    dy = rng.normal(size=(4, 6))
+    dW = O.embedding_bwd(dy, ids, O.VOCAB)
+    np.testing.assert_allclose(dW[3], dy[0] + dy[2]); np.testing.assert_array_equal(dW[5], 0.0)
+    np.testing.assert_allclose(dW[256], dy[1])
+
+
+# ----------------------------------------------------------------- AdamW
+def test_adamw_two_step_closed_form():
+    """crates/sejong-train/examples/system_check.rs:135-163: gradient 0.25 then
+    0 (the second update sees a zero-filled gradient), lr 1e-3, defaults."""
+    b1, b2, eps, wd, lr = 0.9, 0.95, 0.0, 0.1, 0.001
+    w0 = 0.3
+    w, m, v = np.array([w0]), np.zeros(1), np.zeros(1)
+    expected, em, ev = w0, 0.0, 0.0
+    for step, g in enumerate([0.25, 0.0]):
+        ib1 = 1 / (1 - np.float32(b1) ** np.float32(step + 1))
+        ib2 = 1 / (1 - np.float32(b2) ** np.float32(step + 1))
+        w, m, v = O.adamw(w, np.array([g]), m, v, lr, b1, b2, eps, wd, ib1, ib2, 1.0)
+        em = b1 * em + (1 - b1) * g
+        ev = b2 * ev + (1 - b2) * g * g
+        expected = expected * (1 - lr * wd) - lr * (em / (1 - b1 ** (step + 1))) / (math.sqrt(ev / (1 - b2 ** (step + 1))) + eps)
+    assert abs(w[0] - expected) < 2e-7
+    # zero gradient and zero state: the guarded denominator leaves only decay
+    w2, _, _ = O.adamw(np.array([1.0]), np.zeros(1), np.zeros(1), np.zeros(1), lr, b1, b2, 0.0, wd, 10.0, 20.0, 1.0)
+    assert w2[0] == 1.0 * (1 - lr * wd)
+
+
+# --------------------------------------------------------------- routing
+def test_router_closed_form():
+    """Closed-form router check, gpu/examples/hierarchy_check.rs:164-222."""
+    logits = np.array([0.2, 1.1, -0.7, 0.6, -0.4, 1.4, -0.1, 0.8, 1.7, 2.1, 0.2, -1.0], np.float32).reshape(4, 3)
+    ids, w = O.route_topk(logits, 2)
+    x = values(20, 8).reshape(4, 5)
+    # combine with expert e scaling its input by (e+1); seed dy = 1
+    for row in range(4):
+        order = sorted(range(3), key=lambda j: -logits[row, j])
+        assert list(ids[row]) == order[:2]
+        norm = np.exp(logits[row].astype(np.float64)).sum()
+        np.testing.assert_allclose(w[row], np.exp(logits[row, order[:2]].astype(np.float64)) / norm, rtol=1e-12)
+        factor = sum(np.exp(float(logits[row, j])) / norm * (j + 1) for j in order[:2])
+        s = x[row].sum()
+        # d/d weight_k of sum(out) = (e_k+1) * sum(x);  route backward gives dl
+        dyk = np.array([[(ids[row, k] + 1) * s for k in range(2)]])
+        dl = O.route_topk_bwd(logits[row:row + 1], ids[row:row + 1], w[row:row + 1], dyk)[0]
+        for j in range(3):
+            up = (j + 1) if j in order[:2] else 0
+            np.testing.assert_allclose(dl[j], np.exp(float(logits[row, j])) / norm * s * (up - factor), rtol=1e-10, atol=1e-12)
+
+
+def test_router_ties_lowest_index_and_pack_order():
+    logits = np.array([[1.0, 1.0, 0.5, 1.0], [0.0, 0.0, 0.0, 0.0], [3.0, -1.0, 3.0, 2.0]], np.float32)
+    ids, _ = O.route_topk(logits, 2)
+    np.testing.assert_array_equal(ids, [[0, 1], [0, 1], [0, 2]])
+    tokens, slots, counts = O.route_pack(ids, 4)
+    np.testing.assert_array_equal(counts, [3, 2, 1, 0])
+    np.testing.assert_array_equal(slots[0, :3], [0, 2, 4]); np.testing.assert_array_equal(tokens[0, :3], [0, 1, 2])
+    np.testing.assert_array_equal(slots[1, :2], [1, 3]); np.testing.assert_array_equal(slots[2, :1], [5])
+
+
+# ----------------------------------------------------------------- model
+TINY = dict(d=16, layers=2, hq=4, hk=2, ffn=24, T=6, B=2, eps=1e-6, theta=10000.0)
+
+
+def _tiny_inputs(cfg, seed=0, std=0.3):
+    n = O.model_param_count(cfg["d"], cfg["layers"], cfg["hq"], cfg["hk"], cfg["ffn"])
+    rng = np.random.default_rng(seed)
+    p = rng.normal(0, std, n)
+    ids = rng.integers(0, 256, cfg["T"] * cfg["B"]).astype(np.int32)
+    tg = rng.integers(0, 256, cfg["T"] * cfg["B"]).astype(np.int32)
+    return p, ids, tg
+
+
+def test_model_directional_derivative():
+    """FD directional derivative of the full loss (system_check.rs:53-107),
+    in exact (unrounded) mode so the tolerance can be tight."""
+    p, ids, tg = _tiny_inputs(TINY)
+    loss, g, _, _ = O.model_fwd_bwd(TINY, p, ids, tg, dtype="none")
+    rng = np.random.default_rng(112)
+    for _ in range(3):
+        d = rng.normal(size=p.size) / math.sqrt(p.size)
+        eps = 1e-5
+        fd = (O.model_loss(TINY, p + eps * d, ids, tg, "none") - O.model_loss(TINY, p - eps * d, ids, tg, "none")) / (2 * eps)
+        an = (g * d).sum()
+        assert abs(fd - an) < 1e-7 + 1e-6 * abs(an), (fd, an)
+
+
+def test_model_per_tensor_fd_and_f32_mode():
+    # each parameter tensor separately (catches a wrong gradient on one member)
+    cfg = dict(TINY, layers=1)
+    p, ids, tg = _tiny_inputs(cfg, seed=3)
+    _, g, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype="none")
+    d, J, F, V = cfg["d"], cfg["d"] // cfg["hq"] * cfg["hk"], cfg["ffn"], O.VOCAB
+    sizes = [V * d, d, d, d * d, d * J, d * J, d * d, d * F, d * F, F * d, d, d * V]
+    rng = np.random.default_rng(5)
+    off = 0
+    for n in sizes:
+        e = np.zeros(p.size); e[off:off + n] = rng.normal(size=n)
+        eps = 1e-5
+        fd = (O.model_loss(cfg, p + eps * e, ids, tg, "none") - O.model_loss(cfg, p - eps * e, ids, tg, "none")) / (2 * eps)
+        an = (g * e).sum()
+        assert abs(fd - an) < 1e-8 + 1e-6 * abs(an), (off, fd, an)
+        off += n
+    # f32 storage mode stays within f32 roundoff of the exact mode
+    l32, g32, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype="f32")
+    lx, gx, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype="none")
+    assert abs(l32 - lx) < 1e-5 and np.linalg.norm(g32 - gx) < 1e-4 * np.linalg.norm(gx)
+
+
+def test_model_causal_prefix_and_batch_separation():
+    p, ids, tg = _tiny_inputs(TINY, seed=9)
+    _, _, rows, _ = O.model_fwd_bwd(TINY, p, ids, tg, dtype="bf16")
+    ids2 = ids.copy(); ids2[4] = (ids2[4] + 1) % 256  # batch 0, position 4
+    _, _, rows2, _ = O.model_fwd_bwd(TINY, p, ids2, tg, dtype="bf16")
+    T = TINY["T"]
+    np.testing.assert_array_equal(rows[:4], rows2[:4])      # causal prefix
+    np.testing.assert_array_equal(rows[T:], rows2[T:])      # other sequence
+    assert rows[4] != rows2[4]
