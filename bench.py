@@ -115,7 +115,6 @@ def main():
         sys.exit(2)
 
     import numpy as np
-    import torch
     from sejong_amd.model import Model, byte_batch, config, init_params
     from sejong_amd.rng import Rng
 
@@ -128,21 +127,15 @@ def main():
     ids, tg = byte_batch(Rng(tc.seed), tc.batch, tc.sequence)
     model.set_batch(ids, tg)  # resident in HBM before timing
     model.use_graph(not args.no_graph)
-    stream = torch.cuda.ExternalStream(model.stream)
 
     for _ in range(args.warmup):
         model.train_step(tc.learning_rate)
-    loss0, _ = model.read_loss()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    loss0, _ = model.read_loss()  # synchronises the model stream
+    model.synchronize()
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        model.train_step(tc.learning_rate)
-    end.record(stream)
-    torch.cuda.synchronize()
+    gpu_ms = model.time_steps(args.steps, tc.learning_rate)  # HIP events around the K steps
+    model.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(end)
     loss, gnorm = model.read_loss()
     ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
     log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events {gpu_ms / args.steps:.4f}, "

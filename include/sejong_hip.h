@@ -17,8 +17,9 @@
  *    its comment says so (the model calls that read results back).
  *  - All pointers are caller-owned device pointers, row-major 2-D with an
  *    explicit leading dimension (`ld*`, in elements).  No call allocates
- *    device memory except sj_model_create.  Calls that need scratch take a
- *    `workspace` pointer sized by the matching *_workspace_bytes query.
+ *    device memory except sj_alloc and sj_model_create.  Calls that need
+ *    scratch take a `workspace` pointer sized by the matching
+ *    *_workspace_bytes query.
  *  - dtypes use the reference's DType order (crates/sejong-core/src/lib.rs:
  *    34-41) plus bf16: SJ_F32=0, SJ_F64=1, SJ_F16=2, SJ_I32=3, SJ_BF16=4.
  *    The kernels compute in fp32 (FP64 for norms and loss sums, as the
@@ -54,6 +55,20 @@ const char *sj_last_error(void);
 /* Library / device identification: writes the gfx arch name (e.g. "gfx950")
  * and CU count of the current device. */
 int sj_device_info(char *arch, size_t arch_len, int *compute_units);
+
+/* Device memory, transfers and timing for callers without their own HIP
+ * allocator (the reference Engine's empty / from_f32 / to_f32, crates/
+ * sejong-gpu/src/lib.rs:234-365, and EventPair timing, hip.rs:59-112).
+ * Transfers are synchronous; sj_event_elapsed waits for `end`. */
+int sj_alloc(size_t bytes, void **ptr);
+int sj_free(void *ptr);
+int sj_upload(void *dst, const void *src, size_t bytes);
+int sj_download(void *dst, const void *src, size_t bytes);
+int sj_synchronize(void *stream);
+int sj_event_create(void **ev);
+int sj_event_destroy(void *ev);
+int sj_event_record(void *ev, void *stream);
+int sj_event_elapsed(void *start, void *end, float *ms);
 
 /* ---------------------------------------------------------- elementwise */
 
@@ -298,6 +313,13 @@ int sj_model_read_loss(sj_model *m, double *loss, double *grad_norm);
 int sj_model_profile(sj_model *m, int on);
 long sj_model_profile_collect(sj_model *m);
 int sj_model_profile_entry(sj_model *m, long i, const char **name, double *total_ms, long *calls);
+/* The stored forward activations of the last step in a fixed pack order
+ * (per layer x, z, q, k, v, o, lse, x1, z2, g, u, h; then the last residual
+ * x_L, the final-norm output and the fp32 logits), converted to fp32 (exact
+ * for bf16 storage).  Used to check the backward conditioned on the stored
+ * operands.  Synchronous. */
+long sj_model_activation_count(const sj_model *m);
+int sj_model_export_activations(sj_model *m, float *host);
 /* Device pointers of internal buffers for callers that time or inspect
  * kernels directly (what: "logits", "loss_rows", "ids", "targets"). */
 int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);

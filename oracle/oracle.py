@@ -66,6 +66,10 @@ def _declare(L):
     L.or_route_topk_bwd.argtypes = [_F, _I, _D, _D, _D, _L, _L, _L]
     L.or_route_pack.argtypes = [_I, _I, _I, _I, _L, _L, _L]
     L.or_model_param_count.argtypes = [_L] * 5; L.or_model_param_count.restype = _L
+    L.or_model_acts_count.argtypes = [_L] * 7; L.or_model_acts_count.restype = _L
+    L.or_model_forward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _D]
+    L.or_model_backward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _D, _I, _I, _D, _D]
+    L.or_model_backward.restype = ctypes.c_double
     L.or_model_fwd_bwd.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I, _D, _D, _D]
     L.or_model_fwd_bwd.restype = ctypes.c_double
     L.or_model_loss.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I]
@@ -262,6 +266,46 @@ def model_fwd_bwd(cfg, params, ids, targets, dtype="f32", want_logits=False):
     loss = lib().or_model_fwd_bwd(d, layers, hq, hk, ffn, T, B, cfg.get("eps", 1e-6), cfg.get("theta", 10000.0),
                                   DTYPE_CODE[dtype], pp, pi, pt, pg, pr, plg)
     return loss, grads, rows, logits
+
+
+def _dims(cfg):
+    return (cfg["d"], cfg["layers"], cfg["hq"], cfg["hk"], cfg["ffn"], cfg["T"], cfg["B"])
+
+
+def model_acts_count(cfg):
+    return lib().or_model_acts_count(*_dims(cfg))
+
+
+def model_forward(cfg, params, ids, dtype="f32"):
+    """Activation pack (see or_model_acts_count) of the forward pass."""
+    params, pp = _d(params); ids, pi = _i(ids)
+    acts, pa = _out(model_acts_count(cfg))
+    lib().or_model_forward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0), DTYPE_CODE[dtype],
+                           pp, pi, pa)
+    return acts
+
+
+def model_backward(cfg, params, acts, ids, targets, dtype="f32"):
+    """Loss, reference-layout gradients and per-row losses from an
+    activation pack (e.g. the device's stored activations)."""
+    params, pp = _d(params); acts, pa = _d(acts); ids, pi = _i(ids); targets, pt = _i(targets)
+    grads, pg = _out(params.size); rows, pr = _out(cfg["T"] * cfg["B"])
+    loss = lib().or_model_backward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0),
+                                   DTYPE_CODE[dtype], pp, pa, pi, pt, pg, pr)
+    return loss, grads, rows
+
+
+def acts_layout(cfg):
+    """[(name, layer, size)] of the activation pack, in order."""
+    d, L, hq, hk, F, T, B = _dims(cfg)
+    M, J = T * B, d // hq * hk
+    out = []
+    for l in range(L):
+        out += [("x", l, M * d), ("z", l, M * d), ("qr", l, M * d), ("kr", l, M * J), ("v", l, M * J),
+                ("o", l, M * d), ("lse", l, M * hq), ("x1", l, M * d), ("z2", l, M * d), ("g", l, M * F),
+                ("u", l, M * F), ("h", l, M * F)]
+    out += [("xL", -1, M * d), ("hn", -1, M * d), ("logits", -1, M * VOCAB)]
+    return out
 
 
 def model_loss(cfg, params, ids, targets, dtype="f32"):

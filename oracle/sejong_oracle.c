@@ -491,9 +491,204 @@ static double *dup_round(const double *x, long n, int dtype) {
     return y;
 }
 
+/* Activation pack: the forward values every backward rule reads, in the
+ * storage dtype of the step (already rounded), laid out per layer as
+ *   x [M d], z [M d], qr [M d], kr [M J], v [M J], o [M d], lse [M HQ],
+ *   x1 [M d], z2 [M d], g [M F], u [M F], h [M F]
+ * followed by xL [M d], hn [M d], logits [M V].  The device step exports
+ * the same pack, so the backward can be checked conditioned on the device's
+ * stored operands (the reference checks condition the same way). */
+long or_model_acts_count(long d, long layers, long hq, long hk, long ffn, long T, long B) {
+    long M = T * B, J = d / hq * hk;
+    long per = 6 * M * d + 2 * M * J + M * hq + 3 * M * ffn;
+    return layers * per + 2 * M * d + M * OR_VOCAB;
+}
+
 typedef struct {
-    double *x, *z, *q, *k, *v, *qr, *kr, *o, *lse, *x1, *z2, *g, *u, *h;
-} layer_acts;
+    const double *an, *fn, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    long o_an, o_fn, o_wq, o_wk, o_wv, o_wo, o_wg, o_wu, o_wd;
+} lw;
+
+typedef struct {
+    long off_emb, off_final, off_out, total;
+    lw *L;
+    double *C; /* compute copies */
+} plan_t;
+
+static void make_plan(const or_model_cfg *c, const double *params, plan_t *pl) {
+    const long d = c->d, V = OR_VOCAB, J = c->d / c->hq * c->hk, F = c->ffn;
+    long off = 0;
+    pl->off_emb = off; off += V * d;
+    pl->L = (lw *)calloc((size_t)c->layers, sizeof(lw));
+    for (long l = 0; l < c->layers; l++) {
+        lw *y = &pl->L[l];
+        y->o_an = off; off += d;
+        y->o_fn = off; off += d;
+        y->o_wq = off; off += d * d;
+        y->o_wk = off; off += d * J;
+        y->o_wv = off; off += d * J;
+        y->o_wo = off; off += d * d;
+        y->o_wg = off; off += d * F;
+        y->o_wu = off; off += d * F;
+        y->o_wd = off; off += F * d;
+    }
+    pl->off_final = off; off += d;
+    pl->off_out = off; off += d * V;
+    pl->total = off;
+    /* compute copies: bind() casts every master to compute precision
+     * (model lib.rs:214-219); the head keeps the fp32 master (lib.rs:336-340) */
+    pl->C = dup_round(params, off, c->dtype);
+    for (long l = 0; l < c->layers; l++) {
+        lw *y = &pl->L[l];
+        y->an = pl->C + y->o_an; y->fn = pl->C + y->o_fn; y->wq = pl->C + y->o_wq;
+        y->wk = pl->C + y->o_wk; y->wv = pl->C + y->o_wv; y->wo = pl->C + y->o_wo;
+        y->wg = pl->C + y->o_wg; y->wu = pl->C + y->o_wu; y->wd = pl->C + y->o_wd;
+    }
+}
+
+typedef struct {
+    double *x, *z, *qr, *kr, *v, *o, *lse, *x1, *z2, *g, *u, *h;
+} layer_view;
+
+static void view_acts(const or_model_cfg *c, double *acts, layer_view *lv, double **xl, double **hn,
+                      double **logits) {
+    const long M = c->T * c->B, d = c->d, J = c->d / c->hq * c->hk, F = c->ffn;
+    double *p = acts;
+    for (long l = 0; l < c->layers; l++) {
+        layer_view *a = &lv[l];
+        a->x = p; p += M * d;
+        a->z = p; p += M * d;
+        a->qr = p; p += M * d;
+        a->kr = p; p += M * J;
+        a->v = p; p += M * J;
+        a->o = p; p += M * d;
+        a->lse = p; p += M * c->hq;
+        a->x1 = p; p += M * d;
+        a->z2 = p; p += M * d;
+        a->g = p; p += M * F;
+        a->u = p; p += M * F;
+        a->h = p; p += M * F;
+    }
+    *xl = p; p += M * d;
+    *hn = p; p += M * d;
+    *logits = p;
+}
+
+#define ALLOC(n) ((double *)malloc(sizeof(double) * (size_t)(n)))
+
+/* Forward of Block::apply per layer + head, writing the activation pack
+ * (rounded to the storage dtype where the reference kernels store). */
+void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                      double theta, int dtype, const double *params, const int32_t *ids, double *acts) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
+    plan_t pl;
+    make_plan(&cf, params, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, acts, lv, &xl, &hn, &logits);
+    double *q = ALLOC(M * d), *k = ALLOC(M * J), *tmp = ALLOC(M * (d > F ? d : F));
+    const int rd = dtype < 0 ? -1 : 0; /* fp32 storage of LSE / logits */
+    or_embedding_fwd(pl.C + pl.off_emb, ids, lv[0].x, M, d);
+    for (long l = 0; l < layers; l++) {
+        layer_view *a = &lv[l];
+        lw *y = &pl.L[l];
+        double *xnext = (l + 1 < layers) ? lv[l + 1].x : xl;
+        or_rmsnorm_fwd(a->x, y->an, a->z, M, d, eps); or_round(a->z, M * d, dtype);
+        or_matmul(a->z, y->wq, q, M, d, d, 0, 0); or_round(q, M * d, dtype);
+        or_matmul(a->z, y->wk, k, M, J, d, 0, 0); or_round(k, M * J, dtype);
+        or_matmul(a->z, y->wv, a->v, M, J, d, 0, 0); or_round(a->v, M * J, dtype);
+        or_rope(q, a->qr, M, T, hq, Dh, 0, theta, 0); or_round(a->qr, M * d, dtype);
+        or_rope(k, a->kr, M, T, hk, Dh, 0, theta, 0); or_round(a->kr, M * J, dtype);
+        or_attention_fwd(a->qr, a->kr, a->v, a->o, a->lse, B, T, hq, hk, Dh, 0);
+        or_round(a->o, M * d, dtype); or_round(a->lse, M * hq, rd);
+        or_matmul(a->o, y->wo, tmp, M, d, d, 0, 0); or_round(tmp, M * d, dtype);
+        for (long i = 0; i < M * d; i++) a->x1[i] = a->x[i] + tmp[i];
+        or_round(a->x1, M * d, dtype);
+        or_rmsnorm_fwd(a->x1, y->fn, a->z2, M, d, eps); or_round(a->z2, M * d, dtype);
+        or_matmul(a->z2, y->wg, a->g, M, F, d, 0, 0); or_round(a->g, M * F, dtype);
+        or_matmul(a->z2, y->wu, a->u, M, F, d, 0, 0); or_round(a->u, M * F, dtype);
+        or_swiglu_fwd(a->g, a->u, a->h, M * F); or_round(a->h, M * F, dtype);
+        or_matmul(a->h, y->wd, tmp, M, d, F, 0, 0); or_round(tmp, M * d, dtype);
+        for (long i = 0; i < M * d; i++) xnext[i] = a->x1[i] + tmp[i];
+        or_round(xnext, M * d, dtype);
+    }
+    or_rmsnorm_fwd(xl, pl.C + pl.off_final, hn, M, d, eps);
+    or_round(hn, M * d, dtype); /* then cast to F32: exact */
+    or_matmul(hn, params + pl.off_out, logits, M, V, d, 0, 0);
+    or_round(logits, M * V, rd);
+    free(q); free(k); free(tmp); free(lv); free(pl.L); free(pl.C);
+}
+
+/* Backward (graph.rs:567-911 in one block's fixed order) from an
+ * activation pack: CE on the stored logits with the mean seed, head, final
+ * norm, then per layer down / SwiGLU / gate+up / ffn norm / attention
+ * output / attention (+ inverse RoPE) / QKV / attention norm, embedding.
+ * grads: reference layout (FP64).  Returns the mean loss of the logits. */
+double or_model_backward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                         double theta, int dtype, const double *params, const double *acts_in,
+                         const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
+    plan_t pl;
+    make_plan(&cf, params, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, (double *)acts_in, lv, &xl, &hn, &logits);
+    double *lrow = ALLOC(M), *dlog = ALLOC(M * V);
+    /* seed scale/count, graph.rs:539-549 (f32 division in the reference) */
+    double seed = (double)(1.0f / (float)M);
+    or_cross_entropy(logits, targets, lrow, dlog, M, V, seed);
+    double loss = 0.0;
+    for (long i = 0; i < M; i++) loss += lrow[i];
+    loss /= (double)M;
+    if (loss_rows) memcpy(loss_rows, lrow, sizeof(double) * (size_t)M);
+    memset(grads, 0, sizeof(double) * (size_t)pl.total);
+    const double *wout = params + pl.off_out;
+    double *dx = ALLOC(M * d), *dres = ALLOC(M * d);
+    or_matmul(dlog, wout, dx, M, d, V, 0, 1);               /* dh = dlogits W^T */
+    or_matmul(hn, dlog, grads + pl.off_out, d, V, M, 1, 0); /* dW_out = h^T dlogits */
+    or_rmsnorm_bwd(xl, pl.C + pl.off_final, dx, NULL, dres, grads + pl.off_final, M, d, eps);
+    double *dbig = ALLOC(M * F), *dg = ALLOC(M * F), *du = ALLOC(M * F);
+    double *dz = ALLOC(M * d), *dtmp = ALLOC(M * d), *dx1 = ALLOC(M * d), *dO = ALLOC(M * d);
+    double *dq = ALLOC(M * d), *dk = ALLOC(M * J), *dv = ALLOC(M * J);
+    double *dqr = ALLOC(M * d), *dkr = ALLOC(M * J), *dxn = ALLOC(M * d);
+    for (long l = layers - 1; l >= 0; l--) {
+        layer_view *a = &lv[l];
+        lw *y = &pl.L[l];
+        /* x_{l+1} = x1 + down(h): dres flows to x1 and to down's output */
+        or_matmul(dres, y->wd, dbig, M, F, d, 0, 1);              /* dh */
+        or_matmul(a->h, dres, grads + y->o_wd, F, d, M, 1, 0);    /* dW_down */
+        or_swiglu_bwd(a->g, a->u, dbig, dg, du, M * F);
+        or_matmul(dg, y->wg, dz, M, d, F, 0, 1);
+        or_matmul(du, y->wu, dtmp, M, d, F, 0, 1);
+        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
+        or_matmul(a->z2, dg, grads + y->o_wg, d, F, M, 1, 0);
+        or_matmul(a->z2, du, grads + y->o_wu, d, F, M, 1, 0);
+        or_rmsnorm_bwd(a->x1, y->fn, dz, dres, dx1, grads + y->o_fn, M, d, eps);
+        /* x1 = x + attention_output(o) */
+        or_matmul(dx1, y->wo, dO, M, d, d, 0, 1);
+        or_matmul(a->o, dx1, grads + y->o_wo, d, d, M, 1, 0);
+        or_attention_bwd(a->qr, a->kr, a->v, a->o, a->lse, dO, dqr, dkr, dv, NULL, B, T, hq, hk, Dh, 0);
+        or_rope(dqr, dq, M, T, hq, Dh, 0, theta, 1);
+        or_rope(dkr, dk, M, T, hk, Dh, 0, theta, 1);
+        or_matmul(dq, y->wq, dz, M, d, d, 0, 1);
+        or_matmul(dk, y->wk, dtmp, M, d, J, 0, 1);
+        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
+        or_matmul(dv, y->wv, dtmp, M, d, J, 0, 1);
+        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
+        or_matmul(a->z, dq, grads + y->o_wq, d, d, M, 1, 0);
+        or_matmul(a->z, dk, grads + y->o_wk, d, J, M, 1, 0);
+        or_matmul(a->z, dv, grads + y->o_wv, d, J, M, 1, 0);
+        or_rmsnorm_bwd(a->x, y->an, dz, dx1, dxn, grads + y->o_an, M, d, eps);
+        double *t = dres; dres = dxn; dxn = t;
+    }
+    or_embedding_bwd(dres, ids, grads + pl.off_emb, M, d, V);
+    free(lrow); free(dlog); free(dx); free(dres); free(dbig); free(dg); free(du); free(dz); free(dtmp);
+    free(dx1); free(dO); free(dq); free(dk); free(dv); free(dqr); free(dkr); free(dxn);
+    free(lv); free(pl.L); free(pl.C);
+    return loss;
+}
 
 /* One training forward+backward.  params: reference layout (above), fp32
  * master values.  grads: same layout, receives dL/dparam (FP64).  Returns
@@ -504,153 +699,19 @@ double or_model_fwd_bwd(long d, long layers, long hq, long hk, long ffn,
                         const double *params, const int32_t *ids,
                         const int32_t *targets, double *grads,
                         double *loss_rows, double *logits_out) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
-    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
-    const long np = or_param_count_internal(&cf);
-    (void)np;
-    /* compute copies: bind() casts every master to compute precision
-     * (model lib.rs:214-219); the head uses the fp32 master (lib.rs:336-340). */
-    const double *P = params;
-    long off = 0;
-    const double *emb = P + off; off += V * d;
-    typedef struct { const double *an, *fn, *wq, *wk, *wv, *wo, *wg, *wu, *wd; long o_an, o_fn, o_wq, o_wk, o_wv, o_wo, o_wg, o_wu, o_wd; } lw;
-    lw *L = (lw *)calloc((size_t)layers, sizeof(lw));
-    for (long l = 0; l < layers; l++) {
-        L[l].o_an = off; off += d;
-        L[l].o_fn = off; off += d;
-        L[l].o_wq = off; off += d * d;
-        L[l].o_wk = off; off += d * J;
-        L[l].o_wv = off; off += d * J;
-        L[l].o_wo = off; off += d * d;
-        L[l].o_wg = off; off += d * F;
-        L[l].o_wu = off; off += d * F;
-        L[l].o_wd = off; off += F * d;
+    long na = or_model_acts_count(d, layers, hq, hk, ffn, T, B);
+    double *acts = ALLOC(na);
+    or_model_forward(d, layers, hq, hk, ffn, T, B, eps, theta, dtype, params, ids, acts);
+    if (logits_out) {
+        long M = T * B;
+        memcpy(logits_out, acts + na - M * OR_VOCAB, sizeof(double) * (size_t)(M * OR_VOCAB));
     }
-    long o_final = off; off += d;
-    long o_out = off; off += d * V;
-    double *C = dup_round(params, off, dtype); /* compute copies */
-    for (long l = 0; l < layers; l++) {
-        L[l].an = C + L[l].o_an; L[l].fn = C + L[l].o_fn; L[l].wq = C + L[l].o_wq;
-        L[l].wk = C + L[l].o_wk; L[l].wv = C + L[l].o_wv; L[l].wo = C + L[l].o_wo;
-        L[l].wg = C + L[l].o_wg; L[l].wu = C + L[l].o_wu; L[l].wd = C + L[l].o_wd;
-    }
-    const double *embc = C + (emb - P);
-    const double *finalc = C + o_final;
-    const double *wout = P + o_out; /* fp32 master */
-
-#define ALLOC(n) ((double *)malloc(sizeof(double) * (size_t)(n)))
-    layer_acts *A = (layer_acts *)calloc((size_t)layers, sizeof(layer_acts));
-    double *x = ALLOC(M * d);
-    or_embedding_fwd(embc, ids, x, M, d); /* already rounded */
-    double *tmp = ALLOC(M * (d > F ? d : F));
-    for (long l = 0; l < layers; l++) {
-        layer_acts *a = &A[l];
-        a->x = x;
-        a->z = ALLOC(M * d);
-        or_rmsnorm_fwd(x, L[l].an, a->z, M, d, eps);
-        or_round(a->z, M * d, dtype);
-        a->q = ALLOC(M * d); a->k = ALLOC(M * J); a->v = ALLOC(M * J);
-        or_matmul(a->z, L[l].wq, a->q, M, d, d, 0, 0); or_round(a->q, M * d, dtype);
-        or_matmul(a->z, L[l].wk, a->k, M, J, d, 0, 0); or_round(a->k, M * J, dtype);
-        or_matmul(a->z, L[l].wv, a->v, M, J, d, 0, 0); or_round(a->v, M * J, dtype);
-        a->qr = ALLOC(M * d); a->kr = ALLOC(M * J);
-        or_rope(a->q, a->qr, M, T, hq, Dh, 0, theta, 0); or_round(a->qr, M * d, dtype);
-        or_rope(a->k, a->kr, M, T, hk, Dh, 0, theta, 0); or_round(a->kr, M * J, dtype);
-        a->o = ALLOC(M * d); a->lse = ALLOC(M * hq);
-        or_attention_fwd(a->qr, a->kr, a->v, a->o, a->lse, B, T, hq, hk, Dh, 0);
-        or_round(a->o, M * d, dtype);
-        or_round(a->lse, M * hq, dtype < 0 ? -1 : 0);
-        or_matmul(a->o, L[l].wo, tmp, M, d, d, 0, 0); or_round(tmp, M * d, dtype);
-        a->x1 = ALLOC(M * d);
-        for (long i = 0; i < M * d; i++) a->x1[i] = x[i] + tmp[i];
-        or_round(a->x1, M * d, dtype);
-        a->z2 = ALLOC(M * d);
-        or_rmsnorm_fwd(a->x1, L[l].fn, a->z2, M, d, eps); or_round(a->z2, M * d, dtype);
-        a->g = ALLOC(M * F); a->u = ALLOC(M * F); a->h = ALLOC(M * F);
-        or_matmul(a->z2, L[l].wg, a->g, M, F, d, 0, 0); or_round(a->g, M * F, dtype);
-        or_matmul(a->z2, L[l].wu, a->u, M, F, d, 0, 0); or_round(a->u, M * F, dtype);
-        or_swiglu_fwd(a->g, a->u, a->h, M * F); or_round(a->h, M * F, dtype);
-        or_matmul(a->h, L[l].wd, tmp, M, d, F, 0, 0); or_round(tmp, M * d, dtype);
-        double *x2 = ALLOC(M * d);
-        for (long i = 0; i < M * d; i++) x2[i] = a->x1[i] + tmp[i];
-        or_round(x2, M * d, dtype);
-        x = x2;
-    }
-    double *hn = ALLOC(M * d);
-    or_rmsnorm_fwd(x, finalc, hn, M, d, eps);
-    or_round(hn, M * d, dtype); /* then cast to F32: exact */
-    double *logits = ALLOC(M * V);
-    or_matmul(hn, wout, logits, M, V, d, 0, 0);
-    or_round(logits, M * V, dtype < 0 ? -1 : 0);
-    if (logits_out) memcpy(logits_out, logits, sizeof(double) * (size_t)(M * V));
-    double *lrow = ALLOC(M), *dlog = ALLOC(M * V);
-    /* seed scale/count, graph.rs:539-549 (f32 division in the reference) */
-    double seed = (double)(1.0f / (float)M);
-    or_cross_entropy(logits, targets, lrow, dlog, M, V, seed);
-    double loss = 0.0;
-    for (long i = 0; i < M; i++) loss += lrow[i];
-    loss /= (double)M;
-    if (loss_rows) memcpy(loss_rows, lrow, sizeof(double) * (size_t)M);
-
-    /* ------------------------------ backward */
-    memset(grads, 0, sizeof(double) * (size_t)off);
-    double *dx = ALLOC(M * d);
-    or_matmul(dlog, wout, dx, M, d, V, 0, 1);             /* dh = dlogits W^T */
-    or_matmul(hn, dlog, grads + o_out, d, V, M, 1, 0);    /* dW_out = h^T dlogits */
-    double *dres = ALLOC(M * d);
-    or_rmsnorm_bwd(x, finalc, dx, NULL, dres, grads + o_final, M, d, eps);
-    double *dbig = ALLOC(M * F), *dg = ALLOC(M * F), *du = ALLOC(M * F);
-    double *dz = ALLOC(M * d), *dtmp = ALLOC(M * d);
-    double *dq = ALLOC(M * d), *dk = ALLOC(M * J), *dv = ALLOC(M * J);
-    double *dqr = ALLOC(M * d), *dkr = ALLOC(M * J);
-    for (long l = layers - 1; l >= 0; l--) {
-        layer_acts *a = &A[l];
-        /* x2 = x1 + f: dres flows to x1 and to f */
-        or_matmul(dres, L[l].wd, dbig, M, F, d, 0, 1);            /* dh */
-        or_matmul(a->h, dres, grads + L[l].o_wd, F, d, M, 1, 0);  /* dW_down */
-        or_swiglu_bwd(a->g, a->u, dbig, dg, du, M * F);
-        or_matmul(dg, L[l].wg, dz, M, d, F, 0, 1);
-        or_matmul(du, L[l].wu, dtmp, M, d, F, 0, 1);
-        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
-        or_matmul(a->z2, dg, grads + L[l].o_wg, d, F, M, 1, 0);
-        or_matmul(a->z2, du, grads + L[l].o_wu, d, F, M, 1, 0);
-        double *dx1 = ALLOC(M * d);
-        or_rmsnorm_bwd(a->x1, L[l].fn, dz, dres, dx1, grads + L[l].o_fn, M, d, eps);
-        /* x1 = x + attn_out(o) */
-        double *dO = ALLOC(M * d);
-        or_matmul(dx1, L[l].wo, dO, M, d, d, 0, 1);
-        or_matmul(a->o, dx1, grads + L[l].o_wo, d, d, M, 1, 0);
-        or_attention_bwd(a->qr, a->kr, a->v, a->o, a->lse, dO, dqr, dkr, dv, NULL, B, T, hq, hk, Dh, 0);
-        or_rope(dqr, dq, M, T, hq, Dh, 0, theta, 1);
-        or_rope(dkr, dk, M, T, hk, Dh, 0, theta, 1);
-        or_matmul(dq, L[l].wq, dz, M, d, d, 0, 1);
-        or_matmul(dk, L[l].wk, dtmp, M, d, J, 0, 1);
-        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
-        or_matmul(dv, L[l].wv, dtmp, M, d, J, 0, 1);
-        for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
-        or_matmul(a->z, dq, grads + L[l].o_wq, d, d, M, 1, 0);
-        or_matmul(a->z, dk, grads + L[l].o_wk, d, J, M, 1, 0);
-        or_matmul(a->z, dv, grads + L[l].o_wv, d, J, M, 1, 0);
-        double *dxn = ALLOC(M * d);
-        or_rmsnorm_bwd(a->x, L[l].an, dz, dx1, dxn, grads + L[l].o_an, M, d, eps);
-        free(dx1); free(dO);
-        free(dres);
-        dres = dxn;
-    }
-    or_embedding_bwd(dres, ids, grads + (emb - P), M, d, V);
-
-    /* cleanup */
-    for (long l = 0; l < layers; l++) {
-        layer_acts *a = &A[l];
-        free(a->x); free(a->z); free(a->q); free(a->k); free(a->v); free(a->qr); free(a->kr);
-        free(a->o); free(a->lse); free(a->x1); free(a->z2); free(a->g); free(a->u); free(a->h);
-    }
-    free(x); free(A); free(L); free(C); free(tmp); free(hn); free(logits); free(lrow); free(dlog);
-    free(dx); free(dres); free(dbig); free(dg); free(du); free(dz); free(dtmp);
-    free(dq); free(dk); free(dv); free(dqr); free(dkr);
-#undef ALLOC
+    double loss = or_model_backward(d, layers, hq, hk, ffn, T, B, eps, theta, dtype, params, acts, ids,
+                                    targets, grads, loss_rows);
+    free(acts);
     return loss;
 }
+#undef ALLOC
 
 /* Loss only (forward), for finite-difference checks. */
 double or_model_loss(long d, long layers, long hq, long hk, long ffn, long T,

@@ -48,6 +48,15 @@ SIGNATURES = {
     "sj_status_string": (ctypes.c_char_p, [_I]),
     "sj_last_error": (ctypes.c_char_p, []),
     "sj_device_info": (_I, [ctypes.c_char_p, _S, ctypes.POINTER(_I)]),
+    "sj_alloc": (_I, [_S, ctypes.POINTER(_P)]),
+    "sj_free": (_I, [_P]),
+    "sj_upload": (_I, [_P, _P, _S]),
+    "sj_download": (_I, [_P, _P, _S]),
+    "sj_synchronize": (_I, [_P]),
+    "sj_event_create": (_I, [ctypes.POINTER(_P)]),
+    "sj_event_destroy": (_I, [_P]),
+    "sj_event_record": (_I, [_P, _P]),
+    "sj_event_elapsed": (_I, [_P, _P, ctypes.POINTER(_F)]),
     "sj_fill": (_I, [_P, _P, _I, _L, _F]),
     "sj_cast": (_I, [_P, _P, _I, _P, _I, _L]),
     "sj_add": (_I, [_P, _P, _I, _P, _I, _P, _I, _L, _F]),
@@ -97,6 +106,8 @@ SIGNATURES = {
     "sj_model_profile_collect": (_L, [_P]),
     "sj_model_profile_entry": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(_L)]),
+    "sj_model_activation_count": (_L, [_P]),
+    "sj_model_export_activations": (_I, [_P, _P]),
     "sj_model_buffer": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_L)]),
 }
 

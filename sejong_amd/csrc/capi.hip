@@ -49,3 +49,67 @@ extern "C" int sj_device_info(char* arch, size_t arch_len, int* compute_units) {
   if (compute_units) *compute_units = prop.multiProcessorCount;
   return SJ_OK;
 }
+
+// ------------------------------------------------ device memory and events
+// Host utilities mirroring the reference Engine's empty / from_* / to_*
+// transfers (crates/sejong-gpu/src/lib.rs:234-365) for callers that do not
+// bring their own HIP allocator (the test harness and bench.py).
+
+extern "C" int sj_alloc(size_t bytes, void** ptr) {
+  SJ_REQUIRE(ptr, "alloc: null");
+  hipError_t e = hipMalloc(ptr, bytes ? bytes : 256);
+  if (e != hipSuccess) {
+    size_t fr = 0, tot = 0;
+    hipMemGetInfo(&fr, &tot);
+    return sjh::fail(SJ_ERR_CAPACITY, "allocation: required %zu bytes, available %zu bytes", bytes, fr);
+  }
+  return SJ_OK;
+}
+
+extern "C" int sj_free(void* ptr) {
+  if (ptr) SJ_HIP(hipFree(ptr));
+  return SJ_OK;
+}
+
+extern "C" int sj_upload(void* dst, const void* src, size_t bytes) {
+  SJ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return SJ_OK;
+}
+
+extern "C" int sj_download(void* dst, const void* src, size_t bytes) {
+  SJ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return SJ_OK;
+}
+
+extern "C" int sj_synchronize(void* stream) {
+  if (stream)
+    SJ_HIP(hipStreamSynchronize((hipStream_t)stream));
+  else
+    SJ_HIP(hipDeviceSynchronize());
+  return SJ_OK;
+}
+
+extern "C" int sj_event_create(void** ev) {
+  SJ_REQUIRE(ev, "event: null");
+  hipEvent_t e;
+  SJ_HIP(hipEventCreate(&e));
+  *ev = (void*)e;
+  return SJ_OK;
+}
+
+extern "C" int sj_event_destroy(void* ev) {
+  if (ev) SJ_HIP(hipEventDestroy((hipEvent_t)ev));
+  return SJ_OK;
+}
+
+extern "C" int sj_event_record(void* ev, void* stream) {
+  SJ_HIP(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+  return SJ_OK;
+}
+
+extern "C" int sj_event_elapsed(void* start, void* end, float* ms) {
+  SJ_REQUIRE(ms, "event_elapsed: null");
+  SJ_HIP(hipEventSynchronize((hipEvent_t)end));
+  SJ_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+  return SJ_OK;
+}

@@ -636,6 +636,60 @@ extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) 
   return SJ_OK;
 }
 
+// Activation pack in the oracle's order (per layer x, z, q, k, v, o, lse,
+// x1, z2, g, u, h; then x_L, hn, logits), converted to fp32 (exact for bf16).
+extern "C" long sj_model_activation_count(const sj_model* m) {
+  if (!m) return -1;
+  const long M = m->M, d = m->d, J = m->J, F = m->F;
+  return m->L * (6 * M * d + 2 * M * J + M * m->HQ + 3 * M * F) + 2 * M * d + M * m->V;
+}
+
+static int export_matrix(sj_model* m, const void* dev, int dt, long rows, long ld, long col0, long cols,
+                         float* host) {
+  size_t es = dt == SJ_BF16 ? 2 : 4;
+  std::vector<uint8_t> raw((size_t)rows * ld * es);
+  SJ_HIP(hipMemcpy(raw.data(), dev, raw.size(), hipMemcpyDeviceToHost));
+  for (long r = 0; r < rows; r++)
+    for (long c = 0; c < cols; c++) {
+      size_t i = (size_t)r * ld + col0 + c;
+      float v;
+      if (dt == SJ_BF16) {
+        uint32_t b = (uint32_t)((const uint16_t*)raw.data())[i] << 16;
+        memcpy(&v, &b, 4);
+      } else {
+        v = ((const float*)raw.data())[i];
+      }
+      host[(size_t)r * cols + c] = v;
+    }
+  return SJ_OK;
+}
+
+extern "C" int sj_model_export_activations(sj_model* m, float* host) {
+  SJ_REQUIRE(m && host, "export_activations: null");
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
+  const int dt = m->dt;
+  float* p = host;
+  for (long l = 0; l < m->L; l++) {
+    TRY(export_matrix(m, m->x[l], dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->z[l], dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d, J, p)); p += M * J;
+    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d + J, J, p)); p += M * J;
+    TRY(export_matrix(m, m->o[l], dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->lse[l], SJ_F32, M, m->HQ, 0, m->HQ, p)); p += M * m->HQ;
+    TRY(export_matrix(m, m->x1[l], dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->z2[l], dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, m->gg[l], dt, M, F, 0, F, p)); p += M * F;
+    TRY(export_matrix(m, m->uu[l], dt, M, F, 0, F, p)); p += M * F;
+    TRY(export_matrix(m, m->hh[l], dt, M, F, 0, F, p)); p += M * F;
+  }
+  TRY(export_matrix(m, m->x[m->L], dt, M, d, 0, d, p)); p += M * d;
+  TRY(export_matrix(m, m->hn, dt, M, d, 0, d, p)); p += M * d;
+  TRY(export_matrix(m, m->logits, SJ_F32, M, m->Vp, 0, m->V, p));
+  return SJ_OK;
+}
+
 extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* elements) {
   SJ_REQUIRE(m && what && ptr, "buffer: null");
   std::string w(what);

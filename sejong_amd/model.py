@@ -223,6 +223,33 @@ class Model:
         N.api.sj_model_read_loss(self.h, ctypes.byref(loss), ctypes.byref(norm))
         return loss.value, norm.value
 
+    def activation_count(self) -> int:
+        return N.load().sj_model_activation_count(self.h)
+
+    def export_activations(self, out: np.ndarray):
+        assert out.dtype == np.float32 and out.size == self.activation_count()
+        N.api.sj_model_export_activations(self.h, _np_ptr(out))
+
+    def time_steps(self, steps: int, lr: float | None = None) -> float:
+        """Milliseconds for `steps` train steps between two HIP events on the
+        model stream (synchronises)."""
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        N.api.sj_event_create(ctypes.byref(a)); N.api.sj_event_create(ctypes.byref(b))
+        try:
+            s = ctypes.c_void_p(self.stream)
+            N.api.sj_event_record(a, s)
+            for _ in range(steps):
+                self.train_step(lr)
+            N.api.sj_event_record(b, s)
+            ms = ctypes.c_float()
+            N.api.sj_event_elapsed(a, b, ctypes.byref(ms))
+            return ms.value
+        finally:
+            N.api.sj_event_destroy(a); N.api.sj_event_destroy(b)
+
+    def synchronize(self):
+        N.api.sj_synchronize(ctypes.c_void_p(self.stream))
+
     def profile(self, on: bool = True):
         N.api.sj_model_profile(self.h, int(on))
 

@@ -17,3 +17,12 @@ def oracle():
     from oracle import oracle as o
     o.lib()
     return o
+
+
+@pytest.fixture(autouse=True)
+def _release_device_buffers(request):
+    yield
+    if request.node.get_closest_marker("gpu"):
+        from tests import gpu_util
+        if gpu_util.LIVE:
+            gpu_util.release_all()
