@@ -124,6 +124,18 @@ size_t sj_rmsnorm_bwd_workspace_bytes(long rows, long d);
 int sj_rmsnorm_bwd(void *stream, const void *x, int x_dtype, const void *w, int w_dtype,
                    const float *dy, const float *dx_acc, float *dx, float *dw,
                    long rows, long d, float eps, void *workspace, size_t workspace_bytes);
+/* MFMA-layout forms used by the bf16 step (same formulas as above, bf16 x
+ * and w): the forward also writes y transposed, y_t [d][ldt] (the A operand
+ * of the dW GEMMs); the backward (d <= 1024) also writes dx as hi/lo bf16
+ * planes, normal [rows][d] and transposed [d][ldt] (dX / dW GEMM operands
+ * of the layer below).  Workspace: sj_rmsnorm_bwd_p_workspace_bytes. */
+int sj_rmsnorm_fwd_t(void *stream, const uint16_t *x, const uint16_t *w, uint16_t *y, uint16_t *y_t,
+                     long ldt, long rows, long d, float eps);
+size_t sj_rmsnorm_bwd_p_workspace_bytes(long rows, long d);
+int sj_rmsnorm_bwd_p(void *stream, const uint16_t *x, const uint16_t *w, const float *dy,
+                     const float *dx_acc, float *dx, float *dw, uint16_t *dx_hi, uint16_t *dx_lo,
+                     uint16_t *dx_t_hi, uint16_t *dx_t_lo, long ldt, long rows, long d, float eps,
+                     void *workspace, size_t workspace_bytes);
 
 /* ----------------------------------------------------------------- GEMM */
 
@@ -175,6 +187,45 @@ int sj_down_bwd_swiglu(void *stream, const float *dy, long lddy, long M, long D,
                        const void *w_down, long ldw, long F, const void *g, const void *u,
                        long ldgu_in, int gu_dtype, float *dgu, long lddgu);
 
+/* ---------------------------------------------- MFMA-layout GEMM family
+ * The same ops with every operand in the layout the MFMA streams: bf16
+ * planes stored k-contiguous ([rows][K], leading dimension a multiple of 8,
+ * 16-byte aligned).  An fp32 operand is passed as two planes hi = RNE(x),
+ * lo = RNE(x - hi) (products hi*hi + hi*lo + lo*hi); a weight used as B in
+ * the forward is passed transposed ([N][K]).  Tiles are streamed
+ * global -> LDS with global_load_lds_dwordx4, three stages deep.  These are
+ * what the step driver calls; the entries above keep the reference layouts.
+ *
+ * C[M,N] (+)= A B with A planes [M][K] (a_lo nullable) and B planes [N][K]
+ * (b_lo nullable; at most one operand split).  Split-K through `workspace`
+ * (sj_gemm_planes_workspace_bytes) with a fixed-order reduction. */
+size_t sj_gemm_planes_workspace_bytes(long M, long N, long K);
+int sj_gemm_planes(void *stream, long M, long N, long K, const uint16_t *a_hi, const uint16_t *a_lo,
+                   long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, void *c, int c_dtype,
+                   long ldc, int accumulate, void *workspace, size_t workspace_bytes);
+/* Engine::project_qkv (projection_ops.rs:6-43) + fused RoPE with the weights
+ * transposed in one [N+2KV][D] buffer (query rows, then key, then value);
+ * output one [M][N+2KV] bf16 buffer (q | k | v columns). */
+int sj_qkv_fwd_t(void *stream, const uint16_t *x, long ldx, long M, long D, const uint16_t *wqkv_t,
+                 long ldw, long N, long KV, uint16_t *qkv, long ldo, const float *rope_table, long rope_t,
+                 long head_dim);
+/* Engine::gate_up (projection_ops.rs:45-79) with transposed weights
+ * ([F][D] each); h_t (nullable) receives h transposed [F][M] (the A operand
+ * of the down projection's dW). */
+int sj_gate_up_fwd_t(void *stream, const uint16_t *x, long ldx, long M, long D, const uint16_t *wg_t,
+                     const uint16_t *wu_t, long ldw, long F, uint16_t *g, uint16_t *u, uint16_t *h, long ldo,
+                     uint16_t *h_t, long ldht);
+/* matmul + residual add (architecture.rs:226-227, :245) with W^T [N][K]. */
+int sj_linear_residual_fwd_t(void *stream, const uint16_t *x, long ldx, long M, long K, const uint16_t *w_t,
+                             long ldw, long N, const uint16_t *r, long ldr, uint16_t *y, long ldy);
+/* Down-projection dX fused with Engine::swiglu_backward (lib.rs:711-733):
+ * dY as planes [M][D], W_down [F][D] (its natural layout is k-contiguous
+ * here); writes dG|dU as hi/lo planes [M][2F] and transposed [2F][M]. */
+int sj_down_bwd_swiglu_p(void *stream, const uint16_t *dy_hi, const uint16_t *dy_lo, long lddy, long M,
+                         long D, const uint16_t *w_down, long ldw, long F, const uint16_t *g,
+                         const uint16_t *u, long ldgu, uint16_t *dgu_hi, uint16_t *dgu_lo, long lddgu,
+                         uint16_t *dgu_t_hi, uint16_t *dgu_t_lo, long lddgu_t);
+
 /* ------------------------------------------------------------ Attention */
 
 /* Engine::attention_grouped, crates/sejong-gpu/src/hierarchy_ops.rs:10-72
@@ -197,6 +248,21 @@ int sj_attention_bwd(void *stream, const void *q, long ldq, const void *k, long 
                      const float *dout, long lddo, float *dq, long lddq, float *dk, long lddk,
                      float *dv, long lddv, float *delta, int dtype, long batch, long t,
                      long hq, long hk, long head_dim, long window, const float *rope_table);
+/* MFMA-layout forms (bf16, head_dim 64, full causal).  sj_attention_fwd_t
+ * also writes O transposed, o_t [hq*64][ldot].  sj_attention_bwd_p writes
+ * dQ|dK|dV (inverse RoPE applied to dQ, dK) as hi/lo bf16 planes: normal
+ * g [B*T][ldg] with dQ in columns [0, hq*64), dK then dV after it, and
+ * transposed g_t [(hq+2hk)*64][ldgt] -- the operands of the QKV
+ * projection's dX and dW GEMMs.  Both need t % 4 == 0 when batch > 1 and
+ * ldot, ldgt multiples of 4. */
+int sj_attention_fwd_t(void *stream, const uint16_t *q, long ldq, const uint16_t *k, long ldk,
+                       const uint16_t *v, long ldv, uint16_t *o, long ldo, float *lse, uint16_t *o_t,
+                       long ldot, long batch, long t, long hq, long hk, long head_dim);
+int sj_attention_bwd_p(void *stream, const uint16_t *q, long ldq, const uint16_t *k, long ldk,
+                       const uint16_t *v, long ldv, const uint16_t *o, long ldo, const float *lse,
+                       const float *dout, long lddo, float *delta, long batch, long t, long hq, long hk,
+                       long head_dim, const float *rope_table, uint16_t *g_hi, uint16_t *g_lo, long ldg,
+                       uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt);
 
 /* -------------------------------------------------------- Cross entropy */
 

@@ -70,6 +70,12 @@ SIGNATURES = {
     "sj_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _I, _P, _L, _L, _F]),
     "sj_rmsnorm_bwd_workspace_bytes": (_S, [_L, _L]),
     "sj_rmsnorm_bwd": (_I, [_P, _P, _I, _P, _I, _P, _P, _P, _P, _L, _L, _F, _P, _S]),
+    "sj_rmsnorm_fwd_t": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _F]),
+    "sj_rmsnorm_bwd_p_workspace_bytes": (_S, [_L, _L]),
+    "sj_rmsnorm_bwd_p": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _F, _P, _S]),
+    "sj_attention_fwd_t": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _L]),
+    "sj_attention_bwd_p": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P,
+                                _P, _P, _L, _P, _P, _L]),
     "sj_gemm_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_gemm": (_I, [_P, _I, _I, _L, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _I, _P, _S]),
     "sj_qkv_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _I,
@@ -77,6 +83,12 @@ SIGNATURES = {
     "sj_gate_up_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _L, _P, _P, _P, _L, _I]),
     "sj_linear_residual_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _L, _I]),
     "sj_down_bwd_swiglu": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _P, _L, _I, _P, _L]),
+    "sj_gemm_planes_workspace_bytes": (_S, [_L, _L, _L]),
+    "sj_gemm_planes": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
+    "sj_qkv_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _P, _L, _L]),
+    "sj_gate_up_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _P, _P, _L, _P, _L]),
+    "sj_linear_residual_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _L]),
+    "sj_down_bwd_swiglu_p": (_I, [_P, _P, _P, _L, _L, _L, _P, _L, _L, _P, _P, _L, _P, _P, _L, _P, _P, _L]),
     "sj_attention_fwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _I, _L, _L, _L, _L, _L, _L]),
     "sj_attention_bwd": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _L, _P,
                               _I, _L, _L, _L, _L, _L, _L, _P]),

@@ -137,7 +137,36 @@ struct AttnArgs {
   long lddq, lddk, lddv;
   long T, HQ, HK;
   const float* rope;  // inverse-rope table (cos, sin) [T][DH/2] or null
+  // MFMA-layout outputs (null: not written)
+  bf16_t* ot;  // O^T [HQ*DH][ldot] (forward)
+  long ldot;
+  // backward as hi/lo planes instead of fp32: normal [rows][ldp] at the
+  // q / k / v column offsets, transposed [cols][ldtp] at the row offsets
+  bf16_t *pq[2], *pk[2], *pv[2], *tq[2], *tk[2], *tv[2];
+  long ldp, ldtp;
 };
+
+// store one lane's 4 consecutive rows of column `col` of a gradient as
+// hi/lo planes: normal rows (row0+r)*ldp + col, transposed col*ldtp + row0..+3
+__device__ __forceinline__ void store_planes(bf16_t* const* pn, bf16_t* const* pt, long ldp, long ldtp, long row0,
+                                             long col, const float* v, int nvalid) {
+  bf16_t h[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) split_bf(v[r], h[r], l[r]);
+  for (int r = 0; r < nvalid; r++) {
+    pn[0][(row0 + r) * ldp + col] = h[r];
+    pn[1][(row0 + r) * ldp + col] = l[r];
+  }
+  if (nvalid == 4) {
+    *(u32x2*)(pt[0] + col * ldtp + row0) = u32x2{pack2(h[0], h[1]), pack2(h[2], h[3])};
+    *(u32x2*)(pt[1] + col * ldtp + row0) = u32x2{pack2(l[0], l[1]), pack2(l[2], l[3])};
+  } else {
+    for (int r = 0; r < nvalid; r++) {
+      pt[0][col * ldtp + row0 + r] = h[r];
+      pt[1][col * ldtp + row0 + r] = l[r];
+    }
+  }
+}
 
 // ------------------------------------------------------------------ forward
 __global__ __launch_bounds__(256) void k_attn_fwd(AttnArgs a) {
@@ -226,15 +255,31 @@ __global__ __launch_bounds__(256) void k_attn_fwd(AttnArgs a) {
       }
     }
   }
-  // normalise and store
+  // normalise and store (and O^T: this lane's 4 consecutive queries)
+  float on[4][4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     float l = __shfl(lrow, 4 * g + r, 64);
     long qpos = qrow0 + 4 * g + r;
+#pragma unroll
+    for (int d = 0; d < 4; d++) on[d][r] = o[d][r] / l;
     if (qpos < T) {
       bf16_t* orow = a.out + (b * T + qpos) * a.ldo + h * DH;
 #pragma unroll
-      for (int d = 0; d < 4; d++) orow[16 * d + j] = f2bf(o[d][r] / l);
+      for (int d = 0; d < 4; d++) orow[16 * d + j] = f2bf(on[d][r]);
+    }
+  }
+  if (a.ot) {
+    const long q0 = qrow0 + 4 * g;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      bf16_t* dst = a.ot + (h * DH + 16 * d + j) * a.ldot + b * T + q0;
+      if (q0 + 4 <= T) {
+        *(u32x2*)dst = u32x2{pack2(f2bf(on[d][0]), f2bf(on[d][1])), pack2(f2bf(on[d][2]), f2bf(on[d][3]))};
+      } else {
+        for (int r = 0; r < 4; r++)
+          if (q0 + r < T) dst[r] = f2bf(on[d][r]);
+      }
     }
   }
   if (g == 0 && myq < T) a.lse[(b * T + myq) * a.HQ + h] = (mrow + log2f(lrow)) * LN2;
@@ -335,6 +380,7 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
     }
   }
   // epilogue: optional inverse RoPE, pair (2i, 2i+1) in lanes (l, l^1)
+  float outv[4][4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     long qpos = qrow0 + 4 * g + r;
@@ -347,8 +393,16 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
         float2 cs = *(const float2*)(a.rope + 2 * (qpos * (DH / 2) + (col >> 1)));
         x = (j & 1) ? (x * cs.x - y * cs.y) : (x * cs.x + y * cs.y);
       }
-      if (qpos < T) a.dq[(b * T + qpos) * a.lddq + h * DH + col] = x;
+      outv[d][r] = x;
+      if (!a.pq[0] && qpos < T) a.dq[(b * T + qpos) * a.lddq + h * DH + col] = x;
     }
+  }
+  if (a.pq[0]) {
+    const long q0 = qrow0 + 4 * g;
+    const int nv = (int)(T - q0 < 4 ? (T - q0 > 0 ? T - q0 : 0) : 4);
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      store_planes(a.pq, a.tq, a.ldp, a.ldtp, b * T + q0, h * DH + 16 * d + j, outv[d], nv);
   }
 }
 
@@ -443,6 +497,7 @@ __global__ __launch_bounds__(256) void k_attn_dkv(AttnArgs a) {
       }
     }
   }
+  float kout[4][4], vout[4][4];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     long kpos = krow0 + 4 * g + r;
@@ -455,10 +510,21 @@ __global__ __launch_bounds__(256) void k_attn_dkv(AttnArgs a) {
         float2 cs = *(const float2*)(a.rope + 2 * (kpos * (DH / 2) + (col >> 1)));
         x = (j & 1) ? (x * cs.x - y * cs.y) : (x * cs.x + y * cs.y);
       }
-      if (kpos < T) {
+      kout[d][r] = x;
+      vout[d][r] = dv[d][r];
+      if (!a.pk[0] && kpos < T) {
         a.dk[(b * T + kpos) * a.lddk + kvh * DH + col] = x;
         a.dv[(b * T + kpos) * a.lddv + kvh * DH + col] = dv[d][r];
       }
+    }
+  }
+  if (a.pk[0]) {
+    const long k0 = krow0 + 4 * g;
+    const int nv = (int)(T - k0 < 4 ? (T - k0 > 0 ? T - k0 : 0) : 4);
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      store_planes(a.pk, a.tk, a.ldp, a.ldtp, b * T + k0, kvh * DH + 16 * d + j, kout[d], nv);
+      store_planes(a.pv, a.tv, a.ldp, a.ldtp, b * T + k0, kvh * DH + 16 * d + j, vout[d], nv);
     }
   }
 }
@@ -698,5 +764,60 @@ extern "C" int sj_attention_bwd(void* stream, const void* q, long ldq, const voi
     hipLaunchKernelGGL(k_attn_dkv_rows, dim3((unsigned)((krows + 3) / 4)), dim3(256), 0, s, a);
   }
   SJ_LAUNCH_CHECK("hierarchy_attention_backward");
+  return SJ_OK;
+}
+
+namespace sjh {
+int attention_prepare() { return SJ_OK; }
+}  // namespace sjh
+
+extern "C" int sj_attention_fwd_t(void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
+                                  const uint16_t* v, long ldv, uint16_t* o, long ldo, float* lse, uint16_t* o_t,
+                                  long ldot, long batch, long t, long hq, long hk, long head_dim) {
+  SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim == DH && ldot >= batch * t &&
+                 ldot % 4 == 0 && ((uintptr_t)o_t & 7) == 0 && (batch == 1 || t % 4 == 0),
+             "grouped attention (transposed output): head_dim must be %d", DH);
+  SJ_REQUIRE(use_mfma(SJ_BF16, head_dim, 0, t, ldq, ldk, ldv, ldo, q, k, v, o), "grouped attention: alignment");
+  AttnArgs a = {};
+  a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+  a.out = (bf16_t*)o; a.lse = lse; a.T = t; a.HQ = hq; a.HK = hk;
+  a.ot = (bf16_t*)o_t; a.ldot = ldot;
+  hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  SJ_LAUNCH_CHECK("hierarchy_attention_t");
+  return SJ_OK;
+}
+
+extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
+                                  const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
+                                  const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
+                                  long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                                  uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
+  SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim == DH &&
+                 ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ldgt % 4 == 0 && lddo % 4 == 0 && (batch == 1 || t % 4 == 0) &&
+                 ((uintptr_t)dout & 15) == 0 && ((uintptr_t)gt_hi & 7) == 0 && ((uintptr_t)gt_lo & 7) == 0,
+             "grouped attention backward (planes): shape/alignment");
+  SJ_REQUIRE(use_mfma(SJ_BF16, head_dim, 0, t, ldq, ldk, ldv, ldo, q, k, v, o), "grouped attention: alignment");
+  AttnArgs a = {};
+  a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.o = (const bf16_t*)o;
+  a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
+  a.lse = (float*)lse; a.dout = dout; a.lddo = lddo; a.delta = delta;
+  a.T = t; a.HQ = hq; a.HK = hk; a.rope = rope_table;
+  const long N = hq * DH, KV = hk * DH;
+  bf16_t* gh = (bf16_t*)g_hi; bf16_t* gl = (bf16_t*)g_lo;
+  bf16_t* th = (bf16_t*)gt_hi; bf16_t* tl = (bf16_t*)gt_lo;
+  a.pq[0] = gh; a.pq[1] = gl; a.pk[0] = gh + N; a.pk[1] = gl + N; a.pv[0] = gh + N + KV; a.pv[1] = gl + N + KV;
+  a.tq[0] = th; a.tq[1] = tl; a.tk[0] = th; a.tk[1] = tl; a.tv[0] = th; a.tv[1] = tl;
+  // transposed rows: dq rows [0, N), dk rows [N, N+KV), dv rows [N+KV, N+2KV):
+  // the column index passed to store_planes already includes the head
+  // offset, so shift the base by the block of rows instead
+  a.tk[0] = th + N * ldgt; a.tk[1] = tl + N * ldgt; a.tv[0] = th + (N + KV) * ldgt; a.tv[1] = tl + (N + KV) * ldgt;
+  a.ldp = ldg; a.ldtp = ldgt;
+  hipStream_t s = (hipStream_t)stream;
+  unsigned nb = (unsigned)((t + QB - 1) / QB);
+  hipLaunchKernelGGL(k_attn_dq, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_attn_dkv, dim3(nb, (unsigned)hk, (unsigned)batch), dim3(256), 0, s, a);
+  SJ_LAUNCH_CHECK("hierarchy_attention_backward_p");
   return SJ_OK;
 }

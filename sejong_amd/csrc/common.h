@@ -88,6 +88,10 @@ namespace sjh {
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);
+// one-time kernel attribute setup (dynamic LDS limits), outside capture
+int norm_prepare();
+int gemm_fast_prepare();
+int attention_prepare();
 }  // namespace sjh
 
 #define SJ_REQUIRE(cond, ...)                                  \

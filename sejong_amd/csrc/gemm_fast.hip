@@ -1,0 +1,694 @@
+// Streaming bf16 MFMA GEMM for operands laid out for the MFMA (gfx950).
+//
+// Every operand is one or two bf16 planes stored k-contiguous ([rows][K],
+// row stride ld): an fp32 operand arrives pre-split as hi = RNE(x),
+// lo = RNE(x - hi) by its producer, and an operand whose natural layout is
+// row-contiguous (weights in the forward, activations / gradients in dW)
+// arrives as the transposed copy its producer wrote.  The k-loop therefore
+// only moves bytes: tiles go global -> LDS with global_load_lds_dwordx4 (no
+// registers), three stages deep, BK = 64.  Each 16-byte chunk c of LDS row r
+// is stored at position c ^ (r & 7) (the XOR is applied to the global
+// address each lane fetches, since a DMA lane always writes base + 16*lane),
+// so MFMA fragment reads (16 rows x one chunk) hit distinct banks without
+// padding.  Products: hi*hi + hi*lo + lo*hi on v_mfma_f32_16x16x32_bf16.
+//
+// Epilogues fuse the op after each projection of Block::apply (crates/
+// sejong-model/src/architecture.rs:200-247) and write the layouts the next
+// GEMMs read:
+//   QKV + RoPE (bf16), residual add (bf16), gate/up + SwiGLU (g, u, h and
+//   h^T), SwiGLU derivative of the down dX (dG|dU as hi/lo planes, normal
+//   and transposed), plain fp32 / bf16 stores and split-K partials.
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "common.h"
+
+using namespace sj;
+
+namespace sjh {
+int gemm_fast_prepare();
+}
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int BK = 64;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __attribute__((aligned(64))) uint8_t g_zero16[64];  // zero source for masked DMA lanes
+
+enum Epi { E_STORE = 0, E_PARTIAL = 1, E_QKV = 2, E_RESID = 3, E_GATEUP = 4, E_SWIGLU_BWD = 5 };
+
+struct FParams {
+  const bf16_t* a[2];  // A planes (hi, lo), [M][K] k-contiguous
+  long lda;
+  const bf16_t* b[2][3];  // B planes x segments (QKV: Wq^T,Wk^T,Wv^T; gate/up: Wg^T,Wu^T), [N][K]
+  long ldb[3];
+  long seg_n[3];
+  int nseg;
+  long M, N, K;
+  // outputs
+  void* c[4];
+  long ldc[4];
+  int c_bf16, accumulate;
+  // residual / swiglu inputs
+  const bf16_t* r;
+  long ldr;
+  const bf16_t* gin;
+  const bf16_t* uin;
+  long ldgu;
+  long F;
+  // rope
+  const float* rope;
+  long rope_t, head_dim, rope_cols;
+  // split-K
+  long kchunk;
+  float* partial;
+  int xcd_remap;
+};
+
+int g_remap = -1;
+int xcd_remap() {
+  if (g_remap < 0) {
+    const char* e = getenv("SJ_GEMM_XCD_REMAP");
+    g_remap = e ? atoi(e) != 0 : 1;
+  }
+  return g_remap;
+}
+
+// s_waitcnt vmcnt(N) with the other counters unconstrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// One LDS-DMA: each lane's 16 bytes at `src` land in LDS at lds_addr +
+// 16 * lane.  Issued through inline asm so the compiler does not treat later
+// LDS reads as dependent on it (it would otherwise wait for vmcnt(0) before
+// every ds_read and drain the pipeline); completion is tracked explicitly
+// with wait_vm before the barrier that publishes a stage.  M0 written by
+// S_MOV needs one wait state before the LDS-DMA.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ void block_barrier() {
+  // LDS reads of the previous stage are complete, then a plain s_barrier
+  // (no release fence: it would wait for the DMA still in flight)
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ bf16x8 frag(const bf16_t* tile, int row, int chunk) {
+  return __builtin_bit_cast(bf16x8, *(const u32x4*)(tile + row * BK + ((chunk ^ (row & 7)) << 3)));
+}
+
+__device__ __forceinline__ float sigm(float g) { return 1.f / (1.f + expf(-g)); }
+__device__ __forceinline__ float rnd(float v, int bf) { return bf ? round_bf(v) : v; }
+__device__ __forceinline__ void put(void* c, long i, float v, int bf) {
+  if (bf)
+    ((bf16_t*)c)[i] = f2bf(v);
+  else
+    ((float*)c)[i] = v;
+}
+// 4 consecutive bf16 (transposed store of one lane's 4 rows)
+__device__ __forceinline__ void put4(bf16_t* p, const float* v) {
+  *(u32x2*)p = u32x2{pack2(f2bf(v[0]), f2bf(v[1])), pack2(f2bf(v[2]), f2bf(v[3]))};
+}
+__device__ __forceinline__ void put4_split(bf16_t* hi, bf16_t* lo, const float* v) {
+  bf16_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) split_bf(v[i], h[i], l[i]);
+  *(u32x2*)hi = u32x2{pack2(h[0], h[1]), pack2(h[2], h[3])};
+  *(u32x2*)lo = u32x2{pack2(l[0], l[1]), pack2(l[2], l[3])};
+}
+
+// pipeline depth: 4 stages when a stage fits 40 KB, else 3 (LDS <= 160 KB)
+template <int BM, int BN, int PA, int PB, int EPI>
+constexpr int stages() {
+  constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
+  return (BM * PA + BN * PB * NBM) * BK * 2 <= 40 * 1024 ? 4 : 3;
+}
+
+template <int BM, int BN, int PA, int PB, int EPI>
+__global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
+  constexpr bool DUAL = EPI == E_GATEUP;
+  constexpr int NBM = DUAL ? 2 : 1;
+  constexpr int NS = stages<BM, BN, PA, PB, EPI>();
+  constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 16, NB = WN / 16;
+  constexpr int AROWS = BM * PA, BROWS = BN * PB * NBM;
+  constexpr int STAGE_ROWS = AROWS + BROWS;
+  constexpr int BLOCKS8 = STAGE_ROWS / 8;       // DMA instructions per stage
+  constexpr int PER_WAVE = BLOCKS8 / 4;
+  static_assert(BLOCKS8 % 4 == 0, "tile rows must split evenly over the 4 waves");
+  static_assert(PER_WAVE * (NS - 2) < 64, "outstanding DMA beyond vmcnt range");
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS * STAGE_ROWS * BK
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // XCD-aware tile order: workgroups are dispatched round-robin over the 8
+  // XCDs (linear id b -> XCD b % 8), each with its own L2.  Give XCD k a
+  // contiguous run of the row-major tile order so the tiles that share A rows
+  // (and split-K slices) meet in one L2.
+  const unsigned nx = gridDim.x, ny = gridDim.y, nz = gridDim.z;
+  const unsigned nb = nx * ny * nz;
+  const unsigned b = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  unsigned logical = b;
+  if (p.xcd_remap) {
+    const unsigned xcd = b & 7, local = b >> 3, q8 = nb >> 3, r8x = nb & 7;
+    logical = xcd * q8 + (xcd < r8x ? xcd : r8x) + local;
+  }
+  const unsigned tx = logical % nx, ty = (logical / nx) % ny, tz = logical / (nx * ny);
+  const long m0 = (long)ty * BM, n0 = (long)tx * BN;
+  int seg = 0;
+#pragma unroll
+  for (int s = 1; s < 3; s++)
+    if (s < p.nseg && n0 >= p.seg_n[s]) seg = s;
+  const long nl0 = n0 - p.seg_n[seg];
+  const long seg_end = (seg + 1 < p.nseg) ? p.seg_n[seg + 1] : p.N;
+  const long nrows_b = seg_end - p.seg_n[seg];
+
+  long kbeg = 0, kend = p.K;
+  if (EPI == E_PARTIAL) {
+    kbeg = (long)tz * p.kchunk;
+    kend = kbeg + p.kchunk < p.K ? kbeg + p.kchunk : p.K;
+  }
+  const int nk = (int)((kend - kbeg + BK - 1) / BK);
+
+  // Per-lane DMA sources of this wave's PER_WAVE 8-row blocks (fixed over
+  // k): block j covers stage rows 8*(wave + 4j).  Row r of a block holds
+  // 16-byte chunk c = (s & 7) ^ (r & 7) at slot s; since every block starts
+  // at a multiple of 8, r & 7 = s >> 3 and c depends on the lane only.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int sl = lane;
+  const int c8 = (((sl & 7) ^ (sl >> 3)) << 3);
+  const bf16_t* src[PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < PER_WAVE; j++) {
+    const int r8 = (wave_s + 4 * j) * 8;
+    const bf16_t* base;
+    long ld, row, rows;
+    if (r8 < AROWS) {
+      const int pl = r8 / BM;
+      base = pl ? p.a[1] : p.a[0];
+      ld = p.lda;
+      row = m0 + (r8 % BM) + (sl >> 3);
+      rows = p.M;
+    } else {
+      const int rb = r8 - AROWS;
+      const int q = rb / (BN * PB), pl = (rb % (BN * PB)) / BN;
+      const int sg = DUAL ? q : seg;
+      base = pl ? p.b[1][sg] : p.b[0][sg];
+      ld = p.ldb[sg];
+      row = nl0 + (rb % BN) + (sl >> 3);
+      rows = nrows_b;
+    }
+    src[j] = row < rows ? base + row * ld + kbeg + c8 : nullptr;
+  }
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
+  auto issue = [&](int it, int buf) {
+    const long k0 = (long)it * BK;  // relative to kbeg
+    const bool kin = kbeg + k0 + c8 + 8 <= kend;
+    const uint32_t sbase = lds_base + (uint32_t)(buf * STAGE_ROWS * BK * 2) + (uint32_t)(wave_s * 8 * BK * 2);
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; j++) {
+      const void* a = (src[j] && kin) ? (const void*)(src[j] + k0) : (const void*)g_zero16;
+      dma16(a, sbase + (uint32_t)(j * 32 * BK * 2));
+    }
+  };
+
+  f32x4 acc[NBM][MB][NB];
+#pragma unroll
+  for (int q = 0; q < NBM; q++)
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int j = 0; j < NB; j++) acc[q][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, fg = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < NS - 1; s++)
+    if (s < nk) issue(s, s);
+  for (int it = 0; it < nk; it++) {
+    // wait for this wave's DMA of stage `it`; the stages issued after it
+    // (up to NS - 2) may stay in flight
+    const int after = (nk - 1 - it) < (NS - 2) ? (nk - 1 - it) : (NS - 2);
+    if (after >= 2)
+      wait_vm<PER_WAVE * 2>();
+    else if (after == 1)
+      wait_vm<PER_WAVE>();
+    else
+      wait_vm<0>();
+    block_barrier();
+    if (it + NS - 1 < nk) issue(it + NS - 1, (it + NS - 1) % NS);
+    const bf16_t* st = lds + (it % NS) * STAGE_ROWS * BK;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int ch = 4 * h + fg;
+      bf16x8 ah[MB], al[MB];
+#pragma unroll
+      for (int i = 0; i < MB; i++) {
+        const int row = wm * WM + i * 16 + fr;
+        ah[i] = frag(st, row, ch);
+        if constexpr (PA == 2) al[i] = frag(st + BM * BK, row, ch);
+      }
+#pragma unroll
+      for (int q = 0; q < NBM; q++) {
+        const bf16_t* bt = st + (AROWS + q * BN * PB) * BK;
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+          const int row = wn * WN + j * 16 + fr;
+          bf16x8 bh = frag(bt, row, ch);
+          bf16x8 bl;
+          if constexpr (PB == 2) bl = frag(bt + BN * BK, row, ch);
+#pragma unroll
+          for (int i = 0; i < MB; i++) {
+            acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh, acc[q][i][j], 0, 0, 0);
+            if constexpr (PB == 2) acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl, acc[q][i][j], 0, 0, 0);
+            if constexpr (PA == 2) acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh, acc[q][i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // ------------------------------------------------------------ epilogue
+  // acc[q][i][j][r] = C[m0 + wm*WM + 16i + 4*(lane/16) + r][n0 + wn*WN + 16j + lane%16]
+  const int cc = lane & 15;
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const long mb = m0 + wm * WM + i * 16 + fg * 4;  // first of this lane's 4 rows
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const long ncol = n0 + wn * WN + j * 16 + cc;
+      const long nloc = ncol - p.seg_n[seg];
+      const bool colok = ncol < p.N;
+      float v[4] = {acc[0][i][j][0], acc[0][i][j][1], acc[0][i][j][2], acc[0][i][j][3]};
+      if constexpr (EPI == E_SWIGLU_BWD) {
+        // v = dH; dG = dH*u*s*(1+g(1-s)), dU = dH*g*s  (kernels.py:95-101)
+        float dg[4], du[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const long m = mb + r;
+          float g = 0.f, u = 0.f;
+          if (m < p.M && colok) {
+            g = bf2f(p.gin[m * p.ldgu + ncol]);
+            u = bf2f(p.uin[m * p.ldgu + ncol]);
+          }
+          const float s = sigm(g);
+          dg[r] = v[r] * u * s * (1.f + g * (1.f - s));
+          du[r] = v[r] * g * s;
+          if (m < p.M && colok) {
+            bf16_t h, l;
+            split_bf(dg[r], h, l);
+            ((bf16_t*)p.c[0])[m * p.ldc[0] + ncol] = h;
+            ((bf16_t*)p.c[1])[m * p.ldc[0] + ncol] = l;
+            split_bf(du[r], h, l);
+            ((bf16_t*)p.c[0])[m * p.ldc[0] + p.F + ncol] = h;
+            ((bf16_t*)p.c[1])[m * p.ldc[0] + p.F + ncol] = l;
+          }
+        }
+        if (colok && mb + 4 <= p.M) {  // transposed planes [2F][M]
+          put4_split((bf16_t*)p.c[2] + ncol * p.ldc[2] + mb, (bf16_t*)p.c[3] + ncol * p.ldc[2] + mb, dg);
+          put4_split((bf16_t*)p.c[2] + (p.F + ncol) * p.ldc[2] + mb, (bf16_t*)p.c[3] + (p.F + ncol) * p.ldc[2] + mb,
+                     du);
+        } else if (colok) {
+          for (int r = 0; r < 4; r++)
+            if (mb + r < p.M) {
+              bf16_t h, l;
+              split_bf(dg[r], h, l);
+              ((bf16_t*)p.c[2])[ncol * p.ldc[2] + mb + r] = h;
+              ((bf16_t*)p.c[3])[ncol * p.ldc[2] + mb + r] = l;
+              split_bf(du[r], h, l);
+              ((bf16_t*)p.c[2])[(p.F + ncol) * p.ldc[2] + mb + r] = h;
+              ((bf16_t*)p.c[3])[(p.F + ncol) * p.ldc[2] + mb + r] = l;
+            }
+        }
+      } else if constexpr (EPI == E_GATEUP) {
+        float hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const long m = mb + r;
+          const float g = round_bf(v[r]);
+          const float u = round_bf(acc[1][i][j][r]);
+          hv[r] = g * sigm(g) * u;
+          if (m < p.M && colok) {
+            const long idx = m * p.ldc[0] + ncol;
+            ((bf16_t*)p.c[0])[idx] = f2bf(g);
+            ((bf16_t*)p.c[1])[idx] = f2bf(u);
+            ((bf16_t*)p.c[2])[idx] = f2bf(hv[r]);
+          }
+        }
+        if (p.c[3] && colok) {  // h^T [F][M]
+          if (mb + 4 <= p.M)
+            put4((bf16_t*)p.c[3] + ncol * p.ldc[3] + mb, hv);
+          else
+            for (int r = 0; r < 4; r++)
+              if (mb + r < p.M) ((bf16_t*)p.c[3])[ncol * p.ldc[3] + mb + r] = f2bf(hv[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const long m = mb + r;
+          if constexpr (EPI == E_QKV) {
+            const float a = round_bf(v[r]);
+            const float b = __shfl_xor(a, 1, 64);
+            float outv = a;
+            if (ncol < p.rope_cols) {
+              const long pos = m % p.rope_t;
+              const long pair = (nloc % p.head_dim) >> 1;
+              const float2 cs = *(const float2*)(p.rope + 2 * (pos * (p.head_dim >> 1) + pair));
+              outv = (cc & 1) ? (b * cs.y + a * cs.x) : (a * cs.x - b * cs.y);
+            }
+            if (m < p.M && colok) ((bf16_t*)p.c[seg])[m * p.ldc[seg] + nloc] = f2bf(outv);
+          } else if constexpr (EPI == E_RESID) {
+            if (m < p.M && colok) {
+              const float a = round_bf(v[r]);
+              ((bf16_t*)p.c[0])[m * p.ldc[0] + ncol] = f2bf(bf2f(p.r[m * p.ldr + ncol]) + a);
+            }
+          } else if constexpr (EPI == E_PARTIAL) {
+            if (m < p.M && colok) p.partial[((long)tz * p.M + m) * p.N + ncol] = v[r];
+          } else {  // E_STORE
+            if (m < p.M && colok) {
+              const long idx = m * p.ldc[0] + ncol;
+              if (p.c_bf16)
+                ((bf16_t*)p.c[0])[idx] = f2bf(v[r]);
+              else if (p.accumulate)
+                ((float*)p.c[0])[idx] += v[r];
+              else
+                ((float*)p.c[0])[idx] = v[r];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict__ partial, int splits, long M, long N,
+                                                         void* c, long ldc, int c_bf16, int accumulate) {
+  const long total = M * N;
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
+    float s = 0.f;
+    for (int z = 0; z < splits; z++) s += partial[(long)z * total + i];
+    const long m = i / N, n = i - m * N;
+    const long idx = m * ldc + n;
+    if (c_bf16)
+      ((bf16_t*)c)[idx] = f2bf(s);
+    else if (accumulate)
+      ((float*)c)[idx] += s;
+    else
+      ((float*)c)[idx] = s;
+  }
+}
+
+template <int BM, int BN, int PA, int PB, int EPI>
+int launch(hipStream_t s, const FParams& p, int splits) {
+  constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
+  constexpr size_t lds = (size_t)stages<BM, BN, PA, PB, EPI>() * (BM * PA + BN * PB * NBM) * BK * 2;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  auto kern = k_gemm_fast<BM, BN, PA, PB, EPI>;
+  const_cast<FParams&>(p).xcd_remap = xcd_remap();
+  dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
+  hipLaunchKernelGGL(kern, grid, dim3(NT), lds, s, p);
+  return SJ_OK;
+}
+
+int g_cu = 0;
+int cus() {
+  if (!g_cu) {
+    int dev = 0, cu = 256;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      g_cu = cu;
+    else
+      g_cu = 256;
+  }
+  return g_cu;
+}
+
+inline long tiles(long M, long N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+// Tile heuristic: largest tile with >= 1 workgroup per CU, else 64x64.
+// SJ_GEMM_TILE=<bm>x<bn> (64 or 128 each) overrides it, for tuning sweeps.
+void pick(long M, long N, int& bm, int& bn) {
+  static int obm = -1, obn = -1;
+  if (obm < 0) {
+    obm = obn = 0;
+    if (const char* e = getenv("SJ_GEMM_TILE")) {
+      int a = 0, b = 0;
+      if (sscanf(e, "%dx%d", &a, &b) == 2 && (a == 64 || a == 128) && (b == 64 || b == 128)) {
+        obm = a;
+        obn = b;
+      }
+    }
+  }
+  if (obm) {
+    bm = obm;
+    bn = obn;
+    return;
+  }
+  const long cu = cus();
+  if (tiles(M, N, 128, 128) >= cu) { bm = 128; bn = 128; return; }
+  if (tiles(M, N, 128, 64) >= cu) { bm = 128; bn = 64; return; }
+  if (tiles(M, N, 64, 128) >= cu) { bm = 64; bn = 128; return; }
+  bm = 64; bn = 64;
+}
+
+int splits_for(long M, long N, long K, int bm, int bn) {
+  const long t = tiles(M, N, bm, bn), cu = cus();
+  if (t >= cu || K < 1024) return 1;
+  long s = (2 * cu + t - 1) / t;
+  if (s > K / 256) s = K / 256;
+  if (s > 32) s = 32;
+  return s < 1 ? 1 : (int)s;
+}
+
+template <int EPI, int PA, int PB>
+int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
+  if (bm == 128 && bn == 128) return launch<128, 128, PA, PB, EPI>(s, p, splits);
+  if (bm == 128 && bn == 64) return launch<128, 64, PA, PB, EPI>(s, p, splits);
+  if (bm == 64 && bn == 128) return launch<64, 128, PA, PB, EPI>(s, p, splits);
+  return launch<64, 64, PA, PB, EPI>(s, p, splits);
+}
+
+// plane combinations each epilogue is used with: forward epilogues read
+// one-plane operands, the SwiGLU derivative a split dY, plain GEMMs any
+template <int EPI, int PA, int PB>
+constexpr bool plane_combo() {
+  if (EPI == E_STORE || EPI == E_PARTIAL) return !(PA == 2 && PB == 2);
+  if (EPI == E_SWIGLU_BWD) return PA == 2 && PB == 1;
+  return PA == 1 && PB == 1;
+}
+
+template <int EPI>
+int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int bn, int splits) {
+  if constexpr (plane_combo<EPI, 1, 1>())
+    if (pa == 1 && pb == 1) return launch_tile<EPI, 1, 1>(s, p, bm, bn, splits);
+  if constexpr (plane_combo<EPI, 2, 1>())
+    if (pa == 2 && pb == 1) return launch_tile<EPI, 2, 1>(s, p, bm, bn, splits);
+  if constexpr (plane_combo<EPI, 1, 2>())
+    if (pa == 1 && pb == 2) return launch_tile<EPI, 1, 2>(s, p, bm, bn, splits);
+  return sjh::fail(SJ_ERR_UNSUPPORTED, "gemm: planes %d/%d for this epilogue", pa, pb);
+}
+
+bool ok16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
+template <int BM, int BN, int PA, int PB, int EPI>
+int set_attr() {
+  constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
+  constexpr size_t lds = (size_t)stages<BM, BN, PA, PB, EPI>() * (BM * PA + BN * PB * NBM) * BK * 2;
+  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_fast<BM, BN, PA, PB, EPI>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  return e == hipSuccess ? SJ_OK : sjh::hip_check(e, "gemm: LDS attribute");
+}
+template <int EPI, int PA, int PB>
+int set_attrs_tiles() {
+  int s = set_attr<128, 128, PA, PB, EPI>();
+  if (!s) s = set_attr<128, 64, PA, PB, EPI>();
+  if (!s) s = set_attr<64, 128, PA, PB, EPI>();
+  if (!s) s = set_attr<64, 64, PA, PB, EPI>();
+  return s;
+}
+template <int EPI>
+int set_attrs_planes() {
+  int s = SJ_OK;
+  if constexpr (plane_combo<EPI, 1, 1>()) s = set_attrs_tiles<EPI, 1, 1>();
+  if constexpr (plane_combo<EPI, 2, 1>()) if (!s) s = set_attrs_tiles<EPI, 2, 1>();
+  if constexpr (plane_combo<EPI, 1, 2>()) if (!s) s = set_attrs_tiles<EPI, 1, 2>();
+  return s;
+}
+
+}  // namespace
+
+// Raise the dynamic-LDS limit of every instantiation once (outside any
+// stream capture); called by sj_model_create and lazily by the entry points.
+namespace sjh {
+int gemm_fast_prepare() {
+  static int done = 0, status = SJ_OK;
+  if (done) return status;
+  done = 1;
+  status = set_attrs_planes<E_STORE>();
+  if (!status) status = set_attrs_planes<E_PARTIAL>();
+  if (!status) status = set_attrs_planes<E_QKV>();
+  if (!status) status = set_attrs_planes<E_RESID>();
+  if (!status) status = set_attrs_planes<E_GATEUP>();
+  if (!status) status = set_attrs_planes<E_SWIGLU_BWD>();
+  return status;
+}
+}  // namespace sjh
+
+// ================================================================ C ABI
+
+extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
+  int bm, bn;
+  pick(M, N, bm, bn);
+  int s = splits_for(M, N, K, bm, bn);
+  return s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
+}
+
+extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
+                              long lda, const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype,
+                              long ldc, int accumulate, void* workspace, size_t workspace_bytes) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
+                 ldc >= N,
+             "matmul planes: M %ld N %ld K %ld lda %ld ldb %ld (K and ld must be multiples of 8)", M, N, K, lda, ldb);
+  SJ_REQUIRE(a_hi && b_hi && ok16(a_hi) && ok16(b_hi) && (!a_lo || ok16(a_lo)) && (!b_lo || ok16(b_lo)),
+             "matmul planes: 16-byte aligned planes required");
+  SJ_REQUIRE(!(a_lo && b_lo), "matmul planes: at most one split operand");
+  SJ_REQUIRE(c_dtype == SJ_F32 || c_dtype == SJ_BF16, "matmul planes: output dtype %d", c_dtype);
+  SJ_REQUIRE(!(accumulate && c_dtype == SJ_BF16), "matmul: accumulate needs an fp32 output");
+  if (M == 0 || N == 0 || K == 0) return SJ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  FParams p = {};
+  p.a[0] = (const bf16_t*)a_hi; p.a[1] = (const bf16_t*)a_lo; p.lda = lda;
+  p.b[0][0] = (const bf16_t*)b_hi; p.b[1][0] = (const bf16_t*)b_lo; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;
+  p.M = M; p.N = N; p.K = K;
+  p.c[0] = c; p.ldc[0] = ldc; p.c_bf16 = c_dtype == SJ_BF16; p.accumulate = accumulate;
+  const int pa = a_lo ? 2 : 1, pb = b_lo ? 2 : 1;
+  int bm, bn;
+  pick(M, N, bm, bn);
+  int splits = splits_for(M, N, K, bm, bn);
+  if (splits > 1 && workspace && workspace_bytes >= sizeof(float) * (size_t)splits * M * N) {
+    long kchunk = (K + splits - 1) / splits;
+    kchunk = (kchunk + BK - 1) / BK * BK;
+    splits = (int)((K + kchunk - 1) / kchunk);
+    p.kchunk = kchunk;
+    p.partial = (float*)workspace;
+    int st = launch_planes<E_PARTIAL>(s, p, pa, pb, bm, bn, splits);
+    if (st) return st;
+    long total = M * N, blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(k_reduce_partials, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)workspace, splits, M,
+                       N, c, ldc, (int)p.c_bf16, accumulate);
+  } else {
+    int st = launch_planes<E_STORE>(s, p, pa, pb, bm, bn, 1);
+    if (st) return st;
+  }
+  SJ_LAUNCH_CHECK("matmul planes");
+  return SJ_OK;
+}
+
+extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t,
+                            long ldw, long N, long KV, uint16_t* qkv, long ldo, const float* rope_table, long rope_t,
+                            long head_dim) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D &&
+                 ldo >= N + 2 * KV && N % 64 == 0 && KV % 64 == 0 && ok16(x) && ok16(wqkv_t),
+             "project_qkv (transposed weights): shape/alignment");
+  if (rope_table) SJ_REQUIRE(rope_t > 0 && head_dim > 0 && head_dim % 2 == 0 && N % head_dim == 0 && KV % head_dim == 0,
+                             "project_qkv rope: t %ld head_dim %ld", rope_t, head_dim);
+  if (M == 0) return SJ_OK;
+  FParams p = {};
+  p.a[0] = (const bf16_t*)x; p.lda = ldx;
+  const bf16_t* w = (const bf16_t*)wqkv_t;
+  p.b[0][0] = w; p.b[0][1] = w + N * ldw; p.b[0][2] = w + (N + KV) * ldw;
+  p.ldb[0] = p.ldb[1] = p.ldb[2] = ldw;
+  p.seg_n[0] = 0; p.seg_n[1] = N; p.seg_n[2] = N + KV; p.nseg = 3;
+  bf16_t* o = (bf16_t*)qkv;
+  p.c[0] = o; p.c[1] = o + N; p.c[2] = o + N + KV;
+  p.ldc[0] = p.ldc[1] = p.ldc[2] = ldo;
+  p.M = M; p.N = N + 2 * KV; p.K = D; p.c_bf16 = 1;
+  p.rope = rope_table; p.rope_t = rope_t > 0 ? rope_t : 1; p.head_dim = head_dim > 0 ? head_dim : 2;
+  p.rope_cols = rope_table ? N + KV : 0;
+  int bm, bn;
+  pick(M, N + 2 * KV, bm, bn);
+  if (N % bn || KV % bn) bn = 64;
+  int st = launch_planes<E_QKV>((hipStream_t)stream, p, 1, 1, bm, bn, 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("project_qkv");
+  return SJ_OK;
+}
+
+extern "C" int sj_gate_up_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wg_t,
+                                const uint16_t* wu_t, long ldw, long F, uint16_t* g, uint16_t* u, uint16_t* h, long ldo,
+                                uint16_t* h_t, long ldht) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D && ldo >= F &&
+                 ok16(x) && ok16(wg_t) && ok16(wu_t) && (!h_t || (ldht >= M && ldht % 4 == 0)),
+             "gate_up (transposed weights): shape/alignment");
+  if (M == 0) return SJ_OK;
+  FParams p = {};
+  p.a[0] = (const bf16_t*)x; p.lda = ldx;
+  p.b[0][0] = (const bf16_t*)wg_t; p.b[0][1] = (const bf16_t*)wu_t; p.ldb[0] = p.ldb[1] = ldw;
+  p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = g; p.c[1] = u; p.c[2] = h; p.c[3] = h_t; p.ldc[0] = ldo; p.ldc[3] = ldht;
+  p.M = M; p.N = F; p.K = D; p.c_bf16 = 1;
+  int bm, bn;
+  pick(M, F, bm, bn);
+  if (bm == 128 && bn == 128) bn = 64;  // dual accumulators: keep the wave tile at 64x32
+  int st = launch_planes<E_GATEUP>((hipStream_t)stream, p, 1, 1, bm, bn, 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("gate_up");
+  return SJ_OK;
+}
+
+extern "C" int sj_linear_residual_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long K,
+                                        const uint16_t* w_t, long ldw, long N, const uint16_t* r, long ldr,
+                                        uint16_t* y, long ldy) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && K > 0 && K % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= K && ldw >= K && ldr >= N &&
+                 ldy >= N && ok16(x) && ok16(w_t),
+             "linear_residual (transposed weights): shape/alignment");
+  if (M == 0) return SJ_OK;
+  FParams p = {};
+  p.a[0] = (const bf16_t*)x; p.lda = ldx;
+  p.b[0][0] = (const bf16_t*)w_t; p.ldb[0] = ldw; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = y; p.ldc[0] = ldy; p.r = (const bf16_t*)r; p.ldr = ldr;
+  p.M = M; p.N = N; p.K = K; p.c_bf16 = 1;
+  int bm, bn;
+  pick(M, N, bm, bn);
+  int st = launch_planes<E_RESID>((hipStream_t)stream, p, 1, 1, bm, bn, 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("linear_residual");
+  return SJ_OK;
+}
+
+extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const uint16_t* dy_lo, long lddy, long M,
+                                    long D, const uint16_t* w_down, long ldw, long F, const uint16_t* g,
+                                    const uint16_t* u, long ldgu, uint16_t* dgu_hi, uint16_t* dgu_lo, long lddgu,
+                                    uint16_t* dgu_t_hi, uint16_t* dgu_t_lo, long lddgu_t) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && lddy % 8 == 0 && ldw % 8 == 0 && lddy >= D && ldw >= D && ldgu >= F &&
+                 lddgu >= 2 * F && lddgu_t >= M && lddgu_t % 4 == 0 && ok16(dy_hi) && ok16(dy_lo) && ok16(w_down),
+             "swiglu_backward (planes): shape/alignment");
+  if (M == 0) return SJ_OK;
+  FParams p = {};
+  p.a[0] = (const bf16_t*)dy_hi; p.a[1] = (const bf16_t*)dy_lo; p.lda = lddy;
+  p.b[0][0] = (const bf16_t*)w_down; p.ldb[0] = ldw; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = dgu_hi; p.c[1] = dgu_lo; p.c[2] = dgu_t_hi; p.c[3] = dgu_t_lo; p.ldc[0] = lddgu; p.ldc[2] = lddgu_t;
+  p.gin = (const bf16_t*)g; p.uin = (const bf16_t*)u; p.ldgu = ldgu; p.F = F;
+  p.M = M; p.N = F; p.K = D;
+  int bm, bn;
+  pick(M, F, bm, bn);
+  int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("swiglu_backward");
+  return SJ_OK;
+}

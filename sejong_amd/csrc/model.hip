@@ -20,8 +20,17 @@
 //               (gate|up), down [F][d]; output [d][Vp] (Vp = V rounded up
 //               to 8, padding columns stay zero)
 // Exchange with the host uses the reference layout (architecture.rs:63-137).
+//
+// bf16 steps run the MFMA-layout kernels: every GEMM operand is streamed
+// k-contiguous, so the step keeps, next to the bf16 mirror, a transposed
+// mirror of the four projection matrices per layer (forward B operands,
+// rebuilt by one batched transpose after each AdamW update), writes the
+// normalised activations, O and h also transposed ([cols][rows], the A
+// operands of the dW GEMMs), and carries the fp32 gradients dY that feed
+// GEMMs as hi/lo bf16 planes in both orientations (dX and dW operands).
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -47,6 +56,59 @@ struct Layer {
   long an, fn, qkv, wo, gu, down;  // internal offsets
 };
 
+// one matrix of the batched bf16 transpose: src [rows][cols] -> dst [cols][rows]
+struct TJob {
+  long off;    // element offset in both the mirror and the transposed mirror
+  long rows, cols;
+  long tile0;  // first 64x64 tile of this job in the flat tile index
+  long tiles_c;
+};
+
+__global__ __launch_bounds__(256) void k_transpose_jobs(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                        const TJob* __restrict__ jobs, int njobs) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 72];
+  const long b = blockIdx.x;
+  int ji = 0;
+  while (ji + 1 < njobs && b >= jobs[ji + 1].tile0) ji++;
+  const long off = jobs[ji].off, rows = jobs[ji].rows, cols = jobs[ji].cols;
+  const long lt = b - jobs[ji].tile0;
+  const long r0 = (lt / jobs[ji].tiles_c) * 64, c0 = (lt % jobs[ji].tiles_c) * 64;
+  const uint16_t* S = src + off;
+  uint16_t* D = dst + off;
+  const int t = threadIdx.x;
+  const bool vec = (rows & 7) == 0 && (cols & 7) == 0 && r0 + 64 <= rows && c0 + 64 <= cols;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int r = (t >> 3) + 32 * p, c = (t & 7) * 8;
+    uint16_t v[8];
+    if (vec) {
+      sj::u32x4 w = *(const sj::u32x4*)(S + (r0 + r) * cols + c0 + c);
+      for (int i = 0; i < 4; i++) {
+        v[2 * i] = (uint16_t)(w[i] & 0xffffu);
+        v[2 * i + 1] = (uint16_t)(w[i] >> 16);
+      }
+    } else {
+      for (int i = 0; i < 8; i++)
+        v[i] = (r0 + r < rows && c0 + c + i < cols) ? S[(r0 + r) * cols + c0 + c + i] : (uint16_t)0;
+    }
+    for (int i = 0; i < 8; i++) tile[r * 72 + c + i] = v[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int oc = (t >> 3) + 32 * p, orr = (t & 7) * 8;  // source column oc, source rows orr..+7
+    uint16_t v[8];
+    for (int i = 0; i < 8; i++) v[i] = tile[(orr + i) * 72 + oc];
+    if (vec) {
+      *(sj::u32x4*)(D + (c0 + oc) * rows + r0 + orr) =
+          sj::u32x4{sj::pack2(v[0], v[1]), sj::pack2(v[2], v[3]), sj::pack2(v[4], v[5]), sj::pack2(v[6], v[7])};
+    } else if (c0 + oc < cols) {
+      for (int i = 0; i < 8; i++)
+        if (r0 + orr + i < rows) D[(c0 + oc) * rows + r0 + orr + i] = v[i];
+    }
+  }
+}
+
 }  // namespace
 
 struct sj_model {
@@ -65,6 +127,15 @@ struct sj_model {
   long emb, final_norm, out;
   float *w = nullptr, *g = nullptr, *m = nullptr, *v = nullptr;
   uint16_t* mirror = nullptr;  // bf16 compute copy (dt == bf16)
+  // MFMA-layout path (bf16, head_dim 64)
+  bool planes = false;
+  long ldt = 0;                   // leading dimension of [cols][rows] activations (M rounded to 8)
+  uint16_t* mirror_t = nullptr;   // transposed projection matrices, same offsets as the mirror
+  TJob* tjobs = nullptr;
+  int tjob_n = 0;
+  long tjob_tiles = 0;
+  std::vector<uint16_t*> zt, ot, z2t, ht;  // transposed activations per layer
+  uint16_t *rp[4] = {}, *xp[4] = {}, *qp[4] = {}, *gp[4] = {};  // gradient planes: hi, lo, hi^T, lo^T
   // activations
   std::vector<void*> x;  // L+1 residual stream tensors
   std::vector<void*> z, qkv, o, x1, z2, gg, uu, hh;
@@ -211,9 +282,18 @@ const void* wc(const sj_model* m, long off) {
   return m->dt == SJ_BF16 ? (const void*)(m->mirror + off) : (const void*)(m->w + off);
 }
 
+int transpose_mirror(sj_model* m) {
+  if (!m->planes) return SJ_OK;
+  hipLaunchKernelGGL(k_transpose_jobs, dim3((unsigned)m->tjob_tiles), dim3(256), 0, m->stream, m->mirror, m->mirror_t,
+                     m->tjobs, m->tjob_n);
+  SJ_LAUNCH_CHECK("mirror transpose");
+  return SJ_OK;
+}
+
 int refresh_mirror(sj_model* m) {
   if (m->dt != SJ_BF16) return SJ_OK;
-  return sj_cast(m->stream, m->w, SJ_F32, m->mirror, SJ_BF16, m->n_params);
+  TRY(sj_cast(m->stream, m->w, SJ_F32, m->mirror, SJ_BF16, m->n_params));
+  return transpose_mirror(m);
 }
 
 // ---------------------------------------------------------------- forward
@@ -223,7 +303,24 @@ int forward(sj_model* m) {
   const int dt = m->dt;
   const float eps = m->c.norm_epsilon;
   OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, M, d));
-  for (long l = 0; l < m->L; l++) {
+  for (long l = 0; l < m->L && m->planes; l++) {
+    const Layer& y = m->layers[l];
+    uint16_t* qkv = (uint16_t*)m->qkv[l];
+    const uint16_t *W = m->mirror, *WT = m->mirror_t;
+    const uint16_t *x = (const uint16_t*)m->x[l], *x1 = (const uint16_t*)m->x1[l];
+    uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
+    uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], m->ldt, M, d, eps));
+    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, m->rope, m->T, m->Dh));
+    OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l], m->ldt,
+                                           m->B, m->T, m->HQ, m->HK, m->Dh));
+    OP("attn_out_residual", sj_linear_residual_fwd_t(s, o, d, M, d, WT + y.wo, d, d, x, d, (uint16_t*)m->x1[l], d));
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], m->ldt, M, d, eps));
+    OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F, m->ht[l],
+                                          m->ldt));
+    OP("down_residual", sj_linear_residual_fwd_t(s, hh, F, M, F, WT + y.down, F, d, x1, d, (uint16_t*)m->x[l + 1], d));
+  }
+  for (long l = 0; l < m->L && !m->planes; l++) {
     const Layer& y = m->layers[l];
     char* qkv = (char*)m->qkv[l];
     OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[l], dt, wc(m, y.an), dt, m->z[l], M, d, eps));
@@ -262,6 +359,48 @@ int backward(sj_model* m) {
   OP("head_dw", sj_gemm(s, 1, 0, d, m->V, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0, m->ws,
               m->ws_bytes));
   int cur = 0;
+  if (m->planes) {
+    const uint16_t* W = m->mirror;
+    const long ldt = m->ldt;
+    void* ws = m->ws;
+    const size_t wsb = m->ws_bytes;
+    uint16_t **rp = m->rp, **xp = m->xp, **qp = m->qp, **gp = m->gp;
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[m->L], W + m->final_norm, m->dz, nullptr, m->dres[cur],
+                                       G + m->final_norm, rp[0], rp[1], rp[2], rp[3], ldt, M, d, eps, ws, wsb));
+    for (long l = m->L - 1; l >= 0; l--) {
+      const Layer& y = m->layers[l];
+      const uint16_t* qkv = (const uint16_t*)m->qkv[l];
+      // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
+      OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, rp[0], rp[1], d, M, d, W + y.down, d, F, (const uint16_t*)m->gg[l],
+                                                (const uint16_t*)m->uu[l], F, gp[0], gp[1], 2 * F, gp[2], gp[3], ldt));
+      OP("down_dw", sj_gemm_planes(s, F, d, M, m->ht[l], nullptr, ldt, rp[2], rp[3], ldt, G + y.down, SJ_F32, d, 0, ws, wsb));
+      OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, gp[0], gp[1], 2 * F, W + y.gu, nullptr, 2 * F, m->dz, SJ_F32, d, 0, ws,
+                                      wsb));
+      OP("gate_up_dw", sj_gemm_planes(s, d, 2 * F, M, m->z2t[l], nullptr, ldt, gp[2], gp[3], ldt, G + y.gu, SJ_F32, 2 * F, 0,
+                                      ws, wsb));
+      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1, G + y.fn,
+                                         xp[0], xp[1], xp[2], xp[3], ldt, M, d, eps, ws, wsb));
+      // x1 = x + attention_output(o)
+      OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws, wsb));
+      OP("attn_out_dw", sj_gemm_planes(s, d, d, M, m->ot[l], nullptr, ldt, xp[2], xp[3], ldt, G + y.wo, SJ_F32, d, 0, ws,
+                                       wsb));
+      OP("attention_bwd", sj_attention_bwd_p(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
+                                             m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope,
+                                             qp[0], qp[1], NQ, qp[2], qp[3], ldt));
+      OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
+      OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0, ws,
+                                  wsb));
+      if (l > 0)
+        OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[l], W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
+                                           G + y.an, rp[0], rp[1], rp[2], rp[3], ldt, M, d, eps, ws, wsb));
+      else  // nothing below consumes the planes of the embedding gradient
+        OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[l], dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
+                                         eps, ws, wsb));
+      cur ^= 1;
+    }
+    OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, M, d, m->V, nullptr, 0));
+    return SJ_OK;
+  }
   OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->dz, nullptr, m->dres[cur], G + m->final_norm, M,
                      d, eps, m->ws, m->ws_bytes));
   for (long l = m->L - 1; l >= 0; l--) {
@@ -296,6 +435,7 @@ int update(sj_model* m) {
   OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
   OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
                      m->n_nodecay, m->step_dev, m->sumsq, m->status));
+  if (m->planes) OP("mirror_transpose", transpose_mirror(m));
   return SJ_OK;
 }
 
@@ -348,6 +488,15 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   m->NQKV = m->d + 2 * m->J;
   m->dt = c.precision;
   m->esz = m->dt == SJ_BF16 ? 2 : 4;
+  {
+    // MFMA-layout path: bf16, 64-wide heads, 8-aligned widths, d <= 1024
+    // (RMSNorm backward row staging), 4-row aligned sequences
+    const char* env = getenv("SJ_PLANES");
+    const bool want = !(env && env[0] == '0');
+    m->planes = want && m->dt == SJ_BF16 && m->Dh == 64 && m->d % 8 == 0 && m->F % 8 == 0 && m->d <= 1024 &&
+                (m->B == 1 || m->T % 4 == 0);
+    m->ldt = (m->M + 7) / 8 * 8;
+  }
   build_layout(m);
   int st = SJ_OK;
   auto fail_cleanup = [&](int s) {
@@ -367,6 +516,28 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   ALLOC(m->m, P * 4);
   ALLOC(m->v, P * 4);
   if (m->dt == SJ_BF16) ALLOC(m->mirror, P * 2);
+  if (m->planes) {
+    ALLOC(m->mirror_t, P * 2);
+    // transpose jobs: the four projection matrices of every layer
+    std::vector<TJob> jobs;
+    long tiles = 0;
+    auto job = [&](long off, long rows, long cols) {
+      TJob j{off, rows, cols, tiles, (cols + 63) / 64};
+      tiles += ((rows + 63) / 64) * j.tiles_c;
+      jobs.push_back(j);
+    };
+    for (const Layer& y : m->layers) {
+      job(y.qkv, m->d, m->NQKV);
+      job(y.wo, m->d, m->d);
+      job(y.gu, m->d, 2 * m->F);
+      job(y.down, m->F, m->d);
+    }
+    m->tjob_n = (int)jobs.size();
+    m->tjob_tiles = tiles;
+    ALLOC(m->tjobs, sizeof(TJob) * jobs.size());
+    if (hipMemcpy(m->tjobs, jobs.data(), sizeof(TJob) * jobs.size(), hipMemcpyHostToDevice) != hipSuccess)
+      return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: transpose job table"));
+  }
   const size_t M = (size_t)m->M, d = (size_t)m->d, F = (size_t)m->F, es = m->esz;
   m->x.resize(m->L + 1);
   for (long l = 0; l <= m->L; l++) ALLOC(m->x[l], M * d * es);
@@ -382,6 +553,24 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
     ALLOC(m->gg[l], M * F * es);
     ALLOC(m->uu[l], M * F * es);
     ALLOC(m->hh[l], M * F * es);
+  }
+  if (m->planes) {
+    const size_t MT = (size_t)m->ldt;
+    m->zt.resize(m->L); m->ot.resize(m->L); m->z2t.resize(m->L); m->ht.resize(m->L);
+    for (long l = 0; l < m->L; l++) {
+      ALLOC(m->zt[l], d * MT * 2);
+      ALLOC(m->ot[l], d * MT * 2);
+      ALLOC(m->z2t[l], d * MT * 2);
+      ALLOC(m->ht[l], F * MT * 2);
+    }
+    const size_t NQ = (size_t)m->NQKV;
+    for (int i = 0; i < 4; i++) {
+      const size_t rows = i < 2 ? M : MT;
+      ALLOC(m->rp[i], rows * d * 2);
+      ALLOC(m->xp[i], rows * d * 2);
+      ALLOC(m->qp[i], rows * NQ * 2);
+      ALLOC(m->gp[i], rows * 2 * F * 2);
+    }
   }
   ALLOC(m->hn, M * d * es);
   ALLOC(m->logits, M * (size_t)m->Vp * 4);
@@ -416,6 +605,16 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   upd(sj_gemm_workspace_bytes(m->d, m->NQKV, Mi));
   upd(sj_gemm_workspace_bytes(Mi, m->d, 2 * m->F));
   upd(sj_gemm_workspace_bytes(Mi, m->d, m->NQKV));
+  if (m->planes) {
+    upd(sj_rmsnorm_bwd_p_workspace_bytes(Mi, m->d));
+    upd(sj_gemm_planes_workspace_bytes(m->F, m->d, Mi));
+    upd(sj_gemm_planes_workspace_bytes(m->d, 2 * m->F, Mi));
+    upd(sj_gemm_planes_workspace_bytes(m->d, m->d, Mi));
+    upd(sj_gemm_planes_workspace_bytes(m->d, m->NQKV, Mi));
+    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, 2 * m->F));
+    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->d));
+    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->NQKV));
+  }
   m->ws_bytes = ws;
   ALLOC(m->ws, ws);
 #undef ALLOC
@@ -430,6 +629,23 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   for (void* p : {(void*)m->w, (void*)m->g, (void*)m->m, (void*)m->v})
     if (e == hipSuccess) e = hipMemsetAsync(p, 0, P * 4, s);
   if (e == hipSuccess && m->mirror) e = hipMemsetAsync(m->mirror, 0, P * 2, s);
+  if (e == hipSuccess && m->mirror_t) e = hipMemsetAsync(m->mirror_t, 0, P * 2, s);
+  // padding columns [M, ldt) of the transposed activations stay zero
+  for (auto* v : {&m->zt, &m->ot, &m->z2t, &m->ht})
+    for (uint16_t* q : *v)
+      if (e == hipSuccess) e = hipMemsetAsync(q, 0, (size_t)(v == &m->ht ? m->F : m->d) * (size_t)m->ldt * 2, s);
+  for (int i = 2; i < 4 && m->planes; i++) {
+    if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, (size_t)m->ldt * d * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->xp[i], 0, (size_t)m->ldt * d * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->qp[i], 0, (size_t)m->ldt * (size_t)m->NQKV * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->gp[i], 0, (size_t)m->ldt * 2 * F * 2, s);
+  }
+  if (e == hipSuccess && m->planes) {
+    int ps = sjh::norm_prepare();
+    if (!ps) ps = sjh::gemm_fast_prepare();
+    if (!ps) ps = sjh::attention_prepare();
+    if (ps) return fail_cleanup(ps);
+  }
   if (e == hipSuccess) e = hipMemsetAsync(m->status, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, 64, s);
   if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: clear arenas"));
@@ -702,6 +918,7 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   else if (w == "params") { *ptr = m->w; n = m->n_params; }
   else if (w == "grads") { *ptr = m->g; n = m->n_params; }
   else if (w == "mirror") { *ptr = m->mirror; n = m->mirror ? m->n_params : 0; }
+  else if (w == "mirror_t") { *ptr = m->mirror_t; n = m->mirror_t ? m->n_params : 0; }
   else if (w == "workspace") { *ptr = m->ws; n = (long)m->ws_bytes; }
   else if (w == "stream") { *ptr = (void*)m->stream; n = 0; }
   else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);

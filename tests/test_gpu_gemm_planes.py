@@ -1,0 +1,240 @@
+"""Parity of the MFMA-layout GEMM family (bf16 k-contiguous planes, LDS-DMA
+streaming) against the FP64 oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import assert_stored_close, dev, empty, rel, rnd, sync, zeros
+
+pytestmark = pytest.mark.gpu
+
+BF, F32 = 4, 0
+cf = ctypes.c_float
+
+
+@pytest.fixture(scope="module")
+def api():
+    from sejong_amd import _native as N
+    N.load()
+    return N.api
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from sejong_amd import _native as N
+    return N.load()
+
+
+def split(x):
+    """fp32 value -> (hi, lo) bf16 planes as float64 arrays."""
+    x32 = np.asarray(x, np.float32).astype(np.float64)
+    hi = O.round_to(x32, "bf16")
+    return hi, O.round_to(x32 - hi, "bf16")
+
+
+PLANE_CASES = [
+    # M, N, K, split_a, split_b, cdt
+    (4096, 640, 384, False, False, "f32"),
+    (4096, 384, 2048, True, False, "f32"),      # dX with split dY
+    (384, 640, 4096, False, True, "f32"),       # dW with split dY^T, split-K
+    (1000, 200, 200, False, False, "bf16"),     # edges: ragged M/N, K % 64 != 0
+    (384, 384, 4096, True, False, "f32"),
+    (130, 1030, 72, False, True, "f32"),
+]
+
+
+@pytest.mark.parametrize("M,N,K,sa,sb,cdt", PLANE_CASES)
+def test_gemm_planes(api, lib, M, N, K, sa, sb, cdt):
+    rng = np.random.default_rng(M * 7 + N + K)
+    A = rng.normal(0, 1, (M, K)).astype(np.float32).astype(np.float64)
+    B = rng.normal(0, 1, (N, K)).astype(np.float32).astype(np.float64)
+    if not sa:
+        A = O.round_to(A, "bf16")
+    if not sb:
+        B = O.round_to(B, "bf16")
+    ah, al = split(A) if sa else (A, None)
+    bh, bl = split(B) if sb else (B, None)
+    dAh, dBh = dev(ah, "bf16"), dev(bh, "bf16")
+    dAl = dev(al, "bf16") if sa else None
+    dBl = dev(bl, "bf16") if sb else None
+    C = zeros(M * N, cdt)
+    ws = empty(max(lib.sj_gemm_planes_workspace_bytes(M, N, K), 256), "u8")
+    api.sj_gemm_planes(None, M, N, K, dAh.p, dAl.p if sa else None, K, dBh.p, dBl.p if sb else None, K, C.p,
+                       BF if cdt == "bf16" else F32, N, 0, ws.p, ws.nbytes)
+    sync()
+    ref = O.matmul(A, B, 0, 1)
+    if cdt == "bf16":
+        assert_stored_close(C.host(), ref, "bf16", "planes", terms=O.matmul(np.abs(A), np.abs(B), 0, 1))
+    else:
+        r = rel(C.host(), ref)
+        assert r < (1e-5 if not (sa or sb) else 3e-5), r
+
+
+def test_gemm_planes_accumulate(api, lib):
+    rng = np.random.default_rng(11)
+    M, N, K = 384, 384, 4096
+    A = O.round_to(rng.normal(0, 1, (M, K)), "bf16")
+    B = rng.normal(0, 1, (N, K)).astype(np.float32).astype(np.float64)
+    bh, bl = split(B)
+    C0 = rng.normal(0, 1, (M, N)).astype(np.float32).astype(np.float64)
+    C = dev(C0)
+    ws = empty(max(lib.sj_gemm_planes_workspace_bytes(M, N, K), 256), "u8")
+    api.sj_gemm_planes(None, M, N, K, dev(A, "bf16").p, None, K, dev(bh, "bf16").p, dev(bl, "bf16").p, K, C.p, F32, N, 1,
+                       ws.p, ws.nbytes)
+    sync()
+    assert rel(C.host(), (C0 + O.matmul(A, B, 0, 1)).ravel()) < 3e-5
+
+
+def _pairmax(a, M, H, Dh):
+    return np.repeat(np.abs(a).reshape(M, H, Dh // 2, 2).max(-1), 2, -1).reshape(M, H * Dh)
+
+
+def test_qkv_t_rope(api):
+    rng = np.random.default_rng(12)
+    T, B, D, HQ, HK = 256, 2, 384, 6, 2
+    Dh = D // HQ; J = HK * Dh; M = T * B; NQ = D + 2 * J
+    x = O.round_to(rng.normal(0, 1, (M, D)), "bf16")
+    w = O.round_to(rng.normal(0, 0.05, (D, NQ)), "bf16")  # [D][q|k|v]
+    tab = empty(T * Dh)
+    api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
+    out = empty(M * NQ, "bf16")
+    api.sj_qkv_fwd_t(None, dev(x, "bf16").p, D, M, D, dev(w.T.copy(), "bf16").p, D, D, J, out.p, NQ, tab.p, T, Dh)
+    sync()
+    got = out.host().reshape(M, NQ)
+    q = O.round_to(x @ w[:, :D], "bf16"); k = O.round_to(x @ w[:, D:D + J], "bf16")
+    aq = np.abs(x) @ np.abs(w)
+    assert_stored_close(got[:, :D], O.rope(q, T, HQ, Dh), "bf16", "q", ulps=2,
+                        terms=_pairmax(aq[:, :D], M, HQ, Dh) + 2 ** 10 * _pairmax(q, M, HQ, Dh))
+    assert_stored_close(got[:, D:D + J], O.rope(k, T, HK, Dh), "bf16", "k", ulps=2,
+                        terms=_pairmax(aq[:, D:D + J], M, HK, Dh) + 2 ** 10 * _pairmax(k, M, HK, Dh))
+    assert_stored_close(got[:, D + J:], x @ w[:, D + J:], "bf16", "v", terms=aq[:, D + J:])
+
+
+def test_gate_up_t_and_residual_t(api):
+    rng = np.random.default_rng(13)
+    M, D, F = 1024, 384, 1024
+    x = O.round_to(rng.normal(0, 1, (M, D)), "bf16")
+    wg = O.round_to(rng.normal(0, 0.05, (D, F)), "bf16"); wu = O.round_to(rng.normal(0, 0.05, (D, F)), "bf16")
+    G, U, H, HT = (empty(M * F, "bf16") for _ in range(4))
+    api.sj_gate_up_fwd_t(None, dev(x, "bf16").p, D, M, D, dev(wg.T.copy(), "bf16").p, dev(wu.T.copy(), "bf16").p, D, F,
+                         G.p, U.p, H.p, F, HT.p, M)
+    sync()
+    ax = np.abs(x)
+    assert_stored_close(G.host(), x @ wg, "bf16", "g", terms=ax @ np.abs(wg))
+    assert_stored_close(U.host(), x @ wu, "bf16", "u", terms=ax @ np.abs(wu))
+    g, u = G.host().reshape(M, F), U.host().reshape(M, F)
+    h = H.host().reshape(M, F)
+    assert_stored_close(h, O.swiglu_fwd(g, u), "bf16", "h")
+    np.testing.assert_array_equal(HT.host().reshape(F, M), h.T)
+    wd = O.round_to(rng.normal(0, 0.05, (F, D)), "bf16"); r = O.round_to(rng.normal(0, 1, (M, D)), "bf16")
+    Y = empty(M * D, "bf16")
+    api.sj_linear_residual_fwd_t(None, H.p, F, M, F, dev(wd.T.copy(), "bf16").p, F, D, dev(r, "bf16").p, D, Y.p, D)
+    sync()
+    a = h @ wd
+    assert_stored_close(Y.host(), r + a, "bf16", "residual", ulps=2,
+                        terms=np.abs(h) @ np.abs(wd) + 2 ** 9 * np.abs(a))
+
+
+def test_down_bwd_swiglu_planes(api):
+    rng = np.random.default_rng(14)
+    M, D, F = 1024, 384, 1024
+    dy = rng.normal(0, 1e-4, (M, D)).astype(np.float32).astype(np.float64)
+    dh_, dl_ = split(dy)
+    wd = O.round_to(rng.normal(0, 0.05, (F, D)), "bf16")
+    g = O.round_to(rng.normal(0, 1, (M, F)), "bf16"); u = O.round_to(rng.normal(0, 1, (M, F)), "bf16")
+    Hn, Ln, Ht, Lt = (empty(M * 2 * F, "bf16") for _ in range(4))
+    api.sj_down_bwd_swiglu_p(None, dev(dh_, "bf16").p, dev(dl_, "bf16").p, D, M, D, dev(wd, "bf16").p, D, F,
+                             dev(g, "bf16").p, dev(u, "bf16").p, F, Hn.p, Ln.p, 2 * F, Ht.p, Lt.p, M)
+    sync()
+    dg, du = O.swiglu_bwd(g, u, O.matmul(dy, wd, 0, 1))
+    ref = np.concatenate([dg, du], 1)
+    got = (Hn.host() + Ln.host()).reshape(M, 2 * F)
+    assert rel(got, ref) < 3e-5
+    np.testing.assert_array_equal(Ht.host().reshape(2 * F, M), Hn.host().reshape(M, 2 * F).T)
+    np.testing.assert_array_equal(Lt.host().reshape(2 * F, M), Ln.host().reshape(M, 2 * F).T)
+    # hi is the RNE bf16 of the value and lo the rest: |lo| <= half an ulp of hi
+    hi, lo = Hn.host(), Ln.host()
+    assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
+
+
+def _check_planes(hi, lo, x):
+    """hi = RNE_bf16(x), lo = RNE_bf16(x - hi), bit for bit (x: the fp32 values)."""
+    x = np.asarray(x, np.float32).astype(np.float64)
+    h = O.round_to(x, "bf16")
+    np.testing.assert_array_equal(hi, h)
+    np.testing.assert_array_equal(lo, O.round_to(x - h, "bf16"))
+
+
+@pytest.mark.parametrize("R,D,ldt", [(1000, 384, 1000), (33, 1024, 40), (4096, 384, 4096)])
+def test_rmsnorm_t_and_planes(api, lib, R, D, ldt):
+    rng = np.random.default_rng(R + D)
+    x = rnd((R, D), "bf16", rng); w = rnd(D, "bf16", rng)
+    dy = rng.normal(0, 1e-3, (R, D)).astype(np.float32).astype(np.float64)
+    acc = rng.normal(0, 1e-3, (R, D)).astype(np.float32).astype(np.float64)
+    eps = 1e-6
+    X, W = dev(x, "bf16"), dev(w, "bf16")
+    Y, Y2, YT = empty(R * D, "bf16"), empty(R * D, "bf16"), zeros(D * ldt, "bf16")
+    api.sj_rmsnorm_fwd(None, X.p, BF, W.p, BF, Y.p, R, D, cf(eps))
+    api.sj_rmsnorm_fwd_t(None, X.p, W.p, Y2.p, YT.p, ldt, R, D, cf(eps))
+    DX, DW = empty(R * D), empty(D)
+    Hn, Ln = empty(R * D, "bf16"), empty(R * D, "bf16")
+    Ht, Lt = zeros(D * ldt, "bf16"), zeros(D * ldt, "bf16")
+    wsb = empty(max(lib.sj_rmsnorm_bwd_p_workspace_bytes(R, D), 256), "u8")
+    api.sj_rmsnorm_bwd_p(None, X.p, W.p, dev(dy).p, dev(acc).p, DX.p, DW.p, Hn.p, Ln.p, Ht.p, Lt.p, ldt, R, D,
+                         cf(eps), wsb.p, wsb.nbytes)
+    sync()
+    y = Y.host().reshape(R, D)
+    np.testing.assert_array_equal(Y2.host().reshape(R, D), y)   # same formula as the plain entry
+    yt = YT.host().reshape(D, ldt)
+    np.testing.assert_array_equal(yt[:, :R], y.T)
+    assert not yt[:, R:].any()                                   # padding columns untouched
+    dx, dw = O.rmsnorm_bwd(x, w, dy, eps, dx_acc=acc)
+    dxd = DX.host().reshape(R, D)
+    assert rel(dxd, dx) < 1e-5 and rel(DW.host(), dw) < 1e-5
+    hi, lo = Hn.host().reshape(R, D), Ln.host().reshape(R, D)
+    _check_planes(hi, lo, dxd)
+    np.testing.assert_array_equal(Ht.host().reshape(D, ldt)[:, :R], hi.T)
+    np.testing.assert_array_equal(Lt.host().reshape(D, ldt)[:, :R], lo.T)
+
+
+@pytest.mark.parametrize("B,T,HQ,HK", [(2, 256, 6, 2), (1, 200, 4, 4)])
+def test_attention_t_and_planes(api, B, T, HQ, HK):
+    Dh = 64
+    rng = np.random.default_rng(B * T + HQ + 5)
+    M = B * T; N = HQ * Dh; KV = HK * Dh; NG = N + 2 * KV
+    q = rnd((M, N), "bf16", rng); k = rnd((M, KV), "bf16", rng); v = rnd((M, KV), "bf16", rng)
+    do = rng.normal(0, 1e-4, (M, N)).astype(np.float32).astype(np.float64)
+    Q, K, V, DO = dev(q, "bf16"), dev(k, "bf16"), dev(v, "bf16"), dev(do)
+    ldot = (M + 7) // 8 * 8
+    O1, L1, O2, L2, OT = empty(M * N, "bf16"), empty(M * HQ), empty(M * N, "bf16"), empty(M * HQ), zeros(N * ldot, "bf16")
+    print(f"[attention_t] B={B} T={T} HQ={HQ} HK={HK}", flush=True)
+    api.sj_attention_fwd(None, Q.p, N, K.p, KV, V.p, KV, O1.p, N, L1.p, BF, B, T, HQ, HK, Dh, 0)
+    api.sj_attention_fwd_t(None, Q.p, N, K.p, KV, V.p, KV, O2.p, N, L2.p, OT.p, ldot, B, T, HQ, HK, Dh)
+    sync()
+    o = O1.host().reshape(M, N)
+    np.testing.assert_array_equal(O2.host().reshape(M, N), o)
+    np.testing.assert_array_equal(L2.host(), L1.host())
+    np.testing.assert_array_equal(OT.host().reshape(N, ldot)[:, :M], o.T)
+    tab = empty(T * Dh)
+    api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
+    dQ, dK, dV, De = empty(M * N), empty(M * KV), empty(M * KV), empty(M * HQ)
+    api.sj_attention_bwd(None, Q.p, N, K.p, KV, V.p, KV, O1.p, N, L1.p, DO.p, N, dQ.p, N, dK.p, KV, dV.p, KV, De.p,
+                         BF, B, T, HQ, HK, Dh, 0, tab.p)
+    Gh, Gl, Th, Tl, De2 = (empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldot, "bf16"),
+                           zeros(NG * ldot, "bf16"), empty(M * HQ))
+    api.sj_attention_bwd_p(None, Q.p, N, K.p, KV, V.p, KV, O1.p, N, L1.p, DO.p, N, De2.p, B, T, HQ, HK, Dh, tab.p,
+                           Gh.p, Gl.p, NG, Th.p, Tl.p, ldot)
+    sync()
+    np.testing.assert_array_equal(De2.host(), De.host())
+    ref = np.concatenate([dQ.host().reshape(M, N), dK.host().reshape(M, KV), dV.host().reshape(M, KV)], 1)
+    hi, lo = Gh.host().reshape(M, NG), Gl.host().reshape(M, NG)
+    _check_planes(hi, lo, ref)                                   # same arithmetic as the fp32 entry
+    np.testing.assert_array_equal(Th.host().reshape(NG, ldot)[:, :M], hi.T)
+    np.testing.assert_array_equal(Tl.host().reshape(NG, ldot)[:, :M], lo.T)
+    # and the oracle
+    dq, dk, dv, _ = O.attention_bwd(q, k, v, o, L1.host(), do, B, T, HQ, HK, Dh, 0)
+    dq = O.rope(dq, T, HQ, Dh, inverse=True); dk = O.rope(dk, T, HK, Dh, inverse=True)
+    assert rel((hi + lo)[:, :N], dq) < 1e-4 and rel((hi + lo)[:, N:N + KV], dk) < 1e-4
+    assert rel((hi + lo)[:, N + KV:], dv) < 1e-4
