@@ -30,6 +30,12 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
+# single-kernel ops and the kernel each one launches (rocprofv3 names)
+OP_KERNEL = {"attention_bwd_dkv": "k_attn_dkv", "attention_bwd_dq": "k_attn_dq", "attention_fwd": "k_attn_fwd",
+             "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd",
+             "cross_entropy": "k_cross_entropy"}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -40,6 +46,7 @@ def op_work(op: str, mc, tc):
     d, F, V = mc.width, mc.ffn_width, 257
     J = mc.head_dim * mc.kv
     es = 2 if mc.precision == "bf16" else 4
+    planes = mc.precision == "bf16" and mc.head_dim == 64 and os.environ.get("SJ_PLANES", "1") != "0"
     attn_fwd = tc.batch * mc.heads * 4 * mc.head_dim * tc.sequence * (tc.sequence + 1) / 2
     P = sum(math.prod(s) for _, s, _ in __import__("sejong_amd.model", fromlist=["layout"]).layout(mc))
     table = {
@@ -48,6 +55,11 @@ def op_work(op: str, mc, tc):
         "qkv_dw": ("flop", 2 * M * d * (d + 2 * J)),
         "attention_fwd": ("flop", attn_fwd),
         "attention_bwd": ("flop", 2.5 * attn_fwd),
+        # split kernels: dQ recomputes S and dP and forms dQ (3 products of
+        # the forward's size / 2); dK/dV recomputes S and dP, forms dV, dK (4)
+        "attention_bwd_dq": ("flop", 1.5 * attn_fwd),
+        "attention_bwd_dkv": ("flop", 2.0 * attn_fwd),
+        "mirror_transpose": ("byte", 2 * 2 * mc.layers * (d * (d + 2 * J) + d * d + 3 * d * F)),
         "attn_out_residual": ("flop", 2 * M * d * d),
         "attn_out_dx": ("flop", 2 * M * d * d),
         "attn_out_dw": ("flop", 2 * M * d * d),
@@ -60,8 +72,10 @@ def op_work(op: str, mc, tc):
         "head_fwd": ("flop", 2 * M * d * V),
         "head_dx": ("flop", 2 * M * d * V),
         "head_dw": ("flop", 2 * M * d * V),
-        "rmsnorm": ("byte", 2 * M * d * es + d * es),
-        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4) + d * es),
+        # plane path: y and y^T written; backward also writes hi/lo planes
+        # in both orientations (4 bf16 copies of dx)
+        "rmsnorm": ("byte", (3 if planes else 2) * M * d * es + d * es),
+        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es),
         "cross_entropy": ("byte", 2 * M * V * 4 + M * 8),
         "loss_summary": ("byte", M * 4),
         "embedding": ("byte", M * 4 + 2 * M * d * es),
@@ -97,6 +111,25 @@ def cpu_baseline(mc, tc, sample_batch: int):
                       f"(FP64 oracle fwd+bwd+AdamW, {dt:.2f} s)", "ms_per_step_sample": dt * 1e3}
 
 
+def copy_probe(mib: int):
+    """A plain copy of known size (reads and writes mib MiB) for scaling the
+    FETCH_SIZE / WRITE_SIZE counters: one k_cast dispatch per repeat."""
+    import ctypes
+    from sejong_amd import _native as N
+    N.load()
+    n = mib * (1 << 20) // 4
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    N.api.sj_alloc(n * 4, ctypes.byref(a)); N.api.sj_alloc(n * 4, ctypes.byref(b))
+    N.api.sj_fill(None, a, 0, n, ctypes.c_float(1.0))
+    N.api.sj_synchronize(None)
+    for _ in range(3):
+        N.api.sj_cast(None, a, 0, b, 0, n)
+    N.api.sj_synchronize(None)
+    N.api.sj_free(a); N.api.sj_free(b)
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "dispatches": 3}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,12 +140,20 @@ def main():
     ap.add_argument("--cpu-sample-batch", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
+    ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a plain fp32 copy kernel (sj_cast) over this many MiB, 3 times, and exit: "
+                         "the calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
               "(each box has one GPU; sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
 
     import numpy as np
     from sejong_amd.model import Model, byte_batch, config, init_params
@@ -141,11 +182,15 @@ def main():
     log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events {gpu_ms / args.steps:.4f}, "
         f"wall {wall * 1e3 / args.steps:.4f}); loss {loss0:.5f} -> {loss:.5f}, |g| {gnorm:.4f}")
 
-    # live per-op timing: one eager step with a HIP event pair around every op
+    # live per-op timing: eager steps with a HIP event pair around every op
+    # on the model stream, averaged over the profiled steps
     model.profile(True)
-    model.train_step(tc.learning_rate)
+    for _ in range(max(1, args.profile_steps)):
+        model.train_step(tc.learning_rate)
     prof = model.profile_collect()
     model.profile(False)
+    nprof = max(1, args.profile_steps)
+    prof = {op: (ms / nprof, calls // nprof) for op, (ms, calls) in prof.items()}
     prof_total = sum(ms for ms, _ in prof.values())
     rows = []
     for op, (ms, calls) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
@@ -161,16 +206,16 @@ def main():
             f"{rate:9.2f} {'TFLOP/s' if kind == 'flop' else 'GB/s'}  ({100 * rate / peak:.1f}% of peak)")
     dom = rows[0]
     kind, work = op_work(dom["op"], mc, tc)
+    # HBM bytes per dispatch of the dominant kernel, from the committed
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE runs (copy-kernel calibrated)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        try:
-            traffic = json.load(open(tpath)).get(args.config, {}).get(dom["op"])
-        except Exception:
-            traffic = None
+    kname = OP_KERNEL.get(dom["op"])
+    if kname and os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get(args.config, {}).get("bytes_per_dispatch", {}).get(kname)
     roofline = {"bound": dom["bound"], "achieved": dom["achieved"],
                 "peak": PEAK_BF16_TFLOPS if kind == "flop" else PEAK_HBM_GBS, "unit": dom["unit"],
-                "frac": dom["frac"], "traffic": traffic, "kernel": dom["op"],
+                "frac": dom["frac"], "traffic": traffic, "op": dom["op"], "kernel": kname or dom["op"],
                 "work_per_launch": work, "avg_launch_us": dom["avg_us"]}
     # whole-step MFMA fraction (algorithmic GEMM + attention flops / step time)
     step_flops = sum(op_work(op, mc, tc)[1] * calls for op, (_, calls) in prof.items()

@@ -789,11 +789,12 @@ extern "C" int sj_attention_fwd_t(void* stream, const uint16_t* q, long ldq, con
   return SJ_OK;
 }
 
-extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
-                                  const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
-                                  const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
-                                  long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                                  uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
+// parts: 1 = dQ kernel (also writes Delta), 2 = dK/dV kernel (reads Delta), 3 = both
+int sjh::attention_bwd_p_parts(int parts, void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
+                               const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
+                               const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
+                               long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                               uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
   SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim == DH &&
                  ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ldgt % 4 == 0 && lddo % 4 == 0 && (batch == 1 || t % 4 == 0) &&
                  ((uintptr_t)dout & 15) == 0 && ((uintptr_t)gt_hi & 7) == 0 && ((uintptr_t)gt_lo & 7) == 0,
@@ -816,8 +817,17 @@ extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, con
   a.ldp = ldg; a.ldtp = ldgt;
   hipStream_t s = (hipStream_t)stream;
   unsigned nb = (unsigned)((t + QB - 1) / QB);
-  hipLaunchKernelGGL(k_attn_dq, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(k_attn_dkv, dim3(nb, (unsigned)hk, (unsigned)batch), dim3(256), 0, s, a);
+  if (parts & 1) hipLaunchKernelGGL(k_attn_dq, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a);
+  if (parts & 2) hipLaunchKernelGGL(k_attn_dkv, dim3(nb, (unsigned)hk, (unsigned)batch), dim3(256), 0, s, a);
   SJ_LAUNCH_CHECK("hierarchy_attention_backward_p");
   return SJ_OK;
+}
+
+extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
+                                  const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
+                                  const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
+                                  long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                                  uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
+  return sjh::attention_bwd_p_parts(3, stream, q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, delta, batch, t, hq,
+                                    hk, head_dim, rope_table, g_hi, g_lo, ldg, gt_hi, gt_lo, ldgt);
 }

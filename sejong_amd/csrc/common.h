@@ -92,6 +92,12 @@ int hip_check(hipError_t e, const char* what);
 int norm_prepare();
 int gemm_fast_prepare();
 int attention_prepare();
+// sj_attention_bwd_p split so a caller can time its two kernels apart
+int attention_bwd_p_parts(int parts, void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
+                          const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
+                          const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
+                          long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                          uint16_t* gt_hi, uint16_t* gt_lo, long ldgt);
 }  // namespace sjh
 
 #define SJ_REQUIRE(cond, ...)                                  \

@@ -384,9 +384,11 @@ int backward(sj_model* m) {
       OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws, wsb));
       OP("attn_out_dw", sj_gemm_planes(s, d, d, M, m->ot[l], nullptr, ldt, xp[2], xp[3], ldt, G + y.wo, SJ_F32, d, 0, ws,
                                        wsb));
-      OP("attention_bwd", sj_attention_bwd_p(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
-                                             m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope,
-                                             qp[0], qp[1], NQ, qp[2], qp[3], ldt));
+      for (int part = 1; part <= 2; part++)
+        OP(part == 1 ? "attention_bwd_dq" : "attention_bwd_dkv",
+           sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
+                                      m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0],
+                                      qp[1], NQ, qp[2], qp[3], ldt));
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
       OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0, ws,
                                   wsb));
