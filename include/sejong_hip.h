@@ -264,6 +264,96 @@ int sj_attention_bwd_p(void *stream, const uint16_t *q, long ldq, const uint16_t
                        long head_dim, const float *rope_table, uint16_t *g_hi, uint16_t *g_lo, long ldg,
                        uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt);
 
+/* ---------------------------------------------------- Mixture of experts
+ * The MoE FFN of Block::apply (crates/sejong-model/src/architecture.rs:
+ * 229-242) without host synchronisation: experts <= 32, top_k <= 8.  The
+ * packed layout groups the routed slots by expert (ascending slot order
+ * inside an expert, the reference's pack order) in segments starting at
+ * multiples of 64 rows: segment e is rows [offsets[e], offsets[e+1]) of a
+ * [capacity][*] matrix, of which the first counts[e] are real and the rest
+ * zero padding.  pslot[row] = routed slot (token*top_k + k) or -1;
+ * ppos[slot] = its packed row. */
+
+/* Engine::route_topk, crates/sejong-gpu/src/hierarchy_ops.rs:280-295 (kernel
+ * hierarchy_route_topk, hierarchy.py:175-191): softmax of each row's
+ * logits (fp32 math), top_k rounds of argmax with the lowest index on ties,
+ * weight = the full-softmax probability.  ids i32 and weights fp32 [rows][top_k]. */
+int sj_route_topk(void *stream, const void *logits, int dtype, long rows, long experts, long top_k,
+                  int32_t *ids, float *weights);
+/* Router projection (Linear::apply, architecture.rs:230: logits = z W_router
+ * stored in z's dtype, bf16) fused with sj_route_topk; w_router [d][experts]. */
+int sj_router_topk(void *stream, const uint16_t *z, long ldz, const uint16_t *w_router, long d, long rows,
+                   long experts, long top_k, uint16_t *logits, int32_t *ids, float *weights);
+/* Engine::route_topk_backward, hierarchy_ops.rs:297-329 (hierarchy.py:194-209):
+ * dx = p * (dy_selected - sum_k w_k dy_k), fp32 [rows][experts]. */
+int sj_route_topk_bwd(void *stream, const void *logits, int dtype, const int32_t *ids, const float *weights,
+                      const float *dy, float *dx, long rows, long experts, long top_k);
+/* Engine::expert_routes, hierarchy_ops.rs:331-378 (hierarchy_route_pack,
+ * hierarchy.py:212-225) with the counts kept on the device: tokens/slots
+ * (nullable) in the reference's [experts][rows*top_k] layout, counts
+ * [experts], offsets [experts+1], pslot [capacity], ppos [rows*top_k].
+ * capacity >= sj_route_pack_capacity(rows*top_k, experts). */
+long sj_route_pack_capacity(long slots, long experts);
+int sj_route_pack(void *stream, const int32_t *ids, long rows, long top_k, long experts, int32_t *tokens,
+                  int32_t *slots, int32_t *counts, int32_t *offsets, int32_t *pslot, int32_t *ppos,
+                  long capacity);
+/* Engine::gather (crates/sejong-gpu/src/lib.rs:1010-1028) of every
+ * expert's input rows in one pass: y [capacity][d] (bf16, zero padding
+ * rows) and y_t (nullable) = y transposed [d][ldt] (the expert dW operand).
+ * d <= 1024. */
+int sj_moe_gather(void *stream, const uint16_t *x, long ldx, long d, const int32_t *pslot, long top_k,
+                  long capacity, uint16_t *y, uint16_t *y_t, long ldt);
+/* Engine::expert_combine, hierarchy_ops.rs:380-414 (hierarchy.py:228-235):
+ * u[t] = bf16(sum over the token's experts, ascending, of w*y) with each
+ * product rounded to fp32 before its add, then out = bf16(residual + u)
+ * (the residual add of architecture.rs:245; residual nullable). */
+int sj_moe_combine(void *stream, const uint16_t *yp, long ldy, long d, const int32_t *ids, const int32_t *ppos,
+                   const float *weights, long rows, long top_k, const uint16_t *residual, long ldr,
+                   uint16_t *out, long ldo);
+/* Engine::expert_combine_backward, hierarchy_ops.rs:416-454
+ * (hierarchy.py:238-251): dx[row] = dy[token] * w[slot] as hi/lo planes,
+ * normal [capacity][d] and transposed [d][ldt], and dweights[slot] =
+ * sum_c y[row][c] dy[token][c].  d <= 1024. */
+int sj_moe_combine_bwd(void *stream, const uint16_t *yp, long ldy, long d, const int32_t *pslot,
+                       const float *weights, long top_k, long capacity, const float *dy, long lddy,
+                       uint16_t *dx_hi, uint16_t *dx_lo, uint16_t *dx_t_hi, uint16_t *dx_t_lo, long ldt,
+                       float *dweights);
+/* Engine::gather_backward (lib.rs:1030-1050) summed per token without
+ * atomics (expert order ascending), fused with Engine::route_topk_backward
+ * (when logits is non-null: dlogits fp32 [rows][experts]) and the router's
+ * dX (dlogits W_router^T, when w_router is non-null) and the tape's
+ * accumulation into dz_acc (nullable): dz = dz_acc + sum + router dX. */
+int sj_moe_gather_bwd(void *stream, const float *dxp, long lddx, long d, const int32_t *ids, const int32_t *ppos,
+                      const float *weights, const uint16_t *logits, const float *dweights,
+                      const uint16_t *w_router, long rows, long top_k, long experts, const float *dz_acc,
+                      long ldacc, float *dz, long lddz, float *dlogits);
+/* Grouped expert GEMMs: the per-expert loop of architecture.rs:233-239 and
+ * its backward (graph.rs:829-851) in one launch each, expert e's weights at
+ * base + e*w_stride.  gate/up with transposed weights [F][D] per expert
+ * (SwiGLU epilogue, h_t [F][ldht] nullable); down with W_down^T [D][F]
+ * (bf16 output); down dX fused with the SwiGLU derivative (dY planes, W_down
+ * [F][D], dG|dU planes normal and transposed); a row-grouped dX GEMM
+ * C[capacity][N] = A B_e with B_e [N][K]; and per-expert dW
+ * C_e[M][N] = A^T B over the expert's rows (A [M][capacity] bf16, B planes
+ * [N][capacity]), C_e at c + e*c_stride. */
+int sj_moe_gate_up_fwd(void *stream, const int32_t *offsets, long experts, long capacity, const uint16_t *x,
+                       long ldx, long D, const uint16_t *wg_t, const uint16_t *wu_t, long ldw, long w_stride,
+                       long F, uint16_t *g, uint16_t *u, uint16_t *h, long ldo, uint16_t *h_t, long ldht);
+int sj_moe_down_fwd(void *stream, const int32_t *offsets, long experts, long capacity, const uint16_t *h,
+                    long ldh, long F, const uint16_t *wd_t, long ldw, long w_stride, long D, uint16_t *y,
+                    long ldy);
+int sj_moe_down_bwd_swiglu_p(void *stream, const int32_t *offsets, long experts, long capacity,
+                             const uint16_t *dy_hi, const uint16_t *dy_lo, long lddy, long D,
+                             const uint16_t *w_down, long ldw, long w_stride, long F, const uint16_t *g,
+                             const uint16_t *u, long ldgu, uint16_t *dgu_hi, uint16_t *dgu_lo, long lddgu,
+                             uint16_t *dgu_t_hi, uint16_t *dgu_t_lo, long ldt);
+int sj_moe_gemm_rows(void *stream, const int32_t *offsets, long experts, long capacity, long N, long K,
+                     const uint16_t *a_hi, const uint16_t *a_lo, long lda, const uint16_t *b, long ldb,
+                     long b_stride, float *c, long ldc, int accumulate);
+int sj_moe_gemm_dw(void *stream, const int32_t *offsets, long experts, long capacity, long M, long N,
+                   const uint16_t *a, long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, float *c,
+                   long ldc, long c_stride);
+
 /* -------------------------------------------------------- Cross entropy */
 
 /* Engine::cross_entropy + cross_entropy_backward, lib.rs:881-913 (kernels

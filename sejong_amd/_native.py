@@ -73,6 +73,21 @@ SIGNATURES = {
     "sj_rmsnorm_fwd_t": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _F]),
     "sj_rmsnorm_bwd_p_workspace_bytes": (_S, [_L, _L]),
     "sj_rmsnorm_bwd_p": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _F, _P, _S]),
+    "sj_route_topk": (_I, [_P, _P, _I, _L, _L, _L, _P, _P]),
+    "sj_router_topk": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _P, _P, _P]),
+    "sj_route_topk_bwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _L, _L, _L]),
+    "sj_route_pack_capacity": (_L, [_L, _L]),
+    "sj_route_pack": (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _P, _L]),
+    "sj_moe_gather": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _L]),
+    "sj_moe_combine": (_I, [_P, _P, _L, _L, _P, _P, _P, _L, _L, _P, _L, _P, _L]),
+    "sj_moe_combine_bwd": (_I, [_P, _P, _L, _L, _P, _P, _L, _L, _P, _L, _P, _P, _P, _P, _L, _P]),
+    "sj_moe_gather_bwd": (_I, [_P, _P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _L, _P, _L, _P, _L, _P]),
+    "sj_moe_gate_up_fwd": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _L, _L, _L, _P, _P, _P, _L, _P, _L]),
+    "sj_moe_down_fwd": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _L, _L, _L, _P, _L]),
+    "sj_moe_down_bwd_swiglu_p": (_I, [_P, _P, _L, _L, _P, _P, _L, _L, _P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P,
+                                      _P, _L]),
+    "sj_moe_gemm_rows": (_I, [_P, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _L, _P, _L, _I]),
+    "sj_moe_gemm_dw": (_I, [_P, _P, _L, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _L]),
     "sj_attention_fwd_t": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _L]),
     "sj_attention_bwd_p": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P,
                                 _P, _P, _L, _P, _P, _L]),

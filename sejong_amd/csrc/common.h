@@ -38,6 +38,13 @@ __device__ __forceinline__ void split_bf(float x, bf16_t& hi, bf16_t& lo) {
   lo = f2bf(x - bf2f(hi));
 }
 
+// a * b rounded to fp32 and never fused into a following add (so a split
+// of the product sees the stored fp32 value)
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 __device__ __forceinline__ uint32_t pack2(bf16_t a, bf16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
 // Load a value of dtype `dt` (SJ_F32 or SJ_BF16) at index i as float.

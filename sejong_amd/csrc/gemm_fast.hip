@@ -67,6 +67,15 @@ struct FParams {
   long kchunk;
   float* partial;
   int xcd_remap;
+  // grouped (MoE) launches over expert segments given by device offsets
+  // goff[0..gE] (multiples of 64):
+  //   gmode 1: rows of the packed matrix; a tile's expert is the segment
+  //            holding its first row (BM = 64), B is read at b + e*gstride_b;
+  //   gmode 2: blockIdx.z = expert; K range [goff[e], goff[e+1]), C is
+  //            written at c + e*gstride_c (per-expert dW).
+  const int* goff;
+  int gE, gmode;
+  long gstride_b, gstride_c;
 };
 
 int g_remap = -1;
@@ -165,6 +174,15 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   }
   const unsigned tx = logical % nx, ty = (logical / nx) % ny, tz = logical / (nx * ny);
   const long m0 = (long)ty * BM, n0 = (long)tx * BN;
+  int ge = 0;
+  if (p.gmode == 1) {
+    if (m0 >= p.goff[p.gE]) return;  // beyond the last expert segment: the whole workgroup leaves
+    while (ge + 1 < p.gE && m0 >= p.goff[ge + 1]) ge++;
+  } else if (p.gmode == 2) {
+    ge = (int)tz;
+  }
+  const long boff = p.gmode == 1 ? (long)ge * p.gstride_b : 0;
+  const long coff = p.gmode == 2 ? (long)ge * p.gstride_c : 0;
   int seg = 0;
 #pragma unroll
   for (int s = 1; s < 3; s++)
@@ -174,7 +192,10 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   const long nrows_b = seg_end - p.seg_n[seg];
 
   long kbeg = 0, kend = p.K;
-  if (EPI == E_PARTIAL) {
+  if (p.gmode == 2) {
+    kbeg = p.goff[ge];
+    kend = p.goff[ge + 1];
+  } else if (EPI == E_PARTIAL) {
     kbeg = (long)tz * p.kchunk;
     kend = kbeg + p.kchunk < p.K ? kbeg + p.kchunk : p.K;
   }
@@ -203,7 +224,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       const int rb = r8 - AROWS;
       const int q = rb / (BN * PB), pl = (rb % (BN * PB)) / BN;
       const int sg = DUAL ? q : seg;
-      base = pl ? p.b[1][sg] : p.b[0][sg];
+      base = (pl ? p.b[1][sg] : p.b[0][sg]) + boff;
       ld = p.ldb[sg];
       row = nl0 + (rb % BN) + (sl >> 3);
       rows = nrows_b;
@@ -375,7 +396,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
             if (m < p.M && colok) p.partial[((long)tz * p.M + m) * p.N + ncol] = v[r];
           } else {  // E_STORE
             if (m < p.M && colok) {
-              const long idx = m * p.ldc[0] + ncol;
+              const long idx = coff + m * p.ldc[0] + ncol;
               if (p.c_bf16)
                 ((bf16_t*)p.c[0])[idx] = f2bf(v[r]);
               else if (p.accumulate)
@@ -414,6 +435,7 @@ int launch(hipStream_t s, const FParams& p, int splits) {
   static_assert(lds <= 160 * 1024, "LDS budget");
   auto kern = k_gemm_fast<BM, BN, PA, PB, EPI>;
   const_cast<FParams&>(p).xcd_remap = xcd_remap();
+  // grid z: split-K slices, or the experts of a per-expert dW launch
   dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
   hipLaunchKernelGGL(kern, grid, dim3(NT), lds, s, p);
   return SJ_OK;
@@ -690,5 +712,123 @@ extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const u
   int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("swiglu_backward");
+  return SJ_OK;
+}
+
+// ====================================================== grouped (MoE) GEMMs
+// Expert segments come from sj_route_pack's device offsets (64-row aligned),
+// so no count ever travels to the host: row-mode grids cover the packed
+// capacity and workgroups past the last segment leave at once.
+
+namespace {
+int grouped_bn(long cap, long N) { return tiles(cap, N, 64, 128) >= cus() ? 128 : 64; }
+bool grouped_ok(const int32_t* off, long experts, long cap) {
+  return off && experts > 0 && experts <= 1024 && cap > 0 && cap % 64 == 0;
+}
+}  // namespace
+
+extern "C" int sj_moe_gate_up_fwd(void* stream, const int32_t* offsets, long experts, long capacity,
+                                  const uint16_t* x, long ldx, long D, const uint16_t* wg_t, const uint16_t* wu_t,
+                                  long ldw, long w_stride, long F, uint16_t* g, uint16_t* u, uint16_t* h, long ldo,
+                                  uint16_t* h_t, long ldht) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 &&
+                 ldx >= D && ldw >= D && ldo >= F && w_stride % 8 == 0 && ok16(x) && ok16(wg_t) && ok16(wu_t) &&
+                 (!h_t || (ldht >= capacity && ldht % 4 == 0)),
+             "expert gate_up: shape/alignment (capacity %ld must be a multiple of 64)", capacity);
+  FParams p = {};
+  p.a[0] = (const bf16_t*)x; p.lda = ldx;
+  p.b[0][0] = (const bf16_t*)wg_t; p.b[0][1] = (const bf16_t*)wu_t; p.ldb[0] = p.ldb[1] = ldw;
+  p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = g; p.c[1] = u; p.c[2] = h; p.c[3] = h_t; p.ldc[0] = ldo; p.ldc[3] = ldht;
+  p.M = capacity; p.N = F; p.K = D; p.c_bf16 = 1;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
+  int st = launch_planes<E_GATEUP>((hipStream_t)stream, p, 1, 1, 64, grouped_bn(capacity, F), 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert gate_up");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_down_fwd(void* stream, const int32_t* offsets, long experts, long capacity, const uint16_t* h,
+                               long ldh, long F, const uint16_t* wd_t, long ldw, long w_stride, long D, uint16_t* y,
+                               long ldy) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && F > 0 && F % 8 == 0 && ldh % 8 == 0 && ldw % 8 == 0 &&
+                 ldh >= F && ldw >= F && ldy >= D && w_stride % 8 == 0 && ok16(h) && ok16(wd_t),
+             "expert down: shape/alignment");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)h; p.lda = ldh;
+  p.b[0][0] = (const bf16_t*)wd_t; p.ldb[0] = ldw; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = y; p.ldc[0] = ldy; p.c_bf16 = 1;
+  p.M = capacity; p.N = D; p.K = F;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
+  int st = launch_planes<E_STORE>((hipStream_t)stream, p, 1, 1, 64, grouped_bn(capacity, D), 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert down");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_down_bwd_swiglu_p(void* stream, const int32_t* offsets, long experts, long capacity,
+                                        const uint16_t* dy_hi, const uint16_t* dy_lo, long lddy, long D,
+                                        const uint16_t* w_down, long ldw, long w_stride, long F, const uint16_t* g,
+                                        const uint16_t* u, long ldgu, uint16_t* dgu_hi, uint16_t* dgu_lo, long lddgu,
+                                        uint16_t* dgu_t_hi, uint16_t* dgu_t_lo, long ldt) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && D > 0 && D % 8 == 0 && lddy % 8 == 0 && ldw % 8 == 0 &&
+                 lddy >= D && ldw >= D && ldgu >= F && lddgu >= 2 * F && ldt >= capacity && ldt % 4 == 0 &&
+                 w_stride % 8 == 0 && ok16(dy_hi) && ok16(dy_lo) && ok16(w_down),
+             "expert swiglu_backward: shape/alignment");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)dy_hi; p.a[1] = (const bf16_t*)dy_lo; p.lda = lddy;
+  p.b[0][0] = (const bf16_t*)w_down; p.ldb[0] = ldw; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = dgu_hi; p.c[1] = dgu_lo; p.c[2] = dgu_t_hi; p.c[3] = dgu_t_lo; p.ldc[0] = lddgu; p.ldc[2] = ldt;
+  p.gin = (const bf16_t*)g; p.uin = (const bf16_t*)u; p.ldgu = ldgu; p.F = F;
+  p.M = capacity; p.N = F; p.K = D;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
+  int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, 64, grouped_bn(capacity, F), 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert swiglu_backward");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_gemm_rows(void* stream, const int32_t* offsets, long experts, long capacity, long N, long K,
+                                const uint16_t* a_hi, const uint16_t* a_lo, long lda, const uint16_t* b, long ldb,
+                                long b_stride, float* c, long ldc, int accumulate) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && N > 0 && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+                 lda >= K && ldb >= K && ldc >= N && b_stride % 8 == 0 && ok16(a_hi) && (!a_lo || ok16(a_lo)) &&
+                 ok16(b),
+             "expert matmul (rows): shape/alignment");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)a_hi; p.a[1] = (const bf16_t*)a_lo; p.lda = lda;
+  p.b[0][0] = (const bf16_t*)b; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = c; p.ldc[0] = ldc; p.accumulate = accumulate;
+  p.M = capacity; p.N = N; p.K = K;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = b_stride;
+  int st = launch_planes<E_STORE>((hipStream_t)stream, p, a_lo ? 2 : 1, 1, 64, grouped_bn(capacity, N), 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert matmul (rows)");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_gemm_dw(void* stream, const int32_t* offsets, long experts, long capacity, long M, long N,
+                              const uint16_t* a, long lda, const uint16_t* b_hi, const uint16_t* b_lo, long ldb,
+                              float* c, long ldc, long c_stride) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && experts <= 65535 && M > 0 && N > 0 && lda % 8 == 0 &&
+                 ldb % 8 == 0 && lda >= capacity && ldb >= capacity && ldc >= N && ok16(a) && ok16(b_hi) &&
+                 (!b_lo || ok16(b_lo)),
+             "expert matmul (dW): shape/alignment");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)a; p.lda = lda;
+  p.b[0][0] = (const bf16_t*)b_hi; p.b[1][0] = (const bf16_t*)b_lo; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = c; p.ldc[0] = ldc;
+  p.M = M; p.N = N; p.K = capacity;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 2; p.gstride_c = c_stride;
+  int bm, bn;
+  pick(M * experts, N, bm, bn);
+  int st = launch_planes<E_STORE>((hipStream_t)stream, p, 1, b_lo ? 2 : 1, bm, bn, (int)experts);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert matmul (dW)");
   return SJ_OK;
 }

@@ -1,0 +1,582 @@
+// Mixture-of-experts FFN around the grouped GEMMs (gfx950).
+//
+// The reference runs the MoE FFN of Block::apply (crates/sejong-model/src/
+// architecture.rs:229-242) as: router matmul -> route_topk -> expert_routes
+// (pack + a D2H read of the counts, hierarchy_ops.rs:331-378) -> per expert
+// gather + gate_up + down -> expert_combine (fp32 atomics).  Here:
+//   k_router_topk   router logits (bf16, as the reference stores them) and
+//                   top-k routing in one pass, one wavefront per token;
+//   k_route_pack    one workgroup: per-expert counts, 64-row aligned segment
+//                   offsets and a stable slot-ordered packing, all on device;
+//   k_moe_gather    packed expert inputs (zero padding rows) and their
+//                   transpose (the dW operand);
+//   grouped GEMMs   (gemm_fast.hip) run every expert in one launch;
+//   k_moe_combine   weighted sum of a token's expert outputs in ascending
+//                   expert order (the order the reference's per-expert
+//                   launches add in) + the residual add;
+// and the backward: k_moe_combine_bwd (dX of each expert output as hi/lo
+// planes, normal and transposed, and the routing-weight gradient) and
+// k_moe_gather_bwd (route_topk backward + router dX + the gather's
+// scatter-add, summed per token without atomics).
+#include <math.h>
+
+#include "common.h"
+
+using namespace sj;
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int EMAX = 32;  // experts per layer supported by these kernels
+constexpr int KMAX = 8;   // top-k
+constexpr int SEG = 64;   // expert segment alignment in the packed layout
+
+long pack_capacity(long S, long E) { return (S + (SEG - 1) * E + SEG - 1) / SEG * SEG; }
+
+// top-k of E scores (registers, unrolled over EMAX): softmax over all E,
+// K rounds of argmax with the lowest index on ties, weight = full-softmax
+// probability (hierarchy.py:175-191)
+__device__ __forceinline__ void topk_rows(const float* sc_in, int E, int K, int32_t* ids, float* wout) {
+  float sc[EMAX];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) {
+    sc[e] = e < E ? sc_in[e] : -INFINITY;
+    mx = fmaxf(mx, sc[e]);
+  }
+  float den = 0.f;
+#pragma unroll
+  for (int e = 0; e < EMAX; e++)
+    if (e < E) den += expf(sc[e] - mx);
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    if (k >= K) break;
+    float best = -INFINITY;
+    int idx = E;
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e < E && (sc[e] > best || (idx == E && sc[e] == best))) {
+        best = sc[e];
+        idx = e;
+      }
+    ids[k] = idx;
+    wout[k] = expf(best - mx) / den;
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e == idx) sc[e] = -INFINITY;
+  }
+}
+
+// logits = round_bf16(z W_r) (W_r [d][E] bf16), then routing.  One wave
+// per token; lane l accumulates columns l, l+64, ... for every expert.
+__global__ __launch_bounds__(NT) void k_router_topk(const bf16_t* __restrict__ z, long ldz, const bf16_t* __restrict__ wr,
+                                                    long d, long R, int E, int K, bf16_t* __restrict__ logits,
+                                                    int32_t* __restrict__ ids, float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const long r = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (r >= R) return;
+  float acc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) acc[e] = 0.f;
+  for (long c = lane; c < d; c += 64) {
+    const float zv = bf2f(z[r * ldz + c]);
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e < E) acc[e] += zv * bf2f(wr[c * E + e]);
+  }
+  float sc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) {
+    sc[e] = 0.f;
+    if (e < E) sc[e] = round_bf(wave_sum(acc[e]));
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e < E) logits[r * E + e] = f2bf(sc[e]);
+    int32_t id[KMAX];
+    float w[KMAX];
+    topk_rows(sc, E, K, id, w);
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+      if (k < K) {
+        ids[r * K + k] = id[k];
+        weights[r * K + k] = w[k];
+      }
+  }
+}
+
+// routing from stored logits (Engine::route_topk), one thread per row
+__global__ __launch_bounds__(NT) void k_route_topk(const void* __restrict__ x, int xd, long R, int E, int K,
+                                                   int32_t* __restrict__ ids, float* __restrict__ weights) {
+  const long r = blockIdx.x * (long)NT + threadIdx.x;
+  if (r >= R) return;
+  float sc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) sc[e] = e < E ? load_as_f32(x, xd, r * E + e) : 0.f;
+  int32_t id[KMAX];
+  float w[KMAX];
+  topk_rows(sc, E, K, id, w);
+#pragma unroll
+  for (int k = 0; k < KMAX; k++)
+    if (k < K) {
+      ids[r * K + k] = id[k];
+      weights[r * K + k] = w[k];
+    }
+}
+
+// Engine::route_topk_backward (hierarchy.py:194-209): dx = p (dy_sel - sum_k w_k dy_k)
+__device__ __forceinline__ void route_bwd_row(const float* lg, int E, int K, const int32_t* id, const float* w,
+                                              const float* dy, float* dx) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EMAX; e++)
+    if (e < E) mx = fmaxf(mx, lg[e]);
+  float den = 0.f, ex[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) {
+    ex[e] = e < E ? expf(lg[e] - mx) : 0.f;
+    den += ex[e];
+  }
+  float total = 0.f, sel[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) sel[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    if (k >= K) break;
+    total += w[k] * dy[k];
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e == id[k]) sel[e] += dy[k];
+  }
+#pragma unroll
+  for (int e = 0; e < EMAX; e++)
+    if (e < E) dx[e] = ex[e] / den * (sel[e] - total);
+}
+
+__global__ __launch_bounds__(NT) void k_route_topk_bwd(const void* __restrict__ x, int xd, const int32_t* __restrict__ ids,
+                                                       const float* __restrict__ weights, const float* __restrict__ dy,
+                                                       float* __restrict__ dx, long R, int E, int K) {
+  const long r = blockIdx.x * (long)NT + threadIdx.x;
+  if (r >= R) return;
+  float lg[EMAX], d[EMAX], w[KMAX], g[KMAX];
+  int32_t id[KMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) lg[e] = e < E ? load_as_f32(x, xd, r * E + e) : 0.f;
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    id[k] = k < K ? ids[r * K + k] : -1;
+    w[k] = k < K ? weights[r * K + k] : 0.f;
+    g[k] = k < K ? dy[r * K + k] : 0.f;
+  }
+  route_bwd_row(lg, E, K, id, w, g, d);
+#pragma unroll
+  for (int e = 0; e < EMAX; e++)
+    if (e < E) dx[r * E + e] = d[e];
+}
+
+// Engine::expert_routes (hierarchy_route_pack, hierarchy.py:212-225) without
+// the host read: one workgroup.  Thread t owns slots [t*chunk, (t+1)*chunk);
+// per-expert counts of each thread are scanned (one wavefront per expert) to
+// give every slot its stable rank, the segments are laid out at 64-row
+// aligned offsets, and padding rows get slot -1.
+__global__ __launch_bounds__(NT) void k_route_pack(const int32_t* __restrict__ ids, long S, int K, int E, long cap,
+                                                   int32_t* __restrict__ tokens, int32_t* __restrict__ slots,
+                                                   int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                   int32_t* __restrict__ pslot, int32_t* __restrict__ ppos) {
+  __shared__ int cnt[EMAX][NT];
+  __shared__ int tot[EMAX];
+  __shared__ int off[EMAX + 1];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const long chunk = (S + NT - 1) / NT;
+  const long s0 = t * chunk, s1 = s0 + chunk < S ? s0 + chunk : S;
+  for (int e = 0; e < E; e++) cnt[e][t] = 0;
+  for (long s = s0; s < s1; s++) {
+    const int e = ids[s];
+    if (e >= 0 && e < E) cnt[e][t]++;
+  }
+  __syncthreads();
+  // exclusive scan of cnt[e][0..NT) per expert: 4 per lane + wave scan
+  for (int e = wv; e < E; e += NT / 64) {
+    int v[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[i] = cnt[e][4 * lane + i];
+      sum += v[i];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      cnt[e][4 * lane + i] = run;
+      run += v[i];
+    }
+    if (lane == 63) tot[e] = incl;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int o = 0;
+    for (int e = 0; e < E; e++) {
+      off[e] = o;
+      o += (tot[e] + SEG - 1) / SEG * SEG;
+    }
+    off[E] = o;
+  }
+  __syncthreads();
+  if (t <= E) offsets[t] = off[t];
+  if (t < E && counts) counts[t] = tot[t];
+  for (long s = s0; s < s1; s++) {
+    const int e = ids[s];
+    if (e < 0 || e >= E) {
+      ppos[s] = -1;
+      continue;
+    }
+    const int rank = cnt[e][t]++;
+    const int pos = off[e] + rank;
+    pslot[pos] = (int32_t)s;
+    ppos[s] = pos;
+    if (tokens) tokens[(long)e * S + rank] = (int32_t)(s / K);
+    if (slots) slots[(long)e * S + rank] = (int32_t)s;
+  }
+  for (int e = 0; e < E; e++) {
+    const long i = off[e] + tot[e] + t;
+    if (t < SEG && i < off[e + 1]) pslot[i] = -1;
+  }
+  for (long i = off[E] + t; i < cap; i += NT) pslot[i] = -1;
+}
+
+// packed rows: y[p] = x[token of pslot[p]] (zero for padding), plus y^T
+// [d][ldt] staged through LDS in blocks of TR rows (d <= 1024)
+constexpr int TR = 32;
+__global__ __launch_bounds__(NT) void k_moe_gather(const bf16_t* __restrict__ x, long ldx, long d,
+                                                   const int32_t* __restrict__ pslot, int K, long cap,
+                                                   bf16_t* __restrict__ y, bf16_t* __restrict__ yt, long ldt) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // [TR][d]
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const long p0 = blockIdx.x * (long)TR;
+  for (int rr = wv; rr < TR; rr += 4) {
+    const long p = p0 + rr;
+    const int s = p < cap ? pslot[p] : -1;
+    const long tok = s >= 0 ? s / K : -1;
+    for (long c = 2 * lane; c < d; c += 128) {
+      const uint32_t v = tok >= 0 ? *(const uint32_t*)(x + tok * ldx + c) : 0u;
+      if (p < cap) *(uint32_t*)(y + p * d + c) = v;
+      *(uint32_t*)(stage + rr * d + c) = v;
+    }
+  }
+  if (!yt) return;
+  __syncthreads();
+  for (long q = threadIdx.x; q < d * (TR / 8); q += NT) {
+    const long c = q / (TR / 8);
+    const int ch = (int)(q % (TR / 8));
+    bf16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = stage[(ch * 8 + i) * d + c];
+    const long rbase = p0 + ch * 8;
+    bf16_t* dst = yt + c * ldt + rbase;
+    if (rbase + 8 <= cap)
+      *(u32x4*)dst = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+  }
+}
+
+// a token's K (expert, packed position, weight) in ascending expert order
+// (unrolled compare-exchange over KMAX entries; unused entries sort last)
+__device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, const int32_t* ppos, const float* w,
+                                            int* pos, float* wk) {
+  int e[KMAX], n = 0;
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    const int pk = k < K ? ppos[t * K + k] : -1;
+    e[k] = pk >= 0 ? ids[t * K + k] : 0x7fffffff;
+    pos[k] = pk;
+    wk[k] = (pk >= 0 && w) ? w[t * K + k] : 0.f;
+    n += pk >= 0;
+  }
+#pragma unroll
+  for (int i = 0; i < KMAX; i++)
+#pragma unroll
+    for (int j = 0; j + 1 < KMAX - i; j++)
+      if (e[j] > e[j + 1]) {
+        const int te = e[j], tp = pos[j];
+        const float tw = wk[j];
+        e[j] = e[j + 1]; pos[j] = pos[j + 1]; wk[j] = wk[j + 1];
+        e[j + 1] = te; pos[j + 1] = tp; wk[j + 1] = tw;
+      }
+  return n;
+}
+
+// Engine::expert_combine (hierarchy.py:228-235) + the residual add of
+// Block::apply (architecture.rs:245): u = bf16(sum_e w*y_e) with each
+// product rounded before its add (the reference's atomic_add of weight*value,
+// launches in expert order), out = bf16(residual + u).  One wave per token.
+__global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ yp, long ldy, long d,
+                                                    const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
+                                                    const float* __restrict__ weights, long R, int K,
+                                                    const bf16_t* __restrict__ residual, long ldr,
+                                                    bf16_t* __restrict__ out, long ldo) {
+  const int lane = threadIdx.x & 63;
+  const long t = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (t >= R) return;
+  int pos[KMAX];
+  float wk[KMAX];
+  const int n = token_routes(t, K, ids, ppos, weights, pos, wk);
+  for (long c = 2 * lane; c < d; c += 128) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int j = 0; j < KMAX; j++) {
+      if (j >= n) break;
+      const uint32_t v = *(const uint32_t*)(yp + pos[j] * ldy + c);
+      a = a + mul_rn(wk[j], bf2f((bf16_t)(v & 0xffffu)));
+      b = b + mul_rn(wk[j], bf2f((bf16_t)(v >> 16)));
+    }
+    a = round_bf(a);
+    b = round_bf(b);
+    if (residual) {
+      const uint32_t rv = *(const uint32_t*)(residual + t * ldr + c);
+      a = bf2f((bf16_t)(rv & 0xffffu)) + a;
+      b = bf2f((bf16_t)(rv >> 16)) + b;
+    }
+    *(uint32_t*)(out + t * ldo + c) = pack2(f2bf(a), f2bf(b));
+  }
+}
+
+// Engine::expert_combine_backward (hierarchy.py:238-251) for all experts:
+// dx[p] = dy[token] * w[slot] (as hi/lo planes, normal [cap][d] and
+// transposed [d][ldt]) and dw[slot] = sum_c y[p][c] dy[token][c].
+constexpr int TRB = 16;
+__global__ __launch_bounds__(NT) void k_moe_combine_bwd(const bf16_t* __restrict__ yp, long ldy, long d,
+                                                        const int32_t* __restrict__ pslot, const float* __restrict__ weights,
+                                                        int K, long cap, const float* __restrict__ dy, long lddy,
+                                                        bf16_t* __restrict__ hi, bf16_t* __restrict__ lo,
+                                                        bf16_t* __restrict__ hit, bf16_t* __restrict__ lot, long ldt,
+                                                        float* __restrict__ dw) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // hi [TRB][d], lo [TRB][d]
+  bf16_t* shi = stage;
+  bf16_t* slo = stage + TRB * d;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const long p0 = blockIdx.x * (long)TRB;
+  for (int rr = wv; rr < TRB; rr += 4) {
+    const long p = p0 + rr;
+    const int s = p < cap ? pslot[p] : -1;
+    const long tok = s >= 0 ? s / K : -1;
+    const float w = s >= 0 ? weights[s] : 0.f;
+    float dot = 0.f;
+    for (long c = 2 * lane; c < d; c += 128) {
+      uint32_t ph = 0u, pl = 0u;
+      if (tok >= 0) {
+        const float2 g = *(const float2*)(dy + tok * lddy + c);
+        const uint32_t yv = *(const uint32_t*)(yp + p * ldy + c);
+        dot += bf2f((bf16_t)(yv & 0xffffu)) * g.x + bf2f((bf16_t)(yv >> 16)) * g.y;
+        bf16_t ha, la, hb, lb;
+        // dx is the fp32 product (the reference stores it in fp32): round it
+        // before the split so the lo plane is not formed from a fused product
+        split_bf(mul_rn(g.x, w), ha, la);
+        split_bf(mul_rn(g.y, w), hb, lb);
+        ph = pack2(ha, hb);
+        pl = pack2(la, lb);
+      }
+      if (p < cap) {
+        *(uint32_t*)(hi + p * d + c) = ph;
+        *(uint32_t*)(lo + p * d + c) = pl;
+      }
+      *(uint32_t*)(shi + rr * d + c) = ph;
+      *(uint32_t*)(slo + rr * d + c) = pl;
+    }
+    dot = wave_sum(dot);
+    if (lane == 0 && s >= 0) dw[s] = dot;
+  }
+  __syncthreads();
+  for (long q = threadIdx.x; q < 2 * d * (TRB / 8); q += NT) {
+    const int plane = q >= d * (TRB / 8);
+    const long qq = plane ? q - d * (TRB / 8) : q;
+    const long c = qq / (TRB / 8);
+    const int ch = (int)(qq % (TRB / 8));
+    const bf16_t* src = plane ? slo : shi;
+    bf16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = src[(ch * 8 + i) * d + c];
+    const long rbase = p0 + ch * 8;
+    if (rbase + 8 <= cap)
+      *(u32x4*)((plane ? lot : hit) + c * ldt + rbase) =
+          u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+  }
+}
+
+// Per token: route_topk backward (dlogits), router dX (dlogits W_r^T,
+// W_r [d][E] bf16), the gather's scatter-add (sum of the token's expert
+// input gradients in ascending expert order) and the tape's accumulation
+// into dz_acc.  One wave per token; no atomics.
+__global__ __launch_bounds__(NT) void k_moe_gather_bwd(const float* __restrict__ dxp, long lddx, long d,
+                                                       const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
+                                                       const float* __restrict__ weights, const bf16_t* __restrict__ logits,
+                                                       const float* __restrict__ dweights, const bf16_t* __restrict__ wr,
+                                                       long R, int K, int E, const float* __restrict__ acc, long ldacc,
+                                                       float* __restrict__ dz, long lddz, float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63;
+  const long t = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (t >= R) return;
+  float dl[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) dl[e] = 0.f;
+  if (logits) {
+    float lg[EMAX], w[KMAX], g[KMAX];
+    int32_t id[KMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; e++) lg[e] = e < E ? bf2f(logits[t * E + e]) : 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+      id[k] = k < K ? ids[t * K + k] : -1;
+      w[k] = k < K ? weights[t * K + k] : 0.f;
+      g[k] = k < K ? dweights[t * K + k] : 0.f;
+    }
+    route_bwd_row(lg, E, K, id, w, g, dl);
+    if (lane < E) {
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < EMAX; e++)
+        if (e == lane) v = dl[e];
+      dlogits[t * E + lane] = v;
+    }
+  }
+  int pos[KMAX];
+  float unused[KMAX];
+  const int n = token_routes(t, K, ids, ppos, nullptr, pos, unused);
+  for (long c = lane; c < d; c += 64) {
+    float s = acc ? acc[t * ldacc + c] : 0.f;
+    float ex = 0.f;
+#pragma unroll
+    for (int j = 0; j < KMAX; j++)
+      if (j < n) ex += dxp[pos[j] * lddx + c];
+    s += ex;
+    if (logits && wr) {
+      float r = 0.f;
+#pragma unroll
+      for (int e = 0; e < EMAX; e++)
+        if (e < E) r += dl[e] * bf2f(wr[c * E + e]);
+      s += r;
+    }
+    dz[t * lddz + c] = s;
+  }
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" long sj_route_pack_capacity(long slots, long experts) {
+  if (slots < 0 || experts <= 0) return -1;
+  return pack_capacity(slots, experts);
+}
+
+extern "C" int sj_router_topk(void* stream, const uint16_t* z, long ldz, const uint16_t* w_router, long d, long rows,
+                              long experts, long top_k, uint16_t* logits, int32_t* ids, float* weights) {
+  SJ_REQUIRE(rows >= 0 && d > 0 && ldz >= d && experts > 0 && experts <= EMAX && top_k > 0 && top_k <= KMAX &&
+                 top_k <= experts && logits && ids && weights,
+             "router top-k dimensions (experts <= %d, top_k <= %d)", EMAX, KMAX);
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream,
+                     (const bf16_t*)z, ldz, (const bf16_t*)w_router, d, rows, (int)experts, (int)top_k,
+                     (bf16_t*)logits, ids, weights);
+  SJ_LAUNCH_CHECK("router_topk");
+  return SJ_OK;
+}
+
+extern "C" int sj_route_topk(void* stream, const void* logits, int dtype, long rows, long experts, long top_k,
+                             int32_t* ids, float* weights) {
+  SJ_REQUIRE(rows >= 0 && experts > 0 && experts <= EMAX && top_k > 0 && top_k <= KMAX && top_k <= experts &&
+                 (dtype == SJ_F32 || dtype == SJ_BF16),
+             "router top-k dimensions");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_route_topk, dim3((unsigned)((rows + NT - 1) / NT)), dim3(NT), 0, (hipStream_t)stream, logits,
+                     dtype, rows, (int)experts, (int)top_k, ids, weights);
+  SJ_LAUNCH_CHECK("hierarchy_route_topk");
+  return SJ_OK;
+}
+
+extern "C" int sj_route_topk_bwd(void* stream, const void* logits, int dtype, const int32_t* ids, const float* weights,
+                                 const float* dy, float* dx, long rows, long experts, long top_k) {
+  SJ_REQUIRE(rows >= 0 && experts > 0 && experts <= EMAX && top_k > 0 && top_k <= KMAX && top_k <= experts &&
+                 (dtype == SJ_F32 || dtype == SJ_BF16),
+             "router backward dimensions");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_route_topk_bwd, dim3((unsigned)((rows + NT - 1) / NT)), dim3(NT), 0, (hipStream_t)stream,
+                     logits, dtype, ids, weights, dy, dx, rows, (int)experts, (int)top_k);
+  SJ_LAUNCH_CHECK("hierarchy_route_backward");
+  return SJ_OK;
+}
+
+extern "C" int sj_route_pack(void* stream, const int32_t* ids, long rows, long top_k, long experts, int32_t* tokens,
+                             int32_t* slots, int32_t* counts, int32_t* offsets, int32_t* pslot, int32_t* ppos,
+                             long capacity) {
+  const long S = rows * top_k;
+  SJ_REQUIRE(rows >= 0 && top_k > 0 && experts > 0 && experts <= EMAX && S < (1L << 31) && offsets && pslot && ppos &&
+                 capacity >= pack_capacity(S, experts),
+             "expert route dimensions (capacity %ld, need %ld)", capacity, pack_capacity(S, experts));
+  hipLaunchKernelGGL(k_route_pack, dim3(1), dim3(NT), 0, (hipStream_t)stream, ids, S, (int)top_k, (int)experts,
+                     capacity, tokens, slots, counts, offsets, pslot, ppos);
+  SJ_LAUNCH_CHECK("hierarchy_route_pack");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_gather(void* stream, const uint16_t* x, long ldx, long d, const int32_t* pslot, long top_k,
+                             long capacity, uint16_t* y, uint16_t* y_t, long ldt) {
+  SJ_REQUIRE(d > 0 && d % 8 == 0 && d <= 1024 && ldx % 2 == 0 && ldx >= d && top_k > 0 && capacity % 64 == 0 &&
+                 (!y_t || (ldt >= capacity && ldt % 8 == 0 && ((uintptr_t)y_t & 15) == 0)),
+             "gather (experts): d %ld (<= 1024, multiple of 8), capacity %ld", d, capacity);
+  if (capacity == 0) return SJ_OK;
+  const size_t lds = sizeof(bf16_t) * TR * (size_t)d;
+  hipLaunchKernelGGL(k_moe_gather, dim3((unsigned)(capacity / TR)), dim3(NT), lds, (hipStream_t)stream,
+                     (const bf16_t*)x, ldx, d, pslot, (int)top_k, capacity, (bf16_t*)y, (bf16_t*)y_t, ldt);
+  SJ_LAUNCH_CHECK("gather");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_combine(void* stream, const uint16_t* yp, long ldy, long d, const int32_t* ids,
+                              const int32_t* ppos, const float* weights, long rows, long top_k, const uint16_t* residual,
+                              long ldr, uint16_t* out, long ldo) {
+  SJ_REQUIRE(rows >= 0 && d > 0 && d % 2 == 0 && ldy % 2 == 0 && ldo % 2 == 0 && (!residual || ldr % 2 == 0) &&
+                 top_k > 0 && top_k <= KMAX,
+             "expert combine dimensions");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream,
+                     (const bf16_t*)yp, ldy, d, ids, ppos, weights, rows, (int)top_k, (const bf16_t*)residual, ldr,
+                     (bf16_t*)out, ldo);
+  SJ_LAUNCH_CHECK("hierarchy_expert_combine");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_combine_bwd(void* stream, const uint16_t* yp, long ldy, long d, const int32_t* pslot,
+                                  const float* weights, long top_k, long capacity, const float* dy, long lddy,
+                                  uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi, uint16_t* dx_t_lo, long ldt,
+                                  float* dweights) {
+  SJ_REQUIRE(d > 0 && d % 8 == 0 && d <= 1024 && ldy % 2 == 0 && lddy % 2 == 0 && top_k > 0 && capacity % 64 == 0 &&
+                 ldt >= capacity && ldt % 8 == 0 && ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
+             "expert combine backward dimensions");
+  if (capacity == 0) return SJ_OK;
+  const size_t lds = 2 * sizeof(bf16_t) * TRB * (size_t)d;
+  hipLaunchKernelGGL(k_moe_combine_bwd, dim3((unsigned)(capacity / TRB)), dim3(NT), lds, (hipStream_t)stream,
+                     (const bf16_t*)yp, ldy, d, pslot, weights, (int)top_k, capacity, dy, lddy, (bf16_t*)dx_hi,
+                     (bf16_t*)dx_lo, (bf16_t*)dx_t_hi, (bf16_t*)dx_t_lo, ldt, dweights);
+  SJ_LAUNCH_CHECK("hierarchy_expert_backward");
+  return SJ_OK;
+}
+
+extern "C" int sj_moe_gather_bwd(void* stream, const float* dxp, long lddx, long d, const int32_t* ids,
+                                 const int32_t* ppos, const float* weights, const uint16_t* logits,
+                                 const float* dweights, const uint16_t* w_router, long rows, long top_k, long experts,
+                                 const float* dz_acc, long ldacc, float* dz, long lddz, float* dlogits) {
+  SJ_REQUIRE(rows >= 0 && d > 0 && top_k > 0 && top_k <= KMAX && experts > 0 && experts <= EMAX &&
+                 (!logits || (dweights && dlogits)),
+             "gather backward (experts) dimensions");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_moe_gather_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream, dxp, lddx,
+                     d, ids, ppos, weights, (const bf16_t*)logits, dweights, (const bf16_t*)w_router, rows,
+                     (int)top_k, (int)experts, dz_acc, ldacc, dz, lddz, dlogits);
+  SJ_LAUNCH_CHECK("gather_backward");
+  return SJ_OK;
+}

@@ -363,3 +363,57 @@ def test_model_causal_prefix_and_batch_separation():
     np.testing.assert_array_equal(rows[:4], rows2[:4])      # causal prefix
     np.testing.assert_array_equal(rows[T:], rows2[T:])      # other sequence
     assert rows[4] != rows2[4]
+
+
+# ------------------------------------------------------------ MoE FFN
+def _moe_case(rng, M=12, d=8, E=4, F=6, std=0.5):
+    z = rng.normal(0, 1, (M, d))
+    wr = rng.normal(0, 1, (d, E))
+    ex = [(rng.normal(0, std, (d, F)), rng.normal(0, std, (d, F)), rng.normal(0, std, (F, d))) for _ in range(E)]
+    return z, wr, ex
+
+
+def test_moe_backward_finite_difference():
+    from oracle import moe
+    rng = np.random.default_rng(31)
+    z, wr, ex = _moe_case(rng)
+    K = 2
+    R = rng.normal(0, 1, (z.shape[0], z.shape[1]))
+    acts = moe.moe_forward(z, wr, ex, K, dtype=None)
+    dz, dwr, grads, _, _ = moe.moe_backward(z, wr, ex, acts, R)
+
+    def loss(z_, wr_, ex_):
+        a = moe.moe_forward(z_, wr_, ex_, K, dtype=None)
+        assert np.array_equal(a["ids"], acts["ids"])  # routing held fixed by the small step
+        return float(np.sum(a["update"] * R))
+
+    # routing reads fp32 logits (hierarchy.py:178), so the step must be large
+    # against fp32 resolution; the routing stays fixed and O(h^2) is ~1e-6
+    h = 1e-3
+    def fd(arr, i, f):
+        old = arr.flat[i]
+        arr.flat[i] = old + h; lp = f()
+        arr.flat[i] = old - h; lm = f()
+        arr.flat[i] = old
+        return (lp - lm) / (2 * h)
+
+    for i in rng.choice(z.size, 6, replace=False):
+        assert abs(fd(z, i, lambda: loss(z, wr, ex)) - dz.flat[i]) < 2e-4 * (1 + abs(dz.flat[i]))
+    for i in rng.choice(wr.size, 6, replace=False):
+        assert abs(fd(wr, i, lambda: loss(z, wr, ex)) - dwr.flat[i]) < 2e-4 * (1 + abs(dwr.flat[i]))
+    for e in range(len(ex)):
+        for j in range(3):
+            W = ex[e][j]
+            for i in rng.choice(W.size, 3, replace=False):
+                assert abs(fd(W, i, lambda: loss(z, wr, ex)) - grads[e][j].flat[i]) < 2e-4 * (1 + abs(grads[e][j].flat[i]))
+
+
+def test_moe_single_expert_is_dense_ffn():
+    from oracle import moe
+    rng = np.random.default_rng(32)
+    z, wr, ex = _moe_case(rng, M=20, d=16, E=1, F=24)
+    z = O.round_to(z, "bf16")
+    ex = [tuple(O.round_to(w, "bf16") for w in ex[0])]
+    a = moe.moe_forward(z, wr, ex, 1, dtype="bf16")
+    assert np.all(a["w"] == 1.0) and np.all(a["ids"] == 0)
+    np.testing.assert_array_equal(a["update"], moe.dense_ffn(z, *ex[0], dtype="bf16"))
