@@ -160,161 +160,162 @@ __global__ __launch_bounds__(NT) void k_rms_reduce(const float* __restrict__ par
 
 
 // ----------------------------------------------------- MFMA-layout variants
-// Row blocks of TR = 32 rows: each wave normalises 8 rows, the block stages
-// its bf16 outputs in LDS and also writes them transposed ([d][rows], 64 B
-// per column segment), the layout the dW GEMMs stream.
-constexpr int TR = 32;
+// Row blocks of TR = 16 rows on 16 waves, one row per wave, so every row's
+// loads are in flight at once; lanes own column pairs lane + 64 j, j < NP.
+// The block stages its bf16 outputs in LDS and also writes them transposed
+// ([d][rows], 32-byte column segments), the layout the dW GEMMs stream.
+// Row blocks are ordered so each XCD (workgroup b runs on XCD b % 8) takes a
+// contiguous run of them: neighbouring column segments then meet in one L2
+// and leave it as whole lines.
+constexpr int TR = 16;
+constexpr int NTT = 1024;
+
+__device__ __forceinline__ long xcd_block(long b, long nb) {
+  const long xcd = b & 7, local = b >> 3, q = nb >> 3, r = nb & 7;
+  return xcd * q + (xcd < r ? xcd : r) + local;
+}
+
+// 8 rows (row stride d in LDS) of column c -> one 16-byte store, or
+// element stores at the ragged end
+__device__ __forceinline__ void store_col8(bf16_t* dst, const bf16_t* src, long d, long c, long rbase, long rows) {
+  bf16_t v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = src[i * d + c];
+  if (rbase + 8 <= rows) {
+    *(u32x4*)dst = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+  } else {
+    for (int i = 0; i < 8; i++)
+      if (rbase + i < rows) dst[i] = v[i];
+  }
+}
 
 // y = rmsnorm(x) (bf16 x, w) -> y [rows][d] and y_t [d][ldt]
-__global__ __launch_bounds__(NT) void k_rms_fwd_t(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
-                                                  bf16_t* __restrict__ y, bf16_t* __restrict__ yt, long rows,
-                                                  long d, long ldt, float eps) {
+template <int NP>
+__global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                                                   bf16_t* __restrict__ y, bf16_t* __restrict__ yt, long rows,
+                                                   long d, long ldt, float eps) {
   extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // [TR][d]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const long r0 = blockIdx.x * (long)TR;
+  const long r0 = xcd_block(blockIdx.x, gridDim.x) * TR;
   const long pairs = d >> 1;
-  for (int rr = wv; rr < TR; rr += 4) {
-    const long r = r0 + rr;
-    float2 xv[MAXP];
-    float s = 0.f;
+  const long r = r0 + wv;
+  float2 xv[NP];
+  float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      long p = lane + 64L * j;
-      if (p < pairs && r < rows) {
-        xv[j] = ld2<SJ_BF16>(x, r * d + 2 * p);
-        s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
-      }
+  for (int j = 0; j < NP; j++) {
+    const long p = lane + 64L * j;
+    xv[j] = make_float2(0.f, 0.f);
+    if (p < pairs && r < rows) {
+      xv[j] = ld2<SJ_BF16>(x, r * d + 2 * p);
+      s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
     }
-    s = wave_sum(s);
-    const float inv = 1.f / sqrtf(s / (float)d + eps);
+  }
+  s = wave_sum(s);
+  const float inv = 1.f / sqrtf(s / (float)d + eps);
 #pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      long p = lane + 64L * j;
-      if (p < pairs) {
-        float2 wv2 = ld2<SJ_BF16>(w, 2 * p);
-        uint32_t pk = r < rows ? pack2(f2bf(xv[j].x * inv * wv2.x), f2bf(xv[j].y * inv * wv2.y)) : 0u;
-        if (r < rows) *(uint32_t*)(y + r * d + 2 * p) = pk;
-        *(uint32_t*)(stage + rr * d + 2 * p) = pk;
-      }
+  for (int j = 0; j < NP; j++) {
+    const long p = lane + 64L * j;
+    if (p < pairs) {
+      const float2 w2 = ld2<SJ_BF16>(w, 2 * p);
+      const uint32_t pk = r < rows ? pack2(f2bf(xv[j].x * inv * w2.x), f2bf(xv[j].y * inv * w2.y)) : 0u;
+      if (r < rows) *(uint32_t*)(y + r * d + 2 * p) = pk;
+      *(uint32_t*)(stage + wv * d + 2 * p) = pk;
     }
   }
   __syncthreads();
-  // transposed: column c, rows r0..r0+31 -> 4 chunks of 8 bf16
-  for (long q = threadIdx.x; q < d * (TR / 8); q += NT) {
-    const long c = q / (TR / 8);
-    const int ch = (int)(q % (TR / 8));
-    bf16_t v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = stage[(ch * 8 + i) * d + c];
+  for (long q = threadIdx.x; q < 2 * d; q += NTT) {
+    const long c = q >> 1;
+    const int ch = (int)(q & 1);
     const long rbase = r0 + ch * 8;
-    bf16_t* dst = yt + c * ldt + rbase;
-    if (rbase + 8 <= rows) {
-      *(u32x4*)dst = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
-    } else {
-      for (int i = 0; i < 8; i++)
-        if (rbase + i < rows) dst[i] = v[i];
-    }
+    store_col8(yt + c * ldt + rbase, stage + ch * 8 * d, d, c, rbase, rows);
   }
 }
 
 // backward with hi/lo plane outputs of dx (normal and transposed) next to the
-// fp32 dx; dw partial per 32-row block.
-__global__ __launch_bounds__(NT) void k_rms_bwd_p(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
-                                                  const float* __restrict__ dy, const float* __restrict__ dx_acc,
-                                                  float* __restrict__ dx, bf16_t* __restrict__ hi,
-                                                  bf16_t* __restrict__ lo, bf16_t* __restrict__ hit,
-                                                  bf16_t* __restrict__ lot, float* __restrict__ partial, long rows,
-                                                  long d, long ldt, float eps) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // hi [TR][d], lo [TR][d], red [4][d] f32
+// fp32 dx; dw partial per 16-row block (fixed-order sum of its rows)
+template <int NP>
+__global__ __launch_bounds__(NTT) void k_rms_bwd_p(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
+                                                   const float* __restrict__ dy, const float* __restrict__ dx_acc,
+                                                   float* __restrict__ dx, bf16_t* __restrict__ hi,
+                                                   bf16_t* __restrict__ lo, bf16_t* __restrict__ hit,
+                                                   bf16_t* __restrict__ lot, float* __restrict__ partial, long rows,
+                                                   long d, long ldt, float eps) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // hi [TR][d], lo [TR][d], red [TR][d] f32
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const long pairs = d >> 1;
   bf16_t* shi = stage;
   bf16_t* slo = stage + TR * d;
   float* red = (float*)(stage + 2 * TR * d);
-  float2 dwp[MAXP], wreg[MAXP];
+  const long blk = xcd_block(blockIdx.x, gridDim.x);
+  const long r0 = blk * TR;
+  const long r = r0 + wv;
+  const bool ok = r < rows;
+  float2 xv[NP], gv[NP], wr[NP], av[NP];
+  float s = 0.f, sdx = 0.f;
 #pragma unroll
-  for (int j = 0; j < MAXP; j++) {
-    dwp[j] = make_float2(0.f, 0.f);
-    long p = lane + 64L * j;
-    if (p < pairs) wreg[j] = ld2<SJ_BF16>(w, 2 * p);
-  }
-  const long r0 = blockIdx.x * (long)TR;
-  for (int rr = wv; rr < TR; rr += 4) {
-    const long r = r0 + rr;
-    const bool ok = r < rows;
-    float2 xv[MAXP], gv[MAXP];
-    float s = 0.f, sdx = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      long p = lane + 64L * j;
-      if (p < pairs && ok) {
+  for (int j = 0; j < NP; j++) {
+    const long p = lane + 64L * j;
+    xv[j] = gv[j] = wr[j] = av[j] = make_float2(0.f, 0.f);
+    if (p < pairs) {
+      wr[j] = ld2<SJ_BF16>(w, 2 * p);
+      if (ok) {
         xv[j] = ld2<SJ_BF16>(x, r * d + 2 * p);
         gv[j] = *(const float2*)(dy + r * d + 2 * p);
-        s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
-        sdx += gv[j].x * wreg[j].x * xv[j].x + gv[j].y * wreg[j].y * xv[j].y;
-      }
-    }
-    s = wave_sum(s);
-    sdx = wave_sum(sdx);
-    const float inv = rsqrtf(s / (float)d + eps);
-    const float c = (sdx / (float)d) * inv * inv;
-#pragma unroll
-    for (int j = 0; j < MAXP; j++) {
-      long p = lane + 64L * j;
-      if (p < pairs) {
-        uint32_t ph = 0u, pl = 0u;
-        if (ok) {
-          float a = inv * (gv[j].x * wreg[j].x - xv[j].x * c);
-          float b = inv * (gv[j].y * wreg[j].y - xv[j].y * c);
-          if (dx_acc) {
-            float2 acc = *(const float2*)(dx_acc + r * d + 2 * p);
-            a = acc.x + a;
-            b = acc.y + b;
-          }
-          *(float2*)(dx + r * d + 2 * p) = make_float2(a, b);
-          dwp[j].x += gv[j].x * xv[j].x * inv;
-          dwp[j].y += gv[j].y * xv[j].y * inv;
-          bf16_t ha, la, hb, lb;
-          split_bf(a, ha, la);
-          split_bf(b, hb, lb);
-          ph = pack2(ha, hb);
-          pl = pack2(la, lb);
-          *(uint32_t*)(hi + r * d + 2 * p) = ph;
-          *(uint32_t*)(lo + r * d + 2 * p) = pl;
-        }
-        *(uint32_t*)(shi + rr * d + 2 * p) = ph;
-        *(uint32_t*)(slo + rr * d + 2 * p) = pl;
+        if (dx_acc) av[j] = *(const float2*)(dx_acc + r * d + 2 * p);
       }
     }
   }
 #pragma unroll
-  for (int j = 0; j < MAXP; j++) {
-    long p = lane + 64L * j;
+  for (int j = 0; j < NP; j++) {
+    s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
+    sdx += gv[j].x * wr[j].x * xv[j].x + gv[j].y * wr[j].y * xv[j].y;
+  }
+  s = wave_sum(s);
+  sdx = wave_sum(sdx);
+  const float inv = rsqrtf(s / (float)d + eps);
+  const float cc = (sdx / (float)d) * inv * inv;
+#pragma unroll
+  for (int j = 0; j < NP; j++) {
+    const long p = lane + 64L * j;
     if (p < pairs) {
-      red[wv * d + 2 * p] = dwp[j].x;
-      red[wv * d + 2 * p + 1] = dwp[j].y;
+      uint32_t ph = 0u, pl = 0u;
+      float2 dwv = make_float2(0.f, 0.f);
+      if (ok) {
+        float a = inv * (gv[j].x * wr[j].x - xv[j].x * cc);
+        float b = inv * (gv[j].y * wr[j].y - xv[j].y * cc);
+        if (dx_acc) {
+          a = av[j].x + a;
+          b = av[j].y + b;
+        }
+        *(float2*)(dx + r * d + 2 * p) = make_float2(a, b);
+        dwv = make_float2(gv[j].x * xv[j].x * inv, gv[j].y * xv[j].y * inv);
+        bf16_t ha, la, hb, lb;
+        split_bf(a, ha, la);
+        split_bf(b, hb, lb);
+        ph = pack2(ha, hb);
+        pl = pack2(la, lb);
+        *(uint32_t*)(hi + r * d + 2 * p) = ph;
+        *(uint32_t*)(lo + r * d + 2 * p) = pl;
+      }
+      *(uint32_t*)(shi + wv * d + 2 * p) = ph;
+      *(uint32_t*)(slo + wv * d + 2 * p) = pl;
+      *(float2*)(red + wv * d + 2 * p) = dwv;
     }
   }
   __syncthreads();
-  for (long c = threadIdx.x; c < d; c += NT)
-    partial[blockIdx.x * d + c] = ((red[c] + red[d + c]) + red[2 * d + c]) + red[3 * d + c];
-  for (long q = threadIdx.x; q < 2 * d * (TR / 8); q += NT) {
-    const int pl = q >= d * (TR / 8);
-    const long qq = pl ? q - d * (TR / 8) : q;
-    const long c = qq / (TR / 8);
-    const int ch = (int)(qq % (TR / 8));
-    const bf16_t* src = pl ? slo : shi;
-    bf16_t v[8];
+  for (long c = threadIdx.x; c < d; c += NTT) {
+    float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = src[(ch * 8 + i) * d + c];
+    for (int i = 0; i < TR; i++) acc += red[i * d + c];
+    partial[blk * d + c] = acc;
+  }
+  for (long q = threadIdx.x; q < 4 * d; q += NTT) {
+    const int plane = q >= 2 * d;
+    const long qq = plane ? q - 2 * d : q;
+    const long c = qq >> 1;
+    const int ch = (int)(qq & 1);
     const long rbase = r0 + ch * 8;
-    bf16_t* dst = (pl ? lot : hit) + c * ldt + rbase;
-    if (rbase + 8 <= rows) {
-      *(u32x4*)dst = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
-    } else {
-      for (int i = 0; i < 8; i++)
-        if (rbase + i < rows) dst[i] = v[i];
-    }
+    store_col8((plane ? lot : hit) + c * ldt + rbase, (plane ? slo : shi) + ch * 8 * d, d, c, rbase, rows);
   }
 }
 
@@ -375,29 +376,71 @@ extern "C" int sj_rmsnorm_bwd(void* stream, const void* x, int xd, const void* w
 
 // Allow the plane variants up to 160 KB of dynamic LDS (d <= 1024); run
 // once, outside any stream capture (sj_model_create calls it).
+namespace {
+template <int NP>
+hipError_t set_np_attrs() {
+  hipError_t e = hipFuncSetAttribute((const void*)k_rms_bwd_p<NP>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     160 * 1024);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_rms_fwd_t<NP>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  return e;
+}
+}  // namespace
+
 namespace sjh {
 int norm_prepare() {
   static int done = 0, status = SJ_OK;
   if (done) return status;
   done = 1;
-  hipError_t e = hipFuncSetAttribute((const void*)k_rms_bwd_p, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute((const void*)k_rms_fwd_t, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  hipError_t e = set_np_attrs<1>();
+  if (e == hipSuccess) e = set_np_attrs<2>();
+  if (e == hipSuccess) e = set_np_attrs<3>();
+  if (e == hipSuccess) e = set_np_attrs<4>();
+  if (e == hipSuccess) e = set_np_attrs<5>();
+  if (e == hipSuccess) e = set_np_attrs<6>();
+  if (e == hipSuccess) e = set_np_attrs<7>();
+  if (e == hipSuccess) e = set_np_attrs<8>();
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "rmsnorm: LDS attribute");
   return status;
 }
 }  // namespace sjh
 
+namespace {
+template <int NP>
+void launch_fwd_t(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x, const uint16_t* w, uint16_t* y,
+                  uint16_t* y_t, long rows, long d, long ldt, float eps) {
+  hipLaunchKernelGGL(k_rms_fwd_t<NP>, dim3(blocks), dim3(NTT), lds, s, (const bf16_t*)x, (const bf16_t*)w, (bf16_t*)y,
+                     (bf16_t*)y_t, rows, d, ldt, eps);
+}
+template <int NP>
+void launch_bwd_p(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x, const uint16_t* w, const float* dy,
+                  const float* dx_acc, float* dx, uint16_t* hi, uint16_t* lo, uint16_t* hit, uint16_t* lot,
+                  float* partial, long rows, long d, long ldt, float eps) {
+  hipLaunchKernelGGL(k_rms_bwd_p<NP>, dim3(blocks), dim3(NTT), lds, s, (const bf16_t*)x, (const bf16_t*)w, dy, dx_acc,
+                     dx, (bf16_t*)hi, (bf16_t*)lo, (bf16_t*)hit, (bf16_t*)lot, partial, rows, d, ldt, eps);
+}
+}  // namespace
+
 extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t* w, uint16_t* y, uint16_t* y_t,
                                 long ldt, long rows, long d, float eps) {
-  SJ_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 2 * 64 * MAXP && ldt >= rows && ldt % 8 == 0 &&
+  SJ_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 1024 && ldt >= rows && ldt % 8 == 0 &&
                  ((uintptr_t)y_t & 15) == 0,
-             "RMSNorm (transposed output): rows %ld d %ld ldt %ld", rows, d, ldt);
+             "RMSNorm (transposed output): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
   if (rows == 0) return SJ_OK;
   if (int st0 = sjh::norm_prepare()) return st0;
   const size_t lds = sizeof(bf16_t) * TR * (size_t)d;
-  hipLaunchKernelGGL(k_rms_fwd_t, dim3((unsigned)((rows + TR - 1) / TR)), dim3(NT), lds, (hipStream_t)stream,
-                     (const bf16_t*)x, (const bf16_t*)w, (bf16_t*)y, (bf16_t*)y_t, rows, d, ldt, eps);
+  const unsigned blocks = (unsigned)((rows + TR - 1) / TR);
+  hipStream_t s = (hipStream_t)stream;
+  switch ((d / 2 + 63) / 64) {
+    case 1: launch_fwd_t<1>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 2: launch_fwd_t<2>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 3: launch_fwd_t<3>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 4: launch_fwd_t<4>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 5: launch_fwd_t<5>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 6: launch_fwd_t<6>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 7: launch_fwd_t<7>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    default: launch_fwd_t<8>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+  }
   SJ_LAUNCH_CHECK("rmsnorm_t");
   return SJ_OK;
 }
@@ -420,10 +463,19 @@ extern "C" int sj_rmsnorm_bwd_p(void* stream, const uint16_t* x, const uint16_t*
                      workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
   const long groups = (rows + TR - 1) / TR;
-  const size_t lds = 2 * sizeof(bf16_t) * TR * (size_t)d + 4 * sizeof(float) * (size_t)d;
-  hipLaunchKernelGGL(k_rms_bwd_p, dim3((unsigned)groups), dim3(NT), lds, s, (const bf16_t*)x, (const bf16_t*)w, dy,
-                     dx_acc, dx, (bf16_t*)dx_hi, (bf16_t*)dx_lo, (bf16_t*)dx_t_hi, (bf16_t*)dx_t_lo,
-                     (float*)workspace, rows, d, ldt, eps);
+  const size_t lds = 2 * sizeof(bf16_t) * TR * (size_t)d + sizeof(float) * TR * (size_t)d;
+  float* partial = (float*)workspace;
+  const unsigned blocks = (unsigned)groups;
+  switch ((d / 2 + 63) / 64) {
+    case 1: launch_bwd_p<1>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 2: launch_bwd_p<2>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 3: launch_bwd_p<3>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 4: launch_bwd_p<4>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 5: launch_bwd_p<5>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 6: launch_bwd_p<6>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 7: launch_bwd_p<7>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    default: launch_bwd_p<8>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+  }
   hipLaunchKernelGGL(k_rms_reduce, dim3((unsigned)((d + 31) / 32)), dim3(NT), 0, s, (const float*)workspace, dw,
                      groups, d);
   SJ_LAUNCH_CHECK("rmsnorm_backward_p");
