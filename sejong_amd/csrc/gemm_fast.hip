@@ -299,20 +299,37 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   }
 
   // ------------------------------------------------------------ epilogue
-  // acc[q][i][j][r] = C[m0 + wm*WM + 16i + 4*(lane/16) + r][n0 + wn*WN + 16j + lane%16]
+  // acc[q][i][j][r] = C[m0 + wm*WM + 16i + 4*(lane/16) + r][n0 + wn*WN + 16j + lane%16].
+  // Phase 1: every lane applies the epilogue math to its values and leaves
+  // the results in LDS tiles (the pipeline buffers are free now).  Phase 2:
+  // the block writes each tile out in 16-byte chunks along rows (normal
+  // outputs) or along columns (transposed outputs), so every global store
+  // is a full vector and neighbouring lanes fill whole lines.
+  block_barrier();  // every wave has finished reading the last stage
+  constexpr int TLD = BN + 8;          // bf16 tile row stride (elements)
+  constexpr int TP = BM * TLD;         // bf16 tile size (elements)
+  constexpr int TLDF = BN + 4;         // fp32 tile row stride
+  constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : 1;
+  constexpr bool F32T = EPI == E_PARTIAL || EPI == E_STORE;  // fp32 tile unless c_bf16
+  static_assert((size_t)NTILE * TP * 2 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tiles exceed LDS");
+  static_assert((size_t)BM * TLDF * 4 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tile exceeds LDS");
+  bf16_t* T = lds;
+  float* TF = (float*)lds;
+  const bool f32out = F32T && !p.c_bf16;
   const int cc = lane & 15;
 #pragma unroll
   for (int i = 0; i < MB; i++) {
-    const long mb = m0 + wm * WM + i * 16 + fg * 4;  // first of this lane's 4 rows
+    const int rl = wm * WM + i * 16 + fg * 4;  // tile row of this lane's first value
+    const long mb = m0 + rl;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-      const long ncol = n0 + wn * WN + j * 16 + cc;
+      const int cl = wn * WN + j * 16 + cc;
+      const long ncol = n0 + cl;
       const long nloc = ncol - p.seg_n[seg];
       const bool colok = ncol < p.N;
       float v[4] = {acc[0][i][j][0], acc[0][i][j][1], acc[0][i][j][2], acc[0][i][j][3]};
       if constexpr (EPI == E_SWIGLU_BWD) {
         // v = dH; dG = dH*u*s*(1+g(1-s)), dU = dH*g*s  (kernels.py:95-101)
-        float dg[4], du[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const long m = mb + r;
@@ -321,90 +338,184 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
             g = bf2f(p.gin[m * p.ldgu + ncol]);
             u = bf2f(p.uin[m * p.ldgu + ncol]);
           }
-          const float s = sigm(g);
-          dg[r] = v[r] * u * s * (1.f + g * (1.f - s));
-          du[r] = v[r] * g * s;
-          if (m < p.M && colok) {
-            bf16_t h, l;
-            split_bf(dg[r], h, l);
-            ((bf16_t*)p.c[0])[m * p.ldc[0] + ncol] = h;
-            ((bf16_t*)p.c[1])[m * p.ldc[0] + ncol] = l;
-            split_bf(du[r], h, l);
-            ((bf16_t*)p.c[0])[m * p.ldc[0] + p.F + ncol] = h;
-            ((bf16_t*)p.c[1])[m * p.ldc[0] + p.F + ncol] = l;
-          }
-        }
-        if (colok && mb + 4 <= p.M) {  // transposed planes [2F][M]
-          put4_split((bf16_t*)p.c[2] + ncol * p.ldc[2] + mb, (bf16_t*)p.c[3] + ncol * p.ldc[2] + mb, dg);
-          put4_split((bf16_t*)p.c[2] + (p.F + ncol) * p.ldc[2] + mb, (bf16_t*)p.c[3] + (p.F + ncol) * p.ldc[2] + mb,
-                     du);
-        } else if (colok) {
-          for (int r = 0; r < 4; r++)
-            if (mb + r < p.M) {
-              bf16_t h, l;
-              split_bf(dg[r], h, l);
-              ((bf16_t*)p.c[2])[ncol * p.ldc[2] + mb + r] = h;
-              ((bf16_t*)p.c[3])[ncol * p.ldc[2] + mb + r] = l;
-              split_bf(du[r], h, l);
-              ((bf16_t*)p.c[2])[(p.F + ncol) * p.ldc[2] + mb + r] = h;
-              ((bf16_t*)p.c[3])[(p.F + ncol) * p.ldc[2] + mb + r] = l;
-            }
+          const float sg = sigm(g);
+          const float dg = v[r] * u * sg * (1.f + g * (1.f - sg));
+          const float du = v[r] * g * sg;
+          bf16_t h, l;
+          split_bf(dg, h, l);
+          T[(rl + r) * TLD + cl] = h;
+          T[TP + (rl + r) * TLD + cl] = l;
+          split_bf(du, h, l);
+          T[2 * TP + (rl + r) * TLD + cl] = h;
+          T[3 * TP + (rl + r) * TLD + cl] = l;
         }
       } else if constexpr (EPI == E_GATEUP) {
-        float hv[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const long m = mb + r;
           const float g = round_bf(v[r]);
           const float u = round_bf(acc[1][i][j][r]);
-          hv[r] = g * sigm(g) * u;
-          if (m < p.M && colok) {
-            const long idx = m * p.ldc[0] + ncol;
-            ((bf16_t*)p.c[0])[idx] = f2bf(g);
-            ((bf16_t*)p.c[1])[idx] = f2bf(u);
-            ((bf16_t*)p.c[2])[idx] = f2bf(hv[r]);
-          }
+          T[(rl + r) * TLD + cl] = f2bf(g);
+          T[TP + (rl + r) * TLD + cl] = f2bf(u);
+          T[2 * TP + (rl + r) * TLD + cl] = f2bf(g * sigm(g) * u);
         }
-        if (p.c[3] && colok) {  // h^T [F][M]
-          if (mb + 4 <= p.M)
-            put4((bf16_t*)p.c[3] + ncol * p.ldc[3] + mb, hv);
-          else
-            for (int r = 0; r < 4; r++)
-              if (mb + r < p.M) ((bf16_t*)p.c[3])[ncol * p.ldc[3] + mb + r] = f2bf(hv[r]);
+      } else if constexpr (EPI == E_QKV) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) T[(rl + r) * TLD + cl] = f2bf(v[r]);  // RoPE is applied in phase 2
+      } else if constexpr (EPI == E_RESID) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) T[(rl + r) * TLD + cl] = f2bf(v[r]);  // round_bf(v), added in phase 2
+      } else {  // E_STORE / E_PARTIAL
+        if (f32out) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) TF[(rl + r) * TLDF + cl] = v[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; r++) T[(rl + r) * TLD + cl] = f2bf(v[r]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2
+  const int tid = threadIdx.x;
+  // rows: 8 bf16 of tile row r, cols c8..c8+7 -> dst row m, col n
+  auto rows_bf16 = [&](const bf16_t* t, auto dst_of) {
+    constexpr int CPR = BN / 8;
+    for (int q = tid; q < BM * CPR; q += NT) {
+      const int r = q / CPR, c8 = (q % CPR) * 8;
+      const long m = m0 + r, n = n0 + c8;
+      if (m >= p.M || n >= p.N) continue;
+      const u32x4 val = *(const u32x4*)(t + r * TLD + c8);
+      dst_of(m, n, val, t + r * TLD + c8);
+    }
+  };
+  // columns: 8 rows of tile column c -> transposed dst[n][m..m+7]
+  auto cols_bf16 = [&](const bf16_t* t, bf16_t* dst, long ldt) {
+    constexpr int RPC = BM / 8;
+    for (int q = tid; q < BN * RPC; q += NT) {
+      const int c = q / RPC, r8 = (q % RPC) * 8;
+      const long n = n0 + c, m = m0 + r8;
+      if (n >= p.N || m >= p.M) continue;
+      bf16_t v8[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) v8[i] = t[(r8 + i) * TLD + c];
+      bf16_t* d = dst + n * ldt + m;
+      if (m + 8 <= p.M && (((uintptr_t)d & 15) == 0)) {
+        *(u32x4*)d = u32x4{pack2(v8[0], v8[1]), pack2(v8[2], v8[3]), pack2(v8[4], v8[5]), pack2(v8[6], v8[7])};
+      } else {
+        for (int i = 0; i < 8; i++)
+          if (m + i < p.M) d[i] = v8[i];
+      }
+    }
+  };
+  // plain bf16 store of a chunk at d (8 values, n..n+7 of a row)
+  auto put8 = [&](bf16_t* d, long n, const u32x4& val, const bf16_t* src) {
+    if (n + 8 <= p.N && (((uintptr_t)d & 15) == 0)) {
+      *(u32x4*)d = val;
+    } else {
+      for (int i = 0; i < 8; i++)
+        if (n + i < p.N) d[i] = src[i];
+    }
+  };
+
+  if constexpr (EPI == E_SWIGLU_BWD) {
+    bf16_t* c0 = (bf16_t*)p.c[0];
+    bf16_t* c1 = (bf16_t*)p.c[1];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; t4++) {
+      bf16_t* base = (t4 & 1) ? c1 : c0;
+      const long coloff = (t4 >> 1) ? p.F : 0;
+      rows_bf16(T + t4 * TP, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+        put8(base + m * p.ldc[0] + coloff + n, n, val, src);
+      });
+      bf16_t* tb = (t4 & 1) ? (bf16_t*)p.c[3] : (bf16_t*)p.c[2];
+      cols_bf16(T + t4 * TP, tb + coloff * p.ldc[2], p.ldc[2]);
+    }
+  } else if constexpr (EPI == E_GATEUP) {
+#pragma unroll
+    for (int t3 = 0; t3 < 3; t3++) {
+      bf16_t* base = (bf16_t*)p.c[t3];
+      rows_bf16(T + t3 * TP, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+        put8(base + m * p.ldc[0] + n, n, val, src);
+      });
+    }
+    if (p.c[3]) cols_bf16(T + 2 * TP, (bf16_t*)p.c[3], p.ldc[3]);
+  } else if constexpr (EPI == E_QKV) {
+    // RoPE on the stored (bf16-rounded) q and k values: pairs (2i, 2i+1) of
+    // a chunk rotate by the angle of (token position, pair index), cos/sin
+    // read from the table as one run per chunk (kernels.py:103-113)
+    const int T32 = (int)p.rope_t, hd = (int)p.head_dim;
+    rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+      int sg = 0;
+      for (int s2 = 1; s2 < 3; s2++)
+        if (s2 < p.nseg && n >= p.seg_n[s2]) sg = s2;
+      const long nl = n - p.seg_n[sg];
+      u32x4 o = val;
+      bf16_t rot[8];
+      if (n < p.rope_cols) {
+        const int pos = (int)((unsigned)m % (unsigned)T32);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int pair = ((int)(nl + 2 * k) % hd) >> 1;
+          const float2 cs = *(const float2*)(p.rope + 2 * (pos * (hd >> 1) + pair));
+          const float a = bf2f((bf16_t)(val[k] & 0xffffu)), b = bf2f((bf16_t)(val[k] >> 16));
+          rot[2 * k] = f2bf(a * cs.x - b * cs.y);
+          rot[2 * k + 1] = f2bf(b * cs.x + a * cs.y);
+          o[k] = pack2(rot[2 * k], rot[2 * k + 1]);
         }
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const long m = mb + r;
-          if constexpr (EPI == E_QKV) {
-            const float a = round_bf(v[r]);
-            const float b = __shfl_xor(a, 1, 64);
-            float outv = a;
-            if (ncol < p.rope_cols) {
-              const long pos = m % p.rope_t;
-              const long pair = (nloc % p.head_dim) >> 1;
-              const float2 cs = *(const float2*)(p.rope + 2 * (pos * (p.head_dim >> 1) + pair));
-              outv = (cc & 1) ? (b * cs.y + a * cs.x) : (a * cs.x - b * cs.y);
-            }
-            if (m < p.M && colok) ((bf16_t*)p.c[seg])[m * p.ldc[seg] + nloc] = f2bf(outv);
-          } else if constexpr (EPI == E_RESID) {
-            if (m < p.M && colok) {
-              const float a = round_bf(v[r]);
-              ((bf16_t*)p.c[0])[m * p.ldc[0] + ncol] = f2bf(bf2f(p.r[m * p.ldr + ncol]) + a);
-            }
-          } else if constexpr (EPI == E_PARTIAL) {
-            if (m < p.M && colok) p.partial[((long)tz * p.M + m) * p.N + ncol] = v[r];
-          } else {  // E_STORE
-            if (m < p.M && colok) {
-              const long idx = coff + m * p.ldc[0] + ncol;
-              if (p.c_bf16)
-                ((bf16_t*)p.c[0])[idx] = f2bf(v[r]);
-              else if (p.accumulate)
-                ((float*)p.c[0])[idx] += v[r];
-              else
-                ((float*)p.c[0])[idx] = v[r];
-            }
+        for (int k = 0; k < 8; k++) rot[k] = src[k];
+      }
+      put8((bf16_t*)p.c[sg] + m * p.ldc[sg] + nl, n, o, rot);
+    });
+  } else if constexpr (EPI == E_RESID) {
+    rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+      const bf16_t* rr = p.r + m * p.ldr + n;
+      bf16_t* d = (bf16_t*)p.c[0] + m * p.ldc[0] + n;
+      if (n + 8 <= p.N && (((uintptr_t)d & 15) == 0) && (((uintptr_t)rr & 15) == 0)) {
+        const u32x4 rv = *(const u32x4*)rr;
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float a0 = bf2f((bf16_t)(rv[k] & 0xffffu)) + bf2f((bf16_t)(val[k] & 0xffffu));
+          const float a1 = bf2f((bf16_t)(rv[k] >> 16)) + bf2f((bf16_t)(val[k] >> 16));
+          o[k] = pack2(f2bf(a0), f2bf(a1));
+        }
+        *(u32x4*)d = o;
+      } else {
+        for (int i = 0; i < 8; i++)
+          if (n + i < p.N) d[i] = f2bf(bf2f(rr[i]) + bf2f(src[i]));
+      }
+    });
+  } else {  // E_STORE / E_PARTIAL
+    if (!f32out) {
+      rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+        put8((bf16_t*)p.c[0] + coff + m * p.ldc[0] + n, n, val, src);
+      });
+    } else {
+      constexpr int CPR = BN / 4;
+      float* dst0 = EPI == E_PARTIAL ? p.partial + (long)tz * p.M * p.N : (float*)p.c[0] + coff;
+      const long ldd = EPI == E_PARTIAL ? p.N : p.ldc[0];
+      const bool acc_out = EPI == E_STORE && p.accumulate;
+      for (int q = tid; q < BM * CPR; q += NT) {
+        const int r = q / CPR, c4 = (q % CPR) * 4;
+        const long m = m0 + r, n = n0 + c4;
+        if (m >= p.M || n >= p.N) continue;
+        const float4 val = *(const float4*)(TF + r * TLDF + c4);
+        float* d = dst0 + m * ldd + n;
+        if (n + 4 <= p.N && (((uintptr_t)d & 15) == 0)) {
+          if (acc_out) {
+            const float4 o = *(const float4*)d;
+            *(float4*)d = make_float4(o.x + val.x, o.y + val.y, o.z + val.z, o.w + val.w);
+          } else {
+            *(float4*)d = val;
           }
+        } else {
+          const float vv[4] = {val.x, val.y, val.z, val.w};
+          for (int k = 0; k < 4; k++)
+            if (n + k < p.N) d[k] = acc_out ? d[k] + vv[k] : vv[k];
         }
       }
     }
@@ -482,7 +593,51 @@ void pick(long M, long N, int& bm, int& bn) {
   bm = 64; bn = 64;
 }
 
+// Split-K count: enough slices for ~2 workgroups per CU when the tiles
+// alone do not fill the chip.  SJ_GEMM_SPLITS=<n> overrides it (sweeps).
+int splits_for(long M, long N, long K, int bm, int bn);
+
+// Tile and split-K plan of sj_gemm_planes (measured on the cfg2 shapes):
+// dW-shaped products (small output, K >= 2048) take 4 K slices and the
+// largest tile that still gives >= 144 workgroups; split-A products (dX)
+// with K <= 1024 and N a multiple of 128 take 64x128 tiles when those
+// cover half the CUs; the rest use pick().
+void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
+  const long cu = cus();
+  const char* et = getenv("SJ_GEMM_TILE");
+  const char* es = getenv("SJ_GEMM_SPLITS");
+  if (!et && !es) {
+    if (tiles(M, N, 64, 64) < cu && K >= 2048) {
+      splits = K / 256 < 4 ? (int)(K / 256) : 4;
+      const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+      for (const auto& c : cand)
+        if (tiles(M, N, c[0], c[1]) * splits >= 144 || (c[0] == 64 && c[1] == 64)) {
+          bm = c[0];
+          bn = c[1];
+          return;
+        }
+    }
+    if (pa == 2 && K <= 1024 && N % 128 == 0 && tiles(M, N, 64, 128) * 2 >= cu) {
+      bm = 64;
+      bn = 128;
+      splits = splits_for(M, N, K, bm, bn);
+      return;
+    }
+  }
+  pick(M, N, bm, bn);
+  splits = splits_for(M, N, K, bm, bn);
+}
+
 int splits_for(long M, long N, long K, int bm, int bn) {
+  static int ov = -1;
+  if (ov < 0) {
+    const char* e = getenv("SJ_GEMM_SPLITS");
+    ov = e ? atoi(e) : 0;
+  }
+  if (ov > 0) {
+    long s = ov < K / 64 ? ov : K / 64;
+    return s < 1 ? 1 : (int)s;
+  }
   const long t = tiles(M, N, bm, bn), cu = cus();
   if (t >= cu || K < 1024) return 1;
   long s = (2 * cu + t - 1) / t;
@@ -568,10 +723,15 @@ int gemm_fast_prepare() {
 // ================================================================ C ABI
 
 extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
-  int bm, bn;
-  pick(M, N, bm, bn);
-  int s = splits_for(M, N, K, bm, bn);
-  return s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
+  // the larger of the plans for a split and an unsplit A operand
+  size_t need = 0;
+  for (int pa = 1; pa <= 2; pa++) {
+    int bm, bn, s;
+    plan(M, N, K, pa, bm, bn, s);
+    const size_t b = s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
+    need = b > need ? b : need;
+  }
+  return need;
 }
 
 extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
@@ -594,9 +754,8 @@ extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16
   p.M = M; p.N = N; p.K = K;
   p.c[0] = c; p.ldc[0] = ldc; p.c_bf16 = c_dtype == SJ_BF16; p.accumulate = accumulate;
   const int pa = a_lo ? 2 : 1, pb = b_lo ? 2 : 1;
-  int bm, bn;
-  pick(M, N, bm, bn);
-  int splits = splits_for(M, N, K, bm, bn);
+  int bm, bn, splits;
+  plan(M, N, K, pa, bm, bn, splits);
   if (splits > 1 && workspace && workspace_bytes >= sizeof(float) * (size_t)splits * M * N) {
     long kchunk = (K + splits - 1) / splits;
     kchunk = (kchunk + BK - 1) / BK * BK;
@@ -624,7 +783,8 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
   SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D &&
                  ldo >= N + 2 * KV && N % 64 == 0 && KV % 64 == 0 && ok16(x) && ok16(wqkv_t),
              "project_qkv (transposed weights): shape/alignment");
-  if (rope_table) SJ_REQUIRE(rope_t > 0 && head_dim > 0 && head_dim % 2 == 0 && N % head_dim == 0 && KV % head_dim == 0,
+  if (rope_table) SJ_REQUIRE(rope_t > 0 && head_dim > 0 && head_dim % 2 == 0 && N % head_dim == 0 && KV % head_dim == 0 &&
+                                 M < (1L << 31),
                              "project_qkv rope: t %ld head_dim %ld", rope_t, head_dim);
   if (M == 0) return SJ_OK;
   FParams p = {};
@@ -639,9 +799,11 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
   p.M = M; p.N = N + 2 * KV; p.K = D; p.c_bf16 = 1;
   p.rope = rope_table; p.rope_t = rope_t > 0 ? rope_t : 1; p.head_dim = head_dim > 0 ? head_dim : 2;
   p.rope_cols = rope_table ? N + KV : 0;
-  int bm, bn;
-  pick(M, N + 2 * KV, bm, bn);
-  if (N % bn || KV % bn) bn = 64;
+  int bm = 64, bn = 64;  // measured best at the cfg2 shape
+  if (getenv("SJ_GEMM_TILE")) {
+    pick(M, N + 2 * KV, bm, bn);
+    if (N % bn || KV % bn) bn = 64;
+  }
   int st = launch_planes<E_QKV>((hipStream_t)stream, p, 1, 1, bm, bn, 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("project_qkv");
@@ -707,8 +869,8 @@ extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const u
   p.c[0] = dgu_hi; p.c[1] = dgu_lo; p.c[2] = dgu_t_hi; p.c[3] = dgu_t_lo; p.ldc[0] = lddgu; p.ldc[2] = lddgu_t;
   p.gin = (const bf16_t*)g; p.uin = (const bf16_t*)u; p.ldgu = ldgu; p.F = F;
   p.M = M; p.N = F; p.K = D;
-  int bm, bn;
-  pick(M, F, bm, bn);
+  int bm, bn, splits;
+  plan(M, F, D, 2, bm, bn, splits);
   int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("swiglu_backward");
