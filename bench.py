@@ -31,7 +31,7 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
 # single-kernel ops and the kernel each one launches (rocprofv3 names)
-OP_KERNEL = {"attention_bwd_dkv": "k_attn_dkv", "attention_bwd_dq": "k_attn_dq", "attention_fwd": "k_attn_fwd",
+OP_KERNEL = {"attention_bwd_dkv": "k_attn_dkv_h", "attention_bwd_kv_reduce": "k_attn_kv_reduce", "attention_bwd_dq": "k_attn_dq", "attention_fwd": "k_attn_fwd",
              "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd",
              "cross_entropy": "k_cross_entropy"}
 
@@ -59,6 +59,8 @@ def op_work(op: str, mc, tc):
         # the forward's size / 2); dK/dV recomputes S and dP, forms dV, dK (4)
         "attention_bwd_dq": ("flop", 1.5 * attn_fwd),
         "attention_bwd_dkv": ("flop", 2.0 * attn_fwd),
+        # group sum of the per-head fp32 dK|dV partials, planes out
+        "attention_bwd_kv_reduce": ("byte", (mc.heads // mc.kv) * M * 2 * J * 4 + 4 * M * 2 * J * 2),
         "mirror_transpose": ("byte", 2 * 2 * mc.layers * (d * (d + 2 * J) + d * d + 3 * d * F)),
         "attn_out_residual": ("flop", 2 * M * d * d),
         "attn_out_dx": ("flop", 2 * M * d * d),

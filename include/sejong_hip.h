@@ -253,8 +253,10 @@ int sj_attention_bwd(void *stream, const void *q, long ldq, const void *k, long 
  * dQ|dK|dV (inverse RoPE applied to dQ, dK) as hi/lo bf16 planes: normal
  * g [B*T][ldg] with dQ in columns [0, hq*64), dK then dV after it, and
  * transposed g_t [(hq+2hk)*64][ldgt] -- the operands of the QKV
- * projection's dX and dW GEMMs.  Both need t % 4 == 0 when batch > 1 and
- * ldot, ldgt multiples of 4. */
+ * projection's dX and dW GEMMs.  Both need t % 4 == 0 when batch > 1;
+ * ldot a multiple of 4, ldgt of 8.  The backward sums dK / dV over the
+ * group's query heads through `workspace`
+ * (sj_attention_bwd_p_workspace_bytes) in a fixed order. */
 int sj_attention_fwd_t(void *stream, const uint16_t *q, long ldq, const uint16_t *k, long ldk,
                        const uint16_t *v, long ldv, uint16_t *o, long ldo, float *lse, uint16_t *o_t,
                        long ldot, long batch, long t, long hq, long hk, long head_dim);
@@ -262,7 +264,8 @@ int sj_attention_bwd_p(void *stream, const uint16_t *q, long ldq, const uint16_t
                        const uint16_t *v, long ldv, const uint16_t *o, long ldo, const float *lse,
                        const float *dout, long lddo, float *delta, long batch, long t, long hq, long hk,
                        long head_dim, const float *rope_table, uint16_t *g_hi, uint16_t *g_lo, long ldg,
-                       uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt);
+                       uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt, void *workspace, size_t workspace_bytes);
+size_t sj_attention_bwd_p_workspace_bytes(long batch, long t, long hq, long hk, long head_dim);
 
 /* ---------------------------------------------------- Mixture of experts
  * The MoE FFN of Block::apply (crates/sejong-model/src/architecture.rs:

@@ -90,7 +90,8 @@ SIGNATURES = {
     "sj_moe_gemm_dw": (_I, [_P, _P, _L, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _L]),
     "sj_attention_fwd_t": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _L]),
     "sj_attention_bwd_p": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P,
-                                _P, _P, _L, _P, _P, _L]),
+                                _P, _P, _L, _P, _P, _L, _P, _S]),
+    "sj_attention_bwd_p_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
     "sj_gemm_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_gemm": (_I, [_P, _I, _I, _L, _L, _L, _P, _I, _L, _P, _I, _L, _P, _I, _L, _I, _P, _S]),
     "sj_qkv_fwd": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _L, _L, _P, _L, _P, _L, _P, _L, _I,

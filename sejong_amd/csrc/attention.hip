@@ -341,12 +341,39 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
   for (int d = 0; d < 4; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const bf16_t* kbase = a.k + b * T * a.ldk + kvh * DH;
   const bf16_t* vbase = a.v + b * T * a.ldv + kvh * DH;
+  // the next key block is fetched into registers while this one computes
+  u32x4 pk[2], pv[2];
+  auto fetch = [&](long kb) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      const long row = kb * QB + r;
+      pk[p] = pv[p] = u32x4{0, 0, 0, 0};
+      if (row < T) {
+        pk[p] = *(const u32x4*)(kbase + row * a.ldk + c8);
+        pv[p] = *(const u32x4*)(vbase + row * a.ldv + c8);
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      *(u32x4*)(sK + r * LS + c8) = pk[p];
+      *(u32x4*)(sV + r * LS + c8) = pv[p];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sKt[(c8 + 2 * i) * LS + r] = (bf16_t)(pk[p][i] & 0xffffu);
+        sKt[(c8 + 2 * i + 1) * LS + r] = (bf16_t)(pk[p][i] >> 16);
+      }
+    }
+  };
+  fetch(0);
   for (long kb = 0; kb <= qb; kb++) {
     __syncthreads();
-    stage_bf16(sK, kbase, a.ldk, kb * QB, T, 0);
-    stage_bf16(sV, vbase, a.ldv, kb * QB, T, 0);
-    stage_bf16_t(sKt, kbase, a.ldk, kb * QB, T, 0);
+    commit();
     __syncthreads();
+    if (kb < qb) fetch(kb + 1);
     float ds[4][4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++) {
@@ -525,6 +552,244 @@ __global__ __launch_bounds__(256) void k_attn_dkv(AttnArgs a) {
     for (int d = 0; d < 4; d++) {
       store_planes(a.pk, a.tk, a.ldp, a.ldtp, b * T + k0, kvh * DH + 16 * d + j, kout[d], nv);
       store_planes(a.pv, a.tv, a.ldp, a.ldtp, b * T + k0, kvh * DH + 16 * d + j, vout[d], nv);
+    }
+  }
+}
+
+// --------------------------------------- backward dKV, one query head each
+// MFMA-layout path.  Workgroup (key block, query head, batch): the dK / dV
+// contribution of ONE query head of the group, fp32, into
+// part[gi][row][dK | dV] (gi = head index inside its group); the next query
+// block is fetched into registers while the current one computes, and the
+// transposed LDS tiles (Q^T, dO^T) are written from those registers.  The
+// group sum (fixed order), the inverse RoPE of dK and the plane split happen
+// in k_attn_kv_reduce.  3x the workgroups of k_attn_dkv and a third of the
+// serial loop, for one extra pass over 3 * B*T * 2*KV floats.
+__global__ __launch_bounds__(256) void k_attn_dkv_h(AttnArgs a, float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) bf16_t smem[6 * QB * LS];
+  bf16_t* sQ = smem;
+  bf16_t* sQt = smem + QB * LS;
+  bf16_t* sDh = smem + 2 * QB * LS;
+  bf16_t* sDl = smem + 3 * QB * LS;
+  bf16_t* sDth = smem + 4 * QB * LS;
+  bf16_t* sDtl = smem + 5 * QB * LS;
+  __shared__ float sL[QB], sD[QB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const long kb = blockIdx.x;
+  const long h = blockIdx.y, b = blockIdx.z;
+  const long T = a.T;
+  const long group = a.HQ / a.HK;
+  const long kvh = h / group, gi = h % group;
+  const long krow0 = kb * QB + wave * 16;
+  const long myk = krow0 + j;
+  const float sc = 0.125f * LOG2E;
+
+  bf16x8 kf[2], vf[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    u32x4 kv = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
+    if (myk < T) {
+      kv = *(const u32x4*)(a.k + (b * T + myk) * a.ldk + kvh * DH + 32 * c + 8 * g);
+      vv = *(const u32x4*)(a.v + (b * T + myk) * a.ldv + kvh * DH + 32 * c + 8 * g);
+    }
+    kf[c] = as_bf8(kv);
+    vf[c] = as_bf8(vv);
+  }
+  f32x4 dk[4], dv[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bf16_t* qbase = a.q + b * T * a.ldq + h * DH;
+  const float* dbase = a.dout + b * T * a.lddo + h * DH;
+  u32x4 pq[2];
+  float4 pd[2][2];
+  float pl = 0.f, pdl = 0.f;
+  auto fetch = [&](long qb) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      const long row = qb * QB + r;
+      pq[p] = u32x4{0, 0, 0, 0};
+      pd[p][0] = pd[p][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < T) {
+        pq[p] = *(const u32x4*)(qbase + row * a.ldq + c8);
+        pd[p][0] = *(const float4*)(dbase + row * a.lddo + c8);
+        pd[p][1] = *(const float4*)(dbase + row * a.lddo + c8 + 4);
+      }
+    }
+    if (threadIdx.x < QB) {
+      const long q = qb * QB + threadIdx.x;
+      pl = q < T ? a.lse[(b * T + q) * a.HQ + h] * LOG2E : 0.f;
+      pdl = q < T ? a.delta[(b * T + q) * a.HQ + h] : 0.f;
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      *(u32x4*)(sQ + r * LS + c8) = pq[p];
+      float v8[8] = {pd[p][0].x, pd[p][0].y, pd[p][0].z, pd[p][0].w, pd[p][1].x, pd[p][1].y, pd[p][1].z, pd[p][1].w};
+      bf16_t hh[8], ll[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) split_bf(v8[i], hh[i], ll[i]);
+      *(u32x4*)(sDh + r * LS + c8) = u32x4{pack2(hh[0], hh[1]), pack2(hh[2], hh[3]), pack2(hh[4], hh[5]), pack2(hh[6], hh[7])};
+      *(u32x4*)(sDl + r * LS + c8) = u32x4{pack2(ll[0], ll[1]), pack2(ll[2], ll[3]), pack2(ll[4], ll[5]), pack2(ll[6], ll[7])};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sQt[(c8 + 2 * i) * LS + r] = (bf16_t)(pq[p][i] & 0xffffu);
+        sQt[(c8 + 2 * i + 1) * LS + r] = (bf16_t)(pq[p][i] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        sDth[(c8 + i) * LS + r] = hh[i];
+        sDtl[(c8 + i) * LS + r] = ll[i];
+      }
+    }
+    if (threadIdx.x < QB) {
+      sL[threadIdx.x] = pl;
+      sD[threadIdx.x] = pdl;
+    }
+  };
+
+  const long nqb = (T + QB - 1) / QB;
+  fetch(kb);
+  for (long qb = kb; qb < nqb; qb++) {
+    __syncthreads();
+    commit();
+    __syncthreads();
+    if (qb + 1 < nqb) fetch(qb + 1);
+    float pp[4][4], ds[4][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        st = mfma(as_bf8(*(const u32x4*)(sQ + (sb * 16 + j) * LS + 32 * c + 8 * g)), kf[c], st);
+        dp = mfma(as_bf8(*(const u32x4*)(sDh + (sb * 16 + j) * LS + 32 * c + 8 * g)), vf[c], dp);
+        dp = mfma(as_bf8(*(const u32x4*)(sDl + (sb * 16 + j) * LS + 32 * c + 8 * g)), vf[c], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        int ql = sb * 16 + 4 * g + r;
+        long q = qb * QB + ql;
+        float p = (q >= myk && q < T && myk < T) ? exp2f(st[r] * sc - sL[ql]) : 0.f;
+        pp[sb][r] = p;
+        ds[sb][r] = p * (dp[r] - sD[ql]) * 0.125f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      float p8[8] = {pp[2 * c][0], pp[2 * c][1], pp[2 * c][2], pp[2 * c][3],
+                     pp[2 * c + 1][0], pp[2 * c + 1][1], pp[2 * c + 1][2], pp[2 * c + 1][3]};
+      float s8[8] = {ds[2 * c][0], ds[2 * c][1], ds[2 * c][2], ds[2 * c][3],
+                     ds[2 * c + 1][0], ds[2 * c + 1][1], ds[2 * c + 1][2], ds[2 * c + 1][3]};
+      bf16x8 ph, plo, sh, sl;
+      split8(p8, ph, plo);
+      split8(s8, sh, sl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const int ra = 32 * c + 4 * g, rb = 32 * c + 16 + 4 * g;
+        bf16x8 doh = ld_perm(sDth + (16 * d + j) * LS, ra, rb);
+        bf16x8 dol = ld_perm(sDtl + (16 * d + j) * LS, ra, rb);
+        bf16x8 qt = ld_perm(sQt + (16 * d + j) * LS, ra, rb);
+        dv[d] = mfma(ph, doh, dv[d]);
+        dv[d] = mfma(ph, dol, dv[d]);
+        dv[d] = mfma(plo, doh, dv[d]);
+        dk[d] = mfma(sh, qt, dk[d]);
+        dk[d] = mfma(sl, qt, dk[d]);
+      }
+    }
+  }
+  // stage the block's dK | dV (64 keys x 128 fp32) in LDS, then row stores
+  __syncthreads();
+  constexpr int OLD = 2 * DH + 4;
+  float* so = (float*)smem;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int kr = wave * 16 + 4 * g + r;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      so[kr * OLD + 16 * d + j] = dk[d][r];
+      so[kr * OLD + DH + 16 * d + j] = dv[d][r];
+    }
+  }
+  __syncthreads();
+  const long KV = a.HK * DH, M = a.T * (long)gridDim.z;
+  for (int q = threadIdx.x; q < QB * (2 * DH / 4); q += 256) {
+    const int kr = q / (2 * DH / 4), c4 = (q % (2 * DH / 4)) * 4;
+    const long key = kb * QB + kr;
+    if (key >= T) continue;
+    const long col = c4 < DH ? kvh * DH + c4 : KV + kvh * DH + (c4 - DH);
+    *(float4*)(part + (gi * M + b * T + key) * 2 * KV + col) = *(const float4*)(so + kr * OLD + c4);
+  }
+}
+
+// dK = sum over the group's query heads (fixed order) with the inverse RoPE,
+// dV = sum; both as hi/lo planes, normal (columns N.. of the [rows][ldg]
+// gradient) and transposed (rows N.. of [.][ldgt]).  Thread: one column pair
+// of dK or dV over 8 rows of a 16-row block (XCD-contiguous block order, so
+// the 16-byte transposed pieces of neighbouring blocks meet in one L2).
+constexpr int KVR_ROWS = 8;
+__global__ __launch_bounds__(256) void k_attn_kv_reduce(const float* __restrict__ part, int group, long M, long T,
+                                                        long N, long KV, const float* __restrict__ rope,
+                                                        bf16_t* __restrict__ gh, bf16_t* __restrict__ gl, long ldg,
+                                                        bf16_t* __restrict__ th, bf16_t* __restrict__ tl, long ldgt) {
+  const long nb = gridDim.x, bx = blockIdx.x;
+  const long xcd = bx & 7, local = bx >> 3, q8 = nb >> 3, r8 = nb & 7;
+  const long row0 = (xcd * q8 + (xcd < r8 ? xcd : r8) + local) * (2 * KVR_ROWS) + (threadIdx.x >> 7) * KVR_ROWS;
+  const int sel = (threadIdx.x >> 6) & 1;  // 0: dK, 1: dV
+  for (long pc = threadIdx.x & 63; pc < KV / 2; pc += 64) {
+    const long col = 2 * pc;
+    const long gcol = N + sel * KV + col;
+    uint32_t h0[KVR_ROWS / 2], h1[KVR_ROWS / 2], l0[KVR_ROWS / 2], l1[KVR_ROWS / 2];
+#pragma unroll
+    for (int i = 0; i < KVR_ROWS; i++) {
+      const long row = row0 + i;
+      float x = 0.f, y = 0.f;
+      if (row < M) {
+        for (int gi = 0; gi < group; gi++) {
+          const float2 v = *(const float2*)(part + ((long)gi * M + row) * 2 * KV + sel * KV + col);
+          x += v.x;
+          y += v.y;
+        }
+        if (sel == 0 && rope) {
+          const long pos = row % T;
+          const float2 cs = *(const float2*)(rope + 2 * (pos * (DH / 2) + ((col % DH) >> 1)));
+          const float xe = x * cs.x + y * cs.y, yo = y * cs.x - x * cs.y;
+          x = xe;
+          y = yo;
+        }
+      }
+      bf16_t hx, lx, hy, ly;
+      split_bf(x, hx, lx);
+      split_bf(y, hy, ly);
+      if (row < M) {
+        *(uint32_t*)(gh + row * ldg + gcol) = pack2(hx, hy);
+        *(uint32_t*)(gl + row * ldg + gcol) = pack2(lx, ly);
+      }
+      if (i & 1) {
+        h0[i >> 1] |= (uint32_t)hx << 16; h1[i >> 1] |= (uint32_t)hy << 16;
+        l0[i >> 1] |= (uint32_t)lx << 16; l1[i >> 1] |= (uint32_t)ly << 16;
+      } else {
+        h0[i >> 1] = hx; h1[i >> 1] = hy; l0[i >> 1] = lx; l1[i >> 1] = ly;
+      }
+    }
+    if (row0 + KVR_ROWS <= M) {
+      *(u32x4*)(th + gcol * ldgt + row0) = u32x4{h0[0], h0[1], h0[2], h0[3]};
+      *(u32x4*)(th + (gcol + 1) * ldgt + row0) = u32x4{h1[0], h1[1], h1[2], h1[3]};
+      *(u32x4*)(tl + gcol * ldgt + row0) = u32x4{l0[0], l0[1], l0[2], l0[3]};
+      *(u32x4*)(tl + (gcol + 1) * ldgt + row0) = u32x4{l1[0], l1[1], l1[2], l1[3]};
+    } else {
+#pragma unroll
+      for (int i = 0; i < KVR_ROWS; i++) {
+        if (row0 + i >= M) break;
+        const int sh = (i & 1) * 16;
+        th[gcol * ldgt + row0 + i] = (bf16_t)(h0[i >> 1] >> sh);
+        th[(gcol + 1) * ldgt + row0 + i] = (bf16_t)(h1[i >> 1] >> sh);
+        tl[gcol * ldgt + row0 + i] = (bf16_t)(l0[i >> 1] >> sh);
+        tl[(gcol + 1) * ldgt + row0 + i] = (bf16_t)(l1[i >> 1] >> sh);
+      }
     }
   }
 }
@@ -789,17 +1054,27 @@ extern "C" int sj_attention_fwd_t(void* stream, const uint16_t* q, long ldq, con
   return SJ_OK;
 }
 
-// parts: 1 = dQ kernel (also writes Delta), 2 = dK/dV kernel (reads Delta), 3 = both
+extern "C" size_t sj_attention_bwd_p_workspace_bytes(long batch, long t, long hq, long hk, long head_dim) {
+  if (batch <= 0 || t <= 0 || hq <= 0 || hk <= 0 || hq % hk) return 0;
+  return sizeof(float) * (size_t)(hq / hk) * (size_t)(batch * t) * (size_t)(2 * hk * head_dim);
+}
+
+// parts: 1 = dQ kernel (also writes Delta), 2 = per-head dK/dV partials
+// (reads Delta), 4 = group reduce into planes; 7 = all
 int sjh::attention_bwd_p_parts(int parts, void* stream, const uint16_t* q, long ldq, const uint16_t* k, long ldk,
                                const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
                                const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
                                long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                               uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
+                               uint16_t* gt_hi, uint16_t* gt_lo, long ldgt, void* workspace, size_t workspace_bytes) {
   SJ_REQUIRE(batch > 0 && t > 0 && hq > 0 && hk > 0 && hq % hk == 0 && head_dim == DH &&
-                 ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ldgt % 4 == 0 && lddo % 4 == 0 && (batch == 1 || t % 4 == 0) &&
-                 ((uintptr_t)dout & 15) == 0 && ((uintptr_t)gt_hi & 7) == 0 && ((uintptr_t)gt_lo & 7) == 0,
+                 ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ldgt % 8 == 0 && lddo % 4 == 0 && (batch == 1 || t % 4 == 0) &&
+                 ((uintptr_t)dout & 15) == 0 && ((uintptr_t)gt_hi & 15) == 0 && ((uintptr_t)gt_lo & 15) == 0,
              "grouped attention backward (planes): shape/alignment");
   SJ_REQUIRE(use_mfma(SJ_BF16, head_dim, 0, t, ldq, ldk, ldv, ldo, q, k, v, o), "grouped attention: alignment");
+  const size_t need = sj_attention_bwd_p_workspace_bytes(batch, t, hq, hk, head_dim);
+  if ((parts & 6) && (!workspace || workspace_bytes < need))
+    return sjh::fail(SJ_ERR_CAPACITY, "attention_backward: required %zu bytes, available %zu bytes", need,
+                     workspace_bytes);
   AttnArgs a = {};
   a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.o = (const bf16_t*)o;
   a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
@@ -818,7 +1093,14 @@ int sjh::attention_bwd_p_parts(int parts, void* stream, const uint16_t* q, long 
   hipStream_t s = (hipStream_t)stream;
   unsigned nb = (unsigned)((t + QB - 1) / QB);
   if (parts & 1) hipLaunchKernelGGL(k_attn_dq, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a);
-  if (parts & 2) hipLaunchKernelGGL(k_attn_dkv, dim3(nb, (unsigned)hk, (unsigned)batch), dim3(256), 0, s, a);
+  if (parts & 2)
+    hipLaunchKernelGGL(k_attn_dkv_h, dim3(nb, (unsigned)hq, (unsigned)batch), dim3(256), 0, s, a, (float*)workspace);
+  if (parts & 4) {
+    const long M = batch * t;
+    hipLaunchKernelGGL(k_attn_kv_reduce, dim3((unsigned)((M + 2 * KVR_ROWS - 1) / (2 * KVR_ROWS))), dim3(256), 0, s,
+                       (const float*)workspace,
+                       (int)(hq / hk), M, t, N, KV, rope_table, gh, gl, ldg, th, tl, ldgt);
+  }
   SJ_LAUNCH_CHECK("hierarchy_attention_backward_p");
   return SJ_OK;
 }
@@ -827,7 +1109,9 @@ extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, con
                                   const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
                                   const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
                                   long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                                  uint16_t* gt_hi, uint16_t* gt_lo, long ldgt) {
-  return sjh::attention_bwd_p_parts(3, stream, q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, delta, batch, t, hq,
-                                    hk, head_dim, rope_table, g_hi, g_lo, ldg, gt_hi, gt_lo, ldgt);
+                                  uint16_t* gt_hi, uint16_t* gt_lo, long ldgt, void* workspace,
+                                  size_t workspace_bytes) {
+  return sjh::attention_bwd_p_parts(7, stream, q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, delta, batch, t, hq,
+                                    hk, head_dim, rope_table, g_hi, g_lo, ldg, gt_hi, gt_lo, ldgt, workspace,
+                                    workspace_bytes);
 }

@@ -104,7 +104,7 @@ int attention_bwd_p_parts(int parts, void* stream, const uint16_t* q, long ldq, 
                           const uint16_t* v, long ldv, const uint16_t* o, long ldo, const float* lse,
                           const float* dout, long lddo, float* delta, long batch, long t, long hq, long hk,
                           long head_dim, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                          uint16_t* gt_hi, uint16_t* gt_lo, long ldgt);
+                          uint16_t* gt_hi, uint16_t* gt_lo, long ldgt, void* workspace, size_t workspace_bytes);
 }  // namespace sjh
 
 #define SJ_REQUIRE(cond, ...)                                  \

@@ -384,11 +384,11 @@ int backward(sj_model* m) {
       OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws, wsb));
       OP("attn_out_dw", sj_gemm_planes(s, d, d, M, m->ot[l], nullptr, ldt, xp[2], xp[3], ldt, G + y.wo, SJ_F32, d, 0, ws,
                                        wsb));
-      for (int part = 1; part <= 2; part++)
-        OP(part == 1 ? "attention_bwd_dq" : "attention_bwd_dkv",
+      for (int part = 1; part <= 4; part <<= 1)
+        OP(part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce",
            sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
                                       m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0],
-                                      qp[1], NQ, qp[2], qp[3], ldt));
+                                      qp[1], NQ, qp[2], qp[3], ldt, ws, wsb));
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
       OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0, ws,
                                   wsb));
@@ -609,6 +609,7 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   upd(sj_gemm_workspace_bytes(Mi, m->d, m->NQKV));
   if (m->planes) {
     upd(sj_rmsnorm_bwd_p_workspace_bytes(Mi, m->d));
+    upd(sj_attention_bwd_p_workspace_bytes(m->B, m->T, m->HQ, m->HK, m->Dh));
     upd(sj_gemm_planes_workspace_bytes(m->F, m->d, Mi));
     upd(sj_gemm_planes_workspace_bytes(m->d, 2 * m->F, Mi));
     upd(sj_gemm_planes_workspace_bytes(m->d, m->d, Mi));

@@ -200,7 +200,7 @@ def test_rmsnorm_t_and_planes(api, lib, R, D, ldt):
 
 
 @pytest.mark.parametrize("B,T,HQ,HK", [(2, 256, 6, 2), (1, 200, 4, 4)])
-def test_attention_t_and_planes(api, B, T, HQ, HK):
+def test_attention_t_and_planes(api, lib, B, T, HQ, HK):
     Dh = 64
     rng = np.random.default_rng(B * T + HQ + 5)
     M = B * T; N = HQ * Dh; KV = HK * Dh; NG = N + 2 * KV
@@ -224,13 +224,18 @@ def test_attention_t_and_planes(api, B, T, HQ, HK):
                          BF, B, T, HQ, HK, Dh, 0, tab.p)
     Gh, Gl, Th, Tl, De2 = (empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldot, "bf16"),
                            zeros(NG * ldot, "bf16"), empty(M * HQ))
+    wsa = empty(max(lib.sj_attention_bwd_p_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
     api.sj_attention_bwd_p(None, Q.p, N, K.p, KV, V.p, KV, O1.p, N, L1.p, DO.p, N, De2.p, B, T, HQ, HK, Dh, tab.p,
-                           Gh.p, Gl.p, NG, Th.p, Tl.p, ldot)
+                           Gh.p, Gl.p, NG, Th.p, Tl.p, ldot, wsa.p, wsa.nbytes)
     sync()
     np.testing.assert_array_equal(De2.host(), De.host())
     ref = np.concatenate([dQ.host().reshape(M, N), dK.host().reshape(M, KV), dV.host().reshape(M, KV)], 1)
     hi, lo = Gh.host().reshape(M, NG), Gl.host().reshape(M, NG)
-    _check_planes(hi, lo, ref)                                   # same arithmetic as the fp32 entry
+    _check_planes(hi[:, :N], lo[:, :N], ref[:, :N])              # dQ: same arithmetic as the fp32 entry
+    # dK / dV: per-head partials summed over the group after the loop (a
+    # different fp32 order than the fp32 entry's accumulators)
+    assert rel((hi + lo)[:, N:], ref[:, N:]) < 1e-5
+    assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
     np.testing.assert_array_equal(Th.host().reshape(NG, ldot)[:, :M], hi.T)
     np.testing.assert_array_equal(Tl.host().reshape(NG, ldot)[:, :M], lo.T)
     # and the oracle
