@@ -197,7 +197,8 @@ int sj_down_bwd_swiglu(void *stream, const float *dy, long lddy, long M, long D,
  * what the step driver calls; the entries above keep the reference layouts.
  *
  * C[M,N] (+)= A B with A planes [M][K] (a_lo nullable) and B planes [N][K]
- * (b_lo nullable; at most one operand split).  Split-K through `workspace`
+ * (b_lo nullable; with both split the products are hi*hi + hi*lo + lo*hi).
+ * Split-K through `workspace`
  * (sj_gemm_planes_workspace_bytes) with a fixed-order reduction. */
 size_t sj_gemm_planes_workspace_bytes(long M, long N, long K);
 int sj_gemm_planes(void *stream, long M, long N, long K, const uint16_t *a_hi, const uint16_t *a_lo,
@@ -356,6 +357,94 @@ int sj_moe_gemm_rows(void *stream, const int32_t *offsets, long experts, long ca
 int sj_moe_gemm_dw(void *stream, const int32_t *offsets, long experts, long capacity, long M, long N,
                    const uint16_t *a, long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, float *c,
                    long ldc, long c_stride);
+
+/* ------------------------------------------------------- Parameter VJP
+ * Forward-basis parameter VJP and factored selected-row SGD
+ * (crates/sejong-gpu/src/parameter_vjp.rs, python/sejong_kernels/ops/
+ * parameter.py).  For Y = X W with X [n tokens][a features]: a rank-R token
+ * basis Q [n][R] from R donor columns, S selected feature blocks of
+ * block_rows rows, and the weight gradient as left [a][R] x right [R][b]
+ * plus the selected rows (tail [k][b], k = S*block_rows) placed by
+ * row_map [a] (-1 = not selected). */
+
+/* budget, parameter_vjp.rs:85-97: rank = min(rank, n, a, donor), blocks =
+ * ceil(a / block_rows), selected = clamp(ceil(blocks * fraction), 1, blocks). */
+int sj_pvjp_budget(long rank, double residual_fraction, long block_rows, long n, long a, long donor,
+                   long *out_rank, long *out_blocks, long *out_selected);
+/* selects_compression, parameter_vjp.rs:100-130 (the tile-padded cost
+ * model, exact integer arithmetic): 1 when the factored form is cheaper. */
+int sj_pvjp_selects_compression(long rank, double residual_fraction, long block_rows, long n, long a, long b,
+                                long donor, long uses);
+/* The CGS2 drop threshold of prepare_parameter_vjp_reusing,
+ * parameter_vjp.rs:214-220 (f32). */
+float sj_pvjp_basis_tolerance(long rows, long rank);
+/* kernel parameter_indices (parameter.py:25-62), launched by
+ * prepare_parameter_vjp_reusing (parameter_vjp.rs:181-207) with seed = one
+ * Rng::next_u64 of the caller's stream: partial Fisher-Yates of `rank`
+ * donor columns then `selected` feature blocks on one SplitMix64 stream.
+ * scratch i32 [donor_width + feature_blocks]; columns [rank]; rows
+ * [selected*block_rows] (-1 past a); map [a]. */
+int sj_pvjp_indices(void *stream, uint64_t seed, long a, long donor_width, long feature_blocks, long selected,
+                    long rank, long block_rows, int32_t *scratch, int32_t *columns, int32_t *rows,
+                    int32_t *map);
+/* kernels parameter_basis / parameter_basis_register (parameter.py:65-128):
+ * Q fp32 [n][rank] by classical Gram-Schmidt twice over the donor columns
+ * (y [n][ldy], f32 or bf16), a column zeroed when |v|^2 <= eps^2 |orig|^2.
+ * rank <= 64. */
+int sj_pvjp_basis(void *stream, const void *y, int dtype, long ldy, long n, const int32_t *columns, long rank,
+                  float eps, float *q);
+/* kernels parameter_prepare / parameter_residual (parameter.py:131-190)
+ * with X given transposed (x_t [a][ldxt] bf16, columns n .. n rounded up
+ * to 8 zero): left = X^T Q fp32 [a][rank];
+ * e = [Q^T ; (X[:, row] - Q left[row]^T) * inverse] fp32 [rank+k][lde] and
+ * as hi/lo planes (zero rows for row = -1).  Workspace:
+ * sj_pvjp_prepare_workspace_bytes. */
+size_t sj_pvjp_prepare_workspace_bytes(long a, long n, long rank);
+int sj_pvjp_prepare(void *stream, const uint16_t *x_t, long ldxt, long a, long n, const float *q, long rank,
+                    const int32_t *rows, long k, float inverse, float *left, float *e, uint16_t *e_hi,
+                    uint16_t *e_lo, long lde, void *workspace, size_t workspace_bytes);
+/* Engine::parameter_vjp, parameter_vjp.rs:308-320: coefficients = E dY
+ * [rows][b] (right = rows 0..rank-1, tail = the rest) from the E planes and
+ * dY^T planes [b][lddy] (columns past n zero).  Workspace:
+ * sj_pvjp_vjp_workspace_bytes. */
+size_t sj_pvjp_vjp_workspace_bytes(long rows, long b, long n);
+int sj_pvjp_vjp(void *stream, const uint16_t *e_hi, const uint16_t *e_lo, long lde, long rows, long n,
+                const uint16_t *dy_t_hi, const uint16_t *dy_t_lo, long lddy, long b, float *coefficients,
+                long ldc, void *workspace, size_t workspace_bytes);
+/* GradientPlan (parameter_vjp.rs:329-530; kernels parameter.py:193-291):
+ * per parameter W [rows][cols] fp32, G = dense (nullable) + sum over its
+ * terms of scale * (left right + tail rows placed by row_map).  Terms of a
+ * parameter are terms[term_begin .. term_begin+term_count).  decay != 0
+ * marks ndim > 1 (weight decay applies). */
+typedef struct {
+  float *w;
+  const float *dense;
+  long rows, cols;
+  int decay;
+  long term_begin, term_count;
+} sj_factored_param;
+typedef struct {
+  const float *left;     /* [rows][rank] */
+  const float *right;    /* [rank][cols] */
+  const float *tail;     /* [k][cols] */
+  const int32_t *row_map; /* [rows] */
+  long rank;
+  float scale;
+} sj_factored_term;
+/* GradientPlan::new + pack on the host: fills `host_meta`
+ * (sj_factored_meta_bytes) with the device table the caller uploads, and
+ * the number of 16x256 tiles. */
+size_t sj_factored_meta_bytes(long nparams, long nterms);
+int sj_factored_pack(const sj_factored_param *params, long nparams, const sj_factored_term *terms, long nterms,
+                     void *host_meta, size_t bytes, long *tiles);
+/* GradientPlan::tiles: action 0 materialize (G written into w), 1 update
+ * W = W*(1 - decay [ndim>1]) - lr*G with lr = learning_rate*clipping and
+ * decay = learning_rate*weight_decay (parameter_vjp.rs:502-518), 2 FP64
+ * sum of G^2 per tile into partials [tiles] (GradientPlan::norm). */
+int sj_factored_apply(void *stream, const void *meta, long tiles, int action, float lr, float decay,
+                      double *partials);
+/* Fixed-order FP64 sum (the host sum of GradientPlan::norm, on device). */
+int sj_sum_f64(void *stream, const double *x, long n, double *out);
 
 /* -------------------------------------------------------- Cross entropy */
 

@@ -18,6 +18,19 @@ _L = ctypes.c_long
 _I = ctypes.c_int
 _F = ctypes.c_float
 _S = ctypes.c_size_t
+_DB = ctypes.c_double
+_U64 = ctypes.c_uint64
+
+
+class FactoredParam(ctypes.Structure):
+    """sj_factored_param of include/sejong_hip.h."""
+    _fields_ = [("w", _P), ("dense", _P), ("rows", _L), ("cols", _L), ("decay", _I), ("term_begin", _L),
+                ("term_count", _L)]
+
+
+class FactoredTerm(ctypes.Structure):
+    """sj_factored_term of include/sejong_hip.h."""
+    _fields_ = [("left", _P), ("right", _P), ("tail", _P), ("row_map", _P), ("rank", _L), ("scale", _F)]
 
 
 class SejongError(RuntimeError):
@@ -88,6 +101,19 @@ SIGNATURES = {
                                       _P, _L]),
     "sj_moe_gemm_rows": (_I, [_P, _P, _L, _L, _L, _L, _P, _P, _L, _P, _L, _L, _P, _L, _I]),
     "sj_moe_gemm_dw": (_I, [_P, _P, _L, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _L]),
+    "sj_pvjp_budget": (_I, [_L, _DB, _L, _L, _L, _L, _P, _P, _P]),
+    "sj_pvjp_selects_compression": (_I, [_L, _DB, _L, _L, _L, _L, _L, _L]),
+    "sj_pvjp_basis_tolerance": (_F, [_L, _L]),
+    "sj_pvjp_indices": (_I, [_P, _U64, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P]),
+    "sj_pvjp_basis": (_I, [_P, _P, _I, _L, _L, _P, _L, _F, _P]),
+    "sj_pvjp_prepare_workspace_bytes": (_S, [_L, _L, _L]),
+    "sj_pvjp_prepare": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _F, _P, _P, _P, _P, _L, _P, _S]),
+    "sj_pvjp_vjp_workspace_bytes": (_S, [_L, _L, _L]),
+    "sj_pvjp_vjp": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _L, _P, _S]),
+    "sj_factored_meta_bytes": (_S, [_L, _L]),
+    "sj_factored_pack": (_I, [_P, _L, _P, _L, _P, _S, _P]),
+    "sj_factored_apply": (_I, [_P, _P, _L, _I, _F, _F, _P]),
+    "sj_sum_f64": (_I, [_P, _P, _L, _P]),
     "sj_attention_fwd_t": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _L]),
     "sj_attention_bwd_p": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P,
                                 _P, _P, _L, _P, _P, _L, _P, _S]),

@@ -648,7 +648,12 @@ int splits_for(long M, long N, long K, int bm, int bn) {
 
 template <int EPI, int PA, int PB>
 int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
-  if (bm == 128 && bn == 128) return launch<128, 128, PA, PB, EPI>(s, p, splits);
+  // both operands split: a 128x128 stage does not fit three deep in LDS
+  if constexpr (PA == 2 && PB == 2) {
+    if (bm == 128 && bn == 128) bn = 64;
+  } else {
+    if (bm == 128 && bn == 128) return launch<128, 128, PA, PB, EPI>(s, p, splits);
+  }
   if (bm == 128 && bn == 64) return launch<128, 64, PA, PB, EPI>(s, p, splits);
   if (bm == 64 && bn == 128) return launch<64, 128, PA, PB, EPI>(s, p, splits);
   return launch<64, 64, PA, PB, EPI>(s, p, splits);
@@ -658,7 +663,7 @@ int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
 // one-plane operands, the SwiGLU derivative a split dY, plain GEMMs any
 template <int EPI, int PA, int PB>
 constexpr bool plane_combo() {
-  if (EPI == E_STORE || EPI == E_PARTIAL) return !(PA == 2 && PB == 2);
+  if (EPI == E_STORE || EPI == E_PARTIAL) return true;
   if (EPI == E_SWIGLU_BWD) return PA == 2 && PB == 1;
   return PA == 1 && PB == 1;
 }
@@ -671,6 +676,8 @@ int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int b
     if (pa == 2 && pb == 1) return launch_tile<EPI, 2, 1>(s, p, bm, bn, splits);
   if constexpr (plane_combo<EPI, 1, 2>())
     if (pa == 1 && pb == 2) return launch_tile<EPI, 1, 2>(s, p, bm, bn, splits);
+  if constexpr (plane_combo<EPI, 2, 2>())
+    if (pa == 2 && pb == 2) return launch_tile<EPI, 2, 2>(s, p, bm, bn, splits);
   return sjh::fail(SJ_ERR_UNSUPPORTED, "gemm: planes %d/%d for this epilogue", pa, pb);
 }
 
@@ -686,7 +693,8 @@ int set_attr() {
 }
 template <int EPI, int PA, int PB>
 int set_attrs_tiles() {
-  int s = set_attr<128, 128, PA, PB, EPI>();
+  int s = SJ_OK;
+  if constexpr (!(PA == 2 && PB == 2)) s = set_attr<128, 128, PA, PB, EPI>();
   if (!s) s = set_attr<128, 64, PA, PB, EPI>();
   if (!s) s = set_attr<64, 128, PA, PB, EPI>();
   if (!s) s = set_attr<64, 64, PA, PB, EPI>();
@@ -698,6 +706,7 @@ int set_attrs_planes() {
   if constexpr (plane_combo<EPI, 1, 1>()) s = set_attrs_tiles<EPI, 1, 1>();
   if constexpr (plane_combo<EPI, 2, 1>()) if (!s) s = set_attrs_tiles<EPI, 2, 1>();
   if constexpr (plane_combo<EPI, 1, 2>()) if (!s) s = set_attrs_tiles<EPI, 1, 2>();
+  if constexpr (plane_combo<EPI, 2, 2>()) if (!s) s = set_attrs_tiles<EPI, 2, 2>();
   return s;
 }
 
@@ -743,7 +752,6 @@ extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16
              "matmul planes: M %ld N %ld K %ld lda %ld ldb %ld (K and ld must be multiples of 8)", M, N, K, lda, ldb);
   SJ_REQUIRE(a_hi && b_hi && ok16(a_hi) && ok16(b_hi) && (!a_lo || ok16(a_lo)) && (!b_lo || ok16(b_lo)),
              "matmul planes: 16-byte aligned planes required");
-  SJ_REQUIRE(!(a_lo && b_lo), "matmul planes: at most one split operand");
   SJ_REQUIRE(c_dtype == SJ_F32 || c_dtype == SJ_BF16, "matmul planes: output dtype %d", c_dtype);
   SJ_REQUIRE(!(accumulate && c_dtype == SJ_BF16), "matmul: accumulate needs an fp32 output");
   if (M == 0 || N == 0 || K == 0) return SJ_OK;

@@ -1,0 +1,501 @@
+// Forward-basis parameter VJP and the factored selected-row SGD (gfx950).
+//
+// Reference: crates/sejong-gpu/src/parameter_vjp.rs and
+// python/sejong_kernels/ops/parameter.py.  For a projection Y = X W with a
+// shared input X [n][a] (tokens x features):
+//   indices   one SplitMix64 stream (seeded by one host draw) picks R donor
+//             columns and S feature blocks by partial Fisher-Yates;
+//   basis     Q [n][R] = classical Gram-Schmidt applied twice to the picked
+//             donor columns, a column dropped when its residual norm falls
+//             below the roundoff threshold;
+//   prepare   A = X^T Q [a][R] and E = [Q^T ; (X[:, row] - Q A[row]^T) *
+//             blocks/selected for the selected rows] [R+k][n];
+//   vjp       coefficients = E dY [R+k][b]: right = the first R rows, tail
+//             the rest;
+//   apply     per parameter tile, G = dense + sum_terms scale (left right +
+//             tail rows placed by row_map), then W update, or G written out,
+//             or the FP64 sum of G^2.
+// MI355X layout: X is read transposed (X^T [a][n], the layout the step
+// already keeps for the dW GEMMs), so the feature rows of the residual are
+// contiguous; E is kept as fp32 plus hi/lo bf16 planes, the operand form of
+// the plane GEMMs that compute A and the coefficients.
+#include <math.h>
+#include <string.h>
+
+#include "common.h"
+
+using namespace sj;
+
+namespace {
+
+// ----------------------------------------------------------------- indices
+__device__ __forceinline__ uint64_t splitmix_next(uint64_t& s) {
+  s += 0x9e3779b97f4a7c15ULL;
+  uint64_t z = s;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+  return z ^ (z >> 31);
+}
+// Rng::index (crates/sejong-core/src/lib.rs:610-619, parameter.py:17-22)
+__device__ __forceinline__ uint64_t splitmix_index(uint64_t& s, uint64_t n) {
+  const uint64_t threshold = (0 - n) % n;
+  for (;;) {
+    const uint64_t x = splitmix_next(s);
+    if (x >= threshold) return x % n;
+  }
+}
+
+// parameter_indices (parameter.py:25-62).  One workgroup: the scratch
+// permutations and the map are initialised in parallel, the draws are
+// serial (each depends on the stream state) in lane 0, and the rows of a
+// picked block are written by all lanes.
+__global__ __launch_bounds__(256) void k_pvjp_indices(int32_t* __restrict__ scratch, int32_t* __restrict__ columns,
+                                                      int32_t* __restrict__ rows, int32_t* __restrict__ map, long A,
+                                                      long B, long NB, long S, long R, long group, uint64_t seed) {
+  __shared__ int32_t picked;
+  const int t = threadIdx.x;
+  for (long i = t; i < B; i += 256) scratch[i] = (int32_t)i;
+  for (long i = t; i < NB; i += 256) scratch[B + i] = (int32_t)i;
+  for (long i = t; i < A; i += 256) map[i] = -1;
+  __syncthreads();
+  uint64_t state = seed;
+  if (t == 0) {
+    for (long i = 0; i < R; i++) {
+      const long j = i + (long)splitmix_index(state, (uint64_t)(B - i));
+      const int32_t old = scratch[i], value = scratch[j];
+      scratch[i] = value;
+      scratch[j] = old;
+      columns[i] = value;
+    }
+  }
+  for (long i = 0; i < S; i++) {
+    if (t == 0) {
+      const long j = i + (long)splitmix_index(state, (uint64_t)(NB - i));
+      const int32_t old = scratch[B + i], value = scratch[B + j];
+      scratch[B + i] = value;
+      scratch[B + j] = old;
+      picked = value;
+    }
+    __syncthreads();
+    const long value = picked;
+    for (long off = t; off < group; off += 256) {
+      const long index = value * group + off, position = i * group + off;
+      rows[position] = index < A ? (int32_t)index : -1;
+      if (index < A) map[index] = (int32_t)position;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------- basis
+// parameter_basis (parameter.py:85-128) in one workgroup of 1024 threads:
+// column c is loaded from the donor, its projection on columns 0..c-1 is
+// removed twice (coefficients by block reductions), and it is normalised
+// or zeroed.  Q [n][R] lives in global memory (L2 resident); R <= 64.
+constexpr int BT = 1024;
+constexpr int RMAX = 64;
+__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < BT / 64; i++) s += red[i];
+  return s;
+}
+
+__global__ __launch_bounds__(BT) void k_pvjp_basis(const void* __restrict__ y, int ydt, long ldy, long n,
+                                                   const int32_t* __restrict__ cols, int R, float eps,
+                                                   float* __restrict__ q) {
+  __shared__ float red[BT / 64];
+  __shared__ float part[BT / 64][RMAX];
+  __shared__ float coef[RMAX];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  for (int c = 0; c < R; c++) {
+    const long col = cols[c];
+    float orig = 0.f;
+    for (long r = t; r < n; r += BT) {
+      const float v = load_as_f32(y, ydt, r * ldy + col);
+      q[r * R + c] = v;
+      orig += v * v;
+    }
+    orig = block_sum_1024(orig, red);
+    for (int rep = 0; rep < 2; rep++) {
+      // coefficients against the previous columns, RMAX at a time
+      float pc[RMAX];
+#pragma unroll
+      for (int i = 0; i < RMAX; i++) pc[i] = 0.f;
+      for (long r = t; r < n; r += BT) {
+        const float v = q[r * R + c];
+#pragma unroll
+        for (int i = 0; i < RMAX; i++)
+          if (i < c) pc[i] += q[r * R + i] * v;
+      }
+#pragma unroll
+      for (int i = 0; i < RMAX; i++) {
+        if (i >= c) break;
+        const float s = wave_sum(pc[i]);
+        if (lane == 0) part[w][i] = s;
+      }
+      __syncthreads();
+      if (t < c) {
+        float s = 0.f;
+        for (int k = 0; k < BT / 64; k++) s += part[k][t];
+        coef[t] = s;
+      }
+      __syncthreads();
+      for (long r = t; r < n; r += BT) {
+        float v = q[r * R + c];
+        for (int i = 0; i < c; i++) v -= q[r * R + i] * coef[i];
+        q[r * R + c] = v;
+      }
+      __syncthreads();
+    }
+    float mag = 0.f;
+    for (long r = t; r < n; r += BT) {
+      const float v = q[r * R + c];
+      mag += v * v;
+    }
+    mag = block_sum_1024(mag, red);
+    const float inv = mag > eps * eps * orig ? rsqrtf(mag) : 0.f;
+    for (long r = t; r < n; r += BT) q[r * R + c] *= inv;
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------- prepare
+// E[0:R] = Q^T (fp32 and hi/lo planes; the planes double as the B operand
+// of A = X^T Q).  Thread per (r, token).
+__global__ __launch_bounds__(256) void k_pvjp_qt(const float* __restrict__ q, int R, long n, long n8,
+                                                 float* __restrict__ e, bf16_t* __restrict__ eh, bf16_t* __restrict__ el,
+                                                 long lde) {
+  const long i = blockIdx.x * 256L + threadIdx.x;
+  if (i >= (long)R * n8) return;
+  const long r = i / n8, tok = i - r * n8;
+  const float v = tok < n ? q[tok * R + r] : 0.f;  // columns [n, n8) are the GEMM's zero padding
+  e[r * lde + tok] = v;
+  bf16_t h, l;
+  split_bf(v, h, l);
+  eh[r * lde + tok] = h;
+  el[r * lde + tok] = l;
+}
+
+// E[R+i][tok] = (X^T[row_i][tok] - sum_r Q[tok][r] A[row_i][r]) * inverse,
+// zero for row_i = -1 (parameter.py:167-190); fp32 and planes.
+__global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict__ xt, long ldxt,
+                                                       const float* __restrict__ q, int R, long n,
+                                                       const float* __restrict__ left, const int32_t* __restrict__ rows,
+                                                       float inverse, float* __restrict__ e, bf16_t* __restrict__ eh,
+                                                       bf16_t* __restrict__ el, long lde, long n8) {
+  const long i = blockIdx.y;
+  const long tok = blockIdx.x * 256L + threadIdx.x;
+  if (tok >= n8) return;
+  const long row = rows[i];
+  float v = 0.f;
+  if (row >= 0 && tok < n) {
+    float acc = 0.f;
+    for (int r = 0; r < R; r++) acc += q[tok * R + r] * left[row * R + r];
+    v = (bf2f(xt[row * ldxt + tok]) - acc) * inverse;
+  }
+  const long o = (R + i) * lde + tok;
+  e[o] = v;
+  bf16_t h, l;
+  split_bf(v, h, l);
+  eh[o] = h;
+  el[o] = l;
+}
+
+// ------------------------------------------------------------------- apply
+// Device metadata of a factored update: parameters, then terms.
+struct FParam {
+  float* w;
+  const float* dense;
+  long rows, cols, first_tile, col_tiles;
+  int decay, term_begin, term_count, pad;
+};
+struct FTerm {
+  const float* left;
+  const float* right;
+  const float* tail;
+  const int32_t* row_map;
+  long rank;
+  float scale;
+  int pad;
+};
+struct FMetaHeader {
+  long nparams, nterms, tiles, pad;
+};
+
+constexpr int FBM = 16;   // tile rows
+constexpr int FBN = 256;  // tile columns (one per thread)
+
+// parameter_gradient_update / _materialize / _norm (parameter.py:244-291):
+// one workgroup per tile of one parameter (the owner found from the
+// parameters' first tiles).  Action 0 materialize (G into w), 1 update,
+// 2 FP64 sum of G^2 per tile into partials.
+__global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restrict__ meta, int action, float lr,
+                                                        float decay, double* __restrict__ partials) {
+  const FMetaHeader* hd = (const FMetaHeader*)meta;
+  const FParam* params = (const FParam*)(meta + sizeof(FMetaHeader));
+  const FTerm* terms = (const FTerm*)(params + hd->nparams);
+  const long tile = blockIdx.x;
+  long pi = 0;
+  while (pi + 1 < hd->nparams && tile >= params[pi + 1].first_tile) pi++;
+  const FParam P = params[pi];
+  const long local = tile - P.first_tile;
+  const long m0 = (local / P.col_tiles) * FBM, n = (local % P.col_tiles) * FBN + threadIdx.x;
+  const bool colok = n < P.cols;
+  float g[FBM];
+#pragma unroll
+  for (int i = 0; i < FBM; i++) g[i] = 0.f;
+  // head = sum over the terms' ranks of (left * scale) right
+  for (int ti = 0; ti < P.term_count; ti++) {
+    const FTerm tm = terms[P.term_begin + ti];
+    for (long r = 0; r < tm.rank; r++) {
+      const float rv = colok ? tm.right[r * P.cols + n] : 0.f;
+#pragma unroll
+      for (int i = 0; i < FBM; i++) {
+        const long m = m0 + i;
+        const float lv = m < P.rows ? tm.left[m * tm.rank + r] * tm.scale : 0.f;
+        g[i] += lv * rv;
+      }
+    }
+  }
+  // value = dense + head, then the tails
+#pragma unroll
+  for (int i = 0; i < FBM; i++) {
+    const long m = m0 + i;
+    if (P.dense && m < P.rows && colok) g[i] = P.dense[m * P.cols + n] + g[i];
+  }
+  for (int ti = 0; ti < P.term_count; ti++) {
+    const FTerm tm = terms[P.term_begin + ti];
+#pragma unroll
+    for (int i = 0; i < FBM; i++) {
+      const long m = m0 + i;
+      if (m < P.rows && colok) {
+        const int sel = tm.row_map[m];
+        if (sel >= 0) g[i] += tm.tail[(long)sel * P.cols + n] * tm.scale;
+      }
+    }
+  }
+  if (action == 2) {
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < FBM; i++)
+      if (m0 + i < P.rows && colok) s += (double)g[i] * (double)g[i];
+    __shared__ double red[4];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partials[tile] = ((red[0] + red[1]) + red[2]) + red[3];
+    return;
+  }
+  const float keep = (P.decay && action == 1) ? 1.f - decay : 1.f;
+#pragma unroll
+  for (int i = 0; i < FBM; i++) {
+    const long m = m0 + i;
+    if (m < P.rows && colok) {
+      float* wp = P.w + m * P.cols + n;
+      *wp = action == 1 ? *wp * keep - lr * g[i] : g[i];
+    }
+  }
+}
+
+// fixed-order FP64 sum of the per-tile partials (one workgroup)
+__global__ __launch_bounds__(256) void k_sum_f64(const double* __restrict__ x, long n, double* __restrict__ out) {
+  __shared__ double red[4];
+  double s = 0.0;
+  for (long i = threadIdx.x; i < n; i += 256) s += x[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) *out = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" int sj_pvjp_budget(long rank, double residual_fraction, long block_rows, long n, long a, long donor,
+                              long* out_rank, long* out_blocks, long* out_selected) {
+  SJ_REQUIRE(rank > 0 && block_rows > 0 && residual_fraction > 0.0 && residual_fraction <= 1.0 && n > 0 && a > 0 &&
+                 donor > 0,
+             "parameter VJP requires positive rank/block_rows and residual_fraction in (0,1]");
+  long r = rank < n ? rank : n;
+  r = r < a ? r : a;
+  r = r < donor ? r : donor;
+  const long blocks = (a + block_rows - 1) / block_rows;
+  long sel = (long)ceil((double)blocks * residual_fraction);
+  sel = sel < blocks ? sel : blocks;
+  sel = sel > 1 ? sel : 1;
+  if (out_rank) *out_rank = r;
+  if (out_blocks) *out_blocks = blocks;
+  if (out_selected) *out_selected = sel;
+  return SJ_OK;
+}
+
+namespace {
+typedef unsigned __int128 u128;
+u128 issued(long m, long n, long k) {
+  auto up = [](long v, long t) { return (u128)((v + t - 1) / t) * (u128)t; };
+  return 2 * up(m, 16) * up(n, 32) * up(k, 32);
+}
+u128 pow2(long v) {
+  u128 p = 1;
+  while (p < (u128)v) p <<= 1;
+  return p;
+}
+}  // namespace
+
+extern "C" int sj_pvjp_selects_compression(long rank, double residual_fraction, long block_rows, long n, long a,
+                                           long b, long donor, long uses) {
+  if (n < a || uses <= 1) return 0;
+  long r = 0, blocks = 0, sel = 0;
+  if (sj_pvjp_budget(rank, residual_fraction, block_rows, n, a, donor, &r, &blocks, &sel)) return 0;
+  if (sel == blocks) return 0;
+  const long k = sel * block_rows;
+  const u128 padded = (u128)((n + 15) / 16) * 16;
+  const u128 last = r > 0 ? (u128)(r - 1) : 0;
+  const u128 full = last / 32, tail = last % 32;
+  const u128 tri = 32 * full * (full + 1) / 2 + tail * (full + 1);
+  const u128 streaming = 2 * (4 * padded * 32 + padded) * tri + 5 * padded * (u128)r;
+  const u128 resident = 8 * pow2(n) * pow2(r) * (u128)r + 5 * pow2(n) * (u128)r;
+  const u128 qr = streaming > resident ? streaming : resident;
+  const u128 shared = qr + issued(a, r, n) + issued(k, n, r);
+  const u128 own = issued(r + k, b, n) + issued(a, b, r);
+  return own * (u128)uses + shared < issued(a, b, n) * (u128)uses ? 1 : 0;
+}
+
+extern "C" float sj_pvjp_basis_tolerance(long rows, long rank) {
+  const double ops = (double)rows * (4.0 * (double)rank + 1.0);
+  const double roundoff = ops * (1.1920928955078125e-7 / 2.0);
+  const double tol = roundoff < 1.0 ? roundoff / (1.0 - roundoff) : INFINITY;
+  return (float)(tol < 3.4028234663852886e38 ? tol : 3.4028234663852886e38);
+}
+
+extern "C" int sj_pvjp_indices(void* stream, uint64_t seed, long a, long donor_width, long feature_blocks,
+                               long selected, long rank, long block_rows, int32_t* scratch, int32_t* columns,
+                               int32_t* rows, int32_t* map) {
+  SJ_REQUIRE(a >= 0 && donor_width >= 0 && feature_blocks >= 0 && selected >= 0 && rank >= 0 && block_rows > 0 &&
+                 rank <= donor_width && selected <= feature_blocks && donor_width + feature_blocks < (1L << 31) &&
+                 scratch && (rank == 0 || columns) && (selected == 0 || (rows && map)),
+             "parameter_indices: dimensions");
+  hipLaunchKernelGGL(k_pvjp_indices, dim3(1), dim3(256), 0, (hipStream_t)stream, scratch, columns, rows, map, a,
+                     donor_width, feature_blocks, selected, rank, block_rows, seed);
+  SJ_LAUNCH_CHECK("parameter_indices");
+  return SJ_OK;
+}
+
+extern "C" int sj_pvjp_basis(void* stream, const void* y, int dtype, long ldy, long n, const int32_t* columns,
+                             long rank, float eps, float* q) {
+  SJ_REQUIRE(n > 0 && rank > 0 && rank <= RMAX && (dtype == SJ_F32 || dtype == SJ_BF16),
+             "parameter_basis: rank %ld (<= %d)", rank, RMAX);
+  hipLaunchKernelGGL(k_pvjp_basis, dim3(1), dim3(BT), 0, (hipStream_t)stream, y, dtype, ldy, n, columns, (int)rank,
+                     eps, q);
+  SJ_LAUNCH_CHECK("parameter_basis");
+  return SJ_OK;
+}
+
+extern "C" size_t sj_pvjp_prepare_workspace_bytes(long a, long n, long rank) {
+  return sj_gemm_planes_workspace_bytes(a, rank, (n + 7) / 8 * 8);
+}
+
+extern "C" int sj_pvjp_prepare(void* stream, const uint16_t* x_t, long ldxt, long a, long n, const float* q, long rank,
+                               const int32_t* rows, long k, float inverse, float* left, float* e, uint16_t* e_hi,
+                               uint16_t* e_lo, long lde, void* workspace, size_t workspace_bytes) {
+  const long n8 = (n + 7) / 8 * 8;
+  SJ_REQUIRE(a > 0 && n > 0 && rank > 0 && k >= 0 && ldxt >= n8 && ldxt % 8 == 0 && lde >= n8 && lde % 8 == 0 &&
+                 ((uintptr_t)e_hi & 15) == 0 && ((uintptr_t)e_lo & 15) == 0 && ((uintptr_t)x_t & 15) == 0,
+             "parameter_prepare: dimensions (leading dimensions multiples of 8, >= n rounded up to 8)");
+  hipStream_t s = (hipStream_t)stream;
+  const long qn = rank * n8;
+  hipLaunchKernelGGL(k_pvjp_qt, dim3((unsigned)((qn + 255) / 256)), dim3(256), 0, s, q, (int)rank, n, n8, e,
+                     (bf16_t*)e_hi, (bf16_t*)e_lo, lde);
+  SJ_LAUNCH_CHECK("parameter_prepare");
+  // A = X^T Q: A operand X^T [a][n8] bf16 (zero columns past n), B operand
+  // Q^T planes = E[0:R]
+  if (int st = sj_gemm_planes(stream, a, rank, n8, x_t, nullptr, ldxt, e_hi, e_lo, lde, left, SJ_F32, rank, 0,
+                              workspace, workspace_bytes))
+    return st;
+  if (k > 0) {
+    hipLaunchKernelGGL(k_pvjp_residual, dim3((unsigned)((n8 + 255) / 256), (unsigned)k), dim3(256), 0, s,
+                       (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, inverse, e, (bf16_t*)e_hi,
+                       (bf16_t*)e_lo, lde, n8);
+    SJ_LAUNCH_CHECK("parameter_residual");
+  }
+  return SJ_OK;
+}
+
+extern "C" size_t sj_pvjp_vjp_workspace_bytes(long rows, long b, long n) {
+  return sj_gemm_planes_workspace_bytes(rows, b, (n + 7) / 8 * 8);
+}
+
+extern "C" int sj_pvjp_vjp(void* stream, const uint16_t* e_hi, const uint16_t* e_lo, long lde, long rows, long n,
+                           const uint16_t* dy_t_hi, const uint16_t* dy_t_lo, long lddy, long b, float* coefficients,
+                           long ldc, void* workspace, size_t workspace_bytes) {
+  const long n8 = (n + 7) / 8 * 8;
+  SJ_REQUIRE(rows > 0 && n > 0 && b > 0 && ldc >= b && lde >= n8 && lddy >= n8,
+             "parameter_vjp: dimensions (leading dimensions >= n rounded up to 8, zero padded)");
+  return sj_gemm_planes(stream, rows, b, n8, e_hi, e_lo, lde, dy_t_hi, dy_t_lo, lddy, coefficients, SJ_F32, ldc, 0,
+                        workspace, workspace_bytes);
+}
+
+extern "C" size_t sj_factored_meta_bytes(long nparams, long nterms) {
+  return sizeof(FMetaHeader) + sizeof(FParam) * (size_t)nparams + sizeof(FTerm) * (size_t)nterms;
+}
+
+extern "C" int sj_factored_pack(const sj_factored_param* params, long nparams, const sj_factored_term* terms,
+                                long nterms, void* host_meta, size_t bytes, long* tiles) {
+  SJ_REQUIRE(params && nparams > 0 && nterms >= 0 && (nterms == 0 || terms) && host_meta &&
+                 bytes >= sj_factored_meta_bytes(nparams, nterms),
+             "gradient plan requires parameters and a metadata buffer of %zu bytes",
+             sj_factored_meta_bytes(nparams, nterms));
+  uint8_t* out = (uint8_t*)host_meta;
+  FMetaHeader hd = {nparams, nterms, 0, 0};
+  FParam* fp = (FParam*)(out + sizeof(FMetaHeader));
+  FTerm* ft = (FTerm*)(fp + nparams);
+  long t = 0;
+  for (long i = 0; i < nparams; i++) {
+    const sj_factored_param& p = params[i];
+    SJ_REQUIRE(p.w && p.rows > 0 && p.cols > 0 && p.term_begin >= 0 && p.term_count >= 0 &&
+                   p.term_begin + p.term_count <= nterms,
+               "compact SGD parameter %ld: shape or terms", i);
+    FParam q = {};
+    q.w = p.w; q.dense = p.dense; q.rows = p.rows; q.cols = p.cols;
+    q.first_tile = t; q.col_tiles = (p.cols + FBN - 1) / FBN;
+    q.decay = p.decay; q.term_begin = (int)p.term_begin; q.term_count = (int)p.term_count;
+    t += ((p.rows + FBM - 1) / FBM) * q.col_tiles;
+    memcpy(fp + i, &q, sizeof(q));
+  }
+  for (long i = 0; i < nterms; i++) {
+    const sj_factored_term& s = terms[i];
+    SJ_REQUIRE(s.left && s.right && s.tail && s.row_map && s.rank >= 0, "compact SGD term %ld", i);
+    FTerm q = {};
+    q.left = s.left; q.right = s.right; q.tail = s.tail; q.row_map = s.row_map; q.rank = s.rank; q.scale = s.scale;
+    memcpy(ft + i, &q, sizeof(q));
+  }
+  hd.tiles = t;
+  memcpy(out, &hd, sizeof(hd));
+  if (tiles) *tiles = t;
+  return SJ_OK;
+}
+
+extern "C" int sj_factored_apply(void* stream, const void* meta, long tiles, int action, float lr, float decay,
+                                 double* partials) {
+  SJ_REQUIRE(meta && tiles > 0 && tiles < (1L << 31) && action >= 0 && action <= 2 && (action != 2 || partials),
+             "compact SGD apply: action %d", action);
+  hipLaunchKernelGGL(k_factored_apply, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)meta, action, lr, decay, partials);
+  SJ_LAUNCH_CHECK(action == 1 ? "parameter_gradient_update"
+                              : action == 0 ? "parameter_gradient_materialize" : "parameter_gradient_norm");
+  return SJ_OK;
+}
+
+extern "C" int sj_sum_f64(void* stream, const double* x, long n, double* out) {
+  SJ_REQUIRE(x && out && n >= 0, "sum: arguments");
+  hipLaunchKernelGGL(k_sum_f64, dim3(1), dim3(256), 0, (hipStream_t)stream, x, n, out);
+  SJ_LAUNCH_CHECK("sum");
+  return SJ_OK;
+}

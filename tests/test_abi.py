@@ -94,3 +94,28 @@ def test_init_params_std_and_norms():
         elif n > 10000:
             assert abs(seg.std() - 0.02) < 2e-3
         off += n
+
+
+def test_pvjp_host_cost_model_matches_oracle():
+    """sj_pvjp_budget / sj_pvjp_selects_compression / the basis tolerance
+    are host code (no GPU): bit-exact against the oracle's integer
+    restatement of parameter_vjp.rs:85-130, 214-220 over a grid of shapes."""
+    import ctypes
+    from oracle import pvjp
+    from sejong_amd import _native as N
+    lib = N.load()
+    L = ctypes.c_long
+    for rank in (1, 8, 16, 33, 64):
+        for frac in (0.05, 0.1, 0.4, 1.0):
+            for br in (16, 32):
+                for n, a, b, donor, uses in ((16384, 1024, 1024, 5504, 3), (16384, 1024, 5504, 5504, 2),
+                                             (16384, 2752, 1024, 1024, 1), (67, 71, 97, 97, 2), (900, 1024, 64, 64, 2),
+                                             (4096, 384, 640, 1024, 3)):
+                    r, bl, s = L(), L(), L()
+                    assert lib.sj_pvjp_budget(rank, frac, br, n, a, donor, ctypes.byref(r), ctypes.byref(bl),
+                                              ctypes.byref(s)) == 0
+                    assert (r.value, bl.value, s.value) == pvjp.budget(rank, frac, br, n, a, donor)
+                    got = lib.sj_pvjp_selects_compression(rank, frac, br, n, a, b, donor, uses)
+                    assert bool(got) == pvjp.selects_compression(rank, frac, br, n, a, b, donor, uses)
+    for rows, rank in ((67, 33), (16384, 16), (10 ** 8, 64)):
+        assert lib.sj_pvjp_basis_tolerance(rows, rank) == np.float32(pvjp.basis_tolerance(rows, rank))

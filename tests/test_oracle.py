@@ -417,3 +417,98 @@ def test_moe_single_expert_is_dense_ffn():
     a = moe.moe_forward(z, wr, ex, 1, dtype="bf16")
     assert np.all(a["w"] == 1.0) and np.all(a["ids"] == 0)
     np.testing.assert_array_equal(a["update"], moe.dense_ffn(z, *ex[0], dtype="bf16"))
+
+
+# ------------------------------------------------------- parameter VJP
+def test_pvjp_indices_match_reference_check_generator():
+    """parameter_vjp_check.rs:74-100 builds the expected selection with
+    Vec swaps on Rng::new(rng.next_u64()); restated here as text, it must
+    equal the kernel-style restatement on the check's default shape."""
+    from oracle import pvjp
+    n, a, b, rank, frac, block_rows = 67, 71, 97, 33, 0.4, 16
+    seed = O.Rng(42).next_u64()
+    sel = O.Rng(seed)
+    columns = list(range(b))
+    for i in range(rank):
+        j = i + sel.index(b - i)
+        columns[i], columns[j] = columns[j], columns[i]
+    blocks = list(range(-(-a // block_rows)))
+    count = math.ceil(len(blocks) * frac)
+    for i in range(count):
+        j = i + sel.index(len(blocks) - i)
+        blocks[i], blocks[j] = blocks[j], blocks[i]
+    expected_rows = [(i * block_rows + j) if i * block_rows + j < a else -1 for i in blocks[:count] for j in range(block_rows)]
+    r, nb, s = pvjp.budget(rank, frac, block_rows, n, a, b)
+    assert (r, nb, s) == (33, 5, 2)
+    cols, rows, fmap = pvjp.indices(seed, a, b, nb, s, r, block_rows)
+    assert cols.tolist() == columns[:rank]
+    assert rows.tolist() == expected_rows
+    for pos, row in enumerate(rows):
+        if row >= 0:
+            assert fmap[row] == pos
+    assert (fmap >= 0).sum() == (rows >= 0).sum()
+
+
+def test_pvjp_budget_and_compression_cfg5():
+    """cfg5: rank 16, block_rows 32, residual 0.1 over d = 1024 inputs and
+    16384 tokens -> 32 blocks, 4 selected; QKV (3 uses) and gate/up (2 uses)
+    compress, the single-use attention output and down projections do not."""
+    from oracle import pvjp
+    n, d, F = 16384, 1024, 2752
+    assert pvjp.budget(16, 0.1, 32, n, d, F) == (16, 32, 4)
+    assert pvjp.selects_compression(16, 0.1, 32, n, d, 1024, 2 * F, 3)       # query with the widest donor
+    assert pvjp.selects_compression(16, 0.1, 32, n, d, F, 2 * F, 2)          # gate
+    assert not pvjp.selects_compression(16, 0.1, 32, n, d, d, d, 1)          # attention_output
+    assert not pvjp.selects_compression(16, 0.1, 32, n, F, d, d, 1)          # down
+    assert not pvjp.selects_compression(16, 1.0, 32, n, d, F, F, 2)          # every block selected
+    assert pvjp.issued_gemm(17, 33, 1) == 2 * 32 * 64 * 32
+
+
+def test_pvjp_basis_orthonormal_span_and_drop():
+    from oracle import pvjp
+    rng = np.random.default_rng(7)
+    n, b, R = 300, 40, 12
+    Y = rng.normal(0, 1, (n, b))
+    cols = rng.choice(b, R, replace=False)
+    eps = pvjp.basis_tolerance(n, R)
+    Q = pvjp.basis(Y, cols, eps)
+    assert np.abs(Q.T @ Q - np.eye(R)).max() < 1e-12
+    Qr, _ = np.linalg.qr(Y[:, cols])
+    assert np.abs(Q @ Q.T - Qr @ Qr.T).max() < 1e-12
+    Y2 = Y.copy()
+    Y2[:, cols[5]] = 2.0 * Y2[:, cols[2]]                                   # dependent column -> dropped
+    Q2 = pvjp.basis(Y2, cols, eps)
+    assert not Q2[:, 5].any() and abs(np.linalg.norm(Q2[:, 6]) - 1) < 1e-12
+
+
+def test_pvjp_factored_gradient_all_blocks_is_exact():
+    """With every feature row selected (residual weight 1) the factored
+    gradient equals X^T D exactly, for any orthonormal Q."""
+    from oracle import pvjp
+    rng = np.random.default_rng(8)
+    n, a, b, R = 50, 20, 9, 6
+    X, D = rng.normal(0, 1, (n, a)), rng.normal(0, 1, (n, b))
+    Q, _ = np.linalg.qr(rng.normal(0, 1, (n, R)))
+    rows = np.arange(a)
+    A, E = pvjp.prepare(X, Q, rows, 1, 1)
+    coeff = E @ D
+    G = pvjp.factored_gradient(a, b, [(A, coeff[:R], coeff[R:], np.arange(a), 1.0)])
+    assert np.abs(G - X.T @ D).max() < 1e-10
+    # a subset: selected rows carry X^T D, the others the low-rank part
+    rows = np.array([3, 4, 5, -1])
+    fmap = np.full(a, -1); fmap[[3, 4, 5]] = [0, 1, 2]
+    A, E = pvjp.prepare(X, Q, rows, 2, 1)
+    coeff = E @ D
+    G = pvjp.factored_gradient(a, b, [(A, coeff[:R], coeff[R:], fmap, 1.0)])
+    low = A @ (Q.T @ D)
+    assert np.abs(G[0] - low[0]).max() < 1e-10
+    assert np.abs(G[3] - (low[3] + 2 * (X[:, 3] - Q @ A[3]) @ D)).max() < 1e-10
+
+
+def test_pvjp_update_closed_form():
+    from oracle import pvjp
+    W = np.array([[1.0, -2.0], [0.5, 0.25]]); G = np.array([[0.1, 0.2], [-0.3, 0.4]])
+    lr, clip, wd = 0.01, 0.7, 0.02
+    LR = float(np.float32(np.float32(lr) * np.float32(clip))); DEC = float(np.float32(np.float32(lr) * np.float32(wd)))
+    np.testing.assert_allclose(pvjp.factored_update(W, G, lr, clip, wd, True), W * (1 - DEC) - LR * G, rtol=0, atol=0)
+    np.testing.assert_allclose(pvjp.factored_update(W, G, lr, clip, wd, False), W - LR * G, rtol=0, atol=0)
