@@ -132,6 +132,315 @@ def copy_probe(mib: int):
           flush=True)
 
 
+# ------------------------------------------------------------ workloads
+class _Buf:
+    """A device buffer from the library allocator (torch is not loaded:
+    its wheel carries a second HIP runtime)."""
+
+    def __init__(self, api, nbytes, keep):
+        import ctypes
+        self.api = api
+        p = ctypes.c_void_p()
+        api.sj_alloc(max(int(nbytes), 256), ctypes.byref(p))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+        keep.append(self)
+
+    def p(self, offset_bytes=0):
+        import ctypes
+        return ctypes.c_void_p(self.ptr + offset_bytes)
+
+    def upload(self, arr):
+        import ctypes
+        import numpy as np
+        a = np.ascontiguousarray(arr)
+        self.api.sj_upload(self.p(), ctypes.c_void_p(a.ctypes.data), a.nbytes)
+        return self
+
+
+def _bf16(x):
+    import numpy as np
+    return (np.asarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+class _OpTimer:
+    """HIP events around each op on the NULL stream (one profiled pass)."""
+
+    def __init__(self, api):
+        self.api, self.events, self.names = api, [], []
+
+    def op(self, name, fn):
+        import ctypes
+        a, b = ctypes.c_void_p(), ctypes.c_void_p()
+        self.api.sj_event_create(ctypes.byref(a)); self.api.sj_event_create(ctypes.byref(b))
+        self.api.sj_event_record(a, None)
+        fn()
+        self.api.sj_event_record(b, None)
+        self.events.append((a, b)); self.names.append(name)
+
+    def collect(self):
+        import ctypes
+        self.api.sj_synchronize(None)
+        out = {}
+        for name, (a, b) in zip(self.names, self.events):
+            ms = ctypes.c_float()
+            self.api.sj_event_elapsed(a, b, ctypes.byref(ms))
+            t, c = out.get(name, (0.0, 0))
+            out[name] = (t + ms.value, c + 1)
+            self.api.sj_event_destroy(a); self.api.sj_event_destroy(b)
+        return out
+
+
+def _time_region(api, fn, steps):
+    import ctypes
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    api.sj_event_create(ctypes.byref(a)); api.sj_event_create(ctypes.byref(b))
+    api.sj_synchronize(None)
+    t0 = time.perf_counter()
+    api.sj_event_record(a, None)
+    for _ in range(steps):
+        fn(None)
+    api.sj_event_record(b, None)
+    api.sj_synchronize(None)
+    wall = time.perf_counter() - t0
+    ms = ctypes.c_float()
+    api.sj_event_elapsed(a, b, ctypes.byref(ms))
+    api.sj_event_destroy(a); api.sj_event_destroy(b)
+    return max(ms.value, wall * 1e3) / steps
+
+
+def _report(metric, unit, value, ms, args, config, prof, work, dtype, extra=None):
+    rows = []
+    total = sum(t for t, _ in prof.values())
+    for op, (t, c) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
+        kind, w = work.get(op, ("flop", 0.0))
+        avg_us = t * 1e3 / c
+        rate = w / (avg_us * 1e-6) / (1e12 if kind == "flop" else 1e9)
+        peak = PEAK_BF16_TFLOPS if kind == "flop" else PEAK_HBM_GBS
+        rows.append(dict(op=op, calls=c, avg_us=avg_us, kind=kind, rate=rate, frac=rate / peak, work=w))
+        log(f"  {op:24s} x{c:3d} {avg_us:9.2f} us  {100 * t / total:5.1f}%  {rate:9.2f} "
+            f"{'TFLOP/s' if kind == 'flop' else 'GB/s'}  ({100 * rate / peak:.1f}% of peak)")
+    dom = rows[0]
+    out = {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype, "data": "synthetic (numpy seeded normal / SplitMix64 draws)",
+           "config": config,
+           "roofline": {"bound": "mfma" if dom["kind"] == "flop" else "hbm", "achieved": round(dom["rate"], 2),
+                        "peak": PEAK_BF16_TFLOPS if dom["kind"] == "flop" else PEAK_HBM_GBS,
+                        "unit": "TFLOP/s" if dom["kind"] == "flop" else "GB/s", "frac": round(dom["frac"], 4),
+                        "traffic": None, "op": dom["op"], "work_per_launch": dom["work"],
+                        "avg_launch_us": round(dom["avg_us"], 3)},
+           "cpu_baseline": None}
+    if extra:
+        out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+def workload_moe(args):
+    """cfg4: the MoE FFN of 4 layers, d 512, 8 SwiGLU
+    experts of width 1024, top-2, 4096 tokens: router + top-k, device pack,
+    grouped gate/up and down, combine + residual; the backward (combine,
+    grouped down dX + SwiGLU, grouped dW, grouped gate/up dX, gather +
+    routing backward + router dW); AdamW on the fp32 expert masters and
+    the bf16 mirror cast.  Attention is not part of this measurement."""
+    import ctypes
+    import numpy as np
+    from sejong_amd import _native as N
+    lib = N.load(); api = N.api
+    L, M, d, E, F, K = 4, 4096, 512, 8, 1024, 2
+    cf = ctypes.c_float
+    keep = []
+    rng = np.random.default_rng(0)
+    B = lambda nbytes: _Buf(api, nbytes, keep)
+    cap = lib.sj_route_pack_capacity(M * K, E)
+    S = M * K
+    layers = []
+    for l in range(L):
+        wg = rng.normal(0, 0.02, (E, d, F)); wu = rng.normal(0, 0.02, (E, d, F)); wd = rng.normal(0, 0.02, (E, F, d))
+        gu = np.concatenate([wg, wu], 2).astype(np.float32)                    # [E][d][2F]
+        master = np.concatenate([gu.ravel(), wd.astype(np.float32).ravel()])
+        P = master.size
+        y = dict(P=P)
+        y["w"] = B(P * 4).upload(master); y["g"] = B(P * 4); y["m"] = B(P * 4).upload(np.zeros(P, np.float32))
+        y["v"] = B(P * 4).upload(np.zeros(P, np.float32)); y["mirror"] = B(P * 2).upload(_bf16(master))
+        y["gu_t"] = B(E * 2 * F * d * 2).upload(_bf16(np.concatenate([wg.transpose(0, 2, 1), wu.transpose(0, 2, 1)], 1)))
+        y["d_t"] = B(E * d * F * 2).upload(_bf16(wd.transpose(0, 2, 1)))
+        y["wr"] = B(d * E * 2).upload(_bf16(rng.normal(0, d ** -0.5, (d, E))))
+        layers.append(y)
+    z = B(M * d * 2).upload(_bf16(rng.normal(0, 1, (M, d)))); x1 = B(M * d * 2).upload(_bf16(rng.normal(0, 1, (M, d))))
+    out = B(M * d * 2)
+    logits, ids, wts = B(M * E * 2), B(S * 4), B(S * 4)
+    tok, slt, cnt, off, ps, pp = B(E * S * 4), B(E * S * 4), B(E * 4), B((E + 1) * 4), B(cap * 4), B(S * 4)
+    zp, zpt = B(cap * d * 2), B(d * cap * 2)
+    g_, u_, h_, ht = B(cap * F * 2), B(cap * F * 2), B(cap * F * 2), B(F * cap * 2)
+    yp = B(cap * d * 2)
+    dres = B(M * d * 4).upload(rng.normal(0, 1e-3, (M, d)).astype(np.float32))
+    dxh, dxl, dxth, dxtl = (B(cap * d * 2) for _ in range(4))
+    dwts = B(S * 4)
+    dgh, dgl, dgth, dgtl = (B(cap * 2 * F * 2) for _ in range(4))
+    dzp, dz, dlog, dwr = B(cap * d * 4), B(M * d * 4), B(M * E * 4), B(d * E * 4)
+    ws = B(max(lib.sj_gemm_workspace_bytes(d, E, M), 256))
+    api.sj_synchronize(None)
+
+    def step(T):
+        run = (lambda n, f: T.op(n, f)) if T else (lambda n, f: f())
+        for y in layers:
+            run("router_topk", lambda: api.sj_router_topk(None, z.p(), d, y["wr"].p(), d, M, E, K, logits.p(), ids.p(), wts.p()))
+            run("route_pack", lambda: api.sj_route_pack(None, ids.p(), M, K, E, tok.p(), slt.p(), cnt.p(), off.p(), ps.p(), pp.p(), cap))
+            run("moe_gather", lambda: api.sj_moe_gather(None, z.p(), d, d, ps.p(), K, cap, zp.p(), zpt.p(), cap))
+            run("expert_gate_up", lambda: api.sj_moe_gate_up_fwd(None, off.p(), E, cap, zp.p(), d, d, y["gu_t"].p(), y["gu_t"].p(F * d * 2), d, 2 * F * d, F, g_.p(), u_.p(), h_.p(), F, ht.p(), cap))
+            run("expert_down", lambda: api.sj_moe_down_fwd(None, off.p(), E, cap, h_.p(), F, F, y["d_t"].p(), F, d * F, d, yp.p(), d))
+            run("combine_residual", lambda: api.sj_moe_combine(None, yp.p(), d, d, ids.p(), pp.p(), wts.p(), M, K, x1.p(), d, out.p(), d))
+        for y in reversed(layers):
+            gu_off = E * d * 2 * F
+            run("combine_bwd", lambda: api.sj_moe_combine_bwd(None, yp.p(), d, d, ps.p(), wts.p(), K, cap, dres.p(), d, dxh.p(), dxl.p(), dxth.p(), dxtl.p(), cap, dwts.p()))
+            run("expert_down_dx_swiglu", lambda: api.sj_moe_down_bwd_swiglu_p(None, off.p(), E, cap, dxh.p(), dxl.p(), d, d, y["mirror"].p(gu_off * 2), d, F * d, F, g_.p(), u_.p(), F, dgh.p(), dgl.p(), 2 * F, dgth.p(), dgtl.p(), cap))
+            run("expert_down_dw", lambda: api.sj_moe_gemm_dw(None, off.p(), E, cap, F, d, ht.p(), cap, dxth.p(), dxtl.p(), cap, y["g"].p(gu_off * 4), d, F * d))
+            run("expert_gate_up_dx", lambda: api.sj_moe_gemm_rows(None, off.p(), E, cap, d, 2 * F, dgh.p(), dgl.p(), 2 * F, y["mirror"].p(), 2 * F, d * 2 * F, dzp.p(), d, 0))
+            run("expert_gate_up_dw", lambda: api.sj_moe_gemm_dw(None, off.p(), E, cap, d, 2 * F, zpt.p(), cap, dgth.p(), dgtl.p(), cap, y["g"].p(), 2 * F, d * 2 * F))
+            run("gather_route_bwd", lambda: api.sj_moe_gather_bwd(None, dzp.p(), d, d, ids.p(), pp.p(), wts.p(), logits.p(), dwts.p(), y["wr"].p(), M, K, E, dres.p(), d, dz.p(), d, dlog.p()))
+            run("router_dw", lambda: api.sj_gemm(None, 1, 0, d, E, M, z.p(), 4, d, dlog.p(), 0, E, dwr.p(), 0, E, 0, ws.p(), ws.nbytes))
+        for y in layers:
+            run("expert_adamw", lambda: api.sj_adamw(None, y["w"].p(), y["g"].p(), y["m"].p(), y["v"].p(), y["P"], cf(3e-4), cf(0.9), cf(0.95), cf(0.0), cf(0.01), cf(10.0), cf(20.0), cf(1.0)))
+            run("mirror_cast", lambda: api.sj_cast(None, y["w"].p(), 0, y["mirror"].p(), 4, y["P"]))
+
+    for _ in range(args.warmup):
+        step(None)
+    ms = _time_region(api, step, args.steps)
+    T = _OpTimer(api)
+    step(T)
+    prof = T.collect()
+    Pexp = layers[0]["P"]
+    work = {"expert_gate_up": ("flop", 2 * S * d * 2 * F), "expert_down": ("flop", 2 * S * F * d),
+            "expert_down_dx_swiglu": ("flop", 2 * S * F * d), "expert_down_dw": ("flop", 2 * S * F * d),
+            "expert_gate_up_dx": ("flop", 2 * S * d * 2 * F), "expert_gate_up_dw": ("flop", 2 * S * d * 2 * F),
+            "router_topk": ("flop", 2 * M * d * E), "router_dw": ("flop", 2 * M * d * E),
+            "expert_adamw": ("byte", 28 * Pexp), "mirror_cast": ("byte", 6 * Pexp),
+            "moe_gather": ("byte", 3 * M * K * d * 2), "combine_residual": ("byte", M * K * d * 2 + 2 * M * d * 2),
+            "combine_bwd": ("byte", M * K * d * 2 + M * d * 4 + 4 * cap * d * 2),
+            "gather_route_bwd": ("byte", M * K * d * 4 + 2 * M * d * 4), "route_pack": ("byte", 2 * S * 4 * 2)}
+    flops = L * 3 * (2 * S * d * 2 * F + 2 * S * F * d)
+    log(f"[bench moe] {args.steps} steps: {ms:.4f} ms/step; grouped expert GEMM {flops / 1e9:.1f} GF/step "
+        f"-> {flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s")
+    _report("MoE FFN train tokens/sec (grouped-GEMM fwd+bwd + expert AdamW)", "tokens/s", M / (ms * 1e-3), ms, args,
+            {"workload": "cfg4 MoE FFN: 4 layers, d512, 8 SwiGLU experts x 1024, top-2, 4096 tokens, bf16 "
+                         "(attention excluded)", "global_batch": 8, "seq_len": 512, "parallelism": "single-gpu"},
+            prof, work, "bf16",
+            {"expert_gemm_mfma": {"algorithmic_tflop_per_step": round(flops / 1e12, 4),
+                                  "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2)}})
+
+
+def workload_pvjp(args):
+    """cfg5 parameter-VJP pieces of one step: 16384
+    tokens, d 1024, 12 layers, FFN 2752, rank 16, 10% of 32-row blocks.  One
+    index draw and one CGS2 basis (shared by all groups: same n, rank and
+    width), a prepare per projection group (QKV and gate/up of 12 layers),
+    the coefficient GEMM of every compressed member (q, k, v, gate, up), and
+    the factored SGD update over all 133.5M parameters (dense gradients for
+    the single-use projections, embedding, norms and head).  The dense
+    model's own forward/backward GEMMs are not part of this measurement."""
+    import ctypes
+    import numpy as np
+    from sejong_amd import _native as N
+    lib = N.load(); api = N.api
+    n, d, F, L, HQ, HK, V = 16384, 1024, 2752, 12, 16, 4, 257
+    J = d // HQ * HK
+    cf = ctypes.c_float
+    keep = []
+    B = lambda nbytes: _Buf(api, nbytes, keep)
+    rng = np.random.default_rng(1)
+    R, blocks, S = 16, 32, 4
+    k = S * 32
+    seed = 0x1234
+    donor = B(n * 2 * F * 2).upload(_bf16(rng.normal(0, 1, (n, 2 * F))))
+    xt = B(d * n * 2).upload(_bf16(rng.normal(0, 1, (d, n))))
+    scr, cols, rows_, fmap = B((2 * F + blocks) * 4), B(R * 4), B(k * 4), B(d * 4)
+    q = B(n * R * 4)
+    wsb = B(lib.sj_pvjp_basis_workspace_bytes(n, R))
+    eps = lib.sj_pvjp_basis_tolerance(n, R)
+    groups = []
+    for g in range(2 * L):
+        groups.append(dict(left=B(d * R * 4), e=B((R + k) * n * 4), eh=B((R + k) * n * 2), el=B((R + k) * n * 2)))
+    # dY^T planes of a group's members, concatenated as the step keeps them
+    # ([q|k|v] and [gate|up] rows): one coefficient GEMM per group
+    W2 = 2 * F
+    dyh = B(W2 * n * 2).upload(_bf16(rng.normal(0, 1e-4, (W2, n))))
+    dyl = B(W2 * n * 2).upload(np.zeros(W2 * n, np.uint16))
+    wsp = B(max(lib.sj_pvjp_prepare_workspace_bytes(d, n, R), lib.sj_pvjp_vjp_workspace_bytes(R + k, W2, n), 256))
+    # parameters (reference layout shapes) and their gradients
+    members = []   # (rows, cols, group index or None, member width)
+    shapes = [("embedding", V, d, None)]
+    for l in range(L):
+        shapes += [("an", 1, d, None), ("fn", 1, d, None), ("q", d, d, 2 * l), ("k", d, J, 2 * l), ("v", d, J, 2 * l),
+                   ("o", d, d, None), ("gate", d, F, 2 * l + 1), ("up", d, F, 2 * l + 1), ("down", F, d, None)]
+    shapes += [("final_norm", 1, d, None), ("output", d, V, None)]
+    total = sum(r * c for _, r, c, _ in shapes)
+    params, terms, coeffs = [], [], []
+    # coefficients per group [R+k][sum of member widths]; a member's right /
+    # tail are column slices of it (row stride = the group width)
+    gwidth = {}
+    for name, r, c, gi in shapes:
+        if gi is not None:
+            gwidth[gi] = gwidth.get(gi, 0) + c
+    gco = {gi: B((R + k) * wdt * 4) for gi, wdt in gwidth.items()}
+    coeffs = [(gi, gco[gi], wdt) for gi, wdt in sorted(gwidth.items())]
+    col0 = {}
+    for name, r, c, gi in shapes:
+        w = B(r * c * 4).upload(rng.normal(0, 0.02, r * c).astype(np.float32))
+        if gi is None:
+            dense = B(r * c * 4).upload(rng.normal(0, 1e-4, r * c).astype(np.float32))
+            params.append(N.FactoredParam(w.ptr, dense.ptr, r, c, int(r > 1), 0, 0))
+        else:
+            off = col0.get(gi, 0); col0[gi] = off + c
+            base, wdt = gco[gi].ptr, gwidth[gi]
+            terms.append(N.FactoredTerm(groups[gi]["left"].ptr, base + off * 4, base + (R * wdt + off) * 4, fmap.ptr,
+                                        R, 1.0, wdt))
+            params.append(N.FactoredParam(w.ptr, None, r, c, 1, len(terms) - 1, 1))
+    PA = (N.FactoredParam * len(params))(*params)
+    TA = (N.FactoredTerm * len(terms))(*terms)
+    nbytes = lib.sj_factored_meta_bytes(PA, len(params), len(terms))
+    host = np.zeros(nbytes, np.uint8)
+    tiles = ctypes.c_long()
+    api.sj_factored_pack(PA, len(params), TA, len(terms), ctypes.c_void_p(host.ctypes.data), nbytes, ctypes.byref(tiles))
+    meta = B(nbytes).upload(host)
+    part, norm = B(tiles.value * 8), B(8)
+    api.sj_synchronize(None)
+
+    def step(T):
+        run = (lambda nm, f: T.op(nm, f)) if T else (lambda nm, f: f())
+        run("pvjp_indices", lambda: api.sj_pvjp_indices(None, seed, d, 2 * F, blocks, S, R, 32, scr.p(), cols.p(), rows_.p(), fmap.p()))
+        run("pvjp_basis", lambda: api.sj_pvjp_basis(None, donor.p(), 4, 2 * F, n, cols.p(), R, cf(eps), q.p(), wsb.p(), wsb.nbytes))
+        for g in groups:
+            run("pvjp_prepare", lambda: api.sj_pvjp_prepare(None, xt.p(), n, d, n, q.p(), R, rows_.p(), k, cf(blocks / S), g["left"].p(), g["e"].p(), g["eh"].p(), g["el"].p(), n, wsp.p(), wsp.nbytes))
+        for gi, co, c in coeffs:
+            g = groups[gi]
+            run("pvjp_coefficients", lambda: api.sj_pvjp_vjp(None, g["eh"].p(), g["el"].p(), n, R + k, n, dyh.p(), dyl.p(), n, c, co.p(), c, wsp.p(), wsp.nbytes))
+        run("factored_norm", lambda: api.sj_factored_apply(None, meta.p(), tiles.value, 2, cf(0), cf(0), part.p()))
+        run("norm_sum", lambda: api.sj_sum_f64(None, part.p(), tiles.value, norm.p()))
+        run("factored_sgd_update", lambda: api.sj_factored_apply(None, meta.p(), tiles.value, 1, cf(1e-2), cf(0.0), None))
+
+    for _ in range(args.warmup):
+        step(None)
+    ms = _time_region(api, step, args.steps)
+    T = _OpTimer(api)
+    step(T)
+    prof = T.collect()
+    dense_params = sum(r * c for _, r, c, gi in shapes if gi is None)
+    upd_bytes = 8 * total + 4 * dense_params
+    avg_b = sum(c for _, _, c in coeffs) / len(coeffs)
+    work = {"pvjp_prepare": ("flop", 2 * d * R * n), "pvjp_coefficients": ("flop", 2 * (R + k) * avg_b * n),
+            "factored_sgd_update": ("byte", upd_bytes), "factored_norm": ("byte", 4 * total + 4 * dense_params),
+            "pvjp_basis": ("byte", n * R * 4 * 2), "pvjp_indices": ("byte", d * 4), "norm_sum": ("byte", tiles.value * 8)}
+    log(f"[bench pvjp] {args.steps} steps: {ms:.4f} ms/step; {total / 1e6:.2f}M parameters, factored update "
+        f"{upd_bytes / 1e9:.2f} GB")
+    _report("parameter-VJP pieces per training step (tokens/s)", "tokens/s", n / (ms * 1e-3), ms, args,
+            {"workload": "cfg5 parameter-VJP pieces: 16384 tokens, d1024, 12 layers, FFN 2752, rank 16, 10% of "
+                         "32-row blocks (indices + basis + 24 prepares + 60 coefficient GEMMs + factored SGD over "
+                         f"{total / 1e6:.2f}M params; dense forward/backward excluded)",
+             "global_batch": 16, "seq_len": 1024, "parallelism": "single-gpu"},
+            prof, work, "f32")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +452,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
     ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
+    ap.add_argument("--workload", default="step", choices=["step", "moe", "pvjp"],
+                    help="step: the cfg2 training step (default, the headline); moe: the cfg4 MoE FFN; "
+                         "pvjp: the cfg5 parameter-VJP pieces")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain fp32 copy kernel (sj_cast) over this many MiB, 3 times, and exit: "
                          "the calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -155,6 +467,12 @@ def main():
 
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.workload == "moe":
+        workload_moe(args)
+        return
+    if args.workload == "pvjp":
+        workload_pvjp(args)
         return
 
     import numpy as np

@@ -388,11 +388,15 @@ int sj_pvjp_indices(void *stream, uint64_t seed, long a, long donor_width, long 
                     long rank, long block_rows, int32_t *scratch, int32_t *columns, int32_t *rows,
                     int32_t *map);
 /* kernels parameter_basis / parameter_basis_register (parameter.py:65-128):
- * Q fp32 [n][rank] by classical Gram-Schmidt twice over the donor columns
- * (y [n][ldy], f32 or bf16), a column zeroed when |v|^2 <= eps^2 |orig|^2.
- * rank <= 64. */
+ * Q fp32 [n][rank], an orthonormal basis of the picked donor columns (y
+ * [n][ldy], f32 or bf16) in column order, a column zeroed when its residual
+ * after the earlier columns has |v|^2 <= eps^2 |orig|^2.  Computed as
+ * CholeskyQR2 (FP64 Gram, the Cholesky pivot is that residual norm); Q
+ * spans the same space as the reference's CGS2.  rank <= 64.  Workspace:
+ * sj_pvjp_basis_workspace_bytes. */
+size_t sj_pvjp_basis_workspace_bytes(long n, long rank);
 int sj_pvjp_basis(void *stream, const void *y, int dtype, long ldy, long n, const int32_t *columns, long rank,
-                  float eps, float *q);
+                  float eps, float *q, void *workspace, size_t workspace_bytes);
 /* kernels parameter_prepare / parameter_residual (parameter.py:131-190)
  * with X given transposed (x_t [a][ldxt] bf16, columns n .. n rounded up
  * to 8 zero): left = X^T Q fp32 [a][rank];
@@ -425,16 +429,18 @@ typedef struct {
 } sj_factored_param;
 typedef struct {
   const float *left;     /* [rows][rank] */
-  const float *right;    /* [rank][cols] */
-  const float *tail;     /* [k][cols] */
+  const float *right;    /* [rank][ld] */
+  const float *tail;     /* [k][ld] */
   const int32_t *row_map; /* [rows] */
   long rank;
   float scale;
+  long ld;               /* row stride of right and tail; 0 = the parameter's cols */
 } sj_factored_term;
 /* GradientPlan::new + pack on the host: fills `host_meta`
- * (sj_factored_meta_bytes) with the device table the caller uploads, and
- * the number of 16x256 tiles. */
-size_t sj_factored_meta_bytes(long nparams, long nterms);
+ * (sj_factored_meta_bytes) with the device table the caller uploads
+ * (parameters, terms and the owner of every 32x256 tile), and the number
+ * of tiles. */
+size_t sj_factored_meta_bytes(const sj_factored_param *params, long nparams, long nterms);
 int sj_factored_pack(const sj_factored_param *params, long nparams, const sj_factored_term *terms, long nterms,
                      void *host_meta, size_t bytes, long *tiles);
 /* GradientPlan::tiles: action 0 materialize (G written into w), 1 update

@@ -30,7 +30,8 @@ class FactoredParam(ctypes.Structure):
 
 class FactoredTerm(ctypes.Structure):
     """sj_factored_term of include/sejong_hip.h."""
-    _fields_ = [("left", _P), ("right", _P), ("tail", _P), ("row_map", _P), ("rank", _L), ("scale", _F)]
+    _fields_ = [("left", _P), ("right", _P), ("tail", _P), ("row_map", _P), ("rank", _L), ("scale", _F),
+                ("ld", _L)]
 
 
 class SejongError(RuntimeError):
@@ -105,12 +106,13 @@ SIGNATURES = {
     "sj_pvjp_selects_compression": (_I, [_L, _DB, _L, _L, _L, _L, _L, _L]),
     "sj_pvjp_basis_tolerance": (_F, [_L, _L]),
     "sj_pvjp_indices": (_I, [_P, _U64, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P]),
-    "sj_pvjp_basis": (_I, [_P, _P, _I, _L, _L, _P, _L, _F, _P]),
+    "sj_pvjp_basis_workspace_bytes": (_S, [_L, _L]),
+    "sj_pvjp_basis": (_I, [_P, _P, _I, _L, _L, _P, _L, _F, _P, _P, _S]),
     "sj_pvjp_prepare_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_pvjp_prepare": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _F, _P, _P, _P, _P, _L, _P, _S]),
     "sj_pvjp_vjp_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_pvjp_vjp": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _L, _P, _S]),
-    "sj_factored_meta_bytes": (_S, [_L, _L]),
+    "sj_factored_meta_bytes": (_S, [_P, _L, _L]),
     "sj_factored_pack": (_I, [_P, _L, _P, _L, _P, _S, _P]),
     "sj_factored_apply": (_I, [_P, _P, _L, _I, _F, _F, _P]),
     "sj_sum_f64": (_I, [_P, _P, _L, _P]),

@@ -172,7 +172,17 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     const unsigned xcd = b & 7, local = b >> 3, q8 = nb >> 3, r8x = nb & 7;
     logical = xcd * q8 + (xcd < r8x ? xcd : r8x) + local;
   }
-  const unsigned tx = logical % nx, ty = (logical / nx) % ny, tz = logical / (nx * ny);
+  // the smaller tile dimension varies fastest, so consecutive workgroups
+  // (one XCD's run) share the operand of the larger one
+  unsigned tx, ty;
+  if (ny < nx) {
+    ty = logical % ny;
+    tx = (logical / ny) % nx;
+  } else {
+    tx = logical % nx;
+    ty = (logical / nx) % ny;
+  }
+  const unsigned tz = logical / (nx * ny);
   const long m0 = (long)ty * BM, n0 = (long)tx * BN;
   int ge = 0;
   if (p.gmode == 1) {
@@ -598,7 +608,8 @@ void pick(long M, long N, int& bm, int& bn) {
 int splits_for(long M, long N, long K, int bm, int bn);
 
 // Tile and split-K plan of sj_gemm_planes (measured on the cfg2 shapes):
-// dW-shaped products (small output, K >= 2048) take 4 K slices and the
+// very long K (>= 8192) with a small output takes 64x64 tiles and up to 32
+// K slices of >= 512; dW-shaped products (K >= 2048) take 4 K slices and the
 // largest tile that still gives >= 144 workgroups; split-A products (dX)
 // with K <= 1024 and N a multiple of 128 take 64x128 tiles when those
 // cover half the CUs; the rest use pick().
@@ -607,6 +618,18 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
   const char* et = getenv("SJ_GEMM_TILE");
   const char* es = getenv("SJ_GEMM_SPLITS");
   if (!et && !es) {
+    if (tiles(M, N, 64, 64) < cu && K >= 8192) {
+      // very long K (token-contracted products of the parameter VJP): enough
+      // slices of >= 512 for about one workgroup per CU
+      bm = bn = 64;
+      const long t = tiles(M, N, 64, 64);
+      long sp = (cu + t - 1) / t;
+      sp = sp < 4 ? 4 : sp;
+      sp = sp > 32 ? 32 : sp;
+      sp = sp > K / 512 ? K / 512 : sp;
+      splits = (int)sp;
+      return;
+    }
     if (tiles(M, N, 64, 64) < cu && K >= 2048) {
       splits = K / 256 < 4 ? (int)(K / 256) : 4;
       const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};

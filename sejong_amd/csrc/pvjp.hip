@@ -88,80 +88,147 @@ __global__ __launch_bounds__(256) void k_pvjp_indices(int32_t* __restrict__ scra
 }
 
 // ------------------------------------------------------------------- basis
-// parameter_basis (parameter.py:85-128) in one workgroup of 1024 threads:
-// column c is loaded from the donor, its projection on columns 0..c-1 is
-// removed twice (coefficients by block reductions), and it is normalised
-// or zeroed.  Q [n][R] lives in global memory (L2 resident); R <= 64.
-constexpr int BT = 1024;
+// The reference orthonormalises the picked donor columns with classical
+// Gram-Schmidt applied twice in one workgroup (parameter.py:65-128).  Here:
+// CholeskyQR2 -- G = V^T V in FP64 from partial sums over the whole chip, a
+// one-wavefront Cholesky G = L L^T, Q = V L^-T applied row-parallel, and a
+// second pass on Q.  The Cholesky pivot of column c is |v_c - its
+// projection on the earlier columns|^2, the quantity CGS2 tests, so the same
+// drop rule applies: a column whose pivot is <= eps^2 |v_c|^2 gets a zero
+// column in L^-T (and so in Q) and is left out of the later projections.
+// The factored gradient depends on Q only through the projector Q Q^T.
 constexpr int RMAX = 64;
-__device__ __forceinline__ float block_sum_1024(float v, float* red) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __syncthreads();
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float s = 0.f;
+constexpr int GR = 64;      // rows staged per LDS chunk
+constexpr int GBLK = 128;   // workgroups of the Gram pass
+
+// partial Gram of rows: v[row][j] = source value; pass 1 gathers donor
+// columns (dtype f32/bf16), pass 2 reads Q rows.  Pairs i <= j.
+__global__ __launch_bounds__(256) void k_gram_partial(const void* __restrict__ y, int ydt, long ldy,
+                                                      const int32_t* __restrict__ cols, const float* __restrict__ q,
+                                                      long n, int R, double* __restrict__ partial) {
+  __shared__ float sv[GR][RMAX + 1];
+  const int t = threadIdx.x;
+  const int P = R * (R + 1) / 2;
+  double acc[9];
+  int pi[9], pj[9];
 #pragma unroll
-  for (int i = 0; i < BT / 64; i++) s += red[i];
-  return s;
+  for (int u = 0; u < 9; u++) {
+    acc[u] = 0.0;
+    int p = t + 256 * u, i = 0;
+    // pair p -> (i, j), i <= j, row-major over the upper triangle
+    while (p >= R - i && i < R) {
+      p -= R - i;
+      i++;
+    }
+    pi[u] = i < R ? i : 0;
+    pj[u] = i < R ? i + p : 0;
+  }
+  const long per = (n + gridDim.x - 1) / gridDim.x;
+  const long r0 = blockIdx.x * per, r1 = r0 + per < n ? r0 + per : n;
+  for (long c0 = r0; c0 < r1; c0 += GR) {
+    __syncthreads();
+    for (int q2 = t; q2 < GR * R; q2 += 256) {
+      const int rr = q2 / R, j = q2 - rr * R;
+      const long row = c0 + rr;
+      float v = 0.f;
+      if (row < r1) v = q ? q[row * R + j] : load_as_f32(y, ydt, row * ldy + cols[j]);
+      sv[rr][j] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 9; u++) {
+      if (t + 256 * u < P) {
+        const float* ci = &sv[0][pi[u]];
+        const float* cj = &sv[0][pj[u]];
+        double a = 0.0;
+        for (int rr = 0; rr < GR; rr++) a += (double)ci[rr * (RMAX + 1)] * (double)cj[rr * (RMAX + 1)];
+        acc[u] += a;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 9; u++)
+    if (t + 256 * u < P) partial[(long)blockIdx.x * P + t + 256 * u] = acc[u];
 }
 
-__global__ __launch_bounds__(BT) void k_pvjp_basis(const void* __restrict__ y, int ydt, long ldy, long n,
-                                                   const int32_t* __restrict__ cols, int R, float eps,
-                                                   float* __restrict__ q) {
-  __shared__ float red[BT / 64];
-  __shared__ float part[BT / 64][RMAX];
-  __shared__ float coef[RMAX];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+// one wavefront: G = sum of the partials (fixed order), Cholesky in place
+// with the drop rule (pivot <= eps^2 * the column's |v|^2 -> dropped), and
+// T = L^-T with zero columns for dropped ones: lane l owns row l of T
+// (FP64 in t64, fp32 copy in tmat for the apply).
+__global__ __launch_bounds__(64) void k_chol_inv(const double* __restrict__ partial, int nblk, int R, float eps,
+                                                 double* __restrict__ t64, float* __restrict__ tmat) {
+  __shared__ double G[RMAX][RMAX + 1];  // G; L in the lower triangle as it is formed
+  __shared__ double dg[RMAX];
+  __shared__ int keep[RMAX];
+  const int l = threadIdx.x;
+  const int P = R * (R + 1) / 2;
+  for (int p = l; p < P; p += 64) {
+    double sum = 0.0;
+    for (int b = 0; b < nblk; b++) sum += partial[(long)b * P + p];
+    int i = 0, pp = p;
+    while (pp >= R - i) {
+      pp -= R - i;
+      i++;
+    }
+    G[i][i + pp] = sum;
+    G[i + pp][i] = sum;
+  }
+  __syncthreads();
+  if (l < R) dg[l] = G[l][l];
+  __syncthreads();
+  const double e2 = (double)eps * (double)eps;
   for (int c = 0; c < R; c++) {
-    const long col = cols[c];
-    float orig = 0.f;
-    for (long r = t; r < n; r += BT) {
-      const float v = load_as_f32(y, ydt, r * ldy + col);
-      q[r * R + c] = v;
-      orig += v * v;
+    double d = G[c][c];
+    for (int k = 0; k < c; k++) d -= G[c][k] * G[c][k];
+    const bool kp = d > e2 * dg[c] && d > 0.0;
+    const double piv = kp ? sqrt(d) : 0.0;
+    double v = 0.0;
+    if (l > c && l < R && kp) {
+      v = G[l][c];
+      for (int k = 0; k < c; k++) v -= G[l][k] * G[c][k];
+      v /= piv;
     }
-    orig = block_sum_1024(orig, red);
-    for (int rep = 0; rep < 2; rep++) {
-      // coefficients against the previous columns, RMAX at a time
-      float pc[RMAX];
-#pragma unroll
-      for (int i = 0; i < RMAX; i++) pc[i] = 0.f;
-      for (long r = t; r < n; r += BT) {
-        const float v = q[r * R + c];
-#pragma unroll
-        for (int i = 0; i < RMAX; i++)
-          if (i < c) pc[i] += q[r * R + i] * v;
-      }
-#pragma unroll
-      for (int i = 0; i < RMAX; i++) {
-        if (i >= c) break;
-        const float s = wave_sum(pc[i]);
-        if (lane == 0) part[w][i] = s;
-      }
-      __syncthreads();
-      if (t < c) {
-        float s = 0.f;
-        for (int k = 0; k < BT / 64; k++) s += part[k][t];
-        coef[t] = s;
-      }
-      __syncthreads();
-      for (long r = t; r < n; r += BT) {
-        float v = q[r * R + c];
-        for (int i = 0; i < c; i++) v -= q[r * R + i] * coef[i];
-        q[r * R + c] = v;
-      }
-      __syncthreads();
-    }
-    float mag = 0.f;
-    for (long r = t; r < n; r += BT) {
-      const float v = q[r * R + c];
-      mag += v * v;
-    }
-    mag = block_sum_1024(mag, red);
-    const float inv = mag > eps * eps * orig ? rsqrtf(mag) : 0.f;
-    for (long r = t; r < n; r += BT) q[r * R + c] *= inv;
     __syncthreads();
+    if (l > c && l < R) G[l][c] = v;
+    if (l == c) {
+      G[c][c] = piv;
+      keep[c] = kp;
+    }
+    __syncthreads();
+  }
+  for (int j = 0; j < R; j++) {
+    if (l < R) {
+      double v = 0.0;
+      if (keep[j]) {
+        v = l == j ? 1.0 : 0.0;
+        for (int k = 0; k < j; k++) v -= G[j][k] * t64[l * R + k];
+        v /= G[j][j];
+      }
+      t64[l * R + j] = v;
+      tmat[l * R + j] = (float)v;
+    }
+  }
+}
+
+// Q[row] = v[row] T (pass 1 from the donor columns, pass 2 in place)
+__global__ __launch_bounds__(256) void k_basis_apply(const void* __restrict__ y, int ydt, long ldy,
+                                                     const int32_t* __restrict__ cols, float* __restrict__ q, long n,
+                                                     int R, const float* __restrict__ tmat, int from_q) {
+  __shared__ float T[RMAX * RMAX];
+  for (int p = threadIdx.x; p < R * R; p += 256) T[p] = tmat[p];
+  __syncthreads();
+  const long row = blockIdx.x * 256L + threadIdx.x;
+  if (row >= n) return;
+  float v[RMAX];
+#pragma unroll
+  for (int k = 0; k < RMAX; k++)
+    if (k < R) v[k] = from_q ? q[row * R + k] : load_as_f32(y, ydt, row * ldy + cols[k]);
+  for (int j = 0; j < R; j++) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < RMAX; k++)
+      if (k < R) s += v[k] * T[k * R + j];
+    q[row * R + j] = s;
   }
 }
 
@@ -220,16 +287,19 @@ struct FTerm {
   const float* right;
   const float* tail;
   const int32_t* row_map;
-  long rank;
+  long rank, ld;
   float scale;
   int pad;
 };
 struct FMetaHeader {
   long nparams, nterms, tiles, pad;
 };
+// metadata layout: header, params[nparams], terms[nterms], owners[tiles]
+// (the parameter of each tile, as the reference's Owners table)
 
-constexpr int FBM = 16;   // tile rows
+constexpr int FBM = 32;   // tile rows
 constexpr int FBN = 256;  // tile columns (one per thread)
+constexpr int FRMAX = 64; // rank staged per LDS pass
 
 // parameter_gradient_update / _materialize / _norm (parameter.py:244-291):
 // one workgroup per tile of one parameter (the owner found from the
@@ -240,10 +310,10 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
   const FMetaHeader* hd = (const FMetaHeader*)meta;
   const FParam* params = (const FParam*)(meta + sizeof(FMetaHeader));
   const FTerm* terms = (const FTerm*)(params + hd->nparams);
+  const int32_t* owners = (const int32_t*)(terms + hd->nterms);
+  __shared__ float sl[FBM][FRMAX + 1];  // (left * scale) rows of this tile
   const long tile = blockIdx.x;
-  long pi = 0;
-  while (pi + 1 < hd->nparams && tile >= params[pi + 1].first_tile) pi++;
-  const FParam P = params[pi];
+  const FParam P = params[owners[tile]];
   const long local = tile - P.first_tile;
   const long m0 = (local / P.col_tiles) * FBM, n = (local % P.col_tiles) * FBN + threadIdx.x;
   const bool colok = n < P.cols;
@@ -253,13 +323,18 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
   // head = sum over the terms' ranks of (left * scale) right
   for (int ti = 0; ti < P.term_count; ti++) {
     const FTerm tm = terms[P.term_begin + ti];
-    for (long r = 0; r < tm.rank; r++) {
-      const float rv = colok ? tm.right[r * P.cols + n] : 0.f;
+    for (long r0 = 0; r0 < tm.rank; r0 += FRMAX) {
+      const long rn = tm.rank - r0 < FRMAX ? tm.rank - r0 : FRMAX;
+      __syncthreads();
+      for (long q = threadIdx.x; q < FBM * rn; q += 256) {
+        const long i = q / rn, r = q - i * rn, m = m0 + i;
+        sl[i][r] = m < P.rows ? tm.left[m * tm.rank + r0 + r] * tm.scale : 0.f;
+      }
+      __syncthreads();
+      for (long r = 0; r < rn; r++) {
+        const float rv = colok ? tm.right[(r0 + r) * tm.ld + n] : 0.f;
 #pragma unroll
-      for (int i = 0; i < FBM; i++) {
-        const long m = m0 + i;
-        const float lv = m < P.rows ? tm.left[m * tm.rank + r] * tm.scale : 0.f;
-        g[i] += lv * rv;
+        for (int i = 0; i < FBM; i++) g[i] += sl[i][r] * rv;
       }
     }
   }
@@ -276,7 +351,7 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
       const long m = m0 + i;
       if (m < P.rows && colok) {
         const int sel = tm.row_map[m];
-        if (sel >= 0) g[i] += tm.tail[(long)sel * P.cols + n] * tm.scale;
+        if (sel >= 0) g[i] += tm.tail[(long)sel * tm.ld + n] * tm.scale;
       }
     }
   }
@@ -286,6 +361,7 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
     for (int i = 0; i < FBM; i++)
       if (m0 + i < P.rows && colok) s += (double)g[i] * (double)g[i];
     __shared__ double red[4];
+    __syncthreads();
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -388,12 +464,33 @@ extern "C" int sj_pvjp_indices(void* stream, uint64_t seed, long a, long donor_w
   return SJ_OK;
 }
 
+extern "C" size_t sj_pvjp_basis_workspace_bytes(long n, long rank) {
+  (void)n;
+  return sizeof(double) * (size_t)GBLK * (size_t)(rank * (rank + 1) / 2) +
+         (sizeof(double) + sizeof(float)) * (size_t)(rank * rank);
+}
+
 extern "C" int sj_pvjp_basis(void* stream, const void* y, int dtype, long ldy, long n, const int32_t* columns,
-                             long rank, float eps, float* q) {
+                             long rank, float eps, float* q, void* workspace, size_t workspace_bytes) {
   SJ_REQUIRE(n > 0 && rank > 0 && rank <= RMAX && (dtype == SJ_F32 || dtype == SJ_BF16),
              "parameter_basis: rank %ld (<= %d)", rank, RMAX);
-  hipLaunchKernelGGL(k_pvjp_basis, dim3(1), dim3(BT), 0, (hipStream_t)stream, y, dtype, ldy, n, columns, (int)rank,
-                     eps, q);
+  const size_t need = sj_pvjp_basis_workspace_bytes(n, rank);
+  if (!workspace || workspace_bytes < need)
+    return sjh::fail(SJ_ERR_CAPACITY, "parameter_basis: required %zu bytes, available %zu bytes", need,
+                     workspace_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  double* partial = (double*)workspace;
+  double* t64 = partial + (size_t)GBLK * (size_t)(rank * (rank + 1) / 2);
+  float* tmat = (float*)(t64 + rank * rank);
+  const int R = (int)rank;
+  const unsigned rows_blocks = (unsigned)((n + 255) / 256);
+  for (int pass = 0; pass < 2; pass++) {
+    hipLaunchKernelGGL(k_gram_partial, dim3(GBLK), dim3(256), 0, s, y, dtype, ldy, columns, pass ? q : nullptr, n, R,
+                       partial);
+    hipLaunchKernelGGL(k_chol_inv, dim3(1), dim3(64), 0, s, (const double*)partial, GBLK, R, eps, t64, tmat);
+    hipLaunchKernelGGL(k_basis_apply, dim3(rows_blocks), dim3(256), 0, s, y, dtype, ldy, columns, q, n, R,
+                       (const float*)tmat, pass);
+  }
   SJ_LAUNCH_CHECK("parameter_basis");
   return SJ_OK;
 }
@@ -442,16 +539,27 @@ extern "C" int sj_pvjp_vjp(void* stream, const uint16_t* e_hi, const uint16_t* e
                         workspace, workspace_bytes);
 }
 
-extern "C" size_t sj_factored_meta_bytes(long nparams, long nterms) {
-  return sizeof(FMetaHeader) + sizeof(FParam) * (size_t)nparams + sizeof(FTerm) * (size_t)nterms;
+// tiles of a parameter list (the owners table's length)
+static long factored_tiles(const sj_factored_param* params, long nparams) {
+  long t = 0;
+  for (long i = 0; i < nparams; i++)
+    t += ((params[i].rows + FBM - 1) / FBM) * ((params[i].cols + FBN - 1) / FBN);
+  return t;
+}
+
+extern "C" size_t sj_factored_meta_bytes(const sj_factored_param* params, long nparams, long nterms) {
+  if (!params || nparams <= 0 || nterms < 0) return 0;
+  return sizeof(FMetaHeader) + sizeof(FParam) * (size_t)nparams + sizeof(FTerm) * (size_t)nterms +
+         sizeof(int32_t) * (size_t)factored_tiles(params, nparams);
 }
 
 extern "C" int sj_factored_pack(const sj_factored_param* params, long nparams, const sj_factored_term* terms,
                                 long nterms, void* host_meta, size_t bytes, long* tiles) {
   SJ_REQUIRE(params && nparams > 0 && nterms >= 0 && (nterms == 0 || terms) && host_meta &&
-                 bytes >= sj_factored_meta_bytes(nparams, nterms),
+                 bytes >= sj_factored_meta_bytes(params, nparams, nterms) &&
+                 factored_tiles(params, nparams) < (1L << 31),
              "gradient plan requires parameters and a metadata buffer of %zu bytes",
-             sj_factored_meta_bytes(nparams, nterms));
+             sj_factored_meta_bytes(params, nparams, nterms));
   uint8_t* out = (uint8_t*)host_meta;
   FMetaHeader hd = {nparams, nterms, 0, 0};
   FParam* fp = (FParam*)(out + sizeof(FMetaHeader));
@@ -474,10 +582,25 @@ extern "C" int sj_factored_pack(const sj_factored_param* params, long nparams, c
     SJ_REQUIRE(s.left && s.right && s.tail && s.row_map && s.rank >= 0, "compact SGD term %ld", i);
     FTerm q = {};
     q.left = s.left; q.right = s.right; q.tail = s.tail; q.row_map = s.row_map; q.rank = s.rank; q.scale = s.scale;
+    q.ld = s.ld;
     memcpy(ft + i, &q, sizeof(q));
   }
+  // a term's ld defaults to the columns of the parameter that uses it
+  for (long i = 0; i < nparams; i++)
+    for (long j = params[i].term_begin; j < params[i].term_begin + params[i].term_count; j++) {
+      FTerm* q = ft + j;
+      if (q->ld <= 0) q->ld = params[i].cols;
+      SJ_REQUIRE(q->ld >= params[i].cols, "compact SGD term %ld: row stride %ld below %ld columns", j, q->ld,
+                 params[i].cols);
+    }
   hd.tiles = t;
   memcpy(out, &hd, sizeof(hd));
+  int32_t* own = (int32_t*)(ft + nterms);
+  for (long i = 0; i < nparams; i++) {
+    const long first = ((const FParam*)(fp + i))->first_tile;
+    const long count = ((params[i].rows + FBM - 1) / FBM) * ((params[i].cols + FBN - 1) / FBN);
+    for (long j = 0; j < count; j++) own[first + j] = (int32_t)i;
+  }
   if (tiles) *tiles = t;
   return SJ_OK;
 }

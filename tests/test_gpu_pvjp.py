@@ -49,7 +49,8 @@ def _prepare(N, X, Y, rank, frac, block_rows, seed, ydtype="f32"):
     Q = empty(n * R)
     eps = lib.sj_pvjp_basis_tolerance(n, R)
     YD = dev(Y, ydtype)
-    api.sj_pvjp_basis(None, YD.p, BF if ydtype == "bf16" else F32, b, n, COL.p, R, cf(eps), Q.p)
+    wsb = empty(max(lib.sj_pvjp_basis_workspace_bytes(n, R), 256), "u8")
+    api.sj_pvjp_basis(None, YD.p, BF if ydtype == "bf16" else F32, b, n, COL.p, R, cf(eps), Q.p, wsb.p, wsb.nbytes)
     n8 = (n + 7) // 8 * 8
     xt = np.zeros((a, n8)); xt[:, :n] = X.T
     XT = dev(xt, "bf16")
@@ -89,8 +90,8 @@ def _pack(N, params, terms):
         PA[i] = N.FactoredParam(w.ptr, dense.ptr if dense else None, r, c, decay, tb, tc)
     TA = (N.FactoredTerm * max(len(terms), 1))()
     for i, (left, right, tail, fmap, rank, scale) in enumerate(terms):
-        TA[i] = N.FactoredTerm(left.ptr, right.value, tail.value, fmap.ptr, rank, scale)
-    nbytes = lib.sj_factored_meta_bytes(len(params), len(terms))
+        TA[i] = N.FactoredTerm(left.ptr, right.value, tail.value, fmap.ptr, rank, scale, 0)
+    nbytes = lib.sj_factored_meta_bytes(PA, len(params), len(terms))
     host = np.zeros(nbytes, np.uint8)
     tiles = ctypes.c_long()
     api.sj_factored_pack(PA, len(params), TA, len(terms), ctypes.c_void_p(host.ctypes.data), nbytes,
