@@ -155,16 +155,24 @@ __global__ __launch_bounds__(256) void k_gram_partial(const void* __restrict__ y
 // with the drop rule (pivot <= eps^2 * the column's |v|^2 -> dropped), and
 // T = L^-T with zero columns for dropped ones: lane l owns row l of T
 // (FP64 in t64, fp32 copy in tmat for the apply).
-__global__ __launch_bounds__(64) void k_chol_inv(const double* __restrict__ partial, int nblk, int R, float eps,
-                                                 double* __restrict__ t64, float* __restrict__ tmat) {
+__global__ __launch_bounds__(256) void k_chol_inv(const double* __restrict__ partial, int nblk, int R, float eps,
+                                                  double* __restrict__ part4, double* __restrict__ t64,
+                                                  float* __restrict__ tmat) {
   __shared__ double G[RMAX][RMAX + 1];  // G; L in the lower triangle as it is formed
   __shared__ double dg[RMAX];
   __shared__ int keep[RMAX];
-  const int l = threadIdx.x;
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int P = R * (R + 1) / 2;
+  // each wavefront sums a quarter of the blocks (part4 [4][P] in the
+  // workspace), then the four are added in order
   for (int p = l; p < P; p += 64) {
     double sum = 0.0;
-    for (int b = 0; b < nblk; b++) sum += partial[(long)b * P + p];
+    for (int b = wv; b < nblk; b += 4) sum += partial[(long)b * P + p];
+    part4[wv * P + p] = sum;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < P; p += 256) {
+    const double sum = ((part4[p] + part4[P + p]) + part4[2 * P + p]) + part4[3 * P + p];
     int i = 0, pp = p;
     while (pp >= R - i) {
       pp -= R - i;
@@ -174,8 +182,10 @@ __global__ __launch_bounds__(64) void k_chol_inv(const double* __restrict__ part
     G[i + pp][i] = sum;
   }
   __syncthreads();
-  if (l < R) dg[l] = G[l][l];
+  if (wv == 0 && l < R) dg[l] = G[l][l];
   __syncthreads();
+  // the factorisation runs on wavefront 0; the others only keep the
+  // barriers company
   const double e2 = (double)eps * (double)eps;
   for (int c = 0; c < R; c++) {
     double d = G[c][c];
@@ -183,19 +193,20 @@ __global__ __launch_bounds__(64) void k_chol_inv(const double* __restrict__ part
     const bool kp = d > e2 * dg[c] && d > 0.0;
     const double piv = kp ? sqrt(d) : 0.0;
     double v = 0.0;
-    if (l > c && l < R && kp) {
+    if (wv == 0 && l > c && l < R && kp) {
       v = G[l][c];
       for (int k = 0; k < c; k++) v -= G[l][k] * G[c][k];
       v /= piv;
     }
     __syncthreads();
-    if (l > c && l < R) G[l][c] = v;
-    if (l == c) {
+    if (wv == 0 && l > c && l < R) G[l][c] = v;
+    if (wv == 0 && l == c) {
       G[c][c] = piv;
       keep[c] = kp;
     }
     __syncthreads();
   }
+  if (wv != 0) return;
   for (int j = 0; j < R; j++) {
     if (l < R) {
       double v = 0.0;
@@ -250,28 +261,51 @@ __global__ __launch_bounds__(256) void k_pvjp_qt(const float* __restrict__ q, in
 }
 
 // E[R+i][tok] = (X^T[row_i][tok] - sum_r Q[tok][r] A[row_i][r]) * inverse,
-// zero for row_i = -1 (parameter.py:167-190); fp32 and planes.
+// zero for row_i = -1 (parameter.py:167-190); fp32 and planes.  Thread per
+// token: its Q row is read once, the block's RROWS selected rows of A sit
+// in LDS.
+constexpr int RROWS = 16;
 __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict__ xt, long ldxt,
                                                        const float* __restrict__ q, int R, long n,
                                                        const float* __restrict__ left, const int32_t* __restrict__ rows,
-                                                       float inverse, float* __restrict__ e, bf16_t* __restrict__ eh,
-                                                       bf16_t* __restrict__ el, long lde, long n8) {
-  const long i = blockIdx.y;
+                                                       long k, float inverse, float* __restrict__ e,
+                                                       bf16_t* __restrict__ eh, bf16_t* __restrict__ el, long lde,
+                                                       long n8) {
+  __shared__ float sa[RROWS][RMAX];
+  __shared__ long srow[RROWS];
+  const long i0 = blockIdx.y * (long)RROWS;
+  for (int p = threadIdx.x; p < RROWS * R; p += 256) {
+    const int ii = p / R, r = p - ii * R;
+    const long row = i0 + ii < k ? rows[i0 + ii] : -1;
+    sa[ii][r] = row >= 0 ? left[row * R + r] : 0.f;
+  }
+  if (threadIdx.x < RROWS) srow[threadIdx.x] = i0 + threadIdx.x < k ? rows[i0 + threadIdx.x] : -1;
+  __syncthreads();
   const long tok = blockIdx.x * 256L + threadIdx.x;
   if (tok >= n8) return;
-  const long row = rows[i];
-  float v = 0.f;
-  if (row >= 0 && tok < n) {
-    float acc = 0.f;
-    for (int r = 0; r < R; r++) acc += q[tok * R + r] * left[row * R + r];
-    v = (bf2f(xt[row * ldxt + tok]) - acc) * inverse;
+  float qr[RMAX];
+#pragma unroll
+  for (int r = 0; r < RMAX; r++)
+    if (r < R) qr[r] = tok < n ? q[tok * R + r] : 0.f;
+  for (int ii = 0; ii < RROWS; ii++) {
+    const long i = i0 + ii;
+    if (i >= k) break;
+    const long row = srow[ii];
+    float v = 0.f;
+    if (row >= 0 && tok < n) {
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r < RMAX; r++)
+        if (r < R) acc += qr[r] * sa[ii][r];
+      v = (bf2f(xt[row * ldxt + tok]) - acc) * inverse;
+    }
+    const long o = (R + i) * lde + tok;
+    e[o] = v;
+    bf16_t h, l;
+    split_bf(v, h, l);
+    eh[o] = h;
+    el[o] = l;
   }
-  const long o = (R + i) * lde + tok;
-  e[o] = v;
-  bf16_t h, l;
-  split_bf(v, h, l);
-  eh[o] = h;
-  el[o] = l;
 }
 
 // ------------------------------------------------------------------- apply
@@ -297,14 +331,22 @@ struct FMetaHeader {
 // metadata layout: header, params[nparams], terms[nterms], owners[tiles]
 // (the parameter of each tile, as the reference's Owners table)
 
-constexpr int FBM = 32;   // tile rows
-constexpr int FBN = 256;  // tile columns (one per thread)
-constexpr int FRMAX = 64; // rank staged per LDS pass
+constexpr int FBM = 16;    // tile rows
+constexpr int FBN = 1024;  // tile columns: 4 per thread
+constexpr int FRMAX = 64;  // rank staged per LDS pass
+
+// up to 4 floats at p[0..cnt), one 16-byte access when vec
+__device__ __forceinline__ float4 ld4(const float* p, int cnt, bool vec) {
+  if (vec && cnt == 4) return *(const float4*)p;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < cnt; i++) v[i] = p[i];
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // parameter_gradient_update / _materialize / _norm (parameter.py:244-291):
-// one workgroup per tile of one parameter (the owner found from the
-// parameters' first tiles).  Action 0 materialize (G into w), 1 update,
-// 2 FP64 sum of G^2 per tile into partials.
+// one workgroup per 16x1024 tile of one parameter (owner from the table).
+// Action 0 materialize (G into w), 1 update, 2 FP64 sum of G^2 per tile.
 __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restrict__ meta, int action, float lr,
                                                         float decay, double* __restrict__ partials) {
   const FMetaHeader* hd = (const FMetaHeader*)meta;
@@ -315,14 +357,16 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
   const long tile = blockIdx.x;
   const FParam P = params[owners[tile]];
   const long local = tile - P.first_tile;
-  const long m0 = (local / P.col_tiles) * FBM, n = (local % P.col_tiles) * FBN + threadIdx.x;
-  const bool colok = n < P.cols;
-  float g[FBM];
+  const long m0 = (local / P.col_tiles) * FBM, n = (local % P.col_tiles) * FBN + 4 * threadIdx.x;
+  const int cnt = n < P.cols ? (P.cols - n < 4 ? (int)(P.cols - n) : 4) : 0;
+  const bool wvec = (P.cols & 3) == 0 && al16(P.w) && (!P.dense || al16(P.dense));
+  float4 g[FBM];
 #pragma unroll
-  for (int i = 0; i < FBM; i++) g[i] = 0.f;
+  for (int i = 0; i < FBM; i++) g[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   // head = sum over the terms' ranks of (left * scale) right
   for (int ti = 0; ti < P.term_count; ti++) {
     const FTerm tm = terms[P.term_begin + ti];
+    const bool tvec = (tm.ld & 3) == 0 && al16(tm.right) && al16(tm.tail);
     for (long r0 = 0; r0 < tm.rank; r0 += FRMAX) {
       const long rn = tm.rank - r0 < FRMAX ? tm.rank - r0 : FRMAX;
       __syncthreads();
@@ -331,35 +375,55 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
         sl[i][r] = m < P.rows ? tm.left[m * tm.rank + r0 + r] * tm.scale : 0.f;
       }
       __syncthreads();
-      for (long r = 0; r < rn; r++) {
-        const float rv = colok ? tm.right[(r0 + r) * tm.ld + n] : 0.f;
+      if (cnt > 0) {
+        for (long r = 0; r < rn; r++) {
+          const float4 rv = ld4(tm.right + (r0 + r) * tm.ld + n, cnt, tvec);
 #pragma unroll
-        for (int i = 0; i < FBM; i++) g[i] += sl[i][r] * rv;
+          for (int i = 0; i < FBM; i++) {
+            const float a = sl[i][r];
+            g[i].x += a * rv.x; g[i].y += a * rv.y; g[i].z += a * rv.z; g[i].w += a * rv.w;
+          }
+        }
       }
     }
   }
   // value = dense + head, then the tails
-#pragma unroll
-  for (int i = 0; i < FBM; i++) {
-    const long m = m0 + i;
-    if (P.dense && m < P.rows && colok) g[i] = P.dense[m * P.cols + n] + g[i];
-  }
-  for (int ti = 0; ti < P.term_count; ti++) {
-    const FTerm tm = terms[P.term_begin + ti];
+  if (cnt > 0) {
 #pragma unroll
     for (int i = 0; i < FBM; i++) {
       const long m = m0 + i;
-      if (m < P.rows && colok) {
-        const int sel = tm.row_map[m];
-        if (sel >= 0) g[i] += tm.tail[(long)sel * tm.ld + n] * tm.scale;
+      if (P.dense && m < P.rows) {
+        const float4 dv = ld4(P.dense + m * P.cols + n, cnt, wvec);
+        g[i] = make_float4(dv.x + g[i].x, dv.y + g[i].y, dv.z + g[i].z, dv.w + g[i].w);
+      }
+    }
+    for (int ti = 0; ti < P.term_count; ti++) {
+      const FTerm tm = terms[P.term_begin + ti];
+      const bool tvec = (tm.ld & 3) == 0 && al16(tm.right) && al16(tm.tail);
+#pragma unroll
+      for (int i = 0; i < FBM; i++) {
+        const long m = m0 + i;
+        if (m < P.rows) {
+          const int sel = tm.row_map[m];
+          if (sel >= 0) {
+            const float4 tv = ld4(tm.tail + (long)sel * tm.ld + n, cnt, tvec);
+            g[i].x += tv.x * tm.scale; g[i].y += tv.y * tm.scale;
+            g[i].z += tv.z * tm.scale; g[i].w += tv.w * tm.scale;
+          }
+        }
       }
     }
   }
   if (action == 2) {
     double s = 0.0;
+    if (cnt > 0) {
 #pragma unroll
-    for (int i = 0; i < FBM; i++)
-      if (m0 + i < P.rows && colok) s += (double)g[i] * (double)g[i];
+      for (int i = 0; i < FBM; i++) {
+        if (m0 + i >= P.rows) continue;
+        const float v[4] = {g[i].x, g[i].y, g[i].z, g[i].w};
+        for (int c = 0; c < cnt; c++) s += (double)v[c] * (double)v[c];
+      }
+    }
     __shared__ double red[4];
     __syncthreads();
     s = wave_sum(s);
@@ -368,13 +432,24 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
     if (threadIdx.x == 0) partials[tile] = ((red[0] + red[1]) + red[2]) + red[3];
     return;
   }
+  if (cnt == 0) return;
   const float keep = (P.decay && action == 1) ? 1.f - decay : 1.f;
 #pragma unroll
   for (int i = 0; i < FBM; i++) {
     const long m = m0 + i;
-    if (m < P.rows && colok) {
-      float* wp = P.w + m * P.cols + n;
-      *wp = action == 1 ? *wp * keep - lr * g[i] : g[i];
+    if (m >= P.rows) continue;
+    float* wp = P.w + m * P.cols + n;
+    float4 o = g[i];
+    if (action == 1) {
+      const float4 w4 = ld4(wp, cnt, wvec);
+      o = make_float4(w4.x * keep - lr * g[i].x, w4.y * keep - lr * g[i].y, w4.z * keep - lr * g[i].z,
+                      w4.w * keep - lr * g[i].w);
+    }
+    if (wvec && cnt == 4) {
+      *(float4*)wp = o;
+    } else {
+      const float v[4] = {o.x, o.y, o.z, o.w};
+      for (int c = 0; c < cnt; c++) wp[c] = v[c];
     }
   }
 }
@@ -466,7 +541,7 @@ extern "C" int sj_pvjp_indices(void* stream, uint64_t seed, long a, long donor_w
 
 extern "C" size_t sj_pvjp_basis_workspace_bytes(long n, long rank) {
   (void)n;
-  return sizeof(double) * (size_t)GBLK * (size_t)(rank * (rank + 1) / 2) +
+  return sizeof(double) * (size_t)(GBLK + 4) * (size_t)(rank * (rank + 1) / 2) +
          (sizeof(double) + sizeof(float)) * (size_t)(rank * rank);
 }
 
@@ -480,14 +555,15 @@ extern "C" int sj_pvjp_basis(void* stream, const void* y, int dtype, long ldy, l
                      workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
   double* partial = (double*)workspace;
-  double* t64 = partial + (size_t)GBLK * (size_t)(rank * (rank + 1) / 2);
+  double* part4 = partial + (size_t)GBLK * (size_t)(rank * (rank + 1) / 2);
+  double* t64 = part4 + 4 * (size_t)(rank * (rank + 1) / 2);
   float* tmat = (float*)(t64 + rank * rank);
   const int R = (int)rank;
   const unsigned rows_blocks = (unsigned)((n + 255) / 256);
   for (int pass = 0; pass < 2; pass++) {
     hipLaunchKernelGGL(k_gram_partial, dim3(GBLK), dim3(256), 0, s, y, dtype, ldy, columns, pass ? q : nullptr, n, R,
                        partial);
-    hipLaunchKernelGGL(k_chol_inv, dim3(1), dim3(64), 0, s, (const double*)partial, GBLK, R, eps, t64, tmat);
+    hipLaunchKernelGGL(k_chol_inv, dim3(1), dim3(256), 0, s, (const double*)partial, GBLK, R, eps, part4, t64, tmat);
     hipLaunchKernelGGL(k_basis_apply, dim3(rows_blocks), dim3(256), 0, s, y, dtype, ldy, columns, q, n, R,
                        (const float*)tmat, pass);
   }
@@ -517,9 +593,9 @@ extern "C" int sj_pvjp_prepare(void* stream, const uint16_t* x_t, long ldxt, lon
                               workspace, workspace_bytes))
     return st;
   if (k > 0) {
-    hipLaunchKernelGGL(k_pvjp_residual, dim3((unsigned)((n8 + 255) / 256), (unsigned)k), dim3(256), 0, s,
-                       (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, inverse, e, (bf16_t*)e_hi,
-                       (bf16_t*)e_lo, lde, n8);
+    hipLaunchKernelGGL(k_pvjp_residual, dim3((unsigned)((n8 + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
+                       dim3(256), 0, s, (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, k, inverse, e,
+                       (bf16_t*)e_hi, (bf16_t*)e_lo, lde, n8);
     SJ_LAUNCH_CHECK("parameter_residual");
   }
   return SJ_OK;
