@@ -608,8 +608,8 @@ void pick(long M, long N, int& bm, int& bn) {
 int splits_for(long M, long N, long K, int bm, int bn);
 
 // Tile and split-K plan of sj_gemm_planes (measured on the cfg2 shapes):
-// very long K (>= 8192) with a small output takes 64x64 tiles and up to 32
-// K slices of >= 512; dW-shaped products (K >= 2048) take 4 K slices and the
+// very long K (>= 8192, M <= 1024) takes 64x128 tiles (64x64 for N < 128)
+// and 4..16 K slices; dW-shaped products (K >= 2048) take 4 K slices and the
 // largest tile that still gives >= 144 workgroups; split-A products (dX)
 // with K <= 1024 and N a multiple of 128 take 64x128 tiles when those
 // cover half the CUs; the rest use pick().
@@ -618,14 +618,16 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
   const char* et = getenv("SJ_GEMM_TILE");
   const char* es = getenv("SJ_GEMM_SPLITS");
   if (!et && !es) {
-    if (tiles(M, N, 64, 64) < cu && K >= 8192) {
-      // very long K (token-contracted products of the parameter VJP): enough
-      // slices of >= 512 for about one workgroup per CU
-      bm = bn = 64;
-      const long t = tiles(M, N, 64, 64);
-      long sp = (cu + t - 1) / t;
+    if (K >= 8192 && M <= 1024) {
+      // very long K with a short output (token-contracted products of the
+      // parameter VJP): 64-row tiles and K slices of >= 512 for about four
+      // workgroups per CU (measured at 144 x 1536..5504 x 16384)
+      bm = 64;
+      bn = N >= 128 ? 128 : 64;
+      const long t = tiles(M, N, bm, bn);
+      long sp = (4 * cu + t - 1) / t;
       sp = sp < 4 ? 4 : sp;
-      sp = sp > 32 ? 32 : sp;
+      sp = sp > 16 ? 16 : sp;
       sp = sp > K / 512 ? K / 512 : sp;
       splits = (int)sp;
       return;
