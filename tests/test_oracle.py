@@ -512,3 +512,20 @@ def test_pvjp_update_closed_form():
     LR = float(np.float32(np.float32(lr) * np.float32(clip))); DEC = float(np.float32(np.float32(lr) * np.float32(wd)))
     np.testing.assert_allclose(pvjp.factored_update(W, G, lr, clip, wd, True), W * (1 - DEC) - LR * G, rtol=0, atol=0)
     np.testing.assert_allclose(pvjp.factored_update(W, G, lr, clip, wd, False), W - LR * G, rtol=0, atol=0)
+
+
+# --------------------------------------------------------- golden fixtures
+@pytest.mark.parametrize("name", ["cfg1_step", "attention_values", "router", "pvjp_selection", "moe_ffn_tiny"])
+def test_golden_fixture_reproduces(name):
+    """Every committed fixture is what the pinned oracle computes now."""
+    import os
+    from tests.golden import make_golden as G
+    ref = np.load(os.path.join(os.path.dirname(G.__file__), name + ".npz"), allow_pickle=False)
+    got = G.CASES[name]()
+    assert sorted(ref.files) == sorted(got)
+    for key in ref.files:
+        a, b = np.asarray(got[key]), ref[key]
+        if a.dtype.kind in "iu":
+            np.testing.assert_array_equal(a, b, err_msg=key)
+        else:
+            np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-14, err_msg=key)
