@@ -352,9 +352,11 @@ def workload_pvjp(args):
     R, blocks, S = 16, 32, 4
     k = S * 32
     seed = 0x1234
-    donor = B(n * 2 * F * 2).upload(_bf16(rng.normal(0, 1, (n, 2 * F))))
+    # donor: the up projection's output u [n][F] (widest member of the gate/up
+    # group, the last one on ties)
+    donor = B(n * F * 2).upload(_bf16(rng.normal(0, 1, (n, F))))
     xt = B(d * n * 2).upload(_bf16(rng.normal(0, 1, (d, n))))
-    scr, cols, rows_, fmap = B((2 * F + blocks) * 4), B(R * 4), B(k * 4), B(d * 4)
+    scr, cols, rows_, fmap = B((F + blocks) * 4), B(R * 4), B(k * 4), B(d * 4)
     q = B(n * R * 4)
     wsb = B(lib.sj_pvjp_basis_workspace_bytes(n, R))
     eps = lib.sj_pvjp_basis_tolerance(n, R)
@@ -408,8 +410,8 @@ def workload_pvjp(args):
 
     def step(T):
         run = (lambda nm, f: T.op(nm, f)) if T else (lambda nm, f: f())
-        run("pvjp_indices", lambda: api.sj_pvjp_indices(None, seed, d, 2 * F, blocks, S, R, 32, scr.p(), cols.p(), rows_.p(), fmap.p()))
-        run("pvjp_basis", lambda: api.sj_pvjp_basis(None, donor.p(), 4, 2 * F, n, cols.p(), R, cf(eps), q.p(), wsb.p(), wsb.nbytes))
+        run("pvjp_indices", lambda: api.sj_pvjp_indices(None, seed, d, F, blocks, S, R, 32, scr.p(), cols.p(), rows_.p(), fmap.p()))
+        run("pvjp_basis", lambda: api.sj_pvjp_basis(None, donor.p(), 4, F, n, cols.p(), R, cf(eps), q.p(), wsb.p(), wsb.nbytes))
         for g in groups:
             run("pvjp_prepare", lambda: api.sj_pvjp_prepare(None, xt.p(), n, d, n, q.p(), R, rows_.p(), k, cf(blocks / S), g["left"].p(), g["e"].p(), g["eh"].p(), g["el"].p(), n, wsp.p(), wsp.nbytes))
         for gi, co, c in coeffs:

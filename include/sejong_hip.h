@@ -400,8 +400,8 @@ int sj_pvjp_basis(void *stream, const void *y, int dtype, long ldy, long n, cons
 /* kernels parameter_prepare / parameter_residual (parameter.py:131-190)
  * with X given transposed (x_t [a][ldxt] bf16, columns n .. n rounded up
  * to 8 zero): left = X^T Q fp32 [a][rank];
- * e = [Q^T ; (X[:, row] - Q left[row]^T) * inverse] fp32 [rank+k][lde] and
- * as hi/lo planes (zero rows for row = -1).  Workspace:
+ * e (nullable) = [Q^T ; (X[:, row] - Q left[row]^T) * inverse] fp32
+ * [rank+k][lde], and as hi/lo planes (zero rows for row = -1).  Workspace:
  * sj_pvjp_prepare_workspace_bytes. */
 size_t sj_pvjp_prepare_workspace_bytes(long a, long n, long rank);
 int sj_pvjp_prepare(void *stream, const uint16_t *x_t, long ldxt, long a, long n, const float *q, long rank,
@@ -419,13 +419,18 @@ int sj_pvjp_vjp(void *stream, const uint16_t *e_hi, const uint16_t *e_lo, long l
  * per parameter W [rows][cols] fp32, G = dense (nullable) + sum over its
  * terms of scale * (left right + tail rows placed by row_map).  Terms of a
  * parameter are terms[term_begin .. term_begin+term_count).  decay != 0
- * marks ndim > 1 (weight decay applies). */
+ * marks ndim > 1 (weight decay applies).  ld: row stride of w, dense and
+ * mirror (0 = cols; a parameter may be a column block of a wider arena
+ * matrix).  mirror (nullable): receives bf16(W) after an update (the next
+ * step's Model::bind cast, model lib.rs:214-219, fused). */
 typedef struct {
   float *w;
   const float *dense;
   long rows, cols;
   int decay;
   long term_begin, term_count;
+  long ld;
+  uint16_t *mirror;
 } sj_factored_param;
 typedef struct {
   const float *left;     /* [rows][rank] */
@@ -530,6 +535,36 @@ typedef struct {
 
 int sj_model_create(const sj_model_config *cfg, const sj_adam_config *adam, void *stream,
                     sj_model **out);
+/* SGD step driver (control_variate.rs:503-877 with accumulation 1 and no
+ * control-variate blocks): forward, backward, FP64 norm of the compact
+ * gradients and clip, GradientPlan::update W = W (1 - lr wd [ndim>1]) -
+ * lr clip G.  vjp_rank > 0 turns on the parameter VJP
+ * (ParameterVjpConfig, core lib.rs:447-466): Matmul nodes that share an
+ * input with at least as many rows as columns form groups (graph.rs:
+ * 551-566); a group's members that pass selects_compression get factored
+ * gradients from one forward basis per (tokens, rank) and one feature
+ * selection per width (graph.rs:915-1005), drawn with one next_u64 of the
+ * parameter RNG (Rng::new(vjp_seed), carried across steps).  bf16 models
+ * with 64-wide heads only.  loss_scale must be 1. */
+typedef struct {
+  float weight_decay, clip_norm, loss_scale;
+  int clip_enabled;
+  long vjp_rank;                /* 0: dense SGD */
+  double vjp_residual_fraction;
+  long vjp_block_rows;
+  uint64_t vjp_seed;
+} sj_sgd_config;
+int sj_model_create_sgd(const sj_model_config *cfg, const sj_sgd_config *sgd, void *stream, sj_model **out);
+/* GradientPlan::materialize for every parameter of an SGD model: the
+ * gradient arena receives dense + factored G of the last backward (so
+ * sj_model_get_grads returns it).  No-op for AdamW models. */
+int sj_model_materialize_grads(sj_model *m);
+/* VjpStatistics of one step (compressed / dense matrices, basis and
+ * projection groups; control_variate.rs:577-578) and the parameter RNG
+ * state (saved as sgd.parameter_rng, control_variate.rs:216-217). */
+int sj_model_vjp_info(const sj_model *m, long *compressed, long *dense, long *basis_groups,
+                      long *projection_groups, uint64_t *rng_state);
+int sj_model_set_vjp_rng(sj_model *m, uint64_t rng_state);
 int sj_model_destroy(sj_model *m);
 /* Number of parameter tensors / total elements in the reference layout. */
 long sj_model_param_tensors(const sj_model *m);
@@ -549,7 +584,8 @@ int sj_model_set_batch(sj_model *m, const int32_t *ids, const int32_t *targets, 
 /* Forward + backward only (gradients left in the model's gradient arena). */
 int sj_model_forward_backward(sj_model *m);
 /* One full training step: forward, backward, FP64 grad norm, clip, AdamW
- * with learning rate lr (Adam::update increments the step first). */
+ * with learning rate lr (Adam::update increments the step first), or the
+ * SGD update of an SGD model. */
 int sj_model_train_step(sj_model *m, float lr);
 /* Capture the step as a hipGraph on the next sj_model_train_step and replay
  * it afterwards (on != 0), or run eagerly (on == 0). */
@@ -575,7 +611,10 @@ int sj_model_profile_entry(sj_model *m, long i, const char **name, double *total
 long sj_model_activation_count(const sj_model *m);
 int sj_model_export_activations(sj_model *m, float *host);
 /* Device pointers of internal buffers for callers that time or inspect
- * kernels directly (what: "logits", "loss_rows", "ids", "targets"). */
+ * kernels directly (what: "logits", "loss_rows", "ids", "targets",
+ * "params", "grads", "mirror", "mirror_t", "workspace", "stream", and for
+ * parameter-VJP models "vjp_columns", "vjp_rows", "vjp_map" (int32) and
+ * "vjp_basis" (fp32 [tokens][rank])). */
 int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);
 
 #ifdef __cplusplus

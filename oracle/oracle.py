@@ -70,6 +70,8 @@ def _declare(L):
     L.or_model_forward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _D]
     L.or_model_backward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _D, _I, _I, _D, _D]
     L.or_model_backward.restype = ctypes.c_double
+    L.or_model_backward_dys.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _D, _I, _I, _D, _D, _D]
+    L.or_model_backward_dys.restype = ctypes.c_double
     L.or_model_fwd_bwd.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I, _D, _D, _D]
     L.or_model_fwd_bwd.restype = ctypes.c_double
     L.or_model_loss.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I]
@@ -285,14 +287,30 @@ def model_forward(cfg, params, ids, dtype="f32"):
     return acts
 
 
-def model_backward(cfg, params, acts, ids, targets, dtype="f32"):
+def model_backward(cfg, params, acts, ids, targets, dtype="f32", want_dys=False):
     """Loss, reference-layout gradients and per-row losses from an
-    activation pack (e.g. the device's stored activations)."""
+    activation pack (e.g. the device's stored activations).  want_dys adds
+    a list with, per layer, the output gradients of the projection Matmul
+    nodes {"q", "k", "v" (pre-RoPE), "gate", "up"}."""
     params, pp = _d(params); acts, pa = _d(acts); ids, pi = _i(ids); targets, pt = _i(targets)
     grads, pg = _out(params.size); rows, pr = _out(cfg["T"] * cfg["B"])
-    loss = lib().or_model_backward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0),
-                                   DTYPE_CODE[dtype], pp, pa, pi, pt, pg, pr)
-    return loss, grads, rows
+    d, L, hq, hk, F, T, B = _dims(cfg)
+    M, J = T * B, d // hq * hk
+    if not want_dys:
+        loss = lib().or_model_backward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0),
+                                       DTYPE_CODE[dtype], pp, pa, pi, pt, pg, pr)
+        return loss, grads, rows
+    dys, py = _out(L * M * (d + 2 * J + 2 * F))
+    loss = lib().or_model_backward_dys(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0),
+                                       DTYPE_CODE[dtype], pp, pa, pi, pt, pg, pr, py)
+    per, off = [], 0
+    for _ in range(L):
+        layer = {}
+        for name, width in (("q", d), ("k", J), ("v", J), ("gate", F), ("up", F)):
+            layer[name] = dys[off:off + M * width].reshape(M, width)
+            off += M * width
+        per.append(layer)
+    return loss, grads, rows, per
 
 
 def acts_layout(cfg):

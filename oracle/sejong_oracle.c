@@ -625,9 +625,27 @@ void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, l
  * norm, then per layer down / SwiGLU / gate+up / ffn norm / attention
  * output / attention (+ inverse RoPE) / QKV / attention norm, embedding.
  * grads: reference layout (FP64).  Returns the mean loss of the logits. */
+/* or_model_backward with the output gradients of the projection Matmul
+ * nodes kept: dys (nullable) receives per layer, in this order, dY of the
+ * query (pre-RoPE), key (pre-RoPE), value, gate and up projections
+ * ([M][d], [M][J], [M][J], [M][F], [M][F]) -- the dY a parameter VJP
+ * contracts with (graph.rs:829-851, parameter_vjp.rs:308-320). */
+double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                             double theta, int dtype, const double *params, const double *acts_in,
+                             const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows,
+                             double *dys);
+
 double or_model_backward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
                          double theta, int dtype, const double *params, const double *acts_in,
                          const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows) {
+    return or_model_backward_dys(d, layers, hq, hk, ffn, T, B, eps, theta, dtype, params, acts_in, ids, targets,
+                                 grads, loss_rows, NULL);
+}
+
+double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                             double theta, int dtype, const double *params, const double *acts_in,
+                             const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows,
+                             double *dys) {
     or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
     const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
     plan_t pl;
@@ -660,6 +678,11 @@ double or_model_backward(long d, long layers, long hq, long hk, long ffn, long T
         or_matmul(dres, y->wd, dbig, M, F, d, 0, 1);              /* dh */
         or_matmul(a->h, dres, grads + y->o_wd, F, d, M, 1, 0);    /* dW_down */
         or_swiglu_bwd(a->g, a->u, dbig, dg, du, M * F);
+        double *dyl = dys ? dys + l * M * (d + 2 * J + 2 * F) : NULL;
+        if (dyl) {
+            memcpy(dyl + M * (d + 2 * J), dg, sizeof(double) * (size_t)(M * F));
+            memcpy(dyl + M * (d + 2 * J + F), du, sizeof(double) * (size_t)(M * F));
+        }
         or_matmul(dg, y->wg, dz, M, d, F, 0, 1);
         or_matmul(du, y->wu, dtmp, M, d, F, 0, 1);
         for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];
@@ -672,6 +695,11 @@ double or_model_backward(long d, long layers, long hq, long hk, long ffn, long T
         or_attention_bwd(a->qr, a->kr, a->v, a->o, a->lse, dO, dqr, dkr, dv, NULL, B, T, hq, hk, Dh, 0);
         or_rope(dqr, dq, M, T, hq, Dh, 0, theta, 1);
         or_rope(dkr, dk, M, T, hk, Dh, 0, theta, 1);
+        if (dyl) {
+            memcpy(dyl, dq, sizeof(double) * (size_t)(M * d));
+            memcpy(dyl + M * d, dk, sizeof(double) * (size_t)(M * J));
+            memcpy(dyl + M * (d + J), dv, sizeof(double) * (size_t)(M * J));
+        }
         or_matmul(dq, y->wq, dz, M, d, d, 0, 1);
         or_matmul(dk, y->wk, dtmp, M, d, J, 0, 1);
         for (long i = 0; i < M * d; i++) dz[i] += dtmp[i];

@@ -25,7 +25,7 @@ _U64 = ctypes.c_uint64
 class FactoredParam(ctypes.Structure):
     """sj_factored_param of include/sejong_hip.h."""
     _fields_ = [("w", _P), ("dense", _P), ("rows", _L), ("cols", _L), ("decay", _I), ("term_begin", _L),
-                ("term_count", _L)]
+                ("term_count", _L), ("ld", _L), ("mirror", _P)]
 
 
 class FactoredTerm(ctypes.Structure):
@@ -49,6 +49,11 @@ class ModelConfig(ctypes.Structure):
 class AdamConfig(ctypes.Structure):
     _fields_ = [("beta1", _F), ("beta2", _F), ("epsilon", _F), ("weight_decay", _F),
                 ("clip_norm", _F), ("loss_scale", _F), ("clip_enabled", _I)]
+
+
+class SgdConfig(ctypes.Structure):
+    _fields_ = [("weight_decay", _F), ("clip_norm", _F), ("loss_scale", _F), ("clip_enabled", _I),
+                ("vjp_rank", _L), ("vjp_residual_fraction", _DB), ("vjp_block_rows", _L), ("vjp_seed", _U64)]
 
 
 class AdamStep(ctypes.Structure):
@@ -143,6 +148,11 @@ SIGNATURES = {
     "sj_adamw": (_I, [_P, _P, _P, _P, _P, _L, _F, _F, _F, _F, _F, _F, _F, _F]),
     "sj_adamw_multi": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
     "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
+    "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
+    "sj_model_materialize_grads": (_I, [_P]),
+    "sj_model_vjp_info": (_I, [_P, ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L),
+                               ctypes.POINTER(_U64)]),
+    "sj_model_set_vjp_rng": (_I, [_P, _U64]),
     "sj_model_destroy": (_I, [_P]),
     "sj_model_param_tensors": (_L, [_P]),
     "sj_model_param_count": (_L, [_P]),

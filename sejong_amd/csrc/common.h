@@ -91,7 +91,23 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
 }  // namespace sj
 
 // ------------------------------------------------------------- host side
+// Step record of the SGD step driver, staged on the device before each step
+// so a captured step reads this step's values.
+struct sj_sgd_step {
+  float lr, weight_decay, clip_norm;
+  int clip_enabled;
+  uint64_t seed;  // parameter-VJP index seed (one Rng::next_u64 of the parameter RNG)
+};
+
 namespace sjh {
+// parameter_indices with the seed read from device memory
+int pvjp_indices_dev(hipStream_t stream, const uint64_t* seed, long a, long donor_width, long feature_blocks,
+                     long selected, long rank, long block_rows, int32_t* scratch, int32_t* columns, int32_t* rows,
+                     int32_t* map);
+// GradientPlan::update with lr from a staged step record and the clipping
+// factor formed on the device from the FP64 squared norm (nullable: no clip)
+int factored_update_staged(hipStream_t stream, const void* meta, long tiles, const sj_sgd_step* step,
+                           const double* sumsq);
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);

@@ -29,6 +29,7 @@
 // operands of the dW GEMMs), and carries the fp32 gradients dY that feed
 // GEMMs as hi/lo bf16 planes in both orientations (dX and dW operands).
 #include <math.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -50,6 +51,10 @@ struct RefTensor {
   long ref_offset;  // offset in the reference-layout flat vector
   long int_offset;  // offset of element (0,0) in the internal arena
   long int_ld;      // internal row stride
+  // projection-group membership (parameter VJP): kind 0 = q|k|v, 1 = gate|up,
+  // -1 none; member index and first column in the group's concatenated width
+  int layer = -1, kind = -1, member = -1;
+  long col0 = 0;
 };
 
 struct Layer {
@@ -158,6 +163,7 @@ struct sj_model {
   sj_adam_step* step_host = nullptr;
   hipEvent_t step_done[RING] = {};
   long step = 0;
+  long staged = 0;  // SGD step records staged (ring position)
   bool own_stream = false;
   // per-op HIP-event profile (eager steps only)
   bool profiling = false;
@@ -166,6 +172,27 @@ struct sj_model {
   std::vector<std::string> agg_names;
   std::vector<double> agg_ms;
   std::vector<long> agg_calls;
+  // SGD step driver (optimizer 1) and its parameter VJP
+  int optimizer = 0;  // 0 AdamW, 1 SGD
+  sj_sgd_config sgd = {};
+  sj_sgd_step* sgd_dev = nullptr;
+  sj_sgd_step* sgd_host = nullptr;  // pinned ring, as step_host
+  uint64_t vjp_rng = 0;             // parameter RNG state (SplitMix64)
+  bool vjp = false;                 // some group is compressed
+  bool comp[2][3] = {};             // compressed members: [0] q, k, v; [1] gate, up
+  bool group_on[2] = {};            // the group has a compressed member
+  bool group_all[2] = {};           // every member is compressed (no dense dW GEMM)
+  long vjp_R = 0, vjp_blocks = 0, vjp_S = 0, vjp_k = 0;
+  float vjp_inverse = 1.f, vjp_eps = 0.f;
+  long st_compressed = 0, st_dense = 0, st_basis = 0, st_projection = 0;
+  int32_t *vjp_scratch = nullptr, *vjp_cols = nullptr, *vjp_rows = nullptr, *vjp_map = nullptr;
+  float* vjp_q = nullptr;
+  float* vjp_e = nullptr;
+  uint16_t *vjp_eh = nullptr, *vjp_el = nullptr;
+  std::vector<float*> vjp_left[2], vjp_coeff[2];  // per layer: A = X^T Q [d][R]; E dY [R+k][width]
+  uint8_t *fmeta = nullptr, *fmeta_mat = nullptr;  // GradientPlan tables: update, materialize
+  long ftiles = 0;
+  double* fpart = nullptr;
   // graph
   bool use_graph = false;
   hipGraphExec_t exec = nullptr;
@@ -242,8 +269,9 @@ void build_layout(sj_model* m) {
   m->n_params = off;
 
   long ro = 0;
-  auto add = [&](const std::string& name, long rows, long cols, long ioff, long ild) {
-    m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild});
+  auto add = [&](const std::string& name, long rows, long cols, long ioff, long ild, int layer = -1, int kind = -1,
+                 int member = -1, long col0 = 0) {
+    m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild, layer, kind, member, col0});
     ro += rows * cols;
   };
   add("embedding", V, d, m->emb, d);
@@ -252,12 +280,13 @@ void build_layout(sj_model* m) {
     const Layer& y = m->layers[l];
     add(p + "attention_norm", 1, d, y.an, d);
     add(p + "ffn_norm", 1, d, y.fn, d);
-    add(p + "query", d, d, y.qkv, m->NQKV);
-    add(p + "key", d, J, y.qkv + d, m->NQKV);
-    add(p + "value", d, J, y.qkv + d + J, m->NQKV);
+    const int li = (int)l;
+    add(p + "query", d, d, y.qkv, m->NQKV, li, 0, 0, 0);
+    add(p + "key", d, J, y.qkv + d, m->NQKV, li, 0, 1, d);
+    add(p + "value", d, J, y.qkv + d + J, m->NQKV, li, 0, 2, d + J);
     add(p + "attention_output", d, d, y.wo, d);
-    add(p + "gate", d, F, y.gu, 2 * F);
-    add(p + "up", d, F, y.gu + F, 2 * F);
+    add(p + "gate", d, F, y.gu, 2 * F, li, 1, 0, 0);
+    add(p + "up", d, F, y.gu + F, 2 * F, li, 1, 1, F);
     add(p + "down", F, d, y.down, d);
   }
   add("final_norm", 1, d, m->final_norm, d);
@@ -346,6 +375,36 @@ int forward(sj_model* m) {
   return SJ_OK;
 }
 
+// ------------------------------------------------------- parameter VJP
+// One projection group's factored gradient (compressed_parameter_vjp,
+// graph.rs:915-1005): prepare (A = X^T Q and the E rows) from the group's
+// stored input, then E dY over the concatenated member outputs (Engine::
+// parameter_vjp, parameter_vjp.rs:308-320).  The first group of the
+// backward (the last layer's gate/up group) draws the feature selection and
+// the forward basis from the up projection's output (its widest member,
+// the last one on ties: graph.rs:931-934); every later group reuses both
+// (one basis per (tokens, rank), one selection per width, graph.rs:
+// 957-982), so one seed is consumed per step.
+int vjp_group(sj_model* m, long l, int kind) {
+  hipStream_t s = m->stream;
+  const long M = m->M, d = m->d, F = m->F, R = m->vjp_R, k = m->vjp_k, ldt = m->ldt;
+  const long width = kind == 0 ? m->NQKV : 2 * F;
+  if (l == m->L - 1 && kind == 1) {
+    const uint64_t* seed = (const uint64_t*)((const char*)m->sgd_dev + offsetof(sj_sgd_step, seed));
+    OP("pvjp_indices", sjh::pvjp_indices_dev(s, seed, d, F, m->vjp_blocks, m->vjp_S, R, m->sgd.vjp_block_rows,
+                                             m->vjp_scratch, m->vjp_cols, m->vjp_rows, m->vjp_map));
+    OP("pvjp_basis", sj_pvjp_basis(s, m->uu[m->L - 1], SJ_BF16, F, M, m->vjp_cols, R, m->vjp_eps, m->vjp_q, m->ws,
+                                   m->ws_bytes));
+  }
+  const uint16_t* xt = kind == 0 ? m->zt[l] : m->z2t[l];
+  OP("pvjp_prepare", sj_pvjp_prepare(s, xt, ldt, d, M, m->vjp_q, R, m->vjp_rows, k, m->vjp_inverse,
+                                     m->vjp_left[kind][l], nullptr, m->vjp_eh, m->vjp_el, ldt, m->ws, m->ws_bytes));
+  uint16_t* const* dyp = kind == 0 ? m->qp : m->gp;
+  OP("pvjp_coefficients", sj_pvjp_vjp(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dyp[2], dyp[3], ldt, width,
+                                      m->vjp_coeff[kind][l], width, m->ws, m->ws_bytes));
+  return SJ_OK;
+}
+
 // --------------------------------------------------------------- backward
 int backward(sj_model* m) {
   hipStream_t s = m->stream;
@@ -376,8 +435,10 @@ int backward(sj_model* m) {
       OP("down_dw", sj_gemm_planes(s, F, d, M, m->ht[l], nullptr, ldt, rp[2], rp[3], ldt, G + y.down, SJ_F32, d, 0, ws, wsb));
       OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, gp[0], gp[1], 2 * F, W + y.gu, nullptr, 2 * F, m->dz, SJ_F32, d, 0, ws,
                                       wsb));
-      OP("gate_up_dw", sj_gemm_planes(s, d, 2 * F, M, m->z2t[l], nullptr, ldt, gp[2], gp[3], ldt, G + y.gu, SJ_F32, 2 * F, 0,
-                                      ws, wsb));
+      if (m->group_on[1]) TRY(vjp_group(m, l, 1));
+      if (!m->group_all[1])
+        OP("gate_up_dw", sj_gemm_planes(s, d, 2 * F, M, m->z2t[l], nullptr, ldt, gp[2], gp[3], ldt, G + y.gu, SJ_F32,
+                                        2 * F, 0, ws, wsb));
       OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1, G + y.fn,
                                          xp[0], xp[1], xp[2], xp[3], ldt, M, d, eps, ws, wsb));
       // x1 = x + attention_output(o)
@@ -390,8 +451,10 @@ int backward(sj_model* m) {
                                       m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0],
                                       qp[1], NQ, qp[2], qp[3], ldt, ws, wsb));
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
-      OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0, ws,
-                                  wsb));
+      if (m->group_on[0]) TRY(vjp_group(m, l, 0));
+      if (!m->group_all[0])
+        OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0,
+                                    ws, wsb));
       if (l > 0)
         OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[l], W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
                                            G + y.an, rp[0], rp[1], rp[2], rp[3], ldt, M, d, eps, ws, wsb));
@@ -434,6 +497,19 @@ int backward(sj_model* m) {
 }
 
 int update(sj_model* m) {
+  if (m->optimizer == 1) {
+    // compact SGD (control_variate.rs:720-775): FP64 norm of the compact
+    // gradients when clipping is on, then GradientPlan::update, whose kernel
+    // also writes the bf16 mirror
+    if (m->sgd.clip_enabled) {
+      OP("factored_norm", sj_factored_apply(m->stream, m->fmeta, m->ftiles, 2, 0.f, 0.f, m->fpart));
+      OP("norm_sum", sj_sum_f64(m->stream, m->fpart, m->ftiles, m->sumsq));
+    }
+    OP("sgd_update", sjh::factored_update_staged(m->stream, m->fmeta, m->ftiles, m->sgd_dev,
+                                                 m->sgd.clip_enabled ? m->sumsq : nullptr));
+    if (m->planes) OP("mirror_transpose", transpose_mirror(m));
+    return SJ_OK;
+  }
   OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
   OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
                      m->n_nodecay, m->step_dev, m->sumsq, m->status));
@@ -448,6 +524,163 @@ int whole_step(sj_model* m) {
   return SJ_OK;
 }
 
+// Rng::next_u64 (SplitMix64, crates/sejong-core/src/lib.rs:591-609) on the host
+uint64_t splitmix64(uint64_t& s) {
+  s += 0x9e3779b97f4a7c15ULL;
+  uint64_t z = s;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+  return z ^ (z >> 31);
+}
+
+// Compression decisions of the SGD driver, made once: every layer has the
+// same groups, shapes and token count, so compressed_parameter_vjp
+// (graph.rs:915-1005) decides the same way in every layer and step.  Groups
+// by shared input with n >= a rows (graph.rs:551-566): q|k|v on z and
+// gate|up on z2 (attention_output, down and the head are groups of one,
+// never compressed: uses = 1).
+int vjp_decide(sj_model* m) {
+  const sj_sgd_config& c = m->sgd;
+  const long n = m->M, a = m->d;
+  const long total = 7 * m->L + 1;  // Matmul nodes with a parameter operand per step
+  long ranks[2] = {0, 0}, blocks = 0, sel = 0;
+  if (c.vjp_rank > 0) {
+    SJ_REQUIRE(c.vjp_block_rows > 0 && c.vjp_residual_fraction > 0.0 && c.vjp_residual_fraction <= 1.0,
+               "parameter VJP requires positive rank/block_rows and residual_fraction in (0,1]");
+    SJ_REQUIRE(m->planes, "parameter VJP step driver: bf16 models with 64-wide heads (MFMA layout path)");
+    SJ_REQUIRE(c.loss_scale == 1.0f, "parameter VJP step driver: loss_scale must be 1");
+    if (n >= a) {
+      const long widths[2][3] = {{m->d, m->J, m->J}, {m->F, m->F, 0}};
+      const int members[2] = {3, 2};
+      for (int kind = 0; kind < 2; kind++) {
+        long donor = 0;  // widest member output (the last one on ties)
+        for (int i = 0; i < members[kind]; i++)
+          if (widths[kind][i] >= donor) donor = widths[kind][i];
+        bool act[3] = {true, true, true};
+        for (;;) {
+          int count = 0, kept = 0;
+          for (int i = 0; i < members[kind]; i++) count += act[i];
+          if (count == 0) break;
+          for (int i = 0; i < members[kind]; i++) {
+            if (!act[i]) continue;
+            act[i] = sj_pvjp_selects_compression(c.vjp_rank, c.vjp_residual_fraction, c.vjp_block_rows, n, a,
+                                                 widths[kind][i], donor, count) == 1;
+            kept += act[i];
+          }
+          if (kept == count) break;
+        }
+        bool all = true, any = false;
+        for (int i = 0; i < members[kind]; i++) {
+          m->comp[kind][i] = act[i];
+          all = all && act[i];
+          any = any || act[i];
+        }
+        m->group_on[kind] = any;
+        m->group_all[kind] = any && all;
+        if (any) TRY(sj_pvjp_budget(c.vjp_rank, c.vjp_residual_fraction, c.vjp_block_rows, n, a, donor, &ranks[kind],
+                                    &blocks, &sel));
+      }
+    }
+  }
+  m->vjp = m->group_on[0] || m->group_on[1];
+  long compressed = 0;
+  for (int kind = 0; kind < 2; kind++)
+    for (int i = 0; i < 3; i++) compressed += m->comp[kind][i];
+  m->st_compressed = compressed * m->L;
+  m->st_dense = total - m->st_compressed;
+  m->st_basis = m->vjp ? 1 : 0;
+  m->st_projection = m->L * ((long)m->group_on[0] + (long)m->group_on[1]);
+  if (!m->vjp) return SJ_OK;
+  if (!m->group_on[1])
+    return sjh::fail(SJ_ERR_UNSUPPORTED,
+                     "parameter VJP step driver: only q|k|v compresses, and its donor (the pre-RoPE query "
+                     "projection) is not retained");
+  if (m->group_on[0] && ranks[0] != ranks[1])
+    return sjh::fail(SJ_ERR_UNSUPPORTED, "parameter VJP step driver: groups of different rank (%ld, %ld)", ranks[0],
+                     ranks[1]);
+  SJ_REQUIRE(ranks[1] <= 64, "parameter VJP step driver: rank %ld above 64", ranks[1]);
+  m->vjp_R = ranks[1];
+  m->vjp_blocks = blocks;
+  m->vjp_S = sel;
+  m->vjp_k = sel * c.vjp_block_rows;
+  m->vjp_inverse = (float)blocks / (float)sel;  // INVERSE, parameter_vjp.rs:282
+  m->vjp_eps = sj_pvjp_basis_tolerance(n, m->vjp_R);
+  return SJ_OK;
+}
+
+// The GradientPlan tables of an SGD model (GradientPlan::new + pack,
+// parameter_vjp.rs:329-470), built once: every pointer is fixed.  One table
+// updates the masters (and the bf16 mirror); the other materialises G into
+// the gradient arena.
+int build_plan(sj_model* m) {
+  std::vector<sj_factored_param> P, PM;
+  std::vector<sj_factored_term> T;
+  const long R = m->vjp_R;
+  for (const RefTensor& t : m->tensors) {
+    const bool c = m->vjp && t.kind >= 0 && m->comp[t.kind][t.member];
+    sj_factored_param p = {};
+    p.w = m->w + t.int_offset;
+    p.dense = c ? nullptr : m->g + t.int_offset;
+    p.rows = t.rows;
+    p.cols = t.cols;
+    p.decay = t.rows > 1;  // 1-D tensors have rows = 1
+    p.ld = t.int_ld;
+    p.mirror = m->mirror ? m->mirror + t.int_offset : nullptr;
+    if (c) {
+      const long width = t.kind == 0 ? m->NQKV : 2 * m->F;
+      float* co = m->vjp_coeff[t.kind][t.layer];
+      sj_factored_term term = {};
+      term.left = m->vjp_left[t.kind][t.layer];
+      term.right = co + t.col0;
+      term.tail = co + R * width + t.col0;
+      term.row_map = m->vjp_map;
+      term.rank = R;
+      term.scale = 1.f;  // weight 1/accumulation = 1, loss_scale 1 (control_variate.rs:305-309, 619-628)
+      term.ld = width;
+      p.term_begin = (long)T.size();
+      p.term_count = 1;
+      T.push_back(term);
+    }
+    P.push_back(p);
+    sj_factored_param q = p;
+    q.w = m->g + t.int_offset;
+    q.mirror = nullptr;
+    PM.push_back(q);
+  }
+  const size_t bytes = sj_factored_meta_bytes(P.data(), (long)P.size(), (long)T.size());
+  std::vector<uint8_t> host(bytes), hostm(bytes);
+  long tiles = 0, tiles_m = 0;
+  TRY(sj_factored_pack(P.data(), (long)P.size(), T.data(), (long)T.size(), host.data(), bytes, &tiles));
+  TRY(sj_factored_pack(PM.data(), (long)PM.size(), T.data(), (long)T.size(), hostm.data(), bytes, &tiles_m));
+  TRY(dalloc(m, (void**)&m->fmeta, bytes));
+  TRY(dalloc(m, (void**)&m->fmeta_mat, bytes));
+  TRY(dalloc(m, (void**)&m->fpart, sizeof(double) * (size_t)tiles));
+  SJ_HIP(hipMemcpy(m->fmeta, host.data(), bytes, hipMemcpyHostToDevice));
+  SJ_HIP(hipMemcpy(m->fmeta_mat, hostm.data(), bytes, hipMemcpyHostToDevice));
+  m->ftiles = tiles;
+  return SJ_OK;
+}
+
+// Stage the SGD step record (learning rate, clip settings and, with the
+// parameter VJP, this step's seed: one next_u64 of the carried parameter
+// RNG, control_variate.rs:543,577) from the pinned ring.
+int stage_sgd(sj_model* m, float lr) {
+  const int slot = (int)(++m->staged % sj_model::RING);
+  SJ_HIP(hipEventSynchronize(m->step_done[slot]));
+  sj_sgd_step* h = m->sgd_host + slot;
+  h->lr = lr;
+  h->weight_decay = m->sgd.weight_decay;
+  h->clip_norm = m->sgd.clip_norm;
+  h->clip_enabled = m->sgd.clip_enabled;
+  h->seed = m->vjp ? splitmix64(m->vjp_rng) : 0;
+  SJ_HIP(hipMemcpyAsync(m->sgd_dev, h, sizeof(sj_sgd_step), hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipEventRecord(m->step_done[slot], m->stream));
+  return SJ_OK;
+}
+
+int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, void* stream,
+                 sj_model** out);
+
 }  // namespace
 
 // ================================================================ C ABI
@@ -455,6 +688,21 @@ int whole_step(sj_model* m) {
 extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config* adam, void* stream,
                                sj_model** out) {
   SJ_REQUIRE(cfg && adam && out, "model: null argument");
+  return create_model(cfg, adam, nullptr, stream, out);
+}
+
+extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_config* sgd, void* stream,
+                                   sj_model** out) {
+  SJ_REQUIRE(cfg && sgd && out, "model: null argument");
+  SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
+                 (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
+             "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
+  return create_model(cfg, nullptr, sgd, stream, out);
+}
+
+namespace {
+int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, void* stream,
+                 sj_model** out) {
   const sj_model_config& c = *cfg;
   SJ_REQUIRE(c.vocab > 0 && c.width > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.ffn_width > 0 &&
                  c.sequence > 0 && c.batch > 0,
@@ -465,7 +713,12 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   SJ_REQUIRE(c.precision == SJ_F32 || c.precision == SJ_BF16, "precision must be f32 or bf16");
   sj_model* m = new sj_model();
   m->c = c;
-  m->adam = *adam;
+  if (adam) m->adam = *adam;
+  if (sgd) {
+    m->optimizer = 1;
+    m->sgd = *sgd;
+    m->vjp_rng = sgd->vjp_seed;  // Rng::new(seed), control_variate.rs:73
+  }
   m->stream = (hipStream_t)stream;
   if (!m->stream) {
     // graph capture needs a stream other than the null stream
@@ -505,6 +758,10 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
     sj_model_destroy(m);
     return s;
   };
+  if (m->optimizer == 1) {
+    st = vjp_decide(m);
+    if (st) return fail_cleanup(st);
+  }
 #define ALLOC(ptr, bytes)                                    \
   do {                                                       \
     void* _p = nullptr;                                      \
@@ -515,8 +772,10 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   const size_t P = (size_t)m->n_params;
   ALLOC(m->w, P * 4);
   ALLOC(m->g, P * 4);
-  ALLOC(m->m, P * 4);
-  ALLOC(m->v, P * 4);
+  if (m->optimizer == 0) {
+    ALLOC(m->m, P * 4);
+    ALLOC(m->v, P * 4);
+  }
   if (m->dt == SJ_BF16) ALLOC(m->mirror, P * 2);
   if (m->planes) {
     ALLOC(m->mirror_t, P * 2);
@@ -593,6 +852,26 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   ALLOC(m->sumsq, 64);
   ALLOC(m->status, 64);
   ALLOC(m->step_dev, sizeof(sj_adam_step));
+  if (m->optimizer == 1) ALLOC(m->sgd_dev, sizeof(sj_sgd_step));
+  if (m->vjp) {
+    const size_t R = (size_t)m->vjp_R, k = (size_t)m->vjp_k, rows = R + k, MT = (size_t)m->ldt;
+    ALLOC(m->vjp_scratch, sizeof(int32_t) * (F + (size_t)m->vjp_blocks));
+    ALLOC(m->vjp_cols, sizeof(int32_t) * R);
+    ALLOC(m->vjp_rows, sizeof(int32_t) * (k > 0 ? k : 1));
+    ALLOC(m->vjp_map, sizeof(int32_t) * d);
+    ALLOC(m->vjp_q, sizeof(float) * M * R);
+    ALLOC(m->vjp_eh, 2 * rows * MT);
+    ALLOC(m->vjp_el, 2 * rows * MT);
+    for (int kind = 0; kind < 2; kind++) {
+      const size_t width = kind == 0 ? (size_t)m->NQKV : 2 * F;
+      m->vjp_left[kind].assign(m->L, nullptr);
+      m->vjp_coeff[kind].assign(m->L, nullptr);
+      for (long l = 0; l < m->L && m->group_on[kind]; l++) {
+        ALLOC(m->vjp_left[kind][l], sizeof(float) * d * R);
+        ALLOC(m->vjp_coeff[kind][l], sizeof(float) * rows * width);
+      }
+    }
+  }
   // workspace: max over the step's calls
   size_t ws = 0;
   auto upd = [&](size_t b) { ws = b > ws ? b : ws; };
@@ -618,10 +897,20 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
     upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->d));
     upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->NQKV));
   }
+  if (m->vjp) {
+    const long rows = m->vjp_R + m->vjp_k;
+    upd(sj_pvjp_basis_workspace_bytes(Mi, m->vjp_R));
+    upd(sj_pvjp_prepare_workspace_bytes(m->d, Mi, m->vjp_R));
+    upd(sj_pvjp_vjp_workspace_bytes(rows, m->NQKV, Mi));
+    upd(sj_pvjp_vjp_workspace_bytes(rows, 2 * m->F, Mi));
+  }
   m->ws_bytes = ws;
   ALLOC(m->ws, ws);
 #undef ALLOC
   if (hipHostMalloc((void**)&m->step_host, sizeof(sj_adam_step) * sj_model::RING, 0) != hipSuccess)
+    return fail_cleanup(sjh::fail(SJ_ERR_CAPACITY, "model: pinned step buffer"));
+  if (m->optimizer == 1 &&
+      hipHostMalloc((void**)&m->sgd_host, sizeof(sj_sgd_step) * sj_model::RING, 0) != hipSuccess)
     return fail_cleanup(sjh::fail(SJ_ERR_CAPACITY, "model: pinned step buffer"));
   for (int i = 0; i < sj_model::RING; i++)
     if (hipEventCreateWithFlags(&m->step_done[i], hipEventDisableTiming) != hipSuccess)
@@ -630,7 +919,7 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   hipStream_t s = m->stream;
   hipError_t e = hipSuccess;
   for (void* p : {(void*)m->w, (void*)m->g, (void*)m->m, (void*)m->v})
-    if (e == hipSuccess) e = hipMemsetAsync(p, 0, P * 4, s);
+    if (e == hipSuccess && p) e = hipMemsetAsync(p, 0, P * 4, s);
   if (e == hipSuccess && m->mirror) e = hipMemsetAsync(m->mirror, 0, P * 2, s);
   if (e == hipSuccess && m->mirror_t) e = hipMemsetAsync(m->mirror_t, 0, P * 2, s);
   // padding columns [M, ldt) of the transposed activations stay zero
@@ -651,14 +940,22 @@ extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config*
   }
   if (e == hipSuccess) e = hipMemsetAsync(m->status, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(m->sumsq, 0, 64, s);
   if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: clear arenas"));
   st = sj_rope_table(s, m->rope, m->T, m->Dh, c.rope_theta);
   if (st) return fail_cleanup(st);
+  if (m->optimizer == 1) {
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: init sync"));
+    st = build_plan(m);
+    if (st) return fail_cleanup(st);
+  }
   e = hipStreamSynchronize(s);
   if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: init sync"));
   *out = m;
   return SJ_OK;
 }
+}  // namespace
 
 extern "C" int sj_model_destroy(sj_model* m) {
   if (!m) return SJ_OK;
@@ -668,6 +965,7 @@ extern "C" int sj_model_destroy(sj_model* m) {
   for (void* p : m->allocations) hipFree(p);
   for (hipEvent_t e : m->prof_events) hipEventDestroy(e);
   if (m->step_host) hipHostFree(m->step_host);
+  if (m->sgd_host) hipHostFree(m->sgd_host);
   for (int i = 0; i < sj_model::RING; i++)
     if (m->step_done[i]) hipEventDestroy(m->step_done[i]);
   if (m->own_stream) hipStreamDestroy(m->stream);
@@ -720,14 +1018,14 @@ extern "C" int sj_model_get_grads(sj_model* m, float* host) {
   return copy_arena_out(m, m->g, host);
 }
 extern "C" int sj_model_get_adam_state(sj_model* m, float* mh, float* vh, long* step) {
-  SJ_REQUIRE(m, "get_adam_state: null");
+  SJ_REQUIRE(m && m->optimizer == 0, "get_adam_state: AdamW model required");
   if (mh) TRY(copy_arena_out(m, m->m, mh));
   if (vh) TRY(copy_arena_out(m, m->v, vh));
   if (step) *step = m->step;
   return SJ_OK;
 }
 extern "C" int sj_model_set_adam_state(sj_model* m, const float* mh, const float* vh, long step) {
-  SJ_REQUIRE(m && mh && vh && step >= 0, "set_adam_state: arguments");
+  SJ_REQUIRE(m && m->optimizer == 0 && mh && vh && step >= 0, "set_adam_state: arguments (AdamW model)");
   TRY(copy_arena_in(m, mh, m->m));
   TRY(copy_arena_in(m, vh, m->v));
   m->step = step;
@@ -753,6 +1051,7 @@ extern "C" int sj_model_set_batch(sj_model* m, const int32_t* ids, const int32_t
 
 extern "C" int sj_model_forward_backward(sj_model* m) {
   SJ_REQUIRE(m, "forward_backward: null");
+  if (m->optimizer == 1) TRY(stage_sgd(m, 0.f));  // the backward's parameter-VJP seed
   TRY(forward(m));
   TRY(backward(m));
   return SJ_OK;
@@ -764,8 +1063,15 @@ extern "C" int sj_model_use_graph(sj_model* m, int on) {
   return SJ_OK;
 }
 
+static int run_step(sj_model* m);
+
 extern "C" int sj_model_train_step(sj_model* m, float lr) {
   SJ_REQUIRE(m, "train_step: null");
+  if (m->optimizer == 1) {
+    TRY(stage_sgd(m, lr));
+    m->step += 1;
+    return run_step(m);
+  }
   // Adam::update increments the step and forms 1/(1-beta^step) on the host
   // in f32 (crates/sejong-gpu/src/lib.rs:950-951).
   m->step += 1;
@@ -784,6 +1090,11 @@ extern "C" int sj_model_train_step(sj_model* m, float lr) {
   h->clip_enabled = m->adam.clip_enabled;
   SJ_HIP(hipMemcpyAsync(m->step_dev, h, sizeof(sj_adam_step), hipMemcpyHostToDevice, m->stream));
   SJ_HIP(hipEventRecord(m->step_done[slot], m->stream));
+  return run_step(m);
+}
+
+// the step eagerly, or captured once as a hipGraph and replayed
+static int run_step(sj_model* m) {
   if (!m->use_graph || m->profiling) return whole_step(m);
   if (!m->exec) {
     SJ_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
@@ -850,7 +1161,7 @@ extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) 
   SJ_HIP(hipMemcpy(&ss, m->sumsq, sizeof(double), hipMemcpyDeviceToHost));
   SJ_HIP(hipMemcpy(&flag, m->status, sizeof(int32_t), hipMemcpyDeviceToHost));
   if (loss) *loss = l;
-  if (grad_norm) *grad_norm = sqrt(ss) / (double)m->adam.loss_scale;
+  if (grad_norm) *grad_norm = sqrt(ss) / (m->optimizer == 1 ? 1.0 : (double)m->adam.loss_scale);
   if (flag) return sjh::fail(SJ_ERR_NONFINITE, "nonfinite clipping gradient");
   return SJ_OK;
 }
@@ -909,6 +1220,31 @@ extern "C" int sj_model_export_activations(sj_model* m, float* host) {
   return SJ_OK;
 }
 
+extern "C" int sj_model_materialize_grads(sj_model* m) {
+  SJ_REQUIRE(m, "materialize_grads: null");
+  if (m->optimizer != 1) return SJ_OK;
+  TRY(sj_factored_apply(m->stream, m->fmeta_mat, m->ftiles, 0, 0.f, 0.f, nullptr));
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  return SJ_OK;
+}
+
+extern "C" int sj_model_vjp_info(const sj_model* m, long* compressed, long* dense, long* basis_groups,
+                                 long* projection_groups, uint64_t* rng_state) {
+  SJ_REQUIRE(m, "vjp_info: null");
+  if (compressed) *compressed = m->st_compressed;
+  if (dense) *dense = m->st_dense;
+  if (basis_groups) *basis_groups = m->st_basis;
+  if (projection_groups) *projection_groups = m->st_projection;
+  if (rng_state) *rng_state = m->vjp_rng;
+  return SJ_OK;
+}
+
+extern "C" int sj_model_set_vjp_rng(sj_model* m, uint64_t rng_state) {
+  SJ_REQUIRE(m && m->optimizer == 1, "set_vjp_rng: SGD model required");
+  m->vjp_rng = rng_state;
+  return SJ_OK;
+}
+
 extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* elements) {
   SJ_REQUIRE(m && what && ptr, "buffer: null");
   std::string w(what);
@@ -924,6 +1260,10 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   else if (w == "mirror_t") { *ptr = m->mirror_t; n = m->mirror_t ? m->n_params : 0; }
   else if (w == "workspace") { *ptr = m->ws; n = (long)m->ws_bytes; }
   else if (w == "stream") { *ptr = (void*)m->stream; n = 0; }
+  else if (w == "vjp_columns" && m->vjp) { *ptr = m->vjp_cols; n = m->vjp_R; }
+  else if (w == "vjp_rows" && m->vjp) { *ptr = m->vjp_rows; n = m->vjp_k; }
+  else if (w == "vjp_map" && m->vjp) { *ptr = m->vjp_map; n = m->d; }
+  else if (w == "vjp_basis" && m->vjp) { *ptr = m->vjp_q; n = m->M * m->vjp_R; }
   else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);
   if (elements) *elements = n;
   return SJ_OK;

@@ -51,14 +51,15 @@ __device__ __forceinline__ uint64_t splitmix_index(uint64_t& s, uint64_t n) {
 // picked block are written by all lanes.
 __global__ __launch_bounds__(256) void k_pvjp_indices(int32_t* __restrict__ scratch, int32_t* __restrict__ columns,
                                                       int32_t* __restrict__ rows, int32_t* __restrict__ map, long A,
-                                                      long B, long NB, long S, long R, long group, uint64_t seed) {
+                                                      long B, long NB, long S, long R, long group, uint64_t seed,
+                                                      const uint64_t* __restrict__ seed_ptr) {
   __shared__ int32_t picked;
   const int t = threadIdx.x;
   for (long i = t; i < B; i += 256) scratch[i] = (int32_t)i;
   for (long i = t; i < NB; i += 256) scratch[B + i] = (int32_t)i;
   for (long i = t; i < A; i += 256) map[i] = -1;
   __syncthreads();
-  uint64_t state = seed;
+  uint64_t state = seed_ptr ? *seed_ptr : seed;  // a captured step reads the seed its host staged
   if (t == 0) {
     for (long i = 0; i < R; i++) {
       const long j = i + (long)splitmix_index(state, (uint64_t)(B - i));
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(256) void k_pvjp_qt(const float* __restrict__ q, in
   if (i >= (long)R * n8) return;
   const long r = i / n8, tok = i - r * n8;
   const float v = tok < n ? q[tok * R + r] : 0.f;  // columns [n, n8) are the GEMM's zero padding
-  e[r * lde + tok] = v;
+  if (e) e[r * lde + tok] = v;
   bf16_t h, l;
   split_bf(v, h, l);
   eh[r * lde + tok] = h;
@@ -300,7 +301,7 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
       v = (bf2f(xt[row * ldxt + tok]) - acc) * inverse;
     }
     const long o = (R + i) * lde + tok;
-    e[o] = v;
+    if (e) e[o] = v;
     bf16_t h, l;
     split_bf(v, h, l);
     eh[o] = h;
@@ -313,7 +314,8 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
 struct FParam {
   float* w;
   const float* dense;
-  long rows, cols, first_tile, col_tiles;
+  uint16_t* mirror;  // nullable bf16 copy of the updated w
+  long rows, cols, ld, first_tile, col_tiles;
   int decay, term_begin, term_count, pad;
 };
 struct FTerm {
@@ -348,7 +350,9 @@ __device__ __forceinline__ bool al16(const void* p) { return ((uintptr_t)p & 15)
 // one workgroup per 16x1024 tile of one parameter (owner from the table).
 // Action 0 materialize (G into w), 1 update, 2 FP64 sum of G^2 per tile.
 __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restrict__ meta, int action, float lr,
-                                                        float decay, double* __restrict__ partials) {
+                                                        float decay, double* __restrict__ partials,
+                                                        const sj_sgd_step* __restrict__ step,
+                                                        const double* __restrict__ sumsq) {
   const FMetaHeader* hd = (const FMetaHeader*)meta;
   const FParam* params = (const FParam*)(meta + sizeof(FMetaHeader));
   const FTerm* terms = (const FTerm*)(params + hd->nparams);
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
   const long local = tile - P.first_tile;
   const long m0 = (local / P.col_tiles) * FBM, n = (local % P.col_tiles) * FBN + 4 * threadIdx.x;
   const int cnt = n < P.cols ? (P.cols - n < 4 ? (int)(P.cols - n) : 4) : 0;
-  const bool wvec = (P.cols & 3) == 0 && al16(P.w) && (!P.dense || al16(P.dense));
+  const bool wvec = (P.cols & 3) == 0 && (P.ld & 3) == 0 && al16(P.w) && (!P.dense || al16(P.dense));
   float4 g[FBM];
 #pragma unroll
   for (int i = 0; i < FBM; i++) g[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
     for (int i = 0; i < FBM; i++) {
       const long m = m0 + i;
       if (P.dense && m < P.rows) {
-        const float4 dv = ld4(P.dense + m * P.cols + n, cnt, wvec);
+        const float4 dv = ld4(P.dense + m * P.ld + n, cnt, wvec);
         g[i] = make_float4(dv.x + g[i].x, dv.y + g[i].y, dv.z + g[i].z, dv.w + g[i].w);
       }
     }
@@ -433,12 +437,26 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
     return;
   }
   if (cnt == 0) return;
+  if (step) {
+    // the step driver's update: learning rate from the staged step record,
+    // clipping from the FP64 norm of this step (train lib.rs / control_
+    // variate.rs: clipping = clip_norm / norm when enabled and norm >
+    // clip_norm, formed in f64 and rounded to f32; LR = lr * clipping and
+    // DECAY = lr * weight_decay in f32, parameter_vjp.rs:502-518)
+    float clip = 1.f;
+    if (step->clip_enabled && sumsq) {
+      const double nrm = sqrt(fmax(*sumsq, 0.0));
+      if (nrm > (double)step->clip_norm) clip = (float)((double)step->clip_norm / nrm);
+    }
+    lr = mul_rn(step->lr, clip);
+    decay = mul_rn(step->lr, step->weight_decay);
+  }
   const float keep = (P.decay && action == 1) ? 1.f - decay : 1.f;
 #pragma unroll
   for (int i = 0; i < FBM; i++) {
     const long m = m0 + i;
     if (m >= P.rows) continue;
-    float* wp = P.w + m * P.cols + n;
+    float* wp = P.w + m * P.ld + n;
     float4 o = g[i];
     if (action == 1) {
       const float4 w4 = ld4(wp, cnt, wvec);
@@ -450,6 +468,15 @@ __global__ __launch_bounds__(256) void k_factored_apply(const uint8_t* __restric
     } else {
       const float v[4] = {o.x, o.y, o.z, o.w};
       for (int c = 0; c < cnt; c++) wp[c] = v[c];
+    }
+    if (action == 1 && P.mirror) {
+      bf16_t* mp = (bf16_t*)P.mirror + m * P.ld + n;
+      if (wvec && cnt == 4) {
+        *(u32x2*)mp = u32x2{pack2(f2bf(o.x), f2bf(o.y)), pack2(f2bf(o.z), f2bf(o.w))};
+      } else {
+        const float v[4] = {o.x, o.y, o.z, o.w};
+        for (int c = 0; c < cnt; c++) mp[c] = f2bf(v[c]);
+      }
     }
   }
 }
@@ -534,7 +561,21 @@ extern "C" int sj_pvjp_indices(void* stream, uint64_t seed, long a, long donor_w
                  scratch && (rank == 0 || columns) && (selected == 0 || (rows && map)),
              "parameter_indices: dimensions");
   hipLaunchKernelGGL(k_pvjp_indices, dim3(1), dim3(256), 0, (hipStream_t)stream, scratch, columns, rows, map, a,
-                     donor_width, feature_blocks, selected, rank, block_rows, seed);
+                     donor_width, feature_blocks, selected, rank, block_rows, seed, (const uint64_t*)nullptr);
+  SJ_LAUNCH_CHECK("parameter_indices");
+  return SJ_OK;
+}
+
+int sjh::pvjp_indices_dev(hipStream_t stream, const uint64_t* seed, long a, long donor_width, long feature_blocks,
+                          long selected, long rank, long block_rows, int32_t* scratch, int32_t* columns,
+                          int32_t* rows, int32_t* map) {
+  SJ_REQUIRE(seed && a >= 0 && donor_width >= 0 && feature_blocks >= 0 && selected >= 0 && rank >= 0 &&
+                 block_rows > 0 && rank <= donor_width && selected <= feature_blocks &&
+                 donor_width + feature_blocks < (1L << 31) && scratch && (rank == 0 || columns) &&
+                 (selected == 0 || (rows && map)),
+             "parameter_indices: dimensions");
+  hipLaunchKernelGGL(k_pvjp_indices, dim3(1), dim3(256), 0, stream, scratch, columns, rows, map, a, donor_width,
+                     feature_blocks, selected, rank, block_rows, (uint64_t)0, seed);
   SJ_LAUNCH_CHECK("parameter_indices");
   return SJ_OK;
 }
@@ -647,7 +688,10 @@ extern "C" int sj_factored_pack(const sj_factored_param* params, long nparams, c
                    p.term_begin + p.term_count <= nterms,
                "compact SGD parameter %ld: shape or terms", i);
     FParam q = {};
-    q.w = p.w; q.dense = p.dense; q.rows = p.rows; q.cols = p.cols;
+    SJ_REQUIRE(p.ld == 0 || p.ld >= p.cols, "compact SGD parameter %ld: row stride %ld below %ld columns", i, p.ld,
+               p.cols);
+    q.w = p.w; q.dense = p.dense; q.mirror = p.mirror; q.rows = p.rows; q.cols = p.cols;
+    q.ld = p.ld > 0 ? p.ld : p.cols;
     q.first_tile = t; q.col_tiles = (p.cols + FBN - 1) / FBN;
     q.decay = p.decay; q.term_begin = (int)p.term_begin; q.term_count = (int)p.term_count;
     t += ((p.rows + FBM - 1) / FBM) * q.col_tiles;
@@ -686,9 +730,19 @@ extern "C" int sj_factored_apply(void* stream, const void* meta, long tiles, int
   SJ_REQUIRE(meta && tiles > 0 && tiles < (1L << 31) && action >= 0 && action <= 2 && (action != 2 || partials),
              "compact SGD apply: action %d", action);
   hipLaunchKernelGGL(k_factored_apply, dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream,
-                     (const uint8_t*)meta, action, lr, decay, partials);
+                     (const uint8_t*)meta, action, lr, decay, partials, (const sj_sgd_step*)nullptr,
+                     (const double*)nullptr);
   SJ_LAUNCH_CHECK(action == 1 ? "parameter_gradient_update"
                               : action == 0 ? "parameter_gradient_materialize" : "parameter_gradient_norm");
+  return SJ_OK;
+}
+
+int sjh::factored_update_staged(hipStream_t stream, const void* meta, long tiles, const sj_sgd_step* step,
+                                const double* sumsq) {
+  SJ_REQUIRE(meta && step && tiles > 0 && tiles < (1L << 31), "compact SGD update: arguments");
+  hipLaunchKernelGGL(k_factored_apply, dim3((unsigned)tiles), dim3(256), 0, stream, (const uint8_t*)meta, 1, 0.f,
+                     0.f, (double*)nullptr, step, sumsq);
+  SJ_LAUNCH_CHECK("parameter_gradient_update");
   return SJ_OK;
 }
 

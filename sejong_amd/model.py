@@ -59,8 +59,24 @@ class ModelConfig:
 
 
 @dataclass
+class ParameterVjpConfig:
+    """crates/sejong-core/src/lib.rs:447-466."""
+    rank: int = 16
+    residual_fraction: float = 0.25
+    block_rows: int = 32
+    seed: int = 124
+
+    def validate(self):
+        if not (0 < self.rank <= 2 ** 31 - 1 and 0 < self.block_rows <= 2 ** 31 - 1
+                and math.isfinite(self.residual_fraction) and 0.0 < self.residual_fraction <= 1.0):
+            raise ValueError("parameter VJP requires positive rank/block_rows and residual_fraction in (0,1]")
+
+
+@dataclass
 class TrainConfig:
-    """crates/sejong-core/src/lib.rs:308-362 defaults (AdamW subset)."""
+    """crates/sejong-core/src/lib.rs:308-362 defaults (AdamW and SGD subset)."""
+    optimizer: str = "adamw"  # "adamw" | "sgd"
+    parameter_vjp: ParameterVjpConfig | None = None
     sequence: int = 512
     batch: int = 1
     learning_rate: float = 3e-4
@@ -73,6 +89,14 @@ class TrainConfig:
     loss_scale: float = 1.0
     seed: int = 123
 
+    def validate(self):
+        if self.parameter_vjp is not None:
+            if self.optimizer != "sgd":
+                raise ValueError("parameter_vjp uses the compact SGD optimizer")
+            self.parameter_vjp.validate()
+        if self.optimizer not in ("adamw", "sgd"):
+            raise ValueError("optimizer must be adamw or sgd")
+
 
 # BASELINE configurations of this path
 def config(name: str) -> tuple[ModelConfig, TrainConfig]:
@@ -84,6 +108,15 @@ def config(name: str) -> tuple[ModelConfig, TrainConfig]:
         return (ModelConfig(width=384, layers=6, heads=6, kv_heads=2, ffn_width=1024, context=512,
                             precision="bf16"),
                 TrainConfig(sequence=512, batch=8, learning_rate=3e-4, weight_decay=0.01))
+    if name == "cfg5":  # scaled parameter-VJP path: rank 16, 10% residual rows, selected-row SGD lr 1e-2
+        # optimizer settings of configs/sejong-parameter-vjp.toml:35-59 (sgd,
+        # no clipping, no weight decay, accumulation 1, block_rows 32, seed 124)
+        return (ModelConfig(width=1024, layers=12, heads=16, kv_heads=4, ffn_width=2752, context=1024,
+                            precision="bf16"),
+                TrainConfig(optimizer="sgd", sequence=1024, batch=16, learning_rate=1e-2, weight_decay=0.0,
+                            clip_enabled=False,
+                            parameter_vjp=ParameterVjpConfig(rank=16, residual_fraction=0.1, block_rows=32,
+                                                             seed=124)))
     raise KeyError(name)
 
 
@@ -142,10 +175,12 @@ def _np_ptr(a: np.ndarray):
 
 
 class Model:
-    """One byte Transformer resident on the GPU with its AdamW state."""
+    """One byte Transformer resident on the GPU with its optimizer state
+    (AdamW, or SGD with the optional parameter VJP)."""
 
     def __init__(self, mc: ModelConfig, tc: TrainConfig, stream: int | None = None):
         mc.validate()
+        tc.validate()
         if tc.sequence > mc.context:
             raise ValueError("training requires sequence within context")
         self.mc, self.tc = mc, tc
@@ -153,11 +188,20 @@ class Model:
                             ffn_width=mc.ffn_width, sequence=tc.sequence, batch=tc.batch,
                             norm_epsilon=mc.norm_epsilon, rope_theta=mc.rope_theta,
                             precision=N.SJ_BF16 if mc.precision == "bf16" else N.SJ_F32)
-        adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
-                            clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
         handle = ctypes.c_void_p()
-        N.api.sj_model_create(ctypes.byref(cfg), ctypes.byref(adam), ctypes.c_void_p(stream or 0),
-                              ctypes.byref(handle))
+        if tc.optimizer == "sgd":
+            pv = tc.parameter_vjp
+            sgd = N.SgdConfig(weight_decay=tc.weight_decay, clip_norm=tc.clip_norm, loss_scale=tc.loss_scale,
+                              clip_enabled=int(tc.clip_enabled), vjp_rank=pv.rank if pv else 0,
+                              vjp_residual_fraction=pv.residual_fraction if pv else 0.0,
+                              vjp_block_rows=pv.block_rows if pv else 0, vjp_seed=pv.seed if pv else 0)
+            N.api.sj_model_create_sgd(ctypes.byref(cfg), ctypes.byref(sgd), ctypes.c_void_p(stream or 0),
+                                      ctypes.byref(handle))
+        else:
+            adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
+                                clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
+            N.api.sj_model_create(ctypes.byref(cfg), ctypes.byref(adam), ctypes.c_void_p(stream or 0),
+                                  ctypes.byref(handle))
         self.h = handle
         self.count = N.load().sj_model_param_count(self.h)
         assert self.count == param_count(mc), (self.count, param_count(mc))
@@ -195,6 +239,21 @@ class Model:
         a = np.empty(self.count, np.float32)
         N.api.sj_model_get_grads(self.h, _np_ptr(a))
         return a
+
+    def materialize_grads(self):
+        """SGD models: dense + factored gradient of the last backward into the
+        gradient arena (GradientPlan::materialize), read with get_grads."""
+        N.api.sj_model_materialize_grads(self.h)
+
+    def vjp_info(self) -> dict:
+        c, d, b, p, r = ctypes.c_long(), ctypes.c_long(), ctypes.c_long(), ctypes.c_long(), ctypes.c_uint64()
+        N.api.sj_model_vjp_info(self.h, ctypes.byref(c), ctypes.byref(d), ctypes.byref(b), ctypes.byref(p),
+                                ctypes.byref(r))
+        return dict(compressed_matrices=c.value, dense_matrices=d.value, basis_groups=b.value,
+                    projection_groups=p.value, rng_state=r.value)
+
+    def set_vjp_rng(self, state: int):
+        N.api.sj_model_set_vjp_rng(self.h, ctypes.c_uint64(state))
 
     def get_adam_state(self):
         m = np.empty(self.count, np.float32); v = np.empty(self.count, np.float32); st = ctypes.c_long()

@@ -80,8 +80,10 @@ def pvjp_case():
     seed_check = O.Rng(42).next_u64()                             # parameter_vjp_check.rs:61-66, prepare's draw
     c1, r1, m1 = OP.indices(seed_check, 71, 97, 5, 2, 33, 16)
     seed_cfg5 = O.Rng(124).next_u64()                             # cfg5 parameter-VJP seed 124
-    r, blocks, s = OP.budget(16, 0.1, 32, 16384, 1024, 2 * 2752)
-    c5, r5, m5 = OP.indices(seed_cfg5, 1024, 2 * 2752, blocks, s, r, 32)
+    # the first prepare of a cfg5 step is the last layer's gate/up group; its
+    # donor is the up projection (widest member, last on ties: graph.rs:931-934)
+    r, blocks, s = OP.budget(16, 0.1, 32, 16384, 1024, 2752)
+    c5, r5, m5 = OP.indices(seed_cfg5, 1024, 2752, blocks, s, r, 32)
     return dict(seed_check=np.array(seed_check, np.uint64), check_columns=c1, check_rows=r1, check_map=m1,
                 seed_cfg5=np.array(seed_cfg5, np.uint64), cfg5_columns=c5, cfg5_rows=r5, cfg5_map=m5,
                 cfg5_budget=np.array([r, blocks, s]))

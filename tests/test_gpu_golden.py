@@ -102,7 +102,7 @@ def test_pvjp_selection_against_fixture(N, case):
         seed, a, b, blocks, S, R, group = int(g["seed_check"]), 71, 97, 5, 2, 33, 16
     else:
         R, blocks, S = (int(v) for v in g["cfg5_budget"])
-        seed, a, b, group = int(g["seed_cfg5"]), 1024, 2 * 2752, 32
+        seed, a, b, group = int(g["seed_cfg5"]), 1024, 2752, 32
     SCR, COL, ROWS, MAP = empty(b + blocks, "i32"), empty(R, "i32"), empty(S * group, "i32"), empty(a, "i32")
     api.sj_pvjp_indices(None, seed, a, b, blocks, S, R, group, SCR.p, COL.p, ROWS.p, MAP.p)
     sync()

@@ -529,3 +529,32 @@ def test_golden_fixture_reproduces(name):
             np.testing.assert_array_equal(a, b, err_msg=key)
         else:
             np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-14, err_msg=key)
+
+
+def test_model_backward_projection_dys():
+    """The per-layer output gradients of the projection Matmul nodes (the dY
+    a parameter VJP contracts with): X^T dY reproduces each projection's
+    FD-pinned weight gradient (q and k pre-RoPE, as the Matmul node values)."""
+    cfg = dict(TINY)
+    p, ids, tg = _tiny_inputs(cfg, seed=4)
+    acts = O.model_forward(cfg, p, ids, dtype="none")
+    loss, g, _, dys = O.model_backward(cfg, p, acts, ids, tg, dtype="none", want_dys=True)
+    lr, gr, _ = O.model_backward(cfg, p, acts, ids, tg, dtype="none")
+    assert loss == lr and np.array_equal(g, gr)
+    d, J, F, V, M = cfg["d"], cfg["d"] // cfg["hq"] * cfg["hk"], cfg["ffn"], O.VOCAB, cfg["T"] * cfg["B"]
+    A, off = {}, 0
+    for name, layer, size in O.acts_layout(cfg):
+        A[(name, layer)] = acts[off:off + size]
+        off += size
+    off = V * d
+    for l in range(cfg["layers"]):
+        z, z2 = A[("z", l)].reshape(M, d), A[("z2", l)].reshape(M, d)
+        off += 2 * d
+        for name, X, n in (("q", z, d), ("k", z, J), ("v", z, J)):
+            np.testing.assert_allclose((X.T @ dys[l][name]).ravel(), g[off:off + d * n], rtol=1e-9, atol=1e-14)
+            off += d * n
+        off += d * d
+        for name in ("gate", "up"):
+            np.testing.assert_allclose((z2.T @ dys[l][name]).ravel(), g[off:off + d * F], rtol=1e-9, atol=1e-14)
+            off += d * F
+        off += F * d
