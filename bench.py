@@ -85,6 +85,32 @@ def op_work(op: str, mc, tc):
         "grad_norm": ("byte", P * 4),
         "adamw": ("byte", 30 * P),
     }
+    pv = getattr(tc, "parameter_vjp", None)
+    if pv is not None:
+        # parameter VJP (cfg5): rank R, k selected rows; every layer has a
+        # q|k|v and a gate|up group (the step driver checks the decisions)
+        import oracle.pvjp as OP
+        R, blocks, S = OP.budget(pv.rank, pv.residual_fraction, pv.block_rows, M, d, F)
+        k = S * pv.block_rows
+        comp = mc.layers * (d * (d + 2 * J) + 2 * d * F)   # compressed parameters
+        table.update({
+            "pvjp_indices": ("byte", 4 * (F + blocks + R + k + d)),
+            # R donor columns read (bf16) in each of the two passes, Q written twice
+            "pvjp_basis": ("byte", 2 * (2 * M * R + 4 * M * R)),
+            # X^T read for A = X^T Q and its k selected rows again, Q read,
+            # E planes written
+            "pvjp_prepare": ("byte", 2 * d * M + 2 * k * M + 8 * M * R + 4 * (R + k) * M),
+            # E dY over the group's concatenated members (q|k|v and gate|up alternate)
+            "pvjp_coefficients": ("flop", 2 * (R + k) * M * ((d + 2 * J) + 2 * F) / 2),
+            # dense gradients read; factors are small
+            "factored_norm": ("byte", 4 * (P - comp)),
+            "norm_sum": ("byte", 0),
+            # w read + written, bf16 mirror written, dense G read for the
+            # uncompressed parameters
+            "sgd_update": ("byte", 10 * P + 4 * (P - comp)),
+        })
+    elif getattr(tc, "optimizer", "adamw") == "sgd":
+        table.update({"factored_norm": ("byte", 4 * P), "norm_sum": ("byte", 0), "sgd_update": ("byte", 14 * P)})
     return table.get(op, ("flop", 0.0))
 
 
@@ -104,13 +130,19 @@ def cpu_baseline(mc, tc, sample_batch: int):
     loss, g, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype=mc.precision)
     norm = math.sqrt(O.sum_squares(g))
     scale = min(1.0, tc.clip_norm / norm)
-    O.adamw(p, g, np.zeros_like(p), np.zeros_like(p), tc.learning_rate, tc.beta1, tc.beta2, tc.epsilon,
-            tc.weight_decay, 1 / (1 - tc.beta1), 1 / (1 - tc.beta2), scale)
+    if getattr(tc, "optimizer", "adamw") == "sgd":
+        # dense-gradient SGD update (the oracle has no factored step)
+        p -= tc.learning_rate * scale * g
+        what = "FP64 oracle fwd+bwd with dense gradients + SGD"
+    else:
+        O.adamw(p, g, np.zeros_like(p), np.zeros_like(p), tc.learning_rate, tc.beta1, tc.beta2, tc.epsilon,
+                tc.weight_decay, 1 / (1 - tc.beta1), 1 / (1 - tc.beta2), scale)
+        what = "FP64 oracle fwd+bwd+AdamW"
     dt = time.perf_counter() - t0
     tokens = sample_batch * tc.sequence
     return {"value": tokens / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
             "sample": f"{sample_batch} of {tc.batch} sequences x {tc.sequence} bytes of the same workload "
-                      f"(FP64 oracle fwd+bwd+AdamW, {dt:.2f} s)", "ms_per_step_sample": dt * 1e3}
+                      f"({what}, {dt:.2f} s)", "ms_per_step_sample": dt * 1e3}
 
 
 def copy_probe(mib: int):
@@ -569,7 +601,12 @@ def main():
         "dtype": mc.precision,
         "data": "synthetic uniform random bytes (SplitMix64 seed 123), weights N(0,0.02) seed 42",
         "config": {"workload": f"{args.config}: {mc.layers}-layer byte Transformer d{mc.width} GQA "
-                               f"{mc.heads}/{mc.kv} hd{mc.head_dim} SwiGLU {mc.ffn_width}, fwd+bwd+AdamW",
+                               f"{mc.heads}/{mc.kv} hd{mc.head_dim} SwiGLU {mc.ffn_width}, " +
+                               ("fwd+bwd+AdamW" if tc.optimizer == "adamw" else
+                                "fwd+bwd+selected-row SGD" + (
+                                    f" with rank-{tc.parameter_vjp.rank} parameter VJP, "
+                                    f"{tc.parameter_vjp.residual_fraction:g} residual rows"
+                                    if tc.parameter_vjp else "")),
                    "global_batch": tc.batch, "seq_len": tc.sequence, "tokens_per_step": tokens,
                    "parallelism": "single-gpu", "graph": not args.no_graph},
         "step_mfma": {"algorithmic_tflop_per_step": round(step_flops / 1e12, 4),
