@@ -268,6 +268,31 @@ int sj_attention_bwd_p(void *stream, const uint16_t *q, long ldq, const uint16_t
                        uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt, void *workspace, size_t workspace_bytes);
 size_t sj_attention_bwd_p_workspace_bytes(long batch, long t, long hq, long hk, long head_dim);
 
+/* ------------------------------------------- Hierarchical model patches
+ * The byte <-> patch maps of the hierarchical (cfg3) model (hidden_from_
+ * encoded, architecture.rs:368-393).  x, y, bos in the compute dtype (SJ_F32
+ * or SJ_BF16), gradients fp32; sums are formed in the reference's order. */
+/* Engine::patch_pool, hierarchy_ops.rs:149-169 (kernel hierarchy_patch_pool,
+ * hierarchy.py:107-119): y [batch*ceil(t/patch)][d] = mean of each patch's
+ * positions (the last patch of a sequence may be partial and divides by its
+ * own count). */
+int sj_patch_pool(void *stream, const void *x, int dtype, long batch, long t, long d, long patch, void *y);
+/* Engine::patch_pool_backward, hierarchy_ops.rs:171-204
+ * (hierarchy.py:122-131): dx [batch*t][d] = dy[patch of the position] /
+ * count. */
+int sj_patch_pool_bwd(void *stream, const float *dy, long batch, long t, long d, long patch, float *dx);
+/* Engine::patch_broadcast, hierarchy_ops.rs:206-236 (hierarchy.py:134-143):
+ * y [batch*t][d] = x row of the previous patch (positions of patch p see
+ * patch p-1), bos [d] for the first patch. */
+int sj_patch_broadcast(void *stream, const void *x, const void *bos, int dtype, long batch, long t, long d,
+                       long patch, void *y);
+/* Engine::patch_broadcast_backward, hierarchy_ops.rs:238-276
+ * (hierarchy.py:146-172): dx [batch*ceil(t/patch)][d] = sum of dy over the
+ * next patch's positions; dbos [d] = sum over batches of the first patch's
+ * positions. */
+int sj_patch_broadcast_bwd(void *stream, const float *dy, long batch, long t, long d, long patch, float *dx,
+                           float *dbos);
+
 /* ---------------------------------------------------- Mixture of experts
  * The MoE FFN of Block::apply (crates/sejong-model/src/architecture.rs:
  * 229-242) without host synchronisation: experts <= 32, top_k <= 8.  The

@@ -147,6 +147,10 @@ SIGNATURES = {
     "sj_sum_squares": (_I, [_P, _P, _L, _P, _P, _S]),
     "sj_adamw": (_I, [_P, _P, _P, _P, _P, _L, _F, _F, _F, _F, _F, _F, _F, _F]),
     "sj_adamw_multi": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "sj_patch_pool": (_I, [_P, _P, _I, _L, _L, _L, _L, _P]),
+    "sj_patch_pool_bwd": (_I, [_P, _P, _L, _L, _L, _L, _P]),
+    "sj_patch_broadcast": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _P]),
+    "sj_patch_broadcast_bwd": (_I, [_P, _P, _L, _L, _L, _L, _P, _P]),
     "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_materialize_grads": (_I, [_P]),

@@ -558,3 +558,41 @@ def test_model_backward_projection_dys():
             np.testing.assert_allclose((z2.T @ dys[l][name]).ravel(), g[off:off + d * F], rtol=1e-9, atol=1e-14)
             off += d * F
         off += F * d
+
+
+# ------------------------------------------------------ hierarchy patches
+def test_patch_maps_closed_forms():
+    from oracle import hierarchy as OH
+    B, T, d, P = 2, 10, 3, 4     # patches of 4, 4, 2 positions
+    x = np.arange(B * T * d, dtype=np.float64).reshape(B * T, d)
+    y = OH.patch_pool(x, B, T, P).reshape(B, 3, d)
+    xr = x.reshape(B, T, d)
+    np.testing.assert_array_equal(y[:, 0], xr[:, 0:4].mean(1))
+    np.testing.assert_array_equal(y[:, 2], xr[:, 8:10].mean(1))   # partial patch: its own count
+    np.testing.assert_array_equal(OH.patch_pool(np.full((B * T, d), 0.75), B, T, 16), 0.75 * np.ones((B, d)))  # patch > t
+    z = np.arange(B * 3 * d, dtype=np.float64).reshape(B * 3, d)
+    bos = np.array([-1.0, -2.0, -3.0])
+    yb = OH.patch_broadcast(z, bos, B, T, P).reshape(B, T, d)
+    np.testing.assert_array_equal(yb[:, :4], np.broadcast_to(bos, (B, 4, d)))
+    np.testing.assert_array_equal(yb[:, 4:8], np.broadcast_to(z.reshape(B, 3, d)[:, 0:1], (B, 4, d)))
+    np.testing.assert_array_equal(yb[:, 8:], np.broadcast_to(z.reshape(B, 3, d)[:, 1:2], (B, 2, d)))
+
+
+@pytest.mark.parametrize("T,P", [(10, 4), (12, 4), (5, 8), (7, 1)])
+def test_patch_maps_adjoints(T, P):
+    from oracle import hierarchy as OH
+    rng = np.random.default_rng(T * 10 + P)
+    B, d = 3, 5
+    NP = -(-T // P)
+    x = rng.normal(size=(B * T, d)).astype(np.float32).astype(np.float64)
+    yv = rng.normal(size=(B * NP, d)).astype(np.float32).astype(np.float64)
+    lhs = np.sum(OH.patch_pool(x, B, T, P) * yv)
+    rhs = np.sum(x * OH.patch_pool_backward(yv, B, T, P))
+    assert abs(lhs - rhs) < 1e-5 * (1 + abs(lhs))
+    z = rng.normal(size=(B * NP, d)).astype(np.float32).astype(np.float64)
+    bos = rng.normal(size=d).astype(np.float32).astype(np.float64)
+    dy = rng.normal(size=(B * T, d)).astype(np.float32).astype(np.float64)
+    dx, dbos = OH.patch_broadcast_backward(dy, B, T, P)
+    lhs = np.sum(OH.patch_broadcast(z, bos, B, T, P) * dy)
+    rhs = np.sum(z * dx) + np.sum(bos * dbos)
+    assert abs(lhs - rhs) < 1e-5 * (1 + abs(lhs))
