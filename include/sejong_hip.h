@@ -492,6 +492,19 @@ int sj_sum_f64(void *stream, const double *x, long n, double *out);
 int sj_cross_entropy(void *stream, const float *x, long ldx, const int32_t *targets,
                      float *loss, float *dx, long lddx, long rows, long vocab,
                      const float *dy, float dy_scalar);
+/* Engine::gather, lib.rs:1010-1028 (kernel gather, kernels.py:241-245):
+ * y [rows][d] = x[idx[r]] (row stride ldx) in y's dtype (a gather followed
+ * by Graph::cast to F32 when yd = SJ_F32). */
+int sj_gather_rows(void *stream, const void *x, int xd, long ldx, const int32_t *idx, long rows, long d, void *y,
+                   int yd);
+/* Engine::gather_backward, lib.rs:1029-1050: dx [n][d] (row stride ldx) =
+ * 0, then dx[idx[r]] += dy[r] for r in order (fp32). */
+int sj_gather_rows_bwd(void *stream, const float *dy, const int32_t *idx, long rows, long d, float *dx, long ldx,
+                       long n);
+/* Engine::bias_add / bias_reduce, common_ops.rs:46-77 (common.py:28-36):
+ * y = x + bias (row-broadcast); y[c] = sum over rows, in order, of x[r][c]. */
+int sj_bias_add(void *stream, const float *x, long ldx, const float *bias, float *y, long ldy, long rows, long d);
+int sj_bias_reduce(void *stream, const float *x, long ldx, long rows, long d, float *y);
 /* Engine::loss_summary, lib.rs:524-543 (kernels.py:254-262): out[slot] =
  * (sum_i loss[i] in FP64) * weight / n. */
 int sj_loss_summary(void *stream, const float *loss, long n, double *out, long slot, float weight);
@@ -580,6 +593,22 @@ typedef struct {
   uint64_t vjp_seed;
 } sj_sgd_config;
 int sj_model_create_sgd(const sj_model_config *cfg, const sj_sgd_config *sgd, void *stream, sj_model **out);
+/* NativeValue (crates/sejong-model/src/native/value.rs:111-160, trained
+ * by train_value, crates/sejong-train/src/memory.rs:799-1065): the body
+ * (cfg's blocks and final norm) under its own byte embedding [259][d]
+ * (pad 256, BOS 257, SEP 258), the SEP row of each of the batch requests
+ * gathered, cast to F32 and mapped by an affine head [d][values] + bias
+ * [1][values]; loss = mean cross entropy of the value labels.  Parameters
+ * in NativeValue::parameters order (the body without embedding and output,
+ * then native_embedding, native_value, native_bias).  Exactly one of adam
+ * / sgd.  cfg->sequence is the padded request length (>= the longest
+ * prompt + 2: trailing pad bytes do not reach the causal SEP row). */
+int sj_model_create_value(const sj_model_config *cfg, long values, const sj_adam_config *adam,
+                          const sj_sgd_config *sgd, void *stream, sj_model **out);
+/* One packed request batch: ids [batch*sequence] (row r = BOS, prompt,
+ * SEP, pad), positions [batch] (the SEP index of row r, inside row r),
+ * labels [batch].  Synchronous. */
+int sj_model_set_value_batch(sj_model *m, const int32_t *ids, const int32_t *positions, const int32_t *labels);
 /* GradientPlan::materialize for every parameter of an SGD model: the
  * gradient arena receives dense + factored G of the last backward (so
  * sj_model_get_grads returns it).  No-op for AdamW models. */

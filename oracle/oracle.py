@@ -72,6 +72,7 @@ def _declare(L):
     L.or_model_backward.restype = ctypes.c_double
     L.or_model_backward_dys.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _D, _I, _I, _D, _D, _D]
     L.or_model_backward_dys.restype = ctypes.c_double
+    L.or_model_backward_hidden.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _D, _D, _D, _D]
     L.or_model_fwd_bwd.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I, _D, _D, _D]
     L.or_model_fwd_bwd.restype = ctypes.c_double
     L.or_model_loss.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I]
@@ -311,6 +312,24 @@ def model_backward(cfg, params, acts, ids, targets, dtype="f32", want_dys=False)
             off += M * width
         per.append(layer)
     return loss, grads, rows, per
+
+
+def model_backward_hidden(cfg, params, acts, dh, dtype="f32"):
+    """The body's backward from d(final-norm output) dh [M][d] (another head
+    on the body): reference-layout gradients (embedding / output zero) and the
+    gradient at the embedding output [M][d].  acts may stop before the
+    logits."""
+    params, pp = _d(params); dh, pd = _d(dh)
+    a = np.zeros(model_acts_count(cfg))
+    acts = np.asarray(acts, np.float64).ravel()
+    a[:acts.size] = acts
+    a, pa = _d(a)
+    grads, pg = _out(params.size)
+    d, L, hq, hk, F, T, B = _dims(cfg)
+    demb, pe = _out((T * B, d))
+    lib().or_model_backward_hidden(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0), DTYPE_CODE[dtype],
+                                   pp, pa, pd, pg, pe)
+    return grads, demb
 
 
 def acts_layout(cfg):

@@ -642,38 +642,25 @@ double or_model_backward(long d, long layers, long hq, long hk, long ffn, long T
                                  grads, loss_rows, NULL);
 }
 
-double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
-                             double theta, int dtype, const double *params, const double *acts_in,
-                             const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows,
-                             double *dys) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
-    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
-    plan_t pl;
-    make_plan(&cf, params, &pl);
-    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
-    double *xl, *hn, *logits;
-    view_acts(&cf, (double *)acts_in, lv, &xl, &hn, &logits);
-    double *lrow = ALLOC(M), *dlog = ALLOC(M * V);
-    /* seed scale/count, graph.rs:539-549 (f32 division in the reference) */
-    double seed = (double)(1.0f / (float)M);
-    or_cross_entropy(logits, targets, lrow, dlog, M, V, seed);
-    double loss = 0.0;
-    for (long i = 0; i < M; i++) loss += lrow[i];
-    loss /= (double)M;
-    if (loss_rows) memcpy(loss_rows, lrow, sizeof(double) * (size_t)M);
-    memset(grads, 0, sizeof(double) * (size_t)pl.total);
-    const double *wout = params + pl.off_out;
-    double *dx = ALLOC(M * d), *dres = ALLOC(M * d);
-    or_matmul(dlog, wout, dx, M, d, V, 0, 1);               /* dh = dlogits W^T */
-    or_matmul(hn, dlog, grads + pl.off_out, d, V, M, 1, 0); /* dW_out = h^T dlogits */
-    or_rmsnorm_bwd(xl, pl.C + pl.off_final, dx, NULL, dres, grads + pl.off_final, M, d, eps);
+/* The body's backward from dx = d(final norm output) [M][d]: final norm,
+ * then per layer down / SwiGLU / gate+up / ffn norm / attention output /
+ * attention (+ inverse RoPE) / QKV / attention norm.  The gradient at the
+ * embedding output is left in demb [M][d] (nullable: then the embedding
+ * backward into grads runs here, ids < OR_VOCAB). */
+static void body_backward(const or_model_cfg *c, const plan_t *pl, layer_view *lv, const double *xl, double *dx,
+                          const int32_t *ids, double *grads, double *dys, double *demb) {
+    const long d = c->d, layers = c->layers, hq = c->hq, hk = c->hk, T = c->T, B = c->B;
+    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = c->ffn;
+    const double eps = c->eps, theta = c->theta;
+    double *dres = ALLOC(M * d);
+    or_rmsnorm_bwd(xl, pl->C + pl->off_final, dx, NULL, dres, grads + pl->off_final, M, d, eps);
     double *dbig = ALLOC(M * F), *dg = ALLOC(M * F), *du = ALLOC(M * F);
     double *dz = ALLOC(M * d), *dtmp = ALLOC(M * d), *dx1 = ALLOC(M * d), *dO = ALLOC(M * d);
     double *dq = ALLOC(M * d), *dk = ALLOC(M * J), *dv = ALLOC(M * J);
     double *dqr = ALLOC(M * d), *dkr = ALLOC(M * J), *dxn = ALLOC(M * d);
     for (long l = layers - 1; l >= 0; l--) {
         layer_view *a = &lv[l];
-        lw *y = &pl.L[l];
+        const lw *y = &pl->L[l];
         /* x_{l+1} = x1 + down(h): dres flows to x1 and to down's output */
         or_matmul(dres, y->wd, dbig, M, F, d, 0, 1);              /* dh */
         or_matmul(a->h, dres, grads + y->o_wd, F, d, M, 1, 0);    /* dW_down */
@@ -711,11 +698,64 @@ double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, lo
         or_rmsnorm_bwd(a->x, y->an, dz, dx1, dxn, grads + y->o_an, M, d, eps);
         double *t = dres; dres = dxn; dxn = t;
     }
-    or_embedding_bwd(dres, ids, grads + pl.off_emb, M, d, V);
-    free(lrow); free(dlog); free(dx); free(dres); free(dbig); free(dg); free(du); free(dz); free(dtmp);
+    if (demb)
+        memcpy(demb, dres, sizeof(double) * (size_t)(M * d));
+    else
+        or_embedding_bwd(dres, ids, grads + pl->off_emb, M, d, V);
+    free(dres); free(dbig); free(dg); free(du); free(dz); free(dtmp);
     free(dx1); free(dO); free(dq); free(dk); free(dv); free(dqr); free(dkr); free(dxn);
+}
+
+double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                             double theta, int dtype, const double *params, const double *acts_in,
+                             const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows,
+                             double *dys) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    const long M = T * B, V = OR_VOCAB;
+    plan_t pl;
+    make_plan(&cf, params, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, (double *)acts_in, lv, &xl, &hn, &logits);
+    double *lrow = ALLOC(M), *dlog = ALLOC(M * V);
+    /* seed scale/count, graph.rs:539-549 (f32 division in the reference) */
+    double seed = (double)(1.0f / (float)M);
+    or_cross_entropy(logits, targets, lrow, dlog, M, V, seed);
+    double loss = 0.0;
+    for (long i = 0; i < M; i++) loss += lrow[i];
+    loss /= (double)M;
+    if (loss_rows) memcpy(loss_rows, lrow, sizeof(double) * (size_t)M);
+    memset(grads, 0, sizeof(double) * (size_t)pl.total);
+    const double *wout = params + pl.off_out;
+    double *dx = ALLOC(M * d);
+    or_matmul(dlog, wout, dx, M, d, V, 0, 1);               /* dh = dlogits W^T */
+    or_matmul(hn, dlog, grads + pl.off_out, d, V, M, 1, 0); /* dW_out = h^T dlogits */
+    body_backward(&cf, &pl, lv, xl, dx, ids, grads, dys, NULL);
+    free(lrow); free(dlog); free(dx);
     free(lv); free(pl.L); free(pl.C);
     return loss;
+}
+
+/* The body's backward from a given gradient of the final-norm output
+ * dh [M][d] (another head on the body, e.g. NativeValue's affine value
+ * head, native/value.rs:139-146): grads (reference layout; embedding and
+ * output left zero) and the gradient at the embedding output demb [M][d]
+ * for the caller's own embedding. */
+void or_model_backward_hidden(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                              double theta, int dtype, const double *params, const double *acts_in,
+                              const double *dh, double *grads, double *demb) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    const long M = T * B;
+    plan_t pl;
+    make_plan(&cf, params, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, (double *)acts_in, lv, &xl, &hn, &logits);
+    memset(grads, 0, sizeof(double) * (size_t)pl.total);
+    double *dx = ALLOC(M * d);
+    memcpy(dx, dh, sizeof(double) * (size_t)(M * d));
+    body_backward(&cf, &pl, lv, xl, dx, NULL, grads, NULL, demb);
+    free(dx); free(lv); free(pl.L); free(pl.C);
 }
 
 /* One training forward+backward.  params: reference layout (above), fp32

@@ -147,6 +147,10 @@ SIGNATURES = {
     "sj_sum_squares": (_I, [_P, _P, _L, _P, _P, _S]),
     "sj_adamw": (_I, [_P, _P, _P, _P, _P, _L, _F, _F, _F, _F, _F, _F, _F, _F]),
     "sj_adamw_multi": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P]),
+    "sj_gather_rows": (_I, [_P, _P, _I, _L, _P, _L, _L, _P, _I]),
+    "sj_gather_rows_bwd": (_I, [_P, _P, _P, _L, _L, _P, _L, _L]),
+    "sj_bias_add": (_I, [_P, _P, _L, _P, _P, _L, _L, _L]),
+    "sj_bias_reduce": (_I, [_P, _P, _L, _L, _L, _P]),
     "sj_patch_pool": (_I, [_P, _P, _I, _L, _L, _L, _L, _P]),
     "sj_patch_pool_bwd": (_I, [_P, _P, _L, _L, _L, _L, _P]),
     "sj_patch_broadcast": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _P]),
@@ -154,6 +158,9 @@ SIGNATURES = {
     "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_materialize_grads": (_I, [_P]),
+    "sj_model_create_value": (_I, [ctypes.POINTER(ModelConfig), _L, ctypes.POINTER(AdamConfig),
+                                   ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
+    "sj_model_set_value_batch": (_I, [_P, _P, _P, _P]),
     "sj_model_vjp_info": (_I, [_P, ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L),
                                ctypes.POINTER(_U64)]),
     "sj_model_set_vjp_rng": (_I, [_P, _U64]),

@@ -284,6 +284,50 @@ __global__ __launch_bounds__(256) void k_adamw_multi(float* __restrict__ w, cons
   }
 }
 
+
+// Engine::gather (lib.rs:1010-1028): y[r] = x[idx[r]] converted to y's dtype
+__global__ void k_gather_rows(const void* x, int xd, long ldx, const int32_t* idx, void* y, int yd, long rows, long d) {
+  const long total = rows * d;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / d, c = i - r * d;
+    store_from_f32(y, yd, i, load_as_f32(x, xd, (long)idx[r] * ldx + c));
+  }
+}
+
+__global__ void k_zero_rows(float* x, long ldx, long rows, long d) {
+  const long total = rows * d;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / d, c = i - r * d;
+    x[r * ldx + c] = 0.f;
+  }
+}
+
+// Engine::gather_backward (lib.rs:1029-1050): dx = 0, then dx[idx[r]] += dy[r]
+// for r in order (one thread per column: fixed order, repeated rows add up)
+__global__ void k_gather_rows_bwd(const float* dy, const int32_t* idx, float* dx, long ldx, long rows, long d) {
+  const long c = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  for (long r = 0; r < rows; r++) dx[(long)idx[r] * ldx + c] += dy[r * d + c];
+}
+
+// common.py:28-30 bias_add: y[r][c] = x[r][c] + b[c]
+__global__ void k_bias_add(const float* x, long ldx, const float* b, float* y, long ldy, long rows, long d) {
+  const long total = rows * d;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const long r = i / d, c = i - r * d;
+    y[r * ldy + c] = x[r * ldx + c] + b[c];
+  }
+}
+
+// common.py:33-36 bias_reduce: y[c] = sum over rows in order of x[r][c] (fp32)
+__global__ void k_bias_reduce(const float* x, long ldx, float* y, long rows, long d) {
+  const long c = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  float acc = 0.f;
+  for (long r = 0; r < rows; r++) acc += x[r * ldx + c];
+  y[c] = acc;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
@@ -435,5 +479,47 @@ extern "C" int sj_adamw_multi(void* stream, float* w, const float* g, float* m, 
   hipLaunchKernelGGL(k_adamw_multi, dim3(ew_blocks(quads)), dim3(256), 0, (hipStream_t)stream, w, g, m, v,
                      (bf16_t*)mirror, n, n_nodecay, step, sumsq, status);
   SJ_LAUNCH_CHECK("adamw_multi");
+  return SJ_OK;
+}
+
+extern "C" int sj_gather_rows(void* stream, const void* x, int xd, long ldx, const int32_t* idx, long rows, long d,
+                              void* y, int yd) {
+  SJ_REQUIRE(x && idx && y && rows >= 0 && d > 0 && ldx >= d && dtype_ok(xd) && dtype_ok(yd), "gather: arguments");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_gather_rows, dim3(ew_blocks(rows * d)), dim3(EW_THREADS), 0, (hipStream_t)stream, x, xd, ldx,
+                     idx, y, yd, rows, d);
+  SJ_LAUNCH_CHECK("gather");
+  return SJ_OK;
+}
+
+extern "C" int sj_gather_rows_bwd(void* stream, const float* dy, const int32_t* idx, long rows, long d, float* dx,
+                                  long ldx, long n) {
+  SJ_REQUIRE(dy && idx && dx && rows >= 0 && d > 0 && ldx >= d && n > 0, "gather_backward: arguments");
+  hipStream_t s = (hipStream_t)stream;
+  // zero dx with a kernel (not a memset: the call may sit in a captured graph)
+  hipLaunchKernelGGL(k_zero_rows, dim3(ew_blocks(n * d)), dim3(EW_THREADS), 0, s, dx, ldx, n, d);
+  SJ_LAUNCH_CHECK("gather_backward");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_gather_rows_bwd, dim3((unsigned)((d + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0, s, dy,
+                     idx, dx, ldx, rows, d);
+  SJ_LAUNCH_CHECK("gather_backward");
+  return SJ_OK;
+}
+
+extern "C" int sj_bias_add(void* stream, const float* x, long ldx, const float* bias, float* y, long ldy, long rows,
+                           long d) {
+  SJ_REQUIRE(x && bias && y && rows >= 0 && d > 0 && ldx >= d && ldy >= d, "affine bias shape mismatch");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_bias_add, dim3(ew_blocks(rows * d)), dim3(EW_THREADS), 0, (hipStream_t)stream, x, ldx, bias, y,
+                     ldy, rows, d);
+  SJ_LAUNCH_CHECK("bias_add");
+  return SJ_OK;
+}
+
+extern "C" int sj_bias_reduce(void* stream, const float* x, long ldx, long rows, long d, float* y) {
+  SJ_REQUIRE(x && y && rows >= 0 && d > 0 && ldx >= d, "bias gradient shape mismatch");
+  hipLaunchKernelGGL(k_bias_reduce, dim3((unsigned)((d + EW_THREADS - 1) / EW_THREADS)), dim3(EW_THREADS), 0,
+                     (hipStream_t)stream, x, ldx, y, rows, d);
+  SJ_LAUNCH_CHECK("bias_reduce");
   return SJ_OK;
 }

@@ -55,6 +55,7 @@ struct RefTensor {
   // -1 none; member index and first column in the group's concatenated width
   int layer = -1, kind = -1, member = -1;
   long col0 = 0;
+  int ndim = 2;  // the reference tensor's rank (weight decay applies when > 1)
 };
 
 struct Layer {
@@ -121,6 +122,14 @@ struct sj_model {
   sj_adam_config adam;
   hipStream_t stream;
   long V, Vp, d, L, HQ, HK, Dh, J, F, T, B, M, NQKV;
+  // head: HV classes over HR rows (the LM head: V over all M tokens; the
+  // NativeValue head: value_n classes over the B selected SEP rows); Vp =
+  // HV rounded up to 8 (the head's row stride)
+  long HV = 0, HR = 0;
+  long value_n = 0;  // NativeValue head (native/value.rs:111-160) when > 0
+  long bias = 0;     // internal offset of native_bias
+  int32_t *sel = nullptr, *labels = nullptr;  // SEP row of each request, its value label
+  float *hsel = nullptr, *dhsel = nullptr;    // selected hidden rows (fp32) and their gradient
   int dt;
   size_t esz;  // bytes per activation element
   // parameter arenas
@@ -266,20 +275,24 @@ void build_layout(sj_model* m) {
     m->layers[l].down = off; off = align64(off + F * d);
   }
   m->out = off; off = align64(off + d * m->Vp);
+  if (m->value_n) { m->bias = off; off = align64(off + m->Vp); }  // [1][n]: 2-D, so it decays
   m->n_params = off;
 
   long ro = 0;
   auto add = [&](const std::string& name, long rows, long cols, long ioff, long ild, int layer = -1, int kind = -1,
-                 int member = -1, long col0 = 0) {
-    m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild, layer, kind, member, col0});
+                 int member = -1, long col0 = 0, int ndim = 2) {
+    m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild, layer, kind, member, col0, ndim});
     ro += rows * cols;
   };
-  add("embedding", V, d, m->emb, d);
+  // NativeValue::parameters (native/value.rs:89-115): the body without its
+  // embedding and output, then native_embedding [259][d], native_value
+  // [d][n] and native_bias [1][n]
+  if (!m->value_n) add("embedding", V, d, m->emb, d);
   for (long l = 0; l < m->L; l++) {
     std::string p = "layers." + std::to_string(l) + ".";
     const Layer& y = m->layers[l];
-    add(p + "attention_norm", 1, d, y.an, d);
-    add(p + "ffn_norm", 1, d, y.fn, d);
+    add(p + "attention_norm", 1, d, y.an, d, -1, -1, -1, 0, 1);
+    add(p + "ffn_norm", 1, d, y.fn, d, -1, -1, -1, 0, 1);
     const int li = (int)l;
     add(p + "query", d, d, y.qkv, m->NQKV, li, 0, 0, 0);
     add(p + "key", d, J, y.qkv + d, m->NQKV, li, 0, 1, d);
@@ -289,8 +302,14 @@ void build_layout(sj_model* m) {
     add(p + "up", d, F, y.gu + F, 2 * F, li, 1, 1, F);
     add(p + "down", F, d, y.down, d);
   }
-  add("final_norm", 1, d, m->final_norm, d);
-  add("output", d, V, m->out, m->Vp);
+  add("final_norm", 1, d, m->final_norm, d, -1, -1, -1, 0, 1);
+  if (m->value_n) {
+    add("native_embedding", V, d, m->emb, d);
+    add("native_value", d, m->HV, m->out, m->Vp);
+    add("native_bias", 1, m->HV, m->bias, m->Vp);
+  } else {
+    add("output", d, m->HV, m->out, m->Vp);
+  }
   m->ref_count = ro;
 }
 
@@ -365,12 +384,26 @@ int forward(sj_model* m) {
     OP("down_residual", sj_linear_residual_fwd(s, m->hh[l], F, M, F, wc(m, y.down), d, d, m->x1[l], d, m->x[l + 1], d, dt));
   }
   OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->hn, M, d, eps));
+  if (m->value_n) {
+    // NativeValue::forward_batch (native/value.rs:139-146): gather the SEP
+    // rows, cast to F32, affine head (matmul + bias_add), then the mean CE
+    // of the value labels (train_value, memory.rs:977-979)
+    const long R = m->HR, n = m->HV;
+    OP("value_gather", sj_gather_rows(s, m->hn, dt, d, m->sel, R, d, m->hsel, SJ_F32));
+    OP("head_fwd", sj_gemm(s, 0, 0, R, n, d, m->hsel, SJ_F32, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp,
+                           0, m->ws, m->ws_bytes));
+    OP("value_bias", sj_bias_add(s, m->logits, m->Vp, m->w + m->bias, m->logits, m->Vp, R, n));
+    OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->labels, m->loss_rows, m->dlogits, m->Vp, R, n,
+                                         nullptr, 1.0f / (float)R));
+    OP("loss_summary", sj_loss_summary(s, m->loss_rows, R, m->loss, 0, 1.0f));
+    return SJ_OK;
+  }
   // fp32 head on the fp32 master (architecture.rs:160-167); hn's values are
   // exact in fp32 (Graph::cast to F32), so it is read in its storage dtype.
-  OP("head_fwd", sj_gemm(s, 0, 0, M, m->V, d, m->hn, dt, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp, 0, m->ws,
+  OP("head_fwd", sj_gemm(s, 0, 0, M, m->HV, d, m->hn, dt, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp, 0, m->ws,
               m->ws_bytes));
   const float seed = 1.0f / (float)M;  // scale / count, graph.rs:546
-  OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlogits, m->Vp, M, m->V, nullptr, seed));
+  OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlogits, m->Vp, M, m->HV, nullptr, seed));
   OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, 0, 1.0f));
   return SJ_OK;
 }
@@ -412,11 +445,23 @@ int backward(sj_model* m) {
   const int dt = m->dt;
   const float eps = m->c.norm_epsilon;
   float* G = m->g;
+  if (m->value_n) {
+    // affine head backward (bias_reduce, the F32 matmul's dX / dW) and the
+    // gather's backward into the full hidden gradient (zero off the SEP rows)
+    const long R = m->HR, n = m->HV;
+    OP("value_bias_bwd", sj_bias_reduce(s, m->dlogits, m->Vp, R, n, G + m->bias));
+    OP("head_dw", sj_gemm(s, 1, 0, d, n, R, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
+                          m->ws, m->ws_bytes));
+    OP("head_dx", sj_gemm(s, 0, 1, R, d, n, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dhsel, SJ_F32,
+                          d, 0, m->ws, m->ws_bytes));
+    OP("value_scatter", sj_gather_rows_bwd(s, m->dhsel, m->sel, R, d, m->dz, d, M));
+  } else {
   // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
-  OP("head_dx", sj_gemm(s, 0, 1, M, d, m->V, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d, 0, m->ws,
+  OP("head_dx", sj_gemm(s, 0, 1, M, d, m->HV, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d, 0, m->ws,
               m->ws_bytes));
-  OP("head_dw", sj_gemm(s, 1, 0, d, m->V, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0, m->ws,
+  OP("head_dw", sj_gemm(s, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0, m->ws,
               m->ws_bytes));
+  }
   int cur = 0;
   if (m->planes) {
     const uint16_t* W = m->mirror;
@@ -623,7 +668,7 @@ int build_plan(sj_model* m) {
     p.dense = c ? nullptr : m->g + t.int_offset;
     p.rows = t.rows;
     p.cols = t.cols;
-    p.decay = t.rows > 1;  // 1-D tensors have rows = 1
+    p.decay = t.ndim > 1;
     p.ld = t.int_ld;
     p.mirror = m->mirror ? m->mirror + t.int_offset : nullptr;
     if (c) {
@@ -678,8 +723,8 @@ int stage_sgd(sj_model* m, float lr) {
   return SJ_OK;
 }
 
-int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, void* stream,
-                 sj_model** out);
+int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n,
+                 void* stream, sj_model** out);
 
 }  // namespace
 
@@ -688,7 +733,7 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
 extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config* adam, void* stream,
                                sj_model** out) {
   SJ_REQUIRE(cfg && adam && out, "model: null argument");
-  return create_model(cfg, adam, nullptr, stream, out);
+  return create_model(cfg, adam, nullptr, 0, stream, out);
 }
 
 extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_config* sgd, void* stream,
@@ -697,12 +742,24 @@ extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_conf
   SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
                  (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
              "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
-  return create_model(cfg, nullptr, sgd, stream, out);
+  return create_model(cfg, nullptr, sgd, 0, stream, out);
+}
+
+extern "C" int sj_model_create_value(const sj_model_config* cfg, long values, const sj_adam_config* adam,
+                                     const sj_sgd_config* sgd, void* stream, sj_model** out) {
+  SJ_REQUIRE(cfg && out && values > 0 && ((adam != nullptr) != (sgd != nullptr)),
+             "native value model: configuration, values > 0 and exactly one optimizer");
+  SJ_REQUIRE(cfg->sequence >= 3, "native value model: the sequence holds BOS, the prompt and SEP");
+  if (sgd)
+    SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
+                   (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
+               "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
+  return create_model(cfg, adam, sgd, values, stream, out);
 }
 
 namespace {
-int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, void* stream,
-                 sj_model** out) {
+int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n,
+                 void* stream, sj_model** out) {
   const sj_model_config& c = *cfg;
   SJ_REQUIRE(c.vocab > 0 && c.width > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.ffn_width > 0 &&
                  c.sequence > 0 && c.batch > 0,
@@ -728,8 +785,11 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     }
     m->own_stream = true;
   }
-  m->V = c.vocab;
-  m->Vp = (c.vocab + 7) / 8 * 8;
+  m->value_n = value_n;
+  m->V = value_n ? 259 : c.vocab;  // NativeValue: bytes, pad 256, BOS 257, SEP 258 (native/value.rs:15-16)
+  m->HV = value_n ? value_n : m->V;
+  m->HR = value_n ? c.batch : c.sequence * c.batch;
+  m->Vp = (m->HV + 7) / 8 * 8;
   m->d = c.width;
   m->L = c.layers;
   m->HQ = c.heads;
@@ -834,8 +894,14 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     }
   }
   ALLOC(m->hn, M * d * es);
-  ALLOC(m->logits, M * (size_t)m->Vp * 4);
-  ALLOC(m->dlogits, M * (size_t)m->Vp * 4);
+  ALLOC(m->logits, (size_t)m->HR * (size_t)m->Vp * 4);
+  ALLOC(m->dlogits, (size_t)m->HR * (size_t)m->Vp * 4);
+  if (m->value_n) {
+    ALLOC(m->sel, sizeof(int32_t) * (size_t)m->HR);
+    ALLOC(m->labels, sizeof(int32_t) * (size_t)m->HR);
+    ALLOC(m->hsel, sizeof(float) * (size_t)m->HR * d);
+    ALLOC(m->dhsel, sizeof(float) * (size_t)m->HR * d);
+  }
   ALLOC(m->loss_rows, M * 4);
   ALLOC(m->dres[0], M * d * 4);
   ALLOC(m->dres[1], M * d * 4);
@@ -878,8 +944,9 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   const long Mi = m->M;
   upd(sj_rmsnorm_bwd_workspace_bytes(Mi, m->d));
   upd(sj_sum_squares_workspace_bytes(m->n_params));
-  upd(sj_gemm_workspace_bytes(Mi, m->d, m->V));
-  upd(sj_gemm_workspace_bytes(m->d, m->V, Mi));
+  upd(sj_gemm_workspace_bytes(m->HR, m->d, m->HV));
+  upd(sj_gemm_workspace_bytes(m->d, m->HV, m->HR));
+  upd(sj_gemm_workspace_bytes(m->HR, m->HV, m->d));
   upd(sj_gemm_workspace_bytes(m->F, m->d, Mi));
   upd(sj_gemm_workspace_bytes(m->d, 2 * m->F, Mi));
   upd(sj_gemm_workspace_bytes(m->d, m->d, Mi));
@@ -1034,6 +1101,7 @@ extern "C" int sj_model_set_adam_state(sj_model* m, const float* mh, const float
 
 extern "C" int sj_model_set_batch(sj_model* m, const int32_t* ids, const int32_t* targets, int on_device) {
   SJ_REQUIRE(m && ids && targets, "set_batch: null");
+  SJ_REQUIRE(!m->value_n, "set_batch: a native value model takes sj_model_set_value_batch");
   size_t bytes = sizeof(int32_t) * (size_t)m->M;
   if (on_device) {
     SJ_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyDeviceToDevice, m->stream));
@@ -1046,6 +1114,20 @@ extern "C" int sj_model_set_batch(sj_model* m, const int32_t* ids, const int32_t
     SJ_HIP(hipMemcpyAsync(m->targets, targets, bytes, hipMemcpyHostToDevice, m->stream));
     SJ_HIP(hipStreamSynchronize(m->stream));
   }
+  return SJ_OK;
+}
+
+extern "C" int sj_model_set_value_batch(sj_model* m, const int32_t* ids, const int32_t* positions,
+                                        const int32_t* labels) {
+  SJ_REQUIRE(m && m->value_n && ids && positions && labels, "set_value_batch: native value model and arrays");
+  for (long i = 0; i < m->M; i++) SJ_REQUIRE(ids[i] >= 0 && ids[i] < m->V, "native token %ld out of vocabulary", i);
+  for (long r = 0; r < m->HR; r++)
+    SJ_REQUIRE(positions[r] >= r * m->T && positions[r] < (r + 1) * m->T && labels[r] >= 0 && labels[r] < m->value_n,
+               "native request %ld: SEP position outside its row or label outside the values", r);
+  SJ_HIP(hipMemcpyAsync(m->ids, ids, sizeof(int32_t) * (size_t)m->M, hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipMemcpyAsync(m->sel, positions, sizeof(int32_t) * (size_t)m->HR, hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipMemcpyAsync(m->labels, labels, sizeof(int32_t) * (size_t)m->HR, hipMemcpyHostToDevice, m->stream));
+  SJ_HIP(hipStreamSynchronize(m->stream));
   return SJ_OK;
 }
 
@@ -1171,7 +1253,7 @@ extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) 
 extern "C" long sj_model_activation_count(const sj_model* m) {
   if (!m) return -1;
   const long M = m->M, d = m->d, J = m->J, F = m->F;
-  return m->L * (6 * M * d + 2 * M * J + M * m->HQ + 3 * M * F) + 2 * M * d + M * m->V;
+  return m->L * (6 * M * d + 2 * M * J + M * m->HQ + 3 * M * F) + 2 * M * d + m->HR * m->HV;
 }
 
 static int export_matrix(sj_model* m, const void* dev, int dt, long rows, long ld, long col0, long cols,
@@ -1216,7 +1298,7 @@ extern "C" int sj_model_export_activations(sj_model* m, float* host) {
   }
   TRY(export_matrix(m, m->x[m->L], dt, M, d, 0, d, p)); p += M * d;
   TRY(export_matrix(m, m->hn, dt, M, d, 0, d, p)); p += M * d;
-  TRY(export_matrix(m, m->logits, SJ_F32, M, m->Vp, 0, m->V, p));
+  TRY(export_matrix(m, m->logits, SJ_F32, m->HR, m->Vp, 0, m->HV, p));
   return SJ_OK;
 }
 
@@ -1249,8 +1331,8 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   SJ_REQUIRE(m && what && ptr, "buffer: null");
   std::string w(what);
   long n = 0;
-  if (w == "logits") { *ptr = m->logits; n = m->M * m->Vp; }
-  else if (w == "dlogits") { *ptr = m->dlogits; n = m->M * m->Vp; }
+  if (w == "logits") { *ptr = m->logits; n = m->HR * m->Vp; }
+  else if (w == "dlogits") { *ptr = m->dlogits; n = m->HR * m->Vp; }
   else if (w == "loss_rows") { *ptr = m->loss_rows; n = m->M; }
   else if (w == "ids") { *ptr = m->ids; n = m->M; }
   else if (w == "targets") { *ptr = m->targets; n = m->M; }

@@ -136,6 +136,15 @@ def layout(c: ModelConfig) -> list[tuple[str, tuple[int, ...], bool]]:
     return out
 
 
+def value_layout(c: ModelConfig, values: int) -> list[tuple[str, tuple[int, ...], bool]]:
+    """NativeValue::parameters order (native/value.rs:89-115): the body
+    without embedding and output, then the value embedding (259 rows: bytes,
+    pad 256, BOS 257, SEP 258), the value head and its bias."""
+    body = [t for t in layout(c) if t[0] not in ("embedding", "output")]
+    return body + [("native_embedding", (259, c.width), False), ("native_value", (c.width, values), False),
+                   ("native_bias", (1, values), False)]
+
+
 def param_count(c: ModelConfig) -> int:
     return sum(math.prod(s) for _, s, _ in layout(c))
 
@@ -176,9 +185,11 @@ def _np_ptr(a: np.ndarray):
 
 class Model:
     """One byte Transformer resident on the GPU with its optimizer state
-    (AdamW, or SGD with the optional parameter VJP)."""
+    (AdamW, or SGD with the optional parameter VJP).  values > 0 puts the
+    NativeValue head on the body (sejong_amd.value; parameters in
+    NativeValue::parameters order, batches through set_value_batch)."""
 
-    def __init__(self, mc: ModelConfig, tc: TrainConfig, stream: int | None = None):
+    def __init__(self, mc: ModelConfig, tc: TrainConfig, stream: int | None = None, values: int = 0):
         mc.validate()
         tc.validate()
         if tc.sequence > mc.context:
@@ -189,22 +200,29 @@ class Model:
                             norm_epsilon=mc.norm_epsilon, rope_theta=mc.rope_theta,
                             precision=N.SJ_BF16 if mc.precision == "bf16" else N.SJ_F32)
         handle = ctypes.c_void_p()
+        sgd = adam = None
         if tc.optimizer == "sgd":
             pv = tc.parameter_vjp
             sgd = N.SgdConfig(weight_decay=tc.weight_decay, clip_norm=tc.clip_norm, loss_scale=tc.loss_scale,
                               clip_enabled=int(tc.clip_enabled), vjp_rank=pv.rank if pv else 0,
                               vjp_residual_fraction=pv.residual_fraction if pv else 0.0,
                               vjp_block_rows=pv.block_rows if pv else 0, vjp_seed=pv.seed if pv else 0)
-            N.api.sj_model_create_sgd(ctypes.byref(cfg), ctypes.byref(sgd), ctypes.c_void_p(stream or 0),
-                                      ctypes.byref(handle))
         else:
             adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
                                 clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
-            N.api.sj_model_create(ctypes.byref(cfg), ctypes.byref(adam), ctypes.c_void_p(stream or 0),
-                                  ctypes.byref(handle))
+        s = ctypes.c_void_p(stream or 0)
+        if values:
+            N.api.sj_model_create_value(ctypes.byref(cfg), values, ctypes.byref(adam) if adam else None,
+                                        ctypes.byref(sgd) if sgd else None, s, ctypes.byref(handle))
+        elif sgd is not None:
+            N.api.sj_model_create_sgd(ctypes.byref(cfg), ctypes.byref(sgd), s, ctypes.byref(handle))
+        else:
+            N.api.sj_model_create(ctypes.byref(cfg), ctypes.byref(adam), s, ctypes.byref(handle))
         self.h = handle
+        self.values = values
         self.count = N.load().sj_model_param_count(self.h)
-        assert self.count == param_count(mc), (self.count, param_count(mc))
+        expect = param_count(mc) if not values else sum(math.prod(sh) for _, sh, _ in value_layout(mc, values))
+        assert self.count == expect, (self.count, expect)
 
     def close(self):
         if self.h:
@@ -264,6 +282,12 @@ class Model:
         ids = np.ascontiguousarray(ids, dtype=np.int32); tg = np.ascontiguousarray(targets, dtype=np.int32)
         assert ids.size == self.tc.batch * self.tc.sequence == tg.size
         N.api.sj_model_set_batch(self.h, _np_ptr(ids), _np_ptr(tg), 0)
+
+    def set_value_batch(self, ids: np.ndarray, positions: np.ndarray, labels: np.ndarray):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32); lab = np.ascontiguousarray(labels, dtype=np.int32)
+        assert ids.size == self.tc.batch * self.tc.sequence and pos.size == lab.size == self.tc.batch
+        N.api.sj_model_set_value_batch(self.h, _np_ptr(ids), _np_ptr(pos), _np_ptr(lab))
 
     def set_batch_device(self, ids_ptr: int, targets_ptr: int):
         N.api.sj_model_set_batch(self.h, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(targets_ptr), 1)

@@ -596,3 +596,26 @@ def test_patch_maps_adjoints(T, P):
     lhs = np.sum(OH.patch_broadcast(z, bos, B, T, P) * dy)
     rhs = np.sum(z * dx) + np.sum(bos * dbos)
     assert abs(lhs - rhs) < 1e-5 * (1 + abs(lhs))
+
+
+def test_model_backward_hidden_matches_lm_head():
+    """The body backward from a given final-norm gradient reproduces the
+    FD-pinned full backward when fed the LM head's own dh, with the
+    embedding gradient formed from the returned embedding-output gradient."""
+    cfg = dict(TINY)
+    p, ids, tg = _tiny_inputs(cfg, seed=6)
+    acts = O.model_forward(cfg, p, ids, dtype="none")
+    loss, g, _ = O.model_backward(cfg, p, acts, ids, tg, dtype="none")
+    d, M, V = cfg["d"], cfg["T"] * cfg["B"], O.VOCAB
+    A, off = {}, 0
+    for name, layer, size in O.acts_layout(cfg):
+        A[(name, layer)] = acts[off:off + size]
+        off += size
+    logits = A[("logits", -1)].reshape(M, V)
+    _, dlog = O.cross_entropy(logits, tg, float(np.float32(1.0) / np.float32(M)))  # the f32 seed
+    wout = p[-d * V:].reshape(d, V)
+    dh = dlog @ wout.T
+    gh, demb = O.model_backward_hidden(cfg, p, acts, dh, dtype="none")
+    n = g.size
+    np.testing.assert_allclose(gh[V * d:n - d * V], g[V * d:n - d * V], rtol=1e-10, atol=1e-15)
+    np.testing.assert_allclose(O.embedding_bwd(demb, ids, V).ravel(), g[:V * d], rtol=1e-10, atol=1e-15)
