@@ -168,121 +168,183 @@ __device__ __forceinline__ void store_planes(bf16_t* const* pn, bf16_t* const* p
   }
 }
 
+// two floats -> packed bf16 pair (RNE, one v_cvt_pk_bf16_f32)
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){a, b}, bf16x2v));
+}
+// hi/lo split of 8 floats with packed conversions: hi = RNE(x), lo = RNE(x - hi)
+__device__ __forceinline__ void split8p(const float* v, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t hp = cvt2(v[2 * i], v[2 * i + 1]);
+    h[i] = hp;
+    l[i] = cvt2(v[2 * i] - __uint_as_float(hp << 16), v[2 * i + 1] - __uint_as_float(hp & 0xffff0000u));
+  }
+  hi = as_bf8(h);
+  lo = as_bf8(l);
+}
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ------------------------------------------------------------------ forward
+// Lane (j, g) of wave w owns query q = 64*qb + 16w + j.  S^T = K Q^T puts
+// the scores of keys 16sb + 4g + r of that query in the lane (raw dot
+// products; the scale folds into the exp2 argument), so the online-softmax
+// statistics are per lane after two cross-row shuffles, and O^T = V^T P^T
+// (A = V^T rows in the permuted key order of the lane's k-slots, B = the
+// lane's own P as hi/lo) leaves O^T[dims 16d + 4g + r][q] in the same lane:
+// the rescale and the final normalisation need no shuffles.  Masks are
+// applied on the diagonal block only (and past T when T is ragged).
+template <bool FULLT>
 __global__ __launch_bounds__(256) void k_attn_fwd(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t sK[QB * LS];
   __shared__ __attribute__((aligned(16))) bf16_t sVt[DH * LS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, j = lane & 15;
-  const long qb = (long)gridDim.x - 1 - blockIdx.x;  // longest blocks first
-  const long h = blockIdx.y, b = blockIdx.z;
-  const long kvh = h / (a.HQ / a.HK);
-  const long T = a.T;
-  const long qrow0 = qb * QB + wave * 16;  // first query (position) of this wave
-  const long myq = qrow0 + j;              // query whose stats this lane holds
-  const float sc = 0.125f * LOG2E;         // DH^-1/2 * log2(e)
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int kvh = h / (int)(a.HQ / a.HK);
+  const int T = (int)a.T;
+  const int qloc = wave * 16 + j;
+  const int myq = qb * QB + qloc;
+  const float sc = 0.125f * LOG2E;  // DH^-1/2 * log2(e)
+  const int ldk = (int)a.ldk, ldv = (int)a.ldv;
 
   bf16x8 qf[2];
+  {
+    const bf16_t* qrow = a.q + ((size_t)b * T + myq) * a.ldq + h * DH;
 #pragma unroll
-  for (int c = 0; c < 2; c++) {
-    u32x4 v = u32x4{0, 0, 0, 0};
-    if (myq < T) v = *(const u32x4*)(a.q + (b * T + myq) * a.ldq + h * DH + 32 * c + 8 * g);
-    qf[c] = as_bf8(v);
+    for (int c = 0; c < 2; c++)
+      qf[c] = as_bf8((FULLT || myq < T) ? *(const u32x4*)(qrow + 32 * c + 8 * g) : u32x4{0, 0, 0, 0});
   }
   f32x4 o[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float mrow = -INFINITY, lrow = 0.f;
+  float m = -INFINITY, l = 0.f;  // running max (scaled, log2 units) and sum of this lane's query
 
-  const bf16_t* kbase = a.k + b * T * a.ldk + kvh * DH;
-  const bf16_t* vbase = a.v + b * T * a.ldv + kvh * DH;
-  for (long kb = 0; kb <= qb; kb++) {
+  const bf16_t* kbase = a.k + (size_t)b * T * a.ldk + kvh * DH;
+  const bf16_t* vbase = a.v + (size_t)b * T * a.ldv + kvh * DH;
+  // the next key block is fetched into registers while this one computes:
+  // K as 16-byte row chunks, V as the 8-row x 2-column pieces of its
+  // transposed LDS tile (two 16-byte LDS runs per piece)
+  u32x4 pk[2];
+  uint32_t pv[8];
+  const int vrg = threadIdx.x >> 5, vcp = threadIdx.x & 31;
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      const int row = kb * QB + r;
+      pk[p] = (FULLT || row < T) ? *(const u32x4*)(kbase + row * ldk + c8) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int row = kb * QB + vrg * 8 + i;
+      pv[i] = (FULLT || row < T) ? *(const uint32_t*)(vbase + row * ldv + 2 * vcp) : 0u;
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
+      *(u32x4*)(sK + r * LS + c8) = pk[p];
+    }
+    bf16_t* d0 = sVt + (2 * vcp) * LS + vrg * 8;
+    *(u32x4*)d0 = u32x4{(pv[0] & 0xffffu) | (pv[1] << 16), (pv[2] & 0xffffu) | (pv[3] << 16),
+                        (pv[4] & 0xffffu) | (pv[5] << 16), (pv[6] & 0xffffu) | (pv[7] << 16)};
+    *(u32x4*)(d0 + LS) = u32x4{(pv[0] >> 16) | (pv[1] & 0xffff0000u), (pv[2] >> 16) | (pv[3] & 0xffff0000u),
+                               (pv[4] >> 16) | (pv[5] & 0xffff0000u), (pv[6] >> 16) | (pv[7] & 0xffff0000u)};
+  };
+  fetch(0);
+  for (int kb = 0; kb <= qb; kb++) {
     __syncthreads();
-    stage_bf16(sK, kbase, a.ldk, kb * QB, T, 0);
-    stage_bf16_t(sVt, vbase, a.ldv, kb * QB, T, 0);
+    commit();
     __syncthreads();
-    float s[4][4];
+    if (kb < qb) fetch(kb + 1);
+    f32x4 st[4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++) {
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      st[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < 2; c++) acc = mfma(as_bf8(*(const u32x4*)(sK + (sb * 16 + j) * LS + 32 * c + 8 * g)), qf[c], acc);
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        long key = kb * QB + sb * 16 + 4 * g + r;
-        s[sb][r] = (key <= myq && key < T) ? acc[r] * sc : -INFINITY;
-      }
+      for (int c = 0; c < 2; c++)
+        st[sb] = mfma(as_bf8(*(const u32x4*)(sK + (sb * 16 + j) * LS + 32 * c + 8 * g)), qf[c], st[sb]);
     }
-    float bm = -INFINITY;
+    if (kb == qb) {  // causal mask inside the diagonal block
 #pragma unroll
-    for (int sb = 0; sb < 4; sb++)
+      for (int sb = 0; sb < 4; sb++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) bm = fmaxf(bm, s[sb][r]);
+        for (int r = 0; r < 4; r++)
+          if (sb * 16 + 4 * g + r > qloc) st[sb][r] = -INFINITY;
+    }
+    if (!FULLT && (kb + 1) * QB > T) {
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (kb * QB + sb * 16 + 4 * g + r >= T) st[sb][r] = -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
+                     fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
+    bm = fmaxf(bm, fmaxf(fmaxf(fmaxf(st[2][0], st[2][1]), fmaxf(st[2][2], st[2][3])),
+                         fmaxf(fmaxf(st[3][0], st[3][1]), fmaxf(st[3][2], st[3][3]))));
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float mnew = fmaxf(mrow, bm);
-    const float alpha = exp2f(mrow - mnew);  // 0 on the first block
+    const float mnew = fmaxf(m, bm * sc);  // finite: key 0 is visible to every query
+    const float alpha = fexp2(m - mnew);   // 0 on the first block
     float ps = 0.f;
+    float pr[4][4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        s[sb][r] = exp2f(s[sb][r] - mnew);
-        ps += s[sb][r];
+        pr[sb][r] = fexp2(fmaf(st[sb][r], sc, -mnew));
+        ps += pr[sb][r];
       }
     ps += __shfl_xor(ps, 16, 64);
     ps += __shfl_xor(ps, 32, 64);
-    lrow = lrow * alpha + ps;
-    mrow = mnew;
-    // rescale O rows (queries 4g + r) by their alpha
+    l = fmaf(l, alpha, ps);
+    m = mnew;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      float al = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-      for (int d = 0; d < 4; d++) o[d][r] *= al;
-    }
+    for (int d = 0; d < 4; d++) o[d] *= alpha;
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      float pv[8] = {s[2 * c][0], s[2 * c][1], s[2 * c][2], s[2 * c][3],
-                     s[2 * c + 1][0], s[2 * c + 1][1], s[2 * c + 1][2], s[2 * c + 1][3]};
+      const float p8[8] = {pr[2 * c][0], pr[2 * c][1], pr[2 * c][2], pr[2 * c][3],
+                           pr[2 * c + 1][0], pr[2 * c + 1][1], pr[2 * c + 1][2], pr[2 * c + 1][3]};
       bf16x8 ph, pl;
-      split8(pv, ph, pl);
+      split8p(p8, ph, pl);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        bf16x8 vf = ld_perm(sVt + (16 * d + j) * LS, 32 * c + 4 * g, 32 * c + 16 + 4 * g);
-        o[d] = mfma(ph, vf, o[d]);
-        o[d] = mfma(pl, vf, o[d]);
+        const bf16x8 vf = ld_perm(sVt + (16 * d + j) * LS, 32 * c + 4 * g, 32 * c + 16 + 4 * g);
+        o[d] = mfma(vf, ph, o[d]);
+        o[d] = mfma(vf, pl, o[d]);
       }
     }
   }
-  // normalise and store (and O^T: this lane's 4 consecutive queries)
-  float on[4][4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    float l = __shfl(lrow, 4 * g + r, 64);
-    long qpos = qrow0 + 4 * g + r;
-#pragma unroll
-    for (int d = 0; d < 4; d++) on[d][r] = o[d][r] / l;
-    if (qpos < T) {
-      bf16_t* orow = a.out + (b * T + qpos) * a.ldo + h * DH;
-#pragma unroll
-      for (int d = 0; d < 4; d++) orow[16 * d + j] = f2bf(on[d][r]);
-    }
-  }
-  if (a.ot) {
-    const long q0 = qrow0 + 4 * g;
+  // O[q][16d + 4g + r] = o[d][r] / l: 4 consecutive dims per store; O^T rows
+  if (FULLT || myq < T) {
+    const float il = 1.f / l;
+    bf16_t* orow = a.out + ((size_t)b * T + myq) * a.ldo + h * DH;
 #pragma unroll
     for (int d = 0; d < 4; d++) {
-      bf16_t* dst = a.ot + (h * DH + 16 * d + j) * a.ldot + b * T + q0;
-      if (q0 + 4 <= T) {
-        *(u32x2*)dst = u32x2{pack2(f2bf(on[d][0]), f2bf(on[d][1])), pack2(f2bf(on[d][2]), f2bf(on[d][3]))};
-      } else {
-        for (int r = 0; r < 4; r++)
-          if (q0 + r < T) dst[r] = f2bf(on[d][r]);
+      const float v0 = o[d][0] * il, v1 = o[d][1] * il, v2 = o[d][2] * il, v3 = o[d][3] * il;
+      *(u32x2*)(orow + 16 * d + 4 * g) = u32x2{cvt2(v0, v1), cvt2(v2, v3)};
+      if (a.ot) {
+        bf16_t* dst = a.ot + (size_t)(h * DH + 16 * d + 4 * g) * a.ldot + (size_t)b * T + myq;
+        dst[0] = f2bf(v0);
+        dst[a.ldot] = f2bf(v1);
+        dst[2 * a.ldot] = f2bf(v2);
+        dst[3 * a.ldot] = f2bf(v3);
       }
     }
+    if (g == 0) a.lse[((size_t)b * T + myq) * a.HQ + h] = (m + log2f(l)) * LN2;
   }
-  if (g == 0 && myq < T) a.lse[(b * T + myq) * a.HQ + h] = (mrow + log2f(lrow)) * LN2;
+}
+
+template <typename K>
+void launch_attn(K kernel_full, K kernel_ragged, hipStream_t s, const AttnArgs& a, dim3 grid) {
+  hipLaunchKernelGGL((a.T % QB == 0) ? kernel_full : kernel_ragged, grid, dim3(256), 0, s, a);
 }
 
 // ------------------------------------------------------------- backward dQ
@@ -342,7 +404,11 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
   const bf16_t* kbase = a.k + b * T * a.ldk + kvh * DH;
   const bf16_t* vbase = a.v + b * T * a.ldv + kvh * DH;
   // the next key block is fetched into registers while this one computes
+  // (K, V as 16-byte row chunks; K again as the 8-row x 2-column pieces of
+  // the transposed tile, written to LDS as two 16-byte runs)
   u32x4 pk[2], pv[2];
+  uint32_t pkt[8];
+  const int trg = threadIdx.x >> 5, tcp = threadIdx.x & 31;
   auto fetch = [&](long kb) {
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -354,6 +420,11 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
         pv[p] = *(const u32x4*)(vbase + row * a.ldv + c8);
       }
     }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const long row = kb * QB + trg * 8 + i;
+      pkt[i] = row < T ? *(const uint32_t*)(kbase + row * a.ldk + 2 * tcp) : 0u;
+    }
   };
   auto commit = [&]() {
 #pragma unroll
@@ -361,12 +432,12 @@ __global__ __launch_bounds__(256) void k_attn_dq(AttnArgs a) {
       const int ch = threadIdx.x + p * 256, r = ch >> 3, c8 = (ch & 7) * 8;
       *(u32x4*)(sK + r * LS + c8) = pk[p];
       *(u32x4*)(sV + r * LS + c8) = pv[p];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        sKt[(c8 + 2 * i) * LS + r] = (bf16_t)(pk[p][i] & 0xffffu);
-        sKt[(c8 + 2 * i + 1) * LS + r] = (bf16_t)(pk[p][i] >> 16);
-      }
     }
+    bf16_t* d0 = sKt + (2 * tcp) * LS + trg * 8;
+    *(u32x4*)d0 = u32x4{(pkt[0] & 0xffffu) | (pkt[1] << 16), (pkt[2] & 0xffffu) | (pkt[3] << 16),
+                        (pkt[4] & 0xffffu) | (pkt[5] << 16), (pkt[6] & 0xffffu) | (pkt[7] << 16)};
+    *(u32x4*)(d0 + LS) = u32x4{(pkt[0] >> 16) | (pkt[1] & 0xffff0000u), (pkt[2] >> 16) | (pkt[3] & 0xffff0000u),
+                               (pkt[4] >> 16) | (pkt[5] & 0xffff0000u), (pkt[6] >> 16) | (pkt[7] & 0xffff0000u)};
   };
   fetch(0);
   for (long kb = 0; kb <= qb; kb++) {
@@ -602,9 +673,15 @@ __global__ __launch_bounds__(256) void k_attn_dkv_h(AttnArgs a, float* __restric
 
   const bf16_t* qbase = a.q + b * T * a.ldq + h * DH;
   const float* dbase = a.dout + b * T * a.lddo + h * DH;
+  // next query block in registers: Q and dO as row chunks, and again as the
+  // 8-row x 2-column pieces of their transposed LDS tiles (two 16-byte runs
+  // per piece instead of scattered 2-byte stores)
   u32x4 pq[2];
   float4 pd[2][2];
+  uint32_t pqt[8];
+  float2 pdt[8];
   float pl = 0.f, pdl = 0.f;
+  const int trg = threadIdx.x >> 5, tcp = threadIdx.x & 31;
   auto fetch = [&](long qb) {
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -616,6 +693,16 @@ __global__ __launch_bounds__(256) void k_attn_dkv_h(AttnArgs a, float* __restric
         pq[p] = *(const u32x4*)(qbase + row * a.ldq + c8);
         pd[p][0] = *(const float4*)(dbase + row * a.lddo + c8);
         pd[p][1] = *(const float4*)(dbase + row * a.lddo + c8 + 4);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const long row = qb * QB + trg * 8 + i;
+      pqt[i] = 0u;
+      pdt[i] = make_float2(0.f, 0.f);
+      if (row < T) {
+        pqt[i] = *(const uint32_t*)(qbase + row * a.ldq + 2 * tcp);
+        pdt[i] = *(const float2*)(dbase + row * a.lddo + 2 * tcp);
       }
     }
     if (threadIdx.x < QB) {
@@ -635,17 +722,24 @@ __global__ __launch_bounds__(256) void k_attn_dkv_h(AttnArgs a, float* __restric
       for (int i = 0; i < 8; i++) split_bf(v8[i], hh[i], ll[i]);
       *(u32x4*)(sDh + r * LS + c8) = u32x4{pack2(hh[0], hh[1]), pack2(hh[2], hh[3]), pack2(hh[4], hh[5]), pack2(hh[6], hh[7])};
       *(u32x4*)(sDl + r * LS + c8) = u32x4{pack2(ll[0], ll[1]), pack2(ll[2], ll[3]), pack2(ll[4], ll[5]), pack2(ll[6], ll[7])};
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        sQt[(c8 + 2 * i) * LS + r] = (bf16_t)(pq[p][i] & 0xffffu);
-        sQt[(c8 + 2 * i + 1) * LS + r] = (bf16_t)(pq[p][i] >> 16);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        sDth[(c8 + i) * LS + r] = hh[i];
-        sDtl[(c8 + i) * LS + r] = ll[i];
-      }
     }
+    bf16_t* d0 = sQt + (2 * tcp) * LS + trg * 8;
+    *(u32x4*)d0 = u32x4{(pqt[0] & 0xffffu) | (pqt[1] << 16), (pqt[2] & 0xffffu) | (pqt[3] << 16),
+                        (pqt[4] & 0xffffu) | (pqt[5] << 16), (pqt[6] & 0xffffu) | (pqt[7] << 16)};
+    *(u32x4*)(d0 + LS) = u32x4{(pqt[0] >> 16) | (pqt[1] & 0xffff0000u), (pqt[2] >> 16) | (pqt[3] & 0xffff0000u),
+                               (pqt[4] >> 16) | (pqt[5] & 0xffff0000u), (pqt[6] >> 16) | (pqt[7] & 0xffff0000u)};
+    bf16_t h0[8], l0[8], h1[8], l1[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      split_bf(pdt[i].x, h0[i], l0[i]);
+      split_bf(pdt[i].y, h1[i], l1[i]);
+    }
+    bf16_t* e = sDth + (2 * tcp) * LS + trg * 8;
+    *(u32x4*)e = u32x4{pack2(h0[0], h0[1]), pack2(h0[2], h0[3]), pack2(h0[4], h0[5]), pack2(h0[6], h0[7])};
+    *(u32x4*)(e + LS) = u32x4{pack2(h1[0], h1[1]), pack2(h1[2], h1[3]), pack2(h1[4], h1[5]), pack2(h1[6], h1[7])};
+    e = sDtl + (2 * tcp) * LS + trg * 8;
+    *(u32x4*)e = u32x4{pack2(l0[0], l0[1]), pack2(l0[2], l0[3]), pack2(l0[4], l0[5]), pack2(l0[6], l0[7])};
+    *(u32x4*)(e + LS) = u32x4{pack2(l1[0], l1[1]), pack2(l1[2], l1[3]), pack2(l1[4], l1[5]), pack2(l1[6], l1[7])};
     if (threadIdx.x < QB) {
       sL[threadIdx.x] = pl;
       sD[threadIdx.x] = pdl;
@@ -956,6 +1050,11 @@ bool use_mfma(int dtype, long head_dim, long window, long t, long ldq, long ldk,
   if (dtype != SJ_BF16 || head_dim != DH) return false;
   if (window > 0 && window < t) return false;
   if ((ldq | ldk | ldv | ldo) % 8) return false;
+  // in-sequence offsets (row * leading dimension) are 32-bit in the kernels
+  long ld = ldq > ldk ? ldq : ldk;
+  ld = ld > ldv ? ld : ldv;
+  ld = ld > ldo ? ld : ldo;
+  if (t * ld >= (1L << 31)) return false;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16) return false;
   return true;
 }
@@ -977,8 +1076,8 @@ extern "C" int sj_attention_fwd(void* stream, const void* q, long ldq, const voi
     a.q = (const bf16_t*)q; a.k = (const bf16_t*)k; a.v = (const bf16_t*)v;
     a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
     a.out = (bf16_t*)o; a.lse = lse; a.T = t; a.HQ = hq; a.HK = hk;
-    hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch), dim3(256), 0, s,
-                       a);
+    launch_attn(k_attn_fwd<true>, k_attn_fwd<false>, s, a,
+                dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch));
   } else {
     RowArgs a = {};
     a.q = q; a.k = k; a.v = v; a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
@@ -1048,8 +1147,8 @@ extern "C" int sj_attention_fwd_t(void* stream, const uint16_t* q, long ldq, con
   a.ldq = ldq; a.ldk = ldk; a.ldv = ldv; a.ldo = ldo;
   a.out = (bf16_t*)o; a.lse = lse; a.T = t; a.HQ = hq; a.HK = hk;
   a.ot = (bf16_t*)o_t; a.ldot = ldot;
-  hipLaunchKernelGGL(k_attn_fwd, dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  launch_attn(k_attn_fwd<true>, k_attn_fwd<false>, (hipStream_t)stream, a,
+              dim3((unsigned)((t + QB - 1) / QB), (unsigned)hq, (unsigned)batch));
   SJ_LAUNCH_CHECK("hierarchy_attention_t");
   return SJ_OK;
 }
@@ -1114,4 +1213,14 @@ extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, con
   return sjh::attention_bwd_p_parts(7, stream, q, ldq, k, ldk, v, ldv, o, ldo, lse, dout, lddo, delta, batch, t, hq,
                                     hk, head_dim, rope_table, g_hi, g_lo, ldg, gt_hi, gt_lo, ldgt, workspace,
                                     workspace_bytes);
+}
+
+int sjh::attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
+                             const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi,
+                             uint16_t* gt_lo, long ldgt) {
+  hipLaunchKernelGGL(k_attn_kv_reduce, dim3((unsigned)((M + 2 * KVR_ROWS - 1) / (2 * KVR_ROWS))), dim3(256), 0, s, part,
+                     (int)group, M, T, N, KV, rope, (bf16_t*)g_hi, (bf16_t*)g_lo, ldg, (bf16_t*)gt_hi, (bf16_t*)gt_lo,
+                     ldgt);
+  SJ_LAUNCH_CHECK("hierarchy_attention_kv_reduce");
+  return SJ_OK;
 }

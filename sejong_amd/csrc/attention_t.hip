@@ -1,0 +1,606 @@
+// GQA causal attention for the MFMA-layout step (bf16 storage, head_dim 64,
+// T a multiple of 64), forward and backward, fed by producers that already
+// wrote every operand in the orientation the MFMA wants:
+//   q|k|v [M][NQKV] and its transpose qkv_t [NQKV][ldt] (the QKV projection
+//   writes both, RoPE applied), dO as hi/lo planes [M][NQ] and transposed
+//   [NQ][ldt] (the attention-output projection's dX writes both), LSE and
+//   Delta transposed [HQ][ldt].
+// So no kernel transposes or splits a tile: every 64 x 64 tile streams
+// global -> LDS with global_load_lds_dwordx4, three stages deep, XOR-
+// swizzled (chunk c of row r at c ^ (r & 7)), and MFMA fragments are single
+// 16-byte LDS reads.
+//
+// Layout trick: the rows of each 16-row block of S are read in a permuted
+// key (or query) order, row i of block sb = 32(sb/2) + 8(i/4) + 4(sb%2) +
+// i%4, so the 8 k-slots a lane contributes to the following P-product are 8
+// consecutive keys -- one 16-byte chunk of the transposed tile.
+//
+// Forward (hierarchy.py:7-39): lane (j, g) of wave w owns query 64qb + 16w
+// + j; S^T = K Q^T, online softmax per lane (two cross-row shuffles), O^T =
+// V^T P^T with P as hi/lo.  Backward (hierarchy.py:42-104): dQ^T = K^T dS^T
+// per query block (writes Delta), then per (key block, query head) dK^T =
+// Q^T dS and dV^T = dO^T P into fp32 per-head partials that the group
+// reduce of attention.hip sums in a fixed order (no atomics).
+#include <math.h>
+
+#include "common.h"
+
+using namespace sj;
+
+namespace {
+
+constexpr int DH = 64;
+constexpr int QB = 64;
+constexpr int NST = 3;             // pipeline stages
+constexpr int TILE = 64 * 64;      // bf16 elements per tile
+constexpr int TBYTES = TILE * 2;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+__device__ __attribute__((aligned(64))) uint8_t g_zero_t[64];  // zero source for masked DMA lanes
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// LDS-DMA of one 16-byte chunk per lane to lds_addr + 16 * lane
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// chunk `ch` (8 bf16) of row `row` of a swizzled tile
+__device__ __forceinline__ bf16x8 tf(const bf16_t* tile, int row, int ch) {
+  return as_bf8(*(const u32x4*)(tile + row * 64 + ((ch ^ (row & 7)) << 3)));
+}
+// permuted row of block sb read by A-operand lane j (see the file comment)
+__device__ __forceinline__ int prow(int sb, int j) { return 32 * (sb >> 1) + 8 * (j >> 2) + 4 * (sb & 1) + (j & 3); }
+
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){a, b}, bf16x2v));
+}
+__device__ __forceinline__ void split8p(const float* v, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t hp = cvt2(v[2 * i], v[2 * i + 1]);
+    h[i] = hp;
+    l[i] = cvt2(v[2 * i] - __uint_as_float(hp << 16), v[2 * i + 1] - __uint_as_float(hp & 0xffff0000u));
+  }
+  hi = as_bf8(h);
+  lo = as_bf8(l);
+}
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float bflo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+struct TArgs {
+  const bf16_t* qkv;  // [M][ldqkv]: q (HQ*64) | k (HK*64) | v (HK*64), q and k after RoPE
+  long ldqkv;
+  const bf16_t* qkvt;  // [NQKV][ldt]
+  long ldt;
+  int T, HQ, HK;
+  // forward
+  bf16_t* o;  // [M][ldo]
+  long ldo;
+  float* lse;    // [M][HQ] (reference layout, nullable)
+  float* lse_t;  // [HQ][ldt]
+  bf16_t* ot;    // O^T [HQ*64][ldot] (nullable)
+  long ldot;
+  // backward
+  const bf16_t* ob;  // O (for Delta)
+  const bf16_t *dh, *dl;  // dO planes [M][lddo]
+  long lddo;
+  const bf16_t *dth, *dtl;  // dO^T planes [HQ*64][lddot]
+  long lddot;
+  const float* lse_in_t;  // [HQ][ldt]
+  float* delta_t;         // [HQ][ldt]
+  const float* rope;      // inverse-RoPE table (cos, sin) [T][32] or null
+  bf16_t *gq[2], *gqt[2];  // dQ planes: normal [M][ldg] at columns h*64, transposed [.][ldgt] at rows h*64
+  long ldg, ldgt;
+  float* part;  // [group][M][2*HK*64] per-head dK | dV
+};
+
+// DMA of one 64 x 64 bf16 tile (rows r of `src` with stride ld, 8 chunks of
+// 16 bytes each): wave w moves rows 16w .. 16w+15 (two instructions).
+// valid(r) false -> zeros.
+template <typename Valid>
+__device__ __forceinline__ void dma_tile(const bf16_t* src, long ld, uint32_t lds_tile, int wave, int lane,
+                                         Valid valid) {
+  const int rl = lane >> 3, ch = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int r0 = wave * 16 + 8 * k;
+    const int r = r0 + rl;
+    const void* s = valid(r) ? (const void*)(src + r * ld + ch * 8) : (const void*)g_zero_t;
+    dma16(s, lds_tile + (uint32_t)(r0 * 128));
+  }
+}
+
+// ------------------------------------------------------------------ forward
+__global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [K | V^T]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int g = lane >> 4, j = lane & 15;
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qloc = wave * 16 + j, myq = qb * QB + qloc;
+  const long row0 = (long)b * T;
+  const float sc = 0.125f * LOG2E;
+
+  bf16x8 qf[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) qf[c] = as_bf8(*(const u32x4*)(a.qkv + (row0 + myq) * a.ldqkv + h * DH + 32 * c + 8 * g));
+
+  const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
+  const bf16_t* vtsrc = a.qkvt + (long)(NQ + NK + kvh * DH) * a.ldt + row0;
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  auto issue = [&](int kb, int buf) {
+    const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
+    dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
+    dma_tile(vtsrc + kb * QB, a.ldt, st + TBYTES, wave_s, lane, [](int) { return true; });
+  };
+  f32x4 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  wait_vm<0>();  // the fragments above are in registers before the DMA stream starts
+
+#pragma unroll
+  for (int s = 0; s < NST - 1; s++)
+    if (s <= qb) issue(s, s);
+  for (int kb = 0; kb <= qb; kb++) {
+    if (kb < qb) wait_vm<4>(); else wait_vm<0>();
+    block_barrier();
+    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (kb + NST - 1) % NST);
+    const bf16_t* sK = lds + (kb % NST) * 2 * TILE;
+    const bf16_t* sVt = sK + TILE;
+    f32x4 st[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      st[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int kr = prow(sb, j);
+#pragma unroll
+      for (int c = 0; c < 2; c++) st[sb] = mfma(tf(sK, kr, 4 * c + g), qf[c], st[sb]);
+    }
+    if (kb == qb) {  // causal mask inside the diagonal block: key 32c + 8g + 4s + r
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r > qloc) st[sb][r] = -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
+                     fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
+    bm = fmaxf(bm, fmaxf(fmaxf(fmaxf(st[2][0], st[2][1]), fmaxf(st[2][2], st[2][3])),
+                         fmaxf(fmaxf(st[3][0], st[3][1]), fmaxf(st[3][2], st[3][3]))));
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float mnew = fmaxf(m, bm * sc);
+    const float alpha = fexp2(m - mnew);
+    float pr[4][4], ps = 0.f;
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        pr[sb][r] = fexp2(fmaf(st[sb][r], sc, -mnew));
+        ps += pr[sb][r];
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = fmaf(l, alpha, ps);
+    m = mnew;
+#pragma unroll
+    for (int d = 0; d < 4; d++) o[d] *= alpha;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float p8[8] = {pr[2 * c][0], pr[2 * c][1], pr[2 * c][2], pr[2 * c][3],
+                           pr[2 * c + 1][0], pr[2 * c + 1][1], pr[2 * c + 1][2], pr[2 * c + 1][3]};
+      bf16x8 ph, pl;
+      split8p(p8, ph, pl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const bf16x8 vf = tf(sVt, 16 * d + j, 4 * c + g);
+        o[d] = mfma(vf, ph, o[d]);
+        o[d] = mfma(vf, pl, o[d]);
+      }
+    }
+  }
+  const float il = 1.f / l;
+  bf16_t* orow = a.o + (row0 + myq) * a.ldo + h * DH;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    const float v0 = o[d][0] * il, v1 = o[d][1] * il, v2 = o[d][2] * il, v3 = o[d][3] * il;
+    *(u32x2*)(orow + 16 * d + 4 * g) = u32x2{cvt2(v0, v1), cvt2(v2, v3)};
+    if (a.ot) {
+      bf16_t* dst = a.ot + (long)(h * DH + 16 * d + 4 * g) * a.ldot + row0 + myq;
+      const uint32_t w01 = cvt2(v0, v1), w23 = cvt2(v2, v3);
+      dst[0] = (bf16_t)(w01 & 0xffffu);
+      dst[a.ldot] = (bf16_t)(w01 >> 16);
+      dst[2 * a.ldot] = (bf16_t)(w23 & 0xffffu);
+      dst[3 * a.ldot] = (bf16_t)(w23 >> 16);
+    }
+  }
+  if (g == 0) {
+    const float lse = (m + log2f(l)) * LN2;
+    if (a.lse) a.lse[(row0 + myq) * a.HQ + h] = lse;
+    a.lse_t[(long)h * a.ldt + row0 + myq] = lse;
+  }
+}
+
+// ------------------------------------------------------------- backward dQ
+__global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [K | V | K^T]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int g = lane >> 4, j = lane & 15;
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, NQ = a.HQ * DH;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qloc = wave * 16 + j, myq = qb * QB + qloc;
+  const long row0 = (long)b * T, qrow = row0 + myq;
+  const float sc = 0.125f * LOG2E;
+
+  // this lane's query: Q, dO (hi, lo) fragments; Delta = sum dO * O
+  bf16x8 qf[2], dhf[2], dlf[2];
+  float dpart = 0.f;
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const int col = h * DH + 32 * c + 8 * g;
+    qf[c] = as_bf8(*(const u32x4*)(a.qkv + qrow * a.ldqkv + col));
+    const u32x4 hv = *(const u32x4*)(a.dh + qrow * a.lddo + col);
+    const u32x4 lv = *(const u32x4*)(a.dl + qrow * a.lddo + col);
+    const u32x4 ov = *(const u32x4*)(a.ob + qrow * a.ldo + col);
+    dhf[c] = as_bf8(hv);
+    dlf[c] = as_bf8(lv);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      dpart += (bflo(hv[i]) + bflo(lv[i])) * bflo(ov[i]);
+      dpart += (bfhi(hv[i]) + bfhi(lv[i])) * bfhi(ov[i]);
+    }
+  }
+  dpart += __shfl_xor(dpart, 16, 64);
+  dpart += __shfl_xor(dpart, 32, 64);
+  const float delta = dpart;
+  const float lse2 = a.lse_in_t[(long)h * a.ldt + qrow] * LOG2E;
+  if (g == 0) a.delta_t[(long)h * a.ldt + qrow] = delta;
+
+  const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
+  const bf16_t* vsrc = ksrc + a.HK * DH;
+  const bf16_t* ktsrc = a.qkvt + (long)(NQ + kvh * DH) * a.ldt + row0;
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  auto issue = [&](int kb, int buf) {
+    const uint32_t st = base + (uint32_t)(buf * 3 * TBYTES);
+    dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
+    dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(ktsrc + kb * QB, a.ldt, st + 2 * TBYTES, wave_s, lane, [](int) { return true; });
+  };
+  f32x4 dq[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  wait_vm<0>();
+#pragma unroll
+  for (int s = 0; s < NST - 1; s++)
+    if (s <= qb) issue(s, s);
+  for (int kb = 0; kb <= qb; kb++) {
+    if (kb < qb) wait_vm<6>(); else wait_vm<0>();
+    block_barrier();
+    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (kb + NST - 1) % NST);
+    const bf16_t* sK = lds + (kb % NST) * 3 * TILE;
+    const bf16_t* sV = sK + TILE;
+    const bf16_t* sKt = sK + 2 * TILE;
+    float ds[4][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int kr = prow(sb, j);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        st = mfma(tf(sK, kr, 4 * c + g), qf[c], st);
+        const bf16x8 vf = tf(sV, kr, 4 * c + g);
+        dp = mfma(vf, dhf[c], dp);
+        dp = mfma(vf, dlf[c], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float p = fexp2(fmaf(st[r], sc, -lse2));
+        if (kb == qb && 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r > qloc) p = 0.f;
+        ds[sb][r] = p * (dp[r] - delta) * 0.125f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float s8[8] = {ds[2 * c][0], ds[2 * c][1], ds[2 * c][2], ds[2 * c][3],
+                           ds[2 * c + 1][0], ds[2 * c + 1][1], ds[2 * c + 1][2], ds[2 * c + 1][3]};
+      bf16x8 sh, sl;
+      split8p(s8, sh, sl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const bf16x8 kt = tf(sKt, 16 * d + j, 4 * c + g);
+        dq[d] = mfma(kt, sh, dq[d]);
+        dq[d] = mfma(kt, sl, dq[d]);
+      }
+    }
+  }
+  // lane holds dQ^T[16d + 4g + r][query]: inverse RoPE on the pairs (r, r^1),
+  // then hi/lo planes, normal (4 consecutive columns) and transposed
+  const int pos = myq;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    float v[4] = {dq[d][0], dq[d][1], dq[d][2], dq[d][3]};
+    if (a.rope) {
+#pragma unroll
+      for (int pr = 0; pr < 2; pr++) {
+        const int col = 16 * d + 4 * g + 2 * pr;
+        const float2 cs = *(const float2*)(a.rope + 2 * (pos * (DH / 2) + (col >> 1)));
+        const float x = v[2 * pr], y = v[2 * pr + 1];
+        v[2 * pr] = x * cs.x + y * cs.y;
+        v[2 * pr + 1] = y * cs.x - x * cs.y;
+      }
+    }
+    const uint32_t h01 = cvt2(v[0], v[1]), h23 = cvt2(v[2], v[3]);
+    const uint32_t l01 = cvt2(v[0] - bflo(h01), v[1] - bfhi(h01)), l23 = cvt2(v[2] - bflo(h23), v[3] - bfhi(h23));
+    const long col = h * DH + 16 * d + 4 * g;
+    *(u32x2*)(a.gq[0] + qrow * a.ldg + col) = u32x2{h01, h23};
+    *(u32x2*)(a.gq[1] + qrow * a.ldg + col) = u32x2{l01, l23};
+    const uint32_t hs[4] = {h01 & 0xffffu, h01 >> 16, h23 & 0xffffu, h23 >> 16};
+    const uint32_t ls[4] = {l01 & 0xffffu, l01 >> 16, l23 & 0xffffu, l23 >> 16};
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      a.gqt[0][(col + r) * a.ldgt + qrow] = (bf16_t)hs[r];
+      a.gqt[1][(col + r) * a.ldgt + qrow] = (bf16_t)ls[r];
+    }
+  }
+}
+
+// ------------------------------------------------------------ backward dKV
+// Workgroup (key block, query head, batch): this head's dK | dV share, fp32,
+// into part[gi][row][dK | dV] (gi = head index inside its group).
+__global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [Q | dOh | dOl | Q^T | dO^T h | dO^T l | LSE,Delta]
+  constexpr int SROW = 6 * TILE + 512;  // stage size in bf16 elements (+1 KB of LSE / Delta)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int g = lane >> 4, j = lane & 15;
+  const int kb = blockIdx.x;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
+  const int group = a.HQ / a.HK;
+  const int kvh = h / group, gi = h % group;
+  const int kloc = wave * 16 + j;
+  const long row0 = (long)b * T, krow = row0 + kb * QB + kloc;
+  const float sc = 0.125f * LOG2E;
+
+  bf16x8 kf[2], vf[2];
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    kf[c] = as_bf8(*(const u32x4*)(a.qkv + krow * a.ldqkv + NQ + kvh * DH + 32 * c + 8 * g));
+    vf[c] = as_bf8(*(const u32x4*)(a.qkv + krow * a.ldqkv + NQ + NK + kvh * DH + 32 * c + 8 * g));
+  }
+  const bf16_t* qsrc = a.qkv + row0 * a.ldqkv + h * DH;
+  const bf16_t* dhsrc = a.dh + row0 * a.lddo + h * DH;
+  const bf16_t* dlsrc = a.dl + row0 * a.lddo + h * DH;
+  const bf16_t* qtsrc = a.qkvt + (long)h * DH * a.ldt + row0;
+  const bf16_t* dthsrc = a.dth + (long)h * DH * a.lddot + row0;
+  const bf16_t* dtlsrc = a.dtl + (long)h * DH * a.lddot + row0;
+  const float* lsesrc = a.lse_in_t + (long)h * a.ldt + row0;
+  const float* dlsrc2 = a.delta_t + (long)h * a.ldt + row0;
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  auto issue = [&](int qb, int buf) {
+    const uint32_t st = base + (uint32_t)(buf * SROW * 2);
+    const long q0 = (long)qb * QB;
+    dma_tile(qsrc + q0 * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
+    dma_tile(dhsrc + q0 * a.lddo, a.lddo, st + TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(dlsrc + q0 * a.lddo, a.lddo, st + 2 * TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(qtsrc + q0, a.ldt, st + 3 * TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(dthsrc + q0, a.lddot, st + 4 * TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(dtlsrc + q0, a.lddot, st + 5 * TBYTES, wave_s, lane, [](int) { return true; });
+    if (wave_s == 0) {  // LSE (lanes 0-15) and Delta (16-31) of the block's 64 queries
+      const void* s = lane < 16 ? (const void*)(lsesrc + q0 + 4 * lane)
+                                : lane < 32 ? (const void*)(dlsrc2 + q0 + 4 * (lane - 16)) : (const void*)g_zero_t;
+      dma16(s, st + 6 * TBYTES);
+    }
+  };
+  f32x4 dk[4], dv[4];
+#pragma unroll
+  for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nqb = T / QB;
+  wait_vm<0>();
+#pragma unroll
+  for (int s = 0; s < NST - 1; s++)
+    if (kb + s < nqb) issue(kb + s, s);
+  for (int qb = kb; qb < nqb; qb++) {
+    const int it = qb - kb;
+    if (qb + 1 < nqb) {
+      if (wave_s == 0) wait_vm<13>(); else wait_vm<12>();
+    } else {
+      wait_vm<0>();
+    }
+    block_barrier();
+    if (qb + NST - 1 < nqb) issue(qb + NST - 1, (it + NST - 1) % NST);
+    const bf16_t* sQ = lds + (it % NST) * SROW;
+    const bf16_t* sDh = sQ + TILE;
+    const bf16_t* sDl = sQ + 2 * TILE;
+    const bf16_t* sQt = sQ + 3 * TILE;
+    const bf16_t* sDth = sQ + 4 * TILE;
+    const bf16_t* sDtl = sQ + 5 * TILE;
+    const float* sL = (const float*)(sQ + 6 * TILE);
+    const float* sD = sL + 64;
+    float pp[4][4], ds[4][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++) {
+      f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int qr = prow(sb, j);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        st = mfma(tf(sQ, qr, 4 * c + g), kf[c], st);
+        dp = mfma(tf(sDh, qr, 4 * c + g), vf[c], dp);
+        dp = mfma(tf(sDl, qr, 4 * c + g), vf[c], dp);
+      }
+      const int q4 = 32 * (sb >> 1) + 8 * g + 4 * (sb & 1);  // this lane's 4 queries: q4 .. q4+3
+      const float4 l4 = *(const float4*)(sL + q4);
+      const float4 d4 = *(const float4*)(sD + q4);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float p = fexp2(fmaf(st[r], sc, -lv[r] * LOG2E));
+        if (qb == kb && q4 + r < kloc) p = 0.f;
+        pp[sb][r] = p;
+        ds[sb][r] = p * (dp[r] - dv4[r]) * 0.125f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float p8[8] = {pp[2 * c][0], pp[2 * c][1], pp[2 * c][2], pp[2 * c][3],
+                           pp[2 * c + 1][0], pp[2 * c + 1][1], pp[2 * c + 1][2], pp[2 * c + 1][3]};
+      const float s8[8] = {ds[2 * c][0], ds[2 * c][1], ds[2 * c][2], ds[2 * c][3],
+                           ds[2 * c + 1][0], ds[2 * c + 1][1], ds[2 * c + 1][2], ds[2 * c + 1][3]};
+      bf16x8 ph, pl, sh, sl;
+      split8p(p8, ph, pl);
+      split8p(s8, sh, sl);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const int rr = 16 * d + j, ch = 4 * c + g;
+        const bf16x8 doh = tf(sDth, rr, ch), dol = tf(sDtl, rr, ch), qt = tf(sQt, rr, ch);
+        dv[d] = mfma(doh, ph, dv[d]);
+        dv[d] = mfma(dol, ph, dv[d]);
+        dv[d] = mfma(doh, pl, dv[d]);
+        dk[d] = mfma(qt, sh, dk[d]);
+        dk[d] = mfma(qt, sl, dk[d]);
+      }
+    }
+  }
+  // lane holds dK^T / dV^T [16d + 4g + r][key]: 4 consecutive columns of the partial row
+  const long M = (long)T * gridDim.z;
+  float* prow_ = a.part + ((long)gi * M + krow) * 2 * NK + kvh * DH;
+#pragma unroll
+  for (int d = 0; d < 4; d++) {
+    *(float4*)(prow_ + 16 * d + 4 * g) = make_float4(dk[d][0], dk[d][1], dk[d][2], dk[d][3]);
+    *(float4*)(prow_ + NK + 16 * d + 4 * g) = make_float4(dv[d][0], dv[d][1], dv[d][2], dv[d][3]);
+  }
+}
+
+constexpr size_t LDS_FWD = (size_t)NST * 2 * TBYTES;
+constexpr size_t LDS_DQ = (size_t)NST * 3 * TBYTES;
+constexpr size_t LDS_DKV = (size_t)NST * (6 * TBYTES + 1024);
+static_assert(LDS_DKV <= 160 * 1024, "LDS budget");
+
+}  // namespace
+
+int sjh::attention_t_prepare() {
+  static int done = 0, status = SJ_OK;
+  if (done) return status;
+  done = 1;
+  hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
+  status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
+  return status;
+}
+
+static int check_t(const void* qkv, long ldqkv, const void* qkvt, long ldt, long batch, long t, long hq, long hk,
+                   long head_dim) {
+  SJ_REQUIRE(qkv && qkvt && batch > 0 && t > 0 && t % QB == 0 && hq > 0 && hk > 0 && hq % hk == 0 &&
+                 head_dim == DH && ldqkv >= (hq + 2 * hk) * DH && ldqkv % 8 == 0 && ldt >= batch * t &&
+                 ldt % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)qkvt & 15) == 0 &&
+                 t * ldqkv < (1L << 31),
+             "grouped attention (transposed operands): bf16, head_dim 64, t %% 64 == 0, aligned q|k|v and "
+             "q|k|v^T [.][ldt >= batch*t]");
+  return SJ_OK;
+}
+
+extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
+                                   long batch, long t, long hq, long hk, long head_dim, uint16_t* o, long ldo,
+                                   float* lse, float* lse_t, uint16_t* o_t, long ldot) {
+  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim)) return st;
+  SJ_REQUIRE(o && lse_t && ldo >= hq * DH && ldo % 8 == 0 && ((uintptr_t)o & 15) == 0 && (!o_t || ldot >= batch * t),
+             "grouped attention: outputs");
+  if (int st = sjh::attention_t_prepare()) return st;
+  TArgs a = {};
+  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
+  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk;
+  a.o = (bf16_t*)o; a.ldo = ldo; a.lse = lse; a.lse_t = lse_t; a.ot = (bf16_t*)o_t; a.ldot = ldot;
+  hipLaunchKernelGGL(k_attn2_fwd, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
+                     (hipStream_t)stream, a);
+  SJ_LAUNCH_CHECK("hierarchy_attention");
+  return SJ_OK;
+}
+
+extern "C" size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long hq, long hk, long head_dim) {
+  return sizeof(float) * (size_t)(hq / (hk > 0 ? hk : 1)) * (size_t)(batch * t) * (size_t)(2 * hk * head_dim);
+}
+
+int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t,
+                                long ldt, const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
+                                const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
+                                long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
+                                const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                                uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim)) return st;
+  SJ_REQUIRE(o && lse_t && do_hi && do_lo && do_t_hi && do_t_lo && delta_t && g_hi && g_lo && g_t_hi && g_t_lo &&
+                 lddo >= hq * DH && lddo % 8 == 0 && lddot >= batch * t && lddot % 8 == 0 && ldo % 8 == 0 &&
+                 ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ((uintptr_t)do_hi & 15) == 0 &&
+                 ((uintptr_t)do_lo & 15) == 0 && ((uintptr_t)do_t_hi & 15) == 0 && ((uintptr_t)do_t_lo & 15) == 0 &&
+                 ((uintptr_t)o & 15) == 0 && ldg % 4 == 0,
+             "grouped attention backward (transposed operands): buffers");
+  const size_t need = sj_attention_bwd_tt_workspace_bytes(batch, t, hq, hk, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return sjh::fail(SJ_ERR_CAPACITY, "attention backward: required %zu bytes, available %zu bytes", need,
+                     workspace_bytes);
+  if (int st = sjh::attention_t_prepare()) return st;
+  hipStream_t s = (hipStream_t)stream;
+  TArgs a = {};
+  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
+  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk;
+  a.ob = (const bf16_t*)o; a.ldo = ldo;
+  a.dh = (const bf16_t*)do_hi; a.dl = (const bf16_t*)do_lo; a.lddo = lddo;
+  a.dth = (const bf16_t*)do_t_hi; a.dtl = (const bf16_t*)do_t_lo; a.lddot = lddot;
+  a.lse_in_t = lse_t; a.delta_t = delta_t; a.rope = rope_table;
+  a.gq[0] = (bf16_t*)g_hi; a.gq[1] = (bf16_t*)g_lo; a.gqt[0] = (bf16_t*)g_t_hi; a.gqt[1] = (bf16_t*)g_t_lo;
+  a.ldg = ldg; a.ldgt = ldgt;
+  a.part = (float*)workspace;
+  const dim3 grid((unsigned)(t / QB), (unsigned)hq, (unsigned)batch);
+  if (parts & 1) {
+    hipLaunchKernelGGL(k_attn2_dq, grid, dim3(256), LDS_DQ, s, a);
+    SJ_LAUNCH_CHECK("hierarchy_attention_dq");
+  }
+  if (parts & 2) {
+    hipLaunchKernelGGL(k_attn2_dkv, grid, dim3(256), LDS_DKV, s, a);
+    SJ_LAUNCH_CHECK("hierarchy_attention_dkv");
+  }
+  if (parts & 4) {
+    const long M = batch * t;
+    if (int st = sjh::attention_kv_reduce(s, a.part, hq / hk, M, t, hq * DH, hk * DH, rope_table, g_hi, g_lo, ldg,
+                                          g_t_hi, g_t_lo, ldgt))
+      return st;
+  }
+  return SJ_OK;
+}
+
+extern "C" int sj_attention_bwd_tt(void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
+                                   const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
+                                   const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
+                                   long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
+                                   const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                                   uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+  return sjh::attention_bwd_tt_parts(7, stream, qkv, ldqkv, qkv_t, ldt, o, ldo, lse_t, do_hi, do_lo, lddo, do_t_hi,
+                                     do_t_lo, lddot, delta_t, batch, t, hq, hk, head_dim, rope_table, g_hi, g_lo, ldg,
+                                     g_t_hi, g_t_lo, ldgt, workspace, workspace_bytes);
+}

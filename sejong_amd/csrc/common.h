@@ -108,6 +108,18 @@ int pvjp_indices_dev(hipStream_t stream, const uint64_t* seed, long a, long dono
 // factor formed on the device from the FP64 squared norm (nullable: no clip)
 int factored_update_staged(hipStream_t stream, const void* meta, long tiles, const sj_sgd_step* step,
                            const double* sumsq);
+// attention over transposed operands (attention_t.hip) and the group reduce
+// of the per-head dK | dV partials it shares with attention.hip
+int attention_t_prepare();
+int attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
+                        const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi, uint16_t* gt_lo,
+                        long ldgt);
+int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
+                           const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
+                           const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
+                           long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
+                           const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                           uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);

@@ -39,7 +39,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __attribute__((aligned(64))) uint8_t g_zero16[64];  // zero source for masked DMA lanes
 
-enum Epi { E_STORE = 0, E_PARTIAL = 1, E_QKV = 2, E_RESID = 3, E_GATEUP = 4, E_SWIGLU_BWD = 5 };
+enum Epi { E_STORE = 0, E_PARTIAL = 1, E_QKV = 2, E_RESID = 3, E_GATEUP = 4, E_SWIGLU_BWD = 5, E_PLANES = 6 };
 
 struct FParams {
   const bf16_t* a[2];  // A planes (hi, lo), [M][K] k-contiguous
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   constexpr int TLD = BN + 8;          // bf16 tile row stride (elements)
   constexpr int TP = BM * TLD;         // bf16 tile size (elements)
   constexpr int TLDF = BN + 4;         // fp32 tile row stride
-  constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : 1;
+  constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : EPI == E_PLANES ? 2 : 1;
   constexpr bool F32T = EPI == E_PARTIAL || EPI == E_STORE;  // fp32 tile unless c_bf16
   static_assert((size_t)NTILE * TP * 2 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tiles exceed LDS");
   static_assert((size_t)BM * TLDF * 4 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tile exceeds LDS");
@@ -367,6 +367,14 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
           T[(rl + r) * TLD + cl] = f2bf(g);
           T[TP + (rl + r) * TLD + cl] = f2bf(u);
           T[2 * TP + (rl + r) * TLD + cl] = f2bf(g * sigm(g) * u);
+        }
+      } else if constexpr (EPI == E_PLANES) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          bf16_t h, l;
+          split_bf(v[r], h, l);
+          T[(rl + r) * TLD + cl] = h;
+          T[TP + (rl + r) * TLD + cl] = l;
         }
       } else if constexpr (EPI == E_QKV) {
 #pragma unroll
@@ -442,6 +450,15 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       bf16_t* tb = (t4 & 1) ? (bf16_t*)p.c[3] : (bf16_t*)p.c[2];
       cols_bf16(T + t4 * TP, tb + coloff * p.ldc[2], p.ldc[2]);
     }
+  } else if constexpr (EPI == E_PLANES) {
+#pragma unroll
+    for (int t2 = 0; t2 < 2; t2++) {
+      bf16_t* base = (bf16_t*)p.c[t2];
+      rows_bf16(T + t2 * TP, [&](long m, long n, const u32x4& val, const bf16_t* src) {
+        put8(base + m * p.ldc[0] + n, n, val, src);
+      });
+      cols_bf16(T + t2 * TP, (bf16_t*)p.c[2 + t2], p.ldc[2]);
+    }
   } else if constexpr (EPI == E_GATEUP) {
 #pragma unroll
     for (int t3 = 0; t3 < 3; t3++) {
@@ -474,12 +491,17 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
           rot[2 * k + 1] = f2bf(b * cs.x + a * cs.y);
           o[k] = pack2(rot[2 * k], rot[2 * k + 1]);
         }
+        if (p.c[3]) *(u32x4*)const_cast<bf16_t*>(src) = o;  // the rotated chunk feeds the transposed copy
       } else {
 #pragma unroll
         for (int k = 0; k < 8; k++) rot[k] = src[k];
       }
       put8((bf16_t*)p.c[sg] + m * p.ldc[sg] + nl, n, o, rot);
     });
+    if (p.c[3]) {  // q|k|v transposed [N][ldc[3]] (the attention kernels' Q^T, K^T, V^T tiles)
+      __syncthreads();
+      cols_bf16(T, (bf16_t*)p.c[3], p.ldc[3]);
+    }
   } else if constexpr (EPI == E_RESID) {
     rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
       const bf16_t* rr = p.r + m * p.ldr + n;
@@ -689,7 +711,7 @@ int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
 template <int EPI, int PA, int PB>
 constexpr bool plane_combo() {
   if (EPI == E_STORE || EPI == E_PARTIAL) return true;
-  if (EPI == E_SWIGLU_BWD) return PA == 2 && PB == 1;
+  if (EPI == E_SWIGLU_BWD || EPI == E_PLANES) return PA == 2 && PB == 1;
   return PA == 1 && PB == 1;
 }
 
@@ -750,6 +772,7 @@ int gemm_fast_prepare() {
   if (!status) status = set_attrs_planes<E_RESID>();
   if (!status) status = set_attrs_planes<E_GATEUP>();
   if (!status) status = set_attrs_planes<E_SWIGLU_BWD>();
+  if (!status) status = set_attrs_planes<E_PLANES>();
   return status;
 }
 }  // namespace sjh
@@ -809,9 +832,33 @@ extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16
   return SJ_OK;
 }
 
+extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, const uint16_t* a_hi,
+                                         const uint16_t* a_lo, long lda, const uint16_t* b, long ldb, uint16_t* c_hi,
+                                         uint16_t* c_lo, long ldc, uint16_t* c_t_hi, uint16_t* c_t_lo, long ldct) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
+                 ldc >= N && ldct >= M && ldct % 8 == 0,
+             "matmul planes out: M %ld N %ld K %ld (K, ld multiples of 8)", M, N, K);
+  SJ_REQUIRE(a_hi && a_lo && b && c_hi && c_lo && c_t_hi && c_t_lo && ok16(a_hi) && ok16(a_lo) && ok16(b) &&
+                 ok16(c_t_hi) && ok16(c_t_lo),
+             "matmul planes out: 16-byte aligned operands required");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)a_hi; p.a[1] = (const bf16_t*)a_lo; p.lda = lda;
+  p.b[0][0] = (const bf16_t*)b; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;
+  p.M = M; p.N = N; p.K = K;
+  p.c[0] = c_hi; p.c[1] = c_lo; p.c[2] = c_t_hi; p.c[3] = c_t_lo;
+  p.ldc[0] = ldc; p.ldc[2] = ldct;
+  int bm, bn, splits;
+  plan(M, N, K, 2, bm, bn, splits);
+  int st = launch_planes<E_PLANES>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("matmul planes out");
+  return SJ_OK;
+}
+
 extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t,
                             long ldw, long N, long KV, uint16_t* qkv, long ldo, const float* rope_table, long rope_t,
-                            long head_dim) {
+                            long head_dim, uint16_t* qkv_t, long ldqt) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
   SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D &&
                  ldo >= N + 2 * KV && N % 64 == 0 && KV % 64 == 0 && ok16(x) && ok16(wqkv_t),
@@ -832,6 +879,11 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
   p.M = M; p.N = N + 2 * KV; p.K = D; p.c_bf16 = 1;
   p.rope = rope_table; p.rope_t = rope_t > 0 ? rope_t : 1; p.head_dim = head_dim > 0 ? head_dim : 2;
   p.rope_cols = rope_table ? N + KV : 0;
+  if (qkv_t) {
+    SJ_REQUIRE(ldqt >= M && ldqt % 8 == 0 && ok16(qkv_t), "project_qkv transposed output: ld %ld", ldqt);
+    p.c[3] = qkv_t;
+    p.ldc[3] = ldqt;
+  }
   int bm = 64, bn = 64;  // measured best at the cfg2 shape
   if (getenv("SJ_GEMM_TILE")) {
     pick(M, N + 2 * KV, bm, bn);

@@ -149,6 +149,13 @@ struct sj_model {
   int tjob_n = 0;
   long tjob_tiles = 0;
   std::vector<uint16_t*> zt, ot, z2t, ht;  // transposed activations per layer
+  // attention over producer-transposed operands (T a multiple of 64): q|k|v^T
+  // and LSE^T per layer, dO planes in both orientations and Delta^T scratch
+  bool attn_tt = false;
+  std::vector<uint16_t*> qkvt;
+  std::vector<float*> lset;
+  uint16_t* dop[4] = {};  // dO hi, lo [M][d]; hi^T, lo^T [d][ldt]
+  float* deltat = nullptr;
   uint16_t *rp[4] = {}, *xp[4] = {}, *qp[4] = {}, *gp[4] = {};  // gradient planes: hi, lo, hi^T, lo^T
   // activations
   std::vector<void*> x;  // L+1 residual stream tensors
@@ -359,9 +366,14 @@ int forward(sj_model* m) {
     uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
     uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
     OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], m->ldt, M, d, eps));
-    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, m->rope, m->T, m->Dh));
-    OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l], m->ldt,
-                                           m->B, m->T, m->HQ, m->HK, m->Dh));
+    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, m->rope, m->T, m->Dh,
+                                m->attn_tt ? m->qkvt[l] : nullptr, m->ldt));
+    if (m->attn_tt)
+      OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, m->qkvt[l], m->ldt, m->B, m->T, m->HQ, m->HK, m->Dh, o, d,
+                                              m->lse[l], m->lset[l], m->ot[l], m->ldt));
+    else
+      OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l],
+                                             m->ldt, m->B, m->T, m->HQ, m->HK, m->Dh));
     OP("attn_out_residual", sj_linear_residual_fwd_t(s, o, d, M, d, WT + y.wo, d, d, x, d, (uint16_t*)m->x1[l], d));
     OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], m->ldt, M, d, eps));
     OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F, m->ht[l],
@@ -487,14 +499,26 @@ int backward(sj_model* m) {
       OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1, G + y.fn,
                                          xp[0], xp[1], xp[2], xp[3], ldt, M, d, eps, ws, wsb));
       // x1 = x + attention_output(o)
-      OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws, wsb));
+      if (m->attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
+        OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, xp[0], xp[1], d, W + y.wo, d, m->dop[0], m->dop[1], d,
+                                                   m->dop[2], m->dop[3], ldt));
+      else
+        OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
+                                         wsb));
       OP("attn_out_dw", sj_gemm_planes(s, d, d, M, m->ot[l], nullptr, ldt, xp[2], xp[3], ldt, G + y.wo, SJ_F32, d, 0, ws,
                                        wsb));
-      for (int part = 1; part <= 4; part <<= 1)
-        OP(part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce",
-           sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
-                                      m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0],
-                                      qp[1], NQ, qp[2], qp[3], ldt, ws, wsb));
+      for (int part = 1; part <= 4; part <<= 1) {
+        const char* nm = part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce";
+        if (m->attn_tt)
+          OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, m->qkvt[l], ldt, (const uint16_t*)m->o[l], d,
+                                             m->lset[l], m->dop[0], m->dop[1], d, m->dop[2], m->dop[3], ldt,
+                                             m->deltat, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0], qp[1], NQ,
+                                             qp[2], qp[3], ldt, ws, wsb));
+        else
+          OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
+                                            m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope,
+                                            qp[0], qp[1], NQ, qp[2], qp[3], ldt, ws, wsb));
+      }
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
       if (m->group_on[0]) TRY(vjp_group(m, l, 0));
       if (!m->group_all[0])
@@ -811,6 +835,8 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     m->planes = want && m->dt == SJ_BF16 && m->Dh == 64 && m->d % 8 == 0 && m->F % 8 == 0 && m->d <= 1024 &&
                 (m->B == 1 || m->T % 4 == 0);
     m->ldt = (m->M + 7) / 8 * 8;
+    const char* ev = getenv("SJ_ATTN_TT");
+    m->attn_tt = m->planes && m->T % 64 == 0 && !(ev && ev[0] == '0');
   }
   build_layout(m);
   int st = SJ_OK;
@@ -885,6 +911,16 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
       ALLOC(m->ht[l], F * MT * 2);
     }
     const size_t NQ = (size_t)m->NQKV;
+    if (m->attn_tt) {
+      m->qkvt.resize(m->L);
+      m->lset.resize(m->L);
+      for (long l = 0; l < m->L; l++) {
+        ALLOC(m->qkvt[l], NQ * MT * 2);
+        ALLOC(m->lset[l], (size_t)m->HQ * MT * 4);
+      }
+      for (int i = 0; i < 4; i++) ALLOC(m->dop[i], (i < 2 ? M : MT) * d * 2);
+      ALLOC(m->deltat, (size_t)m->HQ * MT * 4);
+    }
     for (int i = 0; i < 4; i++) {
       const size_t rows = i < 2 ? M : MT;
       ALLOC(m->rp[i], rows * d * 2);
@@ -956,6 +992,7 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   if (m->planes) {
     upd(sj_rmsnorm_bwd_p_workspace_bytes(Mi, m->d));
     upd(sj_attention_bwd_p_workspace_bytes(m->B, m->T, m->HQ, m->HK, m->Dh));
+    upd(sj_attention_bwd_tt_workspace_bytes(m->B, m->T, m->HQ, m->HK, m->Dh));
     upd(sj_gemm_planes_workspace_bytes(m->F, m->d, Mi));
     upd(sj_gemm_planes_workspace_bytes(m->d, 2 * m->F, Mi));
     upd(sj_gemm_planes_workspace_bytes(m->d, m->d, Mi));
@@ -1003,6 +1040,7 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     int ps = sjh::norm_prepare();
     if (!ps) ps = sjh::gemm_fast_prepare();
     if (!ps) ps = sjh::attention_prepare();
+    if (!ps) ps = sjh::attention_t_prepare();
     if (ps) return fail_cleanup(ps);
   }
   if (e == hipSuccess) e = hipMemsetAsync(m->status, 0, 64, s);

@@ -100,9 +100,14 @@ def test_qkv_t_rope(api):
     tab = empty(T * Dh)
     api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
     out = empty(M * NQ, "bf16")
-    api.sj_qkv_fwd_t(None, dev(x, "bf16").p, D, M, D, dev(w.T.copy(), "bf16").p, D, D, J, out.p, NQ, tab.p, T, Dh)
+    ldt = M + 8
+    out_t = zeros(NQ * ldt, "bf16")
+    api.sj_qkv_fwd_t(None, dev(x, "bf16").p, D, M, D, dev(w.T.copy(), "bf16").p, D, D, J, out.p, NQ, tab.p, T, Dh,
+                     out_t.p, ldt)
     sync()
     got = out.host().reshape(M, NQ)
+    # the transposed copy holds the same stored values (q, k after RoPE)
+    np.testing.assert_array_equal(out_t.host().reshape(NQ, ldt)[:, :M], got.T)
     q = O.round_to(x @ w[:, :D], "bf16"); k = O.round_to(x @ w[:, D:D + J], "bf16")
     aq = np.abs(x) @ np.abs(w)
     assert_stored_close(got[:, :D], O.rope(q, T, HQ, Dh), "bf16", "q", ulps=2,
@@ -243,3 +248,90 @@ def test_attention_t_and_planes(api, lib, B, T, HQ, HK):
     dq = O.rope(dq, T, HQ, Dh, inverse=True); dk = O.rope(dk, T, HK, Dh, inverse=True)
     assert rel((hi + lo)[:, :N], dq) < 1e-4 and rel((hi + lo)[:, N:N + KV], dk) < 1e-4
     assert rel((hi + lo)[:, N + KV:], dv) < 1e-4
+
+
+@pytest.mark.parametrize("B,T,HQ,HK", [(2, 256, 6, 2), (1, 512, 4, 4), (2, 128, 8, 1)])
+def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK):
+    """The step's attention over producer-transposed operands (qkv^T, dO
+    planes in both orientations) against the fp32 row kernels and the FP64
+    oracle on the same stored inputs."""
+    Dh = 64
+    rng = np.random.default_rng(B * T + HQ * 7 + HK)
+    M = B * T; N = HQ * Dh; KV = HK * Dh; NG = N + 2 * KV
+    ldq = NG + 8
+    ldt = M + 8
+    qkv = rnd((M, NG), "bf16", rng)
+    QKV = dev(np.concatenate([qkv, np.zeros((M, ldq - NG))], 1), "bf16")
+    QKVT = dev(np.concatenate([qkv.T, np.zeros((NG, ldt - M))], 1), "bf16")
+    q, k, v = qkv[:, :N], qkv[:, N:N + KV], qkv[:, N + KV:]
+    print(f"[attention_tt] B={B} T={T} HQ={HQ} HK={HK}", flush=True)
+    O1, L1 = empty(M * N, "bf16"), empty(M * HQ)
+    api.sj_attention_fwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O1.p, N, L1.p, BF, B, T, HQ, HK, Dh, 0)
+    O2, L2, LT, OT = empty(M * N, "bf16"), empty(M * HQ), zeros(HQ * ldt), zeros(N * ldt, "bf16")
+    api.sj_attention_fwd_tt(None, QKV.p, ldq, QKVT.p, ldt, B, T, HQ, HK, Dh, O2.p, N, L2.p, LT.p, OT.p, ldt)
+    sync()
+    o1, o2 = O1.host().reshape(M, N), O2.host().reshape(M, N)
+    # one storage ulp, plus the accumulation error of a result that cancels
+    # (bounded through the same attention over |v|)
+    o_abs, _ = O.attention_fwd(q, k, np.abs(v), B, T, HQ, HK, Dh)
+    bad = np.abs(o2 - o1) > 2.0 ** -7 * np.abs(o1) + 2.0 ** -14 * o_abs + 1e-30
+    if bad.any():
+        r, c = np.nonzero(bad)
+        print(f"[attention_tt] {bad.sum()} O elements beyond one ulp; rows%64 {np.unique(r % T % 64)[:20]} "
+              f"pos {np.unique(r % T)[:10]} heads {np.unique(c // 64)} dims {np.unique(c % 64)[:20]}; "
+              f"worst rel {np.max(np.abs(o2 - o1)[bad] / (np.abs(o1[bad]) + 1e-30)):.3e} rel(all) {rel(o2, o1):.3e}",
+              flush=True)
+    assert not bad.any(), "O beyond one bf16 ulp of the row kernel"
+    assert rel(L2.host(), L1.host()) < 1e-6
+    np.testing.assert_array_equal(LT.host().reshape(HQ, ldt)[:, :M], L2.host().reshape(M, HQ).T)
+    np.testing.assert_array_equal(OT.host().reshape(N, ldt)[:, :M], o2.T)
+    # backward from dO planes (both orientations), against the fp32 row path on the same O and LSE
+    do = rng.normal(0, 1e-4, (M, N)).astype(np.float32).astype(np.float64)
+    dh = O.round_to(do, "bf16"); dl = O.round_to(do - dh, "bf16")
+    DH_, DL_ = dev(dh, "bf16"), dev(dl, "bf16")
+    DTH = dev(np.concatenate([dh.T, np.zeros((N, ldt - M))], 1), "bf16")
+    DTL = dev(np.concatenate([dl.T, np.zeros((N, ldt - M))], 1), "bf16")
+    tab = empty(T * Dh)
+    api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
+    dof = dh + dl                                                  # the dO the planes carry
+    DOF = dev(dof)
+    dQ, dK, dV, De = empty(M * N), empty(M * KV), empty(M * KV), empty(M * HQ)
+    api.sj_attention_bwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O2.p, N, L2.p, DOF.p, N, dQ.p, N,
+                         dK.p, KV, dV.p, KV, De.p, BF, B, T, HQ, HK, Dh, 0, tab.p)
+    Gh, Gl, Th, Tl = empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldt, "bf16"), zeros(NG * ldt, "bf16")
+    DT = zeros(HQ * ldt)
+    ws = empty(max(lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
+    api.sj_attention_bwd_tt(None, QKV.p, ldq, QKVT.p, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DTH.p, DTL.p, ldt, DT.p,
+                            B, T, HQ, HK, Dh, tab.p, Gh.p, Gl.p, NG, Th.p, Tl.p, ldt, ws.p, ws.nbytes)
+    sync()
+    assert rel(DT.host().reshape(HQ, ldt)[:, :M], De.host().reshape(M, HQ).T) < 1e-5
+    ref = np.concatenate([dQ.host().reshape(M, N), dK.host().reshape(M, KV), dV.host().reshape(M, KV)], 1)
+    hi, lo = Gh.host().reshape(M, NG), Gl.host().reshape(M, NG)
+    got = hi + lo
+    for name, sl in (("dq", slice(0, N)), ("dk", slice(N, N + KV)), ("dv", slice(N + KV, NG))):
+        assert rel(got[:, sl], ref[:, sl]) < 1e-5, (name, rel(got[:, sl], ref[:, sl]))
+    assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
+    np.testing.assert_array_equal(Th.host().reshape(NG, ldt)[:, :M], hi.T)
+    np.testing.assert_array_equal(Tl.host().reshape(NG, ldt)[:, :M], lo.T)
+    dq, dk, dv, _ = O.attention_bwd(q, k, v, o2, L2.host(), dof, B, T, HQ, HK, Dh, 0)
+    dq = O.rope(dq, T, HQ, Dh, inverse=True); dk = O.rope(dk, T, HK, Dh, inverse=True)
+    assert rel(got[:, :N], dq) < 1e-4 and rel(got[:, N:N + KV], dk) < 1e-4 and rel(got[:, N + KV:], dv) < 1e-4
+
+
+def test_gemm_planes_split_out(api):
+    rng = np.random.default_rng(21)
+    M, N, K = 512, 384, 384
+    a = rng.normal(0, 1e-3, (M, K)).astype(np.float32).astype(np.float64)
+    ah = O.round_to(a, "bf16"); al = O.round_to(a - ah, "bf16")
+    w = O.round_to(rng.normal(0, 0.05, (N, K)), "bf16")            # W^T [N][K]
+    ldt = M + 8
+    Ch, Cl, Th, Tl = empty(M * N, "bf16"), empty(M * N, "bf16"), zeros(N * ldt, "bf16"), zeros(N * ldt, "bf16")
+    api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, Ch.p,
+                                 Cl.p, N, Th.p, Tl.p, ldt)
+    sync()
+    hi, lo = Ch.host().reshape(M, N), Cl.host().reshape(M, N)
+    assert rel(hi + lo, (ah + al) @ w.T) < 1e-5
+    assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
+    np.testing.assert_array_equal(hi, O.round_to(hi + lo, "bf16"))
+    np.testing.assert_array_equal(Th.host().reshape(N, ldt)[:, :M], hi.T)
+    np.testing.assert_array_equal(Tl.host().reshape(N, ldt)[:, :M], lo.T)
