@@ -137,18 +137,27 @@ __device__ __forceinline__ void put4_split(bf16_t* hi, bf16_t* lo, const float* 
   *(u32x2*)lo = u32x2{pack2(l[0], l[1]), pack2(l[2], l[3])};
 }
 
-// pipeline depth: 4 stages when a stage fits 40 KB, else 3 (LDS <= 160 KB)
-template <int BM, int BN, int PA, int PB, int EPI>
-constexpr int stages() {
+// Pipeline depth: two stages (double buffering).  Measured on gfx950: a
+// workgroup's LDS footprint decides how many share a CU, and for the step's
+// K (384..4096) a second resident workgroup hides more latency than deeper
+// prefetch (64x128 tiles at K = 384: 28.3 -> 19.9 us; at K = 3072: 112 ->
+// 84 us).  The LDS block is the larger of the two stages and the epilogue's
+// staging tiles.
+template <int BM, int BN, int PA, int PB, int EPI, int NS>
+constexpr size_t lds_bytes() {
   constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
-  return (BM * PA + BN * PB * NBM) * BK * 2 <= 40 * 1024 ? 4 : 3;
+  constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : EPI == E_PLANES ? 2 : 1;
+  constexpr size_t pipe = (size_t)NS * (BM * PA + BN * PB * NBM) * BK * 2;
+  constexpr size_t ep1 = (size_t)NTILE * BM * (BN + 8) * 2;
+  constexpr size_t ep2 = (EPI == E_STORE || EPI == E_PARTIAL) ? (size_t)BM * (BN + 4) * 4 : 0;
+  constexpr size_t e = ep1 > ep2 ? ep1 : ep2;
+  return pipe > e ? pipe : e;
 }
 
-template <int BM, int BN, int PA, int PB, int EPI>
+template <int BM, int BN, int PA, int PB, int EPI, int NS>
 __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   constexpr bool DUAL = EPI == E_GATEUP;
   constexpr int NBM = DUAL ? 2 : 1;
-  constexpr int NS = stages<BM, BN, PA, PB, EPI>();
   constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 16, NB = WN / 16;
   constexpr int AROWS = BM * PA, BROWS = BN * PB * NBM;
   constexpr int STAGE_ROWS = AROWS + BROWS;
@@ -321,8 +330,8 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   constexpr int TLDF = BN + 4;         // fp32 tile row stride
   constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : EPI == E_PLANES ? 2 : 1;
   constexpr bool F32T = EPI == E_PARTIAL || EPI == E_STORE;  // fp32 tile unless c_bf16
-  static_assert((size_t)NTILE * TP * 2 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tiles exceed LDS");
-  static_assert((size_t)BM * TLDF * 4 <= (size_t)NS * STAGE_ROWS * BK * 2, "epilogue tile exceeds LDS");
+  static_assert((size_t)NTILE * TP * 2 <= lds_bytes<BM, BN, PA, PB, EPI, NS>(), "epilogue tiles exceed LDS");
+  static_assert(!F32T || (size_t)BM * TLDF * 4 <= lds_bytes<BM, BN, PA, PB, EPI, NS>(), "epilogue tile exceeds LDS");
   bf16_t* T = lds;
   float* TF = (float*)lds;
   const bool f32out = F32T && !p.c_bf16;
@@ -571,17 +580,59 @@ __global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict
   }
 }
 
-template <int BM, int BN, int PA, int PB, int EPI>
-int launch(hipStream_t s, const FParams& p, int splits) {
+template <int BM, int BN, int PA, int PB, int EPI, int NS>
+int launch_ns(hipStream_t s, const FParams& p, int splits) {
   constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
-  constexpr size_t lds = (size_t)stages<BM, BN, PA, PB, EPI>() * (BM * PA + BN * PB * NBM) * BK * 2;
+  constexpr size_t lds = lds_bytes<BM, BN, PA, PB, EPI, NS>();
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = k_gemm_fast<BM, BN, PA, PB, EPI>;
+  auto kern = k_gemm_fast<BM, BN, PA, PB, EPI, NS>;
   const_cast<FParams&>(p).xcd_remap = xcd_remap();
   // grid z: split-K slices, or the experts of a per-expert dW launch
   dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
   hipLaunchKernelGGL(kern, grid, dim3(NT), lds, s, p);
   return SJ_OK;
+}
+
+// Pipeline depth (measured on gfx950 over the cfg2 and cfg5 step GEMMs):
+// three stages when every workgroup of the launch is resident at three
+// (deeper prefetch, nothing gained by more residency); otherwise two when
+// two stages let more workgroups share a CU (64x128 tiles at K = 384:
+// 28.3 -> 19.9 us), else three.  Residency comes from the runtime's
+// occupancy query (LDS and registers of that instantiation).
+// SJ_GEMM_STAGES=2|3 overrides it (sweeps).
+int g_stages = -1;
+int cus();
+template <int BM, int BN, int PA, int PB, int EPI, int NS>
+int resident() {
+  static int occ = -1;
+  if (occ < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemm_fast<BM, BN, PA, PB, EPI, NS>, NT,
+                                                     lds_bytes<BM, BN, PA, PB, EPI, NS>()) != hipSuccess)
+      n = 1;
+    occ = n > 0 ? n : 1;
+  }
+  return occ;
+}
+template <int BM, int BN, int PA, int PB, int EPI>
+int launch(hipStream_t s, const FParams& p, int splits) {
+  if (g_stages < 0) {
+    const char* e = getenv("SJ_GEMM_STAGES");
+    g_stages = e ? atoi(e) : 0;
+  }
+  constexpr bool three = lds_bytes<BM, BN, PA, PB, EPI, 3>() <= 160 * 1024;
+  int ns = 2;
+  if constexpr (three) {
+    if (g_stages == 2 || g_stages == 3) {
+      ns = g_stages;
+    } else {
+      const long wgs = ((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM) * (long)splits;
+      const int o3 = resident<BM, BN, PA, PB, EPI, 3>(), o2 = resident<BM, BN, PA, PB, EPI, 2>();
+      ns = (wgs <= (long)o3 * cus() || o2 <= o3) ? 3 : 2;
+    }
+    if (ns == 3) return launch_ns<BM, BN, PA, PB, EPI, 3>(s, p, splits);
+  }
+  return launch_ns<BM, BN, PA, PB, EPI, 2>(s, p, splits);
 }
 
 int g_cu = 0;
@@ -730,13 +781,19 @@ int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int b
 
 bool ok16(const void* q) { return ((uintptr_t)q & 15) == 0; }
 
-template <int BM, int BN, int PA, int PB, int EPI>
-int set_attr() {
-  constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
-  constexpr size_t lds = (size_t)stages<BM, BN, PA, PB, EPI>() * (BM * PA + BN * PB * NBM) * BK * 2;
-  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_fast<BM, BN, PA, PB, EPI>,
+template <int BM, int BN, int PA, int PB, int EPI, int NS>
+int set_attr_ns() {
+  constexpr size_t lds = lds_bytes<BM, BN, PA, PB, EPI, NS>();
+  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_fast<BM, BN, PA, PB, EPI, NS>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   return e == hipSuccess ? SJ_OK : sjh::hip_check(e, "gemm: LDS attribute");
+}
+template <int BM, int BN, int PA, int PB, int EPI>
+int set_attr() {
+  int st = set_attr_ns<BM, BN, PA, PB, EPI, 2>();
+  if constexpr (lds_bytes<BM, BN, PA, PB, EPI, 3>() <= 160 * 1024)
+    if (!st) st = set_attr_ns<BM, BN, PA, PB, EPI, 3>();
+  return st;
 }
 template <int EPI, int PA, int PB>
 int set_attrs_tiles() {
