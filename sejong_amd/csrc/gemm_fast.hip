@@ -680,21 +680,23 @@ void pick(long M, long N, int& bm, int& bn) {
 // alone do not fill the chip.  SJ_GEMM_SPLITS=<n> overrides it (sweeps).
 int splits_for(long M, long N, long K, int bm, int bn);
 
-// Tile and split-K plan of sj_gemm_planes (measured on the cfg2 shapes):
-// very long K (>= 8192, M <= 1024) takes 64x128 tiles (64x64 for N < 128)
-// and 4..16 K slices; dW-shaped products (K >= 2048) take 4 K slices and the
-// largest tile that still gives >= 144 workgroups; split-A products (dX)
-// with K <= 1024 and N a multiple of 128 take 64x128 tiles when those
-// cover half the CUs; the rest use pick().
+// Tile and split-K plan of sj_gemm_planes (measured on the cfg2 and cfg5
+// step shapes with the occupancy-chosen pipeline depth):
+//   very long K (>= 8192) with a short output (M <= 512 or N <= 64: the
+//   token-contracted products of the parameter VJP): 64x128 tiles (64x64
+//   for N < 128) and 4..16 K slices of >= 512;
+//   dW-shaped products (K >= 2048, at most one 64x64 tile per CU): 4 K
+//   slices and the largest tile giving min(2 per CU, 4 x the 64x64 tiles)
+//   workgroups (cfg5 attention-output dW: 128x64 x 4 slices, 115 -> 90 us);
+//   split-A products (dX): 64x128 tiles when they give two per CU, else
+//   64x64 (cfg5 down dX: 662 -> 499 us; cfg2 dX: 64x64);
+//   the rest pick().
 void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
   const long cu = cus();
   const char* et = getenv("SJ_GEMM_TILE");
   const char* es = getenv("SJ_GEMM_SPLITS");
   if (!et && !es) {
-    if (K >= 8192 && M <= 1024) {
-      // very long K with a short output (token-contracted products of the
-      // parameter VJP): 64-row tiles and K slices of >= 512 for about four
-      // workgroups per CU (measured at 144 x 1536..5504 x 16384)
+    if (K >= 8192 && (M <= 512 || N <= 64)) {
       bm = 64;
       bn = N >= 128 ? 128 : 64;
       const long t = tiles(M, N, bm, bn);
@@ -705,19 +707,21 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
       splits = (int)sp;
       return;
     }
-    if (tiles(M, N, 64, 64) < cu && K >= 2048) {
+    if (tiles(M, N, 64, 64) <= cu && K >= 2048) {
       splits = K / 256 < 4 ? (int)(K / 256) : 4;
+      long want = tiles(M, N, 64, 64) * splits;
+      want = want < 2 * cu ? want : 2 * cu;
       const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
       for (const auto& c : cand)
-        if (tiles(M, N, c[0], c[1]) * splits >= 144 || (c[0] == 64 && c[1] == 64)) {
+        if (tiles(M, N, c[0], c[1]) * splits >= want || (c[0] == 64 && c[1] == 64)) {
           bm = c[0];
           bn = c[1];
           return;
         }
     }
-    if (pa == 2 && K <= 1024 && N % 128 == 0 && tiles(M, N, 64, 128) * 2 >= cu) {
+    if (pa == 2) {
       bm = 64;
-      bn = 128;
+      bn = tiles(M, N, 64, 128) >= 2 * cu ? 128 : 64;
       splits = splits_for(M, N, K, bm, bn);
       return;
     }
@@ -941,7 +945,8 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
     p.c[3] = qkv_t;
     p.ldc[3] = ldqt;
   }
-  int bm = 64, bn = 64;  // measured best at the cfg2 shape
+  // 64x128 tiles once they give two per CU (cfg5: 105 -> 96 us), else 64x64
+  int bm = 64, bn = tiles(M, N + 2 * KV, 64, 128) >= 2 * cus() && N % 128 == 0 && KV % 128 == 0 ? 128 : 64;
   if (getenv("SJ_GEMM_TILE")) {
     pick(M, N + 2 * KV, bm, bn);
     if (N % bn || KV % bn) bn = 64;
