@@ -157,6 +157,15 @@ struct sj_model {
   uint16_t* dop[4] = {};  // dO hi, lo [M][d]; hi^T, lo^T [d][ldt]
   float* deltat = nullptr;
   uint16_t *rp[4] = {}, *xp[4] = {}, *qp[4] = {}, *gp[4] = {};  // gradient planes: hi, lo, hi^T, lo^T
+  // The dW products (and the parameter-VJP groups) run on a second stream
+  // beside the dX chain; their transposed operand planes alternate by layer
+  // parity ([kind][parity][hi, lo]; kind r, g, x, q) so the dX chain can
+  // write layer l-1's while layer l's are still read.  Events: written
+  // (second stream waits) and read (dX chain waits before overwriting).
+  hipStream_t stream2 = nullptr;
+  uint16_t* pt[4][2][2] = {};
+  hipEvent_t ev_w[4][2] = {}, ev_r[4][2] = {}, ev_fork = nullptr, ev_join = nullptr;
+  void* ws2 = nullptr;
   // activations
   std::vector<void*> x;  // L+1 residual stream tensors
   std::vector<void*> z, qkv, o, x1, z2, gg, uu, hh;
@@ -430,23 +439,20 @@ int forward(sj_model* m) {
 // the last one on ties: graph.rs:931-934); every later group reuses both
 // (one basis per (tokens, rank), one selection per width, graph.rs:
 // 957-982), so one seed is consumed per step.
-int vjp_group(sj_model* m, long l, int kind) {
-  hipStream_t s = m->stream;
+int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb, uint16_t* const* dyt) {
   const long M = m->M, d = m->d, F = m->F, R = m->vjp_R, k = m->vjp_k, ldt = m->ldt;
   const long width = kind == 0 ? m->NQKV : 2 * F;
   if (l == m->L - 1 && kind == 1) {
     const uint64_t* seed = (const uint64_t*)((const char*)m->sgd_dev + offsetof(sj_sgd_step, seed));
     OP("pvjp_indices", sjh::pvjp_indices_dev(s, seed, d, F, m->vjp_blocks, m->vjp_S, R, m->sgd.vjp_block_rows,
                                              m->vjp_scratch, m->vjp_cols, m->vjp_rows, m->vjp_map));
-    OP("pvjp_basis", sj_pvjp_basis(s, m->uu[m->L - 1], SJ_BF16, F, M, m->vjp_cols, R, m->vjp_eps, m->vjp_q, m->ws,
-                                   m->ws_bytes));
+    OP("pvjp_basis", sj_pvjp_basis(s, m->uu[m->L - 1], SJ_BF16, F, M, m->vjp_cols, R, m->vjp_eps, m->vjp_q, ws, wsb));
   }
   const uint16_t* xt = kind == 0 ? m->zt[l] : m->z2t[l];
   OP("pvjp_prepare", sj_pvjp_prepare(s, xt, ldt, d, M, m->vjp_q, R, m->vjp_rows, k, m->vjp_inverse,
-                                     m->vjp_left[kind][l], nullptr, m->vjp_eh, m->vjp_el, ldt, m->ws, m->ws_bytes));
-  uint16_t* const* dyp = kind == 0 ? m->qp : m->gp;
-  OP("pvjp_coefficients", sj_pvjp_vjp(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dyp[2], dyp[3], ldt, width,
-                                      m->vjp_coeff[kind][l], width, m->ws, m->ws_bytes));
+                                     m->vjp_left[kind][l], nullptr, m->vjp_eh, m->vjp_el, ldt, ws, wsb));
+  OP("pvjp_coefficients", sj_pvjp_vjp(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dyt[0], dyt[1], ldt, width,
+                                      m->vjp_coeff[kind][l], width, ws, wsb));
   return SJ_OK;
 }
 
@@ -481,23 +487,66 @@ int backward(sj_model* m) {
     void* ws = m->ws;
     const size_t wsb = m->ws_bytes;
     uint16_t **rp = m->rp, **xp = m->xp, **qp = m->qp, **gp = m->gp;
-    OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[m->L], W + m->final_norm, m->dz, nullptr, m->dres[cur],
-                                       G + m->final_norm, rp[0], rp[1], rp[2], rp[3], ldt, M, d, eps, ws, wsb));
+    // second stream for the dW side (eager per-op profiling keeps one stream)
+    const bool two = !m->profiling;
+    hipStream_t s2 = two ? m->stream2 : s;
+    void* ws2 = two ? m->ws2 : ws;
+    enum { KR = 0, KG = 1, KX = 2, KQ = 3 };
+    auto written = [&](int k, int p) -> int {  // s2 may read planes (k, p) from here on
+      if (!two) return SJ_OK;
+      SJ_HIP(hipEventRecord(m->ev_w[k][p], s));
+      SJ_HIP(hipStreamWaitEvent(s2, m->ev_w[k][p], 0));
+      return SJ_OK;
+    };
+    auto read = [&](int k, int p) -> int {  // s2 is done with planes (k, p)
+      if (!two) return SJ_OK;
+      SJ_HIP(hipEventRecord(m->ev_r[k][p], s2));
+      return SJ_OK;
+    };
+    auto reuse = [&](int k, int p) -> int {  // the dX chain may overwrite planes (k, p)
+      if (!two) return SJ_OK;
+      SJ_HIP(hipStreamWaitEvent(s, m->ev_r[k][p], 0));
+      return SJ_OK;
+    };
+    if (two) {
+      SJ_HIP(hipEventRecord(m->ev_fork, s));
+      SJ_HIP(hipStreamWaitEvent(s2, m->ev_fork, 0));
+      for (int k = 0; k < 4; k++)
+        for (int p = 0; p < 2; p++) TRY(read(k, p));
+    }
+    auto T = [&](int k, int p) { return m->pt[k][p]; };
+    {
+      const int p = (int)((m->L - 1) & 1);
+      TRY(reuse(KR, p));
+      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[m->L], W + m->final_norm, m->dz, nullptr,
+                                         m->dres[cur], G + m->final_norm, rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M,
+                                         d, eps, ws, wsb));
+      TRY(written(KR, p));
+    }
     for (long l = m->L - 1; l >= 0; l--) {
       const Layer& y = m->layers[l];
       const uint16_t* qkv = (const uint16_t*)m->qkv[l];
+      const int p = (int)(l & 1);
       // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
+      TRY(reuse(KG, p));
       OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, rp[0], rp[1], d, M, d, W + y.down, d, F, (const uint16_t*)m->gg[l],
-                                                (const uint16_t*)m->uu[l], F, gp[0], gp[1], 2 * F, gp[2], gp[3], ldt));
-      OP("down_dw", sj_gemm_planes(s, F, d, M, m->ht[l], nullptr, ldt, rp[2], rp[3], ldt, G + y.down, SJ_F32, d, 0, ws, wsb));
+                                                (const uint16_t*)m->uu[l], F, gp[0], gp[1], 2 * F, T(KG, p)[0],
+                                                T(KG, p)[1], ldt));
+      TRY(written(KG, p));
+      OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt, G + y.down,
+                                   SJ_F32, d, 0, ws2, wsb));
+      TRY(read(KR, p));
       OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, gp[0], gp[1], 2 * F, W + y.gu, nullptr, 2 * F, m->dz, SJ_F32, d, 0, ws,
                                       wsb));
-      if (m->group_on[1]) TRY(vjp_group(m, l, 1));
+      if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, T(KG, p)));
       if (!m->group_all[1])
-        OP("gate_up_dw", sj_gemm_planes(s, d, 2 * F, M, m->z2t[l], nullptr, ldt, gp[2], gp[3], ldt, G + y.gu, SJ_F32,
-                                        2 * F, 0, ws, wsb));
+        OP("gate_up_dw", sj_gemm_planes(s2, d, 2 * F, M, m->z2t[l], nullptr, ldt, T(KG, p)[0], T(KG, p)[1], ldt,
+                                        G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
+      TRY(read(KG, p));
+      TRY(reuse(KX, p));
       OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1, G + y.fn,
-                                         xp[0], xp[1], xp[2], xp[3], ldt, M, d, eps, ws, wsb));
+                                         xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps, ws, wsb));
+      TRY(written(KX, p));
       // x1 = x + attention_output(o)
       if (m->attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
         OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, xp[0], xp[1], d, W + y.wo, d, m->dop[0], m->dop[1], d,
@@ -505,34 +554,46 @@ int backward(sj_model* m) {
       else
         OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
                                          wsb));
-      OP("attn_out_dw", sj_gemm_planes(s, d, d, M, m->ot[l], nullptr, ldt, xp[2], xp[3], ldt, G + y.wo, SJ_F32, d, 0, ws,
-                                       wsb));
+      OP("attn_out_dw", sj_gemm_planes(s2, d, d, M, m->ot[l], nullptr, ldt, T(KX, p)[0], T(KX, p)[1], ldt, G + y.wo,
+                                       SJ_F32, d, 0, ws2, wsb));
+      TRY(read(KX, p));
+      TRY(reuse(KQ, p));
       for (int part = 1; part <= 4; part <<= 1) {
         const char* nm = part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce";
         if (m->attn_tt)
           OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, m->qkvt[l], ldt, (const uint16_t*)m->o[l], d,
                                              m->lset[l], m->dop[0], m->dop[1], d, m->dop[2], m->dop[3], ldt,
                                              m->deltat, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0], qp[1], NQ,
-                                             qp[2], qp[3], ldt, ws, wsb));
+                                             T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
         else
           OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
                                             m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope,
-                                            qp[0], qp[1], NQ, qp[2], qp[3], ldt, ws, wsb));
+                                            qp[0], qp[1], NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
       }
+      TRY(written(KQ, p));
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
-      if (m->group_on[0]) TRY(vjp_group(m, l, 0));
+      if (m->group_on[0]) TRY(vjp_group(m, l, 0, s2, ws2, wsb, T(KQ, p)));
       if (!m->group_all[0])
-        OP("qkv_dw", sj_gemm_planes(s, d, NQ, M, m->zt[l], nullptr, ldt, qp[2], qp[3], ldt, G + y.qkv, SJ_F32, NQ, 0,
-                                    ws, wsb));
-      if (l > 0)
+        OP("qkv_dw", sj_gemm_planes(s2, d, NQ, M, m->zt[l], nullptr, ldt, T(KQ, p)[0], T(KQ, p)[1], ldt, G + y.qkv,
+                                    SJ_F32, NQ, 0, ws2, wsb));
+      TRY(read(KQ, p));
+      if (l > 0) {
+        const int pn = (int)((l - 1) & 1);
+        TRY(reuse(KR, pn));
         OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[l], W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
-                                           G + y.an, rp[0], rp[1], rp[2], rp[3], ldt, M, d, eps, ws, wsb));
-      else  // nothing below consumes the planes of the embedding gradient
+                                           G + y.an, rp[0], rp[1], T(KR, pn)[0], T(KR, pn)[1], ldt, M, d, eps, ws, wsb));
+        TRY(written(KR, pn));
+      } else {  // nothing below consumes the planes of the embedding gradient
         OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[l], dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
                                          eps, ws, wsb));
+      }
       cur ^= 1;
     }
     OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, M, d, m->V, nullptr, 0));
+    if (two) {  // the update reads every gradient
+      SJ_HIP(hipEventRecord(m->ev_join, s2));
+      SJ_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
+    }
     return SJ_OK;
   }
   OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->dz, nullptr, m->dres[cur], G + m->final_norm, M,
@@ -928,6 +989,14 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
       ALLOC(m->qp[i], rows * NQ * 2);
       ALLOC(m->gp[i], rows * 2 * F * 2);
     }
+    // transposed planes by layer parity: parity 0 is the set above
+    uint16_t** base[4] = {m->rp, m->gp, m->xp, m->qp};
+    const size_t cols[4] = {d, 2 * F, d, NQ};
+    for (int k = 0; k < 4; k++)
+      for (int i = 0; i < 2; i++) {
+        m->pt[k][0][i] = base[k][2 + i];
+        ALLOC(m->pt[k][1][i], cols[k] * MT * 2);
+      }
   }
   ALLOC(m->hn, M * d * es);
   ALLOC(m->logits, (size_t)m->HR * (size_t)m->Vp * 4);
@@ -1010,6 +1079,7 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   }
   m->ws_bytes = ws;
   ALLOC(m->ws, ws);
+  if (m->planes) ALLOC(m->ws2, ws);
 #undef ALLOC
   if (hipHostMalloc((void**)&m->step_host, sizeof(sj_adam_step) * sj_model::RING, 0) != hipSuccess)
     return fail_cleanup(sjh::fail(SJ_ERR_CAPACITY, "model: pinned step buffer"));
@@ -1030,6 +1100,21 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   for (auto* v : {&m->zt, &m->ot, &m->z2t, &m->ht})
     for (uint16_t* q : *v)
       if (e == hipSuccess) e = hipMemsetAsync(q, 0, (size_t)(v == &m->ht ? m->F : m->d) * (size_t)m->ldt * 2, s);
+  for (int k = 0; k < 4 && m->planes; k++)
+    for (int i = 0; i < 2; i++)
+      if (e == hipSuccess)
+        e = hipMemsetAsync(m->pt[k][1][i], 0,
+                           (size_t)m->ldt * (size_t)(k == 1 ? 2 * F : k == 3 ? m->NQKV : m->d) * 2, s);
+  if (e == hipSuccess && m->planes) {
+    e = hipStreamCreate(&m->stream2);
+    for (int k = 0; k < 4 && e == hipSuccess; k++)
+      for (int p = 0; p < 2 && e == hipSuccess; p++) {
+        e = hipEventCreateWithFlags(&m->ev_w[k][p], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_r[k][p], hipEventDisableTiming);
+      }
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
+  }
   for (int i = 2; i < 4 && m->planes; i++) {
     if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, (size_t)m->ldt * d * 2, s);
     if (e == hipSuccess) e = hipMemsetAsync(m->xp[i], 0, (size_t)m->ldt * d * 2, s);
@@ -1073,6 +1158,17 @@ extern "C" int sj_model_destroy(sj_model* m) {
   if (m->sgd_host) hipHostFree(m->sgd_host);
   for (int i = 0; i < sj_model::RING; i++)
     if (m->step_done[i]) hipEventDestroy(m->step_done[i]);
+  for (int k = 0; k < 4; k++)
+    for (int p = 0; p < 2; p++) {
+      if (m->ev_w[k][p]) hipEventDestroy(m->ev_w[k][p]);
+      if (m->ev_r[k][p]) hipEventDestroy(m->ev_r[k][p]);
+    }
+  if (m->ev_fork) hipEventDestroy(m->ev_fork);
+  if (m->ev_join) hipEventDestroy(m->ev_join);
+  if (m->stream2) {
+    hipStreamSynchronize(m->stream2);
+    hipStreamDestroy(m->stream2);
+  }
   if (m->own_stream) hipStreamDestroy(m->stream);
   delete m;
   return SJ_OK;
