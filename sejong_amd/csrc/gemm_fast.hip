@@ -685,9 +685,10 @@ int splits_for(long M, long N, long K, int bm, int bn);
 //   very long K (>= 8192) with a short output (M <= 512 or N <= 64: the
 //   token-contracted products of the parameter VJP): 64x128 tiles (64x64
 //   for N < 128) and 4..16 K slices of >= 512;
-//   dW-shaped products (K >= 2048, at most one 64x64 tile per CU): 4 K
-//   slices and the largest tile giving min(2 per CU, 4 x the 64x64 tiles)
-//   workgroups (cfg5 attention-output dW: 128x64 x 4 slices, 115 -> 90 us);
+//   dW-shaped products (K >= 2048, at most one 64x64 tile per CU): one K
+//   slice up to K = 4096, else 4, and the largest tile giving min(2 per CU,
+//   slices x the 64x64 tiles) workgroups (cfg5 attention-output dW: 128x64
+//   x 4 slices, 115 -> 90 us); SJ_GEMM_DW_SPLITS overrides the slices;
 //   split-A products (dX): 64x128 tiles when they give two per CU, else
 //   64x64 (cfg5 down dX: 662 -> 499 us; cfg2 dX: 64x64);
 //   the rest pick().
@@ -708,7 +709,15 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
       return;
     }
     if (tiles(M, N, 64, 64) <= cu && K >= 2048) {
-      splits = K / 256 < 4 ? (int)(K / 256) : 4;
+      static int dws = -1;
+      if (dws < 0) {
+        const char* e = getenv("SJ_GEMM_DW_SPLITS");  // sweeps
+        dws = e ? atoi(e) : 0;
+      }
+      // the step runs dW beside the dX chain on its own stream: one slice up to
+      // K = 4096 (cfg2: no partials pass, 2.24 -> 2.20 ms), four beyond (cfg5)
+      const int want_s = dws > 0 ? dws : (K <= 4096 ? 1 : 4);
+      splits = K / 256 < want_s ? (int)(K / 256) : want_s;
       long want = tiles(M, N, 64, 64) * splits;
       want = want < 2 * cu ? want : 2 * cu;
       const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
