@@ -31,7 +31,11 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
 # single-kernel ops and the kernel each one launches (rocprofv3 names)
-OP_KERNEL = {"attention_bwd_dkv": "k_attn_dkv_h", "attention_bwd_kv_reduce": "k_attn_kv_reduce", "attention_bwd_dq": "k_attn_dq", "attention_fwd": "k_attn_fwd",
+# op -> the one kernel it launches (where it launches exactly one), for the
+# rocprofv3 traffic lookup; attention runs the transposed-operand kernels when
+# the step keeps bf16 planes and T is a multiple of 64
+OP_KERNEL = {"attention_bwd_dkv": "k_attn2_dkv", "attention_bwd_kv_reduce": "k_attn_kv_reduce",
+             "attention_bwd_dq": "k_attn2_dq", "attention_fwd": "k_attn2_fwd",
              "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd",
              "cross_entropy": "k_cross_entropy"}
 

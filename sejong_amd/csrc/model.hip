@@ -70,6 +70,14 @@ struct TJob {
   long tiles_c;
 };
 
+// Keeps the profiled stream busy for `n` sleeps of ~8k clocks each while the
+// host enqueues a whole eager step behind it, so the event pairs around each
+// op time the GPU's work rather than the host's launch gaps.  Bounded: every
+// wave leaves after n iterations.
+__global__ __launch_bounds__(64) void k_profile_hold(int n) {
+  for (int i = 0; i < n; i++) __builtin_amdgcn_s_sleep(127);
+}
+
 __global__ __launch_bounds__(256) void k_transpose_jobs(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                         const TJob* __restrict__ jobs, int njobs) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 72];
@@ -1311,7 +1319,13 @@ extern "C" int sj_model_train_step(sj_model* m, float lr) {
 
 // the step eagerly, or captured once as a hipGraph and replayed
 static int run_step(sj_model* m) {
-  if (!m->use_graph || m->profiling) return whole_step(m);
+  if (m->profiling) {
+    // ~5 ms at 2.4 GHz: longer than the host needs to enqueue one step
+    k_profile_hold<<<1, 64, 0, m->stream>>>(1500);
+    SJ_LAUNCH_CHECK("profile hold");
+    return whole_step(m);
+  }
+  if (!m->use_graph) return whole_step(m);
   if (!m->exec) {
     SJ_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
     int st = whole_step(m);
