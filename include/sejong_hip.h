@@ -303,7 +303,8 @@ int sj_patch_broadcast_bwd(void *stream, const float *dy, long batch, long t, lo
                            float *dbos);
 
 /* The step's attention over operands its producers wrote in MFMA layout
- * (bf16, head_dim 64, t a multiple of 64): qkv [batch*t][ldqkv] (q | k | v
+ * (bf16, head_dim 64, t a multiple of 64; window as sj_attention_fwd: a
+ * query sees the `window` last positions up to itself, 0 = all): qkv [batch*t][ldqkv] (q | k | v
  * columns, q and k after RoPE) with its transpose qkv_t [(hq+2hk)*64][ldt]
  * (sj_qkv_fwd_t's second output).  Forward = hierarchy_attention
  * (hierarchy.py:7-39): o [rows][ldo], lse [rows][hq] (nullable, the
@@ -314,15 +315,15 @@ int sj_patch_broadcast_bwd(void *stream, const float *dy, long batch, long t, lo
  * dQ | dK | dV (inverse RoPE on dQ, dK) as hi/lo planes like
  * sj_attention_bwd_p; workspace sj_attention_bwd_tt_workspace_bytes. */
 int sj_attention_fwd_tt(void *stream, const uint16_t *qkv, long ldqkv, const uint16_t *qkv_t, long ldt, long batch,
-                        long t, long hq, long hk, long head_dim, uint16_t *o, long ldo, float *lse, float *lse_t,
-                        uint16_t *o_t, long ldot);
+                        long t, long hq, long hk, long head_dim, long window, uint16_t *o, long ldo, float *lse,
+                        float *lse_t, uint16_t *o_t, long ldot);
 size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long hq, long hk, long head_dim);
 int sj_attention_bwd_tt(void *stream, const uint16_t *qkv, long ldqkv, const uint16_t *qkv_t, long ldt,
                         const uint16_t *o, long ldo, const float *lse_t, const uint16_t *do_hi, const uint16_t *do_lo,
                         long lddo, const uint16_t *do_t_hi, const uint16_t *do_t_lo, long lddot, float *delta_t,
-                        long batch, long t, long hq, long hk, long head_dim, const float *rope_table, uint16_t *g_hi,
-                        uint16_t *g_lo, long ldg, uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt, void *workspace,
-                        size_t workspace_bytes);
+                        long batch, long t, long hq, long hk, long head_dim, long window, const float *rope_table,
+                        uint16_t *g_hi, uint16_t *g_lo, long ldg, uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt,
+                        void *workspace, size_t workspace_bytes);
 
 /* ---------------------------------------------------- Mixture of experts
  * The MoE FFN of Block::apply (crates/sejong-model/src/architecture.rs:
@@ -604,6 +605,31 @@ typedef struct {
 
 int sj_model_create(const sj_model_config *cfg, const sj_adam_config *adam, void *stream,
                     sj_model **out);
+/* The hierarchical byte model (ModelConfig::hierarchy, core lib.rs:83-98;
+ * architecture.rs:96-137 and 317-393): byte embedding [vocab][encoder
+ * width] -> encoder blocks (local window) -> encoder_norm -> patch mean
+ * pool (patch_size bytes) -> encoder_to_global -> cfg's blocks over
+ * ceil(sequence / patch_size) patches -> global_norm -> global_to_decoder,
+ * shifted by one patch behind global_bos's row (patch_broadcast) and added
+ * to encoder_to_decoder of the encoded bytes -> decoder blocks (local
+ * window) -> decoder_norm -> output_projection -> final_norm -> fp32 head.
+ * cfg describes the global stage (width, layers, heads, kv_heads,
+ * ffn_width) and the byte sequence; the local stages use heads = kv_heads.
+ * Parameters in the reference layout order (sj_model_param_info);
+ * input_projection (used only by injected inputs) keeps a zero gradient.
+ * AdamW only.  sj_model_export_activations packs, per stage, the per-layer
+ * activations, the stage's last residual and its closing-norm output, then
+ * the pooled patches, global_to_decoder's output, the projected BOS row,
+ * the broadcast rows, encoder_to_decoder's output, output_projection's
+ * output and the final-norm output, then the logits. */
+typedef struct {
+  long patch_size;
+  long encoder_width, encoder_layers, encoder_heads, encoder_ffn_width;
+  long decoder_width, decoder_layers, decoder_heads, decoder_ffn_width;
+  long local_window; /* a byte sees the local_window last positions up to itself */
+} sj_hierarchy_config;
+int sj_model_create_hierarchy(const sj_model_config *cfg, const sj_hierarchy_config *hierarchy,
+                              const sj_adam_config *adam, void *stream, sj_model **out);
 /* SGD step driver (control_variate.rs:503-877 with accumulation 1 and no
  * control-variate blocks): forward, backward, FP64 norm of the compact
  * gradients and clip, GradientPlan::update W = W (1 - lr wd [ndim>1]) -

@@ -77,6 +77,9 @@ def _declare(L):
     L.or_model_fwd_bwd.restype = ctypes.c_double
     L.or_model_loss.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _D, _I, _I]
     L.or_model_loss.restype = ctypes.c_double
+    L.or_stage_acts_count.argtypes = [_L] * 7; L.or_stage_acts_count.restype = _L
+    L.or_stage_forward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _L, _D, _D, _D]
+    L.or_stage_backward.argtypes = [_L] * 7 + [ctypes.c_double] * 2 + [ctypes.c_int, _L, _D, _D, _D, _D, _D]
     L.or_num_threads.restype = ctypes.c_int
 
 
@@ -343,6 +346,34 @@ def acts_layout(cfg):
                 ("u", l, M * F), ("h", l, M * F)]
     out += [("xL", -1, M * d), ("hn", -1, M * d), ("logits", -1, M * VOCAB)]
     return out
+
+
+def stage_acts_count(cfg):
+    return lib().or_stage_acts_count(*_dims(cfg))
+
+
+def stage_forward(cfg, sparams, x_in, dtype="f32"):
+    """One stage of the hierarchical model (or_stage_forward): cfg as the
+    model's plus "window"; sparams = the stage's tensors in stage_layout
+    order then its closing norm; x_in [M][d].  Returns the stage's
+    activation pack (per layer as acts_layout, then the last residual and
+    the closing norm's output)."""
+    sparams, pp = _d(sparams); x_in, px = _d(x_in)
+    acts, pa = _out(stage_acts_count(cfg))
+    lib().or_stage_forward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0), DTYPE_CODE[dtype],
+                           cfg.get("window", 0), pp, px, pa)
+    return acts
+
+
+def stage_backward(cfg, sparams, acts, dz, dtype="f32"):
+    """(gradients in the sparams layout, d(stage input)) from d(closing
+    norm output) dz [M][d]."""
+    sparams, pp = _d(sparams); acts, pa = _d(acts); dz, pd = _d(dz)
+    grads, pg = _out(sparams.size)
+    dx, pdx = _out((cfg["T"] * cfg["B"], cfg["d"]))
+    lib().or_stage_backward(*_dims(cfg), cfg.get("eps", 1e-6), cfg.get("theta", 10000.0), DTYPE_CODE[dtype],
+                            cfg.get("window", 0), pp, pa, pd, pg, pdx)
+    return grads, dx
 
 
 def model_loss(cfg, params, ids, targets, dtype="f32"):

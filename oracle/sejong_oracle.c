@@ -471,6 +471,7 @@ typedef struct {
     long d, layers, hq, hk, ffn, T, B;
     double eps, theta;
     int dtype; /* 0 f32, 4 bf16, negative = no rounding (exact FP64) */
+    long window; /* local causal window of the hierarchical stages (0: none) */
 } or_model_cfg;
 
 static long or_param_count_internal(const or_model_cfg *c) {
@@ -480,7 +481,7 @@ static long or_param_count_internal(const or_model_cfg *c) {
 }
 
 long or_model_param_count(long d, long layers, long hq, long hk, long ffn) {
-    or_model_cfg c = {d, layers, hq, hk, ffn, 1, 1, 0, 0, 0};
+    or_model_cfg c = {d, layers, hq, hk, ffn, 1, 1, 0, 0, 0, 0};
     return or_param_count_internal(&c);
 }
 
@@ -576,23 +577,18 @@ static void view_acts(const or_model_cfg *c, double *acts, layer_view *lv, doubl
 
 #define ALLOC(n) ((double *)malloc(sizeof(double) * (size_t)(n)))
 
-/* Forward of Block::apply per layer + head, writing the activation pack
- * (rounded to the storage dtype where the reference kernels store). */
-void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
-                      double theta, int dtype, const double *params, const int32_t *ids, double *acts) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
-    const long M = T * B, V = OR_VOCAB, Dh = d / hq, J = Dh * hk, F = ffn;
-    plan_t pl;
-    make_plan(&cf, params, &pl);
-    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
-    double *xl, *hn, *logits;
-    view_acts(&cf, acts, lv, &xl, &hn, &logits);
+/* Block::apply per layer from lv[0].x (architecture.rs:200-247, window as
+ * hierarchy.py:24), then the closing norm into hn, rounded to the storage
+ * dtype where the reference kernels store. */
+static void body_forward(const or_model_cfg *c, const plan_t *pl, layer_view *lv, double *xl, double *hn) {
+    const long d = c->d, layers = c->layers, hq = c->hq, hk = c->hk, T = c->T, B = c->B;
+    const long M = T * B, Dh = d / hq, J = Dh * hk, F = c->ffn;
+    const double eps = c->eps, theta = c->theta;
+    const int dtype = c->dtype, rd = dtype < 0 ? -1 : 0; /* fp32 storage of LSE */
     double *q = ALLOC(M * d), *k = ALLOC(M * J), *tmp = ALLOC(M * (d > F ? d : F));
-    const int rd = dtype < 0 ? -1 : 0; /* fp32 storage of LSE / logits */
-    or_embedding_fwd(pl.C + pl.off_emb, ids, lv[0].x, M, d);
     for (long l = 0; l < layers; l++) {
         layer_view *a = &lv[l];
-        lw *y = &pl.L[l];
+        const lw *y = &pl->L[l];
         double *xnext = (l + 1 < layers) ? lv[l + 1].x : xl;
         or_rmsnorm_fwd(a->x, y->an, a->z, M, d, eps); or_round(a->z, M * d, dtype);
         or_matmul(a->z, y->wq, q, M, d, d, 0, 0); or_round(q, M * d, dtype);
@@ -600,7 +596,7 @@ void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, l
         or_matmul(a->z, y->wv, a->v, M, J, d, 0, 0); or_round(a->v, M * J, dtype);
         or_rope(q, a->qr, M, T, hq, Dh, 0, theta, 0); or_round(a->qr, M * d, dtype);
         or_rope(k, a->kr, M, T, hk, Dh, 0, theta, 0); or_round(a->kr, M * J, dtype);
-        or_attention_fwd(a->qr, a->kr, a->v, a->o, a->lse, B, T, hq, hk, Dh, 0);
+        or_attention_fwd(a->qr, a->kr, a->v, a->o, a->lse, B, T, hq, hk, Dh, c->window);
         or_round(a->o, M * d, dtype); or_round(a->lse, M * hq, rd);
         or_matmul(a->o, y->wo, tmp, M, d, d, 0, 0); or_round(tmp, M * d, dtype);
         for (long i = 0; i < M * d; i++) a->x1[i] = a->x[i] + tmp[i];
@@ -613,11 +609,28 @@ void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, l
         for (long i = 0; i < M * d; i++) xnext[i] = a->x1[i] + tmp[i];
         or_round(xnext, M * d, dtype);
     }
-    or_rmsnorm_fwd(xl, pl.C + pl.off_final, hn, M, d, eps);
+    or_rmsnorm_fwd(xl, pl->C + pl->off_final, hn, M, d, eps);
     or_round(hn, M * d, dtype); /* then cast to F32: exact */
+    free(q); free(k); free(tmp);
+}
+
+/* Forward of Block::apply per layer + head, writing the activation pack
+ * (rounded to the storage dtype where the reference kernels store). */
+void or_model_forward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
+                      double theta, int dtype, const double *params, const int32_t *ids, double *acts) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, 0};
+    const long M = T * B, V = OR_VOCAB;
+    plan_t pl;
+    make_plan(&cf, params, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, acts, lv, &xl, &hn, &logits);
+    const int rd = dtype < 0 ? -1 : 0; /* fp32 storage of the logits */
+    or_embedding_fwd(pl.C + pl.off_emb, ids, lv[0].x, M, d);
+    body_forward(&cf, &pl, lv, xl, hn);
     or_matmul(hn, params + pl.off_out, logits, M, V, d, 0, 0);
     or_round(logits, M * V, rd);
-    free(q); free(k); free(tmp); free(lv); free(pl.L); free(pl.C);
+    free(lv); free(pl.L); free(pl.C);
 }
 
 /* Backward (graph.rs:567-911 in one block's fixed order) from an
@@ -679,7 +692,7 @@ static void body_backward(const or_model_cfg *c, const plan_t *pl, layer_view *l
         /* x1 = x + attention_output(o) */
         or_matmul(dx1, y->wo, dO, M, d, d, 0, 1);
         or_matmul(a->o, dx1, grads + y->o_wo, d, d, M, 1, 0);
-        or_attention_bwd(a->qr, a->kr, a->v, a->o, a->lse, dO, dqr, dkr, dv, NULL, B, T, hq, hk, Dh, 0);
+        or_attention_bwd(a->qr, a->kr, a->v, a->o, a->lse, dO, dqr, dkr, dv, NULL, B, T, hq, hk, Dh, c->window);
         or_rope(dqr, dq, M, T, hq, Dh, 0, theta, 1);
         or_rope(dkr, dk, M, T, hk, Dh, 0, theta, 1);
         if (dyl) {
@@ -710,7 +723,7 @@ double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, lo
                              double theta, int dtype, const double *params, const double *acts_in,
                              const int32_t *ids, const int32_t *targets, double *grads, double *loss_rows,
                              double *dys) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, 0};
     const long M = T * B, V = OR_VOCAB;
     plan_t pl;
     make_plan(&cf, params, &pl);
@@ -744,7 +757,7 @@ double or_model_backward_dys(long d, long layers, long hq, long hk, long ffn, lo
 void or_model_backward_hidden(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps,
                               double theta, int dtype, const double *params, const double *acts_in,
                               const double *dh, double *grads, double *demb) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, 0};
     const long M = T * B;
     plan_t pl;
     make_plan(&cf, params, &pl);
@@ -756,6 +769,70 @@ void or_model_backward_hidden(long d, long layers, long hq, long hk, long ffn, l
     memcpy(dx, dh, sizeof(double) * (size_t)(M * d));
     body_backward(&cf, &pl, lv, xl, dx, NULL, grads, NULL, demb);
     free(dx); free(lv); free(pl.L); free(pl.C);
+}
+
+/* One stage of the hierarchical model (architecture.rs:368-393): a run of
+ * blocks with its own width, heads, FFN, sequence and local window, closed
+ * by its norm.  sparams: per layer the nine tensors in stage_layout order
+ * (architecture.rs:63-95), then the closing norm [d].  The activation pack
+ * is the model's per-layer pack followed by the stage's last residual and
+ * the closing norm's output. */
+static double *stage_padded(const or_model_cfg *c, const double *sparams, long *total) {
+    const long d = c->d, V = OR_VOCAB;
+    long n = or_param_count_internal(c);
+    long body = n - V * d - d - d * V; /* layer tensors */
+    double *p = (double *)calloc((size_t)n, sizeof(double));
+    memcpy(p + V * d, sparams, sizeof(double) * (size_t)(body + d));
+    *total = n;
+    return p;
+}
+
+long or_stage_acts_count(long d, long layers, long hq, long hk, long ffn, long T, long B) {
+    long M = T * B, J = d / hq * hk;
+    return layers * (6 * M * d + 2 * M * J + M * hq + 3 * M * ffn) + 2 * M * d;
+}
+
+void or_stage_forward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps, double theta,
+                      int dtype, long window, const double *sparams, const double *x_in, double *acts) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, window};
+    long total;
+    double *padded = stage_padded(&cf, sparams, &total);
+    plan_t pl;
+    make_plan(&cf, padded, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)(layers > 0 ? layers : 1), sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, acts, lv, &xl, &hn, &logits);
+    const long M = T * B;
+    if (layers > 0) memcpy(lv[0].x, x_in, sizeof(double) * (size_t)(M * d));
+    else memcpy(xl, x_in, sizeof(double) * (size_t)(M * d));
+    if (layers > 0) body_forward(&cf, &pl, lv, xl, hn);
+    else {
+        or_rmsnorm_fwd(xl, pl.C + pl.off_final, hn, M, d, eps);
+        or_round(hn, M * d, dtype);
+    }
+    free(lv); free(pl.L); free(pl.C); free(padded);
+}
+
+/* dz = d(closing norm output) [M][d]; grads: the stage's tensors (sparams
+ * layout); dx_in: d(stage input). */
+void or_stage_backward(long d, long layers, long hq, long hk, long ffn, long T, long B, double eps, double theta,
+                       int dtype, long window, const double *sparams, const double *acts_in, const double *dz,
+                       double *grads, double *dx_in) {
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, window};
+    long total;
+    double *padded = stage_padded(&cf, sparams, &total);
+    plan_t pl;
+    make_plan(&cf, padded, &pl);
+    layer_view *lv = (layer_view *)calloc((size_t)layers, sizeof(layer_view));
+    double *xl, *hn, *logits;
+    view_acts(&cf, (double *)acts_in, lv, &xl, &hn, &logits);
+    const long M = T * B, V = OR_VOCAB;
+    double *g = (double *)calloc((size_t)total, sizeof(double));
+    double *dx = ALLOC(M * d);
+    memcpy(dx, dz, sizeof(double) * (size_t)(M * d));
+    body_backward(&cf, &pl, lv, xl, dx, NULL, g, NULL, dx_in);
+    memcpy(grads, g + V * d, sizeof(double) * (size_t)(total - V * d - d * V));
+    free(dx); free(g); free(lv); free(pl.L); free(pl.C); free(padded);
 }
 
 /* One training forward+backward.  params: reference layout (above), fp32
@@ -786,7 +863,7 @@ double or_model_loss(long d, long layers, long hq, long hk, long ffn, long T,
                      long B, double eps, double theta, int dtype,
                      const double *params, const int32_t *ids,
                      const int32_t *targets) {
-    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype};
+    or_model_cfg cf = {d, layers, hq, hk, ffn, T, B, eps, theta, dtype, 0};
     long n = or_param_count_internal(&cf);
     double *g = (double *)malloc(sizeof(double) * (size_t)n);
     double loss = or_model_fwd_bwd(d, layers, hq, hk, ffn, T, B, eps, theta, dtype,

@@ -46,6 +46,12 @@ class ModelConfig(ctypes.Structure):
                 ("rope_theta", _F), ("precision", _I)]
 
 
+class HierarchyConfig(ctypes.Structure):
+    _fields_ = [("patch_size", _L), ("encoder_width", _L), ("encoder_layers", _L), ("encoder_heads", _L),
+                ("encoder_ffn_width", _L), ("decoder_width", _L), ("decoder_layers", _L), ("decoder_heads", _L),
+                ("decoder_ffn_width", _L), ("local_window", _L)]
+
+
 class AdamConfig(ctypes.Structure):
     _fields_ = [("beta1", _F), ("beta2", _F), ("epsilon", _F), ("weight_decay", _F),
                 ("clip_norm", _F), ("loss_scale", _F), ("clip_enabled", _I)]
@@ -134,9 +140,9 @@ SIGNATURES = {
     "sj_down_bwd_swiglu": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _P, _L, _I, _P, _L]),
     "sj_gemm_planes_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_gemm_planes": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
-    "sj_attention_fwd_tt": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _L]),
+    "sj_attention_fwd_tt": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _L]),
     "sj_attention_bwd_tt_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
-    "sj_attention_bwd_tt": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P,
+    "sj_attention_bwd_tt": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P,
                                  _P, _P, _L, _P, _P, _L, _P, _S]),
     "sj_gemm_planes_split_out": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _P, _L, _P, _P, _L]),
     "sj_qkv_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _P, _L, _L, _P, _L]),
@@ -161,6 +167,8 @@ SIGNATURES = {
     "sj_patch_broadcast": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _P]),
     "sj_patch_broadcast_bwd": (_I, [_P, _P, _L, _L, _L, _L, _P, _P]),
     "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
+    "sj_model_create_hierarchy": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(HierarchyConfig),
+                                       ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_materialize_grads": (_I, [_P]),
     "sj_model_create_value": (_I, [ctypes.POINTER(ModelConfig), _L, ctypes.POINTER(AdamConfig),

@@ -91,6 +91,7 @@ struct TArgs {
   const bf16_t* qkvt;  // [NQKV][ldt]
   long ldt;
   int T, HQ, HK;
+  int window;  // keys visible to a query: the `window` last positions up to it (0: every earlier one)
   // forward
   bf16_t* o;  // [M][ldo]
   long ldo;
@@ -158,16 +159,20 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
 #pragma unroll
   for (int d = 0; d < 4; d++) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
+  // first key block any query of this block sees (window: keys myq-window+1 .. myq)
+  const int W = a.window;
+  const int kb0 = W > 0 && qb * QB - W + 1 > 0 ? (qb * QB - W + 1) / QB : 0;
   wait_vm<0>();  // the fragments above are in registers before the DMA stream starts
 
 #pragma unroll
   for (int s = 0; s < NST - 1; s++)
-    if (s <= qb) issue(s, s);
-  for (int kb = 0; kb <= qb; kb++) {
+    if (kb0 + s <= qb) issue(kb0 + s, s);
+  for (int kb = kb0; kb <= qb; kb++) {
+    const int it = kb - kb0;
     if (kb < qb) wait_vm<4>(); else wait_vm<0>();
     block_barrier();
-    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (kb + NST - 1) % NST);
-    const bf16_t* sK = lds + (kb % NST) * 2 * TILE;
+    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (it + NST - 1) % NST);
+    const bf16_t* sK = lds + (it % NST) * 2 * TILE;
     const bf16_t* sVt = sK + TILE;
     f32x4 st[4];
 #pragma unroll
@@ -184,6 +189,13 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
         for (int r = 0; r < 4; r++)
           if (32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r > qloc) st[sb][r] = -INFINITY;
     }
+    if (W > 0 && kb * QB < qb * QB + QB - W) {  // keys before some query's window
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (kb * QB + 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r < myq - W + 1) st[sb][r] = -INFINITY;
+    }
     float bm = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
                      fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
     bm = fmaxf(bm, fmaxf(fmaxf(fmaxf(st[2][0], st[2][1]), fmaxf(st[2][2], st[2][3])),
@@ -191,13 +203,16 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mnew = fmaxf(m, bm * sc);
-    const float alpha = fexp2(m - mnew);
+    // a row whose keys so far are all outside its window keeps m = -inf: its
+    // terms are exp2(-inf) = 0 against the reference point 0
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = fexp2(m - mref);
     float pr[4][4], ps = 0.f;
 #pragma unroll
     for (int sb = 0; sb < 4; sb++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        pr[sb][r] = fexp2(fmaf(st[sb][r], sc, -mnew));
+        pr[sb][r] = fexp2(fmaf(st[sb][r], sc, -mref));
         ps += pr[sb][r];
       }
     ps += __shfl_xor(ps, 16, 64);
@@ -293,15 +308,19 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
   f32x4 dq[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int W = a.window;
+  const int kb0 = W > 0 && qb * QB - W + 1 > 0 ? (qb * QB - W + 1) / QB : 0;
+  const bool low_edge_possible = W > 0;
   wait_vm<0>();
 #pragma unroll
   for (int s = 0; s < NST - 1; s++)
-    if (s <= qb) issue(s, s);
-  for (int kb = 0; kb <= qb; kb++) {
+    if (kb0 + s <= qb) issue(kb0 + s, s);
+  for (int kb = kb0; kb <= qb; kb++) {
+    const int it = kb - kb0;
     if (kb < qb) wait_vm<6>(); else wait_vm<0>();
     block_barrier();
-    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (kb + NST - 1) % NST);
-    const bf16_t* sK = lds + (kb % NST) * 3 * TILE;
+    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (it + NST - 1) % NST);
+    const bf16_t* sK = lds + (it % NST) * 3 * TILE;
     const bf16_t* sV = sK + TILE;
     const bf16_t* sKt = sK + 2 * TILE;
     float ds[4][4];
@@ -319,7 +338,9 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         float p = fexp2(fmaf(st[r], sc, -lse2));
-        if (kb == qb && 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r > qloc) p = 0.f;
+        const int kk = 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r;
+        if (kb == qb && kk > qloc) p = 0.f;
+        if (low_edge_possible && kb * QB + kk < myq - W + 1) p = 0.f;
         ds[sb][r] = p * (dp[r] - delta) * 0.125f;
       }
     }
@@ -419,7 +440,10 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
   f32x4 dk[4], dv[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int nqb = T / QB;
+  // last query block that sees a key of this block (window: queries key .. key+window-1)
+  const int W = a.window;
+  int nqb = T / QB;
+  if (W > 0 && (kb * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (kb * QB + QB - 1 + W - 1) / QB + 1;
   wait_vm<0>();
 #pragma unroll
   for (int s = 0; s < NST - 1; s++)
@@ -460,6 +484,7 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
       for (int r = 0; r < 4; r++) {
         float p = fexp2(fmaf(st[r], sc, -lv[r] * LOG2E));
         if (qb == kb && q4 + r < kloc) p = 0.f;
+        if (W > 0 && qb * QB + q4 + r > kb * QB + kloc + W - 1) p = 0.f;
         pp[sb][r] = p;
         ds[sb][r] = p * (dp[r] - dv4[r]) * 0.125f;
       }
@@ -516,8 +541,8 @@ int sjh::attention_t_prepare() {
 }
 
 static int check_t(const void* qkv, long ldqkv, const void* qkvt, long ldt, long batch, long t, long hq, long hk,
-                   long head_dim) {
-  SJ_REQUIRE(qkv && qkvt && batch > 0 && t > 0 && t % QB == 0 && hq > 0 && hk > 0 && hq % hk == 0 &&
+                   long head_dim, long window) {
+  SJ_REQUIRE(qkv && qkvt && batch > 0 && t > 0 && t % QB == 0 && hq > 0 && hk > 0 && hq % hk == 0 && window >= 0 &&
                  head_dim == DH && ldqkv >= (hq + 2 * hk) * DH && ldqkv % 8 == 0 && ldt >= batch * t &&
                  ldt % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)qkvt & 15) == 0 &&
                  t * ldqkv < (1L << 31),
@@ -527,15 +552,15 @@ static int check_t(const void* qkv, long ldqkv, const void* qkvt, long ldt, long
 }
 
 extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
-                                   long batch, long t, long hq, long hk, long head_dim, uint16_t* o, long ldo,
-                                   float* lse, float* lse_t, uint16_t* o_t, long ldot) {
-  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim)) return st;
+                                   long batch, long t, long hq, long hk, long head_dim, long window, uint16_t* o,
+                                   long ldo, float* lse, float* lse_t, uint16_t* o_t, long ldot) {
+  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim, window)) return st;
   SJ_REQUIRE(o && lse_t && ldo >= hq * DH && ldo % 8 == 0 && ((uintptr_t)o & 15) == 0 && (!o_t || ldot >= batch * t),
              "grouped attention: outputs");
   if (int st = sjh::attention_t_prepare()) return st;
   TArgs a = {};
   a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
-  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk;
+  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk; a.window = window < t ? (int)window : 0;
   a.o = (bf16_t*)o; a.ldo = ldo; a.lse = lse; a.lse_t = lse_t; a.ot = (bf16_t*)o_t; a.ldot = ldot;
   hipLaunchKernelGGL(k_attn2_fwd, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
                      (hipStream_t)stream, a);
@@ -551,9 +576,10 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
                                 long ldt, const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
                                 const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
                                 long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                                const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
-                                uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
-  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim)) return st;
+                                long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                                uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace,
+                                size_t workspace_bytes) {
+  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim, window)) return st;
   SJ_REQUIRE(o && lse_t && do_hi && do_lo && do_t_hi && do_t_lo && delta_t && g_hi && g_lo && g_t_hi && g_t_lo &&
                  lddo >= hq * DH && lddo % 8 == 0 && lddot >= batch * t && lddot % 8 == 0 && ldo % 8 == 0 &&
                  ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ((uintptr_t)do_hi & 15) == 0 &&
@@ -568,7 +594,7 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   hipStream_t s = (hipStream_t)stream;
   TArgs a = {};
   a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
-  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk;
+  a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk; a.window = window < t ? (int)window : 0;
   a.ob = (const bf16_t*)o; a.ldo = ldo;
   a.dh = (const bf16_t*)do_hi; a.dl = (const bf16_t*)do_lo; a.lddo = lddo;
   a.dth = (const bf16_t*)do_t_hi; a.dtl = (const bf16_t*)do_t_lo; a.lddot = lddot;
@@ -598,9 +624,10 @@ extern "C" int sj_attention_bwd_tt(void* stream, const uint16_t* qkv, long ldqkv
                                    const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
                                    const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
                                    long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                                   const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
-                                   uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+                                   long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                                   uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace,
+                                   size_t workspace_bytes) {
   return sjh::attention_bwd_tt_parts(7, stream, qkv, ldqkv, qkv_t, ldt, o, ldo, lse_t, do_hi, do_lo, lddo, do_t_hi,
-                                     do_t_lo, lddot, delta_t, batch, t, hq, hk, head_dim, rope_table, g_hi, g_lo, ldg,
-                                     g_t_hi, g_t_lo, ldgt, workspace, workspace_bytes);
+                                     do_t_lo, lddot, delta_t, batch, t, hq, hk, head_dim, window, rope_table, g_hi,
+                                     g_lo, ldg, g_t_hi, g_t_lo, ldgt, workspace, workspace_bytes);
 }

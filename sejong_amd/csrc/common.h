@@ -118,8 +118,8 @@ int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ld
                            const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
                            const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
                            long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                           const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
-                           uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
+                           long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
+                           uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);

@@ -21,6 +21,13 @@
 //               to 8, padding columns stay zero)
 // Exchange with the host uses the reference layout (architecture.rs:63-137).
 //
+// The hierarchical byte model (cfg3: ModelConfig::hierarchy, architecture.rs:
+// 368-393) runs three stages through the same per-layer code: the byte
+// encoder (local window), the global stack over patches and the byte decoder
+// (local window), each a run of blocks with its own widths and sequence and
+// its closing norm, joined by patch pooling / broadcast and the projections
+// between the widths.
+//
 // bf16 steps run the MFMA-layout kernels: every GEMM operand is streamed
 // k-contiguous, so the step keeps, next to the bf16 mirror, a transposed
 // mirror of the four projection matrices per layer (forward B operands,
@@ -60,6 +67,24 @@ struct RefTensor {
 
 struct Layer {
   long an, fn, qkv, wo, gu, down;  // internal offsets
+  int stage = 0;
+};
+
+// One run of blocks and its closing norm: the dense model has one (closed by
+// the final norm); the hierarchical model has the encoder (closed by
+// encoder_norm), the global stack (global_norm) and the decoder
+// (decoder_norm).  Layer l of stage s reads x[l + s] and writes x[l + s + 1].
+struct Stage {
+  std::string prefix;         // parameter names: "<prefix>.<i>.<tensor>"
+  int index = 0;
+  long first = 0, count = 0;  // layers [first, first + count)
+  long d = 0, HQ = 0, HK = 0, Dh = 0, J = 0, F = 0, NQKV = 0, T = 0, M = 0, ldt = 0;
+  long window = 0;            // local causal window (0: every earlier position)
+  long depth = 0;             // layers of the stage (initialisation scale)
+  long norm = 0;              // internal offset of the closing norm's weight
+  bool attn_tt = false;
+  float* rope = nullptr;      // RoPE table [T][Dh/2] (cos, sin)
+  void* out = nullptr;        // closing norm output [M][d], compute dtype
 };
 
 // one matrix of the batched bf16 transpose: src [rows][cols] -> dst [cols][rows]
@@ -130,6 +155,14 @@ struct sj_model {
   sj_adam_config adam;
   hipStream_t stream;
   long V, Vp, d, L, HQ, HK, Dh, J, F, T, B, M, NQKV;
+  // stages (one for the dense model); d and M above are the head's width
+  // and rows (the final norm's), the dense model's block shape otherwise
+  std::vector<Stage> stages;
+  bool hier = false;
+  long P = 0;                                   // bytes per patch
+  long h_inproj = 0, h_e2g = 0, h_e2d = 0, h_g2d = 0, h_bos = 0, h_op = 0;  // glue parameters
+  void *pooled = nullptr, *gd = nullptr, *bosd = nullptr, *zb = nullptr, *bytes = nullptr, *opo = nullptr;
+  float* hg[8] = {};                            // glue backward scratch
   // head: HV classes over HR rows (the LM head: V over all M tokens; the
   // NativeValue head: value_n classes over the B selected SEP rows); Vp =
   // HV rounded up to 8 (the head's row stride)
@@ -282,50 +315,99 @@ int prof_end(sj_model* m) {
 
 // Build reference-layout tensor list and the internal arena layout.
 void build_layout(sj_model* m) {
-  const long d = m->d, J = m->J, F = m->F, V = m->V;
-  long off = 0;
+  const long V = m->V;
+  long off = 0, ro = 0;
   m->layers.resize(m->L);
-  for (long l = 0; l < m->L; l++) {
-    m->layers[l].an = off; off = align64(off + d);
-    m->layers[l].fn = off; off = align64(off + d);
-  }
-  m->final_norm = off; off = align64(off + d);
-  m->n_nodecay = off;
-  m->emb = off; off = align64(off + V * d);
-  for (long l = 0; l < m->L; l++) {
-    m->layers[l].qkv = off; off = align64(off + d * m->NQKV);
-    m->layers[l].wo = off; off = align64(off + d * d);
-    m->layers[l].gu = off; off = align64(off + d * 2 * F);
-    m->layers[l].down = off; off = align64(off + F * d);
-  }
-  m->out = off; off = align64(off + d * m->Vp);
-  if (m->value_n) { m->bias = off; off = align64(off + m->Vp); }  // [1][n]: 2-D, so it decays
-  m->n_params = off;
-
-  long ro = 0;
   auto add = [&](const std::string& name, long rows, long cols, long ioff, long ild, int layer = -1, int kind = -1,
                  int member = -1, long col0 = 0, int ndim = 2) {
     m->tensors.push_back(RefTensor{name, rows, cols, ro, ioff, ild, layer, kind, member, col0, ndim});
     ro += rows * cols;
   };
+  // [no decay] the 1-D tensors: per layer attention_norm, ffn_norm; the
+  // closing norms; final_norm
+  for (Stage& S : m->stages)
+    for (long l = S.first; l < S.first + S.count; l++) {
+      m->layers[l].stage = S.index;
+      m->layers[l].an = off; off = align64(off + S.d);
+      m->layers[l].fn = off; off = align64(off + S.d);
+    }
+  for (Stage& S : m->stages)
+    if (m->hier) { S.norm = off; off = align64(off + S.d); }
+  m->final_norm = off; off = align64(off + m->d);
+  if (!m->hier) m->stages[0].norm = m->final_norm;
+  m->n_nodecay = off;
+  // [decay] embedding, the block matrices, the hierarchy's projections and
+  // BOS row, the head
+  m->emb = off; off = align64(off + V * m->stages[0].d);
+  for (Stage& S : m->stages)
+    for (long l = S.first; l < S.first + S.count; l++) {
+      m->layers[l].qkv = off; off = align64(off + S.d * S.NQKV);
+      m->layers[l].wo = off; off = align64(off + S.d * S.d);
+      m->layers[l].gu = off; off = align64(off + S.d * 2 * S.F);
+      m->layers[l].down = off; off = align64(off + S.F * S.d);
+    }
+  if (m->hier) {
+    const long de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d;
+    m->h_inproj = off; off = align64(off + dg * de);
+    m->h_e2g = off; off = align64(off + de * dg);
+    m->h_e2d = off; off = align64(off + de * dd);
+    m->h_g2d = off; off = align64(off + dg * dd);
+    m->h_bos = off; off = align64(off + dg);
+    m->h_op = off; off = align64(off + dd * dg);
+  }
+  m->out = off; off = align64(off + m->d * m->Vp);
+  if (m->value_n) { m->bias = off; off = align64(off + m->Vp); }  // [1][n]: 2-D, so it decays
+  m->n_params = off;
+
+  // stage_layout (architecture.rs:63-95): per layer the two norms, the four
+  // attention matrices, gate, up, down
+  auto blocks = [&](const Stage& S) {
+    const long d = S.d, J = S.J, F = S.F;
+    for (long l = S.first; l < S.first + S.count; l++) {
+      std::string p = S.prefix + "." + std::to_string(l - S.first) + ".";
+      const Layer& y = m->layers[l];
+      add(p + "attention_norm", 1, d, y.an, d, -1, -1, -1, 0, 1);
+      add(p + "ffn_norm", 1, d, y.fn, d, -1, -1, -1, 0, 1);
+      const int li = (int)l;
+      add(p + "query", d, d, y.qkv, S.NQKV, li, 0, 0, 0);
+      add(p + "key", d, J, y.qkv + d, S.NQKV, li, 0, 1, d);
+      add(p + "value", d, J, y.qkv + d + J, S.NQKV, li, 0, 2, d + J);
+      add(p + "attention_output", d, d, y.wo, d);
+      add(p + "gate", d, F, y.gu, 2 * F, li, 1, 0, 0);
+      add(p + "up", d, F, y.gu + F, 2 * F, li, 1, 1, F);
+      add(p + "down", F, d, y.down, d);
+    }
+  };
+  const long d = m->d;
+  if (m->hier) {
+    // layout (architecture.rs:96-137): embedding, encoder blocks,
+    // encoder_norm, input_projection, encoder_to_global, encoder_to_decoder,
+    // global_to_decoder, global_bos, global_norm, global blocks, decoder
+    // blocks, decoder_norm, output_projection, final_norm, output
+    const Stage &E = m->stages[0], &G = m->stages[1], &D = m->stages[2];
+    add("embedding", V, E.d, m->emb, E.d);
+    blocks(E);
+    add("encoder_norm", 1, E.d, E.norm, E.d, -1, -1, -1, 0, 1);
+    add("input_projection", G.d, E.d, m->h_inproj, E.d);
+    add("encoder_to_global", E.d, G.d, m->h_e2g, G.d);
+    add("encoder_to_decoder", E.d, D.d, m->h_e2d, D.d);
+    add("global_to_decoder", G.d, D.d, m->h_g2d, D.d);
+    add("global_bos", 1, G.d, m->h_bos, G.d);
+    add("global_norm", 1, G.d, G.norm, G.d, -1, -1, -1, 0, 1);
+    blocks(G);
+    blocks(D);
+    add("decoder_norm", 1, D.d, D.norm, D.d, -1, -1, -1, 0, 1);
+    add("output_projection", D.d, G.d, m->h_op, G.d);
+    add("final_norm", 1, d, m->final_norm, d, -1, -1, -1, 0, 1);
+    add("output", d, m->HV, m->out, m->Vp);
+    m->ref_count = ro;
+    return;
+  }
   // NativeValue::parameters (native/value.rs:89-115): the body without its
   // embedding and output, then native_embedding [259][d], native_value
   // [d][n] and native_bias [1][n]
   if (!m->value_n) add("embedding", V, d, m->emb, d);
-  for (long l = 0; l < m->L; l++) {
-    std::string p = "layers." + std::to_string(l) + ".";
-    const Layer& y = m->layers[l];
-    add(p + "attention_norm", 1, d, y.an, d, -1, -1, -1, 0, 1);
-    add(p + "ffn_norm", 1, d, y.fn, d, -1, -1, -1, 0, 1);
-    const int li = (int)l;
-    add(p + "query", d, d, y.qkv, m->NQKV, li, 0, 0, 0);
-    add(p + "key", d, J, y.qkv + d, m->NQKV, li, 0, 1, d);
-    add(p + "value", d, J, y.qkv + d + J, m->NQKV, li, 0, 2, d + J);
-    add(p + "attention_output", d, d, y.wo, d);
-    add(p + "gate", d, F, y.gu, 2 * F, li, 1, 0, 0);
-    add(p + "up", d, F, y.gu + F, 2 * F, li, 1, 1, F);
-    add(p + "down", F, d, y.down, d);
-  }
+  blocks(m->stages[0]);
   add("final_norm", 1, d, m->final_norm, d, -1, -1, -1, 0, 1);
   if (m->value_n) {
     add("native_embedding", V, d, m->emb, d);
@@ -369,50 +451,99 @@ int refresh_mirror(sj_model* m) {
 }
 
 // ---------------------------------------------------------------- forward
-int forward(sj_model* m) {
+// stored activations of layer l: its input and output on the residual stream
+void* xin(const sj_model* m, long l) { return m->x[l + m->layers[l].stage]; }
+void* xout(const sj_model* m, long l) { return m->x[l + m->layers[l].stage + 1]; }
+// the stage's last residual (the closing norm's input)
+void* xtop(const sj_model* m, const Stage& S) { return m->x[S.first + S.count + S.index]; }
+
+// Block::apply for every layer of stage si (architecture.rs:200-247), then
+// its closing norm into S.out
+int stage_forward(sj_model* m, int si) {
+  const Stage& S = m->stages[si];
   hipStream_t s = m->stream;
-  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
+  const long M = S.M, d = S.d, J = S.J, F = S.F, NQ = S.NQKV, ldt = S.ldt;
   const int dt = m->dt;
   const float eps = m->c.norm_epsilon;
-  OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, M, d));
-  for (long l = 0; l < m->L && m->planes; l++) {
+  for (long l = S.first; l < S.first + S.count && m->planes; l++) {
     const Layer& y = m->layers[l];
     uint16_t* qkv = (uint16_t*)m->qkv[l];
     const uint16_t *W = m->mirror, *WT = m->mirror_t;
-    const uint16_t *x = (const uint16_t*)m->x[l], *x1 = (const uint16_t*)m->x1[l];
+    const uint16_t *x = (const uint16_t*)xin(m, l), *x1 = (const uint16_t*)m->x1[l];
     uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
     uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
-    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], m->ldt, M, d, eps));
-    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, m->rope, m->T, m->Dh,
-                                m->attn_tt ? m->qkvt[l] : nullptr, m->ldt));
-    if (m->attn_tt)
-      OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, m->qkvt[l], m->ldt, m->B, m->T, m->HQ, m->HK, m->Dh, o, d,
-                                              m->lse[l], m->lset[l], m->ot[l], m->ldt));
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], ldt, M, d, eps));
+    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, S.rope, S.T, S.Dh,
+                                S.attn_tt ? m->qkvt[l] : nullptr, ldt));
+    if (S.attn_tt)
+      OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, m->qkvt[l], ldt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, o,
+                                              d, m->lse[l], m->lset[l], m->ot[l], ldt));
     else
       OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l],
-                                             m->ldt, m->B, m->T, m->HQ, m->HK, m->Dh));
+                                             ldt, m->B, S.T, S.HQ, S.HK, S.Dh));
     OP("attn_out_residual", sj_linear_residual_fwd_t(s, o, d, M, d, WT + y.wo, d, d, x, d, (uint16_t*)m->x1[l], d));
-    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], m->ldt, M, d, eps));
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], ldt, M, d, eps));
     OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F, m->ht[l],
-                                          m->ldt));
-    OP("down_residual", sj_linear_residual_fwd_t(s, hh, F, M, F, WT + y.down, F, d, x1, d, (uint16_t*)m->x[l + 1], d));
+                                          ldt));
+    OP("down_residual", sj_linear_residual_fwd_t(s, hh, F, M, F, WT + y.down, F, d, x1, d, (uint16_t*)xout(m, l), d));
   }
-  for (long l = 0; l < m->L && !m->planes; l++) {
+  for (long l = S.first; l < S.first + S.count && !m->planes; l++) {
     const Layer& y = m->layers[l];
     char* qkv = (char*)m->qkv[l];
-    OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[l], dt, wc(m, y.an), dt, m->z[l], M, d, eps));
+    OP("rmsnorm", sj_rmsnorm_fwd(s, xin(m, l), dt, wc(m, y.an), dt, m->z[l], M, d, eps));
     const char* wq = (const char*)wc(m, y.qkv);
     OP("qkv_rope", sj_qkv_fwd(s, m->z[l], d, M, d, wq, NQ, wq + d * m->esz, NQ, wq + (d + J) * m->esz, NQ, d, J, qkv, NQ,
-                   qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, dt, m->rope, m->T, m->Dh));
-    OP("attention_fwd", sj_attention_fwd(s, qkv, NQ, qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, m->o[l], d, m->lse[l], dt, m->B,
-                         m->T, m->HQ, m->HK, m->Dh, 0));
-    OP("attn_out_residual", sj_linear_residual_fwd(s, m->o[l], d, M, d, wc(m, y.wo), d, d, m->x[l], d, m->x1[l], d, dt));
+                   qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, dt, S.rope, S.T, S.Dh));
+    OP("attention_fwd", sj_attention_fwd(s, qkv, NQ, qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, m->o[l], d,
+                                         m->lse[l], dt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window));
+    OP("attn_out_residual", sj_linear_residual_fwd(s, m->o[l], d, M, d, wc(m, y.wo), d, d, xin(m, l), d, m->x1[l], d, dt));
     OP("rmsnorm", sj_rmsnorm_fwd(s, m->x1[l], dt, wc(m, y.fn), dt, m->z2[l], M, d, eps));
     const char* wg = (const char*)wc(m, y.gu);
     OP("gate_up_swiglu", sj_gate_up_fwd(s, m->z2[l], d, M, d, wg, 2 * F, wg + F * m->esz, 2 * F, F, m->gg[l], m->uu[l], m->hh[l], F, dt));
-    OP("down_residual", sj_linear_residual_fwd(s, m->hh[l], F, M, F, wc(m, y.down), d, d, m->x1[l], d, m->x[l + 1], d, dt));
+    OP("down_residual", sj_linear_residual_fwd(s, m->hh[l], F, M, F, wc(m, y.down), d, d, m->x1[l], d, xout(m, l), d, dt));
   }
-  OP("rmsnorm", sj_rmsnorm_fwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->hn, M, d, eps));
+  OP("rmsnorm", sj_rmsnorm_fwd(s, xtop(m, S), dt, wc(m, S.norm), dt, S.out, M, d, eps));
+  return SJ_OK;
+}
+
+// hidden_from_encoded (architecture.rs:368-393) after the encoder stage:
+// pool the encoded bytes into patches, encoder_to_global, the global stage,
+// global_to_decoder of its output and of the BOS row, the shift-by-one-patch
+// broadcast added to encoder_to_decoder of the encoded bytes, the decoder
+// stage, output_projection and the final norm (into hn).  Every product
+// stores in the compute dtype (Graph::matmul, graph.rs:212-221).
+int hierarchy_forward(sj_model* m) {
+  hipStream_t s = m->stream;
+  const int dt = m->dt;
+  const float eps = m->c.norm_epsilon;
+  const Stage &E = m->stages[0], &G = m->stages[1], &D = m->stages[2];
+  const long B = m->B, P = m->P, de = E.d, dg = G.d, dd = D.d, Ml = E.M, Mg = G.M;
+  void* ws = m->ws;
+  const size_t wsb = m->ws_bytes;
+  OP("patch_pool", sj_patch_pool(s, E.out, dt, B, E.T, de, P, m->pooled));
+  OP("encoder_to_global", sj_gemm(s, 0, 0, Mg, dg, de, m->pooled, dt, de, wc(m, m->h_e2g), dt, dg, xin(m, G.first), dt,
+                                  dg, 0, ws, wsb));
+  TRY(stage_forward(m, 1));
+  OP("global_to_decoder", sj_gemm(s, 0, 0, Mg, dd, dg, G.out, dt, dg, wc(m, m->h_g2d), dt, dd, m->gd, dt, dd, 0, ws, wsb));
+  OP("bos_to_decoder", sj_gemm(s, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, m->bosd, dt, dd, 0,
+                               ws, wsb));
+  OP("patch_broadcast", sj_patch_broadcast(s, m->gd, m->bosd, dt, B, E.T, dd, P, m->zb));
+  OP("encoder_to_decoder", sj_gemm(s, 0, 0, Ml, dd, de, E.out, dt, de, wc(m, m->h_e2d), dt, dd, m->bytes, dt, dd, 0, ws,
+                                   wsb));
+  OP("decoder_input", sj_add(s, m->bytes, dt, m->zb, dt, xin(m, D.first), dt, Ml * dd, 1.f));
+  TRY(stage_forward(m, 2));
+  OP("output_projection", sj_gemm(s, 0, 0, Ml, dg, dd, D.out, dt, dd, wc(m, m->h_op), dt, dg, m->opo, dt, dg, 0, ws, wsb));
+  OP("rmsnorm", sj_rmsnorm_fwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->hn, Ml, dg, eps));
+  return SJ_OK;
+}
+
+int forward(sj_model* m) {
+  hipStream_t s = m->stream;
+  const long M = m->M, d = m->d;
+  const int dt = m->dt;
+  OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, m->stages[0].M, m->stages[0].d));
+  TRY(stage_forward(m, 0));
+  if (m->hier) TRY(hierarchy_forward(m));
   if (m->value_n) {
     // NativeValue::forward_batch (native/value.rs:139-146): gather the SEP
     // rows, cast to F32, affine head (matmul + bias_add), then the mean CE
@@ -465,38 +596,30 @@ int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb
 }
 
 // --------------------------------------------------------------- backward
-int backward(sj_model* m) {
+// The dW products (and parameter-VJP groups) run on a second stream beside
+// the dX chain (planes path, graph and plain eager steps; per-op profiling
+// keeps one stream).
+bool two_streams(const sj_model* m) { return m->planes && !m->profiling; }
+
+// Backward of stage si from dzin = d(closing norm output) [M][d] (fp32):
+// the closing norm, then per layer from the top down / SwiGLU / gate+up /
+// ffn norm / attention output / attention (+ inverse RoPE) / QKV /
+// attention norm (graph.rs:567-911 in one block's order).  Leaves
+// d(stage input) in m->dres[cur].
+int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
+  const Stage& S = m->stages[si];
   hipStream_t s = m->stream;
-  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
+  const long M = S.M, d = S.d, J = S.J, F = S.F, NQ = S.NQKV, ldt = S.ldt;
+  const long top = S.first + S.count - 1;
   const int dt = m->dt;
   const float eps = m->c.norm_epsilon;
   float* G = m->g;
-  if (m->value_n) {
-    // affine head backward (bias_reduce, the F32 matmul's dX / dW) and the
-    // gather's backward into the full hidden gradient (zero off the SEP rows)
-    const long R = m->HR, n = m->HV;
-    OP("value_bias_bwd", sj_bias_reduce(s, m->dlogits, m->Vp, R, n, G + m->bias));
-    OP("head_dw", sj_gemm(s, 1, 0, d, n, R, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
-                          m->ws, m->ws_bytes));
-    OP("head_dx", sj_gemm(s, 0, 1, R, d, n, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dhsel, SJ_F32,
-                          d, 0, m->ws, m->ws_bytes));
-    OP("value_scatter", sj_gather_rows_bwd(s, m->dhsel, m->sel, R, d, m->dz, d, M));
-  } else {
-  // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
-  OP("head_dx", sj_gemm(s, 0, 1, M, d, m->HV, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d, 0, m->ws,
-              m->ws_bytes));
-  OP("head_dw", sj_gemm(s, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0, m->ws,
-              m->ws_bytes));
-  }
-  int cur = 0;
   if (m->planes) {
     const uint16_t* W = m->mirror;
-    const long ldt = m->ldt;
     void* ws = m->ws;
     const size_t wsb = m->ws_bytes;
     uint16_t **rp = m->rp, **xp = m->xp, **qp = m->qp, **gp = m->gp;
-    // second stream for the dW side (eager per-op profiling keeps one stream)
-    const bool two = !m->profiling;
+    const bool two = two_streams(m);
     hipStream_t s2 = two ? m->stream2 : s;
     void* ws2 = two ? m->ws2 : ws;
     enum { KR = 0, KG = 1, KX = 2, KQ = 3 };
@@ -516,22 +639,15 @@ int backward(sj_model* m) {
       SJ_HIP(hipStreamWaitEvent(s, m->ev_r[k][p], 0));
       return SJ_OK;
     };
-    if (two) {
-      SJ_HIP(hipEventRecord(m->ev_fork, s));
-      SJ_HIP(hipStreamWaitEvent(s2, m->ev_fork, 0));
-      for (int k = 0; k < 4; k++)
-        for (int p = 0; p < 2; p++) TRY(read(k, p));
-    }
     auto T = [&](int k, int p) { return m->pt[k][p]; };
     {
-      const int p = (int)((m->L - 1) & 1);
+      const int p = (int)(top & 1);
       TRY(reuse(KR, p));
-      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[m->L], W + m->final_norm, m->dz, nullptr,
-                                         m->dres[cur], G + m->final_norm, rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M,
-                                         d, eps, ws, wsb));
+      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)xtop(m, S), W + S.norm, dzin, nullptr, m->dres[cur],
+                                         G + S.norm, rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M, d, eps, ws, wsb));
       TRY(written(KR, p));
     }
-    for (long l = m->L - 1; l >= 0; l--) {
+    for (long l = top; l >= S.first; l--) {
       const Layer& y = m->layers[l];
       const uint16_t* qkv = (const uint16_t*)m->qkv[l];
       const int p = (int)(l & 1);
@@ -556,7 +672,7 @@ int backward(sj_model* m) {
                                          xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps, ws, wsb));
       TRY(written(KX, p));
       // x1 = x + attention_output(o)
-      if (m->attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
+      if (S.attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
         OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, xp[0], xp[1], d, W + y.wo, d, m->dop[0], m->dop[1], d,
                                                    m->dop[2], m->dop[3], ldt));
       else
@@ -568,14 +684,14 @@ int backward(sj_model* m) {
       TRY(reuse(KQ, p));
       for (int part = 1; part <= 4; part <<= 1) {
         const char* nm = part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce";
-        if (m->attn_tt)
+        if (S.attn_tt)
           OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, m->qkvt[l], ldt, (const uint16_t*)m->o[l], d,
                                              m->lset[l], m->dop[0], m->dop[1], d, m->dop[2], m->dop[3], ldt,
-                                             m->deltat, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope, qp[0], qp[1], NQ,
-                                             T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
+                                             m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, S.rope, qp[0], qp[1],
+                                             NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
         else
           OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
-                                            m->lse[l], m->dO, d, m->delta, m->B, m->T, m->HQ, m->HK, m->Dh, m->rope,
+                                            m->lse[l], m->dO, d, m->delta, m->B, S.T, S.HQ, S.HK, S.Dh, S.rope,
                                             qp[0], qp[1], NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
       }
       TRY(written(KQ, p));
@@ -585,28 +701,23 @@ int backward(sj_model* m) {
         OP("qkv_dw", sj_gemm_planes(s2, d, NQ, M, m->zt[l], nullptr, ldt, T(KQ, p)[0], T(KQ, p)[1], ldt, G + y.qkv,
                                     SJ_F32, NQ, 0, ws2, wsb));
       TRY(read(KQ, p));
-      if (l > 0) {
+      if (l > S.first) {
         const int pn = (int)((l - 1) & 1);
         TRY(reuse(KR, pn));
-        OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x[l], W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
+        OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)xin(m, l), W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
                                            G + y.an, rp[0], rp[1], T(KR, pn)[0], T(KR, pn)[1], ldt, M, d, eps, ws, wsb));
         TRY(written(KR, pn));
-      } else {  // nothing below consumes the planes of the embedding gradient
-        OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[l], dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
+      } else {  // the stage input's gradient feeds row-layout consumers only
+        OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xin(m, l), dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
                                          eps, ws, wsb));
       }
       cur ^= 1;
     }
-    OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, M, d, m->V, nullptr, 0));
-    if (two) {  // the update reads every gradient
-      SJ_HIP(hipEventRecord(m->ev_join, s2));
-      SJ_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
-    }
     return SJ_OK;
   }
-  OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[m->L], dt, wc(m, m->final_norm), dt, m->dz, nullptr, m->dres[cur], G + m->final_norm, M,
-                     d, eps, m->ws, m->ws_bytes));
-  for (long l = m->L - 1; l >= 0; l--) {
+  OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xtop(m, S), dt, wc(m, S.norm), dt, dzin, nullptr, m->dres[cur], G + S.norm, M, d,
+                                   eps, m->ws, m->ws_bytes));
+  for (long l = top; l >= S.first; l--) {
     const Layer& y = m->layers[l];
     float* dres = m->dres[cur];
     // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
@@ -622,15 +733,104 @@ int backward(sj_model* m) {
     OP("attn_out_dw", sj_gemm(s, 1, 0, d, d, M, m->o[l], dt, d, m->dx1, SJ_F32, d, G + y.wo, SJ_F32, d, 0, m->ws, m->ws_bytes));
     char* qkv = (char*)m->qkv[l];
     OP("attention_bwd", sj_attention_bwd(s, qkv, NQ, qkv + d * m->esz, NQ, qkv + (d + J) * m->esz, NQ, m->o[l], d, m->lse[l], m->dO, d,
-                         m->dqkv, NQ, m->dqkv + d, NQ, m->dqkv + d + J, NQ, m->delta, dt, m->B, m->T, m->HQ, m->HK,
-                         m->Dh, 0, m->rope));
+                         m->dqkv, NQ, m->dqkv + d, NQ, m->dqkv + d + J, NQ, m->delta, dt, m->B, S.T, S.HQ, S.HK,
+                         S.Dh, S.window, S.rope));
     OP("qkv_dx", sj_gemm(s, 0, 1, M, d, NQ, m->dqkv, SJ_F32, NQ, wc(m, y.qkv), dt, NQ, m->dz, SJ_F32, d, 0, m->ws, m->ws_bytes));
     OP("qkv_dw", sj_gemm(s, 1, 0, d, NQ, M, m->z[l], dt, d, m->dqkv, SJ_F32, NQ, G + y.qkv, SJ_F32, NQ, 0, m->ws, m->ws_bytes));
-    OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->x[l], dt, wc(m, y.an), dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d, eps, m->ws,
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xin(m, l), dt, wc(m, y.an), dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d, eps, m->ws,
                        m->ws_bytes));
     cur ^= 1;
   }
-  OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, M, d, m->V, nullptr, 0));
+  return SJ_OK;
+}
+
+// Reverse of hierarchy_forward (graph.rs rules for Norm, Matmul, Add,
+// PatchBroadcast, PatchPool): m->dz holds d(hn) [Ml][width].  The encoded
+// bytes feed both the pool and encoder_to_decoder, global_to_decoder both
+// the patch rows and the BOS row: those gradients are summed in fp32
+// (graph.rs:503-513).
+int hierarchy_backward(sj_model* m, int& cur) {
+  hipStream_t s = m->stream;
+  const int dt = m->dt;
+  const float eps = m->c.norm_epsilon;
+  float* G = m->g;
+  const Stage &E = m->stages[0], &Gs = m->stages[1], &D = m->stages[2];
+  const long B = m->B, P = m->P, de = E.d, dg = Gs.d, dd = D.d, Ml = E.M, Mg = Gs.M;
+  void* ws = m->ws;
+  const size_t wsb = m->ws_bytes;
+  float** hg = m->hg;
+  OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->dz, nullptr, hg[0], G + m->final_norm,
+                                   Ml, dg, eps, ws, wsb));
+  OP("output_projection_dx", sj_gemm(s, 0, 1, Ml, dd, dg, hg[0], SJ_F32, dg, wc(m, m->h_op), dt, dg, hg[1], SJ_F32, dd,
+                                     0, ws, wsb));
+  OP("output_projection_dw", sj_gemm(s, 1, 0, dd, dg, Ml, D.out, dt, dd, hg[0], SJ_F32, dg, G + m->h_op, SJ_F32, dg, 0,
+                                     ws, wsb));
+  TRY(stage_backward(m, 2, hg[1], cur));
+  const float* dxd = m->dres[cur];  // d(decoder input) = d(bytes) = d(broadcast output)
+  OP("encoder_to_decoder_dx", sj_gemm(s, 0, 1, Ml, de, dd, dxd, SJ_F32, dd, wc(m, m->h_e2d), dt, dd, hg[2], SJ_F32, de,
+                                      0, ws, wsb));
+  OP("encoder_to_decoder_dw", sj_gemm(s, 1, 0, de, dd, Ml, E.out, dt, de, dxd, SJ_F32, dd, G + m->h_e2d, SJ_F32, dd, 0,
+                                      ws, wsb));
+  OP("patch_broadcast_bwd", sj_patch_broadcast_bwd(s, dxd, B, E.T, dd, P, hg[3], hg[4]));
+  OP("global_to_decoder_dw", sj_gemm(s, 1, 0, dg, dd, Mg, Gs.out, dt, dg, hg[3], SJ_F32, dd, G + m->h_g2d, SJ_F32, dd, 0,
+                                     ws, wsb));
+  OP("bos_to_decoder_dw", sj_gemm(s, 1, 0, dg, dd, 1, wc(m, m->h_bos), dt, dg, hg[4], SJ_F32, dd, G + m->h_g2d, SJ_F32,
+                                  dd, 1, ws, wsb));
+  OP("bos_to_decoder_dx", sj_gemm(s, 0, 1, 1, dg, dd, hg[4], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, G + m->h_bos, SJ_F32,
+                                  dg, 0, ws, wsb));
+  OP("global_to_decoder_dx", sj_gemm(s, 0, 1, Mg, dg, dd, hg[3], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, hg[5], SJ_F32, dg,
+                                     0, ws, wsb));
+  TRY(stage_backward(m, 1, hg[5], cur));
+  const float* dxg = m->dres[cur];  // d(global input)
+  OP("encoder_to_global_dx", sj_gemm(s, 0, 1, Mg, de, dg, dxg, SJ_F32, dg, wc(m, m->h_e2g), dt, dg, hg[6], SJ_F32, de,
+                                     0, ws, wsb));
+  OP("encoder_to_global_dw", sj_gemm(s, 1, 0, de, dg, Mg, m->pooled, dt, de, dxg, SJ_F32, dg, G + m->h_e2g, SJ_F32, dg,
+                                     0, ws, wsb));
+  OP("patch_pool_bwd", sj_patch_pool_bwd(s, hg[6], B, E.T, de, P, hg[7]));
+  OP("encoded_grad_sum", sj_add(s, hg[2], SJ_F32, hg[7], SJ_F32, hg[7], SJ_F32, Ml * de, 1.f));
+  return stage_backward(m, 0, hg[7], cur);
+}
+
+int backward(sj_model* m) {
+  hipStream_t s = m->stream;
+  const long M = m->M, d = m->d;
+  const int dt = m->dt;
+  float* G = m->g;
+  if (m->value_n) {
+    // affine head backward (bias_reduce, the F32 matmul's dX / dW) and the
+    // gather's backward into the full hidden gradient (zero off the SEP rows)
+    const long R = m->HR, n = m->HV;
+    OP("value_bias_bwd", sj_bias_reduce(s, m->dlogits, m->Vp, R, n, G + m->bias));
+    OP("head_dw", sj_gemm(s, 1, 0, d, n, R, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
+                          m->ws, m->ws_bytes));
+    OP("head_dx", sj_gemm(s, 0, 1, R, d, n, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dhsel, SJ_F32,
+                          d, 0, m->ws, m->ws_bytes));
+    OP("value_scatter", sj_gather_rows_bwd(s, m->dhsel, m->sel, R, d, m->dz, d, M));
+  } else {
+    // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
+    OP("head_dx", sj_gemm(s, 0, 1, M, d, m->HV, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d,
+                          0, m->ws, m->ws_bytes));
+    OP("head_dw", sj_gemm(s, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
+                          m->ws, m->ws_bytes));
+  }
+  const bool two = two_streams(m);
+  if (two) {  // fork; every plane buffer starts out free for the dX chain
+    SJ_HIP(hipEventRecord(m->ev_fork, s));
+    SJ_HIP(hipStreamWaitEvent(m->stream2, m->ev_fork, 0));
+    for (int k = 0; k < 4; k++)
+      for (int p = 0; p < 2; p++) SJ_HIP(hipEventRecord(m->ev_r[k][p], m->stream2));
+  }
+  int cur = 0;
+  if (m->hier)
+    TRY(hierarchy_backward(m, cur));
+  else
+    TRY(stage_backward(m, 0, m->dz, cur));
+  OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, m->stages[0].M, m->stages[0].d, m->V,
+                                       nullptr, 0));
+  if (two) {  // the update reads every gradient
+    SJ_HIP(hipEventRecord(m->ev_join, m->stream2));
+    SJ_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
+  }
   return SJ_OK;
 }
 
@@ -816,8 +1016,8 @@ int stage_sgd(sj_model* m, float lr) {
   return SJ_OK;
 }
 
-int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n,
-                 void* stream, sj_model** out);
+int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_adam_config* adam,
+                 const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out);
 
 }  // namespace
 
@@ -826,7 +1026,13 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
 extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config* adam, void* stream,
                                sj_model** out) {
   SJ_REQUIRE(cfg && adam && out, "model: null argument");
-  return create_model(cfg, adam, nullptr, 0, stream, out);
+  return create_model(cfg, nullptr, adam, nullptr, 0, stream, out);
+}
+
+extern "C" int sj_model_create_hierarchy(const sj_model_config* cfg, const sj_hierarchy_config* hierarchy,
+                                         const sj_adam_config* adam, void* stream, sj_model** out) {
+  SJ_REQUIRE(cfg && hierarchy && adam && out, "model: null argument");
+  return create_model(cfg, hierarchy, adam, nullptr, 0, stream, out);
 }
 
 extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_config* sgd, void* stream,
@@ -835,7 +1041,7 @@ extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_conf
   SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
                  (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
              "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
-  return create_model(cfg, nullptr, sgd, 0, stream, out);
+  return create_model(cfg, nullptr, nullptr, sgd, 0, stream, out);
 }
 
 extern "C" int sj_model_create_value(const sj_model_config* cfg, long values, const sj_adam_config* adam,
@@ -847,12 +1053,12 @@ extern "C" int sj_model_create_value(const sj_model_config* cfg, long values, co
     SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
                    (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
                "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
-  return create_model(cfg, adam, sgd, values, stream, out);
+  return create_model(cfg, nullptr, adam, sgd, values, stream, out);
 }
 
 namespace {
-int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n,
-                 void* stream, sj_model** out) {
+int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_adam_config* adam,
+                 const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out) {
   const sj_model_config& c = *cfg;
   SJ_REQUIRE(c.vocab > 0 && c.width > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.ffn_width > 0 &&
                  c.sequence > 0 && c.batch > 0,
@@ -861,6 +1067,17 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   SJ_REQUIRE((c.width / c.heads) % 2 == 0, "RoPE requires an even head width");
   SJ_REQUIRE(c.heads % c.kv_heads == 0, "heads must be divisible by kv_heads");
   SJ_REQUIRE(c.precision == SJ_F32 || c.precision == SJ_BF16, "precision must be f32 or bf16");
+  if (hc) {
+    // HierarchyConfig checks (core lib.rs:81-98, ModelConfig::validate)
+    SJ_REQUIRE(hc->patch_size > 0 && hc->encoder_width > 0 && hc->encoder_layers > 0 && hc->encoder_heads > 0 &&
+                   hc->encoder_ffn_width > 0 && hc->decoder_width > 0 && hc->decoder_layers > 0 &&
+                   hc->decoder_heads > 0 && hc->decoder_ffn_width > 0 && hc->local_window > 0,
+               "hierarchy: patch size, widths, layers, heads, FFN widths and local window must be positive");
+    SJ_REQUIRE(hc->encoder_width % hc->encoder_heads == 0 && hc->decoder_width % hc->decoder_heads == 0 &&
+                   (hc->encoder_width / hc->encoder_heads) % 2 == 0 && (hc->decoder_width / hc->decoder_heads) % 2 == 0,
+               "hierarchy: local widths must split into even heads");
+    SJ_REQUIRE(!value_n && !sgd, "hierarchy: the hierarchical model trains with AdamW on the byte objective");
+  }
   sj_model* m = new sj_model();
   m->c = c;
   if (adam) m->adam = *adam;
@@ -884,7 +1101,6 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   m->HR = value_n ? c.batch : c.sequence * c.batch;
   m->Vp = (m->HV + 7) / 8 * 8;
   m->d = c.width;
-  m->L = c.layers;
   m->HQ = c.heads;
   m->HK = c.kv_heads;
   m->Dh = c.width / c.heads;
@@ -896,16 +1112,54 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   m->NQKV = m->d + 2 * m->J;
   m->dt = c.precision;
   m->esz = m->dt == SJ_BF16 ? 2 : 4;
+  m->ldt = (m->M + 7) / 8 * 8;
+  // stages: (prefix, layers, width, heads, kv heads, FFN, sequence, window)
+  auto stage = [&](const char* prefix, long layers, long d, long hq, long hk, long F, long T, long window) {
+    Stage S;
+    S.prefix = prefix;
+    S.index = (int)m->stages.size();
+    S.first = m->stages.empty() ? 0 : m->stages.back().first + m->stages.back().count;
+    S.count = layers;
+    S.depth = layers;
+    S.d = d; S.HQ = hq; S.HK = hk; S.Dh = d / hq; S.J = S.Dh * hk; S.F = F; S.NQKV = d + 2 * S.J;
+    S.T = T; S.M = T * c.batch; S.ldt = (S.M + 7) / 8 * 8;
+    S.window = window < T ? window : 0;
+    m->stages.push_back(S);
+  };
+  if (hc) {
+    m->hier = true;
+    m->P = hc->patch_size;
+    const long Tg = (c.sequence + m->P - 1) / m->P;  // sequence.div_ceil(patch)
+    stage("encoder", hc->encoder_layers, hc->encoder_width, hc->encoder_heads, hc->encoder_heads,
+          hc->encoder_ffn_width, c.sequence, hc->local_window);
+    stage("layers", c.layers, c.width, c.heads, c.kv_heads, c.ffn_width, Tg, 0);
+    stage("decoder", hc->decoder_layers, hc->decoder_width, hc->decoder_heads, hc->decoder_heads,
+          hc->decoder_ffn_width, c.sequence, hc->local_window);
+  } else {
+    stage("layers", c.layers, c.width, c.heads, c.kv_heads, c.ffn_width, c.sequence, 0);
+  }
+  m->L = 0;
+  for (const Stage& S : m->stages) m->L += S.count;
   {
     // MFMA-layout path: bf16, 64-wide heads, 8-aligned widths, d <= 1024
-    // (RMSNorm backward row staging), 4-row aligned sequences
+    // (RMSNorm backward row staging), 4-row aligned sequences; windowed
+    // stages need the transposed-operand attention (T a multiple of 64)
     const char* env = getenv("SJ_PLANES");
-    const bool want = !(env && env[0] == '0');
-    m->planes = want && m->dt == SJ_BF16 && m->Dh == 64 && m->d % 8 == 0 && m->F % 8 == 0 && m->d <= 1024 &&
-                (m->B == 1 || m->T % 4 == 0);
-    m->ldt = (m->M + 7) / 8 * 8;
     const char* ev = getenv("SJ_ATTN_TT");
-    m->attn_tt = m->planes && m->T % 64 == 0 && !(ev && ev[0] == '0');
+    const bool want = !(env && env[0] == '0'), want_tt = !(ev && ev[0] == '0');
+    bool planes = want && m->dt == SJ_BF16;
+    for (Stage& S : m->stages) {
+      planes = planes && S.Dh == 64 && S.d % 8 == 0 && S.F % 8 == 0 && S.d <= 1024 && (m->B == 1 || S.T % 4 == 0);
+      S.attn_tt = want_tt && S.T % 64 == 0;
+      if (S.window > 0 && !S.attn_tt) planes = false;
+    }
+    if (m->hier) {  // the glue's row-layout products need 8-aligned widths; stages share
+      planes = planes && m->d % 8 == 0;  // transposed plane buffers, so no padding columns either
+      for (const Stage& S : m->stages) planes = planes && S.M % 8 == 0;
+    }
+    m->planes = planes;
+    for (Stage& S : m->stages) S.attn_tt = S.attn_tt && planes;
+    m->attn_tt = m->stages[0].attn_tt;
   }
   build_layout(m);
   int st = SJ_OK;
@@ -942,11 +1196,13 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
       tiles += ((rows + 63) / 64) * j.tiles_c;
       jobs.push_back(j);
     };
-    for (const Layer& y : m->layers) {
-      job(y.qkv, m->d, m->NQKV);
-      job(y.wo, m->d, m->d);
-      job(y.gu, m->d, 2 * m->F);
-      job(y.down, m->F, m->d);
+    for (long l = 0; l < m->L; l++) {
+      const Layer& y = m->layers[l];
+      const Stage& S = m->stages[y.stage];
+      job(y.qkv, S.d, S.NQKV);
+      job(y.wo, S.d, S.d);
+      job(y.gu, S.d, 2 * S.F);
+      job(y.down, S.F, S.d);
     }
     m->tjob_n = (int)jobs.size();
     m->tjob_tiles = tiles;
@@ -954,16 +1210,29 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     if (hipMemcpy(m->tjobs, jobs.data(), sizeof(TJob) * jobs.size(), hipMemcpyHostToDevice) != hipSuccess)
       return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: transpose job table"));
   }
-  const size_t M = (size_t)m->M, d = (size_t)m->d, F = (size_t)m->F, es = m->esz;
-  m->x.resize(m->L + 1);
-  for (long l = 0; l <= m->L; l++) ALLOC(m->x[l], M * d * es);
+  const size_t es = m->esz;
+  // largest per-stage extents (shared scratch) and the head's
+  size_t mxMd = (size_t)m->M * (size_t)m->d, mxMF = 0, mxMNQ = 0, mxMHQ = 0, mxTd = 0, mxT = 0, mxLd = 0;
+  size_t mxLF = 0, mxLNQ = 0, mxLHQ = 0;
+  for (const Stage& S : m->stages) {
+    auto mx = [](size_t& a, size_t b) { a = b > a ? b : a; };
+    mx(mxMd, (size_t)(S.M * S.d)); mx(mxMF, (size_t)(S.M * S.F)); mx(mxMNQ, (size_t)(S.M * S.NQKV));
+    mx(mxMHQ, (size_t)(S.M * S.HQ)); mx(mxTd, (size_t)(S.T * S.Dh)); mx(mxT, (size_t)S.T);
+    mx(mxLd, (size_t)(S.ldt * S.d)); mx(mxLF, (size_t)(S.ldt * S.F)); mx(mxLNQ, (size_t)(S.ldt * S.NQKV));
+    mx(mxLHQ, (size_t)(S.ldt * S.HQ));
+  }
+  m->x.resize(m->L + m->stages.size());
+  for (const Stage& S : m->stages)
+    for (long i = 0; i <= S.count; i++) ALLOC(m->x[S.first + S.index + i], (size_t)(S.M * S.d) * es);
   m->z.resize(m->L); m->qkv.resize(m->L); m->o.resize(m->L); m->x1.resize(m->L); m->z2.resize(m->L);
   m->gg.resize(m->L); m->uu.resize(m->L); m->hh.resize(m->L); m->lse.resize(m->L);
   for (long l = 0; l < m->L; l++) {
+    const Stage& S = m->stages[m->layers[l].stage];
+    const size_t M = (size_t)S.M, d = (size_t)S.d, F = (size_t)S.F;
     ALLOC(m->z[l], M * d * es);
-    ALLOC(m->qkv[l], M * (size_t)m->NQKV * es);
+    ALLOC(m->qkv[l], M * (size_t)S.NQKV * es);
     ALLOC(m->o[l], M * d * es);
-    ALLOC(m->lse[l], M * (size_t)m->HQ * 4);
+    ALLOC(m->lse[l], M * (size_t)S.HQ * 4);
     ALLOC(m->x1[l], M * d * es);
     ALLOC(m->z2[l], M * d * es);
     ALLOC(m->gg[l], M * F * es);
@@ -971,67 +1240,87 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     ALLOC(m->hh[l], M * F * es);
   }
   if (m->planes) {
-    const size_t MT = (size_t)m->ldt;
     m->zt.resize(m->L); m->ot.resize(m->L); m->z2t.resize(m->L); m->ht.resize(m->L);
     for (long l = 0; l < m->L; l++) {
+      const Stage& S = m->stages[m->layers[l].stage];
+      const size_t MT = (size_t)S.ldt, d = (size_t)S.d;
       ALLOC(m->zt[l], d * MT * 2);
       ALLOC(m->ot[l], d * MT * 2);
       ALLOC(m->z2t[l], d * MT * 2);
-      ALLOC(m->ht[l], F * MT * 2);
+      ALLOC(m->ht[l], (size_t)S.F * MT * 2);
     }
-    const size_t NQ = (size_t)m->NQKV;
-    if (m->attn_tt) {
-      m->qkvt.resize(m->L);
-      m->lset.resize(m->L);
+    bool any_tt = false;
+    for (const Stage& S : m->stages) any_tt = any_tt || S.attn_tt;
+    if (any_tt) {
+      m->qkvt.assign(m->L, nullptr);
+      m->lset.assign(m->L, nullptr);
       for (long l = 0; l < m->L; l++) {
-        ALLOC(m->qkvt[l], NQ * MT * 2);
-        ALLOC(m->lset[l], (size_t)m->HQ * MT * 4);
+        const Stage& S = m->stages[m->layers[l].stage];
+        if (!S.attn_tt) continue;
+        ALLOC(m->qkvt[l], (size_t)S.NQKV * (size_t)S.ldt * 2);
+        ALLOC(m->lset[l], (size_t)S.HQ * (size_t)S.ldt * 4);
       }
-      for (int i = 0; i < 4; i++) ALLOC(m->dop[i], (i < 2 ? M : MT) * d * 2);
-      ALLOC(m->deltat, (size_t)m->HQ * MT * 4);
+      for (int i = 0; i < 4; i++) ALLOC(m->dop[i], (i < 2 ? mxMd : mxLd) * 2);
+      ALLOC(m->deltat, mxLHQ * 4);
     }
     for (int i = 0; i < 4; i++) {
-      const size_t rows = i < 2 ? M : MT;
-      ALLOC(m->rp[i], rows * d * 2);
-      ALLOC(m->xp[i], rows * d * 2);
-      ALLOC(m->qp[i], rows * NQ * 2);
-      ALLOC(m->gp[i], rows * 2 * F * 2);
+      ALLOC(m->rp[i], (i < 2 ? mxMd : mxLd) * 2);
+      ALLOC(m->xp[i], (i < 2 ? mxMd : mxLd) * 2);
+      ALLOC(m->qp[i], (i < 2 ? mxMNQ : mxLNQ) * 2);
+      ALLOC(m->gp[i], (i < 2 ? mxMF : mxLF) * 2 * 2);
     }
     // transposed planes by layer parity: parity 0 is the set above
     uint16_t** base[4] = {m->rp, m->gp, m->xp, m->qp};
-    const size_t cols[4] = {d, 2 * F, d, NQ};
+    const size_t sizes[4] = {mxLd, 2 * mxLF, mxLd, mxLNQ};
     for (int k = 0; k < 4; k++)
       for (int i = 0; i < 2; i++) {
         m->pt[k][0][i] = base[k][2 + i];
-        ALLOC(m->pt[k][1][i], cols[k] * MT * 2);
+        ALLOC(m->pt[k][1][i], sizes[k] * 2);
       }
   }
-  ALLOC(m->hn, M * d * es);
+  ALLOC(m->hn, (size_t)m->M * (size_t)m->d * es);
+  if (m->hier) {
+    Stage &E = m->stages[0], &Gs = m->stages[1], &D = m->stages[2];
+    for (Stage* S : {&E, &Gs, &D}) ALLOC(S->out, (size_t)(S->M * S->d) * es);
+    ALLOC(m->pooled, (size_t)(Gs.M * E.d) * es);
+    ALLOC(m->gd, (size_t)(Gs.M * D.d) * es);
+    ALLOC(m->bosd, (size_t)D.d * es + 256);
+    ALLOC(m->zb, (size_t)(E.M * D.d) * es);
+    ALLOC(m->bytes, (size_t)(E.M * D.d) * es);
+    ALLOC(m->opo, (size_t)(E.M * Gs.d) * es);
+    const size_t hsz[8] = {(size_t)(E.M * Gs.d), (size_t)(E.M * D.d), (size_t)(E.M * E.d), (size_t)(Gs.M * D.d),
+                           (size_t)D.d, (size_t)(Gs.M * Gs.d), (size_t)(Gs.M * E.d), (size_t)(E.M * E.d)};
+    for (int i = 0; i < 8; i++) ALLOC(m->hg[i], hsz[i] * 4);
+  } else {
+    m->stages[0].out = m->hn;
+  }
   ALLOC(m->logits, (size_t)m->HR * (size_t)m->Vp * 4);
   ALLOC(m->dlogits, (size_t)m->HR * (size_t)m->Vp * 4);
   if (m->value_n) {
     ALLOC(m->sel, sizeof(int32_t) * (size_t)m->HR);
     ALLOC(m->labels, sizeof(int32_t) * (size_t)m->HR);
-    ALLOC(m->hsel, sizeof(float) * (size_t)m->HR * d);
-    ALLOC(m->dhsel, sizeof(float) * (size_t)m->HR * d);
+    ALLOC(m->hsel, sizeof(float) * (size_t)m->HR * (size_t)m->d);
+    ALLOC(m->dhsel, sizeof(float) * (size_t)m->HR * (size_t)m->d);
   }
-  ALLOC(m->loss_rows, M * 4);
-  ALLOC(m->dres[0], M * d * 4);
-  ALLOC(m->dres[1], M * d * 4);
-  ALLOC(m->dx1, M * d * 4);
-  ALLOC(m->dO, M * d * 4);
-  ALLOC(m->dz, M * d * 4);
-  ALLOC(m->dqkv, M * (size_t)m->NQKV * 4);
-  ALLOC(m->dgu, M * 2 * F * 4);
-  ALLOC(m->delta, M * (size_t)m->HQ * 4);
-  ALLOC(m->rope, (size_t)m->T * (size_t)m->Dh * 4);
-  ALLOC(m->ids, M * 4);
-  ALLOC(m->targets, M * 4);
+  ALLOC(m->loss_rows, (size_t)m->M * 4);
+  ALLOC(m->dres[0], mxMd * 4);
+  ALLOC(m->dres[1], mxMd * 4);
+  ALLOC(m->dx1, mxMd * 4);
+  ALLOC(m->dO, mxMd * 4);
+  ALLOC(m->dz, mxMd * 4);
+  ALLOC(m->dqkv, mxMNQ * 4);
+  ALLOC(m->dgu, mxMF * 2 * 4);
+  ALLOC(m->delta, mxMHQ * 4);
+  for (Stage& S : m->stages) ALLOC(S.rope, (size_t)(S.T * S.Dh) * 4);
+  m->rope = m->stages[0].rope;
+  ALLOC(m->ids, (size_t)m->M * 4);
+  ALLOC(m->targets, (size_t)m->M * 4);
   ALLOC(m->loss, 64);
   ALLOC(m->sumsq, 64);
   ALLOC(m->status, 64);
   ALLOC(m->step_dev, sizeof(sj_adam_step));
   if (m->optimizer == 1) ALLOC(m->sgd_dev, sizeof(sj_sgd_step));
+  const size_t M = (size_t)m->M, d = (size_t)m->d, F = (size_t)m->F;
   if (m->vjp) {
     const size_t R = (size_t)m->vjp_R, k = (size_t)m->vjp_k, rows = R + k, MT = (size_t)m->ldt;
     ALLOC(m->vjp_scratch, sizeof(int32_t) * (F + (size_t)m->vjp_blocks));
@@ -1054,36 +1343,47 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   // workspace: max over the step's calls
   size_t ws = 0;
   auto upd = [&](size_t b) { ws = b > ws ? b : ws; };
-  const long Mi = m->M;
-  upd(sj_rmsnorm_bwd_workspace_bytes(Mi, m->d));
+  upd(sj_rmsnorm_bwd_workspace_bytes(m->M, m->d));
   upd(sj_sum_squares_workspace_bytes(m->n_params));
   upd(sj_gemm_workspace_bytes(m->HR, m->d, m->HV));
   upd(sj_gemm_workspace_bytes(m->d, m->HV, m->HR));
   upd(sj_gemm_workspace_bytes(m->HR, m->HV, m->d));
-  upd(sj_gemm_workspace_bytes(m->F, m->d, Mi));
-  upd(sj_gemm_workspace_bytes(m->d, 2 * m->F, Mi));
-  upd(sj_gemm_workspace_bytes(m->d, m->d, Mi));
-  upd(sj_gemm_workspace_bytes(m->d, m->NQKV, Mi));
-  upd(sj_gemm_workspace_bytes(Mi, m->d, 2 * m->F));
-  upd(sj_gemm_workspace_bytes(Mi, m->d, m->NQKV));
-  if (m->planes) {
-    upd(sj_rmsnorm_bwd_p_workspace_bytes(Mi, m->d));
-    upd(sj_attention_bwd_p_workspace_bytes(m->B, m->T, m->HQ, m->HK, m->Dh));
-    upd(sj_attention_bwd_tt_workspace_bytes(m->B, m->T, m->HQ, m->HK, m->Dh));
-    upd(sj_gemm_planes_workspace_bytes(m->F, m->d, Mi));
-    upd(sj_gemm_planes_workspace_bytes(m->d, 2 * m->F, Mi));
-    upd(sj_gemm_planes_workspace_bytes(m->d, m->d, Mi));
-    upd(sj_gemm_planes_workspace_bytes(m->d, m->NQKV, Mi));
-    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, 2 * m->F));
-    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->d));
-    upd(sj_gemm_planes_workspace_bytes(Mi, m->d, m->NQKV));
+  for (const Stage& S : m->stages) {
+    const long Mi = S.M;
+    upd(sj_rmsnorm_bwd_workspace_bytes(Mi, S.d));
+    upd(sj_gemm_workspace_bytes(S.F, S.d, Mi));
+    upd(sj_gemm_workspace_bytes(S.d, 2 * S.F, Mi));
+    upd(sj_gemm_workspace_bytes(S.d, S.d, Mi));
+    upd(sj_gemm_workspace_bytes(S.d, S.NQKV, Mi));
+    upd(sj_gemm_workspace_bytes(Mi, S.d, 2 * S.F));
+    upd(sj_gemm_workspace_bytes(Mi, S.d, S.NQKV));
+    if (m->planes) {
+      upd(sj_rmsnorm_bwd_p_workspace_bytes(Mi, S.d));
+      upd(sj_attention_bwd_p_workspace_bytes(m->B, S.T, S.HQ, S.HK, S.Dh));
+      upd(sj_attention_bwd_tt_workspace_bytes(m->B, S.T, S.HQ, S.HK, S.Dh));
+      upd(sj_gemm_planes_workspace_bytes(S.F, S.d, Mi));
+      upd(sj_gemm_planes_workspace_bytes(S.d, 2 * S.F, Mi));
+      upd(sj_gemm_planes_workspace_bytes(S.d, S.d, Mi));
+      upd(sj_gemm_planes_workspace_bytes(S.d, S.NQKV, Mi));
+      upd(sj_gemm_planes_workspace_bytes(Mi, S.d, 2 * S.F));
+      upd(sj_gemm_planes_workspace_bytes(Mi, S.d, S.d));
+      upd(sj_gemm_planes_workspace_bytes(Mi, S.d, S.NQKV));
+    }
+  }
+  if (m->hier) {
+    const Stage &E = m->stages[0], &Gs = m->stages[1], &D = m->stages[2];
+    const long de = E.d, dg = Gs.d, dd = D.d, Ml = E.M, Mg = Gs.M;
+    const long shapes[][3] = {{Mg, dg, de}, {Mg, dd, dg}, {1, dd, dg}, {Ml, dd, de}, {Ml, dg, dd},
+                              {Ml, dd, dg}, {dd, dg, Ml}, {Ml, de, dd}, {de, dd, Ml}, {dg, dd, Mg},
+                              {dg, dd, 1},  {1, dg, dd},  {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}};
+    for (const auto& sh : shapes) upd(sj_gemm_workspace_bytes(sh[0], sh[1], sh[2]));
   }
   if (m->vjp) {
     const long rows = m->vjp_R + m->vjp_k;
-    upd(sj_pvjp_basis_workspace_bytes(Mi, m->vjp_R));
-    upd(sj_pvjp_prepare_workspace_bytes(m->d, Mi, m->vjp_R));
-    upd(sj_pvjp_vjp_workspace_bytes(rows, m->NQKV, Mi));
-    upd(sj_pvjp_vjp_workspace_bytes(rows, 2 * m->F, Mi));
+    upd(sj_pvjp_basis_workspace_bytes(m->M, m->vjp_R));
+    upd(sj_pvjp_prepare_workspace_bytes(m->d, m->M, m->vjp_R));
+    upd(sj_pvjp_vjp_workspace_bytes(rows, m->NQKV, m->M));
+    upd(sj_pvjp_vjp_workspace_bytes(rows, 2 * m->F, m->M));
   }
   m->ws_bytes = ws;
   ALLOC(m->ws, ws);
@@ -1105,14 +1405,19 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   if (e == hipSuccess && m->mirror) e = hipMemsetAsync(m->mirror, 0, P * 2, s);
   if (e == hipSuccess && m->mirror_t) e = hipMemsetAsync(m->mirror_t, 0, P * 2, s);
   // padding columns [M, ldt) of the transposed activations stay zero
-  for (auto* v : {&m->zt, &m->ot, &m->z2t, &m->ht})
-    for (uint16_t* q : *v)
-      if (e == hipSuccess) e = hipMemsetAsync(q, 0, (size_t)(v == &m->ht ? m->F : m->d) * (size_t)m->ldt * 2, s);
-  for (int k = 0; k < 4 && m->planes; k++)
-    for (int i = 0; i < 2; i++)
-      if (e == hipSuccess)
-        e = hipMemsetAsync(m->pt[k][1][i], 0,
-                           (size_t)m->ldt * (size_t)(k == 1 ? 2 * F : k == 3 ? m->NQKV : m->d) * 2, s);
+  for (long l = 0; l < m->L && m->planes; l++) {
+    const Stage& S = m->stages[m->layers[l].stage];
+    const size_t MT = (size_t)S.ldt;
+    for (uint16_t* q : {m->zt[l], m->ot[l], m->z2t[l]})
+      if (e == hipSuccess) e = hipMemsetAsync(q, 0, (size_t)S.d * MT * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->ht[l], 0, (size_t)S.F * MT * 2, s);
+  }
+  {
+    const size_t sizes[4] = {mxLd, 2 * mxLF, mxLd, mxLNQ};
+    for (int k = 0; k < 4 && m->planes; k++)
+      for (int i = 0; i < 2; i++)
+        if (e == hipSuccess) e = hipMemsetAsync(m->pt[k][1][i], 0, sizes[k] * 2, s);
+  }
   if (e == hipSuccess && m->planes) {
     e = hipStreamCreate(&m->stream2);
     for (int k = 0; k < 4 && e == hipSuccess; k++)
@@ -1124,10 +1429,10 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
   }
   for (int i = 2; i < 4 && m->planes; i++) {
-    if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, (size_t)m->ldt * d * 2, s);
-    if (e == hipSuccess) e = hipMemsetAsync(m->xp[i], 0, (size_t)m->ldt * d * 2, s);
-    if (e == hipSuccess) e = hipMemsetAsync(m->qp[i], 0, (size_t)m->ldt * (size_t)m->NQKV * 2, s);
-    if (e == hipSuccess) e = hipMemsetAsync(m->gp[i], 0, (size_t)m->ldt * 2 * F * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, mxLd * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->xp[i], 0, mxLd * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->qp[i], 0, mxLNQ * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->gp[i], 0, mxLF * 2 * 2, s);
   }
   if (e == hipSuccess && m->planes) {
     int ps = sjh::norm_prepare();
@@ -1140,8 +1445,12 @@ int create_model(const sj_model_config* cfg, const sj_adam_config* adam, const s
   if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, 64, s);
   if (e == hipSuccess) e = hipMemsetAsync(m->sumsq, 0, 64, s);
   if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: clear arenas"));
-  st = sj_rope_table(s, m->rope, m->T, m->Dh, c.rope_theta);
-  if (st) return fail_cleanup(st);
+  for (const Stage& S : m->stages) {
+    st = sj_rope_table(s, S.rope, S.T, S.Dh, c.rope_theta);
+    if (st) return fail_cleanup(st);
+  }
+  (void)mxTd;
+  (void)mxT;
   if (m->optimizer == 1) {
     e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: init sync"));
@@ -1400,8 +1709,14 @@ extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) 
 // x1, z2, g, u, h; then x_L, hn, logits), converted to fp32 (exact for bf16).
 extern "C" long sj_model_activation_count(const sj_model* m) {
   if (!m) return -1;
-  const long M = m->M, d = m->d, J = m->J, F = m->F;
-  return m->L * (6 * M * d + 2 * M * J + M * m->HQ + 3 * M * F) + 2 * M * d + m->HR * m->HV;
+  long n = 0;
+  for (const Stage& S : m->stages)
+    n += S.count * (6 * S.M * S.d + 2 * S.M * S.J + S.M * S.HQ + 3 * S.M * S.F) + 2 * S.M * S.d;
+  if (m->hier) {
+    const Stage &E = m->stages[0], &G = m->stages[1], &D = m->stages[2];
+    n += G.M * E.d + G.M * D.d + D.d + 2 * E.M * D.d + 2 * E.M * G.d;
+  }
+  return n + m->HR * m->HV;
 }
 
 static int export_matrix(sj_model* m, const void* dev, int dt, long rows, long ld, long col0, long cols,
@@ -1427,25 +1742,37 @@ static int export_matrix(sj_model* m, const void* dev, int dt, long rows, long l
 extern "C" int sj_model_export_activations(sj_model* m, float* host) {
   SJ_REQUIRE(m && host, "export_activations: null");
   SJ_HIP(hipStreamSynchronize(m->stream));
-  const long M = m->M, d = m->d, J = m->J, F = m->F, NQ = m->NQKV;
   const int dt = m->dt;
   float* p = host;
-  for (long l = 0; l < m->L; l++) {
-    TRY(export_matrix(m, m->x[l], dt, M, d, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->z[l], dt, M, d, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d, J, p)); p += M * J;
-    TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d + J, J, p)); p += M * J;
-    TRY(export_matrix(m, m->o[l], dt, M, d, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->lse[l], SJ_F32, M, m->HQ, 0, m->HQ, p)); p += M * m->HQ;
-    TRY(export_matrix(m, m->x1[l], dt, M, d, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->z2[l], dt, M, d, 0, d, p)); p += M * d;
-    TRY(export_matrix(m, m->gg[l], dt, M, F, 0, F, p)); p += M * F;
-    TRY(export_matrix(m, m->uu[l], dt, M, F, 0, F, p)); p += M * F;
-    TRY(export_matrix(m, m->hh[l], dt, M, F, 0, F, p)); p += M * F;
+  for (const Stage& S : m->stages) {
+    const long M = S.M, d = S.d, J = S.J, F = S.F, NQ = S.NQKV;
+    for (long l = S.first; l < S.first + S.count; l++) {
+      TRY(export_matrix(m, xin(m, l), dt, M, d, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->z[l], dt, M, d, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->qkv[l], dt, M, NQ, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d, J, p)); p += M * J;
+      TRY(export_matrix(m, m->qkv[l], dt, M, NQ, d + J, J, p)); p += M * J;
+      TRY(export_matrix(m, m->o[l], dt, M, d, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->lse[l], SJ_F32, M, S.HQ, 0, S.HQ, p)); p += M * S.HQ;
+      TRY(export_matrix(m, m->x1[l], dt, M, d, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->z2[l], dt, M, d, 0, d, p)); p += M * d;
+      TRY(export_matrix(m, m->gg[l], dt, M, F, 0, F, p)); p += M * F;
+      TRY(export_matrix(m, m->uu[l], dt, M, F, 0, F, p)); p += M * F;
+      TRY(export_matrix(m, m->hh[l], dt, M, F, 0, F, p)); p += M * F;
+    }
+    TRY(export_matrix(m, xtop(m, S), dt, M, d, 0, d, p)); p += M * d;
+    TRY(export_matrix(m, S.out, dt, M, d, 0, d, p)); p += M * d;
   }
-  TRY(export_matrix(m, m->x[m->L], dt, M, d, 0, d, p)); p += M * d;
-  TRY(export_matrix(m, m->hn, dt, M, d, 0, d, p)); p += M * d;
+  if (m->hier) {
+    const Stage &E = m->stages[0], &G = m->stages[1], &D = m->stages[2];
+    TRY(export_matrix(m, m->pooled, dt, G.M, E.d, 0, E.d, p)); p += G.M * E.d;
+    TRY(export_matrix(m, m->gd, dt, G.M, D.d, 0, D.d, p)); p += G.M * D.d;
+    TRY(export_matrix(m, m->bosd, dt, 1, D.d, 0, D.d, p)); p += D.d;
+    TRY(export_matrix(m, m->zb, dt, E.M, D.d, 0, D.d, p)); p += E.M * D.d;
+    TRY(export_matrix(m, m->bytes, dt, E.M, D.d, 0, D.d, p)); p += E.M * D.d;
+    TRY(export_matrix(m, m->opo, dt, E.M, G.d, 0, G.d, p)); p += E.M * G.d;
+    TRY(export_matrix(m, m->hn, dt, E.M, G.d, 0, G.d, p)); p += E.M * G.d;
+  }
   TRY(export_matrix(m, m->logits, SJ_F32, m->HR, m->Vp, 0, m->HV, p));
   return SJ_OK;
 }

@@ -24,8 +24,25 @@ F32_EPSILON = float(np.finfo(np.float32).eps)
 
 
 @dataclass
+class HierarchyConfig:
+    """crates/sejong-core/src/lib.rs:83-98: byte encoder and decoder around
+    the global stack, which runs over patches of patch_size bytes."""
+    patch_size: int = 4
+    encoder_width: int = 256
+    encoder_layers: int = 2
+    encoder_heads: int = 4
+    encoder_ffn_width: int = 768
+    decoder_width: int = 256
+    decoder_layers: int = 2
+    decoder_heads: int = 4
+    decoder_ffn_width: int = 768
+    local_window: int = 128
+
+
+@dataclass
 class ModelConfig:
-    """crates/sejong-core/src/lib.rs:60-111 (dense subset used by this path)."""
+    """crates/sejong-core/src/lib.rs:60-111 (dense and hierarchical models;
+    no experts on this path)."""
     width: int = 512
     layers: int = 8
     heads: int = 8
@@ -36,6 +53,7 @@ class ModelConfig:
     norm_epsilon: float = F32_EPSILON
     precision: str = "bf16"  # "f32" | "bf16"
     seed: int = 42
+    hierarchy: HierarchyConfig | None = None
 
     @property
     def kv(self) -> int:
@@ -56,6 +74,14 @@ class ModelConfig:
             raise ValueError("heads must be divisible by kv_heads")
         if self.precision not in ("f32", "bf16"):
             raise ValueError("precision must be f32 or bf16")
+        h = self.hierarchy
+        if h is not None:  # core lib.rs:163-190
+            if not (0 < h.patch_size <= self.context and h.local_window > 0):
+                raise ValueError("patch_size must be in 1..=context and local_window must be positive")
+            for w, l, hd, f in ((h.encoder_width, h.encoder_layers, h.encoder_heads, h.encoder_ffn_width),
+                                (h.decoder_width, h.decoder_layers, h.decoder_heads, h.decoder_ffn_width)):
+                if not (w > 0 and l > 0 and hd > 0 and f > 0 and w % hd == 0 and (w // hd) % 2 == 0):
+                    raise ValueError("hierarchy stages require positive dimensions and an even head width")
 
 
 @dataclass
@@ -117,23 +143,46 @@ def config(name: str) -> tuple[ModelConfig, TrainConfig]:
                             clip_enabled=False,
                             parameter_vjp=ParameterVjpConfig(rank=16, residual_fraction=0.1, block_rows=32,
                                                              seed=124)))
+    if name == "cfg3":  # hierarchical byte model; local FFN 3 x width and window 128 (configs/sejong.toml:16-25)
+        return (ModelConfig(width=512, layers=8, heads=8, kv_heads=2, ffn_width=1376, context=1024, precision="bf16",
+                            hierarchy=HierarchyConfig(patch_size=4, encoder_width=256, encoder_layers=2,
+                                                      encoder_heads=4, encoder_ffn_width=768, decoder_width=256,
+                                                      decoder_layers=2, decoder_heads=4, decoder_ffn_width=768,
+                                                      local_window=128)),
+                TrainConfig(sequence=1024, batch=8, learning_rate=3e-4, weight_decay=0.01))
     raise KeyError(name)
 
 
-def layout(c: ModelConfig) -> list[tuple[str, tuple[int, ...], bool]]:
-    """(name, shape, is_norm) in the reference order (architecture.rs:63-137,
-    dense global stage)."""
-    d, kv = c.width, c.width // c.heads * c.kv
-    out = [("embedding", (VOCAB, d), False)]
-    for i in range(c.layers):
-        p = f"layers.{i}"
+def _stage_layout(prefix: str, d: int, layers: int, heads: int, kv_heads: int, ffn: int):
+    """stage_layout (architecture.rs:63-95)."""
+    kv = d // heads * kv_heads
+    out = []
+    for i in range(layers):
+        p = f"{prefix}.{i}"
         out += [(f"{p}.attention_norm", (d,), True), (f"{p}.ffn_norm", (d,), True),
                 (f"{p}.query", (d, d), False), (f"{p}.key", (d, kv), False), (f"{p}.value", (d, kv), False),
                 (f"{p}.attention_output", (d, d), False),
-                (f"{p}.gate", (d, c.ffn_width), False), (f"{p}.up", (d, c.ffn_width), False),
-                (f"{p}.down", (c.ffn_width, d), False)]
-    out += [("final_norm", (d,), True), ("output", (d, VOCAB), False)]
+                (f"{p}.gate", (d, ffn), False), (f"{p}.up", (d, ffn), False), (f"{p}.down", (ffn, d), False)]
     return out
+
+
+def layout(c: ModelConfig) -> list[tuple[str, tuple[int, ...], bool]]:
+    """(name, shape, is_norm) in the reference order (architecture.rs:96-137)."""
+    d = c.width
+    h = c.hierarchy
+    glob = _stage_layout("layers", d, c.layers, c.heads, c.kv, c.ffn_width)
+    if h is None:
+        return [("embedding", (VOCAB, d), False)] + glob + [("final_norm", (d,), True), ("output", (d, VOCAB), False)]
+    de, dd = h.encoder_width, h.decoder_width
+    return ([("embedding", (VOCAB, de), False)]
+            + _stage_layout("encoder", de, h.encoder_layers, h.encoder_heads, h.encoder_heads, h.encoder_ffn_width)
+            + [("encoder_norm", (de,), True), ("input_projection", (d, de), False),
+               ("encoder_to_global", (de, d), False), ("encoder_to_decoder", (de, dd), False),
+               ("global_to_decoder", (d, dd), False), ("global_bos", (1, d), False), ("global_norm", (d,), True)]
+            + glob
+            + _stage_layout("decoder", dd, h.decoder_layers, h.decoder_heads, h.decoder_heads, h.decoder_ffn_width)
+            + [("decoder_norm", (dd,), True), ("output_projection", (dd, d), False),
+               ("final_norm", (d,), True), ("output", (d, VOCAB), False)])
 
 
 def value_layout(c: ModelConfig, values: int) -> list[tuple[str, tuple[int, ...], bool]]:
@@ -152,19 +201,29 @@ def param_count(c: ModelConfig) -> int:
 def init_params(c: ModelConfig, std: float | None = 0.02, seed: int | None = None) -> np.ndarray:
     """Flat fp32 masters in the reference layout.  std=None restates
     Model::initialize (model lib.rs:83-115): N(0, 1/sqrt(fan_in)), /sqrt(2
-    depth) for down / attention_output, embedding 1/sqrt(d); otherwise every
-    matrix is N(0, std) (the BASELINE weights).  Norm weights are 1."""
+    depth) for down / attention_output (depth = the layers of the tensor's
+    stage), embedding 1/sqrt(d); otherwise every matrix is N(0, std) (the
+    BASELINE weights).  Norm weights are 1, global_bos 0."""
     rng = Rng(c.seed if seed is None else seed)
+    h = c.hierarchy
     parts = []
     for name, shape, norm in layout(c):
         n = math.prod(shape)
         if norm:
             parts.append(np.ones(n))
             continue
+        if name == "global_bos":
+            parts.append(np.zeros(n))
+            continue
         if std is None:
             s = 1.0 / math.sqrt(shape[1] if name == "embedding" else shape[0])
+            depth = c.layers
+            if h is not None and name.startswith("encoder."):
+                depth = h.encoder_layers
+            elif h is not None and name.startswith("decoder."):
+                depth = h.decoder_layers
             if name.endswith(".down") or name.endswith(".attention_output"):
-                s /= math.sqrt(2.0 * c.layers)
+                s /= math.sqrt(2.0 * depth)
         else:
             s = std
         parts.append(rng.normal(n, s))
@@ -211,7 +270,18 @@ class Model:
             adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
                                 clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
         s = ctypes.c_void_p(stream or 0)
-        if values:
+        if mc.hierarchy is not None:
+            if values or sgd is not None:
+                raise ValueError("the hierarchical model trains with AdamW on the byte objective")
+            h = mc.hierarchy
+            hc = N.HierarchyConfig(patch_size=h.patch_size, encoder_width=h.encoder_width,
+                                   encoder_layers=h.encoder_layers, encoder_heads=h.encoder_heads,
+                                   encoder_ffn_width=h.encoder_ffn_width, decoder_width=h.decoder_width,
+                                   decoder_layers=h.decoder_layers, decoder_heads=h.decoder_heads,
+                                   decoder_ffn_width=h.decoder_ffn_width, local_window=h.local_window)
+            N.api.sj_model_create_hierarchy(ctypes.byref(cfg), ctypes.byref(hc), ctypes.byref(adam), s,
+                                            ctypes.byref(handle))
+        elif values:
             N.api.sj_model_create_value(ctypes.byref(cfg), values, ctypes.byref(adam) if adam else None,
                                         ctypes.byref(sgd) if sgd else None, s, ctypes.byref(handle))
         elif sgd is not None:

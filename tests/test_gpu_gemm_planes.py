@@ -250,11 +250,14 @@ def test_attention_t_and_planes(api, lib, B, T, HQ, HK):
     assert rel((hi + lo)[:, N + KV:], dv) < 1e-4
 
 
-@pytest.mark.parametrize("B,T,HQ,HK", [(2, 256, 6, 2), (1, 512, 4, 4), (2, 128, 8, 1)])
-def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK):
+@pytest.mark.parametrize("B,T,HQ,HK,W", [(2, 256, 6, 2, 0), (1, 512, 4, 4, 0), (2, 128, 8, 1, 0), (2, 256, 4, 2, 128),
+                                         (1, 320, 4, 1, 100), (2, 192, 4, 4, 32)])
+def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     """The step's attention over producer-transposed operands (qkv^T, dO
     planes in both orientations) against the fp32 row kernels and the FP64
-    oracle on the same stored inputs."""
+    oracle on the same stored inputs; W > 0 is the local stages' sliding
+    window (hierarchy.py:24,60,87), including windows that are not a
+    multiple of the 64-key block and one shorter than a block."""
     Dh = 64
     rng = np.random.default_rng(B * T + HQ * 7 + HK)
     M = B * T; N = HQ * Dh; KV = HK * Dh; NG = N + 2 * KV
@@ -264,16 +267,16 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK):
     QKV = dev(np.concatenate([qkv, np.zeros((M, ldq - NG))], 1), "bf16")
     QKVT = dev(np.concatenate([qkv.T, np.zeros((NG, ldt - M))], 1), "bf16")
     q, k, v = qkv[:, :N], qkv[:, N:N + KV], qkv[:, N + KV:]
-    print(f"[attention_tt] B={B} T={T} HQ={HQ} HK={HK}", flush=True)
+    print(f"[attention_tt] B={B} T={T} HQ={HQ} HK={HK} W={W}", flush=True)
     O1, L1 = empty(M * N, "bf16"), empty(M * HQ)
-    api.sj_attention_fwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O1.p, N, L1.p, BF, B, T, HQ, HK, Dh, 0)
+    api.sj_attention_fwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O1.p, N, L1.p, BF, B, T, HQ, HK, Dh, W)
     O2, L2, LT, OT = empty(M * N, "bf16"), empty(M * HQ), zeros(HQ * ldt), zeros(N * ldt, "bf16")
-    api.sj_attention_fwd_tt(None, QKV.p, ldq, QKVT.p, ldt, B, T, HQ, HK, Dh, O2.p, N, L2.p, LT.p, OT.p, ldt)
+    api.sj_attention_fwd_tt(None, QKV.p, ldq, QKVT.p, ldt, B, T, HQ, HK, Dh, W, O2.p, N, L2.p, LT.p, OT.p, ldt)
     sync()
     o1, o2 = O1.host().reshape(M, N), O2.host().reshape(M, N)
     # one storage ulp, plus the accumulation error of a result that cancels
     # (bounded through the same attention over |v|)
-    o_abs, _ = O.attention_fwd(q, k, np.abs(v), B, T, HQ, HK, Dh)
+    o_abs, _ = O.attention_fwd(q, k, np.abs(v), B, T, HQ, HK, Dh, W)
     bad = np.abs(o2 - o1) > 2.0 ** -7 * np.abs(o1) + 2.0 ** -14 * o_abs + 1e-30
     if bad.any():
         r, c = np.nonzero(bad)
@@ -297,12 +300,12 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK):
     DOF = dev(dof)
     dQ, dK, dV, De = empty(M * N), empty(M * KV), empty(M * KV), empty(M * HQ)
     api.sj_attention_bwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O2.p, N, L2.p, DOF.p, N, dQ.p, N,
-                         dK.p, KV, dV.p, KV, De.p, BF, B, T, HQ, HK, Dh, 0, tab.p)
+                         dK.p, KV, dV.p, KV, De.p, BF, B, T, HQ, HK, Dh, W, tab.p)
     Gh, Gl, Th, Tl = empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldt, "bf16"), zeros(NG * ldt, "bf16")
     DT = zeros(HQ * ldt)
     ws = empty(max(lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
     api.sj_attention_bwd_tt(None, QKV.p, ldq, QKVT.p, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DTH.p, DTL.p, ldt, DT.p,
-                            B, T, HQ, HK, Dh, tab.p, Gh.p, Gl.p, NG, Th.p, Tl.p, ldt, ws.p, ws.nbytes)
+                            B, T, HQ, HK, Dh, W, tab.p, Gh.p, Gl.p, NG, Th.p, Tl.p, ldt, ws.p, ws.nbytes)
     sync()
     assert rel(DT.host().reshape(HQ, ldt)[:, :M], De.host().reshape(M, HQ).T) < 1e-5
     ref = np.concatenate([dQ.host().reshape(M, N), dK.host().reshape(M, KV), dV.host().reshape(M, KV)], 1)
@@ -313,7 +316,7 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK):
     assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
     np.testing.assert_array_equal(Th.host().reshape(NG, ldt)[:, :M], hi.T)
     np.testing.assert_array_equal(Tl.host().reshape(NG, ldt)[:, :M], lo.T)
-    dq, dk, dv, _ = O.attention_bwd(q, k, v, o2, L2.host(), dof, B, T, HQ, HK, Dh, 0)
+    dq, dk, dv, _ = O.attention_bwd(q, k, v, o2, L2.host(), dof, B, T, HQ, HK, Dh, W)
     dq = O.rope(dq, T, HQ, Dh, inverse=True); dk = O.rope(dk, T, HK, Dh, inverse=True)
     assert rel(got[:, :N], dq) < 1e-4 and rel(got[:, N:N + KV], dk) < 1e-4 and rel(got[:, N + KV:], dv) < 1e-4
 

@@ -619,3 +619,81 @@ def test_model_backward_hidden_matches_lm_head():
     n = g.size
     np.testing.assert_allclose(gh[V * d:n - d * V], g[V * d:n - d * V], rtol=1e-10, atol=1e-15)
     np.testing.assert_allclose(O.embedding_bwd(demb, ids, V).ravel(), g[:V * d], rtol=1e-10, atol=1e-15)
+
+
+def _hier_cfg(window=6):
+    return dict(d=32, layers=1, hq=4, hk=2, ffn=48, T=16, B=2, P=4, window=window, de=16, le=1, he=2, fe=40,
+                dd=16, ld=2, hd=2, fd=24, eps=1e-6, theta=10000.0)
+
+
+def test_hierarchy_model_gradient_finite_difference():
+    """The hierarchical model's composed backward (encoder, pool,
+    encoder_to_global, global stack, global_to_decoder of patches and BOS,
+    broadcast, encoder_to_decoder, decoder, output_projection, final norm,
+    head) against central differences of its own FP64 loss, for entries of
+    every glue tensor and of each stage (window 6 < T = 16)."""
+    from oracle import hierarchy as H
+    cfg = _hier_cfg()
+    table, total = H._offsets(cfg)
+    rng = np.random.default_rng(5)
+    p = rng.normal(0, 0.3, total)
+    for name, (o, shape) in table.items():
+        if name.endswith("norm"):
+            p[o:o + int(np.prod(shape))] = 1.0 + rng.normal(0, 0.1, int(np.prod(shape)))
+    M = cfg["B"] * cfg["T"]
+    ids = rng.integers(0, 256, M).astype(np.int32)
+    tg = rng.integers(0, 256, M).astype(np.int32)
+    acts = H.model_forward(cfg, p, ids, "none")
+    loss, g = H.model_backward(cfg, p, acts, ids, tg, "none")
+    assert abs(loss - H.model_loss(cfg, p, ids, tg)) < 1e-12
+    names = ["embedding", "encoder.0.query", "encoder.0.down", "encoder_norm", "encoder_to_global",
+             "encoder_to_decoder", "global_to_decoder", "global_bos", "global_norm", "layers.0.key",
+             "layers.0.up", "decoder.1.value", "decoder.0.gate", "decoder_norm", "output_projection",
+             "final_norm", "output", "encoder.0.attention_norm", "decoder.1.ffn_norm"]
+    h = 1e-5
+    worst = 0.0
+    for name in names:
+        o, shape = table[name]
+        n = int(np.prod(shape))
+        idx = [o + i for i in rng.choice(n, size=min(n, 3), replace=False)]
+        if name == "embedding":
+            idx = [o + int(ids[0]) * cfg["de"] + 1, o + int(ids[5]) * cfg["de"] + 3]
+        for i in idx:
+            pp, pm = p.copy(), p.copy()
+            pp[i] += h
+            pm[i] -= h
+            fd = (H.model_loss(cfg, pp, ids, tg) - H.model_loss(cfg, pm, ids, tg)) / (2 * h)
+            err = abs(fd - g[i]) / (abs(fd) + 1e-6)
+            worst = max(worst, err)
+            assert err < 1e-4, (name, i, fd, g[i])
+    # input_projection only serves injected inputs: zero gradient
+    o, shape = table["input_projection"]
+    assert not np.any(g[o:o + int(np.prod(shape))])
+    print(f"[hierarchy] worst FD relative error {worst:.2e}")
+
+
+def test_hierarchy_window_and_stage_reduce_to_dense_blocks():
+    """A stage with a window at least its sequence is the dense model's
+    body: the stage forward's activations equal or_model_forward's for the
+    same blocks and input embedding, and a window shorter than the sequence
+    changes them (it is applied)."""
+    cfg = dict(d=16, layers=2, hq=2, hk=1, ffn=24, T=12, B=2, eps=1e-6, theta=10000.0)
+    rng = np.random.default_rng(9)
+    n = O.model_param_count(16, 2, 2, 1, 24)
+    p = rng.normal(0, 0.3, n)
+    M = 24
+    ids = rng.integers(0, 256, M).astype(np.int32)
+    acts = O.model_forward(cfg, p, ids, "none")
+    V, d = O.VOCAB, 16
+    body = p[V * d:n - d * V]                    # layers + final norm (the stage layout)
+    x0 = p[:V * d].reshape(V, d)[ids]
+    st = O.stage_forward(dict(cfg, window=12), body, x0, "none")
+    np.testing.assert_allclose(st, acts[:st.size], rtol=0, atol=1e-12)
+    st_w = O.stage_forward(dict(cfg, window=5), body, x0, "none")
+    assert np.max(np.abs(st_w - st)) > 1e-3
+    # the stage backward equals the dense body backward through model_backward_hidden
+    dz = rng.normal(0, 1, (M, d))
+    g_dense, demb = O.model_backward_hidden(cfg, p, acts, dz, "none")
+    g_stage, dx = O.stage_backward(dict(cfg, window=0), body, st, dz, "none")
+    np.testing.assert_allclose(g_stage, g_dense[V * d:n - d * V], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dx, demb, rtol=1e-12, atol=1e-12)
