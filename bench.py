@@ -44,8 +44,87 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _attn_pairs(T, window):
+    """(query, key) pairs a causal head visits: T(T+1)/2, or with a local
+    window W < T, W(W+1)/2 + (T-W)W."""
+    if window and window < T:
+        return window * (window + 1) / 2 + (T - window) * window
+    return T * (T + 1) / 2
+
+
+def _hier_ops(mc, tc):
+    """Per-step (kind, total work, calls) of every op of the hierarchical
+    step (cfg3): the block ops summed over the three stages, the glue."""
+    h = mc.hierarchy
+    B, T, P = tc.batch, tc.sequence, h.patch_size
+    Tg = -(-T // P)
+    es = 2 if mc.precision == "bf16" else 4
+    planes = mc.precision == "bf16"
+    stages = [(h.encoder_layers, h.encoder_width, h.encoder_heads, h.encoder_heads, h.encoder_ffn_width, T,
+               h.local_window),
+              (mc.layers, mc.width, mc.heads, mc.kv, mc.ffn_width, Tg, 0),
+              (h.decoder_layers, h.decoder_width, h.decoder_heads, h.decoder_heads, h.decoder_ffn_width, T,
+               h.local_window)]
+    tot = {}
+
+    def add(op, kind, w, n=1):
+        k, t, c = tot.get(op, (kind, 0.0, 0))
+        tot[op] = (kind, t + w * n, c + n)
+    for L, d, hq, hk, F, Ts, W in stages:
+        M, J = B * Ts, d // hq * hk
+        af = B * hq * 4 * (d // hq) * _attn_pairs(Ts, W)
+        for op, kind, w in (("qkv_rope", "flop", 2 * M * d * (d + 2 * J)), ("qkv_dx", "flop", 2 * M * d * (d + 2 * J)),
+                            ("qkv_dw", "flop", 2 * M * d * (d + 2 * J)), ("attention_fwd", "flop", af),
+                            ("attention_bwd", "flop", 2.5 * af), ("attention_bwd_dq", "flop", 1.5 * af),
+                            ("attention_bwd_dkv", "flop", 2.0 * af),
+                            ("attention_bwd_kv_reduce", "byte", (hq // hk) * M * 2 * J * 4 + 4 * M * 2 * J * 2),
+                            ("attn_out_residual", "flop", 2 * M * d * d), ("attn_out_dx", "flop", 2 * M * d * d),
+                            ("attn_out_dw", "flop", 2 * M * d * d), ("gate_up_swiglu", "flop", 4 * M * d * F),
+                            ("gate_up_dx", "flop", 4 * M * d * F), ("gate_up_dw", "flop", 4 * M * d * F),
+                            ("down_residual", "flop", 2 * M * F * d), ("down_dx_swiglu", "flop", 2 * M * F * d),
+                            ("down_dw", "flop", 2 * M * F * d)):
+            add(op, kind, w, L)
+        add("rmsnorm", "byte", (3 if planes else 2) * M * d * es + d * es, 2 * L)
+        add("rmsnorm", "byte", 2 * M * d * es + d * es)                       # closing norm
+        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es, 2 * L)
+        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es)
+    de, dg, dd = h.encoder_width, mc.width, h.decoder_width
+    Ml, Mg, V = B * T, B * Tg, 257
+    for op, kind, w in (("patch_pool", "byte", Ml * de * es + Mg * de * es),
+                        ("encoder_to_global", "flop", 2 * Mg * de * dg), ("global_to_decoder", "flop", 2 * Mg * dg * dd),
+                        ("bos_to_decoder", "flop", 2 * dg * dd), ("patch_broadcast", "byte", Ml * dd * es + Mg * dd * es),
+                        ("encoder_to_decoder", "flop", 2 * Ml * de * dd), ("decoder_input", "byte", 3 * Ml * dd * es),
+                        ("output_projection", "flop", 2 * Ml * dd * dg), ("output_projection_dx", "flop", 2 * Ml * dd * dg),
+                        ("output_projection_dw", "flop", 2 * Ml * dd * dg),
+                        ("encoder_to_decoder_dx", "flop", 2 * Ml * de * dd), ("encoder_to_decoder_dw", "flop", 2 * Ml * de * dd),
+                        ("patch_broadcast_bwd", "byte", Ml * dd * 4 + Mg * dd * 4 + dd * 4),
+                        ("global_to_decoder_dw", "flop", 2 * Mg * dg * dd), ("bos_to_decoder_dw", "flop", 2 * dg * dd),
+                        ("bos_to_decoder_dx", "flop", 2 * dg * dd), ("global_to_decoder_dx", "flop", 2 * Mg * dg * dd),
+                        ("encoder_to_global_dx", "flop", 2 * Mg * de * dg), ("encoder_to_global_dw", "flop", 2 * Mg * de * dg),
+                        ("patch_pool_bwd", "byte", Mg * de * 4 + Ml * de * 4), ("encoded_grad_sum", "byte", 3 * Ml * de * 4),
+                        ("head_fwd", "flop", 2 * Ml * dg * V), ("head_dx", "flop", 2 * Ml * dg * V),
+                        ("head_dw", "flop", 2 * Ml * dg * V), ("cross_entropy", "byte", 2 * Ml * V * 4 + Ml * 8),
+                        ("loss_summary", "byte", Ml * 4), ("embedding", "byte", Ml * 4 + 2 * Ml * de * es),
+                        ("embedding_bwd", "byte", Ml * de * 4 + V * de * 4 + Ml * 4)):
+        add(op, kind, w)
+    add("rmsnorm", "byte", 2 * Ml * dg * es + dg * es)                            # final norm
+    add("rmsnorm_bwd", "byte", Ml * dg * (es + 4 + 4 + 4) + dg * es)
+    import sejong_amd.model as SM
+    Pn = sum(math.prod(sh) for _, sh, _ in SM.layout(mc))
+    mt = sum(L * (d * (d + 2 * (d // hq * hk)) + d * d + 3 * d * F) for L, d, hq, hk, F, _, _ in stages)
+    add("grad_norm", "byte", Pn * 4)
+    add("adamw", "byte", 30 * Pn)
+    add("mirror_transpose", "byte", 2 * 2 * mt)
+    return tot
+
+
 def op_work(op: str, mc, tc):
-    """Algorithmic work of ONE launch of a step op: ("flop", F) or ("byte", B)."""
+    """Algorithmic work of ONE launch of a step op: ("flop", F) or ("byte", B)
+    (for the hierarchical model: the op's per-step total over its launches
+    divided by their number, the launches of one name differing by stage)."""
+    if getattr(mc, "hierarchy", None) is not None:
+        kind, total, calls = _hier_ops(mc, tc).get(op, ("flop", 0.0, 1))
+        return kind, total / calls
     M = tc.batch * tc.sequence
     d, F, V = mc.width, mc.ffn_width, 257
     J = mc.head_dim * mc.kv
@@ -118,6 +197,13 @@ def op_work(op: str, mc, tc):
     return table.get(op, ("flop", 0.0))
 
 
+def _hier_name(name, mc):
+    h = mc.hierarchy
+    return (f"{name}: hierarchical byte model, encoder {h.encoder_layers}x d{h.encoder_width} and decoder "
+            f"{h.decoder_layers}x d{h.decoder_width} (window {h.local_window}), global {mc.layers}x d{mc.width} "
+            f"GQA {mc.heads}/{mc.kv} SwiGLU {mc.ffn_width} over {h.patch_size}-byte patches, ")
+
+
 def cpu_baseline(mc, tc, sample_batch: int):
     """FP64 oracle (OpenMP over all host threads) on `sample_batch`
     sequences of the same workload: forward + backward + AdamW."""
@@ -131,7 +217,16 @@ def cpu_baseline(mc, tc, sample_batch: int):
     cfg = dict(d=mc.width, layers=mc.layers, hq=mc.heads, hk=mc.kv, ffn=mc.ffn_width, T=tc.sequence,
                B=sample_batch, eps=mc.norm_epsilon, theta=mc.rope_theta)
     t0 = time.perf_counter()
-    loss, g, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype=mc.precision)
+    if mc.hierarchy is not None:
+        from oracle import hierarchy as H
+        h = mc.hierarchy
+        hc = dict(cfg, P=h.patch_size, window=h.local_window, de=h.encoder_width, le=h.encoder_layers,
+                  he=h.encoder_heads, fe=h.encoder_ffn_width, dd=h.decoder_width, ld=h.decoder_layers,
+                  hd=h.decoder_heads, fd=h.decoder_ffn_width)
+        acts = H.model_forward(hc, p, ids, mc.precision)
+        loss, g = H.model_backward(hc, p, acts, ids, tg, mc.precision)
+    else:
+        loss, g, _, _ = O.model_fwd_bwd(cfg, p, ids, tg, dtype=mc.precision)
     norm = math.sqrt(O.sum_squares(g))
     scale = min(1.0, tc.clip_norm / norm)
     if getattr(tc, "optimizer", "adamw") == "sgd":
@@ -486,7 +581,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=2)
+    ap.add_argument("--cpu-sample-batch", type=int, default=0,
+                    help="sequences the CPU baseline runs (default 2; 1 for the hierarchical model)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
     ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
@@ -588,7 +684,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (FP64 oracle) ...")
-        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch)
+        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch or (1 if mc.hierarchy is not None else 2))
         log(f"[bench] cpu baseline {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
 
     out = {
@@ -604,8 +700,9 @@ def main():
         "vs_baseline": None,
         "dtype": mc.precision,
         "data": "synthetic uniform random bytes (SplitMix64 seed 123), weights N(0,0.02) seed 42",
-        "config": {"workload": f"{args.config}: {mc.layers}-layer byte Transformer d{mc.width} GQA "
-                               f"{mc.heads}/{mc.kv} hd{mc.head_dim} SwiGLU {mc.ffn_width}, " +
+        "config": {"workload": (_hier_name(args.config, mc) if mc.hierarchy is not None else
+                                f"{args.config}: {mc.layers}-layer byte Transformer d{mc.width} GQA "
+                                f"{mc.heads}/{mc.kv} hd{mc.head_dim} SwiGLU {mc.ffn_width}, ") +
                                ("fwd+bwd+AdamW" if tc.optimizer == "adamw" else
                                 "fwd+bwd+selected-row SGD" + (
                                     f" with rank-{tc.parameter_vjp.rank} parameter VJP, "
