@@ -43,6 +43,7 @@ extern "C" {
 #define SJ_ERR_HIP 3         /* HIP runtime error (hip.rs:47-57)             */
 #define SJ_ERR_UNSUPPORTED 4 /* dtype / layout combination not implemented  */
 #define SJ_ERR_NONFINITE 5   /* non-finite clipping gradient (train lib.rs:210) */
+#define SJ_ERR_IO 6          /* file read / write (Error::Io)               */
 
 #define SJ_F32 0
 #define SJ_F64 1
@@ -676,6 +677,9 @@ int sj_model_materialize_grads(sj_model *m);
 int sj_model_vjp_info(const sj_model *m, long *compressed, long *dense, long *basis_groups,
                       long *projection_groups, uint64_t *rng_state);
 int sj_model_set_vjp_rng(sj_model *m, uint64_t rng_state);
+/* Updates applied so far (Adam's step / the SGD state's step; the
+ * checkpoint manifest's step). */
+long sj_model_steps(const sj_model *m);
 int sj_model_destroy(sj_model *m);
 /* Number of parameter tensors / total elements in the reference layout. */
 long sj_model_param_tensors(const sj_model *m);
@@ -727,6 +731,30 @@ int sj_model_export_activations(sj_model *m, float *host);
  * parameter-VJP models "vjp_columns", "vjp_rows", "vjp_map" (int32) and
  * "vjp_basis" (fp32 [tokens][rank])). */
 int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);
+
+/* ----------------------------------------------------------- Checkpoints
+ * Host code (no device work).  Files in the safetensors format of the
+ * crate the reference pins (0.8.0): save_tensors / load_tensors, crates/
+ * sejong-model/src/lib.rs:456-538.  Tensors are F32; tensor i has rank
+ * ranks[i] and its dimensions next in dims (concatenated). */
+/* save_tensors: written in byte-wise name order. */
+int sj_safetensors_write(const char *path, long count, const char *const *names, const long *ranks,
+                         const long *dims, const float *const *data);
+/* The header JSON (validated: every tensor's byte range inside the file);
+ * out (nullable) receives it NUL-terminated when capacity > *length. */
+int sj_safetensors_header(const char *path, char *out, size_t capacity, size_t *length);
+/* One F32 tensor of count elements by name; non-finite values are an error
+ * (load_tensors, lib.rs:509-537). */
+int sj_safetensors_read(const char *path, const char *name, float *out, long count);
+/* Model::save (lib.rs:395-442): fails if directory exists; writes
+ * weights.safetensors, optimizer.safetensors (n_optimizer > 0) and
+ * manifest.json (the given text) into a staging directory
+ * <parent>/.<name>.<pid>.tmp, renames it onto directory, and removes the
+ * staging directory on failure. */
+int sj_checkpoint_save(const char *directory, const char *manifest_json, long n_weights,
+                       const char *const *weight_names, const long *weight_ranks, const long *weight_dims,
+                       const float *const *weight_data, long n_optimizer, const char *const *optimizer_names,
+                       const long *optimizer_ranks, const long *optimizer_dims, const float *const *optimizer_data);
 
 #ifdef __cplusplus
 }

@@ -167,6 +167,10 @@ SIGNATURES = {
     "sj_patch_broadcast": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _P]),
     "sj_patch_broadcast_bwd": (_I, [_P, _P, _L, _L, _L, _L, _P, _P]),
     "sj_model_create": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
+    "sj_safetensors_write": (_I, [ctypes.c_char_p, _L, _P, _P, _P, _P]),
+    "sj_safetensors_header": (_I, [ctypes.c_char_p, _P, _S, ctypes.POINTER(_S)]),
+    "sj_safetensors_read": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _L]),
+    "sj_checkpoint_save": (_I, [ctypes.c_char_p, ctypes.c_char_p, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P]),
     "sj_model_create_hierarchy": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(HierarchyConfig),
                                        ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),
@@ -177,6 +181,7 @@ SIGNATURES = {
     "sj_model_vjp_info": (_I, [_P, ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L), ctypes.POINTER(_L),
                                ctypes.POINTER(_U64)]),
     "sj_model_set_vjp_rng": (_I, [_P, _U64]),
+    "sj_model_steps": (_L, [_P]),
     "sj_model_destroy": (_I, [_P]),
     "sj_model_param_tensors": (_L, [_P]),
     "sj_model_param_count": (_L, [_P]),

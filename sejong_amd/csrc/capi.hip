@@ -31,6 +31,7 @@ extern "C" const char* sj_status_string(int status) {
     case SJ_ERR_HIP: return "HIP runtime error";
     case SJ_ERR_UNSUPPORTED: return "unsupported dtype or layout";
     case SJ_ERR_NONFINITE: return "nonfinite clipping gradient";
+    case SJ_ERR_IO: return "file read or write error";
     default: return "unknown status";
   }
 }

@@ -1796,6 +1796,8 @@ extern "C" int sj_model_vjp_info(const sj_model* m, long* compressed, long* dens
   return SJ_OK;
 }
 
+extern "C" long sj_model_steps(const sj_model* m) { return m ? m->step : -1; }
+
 extern "C" int sj_model_set_vjp_rng(sj_model* m, uint64_t rng_state) {
   SJ_REQUIRE(m && m->optimizer == 1, "set_vjp_rng: SGD model required");
   m->vjp_rng = rng_state;

@@ -54,6 +54,7 @@ class ModelConfig:
     precision: str = "bf16"  # "f32" | "bf16"
     seed: int = 42
     hierarchy: HierarchyConfig | None = None
+    id: str = "sejong"
 
     @property
     def kv(self) -> int:
@@ -347,6 +348,25 @@ class Model:
         m = np.empty(self.count, np.float32); v = np.empty(self.count, np.float32); st = ctypes.c_long()
         N.api.sj_model_get_adam_state(self.h, _np_ptr(m), _np_ptr(v), ctypes.byref(st))
         return m, v, st.value
+
+    def set_adam_state(self, m: np.ndarray, v: np.ndarray, step: int):
+        m = np.ascontiguousarray(m, np.float32); v = np.ascontiguousarray(v, np.float32)
+        assert m.size == self.count and v.size == self.count
+        N.api.sj_model_set_adam_state(self.h, _np_ptr(m), _np_ptr(v), step)
+
+    def steps(self) -> int:
+        """Updates applied so far (the checkpoint manifest's step)."""
+        return N.api.sj_model_steps(self.h)
+
+    def save(self, directory: str, **kw):
+        """Reference-compatible checkpoint (sejong_amd.checkpoint.save)."""
+        from . import checkpoint
+        checkpoint.save(self, directory, **kw)
+
+    def load(self, directory: str) -> dict:
+        """Resume parameters and optimizer state (sejong_amd.checkpoint.load_into)."""
+        from . import checkpoint
+        return checkpoint.load_into(self, directory)
 
     def set_batch(self, ids: np.ndarray, targets: np.ndarray):
         ids = np.ascontiguousarray(ids, dtype=np.int32); tg = np.ascontiguousarray(targets, dtype=np.int32)
