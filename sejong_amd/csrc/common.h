@@ -88,6 +88,13 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
   return s;
 }
 
+// one norm-weight gradient reduction: dw[c] = sum_g partial[g][c]
+struct RmsReduceJob {
+  const float* partial;
+  float* dw;
+  long groups, d;
+};
+
 }  // namespace sj
 
 // ------------------------------------------------------------- host side
@@ -123,6 +130,12 @@ int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ld
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);
+// sj_rmsnorm_bwd_p with the dw reduce left to rmsnorm_reduce_multi (partial:
+// sj_rmsnorm_bwd_p_workspace_bytes of its own)
+int rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, const float* dy, const float* dx_acc,
+                           float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi, uint16_t* dx_t_lo,
+                           long ldt, long rows, long d, float eps, float* partial);
+int rmsnorm_reduce_multi(void* stream, const sj::RmsReduceJob* jobs, long njobs, long max_d);
 // one-time kernel attribute setup (dynamic LDS limits), outside capture
 int norm_prepare();
 int gemm_fast_prepare();

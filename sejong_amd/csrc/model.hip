@@ -205,7 +205,15 @@ struct sj_model {
   // (second stream waits) and read (dX chain waits before overwriting).
   hipStream_t stream2 = nullptr;
   uint16_t* pt[4][2][2] = {};
-  hipEvent_t ev_w[4][2] = {}, ev_r[4][2] = {}, ev_fork = nullptr, ev_join = nullptr;
+  hipEvent_t ev_w[4][2] = {}, ev_r[4][2] = {}, ev_fork = nullptr, ev_join = nullptr, ev_norm = nullptr;
+  // norm-weight gradients of the planes path: every RMSNorm backward leaves
+  // its per-row-block partial sums in a slot of its own, and one batched
+  // reduce at the end of the backward (second stream) forms all dw
+  float* norm_part = nullptr;
+  sj::RmsReduceJob* norm_jobs = nullptr;
+  long norm_njobs = 0, norm_maxd = 0;
+  std::vector<long> slot_close, slot_fn, slot_an;  // per stage / per layer (-1: row kernel)
+  std::vector<float*> slot_ptr;
   void* ws2 = nullptr;
   // activations
   std::vector<void*> x;  // L+1 residual stream tensors
@@ -643,8 +651,9 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
     {
       const int p = (int)(top & 1);
       TRY(reuse(KR, p));
-      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)xtop(m, S), W + S.norm, dzin, nullptr, m->dres[cur],
-                                         G + S.norm, rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M, d, eps, ws, wsb));
+      OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)xtop(m, S), W + S.norm, dzin, nullptr,
+                                                    m->dres[cur], rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M, d,
+                                                    eps, m->slot_ptr[m->slot_close[si]]));
       TRY(written(KR, p));
     }
     for (long l = top; l >= S.first; l--) {
@@ -668,8 +677,9 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                         G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       TRY(read(KG, p));
       TRY(reuse(KX, p));
-      OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1, G + y.fn,
-                                         xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps, ws, wsb));
+      OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1,
+                                                    xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps,
+                                                    m->slot_ptr[m->slot_fn[l]]));
       TRY(written(KX, p));
       // x1 = x + attention_output(o)
       if (S.attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
@@ -704,8 +714,9 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       if (l > S.first) {
         const int pn = (int)((l - 1) & 1);
         TRY(reuse(KR, pn));
-        OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)xin(m, l), W + y.an, m->dz, m->dx1, m->dres[cur ^ 1],
-                                           G + y.an, rp[0], rp[1], T(KR, pn)[0], T(KR, pn)[1], ldt, M, d, eps, ws, wsb));
+        OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)xin(m, l), W + y.an, m->dz, m->dx1,
+                                                      m->dres[cur ^ 1], rp[0], rp[1], T(KR, pn)[0], T(KR, pn)[1], ldt,
+                                                      M, d, eps, m->slot_ptr[m->slot_an[l]]));
         TRY(written(KR, pn));
       } else {  // the stage input's gradient feeds row-layout consumers only
         OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xin(m, l), dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
@@ -825,6 +836,15 @@ int backward(sj_model* m) {
     TRY(hierarchy_backward(m, cur));
   else
     TRY(stage_backward(m, 0, m->dz, cur));
+  if (m->planes) {  // every norm-weight gradient, off the dX chain
+    hipStream_t sr = s;
+    if (two) {
+      SJ_HIP(hipEventRecord(m->ev_norm, s));
+      SJ_HIP(hipStreamWaitEvent(m->stream2, m->ev_norm, 0));
+      sr = m->stream2;
+    }
+    OP("rmsnorm_dw_reduce", sjh::rmsnorm_reduce_multi(sr, m->norm_jobs, m->norm_njobs, m->norm_maxd));
+  }
   OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, m->stages[0].M, m->stages[0].d, m->V,
                                        nullptr, 0));
   if (two) {  // the update reads every gradient
@@ -1277,6 +1297,38 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
         m->pt[k][0][i] = base[k][2 + i];
         ALLOC(m->pt[k][1][i], sizes[k] * 2);
       }
+    // norm-weight partial slots: the closing norm of every stage, and per
+    // layer the ffn norm and (above the stage's first layer) the attention norm
+    std::vector<sj::RmsReduceJob> jobs;
+    std::vector<size_t> offs;
+    size_t total = 0;
+    auto slot = [&](const Stage& S, long woff) -> long {
+      const size_t n = sj_rmsnorm_bwd_p_workspace_bytes(S.M, S.d) / sizeof(float);
+      jobs.push_back(sj::RmsReduceJob{nullptr, m->g + woff, (long)(n / (size_t)S.d), S.d});
+      offs.push_back(total);
+      total += (n + 63) / 64 * 64;
+      m->norm_maxd = S.d > m->norm_maxd ? S.d : m->norm_maxd;
+      return (long)jobs.size() - 1;
+    };
+    m->slot_fn.assign(m->L, -1);
+    m->slot_an.assign(m->L, -1);
+    for (const Stage& S : m->stages) {
+      m->slot_close.push_back(slot(S, S.norm));
+      for (long l = S.first; l < S.first + S.count; l++) {
+        m->slot_fn[l] = slot(S, m->layers[l].fn);
+        if (l > S.first) m->slot_an[l] = slot(S, m->layers[l].an);
+      }
+    }
+    ALLOC(m->norm_part, total * sizeof(float));
+    for (size_t i = 0; i < jobs.size(); i++) {
+      jobs[i].partial = m->norm_part + offs[i];
+      m->slot_ptr.push_back(m->norm_part + offs[i]);
+    }
+    m->norm_njobs = (long)jobs.size();
+    ALLOC(m->norm_jobs, sizeof(sj::RmsReduceJob) * jobs.size());
+    if (hipMemcpy(m->norm_jobs, jobs.data(), sizeof(sj::RmsReduceJob) * jobs.size(), hipMemcpyHostToDevice) !=
+        hipSuccess)
+      return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: norm reduce table"));
   }
   ALLOC(m->hn, (size_t)m->M * (size_t)m->d * es);
   if (m->hier) {
@@ -1427,6 +1479,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       }
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_norm, hipEventDisableTiming);
   }
   for (int i = 2; i < 4 && m->planes; i++) {
     if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, mxLd * 2, s);
@@ -1482,6 +1535,7 @@ extern "C" int sj_model_destroy(sj_model* m) {
     }
   if (m->ev_fork) hipEventDestroy(m->ev_fork);
   if (m->ev_join) hipEventDestroy(m->ev_join);
+  if (m->ev_norm) hipEventDestroy(m->ev_norm);
   if (m->stream2) {
     hipStreamSynchronize(m->stream2);
     hipStreamDestroy(m->stream2);

@@ -159,6 +159,37 @@ __global__ __launch_bounds__(NT) void k_rms_reduce(const float* __restrict__ par
 }
 
 
+// Many reductions in one launch (blockIdx.y = job): the norm-weight
+// gradients of a whole backward, summed after the dX chain has passed.
+__global__ __launch_bounds__(NT) void k_rms_reduce_multi(const sj::RmsReduceJob* __restrict__ jobs) {
+  const sj::RmsReduceJob jb = jobs[blockIdx.y];
+  __shared__ float red[8][32];
+  const int col = threadIdx.x & 31, sl = threadIdx.x >> 5;
+  const long c = blockIdx.x * 32L + col;
+  if (blockIdx.x * 32L >= jb.d) return;  // whole workgroup past this job's columns
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  const long groups = jb.groups, d = jb.d;
+  const float* partial = jb.partial;
+  if (c < d) {
+    long g = sl;
+    for (; g + 24 < groups; g += 32) {
+      a0 += partial[g * d + c];
+      a1 += partial[(g + 8) * d + c];
+      a2 += partial[(g + 16) * d + c];
+      a3 += partial[(g + 24) * d + c];
+    }
+    for (; g < groups; g += 8) a0 += partial[g * d + c];
+  }
+  red[sl][col] = (a0 + a1) + (a2 + a3);
+  __syncthreads();
+  if (sl == 0 && c < d) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) s += red[i][col];
+    jb.dw[c] = s;
+  }
+}
+
 // ----------------------------------------------------- MFMA-layout variants
 // Row blocks of TR = 16 rows on 16 waves, one row per wave, so every row's
 // loads are in flight at once; lanes own column pairs lane + 64 j, j < NP.
@@ -442,6 +473,41 @@ extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t*
     default: launch_fwd_t<8>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
   }
   SJ_LAUNCH_CHECK("rmsnorm_t");
+  return SJ_OK;
+}
+
+// sj_rmsnorm_bwd_p without its dw reduce: the partial sums [groups][d]
+// stay in `partial` for sjh::rmsnorm_reduce_multi
+int sjh::rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, const float* dy,
+                                const float* dx_acc, float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi,
+                                uint16_t* dx_t_lo, long ldt, long rows, long d, float eps, float* partial) {
+  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && ldt >= rows && ldt % 8 == 0 && partial &&
+                 ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
+             "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
+  if (int st0 = sjh::norm_prepare()) return st0;
+  hipStream_t s = (hipStream_t)stream;
+  const long groups = (rows + TR - 1) / TR;
+  const size_t lds = 2 * sizeof(bf16_t) * TR * (size_t)d + sizeof(float) * TR * (size_t)d;
+  const unsigned blocks = (unsigned)groups;
+  switch ((d / 2 + 63) / 64) {
+    case 1: launch_bwd_p<1>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 2: launch_bwd_p<2>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 3: launch_bwd_p<3>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 4: launch_bwd_p<4>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 5: launch_bwd_p<5>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 6: launch_bwd_p<6>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    case 7: launch_bwd_p<7>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+    default: launch_bwd_p<8>(s, blocks, lds, x, w, dy, dx_acc, dx, dx_hi, dx_lo, dx_t_hi, dx_t_lo, partial, rows, d, ldt, eps); break;
+  }
+  SJ_LAUNCH_CHECK("rmsnorm_backward_p");
+  return SJ_OK;
+}
+
+int sjh::rmsnorm_reduce_multi(void* stream, const sj::RmsReduceJob* jobs, long njobs, long max_d) {
+  SJ_REQUIRE(jobs && njobs > 0 && njobs < 65536 && max_d > 0, "rmsnorm reduce: %ld jobs", njobs);
+  hipLaunchKernelGGL(k_rms_reduce_multi, dim3((unsigned)((max_d + 31) / 32), (unsigned)njobs), dim3(NT), 0,
+                     (hipStream_t)stream, jobs);
+  SJ_LAUNCH_CHECK("rmsnorm_backward_reduce");
   return SJ_OK;
 }
 
