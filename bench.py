@@ -168,6 +168,25 @@ def op_work(op: str, mc, tc):
         "grad_norm": ("byte", P * 4),
         "adamw": ("byte", 30 * P),
     }
+    ex = getattr(mc, "experts", None)
+    if ex is not None:
+        # MoE FFN (cfg4): S = M * top_k routed rows; the grouped expert
+        # products count the routed rows only (not the 64-row segment padding)
+        E, Fe, K = ex.count, ex.ffn_width, ex.top_k
+        S = M * K
+        cap = S + 63 * E
+        table.update({
+            "mirror_transpose": ("byte", 2 * 2 * mc.layers * (d * (d + 2 * J) + d * d + 3 * E * d * Fe)),
+            "router_topk": ("flop", 2 * M * d * E), "router_dw": ("flop", 2 * M * d * E),
+            "route_pack": ("byte", 2 * S * 4 * 2),
+            "moe_gather": ("byte", 3 * S * d * 2),
+            "expert_gate_up": ("flop", 2 * S * d * 2 * Fe), "expert_down": ("flop", 2 * S * Fe * d),
+            "combine_residual": ("byte", S * d * 2 + 2 * M * d * 2),
+            "combine_bwd": ("byte", S * d * 2 + M * d * 4 + 4 * cap * d * 2),
+            "expert_down_dx_swiglu": ("flop", 2 * S * Fe * d), "expert_down_dw": ("flop", 2 * S * Fe * d),
+            "expert_gate_up_dx": ("flop", 2 * S * d * 2 * Fe), "expert_gate_up_dw": ("flop", 2 * S * d * 2 * Fe),
+            "gather_route_bwd": ("byte", S * d * 4 + 2 * M * d * 4),
+        })
     pv = getattr(tc, "parameter_vjp", None)
     if pv is not None:
         # parameter VJP (cfg5): rank R, k selected rows; every layer has a
@@ -217,7 +236,13 @@ def cpu_baseline(mc, tc, sample_batch: int):
     cfg = dict(d=mc.width, layers=mc.layers, hq=mc.heads, hk=mc.kv, ffn=mc.ffn_width, T=tc.sequence,
                B=sample_batch, eps=mc.norm_epsilon, theta=mc.rope_theta)
     t0 = time.perf_counter()
-    if mc.hierarchy is not None:
+    if getattr(mc, "experts", None) is not None:
+        from oracle import moe as OM
+        ex = mc.experts
+        mcfg = dict(cfg, E=ex.count, K=ex.top_k, fe=ex.ffn_width)
+        acts = OM.model_forward(mcfg, p, ids, mc.precision)
+        loss, g, _ = OM.model_backward(mcfg, p, acts, ids, tg, mc.precision)
+    elif mc.hierarchy is not None:
         from oracle import hierarchy as H
         h = mc.hierarchy
         hc = dict(cfg, P=h.patch_size, window=h.local_window, de=h.encoder_width, le=h.encoder_layers,
@@ -582,7 +607,7 @@ def main():
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=0,
-                    help="sequences the CPU baseline runs (default 2; 1 for the hierarchical model)")
+                    help="sequences the CPU baseline runs (default 2; 1 for the hierarchical and MoE models)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
     ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
@@ -684,7 +709,8 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (FP64 oracle) ...")
-        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch or (1 if mc.hierarchy is not None else 2))
+        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch or
+                           (1 if mc.hierarchy is not None or getattr(mc, "experts", None) is not None else 2))
         log(f"[bench] cpu baseline {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
 
     out = {
@@ -699,8 +725,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": mc.precision,
-        "data": "synthetic uniform random bytes (SplitMix64 seed 123), weights N(0,0.02) seed 42",
+        "data": "synthetic uniform random bytes (SplitMix64 seed 123), weights N(0,0.02) seed 42" +
+                (", routers N(0,1/d) (logits N(0,1))" if getattr(mc, "experts", None) is not None else ""),
         "config": {"workload": (_hier_name(args.config, mc) if mc.hierarchy is not None else
+                                f"{args.config}: {mc.layers}-layer MoE byte Transformer d{mc.width} GQA "
+                                f"{mc.heads}/{mc.kv} hd{mc.head_dim}, {mc.experts.count} SwiGLU experts x "
+                                f"{mc.experts.ffn_width} top-{mc.experts.top_k}, "
+                                if getattr(mc, "experts", None) is not None else
                                 f"{args.config}: {mc.layers}-layer byte Transformer d{mc.width} GQA "
                                 f"{mc.heads}/{mc.kv} hd{mc.head_dim} SwiGLU {mc.ffn_width}, ") +
                                ("fwd+bwd+AdamW" if tc.optimizer == "adamw" else

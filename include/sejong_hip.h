@@ -623,6 +623,20 @@ int sj_model_create(const sj_model_config *cfg, const sj_adam_config *adam, void
  * the pooled patches, global_to_decoder's output, the projected BOS row,
  * the broadcast rows, encoder_to_decoder's output, output_projection's
  * output and the final-norm output, then the logits. */
+/* The MoE byte Transformer (ModelConfig::experts, core lib.rs:100-106;
+ * Block::apply's MoE branch, architecture.rs:229-242): every block's FFN is
+ * count SwiGLU experts of ffn_width behind a router [d][count] with top_k
+ * routing (cfg's ffn_width is unused).  Parameters per layer in
+ * stage_layout order: the norms and attention matrices, experts.<e>.gate /
+ * up / down for every expert, then router.  bf16 with 64-wide heads (the
+ * MFMA-layout step), experts <= 32, top_k <= 8, width <= 1024; AdamW.  The
+ * activation pack replaces a layer's g, u, h by its router logits
+ * [rows][count]. */
+typedef struct {
+  long count, top_k, ffn_width;
+} sj_expert_config;
+int sj_model_create_experts(const sj_model_config *cfg, const sj_expert_config *experts, const sj_adam_config *adam,
+                            void *stream, sj_model **out);
 typedef struct {
   long patch_size;
   long encoder_width, encoder_layers, encoder_heads, encoder_ffn_width;
@@ -729,7 +743,9 @@ int sj_model_export_activations(sj_model *m, float *host);
  * kernels directly (what: "logits", "loss_rows", "ids", "targets",
  * "params", "grads", "mirror", "mirror_t", "workspace", "stream", and for
  * parameter-VJP models "vjp_columns", "vjp_rows", "vjp_map" (int32) and
- * "vjp_basis" (fp32 [tokens][rank])). */
+ * "vjp_basis" (fp32 [tokens][rank]); for MoE models, per layer l,
+ * "route_ids.<l>" (int32 [rows][top_k]), "route_weights.<l>" (fp32),
+ * "route_counts.<l>" and "route_offsets.<l>" (int32)). */
 int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);
 
 /* ----------------------------------------------------------- Checkpoints

@@ -46,6 +46,10 @@ class ModelConfig(ctypes.Structure):
                 ("rope_theta", _F), ("precision", _I)]
 
 
+class ExpertConfig(ctypes.Structure):
+    _fields_ = [("count", _L), ("top_k", _L), ("ffn_width", _L)]
+
+
 class HierarchyConfig(ctypes.Structure):
     _fields_ = [("patch_size", _L), ("encoder_width", _L), ("encoder_layers", _L), ("encoder_heads", _L),
                 ("encoder_ffn_width", _L), ("decoder_width", _L), ("decoder_layers", _L), ("decoder_heads", _L),
@@ -171,6 +175,8 @@ SIGNATURES = {
     "sj_safetensors_header": (_I, [ctypes.c_char_p, _P, _S, ctypes.POINTER(_S)]),
     "sj_safetensors_read": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _L]),
     "sj_checkpoint_save": (_I, [ctypes.c_char_p, ctypes.c_char_p, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P]),
+    "sj_model_create_experts": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(ExpertConfig),
+                                     ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_hierarchy": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(HierarchyConfig),
                                        ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_sgd": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(SgdConfig), _P, ctypes.POINTER(_P)]),

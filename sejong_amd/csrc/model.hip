@@ -67,6 +67,7 @@ struct RefTensor {
 
 struct Layer {
   long an, fn, qkv, wo, gu, down;  // internal offsets
+  long router = 0;                 // MoE: router [d][E] (gu = [E][d][2F], down = [E][F][d])
   int stage = 0;
 };
 
@@ -163,6 +164,15 @@ struct sj_model {
   long h_inproj = 0, h_e2g = 0, h_e2d = 0, h_g2d = 0, h_bos = 0, h_op = 0;  // glue parameters
   void *pooled = nullptr, *gd = nullptr, *bosd = nullptr, *zb = nullptr, *bytes = nullptr, *opo = nullptr;
   float* hg[8] = {};                            // glue backward scratch
+  // mixture of experts (every block; F is the expert width): routing, the
+  // packed expert rows and, per layer, the backward planes the dW stream reads
+  long E = 0, K = 0, cap = 0;
+  std::vector<uint16_t*> mlog, mzp, mzpt, myp;
+  std::vector<int32_t*> mids, mcnt, moff, mps, mpp;
+  std::vector<float*> mwts, mdwts, mdlog;
+  std::vector<uint16_t*> mdx[4], mdg[4];        // [layer]: hi, lo [cap][*]; hi^T, lo^T [*][cap]
+  float* mdzp = nullptr;
+  std::vector<hipEvent_t> ev_moe[2];
   // head: HV classes over HR rows (the LM head: V over all M tokens; the
   // NativeValue head: value_n classes over the B selected SEP rows); Vp =
   // HV rounded up to 8 (the head's row stride)
@@ -347,12 +357,14 @@ void build_layout(sj_model* m) {
   // [decay] embedding, the block matrices, the hierarchy's projections and
   // BOS row, the head
   m->emb = off; off = align64(off + V * m->stages[0].d);
+  const long NE = m->E > 0 ? m->E : 1;  // expert copies of gate|up and down
   for (Stage& S : m->stages)
     for (long l = S.first; l < S.first + S.count; l++) {
       m->layers[l].qkv = off; off = align64(off + S.d * S.NQKV);
       m->layers[l].wo = off; off = align64(off + S.d * S.d);
-      m->layers[l].gu = off; off = align64(off + S.d * 2 * S.F);
-      m->layers[l].down = off; off = align64(off + S.F * S.d);
+      m->layers[l].gu = off; off = align64(off + NE * S.d * 2 * S.F);
+      m->layers[l].down = off; off = align64(off + NE * S.F * S.d);
+      if (m->E) { m->layers[l].router = off; off = align64(off + S.d * m->E); }
     }
   if (m->hier) {
     const long de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d;
@@ -381,6 +393,16 @@ void build_layout(sj_model* m) {
       add(p + "key", d, J, y.qkv + d, S.NQKV, li, 0, 1, d);
       add(p + "value", d, J, y.qkv + d + J, S.NQKV, li, 0, 2, d + J);
       add(p + "attention_output", d, d, y.wo, d);
+      if (m->E) {  // experts.<e>.gate / up / down, then router
+        for (long e = 0; e < m->E; e++) {
+          const std::string q = p + "experts." + std::to_string(e) + ".";
+          add(q + "gate", d, F, y.gu + e * d * 2 * F, 2 * F);
+          add(q + "up", d, F, y.gu + e * d * 2 * F + F, 2 * F);
+          add(q + "down", F, d, y.down + e * F * d, d);
+        }
+        add(p + "router", d, m->E, y.router, m->E);
+        continue;
+      }
       add(p + "gate", d, F, y.gu, 2 * F, li, 1, 0, 0);
       add(p + "up", d, F, y.gu + F, 2 * F, li, 1, 1, F);
       add(p + "down", F, d, y.down, d);
@@ -491,6 +513,19 @@ int stage_forward(sj_model* m, int si) {
                                              ldt, m->B, S.T, S.HQ, S.HK, S.Dh));
     OP("attn_out_residual", sj_linear_residual_fwd_t(s, o, d, M, d, WT + y.wo, d, d, x, d, (uint16_t*)m->x1[l], d));
     OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], ldt, M, d, eps));
+    if (m->E) {  // Block::apply's MoE branch (architecture.rs:229-242), packed by expert on the device
+      const long E = m->E, K = m->K, cap = m->cap;
+      OP("router_topk", sj_router_topk(s, z2, d, W + y.router, d, M, E, K, m->mlog[l], m->mids[l], m->mwts[l]));
+      OP("route_pack", sj_route_pack(s, m->mids[l], M, K, E, nullptr, nullptr, m->mcnt[l], m->moff[l], m->mps[l],
+                                     m->mpp[l], cap));
+      OP("moe_gather", sj_moe_gather(s, z2, d, d, m->mps[l], K, cap, m->mzp[l], m->mzpt[l], cap));
+      OP("expert_gate_up", sj_moe_gate_up_fwd(s, m->moff[l], E, cap, m->mzp[l], d, d, WT + y.gu, WT + y.gu + F * d, d,
+                                              2 * F * d, F, gg, uu, hh, F, m->ht[l], cap));
+      OP("expert_down", sj_moe_down_fwd(s, m->moff[l], E, cap, hh, F, F, WT + y.down, F, d * F, d, m->myp[l], d));
+      OP("combine_residual", sj_moe_combine(s, m->myp[l], d, d, m->mids[l], m->mpp[l], m->mwts[l], M, K, x1, d,
+                                            (uint16_t*)xout(m, l), d));
+      continue;
+    }
     OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F, m->ht[l],
                                           ldt));
     OP("down_residual", sj_linear_residual_fwd_t(s, hh, F, M, F, WT + y.down, F, d, x1, d, (uint16_t*)xout(m, l), d));
@@ -660,6 +695,42 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       const Layer& y = m->layers[l];
       const uint16_t* qkv = (const uint16_t*)m->qkv[l];
       const int p = (int)(l & 1);
+      if (m->E) {
+        // x_{l+1} = x1 + combine(experts(z2)): combine backward (dY of every
+        // packed row, routing-weight gradients), the experts' down dX with the
+        // SwiGLU derivative, gate|up dX, the gather's sum with the routing and
+        // router backward into dz; the experts' and router's dW on the second
+        // stream from this layer's own planes
+        const long E = m->E, K = m->K, cap = m->cap;
+        uint16_t* mx[4] = {m->mdx[0][l], m->mdx[1][l], m->mdx[2][l], m->mdx[3][l]};
+        uint16_t* mg[4] = {m->mdg[0][l], m->mdg[1][l], m->mdg[2][l], m->mdg[3][l]};
+        TRY(read(KR, p));  // the rp transposed planes go unread here
+        OP("combine_bwd", sj_moe_combine_bwd(s, m->myp[l], d, d, m->mps[l], m->mwts[l], K, cap, m->dres[cur], d, mx[0],
+                                             mx[1], mx[2], mx[3], cap, m->mdwts[l]));
+        OP("expert_down_dx_swiglu", sj_moe_down_bwd_swiglu_p(s, m->moff[l], E, cap, mx[0], mx[1], d, d, W + y.down, d,
+                                                             F * d, F, (const uint16_t*)m->gg[l],
+                                                             (const uint16_t*)m->uu[l], F, mg[0], mg[1], 2 * F, mg[2],
+                                                             mg[3], cap));
+        if (two) {
+          SJ_HIP(hipEventRecord(m->ev_moe[0][l], s));
+          SJ_HIP(hipStreamWaitEvent(s2, m->ev_moe[0][l], 0));
+        }
+        OP("expert_down_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, F, d, m->ht[l], cap, mx[2], mx[3], cap, G + y.down,
+                                            d, F * d));
+        OP("expert_gate_up_dx", sj_moe_gemm_rows(s, m->moff[l], E, cap, d, 2 * F, mg[0], mg[1], 2 * F, W + y.gu, 2 * F,
+                                                 d * 2 * F, m->mdzp, d, 0));
+        OP("expert_gate_up_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, d, 2 * F, m->mzpt[l], cap, mg[2], mg[3], cap,
+                                               G + y.gu, 2 * F, d * 2 * F));
+        OP("gather_route_bwd", sj_moe_gather_bwd(s, m->mdzp, d, d, m->mids[l], m->mpp[l], m->mwts[l], m->mlog[l],
+                                                 m->mdwts[l], W + y.router, M, K, E, nullptr, d, m->dz, d,
+                                                 m->mdlog[l]));
+        if (two) {
+          SJ_HIP(hipEventRecord(m->ev_moe[1][l], s));
+          SJ_HIP(hipStreamWaitEvent(s2, m->ev_moe[1][l], 0));
+        }
+        OP("router_dw", sj_gemm(s2, 1, 0, d, E, M, m->z2[l], SJ_BF16, d, m->mdlog[l], SJ_F32, E, G + y.router, SJ_F32, E,
+                                0, ws2, wsb));
+      } else {
       // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
       TRY(reuse(KG, p));
       OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, rp[0], rp[1], d, M, d, W + y.down, d, F, (const uint16_t*)m->gg[l],
@@ -676,6 +747,7 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         OP("gate_up_dw", sj_gemm_planes(s2, d, 2 * F, M, m->z2t[l], nullptr, ldt, T(KG, p)[0], T(KG, p)[1], ldt,
                                         G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       TRY(read(KG, p));
+      }
       TRY(reuse(KX, p));
       OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1,
                                                     xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps,
@@ -1036,8 +1108,8 @@ int stage_sgd(sj_model* m, float lr) {
   return SJ_OK;
 }
 
-int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_adam_config* adam,
-                 const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out);
+int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_expert_config* ec,
+                 const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out);
 
 }  // namespace
 
@@ -1046,13 +1118,19 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
 extern "C" int sj_model_create(const sj_model_config* cfg, const sj_adam_config* adam, void* stream,
                                sj_model** out) {
   SJ_REQUIRE(cfg && adam && out, "model: null argument");
-  return create_model(cfg, nullptr, adam, nullptr, 0, stream, out);
+  return create_model(cfg, nullptr, nullptr, adam, nullptr, 0, stream, out);
+}
+
+extern "C" int sj_model_create_experts(const sj_model_config* cfg, const sj_expert_config* experts,
+                                       const sj_adam_config* adam, void* stream, sj_model** out) {
+  SJ_REQUIRE(cfg && experts && adam && out, "model: null argument");
+  return create_model(cfg, nullptr, experts, adam, nullptr, 0, stream, out);
 }
 
 extern "C" int sj_model_create_hierarchy(const sj_model_config* cfg, const sj_hierarchy_config* hierarchy,
                                          const sj_adam_config* adam, void* stream, sj_model** out) {
   SJ_REQUIRE(cfg && hierarchy && adam && out, "model: null argument");
-  return create_model(cfg, hierarchy, adam, nullptr, 0, stream, out);
+  return create_model(cfg, hierarchy, nullptr, adam, nullptr, 0, stream, out);
 }
 
 extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_config* sgd, void* stream,
@@ -1061,7 +1139,7 @@ extern "C" int sj_model_create_sgd(const sj_model_config* cfg, const sj_sgd_conf
   SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
                  (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
              "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
-  return create_model(cfg, nullptr, nullptr, sgd, 0, stream, out);
+  return create_model(cfg, nullptr, nullptr, nullptr, sgd, 0, stream, out);
 }
 
 extern "C" int sj_model_create_value(const sj_model_config* cfg, long values, const sj_adam_config* adam,
@@ -1073,12 +1151,12 @@ extern "C" int sj_model_create_value(const sj_model_config* cfg, long values, co
     SJ_REQUIRE(sgd->loss_scale > 0.f && isfinite(sgd->loss_scale) && sgd->weight_decay >= 0.f &&
                    (!sgd->clip_enabled || (isfinite(sgd->clip_norm) && sgd->clip_norm > 0.f)),
                "optimizer requires nonnegative weight decay, positive loss scale and positive enabled clip norm");
-  return create_model(cfg, nullptr, adam, sgd, values, stream, out);
+  return create_model(cfg, nullptr, nullptr, adam, sgd, values, stream, out);
 }
 
 namespace {
-int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_adam_config* adam,
-                 const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out) {
+int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, const sj_expert_config* ec,
+                 const sj_adam_config* adam, const sj_sgd_config* sgd, long value_n, void* stream, sj_model** out) {
   const sj_model_config& c = *cfg;
   SJ_REQUIRE(c.vocab > 0 && c.width > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 && c.ffn_width > 0 &&
                  c.sequence > 0 && c.batch > 0,
@@ -1097,6 +1175,14 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
                    (hc->encoder_width / hc->encoder_heads) % 2 == 0 && (hc->decoder_width / hc->decoder_heads) % 2 == 0,
                "hierarchy: local widths must split into even heads");
     SJ_REQUIRE(!value_n && !sgd, "hierarchy: the hierarchical model trains with AdamW on the byte objective");
+  }
+  if (ec) {
+    SJ_REQUIRE(ec->count > 0 && ec->count <= 32 && ec->top_k > 0 && ec->top_k <= 8 && ec->top_k <= ec->count &&
+                   ec->ffn_width > 0 && ec->ffn_width % 8 == 0,
+               "experts: 1..32 experts, top_k in 1..min(8, count), ffn_width a positive multiple of 8");
+    SJ_REQUIRE(!hc && !value_n && !sgd, "experts: the MoE model trains with AdamW on the byte objective");
+    SJ_REQUIRE(c.precision == SJ_BF16 && c.width / c.heads == 64 && c.width % 8 == 0 && c.width <= 1024,
+               "experts: the MoE step runs the bf16 MFMA-layout path (64-wide heads, width <= 1024)");
   }
   sj_model* m = new sj_model();
   m->c = c;
@@ -1125,7 +1211,12 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   m->HK = c.kv_heads;
   m->Dh = c.width / c.heads;
   m->J = m->Dh * c.kv_heads;
-  m->F = c.ffn_width;
+  m->F = ec ? ec->ffn_width : c.ffn_width;
+  if (ec) {
+    m->E = ec->count;
+    m->K = ec->top_k;
+    m->cap = sj_route_pack_capacity(c.sequence * c.batch * ec->top_k, ec->count);
+  }
   m->T = c.sequence;
   m->B = c.batch;
   m->M = c.sequence * c.batch;
@@ -1156,7 +1247,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     stage("decoder", hc->decoder_layers, hc->decoder_width, hc->decoder_heads, hc->decoder_heads,
           hc->decoder_ffn_width, c.sequence, hc->local_window);
   } else {
-    stage("layers", c.layers, c.width, c.heads, c.kv_heads, c.ffn_width, c.sequence, 0);
+    stage("layers", c.layers, c.width, c.heads, c.kv_heads, m->F, c.sequence, 0);
   }
   m->L = 0;
   for (const Stage& S : m->stages) m->L += S.count;
@@ -1178,6 +1269,11 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       for (const Stage& S : m->stages) planes = planes && S.M % 8 == 0;
     }
     m->planes = planes;
+    if (m->E && !planes) {
+      if (m->own_stream) hipStreamDestroy(m->stream);
+      delete m;
+      return sjh::fail(SJ_ERR_UNSUPPORTED, "experts: the MoE step needs the MFMA-layout path (SJ_PLANES unset)");
+    }
     for (Stage& S : m->stages) S.attn_tt = S.attn_tt && planes;
     m->attn_tt = m->stages[0].attn_tt;
   }
@@ -1221,8 +1317,10 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       const Stage& S = m->stages[y.stage];
       job(y.qkv, S.d, S.NQKV);
       job(y.wo, S.d, S.d);
-      job(y.gu, S.d, 2 * S.F);
-      job(y.down, S.F, S.d);
+      for (long e = 0; e < (m->E ? m->E : 1); e++) {
+        job(y.gu + e * S.d * 2 * S.F, S.d, 2 * S.F);
+        job(y.down + e * S.F * S.d, S.F, S.d);
+      }
     }
     m->tjob_n = (int)jobs.size();
     m->tjob_tiles = tiles;
@@ -1255,9 +1353,37 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     ALLOC(m->lse[l], M * (size_t)S.HQ * 4);
     ALLOC(m->x1[l], M * d * es);
     ALLOC(m->z2[l], M * d * es);
-    ALLOC(m->gg[l], M * F * es);
-    ALLOC(m->uu[l], M * F * es);
-    ALLOC(m->hh[l], M * F * es);
+    const size_t FR = m->E ? (size_t)m->cap : M;  // rows of g, u, h: the packed expert rows under MoE
+    ALLOC(m->gg[l], FR * F * es);
+    ALLOC(m->uu[l], FR * F * es);
+    ALLOC(m->hh[l], FR * F * es);
+  }
+  if (m->E) {
+    const size_t M = (size_t)m->M, d = (size_t)m->d, F = (size_t)m->F, E = (size_t)m->E, S = M * (size_t)m->K;
+    const size_t cap = (size_t)m->cap;
+    for (auto* v : {&m->mlog, &m->mzp, &m->mzpt, &m->myp}) v->assign(m->L, nullptr);
+    for (auto* v : {&m->mids, &m->mcnt, &m->moff, &m->mps, &m->mpp}) v->assign(m->L, nullptr);
+    for (auto* v : {&m->mwts, &m->mdwts, &m->mdlog}) v->assign(m->L, nullptr);
+    for (int i = 0; i < 4; i++) { m->mdx[i].assign(m->L, nullptr); m->mdg[i].assign(m->L, nullptr); }
+    for (long l = 0; l < m->L; l++) {
+      ALLOC(m->mlog[l], M * E * 2);
+      ALLOC(m->mids[l], S * 4);
+      ALLOC(m->mwts[l], S * 4);
+      ALLOC(m->mcnt[l], E * 4);
+      ALLOC(m->moff[l], (E + 1) * 4);
+      ALLOC(m->mps[l], cap * 4);
+      ALLOC(m->mpp[l], S * 4);
+      ALLOC(m->mzp[l], cap * d * 2);
+      ALLOC(m->mzpt[l], d * cap * 2);
+      ALLOC(m->myp[l], cap * d * 2);
+      ALLOC(m->mdwts[l], S * 4);
+      ALLOC(m->mdlog[l], M * E * 4);
+      for (int i = 0; i < 4; i++) {
+        ALLOC(m->mdx[i][l], cap * d * 2);
+        ALLOC(m->mdg[i][l], cap * 2 * F * 2);
+      }
+    }
+    ALLOC(m->mdzp, cap * d * 4);
   }
   if (m->planes) {
     m->zt.resize(m->L); m->ot.resize(m->L); m->z2t.resize(m->L); m->ht.resize(m->L);
@@ -1267,7 +1393,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       ALLOC(m->zt[l], d * MT * 2);
       ALLOC(m->ot[l], d * MT * 2);
       ALLOC(m->z2t[l], d * MT * 2);
-      ALLOC(m->ht[l], (size_t)S.F * MT * 2);
+      ALLOC(m->ht[l], (size_t)S.F * (m->E ? (size_t)m->cap : MT) * 2);
     }
     bool any_tt = false;
     for (const Stage& S : m->stages) any_tt = any_tt || S.attn_tt;
@@ -1422,6 +1548,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       upd(sj_gemm_planes_workspace_bytes(Mi, S.d, S.NQKV));
     }
   }
+  if (m->E) upd(sj_gemm_workspace_bytes(m->d, m->E, m->M));
   if (m->hier) {
     const Stage &E = m->stages[0], &Gs = m->stages[1], &D = m->stages[2];
     const long de = E.d, dg = Gs.d, dd = D.d, Ml = E.M, Mg = Gs.M;
@@ -1462,7 +1589,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     const size_t MT = (size_t)S.ldt;
     for (uint16_t* q : {m->zt[l], m->ot[l], m->z2t[l]})
       if (e == hipSuccess) e = hipMemsetAsync(q, 0, (size_t)S.d * MT * 2, s);
-    if (e == hipSuccess) e = hipMemsetAsync(m->ht[l], 0, (size_t)S.F * MT * 2, s);
+    if (e == hipSuccess) e = hipMemsetAsync(m->ht[l], 0, (size_t)S.F * (m->E ? (size_t)m->cap : MT) * 2, s);
   }
   {
     const size_t sizes[4] = {mxLd, 2 * mxLF, mxLd, mxLNQ};
@@ -1480,6 +1607,11 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_norm, hipEventDisableTiming);
+    for (int k = 0; k < 2 && m->E; k++) {
+      m->ev_moe[k].assign(m->L, nullptr);
+      for (long l = 0; l < m->L && e == hipSuccess; l++)
+        e = hipEventCreateWithFlags(&m->ev_moe[k][l], hipEventDisableTiming);
+    }
   }
   for (int i = 2; i < 4 && m->planes; i++) {
     if (e == hipSuccess) e = hipMemsetAsync(m->rp[i], 0, mxLd * 2, s);
@@ -1536,6 +1668,9 @@ extern "C" int sj_model_destroy(sj_model* m) {
   if (m->ev_fork) hipEventDestroy(m->ev_fork);
   if (m->ev_join) hipEventDestroy(m->ev_join);
   if (m->ev_norm) hipEventDestroy(m->ev_norm);
+  for (int k = 0; k < 2; k++)
+    for (hipEvent_t ev : m->ev_moe[k])
+      if (ev) hipEventDestroy(ev);
   if (m->stream2) {
     hipStreamSynchronize(m->stream2);
     hipStreamDestroy(m->stream2);
@@ -1765,7 +1900,8 @@ extern "C" long sj_model_activation_count(const sj_model* m) {
   if (!m) return -1;
   long n = 0;
   for (const Stage& S : m->stages)
-    n += S.count * (6 * S.M * S.d + 2 * S.M * S.J + S.M * S.HQ + 3 * S.M * S.F) + 2 * S.M * S.d;
+    n += S.count * (6 * S.M * S.d + 2 * S.M * S.J + S.M * S.HQ + (m->E ? S.M * m->E : 3 * S.M * S.F)) +
+         2 * S.M * S.d;
   if (m->hier) {
     const Stage &E = m->stages[0], &G = m->stages[1], &D = m->stages[2];
     n += G.M * E.d + G.M * D.d + D.d + 2 * E.M * D.d + 2 * E.M * G.d;
@@ -1810,6 +1946,10 @@ extern "C" int sj_model_export_activations(sj_model* m, float* host) {
       TRY(export_matrix(m, m->lse[l], SJ_F32, M, S.HQ, 0, S.HQ, p)); p += M * S.HQ;
       TRY(export_matrix(m, m->x1[l], dt, M, d, 0, d, p)); p += M * d;
       TRY(export_matrix(m, m->z2[l], dt, M, d, 0, d, p)); p += M * d;
+      if (m->E) {  // the router's stored logits stand for g, u, h
+        TRY(export_matrix(m, m->mlog[l], SJ_BF16, M, m->E, 0, m->E, p)); p += M * m->E;
+        continue;
+      }
       TRY(export_matrix(m, m->gg[l], dt, M, F, 0, F, p)); p += M * F;
       TRY(export_matrix(m, m->uu[l], dt, M, F, 0, F, p)); p += M * F;
       TRY(export_matrix(m, m->hh[l], dt, M, F, 0, F, p)); p += M * F;
@@ -1877,6 +2017,19 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   else if (w == "vjp_rows" && m->vjp) { *ptr = m->vjp_rows; n = m->vjp_k; }
   else if (w == "vjp_map" && m->vjp) { *ptr = m->vjp_map; n = m->d; }
   else if (w == "vjp_basis" && m->vjp) { *ptr = m->vjp_q; n = m->M * m->vjp_R; }
+  else if (m->E && w.rfind("route_", 0) == 0 && w.find('.') != std::string::npos) {
+    // route_ids.<l>, route_weights.<l> [rows][top_k], route_counts.<l>
+    // [experts], route_offsets.<l> [experts + 1] of MoE layer l
+    const std::string kind = w.substr(0, w.find('.'));
+    char* end = nullptr;
+    const long l = strtol(w.c_str() + w.find('.') + 1, &end, 10);
+    SJ_REQUIRE(end && *end == 0 && l >= 0 && l < m->L, "buffer: bad layer in %s", what);
+    if (kind == "route_ids") { *ptr = m->mids[l]; n = m->M * m->K; }
+    else if (kind == "route_weights") { *ptr = m->mwts[l]; n = m->M * m->K; }
+    else if (kind == "route_counts") { *ptr = m->mcnt[l]; n = m->E; }
+    else if (kind == "route_offsets") { *ptr = m->moff[l]; n = m->E + 1; }
+    else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);
+  }
   else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);
   if (elements) *elements = n;
   return SJ_OK;

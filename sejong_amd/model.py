@@ -40,6 +40,15 @@ class HierarchyConfig:
 
 
 @dataclass
+class ExpertConfig:
+    """crates/sejong-core/src/lib.rs:100-106: every block's FFN is `count`
+    SwiGLU experts of `ffn_width` with top_k routing."""
+    count: int = 8
+    top_k: int = 2
+    ffn_width: int = 1024
+
+
+@dataclass
 class ModelConfig:
     """crates/sejong-core/src/lib.rs:60-111 (dense and hierarchical models;
     no experts on this path)."""
@@ -55,6 +64,7 @@ class ModelConfig:
     seed: int = 42
     hierarchy: HierarchyConfig | None = None
     id: str = "sejong"
+    experts: ExpertConfig | None = None
 
     @property
     def kv(self) -> int:
@@ -151,10 +161,15 @@ def config(name: str) -> tuple[ModelConfig, TrainConfig]:
                                                       decoder_layers=2, decoder_heads=4, decoder_ffn_width=768,
                                                       local_window=128)),
                 TrainConfig(sequence=1024, batch=8, learning_rate=3e-4, weight_decay=0.01))
+    if name == "cfg4":  # MoE byte Transformer: 8 SwiGLU experts of 1024, top-2 (router logits N(0,1))
+        return (ModelConfig(width=512, layers=4, heads=8, kv_heads=2, ffn_width=1024, context=512, precision="bf16",
+                            experts=ExpertConfig(count=8, top_k=2, ffn_width=1024)),
+                TrainConfig(sequence=512, batch=8, learning_rate=3e-4, weight_decay=0.01))
     raise KeyError(name)
 
 
-def _stage_layout(prefix: str, d: int, layers: int, heads: int, kv_heads: int, ffn: int):
+def _stage_layout(prefix: str, d: int, layers: int, heads: int, kv_heads: int, ffn: int,
+                  experts: ExpertConfig | None = None):
     """stage_layout (architecture.rs:63-95)."""
     kv = d // heads * kv_heads
     out = []
@@ -162,8 +177,15 @@ def _stage_layout(prefix: str, d: int, layers: int, heads: int, kv_heads: int, f
         p = f"{prefix}.{i}"
         out += [(f"{p}.attention_norm", (d,), True), (f"{p}.ffn_norm", (d,), True),
                 (f"{p}.query", (d, d), False), (f"{p}.key", (d, kv), False), (f"{p}.value", (d, kv), False),
-                (f"{p}.attention_output", (d, d), False),
-                (f"{p}.gate", (d, ffn), False), (f"{p}.up", (d, ffn), False), (f"{p}.down", (ffn, d), False)]
+                (f"{p}.attention_output", (d, d), False)]
+        if experts is not None:
+            fe = experts.ffn_width
+            for e in range(experts.count):
+                q = f"{p}.experts.{e}"
+                out += [(f"{q}.gate", (d, fe), False), (f"{q}.up", (d, fe), False), (f"{q}.down", (fe, d), False)]
+            out.append((f"{p}.router", (d, experts.count), False))
+        else:
+            out += [(f"{p}.gate", (d, ffn), False), (f"{p}.up", (d, ffn), False), (f"{p}.down", (ffn, d), False)]
     return out
 
 
@@ -171,7 +193,7 @@ def layout(c: ModelConfig) -> list[tuple[str, tuple[int, ...], bool]]:
     """(name, shape, is_norm) in the reference order (architecture.rs:96-137)."""
     d = c.width
     h = c.hierarchy
-    glob = _stage_layout("layers", d, c.layers, c.heads, c.kv, c.ffn_width)
+    glob = _stage_layout("layers", d, c.layers, c.heads, c.kv, c.ffn_width, c.experts)
     if h is None:
         return [("embedding", (VOCAB, d), False)] + glob + [("final_norm", (d,), True), ("output", (d, VOCAB), False)]
     de, dd = h.encoder_width, h.decoder_width
@@ -203,8 +225,9 @@ def init_params(c: ModelConfig, std: float | None = 0.02, seed: int | None = Non
     """Flat fp32 masters in the reference layout.  std=None restates
     Model::initialize (model lib.rs:83-115): N(0, 1/sqrt(fan_in)), /sqrt(2
     depth) for down / attention_output (depth = the layers of the tensor's
-    stage), embedding 1/sqrt(d); otherwise every matrix is N(0, std) (the
-    BASELINE weights).  Norm weights are 1, global_bos 0."""
+    stage), embedding 1/sqrt(d); otherwise every matrix is N(0, std) except
+    a router, N(0, 1/sqrt(d)) either way (router logits N(0, 1) on unit-RMS
+    rows).  Norm weights are 1, global_bos 0."""
     rng = Rng(c.seed if seed is None else seed)
     h = c.hierarchy
     parts = []
@@ -225,6 +248,8 @@ def init_params(c: ModelConfig, std: float | None = 0.02, seed: int | None = Non
                 depth = h.decoder_layers
             if name.endswith(".down") or name.endswith(".attention_output"):
                 s /= math.sqrt(2.0 * depth)
+        elif name.endswith(".router"):   # cfg4: router logits N(0, 1) over unit-RMS rows
+            s = 1.0 / math.sqrt(shape[0])
         else:
             s = std
         parts.append(rng.normal(n, s))
@@ -271,7 +296,13 @@ class Model:
             adam = N.AdamConfig(beta1=tc.beta1, beta2=tc.beta2, epsilon=tc.epsilon, weight_decay=tc.weight_decay,
                                 clip_norm=tc.clip_norm, loss_scale=tc.loss_scale, clip_enabled=int(tc.clip_enabled))
         s = ctypes.c_void_p(stream or 0)
-        if mc.hierarchy is not None:
+        if mc.experts is not None:
+            if values or sgd is not None or mc.hierarchy is not None:
+                raise ValueError("the MoE model trains with AdamW on the byte objective")
+            ex = N.ExpertConfig(count=mc.experts.count, top_k=mc.experts.top_k, ffn_width=mc.experts.ffn_width)
+            N.api.sj_model_create_experts(ctypes.byref(cfg), ctypes.byref(ex), ctypes.byref(adam), s,
+                                          ctypes.byref(handle))
+        elif mc.hierarchy is not None:
             if values or sgd is not None:
                 raise ValueError("the hierarchical model trains with AdamW on the byte objective")
             h = mc.hierarchy

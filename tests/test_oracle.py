@@ -697,3 +697,86 @@ def test_hierarchy_window_and_stage_reduce_to_dense_blocks():
     g_stage, dx = O.stage_backward(dict(cfg, window=0), body, st, dz, "none")
     np.testing.assert_allclose(g_stage, g_dense[V * d:n - d * V], rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(dx, demb, rtol=1e-12, atol=1e-12)
+
+
+def _moe_model_cfg(E=3, K=2):
+    return dict(d=16, layers=2, hq=2, hk=1, E=E, K=K, fe=12, T=8, B=2, eps=1e-6, theta=10000.0)
+
+
+def _moe_params(cfg, rng):
+    from oracle import moe
+    table, total = moe._offsets(cfg)
+    p = rng.normal(0, 0.3, total)
+    for name, (o, shape) in table.items():
+        if name.endswith("norm"):
+            p[o:o + int(np.prod(shape))] = 1.0 + rng.normal(0, 0.1, int(np.prod(shape)))
+    return table, p
+
+
+def test_moe_model_single_expert_is_dense_model():
+    """E = 1, K = 1: every routing weight is exactly 1, so the MoE model is
+    the dense model with gate / up / down = expert 0's: loss and gradients
+    equal the dense C oracle's (exact FP64 and bf16 storage), and the
+    router's gradient is exactly 0."""
+    from oracle import moe
+    cfg = _moe_model_cfg(E=1, K=1)
+    rng = np.random.default_rng(17)
+    table, p = _moe_params(cfg, rng)
+    keep = np.ones(p.size, bool)
+    for l in range(cfg["layers"]):
+        o, shape = table[f"layers.{l}.router"]
+        keep[o:o + int(np.prod(shape))] = False
+    dense = p[keep]
+    dcfg = dict(d=16, layers=2, hq=2, hk=1, ffn=12, T=8, B=2, eps=1e-6, theta=10000.0)
+    assert dense.size == O.model_param_count(16, 2, 2, 1, 12)
+    M = 16
+    ids = rng.integers(0, 256, M).astype(np.int32)
+    tg = rng.integers(0, 256, M).astype(np.int32)
+    for dtype, tol in (("none", 1e-11), ("bf16", 1e-11)):
+        acts = moe.model_forward(cfg, p, ids, dtype)
+        loss, g, routing = moe.model_backward(cfg, p, acts, ids, tg, dtype)
+        dloss, dg, _, _ = O.model_fwd_bwd(dcfg, dense, ids, tg, dtype)
+        assert abs(loss - dloss) <= tol * abs(dloss), (dtype, loss, dloss)
+        np.testing.assert_allclose(g[keep], dg, rtol=tol, atol=tol * np.abs(dg).max())
+        assert not np.any(g[~keep])
+        for ids_l, w_l, counts, _, _ in routing:
+            assert np.all(ids_l == 0) and np.all(w_l == 1.0) and counts[0] == M
+
+
+def test_moe_model_gradient_finite_difference():
+    """The composed MoE model backward (head, final norm, per layer the
+    MoE FFN with the router, ffn norm, attention, QKV, attention norm,
+    embedding) against central differences of its own exact FP64 loss for
+    entries of every tensor kind (routing held fixed: no top-k swap within
+    the step)."""
+    from oracle import moe
+    cfg = _moe_model_cfg()
+    rng = np.random.default_rng(23)
+    table, p = _moe_params(cfg, rng)
+    M = cfg["B"] * cfg["T"]
+    ids = rng.integers(0, 256, M).astype(np.int32)
+    tg = rng.integers(0, 256, M).astype(np.int32)
+    acts = moe.model_forward(cfg, p, ids, "none")
+    loss, g, routing = moe.model_backward(cfg, p, acts, ids, tg, "none")
+    assert abs(loss - moe.model_loss(cfg, p, ids, tg)) < 1e-12
+    assert all(np.all(r[2] > 0) for r in routing)          # every expert receives rows
+    names = ["embedding", "layers.0.attention_norm", "layers.0.query", "layers.1.key", "layers.0.value",
+             "layers.1.attention_output", "layers.0.ffn_norm", "layers.0.experts.0.gate", "layers.1.experts.2.up",
+             "layers.0.experts.1.down", "layers.0.router", "layers.1.router", "final_norm", "output"]
+    h = 1e-5
+    worst = 0.0
+    for name in names:
+        o, shape = table[name]
+        n = int(np.prod(shape))
+        idx = [o + i for i in rng.choice(n, size=min(n, 3), replace=False)]
+        if name == "embedding":
+            idx = [o + int(ids[0]) * cfg["d"] + 1, o + int(ids[5]) * cfg["d"] + 3]
+        for i in idx:
+            pp, pm = p.copy(), p.copy()
+            pp[i] += h
+            pm[i] -= h
+            fd = (moe.model_loss(cfg, pp, ids, tg) - moe.model_loss(cfg, pm, ids, tg)) / (2 * h)
+            err = abs(fd - g[i]) / (abs(fd) + 1e-6)
+            worst = max(worst, err)
+            assert err < 1e-4, (name, i, fd, g[i])
+    print(f"[moe model] worst FD relative error {worst:.2e}")
