@@ -206,9 +206,10 @@ int sj_gemm_planes(void *stream, long M, long N, long K, const uint16_t *a_hi, c
                    long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, void *c, int c_dtype,
                    long ldc, int accumulate, void *workspace, size_t workspace_bytes);
 /* dX = dY W^T of a projection (graph.rs:829-851) with dY as hi/lo planes
- * [M][K] and W^T [N][K] bf16, its fp32 result written as hi/lo planes in
- * both orientations: c [M][ldc] and c_t [N][ldct] (ldct >= M, multiple of
- * 8) -- the dO operands of the attention backward. */
+ * [M][K] and W^T [N][K] bf16, its fp32 result written as hi/lo planes
+ * c [M][ldc] (the dO operands of the attention backward) and, when c_t_hi
+ * and c_t_lo are non-null, also transposed c_t [N][ldct] (ldct >= M,
+ * multiple of 8). */
 int sj_gemm_planes_split_out(void *stream, long M, long N, long K, const uint16_t *a_hi, const uint16_t *a_lo,
                              long lda, const uint16_t *b, long ldb, uint16_t *c_hi, uint16_t *c_lo, long ldc,
                              uint16_t *c_t_hi, uint16_t *c_t_lo, long ldct);
@@ -303,25 +304,23 @@ int sj_patch_broadcast(void *stream, const void *x, const void *bos, int dtype, 
 int sj_patch_broadcast_bwd(void *stream, const float *dy, long batch, long t, long d, long patch, float *dx,
                            float *dbos);
 
-/* The step's attention over operands its producers wrote in MFMA layout
- * (bf16, head_dim 64, t a multiple of 64; window as sj_attention_fwd: a
- * query sees the `window` last positions up to itself, 0 = all): qkv [batch*t][ldqkv] (q | k | v
- * columns, q and k after RoPE) with its transpose qkv_t [(hq+2hk)*64][ldt]
- * (sj_qkv_fwd_t's second output).  Forward = hierarchy_attention
+/* The step's attention in MFMA layout (bf16, head_dim 64, t a multiple of
+ * 64; window as sj_attention_fwd: a query sees the `window` last positions
+ * up to itself, 0 = all): qkv [batch*t][ldqkv] (q | k | v columns, q and k
+ * after RoPE; sj_qkv_fwd_t's output).  Forward = hierarchy_attention
  * (hierarchy.py:7-39): o [rows][ldo], lse [rows][hq] (nullable, the
  * reference layout) and lse_t [hq][ldt], o_t [hq*64][ldot] (nullable).
  * Backward = hierarchy_attention_dq + _dkv (hierarchy.py:42-104) from dO
- * as hi/lo planes [rows][lddo] and transposed [hq*64][lddot]
- * (sj_gemm_planes_split_out), writing Delta into delta_t [hq][ldt] and
- * dQ | dK | dV (inverse RoPE on dQ, dK) as hi/lo planes like
- * sj_attention_bwd_p; workspace sj_attention_bwd_tt_workspace_bytes. */
-int sj_attention_fwd_tt(void *stream, const uint16_t *qkv, long ldqkv, const uint16_t *qkv_t, long ldt, long batch,
-                        long t, long hq, long hk, long head_dim, long window, uint16_t *o, long ldo, float *lse,
-                        float *lse_t, uint16_t *o_t, long ldot);
+ * as hi/lo planes [rows][lddo] (sj_gemm_planes_split_out), writing Delta
+ * into delta_t [hq][ldt] and dQ | dK | dV (inverse RoPE on dQ, dK) as hi/lo
+ * planes like sj_attention_bwd_p; workspace
+ * sj_attention_bwd_tt_workspace_bytes.  ldt >= batch*t, a multiple of 8. */
+int sj_attention_fwd_tt(void *stream, const uint16_t *qkv, long ldqkv, long ldt, long batch, long t, long hq,
+                        long hk, long head_dim, long window, uint16_t *o, long ldo, float *lse, float *lse_t,
+                        uint16_t *o_t, long ldot);
 size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long hq, long hk, long head_dim);
-int sj_attention_bwd_tt(void *stream, const uint16_t *qkv, long ldqkv, const uint16_t *qkv_t, long ldt,
-                        const uint16_t *o, long ldo, const float *lse_t, const uint16_t *do_hi, const uint16_t *do_lo,
-                        long lddo, const uint16_t *do_t_hi, const uint16_t *do_t_lo, long lddot, float *delta_t,
+int sj_attention_bwd_tt(void *stream, const uint16_t *qkv, long ldqkv, long ldt, const uint16_t *o, long ldo,
+                        const float *lse_t, const uint16_t *do_hi, const uint16_t *do_lo, long lddo, float *delta_t,
                         long batch, long t, long hq, long hk, long head_dim, long window, const float *rope_table,
                         uint16_t *g_hi, uint16_t *g_lo, long ldg, uint16_t *g_t_hi, uint16_t *g_t_lo, long ldgt,
                         void *workspace, size_t workspace_bytes);

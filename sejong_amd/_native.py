@@ -144,9 +144,9 @@ SIGNATURES = {
     "sj_down_bwd_swiglu": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _P, _L, _I, _P, _L]),
     "sj_gemm_planes_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_gemm_planes": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
-    "sj_attention_fwd_tt": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _L]),
+    "sj_attention_fwd_tt": (_I, [_P, _P, _L, _L, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _L]),
     "sj_attention_bwd_tt_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
-    "sj_attention_bwd_tt": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _L, _P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P,
+    "sj_attention_bwd_tt": (_I, [_P, _P, _L, _L, _P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P,
                                  _P, _P, _L, _P, _P, _L, _P, _S]),
     "sj_gemm_planes_split_out": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _P, _L, _P, _P, _L]),
     "sj_qkv_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _P, _L, _L, _P, _L]),

@@ -1,14 +1,13 @@
 // GQA causal attention for the MFMA-layout step (bf16 storage, head_dim 64,
 // T a multiple of 64), forward and backward, fed by producers that already
 // wrote every operand in the orientation the MFMA wants:
-//   q|k|v [M][NQKV] and its transpose qkv_t [NQKV][ldt] (the QKV projection
-//   writes both, RoPE applied), dO as hi/lo planes [M][NQ] and transposed
-//   [NQ][ldt] (the attention-output projection's dX writes both), LSE and
-//   Delta transposed [HQ][ldt].
-// So no kernel transposes or splits a tile: every 64 x 64 tile streams
-// global -> LDS with global_load_lds_dwordx4, three stages deep, XOR-
-// swizzled (chunk c of row r at c ^ (r & 7)), and MFMA fragments are single
-// 16-byte LDS reads.
+//   q|k|v [M][NQKV] (the QKV projection, RoPE applied), dO as hi/lo planes
+//   [M][NQ] (the attention-output projection's dX), LSE and Delta
+//   transposed [HQ][ldt].
+// Every 64 x 64 tile streams global -> LDS in row orientation with
+// global_load_lds_dwordx4, three stages deep, XOR-swizzled (chunk c of row
+// r at c ^ sw(r)); a fragment of the tile itself is one 16-byte LDS read,
+// a fragment of its transpose two ds_read_b64_tr_b16 (tr_frag).
 //
 // Layout trick: the rows of each 16-row block of S are read in a permuted
 // key (or query) order, row i of block sb = 32(sb/2) + 8(i/4) + 4(sb%2) +
@@ -31,7 +30,16 @@ namespace {
 
 constexpr int DH = 64;
 constexpr int QB = 64;
-constexpr int NST = 3;             // pipeline stages
+// DMA pipeline stages per kernel (stages issued ahead = stages - 1)
+#ifndef SJ_ATTN_FWD_STAGES
+#define SJ_ATTN_FWD_STAGES 3
+#endif
+#ifndef SJ_ATTN_DQ_STAGES
+#define SJ_ATTN_DQ_STAGES 3
+#endif
+constexpr int NS_FWD = SJ_ATTN_FWD_STAGES;
+constexpr int NS_DQ = SJ_ATTN_DQ_STAGES;
+constexpr int NST = 3;             // dK/dV stages
 constexpr int TILE = 64 * 64;      // bf16 elements per tile
 constexpr int TBYTES = TILE * 2;
 constexpr float LOG2E = 1.4426950408889634f;
@@ -49,6 +57,19 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
                : "memory", "m0");
 }
+// wait until at most n (0 <= n <= N) stages of PER loads each are in flight
+template <int PER, int N>
+__device__ __forceinline__ void wait_stages(int n) {
+  if constexpr (N > 0) {
+    if (n >= N) {
+      wait_vm<PER * N>();
+      return;
+    }
+    wait_stages<PER, N - 1>(n);
+  } else {
+    wait_vm<0>();
+  }
+}
 __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
   asm volatile("s_barrier" ::: "memory");
@@ -58,12 +79,41 @@ __device__ __forceinline__ bf16x8 as_bf8(u32x4 v) { return __builtin_bit_cast(bf
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+// 16-byte slot of chunk c in row r is c ^ sw(r): the row's low bits spread
+// a column over the slots, and the 8-row block's index moves the rows that
+// a transpose read takes from four consecutive blocks to different banks
+__device__ __forceinline__ int sw(int row) { return (row & 7) ^ (((row >> 3) & 3) << 1); }
 // chunk `ch` (8 bf16) of row `row` of a swizzled tile
 __device__ __forceinline__ bf16x8 tf(const bf16_t* tile, int row, int ch) {
-  return as_bf8(*(const u32x4*)(tile + row * 64 + ((ch ^ (row & 7)) << 3)));
+  return as_bf8(*(const u32x4*)(tile + row * 64 + ((ch ^ sw(row)) << 3)));
 }
 // permuted row of block sb read by A-operand lane j (see the file comment)
 __device__ __forceinline__ int prow(int sb, int j) { return 32 * (sb >> 1) + 8 * (j >> 2) + 4 * (sb & 1) + (j & 3); }
+
+// Transposed MFMA fragment from a swizzled row tile with ds_read_b64_tr_b16:
+// lane (j, g) receives tile[row0 + 8g + 0..7][col0 + j] (eight consecutive
+// rows of one column: the operand of the transposed tile).  Within a group
+// of 16 lanes the instruction hands lane i element (i & 3) of the 8 bytes
+// that source lane 4e + (i >> 2) read, as its e-th value; so source lane
+// 4e + m of the group reads row row0 + 8g + 4h + e at columns col0 + 4m ..
+// +3 (read h = 0, 1 gives rows +0..3 and +4..7).  row0 % 8 == 0, col0 % 16
+// == 0.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ bf16x8 tr_frag(const bf16_t* tile, int row0, int col0, int lane) {
+  const int g = lane >> 4, e = (lane >> 2) & 3, m = lane & 3;
+  const int col = col0 + 4 * m;
+  s16x4 v[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int row = row0 + 8 * g + 4 * h + e;
+    const bf16_t* src = tile + row * 64 + (((col >> 3) ^ sw(row)) << 3) + (col & 7);
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(src));
+  }
+  const s16x8 w = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, w);
+}
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -88,8 +138,7 @@ __device__ __forceinline__ float bfhi(uint32_t w) { return __uint_as_float(w & 0
 struct TArgs {
   const bf16_t* qkv;  // [M][ldqkv]: q (HQ*64) | k (HK*64) | v (HK*64), q and k after RoPE
   long ldqkv;
-  const bf16_t* qkvt;  // [NQKV][ldt]
-  long ldt;
+  long ldt;  // row stride of the transposed [.][rows] buffers
   int T, HQ, HK;
   int window;  // keys visible to a query: the `window` last positions up to it (0: every earlier one)
   // forward
@@ -103,8 +152,6 @@ struct TArgs {
   const bf16_t* ob;  // O (for Delta)
   const bf16_t *dh, *dl;  // dO planes [M][lddo]
   long lddo;
-  const bf16_t *dth, *dtl;  // dO^T planes [HQ*64][lddot]
-  long lddot;
   const float* lse_in_t;  // [HQ][ldt]
   float* delta_t;         // [HQ][ldt]
   const float* rope;      // inverse-RoPE table (cos, sin) [T][32] or null
@@ -119,19 +166,21 @@ struct TArgs {
 template <typename Valid>
 __device__ __forceinline__ void dma_tile(const bf16_t* src, long ld, uint32_t lds_tile, int wave, int lane,
                                          Valid valid) {
-  const int rl = lane >> 3, ch = (lane & 7) ^ (lane >> 3);
+  const int rl = lane >> 3;
 #pragma unroll
   for (int k = 0; k < 2; k++) {
     const int r0 = wave * 16 + 8 * k;
     const int r = r0 + rl;
+    const int ch = (lane & 7) ^ sw(r);  // LDS slot lane & 7 of row r holds source chunk ch
     const void* s = valid(r) ? (const void*)(src + r * ld + ch * 8) : (const void*)g_zero_t;
     dma16(s, lds_tile + (uint32_t)(r0 * 128));
   }
 }
 
 // ------------------------------------------------------------------ forward
+template <int NS>
 __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [K | V^T]
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
@@ -148,12 +197,12 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
   for (int c = 0; c < 2; c++) qf[c] = as_bf8(*(const u32x4*)(a.qkv + (row0 + myq) * a.ldqkv + h * DH + 32 * c + 8 * g));
 
   const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
-  const bf16_t* vtsrc = a.qkvt + (long)(NQ + NK + kvh * DH) * a.ldt + row0;
+  const bf16_t* vsrc = ksrc + NK;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   auto issue = [&](int kb, int buf) {
     const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
     dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
-    dma_tile(vtsrc + kb * QB, a.ldt, st + TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
   };
   f32x4 o[4];
 #pragma unroll
@@ -165,15 +214,15 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
   wait_vm<0>();  // the fragments above are in registers before the DMA stream starts
 
 #pragma unroll
-  for (int s = 0; s < NST - 1; s++)
+  for (int s = 0; s < NS - 1; s++)
     if (kb0 + s <= qb) issue(kb0 + s, s);
   for (int kb = kb0; kb <= qb; kb++) {
     const int it = kb - kb0;
-    if (kb < qb) wait_vm<4>(); else wait_vm<0>();
+    wait_stages<4, NS - 2>(min(NS - 2, qb - kb));
     block_barrier();
-    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (it + NST - 1) % NST);
-    const bf16_t* sK = lds + (it % NST) * 2 * TILE;
-    const bf16_t* sVt = sK + TILE;
+    if (kb + NS - 1 <= qb) issue(kb + NS - 1, (it + NS - 1) % NS);
+    const bf16_t* sK = lds + (it % NS) * 2 * TILE;
+    const bf16_t* sV = sK + TILE;
     f32x4 st[4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++) {
@@ -229,7 +278,7 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
       split8p(p8, ph, pl);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        const bf16x8 vf = tf(sVt, 16 * d + j, 4 * c + g);
+        const bf16x8 vf = tr_frag(sV, 32 * c, 16 * d, lane);  // V^T rows 16d.., keys 32c + 8g ..
         o[d] = mfma(vf, ph, o[d]);
         o[d] = mfma(vf, pl, o[d]);
       }
@@ -258,8 +307,9 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
 }
 
 // ------------------------------------------------------------- backward dQ
+template <int NS>
 __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [K | V | K^T]
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
@@ -297,13 +347,11 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
 
   const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
   const bf16_t* vsrc = ksrc + a.HK * DH;
-  const bf16_t* ktsrc = a.qkvt + (long)(NQ + kvh * DH) * a.ldt + row0;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   auto issue = [&](int kb, int buf) {
-    const uint32_t st = base + (uint32_t)(buf * 3 * TBYTES);
+    const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
     dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
     dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
-    dma_tile(ktsrc + kb * QB, a.ldt, st + 2 * TBYTES, wave_s, lane, [](int) { return true; });
   };
   f32x4 dq[4];
 #pragma unroll
@@ -313,16 +361,15 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
   const bool low_edge_possible = W > 0;
   wait_vm<0>();
 #pragma unroll
-  for (int s = 0; s < NST - 1; s++)
+  for (int s = 0; s < NS - 1; s++)
     if (kb0 + s <= qb) issue(kb0 + s, s);
   for (int kb = kb0; kb <= qb; kb++) {
     const int it = kb - kb0;
-    if (kb < qb) wait_vm<6>(); else wait_vm<0>();
+    wait_stages<4, NS - 2>(min(NS - 2, qb - kb));
     block_barrier();
-    if (kb + NST - 1 <= qb) issue(kb + NST - 1, (it + NST - 1) % NST);
-    const bf16_t* sK = lds + (it % NST) * 3 * TILE;
+    if (kb + NS - 1 <= qb) issue(kb + NS - 1, (it + NS - 1) % NS);
+    const bf16_t* sK = lds + (it % NS) * 2 * TILE;
     const bf16_t* sV = sK + TILE;
-    const bf16_t* sKt = sK + 2 * TILE;
     float ds[4][4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++) {
@@ -352,7 +399,7 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
       split8p(s8, sh, sl);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        const bf16x8 kt = tf(sKt, 16 * d + j, 4 * c + g);
+        const bf16x8 kt = tr_frag(sK, 32 * c, 16 * d, lane);  // K^T rows 16d.., keys 32c + 8g ..
         dq[d] = mfma(kt, sh, dq[d]);
         dq[d] = mfma(kt, sl, dq[d]);
       }
@@ -391,10 +438,13 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
 
 // ------------------------------------------------------------ backward dKV
 // Workgroup (key block, query head, batch): this head's dK | dV share, fp32,
-// into part[gi][row][dK | dV] (gi = head index inside its group).
+// into part[gi][row][dK | dV] (gi = head index inside its group).  A stage
+// holds the query block's Q and dO planes in row orientation only: the
+// products that need them transposed (dV^T = dO^T P, dK^T = Q^T dS) read
+// their fragments with LDS transpose reads.
 __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [Q | dOh | dOl | Q^T | dO^T h | dO^T l | LSE,Delta]
-  constexpr int SROW = 6 * TILE + 512;  // stage size in bf16 elements (+1 KB of LSE / Delta)
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [Q | dOh | dOl | LSE,Delta]
+  constexpr int SROW = 3 * TILE + 512;  // stage size in bf16 elements (+1 KB of LSE / Delta)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
@@ -416,9 +466,6 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
   const bf16_t* qsrc = a.qkv + row0 * a.ldqkv + h * DH;
   const bf16_t* dhsrc = a.dh + row0 * a.lddo + h * DH;
   const bf16_t* dlsrc = a.dl + row0 * a.lddo + h * DH;
-  const bf16_t* qtsrc = a.qkvt + (long)h * DH * a.ldt + row0;
-  const bf16_t* dthsrc = a.dth + (long)h * DH * a.lddot + row0;
-  const bf16_t* dtlsrc = a.dtl + (long)h * DH * a.lddot + row0;
   const float* lsesrc = a.lse_in_t + (long)h * a.ldt + row0;
   const float* dlsrc2 = a.delta_t + (long)h * a.ldt + row0;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
@@ -428,13 +475,10 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
     dma_tile(qsrc + q0 * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
     dma_tile(dhsrc + q0 * a.lddo, a.lddo, st + TBYTES, wave_s, lane, [](int) { return true; });
     dma_tile(dlsrc + q0 * a.lddo, a.lddo, st + 2 * TBYTES, wave_s, lane, [](int) { return true; });
-    dma_tile(qtsrc + q0, a.ldt, st + 3 * TBYTES, wave_s, lane, [](int) { return true; });
-    dma_tile(dthsrc + q0, a.lddot, st + 4 * TBYTES, wave_s, lane, [](int) { return true; });
-    dma_tile(dtlsrc + q0, a.lddot, st + 5 * TBYTES, wave_s, lane, [](int) { return true; });
     if (wave_s == 0) {  // LSE (lanes 0-15) and Delta (16-31) of the block's 64 queries
       const void* s = lane < 16 ? (const void*)(lsesrc + q0 + 4 * lane)
                                 : lane < 32 ? (const void*)(dlsrc2 + q0 + 4 * (lane - 16)) : (const void*)g_zero_t;
-      dma16(s, st + 6 * TBYTES);
+      dma16(s, st + 3 * TBYTES);
     }
   };
   f32x4 dk[4], dv[4];
@@ -451,7 +495,7 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
   for (int qb = kb; qb < nqb; qb++) {
     const int it = qb - kb;
     if (qb + 1 < nqb) {
-      if (wave_s == 0) wait_vm<13>(); else wait_vm<12>();
+      if (wave_s == 0) wait_vm<7>(); else wait_vm<6>();
     } else {
       wait_vm<0>();
     }
@@ -460,10 +504,7 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
     const bf16_t* sQ = lds + (it % NST) * SROW;
     const bf16_t* sDh = sQ + TILE;
     const bf16_t* sDl = sQ + 2 * TILE;
-    const bf16_t* sQt = sQ + 3 * TILE;
-    const bf16_t* sDth = sQ + 4 * TILE;
-    const bf16_t* sDtl = sQ + 5 * TILE;
-    const float* sL = (const float*)(sQ + 6 * TILE);
+    const float* sL = (const float*)(sQ + 3 * TILE);
     const float* sD = sL + 64;
     float pp[4][4], ds[4][4];
 #pragma unroll
@@ -500,8 +541,8 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
       split8p(s8, sh, sl);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        const int rr = 16 * d + j, ch = 4 * c + g;
-        const bf16x8 doh = tf(sDth, rr, ch), dol = tf(sDtl, rr, ch), qt = tf(sQt, rr, ch);
+        const bf16x8 doh = tr_frag(sDh, 32 * c, 16 * d, lane), dol = tr_frag(sDl, 32 * c, 16 * d, lane);
+        const bf16x8 qt = tr_frag(sQ, 32 * c, 16 * d, lane);
         dv[d] = mfma(doh, ph, dv[d]);
         dv[d] = mfma(dol, ph, dv[d]);
         dv[d] = mfma(doh, pl, dv[d]);
@@ -520,9 +561,11 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
   }
 }
 
-constexpr size_t LDS_FWD = (size_t)NST * 2 * TBYTES;
-constexpr size_t LDS_DQ = (size_t)NST * 3 * TBYTES;
-constexpr size_t LDS_DKV = (size_t)NST * (6 * TBYTES + 1024);
+constexpr size_t LDS_FWD = (size_t)NS_FWD * 2 * TBYTES;
+constexpr size_t LDS_DQ = (size_t)NS_DQ * 2 * TBYTES;
+static_assert(NS_FWD >= 2 && NS_DQ >= 2 && LDS_FWD <= 160 * 1024 && LDS_DQ <= 160 * 1024, "LDS budget");
+static_assert((NS_FWD - 2) * 4 < 64 && (NS_DQ - 2) * 4 < 64, "vmcnt range");
+constexpr size_t LDS_DKV = (size_t)NST * (3 * TBYTES + 1024);
 static_assert(LDS_DKV <= 160 * 1024, "LDS budget");
 
 }  // namespace
@@ -531,38 +574,36 @@ int sjh::attention_t_prepare() {
   static int done = 0, status = SJ_OK;
   if (done) return status;
   done = 1;
-  hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
+  hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd<NS_FWD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
   if (e == hipSuccess)
-    e = hipFuncSetAttribute((const void*)k_attn2_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
+    e = hipFuncSetAttribute((const void*)k_attn2_dq<NS_DQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
   return status;
 }
 
-static int check_t(const void* qkv, long ldqkv, const void* qkvt, long ldt, long batch, long t, long hq, long hk,
-                   long head_dim, long window) {
-  SJ_REQUIRE(qkv && qkvt && batch > 0 && t > 0 && t % QB == 0 && hq > 0 && hk > 0 && hq % hk == 0 && window >= 0 &&
+static int check_t(const void* qkv, long ldqkv, long ldt, long batch, long t, long hq, long hk, long head_dim,
+                   long window) {
+  SJ_REQUIRE(qkv && batch > 0 && t > 0 && t % QB == 0 && hq > 0 && hk > 0 && hq % hk == 0 && window >= 0 &&
                  head_dim == DH && ldqkv >= (hq + 2 * hk) * DH && ldqkv % 8 == 0 && ldt >= batch * t &&
-                 ldt % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)qkvt & 15) == 0 &&
-                 t * ldqkv < (1L << 31),
-             "grouped attention (transposed operands): bf16, head_dim 64, t %% 64 == 0, aligned q|k|v and "
-             "q|k|v^T [.][ldt >= batch*t]");
+                 ldt % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && t * ldqkv < (1L << 31),
+             "grouped attention (MFMA layout): bf16, head_dim 64, t %% 64 == 0, aligned q|k|v, ldt >= batch*t");
   return SJ_OK;
 }
 
-extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
-                                   long batch, long t, long hq, long hk, long head_dim, long window, uint16_t* o,
-                                   long ldo, float* lse, float* lse_t, uint16_t* o_t, long ldot) {
-  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim, window)) return st;
+extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv, long ldt, long batch, long t,
+                                   long hq, long hk, long head_dim, long window, uint16_t* o, long ldo, float* lse,
+                                   float* lse_t, uint16_t* o_t, long ldot) {
+  if (int st = check_t(qkv, ldqkv, ldt, batch, t, hq, hk, head_dim, window)) return st;
   SJ_REQUIRE(o && lse_t && ldo >= hq * DH && ldo % 8 == 0 && ((uintptr_t)o & 15) == 0 && (!o_t || ldot >= batch * t),
              "grouped attention: outputs");
   if (int st = sjh::attention_t_prepare()) return st;
   TArgs a = {};
-  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
+  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.ldt = ldt;
   a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk; a.window = window < t ? (int)window : 0;
   a.o = (bf16_t*)o; a.ldo = ldo; a.lse = lse; a.lse_t = lse_t; a.ot = (bf16_t*)o_t; a.ldot = ldot;
-  hipLaunchKernelGGL(k_attn2_fwd, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
+  hipLaunchKernelGGL(k_attn2_fwd<NS_FWD>, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
                      (hipStream_t)stream, a);
   SJ_LAUNCH_CHECK("hierarchy_attention");
   return SJ_OK;
@@ -572,19 +613,16 @@ extern "C" size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long h
   return sizeof(float) * (size_t)(hq / (hk > 0 ? hk : 1)) * (size_t)(batch * t) * (size_t)(2 * hk * head_dim);
 }
 
-int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t,
-                                long ldt, const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
-                                const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
-                                long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                                long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                                uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace,
-                                size_t workspace_bytes) {
-  if (int st = check_t(qkv, ldqkv, qkv_t, ldt, batch, t, hq, hk, head_dim, window)) return st;
-  SJ_REQUIRE(o && lse_t && do_hi && do_lo && do_t_hi && do_t_lo && delta_t && g_hi && g_lo && g_t_hi && g_t_lo &&
-                 lddo >= hq * DH && lddo % 8 == 0 && lddot >= batch * t && lddot % 8 == 0 && ldo % 8 == 0 &&
-                 ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t && ((uintptr_t)do_hi & 15) == 0 &&
-                 ((uintptr_t)do_lo & 15) == 0 && ((uintptr_t)do_t_hi & 15) == 0 && ((uintptr_t)do_t_lo & 15) == 0 &&
-                 ((uintptr_t)o & 15) == 0 && ldg % 4 == 0,
+int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, long ldt, const uint16_t* o,
+                                long ldo, const float* lse_t, const uint16_t* do_hi, const uint16_t* do_lo, long lddo,
+                                float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
+                                const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                                uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+  if (int st = check_t(qkv, ldqkv, ldt, batch, t, hq, hk, head_dim, window)) return st;
+  SJ_REQUIRE(o && lse_t && do_hi && do_lo && delta_t && g_hi && g_lo && g_t_hi && g_t_lo && lddo >= hq * DH &&
+                 lddo % 8 == 0 && ldo % 8 == 0 && ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t &&
+                 ((uintptr_t)do_hi & 15) == 0 && ((uintptr_t)do_lo & 15) == 0 && ((uintptr_t)o & 15) == 0 &&
+                 ldg % 4 == 0,
              "grouped attention backward (transposed operands): buffers");
   const size_t need = sj_attention_bwd_tt_workspace_bytes(batch, t, hq, hk, head_dim);
   if (!workspace || workspace_bytes < need)
@@ -593,18 +631,17 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   if (int st = sjh::attention_t_prepare()) return st;
   hipStream_t s = (hipStream_t)stream;
   TArgs a = {};
-  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.qkvt = (const bf16_t*)qkv_t; a.ldt = ldt;
+  a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.ldt = ldt;
   a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk; a.window = window < t ? (int)window : 0;
   a.ob = (const bf16_t*)o; a.ldo = ldo;
   a.dh = (const bf16_t*)do_hi; a.dl = (const bf16_t*)do_lo; a.lddo = lddo;
-  a.dth = (const bf16_t*)do_t_hi; a.dtl = (const bf16_t*)do_t_lo; a.lddot = lddot;
   a.lse_in_t = lse_t; a.delta_t = delta_t; a.rope = rope_table;
   a.gq[0] = (bf16_t*)g_hi; a.gq[1] = (bf16_t*)g_lo; a.gqt[0] = (bf16_t*)g_t_hi; a.gqt[1] = (bf16_t*)g_t_lo;
   a.ldg = ldg; a.ldgt = ldgt;
   a.part = (float*)workspace;
   const dim3 grid((unsigned)(t / QB), (unsigned)hq, (unsigned)batch);
   if (parts & 1) {
-    hipLaunchKernelGGL(k_attn2_dq, grid, dim3(256), LDS_DQ, s, a);
+    hipLaunchKernelGGL(k_attn2_dq<NS_DQ>, grid, dim3(256), LDS_DQ, s, a);
     SJ_LAUNCH_CHECK("hierarchy_attention_dq");
   }
   if (parts & 2) {
@@ -620,14 +657,12 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   return SJ_OK;
 }
 
-extern "C" int sj_attention_bwd_tt(void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
-                                   const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
-                                   const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
-                                   long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                                   long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                                   uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace,
-                                   size_t workspace_bytes) {
-  return sjh::attention_bwd_tt_parts(7, stream, qkv, ldqkv, qkv_t, ldt, o, ldo, lse_t, do_hi, do_lo, lddo, do_t_hi,
-                                     do_t_lo, lddot, delta_t, batch, t, hq, hk, head_dim, window, rope_table, g_hi,
-                                     g_lo, ldg, g_t_hi, g_t_lo, ldgt, workspace, workspace_bytes);
+extern "C" int sj_attention_bwd_tt(void* stream, const uint16_t* qkv, long ldqkv, long ldt, const uint16_t* o, long ldo,
+                                   const float* lse_t, const uint16_t* do_hi, const uint16_t* do_lo, long lddo,
+                                   float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
+                                   const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                                   uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+  return sjh::attention_bwd_tt_parts(7, stream, qkv, ldqkv, ldt, o, ldo, lse_t, do_hi, do_lo, lddo, delta_t, batch, t,
+                                     hq, hk, head_dim, window, rope_table, g_hi, g_lo, ldg, g_t_hi, g_t_lo, ldgt,
+                                     workspace, workspace_bytes);
 }

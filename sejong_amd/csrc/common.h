@@ -121,12 +121,11 @@ int attention_t_prepare();
 int attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
                         const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi, uint16_t* gt_lo,
                         long ldgt);
-int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, const uint16_t* qkv_t, long ldt,
-                           const uint16_t* o, long ldo, const float* lse_t, const uint16_t* do_hi,
-                           const uint16_t* do_lo, long lddo, const uint16_t* do_t_hi, const uint16_t* do_t_lo,
-                           long lddot, float* delta_t, long batch, long t, long hq, long hk, long head_dim,
-                           long window, const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg,
-                           uint16_t* g_t_hi, uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
+int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, long ldt, const uint16_t* o,
+                           long ldo, const float* lse_t, const uint16_t* do_hi, const uint16_t* do_lo, long lddo,
+                           float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
+                           const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
+                           uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);

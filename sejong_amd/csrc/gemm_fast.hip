@@ -466,7 +466,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       rows_bf16(T + t2 * TP, [&](long m, long n, const u32x4& val, const bf16_t* src) {
         put8(base + m * p.ldc[0] + n, n, val, src);
       });
-      cols_bf16(T + t2 * TP, (bf16_t*)p.c[2 + t2], p.ldc[2]);
+      if (p.c[2 + t2]) cols_bf16(T + t2 * TP, (bf16_t*)p.c[2 + t2], p.ldc[2]);
     }
   } else if constexpr (EPI == E_GATEUP) {
 #pragma unroll
@@ -907,11 +907,11 @@ extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, co
                                          uint16_t* c_lo, long ldc, uint16_t* c_t_hi, uint16_t* c_t_lo, long ldct) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
   SJ_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
-                 ldc >= N && ldct >= M && ldct % 8 == 0,
+                 ldc >= N && (!c_t_hi || (ldct >= M && ldct % 8 == 0)),
              "matmul planes out: M %ld N %ld K %ld (K, ld multiples of 8)", M, N, K);
-  SJ_REQUIRE(a_hi && a_lo && b && c_hi && c_lo && c_t_hi && c_t_lo && ok16(a_hi) && ok16(a_lo) && ok16(b) &&
-                 ok16(c_t_hi) && ok16(c_t_lo),
-             "matmul planes out: 16-byte aligned operands required");
+  SJ_REQUIRE(a_hi && a_lo && b && c_hi && c_lo && !c_t_hi == !c_t_lo && ok16(a_hi) && ok16(a_lo) && ok16(b) &&
+                 (!c_t_hi || (ok16(c_t_hi) && ok16(c_t_lo))),
+             "matmul planes out: 16-byte aligned operands required (transposed outputs both or neither)");
   FParams p = {};
   p.a[0] = (const bf16_t*)a_hi; p.a[1] = (const bf16_t*)a_lo; p.lda = lda;
   p.b[0][0] = (const bf16_t*)b; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;

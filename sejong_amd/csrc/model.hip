@@ -203,9 +203,8 @@ struct sj_model {
   // attention over producer-transposed operands (T a multiple of 64): q|k|v^T
   // and LSE^T per layer, dO planes in both orientations and Delta^T scratch
   bool attn_tt = false;
-  std::vector<uint16_t*> qkvt;
   std::vector<float*> lset;
-  uint16_t* dop[4] = {};  // dO hi, lo [M][d]; hi^T, lo^T [d][ldt]
+  uint16_t* dop[2] = {};  // dO hi, lo [M][d]
   float* deltat = nullptr;
   uint16_t *rp[4] = {}, *xp[4] = {}, *qp[4] = {}, *gp[4] = {};  // gradient planes: hi, lo, hi^T, lo^T
   // The dW products (and the parameter-VJP groups) run on a second stream
@@ -503,11 +502,10 @@ int stage_forward(sj_model* m, int si) {
     uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
     uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
     OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], ldt, M, d, eps));
-    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, S.rope, S.T, S.Dh,
-                                S.attn_tt ? m->qkvt[l] : nullptr, ldt));
+    OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, S.rope, S.T, S.Dh, nullptr, ldt));
     if (S.attn_tt)
-      OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, m->qkvt[l], ldt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, o,
-                                              d, m->lse[l], m->lset[l], m->ot[l], ldt));
+      OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, ldt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, o, d,
+                                              m->lse[l], m->lset[l], m->ot[l], ldt));
     else
       OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l],
                                              ldt, m->B, S.T, S.HQ, S.HK, S.Dh));
@@ -754,9 +752,9 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                                     m->slot_ptr[m->slot_fn[l]]));
       TRY(written(KX, p));
       // x1 = x + attention_output(o)
-      if (S.attn_tt)  // dO as hi/lo planes in both orientations: the attention backward's operands
+      if (S.attn_tt)  // dO as hi/lo planes: the attention backward's operands
         OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, xp[0], xp[1], d, W + y.wo, d, m->dop[0], m->dop[1], d,
-                                                   m->dop[2], m->dop[3], ldt));
+                                                   nullptr, nullptr, 0));
       else
         OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
                                          wsb));
@@ -767,10 +765,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       for (int part = 1; part <= 4; part <<= 1) {
         const char* nm = part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce";
         if (S.attn_tt)
-          OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, m->qkvt[l], ldt, (const uint16_t*)m->o[l], d,
-                                             m->lset[l], m->dop[0], m->dop[1], d, m->dop[2], m->dop[3], ldt,
-                                             m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, S.rope, qp[0], qp[1],
-                                             NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
+          OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, ldt, (const uint16_t*)m->o[l], d, m->lset[l],
+                                             m->dop[0], m->dop[1], d, m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh,
+                                             S.window, S.rope, qp[0], qp[1], NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws,
+                                             wsb));
         else
           OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
                                             m->lse[l], m->dO, d, m->delta, m->B, S.T, S.HQ, S.HK, S.Dh, S.rope,
@@ -1398,15 +1396,13 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     bool any_tt = false;
     for (const Stage& S : m->stages) any_tt = any_tt || S.attn_tt;
     if (any_tt) {
-      m->qkvt.assign(m->L, nullptr);
       m->lset.assign(m->L, nullptr);
       for (long l = 0; l < m->L; l++) {
         const Stage& S = m->stages[m->layers[l].stage];
         if (!S.attn_tt) continue;
-        ALLOC(m->qkvt[l], (size_t)S.NQKV * (size_t)S.ldt * 2);
         ALLOC(m->lset[l], (size_t)S.HQ * (size_t)S.ldt * 4);
       }
-      for (int i = 0; i < 4; i++) ALLOC(m->dop[i], (i < 2 ? mxMd : mxLd) * 2);
+      for (int i = 0; i < 2; i++) ALLOC(m->dop[i], mxMd * 2);
       ALLOC(m->deltat, mxLHQ * 4);
     }
     for (int i = 0; i < 4; i++) {

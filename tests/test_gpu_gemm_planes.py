@@ -253,8 +253,9 @@ def test_attention_t_and_planes(api, lib, B, T, HQ, HK):
 @pytest.mark.parametrize("B,T,HQ,HK,W", [(2, 256, 6, 2, 0), (1, 512, 4, 4, 0), (2, 128, 8, 1, 0), (2, 256, 4, 2, 128),
                                          (1, 320, 4, 1, 100), (2, 192, 4, 4, 32)])
 def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
-    """The step's attention over producer-transposed operands (qkv^T, dO
-    planes in both orientations) against the fp32 row kernels and the FP64
+    """The step's MFMA-layout attention (q|k|v and dO planes in row
+    orientation, transposed fragments by LDS transpose reads) against the
+    fp32 row kernels and the FP64
     oracle on the same stored inputs; W > 0 is the local stages' sliding
     window (hierarchy.py:24,60,87), including windows that are not a
     multiple of the 64-key block and one shorter than a block."""
@@ -265,13 +266,12 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     ldt = M + 8
     qkv = rnd((M, NG), "bf16", rng)
     QKV = dev(np.concatenate([qkv, np.zeros((M, ldq - NG))], 1), "bf16")
-    QKVT = dev(np.concatenate([qkv.T, np.zeros((NG, ldt - M))], 1), "bf16")
     q, k, v = qkv[:, :N], qkv[:, N:N + KV], qkv[:, N + KV:]
     print(f"[attention_tt] B={B} T={T} HQ={HQ} HK={HK} W={W}", flush=True)
     O1, L1 = empty(M * N, "bf16"), empty(M * HQ)
     api.sj_attention_fwd(None, QKV.p, ldq, QKV.at(N), ldq, QKV.at(N + KV), ldq, O1.p, N, L1.p, BF, B, T, HQ, HK, Dh, W)
     O2, L2, LT, OT = empty(M * N, "bf16"), empty(M * HQ), zeros(HQ * ldt), zeros(N * ldt, "bf16")
-    api.sj_attention_fwd_tt(None, QKV.p, ldq, QKVT.p, ldt, B, T, HQ, HK, Dh, W, O2.p, N, L2.p, LT.p, OT.p, ldt)
+    api.sj_attention_fwd_tt(None, QKV.p, ldq, ldt, B, T, HQ, HK, Dh, W, O2.p, N, L2.p, LT.p, OT.p, ldt)
     sync()
     o1, o2 = O1.host().reshape(M, N), O2.host().reshape(M, N)
     # one storage ulp, plus the accumulation error of a result that cancels
@@ -288,12 +288,10 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     assert rel(L2.host(), L1.host()) < 1e-6
     np.testing.assert_array_equal(LT.host().reshape(HQ, ldt)[:, :M], L2.host().reshape(M, HQ).T)
     np.testing.assert_array_equal(OT.host().reshape(N, ldt)[:, :M], o2.T)
-    # backward from dO planes (both orientations), against the fp32 row path on the same O and LSE
+    # backward from dO planes, against the fp32 row path on the same O and LSE
     do = rng.normal(0, 1e-4, (M, N)).astype(np.float32).astype(np.float64)
     dh = O.round_to(do, "bf16"); dl = O.round_to(do - dh, "bf16")
     DH_, DL_ = dev(dh, "bf16"), dev(dl, "bf16")
-    DTH = dev(np.concatenate([dh.T, np.zeros((N, ldt - M))], 1), "bf16")
-    DTL = dev(np.concatenate([dl.T, np.zeros((N, ldt - M))], 1), "bf16")
     tab = empty(T * Dh)
     api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
     dof = dh + dl                                                  # the dO the planes carry
@@ -304,7 +302,7 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     Gh, Gl, Th, Tl = empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldt, "bf16"), zeros(NG * ldt, "bf16")
     DT = zeros(HQ * ldt)
     ws = empty(max(lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
-    api.sj_attention_bwd_tt(None, QKV.p, ldq, QKVT.p, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DTH.p, DTL.p, ldt, DT.p,
+    api.sj_attention_bwd_tt(None, QKV.p, ldq, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DT.p,
                             B, T, HQ, HK, Dh, W, tab.p, Gh.p, Gl.p, NG, Th.p, Tl.p, ldt, ws.p, ws.nbytes)
     sync()
     assert rel(DT.host().reshape(HQ, ldt)[:, :M], De.host().reshape(M, HQ).T) < 1e-5
@@ -343,4 +341,11 @@ def test_gemm_planes_split_out(api):
     np.testing.assert_array_equal(C2h.host(), Ch.host())
     np.testing.assert_array_equal(C2l.host(), Cl.host())
     np.testing.assert_array_equal(Th.host().reshape(N, ldt)[:, :M], hi.T)
+    # transposed outputs are optional: the normal planes are the same bits
+    C3h, C3l = empty(M * N, "bf16"), empty(M * N, "bf16")
+    api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, C3h.p,
+                                 C3l.p, N, None, None, 0)
+    sync()
+    np.testing.assert_array_equal(C3h.host(), Ch.host())
+    np.testing.assert_array_equal(C3l.host(), Cl.host())
     np.testing.assert_array_equal(Tl.host().reshape(N, ldt)[:, :M], lo.T)
