@@ -205,6 +205,15 @@ size_t sj_gemm_planes_workspace_bytes(long M, long N, long K);
 int sj_gemm_planes(void *stream, long M, long N, long K, const uint16_t *a_hi, const uint16_t *a_lo,
                    long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, void *c, int c_dtype,
                    long ldc, int accumulate, void *workspace, size_t workspace_bytes);
+/* dW = X^T dY of a projection (graph.rs:829-851) from row-layout operands:
+ * c [M][ldc] (+)= x^T y with x [K][ldx] (M columns, e.g. the layer input
+ * [tokens][d]) and y [K][ldy] (N columns, e.g. dY as hi/lo planes
+ * [tokens][n]); the tiles are staged in that orientation and the MFMA reads
+ * their transposed fragments from LDS.  M, N, ldx, ldy multiples of 8;
+ * workspace sj_gemm_planes_workspace_bytes(M, N, K). */
+int sj_gemm_planes_tn(void *stream, long M, long N, long K, const uint16_t *x_hi, const uint16_t *x_lo, long ldx,
+                      const uint16_t *y_hi, const uint16_t *y_lo, long ldy, void *c, int c_dtype, long ldc,
+                      int accumulate, void *workspace, size_t workspace_bytes);
 /* dX = dY W^T of a projection (graph.rs:829-851) with dY as hi/lo planes
  * [M][K] and W^T [N][K] bf16, its fp32 result written as hi/lo planes
  * c [M][ldc] (the dO operands of the attention backward) and, when c_t_hi

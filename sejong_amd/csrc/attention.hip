@@ -869,6 +869,7 @@ __global__ __launch_bounds__(256) void k_attn_kv_reduce(const float* __restrict_
         h0[i >> 1] = hx; h1[i >> 1] = hy; l0[i >> 1] = lx; l1[i >> 1] = ly;
       }
     }
+    if (!th) continue;  // transposed planes are optional
     if (row0 + KVR_ROWS <= M) {
       *(u32x4*)(th + gcol * ldgt + row0) = u32x4{h0[0], h0[1], h0[2], h0[3]};
       *(u32x4*)(th + (gcol + 1) * ldgt + row0) = u32x4{h1[0], h1[1], h1[2], h1[3]};

@@ -428,10 +428,12 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
     *(u32x2*)(a.gq[1] + qrow * a.ldg + col) = u32x2{l01, l23};
     const uint32_t hs[4] = {h01 & 0xffffu, h01 >> 16, h23 & 0xffffu, h23 >> 16};
     const uint32_t ls[4] = {l01 & 0xffffu, l01 >> 16, l23 & 0xffffu, l23 >> 16};
+    if (a.gqt[0]) {  // transposed planes (optional)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      a.gqt[0][(col + r) * a.ldgt + qrow] = (bf16_t)hs[r];
-      a.gqt[1][(col + r) * a.ldgt + qrow] = (bf16_t)ls[r];
+      for (int r = 0; r < 4; r++) {
+        a.gqt[0][(col + r) * a.ldgt + qrow] = (bf16_t)hs[r];
+        a.gqt[1][(col + r) * a.ldgt + qrow] = (bf16_t)ls[r];
+      }
     }
   }
 }
@@ -619,8 +621,8 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
                                 const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
                                 uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
   if (int st = check_t(qkv, ldqkv, ldt, batch, t, hq, hk, head_dim, window)) return st;
-  SJ_REQUIRE(o && lse_t && do_hi && do_lo && delta_t && g_hi && g_lo && g_t_hi && g_t_lo && lddo >= hq * DH &&
-                 lddo % 8 == 0 && ldo % 8 == 0 && ldg >= (hq + 2 * hk) * DH && ldgt >= batch * t &&
+  SJ_REQUIRE(o && lse_t && do_hi && do_lo && delta_t && g_hi && g_lo && !g_t_hi == !g_t_lo && lddo >= hq * DH &&
+                 lddo % 8 == 0 && ldo % 8 == 0 && ldg >= (hq + 2 * hk) * DH && (!g_t_hi || ldgt >= batch * t) &&
                  ((uintptr_t)do_hi & 15) == 0 && ((uintptr_t)do_lo & 15) == 0 && ((uintptr_t)o & 15) == 0 &&
                  ldg % 4 == 0,
              "grouped attention backward (transposed operands): buffers");

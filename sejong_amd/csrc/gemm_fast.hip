@@ -117,6 +117,37 @@ __device__ __forceinline__ bf16x8 frag(const bf16_t* tile, int row, int chunk) {
   return __builtin_bit_cast(bf16x8, *(const u32x4*)(tile + row * BK + ((chunk ^ (row & 7)) << 3)));
 }
 
+// Row-layout operands (X [K][M]: each k-row holds the M index contiguous)
+// are staged as 64 k-rows x 64 columns sub-tiles; chunk c of k-row r sits at
+// slot c ^ swt(r).
+__device__ __forceinline__ int swt(int row) {
+  // rows 4q .. 4q+3 (one transpose read's 16-lane group) take slot pairs
+  // 0..3, and the 8-row block index XOR moves rows r and r + 8 (the groups
+  // the LDS serves together) to complementary banks
+  return (((row & 3) << 1) | ((row >> 2) & 1)) ^ (((row >> 3) & 3) << 1);
+}
+// MFMA fragment of the transposed sub-tile with ds_read_b64_tr_b16: lane
+// (j, g) receives tile[row0 + 8g + 0..7][col0 + j].  Within a group of 16
+// lanes the instruction hands lane i element (i & 3) of the 8 bytes that
+// source lane 4e + (i >> 2) read as its e-th value, so source lane 4e + m
+// reads k-row row0 + 8g + 4h + e at columns col0 + 4m .. +3 (h = 0, 1).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ bf16x8 tr_frag(const bf16_t* tile, int row0, int col0, int lane) {
+  const int g = lane >> 4, e = (lane >> 2) & 3, m = lane & 3;
+  const int col = col0 + 4 * m;
+  s16x4 v[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int row = row0 + 8 * g + 4 * h + e;
+    const bf16_t* src = tile + row * BK + (((col >> 3) ^ swt(row)) << 3) + (col & 7);
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(src));
+  }
+  const s16x8 w = __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, w);
+}
+
 __device__ __forceinline__ float sigm(float g) { return 1.f / (1.f + expf(-g)); }
 __device__ __forceinline__ float rnd(float v, int bf) { return bf ? round_bf(v) : v; }
 __device__ __forceinline__ void put(void* c, long i, float v, int bf) {
@@ -154,8 +185,14 @@ constexpr size_t lds_bytes() {
   return pipe > e ? pipe : e;
 }
 
-template <int BM, int BN, int PA, int PB, int EPI, int NS>
+// TM: operand layouts.  Bit 0: A is given as X [K][M] (lda = its k-row
+// stride), bit 1: B as Y [K][N]; C = X^T Y then (the dW form over rows of
+// activations and gradients).  Otherwise operands are [rows][K] k-contiguous.
+template <int BM, int BN, int PA, int PB, int EPI, int NS, int TM = 0>
 __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
+  constexpr bool TA = (TM & 1) != 0, TB = (TM & 2) != 0;
+  static_assert(!(TA || TB) || ((EPI == E_STORE || EPI == E_PARTIAL) && BM % 64 == 0 && BN % 64 == 0),
+                "row-layout operands: plain products with 64-multiple tiles");
   constexpr bool DUAL = EPI == E_GATEUP;
   constexpr int NBM = DUAL ? 2 : 1;
   constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 16, NB = WN / 16;
@@ -227,17 +264,27 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int sl = lane;
   const int c8 = (((sl & 7) ^ (sl >> 3)) << 3);
+  // Row-layout blocks (TM): stage rows r8 .. r8 + 7 of a plane are k-rows
+  // (r8 % 64) + 0..7 of its sub-tile (r8 % BM) / 64, i.e. columns
+  // 64 * subtile .. + 63 of X; the lane loads source chunk
+  // (sl & 7) ^ swt(k-row) of k-row (r8 % 64) + (sl >> 3).
+  // kpos[j]: the lane's largest k offset in the block (valid iff
+  // kbeg + k0 + kpos < kend); kmul[j]: source elements per k step.
   const bf16_t* src[PER_WAVE];
+  int kpos[PER_WAVE];
+  long kmul[PER_WAVE];
 #pragma unroll
   for (int j = 0; j < PER_WAVE; j++) {
     const int r8 = (wave_s + 4 * j) * 8;
     const bf16_t* base;
     long ld, row, rows;
+    bool tr;
     if (r8 < AROWS) {
       const int pl = r8 / BM;
       base = pl ? p.a[1] : p.a[0];
       ld = p.lda;
-      row = m0 + (r8 % BM) + (sl >> 3);
+      tr = TA;
+      row = tr ? m0 + ((r8 % BM) / 64) * 64 : m0 + (r8 % BM) + (sl >> 3);
       rows = p.M;
     } else {
       const int rb = r8 - AROWS;
@@ -245,19 +292,30 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       const int sg = DUAL ? q : seg;
       base = (pl ? p.b[1][sg] : p.b[0][sg]) + boff;
       ld = p.ldb[sg];
-      row = nl0 + (rb % BN) + (sl >> 3);
+      tr = TB;
+      row = tr ? nl0 + ((rb % BN) / 64) * 64 : nl0 + (rb % BN) + (sl >> 3);
       rows = nrows_b;
     }
-    src[j] = row < rows ? base + row * ld + kbeg + c8 : nullptr;
+    if (tr) {
+      const int kr = (r8 % 64) + (sl >> 3);
+      const long col = row + 8 * ((sl & 7) ^ swt(kr));
+      src[j] = col < rows ? base + (kbeg + kr) * ld + col : nullptr;
+      kpos[j] = kr;
+      kmul[j] = ld;
+    } else {
+      src[j] = row < rows ? base + row * ld + kbeg + c8 : nullptr;
+      kpos[j] = c8 + 7;
+      kmul[j] = 1;
+    }
   }
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
   auto issue = [&](int it, int buf) {
     const long k0 = (long)it * BK;  // relative to kbeg
-    const bool kin = kbeg + k0 + c8 + 8 <= kend;
     const uint32_t sbase = lds_base + (uint32_t)(buf * STAGE_ROWS * BK * 2) + (uint32_t)(wave_s * 8 * BK * 2);
 #pragma unroll
     for (int j = 0; j < PER_WAVE; j++) {
-      const void* a = (src[j] && kin) ? (const void*)(src[j] + k0) : (const void*)g_zero16;
+      const bool kin = kbeg + k0 + kpos[j] < kend;
+      const void* a = (src[j] && kin) ? (const void*)(src[j] + k0 * kmul[j]) : (const void*)g_zero16;
       dma16(a, sbase + (uint32_t)(j * 32 * BK * 2));
     }
   };
@@ -294,8 +352,15 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
 #pragma unroll
       for (int i = 0; i < MB; i++) {
         const int row = wm * WM + i * 16 + fr;
-        ah[i] = frag(st, row, ch);
-        if constexpr (PA == 2) al[i] = frag(st + BM * BK, row, ch);
+        if constexpr (TA) {
+          const int r16 = wm * WM + i * 16;
+          const bf16_t* sub = st + (r16 / 64) * 64 * BK;
+          ah[i] = tr_frag(sub, 32 * h, r16 % 64, lane);
+          if constexpr (PA == 2) al[i] = tr_frag(sub + BM * BK, 32 * h, r16 % 64, lane);
+        } else {
+          ah[i] = frag(st, row, ch);
+          if constexpr (PA == 2) al[i] = frag(st + BM * BK, row, ch);
+        }
       }
 #pragma unroll
       for (int q = 0; q < NBM; q++) {
@@ -303,9 +368,16 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
 #pragma unroll
         for (int j = 0; j < NB; j++) {
           const int row = wn * WN + j * 16 + fr;
-          bf16x8 bh = frag(bt, row, ch);
-          bf16x8 bl;
-          if constexpr (PB == 2) bl = frag(bt + BN * BK, row, ch);
+          bf16x8 bh, bl;
+          if constexpr (TB) {
+            const int r16 = wn * WN + j * 16;
+            const bf16_t* sub = bt + (r16 / 64) * 64 * BK;
+            bh = tr_frag(sub, 32 * h, r16 % 64, lane);
+            if constexpr (PB == 2) bl = tr_frag(sub + BN * BK, 32 * h, r16 % 64, lane);
+          } else {
+            bh = frag(bt, row, ch);
+            if constexpr (PB == 2) bl = frag(bt + BN * BK, row, ch);
+          }
 #pragma unroll
           for (int i = 0; i < MB; i++) {
             acc[q][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh, acc[q][i][j], 0, 0, 0);
@@ -457,7 +529,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
         put8(base + m * p.ldc[0] + coloff + n, n, val, src);
       });
       bf16_t* tb = (t4 & 1) ? (bf16_t*)p.c[3] : (bf16_t*)p.c[2];
-      cols_bf16(T + t4 * TP, tb + coloff * p.ldc[2], p.ldc[2]);
+      if (tb) cols_bf16(T + t4 * TP, tb + coloff * p.ldc[2], p.ldc[2]);
     }
   } else if constexpr (EPI == E_PLANES) {
 #pragma unroll
@@ -580,12 +652,12 @@ __global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict
   }
 }
 
-template <int BM, int BN, int PA, int PB, int EPI, int NS>
+template <int BM, int BN, int PA, int PB, int EPI, int NS, int TM = 0>
 int launch_ns(hipStream_t s, const FParams& p, int splits) {
   constexpr int NBM = EPI == E_GATEUP ? 2 : 1;
   constexpr size_t lds = lds_bytes<BM, BN, PA, PB, EPI, NS>();
   static_assert(lds <= 160 * 1024, "LDS budget");
-  auto kern = k_gemm_fast<BM, BN, PA, PB, EPI, NS>;
+  auto kern = k_gemm_fast<BM, BN, PA, PB, EPI, NS, TM>;
   const_cast<FParams&>(p).xcd_remap = xcd_remap();
   // grid z: split-K slices, or the experts of a per-expert dW launch
   dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
@@ -602,19 +674,19 @@ int launch_ns(hipStream_t s, const FParams& p, int splits) {
 // SJ_GEMM_STAGES=2|3 overrides it (sweeps).
 int g_stages = -1;
 int cus();
-template <int BM, int BN, int PA, int PB, int EPI, int NS>
+template <int BM, int BN, int PA, int PB, int EPI, int NS, int TM = 0>
 int resident() {
   static int occ = -1;
   if (occ < 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemm_fast<BM, BN, PA, PB, EPI, NS>, NT,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemm_fast<BM, BN, PA, PB, EPI, NS, TM>, NT,
                                                      lds_bytes<BM, BN, PA, PB, EPI, NS>()) != hipSuccess)
       n = 1;
     occ = n > 0 ? n : 1;
   }
   return occ;
 }
-template <int BM, int BN, int PA, int PB, int EPI>
+template <int BM, int BN, int PA, int PB, int EPI, int TM = 0>
 int launch(hipStream_t s, const FParams& p, int splits) {
   if (g_stages < 0) {
     const char* e = getenv("SJ_GEMM_STAGES");
@@ -627,12 +699,12 @@ int launch(hipStream_t s, const FParams& p, int splits) {
       ns = g_stages;
     } else {
       const long wgs = ((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM) * (long)splits;
-      const int o3 = resident<BM, BN, PA, PB, EPI, 3>(), o2 = resident<BM, BN, PA, PB, EPI, 2>();
+      const int o3 = resident<BM, BN, PA, PB, EPI, 3, TM>(), o2 = resident<BM, BN, PA, PB, EPI, 2, TM>();
       ns = (wgs <= (long)o3 * cus() || o2 <= o3) ? 3 : 2;
     }
-    if (ns == 3) return launch_ns<BM, BN, PA, PB, EPI, 3>(s, p, splits);
+    if (ns == 3) return launch_ns<BM, BN, PA, PB, EPI, 3, TM>(s, p, splits);
   }
-  return launch_ns<BM, BN, PA, PB, EPI, 2>(s, p, splits);
+  return launch_ns<BM, BN, PA, PB, EPI, 2, TM>(s, p, splits);
 }
 
 int g_cu = 0;
@@ -757,17 +829,17 @@ int splits_for(long M, long N, long K, int bm, int bn) {
   return s < 1 ? 1 : (int)s;
 }
 
-template <int EPI, int PA, int PB>
+template <int EPI, int PA, int PB, int TM = 0>
 int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
   // both operands split: a 128x128 stage does not fit three deep in LDS
   if constexpr (PA == 2 && PB == 2) {
     if (bm == 128 && bn == 128) bn = 64;
   } else {
-    if (bm == 128 && bn == 128) return launch<128, 128, PA, PB, EPI>(s, p, splits);
+    if (bm == 128 && bn == 128) return launch<128, 128, PA, PB, EPI, TM>(s, p, splits);
   }
-  if (bm == 128 && bn == 64) return launch<128, 64, PA, PB, EPI>(s, p, splits);
-  if (bm == 64 && bn == 128) return launch<64, 128, PA, PB, EPI>(s, p, splits);
-  return launch<64, 64, PA, PB, EPI>(s, p, splits);
+  if (bm == 128 && bn == 64) return launch<128, 64, PA, PB, EPI, TM>(s, p, splits);
+  if (bm == 64 && bn == 128) return launch<64, 128, PA, PB, EPI, TM>(s, p, splits);
+  return launch<64, 64, PA, PB, EPI, TM>(s, p, splits);
 }
 
 // plane combinations each epilogue is used with: forward epilogues read
@@ -779,51 +851,51 @@ constexpr bool plane_combo() {
   return PA == 1 && PB == 1;
 }
 
-template <int EPI>
+template <int EPI, int TM = 0>
 int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int bn, int splits) {
   if constexpr (plane_combo<EPI, 1, 1>())
-    if (pa == 1 && pb == 1) return launch_tile<EPI, 1, 1>(s, p, bm, bn, splits);
+    if (pa == 1 && pb == 1) return launch_tile<EPI, 1, 1, TM>(s, p, bm, bn, splits);
   if constexpr (plane_combo<EPI, 2, 1>())
-    if (pa == 2 && pb == 1) return launch_tile<EPI, 2, 1>(s, p, bm, bn, splits);
+    if (pa == 2 && pb == 1) return launch_tile<EPI, 2, 1, TM>(s, p, bm, bn, splits);
   if constexpr (plane_combo<EPI, 1, 2>())
-    if (pa == 1 && pb == 2) return launch_tile<EPI, 1, 2>(s, p, bm, bn, splits);
+    if (pa == 1 && pb == 2) return launch_tile<EPI, 1, 2, TM>(s, p, bm, bn, splits);
   if constexpr (plane_combo<EPI, 2, 2>())
-    if (pa == 2 && pb == 2) return launch_tile<EPI, 2, 2>(s, p, bm, bn, splits);
+    if (pa == 2 && pb == 2) return launch_tile<EPI, 2, 2, TM>(s, p, bm, bn, splits);
   return sjh::fail(SJ_ERR_UNSUPPORTED, "gemm: planes %d/%d for this epilogue", pa, pb);
 }
 
 bool ok16(const void* q) { return ((uintptr_t)q & 15) == 0; }
 
-template <int BM, int BN, int PA, int PB, int EPI, int NS>
+template <int BM, int BN, int PA, int PB, int EPI, int NS, int TM = 0>
 int set_attr_ns() {
   constexpr size_t lds = lds_bytes<BM, BN, PA, PB, EPI, NS>();
-  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_fast<BM, BN, PA, PB, EPI, NS>,
+  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_fast<BM, BN, PA, PB, EPI, NS, TM>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   return e == hipSuccess ? SJ_OK : sjh::hip_check(e, "gemm: LDS attribute");
 }
-template <int BM, int BN, int PA, int PB, int EPI>
+template <int BM, int BN, int PA, int PB, int EPI, int TM = 0>
 int set_attr() {
-  int st = set_attr_ns<BM, BN, PA, PB, EPI, 2>();
+  int st = set_attr_ns<BM, BN, PA, PB, EPI, 2, TM>();
   if constexpr (lds_bytes<BM, BN, PA, PB, EPI, 3>() <= 160 * 1024)
-    if (!st) st = set_attr_ns<BM, BN, PA, PB, EPI, 3>();
+    if (!st) st = set_attr_ns<BM, BN, PA, PB, EPI, 3, TM>();
   return st;
 }
-template <int EPI, int PA, int PB>
+template <int EPI, int PA, int PB, int TM = 0>
 int set_attrs_tiles() {
   int s = SJ_OK;
-  if constexpr (!(PA == 2 && PB == 2)) s = set_attr<128, 128, PA, PB, EPI>();
-  if (!s) s = set_attr<128, 64, PA, PB, EPI>();
-  if (!s) s = set_attr<64, 128, PA, PB, EPI>();
-  if (!s) s = set_attr<64, 64, PA, PB, EPI>();
+  if constexpr (!(PA == 2 && PB == 2)) s = set_attr<128, 128, PA, PB, EPI, TM>();
+  if (!s) s = set_attr<128, 64, PA, PB, EPI, TM>();
+  if (!s) s = set_attr<64, 128, PA, PB, EPI, TM>();
+  if (!s) s = set_attr<64, 64, PA, PB, EPI, TM>();
   return s;
 }
-template <int EPI>
+template <int EPI, int TM = 0>
 int set_attrs_planes() {
   int s = SJ_OK;
-  if constexpr (plane_combo<EPI, 1, 1>()) s = set_attrs_tiles<EPI, 1, 1>();
-  if constexpr (plane_combo<EPI, 2, 1>()) if (!s) s = set_attrs_tiles<EPI, 2, 1>();
-  if constexpr (plane_combo<EPI, 1, 2>()) if (!s) s = set_attrs_tiles<EPI, 1, 2>();
-  if constexpr (plane_combo<EPI, 2, 2>()) if (!s) s = set_attrs_tiles<EPI, 2, 2>();
+  if constexpr (plane_combo<EPI, 1, 1>()) s = set_attrs_tiles<EPI, 1, 1, TM>();
+  if constexpr (plane_combo<EPI, 2, 1>()) if (!s) s = set_attrs_tiles<EPI, 2, 1, TM>();
+  if constexpr (plane_combo<EPI, 1, 2>()) if (!s) s = set_attrs_tiles<EPI, 1, 2, TM>();
+  if constexpr (plane_combo<EPI, 2, 2>()) if (!s) s = set_attrs_tiles<EPI, 2, 2, TM>();
   return s;
 }
 
@@ -843,6 +915,8 @@ int gemm_fast_prepare() {
   if (!status) status = set_attrs_planes<E_GATEUP>();
   if (!status) status = set_attrs_planes<E_SWIGLU_BWD>();
   if (!status) status = set_attrs_planes<E_PLANES>();
+  if (!status) status = set_attrs_planes<E_STORE, 3>();
+  if (!status) status = set_attrs_planes<E_PARTIAL, 3>();
   return status;
 }
 }  // namespace sjh
@@ -861,17 +935,11 @@ extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
   return need;
 }
 
-extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
-                              long lda, const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype,
-                              long ldc, int accumulate, void* workspace, size_t workspace_bytes) {
-  if (int st0 = sjh::gemm_fast_prepare()) return st0;
-  SJ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
-                 ldc >= N,
-             "matmul planes: M %ld N %ld K %ld lda %ld ldb %ld (K and ld must be multiples of 8)", M, N, K, lda, ldb);
-  SJ_REQUIRE(a_hi && b_hi && ok16(a_hi) && ok16(b_hi) && (!a_lo || ok16(a_lo)) && (!b_lo || ok16(b_lo)),
-             "matmul planes: 16-byte aligned planes required");
-  SJ_REQUIRE(c_dtype == SJ_F32 || c_dtype == SJ_BF16, "matmul planes: output dtype %d", c_dtype);
-  SJ_REQUIRE(!(accumulate && c_dtype == SJ_BF16), "matmul: accumulate needs an fp32 output");
+namespace {
+template <int TM>
+int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo, long lda,
+                const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype, long ldc, int accumulate,
+                void* workspace, size_t workspace_bytes) {
   if (M == 0 || N == 0 || K == 0) return SJ_OK;
   hipStream_t s = (hipStream_t)stream;
   FParams p = {};
@@ -888,18 +956,50 @@ extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16
     splits = (int)((K + kchunk - 1) / kchunk);
     p.kchunk = kchunk;
     p.partial = (float*)workspace;
-    int st = launch_planes<E_PARTIAL>(s, p, pa, pb, bm, bn, splits);
+    int st = launch_planes<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
     if (st) return st;
     long total = M * N, blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(k_reduce_partials, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)workspace, splits, M,
                        N, c, ldc, (int)p.c_bf16, accumulate);
   } else {
-    int st = launch_planes<E_STORE>(s, p, pa, pb, bm, bn, 1);
+    int st = launch_planes<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
     if (st) return st;
   }
   SJ_LAUNCH_CHECK("matmul planes");
   return SJ_OK;
+}
+}  // namespace
+
+extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
+                              long lda, const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype,
+                              long ldc, int accumulate, void* workspace, size_t workspace_bytes) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
+                 ldc >= N,
+             "matmul planes: M %ld N %ld K %ld lda %ld ldb %ld (K and ld must be multiples of 8)", M, N, K, lda, ldb);
+  SJ_REQUIRE(a_hi && b_hi && ok16(a_hi) && ok16(b_hi) && (!a_lo || ok16(a_lo)) && (!b_lo || ok16(b_lo)),
+             "matmul planes: 16-byte aligned planes required");
+  SJ_REQUIRE(c_dtype == SJ_F32 || c_dtype == SJ_BF16, "matmul planes: output dtype %d", c_dtype);
+  SJ_REQUIRE(!(accumulate && c_dtype == SJ_BF16), "matmul: accumulate needs an fp32 output");
+  return gemm_planes<0>(stream, M, N, K, a_hi, a_lo, lda, b_hi, b_lo, ldb, c, c_dtype, ldc, accumulate, workspace,
+                        workspace_bytes);
+}
+
+extern "C" int sj_gemm_planes_tn(void* stream, long M, long N, long K, const uint16_t* x_hi, const uint16_t* x_lo,
+                                 long ldx, const uint16_t* y_hi, const uint16_t* y_lo, long ldy, void* c, int c_dtype,
+                                 long ldc, int accumulate, void* workspace, size_t workspace_bytes) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M % 8 == 0 && N % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && ldx >= M &&
+                 ldy >= N && ldc >= N,
+             "matmul planes (row-layout operands): M %ld N %ld K %ld ldx %ld ldy %ld (M, N and ld multiples of 8)",
+             M, N, K, ldx, ldy);
+  SJ_REQUIRE(x_hi && y_hi && ok16(x_hi) && ok16(y_hi) && (!x_lo || ok16(x_lo)) && (!y_lo || ok16(y_lo)),
+             "matmul planes (row-layout operands): 16-byte aligned planes required");
+  SJ_REQUIRE(c_dtype == SJ_F32 || c_dtype == SJ_BF16, "matmul planes: output dtype %d", c_dtype);
+  SJ_REQUIRE(!(accumulate && c_dtype == SJ_BF16), "matmul: accumulate needs an fp32 output");
+  return gemm_planes<3>(stream, M, N, K, x_hi, x_lo, ldx, y_hi, y_lo, ldy, c, c_dtype, ldc, accumulate, workspace,
+                        workspace_bytes);
 }
 
 extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, const uint16_t* a_hi,
@@ -1016,8 +1116,9 @@ extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const u
                                     uint16_t* dgu_t_hi, uint16_t* dgu_t_lo, long lddgu_t) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
   SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && lddy % 8 == 0 && ldw % 8 == 0 && lddy >= D && ldw >= D && ldgu >= F &&
-                 lddgu >= 2 * F && lddgu_t >= M && lddgu_t % 4 == 0 && ok16(dy_hi) && ok16(dy_lo) && ok16(w_down),
-             "swiglu_backward (planes): shape/alignment");
+                 lddgu >= 2 * F && !dgu_t_hi == !dgu_t_lo && (!dgu_t_hi || (lddgu_t >= M && lddgu_t % 4 == 0)) &&
+                 ok16(dy_hi) && ok16(dy_lo) && ok16(w_down),
+             "swiglu_backward (planes): shape/alignment (transposed outputs both or neither)");
   if (M == 0) return SJ_OK;
   FParams p = {};
   p.a[0] = (const bf16_t*)dy_hi; p.a[1] = (const bf16_t*)dy_lo; p.lda = lddy;

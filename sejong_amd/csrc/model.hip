@@ -194,6 +194,11 @@ struct sj_model {
   uint16_t* mirror = nullptr;  // bf16 compute copy (dt == bf16)
   // MFMA-layout path (bf16, head_dim 64)
   bool planes = false;
+  // row-layout dW (planes path without the parameter VJP, every stage on the
+  // MFMA-layout attention): the dW products read activations and gradient
+  // planes in row orientation (sj_gemm_planes_tn), so no producer writes a
+  // transposed copy; the gradient planes live in the parity buffers pt
+  bool rowdw = false;
   long ldt = 0;                   // leading dimension of [cols][rows] activations (M rounded to 8)
   uint16_t* mirror_t = nullptr;   // transposed projection matrices, same offsets as the mirror
   TJob* tjobs = nullptr;
@@ -501,16 +506,16 @@ int stage_forward(sj_model* m, int si) {
     const uint16_t *x = (const uint16_t*)xin(m, l), *x1 = (const uint16_t*)m->x1[l];
     uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
     uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
-    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->zt[l], ldt, M, d, eps));
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->rowdw ? nullptr : m->zt[l], ldt, M, d, eps));
     OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, S.rope, S.T, S.Dh, nullptr, ldt));
     if (S.attn_tt)
       OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, ldt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, o, d,
-                                              m->lse[l], m->lset[l], m->ot[l], ldt));
+                                              m->lse[l], m->lset[l], m->rowdw ? nullptr : m->ot[l], ldt));
     else
       OP("attention_fwd", sj_attention_fwd_t(s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, o, d, m->lse[l], m->ot[l],
                                              ldt, m->B, S.T, S.HQ, S.HK, S.Dh));
     OP("attn_out_residual", sj_linear_residual_fwd_t(s, o, d, M, d, WT + y.wo, d, d, x, d, (uint16_t*)m->x1[l], d));
-    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->z2t[l], ldt, M, d, eps));
+    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->rowdw ? nullptr : m->z2t[l], ldt, M, d, eps));
     if (m->E) {  // Block::apply's MoE branch (architecture.rs:229-242), packed by expert on the device
       const long E = m->E, K = m->K, cap = m->cap;
       OP("router_topk", sj_router_topk(s, z2, d, W + y.router, d, M, E, K, m->mlog[l], m->mids[l], m->mwts[l]));
@@ -524,8 +529,8 @@ int stage_forward(sj_model* m, int si) {
                                             (uint16_t*)xout(m, l), d));
       continue;
     }
-    OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F, m->ht[l],
-                                          ldt));
+    OP("gate_up_swiglu", sj_gate_up_fwd_t(s, z2, d, M, d, WT + y.gu, WT + y.gu + F * d, d, F, gg, uu, hh, F,
+                                          m->rowdw ? nullptr : m->ht[l], ldt));
     OP("down_residual", sj_linear_residual_fwd_t(s, hh, F, M, F, WT + y.down, F, d, x1, d, (uint16_t*)xout(m, l), d));
   }
   for (long l = S.first; l < S.first + S.count && !m->planes; l++) {
@@ -681,12 +686,20 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       return SJ_OK;
     };
     auto T = [&](int k, int p) { return m->pt[k][p]; };
+    // gradient planes of kind k for layer parity p: the row-orientation pair
+    // [M][width] the dX products read (and, row-layout dW, the dW products),
+    // and the transposed pair [width][ldt] (nullptr under row-layout dW)
+    uint16_t* const nul[2] = {nullptr, nullptr};
+    uint16_t* const* normal[4] = {rp, gp, xp, qp};
+    const bool rdw = m->rowdw;
+    auto NP = [&](int k, int p) -> uint16_t* const* { return rdw ? m->pt[k][p] : normal[k]; };
+    auto TP = [&](int k, int p) -> uint16_t* const* { return rdw ? nul : m->pt[k][p]; };
     {
       const int p = (int)(top & 1);
       TRY(reuse(KR, p));
       OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)xtop(m, S), W + S.norm, dzin, nullptr,
-                                                    m->dres[cur], rp[0], rp[1], T(KR, p)[0], T(KR, p)[1], ldt, M, d,
-                                                    eps, m->slot_ptr[m->slot_close[si]]));
+                                                    m->dres[cur], NP(KR, p)[0], NP(KR, p)[1], TP(KR, p)[0],
+                                                    TP(KR, p)[1], ldt, M, d, eps, m->slot_ptr[m->slot_close[si]]));
       TRY(written(KR, p));
     }
     for (long l = top; l >= S.first; l--) {
@@ -731,35 +744,46 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       } else {
       // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
       TRY(reuse(KG, p));
-      OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, rp[0], rp[1], d, M, d, W + y.down, d, F, (const uint16_t*)m->gg[l],
-                                                (const uint16_t*)m->uu[l], F, gp[0], gp[1], 2 * F, T(KG, p)[0],
-                                                T(KG, p)[1], ldt));
+      OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, NP(KR, p)[0], NP(KR, p)[1], d, M, d, W + y.down, d, F,
+                                                (const uint16_t*)m->gg[l], (const uint16_t*)m->uu[l], F,
+                                                NP(KG, p)[0], NP(KG, p)[1], 2 * F, TP(KG, p)[0], TP(KG, p)[1], ldt));
       TRY(written(KG, p));
-      OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt, G + y.down,
-                                   SJ_F32, d, 0, ws2, wsb));
+      if (rdw)
+        OP("down_dw", sj_gemm_planes_tn(s2, F, d, M, (const uint16_t*)m->hh[l], nullptr, F, NP(KR, p)[0],
+                                        NP(KR, p)[1], d, G + y.down, SJ_F32, d, 0, ws2, wsb));
+      else
+        OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt, G + y.down,
+                                     SJ_F32, d, 0, ws2, wsb));
       TRY(read(KR, p));
-      OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, gp[0], gp[1], 2 * F, W + y.gu, nullptr, 2 * F, m->dz, SJ_F32, d, 0, ws,
-                                      wsb));
+      OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, NP(KG, p)[0], NP(KG, p)[1], 2 * F, W + y.gu, nullptr, 2 * F,
+                                      m->dz, SJ_F32, d, 0, ws, wsb));
       if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, T(KG, p)));
-      if (!m->group_all[1])
+      if (rdw)
+        OP("gate_up_dw", sj_gemm_planes_tn(s2, d, 2 * F, M, (const uint16_t*)m->z2[l], nullptr, d, NP(KG, p)[0],
+                                           NP(KG, p)[1], 2 * F, G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
+      else if (!m->group_all[1])
         OP("gate_up_dw", sj_gemm_planes(s2, d, 2 * F, M, m->z2t[l], nullptr, ldt, T(KG, p)[0], T(KG, p)[1], ldt,
                                         G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       TRY(read(KG, p));
       }
       TRY(reuse(KX, p));
       OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)m->x1[l], W + y.fn, m->dz, m->dres[cur], m->dx1,
-                                                    xp[0], xp[1], T(KX, p)[0], T(KX, p)[1], ldt, M, d, eps,
-                                                    m->slot_ptr[m->slot_fn[l]]));
+                                                    NP(KX, p)[0], NP(KX, p)[1], TP(KX, p)[0], TP(KX, p)[1], ldt, M, d,
+                                                    eps, m->slot_ptr[m->slot_fn[l]]));
       TRY(written(KX, p));
       // x1 = x + attention_output(o)
       if (S.attn_tt)  // dO as hi/lo planes: the attention backward's operands
-        OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, xp[0], xp[1], d, W + y.wo, d, m->dop[0], m->dop[1], d,
-                                                   nullptr, nullptr, 0));
+        OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, NP(KX, p)[0], NP(KX, p)[1], d, W + y.wo, d, m->dop[0],
+                                                   m->dop[1], d, nullptr, nullptr, 0));
       else
         OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
                                          wsb));
-      OP("attn_out_dw", sj_gemm_planes(s2, d, d, M, m->ot[l], nullptr, ldt, T(KX, p)[0], T(KX, p)[1], ldt, G + y.wo,
-                                       SJ_F32, d, 0, ws2, wsb));
+      if (rdw)
+        OP("attn_out_dw", sj_gemm_planes_tn(s2, d, d, M, (const uint16_t*)m->o[l], nullptr, d, NP(KX, p)[0],
+                                            NP(KX, p)[1], d, G + y.wo, SJ_F32, d, 0, ws2, wsb));
+      else
+        OP("attn_out_dw", sj_gemm_planes(s2, d, d, M, m->ot[l], nullptr, ldt, T(KX, p)[0], T(KX, p)[1], ldt, G + y.wo,
+                                         SJ_F32, d, 0, ws2, wsb));
       TRY(read(KX, p));
       TRY(reuse(KQ, p));
       for (int part = 1; part <= 4; part <<= 1) {
@@ -767,17 +791,21 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         if (S.attn_tt)
           OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, ldt, (const uint16_t*)m->o[l], d, m->lset[l],
                                              m->dop[0], m->dop[1], d, m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh,
-                                             S.window, S.rope, qp[0], qp[1], NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws,
-                                             wsb));
+                                             S.window, S.rope, NP(KQ, p)[0], NP(KQ, p)[1], NQ, TP(KQ, p)[0],
+                                             TP(KQ, p)[1], ldt, ws, wsb));
         else
           OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
                                             m->lse[l], m->dO, d, m->delta, m->B, S.T, S.HQ, S.HK, S.Dh, S.rope,
                                             qp[0], qp[1], NQ, T(KQ, p)[0], T(KQ, p)[1], ldt, ws, wsb));
       }
       TRY(written(KQ, p));
-      OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, qp[0], qp[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d, 0, ws, wsb));
+      OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, NP(KQ, p)[0], NP(KQ, p)[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d,
+                                  0, ws, wsb));
       if (m->group_on[0]) TRY(vjp_group(m, l, 0, s2, ws2, wsb, T(KQ, p)));
-      if (!m->group_all[0])
+      if (rdw)
+        OP("qkv_dw", sj_gemm_planes_tn(s2, d, NQ, M, (const uint16_t*)m->z[l], nullptr, d, NP(KQ, p)[0], NP(KQ, p)[1],
+                                       NQ, G + y.qkv, SJ_F32, NQ, 0, ws2, wsb));
+      else if (!m->group_all[0])
         OP("qkv_dw", sj_gemm_planes(s2, d, NQ, M, m->zt[l], nullptr, ldt, T(KQ, p)[0], T(KQ, p)[1], ldt, G + y.qkv,
                                     SJ_F32, NQ, 0, ws2, wsb));
       TRY(read(KQ, p));
@@ -785,8 +813,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         const int pn = (int)((l - 1) & 1);
         TRY(reuse(KR, pn));
         OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)xin(m, l), W + y.an, m->dz, m->dx1,
-                                                      m->dres[cur ^ 1], rp[0], rp[1], T(KR, pn)[0], T(KR, pn)[1], ldt,
-                                                      M, d, eps, m->slot_ptr[m->slot_an[l]]));
+                                                      m->dres[cur ^ 1], NP(KR, pn)[0], NP(KR, pn)[1], TP(KR, pn)[0],
+                                                      TP(KR, pn)[1], ldt, M, d, eps, m->slot_ptr[m->slot_an[l]]));
         TRY(written(KR, pn));
       } else {  // the stage input's gradient feeds row-layout consumers only
         OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xin(m, l), dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
@@ -1285,6 +1313,8 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     st = vjp_decide(m);
     if (st) return fail_cleanup(st);
   }
+  m->rowdw = m->planes && !m->vjp;
+  for (const Stage& S : m->stages) m->rowdw = m->rowdw && S.attn_tt;
 #define ALLOC(ptr, bytes)                                    \
   do {                                                       \
     void* _p = nullptr;                                      \

@@ -253,6 +253,7 @@ __global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x,
       *(uint32_t*)(stage + wv * d + 2 * p) = pk;
     }
   }
+  if (!yt) return;  // no transposed output: the block is done (uniform)
   __syncthreads();
   for (long q = threadIdx.x; q < 2 * d; q += NTT) {
     const long c = q >> 1;
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(NTT) void k_rms_bwd_p(const bf16_t* __restrict__ x,
     for (int i = 0; i < TR; i++) acc += red[i * d + c];
     partial[blk * d + c] = acc;
   }
-  for (long q = threadIdx.x; q < 4 * d; q += NTT) {
+  for (long q = threadIdx.x; hit && q < 4 * d; q += NTT) {  // transposed planes (optional)
     const int plane = q >= 2 * d;
     const long qq = plane ? q - 2 * d : q;
     const long c = qq >> 1;
@@ -454,7 +455,7 @@ void launch_bwd_p(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x,
 
 extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t* w, uint16_t* y, uint16_t* y_t,
                                 long ldt, long rows, long d, float eps) {
-  SJ_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 1024 && ldt >= rows && ldt % 8 == 0 &&
+  SJ_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 1024 && (!y_t || (ldt >= rows && ldt % 8 == 0)) &&
                  ((uintptr_t)y_t & 15) == 0,
              "RMSNorm (transposed output): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
   if (rows == 0) return SJ_OK;
@@ -481,8 +482,9 @@ extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t*
 int sjh::rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, const float* dy,
                                 const float* dx_acc, float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi,
                                 uint16_t* dx_t_lo, long ldt, long rows, long d, float eps, float* partial) {
-  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && ldt >= rows && ldt % 8 == 0 && partial &&
-                 ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
+  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && partial && !dx_t_hi == !dx_t_lo &&
+                 (!dx_t_hi || (ldt >= rows && ldt % 8 == 0)) && ((uintptr_t)dx_t_hi & 15) == 0 &&
+                 ((uintptr_t)dx_t_lo & 15) == 0,
              "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
   if (int st0 = sjh::norm_prepare()) return st0;
   hipStream_t s = (hipStream_t)stream;
@@ -519,8 +521,9 @@ extern "C" int sj_rmsnorm_bwd_p(void* stream, const uint16_t* x, const uint16_t*
                                 const float* dx_acc, float* dx, float* dw, uint16_t* dx_hi, uint16_t* dx_lo,
                                 uint16_t* dx_t_hi, uint16_t* dx_t_lo, long ldt, long rows, long d, float eps,
                                 void* workspace, size_t workspace_bytes) {
-  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && ldt >= rows && ldt % 8 == 0 &&
-                 ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
+  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && !dx_t_hi == !dx_t_lo &&
+                 (!dx_t_hi || (ldt >= rows && ldt % 8 == 0)) && ((uintptr_t)dx_t_hi & 15) == 0 &&
+                 ((uintptr_t)dx_t_lo & 15) == 0,
              "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
   if (int st0 = sjh::norm_prepare()) return st0;
   size_t need = sj_rmsnorm_bwd_p_workspace_bytes(rows, d);

@@ -72,6 +72,54 @@ def test_gemm_planes(api, lib, M, N, K, sa, sb, cdt):
         assert r < (1e-5 if not (sa or sb) else 3e-5), r
 
 
+TN_CASES = [
+    # M, N, K (tokens), split_x, split_y: the step's dW shapes and ragged / split-K ones
+    (384, 2048, 4096, False, True),    # gate|up dW at cfg2
+    (1024, 384, 4096, False, True),    # down dW
+    (384, 640, 4096, False, True),     # q|k|v dW
+    (136, 200, 1000, False, True),     # M, N not multiples of 64, K not of 64
+    (384, 384, 16384, False, True),    # long K: split-K partials
+    (256, 192, 512, True, True),       # both operands split
+    (64, 64, 40, False, False),        # one tile, K shorter than a stage
+]
+
+
+@pytest.mark.parametrize("M,N,K,sx,sy", TN_CASES)
+def test_gemm_planes_tn_row_layout(api, lib, M, N, K, sx, sy):
+    """C = X^T Y from row-layout operands (X [K][M], Y [K][N], fragments by
+    LDS transpose reads) equals sj_gemm_planes on the transposed copies bit
+    for bit (same k order and operand values) and X^T Y in FP64."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    X = rng.normal(0, 1, (K, M)).astype(np.float32).astype(np.float64)
+    Y = rng.normal(0, 1, (K, N)).astype(np.float32).astype(np.float64)
+    if not sx:
+        X = O.round_to(X, "bf16")
+    if not sy:
+        Y = O.round_to(Y, "bf16")
+    xh, xl = split(X) if sx else (X, None)
+    yh, yl = split(Y) if sy else (Y, None)
+    ldx, ldy = M + 8, N + 16                              # padded row strides
+    pad = lambda a, ld: np.concatenate([a, np.zeros((a.shape[0], ld - a.shape[1]))], 1)
+    Xh, Yh = dev(pad(xh, ldx), "bf16"), dev(pad(yh, ldy), "bf16")
+    Xl = dev(pad(xl, ldx), "bf16") if sx else None
+    Yl = dev(pad(yl, ldy), "bf16") if sy else None
+    ws = empty(max(lib.sj_gemm_planes_workspace_bytes(M, N, K), 256), "u8")
+    C = zeros(M * N)
+    print(f"[gemm_tn] M={M} N={N} K={K} split x/y {sx}/{sy}", flush=True)
+    api.sj_gemm_planes_tn(None, M, N, K, Xh.p, Xl.p if sx else None, ldx, Yh.p, Yl.p if sy else None, ldy, C.p, F32,
+                          N, 0, ws.p, ws.nbytes)
+    Kp = (K + 7) // 8 * 8                                 # k-contiguous copies need K % 8 == 0
+    tr = lambda a: dev(np.concatenate([a.T, np.zeros((a.shape[1], Kp - K))], 1), "bf16")
+    C2 = zeros(M * N)
+    api.sj_gemm_planes(None, M, N, Kp, tr(xh).p, tr(xl).p if sx else None, Kp, tr(yh).p, tr(yl).p if sy else None,
+                       Kp, C2.p, F32, N, 0, ws.p, ws.nbytes)
+    sync()
+    ref = O.matmul(X, Y, 1, 0)
+    assert rel(C.host(), ref) < (1e-5 if not (sx or sy) else 3e-5), rel(C.host(), ref)
+    if Kp == K:
+        np.testing.assert_array_equal(C.host(), C2.host())
+
+
 def test_gemm_planes_accumulate(api, lib):
     rng = np.random.default_rng(11)
     M, N, K = 384, 384, 4096
