@@ -889,6 +889,48 @@ __global__ __launch_bounds__(256) void k_attn_kv_reduce(const float* __restrict_
   }
 }
 
+// The same group reduce without transposed planes: one thread per (row, 8
+// consecutive columns of dK | dV), 16-byte loads of each head's partial
+// (summed in head order, as above) and 16-byte plane stores.
+__global__ __launch_bounds__(256) void k_attn_kv_reduce_rows(const float* __restrict__ part, int group, long M,
+                                                             long T, long N, long KV, const float* __restrict__ rope,
+                                                             bf16_t* __restrict__ gh, bf16_t* __restrict__ gl,
+                                                             long ldg) {
+  const long per_row = (2 * KV) >> 3;
+  const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= M * per_row) return;
+  const long row = item / per_row, c8 = (item - row * per_row) << 3;  // column in [0, 2 KV)
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int gi = 0; gi < group; gi++) {
+    const float4* src = (const float4*)(part + ((long)gi * M + row) * 2 * KV + c8);
+    const float4 a = src[0], b = src[1];
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+    v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+  }
+  if (c8 < KV && rope) {  // inverse RoPE on dK's pairs
+    const long pos = row % T;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const long col = c8 + 2 * k;
+      const float2 cs = *(const float2*)(rope + 2 * (pos * (DH / 2) + ((col % DH) >> 1)));
+      const float x = v[2 * k], y = v[2 * k + 1];
+      v[2 * k] = x * cs.x + y * cs.y;
+      v[2 * k + 1] = y * cs.x - x * cs.y;
+    }
+  }
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    bf16_t ha, la, hb, lb;
+    split_bf(v[2 * k], ha, la);
+    split_bf(v[2 * k + 1], hb, lb);
+    h[k] = pack2(ha, hb);
+    l[k] = pack2(la, lb);
+  }
+  *(u32x4*)(gh + row * ldg + N + c8) = u32x4{h[0], h[1], h[2], h[3]};
+  *(u32x4*)(gl + row * ldg + N + c8) = u32x4{l[0], l[1], l[2], l[3]};
+}
+
 // ----------------------------------------------- wavefront-per-row kernels
 // Any storage dtype, head width <= 128, optional window (hierarchy.py:24,
 // 60, 87).  Lanes span the head dimension; keys are walked in order.
@@ -1219,6 +1261,14 @@ extern "C" int sj_attention_bwd_p(void* stream, const uint16_t* q, long ldq, con
 int sjh::attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
                              const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi,
                              uint16_t* gt_lo, long ldgt) {
+  if (!gt_hi && ldg % 8 == 0 && N % 8 == 0 && KV % 4 == 0 && ((uintptr_t)g_hi & 15) == 0 &&
+      ((uintptr_t)g_lo & 15) == 0 && ((uintptr_t)part & 15) == 0) {
+    const long items = M * (2 * KV / 8);
+    hipLaunchKernelGGL(k_attn_kv_reduce_rows, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, part, (int)group,
+                       M, T, N, KV, rope, (bf16_t*)g_hi, (bf16_t*)g_lo, ldg);
+    SJ_LAUNCH_CHECK("hierarchy_attention_kv_reduce");
+    return SJ_OK;
+  }
   hipLaunchKernelGGL(k_attn_kv_reduce, dim3((unsigned)((M + 2 * KVR_ROWS - 1) / (2 * KVR_ROWS))), dim3(256), 0, s, part,
                      (int)group, M, T, N, KV, rope, (bf16_t*)g_hi, (bf16_t*)g_lo, ldg, (bf16_t*)gt_hi, (bf16_t*)gt_lo,
                      ldgt);

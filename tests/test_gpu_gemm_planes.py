@@ -362,6 +362,13 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)
     np.testing.assert_array_equal(Th.host().reshape(NG, ldt)[:, :M], hi.T)
     np.testing.assert_array_equal(Tl.host().reshape(NG, ldt)[:, :M], lo.T)
+    # transposed outputs are optional (the row-layout dW step): same planes bit for bit
+    G2h, G2l = empty(M * NG, "bf16"), empty(M * NG, "bf16")
+    api.sj_attention_bwd_tt(None, QKV.p, ldq, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DT.p, B, T, HQ, HK, Dh, W, tab.p,
+                            G2h.p, G2l.p, NG, None, None, 0, ws.p, ws.nbytes)
+    sync()
+    np.testing.assert_array_equal(G2h.host().reshape(M, NG), hi)
+    np.testing.assert_array_equal(G2l.host().reshape(M, NG), lo)
     dq, dk, dv, _ = O.attention_bwd(q, k, v, o2, L2.host(), dof, B, T, HQ, HK, Dh, W)
     dq = O.rope(dq, T, HQ, Dh, inverse=True); dk = O.rope(dk, T, HK, Dh, inverse=True)
     assert rel(got[:, :N], dq) < 1e-4 and rel(got[:, N:N + KV], dk) < 1e-4 and rel(got[:, N + KV:], dv) < 1e-4
