@@ -764,7 +764,7 @@ int splits_for(long M, long N, long K, int bm, int bn);
 //   split-A products (dX): 64x128 tiles when they give two per CU, else
 //   64x64 (cfg5 down dX: 662 -> 499 us; cfg2 dX: 64x64);
 //   the rest pick().
-void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
+void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits, bool row_layout = false) {
   const long cu = cus();
   const char* et = getenv("SJ_GEMM_TILE");
   const char* es = getenv("SJ_GEMM_SPLITS");
@@ -787,8 +787,11 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits) {
         dws = e ? atoi(e) : 0;
       }
       // the step runs dW beside the dX chain on its own stream: one slice up to
-      // K = 4096 (cfg2: no partials pass, 2.24 -> 2.20 ms), four beyond (cfg5)
-      const int want_s = dws > 0 ? dws : (K <= 4096 ? 1 : 4);
+      // K = 4096 (cfg2: no partials pass, 2.24 -> 2.20 ms), four beyond (cfg5);
+      // the row-layout form (LDS transpose reads, more LDS traffic per MFMA)
+      // takes four from K = 4096 (cfg2 step 2.004 -> 1.981 ms; at K = 2048,
+      // cfg3's global stage, slices of 512 lose: 4.07 -> 4.15 ms)
+      const int want_s = dws > 0 ? dws : row_layout ? (K >= 4096 ? 4 : 1) : (K <= 4096 ? 1 : 4);
       splits = K / 256 < want_s ? (int)(K / 256) : want_s;
       long want = tiles(M, N, 64, 64) * splits;
       want = want < 2 * cu ? want : 2 * cu;
@@ -924,14 +927,16 @@ int gemm_fast_prepare() {
 // ================================================================ C ABI
 
 extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
-  // the larger of the plans for a split and an unsplit A operand
+  // the largest of the plans for a split and an unsplit A operand, with
+  // k-contiguous and row-layout operands
   size_t need = 0;
-  for (int pa = 1; pa <= 2; pa++) {
-    int bm, bn, s;
-    plan(M, N, K, pa, bm, bn, s);
-    const size_t b = s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
-    need = b > need ? b : need;
-  }
+  for (int pa = 1; pa <= 2; pa++)
+    for (int rl = 0; rl < 2; rl++) {
+      int bm, bn, s;
+      plan(M, N, K, pa, bm, bn, s, rl != 0);
+      const size_t b = s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
+      need = b > need ? b : need;
+    }
   return need;
 }
 
@@ -949,7 +954,7 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
   p.c[0] = c; p.ldc[0] = ldc; p.c_bf16 = c_dtype == SJ_BF16; p.accumulate = accumulate;
   const int pa = a_lo ? 2 : 1, pb = b_lo ? 2 : 1;
   int bm, bn, splits;
-  plan(M, N, K, pa, bm, bn, splits);
+  plan(M, N, K, pa, bm, bn, splits, TM != 0);
   if (splits > 1 && workspace && workspace_bytes >= sizeof(float) * (size_t)splits * M * N) {
     long kchunk = (K + splits - 1) / splits;
     kchunk = (kchunk + BK - 1) / BK * BK;

@@ -87,8 +87,8 @@ TN_CASES = [
 @pytest.mark.parametrize("M,N,K,sx,sy", TN_CASES)
 def test_gemm_planes_tn_row_layout(api, lib, M, N, K, sx, sy):
     """C = X^T Y from row-layout operands (X [K][M], Y [K][N], fragments by
-    LDS transpose reads) equals sj_gemm_planes on the transposed copies bit
-    for bit (same k order and operand values) and X^T Y in FP64."""
+    LDS transpose reads) against X^T Y in FP64 and sj_gemm_planes on the
+    transposed copies (same operand values; the K split may differ)."""
     rng = np.random.default_rng(M + 3 * N + 7 * K)
     X = rng.normal(0, 1, (K, M)).astype(np.float32).astype(np.float64)
     Y = rng.normal(0, 1, (K, N)).astype(np.float32).astype(np.float64)
@@ -116,8 +116,8 @@ def test_gemm_planes_tn_row_layout(api, lib, M, N, K, sx, sy):
     sync()
     ref = O.matmul(X, Y, 1, 0)
     assert rel(C.host(), ref) < (1e-5 if not (sx or sy) else 3e-5), rel(C.host(), ref)
-    if Kp == K:
-        np.testing.assert_array_equal(C.host(), C2.host())
+    if Kp == K:  # same operand values; the plans may split K differently (fp32 partial sums)
+        assert rel(C.host(), C2.host()) < 1e-6
 
 
 def test_gemm_planes_accumulate(api, lib):
