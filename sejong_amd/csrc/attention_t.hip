@@ -158,6 +158,7 @@ struct TArgs {
   bf16_t *gq[2], *gqt[2];  // dQ planes: normal [M][ldg] at columns h*64, transposed [.][ldgt] at rows h*64
   long ldg, ldgt;
   float* part;  // [group][M][2*HK*64] per-head dK | dV
+  int B;        // batch (rows M = B * T)
 };
 
 // DMA of one 64 x 64 bf16 tile (rows r of `src` with stride ld, 8 chunks of
@@ -307,43 +308,30 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
 }
 
 // ------------------------------------------------------------- backward dQ
+// Workgroup (query block qb, query head h, batch b): dQ of its 64 queries,
+// with Delta read from delta_t (k_attn_delta).  lds: NS x [K | V].
 template <int NS>
-__global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
+__device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, int h, int b) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
-  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int T = a.T, NQ = a.HQ * DH;
   const int kvh = h / (a.HQ / a.HK);
   const int qloc = wave * 16 + j, myq = qb * QB + qloc;
   const long row0 = (long)b * T, qrow = row0 + myq;
   const float sc = 0.125f * LOG2E;
 
-  // this lane's query: Q, dO (hi, lo) fragments; Delta = sum dO * O
+  // this lane's query: Q, dO (hi, lo) fragments
   bf16x8 qf[2], dhf[2], dlf[2];
-  float dpart = 0.f;
 #pragma unroll
   for (int c = 0; c < 2; c++) {
     const int col = h * DH + 32 * c + 8 * g;
     qf[c] = as_bf8(*(const u32x4*)(a.qkv + qrow * a.ldqkv + col));
-    const u32x4 hv = *(const u32x4*)(a.dh + qrow * a.lddo + col);
-    const u32x4 lv = *(const u32x4*)(a.dl + qrow * a.lddo + col);
-    const u32x4 ov = *(const u32x4*)(a.ob + qrow * a.ldo + col);
-    dhf[c] = as_bf8(hv);
-    dlf[c] = as_bf8(lv);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      dpart += (bflo(hv[i]) + bflo(lv[i])) * bflo(ov[i]);
-      dpart += (bfhi(hv[i]) + bfhi(lv[i])) * bfhi(ov[i]);
-    }
+    dhf[c] = as_bf8(*(const u32x4*)(a.dh + qrow * a.lddo + col));
+    dlf[c] = as_bf8(*(const u32x4*)(a.dl + qrow * a.lddo + col));
   }
-  dpart += __shfl_xor(dpart, 16, 64);
-  dpart += __shfl_xor(dpart, 32, 64);
-  const float delta = dpart;
+  const float delta = a.delta_t[(long)h * a.ldt + qrow];
   const float lse2 = a.lse_in_t[(long)h * a.ldt + qrow] * LOG2E;
-  if (g == 0) a.delta_t[(long)h * a.ldt + qrow] = delta;
 
   const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
   const bf16_t* vsrc = ksrc + a.HK * DH;
@@ -444,14 +432,12 @@ __global__ __launch_bounds__(256) void k_attn2_dq(TArgs a) {
 // holds the query block's Q and dO planes in row orientation only: the
 // products that need them transposed (dV^T = dO^T P, dK^T = Q^T dS) read
 // their fragments with LDS transpose reads.
-__global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NST x [Q | dOh | dOl | LSE,Delta]
+__device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, int h, int b) {
+  // lds: NST x [Q | dOh | dOl | LSE,Delta]
   constexpr int SROW = 3 * TILE + 512;  // stage size in bf16 elements (+1 KB of LSE / Delta)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
-  const int kb = blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
   const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
   const int group = a.HQ / a.HK;
   const int kvh = h / group, gi = h % group;
@@ -554,7 +540,7 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
     }
   }
   // lane holds dK^T / dV^T [16d + 4g + r][key]: 4 consecutive columns of the partial row
-  const long M = (long)T * gridDim.z;
+  const long M = (long)T * a.B;
   float* prow_ = a.part + ((long)gi * M + krow) * 2 * NK + kvh * DH;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
@@ -563,11 +549,58 @@ __global__ __launch_bounds__(256) void k_attn2_dkv(TArgs a) {
   }
 }
 
+// Delta = sum over the head's 64 columns of dO * O (dO = hi + lo), per
+// (row, query head) into delta_t [HQ][ldt] (hierarchy.py:42-70 computes it
+// in the dQ kernel; here it comes first so dQ and dK/dV are independent).
+// Four lanes per (row, head), 16 columns each, summed (l0 + l1) + (l2 + l3).
+__global__ __launch_bounds__(256) void k_attn_delta(TArgs a) {
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long M = (long)a.T * a.B;
+  const int g = (int)(t & 3);
+  const long rh = t >> 2;
+  const bool ok = rh < M * a.HQ;
+  const long row = ok ? rh / a.HQ : 0;
+  const int h = ok ? (int)(rh % a.HQ) : 0;
+  float dpart = 0.f;
+  if (ok) {
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int col = h * DH + 32 * c + 8 * g;
+      const u32x4 hv = *(const u32x4*)(a.dh + row * a.lddo + col);
+      const u32x4 lv = *(const u32x4*)(a.dl + row * a.lddo + col);
+      const u32x4 ov = *(const u32x4*)(a.ob + row * a.ldo + col);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        dpart += (bflo(hv[i]) + bflo(lv[i])) * bflo(ov[i]);
+        dpart += (bfhi(hv[i]) + bfhi(lv[i])) * bfhi(ov[i]);
+      }
+    }
+  }
+  dpart += __shfl_xor(dpart, 1, 64);
+  dpart += __shfl_xor(dpart, 2, 64);
+  if (ok && g == 0) a.delta_t[(long)h * a.ldt + row] = dpart;
+}
+
+// dQ and dK/dV in one launch (they share only Delta): grid.x = 2 T/64;
+// x < T/64 is the dQ of query block T/64 - 1 - x (longest first), the rest
+// the dK/dV of key block x - T/64 (longest first).  Both roles keep several
+// latency-bound workgroups per CU busy.
+__global__ __launch_bounds__(256) void k_attn2_bwd(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  const int nb = (int)(gridDim.x >> 1), x = (int)blockIdx.x;
+  if (x < nb)
+    attn2_dq<NS_DQ>(a, lds, nb - 1 - x, blockIdx.y, blockIdx.z);
+  else
+    attn2_dkv(a, lds, x - nb, blockIdx.y, blockIdx.z);
+}
+
 constexpr size_t LDS_FWD = (size_t)NS_FWD * 2 * TBYTES;
 constexpr size_t LDS_DQ = (size_t)NS_DQ * 2 * TBYTES;
 static_assert(NS_FWD >= 2 && NS_DQ >= 2 && LDS_FWD <= 160 * 1024 && LDS_DQ <= 160 * 1024, "LDS budget");
 static_assert((NS_FWD - 2) * 4 < 64 && (NS_DQ - 2) * 4 < 64, "vmcnt range");
 constexpr size_t LDS_DKV = (size_t)NST * (3 * TBYTES + 1024);
+constexpr size_t LDS_BWD = LDS_DQ > LDS_DKV ? LDS_DQ : LDS_DKV;
+static_assert(LDS_BWD <= 160 * 1024, "LDS budget");
 static_assert(LDS_DKV <= 160 * 1024, "LDS budget");
 
 }  // namespace
@@ -578,9 +611,7 @@ int sjh::attention_t_prepare() {
   done = 1;
   hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd<NS_FWD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
   if (e == hipSuccess)
-    e = hipFuncSetAttribute((const void*)k_attn2_dq<NS_DQ>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute((const void*)k_attn2_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
+    e = hipFuncSetAttribute((const void*)k_attn2_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BWD);
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
   return status;
 }
@@ -641,14 +672,16 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   a.gq[0] = (bf16_t*)g_hi; a.gq[1] = (bf16_t*)g_lo; a.gqt[0] = (bf16_t*)g_t_hi; a.gqt[1] = (bf16_t*)g_t_lo;
   a.ldg = ldg; a.ldgt = ldgt;
   a.part = (float*)workspace;
-  const dim3 grid((unsigned)(t / QB), (unsigned)hq, (unsigned)batch);
-  if (parts & 1) {
-    hipLaunchKernelGGL(k_attn2_dq<NS_DQ>, grid, dim3(256), LDS_DQ, s, a);
-    SJ_LAUNCH_CHECK("hierarchy_attention_dq");
+  a.B = (int)batch;
+  if (parts & 1) {  // Delta
+    const long threads = 4 * batch * t * hq;
+    hipLaunchKernelGGL(k_attn_delta, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
+    SJ_LAUNCH_CHECK("hierarchy_attention_delta");
   }
-  if (parts & 2) {
-    hipLaunchKernelGGL(k_attn2_dkv, grid, dim3(256), LDS_DKV, s, a);
-    SJ_LAUNCH_CHECK("hierarchy_attention_dkv");
+  if (parts & 2) {  // dQ | dK dV
+    hipLaunchKernelGGL(k_attn2_bwd, dim3((unsigned)(2 * (t / QB)), (unsigned)hq, (unsigned)batch), dim3(256), LDS_BWD,
+                       s, a);
+    SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv");
   }
   if (parts & 4) {
     const long M = batch * t;

@@ -787,7 +787,9 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       TRY(read(KX, p));
       TRY(reuse(KQ, p));
       for (int part = 1; part <= 4; part <<= 1) {
-        const char* nm = part == 1 ? "attention_bwd_dq" : part == 2 ? "attention_bwd_dkv" : "attention_bwd_kv_reduce";
+        const char* nm = part == 4   ? "attention_bwd_kv_reduce"
+                         : S.attn_tt ? (part == 1 ? "attention_bwd_delta" : "attention_bwd_dq_dkv")
+                                     : (part == 1 ? "attention_bwd_dq" : "attention_bwd_dkv");
         if (S.attn_tt)
           OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, ldt, (const uint16_t*)m->o[l], d, m->lset[l],
                                              m->dop[0], m->dop[1], d, m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh,
