@@ -370,12 +370,78 @@ extern "C" int sj_embedding_fwd(void* stream, const void* w, int wd, const int32
 
 extern "C" size_t sj_embedding_bwd_workspace_bytes(long n, long vocab) { return 0; }
 
+// Faster form for d % 4 == 0, d <= 2048: each round scans 16 ids per thread
+// (4096 tokens), compacts the matches in token order with one block scan,
+// then every thread adds up to two float4 columns of the matching rows in
+// that order (the same order, hence the same bits, as k_embedding_bwd).
+constexpr int EMB_IDS = 16;
+__global__ __launch_bounds__(EMB_THREADS) void k_embedding_bwd4(const float* __restrict__ dy,
+                                                                const int32_t* __restrict__ ids,
+                                                                float* __restrict__ dw, long n, long d) {
+  __shared__ int matches[EMB_THREADS * EMB_IDS];
+  __shared__ int wave_total[EMB_THREADS / 64];
+  const int v = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const long d4 = d >> 2;
+  float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  for (long base = 0; base < n; base += (long)EMB_THREADS * EMB_IDS) {
+    const long i0 = base + (long)t * EMB_IDS;
+    uint32_t hit = 0;
+#pragma unroll
+    for (int k = 0; k < EMB_IDS; k++)
+      if (i0 + k < n && ids[i0 + k] == v) hit |= 1u << k;
+    const int cnt = __popc(hit);
+    int incl = cnt;  // inclusive scan over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wave_total[w] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int j = 0; j < EMB_THREADS / 64; j++) {
+      if (j < w) before += wave_total[j];
+      total += wave_total[j];
+    }
+    int pos = before + incl - cnt;
+    while (hit) {
+      const int k = __ffs(hit) - 1;
+      hit &= hit - 1;
+      matches[pos++] = (int)(i0 + k);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const long col = t + (long)c * EMB_THREADS;
+      if (col < d4) {
+        const float4* src = (const float4*)dy + col;
+        for (int m = 0; m < total; m++) {
+          const float4 r = src[(long)matches[m] * d4];
+          acc[c].x += r.x; acc[c].y += r.y; acc[c].z += r.z; acc[c].w += r.w;
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    const long col = t + (long)c * EMB_THREADS;
+    if (col < d4) ((float4*)(dw + (long)v * d))[col] = acc[c];
+  }
+}
+
 extern "C" int sj_embedding_bwd(void* stream, const float* dy, const int32_t* ids, float* dw, long n, long d,
                                 long vocab, void* workspace, size_t workspace_bytes) {
   SJ_REQUIRE(n >= 0 && d > 0 && d <= 8 * EMB_THREADS && vocab > 0, "embedding_backward: n %ld d %ld vocab %ld", n,
              d, vocab);
-  hipLaunchKernelGGL(k_embedding_bwd, dim3((unsigned)vocab), dim3(EMB_THREADS), 0, (hipStream_t)stream, dy, ids, dw,
-                     n, d);
+  if (d % 4 == 0 && d <= 8 * EMB_THREADS && ((uintptr_t)dy & 15) == 0 && ((uintptr_t)dw & 15) == 0)
+    hipLaunchKernelGGL(k_embedding_bwd4, dim3((unsigned)vocab), dim3(EMB_THREADS), 0, (hipStream_t)stream, dy, ids, dw,
+                       n, d);
+  else
+    hipLaunchKernelGGL(k_embedding_bwd, dim3((unsigned)vocab), dim3(EMB_THREADS), 0, (hipStream_t)stream, dy, ids, dw,
+                       n, d);
   SJ_LAUNCH_CHECK("embedding_backward");
   return SJ_OK;
 }

@@ -248,6 +248,26 @@ def test_embedding_forward_backward(api):
     assert rel(dW.host(), O.embedding_bwd(dy, ids, V)) < 1e-6
 
 
+@pytest.mark.parametrize("V,D,Nn,same", [(257, 384, 9000, False), (257, 64, 5000, True), (259, 130, 700, False),
+                                         (257, 1024, 4096, False)])
+def test_embedding_backward_token_order(api, V, D, Nn, same):
+    """The embedding backward sums each row's tokens in token order in fp32
+    (deterministic; bit-equal to that sequential sum): several 4096-token
+    scan rounds, every token on one id (4096 matches in a round), a width
+    that is not a multiple of 4 (the per-column kernel)."""
+    rng = np.random.default_rng(V + D + Nn)
+    ids = (np.full(Nn, 7) if same else rng.integers(0, V, Nn)).astype(np.int32)
+    dy = rng.normal(0, 1, (Nn, D)).astype(np.float32)
+    dW = dev(np.full(V * D, 7.0))
+    print(f"[embedding_bwd] V={V} D={D} N={Nn} same={same}", flush=True)
+    api.sj_embedding_bwd(None, dev(dy.astype(np.float64)).p, dev(ids, "i32").p, dW.p, Nn, D, V, None, 0)
+    sync()
+    ref = np.zeros((V, D), np.float32)
+    for i in range(Nn):
+        ref[ids[i]] += dy[i]
+    np.testing.assert_array_equal(dW.host().reshape(V, D).astype(np.float32), ref)
+
+
 def test_sum_squares_and_adamw(api, lib):
     rng = np.random.default_rng(9)
     n = 1_000_003
