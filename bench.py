@@ -228,6 +228,18 @@ def _hier_name(name, mc):
             f"GQA {mc.heads}/{mc.kv} SwiGLU {mc.ffn_width} over {h.patch_size}-byte patches, ")
 
 
+def cpu_sample_batch(mc, tc) -> int:
+    """Sequences of the CPU baseline sample, sized for about 6-24 s of FP64
+    work on the GPU box's 16 host threads (measured: cfg2 0.93 s per
+    sequence, cfg3 1.6 s, cfg4 0.8 s, cfg5 24 s): the whole batch for cfg2
+    and cfg4, 6 sequences of cfg3, 1 at width >= 1024 (cfg5)."""
+    if mc.hierarchy is not None:
+        return 6
+    if mc.width >= 1024:
+        return 1
+    return tc.batch
+
+
 def cpu_baseline(mc, tc, sample_batch: int):
     """FP64 oracle (OpenMP over all host threads) on `sample_batch`
     sequences of the same workload: forward + backward + AdamW."""
@@ -612,7 +624,7 @@ def main():
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=0,
-                    help="sequences the CPU baseline runs (default 2; 1 for the hierarchical and MoE models)")
+                    help="sequences the CPU baseline runs (default: cpu_sample_batch, about 10 s of FP64 work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
     ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
@@ -714,8 +726,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (FP64 oracle) ...")
-        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch or
-                           (1 if mc.hierarchy is not None or getattr(mc, "experts", None) is not None else 2))
+        cpu = cpu_baseline(mc, tc, args.cpu_sample_batch or cpu_sample_batch(mc, tc))
         log(f"[bench] cpu baseline {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
 
     out = {

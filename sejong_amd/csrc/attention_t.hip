@@ -594,6 +594,19 @@ __global__ __launch_bounds__(256) void k_attn2_bwd(TArgs a) {
     attn2_dkv(a, lds, x - nb, blockIdx.y, blockIdx.z);
 }
 
+// The same roles as separate launches: with thousands of workgroups per role
+// (cfg5: 4096) each kernel fills the chip alone, and the dQ role keeps its
+// smaller LDS and register footprint (more workgroups per CU).
+__global__ __launch_bounds__(256) void k_attn2_bwd_dq(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - (int)blockIdx.x, blockIdx.y, blockIdx.z);
+}
+__global__ __launch_bounds__(256) void k_attn2_bwd_dkv(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  attn2_dkv(a, lds, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+constexpr long SEPARATE_ROLES = 2048;  // workgroups per role from which the roles launch separately
+
 constexpr size_t LDS_FWD = (size_t)NS_FWD * 2 * TBYTES;
 constexpr size_t LDS_DQ = (size_t)NS_DQ * 2 * TBYTES;
 static_assert(NS_FWD >= 2 && NS_DQ >= 2 && LDS_FWD <= 160 * 1024 && LDS_DQ <= 160 * 1024, "LDS budget");
@@ -612,6 +625,10 @@ int sjh::attention_t_prepare() {
   hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd<NS_FWD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BWD);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_bwd_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_bwd_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
   return status;
 }
@@ -679,8 +696,15 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
     SJ_LAUNCH_CHECK("hierarchy_attention_delta");
   }
   if (parts & 2) {  // dQ | dK dV
-    hipLaunchKernelGGL(k_attn2_bwd, dim3((unsigned)(2 * (t / QB)), (unsigned)hq, (unsigned)batch), dim3(256), LDS_BWD,
-                       s, a);
+    const long nb = t / QB;
+    if (nb * hq * batch >= SEPARATE_ROLES) {
+      const dim3 grid((unsigned)nb, (unsigned)hq, (unsigned)batch);
+      hipLaunchKernelGGL(k_attn2_bwd_dq, grid, dim3(256), LDS_DQ, s, a);
+      hipLaunchKernelGGL(k_attn2_bwd_dkv, grid, dim3(256), LDS_DKV, s, a);
+    } else {
+      hipLaunchKernelGGL(k_attn2_bwd, dim3((unsigned)(2 * nb), (unsigned)hq, (unsigned)batch), dim3(256), LDS_BWD, s,
+                         a);
+    }
     SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv");
   }
   if (parts & 4) {
