@@ -382,8 +382,8 @@ int sj_moe_combine(void *stream, const uint16_t *yp, long ldy, long d, const int
                    uint16_t *out, long ldo);
 /* Engine::expert_combine_backward, hierarchy_ops.rs:416-454
  * (hierarchy.py:238-251): dx[row] = dy[token] * w[slot] as hi/lo planes,
- * normal [capacity][d] and transposed [d][ldt], and dweights[slot] =
- * sum_c y[row][c] dy[token][c].  d <= 1024. */
+ * normal [capacity][d] and transposed [d][ldt] (nullable, both or neither),
+ * and dweights[slot] = sum_c y[row][c] dy[token][c].  d <= 1024. */
 int sj_moe_combine_bwd(void *stream, const uint16_t *yp, long ldy, long d, const int32_t *pslot,
                        const float *weights, long top_k, long capacity, const float *dy, long lddy,
                        uint16_t *dx_hi, uint16_t *dx_lo, uint16_t *dx_t_hi, uint16_t *dx_t_lo, long ldt,
@@ -420,6 +420,13 @@ int sj_moe_down_bwd_swiglu_p(void *stream, const int32_t *offsets, long experts,
 int sj_moe_gemm_rows(void *stream, const int32_t *offsets, long experts, long capacity, long N, long K,
                      const uint16_t *a_hi, const uint16_t *a_lo, long lda, const uint16_t *b, long ldb,
                      long b_stride, float *c, long ldc, int accumulate);
+/* The per-expert dW from row-layout operands (no transposed copies): C_e
+ * (+ e*c_stride) [M][N] = X_e^T Y_e over expert e's packed rows, X
+ * [capacity][ldx] (M columns: packed h or expert inputs), Y [capacity][ldy]
+ * (N columns, hi/lo gradient planes).  M, N, ldx, ldy multiples of 8. */
+int sj_moe_gemm_dw_tn(void *stream, const int32_t *offsets, long experts, long capacity, long M, long N,
+                      const uint16_t *x, long ldx, const uint16_t *y_hi, const uint16_t *y_lo, long ldy, float *c,
+                      long ldc, long c_stride);
 int sj_moe_gemm_dw(void *stream, const int32_t *offsets, long experts, long capacity, long M, long N,
                    const uint16_t *a, long lda, const uint16_t *b_hi, const uint16_t *b_lo, long ldb, float *c,
                    long ldc, long c_stride);

@@ -1199,9 +1199,10 @@ extern "C" int sj_moe_down_bwd_swiglu_p(void* stream, const int32_t* offsets, lo
                                         uint16_t* dgu_t_hi, uint16_t* dgu_t_lo, long ldt) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
   SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && D > 0 && D % 8 == 0 && lddy % 8 == 0 && ldw % 8 == 0 &&
-                 lddy >= D && ldw >= D && ldgu >= F && lddgu >= 2 * F && ldt >= capacity && ldt % 4 == 0 &&
-                 w_stride % 8 == 0 && ok16(dy_hi) && ok16(dy_lo) && ok16(w_down),
-             "expert swiglu_backward: shape/alignment");
+                 lddy >= D && ldw >= D && ldgu >= F && lddgu >= 2 * F && !dgu_t_hi == !dgu_t_lo &&
+                 (!dgu_t_hi || (ldt >= capacity && ldt % 4 == 0)) && w_stride % 8 == 0 && ok16(dy_hi) &&
+                 ok16(dy_lo) && ok16(w_down),
+             "expert swiglu_backward: shape/alignment (transposed outputs both or neither)");
   FParams p = {};
   p.a[0] = (const bf16_t*)dy_hi; p.a[1] = (const bf16_t*)dy_lo; p.lda = lddy;
   p.b[0][0] = (const bf16_t*)w_down; p.ldb[0] = ldw; p.seg_n[0] = 0; p.nseg = 1;
@@ -1232,6 +1233,31 @@ extern "C" int sj_moe_gemm_rows(void* stream, const int32_t* offsets, long exper
   int st = launch_planes<E_STORE>((hipStream_t)stream, p, a_lo ? 2 : 1, 1, 64, grouped_bn(capacity, N), 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("expert matmul (rows)");
+  return SJ_OK;
+}
+
+// Per-expert dW from row-layout operands: C_e (+ e * c_stride) [M][N] =
+// X_e^T Y_e over expert e's packed rows [offsets[e], offsets[e+1]) with
+// X [capacity][ldx] (M columns) and Y [capacity][ldy] (N columns, hi/lo).
+extern "C" int sj_moe_gemm_dw_tn(void* stream, const int32_t* offsets, long experts, long capacity, long M, long N,
+                                 const uint16_t* x, long ldx, const uint16_t* y_hi, const uint16_t* y_lo, long ldy,
+                                 float* c, long ldc, long c_stride) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(grouped_ok(offsets, experts, capacity) && experts <= 65535 && M > 0 && N > 0 && M % 8 == 0 &&
+                 N % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && ldx >= M && ldy >= N && ldc >= N && ok16(x) &&
+                 ok16(y_hi) && (!y_lo || ok16(y_lo)),
+             "expert matmul (dW, row-layout operands): shape/alignment");
+  FParams p = {};
+  p.a[0] = (const bf16_t*)x; p.lda = ldx;
+  p.b[0][0] = (const bf16_t*)y_hi; p.b[1][0] = (const bf16_t*)y_lo; p.ldb[0] = ldy; p.seg_n[0] = 0; p.nseg = 1;
+  p.c[0] = c; p.ldc[0] = ldc;
+  p.M = M; p.N = N; p.K = capacity;
+  p.goff = offsets; p.gE = (int)experts; p.gmode = 2; p.gstride_c = c_stride;
+  int bm, bn;
+  pick(M * experts, N, bm, bn);
+  int st = launch_planes<E_STORE, 3>((hipStream_t)stream, p, 1, y_lo ? 2 : 1, bm, bn, (int)experts);
+  if (st) return st;
+  SJ_LAUNCH_CHECK("expert matmul (dW, row layout)");
   return SJ_OK;
 }
 

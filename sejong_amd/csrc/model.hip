@@ -521,9 +521,9 @@ int stage_forward(sj_model* m, int si) {
       OP("router_topk", sj_router_topk(s, z2, d, W + y.router, d, M, E, K, m->mlog[l], m->mids[l], m->mwts[l]));
       OP("route_pack", sj_route_pack(s, m->mids[l], M, K, E, nullptr, nullptr, m->mcnt[l], m->moff[l], m->mps[l],
                                      m->mpp[l], cap));
-      OP("moe_gather", sj_moe_gather(s, z2, d, d, m->mps[l], K, cap, m->mzp[l], m->mzpt[l], cap));
+      OP("moe_gather", sj_moe_gather(s, z2, d, d, m->mps[l], K, cap, m->mzp[l], m->rowdw ? nullptr : m->mzpt[l], cap));
       OP("expert_gate_up", sj_moe_gate_up_fwd(s, m->moff[l], E, cap, m->mzp[l], d, d, WT + y.gu, WT + y.gu + F * d, d,
-                                              2 * F * d, F, gg, uu, hh, F, m->ht[l], cap));
+                                              2 * F * d, F, gg, uu, hh, F, m->rowdw ? nullptr : m->ht[l], cap));
       OP("expert_down", sj_moe_down_fwd(s, m->moff[l], E, cap, hh, F, F, WT + y.down, F, d * F, d, m->myp[l], d));
       OP("combine_residual", sj_moe_combine(s, m->myp[l], d, d, m->mids[l], m->mpp[l], m->mwts[l], M, K, x1, d,
                                             (uint16_t*)xout(m, l), d));
@@ -717,21 +717,30 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         uint16_t* mg[4] = {m->mdg[0][l], m->mdg[1][l], m->mdg[2][l], m->mdg[3][l]};
         TRY(read(KR, p));  // the rp transposed planes go unread here
         OP("combine_bwd", sj_moe_combine_bwd(s, m->myp[l], d, d, m->mps[l], m->mwts[l], K, cap, m->dres[cur], d, mx[0],
-                                             mx[1], mx[2], mx[3], cap, m->mdwts[l]));
+                                             mx[1], rdw ? nullptr : mx[2], rdw ? nullptr : mx[3], cap,
+                                             m->mdwts[l]));
         OP("expert_down_dx_swiglu", sj_moe_down_bwd_swiglu_p(s, m->moff[l], E, cap, mx[0], mx[1], d, d, W + y.down, d,
                                                              F * d, F, (const uint16_t*)m->gg[l],
-                                                             (const uint16_t*)m->uu[l], F, mg[0], mg[1], 2 * F, mg[2],
-                                                             mg[3], cap));
+                                                             (const uint16_t*)m->uu[l], F, mg[0], mg[1], 2 * F,
+                                                             rdw ? nullptr : mg[2], rdw ? nullptr : mg[3], cap));
         if (two) {
           SJ_HIP(hipEventRecord(m->ev_moe[0][l], s));
           SJ_HIP(hipStreamWaitEvent(s2, m->ev_moe[0][l], 0));
         }
-        OP("expert_down_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, F, d, m->ht[l], cap, mx[2], mx[3], cap, G + y.down,
-                                            d, F * d));
+        if (rdw)
+          OP("expert_down_dw", sj_moe_gemm_dw_tn(s2, m->moff[l], E, cap, F, d, (const uint16_t*)m->hh[l], F, mx[0],
+                                                 mx[1], d, G + y.down, d, F * d));
+        else
+          OP("expert_down_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, F, d, m->ht[l], cap, mx[2], mx[3], cap,
+                                              G + y.down, d, F * d));
         OP("expert_gate_up_dx", sj_moe_gemm_rows(s, m->moff[l], E, cap, d, 2 * F, mg[0], mg[1], 2 * F, W + y.gu, 2 * F,
                                                  d * 2 * F, m->mdzp, d, 0));
-        OP("expert_gate_up_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, d, 2 * F, m->mzpt[l], cap, mg[2], mg[3], cap,
-                                               G + y.gu, 2 * F, d * 2 * F));
+        if (rdw)
+          OP("expert_gate_up_dw", sj_moe_gemm_dw_tn(s2, m->moff[l], E, cap, d, 2 * F, m->mzp[l], d, mg[0], mg[1],
+                                                    2 * F, G + y.gu, 2 * F, d * 2 * F));
+        else
+          OP("expert_gate_up_dw", sj_moe_gemm_dw(s2, m->moff[l], E, cap, d, 2 * F, m->mzpt[l], cap, mg[2], mg[3],
+                                                 cap, G + y.gu, 2 * F, d * 2 * F));
         OP("gather_route_bwd", sj_moe_gather_bwd(s, m->mdzp, d, d, m->mids[l], m->mpp[l], m->mwts[l], m->mlog[l],
                                                  m->mdwts[l], W + y.router, M, K, E, nullptr, d, m->dz, d,
                                                  m->mdlog[l]));

@@ -106,6 +106,64 @@ __global__ __launch_bounds__(NT) void k_router_topk(const bf16_t* __restrict__ z
   }
 }
 
+// The same with 16-byte loads (d % 8 == 0, E % 8 == 0, aligned rows): lane
+// l accumulates columns 8l .. 8l+7 (+ 512 i) for every expert from one z
+// chunk and the matching E-wide rows of W_r, then the wave sums.
+__global__ __launch_bounds__(NT) void k_router_topk8(const bf16_t* __restrict__ z, long ldz,
+                                                     const bf16_t* __restrict__ wr, long d, long R, int E, int K,
+                                                     bf16_t* __restrict__ logits, int32_t* __restrict__ ids,
+                                                     float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const long r = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (r >= R) return;
+  float acc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) acc[e] = 0.f;
+  for (long c8 = 8L * lane; c8 < d; c8 += 512) {
+    const u32x4 zv = *(const u32x4*)(z + r * ldz + c8);
+    float zf[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      zf[2 * i] = __uint_as_float(zv[i] << 16);
+      zf[2 * i + 1] = __uint_as_float(zv[i] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const bf16_t* wrow = wr + (c8 + i) * E;
+#pragma unroll
+      for (int e8 = 0; e8 < EMAX; e8 += 8) {
+        if (e8 >= E) break;
+        const u32x4 wv = *(const u32x4*)(wrow + e8);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          acc[e8 + 2 * q] += zf[i] * __uint_as_float(wv[q] << 16);
+          acc[e8 + 2 * q + 1] += zf[i] * __uint_as_float(wv[q] & 0xffff0000u);
+        }
+      }
+    }
+  }
+  float sc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) {
+    sc[e] = 0.f;
+    if (e < E) sc[e] = round_bf(wave_sum(acc[e]));
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int e = 0; e < EMAX; e++)
+      if (e < E) logits[r * E + e] = f2bf(sc[e]);
+    int32_t id[KMAX];
+    float w[KMAX];
+    topk_rows(sc, E, K, id, w);
+#pragma unroll
+    for (int k = 0; k < KMAX; k++)
+      if (k < K) {
+        ids[r * K + k] = id[k];
+        weights[r * K + k] = w[k];
+      }
+  }
+}
+
 // routing from stored logits (Engine::route_topk), one thread per row
 __global__ __launch_bounds__(NT) void k_route_topk(const void* __restrict__ x, int xd, long R, int E, int K,
                                                    int32_t* __restrict__ ids, float* __restrict__ weights) {
@@ -250,6 +308,128 @@ __global__ __launch_bounds__(NT) void k_route_pack(const int32_t* __restrict__ i
   for (long i = off[E] + t; i < cap; i += NT) pslot[i] = -1;
 }
 
+// The same packing with 1024 threads: each owns a run of ceil(S/1024)
+// slots, counts its experts in registers, and one block scan of the counts
+// (two experts per 64-bit word) gives every slot its stable rank.
+constexpr int PNT = 1024;
+__device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_up((uint32_t)v, o, 64), hi = __shfl_up((uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+template <int EP>  // 64-bit count words (two experts each), E <= 2 EP
+__global__ __launch_bounds__(PNT) void k_route_pack_wide(const int32_t* __restrict__ ids, long S, int K, int E, long cap,
+                                                         int32_t* __restrict__ tokens, int32_t* __restrict__ slots,
+                                                         int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ pslot, int32_t* __restrict__ ppos) {
+  constexpr int NW = PNT / 64, EM = 2 * EP;
+  __shared__ uint64_t wsum[NW][EP];
+  __shared__ int tot[EMAX], off[EMAX + 1];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const long per = (S + PNT - 1) / PNT;
+  const long s0 = t * per, s1 = s0 + per < S ? s0 + per : S;
+  const int EH = (E + 1) / 2;
+  // up to 8 of the thread's ids are loaded together and kept for the
+  // placement pass (S <= 8192 at one load round)
+  constexpr int IB = 8;
+  int eid[IB];
+  const bool held = per <= IB;
+#pragma unroll
+  for (int i = 0; i < IB; i++) eid[i] = held && s0 + i < s1 ? ids[s0 + i] : -1;
+  uint64_t pc[EP];
+#pragma unroll
+  for (int j = 0; j < EP; j++) pc[j] = 0;
+  for (long s = s0; s < s1; s++) {
+    int e = 0;
+    if (held) {
+#pragma unroll
+      for (int i = 0; i < IB; i++)
+        if (s - s0 == i) e = eid[i];
+    } else {
+      e = ids[s];
+    }
+#pragma unroll
+    for (int j = 0; j < EP; j++)
+      if (j < EH) pc[j] += (uint64_t)(e == 2 * j) | ((uint64_t)(e == 2 * j + 1) << 32);
+  }
+  // inclusive scan over the wave, then the waves' totals
+  uint64_t incl[EP];
+#pragma unroll
+  for (int j = 0; j < EP; j++) {
+    incl[j] = pc[j];
+    if (j >= EH) continue;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t y = shfl_up64(incl[j], o);
+      if (lane >= o) incl[j] += y;
+    }
+    if (lane == 63) wsum[wv][j] = incl[j];
+  }
+  __syncthreads();
+  uint64_t before[EP];
+#pragma unroll
+  for (int j = 0; j < EP; j++) {
+    before[j] = 0;
+    if (j >= EH) continue;
+    uint64_t all = 0;
+    for (int w = 0; w < NW; w++) {
+      const uint64_t v = wsum[w][j];
+      if (w < wv) before[j] += v;
+      all += v;
+    }
+    if (t == 0) {
+      tot[2 * j] = (int)(uint32_t)all;
+      if (2 * j + 1 < E) tot[2 * j + 1] = (int)(all >> 32);
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    int o = 0;
+    for (int e = 0; e < E; e++) {
+      off[e] = o;
+      o += (tot[e] + SEG - 1) / SEG * SEG;
+    }
+    off[E] = o;
+  }
+  __syncthreads();
+  if (t <= E) offsets[t] = off[t];
+  if (t < E && counts) counts[t] = tot[t];
+  int rank[EM];  // this thread's next rank per expert
+#pragma unroll
+  for (int j = 0; j < EP; j++) {
+    const uint64_t ex = before[j] + incl[j] - pc[j];
+    rank[2 * j] = (int)(uint32_t)ex;
+    rank[2 * j + 1] = (int)(ex >> 32);
+  }
+  for (long s = s0; s < s1; s++) {
+    int e = 0;
+    if (held) {
+#pragma unroll
+      for (int i = 0; i < IB; i++)
+        if (s - s0 == i) e = eid[i];
+    } else {
+      e = ids[s];
+    }
+    if (e < 0 || e >= E) {
+      ppos[s] = -1;
+      continue;
+    }
+    int rk = 0;
+#pragma unroll
+    for (int q = 0; q < EM; q++)
+      if (q == e) rk = rank[q]++;
+    const int pos = off[e] + rk;
+    pslot[pos] = (int32_t)s;
+    ppos[s] = pos;
+    if (tokens) tokens[(long)e * S + rk] = (int32_t)(s / K);
+    if (slots) slots[(long)e * S + rk] = (int32_t)s;
+  }
+  for (int e = 0; e < E; e++) {
+    const long i = off[e] + tot[e] + t;
+    if (t < SEG && i < off[e + 1]) pslot[i] = -1;
+  }
+  for (long i = off[E] + t; i < cap; i += PNT) pslot[i] = -1;
+}
+
 // packed rows: y[p] = x[token of pslot[p]] (zero for padding), plus y^T
 // [d][ldt] staged through LDS in blocks of TR rows (d <= 1024)
 constexpr int TR = 32;
@@ -390,6 +570,7 @@ __global__ __launch_bounds__(NT) void k_moe_combine_bwd(const bf16_t* __restrict
     dot = wave_sum(dot);
     if (lane == 0 && s >= 0) dw[s] = dot;
   }
+  if (!hit) return;  // no transposed planes (uniform over the block)
   __syncthreads();
   for (long q = threadIdx.x; q < 2 * d * (TRB / 8); q += NT) {
     const int plane = q >= d * (TRB / 8);
@@ -464,6 +645,87 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd(const float* __restrict__
   }
 }
 
+// k_moe_gather_bwd with 8 consecutive columns per lane per step (16-byte
+// loads and stores; d % 8 == 0, E % 8 == 0, row strides multiples of 4):
+// every column's arithmetic is the same as above, in the same order.
+__global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict__ dxp, long lddx, long d,
+                                                        const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
+                                                        const float* __restrict__ weights,
+                                                        const bf16_t* __restrict__ logits,
+                                                        const float* __restrict__ dweights,
+                                                        const bf16_t* __restrict__ wr, long R, int K, int E,
+                                                        const float* __restrict__ acc, long ldacc,
+                                                        float* __restrict__ dz, long lddz,
+                                                        float* __restrict__ dlogits) {
+  const int lane = threadIdx.x & 63;
+  const long t = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (t >= R) return;
+  float dl[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) dl[e] = 0.f;
+  if (logits) {
+    float lg[EMAX], w[KMAX], g[KMAX];
+    int32_t id[KMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; e++) lg[e] = e < E ? bf2f(logits[t * E + e]) : 0.f;
+#pragma unroll
+    for (int k = 0; k < KMAX; k++) {
+      id[k] = k < K ? ids[t * K + k] : -1;
+      w[k] = k < K ? weights[t * K + k] : 0.f;
+      g[k] = k < K ? dweights[t * K + k] : 0.f;
+    }
+    route_bwd_row(lg, E, K, id, w, g, dl);
+    if (lane < E) {
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < EMAX; e++)
+        if (e == lane) v = dl[e];
+      dlogits[t * E + lane] = v;
+    }
+  }
+  int pos[KMAX];
+  float unused[KMAX];
+  const int n = token_routes(t, K, ids, ppos, nullptr, pos, unused);
+  for (long c8 = 8L * lane; c8 < d; c8 += 512) {
+    float s[8], ex[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] = ex[i] = 0.f;
+    if (acc) {
+      const float4 a0 = *(const float4*)(acc + t * ldacc + c8), a1 = *(const float4*)(acc + t * ldacc + c8 + 4);
+      s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
+    }
+#pragma unroll
+    for (int j = 0; j < KMAX; j++)
+      if (j < n) {
+        const float4 x0 = *(const float4*)(dxp + pos[j] * lddx + c8), x1 = *(const float4*)(dxp + pos[j] * lddx + c8 + 4);
+        ex[0] += x0.x; ex[1] += x0.y; ex[2] += x0.z; ex[3] += x0.w;
+        ex[4] += x1.x; ex[5] += x1.y; ex[6] += x1.z; ex[7] += x1.w;
+      }
+#pragma unroll
+    for (int i = 0; i < 8; i++) s[i] += ex[i];
+    if (logits && wr) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const bf16_t* wrow = wr + (c8 + i) * E;
+        float r = 0.f;
+#pragma unroll
+        for (int e8 = 0; e8 < EMAX; e8 += 8) {
+          if (e8 >= E) break;
+          const u32x4 wv = *(const u32x4*)(wrow + e8);
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            r += dl[e8 + 2 * q] * __uint_as_float(wv[q] << 16);
+            r += dl[e8 + 2 * q + 1] * __uint_as_float(wv[q] & 0xffff0000u);
+          }
+        }
+        s[i] += r;
+      }
+    }
+    *(float4*)(dz + t * lddz + c8) = make_float4(s[0], s[1], s[2], s[3]);
+    *(float4*)(dz + t * lddz + c8 + 4) = make_float4(s[4], s[5], s[6], s[7]);
+  }
+}
+
 }  // namespace
 
 // ================================================================ C ABI
@@ -479,9 +741,11 @@ extern "C" int sj_router_topk(void* stream, const uint16_t* z, long ldz, const u
                  top_k <= experts && logits && ids && weights,
              "router top-k dimensions (experts <= %d, top_k <= %d)", EMAX, KMAX);
   if (rows == 0) return SJ_OK;
-  hipLaunchKernelGGL(k_router_topk, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream,
-                     (const bf16_t*)z, ldz, (const bf16_t*)w_router, d, rows, (int)experts, (int)top_k,
-                     (bf16_t*)logits, ids, weights);
+  const bool vec = d % 8 == 0 && ldz % 8 == 0 && experts % 8 == 0 && ((uintptr_t)z & 15) == 0 &&
+                   ((uintptr_t)w_router & 15) == 0;
+  hipLaunchKernelGGL(vec ? k_router_topk8 : k_router_topk, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
+                     (hipStream_t)stream, (const bf16_t*)z, ldz, (const bf16_t*)w_router, d, rows, (int)experts,
+                     (int)top_k, (bf16_t*)logits, ids, weights);
   SJ_LAUNCH_CHECK("router_topk");
   return SJ_OK;
 }
@@ -517,8 +781,23 @@ extern "C" int sj_route_pack(void* stream, const int32_t* ids, long rows, long t
   SJ_REQUIRE(rows >= 0 && top_k > 0 && experts > 0 && experts <= EMAX && S < (1L << 31) && offsets && pslot && ppos &&
                  capacity >= pack_capacity(S, experts),
              "expert route dimensions (capacity %ld, need %ld)", capacity, pack_capacity(S, experts));
-  hipLaunchKernelGGL(k_route_pack, dim3(1), dim3(NT), 0, (hipStream_t)stream, ids, S, (int)top_k, (int)experts,
-                     capacity, tokens, slots, counts, offsets, pslot, ppos);
+  hipStream_t s = (hipStream_t)stream;
+  const int E = (int)experts, Kk = (int)top_k;
+  if (E <= 2)
+    hipLaunchKernelGGL(k_route_pack_wide<1>, dim3(1), dim3(PNT), 0, s, ids, S, Kk, E, capacity, tokens, slots, counts,
+                       offsets, pslot, ppos);
+  else if (E <= 4)
+    hipLaunchKernelGGL(k_route_pack_wide<2>, dim3(1), dim3(PNT), 0, s, ids, S, Kk, E, capacity, tokens, slots, counts,
+                       offsets, pslot, ppos);
+  else if (E <= 8)
+    hipLaunchKernelGGL(k_route_pack_wide<4>, dim3(1), dim3(PNT), 0, s, ids, S, Kk, E, capacity, tokens, slots, counts,
+                       offsets, pslot, ppos);
+  else if (E <= 16)
+    hipLaunchKernelGGL(k_route_pack_wide<8>, dim3(1), dim3(PNT), 0, s, ids, S, Kk, E, capacity, tokens, slots, counts,
+                       offsets, pslot, ppos);
+  else
+    hipLaunchKernelGGL(k_route_pack, dim3(1), dim3(NT), 0, s, ids, S, Kk, E, capacity, tokens, slots, counts, offsets,
+                       pslot, ppos);
   SJ_LAUNCH_CHECK("hierarchy_route_pack");
   return SJ_OK;
 }
@@ -555,8 +834,9 @@ extern "C" int sj_moe_combine_bwd(void* stream, const uint16_t* yp, long ldy, lo
                                   uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi, uint16_t* dx_t_lo, long ldt,
                                   float* dweights) {
   SJ_REQUIRE(d > 0 && d % 8 == 0 && d <= 1024 && ldy % 2 == 0 && lddy % 2 == 0 && top_k > 0 && capacity % 64 == 0 &&
-                 ldt >= capacity && ldt % 8 == 0 && ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
-             "expert combine backward dimensions");
+                 !dx_t_hi == !dx_t_lo && (!dx_t_hi || (ldt >= capacity && ldt % 8 == 0)) &&
+                 ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
+             "expert combine backward dimensions (transposed planes both or neither)");
   if (capacity == 0) return SJ_OK;
   const size_t lds = 2 * sizeof(bf16_t) * TRB * (size_t)d;
   hipLaunchKernelGGL(k_moe_combine_bwd, dim3((unsigned)(capacity / TRB)), dim3(NT), lds, (hipStream_t)stream,
@@ -574,9 +854,12 @@ extern "C" int sj_moe_gather_bwd(void* stream, const float* dxp, long lddx, long
                  (!logits || (dweights && dlogits)),
              "gather backward (experts) dimensions");
   if (rows == 0) return SJ_OK;
-  hipLaunchKernelGGL(k_moe_gather_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream, dxp, lddx,
-                     d, ids, ppos, weights, (const bf16_t*)logits, dweights, (const bf16_t*)w_router, rows,
-                     (int)top_k, (int)experts, dz_acc, ldacc, dz, lddz, dlogits);
+  const bool vec = d % 8 == 0 && experts % 8 == 0 && lddx % 4 == 0 && lddz % 4 == 0 && (!dz_acc || ldacc % 4 == 0) &&
+                   ((uintptr_t)dxp & 15) == 0 && ((uintptr_t)dz & 15) == 0 && ((uintptr_t)dz_acc & 15) == 0 &&
+                   ((uintptr_t)w_router & 15) == 0;
+  hipLaunchKernelGGL(vec ? k_moe_gather_bwd8 : k_moe_gather_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
+                     (hipStream_t)stream, dxp, lddx, d, ids, ppos, weights, (const bf16_t*)logits, dweights,
+                     (const bf16_t*)w_router, rows, (int)top_k, (int)experts, dz_acc, ldacc, dz, lddz, dlogits);
   SJ_LAUNCH_CHECK("gather_backward");
   return SJ_OK;
 }

@@ -148,6 +148,10 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     api.sj_moe_gemm_rows(None, OFF.p, E, cap, d, 2 * F, DGH.p, DGL.p, 2 * F, WGU.p, 2 * F, d * 2 * F, DZP.p, d, 0)
     DWGU = empty(E * d * 2 * F)
     api.sj_moe_gemm_dw(None, OFF.p, E, cap, d, 2 * F, ZPT.p, cap, DGTH.p, DGTL.p, cap, DWGU.p, 2 * F, d * 2 * F)
+    # the same dW from row-layout operands (packed h / inputs and the normal planes)
+    DWD2, DWGU2 = empty(E * F * d), empty(E * d * 2 * F)
+    api.sj_moe_gemm_dw_tn(None, OFF.p, E, cap, F, d, H.p, F, DXH.p, DXL.p, d, DWD2.p, d, F * d)
+    api.sj_moe_gemm_dw_tn(None, OFF.p, E, cap, d, 2 * F, ZP.p, d, DGH.p, DGL.p, 2 * F, DWGU2.p, 2 * F, d * 2 * F)
     DZ, DLOG = empty(M * d), empty(M * E)
     api.sj_moe_gather_bwd(None, DZP.p, d, d, IDS.p, PP.p, WTS.p, LOG.p, DWT.p, WR.p, M, K, E, ACC.p, d, DZ.p, d,
                           DLOG.p)
@@ -188,6 +192,7 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
         for got, ref in ((dwgu[e][:, :F], grads_ref[e][0]), (dwgu[e][:, F:], grads_ref[e][1]), (dwd[e], grads_ref[e][2])):
             worst = max(worst, rel(got, ref))
     assert worst < 1e-4, worst
+    assert rel(DWD2.host(), DWD.host()) < 1e-6 and rel(DWGU2.host(), DWGU.host()) < 1e-6
     assert rel(DZ.host(), acc + dz_ref) < 1e-4
     assert rel(DWR.host(), dwr_ref) < 1e-4
     print(f"[moe] worst expert dW rel {worst:.2e}", flush=True)
@@ -212,3 +217,65 @@ def test_route_topk_and_backward_entries(api):
         assert np.all(ids[:10, 0] == 3) and np.all(ids[:10, 1] == 5)
         assert rel(W.host(), w) < 1e-6
         assert rel(DX.host(), O.route_topk_bwd(x.astype(np.float32), ids, W.host().reshape(R, K), dy)) < 1e-5
+
+
+@pytest.mark.parametrize("E,K", [(2, 1), (3, 2), (8, 2), (16, 4), (32, 8)])
+def test_route_pack_all_expert_counts(api, lib, E, K):
+    """The device pack (every template width and the 32-expert form) against
+    the reference's stable slot-order pack (hierarchy.py:212-225) on ids
+    with empty and full experts."""
+    rng = np.random.default_rng(E * 10 + K)
+    M = 2000
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
+    ids[:, 0] = np.where(rng.random(M) < 0.5, 0, ids[:, 0])            # a crowded expert (the pack is per slot)
+    if E > 2:
+        ids[ids == E - 1] = E - 2 if K == 1 else ids[ids == E - 1]        # expert E-1 may stay empty (K = 1)
+    S = M * K
+    cap = lib.sj_route_pack_capacity(S, E)
+    IDS = dev(ids.ravel(), "i32")
+    TOK, SLT = empty(E * S, "i32"), empty(E * S, "i32")
+    CNT, OFF, PS, PP = empty(E, "i32"), empty(E + 1, "i32"), empty(cap, "i32"), empty(S, "i32")
+    print(f"[route_pack] E={E} K={K} S={S}", flush=True)
+    api.sj_route_pack(None, IDS.p, M, K, E, TOK.p, SLT.p, CNT.p, OFF.p, PS.p, PP.p, cap)
+    sync()
+    tokens_ref, slots_ref, counts_ref = O.route_pack(ids, E)
+    counts, off = CNT.host(), OFF.host()
+    np.testing.assert_array_equal(counts, counts_ref)
+    pad = (counts_ref + 63) // 64 * 64
+    np.testing.assert_array_equal(off, np.concatenate([[0], np.cumsum(pad)]))
+    tok, slt, pslot = TOK.host().reshape(E, S), SLT.host().reshape(E, S), PS.host()
+    for e in range(E):
+        c = counts[e]
+        np.testing.assert_array_equal(tok[e, :c], tokens_ref[e, :c])
+        np.testing.assert_array_equal(slt[e, :c], slots_ref[e, :c])
+        np.testing.assert_array_equal(pslot[off[e]:off[e] + c], slots_ref[e, :c])
+        assert np.all(pslot[off[e] + c:off[e + 1]] == -1)
+    assert np.all(pslot[off[E]:] == -1)
+    np.testing.assert_array_equal(pslot[PP.host()], np.arange(S))
+
+
+def test_gather_bwd_vector_form_is_bit_exact(api, lib):
+    """The 16-byte gather/route backward equals the per-column kernel bit
+    for bit (same per-column order); an odd dz stride selects the latter."""
+    rng = np.random.default_rng(77)
+    M, d, E, K = 1000, 256, 8, 2
+    cap = lib.sj_route_pack_capacity(M * K, E)
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
+    IDS = dev(ids.ravel(), "i32")
+    CNT, OFF, PS, PP = empty(E, "i32"), empty(E + 1, "i32"), empty(cap, "i32"), empty(M * K, "i32")
+    api.sj_route_pack(None, IDS.p, M, K, E, None, None, CNT.p, OFF.p, PS.p, PP.p, cap)
+    logits = O.round_to(rng.normal(0, 1, (M, E)), "bf16")
+    _, w = O.route_topk(logits.astype(np.float32), K)
+    dxp = rng.normal(0, 1e-3, (cap, d)).astype(np.float32).astype(np.float64)
+    acc = rng.normal(0, 1e-3, (M, d)).astype(np.float32).astype(np.float64)
+    wr = O.round_to(rng.normal(0, d ** -0.5, (d, E)), "bf16")
+    dwt = rng.normal(0, 1e-2, (M, K)).astype(np.float32).astype(np.float64)
+    args = (dev(dxp).p, d, d, IDS.p, PP.p, dev(w).p, dev(logits, "bf16").p, dev(dwt).p, dev(wr, "bf16").p, M, K, E,
+            dev(acc).p, d)
+    DZ, DL = empty(M * d), empty(M * E)
+    api.sj_moe_gather_bwd(None, *args, DZ.p, d, DL.p)
+    DZ2, DL2 = empty(M * (d + 1)), empty(M * E)
+    api.sj_moe_gather_bwd(None, *args, DZ2.p, d + 1, DL2.p)
+    sync()
+    np.testing.assert_array_equal(DZ.host().reshape(M, d), DZ2.host().reshape(M, d + 1)[:, :d])
+    np.testing.assert_array_equal(DL.host(), DL2.host())
