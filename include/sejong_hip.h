@@ -218,10 +218,14 @@ int sj_gemm_planes_tn(void *stream, long M, long N, long K, const uint16_t *x_hi
  * [M][K] and W^T [N][K] bf16, its fp32 result written as hi/lo planes
  * c [M][ldc] (the dO operands of the attention backward) and, when c_t_hi
  * and c_t_lo are non-null, also transposed c_t [N][ldct] (ldct >= M,
- * multiple of 8). */
+ * multiple of 8).  With delta_t non-null (the attention output's dX), also
+ * the attention backward's Delta (hierarchy.py:42-70): delta_t [N/64][ld]
+ * = per row and 64-column head, the sum of the stored planes times
+ * o [M][ldo]. */
 int sj_gemm_planes_split_out(void *stream, long M, long N, long K, const uint16_t *a_hi, const uint16_t *a_lo,
                              long lda, const uint16_t *b, long ldb, uint16_t *c_hi, uint16_t *c_lo, long ldc,
-                             uint16_t *c_t_hi, uint16_t *c_t_lo, long ldct);
+                             uint16_t *c_t_hi, uint16_t *c_t_lo, long ldct, const uint16_t *o, long ldo,
+                             float *delta_t, long ld_delta);
 /* Engine::project_qkv (projection_ops.rs:6-43) + fused RoPE with the weights
  * transposed in one [N+2KV][D] buffer (query rows, then key, then value);
  * output one [M][N+2KV] bf16 buffer (q | k | v columns) and, when qkv_t is

@@ -150,7 +150,7 @@ SIGNATURES = {
                                  _P, _P, _L, _P, _P, _L, _P, _S]),
     "sj_gemm_planes_tn": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
     "sj_moe_gemm_dw_tn": (_I, [_P, _P, _L, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _L]),
-    "sj_gemm_planes_split_out": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _P, _L, _P, _P, _L]),
+    "sj_gemm_planes_split_out": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _P, _L, _P, _P, _L, _P, _L, _P, _L]),
     "sj_qkv_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _L, _P, _L, _P, _L, _L, _P, _L]),
     "sj_gate_up_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _P, _P, _L, _P, _L]),
     "sj_linear_residual_fwd_t": (_I, [_P, _P, _L, _L, _L, _P, _L, _L, _P, _L, _P, _L]),

@@ -60,6 +60,12 @@ struct FParams {
   const bf16_t* uin;
   long ldgu;
   long F;
+  // E_PLANES: Delta of the attention backward (nullable): delta[h][m] =
+  // sum over head h's 64 columns of the stored dO planes times o
+  const bf16_t* o;
+  long ldo;
+  float* delta;
+  long lddelta;
   // rope
   const float* rope;
   long rope_t, head_dim, rope_cols;
@@ -540,6 +546,36 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       });
       if (p.c[2 + t2]) cols_bf16(T + t2 * TP, (bf16_t*)p.c[2 + t2], p.ldc[2]);
     }
+    if (p.delta) {
+      // Delta[h][m] = sum (hi + lo) * o over head h's columns (n0 and BN are
+      // multiples of 64): four lanes per (row, head), 16 columns each, then
+      // (l0 + l1) + (l2 + l3) -- the order of the standalone Delta pass
+      constexpr int NH = BN / 64;
+      for (int q = threadIdx.x; q < BM * NH * 4; q += NT) {
+        const int g = q & 3, rh = q >> 2, r = rh / NH, hc = rh % NH;
+        const long m = m0 + r, col0 = n0 + 64 * hc;
+        const bool ok = m < p.M && col0 < p.N;
+        float dpart = 0.f;
+        if (ok) {
+#pragma unroll
+          for (int c = 0; c < 2; c++) {
+            const int cl = 64 * hc + 32 * c + 8 * g;
+            const u32x4 hv = *(const u32x4*)(T + r * TLD + cl);
+            const u32x4 lv = *(const u32x4*)(T + TP + r * TLD + cl);
+            const u32x4 ov = *(const u32x4*)(p.o + m * p.ldo + col0 + 32 * c + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              dpart += (__uint_as_float(hv[i] << 16) + __uint_as_float(lv[i] << 16)) * __uint_as_float(ov[i] << 16);
+              dpart += (__uint_as_float(hv[i] & 0xffff0000u) + __uint_as_float(lv[i] & 0xffff0000u)) *
+                       __uint_as_float(ov[i] & 0xffff0000u);
+            }
+          }
+        }
+        dpart += __shfl_xor(dpart, 1, 64);
+        dpart += __shfl_xor(dpart, 2, 64);
+        if (ok && g == 0) p.delta[(col0 / 64) * p.lddelta + m] = dpart;
+      }
+    }
   } else if constexpr (EPI == E_GATEUP) {
 #pragma unroll
     for (int t3 = 0; t3 < 3; t3++) {
@@ -1009,7 +1045,8 @@ extern "C" int sj_gemm_planes_tn(void* stream, long M, long N, long K, const uin
 
 extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, const uint16_t* a_hi,
                                          const uint16_t* a_lo, long lda, const uint16_t* b, long ldb, uint16_t* c_hi,
-                                         uint16_t* c_lo, long ldc, uint16_t* c_t_hi, uint16_t* c_t_lo, long ldct) {
+                                         uint16_t* c_lo, long ldc, uint16_t* c_t_hi, uint16_t* c_t_lo, long ldct,
+                                         const uint16_t* o, long ldo, float* delta_t, long ld_delta) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
   SJ_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K &&
                  ldc >= N && (!c_t_hi || (ldct >= M && ldct % 8 == 0)),
@@ -1017,12 +1054,15 @@ extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, co
   SJ_REQUIRE(a_hi && a_lo && b && c_hi && c_lo && !c_t_hi == !c_t_lo && ok16(a_hi) && ok16(a_lo) && ok16(b) &&
                  (!c_t_hi || (ok16(c_t_hi) && ok16(c_t_lo))),
              "matmul planes out: 16-byte aligned operands required (transposed outputs both or neither)");
+  SJ_REQUIRE(!delta_t || (o && N % 64 == 0 && ldo % 8 == 0 && ldo >= N && ok16(o) && ld_delta >= M),
+             "matmul planes out: Delta needs o [M][ldo] (ldo % 8 == 0) and 64-column heads");
   FParams p = {};
   p.a[0] = (const bf16_t*)a_hi; p.a[1] = (const bf16_t*)a_lo; p.lda = lda;
   p.b[0][0] = (const bf16_t*)b; p.ldb[0] = ldb; p.seg_n[0] = 0; p.nseg = 1;
   p.M = M; p.N = N; p.K = K;
   p.c[0] = c_hi; p.c[1] = c_lo; p.c[2] = c_t_hi; p.c[3] = c_t_lo;
   p.ldc[0] = ldc; p.ldc[2] = ldct;
+  p.o = (const bf16_t*)o; p.ldo = ldo; p.delta = delta_t; p.lddelta = ld_delta;
   int bm, bn, splits;
   plan(M, N, K, 2, bm, bn, splits);
   int st = launch_planes<E_PLANES>((hipStream_t)stream, p, 2, 1, bm, bn, 1);

@@ -783,7 +783,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       // x1 = x + attention_output(o)
       if (S.attn_tt)  // dO as hi/lo planes: the attention backward's operands
         OP("attn_out_dx", sj_gemm_planes_split_out(s, M, d, d, NP(KX, p)[0], NP(KX, p)[1], d, W + y.wo, d, m->dop[0],
-                                                   m->dop[1], d, nullptr, nullptr, 0));
+                                                   m->dop[1], d, nullptr, nullptr, 0, (const uint16_t*)m->o[l], d,
+                                                   m->deltat, ldt));
       else
         OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
                                          wsb));
@@ -795,7 +796,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                          SJ_F32, d, 0, ws2, wsb));
       TRY(read(KX, p));
       TRY(reuse(KQ, p));
-      for (int part = 1; part <= 4; part <<= 1) {
+      // with dO as planes, attn_out_dx's epilogue has written Delta
+      for (int part = S.attn_tt ? 2 : 1; part <= 4; part <<= 1) {
         const char* nm = part == 4   ? "attention_bwd_kv_reduce"
                          : S.attn_tt ? (part == 1 ? "attention_bwd_delta" : "attention_bwd_dq_dkv")
                                      : (part == 1 ? "attention_bwd_dq" : "attention_bwd_dkv");

@@ -383,7 +383,7 @@ def test_gemm_planes_split_out(api):
     ldt = M + 8
     Ch, Cl, Th, Tl = empty(M * N, "bf16"), empty(M * N, "bf16"), zeros(N * ldt, "bf16"), zeros(N * ldt, "bf16")
     api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, Ch.p,
-                                 Cl.p, N, Th.p, Tl.p, ldt)
+                                 Cl.p, N, Th.p, Tl.p, ldt, None, 0, None, 0)
     sync()
     hi, lo = Ch.host().reshape(M, N), Cl.host().reshape(M, N)
     assert rel(hi + lo, (ah + al) @ w.T) < 1e-5
@@ -391,7 +391,7 @@ def test_gemm_planes_split_out(api):
     # deterministic: a second launch writes the same bits
     C2h, C2l = empty(M * N, "bf16"), empty(M * N, "bf16")
     api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, C2h.p,
-                                 C2l.p, N, Th.p, Tl.p, ldt)
+                                 C2l.p, N, Th.p, Tl.p, ldt, None, 0, None, 0)
     sync()
     np.testing.assert_array_equal(C2h.host(), Ch.host())
     np.testing.assert_array_equal(C2l.host(), Cl.host())
@@ -399,8 +399,23 @@ def test_gemm_planes_split_out(api):
     # transposed outputs are optional: the normal planes are the same bits
     C3h, C3l = empty(M * N, "bf16"), empty(M * N, "bf16")
     api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, C3h.p,
-                                 C3l.p, N, None, None, 0)
+                                 C3l.p, N, None, None, 0, None, 0, None, 0)
     sync()
     np.testing.assert_array_equal(C3h.host(), Ch.host())
     np.testing.assert_array_equal(C3l.host(), Cl.host())
     np.testing.assert_array_equal(Tl.host().reshape(N, ldt)[:, :M], lo.T)
+    # Delta of the attention backward from the same epilogue: per row and
+    # 64-column head, the sum of the stored planes times O (the planes are
+    # unchanged by it)
+    o = O.round_to(rng.normal(0, 1, (M, N)), "bf16")
+    ldd = M + 16
+    Dl, C4h, C4l = zeros(N // 64 * ldd, "f32"), empty(M * N, "bf16"), empty(M * N, "bf16")
+    api.sj_gemm_planes_split_out(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p, K, dev(w, "bf16").p, K, C4h.p,
+                                 C4l.p, N, None, None, 0, dev(o, "bf16").p, N, Dl.p, ldd)
+    sync()
+    np.testing.assert_array_equal(C4h.host(), Ch.host())
+    np.testing.assert_array_equal(C4l.host(), Cl.host())
+    want = ((hi + lo) * o).reshape(M, N // 64, 64).sum(-1).T
+    got = Dl.host().reshape(N // 64, ldd)
+    assert np.abs(got[:, :M] - want).max() <= 1e-5 * np.abs(want).max()
+    assert np.all(got[:, M:] == 0)
