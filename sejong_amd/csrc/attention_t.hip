@@ -37,9 +37,23 @@ constexpr int QB = 64;
 #ifndef SJ_ATTN_DQ_STAGES
 #define SJ_ATTN_DQ_STAGES 3
 #endif
+#ifndef SJ_ATTN_DKV_STAGES
+#define SJ_ATTN_DKV_STAGES 2
+#endif
+// waves per SIMD the dK/dV kernels are compiled for (0: the compiler's
+// choice, 2 at their register use); 3 fits their 50 KB of LDS three
+// workgroups to a CU
+#ifndef SJ_ATTN_BWD_WAVES
+#define SJ_ATTN_BWD_WAVES 3
+#endif
+#if SJ_ATTN_BWD_WAVES
+#define SJ_BWD_OCC __attribute__((amdgpu_waves_per_eu(SJ_ATTN_BWD_WAVES, SJ_ATTN_BWD_WAVES)))
+#else
+#define SJ_BWD_OCC
+#endif
 constexpr int NS_FWD = SJ_ATTN_FWD_STAGES;
 constexpr int NS_DQ = SJ_ATTN_DQ_STAGES;
-constexpr int NST = 3;             // dK/dV stages
+constexpr int NST = SJ_ATTN_DKV_STAGES;  // dK/dV stages
 constexpr int TILE = 64 * 64;      // bf16 elements per tile
 constexpr int TBYTES = TILE * 2;
 constexpr float LOG2E = 1.4426950408889634f;
@@ -483,7 +497,9 @@ __device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, i
   for (int qb = kb; qb < nqb; qb++) {
     const int it = qb - kb;
     if (qb + 1 < nqb) {
-      if (wave_s == 0) wait_vm<7>(); else wait_vm<6>();
+      // a stage is 6 DMA instructions per wave (7 on wave 0): leave the
+      // NST - 2 later stages in flight
+      if (wave_s == 0) wait_vm<(NST - 2) * 7>(); else wait_vm<(NST - 2) * 6>();
     } else {
       wait_vm<0>();
     }
@@ -585,7 +601,7 @@ __global__ __launch_bounds__(256) void k_attn_delta(TArgs a) {
 // x < T/64 is the dQ of query block T/64 - 1 - x (longest first), the rest
 // the dK/dV of key block x - T/64 (longest first).  Both roles keep several
 // latency-bound workgroups per CU busy.
-__global__ __launch_bounds__(256) void k_attn2_bwd(TArgs a) {
+__global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   const int nb = (int)(gridDim.x >> 1), x = (int)blockIdx.x;
   if (x < nb)
@@ -601,7 +617,7 @@ __global__ __launch_bounds__(256) void k_attn2_bwd_dq(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - (int)blockIdx.x, blockIdx.y, blockIdx.z);
 }
-__global__ __launch_bounds__(256) void k_attn2_bwd_dkv(TArgs a) {
+__global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd_dkv(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   attn2_dkv(a, lds, blockIdx.x, blockIdx.y, blockIdx.z);
 }
@@ -610,7 +626,7 @@ constexpr long SEPARATE_ROLES = 2048;  // workgroups per role from which the rol
 constexpr size_t LDS_FWD = (size_t)NS_FWD * 2 * TBYTES;
 constexpr size_t LDS_DQ = (size_t)NS_DQ * 2 * TBYTES;
 static_assert(NS_FWD >= 2 && NS_DQ >= 2 && LDS_FWD <= 160 * 1024 && LDS_DQ <= 160 * 1024, "LDS budget");
-static_assert((NS_FWD - 2) * 4 < 64 && (NS_DQ - 2) * 4 < 64, "vmcnt range");
+static_assert((NS_FWD - 2) * 4 < 64 && (NS_DQ - 2) * 4 < 64 && NST >= 2 && (NST - 2) * 7 < 64, "vmcnt range");
 constexpr size_t LDS_DKV = (size_t)NST * (3 * TBYTES + 1024);
 constexpr size_t LDS_BWD = LDS_DQ > LDS_DKV ? LDS_DQ : LDS_DKV;
 static_assert(LDS_BWD <= 160 * 1024, "LDS budget");
