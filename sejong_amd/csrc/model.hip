@@ -923,8 +923,6 @@ int backward(sj_model* m) {
     // gather's backward into the full hidden gradient (zero off the SEP rows)
     const long R = m->HR, n = m->HV;
     OP("value_bias_bwd", sj_bias_reduce(s, m->dlogits, m->Vp, R, n, G + m->bias));
-    OP("head_dw", sj_gemm(s, 1, 0, d, n, R, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
-                          m->ws, m->ws_bytes));
     OP("head_dx", sj_gemm(s, 0, 1, R, d, n, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dhsel, SJ_F32,
                           d, 0, m->ws, m->ws_bytes));
     OP("value_scatter", sj_gather_rows_bwd(s, m->dhsel, m->sel, R, d, m->dz, d, M));
@@ -932,8 +930,6 @@ int backward(sj_model* m) {
     // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
     OP("head_dx", sj_gemm(s, 0, 1, M, d, m->HV, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d,
                           0, m->ws, m->ws_bytes));
-    OP("head_dw", sj_gemm(s, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
-                          m->ws, m->ws_bytes));
   }
   const bool two = two_streams(m);
   if (two) {  // fork; every plane buffer starts out free for the dX chain
@@ -941,6 +937,16 @@ int backward(sj_model* m) {
     SJ_HIP(hipStreamWaitEvent(m->stream2, m->ev_fork, 0));
     for (int k = 0; k < 4; k++)
       for (int p = 0; p < 2; p++) SJ_HIP(hipEventRecord(m->ev_r[k][p], m->stream2));
+  }
+  {  // the head's dW reads only the forward's rows and dlogits: second stream
+    hipStream_t sw = two ? m->stream2 : s;
+    void* wsw = two ? m->ws2 : m->ws;
+    if (m->value_n)
+      OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, m->HR, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32,
+                            m->Vp, 0, wsw, m->ws_bytes));
+    else
+      OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
+                            wsw, m->ws_bytes));
   }
   int cur = 0;
   if (m->hier)
