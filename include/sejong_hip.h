@@ -129,7 +129,8 @@ int sj_rmsnorm_bwd(void *stream, const void *x, int x_dtype, const void *w, int 
  * and w): the forward also writes y transposed, y_t [d][ldt] (the A operand
  * of the dW GEMMs); the backward (d <= 1024) also writes dx as hi/lo bf16
  * planes, normal [rows][d] and transposed [d][ldt] (dX / dW GEMM operands
- * of the layer below).  Workspace: sj_rmsnorm_bwd_p_workspace_bytes. */
+ * of the layer below; each pair optional: both pointers or neither).
+ * Workspace: sj_rmsnorm_bwd_p_workspace_bytes. */
 int sj_rmsnorm_fwd_t(void *stream, const uint16_t *x, const uint16_t *w, uint16_t *y, uint16_t *y_t,
                      long ldt, long rows, long d, float eps);
 size_t sj_rmsnorm_bwd_p_workspace_bytes(long rows, long d);

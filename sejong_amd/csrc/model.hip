@@ -829,9 +829,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                                       m->dres[cur ^ 1], NP(KR, pn)[0], NP(KR, pn)[1], TP(KR, pn)[0],
                                                       TP(KR, pn)[1], ldt, M, d, eps, m->slot_ptr[m->slot_an[l]]));
         TRY(written(KR, pn));
-      } else {  // the stage input's gradient feeds row-layout consumers only
-        OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, xin(m, l), dt, W + y.an, dt, m->dz, m->dx1, m->dres[cur ^ 1], G + y.an, M, d,
-                                         eps, ws, wsb));
+      } else {  // the stage input's gradient feeds row-layout consumers only: fp32, no planes
+        OP("rmsnorm_bwd", sjh::rmsnorm_bwd_p_deferred(s, (const uint16_t*)xin(m, l), W + y.an, m->dz, m->dx1,
+                                                      m->dres[cur ^ 1], nullptr, nullptr, nullptr, nullptr, ldt, M, d,
+                                                      eps, m->slot_ptr[m->slot_an[l]]));
       }
       cur ^= 1;
     }
@@ -1469,7 +1470,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
         ALLOC(m->pt[k][1][i], sizes[k] * 2);
       }
     // norm-weight partial slots: the closing norm of every stage, and per
-    // layer the ffn norm and (above the stage's first layer) the attention norm
+    // layer the ffn norm and the attention norm
     std::vector<sj::RmsReduceJob> jobs;
     std::vector<size_t> offs;
     size_t total = 0;
@@ -1487,7 +1488,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       m->slot_close.push_back(slot(S, S.norm));
       for (long l = S.first; l < S.first + S.count; l++) {
         m->slot_fn[l] = slot(S, m->layers[l].fn);
-        if (l > S.first) m->slot_an[l] = slot(S, m->layers[l].an);
+        m->slot_an[l] = slot(S, m->layers[l].an);
       }
     }
     ALLOC(m->norm_part, total * sizeof(float));

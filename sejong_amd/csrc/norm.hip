@@ -326,8 +326,10 @@ __global__ __launch_bounds__(NTT) void k_rms_bwd_p(const bf16_t* __restrict__ x,
         split_bf(b, hb, lb);
         ph = pack2(ha, hb);
         pl = pack2(la, lb);
-        *(uint32_t*)(hi + r * d + 2 * p) = ph;
-        *(uint32_t*)(lo + r * d + 2 * p) = pl;
+        if (hi) {  // row-layout planes (optional)
+          *(uint32_t*)(hi + r * d + 2 * p) = ph;
+          *(uint32_t*)(lo + r * d + 2 * p) = pl;
+        }
       }
       *(uint32_t*)(shi + wv * d + 2 * p) = ph;
       *(uint32_t*)(slo + wv * d + 2 * p) = pl;
@@ -482,10 +484,10 @@ extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t*
 int sjh::rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, const float* dy,
                                 const float* dx_acc, float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi,
                                 uint16_t* dx_t_lo, long ldt, long rows, long d, float eps, float* partial) {
-  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && partial && !dx_t_hi == !dx_t_lo &&
+  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && partial && !dx_t_hi == !dx_t_lo && !dx_hi == !dx_lo &&
                  (!dx_t_hi || (ldt >= rows && ldt % 8 == 0)) && ((uintptr_t)dx_t_hi & 15) == 0 &&
                  ((uintptr_t)dx_t_lo & 15) == 0,
-             "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
+             "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024; planes both or neither)", rows, d, ldt);
   if (int st0 = sjh::norm_prepare()) return st0;
   hipStream_t s = (hipStream_t)stream;
   const long groups = (rows + TR - 1) / TR;
@@ -521,10 +523,10 @@ extern "C" int sj_rmsnorm_bwd_p(void* stream, const uint16_t* x, const uint16_t*
                                 const float* dx_acc, float* dx, float* dw, uint16_t* dx_hi, uint16_t* dx_lo,
                                 uint16_t* dx_t_hi, uint16_t* dx_t_lo, long ldt, long rows, long d, float eps,
                                 void* workspace, size_t workspace_bytes) {
-  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && !dx_t_hi == !dx_t_lo &&
+  SJ_REQUIRE(rows > 0 && d > 0 && d % 8 == 0 && d <= 1024 && !dx_t_hi == !dx_t_lo && !dx_hi == !dx_lo &&
                  (!dx_t_hi || (ldt >= rows && ldt % 8 == 0)) && ((uintptr_t)dx_t_hi & 15) == 0 &&
                  ((uintptr_t)dx_t_lo & 15) == 0,
-             "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
+             "RMSNorm backward (planes): rows %ld d %ld ldt %ld (d <= 1024; planes both or neither)", rows, d, ldt);
   if (int st0 = sjh::norm_prepare()) return st0;
   size_t need = sj_rmsnorm_bwd_p_workspace_bytes(rows, d);
   if (!workspace || workspace_bytes < need)

@@ -250,6 +250,13 @@ def test_rmsnorm_t_and_planes(api, lib, R, D, ldt):
     _check_planes(hi, lo, dxd)
     np.testing.assert_array_equal(Ht.host().reshape(D, ldt)[:, :R], hi.T)
     np.testing.assert_array_equal(Lt.host().reshape(D, ldt)[:, :R], lo.T)
+    # planes are optional (the stage input's gradient): dx and dw are the same bits
+    DX2, DW2 = empty(R * D), empty(D)
+    api.sj_rmsnorm_bwd_p(None, X.p, W.p, dev(dy).p, dev(acc).p, DX2.p, DW2.p, None, None, None, None, 0, R, D,
+                         cf(eps), wsb.p, wsb.nbytes)
+    sync()
+    np.testing.assert_array_equal(DX2.host(), DX.host())
+    np.testing.assert_array_equal(DW2.host(), DW.host())
 
 
 @pytest.mark.parametrize("B,T,HQ,HK", [(2, 256, 6, 2), (1, 200, 4, 4)])
