@@ -751,19 +751,30 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         OP("router_dw", sj_gemm(s2, 1, 0, d, E, M, m->z2[l], SJ_BF16, d, m->mdlog[l], SJ_F32, E, G + y.router, SJ_F32, E,
                                 0, ws2, wsb));
       } else {
-      // x_{l+1} = x1 + down(h): down's dX fused with the SwiGLU derivative
+      // x_{l+1} = x1 + down(h): down's dW needs only the planes of dY (kind
+      // KR, written above this layer).  While the layer's products leave
+      // CUs idle (M F <= 8 Mi: cfg2, cfg3) it goes on the second stream
+      // before that stream waits for the SwiGLU derivative's planes, beside
+      // the dX product (cfg2 1.865 -> 1.821 ms/step); at cfg5's size it
+      // would slow that product as much as it gains, so it follows it.
+      auto down_dw = [&]() -> int {
+        if (rdw)
+          OP("down_dw", sj_gemm_planes_tn(s2, F, d, M, (const uint16_t*)m->hh[l], nullptr, F, NP(KR, p)[0],
+                                          NP(KR, p)[1], d, G + y.down, SJ_F32, d, 0, ws2, wsb));
+        else
+          OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt,
+                                       G + y.down, SJ_F32, d, 0, ws2, wsb));
+        return read(KR, p);
+      };
+      const bool early_dw = M * F <= (8L << 20);
+      if (early_dw) TRY(down_dw());
+      // down's dX fused with the SwiGLU derivative
       TRY(reuse(KG, p));
       OP("down_dx_swiglu", sj_down_bwd_swiglu_p(s, NP(KR, p)[0], NP(KR, p)[1], d, M, d, W + y.down, d, F,
                                                 (const uint16_t*)m->gg[l], (const uint16_t*)m->uu[l], F,
                                                 NP(KG, p)[0], NP(KG, p)[1], 2 * F, TP(KG, p)[0], TP(KG, p)[1], ldt));
       TRY(written(KG, p));
-      if (rdw)
-        OP("down_dw", sj_gemm_planes_tn(s2, F, d, M, (const uint16_t*)m->hh[l], nullptr, F, NP(KR, p)[0],
-                                        NP(KR, p)[1], d, G + y.down, SJ_F32, d, 0, ws2, wsb));
-      else
-        OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt, G + y.down,
-                                     SJ_F32, d, 0, ws2, wsb));
-      TRY(read(KR, p));
+      if (!early_dw) TRY(down_dw());
       OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, NP(KG, p)[0], NP(KG, p)[1], 2 * F, W + y.gu, nullptr, 2 * F,
                                       m->dz, SJ_F32, d, 0, ws, wsb));
       if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, T(KG, p)));
