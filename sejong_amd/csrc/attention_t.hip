@@ -192,6 +192,28 @@ __device__ __forceinline__ void dma_tile(const bf16_t* src, long ld, uint32_t ld
   }
 }
 
+// Workgroup -> (rank, role, head, sequence).  Workgroups are dispatched
+// round-robin over the 8 XCDs by linear id (id % 8).  The rank r (the causal
+// walk length order: 0 is the longest) varies slowest and (head, sequence)
+// fastest, so each XCD receives the same mix of walk lengths and the whole
+// launch still starts with the longest walks; with the block index fastest,
+// XCD k would receive only block k of every (head, sequence) and the XCD
+// holding the longest walks would finish last.  grid = (roles * nb, H, B).
+struct WgMap {
+  int r, role, h, b;
+};
+__device__ __forceinline__ WgMap wg_map(int roles) {
+  const long H = gridDim.y, HB = H * (long)gridDim.z;
+  const long lin = (long)blockIdx.x + (long)gridDim.x * ((long)blockIdx.y + H * (long)blockIdx.z);
+  const long rem = lin % (roles * HB), hb = rem % HB;
+  WgMap m;
+  m.r = (int)(lin / (roles * HB));
+  m.role = (int)(rem / HB);
+  m.h = (int)(hb % H);
+  m.b = (int)(hb / H);
+  return m;
+}
+
 // ------------------------------------------------------------------ forward
 template <int NS>
 __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
@@ -199,8 +221,9 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
-  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest blocks first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const WgMap wm = wg_map(1);
+  const int qb = (int)gridDim.x - 1 - wm.r;  // longest blocks first
+  const int h = wm.h, b = wm.b;
   const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
   const int kvh = h / (a.HQ / a.HK);
   const int qloc = wave * 16 + j, myq = qb * QB + qloc;
@@ -598,16 +621,17 @@ __global__ __launch_bounds__(256) void k_attn_delta(TArgs a) {
 }
 
 // dQ and dK/dV in one launch (they share only Delta): grid.x = 2 T/64;
-// x < T/64 is the dQ of query block T/64 - 1 - x (longest first), the rest
-// the dK/dV of key block x - T/64 (longest first).  Both roles keep several
+// rank r of role 0 is the dQ of query block T/64 - 1 - r, of role 1 the
+// dK/dV of key block r (both longest first).  Both roles keep several
 // latency-bound workgroups per CU busy.
 __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  const int nb = (int)(gridDim.x >> 1), x = (int)blockIdx.x;
-  if (x < nb)
-    attn2_dq<NS_DQ>(a, lds, nb - 1 - x, blockIdx.y, blockIdx.z);
+  const int nb = (int)(gridDim.x >> 1);
+  const WgMap wm = wg_map(2);
+  if (wm.role == 0)
+    attn2_dq<NS_DQ>(a, lds, nb - 1 - wm.r, wm.h, wm.b);
   else
-    attn2_dkv(a, lds, x - nb, blockIdx.y, blockIdx.z);
+    attn2_dkv(a, lds, wm.r, wm.h, wm.b);
 }
 
 // The same roles as separate launches: with thousands of workgroups per role
@@ -615,11 +639,13 @@ __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd(TArgs a) {
 // smaller LDS and register footprint (more workgroups per CU).
 __global__ __launch_bounds__(256) void k_attn2_bwd_dq(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - (int)blockIdx.x, blockIdx.y, blockIdx.z);
+  const WgMap wm = wg_map(1);
+  attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - wm.r, wm.h, wm.b);
 }
 __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd_dkv(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  attn2_dkv(a, lds, blockIdx.x, blockIdx.y, blockIdx.z);
+  const WgMap wm = wg_map(1);
+  attn2_dkv(a, lds, wm.r, wm.h, wm.b);
 }
 constexpr long SEPARATE_ROLES = 2048;  // workgroups per role from which the roles launch separately
 

@@ -39,7 +39,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __attribute__((aligned(64))) uint8_t g_zero16[64];  // zero source for masked DMA lanes
 
-enum Epi { E_STORE = 0, E_PARTIAL = 1, E_QKV = 2, E_RESID = 3, E_GATEUP = 4, E_SWIGLU_BWD = 5, E_PLANES = 6 };
+// E_SWIGLU_ROWS: the SwiGLU derivative of E_SWIGLU_BWD with row planes only
+// (no transposed outputs): G/U are prefetched as 16-byte vectors before the
+// main loop, dH is staged in LDS as fp32 and each thread writes whole 16-byte
+// chunks of the four planes
+enum Epi { E_STORE = 0, E_PARTIAL = 1, E_QKV = 2, E_RESID = 3, E_GATEUP = 4, E_SWIGLU_BWD = 5, E_PLANES = 6,
+           E_SWIGLU_ROWS = 7 };
 
 struct FParams {
   const bf16_t* a[2];  // A planes (hi, lo), [M][K] k-contiguous
@@ -155,6 +160,16 @@ __device__ __forceinline__ bf16x8 tr_frag(const bf16_t* tile, int row0, int col0
 }
 
 __device__ __forceinline__ float sigm(float g) { return 1.f / (1.f + expf(-g)); }
+// dG = dH*u*s*(1+g(1-s)), dU = dH*g*s with s = sigmoid(g)  (kernels.py:95-101)
+__device__ __forceinline__ void swiglu_bwd1(float dh, float g, float u, float& dg, float& du) {
+  const float sg = sigm(g);
+  dg = dh * u * sg * (1.f + g * (1.f - sg));
+  du = dh * g * sg;
+}
+__device__ __forceinline__ float bf_word(const u32x4& w, int e) {
+  const uint32_t x = w[e >> 1];
+  return __uint_as_float((e & 1) ? (x & 0xffff0000u) : (x << 16));
+}
 __device__ __forceinline__ float rnd(float v, int bf) { return bf ? round_bf(v) : v; }
 __device__ __forceinline__ void put(void* c, long i, float v, int bf) {
   if (bf)
@@ -186,7 +201,7 @@ constexpr size_t lds_bytes() {
   constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : EPI == E_PLANES ? 2 : 1;
   constexpr size_t pipe = (size_t)NS * (BM * PA + BN * PB * NBM) * BK * 2;
   constexpr size_t ep1 = (size_t)NTILE * BM * (BN + 8) * 2;
-  constexpr size_t ep2 = (EPI == E_STORE || EPI == E_PARTIAL) ? (size_t)BM * (BN + 4) * 4 : 0;
+  constexpr size_t ep2 = (EPI == E_STORE || EPI == E_PARTIAL || EPI == E_SWIGLU_ROWS) ? (size_t)BM * (BN + 4) * 4 : 0;
   constexpr size_t e = ep1 > ep2 ? ep1 : ep2;
   return pipe > e ? pipe : e;
 }
@@ -334,6 +349,24 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
 #pragma unroll
       for (int j = 0; j < NB; j++) acc[q][i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // E_SWIGLU_ROWS: this thread's phase-2 chunks of G and U (8 columns of one
+  // tile row each), loaded now so their latency hides under the main loop
+  constexpr bool SROWS = EPI == E_SWIGLU_ROWS;
+  constexpr int CPR8 = BN / 8, NCH = SROWS ? (BM * CPR8 + NT - 1) / NT : 1;
+  u32x4 gpre[NCH], upre[NCH];
+  if constexpr (SROWS) {
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+      const int q = threadIdx.x + i * NT;
+      const long m = m0 + q / CPR8, n = n0 + (q % CPR8) * 8;
+      gpre[i] = upre[i] = u32x4{0u, 0u, 0u, 0u};
+      if (q < BM * CPR8 && m < p.M && n + 8 <= p.N) {
+        gpre[i] = *(const u32x4*)(p.gin + m * p.ldgu + n);
+        upre[i] = *(const u32x4*)(p.uin + m * p.ldgu + n);
+      }
+    }
+  }
+
   const int fr = lane & 15, fg = lane >> 4;
 #pragma unroll
   for (int s = 0; s < NS - 1; s++)
@@ -407,12 +440,12 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   constexpr int TP = BM * TLD;         // bf16 tile size (elements)
   constexpr int TLDF = BN + 4;         // fp32 tile row stride
   constexpr int NTILE = EPI == E_SWIGLU_BWD ? 4 : EPI == E_GATEUP ? 3 : EPI == E_PLANES ? 2 : 1;
-  constexpr bool F32T = EPI == E_PARTIAL || EPI == E_STORE;  // fp32 tile unless c_bf16
+  constexpr bool F32T = EPI == E_PARTIAL || EPI == E_STORE || SROWS;  // fp32 tile unless c_bf16
   static_assert((size_t)NTILE * TP * 2 <= lds_bytes<BM, BN, PA, PB, EPI, NS>(), "epilogue tiles exceed LDS");
   static_assert(!F32T || (size_t)BM * TLDF * 4 <= lds_bytes<BM, BN, PA, PB, EPI, NS>(), "epilogue tile exceeds LDS");
   bf16_t* T = lds;
   float* TF = (float*)lds;
-  const bool f32out = F32T && !p.c_bf16;
+  const bool f32out = F32T && (SROWS || !p.c_bf16);
   const int cc = lane & 15;
 #pragma unroll
   for (int i = 0; i < MB; i++) {
@@ -435,9 +468,8 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
             g = bf2f(p.gin[m * p.ldgu + ncol]);
             u = bf2f(p.uin[m * p.ldgu + ncol]);
           }
-          const float sg = sigm(g);
-          const float dg = v[r] * u * sg * (1.f + g * (1.f - sg));
-          const float du = v[r] * g * sg;
+          float dg, du;
+          swiglu_bwd1(v[r], g, u, dg, du);
           bf16_t h, l;
           split_bf(dg, h, l);
           T[(rl + r) * TLD + cl] = h;
@@ -536,6 +568,34 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       });
       bf16_t* tb = (t4 & 1) ? (bf16_t*)p.c[3] : (bf16_t*)p.c[2];
       if (tb) cols_bf16(T + t4 * TP, tb + coloff * p.ldc[2], p.ldc[2]);
+    }
+  } else if constexpr (SROWS) {
+    bf16_t* c0 = (bf16_t*)p.c[0];
+    bf16_t* c1 = (bf16_t*)p.c[1];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+      const int q = tid + i * NT;
+      const int r = q / CPR8, c8 = (q % CPR8) * 8;
+      const long m = m0 + r, n = n0 + c8;
+      if (q >= BM * CPR8 || m >= p.M || n + 8 > p.N) continue;
+      const float4 d0 = *(const float4*)(TF + r * TLDF + c8);
+      const float4 d1 = *(const float4*)(TF + r * TLDF + c8 + 4);
+      const float dh[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      bf16_t gh[8], gl[8], uh[8], ul[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float dg, du;
+        swiglu_bwd1(dh[e], bf_word(gpre[i], e), bf_word(upre[i], e), dg, du);
+        split_bf(dg, gh[e], gl[e]);
+        split_bf(du, uh[e], ul[e]);
+      }
+      const long o = m * p.ldc[0] + n;
+      *(u32x4*)(c0 + o) = u32x4{pack2(gh[0], gh[1]), pack2(gh[2], gh[3]), pack2(gh[4], gh[5]), pack2(gh[6], gh[7])};
+      *(u32x4*)(c1 + o) = u32x4{pack2(gl[0], gl[1]), pack2(gl[2], gl[3]), pack2(gl[4], gl[5]), pack2(gl[6], gl[7])};
+      *(u32x4*)(c0 + o + p.F) =
+          u32x4{pack2(uh[0], uh[1]), pack2(uh[2], uh[3]), pack2(uh[4], uh[5]), pack2(uh[6], uh[7])};
+      *(u32x4*)(c1 + o + p.F) =
+          u32x4{pack2(ul[0], ul[1]), pack2(ul[2], ul[3]), pack2(ul[4], ul[5]), pack2(ul[6], ul[7])};
     }
   } else if constexpr (EPI == E_PLANES) {
 #pragma unroll
@@ -886,7 +946,7 @@ int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
 template <int EPI, int PA, int PB>
 constexpr bool plane_combo() {
   if (EPI == E_STORE || EPI == E_PARTIAL) return true;
-  if (EPI == E_SWIGLU_BWD || EPI == E_PLANES) return PA == 2 && PB == 1;
+  if (EPI == E_SWIGLU_BWD || EPI == E_SWIGLU_ROWS || EPI == E_PLANES) return PA == 2 && PB == 1;
   return PA == 1 && PB == 1;
 }
 
@@ -904,6 +964,13 @@ int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int b
 }
 
 bool ok16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
+// The row-plane SwiGLU epilogue moves G, U and the four planes in whole
+// 16-byte chunks: no transposed outputs, 8-aligned widths and strides.
+bool swiglu_rows_ok(const FParams& p) {
+  return !p.c[2] && !p.c[3] && p.F % 8 == 0 && p.ldgu % 8 == 0 && p.ldc[0] % 8 == 0 && ok16(p.gin) && ok16(p.uin) &&
+         ok16(p.c[0]) && ok16(p.c[1]);
+}
 
 template <int BM, int BN, int PA, int PB, int EPI, int NS, int TM = 0>
 int set_attr_ns() {
@@ -953,6 +1020,7 @@ int gemm_fast_prepare() {
   if (!status) status = set_attrs_planes<E_RESID>();
   if (!status) status = set_attrs_planes<E_GATEUP>();
   if (!status) status = set_attrs_planes<E_SWIGLU_BWD>();
+  if (!status) status = set_attrs_planes<E_SWIGLU_ROWS>();
   if (!status) status = set_attrs_planes<E_PLANES>();
   if (!status) status = set_attrs_planes<E_STORE, 3>();
   if (!status) status = set_attrs_planes<E_PARTIAL, 3>();
@@ -1173,7 +1241,8 @@ extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const u
   p.M = M; p.N = F; p.K = D;
   int bm, bn, splits;
   plan(M, F, D, 2, bm, bn, splits);
-  int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
+  int st = swiglu_rows_ok(p) ? launch_planes<E_SWIGLU_ROWS>((hipStream_t)stream, p, 2, 1, bm, bn, 1)
+                             : launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, bm, bn, 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("swiglu_backward");
   return SJ_OK;
@@ -1250,7 +1319,9 @@ extern "C" int sj_moe_down_bwd_swiglu_p(void* stream, const int32_t* offsets, lo
   p.gin = (const bf16_t*)g; p.uin = (const bf16_t*)u; p.ldgu = ldgu; p.F = F;
   p.M = capacity; p.N = F; p.K = D;
   p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
-  int st = launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, 64, grouped_bn(capacity, F), 1);
+  const int bn = grouped_bn(capacity, F);
+  int st = swiglu_rows_ok(p) ? launch_planes<E_SWIGLU_ROWS>((hipStream_t)stream, p, 2, 1, 64, bn, 1)
+                             : launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, 64, bn, 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("expert swiglu_backward");
   return SJ_OK;

@@ -190,9 +190,10 @@ def test_gate_up_t_and_residual_t(api):
                         terms=np.abs(h) @ np.abs(wd) + 2 ** 9 * np.abs(a))
 
 
-def test_down_bwd_swiglu_planes(api):
-    rng = np.random.default_rng(14)
-    M, D, F = 1024, 384, 1024
+@pytest.mark.parametrize("M,F", [(1024, 1024), (1000, 200)])
+def test_down_bwd_swiglu_planes(api, M, F):
+    rng = np.random.default_rng(14 + M + F)
+    D = 384
     dy = rng.normal(0, 1e-4, (M, D)).astype(np.float32).astype(np.float64)
     dh_, dl_ = split(dy)
     wd = O.round_to(rng.normal(0, 0.05, (F, D)), "bf16")
@@ -207,6 +208,14 @@ def test_down_bwd_swiglu_planes(api):
     assert rel(got, ref) < 3e-5
     np.testing.assert_array_equal(Ht.host().reshape(2 * F, M), Hn.host().reshape(M, 2 * F).T)
     np.testing.assert_array_equal(Lt.host().reshape(2 * F, M), Ln.host().reshape(M, 2 * F).T)
+    # without transposed outputs the row-plane epilogue (vector G/U prefetch,
+    # fp32 dH tile) writes the same planes bit for bit
+    Hr, Lr = empty(M * 2 * F, "bf16"), empty(M * 2 * F, "bf16")
+    api.sj_down_bwd_swiglu_p(None, dev(dh_, "bf16").p, dev(dl_, "bf16").p, D, M, D, dev(wd, "bf16").p, D, F,
+                             dev(g, "bf16").p, dev(u, "bf16").p, F, Hr.p, Lr.p, 2 * F, None, None, M)
+    sync()
+    np.testing.assert_array_equal(Hr.host(), Hn.host())
+    np.testing.assert_array_equal(Lr.host(), Ln.host())
     # hi is the RNE bf16 of the value and lo the rest: |lo| <= half an ulp of hi
     hi, lo = Hn.host(), Ln.host()
     assert np.all(np.abs(lo) <= 2.0 ** -8 * np.abs(hi) + 1e-38)

@@ -142,6 +142,9 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     DGH, DGL, DGTH, DGTL = (empty(cap * 2 * F, "bf16") for _ in range(4))
     api.sj_moe_down_bwd_swiglu_p(None, OFF.p, E, cap, DXH.p, DXL.p, d, d, WD.p, d, F * d, F, G.p, U.p, F, DGH.p,
                                  DGL.p, 2 * F, DGTH.p, DGTL.p, cap)
+    DGH2, DGL2 = (empty(cap * 2 * F, "bf16") for _ in range(2))
+    api.sj_moe_down_bwd_swiglu_p(None, OFF.p, E, cap, DXH.p, DXL.p, d, d, WD.p, d, F * d, F, G.p, U.p, F, DGH2.p,
+                                 DGL2.p, 2 * F, None, None, cap)
     DWD = empty(E * F * d)
     api.sj_moe_gemm_dw(None, OFF.p, E, cap, F, d, HT.p, cap, DXTH.p, DXTL.p, cap, DWD.p, d, F * d)
     DZP = empty(cap * d)
@@ -170,6 +173,9 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     n = off[E]
     np.testing.assert_array_equal(DGTH.host().reshape(2 * F, cap)[:, :n], dgh[:n].T)
     np.testing.assert_array_equal(DGTL.host().reshape(2 * F, cap)[:, :n], dgl[:n].T)
+    # the row-plane epilogue (no transposed outputs) writes the same planes
+    np.testing.assert_array_equal(DGH2.host().reshape(cap, 2 * F)[:n], dgh[:n])
+    np.testing.assert_array_equal(DGL2.host().reshape(cap, 2 * F)[:n], dgl[:n])
 
     # end to end, conditioned on the device-stored forward activations
     per = []
