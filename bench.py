@@ -700,7 +700,12 @@ def main():
                      "frac": round(rate / peak, 4)})
         log(f"  {op:20s} x{calls:3d} {avg_us:9.2f} us  {100 * ms / prof_total:5.1f}%  "
             f"{rate:9.2f} {'TFLOP/s' if kind == 'flop' else 'GB/s'}  ({100 * rate / peak:.1f}% of peak)")
-    dom = rows[0]
+    # the roofline covers the largest op that launches exactly one kernel, so
+    # its live HIP-event time is that kernel's duration (comparable with the
+    # rocprofv3 average); the split-K dW products launch a partials kernel and
+    # a reduce, and are listed in the per-op table only
+    single = [r for r in rows if r["op"] in OP_KERNEL]
+    dom = single[0] if single else rows[0]
     kind, work = op_work(dom["op"], mc, tc)
     # HBM bytes per dispatch of the dominant kernel, from the committed
     # rocprofv3 FETCH_SIZE / WRITE_SIZE runs (copy-kernel calibrated)
