@@ -230,12 +230,15 @@ __global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x,
   const long r0 = xcd_block(blockIdx.x, gridDim.x) * TR;
   const long pairs = d >> 1;
   const long r = r0 + wv;
-  float2 xv[NP];
+  // the weight pairs are loaded with the row, so no second global-load
+  // latency follows the row reduction
+  float2 xv[NP], wt[NP];
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NP; j++) {
     const long p = lane + 64L * j;
-    xv[j] = make_float2(0.f, 0.f);
+    xv[j] = wt[j] = make_float2(0.f, 0.f);
+    if (p < pairs) wt[j] = ld2<SJ_BF16>(w, 2 * p);
     if (p < pairs && r < rows) {
       xv[j] = ld2<SJ_BF16>(x, r * d + 2 * p);
       s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x,
   for (int j = 0; j < NP; j++) {
     const long p = lane + 64L * j;
     if (p < pairs) {
-      const float2 w2 = ld2<SJ_BF16>(w, 2 * p);
+      const float2 w2 = wt[j];
       const uint32_t pk = r < rows ? pack2(f2bf(xv[j].x * inv * w2.x), f2bf(xv[j].y * inv * w2.y)) : 0u;
       if (r < rows) *(uint32_t*)(y + r * d + 2 * p) = pk;
       *(uint32_t*)(stage + wv * d + 2 * p) = pk;
