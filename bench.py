@@ -196,8 +196,13 @@ def op_work(op: str, mc, tc):
     if pv is not None:
         # parameter VJP (cfg5): rank R, k selected rows; every layer has a
         # q|k|v and a gate|up group (the step driver checks the decisions)
-        import oracle.pvjp as OP
-        R, blocks, S = OP.budget(pv.rank, pv.residual_fraction, pv.block_rows, M, d, F)
+        import ctypes
+
+        from sejong_amd import _native as N
+        out = [ctypes.c_long() for _ in range(3)]
+        N.load()
+        N.api.sj_pvjp_budget(pv.rank, pv.residual_fraction, pv.block_rows, M, d, F, *(ctypes.byref(o) for o in out))
+        R, blocks, S = (o.value for o in out)
         k = S * pv.block_rows
         comp = mc.layers * (d * (d + 2 * J) + 2 * d * F)   # compressed parameters
         table.update({

@@ -14,7 +14,9 @@ libsejong_hip.so (sj_checkpoint_save, sj_safetensors_*).
 The reference's half-precision compute dtype is "f16" (DType, core lib.rs:
 34-41, has no bf16); this framework's half-precision compute is bf16, so a
 bf16 model is recorded as "f16" and a manifest's "f16" loads as bf16.  The
-stored tensors are the fp32 masters either way.
+stored tensors are the fp32 masters either way, but the compute dtype
+changes across the two frameworks, so both directions emit a
+PrecisionMappingWarning unless the caller opts in with half_as_bf16=True.
 """
 from __future__ import annotations
 
@@ -22,6 +24,7 @@ import ctypes
 import json
 import math
 import os
+import warnings
 
 import numpy as np
 
@@ -55,6 +58,18 @@ def rng_state(words) -> int:
     return v
 
 
+class PrecisionMappingWarning(UserWarning):
+    """A bf16 model written with the reference's "f16" compute dtype, or an
+    "f16" manifest loaded as a bf16 model."""
+
+
+def _warn_half(what: str, half_as_bf16: bool):
+    if not half_as_bf16:
+        warnings.warn(PrecisionMappingWarning(
+            f"{what}: the reference's half compute dtype f16 is bf16 here (fp32 masters are stored either way); "
+            "pass half_as_bf16=True to accept the mapping"), stacklevel=3)
+
+
 def model_config_json(mc: ModelConfig) -> dict:
     """ModelConfig's serde form (core lib.rs:55-73), fields in declaration
     order; hierarchy / kv_heads only when set."""
@@ -75,7 +90,7 @@ def model_config_json(mc: ModelConfig) -> dict:
     return out
 
 
-def model_config_from_json(d: dict) -> ModelConfig:
+def model_config_from_json(d: dict, half_as_bf16: bool = False) -> ModelConfig:
     known = {"id", "width", "layers", "heads", "ffn_width", "context", "rope_theta", "norm_epsilon", "precision",
              "seed", "hierarchy", "kv_heads", "experts"}
     extra = set(d) - known
@@ -84,6 +99,8 @@ def model_config_from_json(d: dict) -> ModelConfig:
     if d.get("experts") is not None:
         raise ValueError("mixture-of-experts checkpoints are not loaded by this step driver")
     prec = d.get("precision", "f16")
+    if prec == "f16":
+        _warn_half("loading an f16 manifest as a bf16 model", half_as_bf16)
     prec = {"f16": "bf16", "f32": "f32"}.get(prec)
     if prec is None:
         raise ValueError(f"precision {d.get('precision')} is not a training compute dtype here")
@@ -131,9 +148,12 @@ def split(mc: ModelConfig, flat: np.ndarray):
 
 
 def save_arrays(directory: str, mc: ModelConfig, params: np.ndarray, step: int, optimizer: list | None = None,
-                training: dict | None = None, data_fingerprint: str | None = None, rng_state: int | None = None):
+                training: dict | None = None, data_fingerprint: str | None = None, rng_state: int | None = None,
+                half_as_bf16: bool = False):
     """Model::save of host arrays: params in the reference layout; optimizer
     a [(name, array)] list (or None)."""
+    if mc.precision == "bf16":
+        _warn_half("saving a bf16 model with manifest precision f16", half_as_bf16)
     manifest = {"format": 1, "model": model_config_json(mc), "step": int(step), "weights": WEIGHTS,
                 "optimizer": OPTIMIZER if optimizer else None, "training": training,
                 "data_fingerprint": data_fingerprint, "rng_state": rng_state}
@@ -162,13 +182,14 @@ def optimizer_tensors(model: Model) -> list:
 
 
 def save(model: Model, directory: str, optimizer: bool = True, training: dict | None = None,
-         data_fingerprint: str | None = None, rng_state: int | None = None):
+         data_fingerprint: str | None = None, rng_state: int | None = None, half_as_bf16: bool = False):
     """Model::save of a live model at its current step (the Adam / SGD step
     count), with its optimizer state unless optimizer=False."""
     if model.values:
         raise ValueError("checkpoints cover the byte language model (not the NativeValue head)")
     save_arrays(directory, model.mc, model.get_params(), N.api.sj_model_steps(model.h),
-                optimizer_tensors(model) if optimizer else None, training, data_fingerprint, rng_state)
+                optimizer_tensors(model) if optimizer else None, training, data_fingerprint, rng_state,
+                half_as_bf16=half_as_bf16)
 
 
 def header(path: str) -> dict:
@@ -198,11 +219,11 @@ def load_manifest(directory: str) -> dict:
     return m
 
 
-def load_arrays(directory: str):
+def load_arrays(directory: str, half_as_bf16: bool = False):
     """Model::load (model lib.rs:134-170): (ModelConfig, reference-layout
     parameters, manifest, optimizer tensors by name or None)."""
     m = load_manifest(directory)
-    mc = model_config_from_json(m["model"])
+    mc = model_config_from_json(m["model"], half_as_bf16)
     wpath = os.path.join(directory, m["weights"])
     hdr = {k: v for k, v in header(wpath).items() if k != "__metadata__"}
     expect = layout(mc)
@@ -224,12 +245,12 @@ def load_arrays(directory: str):
     return mc, params, m, opt
 
 
-def load_into(model: Model, directory: str) -> dict:
+def load_into(model: Model, directory: str, half_as_bf16: bool = False) -> dict:
     """Resume a live model from a checkpoint of the same configuration:
     parameters, and the optimizer state (Adam::load_parameters, train
     lib.rs:148-175 with the manifest's step; or the SGD state's parameter
     RNG, control_variate.rs:125-150).  Returns the manifest."""
-    mc, params, m, opt = load_arrays(directory)
+    mc, params, m, opt = load_arrays(directory, half_as_bf16)
     if layout(mc) != layout(model.mc):
         raise ValueError("checkpoint model configuration differs from the live model")
     model.set_params(params)

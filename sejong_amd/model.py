@@ -394,10 +394,10 @@ class Model:
         from . import checkpoint
         checkpoint.save(self, directory, **kw)
 
-    def load(self, directory: str) -> dict:
+    def load(self, directory: str, **kw) -> dict:
         """Resume parameters and optimizer state (sejong_amd.checkpoint.load_into)."""
         from . import checkpoint
-        return checkpoint.load_into(self, directory)
+        return checkpoint.load_into(self, directory, **kw)
 
     def set_batch(self, ids: np.ndarray, targets: np.ndarray):
         ids = np.ascontiguousarray(ids, dtype=np.int32); tg = np.ascontiguousarray(targets, dtype=np.int32)

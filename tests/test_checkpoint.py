@@ -89,7 +89,8 @@ def test_save_load_round_trip_and_manifest(tmp_path, which):
         opt += [(f"m.{name}", rng.normal(size=shape).astype(np.float32)),
                 (f"v.{name}", rng.random(size=shape).astype(np.float32))]
     d = tmp_path / "run" / "step-00000007"
-    C.save_arrays(d, mc, params, 7, opt, training=None, data_fingerprint="abc", rng_state=12345)
+    C.save_arrays(d, mc, params, 7, opt, training=None, data_fingerprint="abc", rng_state=12345,
+                  half_as_bf16=True)
     assert sorted(os.listdir(d)) == ["manifest.json", "optimizer.safetensors", "weights.safetensors"]
     assert [f for f in os.listdir(d.parent) if f.startswith(".")] == []      # no staging left behind
     m = json.loads((d / "manifest.json").read_text())
@@ -103,47 +104,47 @@ def test_save_load_round_trip_and_manifest(tmp_path, which):
     # the weights file is exactly what the reference's save_tensors writes
     ref = stn.save({name: arr for name, arr in C.split(mc, params)})
     assert (d / "weights.safetensors").read_bytes() == ref
-    mc2, p2, m2, o2 = C.load_arrays(d)
+    mc2, p2, m2, o2 = C.load_arrays(d, half_as_bf16=True)
     assert layout(mc2) == layout(mc) and mc2.precision == mc.precision and mc2.hierarchy == mc.hierarchy
     np.testing.assert_array_equal(p2, params)
     for k, v in opt:
         np.testing.assert_array_equal(o2[k], v)
     # Model::save refuses an existing destination
     with pytest.raises(N.SejongError, match="already exists"):
-        C.save_arrays(d, mc, params, 8)
+        C.save_arrays(d, mc, params, 8, half_as_bf16=True)
 
 
 def test_load_rejects_mismatches(tmp_path):
     mc, _ = _small_cfgs()
     params = init_params(mc, std=0.02)
     d = tmp_path / "ck"
-    C.save_arrays(d, mc, params, 1)
+    C.save_arrays(d, mc, params, 1, half_as_bf16=True)
     m = json.loads((d / "manifest.json").read_text())
     # a tensor missing from the weights file
     named = [(n, a) for n, a in C.split(mc, params) if n != "final_norm"]
     os.remove(d / "weights.safetensors")
     _write(d / "weights.safetensors", named)
     with pytest.raises(ValueError, match="tensor count differs"):
-        C.load_arrays(d)
+        C.load_arrays(d, half_as_bf16=True)
     named.append(("final_norm", np.ones(33, np.float32)))
     os.remove(d / "weights.safetensors")
     _write(d / "weights.safetensors", named)
     with pytest.raises(ValueError, match="final_norm shape or dtype differs"):
-        C.load_arrays(d)
+        C.load_arrays(d, half_as_bf16=True)
     m["format"] = 2
     (d / "manifest.json").write_text(json.dumps(m))
     with pytest.raises(ValueError, match="unsupported artifact format 2"):
-        C.load_arrays(d)
+        C.load_arrays(d, half_as_bf16=True)
     m["format"] = 1
     m["weights"] = "../w.safetensors"
     (d / "manifest.json").write_text(json.dumps(m))
     with pytest.raises(ValueError, match="local basenames"):
-        C.load_arrays(d)
+        C.load_arrays(d, half_as_bf16=True)
     m["weights"] = "weights.safetensors"
     m["model"]["unknown"] = 1
     (d / "manifest.json").write_text(json.dumps(m))
     with pytest.raises(ValueError, match="unknown model configuration"):
-        C.load_arrays(d)
+        C.load_arrays(d, half_as_bf16=True)
 
 
 def test_rng_words_round_trip():
@@ -162,5 +163,26 @@ def test_cfg2_manifest_model_fields():
     mc3, _ = config("cfg3")
     j3 = C.model_config_json(mc3)
     assert j3["hierarchy"]["local_window"] == 128 and j3["hierarchy"]["checkpoint_encoder"] is False
-    back = C.model_config_from_json(j3)
+    back = C.model_config_from_json(j3, half_as_bf16=True)
     assert layout(back) == layout(mc3)
+
+
+def test_half_precision_mapping_is_reported(tmp_path):
+    """A bf16 model is written with the reference's f16 compute dtype and an
+    f16 manifest loads as bf16: both directions warn unless the caller opts
+    in; an f32 model round-trips silently."""
+    import warnings
+    mc, _ = _small_cfgs()
+    assert mc.precision == "bf16"
+    params = init_params(mc, std=0.02)
+    with pytest.warns(C.PrecisionMappingWarning, match="manifest precision f16"):
+        C.save_arrays(tmp_path / "a", mc, params, 1)
+    with pytest.warns(C.PrecisionMappingWarning, match="f16 manifest as a bf16"):
+        mc2, _, _, _ = C.load_arrays(tmp_path / "a")
+    assert mc2.precision == "bf16"
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        C.load_arrays(tmp_path / "a", half_as_bf16=True)
+        mc.precision = "f32"
+        C.save_arrays(tmp_path / "b", mc, params, 1)
+        assert C.load_arrays(tmp_path / "b")[0].precision == "f32"

@@ -28,8 +28,8 @@ def test_adamw_resume_is_bit_exact(tmp_path):
     try:
         for _ in range(2):
             a.train_step()
-        a.save(tmp_path / "ck", rng_state=77)
-        man = b.load(tmp_path / "ck")
+        a.save(tmp_path / "ck", rng_state=77, half_as_bf16=True)
+        man = b.load(tmp_path / "ck", half_as_bf16=True)
         assert man["step"] == 2 and man["rng_state"] == 77 and b.steps() == 2
         ma, va, sa = a.get_adam_state()
         mb, vb, sb = b.get_adam_state()
@@ -50,8 +50,8 @@ def test_sgd_parameter_vjp_resume(tmp_path):
     a, b = _pair(mc, tc, 1)
     try:
         a.train_step()
-        a.save(tmp_path / "ck")
-        b.load(tmp_path / "ck")
+        a.save(tmp_path / "ck", half_as_bf16=True)
+        b.load(tmp_path / "ck", half_as_bf16=True)
         assert b.vjp_info()["rng_state"] == a.vjp_info()["rng_state"]
         a.train_step(); b.train_step()
         np.testing.assert_array_equal(a.get_params(), b.get_params())
@@ -70,10 +70,10 @@ def test_hierarchy_checkpoint_round_trip(tmp_path):
     a, b = _pair(mc, tc, 2)
     try:
         a.train_step()
-        a.save(tmp_path / "ck")
-        mc2, params, man, opt = C.load_arrays(tmp_path / "ck")
+        a.save(tmp_path / "ck", half_as_bf16=True)
+        mc2, params, man, opt = C.load_arrays(tmp_path / "ck", half_as_bf16=True)
         assert mc2.hierarchy == mc.hierarchy and man["model"]["precision"] == "f16"
-        b.load(tmp_path / "ck")
+        b.load(tmp_path / "ck", half_as_bf16=True)
         a.train_step(); b.train_step()
         np.testing.assert_array_equal(a.get_params(), b.get_params())
     finally:

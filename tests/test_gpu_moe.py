@@ -71,14 +71,14 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     LOG, IDS, WTS = empty(M * E, "bf16"), empty(M * K, "i32"), empty(M * K)
     api.sj_router_topk(None, Z.p, d, WR.p, d, M, E, K, LOG.p, IDS.p, WTS.p)
     TOK, SLT = zeros(E * M * K, "i32"), zeros(E * M * K, "i32")
-    CNT, OFF, PS, PP = empty(E, "i32"), empty(E + 1, "i32"), empty(cap, "i32"), empty(M * K, "i32")
+    CNT, OFF, PS, PP = empty(E, "i32"), empty(E + 1, "i32"), zeros(cap, "i32"), empty(M * K, "i32")
     api.sj_route_pack(None, IDS.p, M, K, E, TOK.p, SLT.p, CNT.p, OFF.p, PS.p, PP.p, cap)
-    ZP, ZPT = empty(cap * d, "bf16"), empty(d * cap, "bf16")
+    ZP, ZPT = zeros(cap * d, "bf16"), zeros(d * cap, "bf16")
     api.sj_moe_gather(None, Z.p, d, d, PS.p, K, cap, ZP.p, ZPT.p, cap)
-    G, U, H, HT = empty(cap * F, "bf16"), empty(cap * F, "bf16"), empty(cap * F, "bf16"), empty(F * cap, "bf16")
+    G, U, H, HT = zeros(cap * F, "bf16"), zeros(cap * F, "bf16"), zeros(cap * F, "bf16"), zeros(F * cap, "bf16")
     api.sj_moe_gate_up_fwd(None, OFF.p, E, cap, ZP.p, d, d, WGUT.p, WGUT.at(F * d), d, 2 * F * d, F, G.p, U.p, H.p,
                            F, HT.p, cap)
-    YP = empty(cap * d, "bf16")
+    YP = zeros(cap * d, "bf16")
     api.sj_moe_down_fwd(None, OFF.p, E, cap, H.p, F, F, WDT.p, F, d * F, d, YP.p, d)
     OUT = empty(M * d, "bf16")
     api.sj_moe_combine(None, YP.p, d, d, IDS.p, PP.p, WTS.p, M, K, X1.p, d, OUT.p, d)
@@ -136,18 +136,18 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     dup = rng.normal(0, 1e-3, (M, d)).astype(np.float32).astype(np.float64)
     acc = rng.normal(0, 1e-3, (M, d)).astype(np.float32).astype(np.float64)
     DUP, ACC = dev(dup), dev(acc)
-    DXH, DXL, DXTH, DXTL = (empty(cap * d, "bf16") for _ in range(4))
+    DXH, DXL, DXTH, DXTL = (zeros(cap * d, "bf16") for _ in range(4))
     DWT = empty(M * K)
     api.sj_moe_combine_bwd(None, YP.p, d, d, PS.p, WTS.p, K, cap, DUP.p, d, DXH.p, DXL.p, DXTH.p, DXTL.p, cap, DWT.p)
-    DGH, DGL, DGTH, DGTL = (empty(cap * 2 * F, "bf16") for _ in range(4))
+    DGH, DGL, DGTH, DGTL = (zeros(cap * 2 * F, "bf16") for _ in range(4))
     api.sj_moe_down_bwd_swiglu_p(None, OFF.p, E, cap, DXH.p, DXL.p, d, d, WD.p, d, F * d, F, G.p, U.p, F, DGH.p,
                                  DGL.p, 2 * F, DGTH.p, DGTL.p, cap)
-    DGH2, DGL2 = (empty(cap * 2 * F, "bf16") for _ in range(2))
+    DGH2, DGL2 = (zeros(cap * 2 * F, "bf16") for _ in range(2))
     api.sj_moe_down_bwd_swiglu_p(None, OFF.p, E, cap, DXH.p, DXL.p, d, d, WD.p, d, F * d, F, G.p, U.p, F, DGH2.p,
                                  DGL2.p, 2 * F, None, None, cap)
     DWD = empty(E * F * d)
     api.sj_moe_gemm_dw(None, OFF.p, E, cap, F, d, HT.p, cap, DXTH.p, DXTL.p, cap, DWD.p, d, F * d)
-    DZP = empty(cap * d)
+    DZP = zeros(cap * d)
     api.sj_moe_gemm_rows(None, OFF.p, E, cap, d, 2 * F, DGH.p, DGL.p, 2 * F, WGU.p, 2 * F, d * 2 * F, DZP.p, d, 0)
     DWGU = empty(E * d * 2 * F)
     api.sj_moe_gemm_dw(None, OFF.p, E, cap, d, 2 * F, ZPT.p, cap, DGTH.p, DGTL.p, cap, DWGU.p, 2 * F, d * 2 * F)

@@ -780,3 +780,52 @@ def test_moe_model_gradient_finite_difference():
             worst = max(worst, err)
             assert err < 1e-4, (name, i, fd, g[i])
     print(f"[moe model] worst FD relative error {worst:.2e}")
+
+
+def test_sum_squares_against_exact_sums():
+    """or_sum_squares (the FP64 gradient norm, kernels.py:265-287) against
+    sums it cannot share code with: the closed form sum_{i<=n} i^2 =
+    n(n+1)(2n+1)/6 (exact in FP64 at this n), math.fsum of the squares
+    (correctly rounded) on random, large-magnitude and tiny vectors, and
+    numpy's dot."""
+    n = 100000
+    i = np.arange(1, n + 1, dtype=np.float64)
+    assert O.sum_squares(i) == n * (n + 1) * (2 * n + 1) // 6
+    rng = np.random.default_rng(7)
+    for g in (rng.normal(0, 1, 50001), rng.normal(0, 1e100, 4097) * rng.integers(0, 2, 4097),
+              rng.normal(0, 1e-150, 1000), np.float32(rng.normal(0, 3, 9999)).astype(np.float64)):
+        exact = math.fsum(float(v) * float(v) for v in g)
+        got = O.sum_squares(g)
+        assert abs(got - exact) <= 1e-12 * exact, (got, exact)
+        assert abs(got - float(np.dot(g, g))) <= 1e-12 * exact
+    assert O.sum_squares(np.zeros(0)) == 0.0
+    assert O.sum_squares(np.array([-3.0, 4.0])) == 25.0
+
+
+def test_pvjp_basis_tolerance_hand_values():
+    """pvjp.basis_tolerance against parameter_vjp.rs:214-220 evaluated in
+    exact rational arithmetic: operations = rows (4 rank + 1), roundoff =
+    operations * f32::EPSILON / 2 = operations / 2^24, tolerance = roundoff /
+    (1 - roundoff) = operations / (2^24 - operations) while roundoff < 1,
+    else infinity, then min(., f32::MAX) as f32."""
+    from fractions import Fraction
+
+    from oracle import pvjp
+    f32max = float(np.finfo(np.float32).max)
+
+    def by_hand(rows, rank):
+        ops = rows * (4 * rank + 1)
+        if ops >= 2 ** 24:                       # roundoff >= 1 -> inf -> FLT_MAX
+            return np.float32(f32max)
+        return np.float32(float(Fraction(ops, 2 ** 24 - ops)))
+
+    # literal values: 1 / (2^24 - 1), 4355 / 16772861 (the check program's 67 x 16)
+    assert pvjp.basis_tolerance(1, 0) == np.float32(1.0 / 16777215.0)
+    assert pvjp.basis_tolerance(67, 16) == np.float32(4355.0 / 16772861.0)
+    for rows, rank in [(67, 16), (16384, 16), (4096, 16), (97, 33), (1, 1), (8192, 64), (255, 0)]:
+        assert pvjp.basis_tolerance(rows, rank) == by_hand(rows, rank), (rows, rank)
+    # roundoff exactly 1 (rows 2^24, rank 0) and beyond: the infinity branch clamps to FLT_MAX
+    assert pvjp.basis_tolerance(2 ** 24, 0) == np.float32(f32max)
+    assert pvjp.basis_tolerance(1 << 20, 4) == np.float32(f32max)
+    # one operation short of 1: the largest finite tolerance, 2^24 - 1
+    assert pvjp.basis_tolerance(2 ** 24 - 1, 0) == np.float32(16777215.0)
