@@ -138,6 +138,20 @@ int sj_rmsnorm_bwd_p(void *stream, const uint16_t *x, const uint16_t *w, const f
                      const float *dx_acc, float *dx, float *dw, uint16_t *dx_hi, uint16_t *dx_lo,
                      uint16_t *dx_t_hi, uint16_t *dx_t_lo, long ldt, long rows, long d, float eps,
                      void *workspace, size_t workspace_bytes);
+/* No counterpart in the reference.  sj_rmsnorm_bwd_p without a workspace,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the dw
+ * partials live in a file-scope device array of
+ * SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES per GPU, held until the process ends.
+ * Shapes whose partials (ceil(rows / 16) * d * 4 bytes) exceed it return
+ * SJ_ERR_CAPACITY.  The call allocates nothing (no hipMalloc / hipFree);
+ * results are bit-identical to sj_rmsnorm_bwd_p.  All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU (two streams, two
+ * threads) race. */
+#define SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES (4u << 20)
+int sj_rmsnorm_bwd_p_noalloc(void *stream, const uint16_t *x, const uint16_t *w, const float *dy,
+                             const float *dx_acc, float *dx, float *dw, uint16_t *dx_hi, uint16_t *dx_lo,
+                             uint16_t *dx_t_hi, uint16_t *dx_t_lo, long ldt, long rows, long d, float eps);
 
 /* ----------------------------------------------------------------- GEMM */
 

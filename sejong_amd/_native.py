@@ -102,6 +102,7 @@ SIGNATURES = {
     "sj_rmsnorm_fwd_t": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _F]),
     "sj_rmsnorm_bwd_p_workspace_bytes": (_S, [_L, _L]),
     "sj_rmsnorm_bwd_p": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _F, _P, _S]),
+    "sj_rmsnorm_bwd_p_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _F]),
     "sj_route_topk": (_I, [_P, _P, _I, _L, _L, _L, _P, _P]),
     "sj_router_topk": (_I, [_P, _P, _L, _P, _L, _L, _L, _L, _P, _P, _P]),
     "sj_route_topk_bwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _L, _L, _L]),

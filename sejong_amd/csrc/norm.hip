@@ -5,6 +5,8 @@
 // pass (deterministic, no atomics -- the reference's partial/reduce split).
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 using namespace sj;
@@ -554,4 +556,49 @@ extern "C" int sj_rmsnorm_bwd_p(void* stream, const uint16_t* x, const uint16_t*
                      groups, d);
   SJ_LAUNCH_CHECK("rmsnorm_backward_p");
   return SJ_OK;
+}
+
+// ------------------------------------------------ allocation-free backward
+// sj_rmsnorm_bwd_p_noalloc keeps the dw partials in this file-scope array
+// instead of a caller workspace.  Host code never passes `scratch` itself to
+// a kernel (in host code the name is a stand-in, not a device address): the
+// first call on each device resolves the device's own copy with
+// hipGetSymbolAddress, and every launch takes that pointer.
+namespace {
+constexpr size_t NOALLOC_FLOATS = SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES / sizeof(float);
+constexpr int NOALLOC_DEVICES = 64;
+std::mutex g_noalloc_mu;
+float* g_noalloc_ptr[NOALLOC_DEVICES] = {};
+}  // namespace
+static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
+
+extern "C" int sj_rmsnorm_bwd_p_noalloc(void* stream, const uint16_t* x, const uint16_t* w, const float* dy,
+                                        const float* dx_acc, float* dx, float* dw, uint16_t* dx_hi, uint16_t* dx_lo,
+                                        uint16_t* dx_t_hi, uint16_t* dx_t_lo, long ldt, long rows, long d,
+                                        float eps) {
+  SJ_REQUIRE(rows > 0 && d > 0, "RMSNorm backward (no allocation): rows %ld d %ld", rows, d);
+  const size_t need = sj_rmsnorm_bwd_p_workspace_bytes(rows, d);
+  if (need > SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES)
+    return sjh::fail(SJ_ERR_CAPACITY,
+                     "rmsnorm_backward (no allocation): required %zu bytes of scratch, available %zu bytes "
+                     "(ceil(rows / 16) * d * 4 must not exceed SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES)",
+                     need, (size_t)SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES);
+  int dev = 0;
+  SJ_HIP(hipGetDevice(&dev));
+  SJ_REQUIRE(dev >= 0 && dev < NOALLOC_DEVICES, "RMSNorm backward (no allocation): device %d", dev);
+  float* part = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+      void* p = nullptr;
+      hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return sjh::hip_check(e, "rmsnorm_backward (no allocation): hipGetSymbolAddress");
+      g_noalloc_ptr[dev] = (float*)p;
+    }
+    part = g_noalloc_ptr[dev];
+  }
+  // every partial entry [ceil(rows / 16)][d] is written by the row kernel
+  // before the reduce reads it, so nothing needs clearing between calls
+  return sj_rmsnorm_bwd_p(stream, x, w, dy, dx_acc, dx, dw, dx_hi, dx_lo, dx_t_hi, dx_t_lo, ldt, rows, d, eps, part,
+                          need);
 }

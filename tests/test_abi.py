@@ -119,3 +119,14 @@ def test_pvjp_host_cost_model_matches_oracle():
                     assert bool(got) == pvjp.selects_compression(rank, frac, br, n, a, b, donor, uses)
     for rows, rank in ((67, 33), (16384, 16), (10 ** 8, 64)):
         assert lib.sj_pvjp_basis_tolerance(rows, rank) == np.float32(pvjp.basis_tolerance(rows, rank))
+
+
+def test_noalloc_rejects_oversize_before_any_device_call():
+    # the capacity check runs on the host before the device is touched
+    import ctypes
+
+    from sejong_amd import _native as N
+    lib = N.load()
+    st = lib.sj_rmsnorm_bwd_p_noalloc(None, None, None, None, None, None, None, None, None, None, None, 0,
+                                      16 * 1025, 1024, ctypes.c_float(1e-6))
+    assert st == 2 and b"SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES" in lib.sj_last_error()
