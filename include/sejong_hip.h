@@ -283,6 +283,17 @@ int sj_attention_fwd(void *stream, const void *q, long ldq, const void *k, long 
  * (sj_rope_table) the inverse RoPE (rope backward, graph.rs:879-882) is
  * applied to dQ and dK before they are stored.  delta: fp32 [B*T*HQ]
  * scratch/output (Delta of each query row). */
+/* Engine::attention_grouped with an offset (hierarchy_ops.rs:10-70, kernel
+ * hierarchy_attention hierarchy.py:7-39 with OFFSET) as the KV-cache path
+ * calls it (architecture.rs:483-497): tq query rows q [tq][ldq] of one
+ * sequence at positions offset .. offset+tq-1 against the keys and values of
+ * positions 0 .. offset+tq-1, k / v [capacity][ldkv]; causal, optional
+ * window.  A row is computed with the operations of the full forward
+ * (sj_attention_fwd_tt for bf16 head_dim 64, the row kernel otherwise), so
+ * cached and full outputs agree bit for bit.  No LSE (inference). */
+int sj_attention_fwd_cached(void *stream, const void *q, long ldq, const void *k, const void *v, long ldkv,
+                            long capacity, int dtype, long tq, long offset, long hq, long hk, long head_dim,
+                            long window, void *o, long ldo);
 int sj_attention_bwd(void *stream, const void *q, long ldq, const void *k, long ldk,
                      const void *v, long ldv, const void *o, long ldo, const float *lse,
                      const float *dout, long lddo, float *dq, long lddq, float *dk, long lddk,
@@ -757,6 +768,29 @@ int sj_model_use_graph(sj_model *m, int on);
  * model stream).  Returns SJ_ERR_NONFINITE if the last update saw a
  * non-finite norm. */
 int sj_model_read_loss(sj_model *m, double *loss, double *grad_norm);
+/* Forward only (Model::logits + Graph::cross_entropy, model lib.rs:336-340,
+ * graph.rs:539-549): the loss of the staged batch without a backward or an
+ * update -- the `evaluate` pass of the benchmark (benchmark.rs:71-99: BPB =
+ * mean loss / ln 2).  Read the loss with sj_model_read_loss. */
+int sj_model_forward(sj_model *m);
+
+/* KV cache (Cache, model lib.rs:36-50; Model::new_cache / forward_cached /
+ * hidden_cached, lib.rs:359-394; architecture.rs:428-533 and 758-799) for
+ * the byte language models (dense and MoE; bf16 on the MFMA layout or
+ * fp32): per layer the keys and values of one sequence, [capacity][HK *
+ * head_dim] in the compute dtype.  sj_model_forward_cached runs n new tokens
+ * (host array, bytes or EOS) at positions length .. length+n-1 through the
+ * blocks with the training forward's kernels, writes the keys and values
+ * into the cache, and leaves the fp32 logits of the last token in
+ * `logits` (device, [vocab]; nullable).  Errors: "KV cache context limit
+ * reached" past the capacity, "input tokens must be bytes or EOS". */
+typedef struct sj_cache sj_cache;
+int sj_cache_create(sj_model *m, long capacity, sj_cache **out);
+int sj_cache_destroy(sj_cache *c);
+int sj_cache_reset(sj_cache *c);
+long sj_cache_length(const sj_cache *c);
+int sj_model_forward_cached(sj_model *m, sj_cache *c, const int32_t *tokens, long n, float *logits);
+
 /* Per-op timing (the reference's kernel-profile feature, crates/sejong-gpu/
  * src/lib.rs:451-482 and counters.rs:33-56): with profiling on, steps run
  * eagerly and every op is bracketed by a HIP event pair on the model stream.

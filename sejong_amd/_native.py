@@ -205,6 +205,13 @@ SIGNATURES = {
     "sj_model_forward_backward": (_I, [_P]),
     "sj_model_train_step": (_I, [_P, _F]),
     "sj_model_use_graph": (_I, [_P, _I]),
+    "sj_model_forward": (_I, [_P]),
+    "sj_cache_create": (_I, [_P, _L, ctypes.POINTER(_P)]),
+    "sj_cache_destroy": (_I, [_P]),
+    "sj_cache_reset": (_I, [_P]),
+    "sj_cache_length": (_L, [_P]),
+    "sj_model_forward_cached": (_I, [_P, _P, _P, _L, _P]),
+    "sj_attention_fwd_cached": (_I, [_P, _P, _L, _P, _P, _L, _L, _I, _L, _L, _L, _L, _L, _L, _P, _L]),
     "sj_model_read_loss": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "sj_model_profile": (_I, [_P, _I]),
     "sj_model_profile_collect": (_L, [_P]),

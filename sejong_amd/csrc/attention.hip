@@ -946,13 +946,19 @@ struct RowArgs {
   int dt;
   long B, T, HQ, HK, D, window;
   const float* rope;
+  long offset;  // cached forward: T query rows at positions offset .. offset+T-1, keys 0 .. offset+T-1
 };
 
+// CACHED: the query rows of one sequence continue a KV cache (hierarchy.py:
+// 7-39 with OFFSET): row r sits at position offset + r and reads key rows
+// 0 .. offset + r; each row takes the same operations in the same order as
+// in the full forward, so the two agree bit for bit.
+template <bool CACHED>
 __global__ __launch_bounds__(256) void k_attn_fwd_rows(RowArgs a) {
   const int lane = threadIdx.x & 63;
   const long row = blockIdx.x * 4L + (threadIdx.x >> 6);  // (b*T + pos)*HQ + h
   if (row >= a.B * a.T * a.HQ) return;
-  const long h = row % a.HQ, bt = row / a.HQ, pos = bt % a.T, b = bt / a.T;
+  const long h = row % a.HQ, bt = row / a.HQ, pos = CACHED ? a.offset + bt : bt % a.T, b = CACHED ? 0 : bt / a.T;
   const long kvh = h / (a.HQ / a.HK);
   const float scale = 1.f / sqrtf((float)a.D);
   float q[2], acc[2] = {0.f, 0.f};
@@ -984,7 +990,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd_rows(RowArgs a) {
     long d = lane + 64 * i;
     if (d < a.D) store_from_f32(a.out, a.dt, bt * a.ldo + h * a.D + d, acc[i] / l);
   }
-  if (lane == 0) a.lse[row] = m + logf(l);
+  if (!CACHED && lane == 0) a.lse[row] = m + logf(l);
 }
 
 __device__ __forceinline__ void inv_rope_store(float* dst, const float* rope, long pos, long D, int lane, float x0,
@@ -1127,9 +1133,35 @@ extern "C" int sj_attention_fwd(void* stream, const void* q, long ldq, const voi
     a.out = o; a.lse = lse; a.dt = dtype; a.B = batch; a.T = t; a.HQ = hq; a.HK = hk; a.D = head_dim;
     a.window = window;
     long rows = batch * t * hq;
-    hipLaunchKernelGGL(k_attn_fwd_rows, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_attn_fwd_rows<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
   }
   SJ_LAUNCH_CHECK("hierarchy_attention");
+  return SJ_OK;
+}
+
+extern "C" int sj_attention_fwd_cached(void* stream, const void* q, long ldq, const void* k, const void* v, long ldkv,
+                                       long capacity, int dtype, long tq, long offset, long hq, long hk, long head_dim,
+                                       long window, void* o, long ldo) {
+  SJ_REQUIRE(dtype == SJ_F32 || dtype == SJ_BF16, "grouped attention dtype %d", dtype);
+  SJ_REQUIRE(q && k && v && o && tq > 0 && offset >= 0 && offset + tq <= capacity && hq > 0 && hk > 0 &&
+                 hq % hk == 0 && head_dim > 0 && head_dim <= 128 && head_dim % 2 == 0 && window >= 0 &&
+                 ldq >= hq * head_dim && ldo >= hq * head_dim && ldkv >= hk * head_dim,
+             "grouped attention sequence/head dimensions (cached: offset %ld + rows %ld <= capacity %ld)", offset, tq,
+             capacity);
+  hipStream_t s = (hipStream_t)stream;
+  const bool mfma = dtype == SJ_BF16 && head_dim == 64 && ldq % 8 == 0 && ldkv % 8 == 0 && ldo % 8 == 0 &&
+                    ((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 &&
+                    ((uintptr_t)o & 15) == 0;
+  if (mfma)
+    return sjh::attention_fwd_cached_t(stream, (const uint16_t*)q, ldq, (const uint16_t*)k, (const uint16_t*)v, ldkv,
+                                       capacity, tq, offset, hq, hk, window, (uint16_t*)o, ldo);
+  RowArgs a = {};
+  a.q = q; a.k = k; a.v = v; a.ldq = ldq; a.ldk = ldkv; a.ldv = ldkv; a.ldo = ldo;
+  a.out = o; a.dt = dtype; a.B = 1; a.T = tq; a.HQ = hq; a.HK = hk; a.D = head_dim;
+  a.window = window; a.offset = offset;
+  long rows = tq * hq;
+  hipLaunchKernelGGL(k_attn_fwd_rows<true>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, a);
+  SJ_LAUNCH_CHECK("hierarchy_attention (cached)");
   return SJ_OK;
 }
 

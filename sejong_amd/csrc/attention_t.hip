@@ -173,6 +173,12 @@ struct TArgs {
   long ldg, ldgt;
   float* part;  // [group][M][2*HK*64] per-head dK | dV
   int B;        // batch (rows M = B * T)
+  // cached forward (one sequence): queries at positions pos0 .. pos0+nq-1
+  // in qc [nq][ldqc]; keys and values of positions 0 .. pos0+nq-1 in kc / vc
+  // [capacity][ldkc]; query blocks qb0 .. qb0 + gridDim.x - 1
+  const bf16_t *qc, *kc, *vc;
+  long ldqc, ldkc;
+  int pos0, nq, qb0;
 };
 
 // DMA of one 64 x 64 bf16 tile (rows r of `src` with stride ld, 8 chunks of
@@ -215,32 +221,52 @@ __device__ __forceinline__ WgMap wg_map(int roles) {
 }
 
 // ------------------------------------------------------------------ forward
-template <int NS>
-__global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
+// CACHED: the same per-row arithmetic over a KV cache (Model::forward_cached,
+// architecture.rs:474-533): query block qb holds the 64 positions qb*64 ..
+// +63, of which pos0 .. pos0+nq-1 are real (read from qc, written to o at
+// row position - pos0); key rows at or past pos0+nq load as zeros.  A real
+// query sees the same key blocks, masks and operation order as in the full
+// forward, so cached and full outputs agree bit for bit.
+template <int NS, bool CACHED>
+__device__ __forceinline__ void attn2_fwd_body(const TArgs& a, bf16_t* lds) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int g = lane >> 4, j = lane & 15;
   const WgMap wm = wg_map(1);
-  const int qb = (int)gridDim.x - 1 - wm.r;  // longest blocks first
+  const int qb = (CACHED ? a.qb0 : 0) + (int)gridDim.x - 1 - wm.r;  // longest blocks first
   const int h = wm.h, b = wm.b;
   const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
   const int kvh = h / (a.HQ / a.HK);
   const int qloc = wave * 16 + j, myq = qb * QB + qloc;
-  const long row0 = (long)b * T;
+  const long row0 = CACHED ? 0 : (long)b * T;
   const float sc = 0.125f * LOG2E;
+  const bool qreal = !CACHED || (myq >= a.pos0 && myq < a.pos0 + a.nq);
+  const int klen = CACHED ? a.pos0 + a.nq : 0;
 
   bf16x8 qf[2];
 #pragma unroll
-  for (int c = 0; c < 2; c++) qf[c] = as_bf8(*(const u32x4*)(a.qkv + (row0 + myq) * a.ldqkv + h * DH + 32 * c + 8 * g));
+  for (int c = 0; c < 2; c++) {
+    if constexpr (CACHED)
+      qf[c] = qreal ? as_bf8(*(const u32x4*)(a.qc + (long)(myq - a.pos0) * a.ldqc + h * DH + 32 * c + 8 * g))
+                    : as_bf8(u32x4{0u, 0u, 0u, 0u});
+    else
+      qf[c] = as_bf8(*(const u32x4*)(a.qkv + (row0 + myq) * a.ldqkv + h * DH + 32 * c + 8 * g));
+  }
 
-  const bf16_t* ksrc = a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
-  const bf16_t* vsrc = ksrc + NK;
+  const long ldk = CACHED ? a.ldkc : a.ldqkv;
+  const bf16_t* ksrc = CACHED ? a.kc + kvh * DH : a.qkv + row0 * a.ldqkv + NQ + kvh * DH;
+  const bf16_t* vsrc = CACHED ? a.vc + kvh * DH : ksrc + NK;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   auto issue = [&](int kb, int buf) {
     const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
-    dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
-    dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
+    if constexpr (CACHED) {
+      auto valid = [&](int r) { return kb * QB + r < klen; };
+      dma_tile(ksrc + (long)kb * QB * ldk, ldk, st, wave_s, lane, valid);
+      dma_tile(vsrc + (long)kb * QB * ldk, ldk, st + TBYTES, wave_s, lane, valid);
+    } else {
+      dma_tile(ksrc + (long)kb * QB * ldk, ldk, st, wave_s, lane, [](int) { return true; });
+      dma_tile(vsrc + (long)kb * QB * ldk, ldk, st + TBYTES, wave_s, lane, [](int) { return true; });
+    }
   };
   f32x4 o[4];
 #pragma unroll
@@ -323,6 +349,16 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
     }
   }
   const float il = 1.f / l;
+  if constexpr (CACHED) {
+    if (!qreal) return;
+    bf16_t* orow = a.o + (long)(myq - a.pos0) * a.ldo + h * DH;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      const float v0 = o[d][0] * il, v1 = o[d][1] * il, v2 = o[d][2] * il, v3 = o[d][3] * il;
+      *(u32x2*)(orow + 16 * d + 4 * g) = u32x2{cvt2(v0, v1), cvt2(v2, v3)};
+    }
+    return;
+  }
   bf16_t* orow = a.o + (row0 + myq) * a.ldo + h * DH;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
@@ -342,6 +378,16 @@ __global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
     if (a.lse) a.lse[(row0 + myq) * a.HQ + h] = lse;
     a.lse_t[(long)h * a.ldt + row0 + myq] = lse;
   }
+}
+template <int NS>
+__global__ __launch_bounds__(256) void k_attn2_fwd(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
+  attn2_fwd_body<NS, false>(a, lds);
+}
+template <int NS>
+__global__ __launch_bounds__(256) void k_attn2_fwd_cached(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];  // NS x [K | V]
+  attn2_fwd_body<NS, true>(a, lds);
 }
 
 // ------------------------------------------------------------- backward dQ
@@ -666,6 +712,9 @@ int sjh::attention_t_prepare() {
   done = 1;
   hipError_t e = hipFuncSetAttribute((const void*)k_attn2_fwd<NS_FWD>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FWD);
   if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_fwd_cached<NS_FWD>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)LDS_FWD);
+  if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_bwd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BWD);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_bwd_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
@@ -698,6 +747,27 @@ extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv
   hipLaunchKernelGGL(k_attn2_fwd<NS_FWD>, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
                      (hipStream_t)stream, a);
   SJ_LAUNCH_CHECK("hierarchy_attention");
+  return SJ_OK;
+}
+
+// cached forward on the MFMA layout (one sequence; see attn2_fwd_body)
+int sjh::attention_fwd_cached_t(void* stream, const uint16_t* q, long ldq, const uint16_t* k, const uint16_t* v,
+                                long ldkv, long capacity, long tq, long offset, long hq, long hk, long window,
+                                uint16_t* o, long ldo) {
+  SJ_REQUIRE(tq > 0 && offset >= 0 && offset + tq <= capacity && capacity < (1L << 30) &&
+                 (long)capacity * ldkv < (1L << 31) && hq % hk == 0 && ldq >= hq * DH && ldkv >= hk * DH &&
+                 ldo >= hq * DH,
+             "grouped attention (cached, MFMA layout): shapes");
+  if (int st = sjh::attention_t_prepare()) return st;
+  TArgs a = {};
+  a.T = (int)(offset + tq); a.HQ = (int)hq; a.HK = (int)hk; a.window = (int)window; a.B = 1;
+  a.qc = (const bf16_t*)q; a.ldqc = ldq; a.kc = (const bf16_t*)k; a.vc = (const bf16_t*)v; a.ldkc = ldkv;
+  a.pos0 = (int)offset; a.nq = (int)tq; a.qb0 = (int)(offset / QB);
+  a.o = (bf16_t*)o; a.ldo = ldo;
+  const long nb = (offset + tq - 1) / QB - offset / QB + 1;
+  hipLaunchKernelGGL(k_attn2_fwd_cached<NS_FWD>, dim3((unsigned)nb, (unsigned)hq, 1u), dim3(256), LDS_FWD,
+                     (hipStream_t)stream, a);
+  SJ_LAUNCH_CHECK("hierarchy_attention (cached)");
   return SJ_OK;
 }
 

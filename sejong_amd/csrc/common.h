@@ -118,6 +118,13 @@ int factored_update_staged(hipStream_t stream, const void* meta, long tiles, con
 // attention over transposed operands (attention_t.hip) and the group reduce
 // of the per-head dK | dV partials it shares with attention.hip
 int attention_t_prepare();
+// project_qkv (MFMA layout) into separate q, k, v buffers
+int qkv_fwd_t_out(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t, long ldw, long N,
+                  long KV, uint16_t* q, long ldq, uint16_t* k, long ldk, uint16_t* v, long ldv, const float* rope_table,
+                  long rope_t, long head_dim, uint16_t* qkv_t, long ldqt);
+// cached grouped attention on the MFMA layout (bf16, head_dim 64), one sequence
+int attention_fwd_cached_t(void* stream, const uint16_t* q, long ldq, const uint16_t* k, const uint16_t* v, long ldkv,
+                           long capacity, long tq, long offset, long hq, long hk, long window, uint16_t* o, long ldo);
 int attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
                         const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi, uint16_t* gt_lo,
                         long ldgt);

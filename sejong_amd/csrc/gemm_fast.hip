@@ -1139,12 +1139,15 @@ extern "C" int sj_gemm_planes_split_out(void* stream, long M, long N, long K, co
   return SJ_OK;
 }
 
-extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t,
-                            long ldw, long N, long KV, uint16_t* qkv, long ldo, const float* rope_table, long rope_t,
-                            long head_dim, uint16_t* qkv_t, long ldqt) {
+// project_qkv with q, k, v written to separate buffers (the KV-cache path
+// puts k and v straight into the cache rows)
+int sjh::qkv_fwd_t_out(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t, long ldw,
+                       long N, long KV, uint16_t* q, long ldq, uint16_t* k, long ldk, uint16_t* v, long ldv,
+                       const float* rope_table, long rope_t, long head_dim, uint16_t* qkv_t, long ldqt) {
   if (int st0 = sjh::gemm_fast_prepare()) return st0;
-  SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D &&
-                 ldo >= N + 2 * KV && N % 64 == 0 && KV % 64 == 0 && ok16(x) && ok16(wqkv_t),
+  SJ_REQUIRE(M >= 0 && D > 0 && D % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0 && ldx >= D && ldw >= D && ldq >= N &&
+                 ldk >= KV && ldv >= KV && ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && N % 64 == 0 &&
+                 KV % 64 == 0 && ok16(x) && ok16(wqkv_t) && ok16(q) && ok16(k) && ok16(v),
              "project_qkv (transposed weights): shape/alignment");
   if (rope_table) SJ_REQUIRE(rope_t > 0 && head_dim > 0 && head_dim % 2 == 0 && N % head_dim == 0 && KV % head_dim == 0 &&
                                  M < (1L << 31),
@@ -1156,14 +1159,14 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
   p.b[0][0] = w; p.b[0][1] = w + N * ldw; p.b[0][2] = w + (N + KV) * ldw;
   p.ldb[0] = p.ldb[1] = p.ldb[2] = ldw;
   p.seg_n[0] = 0; p.seg_n[1] = N; p.seg_n[2] = N + KV; p.nseg = 3;
-  bf16_t* o = (bf16_t*)qkv;
-  p.c[0] = o; p.c[1] = o + N; p.c[2] = o + N + KV;
-  p.ldc[0] = p.ldc[1] = p.ldc[2] = ldo;
+  p.c[0] = q; p.c[1] = k; p.c[2] = v;
+  p.ldc[0] = ldq; p.ldc[1] = ldk; p.ldc[2] = ldv;
   p.M = M; p.N = N + 2 * KV; p.K = D; p.c_bf16 = 1;
   p.rope = rope_table; p.rope_t = rope_t > 0 ? rope_t : 1; p.head_dim = head_dim > 0 ? head_dim : 2;
   p.rope_cols = rope_table ? N + KV : 0;
   if (qkv_t) {
-    SJ_REQUIRE(ldqt >= M && ldqt % 8 == 0 && ok16(qkv_t), "project_qkv transposed output: ld %ld", ldqt);
+    SJ_REQUIRE(ldq == ldk && ldq == ldv && k == q + N && v == q + N + KV && ldqt >= M && ldqt % 8 == 0 && ok16(qkv_t),
+               "project_qkv transposed output: ld %ld (one q|k|v buffer)", ldqt);
     p.c[3] = qkv_t;
     p.ldc[3] = ldqt;
   }
@@ -1177,6 +1180,14 @@ extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, l
   if (st) return st;
   SJ_LAUNCH_CHECK("project_qkv");
   return SJ_OK;
+}
+
+extern "C" int sj_qkv_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t,
+                            long ldw, long N, long KV, uint16_t* qkv, long ldo, const float* rope_table, long rope_t,
+                            long head_dim, uint16_t* qkv_t, long ldqt) {
+  SJ_REQUIRE(ldo >= N + 2 * KV && ldo % 8 == 0 && ok16(qkv), "project_qkv (transposed weights): shape/alignment");
+  return sjh::qkv_fwd_t_out(stream, x, ldx, M, D, wqkv_t, ldw, N, KV, qkv, ldo, qkv + N, ldo, qkv + N + KV, ldo,
+                            rope_table, rope_t, head_dim, qkv_t, ldqt);
 }
 
 extern "C" int sj_gate_up_fwd_t(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wg_t,

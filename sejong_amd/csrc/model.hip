@@ -2091,3 +2091,202 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   if (elements) *elements = n;
   return SJ_OK;
 }
+
+// ------------------------------------------------------------ KV cache
+// Model::new_cache / forward_cached (model lib.rs:36-50, 359-394;
+// architecture.rs:428-533, 758-799): per layer the keys and values of one
+// sequence, [capacity][HK * head_dim] in the compute dtype, and scratch for
+// up to `capacity` new rows.  A call runs the blocks over the new tokens at
+// positions length .. length + n - 1 with the same kernels as the training
+// forward (RoPE rows of a table over the capacity, the cached attention
+// kernels reading the cache), so each row is computed exactly as in the full
+// forward; then the final norm and the fp32 head on the last row.
+struct sj_cache {
+  sj_model* m = nullptr;
+  long capacity = 0, length = 0;
+  std::vector<void*> keys, values;  // [layer] -> [capacity][J]
+  float* rope = nullptr;            // [capacity][Dh/2] (cos, sin)
+  void *x[2] = {}, *z = nullptr, *q = nullptr, *o = nullptr, *x1 = nullptr, *z2 = nullptr;
+  void *gg = nullptr, *uu = nullptr, *hh = nullptr, *hn = nullptr;
+  int32_t* ids = nullptr;
+  float* logits = nullptr;  // [Vp] fp32, the last row's
+  // mixture of experts: routing and packed rows for up to `capacity` tokens
+  long mcap = 0;
+  uint16_t *mlog = nullptr, *mzp = nullptr, *myp = nullptr;
+  int32_t *mids = nullptr, *mcnt = nullptr, *moff = nullptr, *mps = nullptr, *mpp = nullptr;
+  float* mwts = nullptr;
+  std::vector<void*> allocations;
+};
+
+namespace {
+int calloc_(sj_cache* c, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) {
+    size_t fr = 0, tot = 0;
+    hipMemGetInfo(&fr, &tot);
+    return sjh::fail(SJ_ERR_CAPACITY, "cache allocation: required %zu bytes, available %zu bytes", bytes, fr);
+  }
+  c->allocations.push_back(*p);
+  return hipMemset(*p, 0, bytes) == hipSuccess ? SJ_OK : sjh::fail(SJ_ERR_HIP, "cache allocation: clear");
+}
+
+// the blocks of the dense (or MoE) stage over n new rows at offset L; `top`
+// receives the index of the stage output in c->x
+int cached_blocks(sj_model* m, sj_cache* c, long n, long L, int& top) {
+  const Stage& S = m->stages[0];
+  hipStream_t s = m->stream;
+  const long d = S.d, J = S.J, F = S.F, cap = c->capacity;
+  const int dt = m->dt;
+  const size_t es = m->esz;
+  const float eps = m->c.norm_epsilon;
+  const float* rope = c->rope + L * S.Dh;  // row r of this view is position L + r
+  const long rope_t = cap - L;
+  int cur = 0;
+  for (long l = S.first; l < S.first + S.count; l++) {
+    const Layer& y = m->layers[l];
+    void* x = c->x[cur];
+    void* xo = c->x[cur ^ 1];
+    char* kc = (char*)c->keys[l] + L * J * es;
+    char* vc = (char*)c->values[l] + L * J * es;
+    if (m->planes) {
+      const uint16_t *W = m->mirror, *WT = m->mirror_t;
+      TRY(sj_rmsnorm_fwd_t(s, (const uint16_t*)x, W + y.an, (uint16_t*)c->z, nullptr, 0, n, d, eps));
+      TRY(sjh::qkv_fwd_t_out(s, (const uint16_t*)c->z, d, n, d, WT + y.qkv, d, d, J, (uint16_t*)c->q, d,
+                             (uint16_t*)kc, J, (uint16_t*)vc, J, rope, rope_t, S.Dh, nullptr, 0));
+      TRY(sj_attention_fwd_cached(s, c->q, d, c->keys[l], c->values[l], J, cap, dt, n, L, S.HQ, S.HK, S.Dh, S.window,
+                                  c->o, d));
+      TRY(sj_linear_residual_fwd_t(s, (const uint16_t*)c->o, d, n, d, WT + y.wo, d, d, (const uint16_t*)x, d,
+                                   (uint16_t*)c->x1, d));
+      TRY(sj_rmsnorm_fwd_t(s, (const uint16_t*)c->x1, W + y.fn, (uint16_t*)c->z2, nullptr, 0, n, d, eps));
+      if (m->E) {  // routed experts over the new rows (architecture.rs:516-529)
+        const long E = m->E, K = m->K, mc = sj_route_pack_capacity(n * K, E);
+        TRY(sj_router_topk(s, (const uint16_t*)c->z2, d, W + y.router, d, n, E, K, c->mlog, c->mids, c->mwts));
+        TRY(sj_route_pack(s, c->mids, n, K, E, nullptr, nullptr, c->mcnt, c->moff, c->mps, c->mpp, mc));
+        TRY(sj_moe_gather(s, (const uint16_t*)c->z2, d, d, c->mps, K, mc, c->mzp, nullptr, mc));
+        TRY(sj_moe_gate_up_fwd(s, c->moff, E, mc, c->mzp, d, d, WT + y.gu, WT + y.gu + F * d, d, 2 * F * d, F,
+                               (uint16_t*)c->gg, (uint16_t*)c->uu, (uint16_t*)c->hh, F, nullptr, mc));
+        TRY(sj_moe_down_fwd(s, c->moff, E, mc, (const uint16_t*)c->hh, F, F, WT + y.down, F, d * F, d, c->myp, d));
+        TRY(sj_moe_combine(s, c->myp, d, d, c->mids, c->mpp, c->mwts, n, K, (const uint16_t*)c->x1, d,
+                           (uint16_t*)xo, d));
+      } else {
+        TRY(sj_gate_up_fwd_t(s, (const uint16_t*)c->z2, d, n, d, WT + y.gu, WT + y.gu + F * d, d, F,
+                             (uint16_t*)c->gg, (uint16_t*)c->uu, (uint16_t*)c->hh, F, nullptr, 0));
+        TRY(sj_linear_residual_fwd_t(s, (const uint16_t*)c->hh, F, n, F, WT + y.down, F, d, (const uint16_t*)c->x1, d,
+                                     (uint16_t*)xo, d));
+      }
+    } else {
+      TRY(sj_rmsnorm_fwd(s, x, dt, wc(m, y.an), dt, c->z, n, d, eps));
+      const char* wq = (const char*)wc(m, y.qkv);
+      const long NQ = S.NQKV;
+      TRY(sj_qkv_fwd(s, c->z, d, n, d, wq, NQ, wq + d * es, NQ, wq + (d + J) * es, NQ, d, J, c->q, d, kc, J, vc, J, dt,
+                     rope, rope_t, S.Dh));
+      TRY(sj_attention_fwd_cached(s, c->q, d, c->keys[l], c->values[l], J, cap, dt, n, L, S.HQ, S.HK, S.Dh, S.window,
+                                  c->o, d));
+      TRY(sj_linear_residual_fwd(s, c->o, d, n, d, wc(m, y.wo), d, d, x, d, c->x1, d, dt));
+      TRY(sj_rmsnorm_fwd(s, c->x1, dt, wc(m, y.fn), dt, c->z2, n, d, eps));
+      const char* wg = (const char*)wc(m, y.gu);
+      TRY(sj_gate_up_fwd(s, c->z2, d, n, d, wg, 2 * F, wg + F * es, 2 * F, F, c->gg, c->uu, c->hh, F, dt));
+      TRY(sj_linear_residual_fwd(s, c->hh, F, n, F, wc(m, y.down), d, d, c->x1, d, xo, d, dt));
+    }
+    cur ^= 1;
+  }
+  top = cur;
+  return SJ_OK;
+}
+}  // namespace
+
+extern "C" int sj_cache_create(sj_model* m, long capacity, sj_cache** out) {
+  SJ_REQUIRE(m && out && capacity > 0, "new_cache: arguments");
+  SJ_REQUIRE(!m->hier && !m->value_n, "new_cache: the cached forward covers the byte language models (dense, MoE)");
+  const Stage& S = m->stages[0];
+  SJ_REQUIRE(m->planes ? S.attn_tt : m->dt == SJ_F32,
+             "new_cache: the cached forward needs the MFMA-layout attention (bf16) or fp32 storage");
+  sj_cache* c = new sj_cache();
+  c->m = m;
+  c->capacity = capacity;
+  const size_t es = m->esz;
+  const long d = S.d, J = S.J, F = S.F;
+  int st = SJ_OK;
+  auto A = [&](void** p, size_t bytes) {
+    if (!st) st = calloc_(c, p, bytes);
+  };
+  c->keys.assign(m->L, nullptr);
+  c->values.assign(m->L, nullptr);
+  for (long l = 0; l < m->L; l++) {
+    A(&c->keys[l], (size_t)capacity * J * es);
+    A(&c->values[l], (size_t)capacity * J * es);
+  }
+  A((void**)&c->rope, (size_t)capacity * S.Dh * 4);
+  for (void** p : {&c->x[0], &c->x[1], &c->z, &c->q, &c->o, &c->x1, &c->z2, &c->hn}) A(p, (size_t)capacity * d * es);
+  if (m->E) {
+    c->mcap = sj_route_pack_capacity(capacity * m->K, m->E);
+    const long E = m->E, K = m->K, mc = c->mcap;
+    A((void**)&c->mlog, (size_t)capacity * E * 2);
+    A((void**)&c->mids, (size_t)capacity * K * 4);
+    A((void**)&c->mwts, (size_t)capacity * K * 4);
+    A((void**)&c->mcnt, (size_t)E * 4);
+    A((void**)&c->moff, (size_t)(E + 1) * 4);
+    A((void**)&c->mps, (size_t)mc * 4);
+    A((void**)&c->mpp, (size_t)capacity * K * 4);
+    A((void**)&c->mzp, (size_t)mc * d * 2);
+    A((void**)&c->myp, (size_t)mc * d * 2);
+    for (void** p : {&c->gg, &c->uu, &c->hh}) A(p, (size_t)mc * F * es);
+  } else {
+    for (void** p : {&c->gg, &c->uu, &c->hh}) A(p, (size_t)capacity * F * es);
+  }
+  A((void**)&c->ids, (size_t)capacity * 4);
+  A((void**)&c->logits, (size_t)m->Vp * 4);
+  if (!st) st = sj_rope_table(m->stream, c->rope, capacity, S.Dh, m->c.rope_theta);
+  if (!st && hipStreamSynchronize(m->stream) != hipSuccess) st = sjh::fail(SJ_ERR_HIP, "new_cache: sync");
+  if (st) {
+    sj_cache_destroy(c);
+    return st;
+  }
+  *out = c;
+  return SJ_OK;
+}
+
+extern "C" int sj_cache_destroy(sj_cache* c) {
+  if (!c) return SJ_OK;
+  if (c->m && c->m->stream) hipStreamSynchronize(c->m->stream);
+  for (void* p : c->allocations) hipFree(p);
+  delete c;
+  return SJ_OK;
+}
+
+extern "C" int sj_cache_reset(sj_cache* c) {
+  SJ_REQUIRE(c, "cache reset: null");
+  c->length = 0;
+  return SJ_OK;
+}
+
+extern "C" long sj_cache_length(const sj_cache* c) { return c ? c->length : -1; }
+
+extern "C" int sj_model_forward_cached(sj_model* m, sj_cache* c, const int32_t* tokens, long n, float* logits) {
+  SJ_REQUIRE(m && c && c->m == m && tokens && n > 0, "forward_cached: arguments");
+  for (long i = 0; i < n; i++)
+    SJ_REQUIRE(tokens[i] >= 0 && tokens[i] <= 256 && tokens[i] < m->V, "input tokens must be bytes or EOS");
+  SJ_REQUIRE(c->length + n <= c->capacity, "KV cache context limit reached");
+  hipStream_t s = m->stream;
+  const Stage& S = m->stages[0];
+  const long d = S.d, L = c->length;
+  const int dt = m->dt;
+  SJ_HIP(hipMemcpyAsync(c->ids, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
+  TRY(sj_embedding_fwd(s, wc(m, m->emb), dt, c->ids, c->x[0], dt, n, d));
+  int top = 0;
+  TRY(cached_blocks(m, c, n, L, top));
+  TRY(sj_rmsnorm_fwd(s, c->x[top], dt, wc(m, S.norm), dt, c->hn, n, d, m->c.norm_epsilon));
+  // the last row, cast to F32, times the fp32 output matrix (model lib.rs:370-371)
+  const char* last = (const char*)c->hn + (n - 1) * d * m->esz;
+  TRY(sj_gemm(s, 0, 0, 1, m->HV, d, last, dt, d, m->w + m->out, SJ_F32, m->Vp, c->logits, SJ_F32, m->Vp, 0, nullptr,
+              0));
+  if (logits) SJ_HIP(hipMemcpyAsync(logits, c->logits, (size_t)m->HV * 4, hipMemcpyDeviceToDevice, s));
+  c->length += n;
+  return SJ_OK;
+}
+
+extern "C" int sj_model_forward(sj_model* m) {
+  SJ_REQUIRE(m, "forward: null");
+  return forward(m);
+}

@@ -268,6 +268,46 @@ def _np_ptr(a: np.ndarray):
     return ctypes.c_void_p(a.ctypes.data)
 
 
+def _padded(v: int) -> int:
+    return (v + 7) // 8 * 8
+
+
+class Cache:
+    """Cache (model lib.rs:36-50): the keys and values of one sequence per
+    layer on the GPU, its length and capacity."""
+
+    def __init__(self, model: "Model", capacity: int):
+        self.model = model
+        h = ctypes.c_void_p()
+        N.api.sj_cache_create(model.h, capacity, ctypes.byref(h))
+        self.h = h
+        self.capacity = capacity
+        p = ctypes.c_void_p()
+        N.api.sj_alloc(4 * _padded(VOCAB), ctypes.byref(p))
+        self.dev = p.value
+
+    @property
+    def length(self) -> int:
+        return N.load().sj_cache_length(self.h)
+
+    def reset(self):
+        N.api.sj_cache_reset(self.h)
+
+    def close(self):
+        if self.h:
+            N.api.sj_cache_destroy(self.h)
+            self.h = None
+        if self.dev:
+            N.api.sj_free(ctypes.c_void_p(self.dev))
+            self.dev = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Model:
     """One byte Transformer resident on the GPU with its optimizer state
     (AdamW, or SGD with the optional parameter VJP).  values > 0 puts the
@@ -421,6 +461,35 @@ class Model:
 
     def train_step(self, lr: float | None = None):
         N.api.sj_model_train_step(self.h, ctypes.c_float(self.tc.learning_rate if lr is None else lr))
+
+    def forward(self) -> float:
+        """Forward only (Model::logits + cross_entropy) of the staged batch:
+        its mean loss, no backward and no update."""
+        N.api.sj_model_forward(self.h)
+        return self.read_loss()[0]
+
+    def logits(self) -> np.ndarray:
+        """fp32 logits [rows][vocab] of the last forward (synchronises)."""
+        p, n = self.buffer("logits")
+        self.synchronize()
+        rows = n // _padded(VOCAB)
+        out = np.empty(n, np.float32)
+        N.api.sj_download(_np_ptr(out), ctypes.c_void_p(p), out.nbytes)
+        return out.reshape(rows, _padded(VOCAB))[:, :VOCAB]
+
+    def new_cache(self, capacity: int | None = None) -> "Cache":
+        """Model::new_cache (model lib.rs:359-361): capacity = context."""
+        return Cache(self, self.mc.context if capacity is None else capacity)
+
+    def forward_cached(self, tokens, cache: "Cache") -> np.ndarray:
+        """Model::forward_cached (model lib.rs:362-372): the fp32 logits of
+        the last of `tokens` after running them at the cache's positions."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32).ravel()
+        N.api.sj_model_forward_cached(self.h, cache.h, _np_ptr(t), t.size, ctypes.c_void_p(cache.dev))
+        self.synchronize()
+        out = np.empty(VOCAB, np.float32)
+        N.api.sj_download(_np_ptr(out), ctypes.c_void_p(cache.dev), out.nbytes)
+        return out
 
     def read_loss(self) -> tuple[float, float]:
         loss, norm = ctypes.c_double(), ctypes.c_double()
