@@ -140,3 +140,46 @@ def test_hierarchy_graph_replay_and_adamw():
         assert np.isfinite(e.read_loss()[0])
     finally:
         e.close(); g.close()
+
+
+def test_cfg3_full_configuration_against_oracle():
+    """BASELINE cfg3 at its configuration (global d512 x 8 layers, GQA 8/2,
+    FFN 1376 over 256 patches of 4 bytes; encoder and decoder d256 x 2,
+    4 heads, FFN 768, window 128; T = 1024 bytes; weights N(0, 0.02)) with
+    the batch cut from 8 to 2 sequences to bound the FP64 oracle's time:
+    the backward recomputed in FP64 from the device's stored activations,
+    loss and every gradient within 1e-3 relative."""
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    mc, tc = config("cfg3")
+    tc.batch = 2
+    cfg = _ocfg(mc, tc)
+    params = init_params(mc, std=0.02, seed=42)
+    ids, tg = byte_batch(Rng(123), tc.batch, tc.sequence)
+    model = Model(mc, tc)
+    try:
+        model.set_params(params)
+        model.set_batch(ids, tg)
+        print("[cfg3] full-configuration forward+backward", flush=True)
+        model.forward_backward()
+        loss, _ = model.read_loss()
+        grads = model.get_grads().astype(np.float64)
+        flat = np.empty(model.activation_count(), np.float32)
+        model.export_activations(flat)
+        dev = H.unpack(cfg, flat.astype(np.float64))
+        p64 = params.astype(np.float64)
+        print("[cfg3] oracle forward", flush=True)
+        ref_acts = H.model_forward(cfg, p64, ids, "bf16")
+        for k in ref_acts:
+            assert rel(dev[k], ref_acts[k]) < 3e-2, (k, rel(dev[k], ref_acts[k]))
+        print("[cfg3] oracle backward", flush=True)
+        lref, gref = H.model_backward(cfg, p64, dev, ids, tg, "bf16")
+        assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)
+        errs = _per_tensor(model, grads, gref)
+        worst = max(errs, key=errs.get)
+        print(f"[parity] cfg3 full: loss {loss:.6f} vs {lref:.6f}; worst gradient {worst} {errs[worst]:.2e}",
+              flush=True)
+        for name, e in errs.items():
+            assert e < GRAD_TOL, (name, e)
+    finally:
+        model.close()

@@ -130,3 +130,57 @@ def test_moe_model_graph_replay_and_adamw():
                 assert np.any(w3[off:off + r * c] != params[off:off + r * c]), name
     finally:
         e.close(); g.close()
+
+
+def test_cfg4_full_configuration_against_oracle():
+    """BASELINE cfg4 at its configuration (4 layers, d512, GQA 8/2, every
+    FFN 8 SwiGLU experts of 1024 with top-2 routing, T = 512; weights
+    N(0, 0.02), router N(0, 1/d) so the logits are N(0, 1)) with the batch
+    cut from 8 to 2 sequences for the oracle's time: routing of every layer
+    bit-exact against the rule on the stored logits, loss and every
+    gradient within 1e-3 of the FP64 backward from the stored activations."""
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    mc, tc = config("cfg4")
+    tc.batch = 2
+    cfg = _ocfg(mc, tc)
+    M, K, E = tc.batch * tc.sequence, cfg["K"], cfg["E"]
+    params = init_params(mc, std=0.02, seed=42)
+    ids, tg = byte_batch(Rng(123), tc.batch, tc.sequence)
+    model = Model(mc, tc)
+    try:
+        model.set_params(params)
+        model.set_batch(ids, tg)
+        print("[cfg4] full-configuration forward+backward", flush=True)
+        model.forward_backward()
+        loss, _ = model.read_loss()
+        grads = model.get_grads().astype(np.float64)
+        flat = np.empty(model.activation_count(), np.float32)
+        model.export_activations(flat)
+        dev = OM.unpack(cfg, flat)
+        p64 = params.astype(np.float64)
+        print("[cfg4] oracle forward", flush=True)
+        ref_acts = OM.model_forward(cfg, p64, ids, "bf16")
+        for k in ref_acts:
+            assert rel(dev[k], ref_acts[k]) < 3e-2, (k, rel(dev[k], ref_acts[k]))
+        print("[cfg4] oracle backward", flush=True)
+        lref, gref, routing = OM.model_backward(cfg, p64, dev, ids, tg, "bf16")
+        assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)
+        for l, (rid, rw, counts, _, _) in enumerate(routing):
+            d_ids = _download(model.buffer(f"route_ids.{l}")[0], M * K, np.int32).reshape(M, K)
+            d_w = _download(model.buffer(f"route_weights.{l}")[0], M * K, np.float32).reshape(M, K)
+            d_cnt = _download(model.buffer(f"route_counts.{l}")[0], E, np.int32)
+            np.testing.assert_array_equal(d_ids, rid)
+            assert rel(d_w, rw) < 1e-6
+            np.testing.assert_array_equal(d_cnt, counts)
+        errs = {}
+        for name, (r, c), off in model.param_info():
+            e = gref[off:off + r * c]
+            errs[name] = np.linalg.norm(grads[off:off + r * c] - e) / max(np.linalg.norm(e), 1e-30)
+        worst = max(errs, key=errs.get)
+        print(f"[parity] cfg4 full: loss {loss:.6f} vs {lref:.6f}; worst gradient {worst} {errs[worst]:.2e}",
+              flush=True)
+        for name, e in errs.items():
+            assert e < GRAD_TOL, (name, e)
+    finally:
+        model.close()
