@@ -172,12 +172,16 @@ def test_cfg1_fp32_end_to_end():
         model.close()
 
 
-@pytest.mark.parametrize("name", ["cfg2-2layer", "cfg2"])
+@pytest.mark.parametrize("name", ["cfg2-2layer", "cfg2", "wide-ffn"])
 def test_bf16_conditioned_parity(name):
     from sejong_amd.model import config
     mc, tc = config("cfg2")
     if name == "cfg2-2layer":
         mc.layers, tc.batch, tc.sequence = 2, 2, 256
+    if name == "wide-ffn":
+        # M*F = 4096 * 2304 > 8 Mi: the down-projection dW is enqueued after
+        # the SwiGLU planes are written (the other stream order of the step)
+        mc.layers, mc.ffn_width = 2, 2304
     print(f"[parity] {name}: d={mc.width} L={mc.layers} B={tc.batch} T={tc.sequence} {mc.precision}", flush=True)
     _conditioned_parity(mc, tc)
 
