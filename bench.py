@@ -143,9 +143,10 @@ def op_work(op: str, mc, tc):
         # the forward's size / 2); dK/dV recomputes S and dP, forms dV, dK (4)
         "attention_bwd_dq": ("flop", 1.5 * attn_fwd),
         "attention_bwd_dkv": ("flop", 2.0 * attn_fwd),
-        # one launch of both (the step's MFMA-layout attention), after the
-        # Delta pass (reads dO hi/lo and O, writes Delta)
-        "attention_bwd_dq_dkv": ("flop", 3.5 * attn_fwd),
+        # one launch of both roles (the step's MFMA-layout attention): the
+        # algorithmic backward is 2.5x the forward (dV, dP, dS->dQ, dK; the
+        # S recompute of both roles is issued work, not counted)
+        "attention_bwd_dq_dkv": ("flop", 2.5 * attn_fwd),
         "attention_bwd_delta": ("byte", 3 * M * d * es + M * mc.heads * 4),
         # group sum of the per-head fp32 dK|dV partials, planes out
         "attention_bwd_kv_reduce": ("byte", (mc.heads // mc.kv) * M * 2 * J * 4 + 4 * M * 2 * J * 2),
@@ -633,6 +634,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
     ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
+    ap.add_argument("--cold-steps", type=int, default=1,
+                    help="eager steps timed op by op with a 512 MiB cache flush before every op (0: skip)")
     ap.add_argument("--workload", default="step", choices=["step", "moe", "pvjp"],
                     help="step: the cfg2 training step (default, the headline); moe: the cfg4 MoE FFN; "
                          "pvjp: the cfg5 parameter-VJP pieces")
@@ -692,6 +695,17 @@ def main():
     model.profile(False)
     nprof = max(1, args.profile_steps)
     prof = {op: (ms / nprof, calls // nprof) for op, (ms, calls) in prof.items()}
+    # cold-cache pass: a 512 MiB buffer is written before every op, so the
+    # bandwidth-bound ops read their operands from HBM rather than from the
+    # 256 MB Infinity Cache
+    cold = {}
+    if args.cold_steps > 0:
+        model.profile(True, cold=True)
+        for _ in range(args.cold_steps):
+            model.train_step(tc.learning_rate)
+        cold = model.profile_collect()
+        model.profile(False)
+        cold = {op: (ms / args.cold_steps, calls // args.cold_steps) for op, (ms, calls) in cold.items()}
     prof_total = sum(ms for ms, _ in prof.values())
     rows = []
     for op, (ms, calls) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
@@ -705,6 +719,21 @@ def main():
                      "frac": round(rate / peak, 4)})
         log(f"  {op:20s} x{calls:3d} {avg_us:9.2f} us  {100 * ms / prof_total:5.1f}%  "
             f"{rate:9.2f} {'TFLOP/s' if kind == 'flop' else 'GB/s'}  ({100 * rate / peak:.1f}% of peak)")
+    cold_rows = {}
+    for op, (ms, calls) in prof.items():
+        kind, work = op_work(op, mc, tc)
+        if kind != "byte" or op not in cold or work <= 0:
+            continue
+        hot_us, cold_us = ms * 1e3 / calls, cold[op][0] * 1e3 / max(cold[op][1], 1)
+        cold_rows[op] = {"bytes": int(work), "hot_us": round(hot_us, 3), "cold_us": round(cold_us, 3),
+                         "hot_gbs": round(work / (hot_us * 1e-6) / 1e9, 1),
+                         "cold_gbs": round(work / (cold_us * 1e-6) / 1e9, 1),
+                         "cold_frac": round(work / (cold_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+    if cold_rows:
+        log("  bandwidth-bound ops, hot vs cold cache (512 MiB written before each op):")
+        for op, r in sorted(cold_rows.items(), key=lambda kv: -kv[1]["bytes"]):
+            log(f"  {op:24s} {r['bytes'] / 1e6:8.2f} MB  hot {r['hot_us']:8.2f} us {r['hot_gbs']:8.1f} GB/s  "
+                f"cold {r['cold_us']:8.2f} us {r['cold_gbs']:8.1f} GB/s ({100 * r['cold_frac']:.1f}% of HBM)")
     # the roofline covers the largest op that launches exactly one kernel, so
     # its live HIP-event time is that kernel's duration (comparable with the
     # rocprofv3 average); the split-K dW products launch a partials kernel and
@@ -771,6 +800,7 @@ def main():
                       "achieved_tflops": round(step_tflops, 2), "frac": round(step_tflops / PEAK_BF16_TFLOPS, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cold_cache": cold_rows or None,
         "loss": loss,
     }
     print(json.dumps(out), flush=True)

@@ -796,7 +796,9 @@ int sj_model_forward_cached(sj_model *m, sj_cache *c, const int32_t *tokens, lon
  * eagerly and every op is bracketed by a HIP event pair on the model stream.
  * sj_model_profile_collect synchronises, aggregates the ops recorded since
  * its last call by op name and returns the number of names (or -1);
- * sj_model_profile_entry reads one aggregate. */
+ * sj_model_profile_entry reads one aggregate.  on = 2 times every op
+ * cold: before its event pair the stream writes a 512 MiB buffer (twice the
+ * 256 MB Infinity Cache), so the op's operands come from HBM. */
 int sj_model_profile(sj_model *m, int on);
 long sj_model_profile_collect(sj_model *m);
 int sj_model_profile_entry(sj_model *m, long i, const char **name, double *total_ms, long *calls);

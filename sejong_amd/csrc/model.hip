@@ -255,6 +255,10 @@ struct sj_model {
   bool own_stream = false;
   // per-op HIP-event profile (eager steps only)
   bool profiling = false;
+  // cold-cache profiling: before every op's event pair the stream writes a
+  // buffer twice the Infinity Cache (512 MiB), so the op reads from HBM
+  bool cold = false;
+  float* flush = nullptr;
   std::vector<hipEvent_t> prof_events;
   std::vector<const char*> prof_names;  // one per recorded op
   std::vector<std::string> agg_names;
@@ -308,6 +312,8 @@ int dalloc(sj_model* m, void** p, size_t bytes) {
     if (_s) return _s;      \
   } while (0)
 
+constexpr long FLUSH_FLOATS = 128L << 20;  // 512 MiB
+
 // Run one op; when profiling, bracket it with a pair of events on the model
 // stream (the kernel-profile feature of the reference, lib.rs:451-482).
 int prof_mark(sj_model* m, const char* name) {
@@ -320,6 +326,7 @@ int prof_mark(sj_model* m, const char* name) {
     }
   }
   m->prof_names.push_back(name);
+  if (m->cold && m->flush) TRY(sj_fill(m->stream, m->flush, SJ_F32, FLUSH_FLOATS, 0.f));
   SJ_HIP(hipEventRecord(m->prof_events[2 * k], m->stream));
   return SJ_OK;
 }
@@ -1899,8 +1906,10 @@ static int run_step(sj_model* m) {
 }
 
 extern "C" int sj_model_profile(sj_model* m, int on) {
-  SJ_REQUIRE(m, "profile: null");
+  SJ_REQUIRE(m && on >= 0 && on <= 2, "profile: mode");
+  if (on == 2 && !m->flush) TRY(dalloc(m, (void**)&m->flush, (size_t)FLUSH_FLOATS * 4));
   m->profiling = on != 0;
+  m->cold = on == 2;
   return SJ_OK;
 }
 

@@ -523,8 +523,10 @@ class Model:
     def synchronize(self):
         N.api.sj_synchronize(ctypes.c_void_p(self.stream))
 
-    def profile(self, on: bool = True):
-        N.api.sj_model_profile(self.h, int(on))
+    def profile(self, on: bool = True, cold: bool = False):
+        """Per-op HIP-event timing of eager steps; cold: a 512 MiB buffer is
+        written before each op so its operands come from HBM."""
+        N.api.sj_model_profile(self.h, 2 if (on and cold) else int(on))
 
     def profile_collect(self) -> dict[str, tuple[float, int]]:
         """{op name: (total ms, calls)} for the ops run since the last collect."""
