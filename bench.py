@@ -287,9 +287,75 @@ def cpu_baseline(mc, tc, sample_batch: int):
         what = "FP64 oracle fwd+bwd+AdamW"
     dt = time.perf_counter() - t0
     tokens = sample_batch * tc.sequence
-    return {"value": tokens / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
-            "sample": f"{sample_batch} of {tc.batch} sequences x {tc.sequence} bytes of the same workload "
-                      f"({what}, {dt:.2f} s)", "ms_per_step_sample": dt * 1e3}
+    out = {"value": tokens / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+           "sample": f"{sample_batch} of {tc.batch} sequences x {tc.sequence} bytes of the same workload "
+                     f"({what}, {dt:.2f} s)", "ms_per_step_sample": dt * 1e3, "cpu_model": _cpu_model()}
+    if mc.hierarchy is None and getattr(mc, "experts", None) is None and mc.width < 1024:
+        out.update(cpu_extras(mc, tc))
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_extras(mc, tc) -> dict:
+    """The rest of the CPU plan: the cfg1 step (fp32 block, fwd+bwd+AdamW)
+    and per-kernel FP64 oracle times at this workload's shapes (RMSNorm
+    forward/backward, grouped attention forward/backward, AdamW over every
+    parameter), all on the same host threads."""
+    import numpy as np
+    from oracle import oracle as O
+    from sejong_amd.model import byte_batch, config, init_params, param_count
+    from sejong_amd.rng import Rng
+
+    def timed(f, reps=1):
+        t = time.perf_counter()
+        for _ in range(reps):
+            f()
+        return (time.perf_counter() - t) * 1e3 / reps
+
+    m1, t1 = config("cfg1")
+    p1 = init_params(m1, std=0.02).astype(np.float64)
+    i1, g1 = byte_batch(Rng(t1.seed), t1.batch, t1.sequence)
+    c1 = dict(d=m1.width, layers=m1.layers, hq=m1.heads, hk=m1.kv, ffn=m1.ffn_width, T=t1.sequence, B=t1.batch,
+              eps=m1.norm_epsilon, theta=m1.rope_theta)
+
+    def cfg1_step():
+        loss, g, _, _ = O.model_fwd_bwd(c1, p1, i1, g1, dtype="f32")
+        sc = min(1.0, t1.clip_norm / math.sqrt(O.sum_squares(g)))
+        O.adamw(p1.copy(), g, np.zeros_like(p1), np.zeros_like(p1), t1.learning_rate, t1.beta1, t1.beta2,
+                t1.epsilon, t1.weight_decay, 1 / (1 - t1.beta1), 1 / (1 - t1.beta2), sc)
+    cfg1_ms = timed(cfg1_step, 3)
+    rng = np.random.default_rng(0)
+    M, d, Dh, B, T = tc.batch * tc.sequence, mc.width, mc.head_dim, tc.batch, tc.sequence
+    x = rng.normal(0, 1, (M, d)); w = np.ones(d); dy = rng.normal(0, 1e-3, (M, d))
+    q = rng.normal(0, 1, (M, mc.heads * Dh)); k = rng.normal(0, 1, (M, mc.kv * Dh)); v = rng.normal(0, 1, (M, mc.kv * Dh))
+    o, lse = O.attention_fwd(q, k, v, B, T, mc.heads, mc.kv, Dh)
+    do = rng.normal(0, 1e-3, o.shape)
+    n = param_count(mc)
+    pw, ppw = O._d(rng.normal(0, 0.02, n)); pg, ppg = O._d(rng.normal(0, 1e-3, n))
+    pm, ppm = O._d(np.zeros(n)); pv, ppv = O._d(np.zeros(n))
+    kern = {
+        "rmsnorm_fwd": timed(lambda: O.rmsnorm_fwd(x, w, mc.norm_epsilon), 3),
+        "rmsnorm_bwd": timed(lambda: O.rmsnorm_bwd(x, w, dy, mc.norm_epsilon), 3),
+        "attention_fwd": timed(lambda: O.attention_fwd(q, k, v, B, T, mc.heads, mc.kv, Dh)),
+        "attention_bwd": timed(lambda: O.attention_bwd(q, k, v, o, lse, do, B, T, mc.heads, mc.kv, Dh)),
+        "adamw": timed(lambda: O.lib().or_adamw(ppw, ppg, ppm, ppv, n, tc.learning_rate, tc.beta1, tc.beta2,
+                                                tc.epsilon, tc.weight_decay, 1 / (1 - tc.beta1),
+                                                1 / (1 - tc.beta2), 1.0), 3),
+    }
+    return {"cfg1_step_ms": round(cfg1_ms, 3),
+            "cfg1_tokens_per_s": round(t1.batch * t1.sequence / (cfg1_ms * 1e-3), 1),
+            "kernel_ms": {kk: round(vv, 3) for kk, vv in kern.items()},
+            "kernel_shapes": f"rmsnorm [{M}x{d}]; attention B{B} T{T} heads {mc.heads}/{mc.kv} hd{Dh}; "
+                             f"adamw over {n} parameters"}
 
 
 def copy_probe(mib: int):

@@ -379,6 +379,7 @@ double or_sum_squares(const double *g, long n) {
 void or_adamw(double *w, const double *g, double *m, double *v, long n,
               double lr, double b1, double b2, double eps, double decay,
               double ib1, double ib2, double scale) {
+    #pragma omp parallel for schedule(static)
     for (long i = 0; i < n; i++) {
         double gi = g[i] * scale;
         m[i] = b1 * m[i] + (1.0 - b1) * gi;
