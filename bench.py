@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 # op -> the one kernel it launches (where it launches exactly one), for the
 # rocprofv3 traffic lookup; attention runs the transposed-operand kernels when
 # the step keeps bf16 planes and T is a multiple of 64
-OP_KERNEL = {"attention_bwd_dq_dkv": "k_attn2_bwd", "attention_bwd_delta": "k_attn_delta",
+OP_KERNEL = {"attention_bwd": "k_attn2_bwd", "attention_bwd_dq_dkv": "k_attn2_bwd", "attention_bwd_delta": "k_attn_delta",
              "attention_bwd_kv_reduce": "k_attn_kv_reduce_rows", "attention_fwd": "k_attn2_fwd",
              "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd",
              "cross_entropy": "k_cross_entropy"}
@@ -76,7 +76,7 @@ def _hier_ops(mc, tc):
         for op, kind, w in (("qkv_rope", "flop", 2 * M * d * (d + 2 * J)), ("qkv_dx", "flop", 2 * M * d * (d + 2 * J)),
                             ("qkv_dw", "flop", 2 * M * d * (d + 2 * J)), ("attention_fwd", "flop", af),
                             ("attention_bwd", "flop", 2.5 * af), ("attention_bwd_dq", "flop", 1.5 * af),
-                            ("attention_bwd_dkv", "flop", 2.0 * af), ("attention_bwd_dq_dkv", "flop", 3.5 * af),
+                            ("attention_bwd_dkv", "flop", 2.0 * af), ("attention_bwd_dq_dkv", "flop", 2.5 * af),
                             ("attention_bwd_delta", "byte", 3 * M * d * es + M * hq * 4),
                             ("attention_bwd_kv_reduce", "byte", (hq // hk) * M * 2 * J * 4 + 4 * M * 2 * J * 2),
                             ("attn_out_residual", "flop", 2 * M * d * d), ("attn_out_dx", "flop", 2 * M * d * d),
