@@ -118,6 +118,9 @@ int factored_update_staged(hipStream_t stream, const void* meta, long tiles, con
 // attention over transposed operands (attention_t.hip) and the group reduce
 // of the per-head dK | dV partials it shares with attention.hip
 int attention_t_prepare();
+// cross entropy with dX as hi/lo bf16 planes [rows][ldp] (columns past vocab zero)
+int cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss, uint16_t* dx_hi,
+                         uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar);
 // project_qkv (MFMA layout) into separate q, k, v buffers
 int qkv_fwd_t_out(void* stream, const uint16_t* x, long ldx, long M, long D, const uint16_t* wqkv_t, long ldw, long N,
                   long KV, uint16_t* q, long ldq, uint16_t* k, long ldk, uint16_t* v, long ldv, const float* rope_table,

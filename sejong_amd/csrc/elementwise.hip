@@ -172,6 +172,33 @@ __global__ __launch_bounds__(256) void k_cross_entropy(const float* x, long ldx,
   }
 }
 
+// The same cross entropy with dX left as hi/lo bf16 planes [rows][width]
+// (the output head's dX / dW GEMM operands); columns vocab .. width-1 of the
+// planes are written as zero.
+__global__ __launch_bounds__(256) void k_cross_entropy_planes(const float* x, long ldx, const int32_t* targets,
+                                                              float* loss, bf16_t* dh, bf16_t* dl, long ldp, long rows,
+                                                              long vocab, long width, float dy_scalar) {
+  const int lane = threadIdx.x & 63;
+  long r = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * ldx;
+  float m = -INFINITY;
+  for (long j = lane; j < vocab; j += 64) m = fmaxf(m, xr[j]);
+  m = wave_max(m);
+  float s = 0.f;
+  for (long j = lane; j < vocab; j += 64) s += expf(xr[j] - m);
+  s = wave_sum(s);
+  int tg = targets[r];
+  if (lane == 0) loss[r] = m + logf(s) - xr[tg];
+  const float inv = 1.f / s;
+  for (long j = lane; j < width; j += 64) {
+    bf16_t h = 0, l = 0;
+    if (j < vocab) split_bf((expf(xr[j] - m) * inv - (j == tg ? 1.f : 0.f)) * dy_scalar, h, l);
+    dh[r * ldp + j] = h;
+    dl[r * ldp + j] = l;
+  }
+}
+
 // kernels.py:254-262 (single workgroup, FP64, fixed order)
 __global__ __launch_bounds__(256) void k_loss_summary(const float* loss, long n, double* out, long slot, float weight) {
   __shared__ double red[4];
@@ -514,6 +541,17 @@ extern "C" int sj_cross_entropy(void* stream, const float* x, long ldx, const in
   if (rows == 0) return SJ_OK;
   hipLaunchKernelGGL(k_cross_entropy, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x, ldx,
                      targets, loss, dx, lddx, rows, vocab, dy, dy_scalar);
+  SJ_LAUNCH_CHECK("cross_entropy");
+  return SJ_OK;
+}
+
+int sjh::cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss,
+                              uint16_t* dx_hi, uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar) {
+  SJ_REQUIRE(rows >= 0 && vocab > 0 && ldx >= vocab && ldp >= vocab && dx_hi && dx_lo,
+             "cross entropy (planes) row mismatch");
+  if (rows == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_cross_entropy_planes, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
+                     ldx, targets, loss, (bf16_t*)dx_hi, (bf16_t*)dx_lo, ldp, rows, vocab, ldp, dy_scalar);
   SJ_LAUNCH_CHECK("cross_entropy");
   return SJ_OK;
 }

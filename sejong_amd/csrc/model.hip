@@ -94,6 +94,12 @@ struct TJob {
   long rows, cols;
   long tile0;  // first 64x64 tile of this job in the flat tile index
   long tiles_c;
+  int kind;    // 0: bf16 mirror -> transposed mirror; 1: fp32 master -> hi/lo planes, normal and transposed
+};
+
+// outputs of a kind-1 job: hi, lo [rows][cols] and hi^T, lo^T [cols][rows]
+struct TPlanes {
+  uint16_t *hi, *lo, *hit, *lot;
 };
 
 // Keeps the profiled stream busy for `n` sleeps of ~8k clocks each while the
@@ -105,17 +111,55 @@ __global__ __launch_bounds__(64) void k_profile_hold(int n) {
 }
 
 __global__ __launch_bounds__(256) void k_transpose_jobs(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                                        const TJob* __restrict__ jobs, int njobs) {
+                                                        const TJob* __restrict__ jobs, int njobs,
+                                                        const float* __restrict__ master, TPlanes hp) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 72];
+  __shared__ __attribute__((aligned(16))) uint16_t tile_lo[64 * 72];
   const long b = blockIdx.x;
   int ji = 0;
   while (ji + 1 < njobs && b >= jobs[ji + 1].tile0) ji++;
   const long off = jobs[ji].off, rows = jobs[ji].rows, cols = jobs[ji].cols;
   const long lt = b - jobs[ji].tile0;
   const long r0 = (lt / jobs[ji].tiles_c) * 64, c0 = (lt % jobs[ji].tiles_c) * 64;
+  const int t = threadIdx.x;
+  if (jobs[ji].kind == 1) {
+    // fp32 master tile -> hi = RNE(w), lo = RNE(w - hi), stored [rows][cols]
+    // and transposed [cols][rows] (the output head's GEMM operands)
+    const float* S = master + off;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int r = (t >> 3) + 32 * p, c = (t & 7) * 8;
+      const long gr = r0 + r, gc = c0 + c;
+      uint16_t h[8], l[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float v = (gr < rows && gc + i < cols) ? S[gr * cols + gc + i] : 0.f;
+        sj::split_bf(v, h[i], l[i]);
+        tile[r * 72 + c + i] = h[i];
+        tile_lo[r * 72 + c + i] = l[i];
+      }
+      if (gr < rows)
+        for (int i = 0; i < 8; i++)
+          if (gc + i < cols) {
+            hp.hi[gr * cols + gc + i] = h[i];
+            hp.lo[gr * cols + gc + i] = l[i];
+          }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int oc = (t >> 3) + 32 * p, orr = (t & 7) * 8;
+      if (c0 + oc < cols)
+        for (int i = 0; i < 8; i++)
+          if (r0 + orr + i < rows) {
+            hp.hit[(c0 + oc) * rows + r0 + orr + i] = tile[(orr + i) * 72 + oc];
+            hp.lot[(c0 + oc) * rows + r0 + orr + i] = tile_lo[(orr + i) * 72 + oc];
+          }
+    }
+    return;
+  }
   const uint16_t* S = src + off;
   uint16_t* D = dst + off;
-  const int t = threadIdx.x;
   const bool vec = (rows & 7) == 0 && (cols & 7) == 0 && r0 + 64 <= rows && c0 + 64 <= cols;
 #pragma unroll
   for (int p = 0; p < 2; p++) {
@@ -201,6 +245,13 @@ struct sj_model {
   bool rowdw = false;
   long ldt = 0;                   // leading dimension of [cols][rows] activations (M rounded to 8)
   uint16_t* mirror_t = nullptr;   // transposed projection matrices, same offsets as the mirror
+  // LM head on the planes kernels: W_out as hi/lo planes [d][Vp] and
+  // transposed [Vp][d] (refreshed with the transposed mirror), dlogits as
+  // hi/lo planes [M][Vp] written by the cross entropy
+  bool lm_planes = false;
+  bool defer_loss = false;  // set inside a training step: loss_summary runs after the backward's fork
+  uint16_t* hp[4] = {};
+  uint16_t* dlp[2] = {};
   TJob* tjobs = nullptr;
   int tjob_n = 0;
   long tjob_tiles = 0;
@@ -480,7 +531,7 @@ const void* wc(const sj_model* m, long off) {
 int transpose_mirror(sj_model* m) {
   if (!m->planes) return SJ_OK;
   hipLaunchKernelGGL(k_transpose_jobs, dim3((unsigned)m->tjob_tiles), dim3(256), 0, m->stream, m->mirror, m->mirror_t,
-                     m->tjobs, m->tjob_n);
+                     m->tjobs, m->tjob_n, (const float*)m->w, TPlanes{m->hp[0], m->hp[1], m->hp[2], m->hp[3]});
   SJ_LAUNCH_CHECK("mirror transpose");
   return SJ_OK;
 }
@@ -590,6 +641,16 @@ int hierarchy_forward(sj_model* m) {
   return SJ_OK;
 }
 
+int forward(sj_model* m);
+bool two_streams(const sj_model* m);
+// the step's forward: the loss sum waits for the backward's second stream
+int forward_deferred(sj_model* m) {
+  m->defer_loss = !m->value_n && two_streams(m);
+  const int st = forward(m);
+  if (st) m->defer_loss = false;
+  return st;
+}
+
 int forward(sj_model* m) {
   hipStream_t s = m->stream;
   const long M = m->M, d = m->d;
@@ -613,11 +674,25 @@ int forward(sj_model* m) {
   }
   // fp32 head on the fp32 master (architecture.rs:160-167); hn's values are
   // exact in fp32 (Graph::cast to F32), so it is read in its storage dtype.
-  OP("head_fwd", sj_gemm(s, 0, 0, M, m->HV, d, m->hn, dt, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp, 0, m->ws,
-              m->ws_bytes));
+  // On the planes path the master enters as hi + lo bf16 planes (2^-17
+  // relative) and the cross entropy leaves dlogits as hi/lo planes.
   const float seed = 1.0f / (float)M;  // scale / count, graph.rs:546
-  OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlogits, m->Vp, M, m->HV, nullptr, seed));
-  OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, 0, 1.0f));
+  if (m->lm_planes) {
+    // no split-K (no workspace): a row's sum order does not depend on M,
+    // so the cached forward's one-row product gives the same logits
+    OP("head_fwd", sj_gemm_planes(s, M, m->Vp, d, (const uint16_t*)m->hn, nullptr, d, m->hp[2], m->hp[3], d,
+                                  m->logits, SJ_F32, m->Vp, 0, nullptr, 0));
+    OP("cross_entropy", sjh::cross_entropy_planes(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlp[0], m->dlp[1],
+                                                  m->Vp, M, m->HV, seed));
+  } else {
+    OP("head_fwd", sj_gemm(s, 0, 0, M, m->HV, d, m->hn, dt, d, m->w + m->out, SJ_F32, m->Vp, m->logits, SJ_F32, m->Vp, 0,
+                           m->ws, m->ws_bytes));
+    OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlogits, m->Vp, M, m->HV,
+                                         nullptr, seed));
+  }
+  // the loss sum is read only by read_loss: in a training step it runs on
+  // the second stream after the backward's fork, off the dX chain
+  if (!m->defer_loss) OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, 0, 1.0f));
   return SJ_OK;
 }
 
@@ -945,6 +1020,10 @@ int backward(sj_model* m) {
     OP("head_dx", sj_gemm(s, 0, 1, R, d, n, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dhsel, SJ_F32,
                           d, 0, m->ws, m->ws_bytes));
     OP("value_scatter", sj_gather_rows_bwd(s, m->dhsel, m->sel, R, d, m->dz, d, M));
+  } else if (m->lm_planes) {
+    // head: dh = dlogits W_out^T (hi/lo x hi/lo: three products)
+    OP("head_dx", sj_gemm_planes(s, M, d, m->Vp, m->dlp[0], m->dlp[1], m->Vp, m->hp[0], m->hp[1], m->Vp, m->dz, SJ_F32,
+                                 d, 0, m->ws, m->ws_bytes));
   } else {
     // head: dh = dlogits W_out^T ; dW_out = hn^T dlogits
     OP("head_dx", sj_gemm(s, 0, 1, M, d, m->HV, m->dlogits, SJ_F32, m->Vp, m->w + m->out, SJ_F32, m->Vp, m->dz, SJ_F32, d,
@@ -960,9 +1039,16 @@ int backward(sj_model* m) {
   {  // the head's dW reads only the forward's rows and dlogits: second stream
     hipStream_t sw = two ? m->stream2 : s;
     void* wsw = two ? m->ws2 : m->ws;
+    if (m->defer_loss) {
+      m->defer_loss = false;
+      OP("loss_summary", sj_loss_summary(sw, m->loss_rows, M, m->loss, 0, 1.0f));
+    }
     if (m->value_n)
       OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, m->HR, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32,
                             m->Vp, 0, wsw, m->ws_bytes));
+    else if (m->lm_planes)
+      OP("head_dw", sj_gemm_planes_tn(sw, d, m->Vp, M, (const uint16_t*)m->hn, nullptr, d, m->dlp[0], m->dlp[1], m->Vp,
+                                      G + m->out, SJ_F32, m->Vp, 0, wsw, m->ws_bytes));
     else
       OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
                             wsw, m->ws_bytes));
@@ -1012,7 +1098,7 @@ int update(sj_model* m) {
 }
 
 int whole_step(sj_model* m) {
-  TRY(forward(m));
+  TRY(forward_deferred(m));
   TRY(backward(m));
   TRY(update(m));
   return SJ_OK;
@@ -1333,6 +1419,9 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       for (const Stage& S : m->stages) planes = planes && S.M % 8 == 0;
     }
     m->planes = planes;
+    // the LM head (hn bf16 [M][d] times the fp32 master) on the planes GEMMs
+    // with W_out split hi + lo; the hidden width and rows 8-aligned
+    m->lm_planes = planes && !m->value_n && m->d % 8 == 0 && m->M % 8 == 0;
     if (m->E && !planes) {
       if (m->own_stream) hipStreamDestroy(m->stream);
       delete m;
@@ -1373,11 +1462,16 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     // transpose jobs: the four projection matrices of every layer
     std::vector<TJob> jobs;
     long tiles = 0;
-    auto job = [&](long off, long rows, long cols) {
-      TJob j{off, rows, cols, tiles, (cols + 63) / 64};
+    auto job = [&](long off, long rows, long cols, int kind = 0) {
+      TJob j{off, rows, cols, tiles, (cols + 63) / 64, kind};
       tiles += ((rows + 63) / 64) * j.tiles_c;
       jobs.push_back(j);
     };
+    if (m->lm_planes) {  // the output head's hi/lo planes from its fp32 master
+      for (int k = 0; k < 4; k++) ALLOC(m->hp[k], (size_t)m->d * m->Vp * 2);
+      for (int k = 0; k < 2; k++) ALLOC(m->dlp[k], (size_t)m->M * m->Vp * 2);
+      job(m->out, m->d, m->Vp, 1);
+    }
     for (long l = 0; l < m->L; l++) {
       const Layer& y = m->layers[l];
       const Stage& S = m->stages[y.stage];
@@ -2288,8 +2382,12 @@ extern "C" int sj_model_forward_cached(sj_model* m, sj_cache* c, const int32_t* 
   TRY(sj_rmsnorm_fwd(s, c->x[top], dt, wc(m, S.norm), dt, c->hn, n, d, m->c.norm_epsilon));
   // the last row, cast to F32, times the fp32 output matrix (model lib.rs:370-371)
   const char* last = (const char*)c->hn + (n - 1) * d * m->esz;
-  TRY(sj_gemm(s, 0, 0, 1, m->HV, d, last, dt, d, m->w + m->out, SJ_F32, m->Vp, c->logits, SJ_F32, m->Vp, 0, nullptr,
-              0));
+  if (m->lm_planes)
+    TRY(sj_gemm_planes(s, 1, m->Vp, d, (const uint16_t*)last, nullptr, d, m->hp[2], m->hp[3], d, c->logits, SJ_F32,
+                       m->Vp, 0, nullptr, 0));
+  else
+    TRY(sj_gemm(s, 0, 0, 1, m->HV, d, last, dt, d, m->w + m->out, SJ_F32, m->Vp, c->logits, SJ_F32, m->Vp, 0, nullptr,
+                0));
   if (logits) SJ_HIP(hipMemcpyAsync(logits, c->logits, (size_t)m->HV * 4, hipMemcpyDeviceToDevice, s));
   c->length += n;
   return SJ_OK;
