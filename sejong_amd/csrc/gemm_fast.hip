@@ -117,6 +117,20 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
                : "memory", "m0");
 }
 
+// wait until at most `after` stages (PW DMAs each) of this wave are in
+// flight; after <= S
+template <int PW, int S>
+__device__ __forceinline__ void wait_stages(int after) {
+  if constexpr (S <= 0) {
+    wait_vm<0>();
+  } else {
+    if (after >= S)
+      wait_vm<PW * S>();
+    else
+      wait_stages<PW, S - 1>(after);
+  }
+}
+
 __device__ __forceinline__ void block_barrier() {
   // LDS reads of the previous stage are complete, then a plain s_barrier
   // (no release fence: it would wait for the DMA still in flight)
@@ -291,6 +305,12 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   // (sl & 7) ^ swt(k-row) of k-row (r8 % 64) + (sl >> 3).
   // kpos[j]: the lane's largest k offset in the block (valid iff
   // kbeg + k0 + kpos < kend); kmul[j]: source elements per k step.
+  // Lanes outside the operand read `zero` (kmul 0 keeps them there).  Its
+  // address is held in registers: the DMA asm's memory clobber would
+  // otherwise make the compiler reload it from the GOT, with an lgkmcnt(0)
+  // wait, before every issue.
+  const bf16_t* zero = (const bf16_t*)g_zero16;
+  asm volatile("" : "+s"(zero));
   const bf16_t* src[PER_WAVE];
   int kpos[PER_WAVE];
   long kmul[PER_WAVE];
@@ -320,24 +340,29 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     if (tr) {
       const int kr = (r8 % 64) + (sl >> 3);
       const long col = row + 8 * ((sl & 7) ^ swt(kr));
-      src[j] = col < rows ? base + (kbeg + kr) * ld + col : nullptr;
+      src[j] = col < rows ? base + (kbeg + kr) * ld + col : zero;
       kpos[j] = kr;
-      kmul[j] = ld;
+      kmul[j] = col < rows ? ld : 0;
     } else {
-      src[j] = row < rows ? base + row * ld + kbeg + c8 : nullptr;
+      src[j] = row < rows ? base + row * ld + kbeg + c8 : zero;
       kpos[j] = c8 + 7;
-      kmul[j] = 1;
+      kmul[j] = row < rows ? 1 : 0;
     }
   }
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
+  const long klen = kend - kbeg;
   auto issue = [&](int it, int buf) {
     const long k0 = (long)it * BK;  // relative to kbeg
     const uint32_t sbase = lds_base + (uint32_t)(buf * STAGE_ROWS * BK * 2) + (uint32_t)(wave_s * 8 * BK * 2);
+    if (k0 + BK <= klen) {  // uniform: every lane's k offset is in range
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; j++) {
-      const bool kin = kbeg + k0 + kpos[j] < kend;
-      const void* a = (src[j] && kin) ? (const void*)(src[j] + k0 * kmul[j]) : (const void*)g_zero16;
-      dma16(a, sbase + (uint32_t)(j * 32 * BK * 2));
+      for (int j = 0; j < PER_WAVE; j++) dma16(src[j] + k0 * kmul[j], sbase + (uint32_t)(j * 32 * BK * 2));
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER_WAVE; j++) {
+        const bool kin = k0 + kpos[j] < klen;
+        dma16(kin ? src[j] + k0 * kmul[j] : zero, sbase + (uint32_t)(j * 32 * BK * 2));
+      }
     }
   };
 
@@ -375,12 +400,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     // wait for this wave's DMA of stage `it`; the stages issued after it
     // (up to NS - 2) may stay in flight
     const int after = (nk - 1 - it) < (NS - 2) ? (nk - 1 - it) : (NS - 2);
-    if (after >= 2)
-      wait_vm<PER_WAVE * 2>();
-    else if (after == 1)
-      wait_vm<PER_WAVE>();
-    else
-      wait_vm<0>();
+    wait_stages<PER_WAVE, NS - 2>(after);
     block_barrier();
     if (it + NS - 1 < nk) issue(it + NS - 1, (it + NS - 1) % NS);
     const bf16_t* st = lds + (it % NS) * STAGE_ROWS * BK;
