@@ -9,9 +9,9 @@ AdamW (lr 3e-4, wd 0.01).  Inputs are resident in HBM before timing; the
 step is replayed as a hipGraph (--no-graph for eager launches).
 
 Prints ONE JSON line on stdout (the driver contract); progress goes to
-stderr.  The roofline object covers the op with the largest share of the
-step, timed live with HIP events on the model stream (one profiled eager
-step after the timed region); the cpu_baseline object times the FP64 oracle
+stderr.  The roofline object covers the kernel with the largest share of the
+step's kernel time, timed live with HIP events on the model stream (eager
+steps after the timed region); the cpu_baseline object times the FP64 oracle
 (a C restatement of the reference formulas, OpenMP) on a bounded sample.
 """
 from __future__ import annotations
@@ -30,14 +30,14 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
-# single-kernel ops and the kernel each one launches (rocprofv3 names)
-# op -> the one kernel it launches (where it launches exactly one), for the
-# rocprofv3 traffic lookup; attention runs the transposed-operand kernels when
-# the step keeps bf16 planes and T is a multiple of 64
+# op -> the one kernel it launches (rocprofv3 names) where the library does
+# not name it itself (GEMM ops do, through the profile): the cfg2 step's
+# plane-path kernels (bf16, head_dim 64, T a multiple of 64)
 OP_KERNEL = {"attention_bwd": "k_attn2_bwd", "attention_bwd_dq_dkv": "k_attn2_bwd", "attention_bwd_delta": "k_attn_delta",
-             "attention_bwd_kv_reduce": "k_attn_kv_reduce_rows", "attention_fwd": "k_attn2_fwd",
-             "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd",
-             "cross_entropy": "k_cross_entropy"}
+             "attention_bwd_kv_reduce": "k_attn_kv_reduce_rows", "attention_fwd": "k_attn2_fwd<3>",
+             "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd4",
+             "embedding": "k_embedding_fwd", "cross_entropy": "k_cross_entropy_planes", "rmsnorm": "k_rms_fwd_t<3>",
+             "rmsnorm_bwd": "k_rms_bwd_p<3>", "rmsnorm_dw_reduce": "k_rms_reduce_multi", "loss_summary": "k_loss_summary"}
 
 
 def log(*a):
@@ -225,6 +225,65 @@ def op_work(op: str, mc, tc):
     elif getattr(tc, "optimizer", "adamw") == "sgd":
         table.update({"factored_norm": ("byte", 4 * P), "norm_sum": ("byte", 0), "sgd_update": ("byte", 14 * P)})
     return table.get(op, ("flop", 0.0))
+
+
+# issued MFMA work of a kernel per unit of its algorithmic work: the GEMM
+# kernels multiply hi/lo bf16 planes (PA x PB products, lo x lo skipped); the
+# MFMA-layout attention kernels recompute S and dP and multiply the hi/lo
+# planes of P, dO and dS (forward 3 products for the algorithmic 2; backward
+# 13 for the algorithmic 5)
+def issued_factor(kernel: str) -> float:
+    if kernel.startswith("k_gemm_fast<"):
+        t = [int(x) for x in kernel[len("k_gemm_fast<"):-1].split(",")]
+        pa, pb = t[2], t[3]
+        return float(pa * pb - (1 if pa == 2 and pb == 2 else 0))
+    return {"k_attn2_fwd<3>": 1.5, "k_attn2_bwd": 6.5 / 2.5}.get(kernel, 1.0)
+
+
+def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config):
+    """Roofline of the kernel with the largest share of the profiled step.
+
+    Every op is charged to the kernel it launches: a GEMM op to the GEMM
+    kernel the library names for it, with the time between the events that
+    kernel recorded at its own start and end (no launch gaps, no split-K
+    reduce); any other op to the one kernel of OP_KERNEL (else the op
+    itself) with its event-bracketed time.  The dominant kernel's achieved
+    rate is its algorithmic work summed over its launches divided by its
+    summed time (the average work per launch over the average launch
+    duration)."""
+    per = {}
+    for op, (ms, calls) in prof.items():
+        kind, work = op_work(op, mc, tc)
+        kern = op_kernel.get(op) or OP_KERNEL.get(op) or op
+        kms = kern_only[op][0] if op in kern_only else ms
+        e = per.setdefault(kern, {"ms": 0.0, "calls": 0, "work": 0.0, "kind": kind, "ops": []})
+        e["ms"] += kms
+        e["calls"] += calls
+        e["work"] += work * calls
+        e["ops"].append(op)
+    total = sum(e["ms"] for e in per.values())
+    kern, e = max(per.items(), key=lambda kv: kv[1]["ms"])
+    flop = e["kind"] == "flop"
+    peak = PEAK_BF16_TFLOPS if flop else PEAK_HBM_GBS
+    avg_us = e["ms"] * 1e3 / e["calls"]
+    wpl = e["work"] / e["calls"]
+    rate = wpl / (avg_us * 1e-6) / (1e12 if flop else 1e9)
+    log(f"  dominant kernel {kern}: {100 * e['ms'] / total:.1f}% of the profiled kernel time, {e['calls']} launches "
+        f"({', '.join(e['ops'])}), {avg_us:.2f} us, {rate:.2f} {'TFLOP/s' if flop else 'GB/s'}")
+    # HBM bytes per dispatch of the dominant kernel, from the committed
+    # rocprofv3 TCC EA-request runs
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get(config, {}).get("bytes_per_dispatch", {}).get(kern)
+    out = {"bound": "mfma" if flop else "hbm", "achieved": round(rate, 2), "peak": peak,
+           "unit": "TFLOP/s" if flop else "GB/s", "frac": round(rate / peak, 4), "traffic": traffic,
+           "kernel": kern, "ops": e["ops"], "launches_per_step": e["calls"],
+           "share_of_kernel_time": round(e["ms"] / total, 4), "work_per_launch": wpl, "avg_launch_us": round(avg_us, 3)}
+    if flop:
+        f = issued_factor(kern)
+        out["issued"] = {"work_per_launch": wpl * f, "achieved": round(rate * f, 2), "frac": round(rate * f / peak, 4)}
+    return out
 
 
 def _hier_name(name, mc):
@@ -758,9 +817,13 @@ def main():
     for _ in range(max(1, args.profile_steps)):
         model.train_step(tc.learning_rate)
     prof = model.profile_collect()
+    op_kernel = dict(model.profile_kernels)
     model.profile(False)
     nprof = max(1, args.profile_steps)
     prof = {op: (ms / nprof, calls // nprof) for op, (ms, calls) in prof.items()}
+    # GEMM ops: their GEMM kernel alone (events at its own start and end)
+    kern_only = {op[:-len("#kernel")]: v for op, v in prof.items() if op.endswith("#kernel")}
+    prof = {op: v for op, v in prof.items() if "#" not in op}
     # cold-cache pass: a 512 MiB buffer is written before every op, so the
     # bandwidth-bound ops read their operands from HBM rather than from the
     # 256 MB Infinity Cache
@@ -771,7 +834,8 @@ def main():
             model.train_step(tc.learning_rate)
         cold = model.profile_collect()
         model.profile(False)
-        cold = {op: (ms / args.cold_steps, calls // args.cold_steps) for op, (ms, calls) in cold.items()}
+        cold = {op: (ms / args.cold_steps, calls // args.cold_steps) for op, (ms, calls) in cold.items()
+                if "#" not in op}
     prof_total = sum(ms for ms, _ in prof.values())
     rows = []
     for op, (ms, calls) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
@@ -800,24 +864,7 @@ def main():
         for op, r in sorted(cold_rows.items(), key=lambda kv: -kv[1]["bytes"]):
             log(f"  {op:24s} {r['bytes'] / 1e6:8.2f} MB  hot {r['hot_us']:8.2f} us {r['hot_gbs']:8.1f} GB/s  "
                 f"cold {r['cold_us']:8.2f} us {r['cold_gbs']:8.1f} GB/s ({100 * r['cold_frac']:.1f}% of HBM)")
-    # the roofline covers the largest op that launches exactly one kernel, so
-    # its live HIP-event time is that kernel's duration (comparable with the
-    # rocprofv3 average); the split-K dW products launch a partials kernel and
-    # a reduce, and are listed in the per-op table only
-    single = [r for r in rows if r["op"] in OP_KERNEL]
-    dom = single[0] if single else rows[0]
-    kind, work = op_work(dom["op"], mc, tc)
-    # HBM bytes per dispatch of the dominant kernel, from the committed
-    # rocprofv3 FETCH_SIZE / WRITE_SIZE runs (copy-kernel calibrated)
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    kname = OP_KERNEL.get(dom["op"])
-    if kname and os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get(args.config, {}).get("bytes_per_dispatch", {}).get(kname)
-    roofline = {"bound": dom["bound"], "achieved": dom["achieved"],
-                "peak": PEAK_BF16_TFLOPS if kind == "flop" else PEAK_HBM_GBS, "unit": dom["unit"],
-                "frac": dom["frac"], "traffic": traffic, "op": dom["op"], "kernel": kname or dom["op"],
-                "work_per_launch": work, "avg_launch_us": dom["avg_us"]}
+    roofline = kernel_roofline(prof, kern_only, op_kernel, mc, tc, args.config)
     # whole-step MFMA fraction (algorithmic GEMM + attention flops / step time)
     step_flops = sum(op_work(op, mc, tc)[1] * calls for op, (_, calls) in prof.items()
                      if op_work(op, mc, tc)[0] == "flop")

@@ -798,10 +798,17 @@ int sj_model_forward_cached(sj_model *m, sj_cache *c, const int32_t *tokens, lon
  * its last call by op name and returns the number of names (or -1);
  * sj_model_profile_entry reads one aggregate.  on = 2 times every op
  * cold: before its event pair the stream writes a 512 MiB buffer (twice the
- * 256 MB Infinity Cache), so the op's operands come from HBM. */
+ * 256 MB Infinity Cache), so the op's operands come from HBM.  A GEMM op
+ * also yields an aggregate "<op>#kernel": its GEMM kernel alone, timed by
+ * events at the kernel's own start and end (hipExtLaunchKernel), without
+ * launch gaps or a split-K reduce.  sj_model_profile_kernel names the GEMM
+ * kernel an aggregate's
+ * op launched, as rocprofv3 lists it ("k_gemm_fast<BM, BN, PA, PB, EPI, NS,
+ * TM>"; "" for ops without one); it has no counterpart in the reference. */
 int sj_model_profile(sj_model *m, int on);
 long sj_model_profile_collect(sj_model *m);
 int sj_model_profile_entry(sj_model *m, long i, const char **name, double *total_ms, long *calls);
+int sj_model_profile_kernel(sj_model *m, long i, const char **kernel);
 /* The stored forward activations of the last step in a fixed pack order
  * (per layer x, z, q, k, v, o, lse, x1, z2, g, u, h; then the last residual
  * x_L, the final-norm output and the fp32 logits), converted to fp32 (exact

@@ -215,6 +215,7 @@ SIGNATURES = {
     "sj_model_read_loss": (_I, [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "sj_model_profile": (_I, [_P, _I]),
     "sj_model_profile_collect": (_L, [_P]),
+    "sj_model_profile_kernel": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p)]),
     "sj_model_profile_entry": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(_L)]),
     "sj_model_activation_count": (_L, [_P]),

@@ -11,6 +11,10 @@
 static thread_local char g_last_error[1024] = "";
 
 namespace sjh {
+ProfHook& prof_hook() {
+  static thread_local ProfHook h;
+  return h;
+}
 int fail(int status, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);

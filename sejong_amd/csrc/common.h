@@ -136,6 +136,17 @@ int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ld
                            float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
                            const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
                            uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
+// Profiling hook of the step driver: while one of its ops is timed
+// (sj_model_profile), the op's GEMM kernel is launched with hipExtLaunchKernel
+// recording k0 / k1 at its own start and end (the kernel's duration, apart
+// from launch gaps and any split-K reduce) and notes the kernel's name.
+struct ProfHook {
+  bool on = false;
+  hipEvent_t k0 = nullptr, k1 = nullptr;
+  bool used = false;
+  char kernel[80] = {0};
+};
+ProfHook& prof_hook();
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);

@@ -310,11 +310,14 @@ struct sj_model {
   // buffer twice the Infinity Cache (512 MiB), so the op reads from HBM
   bool cold = false;
   float* flush = nullptr;
-  std::vector<hipEvent_t> prof_events;
+  std::vector<hipEvent_t> prof_events;  // start, end, GEMM kernel start, end per recorded op
   std::vector<const char*> prof_names;  // one per recorded op
+  std::vector<char> prof_kused;         // the op's GEMM kernel recorded its own events
+  std::vector<std::string> prof_kernel; // GEMM kernel the op launched ("" if none)
   std::vector<std::string> agg_names;
   std::vector<double> agg_ms;
   std::vector<long> agg_calls;
+  std::vector<std::string> agg_kernel;
   // SGD step driver (optimizer 1) and its parameter VJP
   int optimizer = 0;  // 0 AdamW, 1 SGD
   sj_sgd_config sgd = {};
@@ -366,11 +369,13 @@ int dalloc(sj_model* m, void** p, size_t bytes) {
 constexpr long FLUSH_FLOATS = 128L << 20;  // 512 MiB
 
 // Run one op; when profiling, bracket it with a pair of events on the model
-// stream (the kernel-profile feature of the reference, lib.rs:451-482).
+// stream (the kernel-profile feature of the reference, lib.rs:451-482).  A
+// GEMM op's kernel also records a second pair at its own start and end
+// (through the GEMM's profiling hook), which notes the kernel's name.
 int prof_mark(sj_model* m, const char* name) {
   size_t k = m->prof_names.size();
-  if (2 * k + 2 > m->prof_events.size()) {
-    for (int i = 0; i < 64; i++) {
+  if (4 * k + 4 > m->prof_events.size()) {
+    for (int i = 0; i < 128; i++) {
       hipEvent_t e;
       SJ_HIP(hipEventCreate(&e));
       m->prof_events.push_back(e);
@@ -378,12 +383,23 @@ int prof_mark(sj_model* m, const char* name) {
   }
   m->prof_names.push_back(name);
   if (m->cold && m->flush) TRY(sj_fill(m->stream, m->flush, SJ_F32, FLUSH_FLOATS, 0.f));
-  SJ_HIP(hipEventRecord(m->prof_events[2 * k], m->stream));
+  SJ_HIP(hipEventRecord(m->prof_events[4 * k], m->stream));
+  sjh::ProfHook& h = sjh::prof_hook();
+  h.on = true;
+  h.k0 = m->prof_events[4 * k + 2];
+  h.k1 = m->prof_events[4 * k + 3];
+  h.used = false;
+  h.kernel[0] = 0;
   return SJ_OK;
 }
 int prof_end(sj_model* m) {
   size_t k = m->prof_names.size() - 1;
-  SJ_HIP(hipEventRecord(m->prof_events[2 * k + 1], m->stream));
+  sjh::ProfHook& h = sjh::prof_hook();
+  m->prof_kused.push_back(h.used ? 1 : 0);
+  m->prof_kernel.emplace_back(h.kernel);
+  h.on = false;
+  h.k0 = h.k1 = nullptr;
+  SJ_HIP(hipEventRecord(m->prof_events[4 * k + 1], m->stream));
   return SJ_OK;
 }
 #define OP(name, call)                         \
@@ -2014,22 +2030,40 @@ extern "C" long sj_model_profile_collect(sj_model* m) {
   m->agg_names.clear();
   m->agg_ms.clear();
   m->agg_calls.clear();
-  for (size_t k = 0; k < m->prof_names.size(); k++) {
-    float ms = 0.f;
-    if (hipEventElapsedTime(&ms, m->prof_events[2 * k], m->prof_events[2 * k + 1]) != hipSuccess) return -1;
-    std::string nm(m->prof_names[k]);
+  m->agg_kernel.clear();
+  auto add = [&](const std::string& nm, float ms, const std::string& kernel) {
     size_t j = 0;
     while (j < m->agg_names.size() && m->agg_names[j] != nm) j++;
     if (j == m->agg_names.size()) {
       m->agg_names.push_back(nm);
       m->agg_ms.push_back(0.0);
       m->agg_calls.push_back(0);
+      m->agg_kernel.push_back(kernel);
     }
     m->agg_ms[j] += ms;
     m->agg_calls[j] += 1;
+  };
+  if (m->prof_kused.size() != m->prof_names.size()) return -1;  // an op was left open
+  for (size_t k = 0; k < m->prof_names.size(); k++) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, m->prof_events[4 * k], m->prof_events[4 * k + 1]) != hipSuccess) return -1;
+    const std::string nm(m->prof_names[k]);
+    add(nm, ms, m->prof_kernel[k]);
+    if (m->prof_kused[k]) {  // the GEMM kernel alone, from its own start to its end
+      if (hipEventElapsedTime(&ms, m->prof_events[4 * k + 2], m->prof_events[4 * k + 3]) != hipSuccess) return -1;
+      add(nm + "#kernel", ms, m->prof_kernel[k]);
+    }
   }
   m->prof_names.clear();
+  m->prof_kused.clear();
+  m->prof_kernel.clear();
   return (long)m->agg_names.size();
+}
+
+extern "C" int sj_model_profile_kernel(sj_model* m, long i, const char** kernel) {
+  SJ_REQUIRE(m && i >= 0 && i < (long)m->agg_kernel.size(), "profile_kernel: index %ld", i);
+  if (kernel) *kernel = m->agg_kernel[i].c_str();
+  return SJ_OK;
 }
 
 extern "C" int sj_model_profile_entry(sj_model* m, long i, const char** name, double* total_ms, long* calls) {

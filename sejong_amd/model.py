@@ -529,15 +529,20 @@ class Model:
         N.api.sj_model_profile(self.h, 2 if (on and cold) else int(on))
 
     def profile_collect(self) -> dict[str, tuple[float, int]]:
-        """{op name: (total ms, calls)} for the ops run since the last collect."""
+        """{op name: (total ms, calls)} for the ops run since the last collect
+        (a split-K GEMM op also as "<op>#kernel": its GEMM kernel alone);
+        profile_kernels then maps each name to the GEMM kernel it launched."""
         n = N.load().sj_model_profile_collect(self.h)
         if n < 0:
             raise N.SejongError(3, "profile collection failed")
-        out = {}
+        out, self.profile_kernels = {}, {}
         for i in range(n):
             name, ms, calls = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_long()
+            kern = ctypes.c_char_p()
             N.api.sj_model_profile_entry(self.h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(calls))
+            N.api.sj_model_profile_kernel(self.h, i, ctypes.byref(kern))
             out[name.value.decode()] = (ms.value, calls.value)
+            self.profile_kernels[name.value.decode()] = (kern.value or b"").decode()
         return out
 
     def buffer(self, what: str) -> tuple[int, int]:

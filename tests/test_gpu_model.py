@@ -247,3 +247,45 @@ def test_graph_replay_equals_eager_and_is_deterministic():
     np.testing.assert_array_equal(out[1][0], out[2][0])
     assert out[0][1] == out[1][1]
     assert out[0][1][-1] < out[0][1][0]  # the loss moves down on a fixed batch
+
+
+def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
+    """Per-op profiling (sj_model_profile) runs the step on one stream and
+    launches each GEMM op's kernel with events at its own start and end: the
+    parameters after two profiled steps equal those of two plain steps
+    bit for bit, every GEMM op reports a "#kernel" aggregate no longer than
+    the op and names a k_gemm_fast instantiation, other ops name none."""
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    mc, tc = config("cfg2")
+    mc.layers, tc.batch, tc.sequence = 2, 2, 128
+    params = init_params(mc, std=0.02)
+    ids, tg = byte_batch(Rng(7), tc.batch, tc.sequence)
+    out = []
+    for prof in (False, True):
+        model = Model(mc, tc)
+        try:
+            model.set_params(params)
+            model.set_batch(ids, tg)
+            model.profile(prof)
+            for _ in range(2):
+                model.train_step(1e-3)
+            if prof:
+                agg = model.profile_collect()
+                kern = dict(model.profile_kernels)
+                model.profile(False)
+            out.append(model.get_params())
+        finally:
+            model.close()
+    np.testing.assert_array_equal(out[0], out[1])
+    gemm_ops = ["qkv_rope", "attn_out_residual", "gate_up_swiglu", "down_residual", "qkv_dx", "qkv_dw",
+                "attn_out_dx", "attn_out_dw", "gate_up_dx", "gate_up_dw", "down_dx_swiglu", "down_dw"]
+    for op in gemm_ops:
+        assert op in agg and op + "#kernel" in agg, op
+        ms, calls = agg[op]
+        kms, kcalls = agg[op + "#kernel"]
+        assert calls == kcalls == 2 * mc.layers, (op, calls, kcalls)
+        assert 0 < kms <= ms, (op, kms, ms)
+        assert kern[op].startswith("k_gemm_fast<") and kern[op] == kern[op + "#kernel"], (op, kern[op])
+    for op in ("attention_fwd", "rmsnorm", "adamw"):
+        assert op in agg and kern[op] == "", (op, kern.get(op))
