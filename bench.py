@@ -758,7 +758,7 @@ def main():
                     help="sequences the CPU baseline runs (default: cpu_sample_batch, about 10 s of FP64 work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels-json", default="", help="also write the per-op profile to this file")
-    ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region")
+    ap.add_argument("--profile-steps", type=int, default=5, help="eager steps timed op by op after the timed region (then as many with each GEMM kernel timed alone)")
     ap.add_argument("--cold-steps", type=int, default=1,
                     help="eager steps timed op by op with a 512 MiB cache flush before every op (0: skip)")
     ap.add_argument("--workload", default="step", choices=["step", "moe", "pvjp"],
@@ -817,13 +817,19 @@ def main():
     for _ in range(max(1, args.profile_steps)):
         model.train_step(tc.learning_rate)
     prof = model.profile_collect()
-    op_kernel = dict(model.profile_kernels)
     model.profile(False)
     nprof = max(1, args.profile_steps)
     prof = {op: (ms / nprof, calls // nprof) for op, (ms, calls) in prof.items()}
-    # GEMM ops: their GEMM kernel alone (events at its own start and end)
-    kern_only = {op[:-len("#kernel")]: v for op, v in prof.items() if op.endswith("#kernel")}
-    prof = {op: v for op, v in prof.items() if "#" not in op}
+    # the same steps again with every GEMM op's kernel timed alone (events
+    # its launch records at the kernel's own start and end)
+    model.profile(True, kernels=True)
+    for _ in range(nprof):
+        model.train_step(tc.learning_rate)
+    kprof = model.profile_collect()
+    op_kernel = dict(model.profile_kernels)
+    model.profile(False)
+    kern_only = {op[:-len("#kernel")]: (ms / nprof, calls // nprof) for op, (ms, calls) in kprof.items()
+                 if op.endswith("#kernel")}
     # cold-cache pass: a 512 MiB buffer is written before every op, so the
     # bandwidth-bound ops read their operands from HBM rather than from the
     # 256 MB Infinity Cache
@@ -834,8 +840,7 @@ def main():
             model.train_step(tc.learning_rate)
         cold = model.profile_collect()
         model.profile(False)
-        cold = {op: (ms / args.cold_steps, calls // args.cold_steps) for op, (ms, calls) in cold.items()
-                if "#" not in op}
+        cold = {op: (ms / args.cold_steps, calls // args.cold_steps) for op, (ms, calls) in cold.items()}
     prof_total = sum(ms for ms, _ in prof.values())
     rows = []
     for op, (ms, calls) in sorted(prof.items(), key=lambda kv: -kv[1][0]):

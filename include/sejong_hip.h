@@ -798,11 +798,12 @@ int sj_model_forward_cached(sj_model *m, sj_cache *c, const int32_t *tokens, lon
  * its last call by op name and returns the number of names (or -1);
  * sj_model_profile_entry reads one aggregate.  on = 2 times every op
  * cold: before its event pair the stream writes a 512 MiB buffer (twice the
- * 256 MB Infinity Cache), so the op's operands come from HBM.  A GEMM op
- * also yields an aggregate "<op>#kernel": its GEMM kernel alone, timed by
- * events at the kernel's own start and end (hipExtLaunchKernel), without
- * launch gaps or a split-K reduce.  sj_model_profile_kernel names the GEMM
- * kernel an aggregate's
+ * 256 MB Infinity Cache), so the op's operands come from HBM.  on = 3 also
+ * times each GEMM op's kernel alone, by events the launch records at the
+ * kernel's own start and end (hipExtLaunchKernel: no launch gaps, no split-K
+ * reduce), as an aggregate "<op>#kernel" (the extra packets lengthen the
+ * op's own pair, so op times come from on = 1).  sj_model_profile_kernel
+ * names the GEMM kernel an aggregate's
  * op launched, as rocprofv3 lists it ("k_gemm_fast<BM, BN, PA, PB, EPI, NS,
  * TM>"; "" for ops without one); it has no counterpart in the reference. */
 int sj_model_profile(sj_model *m, int on);

@@ -137,9 +137,10 @@ int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ld
                            const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
                            uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
 // Profiling hook of the step driver: while one of its ops is timed
-// (sj_model_profile), the op's GEMM kernel is launched with hipExtLaunchKernel
-// recording k0 / k1 at its own start and end (the kernel's duration, apart
-// from launch gaps and any split-K reduce) and notes the kernel's name.
+// (sj_model_profile), the op's GEMM launch notes the kernel's name and, in
+// kernel timing mode (k0 set), launches it with hipExtLaunchKernel recording
+// k0 / k1 at its own start and end (the kernel's duration, apart from launch
+// gaps and any split-K reduce).
 struct ProfHook {
   bool on = false;
   hipEvent_t k0 = nullptr, k1 = nullptr;

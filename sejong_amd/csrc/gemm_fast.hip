@@ -780,13 +780,14 @@ int launch_ns(hipStream_t s, const FParams& p, int splits) {
   // grid z: split-K slices, or the experts of a per-expert dW launch
   dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
   sjh::ProfHook& h = sjh::prof_hook();
-  if (h.on && h.k0) {  // a timed op: events at the kernel's own start and end
+  if (h.on && h.k0) {  // kernel timing: events at the kernel's own start and end
     hipExtLaunchKernelGGL(kern, grid, dim3(NT), (uint32_t)lds, s, h.k0, h.k1, 0u, p);
     h.used = true;
-    snprintf(h.kernel, sizeof(h.kernel), "k_gemm_fast<%d, %d, %d, %d, %d, %d, %d>", BM, BN, PA, PB, EPI, NS, TM);
   } else {
     hipLaunchKernelGGL(kern, grid, dim3(NT), lds, s, p);
   }
+  if (h.on)
+    snprintf(h.kernel, sizeof(h.kernel), "k_gemm_fast<%d, %d, %d, %d, %d, %d, %d>", BM, BN, PA, PB, EPI, NS, TM);
   return SJ_OK;
 }
 

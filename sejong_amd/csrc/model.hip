@@ -309,6 +309,9 @@ struct sj_model {
   // cold-cache profiling: before every op's event pair the stream writes a
   // buffer twice the Infinity Cache (512 MiB), so the op reads from HBM
   bool cold = false;
+  // kernel timing: each GEMM op's kernel records events at its own start and
+  // end (hipExtLaunchKernel; its extra packets lengthen the op's own pair)
+  bool kernel_events = false;
   float* flush = nullptr;
   std::vector<hipEvent_t> prof_events;  // start, end, GEMM kernel start, end per recorded op
   std::vector<const char*> prof_names;  // one per recorded op
@@ -386,8 +389,8 @@ int prof_mark(sj_model* m, const char* name) {
   SJ_HIP(hipEventRecord(m->prof_events[4 * k], m->stream));
   sjh::ProfHook& h = sjh::prof_hook();
   h.on = true;
-  h.k0 = m->prof_events[4 * k + 2];
-  h.k1 = m->prof_events[4 * k + 3];
+  h.k0 = m->kernel_events ? m->prof_events[4 * k + 2] : nullptr;
+  h.k1 = m->kernel_events ? m->prof_events[4 * k + 3] : nullptr;
   h.used = false;
   h.kernel[0] = 0;
   return SJ_OK;
@@ -2016,10 +2019,11 @@ static int run_step(sj_model* m) {
 }
 
 extern "C" int sj_model_profile(sj_model* m, int on) {
-  SJ_REQUIRE(m && on >= 0 && on <= 2, "profile: mode");
+  SJ_REQUIRE(m && on >= 0 && on <= 3, "profile: mode");
   if (on == 2 && !m->flush) TRY(dalloc(m, (void**)&m->flush, (size_t)FLUSH_FLOATS * 4));
   m->profiling = on != 0;
   m->cold = on == 2;
+  m->kernel_events = on == 3;
   return SJ_OK;
 }
 

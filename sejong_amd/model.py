@@ -523,10 +523,11 @@ class Model:
     def synchronize(self):
         N.api.sj_synchronize(ctypes.c_void_p(self.stream))
 
-    def profile(self, on: bool = True, cold: bool = False):
+    def profile(self, on: bool = True, cold: bool = False, kernels: bool = False):
         """Per-op HIP-event timing of eager steps; cold: a 512 MiB buffer is
-        written before each op so its operands come from HBM."""
-        N.api.sj_model_profile(self.h, 2 if (on and cold) else int(on))
+        written before each op so its operands come from HBM; kernels: each
+        GEMM op's kernel is also timed alone ("<op>#kernel" aggregates)."""
+        N.api.sj_model_profile(self.h, 0 if not on else 2 if cold else 3 if kernels else 1)
 
     def profile_collect(self) -> dict[str, tuple[float, int]]:
         """{op name: (total ms, calls)} for the ops run since the last collect

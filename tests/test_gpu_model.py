@@ -250,8 +250,9 @@ def test_graph_replay_equals_eager_and_is_deterministic():
 
 
 def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
-    """Per-op profiling (sj_model_profile) runs the step on one stream and
-    launches each GEMM op's kernel with events at its own start and end: the
+    """Per-op profiling in kernel-timing mode (sj_model_profile 3) runs the
+    step on one stream and launches each GEMM op's kernel with events at its
+    own start and end: the
     parameters after two profiled steps equal those of two plain steps
     bit for bit, every GEMM op reports a "#kernel" aggregate no longer than
     the op and names a k_gemm_fast instantiation, other ops name none."""
@@ -267,7 +268,7 @@ def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
         try:
             model.set_params(params)
             model.set_batch(ids, tg)
-            model.profile(prof)
+            model.profile(prof, kernels=True)
             for _ in range(2):
                 model.train_step(1e-3)
             if prof:
