@@ -243,15 +243,31 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  // The kernel arguments the prologue reads, fetched together at entry and
+  // held in SGPRs: loaded at their first uses, behind branches and address
+  // arithmetic, they cost one dependent kernarg round trip each (about 6000
+  // cycles before the first DMA).
+  long pM = p.M, pN = p.N, pK = p.K, plda = p.lda, pkch = p.kchunk, sn1 = p.seg_n[1], sn2 = p.seg_n[2];
+  int pxr = p.xcd_remap, pgm = p.gmode, pns = p.nseg, pgE = p.gE;
+  const bf16_t *a0 = p.a[0], *a1 = p.a[1];
+  const bf16_t *b00 = p.b[0][0], *b01 = p.b[0][1], *b02 = p.b[0][2], *b10 = p.b[1][0], *b11 = p.b[1][1],
+               *b12 = p.b[1][2];
+  long ldb0 = p.ldb[0], ldb1 = p.ldb[1], ldb2 = p.ldb[2], gsb = p.gstride_b, gsc = p.gstride_c;
+  const int* goff = p.goff;
+  unsigned nx = gridDim.x, ny = gridDim.y, nz = gridDim.z;
+  asm volatile("" : "+s"(pM), "+s"(pN), "+s"(pK), "+s"(plda), "+s"(pkch), "+s"(sn1), "+s"(sn2), "+s"(pxr),
+                    "+s"(pgm), "+s"(pns), "+s"(pgE));
+  asm volatile("" : "+s"(a0), "+s"(a1), "+s"(b00), "+s"(b01), "+s"(b02), "+s"(b10), "+s"(b11), "+s"(b12));
+  asm volatile("" : "+s"(ldb0), "+s"(ldb1), "+s"(ldb2), "+s"(gsb), "+s"(gsc), "+s"(goff), "+s"(nx), "+s"(ny),
+                    "+s"(nz));
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8
   // XCDs (linear id b -> XCD b % 8), each with its own L2.  Give XCD k a
   // contiguous run of the row-major tile order so the tiles that share A rows
   // (and split-K slices) meet in one L2.
-  const unsigned nx = gridDim.x, ny = gridDim.y, nz = gridDim.z;
   const unsigned nb = nx * ny * nz;
   const unsigned b = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
   unsigned logical = b;
-  if (p.xcd_remap) {
+  if (pxr) {
     const unsigned xcd = b & 7, local = b >> 3, q8 = nb >> 3, r8x = nb & 7;
     logical = xcd * q8 + (xcd < r8x ? xcd : r8x) + local;
   }
@@ -268,29 +284,30 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   const unsigned tz = logical / (nx * ny);
   const long m0 = (long)ty * BM, n0 = (long)tx * BN;
   int ge = 0;
-  if (p.gmode == 1) {
-    if (m0 >= p.goff[p.gE]) return;  // beyond the last expert segment: the whole workgroup leaves
-    while (ge + 1 < p.gE && m0 >= p.goff[ge + 1]) ge++;
-  } else if (p.gmode == 2) {
+  if (pgm == 1) {
+    if (m0 >= goff[pgE]) return;  // beyond the last expert segment: the whole workgroup leaves
+    while (ge + 1 < pgE && m0 >= goff[ge + 1]) ge++;
+  } else if (pgm == 2) {
     ge = (int)tz;
   }
-  const long boff = p.gmode == 1 ? (long)ge * p.gstride_b : 0;
-  const long coff = p.gmode == 2 ? (long)ge * p.gstride_c : 0;
+  const long boff = pgm == 1 ? (long)ge * gsb : 0;
+  const long coff = pgm == 2 ? (long)ge * gsc : 0;
   int seg = 0;
 #pragma unroll
   for (int s = 1; s < 3; s++)
-    if (s < p.nseg && n0 >= p.seg_n[s]) seg = s;
-  const long nl0 = n0 - p.seg_n[seg];
-  const long seg_end = (seg + 1 < p.nseg) ? p.seg_n[seg + 1] : p.N;
-  const long nrows_b = seg_end - p.seg_n[seg];
+    if (s < pns && n0 >= (s == 1 ? sn1 : sn2)) seg = s;
+  const long seg0 = seg == 0 ? 0 : seg == 1 ? sn1 : sn2;
+  const long nl0 = n0 - seg0;
+  const long seg_end = (seg + 1 < pns) ? (seg == 0 ? sn1 : sn2) : pN;
+  const long nrows_b = seg_end - seg0;
 
-  long kbeg = 0, kend = p.K;
-  if (p.gmode == 2) {
-    kbeg = p.goff[ge];
-    kend = p.goff[ge + 1];
+  long kbeg = 0, kend = pK;
+  if (pgm == 2) {
+    kbeg = goff[ge];
+    kend = goff[ge + 1];
   } else if (EPI == E_PARTIAL) {
-    kbeg = (long)tz * p.kchunk;
-    kend = kbeg + p.kchunk < p.K ? kbeg + p.kchunk : p.K;
+    kbeg = (long)tz * pkch;
+    kend = kbeg + pkch < pK ? kbeg + pkch : pK;
   }
   const int nk = (int)((kend - kbeg + BK - 1) / BK);
 
@@ -324,17 +341,17 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     bool tr;
     if (r8 < AROWS) {
       const int pl = r8 / BM;
-      base = pl ? p.a[1] : p.a[0];
-      ld = p.lda;
+      base = pl ? a1 : a0;
+      ld = plda;
       tr = TA;
       row = tr ? m0 + ((r8 % BM) / 64) * 64 : m0 + (r8 % BM) + (sl >> 3);
-      rows = p.M;
+      rows = pM;
     } else {
       const int rb = r8 - AROWS;
       const int q = rb / (BN * PB), pl = (rb % (BN * PB)) / BN;
       const int sg = DUAL ? q : seg;
-      base = (pl ? p.b[1][sg] : p.b[0][sg]) + boff;
-      ld = p.ldb[sg];
+      base = (pl ? (sg == 0 ? b10 : sg == 1 ? b11 : b12) : (sg == 0 ? b00 : sg == 1 ? b01 : b02)) + boff;
+      ld = sg == 0 ? ldb0 : sg == 1 ? ldb1 : ldb2;
       tr = TB;
       row = tr ? nl0 + ((rb % BN) / 64) * 64 : nl0 + (rb % BN) + (sl >> 3);
       rows = nrows_b;
@@ -353,6 +370,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   }
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
   const long klen = kend - kbeg;
+  // this wave's share of stage `it` into buffer `buf`
   auto issue = [&](int it, int buf) {
     const long k0 = (long)it * BK;  // relative to kbeg
     const uint32_t sbase = lds_base + (uint32_t)(buf * STAGE_ROWS * BK * 2) + (uint32_t)(wave_s * 8 * BK * 2);
@@ -387,7 +405,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       const int q = threadIdx.x + i * NT;
       const long m = m0 + q / CPR8, n = n0 + (q % CPR8) * 8;
       gpre[i] = upre[i] = u32x4{0u, 0u, 0u, 0u};
-      if (q < BM * CPR8 && m < p.M && n + 8 <= p.N) {
+      if (q < BM * CPR8 && m < pM && n + 8 <= pN) {
         gpre[i] = *(const u32x4*)(p.gin + m * p.ldgu + n);
         upre[i] = *(const u32x4*)(p.uin + m * p.ldgu + n);
       }
@@ -477,8 +495,8 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     for (int j = 0; j < NB; j++) {
       const int cl = wn * WN + j * 16 + cc;
       const long ncol = n0 + cl;
-      const long nloc = ncol - p.seg_n[seg];
-      const bool colok = ncol < p.N;
+      const long nloc = ncol - seg0;
+      const bool colok = ncol < pN;
       float v[4] = {acc[0][i][j][0], acc[0][i][j][1], acc[0][i][j][2], acc[0][i][j][3]};
       if constexpr (EPI == E_SWIGLU_BWD) {
         // v = dH; dG = dH*u*s*(1+g(1-s)), dU = dH*g*s  (kernels.py:95-101)
@@ -486,7 +504,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
         for (int r = 0; r < 4; r++) {
           const long m = mb + r;
           float g = 0.f, u = 0.f;
-          if (m < p.M && colok) {
+          if (m < pM && colok) {
             g = bf2f(p.gin[m * p.ldgu + ncol]);
             u = bf2f(p.uin[m * p.ldgu + ncol]);
           }
@@ -544,7 +562,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     for (int q = tid; q < BM * CPR; q += NT) {
       const int r = q / CPR, c8 = (q % CPR) * 8;
       const long m = m0 + r, n = n0 + c8;
-      if (m >= p.M || n >= p.N) continue;
+      if (m >= pM || n >= pN) continue;
       const u32x4 val = *(const u32x4*)(t + r * TLD + c8);
       dst_of(m, n, val, t + r * TLD + c8);
     }
@@ -555,26 +573,26 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     for (int q = tid; q < BN * RPC; q += NT) {
       const int c = q / RPC, r8 = (q % RPC) * 8;
       const long n = n0 + c, m = m0 + r8;
-      if (n >= p.N || m >= p.M) continue;
+      if (n >= pN || m >= pM) continue;
       bf16_t v8[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) v8[i] = t[(r8 + i) * TLD + c];
       bf16_t* d = dst + n * ldt + m;
-      if (m + 8 <= p.M && (((uintptr_t)d & 15) == 0)) {
+      if (m + 8 <= pM && (((uintptr_t)d & 15) == 0)) {
         *(u32x4*)d = u32x4{pack2(v8[0], v8[1]), pack2(v8[2], v8[3]), pack2(v8[4], v8[5]), pack2(v8[6], v8[7])};
       } else {
         for (int i = 0; i < 8; i++)
-          if (m + i < p.M) d[i] = v8[i];
+          if (m + i < pM) d[i] = v8[i];
       }
     }
   };
   // plain bf16 store of a chunk at d (8 values, n..n+7 of a row)
   auto put8 = [&](bf16_t* d, long n, const u32x4& val, const bf16_t* src) {
-    if (n + 8 <= p.N && (((uintptr_t)d & 15) == 0)) {
+    if (n + 8 <= pN && (((uintptr_t)d & 15) == 0)) {
       *(u32x4*)d = val;
     } else {
       for (int i = 0; i < 8; i++)
-        if (n + i < p.N) d[i] = src[i];
+        if (n + i < pN) d[i] = src[i];
     }
   };
 
@@ -599,7 +617,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       const int q = tid + i * NT;
       const int r = q / CPR8, c8 = (q % CPR8) * 8;
       const long m = m0 + r, n = n0 + c8;
-      if (q >= BM * CPR8 || m >= p.M || n + 8 > p.N) continue;
+      if (q >= BM * CPR8 || m >= pM || n + 8 > pN) continue;
       const float4 d0 = *(const float4*)(TF + r * TLDF + c8);
       const float4 d1 = *(const float4*)(TF + r * TLDF + c8 + 4);
       const float dh[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
@@ -636,7 +654,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       for (int q = threadIdx.x; q < BM * NH * 4; q += NT) {
         const int g = q & 3, rh = q >> 2, r = rh / NH, hc = rh % NH;
         const long m = m0 + r, col0 = n0 + 64 * hc;
-        const bool ok = m < p.M && col0 < p.N;
+        const bool ok = m < pM && col0 < pN;
         float dpart = 0.f;
         if (ok) {
 #pragma unroll
@@ -675,8 +693,8 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
       int sg = 0;
       for (int s2 = 1; s2 < 3; s2++)
-        if (s2 < p.nseg && n >= p.seg_n[s2]) sg = s2;
-      const long nl = n - p.seg_n[sg];
+        if (s2 < pns && n >= (s2 == 1 ? sn1 : sn2)) sg = s2;
+      const long nl = n - (sg == 0 ? 0 : sg == 1 ? sn1 : sn2);
       u32x4 o = val;
       bf16_t rot[8];
       if (n < p.rope_cols) {
@@ -705,7 +723,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     rows_bf16(T, [&](long m, long n, const u32x4& val, const bf16_t* src) {
       const bf16_t* rr = p.r + m * p.ldr + n;
       bf16_t* d = (bf16_t*)p.c[0] + m * p.ldc[0] + n;
-      if (n + 8 <= p.N && (((uintptr_t)d & 15) == 0) && (((uintptr_t)rr & 15) == 0)) {
+      if (n + 8 <= pN && (((uintptr_t)d & 15) == 0) && (((uintptr_t)rr & 15) == 0)) {
         const u32x4 rv = *(const u32x4*)rr;
         u32x4 o;
 #pragma unroll
@@ -717,7 +735,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
         *(u32x4*)d = o;
       } else {
         for (int i = 0; i < 8; i++)
-          if (n + i < p.N) d[i] = f2bf(bf2f(rr[i]) + bf2f(src[i]));
+          if (n + i < pN) d[i] = f2bf(bf2f(rr[i]) + bf2f(src[i]));
       }
     });
   } else {  // E_STORE / E_PARTIAL
@@ -727,16 +745,16 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
       });
     } else {
       constexpr int CPR = BN / 4;
-      float* dst0 = EPI == E_PARTIAL ? p.partial + (long)tz * p.M * p.N : (float*)p.c[0] + coff;
-      const long ldd = EPI == E_PARTIAL ? p.N : p.ldc[0];
+      float* dst0 = EPI == E_PARTIAL ? p.partial + (long)tz * pM * pN : (float*)p.c[0] + coff;
+      const long ldd = EPI == E_PARTIAL ? pN : p.ldc[0];
       const bool acc_out = EPI == E_STORE && p.accumulate;
       for (int q = tid; q < BM * CPR; q += NT) {
         const int r = q / CPR, c4 = (q % CPR) * 4;
         const long m = m0 + r, n = n0 + c4;
-        if (m >= p.M || n >= p.N) continue;
+        if (m >= pM || n >= pN) continue;
         const float4 val = *(const float4*)(TF + r * TLDF + c4);
         float* d = dst0 + m * ldd + n;
-        if (n + 4 <= p.N && (((uintptr_t)d & 15) == 0)) {
+        if (n + 4 <= pN && (((uintptr_t)d & 15) == 0)) {
           if (acc_out) {
             const float4 o = *(const float4*)d;
             *(float4*)d = make_float4(o.x + val.x, o.y + val.y, o.z + val.z, o.w + val.w);
@@ -746,7 +764,7 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
         } else {
           const float vv[4] = {val.x, val.y, val.z, val.w};
           for (int k = 0; k < 4; k++)
-            if (n + k < p.N) d[k] = acc_out ? d[k] + vv[k] : vv[k];
+            if (n + k < pN) d[k] = acc_out ? d[k] + vv[k] : vv[k];
         }
       }
     }
