@@ -819,7 +819,10 @@ long sj_model_activation_count(const sj_model *m);
 int sj_model_export_activations(sj_model *m, float *host);
 /* Device pointers of internal buffers for callers that time or inspect
  * kernels directly (what: "logits", "loss_rows", "ids", "targets",
- * "params", "grads", "mirror", "mirror_t", "workspace", "stream", and for
+ * "params", "grads", "mirror", "mirror_t", "workspace", "stream",
+ * "grad_sq_slots" (fp64: the FP64 squared-norm partials the last backward's
+ * gradient producers wrote; elements 0 when the update summed the arena
+ * instead), and for
  * parameter-VJP models "vjp_columns", "vjp_rows", "vjp_map" (int32) and
  * "vjp_basis" (fp32 [tokens][rank]); for MoE models, per layer l,
  * "route_ids.<l>" (int32 [rows][top_k]), "route_weights.<l>" (fp32),

@@ -15,6 +15,10 @@ ProfHook& prof_hook() {
   static thread_local ProfHook h;
   return h;
 }
+GradSq& grad_sq() {
+  static thread_local GradSq g;
+  return g;
+}
 int fail(int status, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);

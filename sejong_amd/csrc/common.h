@@ -148,6 +148,30 @@ struct ProfHook {
   char kernel[80] = {0};
 };
 ProfHook& prof_hook();
+// Gradient-norm hook of the step driver.  While armed (base set) and `on`
+// (around each call that writes a gradient), the gradient producer (the
+// split-K reduce of a dW product, the norm-weight reduce, the embedding
+// backward) also writes the FP64 sum of squares of the values it stores, one
+// per workgroup, into the next slots of base[0 .. cap); a fixed-order sum
+// over the slots then gives the squared gradient norm without a pass over
+// the gradient arena.  A gradient written any other way (a dW product
+// without split-K) sets `missed`, and the step sums the arena instead.
+struct GradSq {
+  double* base = nullptr;
+  long next = 0, cap = 0;
+  bool missed = false, on = false;
+  double* take(long n) {
+    if (!base || !on) return nullptr;
+    if (next + n > cap) {
+      missed = true;
+      return nullptr;
+    }
+    double* p = base + next;
+    next += n;
+    return p;
+  }
+};
+GradSq& grad_sq();
 // Record a failure message for sj_last_error() and return the status.
 int fail(int status, const char* fmt, ...);
 int hip_check(hipError_t e, const char* what);
@@ -157,6 +181,8 @@ int rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, c
                            float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi, uint16_t* dx_t_lo,
                            long ldt, long rows, long d, float eps, float* partial);
 int rmsnorm_reduce_multi(void* stream, const sj::RmsReduceJob* jobs, long njobs, long max_d);
+// out[0] = FP64 sum of slots[0 .. count) in a fixed order (one workgroup)
+int sum_slots(hipStream_t stream, const double* slots, long count, double* out);
 // one-time kernel attribute setup (dynamic LDS limits), outside capture
 int norm_prepare();
 int gemm_fast_prepare();

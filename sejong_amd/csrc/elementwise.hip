@@ -419,9 +419,11 @@ extern "C" size_t sj_embedding_bwd_workspace_bytes(long n, long vocab) { return 
 // then every thread adds up to two float4 columns of the matching rows in
 // that order (the same order, hence the same bits, as k_embedding_bwd).
 constexpr int EMB_IDS = 16;
+// sq (nullable): FP64 sum of squares of the row this workgroup stores, at
+// sq[blockIdx.x] (the gradient-norm hook)
 __global__ __launch_bounds__(EMB_THREADS) void k_embedding_bwd4(const float* __restrict__ dy,
                                                                 const int32_t* __restrict__ ids,
-                                                                float* __restrict__ dw, long n, long d) {
+                                                                float* __restrict__ dw, long n, long d, double* sq) {
   __shared__ int matches[EMB_THREADS * EMB_IDS];
   __shared__ int wave_total[EMB_THREADS / 64];
   const int v = blockIdx.x;
@@ -469,10 +471,20 @@ __global__ __launch_bounds__(EMB_THREADS) void k_embedding_bwd4(const float* __r
     }
     __syncthreads();
   }
+  double q = 0.0;
 #pragma unroll
   for (int c = 0; c < 2; c++) {
     const long col = t + (long)c * EMB_THREADS;
-    if (col < d4) ((float4*)(dw + (long)v * d))[col] = acc[c];
+    if (col < d4) {
+      ((float4*)(dw + (long)v * d))[col] = acc[c];
+      q += (double)acc[c].x * acc[c].x + (double)acc[c].y * acc[c].y + (double)acc[c].z * acc[c].z +
+           (double)acc[c].w * acc[c].w;
+    }
+  }
+  if (sq) {
+    __shared__ double qred[EMB_THREADS / 64];
+    q = block_sum<double, EMB_THREADS>(q, qred);
+    if (t == 0) sq[blockIdx.x] = q;
   }
 }
 
@@ -480,12 +492,14 @@ extern "C" int sj_embedding_bwd(void* stream, const float* dy, const int32_t* id
                                 long vocab, void* workspace, size_t workspace_bytes) {
   SJ_REQUIRE(n >= 0 && d > 0 && d <= 8 * EMB_THREADS && vocab > 0, "embedding_backward: n %ld d %ld vocab %ld", n,
              d, vocab);
-  if (d % 4 == 0 && d <= 8 * EMB_THREADS && ((uintptr_t)dy & 15) == 0 && ((uintptr_t)dw & 15) == 0)
+  if (d % 4 == 0 && d <= 8 * EMB_THREADS && ((uintptr_t)dy & 15) == 0 && ((uintptr_t)dw & 15) == 0) {
     hipLaunchKernelGGL(k_embedding_bwd4, dim3((unsigned)vocab), dim3(EMB_THREADS), 0, (hipStream_t)stream, dy, ids, dw,
-                       n, d);
-  else
+                       n, d, sjh::grad_sq().take(vocab));
+  } else {
     hipLaunchKernelGGL(k_embedding_bwd, dim3((unsigned)vocab), dim3(EMB_THREADS), 0, (hipStream_t)stream, dy, ids, dw,
                        n, d);
+    if (sjh::grad_sq().base && sjh::grad_sq().on) sjh::grad_sq().missed = true;
+  }
   SJ_LAUNCH_CHECK("embedding_backward");
   return SJ_OK;
 }
@@ -560,6 +574,29 @@ extern "C" int sj_loss_summary(void* stream, const float* loss, long n, double* 
   SJ_REQUIRE(n > 0 && slot >= 0, "loss_summary: n %ld", n);
   hipLaunchKernelGGL(k_loss_summary, dim3(1), dim3(256), 0, (hipStream_t)stream, loss, n, out, slot, weight);
   SJ_LAUNCH_CHECK("loss_summary");
+  return SJ_OK;
+}
+
+// one workgroup of 1024 threads, each summing eight neighbouring slots per
+// trip with all eight loads in flight, then a fixed-order block sum
+__global__ __launch_bounds__(1024) void k_sum_slots(const double* __restrict__ slots, long count, double* out) {
+  __shared__ double red[16];
+  double s = 0.0;
+  for (long i0 = 8L * threadIdx.x; i0 < count; i0 += 8L * 1024) {
+    double v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = i0 + u < count ? slots[i0 + u] : 0.0;
+#pragma unroll
+    for (int u = 0; u < 8; u++) s += v[u];
+  }
+  s = block_sum<double, 1024>(s, red);
+  if (threadIdx.x == 0) out[0] = s;
+}
+
+int sjh::sum_slots(hipStream_t stream, const double* slots, long count, double* out) {
+  SJ_REQUIRE(slots && out && count > 0 && count < (1L << 30), "sum_slots: %ld slots", count);
+  hipLaunchKernelGGL(k_sum_slots, dim3(1), dim3(1024), 0, stream, slots, count, out);
+  SJ_LAUNCH_CHECK("sum_slots");
   return SJ_OK;
 }
 

@@ -771,20 +771,31 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   }
 }
 
+// sq (nullable): FP64 sum of squares of the values this workgroup stores,
+// at sq[blockIdx.x] (the gradient-norm hook)
 __global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict__ partial, int splits, long M, long N,
-                                                         void* c, long ldc, int c_bf16, int accumulate) {
+                                                         void* c, long ldc, int c_bf16, int accumulate, double* sq) {
   const long total = M * N;
+  double q = 0.0;
   for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
     float s = 0.f;
     for (int z = 0; z < splits; z++) s += partial[(long)z * total + i];
     const long m = i / N, n = i - m * N;
     const long idx = m * ldc + n;
-    if (c_bf16)
+    if (c_bf16) {
       ((bf16_t*)c)[idx] = f2bf(s);
-    else if (accumulate)
-      ((float*)c)[idx] += s;
-    else
+    } else if (accumulate) {
+      s += ((float*)c)[idx];
       ((float*)c)[idx] = s;
+    } else {
+      ((float*)c)[idx] = s;
+    }
+    q += (double)s * (double)s;
+  }
+  if (sq) {
+    __shared__ double red[4];
+    q = block_sum<double, 256>(q, red);
+    if (threadIdx.x == 0) sq[blockIdx.x] = q;
   }
 }
 
@@ -937,6 +948,18 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits, bool ro
       // cfg3's global stage, slices of 512 lose: 4.07 -> 4.15 ms)
       const int want_s = dws > 0 ? dws : row_layout ? (K >= 4096 ? 4 : 1) : (K <= 4096 ? 1 : 4);
       splits = K / 256 < want_s ? (int)(K / 256) : want_s;
+      static int dwt_m = -1, dwt_n = 0;
+      if (dwt_m < 0) {
+        dwt_m = 0;
+        if (const char* e = getenv("SJ_GEMM_DW_TILE"))  // sweeps
+          if (sscanf(e, "%dx%d", &dwt_m, &dwt_n) != 2 || (dwt_m != 64 && dwt_m != 128) || (dwt_n != 64 && dwt_n != 128))
+            dwt_m = 0;
+      }
+      if (dwt_m) {
+        bm = dwt_m;
+        bn = dwt_n;
+        return;
+      }
       long want = tiles(M, N, 64, 64) * splits;
       want = want < 2 * cu ? want : 2 * cu;
       const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
@@ -1116,12 +1139,20 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
     int st = launch_planes<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
     if (st) return st;
     long total = M * N, blocks = (total + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
+    double* sq = nullptr;
+    sjh::GradSq& gs = sjh::grad_sq();
+    if (gs.base && gs.on) {  // gradient-norm slots: fewer, longer workgroups
+      if (blocks > 1024) blocks = 1024;
+      sq = gs.take(blocks);
+    } else if (blocks > 4096) {
+      blocks = 4096;
+    }
     hipLaunchKernelGGL(k_reduce_partials, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)workspace, splits, M,
-                       N, c, ldc, (int)p.c_bf16, accumulate);
+                       N, c, ldc, (int)p.c_bf16, accumulate, sq);
   } else {
     int st = launch_planes<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
     if (st) return st;
+    if (sjh::grad_sq().base && sjh::grad_sq().on) sjh::grad_sq().missed = true;
   }
   SJ_LAUNCH_CHECK("matmul planes");
   return SJ_OK;

@@ -294,6 +294,13 @@ struct sj_model {
   float* rope = nullptr;
   int32_t *ids = nullptr, *targets = nullptr;
   double *loss = nullptr, *sumsq = nullptr;
+  // FP64 squared-norm partials written by the gradient producers of the
+  // backward (sjh::GradSq): slots used by the last backward, and whether a
+  // gradient escaped them (then the update sums the arena)
+  static constexpr long GSQ_CAP = 32768;
+  double* gsq = nullptr;
+  long gsq_count = 0;
+  bool gsq_ok = false;
   int32_t* status = nullptr;
   sj_adam_step* step_dev = nullptr;
   // pinned ring of host step records: slot k is reused only after the copy
@@ -410,6 +417,14 @@ int prof_end(sj_model* m) {
     if (m->profiling) TRY(prof_mark(m, name)); \
     TRY(call);                                 \
     if (m->profiling) TRY(prof_end(m));        \
+  } while (0)
+// an op that writes gradients: its producer adds FP64 squared-norm partials
+// (sjh::GradSq) when the backward armed the hook
+#define GOP(name, call)              \
+  do {                               \
+    sjh::grad_sq().on = true;        \
+    OP(name, call);                  \
+    sjh::grad_sq().on = false;       \
   } while (0)
 
 // Build reference-layout tensor list and the internal arena layout.
@@ -662,6 +677,12 @@ int hierarchy_forward(sj_model* m) {
 
 int forward(sj_model* m);
 bool two_streams(const sj_model* m);
+// The gradient-norm partials cover every gradient of the bf16 byte LM step
+// with AdamW (dW products through the split-K reduce, the norm weights, the
+// embedding); the other models sum the arena.
+bool gsq_eligible(const sj_model* m) {
+  return m->planes && m->lm_planes && !m->E && !m->hier && !m->value_n && m->optimizer == 0 && !m->vjp;
+}
 // the step's forward: the loss sum waits for the backward's second stream
 int forward_deferred(sj_model* m) {
   m->defer_loss = !m->value_n && two_streams(m);
@@ -860,10 +881,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       // would slow that product as much as it gains, so it follows it.
       auto down_dw = [&]() -> int {
         if (rdw)
-          OP("down_dw", sj_gemm_planes_tn(s2, F, d, M, (const uint16_t*)m->hh[l], nullptr, F, NP(KR, p)[0],
+          GOP("down_dw", sj_gemm_planes_tn(s2, F, d, M, (const uint16_t*)m->hh[l], nullptr, F, NP(KR, p)[0],
                                           NP(KR, p)[1], d, G + y.down, SJ_F32, d, 0, ws2, wsb));
         else
-          OP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt,
+          GOP("down_dw", sj_gemm_planes(s2, F, d, M, m->ht[l], nullptr, ldt, T(KR, p)[0], T(KR, p)[1], ldt,
                                        G + y.down, SJ_F32, d, 0, ws2, wsb));
         return read(KR, p);
       };
@@ -880,10 +901,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                       m->dz, SJ_F32, d, 0, ws, wsb));
       if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, T(KG, p)));
       if (rdw)
-        OP("gate_up_dw", sj_gemm_planes_tn(s2, d, 2 * F, M, (const uint16_t*)m->z2[l], nullptr, d, NP(KG, p)[0],
+        GOP("gate_up_dw", sj_gemm_planes_tn(s2, d, 2 * F, M, (const uint16_t*)m->z2[l], nullptr, d, NP(KG, p)[0],
                                            NP(KG, p)[1], 2 * F, G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       else if (!m->group_all[1])
-        OP("gate_up_dw", sj_gemm_planes(s2, d, 2 * F, M, m->z2t[l], nullptr, ldt, T(KG, p)[0], T(KG, p)[1], ldt,
+        GOP("gate_up_dw", sj_gemm_planes(s2, d, 2 * F, M, m->z2t[l], nullptr, ldt, T(KG, p)[0], T(KG, p)[1], ldt,
                                         G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       TRY(read(KG, p));
       }
@@ -901,10 +922,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
         OP("attn_out_dx", sj_gemm_planes(s, M, d, d, xp[0], xp[1], d, W + y.wo, nullptr, d, m->dO, SJ_F32, d, 0, ws,
                                          wsb));
       if (rdw)
-        OP("attn_out_dw", sj_gemm_planes_tn(s2, d, d, M, (const uint16_t*)m->o[l], nullptr, d, NP(KX, p)[0],
+        GOP("attn_out_dw", sj_gemm_planes_tn(s2, d, d, M, (const uint16_t*)m->o[l], nullptr, d, NP(KX, p)[0],
                                             NP(KX, p)[1], d, G + y.wo, SJ_F32, d, 0, ws2, wsb));
       else
-        OP("attn_out_dw", sj_gemm_planes(s2, d, d, M, m->ot[l], nullptr, ldt, T(KX, p)[0], T(KX, p)[1], ldt, G + y.wo,
+        GOP("attn_out_dw", sj_gemm_planes(s2, d, d, M, m->ot[l], nullptr, ldt, T(KX, p)[0], T(KX, p)[1], ldt, G + y.wo,
                                          SJ_F32, d, 0, ws2, wsb));
       TRY(read(KX, p));
       TRY(reuse(KQ, p));
@@ -928,10 +949,10 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
                                   0, ws, wsb));
       if (m->group_on[0]) TRY(vjp_group(m, l, 0, s2, ws2, wsb, T(KQ, p)));
       if (rdw)
-        OP("qkv_dw", sj_gemm_planes_tn(s2, d, NQ, M, (const uint16_t*)m->z[l], nullptr, d, NP(KQ, p)[0], NP(KQ, p)[1],
+        GOP("qkv_dw", sj_gemm_planes_tn(s2, d, NQ, M, (const uint16_t*)m->z[l], nullptr, d, NP(KQ, p)[0], NP(KQ, p)[1],
                                        NQ, G + y.qkv, SJ_F32, NQ, 0, ws2, wsb));
       else if (!m->group_all[0])
-        OP("qkv_dw", sj_gemm_planes(s2, d, NQ, M, m->zt[l], nullptr, ldt, T(KQ, p)[0], T(KQ, p)[1], ldt, G + y.qkv,
+        GOP("qkv_dw", sj_gemm_planes(s2, d, NQ, M, m->zt[l], nullptr, ldt, T(KQ, p)[0], T(KQ, p)[1], ldt, G + y.qkv,
                                     SJ_F32, NQ, 0, ws2, wsb));
       TRY(read(KQ, p));
       if (l > S.first) {
@@ -1026,7 +1047,36 @@ int hierarchy_backward(sj_model* m, int& cur) {
   return stage_backward(m, 0, hg[7], cur);
 }
 
+// Arms the gradient-norm hook for one backward; on the way out records how
+// many slots the producers used and whether every gradient went through one.
+struct GsqArm {
+  sj_model* m;
+  explicit GsqArm(sj_model* mm) : m(mm) {
+    sjh::GradSq& g = sjh::grad_sq();
+    g = sjh::GradSq{};
+    if (m->gsq) {
+      g.base = m->gsq;
+      g.cap = sj_model::GSQ_CAP;
+    }
+    m->gsq_ok = false;
+  }
+  ~GsqArm() {
+    sjh::GradSq& g = sjh::grad_sq();
+    m->gsq_count = g.next;
+    m->gsq_ok = g.base && !g.missed && g.next > 0;
+    g = sjh::GradSq{};
+  }
+};
+
+int backward_body(sj_model* m);
 int backward(sj_model* m) {
+  GsqArm arm(m);
+  const int st = backward_body(m);
+  if (st) sjh::grad_sq().missed = true;
+  return st;
+}
+
+int backward_body(sj_model* m) {
   hipStream_t s = m->stream;
   const long M = m->M, d = m->d;
   const int dt = m->dt;
@@ -1066,7 +1116,7 @@ int backward(sj_model* m) {
       OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, m->HR, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32,
                             m->Vp, 0, wsw, m->ws_bytes));
     else if (m->lm_planes)
-      OP("head_dw", sj_gemm_planes_tn(sw, d, m->Vp, M, (const uint16_t*)m->hn, nullptr, d, m->dlp[0], m->dlp[1], m->Vp,
+      GOP("head_dw", sj_gemm_planes_tn(sw, d, m->Vp, M, (const uint16_t*)m->hn, nullptr, d, m->dlp[0], m->dlp[1], m->Vp,
                                       G + m->out, SJ_F32, m->Vp, 0, wsw, m->ws_bytes));
     else
       OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, M, m->hn, dt, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32, m->Vp, 0,
@@ -1084,9 +1134,9 @@ int backward(sj_model* m) {
       SJ_HIP(hipStreamWaitEvent(m->stream2, m->ev_norm, 0));
       sr = m->stream2;
     }
-    OP("rmsnorm_dw_reduce", sjh::rmsnorm_reduce_multi(sr, m->norm_jobs, m->norm_njobs, m->norm_maxd));
+    GOP("rmsnorm_dw_reduce", sjh::rmsnorm_reduce_multi(sr, m->norm_jobs, m->norm_njobs, m->norm_maxd));
   }
-  OP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, m->stages[0].M, m->stages[0].d, m->V,
+  GOP("embedding_bwd", sj_embedding_bwd(s, m->dres[cur], m->ids, G + m->emb, m->stages[0].M, m->stages[0].d, m->V,
                                        nullptr, 0));
   if (two) {  // the update reads every gradient
     SJ_HIP(hipEventRecord(m->ev_join, m->stream2));
@@ -1109,7 +1159,10 @@ int update(sj_model* m) {
     if (m->planes) OP("mirror_transpose", transpose_mirror(m));
     return SJ_OK;
   }
-  OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
+  if (m->gsq_ok)  // the producers' partials, summed in slot order
+    OP("grad_norm", sjh::sum_slots(m->stream, m->gsq, m->gsq_count, m->sumsq));
+  else
+    OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
   OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
                      m->n_nodecay, m->step_dev, m->sumsq, m->status));
   if (m->planes) OP("mirror_transpose", transpose_mirror(m));
@@ -1672,6 +1725,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   ALLOC(m->targets, (size_t)m->M * 4);
   ALLOC(m->loss, 64);
   ALLOC(m->sumsq, 64);
+  if (gsq_eligible(m)) ALLOC(m->gsq, sizeof(double) * (size_t)sj_model::GSQ_CAP);
   ALLOC(m->status, 64);
   ALLOC(m->step_dev, sizeof(sj_adam_step));
   if (m->optimizer == 1) ALLOC(m->sgd_dev, sizeof(sj_sgd_step));
@@ -2211,6 +2265,7 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
   else if (w == "mirror_t") { *ptr = m->mirror_t; n = m->mirror_t ? m->n_params : 0; }
   else if (w == "workspace") { *ptr = m->ws; n = (long)m->ws_bytes; }
   else if (w == "stream") { *ptr = (void*)m->stream; n = 0; }
+  else if (w == "grad_sq_slots") { *ptr = m->gsq; n = m->gsq_ok ? m->gsq_count : 0; }
   else if (w == "vjp_columns" && m->vjp) { *ptr = m->vjp_cols; n = m->vjp_R; }
   else if (w == "vjp_rows" && m->vjp) { *ptr = m->vjp_rows; n = m->vjp_k; }
   else if (w == "vjp_map" && m->vjp) { *ptr = m->vjp_map; n = m->d; }

@@ -163,12 +163,18 @@ __global__ __launch_bounds__(NT) void k_rms_reduce(const float* __restrict__ par
 
 // Many reductions in one launch (blockIdx.y = job): the norm-weight
 // gradients of a whole backward, summed after the dX chain has passed.
-__global__ __launch_bounds__(NT) void k_rms_reduce_multi(const sj::RmsReduceJob* __restrict__ jobs) {
+// sq (nullable): FP64 sum of squares of the workgroup's dw values at
+// sq[blockIdx.y * gridDim.x + blockIdx.x] (the gradient-norm hook)
+__global__ __launch_bounds__(NT) void k_rms_reduce_multi(const sj::RmsReduceJob* __restrict__ jobs, double* sq) {
   const sj::RmsReduceJob jb = jobs[blockIdx.y];
   __shared__ float red[8][32];
+  __shared__ double qred[NT / 64];
   const int col = threadIdx.x & 31, sl = threadIdx.x >> 5;
   const long c = blockIdx.x * 32L + col;
-  if (blockIdx.x * 32L >= jb.d) return;  // whole workgroup past this job's columns
+  if (blockIdx.x * 32L >= jb.d) {  // whole workgroup past this job's columns
+    if (sq && threadIdx.x == 0) sq[blockIdx.y * gridDim.x + blockIdx.x] = 0.0;
+    return;
+  }
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   const long groups = jb.groups, d = jb.d;
   const float* partial = jb.partial;
@@ -184,11 +190,17 @@ __global__ __launch_bounds__(NT) void k_rms_reduce_multi(const sj::RmsReduceJob*
   }
   red[sl][col] = (a0 + a1) + (a2 + a3);
   __syncthreads();
+  double q = 0.0;
   if (sl == 0 && c < d) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) s += red[i][col];
     jb.dw[c] = s;
+    q = (double)s * (double)s;
+  }
+  if (sq) {
+    q = block_sum<double, NT>(q, qred);
+    if (threadIdx.x == 0) sq[blockIdx.y * gridDim.x + blockIdx.x] = q;
   }
 }
 
@@ -514,8 +526,9 @@ int sjh::rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t*
 
 int sjh::rmsnorm_reduce_multi(void* stream, const sj::RmsReduceJob* jobs, long njobs, long max_d) {
   SJ_REQUIRE(jobs && njobs > 0 && njobs < 65536 && max_d > 0, "rmsnorm reduce: %ld jobs", njobs);
-  hipLaunchKernelGGL(k_rms_reduce_multi, dim3((unsigned)((max_d + 31) / 32), (unsigned)njobs), dim3(NT), 0,
-                     (hipStream_t)stream, jobs);
+  const unsigned bx = (unsigned)((max_d + 31) / 32);
+  double* sq = sjh::grad_sq().take((long)bx * njobs);
+  hipLaunchKernelGGL(k_rms_reduce_multi, dim3(bx, (unsigned)njobs), dim3(NT), 0, (hipStream_t)stream, jobs, sq);
   SJ_LAUNCH_CHECK("rmsnorm_backward_reduce");
   return SJ_OK;
 }

@@ -290,3 +290,34 @@ def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
         assert kern[op].startswith("k_gemm_fast<") and kern[op] == kern[op + "#kernel"], (op, kern[op])
     for op in ("attention_fwd", "rmsnorm", "adamw"):
         assert op in agg and kern[op] == "", (op, kern.get(op))
+
+
+def test_gradient_norm_from_producer_partials():
+    """The bf16 step sums the squared gradient norm from FP64 partials its
+    gradient producers write (split-K dW reduce, norm-weight reduce,
+    embedding backward) instead of a pass over the arena: the norm the step
+    reports equals the FP64 norm of the gradients it left, at the full cfg2
+    shape (every dW product split) and at a 2-layer cut, eager and replayed."""
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    for layers, batch in ((6, 8), (2, 2)):
+        mc, tc = config("cfg2")
+        mc.layers, tc.batch = layers, batch
+        params = init_params(mc, std=0.02)
+        ids, tg = byte_batch(Rng(3), tc.batch, tc.sequence)
+        for graph in (False, True):
+            model = Model(mc, tc)
+            try:
+                model.set_params(params)
+                model.set_batch(ids, tg)
+                model.use_graph(graph)
+                for _ in range(2):
+                    model.train_step(1e-3)
+                _, norm = model.read_loss()
+                g = model.get_grads().astype(np.float64)
+                ref = math.sqrt(float(np.dot(g, g)))
+                assert abs(norm - ref) <= 1e-12 * ref, (layers, graph, norm, ref)
+                _, slots = model.buffer("grad_sq_slots")
+                assert slots > 0, (layers, graph)  # the producers' partials were summed
+            finally:
+                model.close()
