@@ -28,6 +28,9 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+# FP64 squared-norm slots the step's gradient producers wrote (0: the update
+# read the whole gradient arena); set from the model after the timed steps
+GRAD_SQ_SLOTS = 0
 
 
 # op -> the one kernel it launches (rocprofv3 names) where the library does
@@ -171,7 +174,8 @@ def op_work(op: str, mc, tc):
         "loss_summary": ("byte", M * 4),
         "embedding": ("byte", M * 4 + 2 * M * d * es),
         "embedding_bwd": ("byte", M * d * 4 + V * d * 4 + M * 4),
-        "grad_norm": ("byte", P * 4),
+        # the arena, or the FP64 partials the gradient producers left
+        "grad_norm": ("byte", 8 * GRAD_SQ_SLOTS if GRAD_SQ_SLOTS else P * 4),
         "adamw": ("byte", 30 * P),
     }
     ex = getattr(mc, "experts", None)
@@ -811,6 +815,8 @@ def main():
     log(f"[bench] {args.steps} steps: {ms_per_step:.4f} ms/step (events {gpu_ms / args.steps:.4f}, "
         f"wall {wall * 1e3 / args.steps:.4f}); loss {loss0:.5f} -> {loss:.5f}, |g| {gnorm:.4f}")
 
+    global GRAD_SQ_SLOTS
+    GRAD_SQ_SLOTS = model.buffer("grad_sq_slots")[1]
     # live per-op timing: eager steps with a HIP event pair around every op
     # on the model stream, averaged over the profiled steps
     model.profile(True)
