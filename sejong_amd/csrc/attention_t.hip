@@ -393,10 +393,13 @@ __global__ __launch_bounds__(256) void k_attn2_fwd_cached(TArgs a) {
 // ------------------------------------------------------------- backward dQ
 // Workgroup (query block qb, query head h, batch b): dQ of its 64 queries,
 // with Delta read from delta_t (k_attn_delta).  lds: NS x [K | V].
+// wl: this wave's 16-query slice (0..3) of the block; dma: whether this wave
+// takes part in staging K | V (the grouped launch shares one copy among the
+// query heads of a KV head)
 template <int NS>
-__device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, int h, int b) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+__device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, int h, int b, int wl, bool dma) {
+  const int lane = threadIdx.x & 63, wave = wl;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wl);
   const int g = lane >> 4, j = lane & 15;
   const int T = a.T, NQ = a.HQ * DH;
   const int kvh = h / (a.HQ / a.HK);
@@ -420,6 +423,7 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
   const bf16_t* vsrc = ksrc + a.HK * DH;
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   auto issue = [&](int kb, int buf) {
+    if (!dma) return;
     const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
     dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
     dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
@@ -510,16 +514,18 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
 }
 
 // ------------------------------------------------------------ backward dKV
-// Workgroup (key block, query head, batch): this head's dK | dV share, fp32,
-// into part[gi][row][dK | dV] (gi = head index inside its group).  A stage
-// holds the query block's Q and dO planes in row orientation only: the
-// products that need them transposed (dV^T = dO^T P, dK^T = Q^T dS) read
+// A stage holds the query block's Q and dO planes in row orientation only:
+// the products that need them transposed (dV^T = dO^T P, dK^T = Q^T dS) read
 // their fragments with LDS transpose reads.
-__device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, int h, int b) {
-  // lds: NST x [Q | dOh | dOl | LSE,Delta]
-  constexpr int SROW = 3 * TILE + 512;  // stage size in bf16 elements (+1 KB of LSE / Delta)
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+constexpr int SROW = 3 * TILE + 512;  // dK/dV stage size in bf16 elements (+1 KB of LSE / Delta)
+
+// The dK / dV accumulation of head h over its query blocks for the 16 keys
+// of slice wl (0..3) of key block kb; lds: NST x [Q | dOh | dOl | LSE,Delta]
+// of this head.  Leaves dK^T / dV^T [16d + 4g + r][key] in dk / dv.
+__device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int kb, int h, int b, int wl,
+                                               f32x4 (&dk)[4], f32x4 (&dv)[4]) {
+  const int lane = threadIdx.x & 63, wave = wl;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wl);
   const int g = lane >> 4, j = lane & 15;
   const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
   const int group = a.HQ / a.HK;
@@ -552,7 +558,6 @@ __device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, i
       dma16(s, st + 3 * TBYTES);
     }
   };
-  f32x4 dk[4], dv[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   // last query block that sees a key of this block (window: queries key .. key+window-1)
@@ -624,6 +629,18 @@ __device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, i
       }
     }
   }
+}
+
+// Workgroup (key block, query head, batch): this head's dK | dV share, fp32,
+// into part[gi][row][dK | dV] (gi = head index inside its group).
+__device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, int h, int b) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  f32x4 dk[4], dv[4];
+  attn2_dkv_core(a, lds, kb, h, b, wave, dk, dv);
+  const int T = a.T, NK = a.HK * DH;
+  const int group = a.HQ / a.HK;
+  const int kvh = h / group, gi = h % group;
+  const long krow = (long)b * T + kb * QB + wave * 16 + j;
   // lane holds dK^T / dV^T [16d + 4g + r][key]: 4 consecutive columns of the partial row
   const long M = (long)T * a.B;
   float* prow_ = a.part + ((long)gi * M + krow) * 2 * NK + kvh * DH;
@@ -675,7 +692,7 @@ __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd(TArgs a) {
   const int nb = (int)(gridDim.x >> 1);
   const WgMap wm = wg_map(2);
   if (wm.role == 0)
-    attn2_dq<NS_DQ>(a, lds, nb - 1 - wm.r, wm.h, wm.b);
+    attn2_dq<NS_DQ>(a, lds, nb - 1 - wm.r, wm.h, wm.b, threadIdx.x >> 6, true);
   else
     attn2_dkv(a, lds, wm.r, wm.h, wm.b);
 }
@@ -686,13 +703,95 @@ __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd(TArgs a) {
 __global__ __launch_bounds__(256) void k_attn2_bwd_dq(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   const WgMap wm = wg_map(1);
-  attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - wm.r, wm.h, wm.b);
+  attn2_dq<NS_DQ>(a, lds, (int)gridDim.x - 1 - wm.r, wm.h, wm.b, threadIdx.x >> 6, true);
 }
 __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd_dkv(TArgs a) {
   extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
   const WgMap wm = wg_map(1);
   attn2_dkv(a, lds, wm.r, wm.h, wm.b);
 }
+
+// ------------------------------------------ grouped backward (no partials)
+// Both roles per KV head instead of per query head: a workgroup of G x 4
+// waves holds the G query heads of KV head kvh (group gi of four waves:
+// query head kvh * G + gi).  Role 0 (dQ of a query block): each group forms
+// its head's dQ from K | V stages that group 0 alone stages for all G.
+// Role 1 (dK | dV of a key block): each group accumulates its head's share
+// over its own Q / dO stages; the groups then add their shares through LDS
+// in head order, ((0 + h0) + h1) + h2 as the group reduce sums the fp32
+// partials, and group 0 applies the inverse RoPE to dK and writes the hi / lo
+// planes.  No per-head partials leave the workgroup and no reduce pass
+// follows.  G x NST stages of dK/dV operands: G <= 3 fits the LDS.
+template <int G>
+__global__ __launch_bounds__(256 * G) SJ_BWD_OCC void k_attn2_bwd_g(TArgs a) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  const int nb = (int)(gridDim.x >> 1);
+  const WgMap wm = wg_map(2);
+  const int w = threadIdx.x >> 6, gi = w >> 2, wl = w & 3;
+  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  const int kvh = wm.h, h = kvh * G + gi;
+  if (wm.role == 0) {
+    attn2_dq<NS_DQ>(a, lds, nb - 1 - wm.r, h, wm.b, wl, gi == 0);
+    return;
+  }
+  const int kb = wm.r;
+  f32x4 dk[4], dv[4];
+  attn2_dkv_core(a, lds + gi * NST * SROW, kb, h, wm.b, wl, dk, dv);
+  block_barrier();  // every group is done reading its stages
+  // group q > 0 leaves vector v (dk 0..3, dv 0..3) of lane L of slice wl at
+  // f32x4 index ((q - 1) * 8 + v) * 256 + wl * 64 + L
+  f32x4* sh = (f32x4*)lds;
+  const int slot = wl * 64 + lane;
+  if (gi > 0) {
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      sh[((gi - 1) * 8 + d) * 256 + slot] = dk[d];
+      sh[((gi - 1) * 8 + 4 + d) * 256 + slot] = dv[d];
+    }
+  }
+  block_barrier();
+  if (gi != 0) return;
+  const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
+  const int kloc = wl * 16 + j, pos = kb * QB + kloc;
+  const long krow = (long)wm.b * T + pos;
+#pragma unroll
+  for (int half = 0; half < 2; half++) {  // dK, then dV
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float s = 0.f;
+        s += half ? dv[d][r] : dk[d][r];
+#pragma unroll
+        for (int q = 1; q < G; q++) s += sh[((q - 1) * 8 + 4 * half + d) * 256 + slot][r];
+        v[r] = s;
+      }
+      if (half == 0 && a.rope) {  // inverse RoPE on dK's pairs (columns 16d + 4g + 2pr, +1)
+#pragma unroll
+        for (int pr = 0; pr < 2; pr++) {
+          const int col = 16 * d + 4 * g + 2 * pr;
+          const float2 cs = *(const float2*)(a.rope + 2 * ((long)pos * (DH / 2) + (col >> 1)));
+          const float x = v[2 * pr], y = v[2 * pr + 1];
+          v[2 * pr] = x * cs.x + y * cs.y;
+          v[2 * pr + 1] = y * cs.x - x * cs.y;
+        }
+      }
+      bf16_t hv[4], lv[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
+      const long col = NQ + half * NK + kvh * DH + 16 * d + 4 * g;
+      *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
+      *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
+    }
+  }
+}
+constexpr int GROUPED_G = 3;  // query heads per KV head of the grouped launch
+constexpr size_t LDS_BWD_G = (size_t)GROUPED_G * NST * SROW * 2 > (size_t)NS_DQ * 2 * TBYTES
+                                 ? (size_t)GROUPED_G * NST * SROW * 2
+                                 : (size_t)NS_DQ * 2 * TBYTES;
+static_assert(LDS_BWD_G <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 * 16 <= LDS_BWD_G, "grouped LDS budget");
+
 constexpr long SEPARATE_ROLES = 2048;  // workgroups per role from which the roles launch separately
 
 constexpr size_t LDS_FWD = (size_t)NS_FWD * 2 * TBYTES;
@@ -705,6 +804,21 @@ static_assert(LDS_BWD <= 160 * 1024, "LDS budget");
 static_assert(LDS_DKV <= 160 * 1024, "LDS budget");
 
 }  // namespace
+
+// SJ_ATTN_GROUPED=0 keeps the per-query-head launch with the group reduce
+// (A/B comparisons)
+static bool grouped_on() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("SJ_ATTN_GROUPED");
+    on = e ? atoi(e) != 0 : 1;
+  }
+  return on != 0;
+}
+
+bool sjh::attention_bwd_grouped(long batch, long t, long hq, long hk, bool transposed) {
+  return hq == GROUPED_G * hk && !transposed && (t / QB) * hq * batch < SEPARATE_ROLES && grouped_on();
+}
 
 int sjh::attention_t_prepare() {
   static int done = 0, status = SJ_OK;
@@ -720,6 +834,9 @@ int sjh::attention_t_prepare() {
     e = hipFuncSetAttribute((const void*)k_attn2_bwd_dq, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DQ);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_bwd_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute((const void*)k_attn2_bwd_g<GROUPED_G>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)LDS_BWD_G);
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
   return status;
 }
@@ -807,8 +924,18 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
     hipLaunchKernelGGL(k_attn_delta, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
     SJ_LAUNCH_CHECK("hierarchy_attention_delta");
   }
+  // the grouped launch (no dK | dV partials, no reduce): G = 3 query heads
+  // per KV head, row planes only, sizes where the two roles share one launch
+  const long nb = t / QB;
+  const bool grouped = sjh::attention_bwd_grouped(batch, t, hq, hk, g_t_hi != nullptr);
+  if ((parts & 2) && grouped) {
+    hipLaunchKernelGGL(k_attn2_bwd_g<GROUPED_G>, dim3((unsigned)(2 * nb), (unsigned)hk, (unsigned)batch),
+                       dim3(256 * GROUPED_G), LDS_BWD_G, s, a);
+    SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv (grouped)");
+    return SJ_OK;  // dK | dV planes written: nothing for the reduce part
+  }
+  if (grouped) return SJ_OK;
   if (parts & 2) {  // dQ | dK dV
-    const long nb = t / QB;
     if (nb * hq * batch >= SEPARATE_ROLES) {
       const dim3 grid((unsigned)nb, (unsigned)hq, (unsigned)batch);
       hipLaunchKernelGGL(k_attn2_bwd_dq, grid, dim3(256), LDS_DQ, s, a);

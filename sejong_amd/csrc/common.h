@@ -118,6 +118,9 @@ int factored_update_staged(hipStream_t stream, const void* meta, long tiles, con
 // attention over transposed operands (attention_t.hip) and the group reduce
 // of the per-head dK | dV partials it shares with attention.hip
 int attention_t_prepare();
+// whether attention_bwd_tt_parts runs the grouped launch for these sizes
+// (dK | dV planes written by part 2, part 4 does nothing)
+bool attention_bwd_grouped(long batch, long t, long hq, long hk, bool transposed);
 // cross entropy with dX as hi/lo bf16 planes [rows][ldp] (columns past vocab zero)
 int cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss, uint16_t* dx_hi,
                          uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar);

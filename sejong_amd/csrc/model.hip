@@ -931,6 +931,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       TRY(reuse(KQ, p));
       // with dO as planes, attn_out_dx's epilogue has written Delta
       for (int part = S.attn_tt ? 2 : 1; part <= 4; part <<= 1) {
+        if (part == 4 && S.attn_tt && sjh::attention_bwd_grouped(m->B, S.T, S.HQ, S.HK, TP(KQ, p)[0] != nullptr))
+          continue;  // the grouped launch wrote the dK | dV planes
         const char* nm = part == 4   ? "attention_bwd_kv_reduce"
                          : S.attn_tt ? (part == 1 ? "attention_bwd_delta" : "attention_bwd_dq_dkv")
                                      : (part == 1 ? "attention_bwd_dq" : "attention_bwd_dkv");
