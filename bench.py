@@ -36,7 +36,7 @@ GRAD_SQ_SLOTS = 0
 # op -> the one kernel it launches (rocprofv3 names) where the library does
 # not name it itself (GEMM ops do, through the profile): the cfg2 step's
 # plane-path kernels (bf16, head_dim 64, T a multiple of 64)
-OP_KERNEL = {"attention_bwd": "k_attn2_bwd", "attention_bwd_dq_dkv": "k_attn2_bwd", "attention_bwd_delta": "k_attn_delta",
+OP_KERNEL = {"attention_bwd": "k_attn2_bwd", "attention_bwd_dq_dkv": "k_attn2_bwd_g<3>", "attention_bwd_delta": "k_attn_delta",
              "attention_bwd_kv_reduce": "k_attn_kv_reduce_rows", "attention_fwd": "k_attn2_fwd<3>",
              "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd4",
              "embedding": "k_embedding_fwd", "cross_entropy": "k_cross_entropy_planes", "rmsnorm": "k_rms_fwd_t<3>",
@@ -241,7 +241,7 @@ def issued_factor(kernel: str) -> float:
         t = [int(x) for x in kernel[len("k_gemm_fast<"):-1].split(",")]
         pa, pb = t[2], t[3]
         return float(pa * pb - (1 if pa == 2 and pb == 2 else 0))
-    return {"k_attn2_fwd<3>": 1.5, "k_attn2_bwd": 6.5 / 2.5}.get(kernel, 1.0)
+    return {"k_attn2_fwd<3>": 1.5, "k_attn2_bwd": 6.5 / 2.5, "k_attn2_bwd_g<3>": 6.5 / 2.5}.get(kernel, 1.0)
 
 
 def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config):
