@@ -110,12 +110,14 @@ __global__ __launch_bounds__(64) void k_profile_hold(int n) {
   for (int i = 0; i < n; i++) __builtin_amdgcn_s_sleep(127);
 }
 
+// jobs[0 .. njobs) with tiles tile_base .. tile_base + gridDim.x - 1 of the
+// flat tile index (a subset of the table: one layer's matrices)
 __global__ __launch_bounds__(256) void k_transpose_jobs(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                         const TJob* __restrict__ jobs, int njobs,
-                                                        const float* __restrict__ master, TPlanes hp) {
+                                                        const float* __restrict__ master, TPlanes hp, long tile_base) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 72];
   __shared__ __attribute__((aligned(16))) uint16_t tile_lo[64 * 72];
-  const long b = blockIdx.x;
+  const long b = tile_base + blockIdx.x;
   int ji = 0;
   while (ji + 1 < njobs && b >= jobs[ji + 1].tile0) ji++;
   const long off = jobs[ji].off, rows = jobs[ji].rows, cols = jobs[ji].cols;
@@ -255,6 +257,18 @@ struct sj_model {
   TJob* tjobs = nullptr;
   int tjob_n = 0;
   long tjob_tiles = 0;
+  // the table in groups for the overlapped refresh: group 0 the output head
+  // (absent without head planes), group 1 + l layer l; job start, job count,
+  // first tile, tile count
+  struct TGroup {
+    int j0, nj;
+    long t0, nt;
+  };
+  std::vector<TGroup> tgroups;
+  std::vector<hipEvent_t> ev_tr;   // group g's transposes done (second stream)
+  hipEvent_t ev_tr_fork = nullptr;
+  bool mt_stale = false;           // the transposed mirror lags the last update
+  bool tr_overlap = false;         // this forward refreshes it on the second stream
   std::vector<uint16_t*> zt, ot, z2t, ht;  // transposed activations per layer
   // attention over producer-transposed operands (T a multiple of 64): q|k|v^T
   // and LSE^T per layer, dO planes in both orientations and Delta^T scratch
@@ -565,8 +579,40 @@ const void* wc(const sj_model* m, long off) {
 int transpose_mirror(sj_model* m) {
   if (!m->planes) return SJ_OK;
   hipLaunchKernelGGL(k_transpose_jobs, dim3((unsigned)m->tjob_tiles), dim3(256), 0, m->stream, m->mirror, m->mirror_t,
-                     m->tjobs, m->tjob_n, (const float*)m->w, TPlanes{m->hp[0], m->hp[1], m->hp[2], m->hp[3]});
+                     m->tjobs, m->tjob_n, (const float*)m->w, TPlanes{m->hp[0], m->hp[1], m->hp[2], m->hp[3]}, 0L);
   SJ_LAUNCH_CHECK("mirror transpose");
+  m->mt_stale = false;
+  return SJ_OK;
+}
+
+// The transposed mirror rebuilt on the second stream one group at a time
+// (layer 0 first, the head last), each group's event marking it done: the
+// forward's layer l waits only for its own matrices, so the rest of the
+// refresh runs beside the forward instead of ahead of it.
+int transpose_mirror_overlapped(sj_model* m) {
+  hipStream_t s2 = m->stream2;
+  SJ_HIP(hipEventRecord(m->ev_tr_fork, m->stream));  // after the last update wrote the mirror
+  SJ_HIP(hipStreamWaitEvent(s2, m->ev_tr_fork, 0));
+  const TPlanes hp{m->hp[0], m->hp[1], m->hp[2], m->hp[3]};
+  const size_t n = m->tgroups.size();
+  for (size_t k = 0; k < n; k++) {
+    const size_t gidx = (k + 1) % n;  // layers first, the head (group 0) last
+    const sj_model::TGroup& g = m->tgroups[gidx];
+    if (g.nt > 0)
+      hipLaunchKernelGGL(k_transpose_jobs, dim3((unsigned)g.nt), dim3(256), 0, s2, m->mirror, m->mirror_t,
+                         m->tjobs + g.j0, g.nj, (const float*)m->w, hp, g.t0);
+    SJ_HIP(hipEventRecord(m->ev_tr[gidx], s2));
+  }
+  SJ_LAUNCH_CHECK("mirror transpose (overlapped)");
+  m->mt_stale = false;
+  return SJ_OK;
+}
+
+// the forward's layer l (group 1 + l) or head (group 0) may read its
+// transposed matrices from here on
+int await_transposed(sj_model* m, hipStream_t s, size_t group) {
+  if (!m->tr_overlap || group >= m->ev_tr.size()) return SJ_OK;
+  SJ_HIP(hipStreamWaitEvent(s, m->ev_tr[group], 0));
   return SJ_OK;
 }
 
@@ -593,6 +639,7 @@ int stage_forward(sj_model* m, int si) {
   const float eps = m->c.norm_epsilon;
   for (long l = S.first; l < S.first + S.count && m->planes; l++) {
     const Layer& y = m->layers[l];
+    TRY(await_transposed(m, s, (size_t)(1 + l)));
     uint16_t* qkv = (uint16_t*)m->qkv[l];
     const uint16_t *W = m->mirror, *WT = m->mirror_t;
     const uint16_t *x = (const uint16_t*)xin(m, l), *x1 = (const uint16_t*)m->x1[l];
@@ -683,10 +730,13 @@ bool two_streams(const sj_model* m);
 bool gsq_eligible(const sj_model* m) {
   return m->planes && m->lm_planes && !m->E && !m->hier && !m->value_n && m->optimizer == 0 && !m->vjp;
 }
-// the step's forward: the loss sum waits for the backward's second stream
+// the step's forward: the loss sum waits for the backward's second stream,
+// and the transposed mirror is rebuilt beside the forward
 int forward_deferred(sj_model* m) {
   m->defer_loss = !m->value_n && two_streams(m);
+  m->tr_overlap = two_streams(m) && !m->tgroups.empty();
   const int st = forward(m);
+  m->tr_overlap = false;
   if (st) m->defer_loss = false;
   return st;
 }
@@ -695,6 +745,10 @@ int forward(sj_model* m) {
   hipStream_t s = m->stream;
   const long M = m->M, d = m->d;
   const int dt = m->dt;
+  if (m->tr_overlap)
+    OP("mirror_transpose", transpose_mirror_overlapped(m));
+  else if (m->mt_stale)
+    OP("mirror_transpose", transpose_mirror(m));
   OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, m->stages[0].M, m->stages[0].d));
   TRY(stage_forward(m, 0));
   if (m->hier) TRY(hierarchy_forward(m));
@@ -720,6 +774,7 @@ int forward(sj_model* m) {
   if (m->lm_planes) {
     // no split-K (no workspace): a row's sum order does not depend on M,
     // so the cached forward's one-row product gives the same logits
+    TRY(await_transposed(m, s, 0));
     OP("head_fwd", sj_gemm_planes(s, M, m->Vp, d, (const uint16_t*)m->hn, nullptr, d, m->hp[2], m->hp[3], d,
                                   m->logits, SJ_F32, m->Vp, 0, nullptr, 0));
     OP("cross_entropy", sjh::cross_entropy_planes(s, m->logits, m->Vp, m->targets, m->loss_rows, m->dlp[0], m->dlp[1],
@@ -1158,7 +1213,7 @@ int update(sj_model* m) {
     }
     OP("sgd_update", sjh::factored_update_staged(m->stream, m->fmeta, m->ftiles, m->sgd_dev,
                                                  m->sgd.clip_enabled ? m->sumsq : nullptr));
-    if (m->planes) OP("mirror_transpose", transpose_mirror(m));
+    m->mt_stale = m->planes;  // the next forward rebuilds the transposed mirror
     return SJ_OK;
   }
   if (m->gsq_ok)  // the producers' partials, summed in slot order
@@ -1167,7 +1222,7 @@ int update(sj_model* m) {
     OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
   OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
                      m->n_nodecay, m->step_dev, m->sumsq, m->status));
-  if (m->planes) OP("mirror_transpose", transpose_mirror(m));
+  m->mt_stale = m->planes;  // the next forward rebuilds the transposed mirror
   return SJ_OK;
 }
 
@@ -1541,20 +1596,27 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       tiles += ((rows + 63) / 64) * j.tiles_c;
       jobs.push_back(j);
     };
+    auto group = [&](int j0, long t0) {
+      m->tgroups.push_back(sj_model::TGroup{j0, (int)jobs.size() - j0, t0, tiles - t0});
+    };
     if (m->lm_planes) {  // the output head's hi/lo planes from its fp32 master
       for (int k = 0; k < 4; k++) ALLOC(m->hp[k], (size_t)m->d * m->Vp * 2);
       for (int k = 0; k < 2; k++) ALLOC(m->dlp[k], (size_t)m->M * m->Vp * 2);
       job(m->out, m->d, m->Vp, 1);
     }
+    group(0, 0);  // group 0: the head (empty without head planes)
     for (long l = 0; l < m->L; l++) {
       const Layer& y = m->layers[l];
       const Stage& S = m->stages[y.stage];
+      const int j0 = (int)jobs.size();
+      const long t0 = tiles;
       job(y.qkv, S.d, S.NQKV);
       job(y.wo, S.d, S.d);
       for (long e = 0; e < (m->E ? m->E : 1); e++) {
         job(y.gu + e * S.d * 2 * S.F, S.d, 2 * S.F);
         job(y.down + e * S.F * S.d, S.F, S.d);
       }
+      group(j0, t0);  // group 1 + l: layer l
     }
     m->tjob_n = (int)jobs.size();
     m->tjob_tiles = tiles;
@@ -1840,6 +1902,10 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_norm, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_tr_fork, hipEventDisableTiming);
+    m->ev_tr.assign(m->tgroups.size(), nullptr);
+    for (size_t g = 0; g < m->ev_tr.size() && e == hipSuccess; g++)
+      e = hipEventCreateWithFlags(&m->ev_tr[g], hipEventDisableTiming);
     for (int k = 0; k < 2 && m->E; k++) {
       m->ev_moe[k].assign(m->L, nullptr);
       for (long l = 0; l < m->L && e == hipSuccess; l++)
@@ -1901,6 +1967,9 @@ extern "C" int sj_model_destroy(sj_model* m) {
   if (m->ev_fork) hipEventDestroy(m->ev_fork);
   if (m->ev_join) hipEventDestroy(m->ev_join);
   if (m->ev_norm) hipEventDestroy(m->ev_norm);
+  if (m->ev_tr_fork) hipEventDestroy(m->ev_tr_fork);
+  for (hipEvent_t ev : m->ev_tr)
+    if (ev) hipEventDestroy(ev);
   for (int k = 0; k < 2; k++)
     for (hipEvent_t ev : m->ev_moe[k])
       if (ev) hipEventDestroy(ev);
@@ -2071,6 +2140,7 @@ static int run_step(sj_model* m) {
     SJ_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
   }
   SJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  m->mt_stale = m->planes;  // the replayed update left the transposed mirror behind
   return SJ_OK;
 }
 
@@ -2470,6 +2540,7 @@ extern "C" int sj_model_forward_cached(sj_model* m, sj_cache* c, const int32_t* 
   const Stage& S = m->stages[0];
   const long d = S.d, L = c->length;
   const int dt = m->dt;
+  if (m->mt_stale) TRY(transpose_mirror(m));  // weights updated since the last forward
   SJ_HIP(hipMemcpyAsync(c->ids, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
   TRY(sj_embedding_fwd(s, wc(m, m->emb), dt, c->ids, c->x[0], dt, n, d));
   int top = 0;
