@@ -232,3 +232,42 @@ def test_cached_measurement_report(tmp_path):
         assert rep["decode_tokens_per_second"] > 0
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_inference_after_training_uses_updated_weights(graph):
+    """A training step leaves the transposed weight mirror to the next
+    forward, which rebuilds it beside its layers; inference after training
+    must still see the updated weights: the trained model's cached decode
+    and full logits equal those of a fresh model given its parameters."""
+    from sejong_amd.benchmark import full_logits
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    mc, tc = config("cfg2")
+    mc.layers, tc.batch, tc.sequence = 2, 2, 128
+    params = init_params(mc, std=0.02)
+    ids, tg = byte_batch(Rng(9), tc.batch, tc.sequence)
+    a = Model(mc, tc)
+    b = Model(mc, tc)
+    try:
+        a.set_params(params)
+        a.set_batch(ids, tg)
+        a.use_graph(graph)
+        for _ in range(3):
+            a.train_step(1e-2)
+        trained = a.get_params()
+        assert np.any(trained != params)
+        seq = np.random.default_rng(4).integers(0, 256, tc.sequence).astype(np.int32)
+        ca = a.new_cache()
+        got = [a.forward_cached(seq[:100], ca)] + [a.forward_cached(seq[p:p + 1], ca) for p in range(100, 104)]
+        b.set_params(trained)
+        cb = b.new_cache()
+        ref = [b.forward_cached(seq[:100], cb)] + [b.forward_cached(seq[p:p + 1], cb) for p in range(100, 104)]
+        for x, y in zip(got, ref):
+            np.testing.assert_array_equal(x, y)
+        a.train_step(1e-2)  # and the forward-only path after another step
+        b.set_params(a.get_params())
+        np.testing.assert_array_equal(full_logits(a, seq), full_logits(b, seq))
+        ca.close(); cb.close()
+    finally:
+        a.close(); b.close()
