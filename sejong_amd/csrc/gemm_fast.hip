@@ -333,22 +333,27 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   const bf16_t* src[PER_WAVE];
   int kpos[PER_WAVE];
   long kmul[PER_WAVE];
+  // Block j of every wave starts at stage row 32 j + 8 wave: with AROWS,
+  // BM and BN multiples of 32, whether it holds A or B, and which plane and
+  // (gate/up) half, follow from j alone, so the unrolled setup has no
+  // per-wave branches.
+  static_assert(AROWS % 32 == 0 && BM % 32 == 0 && BN % 32 == 0, "block-to-operand map");
 #pragma unroll
   for (int j = 0; j < PER_WAVE; j++) {
     const int r8 = (wave_s + 4 * j) * 8;
     const bf16_t* base;
     long ld, row, rows;
     bool tr;
-    if (r8 < AROWS) {
-      const int pl = r8 / BM;
+    if (32 * j < AROWS) {
+      const int pl = (32 * j) / BM;
       base = pl ? a1 : a0;
       ld = plda;
       tr = TA;
       row = tr ? m0 + ((r8 % BM) / 64) * 64 : m0 + (r8 % BM) + (sl >> 3);
       rows = pM;
     } else {
-      const int rb = r8 - AROWS;
-      const int q = rb / (BN * PB), pl = (rb % (BN * PB)) / BN;
+      const int rb = r8 - AROWS, rb32 = 32 * j - AROWS;
+      const int q = rb32 / (BN * PB), pl = (rb32 % (BN * PB)) / BN;
       const int sg = DUAL ? q : seg;
       base = (pl ? (sg == 0 ? b10 : sg == 1 ? b11 : b12) : (sg == 0 ? b00 : sg == 1 ? b01 : b02)) + boff;
       ld = sg == 0 ? ldb0 : sg == 1 ? ldb1 : ldb2;
