@@ -89,6 +89,9 @@ struct FParams {
   const int* goff;
   int gE, gmode;
   long gstride_b, gstride_c;
+  // n / d as (n * m) >> 40 with m = 2^40 / d + 1 (exact for n, d < 2^20):
+  // the grid's smaller tile count and the tiles of one K slice
+  unsigned long long mdiv_lo, mdiv_xy;
 };
 
 int g_remap = -1;
@@ -260,6 +263,9 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   asm volatile("" : "+s"(a0), "+s"(a1), "+s"(b00), "+s"(b01), "+s"(b02), "+s"(b10), "+s"(b11), "+s"(b12));
   asm volatile("" : "+s"(ldb0), "+s"(ldb1), "+s"(ldb2), "+s"(gsb), "+s"(gsc), "+s"(goff), "+s"(nx), "+s"(ny),
                     "+s"(nz));
+  unsigned long long mlo = p.mdiv_lo, mxy = p.mdiv_xy;
+  asm volatile("" : "+s"(mlo), "+s"(mxy));
+  auto fdiv = [](unsigned n, unsigned long long mg) { return (unsigned)(((unsigned long long)n * mg) >> 40); };
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8
   // XCDs (linear id b -> XCD b % 8), each with its own L2.  Give XCD k a
   // contiguous run of the row-major tile order so the tiles that share A rows
@@ -274,14 +280,14 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   // the smaller tile dimension varies fastest, so consecutive workgroups
   // (one XCD's run) share the operand of the larger one
   unsigned tx, ty;
+  const unsigned tz = fdiv(logical, mxy), in = logical - tz * nx * ny;  // index inside one K slice
   if (ny < nx) {
-    ty = logical % ny;
-    tx = (logical / ny) % nx;
+    ty = in - fdiv(in, mlo) * ny;
+    tx = fdiv(in, mlo);
   } else {
-    tx = logical % nx;
-    ty = (logical / nx) % ny;
+    tx = in - fdiv(in, mlo) * nx;
+    ty = fdiv(in, mlo);
   }
-  const unsigned tz = logical / (nx * ny);
   const long m0 = (long)ty * BM, n0 = (long)tx * BN;
   int ge = 0;
   if (pgm == 1) {
@@ -813,6 +819,12 @@ int launch_ns(hipStream_t s, const FParams& p, int splits) {
   const_cast<FParams&>(p).xcd_remap = xcd_remap();
   // grid z: split-K slices, or the experts of a per-expert dW launch
   dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM), (unsigned)splits);
+  if ((unsigned long long)grid.x * grid.y * grid.z >= (1ull << 20))
+    return sjh::fail(SJ_ERR_INVALID, "gemm: %u x %u x %u workgroups (at most 2^20)", grid.x, grid.y, grid.z);
+  auto magic = [](unsigned long long d) { return (1ull << 40) / d + 1; };
+  const unsigned small = grid.y < grid.x ? grid.y : grid.x;
+  const_cast<FParams&>(p).mdiv_lo = magic(small);
+  const_cast<FParams&>(p).mdiv_xy = magic((unsigned long long)grid.x * grid.y);
   sjh::ProfHook& h = sjh::prof_hook();
   if (h.on && h.k0) {  // kernel timing: events at the kernel's own start and end
     hipExtLaunchKernelGGL(kern, grid, dim3(NT), (uint32_t)lds, s, h.k0, h.k1, 0u, p);
