@@ -346,29 +346,34 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   static_assert(AROWS % 32 == 0 && BM % 32 == 0 && BN % 32 == 0, "block-to-operand map");
 #pragma unroll
   for (int j = 0; j < PER_WAVE; j++) {
-    const int r8 = (wave_s + 4 * j) * 8;
+    // stage row 8 wave + 32 j: its offset inside a plane is 8 wave + c32
+    // with c32 = (32 j) % plane rows (8 wave < 32 never carries), so every
+    // per-block term below but 8 wave is a compile-time constant
     const bf16_t* base;
     long ld, row, rows;
     bool tr;
+    int c64;  // (stage row % 64) - 8 wave
     if (32 * j < AROWS) {
-      const int pl = (32 * j) / BM;
+      const int pl = (32 * j) / BM, c32 = (32 * j) % BM;
       base = pl ? a1 : a0;
       ld = plda;
       tr = TA;
-      row = tr ? m0 + ((r8 % BM) / 64) * 64 : m0 + (r8 % BM) + (sl >> 3);
+      row = tr ? m0 + (c32 / 64) * 64 : m0 + wave_s * 8 + c32 + (sl >> 3);
       rows = pM;
+      c64 = c32 % 64;
     } else {
-      const int rb = r8 - AROWS, rb32 = 32 * j - AROWS;
-      const int q = rb32 / (BN * PB), pl = (rb32 % (BN * PB)) / BN;
+      const int rb32 = 32 * j - AROWS;
+      const int q = rb32 / (BN * PB), pl = (rb32 % (BN * PB)) / BN, c32 = rb32 % BN;
       const int sg = DUAL ? q : seg;
       base = (pl ? (sg == 0 ? b10 : sg == 1 ? b11 : b12) : (sg == 0 ? b00 : sg == 1 ? b01 : b02)) + boff;
       ld = sg == 0 ? ldb0 : sg == 1 ? ldb1 : ldb2;
       tr = TB;
-      row = tr ? nl0 + ((rb % BN) / 64) * 64 : nl0 + (rb % BN) + (sl >> 3);
+      row = tr ? nl0 + (c32 / 64) * 64 : nl0 + wave_s * 8 + c32 + (sl >> 3);
       rows = nrows_b;
+      c64 = c32 % 64;
     }
     if (tr) {
-      const int kr = (r8 % 64) + (sl >> 3);
+      const int kr = wave_s * 8 + c64 + (sl >> 3);
       const long col = row + 8 * ((sl & 7) ^ swt(kr));
       src[j] = col < rows ? base + (kbeg + kr) * ld + col : zero;
       kpos[j] = kr;
