@@ -241,6 +241,8 @@ def issued_factor(kernel: str) -> float:
         t = [int(x) for x in kernel[len("k_gemm_fast<"):-1].split(",")]
         pa, pb = t[2], t[3]
         return float(pa * pb - (1 if pa == 2 and pb == 2 else 0))
+    if kernel.startswith("k_gemm_kw<"):  # token-split dW: one X plane times PB planes of Y
+        return float(int(kernel[len("k_gemm_kw<"):-1].split(",")[0]))
     return {"k_attn2_fwd<3>": 1.5, "k_attn2_bwd": 6.5 / 2.5, "k_attn2_bwd_g<3>": 6.5 / 2.5}.get(kernel, 1.0)
 
 

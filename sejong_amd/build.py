@@ -21,6 +21,13 @@ HIPFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
             "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-parameter"]
 
 
+# Per-source flags.  gemm_fast.hip: MFMA accumulators in ordinary VGPRs
+# (gfx950 allows either file); with accumulators in AGPRs the register
+# allocator rotated the token-split dW kernel's accumulators through
+# v_accvgpr moves every step.
+EXTRA = {"gemm_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _hipcc():
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     p = os.path.join(rocm, "bin", "hipcc")
@@ -35,7 +42,7 @@ def build(verbose: bool = False, jobs: int = 6) -> str:
     for src in SOURCES:
         obj = os.path.join(objdir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmd = [_hipcc(), *HIPFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [_hipcc(), *HIPFLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))

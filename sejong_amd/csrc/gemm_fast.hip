@@ -92,6 +92,9 @@ struct FParams {
   // n / d as (n * m) >> 40 with m = 2^40 / d + 1 (exact for n, d < 2^20):
   // the grid's smaller tile count and the tiles of one K slice
   unsigned long long mdiv_lo, mdiv_xy;
+  // k_gemm_kw E_STORE (nullable): FP64 sum of squares of the values each
+  // workgroup stores, at sq[linear workgroup id] (the gradient-norm hook)
+  double* sq;
 };
 
 int g_remap = -1;
@@ -787,6 +790,236 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   }
 }
 
+// ------------------------------------------------------- token-split dW
+// C = X^T Y for row-layout operands (X [K][M] one bf16 plane, Y [K][N] as PB
+// planes): the weight gradient contracted over token rows.  In the k_gemm_fast
+// form both operands reach the MFMA through LDS transpose reads, which the
+// LDS serves at half the rate of ordinary reads, and with a 32x32 tile per
+// wave the LDS port (DMA writes plus fragment reads) bounds a k-step at about
+// four times its MFMA time.  Here every wave owns the whole 64x64 tile: the
+// four waves take interleaved 32-token slices of the workgroup's K range
+// (wave w: tokens 128 s + 32 w .. + 31 at step s), so each fragment read
+// feeds twice the MFMAs.  A wave stages only its own slices, in its own LDS
+// region, and waits only for its own DMA: the main loop has no workgroup
+// barrier.  The four partial tiles are added in LDS in wave order,
+// ((w0 + w1) + w2) + w3, so the result does not depend on timing.
+constexpr int KW_ROWS = 32;                  // tokens per wave step
+constexpr int KW_SUB = KW_ROWS * 64;         // elements of one 32 x 64 sub-tile
+constexpr int KW_TLD = 64 + 4;               // fp32 reduction tile row stride
+
+template <int PB, int NS>
+constexpr size_t kw_lds_bytes() {
+  constexpr size_t pipe = (size_t)4 * NS * (1 + PB) * KW_SUB * 2;
+  constexpr size_t red = (size_t)4 * 64 * KW_TLD * 4;
+  return pipe > red ? pipe : red;
+}
+
+template <int PB, int EPI, int NS>
+__global__ __launch_bounds__(NT) void k_gemm_kw(FParams p) {
+  static_assert(EPI == E_STORE || EPI == E_PARTIAL, "plain products only");
+  constexpr int NSUB = 1 + PB;              // sub-tiles per stage: X, then the Y planes
+  constexpr int STAGE = NSUB * KW_SUB;      // elements of one wave stage
+  constexpr int PER = NSUB * 4;             // DMAs per wave stage (8 token rows each)
+  static_assert(PER * NS < 64, "outstanding DMA beyond vmcnt range");
+  static_assert(NS == 2, "two buffers");
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // kernel arguments fetched together at entry and held in SGPRs
+  long pM = p.M, pN = p.N, pK = p.K, ldx = p.lda, ldy = p.ldb[0], pkch = p.kchunk;
+  const bf16_t *x0 = p.a[0], *y0 = p.b[0][0], *y1 = p.b[1][0];
+  int pxr = p.xcd_remap;
+  unsigned nx = gridDim.x, ny = gridDim.y, nz = gridDim.z;
+  unsigned long long mlo = p.mdiv_lo, mxy = p.mdiv_xy;
+  asm volatile("" : "+s"(pM), "+s"(pN), "+s"(pK), "+s"(ldx), "+s"(ldy), "+s"(pkch), "+s"(pxr));
+  asm volatile("" : "+s"(x0), "+s"(y0), "+s"(y1), "+s"(nx), "+s"(ny), "+s"(nz), "+s"(mlo), "+s"(mxy));
+  auto fdiv = [](unsigned n, unsigned long long mg) { return (unsigned)(((unsigned long long)n * mg) >> 40); };
+  // tile order as in k_gemm_fast: a contiguous run of the tile order per XCD,
+  // the smaller tile dimension fastest
+  const unsigned nb = nx * ny * nz;
+  const unsigned b = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  unsigned logical = b;
+  if (pxr) {
+    const unsigned xcd = b & 7, local = b >> 3, q8 = nb >> 3, r8x = nb & 7;
+    logical = xcd * q8 + (xcd < r8x ? xcd : r8x) + local;
+  }
+  unsigned tx, ty;
+  const unsigned tz = fdiv(logical, mxy), in = logical - tz * nx * ny;
+  if (ny < nx) {
+    ty = in - fdiv(in, mlo) * ny;
+    tx = fdiv(in, mlo);
+  } else {
+    tx = in - fdiv(in, mlo) * nx;
+    ty = fdiv(in, mlo);
+  }
+  const long m0 = (long)ty * 64, n0 = (long)tx * 64;
+  long kbeg = 0, kend = pK;
+  if constexpr (EPI == E_PARTIAL) {
+    kbeg = (long)tz * pkch;
+    kend = kbeg + pkch < pK ? kbeg + pkch : pK;
+  }
+  const long klen = kend - kbeg;
+  const int nsw = (int)(klen / (4 * KW_ROWS));  // steps of every wave (klen is a multiple of 256)
+
+  // DMA sources.  Block j (8 token rows) is rows 8 (j % 4) .. + 7 of
+  // sub-tile j / 4 (0: X, 1: Y hi, 2: Y lo).  Chunk c of k-row r of a
+  // sub-tile sits at slot c ^ swt(r) (the transpose-read swizzle), so the
+  // lane writing slot lane % 8 of k-row kr fetches chunk (lane % 8) ^ swt(kr).
+  // A column past the operand's last (M or N a multiple of 8, not of 64)
+  // reads the last chunk instead: it feeds only outputs of rows or columns
+  // that are never stored.  Every slice is an even number of steps (K and
+  // the slice length are multiples of 256), so no token check is needed.
+  // The DMA takes a uniform base (the step's first token row of the
+  // operand, advanced by scalar arithmetic) plus a fixed 32-bit byte offset
+  // per lane and block: no vector address arithmetic in the loop.
+  uint32_t voff[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int sub = j / 4;
+    const int kr = KW_ROWS * wave + 8 * (j % 4) + (lane >> 3);
+    const long ld = sub == 0 ? ldx : ldy;
+    const long cols = sub == 0 ? pM : pN;
+    long col = (sub == 0 ? m0 : n0) + 8 * ((lane & 7) ^ swt(kr & 31));
+    col = col < cols ? col : cols - 8;
+    voff[j] = (uint32_t)((kr * ld + col) * 2);
+  }
+  const uint32_t lds_wave =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds) + (uint32_t)(wave * NS * STAGE * 2);
+  // step `it` (a step past the wave's last reloads the last one into a
+  // buffer no step reads) into buffer `buf`, blocks [j0, j1)
+  auto issue = [&](int it, int buf, int j0, int j1) {
+    const long st = (long)(it < nsw ? it : nsw - 1) * 4 * KW_ROWS + kbeg;  // first token row of the step
+    const uint8_t* bx = (const uint8_t*)(x0 + st * ldx);
+    const uint8_t* by0 = (const uint8_t*)(y0 + st * ldy);
+    const uint8_t* by1 = (const uint8_t*)(y1 + st * ldy);
+    const uint32_t sb = lds_wave + (uint32_t)(buf * STAGE * 2);
+#pragma unroll
+    for (int j = j0; j < j1; j++) {
+      const uint8_t* bs = j < 4 ? bx : j < 8 ? by0 : by1;
+      asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:0" ::"v"(voff[j]), "s"(bs),
+                   "s"(sb + (uint32_t)(j * 1024))
+                   : "memory", "m0");
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // fragment f of a step: 0..3 the X columns 16f.., 4..7 the Y hi columns
+  // 16 (f - 4).., 8..11 the Y lo columns
+  constexpr int NF = 4 + 4 * PB;
+  auto load_frag = [&](int buf, int f, bf16x8* fr) {
+    const bf16_t* st = lds + (wave * NS + buf) * STAGE;
+    fr[f] = tr_frag(st + (f / 4) * KW_SUB, 0, 16 * (f % 4), lane);
+  };
+  // MFMA q of a step: half q / (NQ / 2) covers column blocks 2 half, + 1;
+  // an accumulator's hi- and lo-plane products are adjacent
+  constexpr int NQ = 16 * PB;
+  auto mfma_q = [&](int q, const bf16x8* fr) {
+    const int r = q % (NQ / 2), pl = r % PB, j = 2 * (q / (NQ / 2)) + (r / (4 * PB)) % 2, i = (r / PB) % 4;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fr[i], fr[4 + 4 * pl + j], acc[i][j], 0, 0, 0);
+  };
+
+  // Software pipeline, two buffers, two steps in flight.  A step's
+  // fragments are read into registers during the previous step, so its
+  // buffer is free when the step starts and step it + 2 is loaded into it,
+  // its DMA blocks between the first half of step it's MFMAs; step it + 1's
+  // transpose reads go between the second half.  The loop is unrolled by
+  // two, so buffers and fragment register sets alternate at compile time.
+  static_assert(NS == 2, "two buffers");
+  bf16x8 fa[NF], fb[NF];
+  auto body = [&](int it, bf16x8* cur, bf16x8* nxt, int bcur, int bnxt) {
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0): step it's reads done
+#pragma unroll
+    for (int q = 0; q < NQ / 2; q++) {
+      mfma_q(q, cur);
+      issue(it + 2, bcur, q * PER / (NQ / 2), (q + 1) * PER / (NQ / 2));
+    }
+    wait_vm<PER>();  // step it + 1 has landed
+#pragma unroll
+    for (int q = NQ / 2; q < NQ; q++) {
+      mfma_q(q, cur);
+      const int q2 = q - NQ / 2;
+#pragma unroll
+      for (int f = q2 * NF / (NQ / 2); f < (q2 + 1) * NF / (NQ / 2); f++) load_frag(bnxt, f, nxt);
+    }
+  };
+  issue(0, 0, 0, PER);
+  issue(1, 1, 0, PER);
+  wait_vm<PER>();  // step 0 has landed
+#pragma unroll
+  for (int f = 0; f < NF; f++) load_frag(0, f, fa);
+  for (int it = 0; it < nsw; it += 2) {  // nsw is even: slices are multiples of 256 tokens
+    body(it, fa, fb, 0, 1);
+    body(it + 1, fb, fa, 1, 0);
+  }
+  wait_vm<0>();  // the trailing reloads land before the LDS is reused
+
+  // ---- the four partial tiles, added in wave order
+  // acc[i][j][r] = C[m0 + 16i + 4 (lane / 16) + r][n0 + 16j + lane % 16]
+  __syncthreads();  // every wave has finished reading its stages
+  float* TF = (float*)lds;
+  const int fg = lane >> 4, cc = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) TF[(wave * 64 + 16 * i + 4 * fg + r) * KW_TLD + 16 * j + cc] = acc[i][j][r];
+  __syncthreads();
+  float* dst0 = EPI == E_PARTIAL ? p.partial + (long)tz * pM * pN : (float*)p.c[0];
+  const long ldd = EPI == E_PARTIAL ? pN : p.ldc[0];
+  const bool acc_out = EPI == E_STORE && p.accumulate;
+  const bool bfout = EPI == E_STORE && p.c_bf16;
+  // every 4-column chunk is a whole vector when the base and the row stride are
+  const bool vec = (ldd & 3) == 0 && ((uintptr_t)(bfout ? p.c[0] : (void*)dst0) & (bfout ? 7 : 15)) == 0;
+  double q = 0.0;
+  for (int c = threadIdx.x; c < 64 * 16; c += NT) {
+    const int r = c >> 4, c4 = (c & 15) * 4;
+    const long m = m0 + r, n = n0 + c4;
+    if (m >= pM || n >= pN) continue;  // N % 8 == 0: a chunk is in or out whole
+    float4 v = *(const float4*)(TF + r * KW_TLD + c4);
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+      const float4 u = *(const float4*)(TF + (w * 64 + r) * KW_TLD + c4);
+      v = make_float4(v.x + u.x, v.y + u.y, v.z + u.z, v.w + u.w);
+    }
+    if (bfout) {
+      bf16_t* d = (bf16_t*)p.c[0] + m * ldd + n;
+      if (vec) {
+        *(u32x2*)d = u32x2{pack2(f2bf(v.x), f2bf(v.y)), pack2(f2bf(v.z), f2bf(v.w))};
+      } else {
+        d[0] = f2bf(v.x); d[1] = f2bf(v.y); d[2] = f2bf(v.z); d[3] = f2bf(v.w);
+      }
+    } else {
+      float* d = dst0 + m * ldd + n;
+      if (vec) {
+        if (acc_out) {
+          const float4 o = *(const float4*)d;
+          v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *(float4*)d = v;
+      } else {
+        if (acc_out) {
+          v.x += d[0]; v.y += d[1]; v.z += d[2]; v.w += d[3];
+        }
+        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+      }
+    }
+    if constexpr (EPI == E_STORE)
+      q += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+  }
+  if (EPI == E_STORE && p.sq) {
+    __shared__ double red[NT / 64];
+    q = block_sum<double, NT>(q, red);
+    if (threadIdx.x == 0) p.sq[b] = q;
+  }
+}
+
 // sq (nullable): FP64 sum of squares of the values this workgroup stores,
 // at sq[blockIdx.x] (the gradient-norm hook)
 __global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict__ partial, int splits, long M, long N,
@@ -840,6 +1073,34 @@ int launch_ns(hipStream_t s, const FParams& p, int splits) {
   if (h.on)
     snprintf(h.kernel, sizeof(h.kernel), "k_gemm_fast<%d, %d, %d, %d, %d, %d, %d>", BM, BN, PA, PB, EPI, NS, TM);
   return SJ_OK;
+}
+
+template <int PB, int EPI, int NS>
+int launch_kw_ns(hipStream_t s, const FParams& p, int splits) {
+  constexpr size_t lds = kw_lds_bytes<PB, NS>();
+  static_assert(lds + 64 <= 160 * 1024, "LDS budget");
+  auto kern = k_gemm_kw<PB, EPI, NS>;
+  const_cast<FParams&>(p).xcd_remap = xcd_remap();
+  dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 63) / 64), (unsigned)splits);
+  if ((unsigned long long)grid.x * grid.y * grid.z >= (1ull << 20))
+    return sjh::fail(SJ_ERR_INVALID, "gemm: %u x %u x %u workgroups (at most 2^20)", grid.x, grid.y, grid.z);
+  auto magic = [](unsigned long long d) { return (1ull << 40) / d + 1; };
+  const unsigned small = grid.y < grid.x ? grid.y : grid.x;
+  const_cast<FParams&>(p).mdiv_lo = magic(small);
+  const_cast<FParams&>(p).mdiv_xy = magic((unsigned long long)grid.x * grid.y);
+  sjh::ProfHook& h = sjh::prof_hook();
+  if (h.on && h.k0) {
+    hipExtLaunchKernelGGL(kern, grid, dim3(NT), (uint32_t)lds, s, h.k0, h.k1, 0u, p);
+    h.used = true;
+  } else {
+    hipLaunchKernelGGL(kern, grid, dim3(NT), lds, s, p);
+  }
+  if (h.on) snprintf(h.kernel, sizeof(h.kernel), "k_gemm_kw<%d, %d, %d>", PB, EPI, NS);
+  return SJ_OK;
+}
+template <int EPI>
+int launch_kw(hipStream_t s, const FParams& p, int pb, int splits) {
+  return pb == 2 ? launch_kw_ns<2, EPI, 2>(s, p, splits) : launch_kw_ns<1, EPI, 2>(s, p, splits);
 }
 
 // Pipeline depth (measured on gfx950 over the cfg2 and cfg5 step GEMMs):
@@ -1021,6 +1282,30 @@ int splits_for(long M, long N, long K, int bm, int bn) {
   return s < 1 ? 1 : (int)s;
 }
 
+// Token-split dW plan (row-layout X with one plane, dW-shaped: K >= 1024, a
+// multiple of 256): 64x64 tiles, one workgroup per CU (96 KB of LDS for
+// split Y), so as many K slices as fill the CUs once, each at least 512
+// tokens.  SJ_GEMM_KW=0
+// selects the k_gemm_fast form; SJ_GEMM_KW_SPLITS=<n> overrides the slices
+// (sweeps).
+bool plan_kw(long M, long N, long K, int pa, int& splits) {
+  static int on = -1, ov = 0;
+  if (on < 0) {
+    const char* e = getenv("SJ_GEMM_KW");
+    on = e ? atoi(e) != 0 : 1;
+    const char* o = getenv("SJ_GEMM_KW_SPLITS");
+    ov = o ? atoi(o) : 0;
+  }
+  if (!on || pa != 1 || K < 1024 || K % 256) return false;
+  const long t = tiles(M, N, 64, 64), cu = cus();
+  if (t > cu) return false;
+  long sp = ov > 0 ? ov : cu / t;
+  if (sp > K / 512) sp = K / 512;
+  if (sp > 16) sp = 16;
+  splits = sp < 1 ? 1 : (int)sp;
+  return true;
+}
+
 template <int EPI, int PA, int PB, int TM = 0>
 int launch_tile(hipStream_t s, const FParams& p, int bm, int bn, int splits) {
   // both operands split: a 128x128 stage does not fit three deep in LDS
@@ -1098,6 +1383,19 @@ int set_attrs_planes() {
   return s;
 }
 
+template <int PB, int EPI, int NS>
+int set_attr_kw() {
+  hipError_t e = hipFuncSetAttribute((const void*)k_gemm_kw<PB, EPI, NS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)kw_lds_bytes<PB, NS>());
+  return e == hipSuccess ? SJ_OK : sjh::hip_check(e, "gemm: LDS attribute");
+}
+template <int EPI>
+int set_attrs_kw() {
+  int s = set_attr_kw<2, EPI, 2>();
+  if (!s) s = set_attr_kw<1, EPI, 2>();
+  return s;
+}
+
 }  // namespace
 
 // Raise the dynamic-LDS limit of every instantiation once (outside any
@@ -1117,6 +1415,8 @@ int gemm_fast_prepare() {
   if (!status) status = set_attrs_planes<E_PLANES>();
   if (!status) status = set_attrs_planes<E_STORE, 3>();
   if (!status) status = set_attrs_planes<E_PARTIAL, 3>();
+  if (!status) status = set_attrs_kw<E_STORE>();
+  if (!status) status = set_attrs_kw<E_PARTIAL>();
   return status;
 }
 }  // namespace sjh
@@ -1131,6 +1431,8 @@ extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
     for (int rl = 0; rl < 2; rl++) {
       int bm, bn, s;
       plan(M, N, K, pa, bm, bn, s, rl != 0);
+      int skw = 1;
+      if (rl && plan_kw(M, N, K, pa, skw) && skw > s) s = skw;  // the token-split dW plan
       const size_t b = s > 1 ? sizeof(float) * (size_t)s * (size_t)M * (size_t)N : 0;
       need = b > need ? b : need;
     }
@@ -1138,6 +1440,43 @@ extern "C" size_t sj_gemm_planes_workspace_bytes(long M, long N, long K) {
 }
 
 namespace {
+// split-K partials and their fixed-order reduce (with the gradient-norm
+// slots when the hook is armed)
+int reduce_partials(hipStream_t s, const FParams& p, int splits, void* workspace) {
+  const long M = p.M, N = p.N;
+  long total = M * N, blocks = (total + 255) / 256;
+  double* sq = nullptr;
+  sjh::GradSq& gs = sjh::grad_sq();
+  if (gs.base && gs.on) {  // gradient-norm slots: fewer, longer workgroups
+    if (blocks > 1024) blocks = 1024;
+    sq = gs.take(blocks);
+  } else if (blocks > 4096) {
+    blocks = 4096;
+  }
+  hipLaunchKernelGGL(k_reduce_partials, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)workspace, splits, M, N,
+                     p.c[0], p.ldc[0], (int)p.c_bf16, p.accumulate, sq);
+  return SJ_OK;
+}
+
+int gemm_kw(hipStream_t s, FParams& p, int pb, int splits, void* workspace, size_t workspace_bytes) {
+  const long M = p.M, N = p.N, K = p.K;
+  if (splits > 1 && workspace && workspace_bytes >= sizeof(float) * (size_t)splits * M * N) {
+    long kchunk = (K + splits - 1) / splits;
+    kchunk = (kchunk + 255) / 256 * 256;  // an even number of 128-token steps
+    splits = (int)((K + kchunk - 1) / kchunk);
+    p.kchunk = kchunk;
+    p.partial = (float*)workspace;
+    if (int st = launch_kw<E_PARTIAL>(s, p, pb, splits)) return st;
+    reduce_partials(s, p, splits, workspace);
+  } else {
+    sjh::GradSq& gs = sjh::grad_sq();
+    if (gs.base && gs.on) p.sq = gs.take(tiles(M, N, 64, 64));  // slot per workgroup, linear id
+    if (int st = launch_kw<E_STORE>(s, p, pb, 1)) return st;
+  }
+  SJ_LAUNCH_CHECK("matmul planes (token-split dW)");
+  return SJ_OK;
+}
+
 template <int TM>
 int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo, long lda,
                 const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype, long ldc, int accumulate,
@@ -1151,6 +1490,8 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
   p.c[0] = c; p.ldc[0] = ldc; p.c_bf16 = c_dtype == SJ_BF16; p.accumulate = accumulate;
   const int pa = a_lo ? 2 : 1, pb = b_lo ? 2 : 1;
   int bm, bn, splits;
+  if constexpr (TM == 3)
+    if (plan_kw(M, N, K, pa, splits)) return gemm_kw(s, p, pb, splits, workspace, workspace_bytes);
   plan(M, N, K, pa, bm, bn, splits, TM != 0);
   if (splits > 1 && workspace && workspace_bytes >= sizeof(float) * (size_t)splits * M * N) {
     long kchunk = (K + splits - 1) / splits;
@@ -1160,17 +1501,7 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
     p.partial = (float*)workspace;
     int st = launch_planes<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
     if (st) return st;
-    long total = M * N, blocks = (total + 255) / 256;
-    double* sq = nullptr;
-    sjh::GradSq& gs = sjh::grad_sq();
-    if (gs.base && gs.on) {  // gradient-norm slots: fewer, longer workgroups
-      if (blocks > 1024) blocks = 1024;
-      sq = gs.take(blocks);
-    } else if (blocks > 4096) {
-      blocks = 4096;
-    }
-    hipLaunchKernelGGL(k_reduce_partials, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)workspace, splits, M,
-                       N, c, ldc, (int)p.c_bf16, accumulate, sq);
+    reduce_partials(s, p, splits, workspace);
   } else {
     int st = launch_planes<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
     if (st) return st;

@@ -1821,6 +1821,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   upd(sj_gemm_workspace_bytes(m->HR, m->d, m->HV));
   upd(sj_gemm_workspace_bytes(m->d, m->HV, m->HR));
   upd(sj_gemm_workspace_bytes(m->HR, m->HV, m->d));
+  if (m->lm_planes) upd(sj_gemm_planes_workspace_bytes(m->d, m->Vp, m->HR));  // head dW
   for (const Stage& S : m->stages) {
     const long Mi = S.M;
     upd(sj_rmsnorm_bwd_workspace_bytes(Mi, S.d));

@@ -81,6 +81,15 @@ TN_CASES = [
     (384, 384, 16384, False, True),    # long K: split-K partials
     (256, 192, 512, True, True),       # both operands split
     (64, 64, 40, False, False),        # one tile, K shorter than a stage
+    # token-split dW kernel (one X plane, K >= 1024 a multiple of 256):
+    # ragged tiles, one or two Y planes, 1..16 K slices
+    (136, 200, 1536, False, True),
+    (200, 136, 2048, False, False),
+    (72, 64, 1280, False, True),
+    (64, 1024, 8192, False, True),
+    # K >= 1024 not a multiple of 256: the k_gemm_fast form
+    (136, 200, 1500, False, True),
+    (200, 136, 2056, False, False),
 ]
 
 
@@ -133,6 +142,29 @@ def test_gemm_planes_accumulate(api, lib):
                        ws.p, ws.nbytes)
     sync()
     assert rel(C.host(), (C0 + O.matmul(A, B, 0, 1)).ravel()) < 3e-5
+
+
+@pytest.mark.parametrize("M,N,K,cdt,accumulate", [(384, 2048, 4096, "f32", 1), (384, 640, 4096, "f32", 1),
+                                                  (384, 2048, 4096, "bf16", 0), (384, 640, 4096, "bf16", 0)])
+def test_gemm_planes_tn_accumulate_and_bf16(api, lib, M, N, K, cdt, accumulate):
+    """Row-layout products with C += X^T Y or a bf16 C, unsplit (the tile
+    count fills the CUs) and split-K (partials and their reduce)."""
+    rng = np.random.default_rng(M + N + K + accumulate)
+    X = O.round_to(rng.normal(0, 1, (K, M)), "bf16")
+    Y = rng.normal(0, 1, (K, N)).astype(np.float32).astype(np.float64)
+    yh, yl = split(Y)
+    C0 = rng.normal(0, 1, (M, N)).astype(np.float32).astype(np.float64) if accumulate else np.zeros((M, N))
+    C = dev(C0) if cdt == "f32" else zeros(M * N, "bf16")
+    ws = empty(max(lib.sj_gemm_planes_workspace_bytes(M, N, K), 256), "u8")
+    print(f"[gemm_tn] M={M} N={N} K={K} {cdt} accumulate {accumulate}", flush=True)
+    api.sj_gemm_planes_tn(None, M, N, K, dev(X, "bf16").p, None, M, dev(yh, "bf16").p, dev(yl, "bf16").p, N, C.p,
+                          F32 if cdt == "f32" else BF, N, accumulate, ws.p, ws.nbytes)
+    sync()
+    ref = (C0 + O.matmul(X, Y, 1, 0)).ravel()
+    if cdt == "bf16":
+        assert_stored_close(C.host(), ref, "bf16", "tn bf16", terms=O.matmul(np.abs(X), np.abs(Y), 1, 0))
+    else:
+        assert rel(C.host(), ref) < 3e-5
 
 
 def _pairmax(a, M, H, Dh):
