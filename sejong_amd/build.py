@@ -21,11 +21,12 @@ HIPFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
             "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-parameter"]
 
 
-# Per-source flags.  gemm_fast.hip: MFMA accumulators in ordinary VGPRs
-# (gfx950 allows either file); with accumulators in AGPRs the register
-# allocator rotated the token-split dW kernel's accumulators through
-# v_accvgpr moves every step.
-EXTRA = {"gemm_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source flags.  The MFMA sources keep their accumulators in ordinary
+# VGPRs (gfx950 allows either file): with accumulators in AGPRs the register
+# allocator rotated them through v_accvgpr moves inside the hot loops (the
+# token-split dW kernel every step, the attention forward's output tile).
+_VGPR_ACC = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+EXTRA = {"gemm_fast.hip": _VGPR_ACC, "attention_t.hip": _VGPR_ACC, "attention.hip": _VGPR_ACC, "gemm.hip": _VGPR_ACC}
 
 
 def _hipcc():
