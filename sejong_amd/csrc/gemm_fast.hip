@@ -120,6 +120,14 @@ __device__ __forceinline__ void wait_vm() {
 // every ds_read and drain the pipeline); completion is tracked explicitly
 // with wait_vm before the barrier that publishes a stage.  M0 written by
 // S_MOV needs one wait state before the LDS-DMA.
+// a pointer every lane holds alike, as a scalar value (the divergence
+// analysis cannot always prove it)
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const unsigned long long v = (unsigned long long)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(uintptr_t)(((unsigned long long)hi << 32) | lo);
+}
+
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
                : "memory", "m0");
@@ -339,9 +347,16 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
   // wait, before every issue.
   const bf16_t* zero = (const bf16_t*)g_zero16;
   asm volatile("" : "+s"(zero));
-  const bf16_t* src[PER_WAVE];
+  // Every block's DMA takes a uniform base (its operand at the tile's first
+  // row or column and the K slice's first k, advanced a stage at a time by
+  // scalar arithmetic) plus a fixed 32-bit byte offset per lane.  A row or
+  // column past the operand reads its last one (rows) or last chunk
+  // (columns) instead: it feeds only outputs that are never stored.  Tokens
+  // past the K range (the last stage of a ragged K) read `zero`.
+  const uint8_t* bj[PER_WAVE];
+  uint32_t voff[PER_WAVE];
+  long kstr[PER_WAVE];  // bytes per stage
   int kpos[PER_WAVE];
-  long kmul[PER_WAVE];
   // Block j of every wave starts at stage row 32 j + 8 wave: with AROWS,
   // BM and BN multiples of 32, whether it holds A or B, and which plane and
   // (gate/up) half, follow from j alone, so the unrolled setup has no
@@ -353,38 +368,43 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     // with c32 = (32 j) % plane rows (8 wave < 32 never carries), so every
     // per-block term below but 8 wave is a compile-time constant
     const bf16_t* base;
-    long ld, row, rows;
+    long ld, row0, rows;
     bool tr;
-    int c64;  // (stage row % 64) - 8 wave
+    int c32;
     if (32 * j < AROWS) {
-      const int pl = (32 * j) / BM, c32 = (32 * j) % BM;
+      const int pl = (32 * j) / BM;
+      c32 = (32 * j) % BM;
       base = pl ? a1 : a0;
       ld = plda;
       tr = TA;
-      row = tr ? m0 + (c32 / 64) * 64 : m0 + wave_s * 8 + c32 + (sl >> 3);
+      row0 = m0;
       rows = pM;
-      c64 = c32 % 64;
     } else {
       const int rb32 = 32 * j - AROWS;
-      const int q = rb32 / (BN * PB), pl = (rb32 % (BN * PB)) / BN, c32 = rb32 % BN;
+      const int q = rb32 / (BN * PB), pl = (rb32 % (BN * PB)) / BN;
+      c32 = rb32 % BN;
       const int sg = DUAL ? q : seg;
       base = (pl ? (sg == 0 ? b10 : sg == 1 ? b11 : b12) : (sg == 0 ? b00 : sg == 1 ? b01 : b02)) + boff;
       ld = sg == 0 ? ldb0 : sg == 1 ? ldb1 : ldb2;
       tr = TB;
-      row = tr ? nl0 + (c32 / 64) * 64 : nl0 + wave_s * 8 + c32 + (sl >> 3);
+      row0 = nl0;
       rows = nrows_b;
-      c64 = c32 % 64;
     }
     if (tr) {
-      const int kr = wave_s * 8 + c64 + (sl >> 3);
-      const long col = row + 8 * ((sl & 7) ^ swt(kr));
-      src[j] = col < rows ? base + (kbeg + kr) * ld + col : zero;
+      const int kr = wave_s * 8 + c32 % 64 + (sl >> 3);
+      long col = row0 + (c32 / 64) * 64 + 8 * ((sl & 7) ^ swt(kr));
+      col = col < rows ? col : rows - 8;
+      bj[j] = uniform_ptr(base + kbeg * ld + row0);
+      voff[j] = (uint32_t)((kr * ld + (col - row0)) * 2);
+      kstr[j] = (long)BK * ld * 2;
       kpos[j] = kr;
-      kmul[j] = col < rows ? ld : 0;
     } else {
-      src[j] = row < rows ? base + row * ld + kbeg + c8 : zero;
+      long row = row0 + wave_s * 8 + c32 + (sl >> 3);
+      row = row < rows ? row : rows - 1;
+      bj[j] = uniform_ptr(base + row0 * ld + kbeg);
+      voff[j] = (uint32_t)(((row - row0) * ld + c8) * 2);
+      kstr[j] = (long)BK * 2;
       kpos[j] = c8 + 7;
-      kmul[j] = row < rows ? 1 : 0;
     }
   }
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
@@ -395,12 +415,16 @@ __global__ __launch_bounds__(NT) void k_gemm_fast(FParams p) {
     const uint32_t sbase = lds_base + (uint32_t)(buf * STAGE_ROWS * BK * 2) + (uint32_t)(wave_s * 8 * BK * 2);
     if (k0 + BK <= klen) {  // uniform: every lane's k offset is in range
 #pragma unroll
-      for (int j = 0; j < PER_WAVE; j++) dma16(src[j] + k0 * kmul[j], sbase + (uint32_t)(j * 32 * BK * 2));
+      for (int j = 0; j < PER_WAVE; j++)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:0" ::"v"(voff[j]),
+                     "s"(bj[j] + it * kstr[j]), "s"(sbase + (uint32_t)(j * 32 * BK * 2))
+                     : "memory", "m0");
     } else {
 #pragma unroll
       for (int j = 0; j < PER_WAVE; j++) {
         const bool kin = k0 + kpos[j] < klen;
-        dma16(kin ? src[j] + k0 * kmul[j] : zero, sbase + (uint32_t)(j * 32 * BK * 2));
+        dma16(kin ? (const void*)(bj[j] + it * kstr[j] + voff[j]) : (const void*)zero,
+              sbase + (uint32_t)(j * 32 * BK * 2));
       }
     }
   };

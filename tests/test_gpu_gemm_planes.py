@@ -42,6 +42,11 @@ PLANE_CASES = [
     (1000, 200, 200, False, False, "bf16"),     # edges: ragged M/N, K % 64 != 0
     (384, 384, 4096, True, False, "f32"),
     (130, 1030, 72, False, True, "f32"),
+    # token-split k-contiguous kernel (B one plane, K a multiple of 128):
+    # ragged M and N, bf16 output, split K, odd step counts
+    (1000, 264, 384, False, False, "bf16"),
+    (136, 100, 1280, True, False, "f32"),
+    (4096, 384, 640, True, False, "f32"),
 ]
 
 
@@ -129,17 +134,26 @@ def test_gemm_planes_tn_row_layout(api, lib, M, N, K, sx, sy):
         assert rel(C.host(), C2.host()) < 1e-6
 
 
-def test_gemm_planes_accumulate(api, lib):
-    rng = np.random.default_rng(11)
-    M, N, K = 384, 384, 4096
-    A = O.round_to(rng.normal(0, 1, (M, K)), "bf16")
+@pytest.mark.parametrize("M,N,K,split_b", [(384, 384, 4096, True), (4096, 384, 2048, False), (256, 384, 4096, False)])
+def test_gemm_planes_accumulate(api, lib, M, N, K, split_b):
+    """C += A B^T with a split B (k_gemm_fast) or a split A (the token-split
+    k-contiguous kernel, unsplit and split-K)."""
+    rng = np.random.default_rng(11 + M)
+    A = rng.normal(0, 1, (M, K)).astype(np.float32).astype(np.float64)
     B = rng.normal(0, 1, (N, K)).astype(np.float32).astype(np.float64)
-    bh, bl = split(B)
+    if split_b:
+        A = O.round_to(A, "bf16")
+        ah, al = A, None
+        bh, bl = split(B)
+    else:
+        B = O.round_to(B, "bf16")
+        ah, al = split(A)
+        bh, bl = B, None
     C0 = rng.normal(0, 1, (M, N)).astype(np.float32).astype(np.float64)
     C = dev(C0)
     ws = empty(max(lib.sj_gemm_planes_workspace_bytes(M, N, K), 256), "u8")
-    api.sj_gemm_planes(None, M, N, K, dev(A, "bf16").p, None, K, dev(bh, "bf16").p, dev(bl, "bf16").p, K, C.p, F32, N, 1,
-                       ws.p, ws.nbytes)
+    api.sj_gemm_planes(None, M, N, K, dev(ah, "bf16").p, dev(al, "bf16").p if al is not None else None, K,
+                       dev(bh, "bf16").p, dev(bl, "bf16").p if bl is not None else None, K, C.p, F32, N, 1, ws.p, ws.nbytes)
     sync()
     assert rel(C.host(), (C0 + O.matmul(A, B, 0, 1)).ravel()) < 3e-5
 
