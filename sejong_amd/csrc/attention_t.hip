@@ -184,6 +184,30 @@ struct TArgs {
 // DMA of one 64 x 64 bf16 tile (rows r of `src` with stride ld, 8 chunks of
 // 16 bytes each): wave w moves rows 16w .. 16w+15 (two instructions).
 // valid(r) false -> zeros.
+// a pointer every lane holds alike, as a scalar value (the divergence
+// analysis cannot always prove it)
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const unsigned long long v = (unsigned long long)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(uintptr_t)(((unsigned long long)hi << 32) | lo);
+}
+// dma_tile with every row valid: a uniform base (the tile's first row) plus
+// a fixed 32-bit byte offset per lane, no vector address arithmetic
+__device__ __forceinline__ void dma_tile_all(const bf16_t* src, long ld, uint32_t lds_tile, int wave, int lane) {
+  const uint8_t* bs = uniform_ptr(src);
+  const int rl = lane >> 3;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int r0 = wave * 16 + 8 * k;
+    const int r = r0 + rl;
+    const int ch = (lane & 7) ^ sw(r);  // LDS slot lane & 7 of row r holds source chunk ch
+    const uint32_t off = (uint32_t)((r * ld + ch * 8) * 2);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:0" ::"v"(off), "s"(bs),
+                 "s"(lds_tile + (uint32_t)(r0 * 128))
+                 : "memory", "m0");
+  }
+}
+
 template <typename Valid>
 __device__ __forceinline__ void dma_tile(const bf16_t* src, long ld, uint32_t lds_tile, int wave, int lane,
                                          Valid valid) {
@@ -264,8 +288,8 @@ __device__ __forceinline__ void attn2_fwd_body(const TArgs& a, bf16_t* lds) {
       dma_tile(ksrc + (long)kb * QB * ldk, ldk, st, wave_s, lane, valid);
       dma_tile(vsrc + (long)kb * QB * ldk, ldk, st + TBYTES, wave_s, lane, valid);
     } else {
-      dma_tile(ksrc + (long)kb * QB * ldk, ldk, st, wave_s, lane, [](int) { return true; });
-      dma_tile(vsrc + (long)kb * QB * ldk, ldk, st + TBYTES, wave_s, lane, [](int) { return true; });
+      dma_tile_all(ksrc + (long)kb * QB * ldk, ldk, st, wave_s, lane);
+      dma_tile_all(vsrc + (long)kb * QB * ldk, ldk, st + TBYTES, wave_s, lane);
     }
   };
   f32x4 o[4];
@@ -425,8 +449,8 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
   auto issue = [&](int kb, int buf) {
     if (!dma) return;
     const uint32_t st = base + (uint32_t)(buf * 2 * TBYTES);
-    dma_tile(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
-    dma_tile(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile_all(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane);
+    dma_tile_all(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane);
   };
   f32x4 dq[4];
 #pragma unroll
@@ -549,9 +573,9 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
   auto issue = [&](int qb, int buf) {
     const uint32_t st = base + (uint32_t)(buf * SROW * 2);
     const long q0 = (long)qb * QB;
-    dma_tile(qsrc + q0 * a.ldqkv, a.ldqkv, st, wave_s, lane, [](int) { return true; });
-    dma_tile(dhsrc + q0 * a.lddo, a.lddo, st + TBYTES, wave_s, lane, [](int) { return true; });
-    dma_tile(dlsrc + q0 * a.lddo, a.lddo, st + 2 * TBYTES, wave_s, lane, [](int) { return true; });
+    dma_tile_all(qsrc + q0 * a.ldqkv, a.ldqkv, st, wave_s, lane);
+    dma_tile_all(dhsrc + q0 * a.lddo, a.lddo, st + TBYTES, wave_s, lane);
+    dma_tile_all(dlsrc + q0 * a.lddo, a.lddo, st + 2 * TBYTES, wave_s, lane);
     if (wave_s == 0) {  // LSE (lanes 0-15) and Delta (16-31) of the block's 64 queries
       const void* s = lane < 16 ? (const void*)(lsesrc + q0 + 4 * lane)
                                 : lane < 32 ? (const void*)(dlsrc2 + q0 + 4 * (lane - 16)) : (const void*)g_zero_t;
@@ -601,11 +625,25 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
       const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        float p = fexp2(fmaf(st[r], sc, -lv[r] * LOG2E));
-        if (qb == kb && q4 + r < kloc) p = 0.f;
-        if (W > 0 && qb * QB + q4 + r > kb * QB + kloc + W - 1) p = 0.f;
+        const float p = fexp2(fmaf(st[r], sc, -lv[r] * LOG2E));
         pp[sb][r] = p;
         ds[sb][r] = p * (dp[r] - dv4[r]) * 0.125f;
+      }
+    }
+    // causal and window masks, only on the blocks that have masked pairs
+    // (uniform): a masked pair gets p = 0 and dS = 0 * (dP - Delta) / 8 (the
+    // sign of that zero follows dP - Delta, as ds * 0 keeps it)
+    if (qb == kb || (W > 0 && qb * QB + QB - 1 > kb * QB + W - 1)) {
+      asm volatile("");  // keeps the branch (not if-converted into selects on every block)
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++) {
+        const int q4 = 32 * (sb >> 1) + 8 * g + 4 * (sb & 1);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if ((qb == kb && q4 + r < kloc) || (W > 0 && qb * QB + q4 + r > kb * QB + kloc + W - 1)) {
+            pp[sb][r] = 0.f;
+            ds[sb][r] *= 0.f;
+          }
       }
     }
 #pragma unroll
