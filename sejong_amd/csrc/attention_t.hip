@@ -22,6 +22,8 @@
 // reduce of attention.hip sums in a fixed order (no atomics).
 #include <math.h>
 
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 using namespace sj;
@@ -888,6 +890,22 @@ static int check_t(const void* qkv, long ldqkv, long ldt, long batch, long t, lo
   return SJ_OK;
 }
 
+
+// One-kernel launch that, while an op is being profiled with kernel events
+// (sjh::ProfHook), records events at the kernel's own start and end, so the
+// kernel's time excludes any wait for CUs held by another stream's work
+template <typename K>
+void launch_timed(K kern, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, const TArgs& a) {
+  sjh::ProfHook& h = sjh::prof_hook();
+  if (h.on && h.k0) {
+    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, h.k0, h.k1, 0u, a);
+    h.used = true;
+  } else {
+    hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+  }
+  if (h.on) snprintf(h.kernel, sizeof(h.kernel), "%s", name);
+}
+
 extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv, long ldt, long batch, long t,
                                    long hq, long hk, long head_dim, long window, uint16_t* o, long ldo, float* lse,
                                    float* lse_t, uint16_t* o_t, long ldot) {
@@ -899,8 +917,8 @@ extern "C" int sj_attention_fwd_tt(void* stream, const uint16_t* qkv, long ldqkv
   a.qkv = (const bf16_t*)qkv; a.ldqkv = ldqkv; a.ldt = ldt;
   a.T = (int)t; a.HQ = (int)hq; a.HK = (int)hk; a.window = window < t ? (int)window : 0;
   a.o = (bf16_t*)o; a.ldo = ldo; a.lse = lse; a.lse_t = lse_t; a.ot = (bf16_t*)o_t; a.ldot = ldot;
-  hipLaunchKernelGGL(k_attn2_fwd<NS_FWD>, dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch), dim3(256), LDS_FWD,
-                     (hipStream_t)stream, a);
+  launch_timed(k_attn2_fwd<NS_FWD>, "k_attn2_fwd<3>", dim3((unsigned)(t / QB), (unsigned)hq, (unsigned)batch),
+               dim3(256), LDS_FWD, (hipStream_t)stream, a);
   SJ_LAUNCH_CHECK("hierarchy_attention");
   return SJ_OK;
 }
@@ -967,8 +985,8 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   const long nb = t / QB;
   const bool grouped = sjh::attention_bwd_grouped(batch, t, hq, hk, g_t_hi != nullptr);
   if ((parts & 2) && grouped) {
-    hipLaunchKernelGGL(k_attn2_bwd_g<GROUPED_G>, dim3((unsigned)(2 * nb), (unsigned)hk, (unsigned)batch),
-                       dim3(256 * GROUPED_G), LDS_BWD_G, s, a);
+    launch_timed(k_attn2_bwd_g<GROUPED_G>, "k_attn2_bwd_g<3>", dim3((unsigned)(2 * nb), (unsigned)hk, (unsigned)batch),
+                 dim3(256 * GROUPED_G), LDS_BWD_G, s, a);
     SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv (grouped)");
     return SJ_OK;  // dK | dV planes written: nothing for the reduce part
   }

@@ -255,7 +255,8 @@ def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
     own start and end: the
     parameters after two profiled steps equal those of two plain steps
     bit for bit, every GEMM op reports a "#kernel" aggregate no longer than
-    the op and names a k_gemm_fast instantiation, other ops name none."""
+    the op and names its GEMM kernel (the attention ops: their attention
+    kernel), other ops name none."""
     from sejong_amd.model import Model, byte_batch, config, init_params
     from sejong_amd.rng import Rng
     mc, tc = config("cfg2")
@@ -287,8 +288,12 @@ def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
         kms, kcalls = agg[op + "#kernel"]
         assert calls == kcalls == 2 * mc.layers, (op, calls, kcalls)
         assert 0 < kms <= ms, (op, kms, ms)
-        assert kern[op].startswith("k_gemm_fast<") and kern[op] == kern[op + "#kernel"], (op, kern[op])
-    for op in ("attention_fwd", "rmsnorm", "adamw"):
+        assert kern[op].startswith(("k_gemm_fast<", "k_gemm_kw<")) and kern[op] == kern[op + "#kernel"], (op, kern[op])
+    # the attention kernels time themselves the same way; other ops name no kernel
+    for op, name in (("attention_fwd", "k_attn2_fwd<3>"), ("attention_bwd_dq_dkv", "k_attn2_bwd_g<3>")):
+        assert op in agg and op + "#kernel" in agg and kern[op] == name, (op, kern.get(op))
+        assert 0 < agg[op + "#kernel"][0] <= agg[op][0], op
+    for op in ("rmsnorm", "adamw"):
         assert op in agg and kern[op] == "", (op, kern.get(op))
 
 
