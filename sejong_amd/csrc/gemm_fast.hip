@@ -1050,7 +1050,33 @@ __global__ __launch_bounds__(256) void k_reduce_partials(const float* __restrict
                                                          void* c, long ldc, int c_bf16, int accumulate, double* sq) {
   const long total = M * N;
   double q = 0.0;
-  for (long i = blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
+  // contiguous C (ldc == N) with 16-byte partials and 16- (fp32) or 8-byte
+  // (bf16) aligned C: four elements per step at the partials' own index
+  // (uniform; the same additions, in slice order from +0, as below)
+  const bool vec = ldc == N && total % 4 == 0 && ((uintptr_t)partial & 15) == 0 &&
+                   ((uintptr_t)c & (c_bf16 ? 7 : 15)) == 0;
+  if (vec) {
+    const long total4 = total / 4;
+    const float4* p4 = (const float4*)partial;
+    for (long t = blockIdx.x * 256L + threadIdx.x; t < total4; t += (long)gridDim.x * 256L) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int z = 0; z < splits; z++) {
+        const float4 v = p4[(long)z * total4 + t];
+        s += f32x4{v.x, v.y, v.z, v.w};
+      }
+      if (c_bf16) {
+        ((u32x2*)c)[t] = u32x2{pack2(f2bf(s[0]), f2bf(s[1])), pack2(f2bf(s[2]), f2bf(s[3]))};
+      } else {
+        if (accumulate) {
+          const float4 o = ((const float4*)c)[t];
+          s += f32x4{o.x, o.y, o.z, o.w};
+        }
+        ((float4*)c)[t] = make_float4(s[0], s[1], s[2], s[3]);
+      }
+      if (sq) q += (double)s[0] * s[0] + (double)s[1] * s[1] + (double)s[2] * s[2] + (double)s[3] * s[3];
+    }
+  }
+  for (long i = vec ? total : blockIdx.x * 256L + threadIdx.x; i < total; i += (long)gridDim.x * 256L) {
     float s = 0.f;
     for (int z = 0; z < splits; z++) s += partial[(long)z * total + i];
     const long m = i / N, n = i - m * N;
@@ -1468,7 +1494,10 @@ namespace {
 // slots when the hook is armed)
 int reduce_partials(hipStream_t s, const FParams& p, int splits, void* workspace) {
   const long M = p.M, N = p.N;
-  long total = M * N, blocks = (total + 255) / 256;
+  // the kernel's 16-byte path (same condition) takes four elements a thread
+  const bool vec = p.ldc[0] == N && (M * N) % 4 == 0 && ((uintptr_t)workspace & 15) == 0 &&
+                   ((uintptr_t)p.c[0] & (p.c_bf16 ? 7 : 15)) == 0;
+  long total = M * N, blocks = (total + (vec ? 1023 : 255)) / (vec ? 1024 : 256);
   double* sq = nullptr;
   sjh::GradSq& gs = sjh::grad_sq();
   if (gs.base && gs.on) {  // gradient-norm slots: fewer, longer workgroups
