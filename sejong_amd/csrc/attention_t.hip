@@ -484,13 +484,21 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
         dp = mfma(vf, dlf[c], dp);
       }
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float p = fexp2(fmaf(st[r], sc, -lse2));
-        const int kk = 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r;
-        if (kb == qb && kk > qloc) p = 0.f;
-        if (low_edge_possible && kb * QB + kk < myq - W + 1) p = 0.f;
-        ds[sb][r] = p * (dp[r] - delta) * 0.125f;
-      }
+      for (int r = 0; r < 4; r++) ds[sb][r] = fexp2(fmaf(st[r], sc, -lse2)) * (dp[r] - delta);
+    }
+    // causal and window masks only on the key blocks that can hold masked
+    // pairs (uniform); a masked pair's dS is 0 * (dP - Delta), as ds * 0
+    // gives it (the 1/8 of dS = P (dP - Delta) / 8 is applied to dQ after
+    // the loop: a power of two, so the planes and sums scale exactly)
+    if (kb == qb || (low_edge_possible && kb * QB < qb * QB + QB - 1 - W + 1)) {
+      asm volatile("");  // keeps the branch (not if-converted into selects on every block)
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int kk = 32 * (sb >> 1) + 8 * g + 4 * (sb & 1) + r;
+          if ((kb == qb && kk > qloc) || (low_edge_possible && kb * QB + kk < myq - W + 1)) ds[sb][r] *= 0.f;
+        }
     }
 #pragma unroll
     for (int c = 0; c < 2; c++) {
@@ -506,6 +514,8 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
       }
     }
   }
+#pragma unroll
+  for (int d = 0; d < 4; d++) dq[d] *= 0.125f;  // dS's 1/8 (1/sqrt(head_dim))
   // lane holds dQ^T[16d + 4g + r][query]: inverse RoPE on the pairs (r, r^1),
   // then hi/lo planes, normal (4 consecutive columns) and transposed
   const int pos = myq;
@@ -629,7 +639,7 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
       for (int r = 0; r < 4; r++) {
         const float p = fexp2(fmaf(st[r], sc, -lv[r] * LOG2E));
         pp[sb][r] = p;
-        ds[sb][r] = p * (dp[r] - dv4[r]) * 0.125f;
+        ds[sb][r] = p * (dp[r] - dv4[r]);  // the 1/8 is applied to dK after the loop
       }
     }
     // causal and window masks, only on the blocks that have masked pairs
@@ -669,6 +679,8 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
       }
     }
   }
+#pragma unroll
+  for (int d = 0; d < 4; d++) dk[d] *= 0.125f;  // dS's 1/8 (1/sqrt(head_dim)): a power of two, exact
 }
 
 // Workgroup (key block, query head, batch): this head's dK | dV share, fp32,
