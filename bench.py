@@ -268,6 +268,8 @@ def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config):
         e["work"] += work * calls
         e["ops"].append(op)
     total = sum(e["ms"] for e in per.values())
+    top = sorted(per.items(), key=lambda kv: -kv[1]["ms"])[:8]
+    log("  kernel time per launch: " + ", ".join(f"{k} {v['ms'] * 1e3 / v['calls']:.2f} us" for k, v in top))
     kern, e = max(per.items(), key=lambda kv: kv[1]["ms"])
     flop = e["kind"] == "flop"
     peak = PEAK_BF16_TFLOPS if flop else PEAK_HBM_GBS

@@ -149,6 +149,7 @@ SIGNATURES = {
     "sj_attention_bwd_tt_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
     "sj_attention_bwd_tt": (_I, [_P, _P, _L, _L, _P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P,
                                  _P, _P, _L, _P, _P, _L, _P, _S]),
+    "sj_attention_bwd_plan": (_I, [_L, _L, _L, _I, _P, _L, _P]),
     "sj_gemm_planes_tn": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
     "sj_moe_gemm_dw_tn": (_I, [_P, _P, _L, _L, _L, _L, _P, _L, _P, _P, _L, _P, _L, _L]),
     "sj_gemm_planes_split_out": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _P, _L, _P, _P, _L, _P, _L, _P, _L]),
@@ -223,7 +224,9 @@ SIGNATURES = {
     "sj_model_buffer": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(_L)]),
 }
 
-STATUS_FUNCS = {n for n, (r, _) in SIGNATURES.items() if r is _I and n not in ("sj_status_string",)}
+# functions whose int result is a status (sj_attention_bwd_plan returns a count)
+STATUS_FUNCS = {n for n, (r, _) in SIGNATURES.items()
+                if r is _I and n not in ("sj_status_string", "sj_attention_bwd_plan")}
 
 _lib = None
 

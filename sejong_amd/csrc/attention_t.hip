@@ -21,6 +21,15 @@
 // Q^T dS and dV^T = dO^T P into fp32 per-head partials that the group
 // reduce of attention.hip sums in a fixed order (no atomics).
 #include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
 
 #include <hip/hip_ext.h>
 
@@ -422,8 +431,24 @@ __global__ __launch_bounds__(256) void k_attn2_fwd_cached(TArgs a) {
 // wl: this wave's 16-query slice (0..3) of the block; dma: whether this wave
 // takes part in staging K | V (the grouped launch shares one copy among the
 // query heads of a KV head)
+// first key block a query of block qb sees (window: keys pos - W + 1 .. pos)
+__device__ __forceinline__ int dq_first_kb(int qb, int W) {
+  return W > 0 && qb * QB - W + 1 > 0 ? (qb * QB - W + 1) / QB : 0;
+}
+// one past the last query block that sees a key of block kb
+__device__ __forceinline__ int dkv_end_qb(int kb, int T, int W) {
+  int nqb = T / QB;
+  if (W > 0 && (kb * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (kb * QB + QB - 1 + W - 1) / QB + 1;
+  return nqb;
+}
+
+// dQ^T of query head h, query block qb, over key blocks klo .. khi (a whole
+// walk is dq_first_kb(qb) .. qb): lane (j, g) of slice wl leaves dQ^T[16d +
+// 4g + r][query 16 wl + j] in dq (before dS's 1/8).  dma: this wave issues
+// the K | V stages (one group of waves stages them for all groups).
 template <int NS>
-__device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, int h, int b, int wl, bool dma) {
+__device__ __forceinline__ void attn2_dq_walk(const TArgs& a, bf16_t* lds, int qb, int h, int b, int wl, bool dma,
+                                              int klo, int khi, f32x4 (&dq)[4]) {
   const int lane = threadIdx.x & 63, wave = wl;
   const int wave_s = __builtin_amdgcn_readfirstlane(wl);
   const int g = lane >> 4, j = lane & 15;
@@ -454,21 +479,19 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
     dma_tile_all(ksrc + (long)kb * QB * a.ldqkv, a.ldqkv, st, wave_s, lane);
     dma_tile_all(vsrc + (long)kb * QB * a.ldqkv, a.ldqkv, st + TBYTES, wave_s, lane);
   };
-  f32x4 dq[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) dq[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int W = a.window;
-  const int kb0 = W > 0 && qb * QB - W + 1 > 0 ? (qb * QB - W + 1) / QB : 0;
   const bool low_edge_possible = W > 0;
   wait_vm<0>();
 #pragma unroll
   for (int s = 0; s < NS - 1; s++)
-    if (kb0 + s <= qb) issue(kb0 + s, s);
-  for (int kb = kb0; kb <= qb; kb++) {
-    const int it = kb - kb0;
-    wait_stages<4, NS - 2>(min(NS - 2, qb - kb));
+    if (klo + s <= khi) issue(klo + s, s);
+  for (int kb = klo; kb <= khi; kb++) {
+    const int it = kb - klo;
+    wait_stages<4, NS - 2>(min(NS - 2, khi - kb));
     block_barrier();
-    if (kb + NS - 1 <= qb) issue(kb + NS - 1, (it + NS - 1) % NS);
+    if (kb + NS - 1 <= khi) issue(kb + NS - 1, (it + NS - 1) % NS);
     const bf16_t* sK = lds + (it % NS) * 2 * TILE;
     const bf16_t* sV = sK + TILE;
     float ds[4][4];
@@ -514,11 +537,18 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
       }
     }
   }
+}
+
+// dQ of query head h, query block qb from the walk's dQ^T (slice wl): dS's
+// 1/8 (1/sqrt(head_dim), a power of two: exact), the inverse RoPE on the
+// pairs (r, r^1), then hi / lo planes, normal (4 consecutive columns) and
+// transposed
+__device__ __forceinline__ void attn2_dq_store(const TArgs& a, int qb, int h, int b, int wl, f32x4 (&dq)[4]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
+  const int myq = qb * QB + wl * 16 + j;
+  const long qrow = (long)b * a.T + myq;
 #pragma unroll
-  for (int d = 0; d < 4; d++) dq[d] *= 0.125f;  // dS's 1/8 (1/sqrt(head_dim))
-  // lane holds dQ^T[16d + 4g + r][query]: inverse RoPE on the pairs (r, r^1),
-  // then hi/lo planes, normal (4 consecutive columns) and transposed
-  const int pos = myq;
+  for (int d = 0; d < 4; d++) dq[d] *= 0.125f;
 #pragma unroll
   for (int d = 0; d < 4; d++) {
     float v[4] = {dq[d][0], dq[d][1], dq[d][2], dq[d][3]};
@@ -526,10 +556,10 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
 #pragma unroll
       for (int pr = 0; pr < 2; pr++) {
         const int col = 16 * d + 4 * g + 2 * pr;
-        const float2 cs = *(const float2*)(a.rope + 2 * (pos * (DH / 2) + (col >> 1)));
+        const float2 c = *(const float2*)(a.rope + 2 * ((long)myq * (DH / 2) + (col >> 1)));
         const float x = v[2 * pr], y = v[2 * pr + 1];
-        v[2 * pr] = x * cs.x + y * cs.y;
-        v[2 * pr + 1] = y * cs.x - x * cs.y;
+        v[2 * pr] = x * c.x + y * c.y;
+        v[2 * pr + 1] = y * c.x - x * c.y;
       }
     }
     const uint32_t h01 = cvt2(v[0], v[1]), h23 = cvt2(v[2], v[3]);
@@ -549,17 +579,26 @@ __device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, in
   }
 }
 
+// dQ of query head h, query block qb: the whole walk, then the planes
+template <int NS>
+__device__ __forceinline__ void attn2_dq(const TArgs& a, bf16_t* lds, int qb, int h, int b, int wl, bool dma) {
+  f32x4 dq[4];
+  attn2_dq_walk<NS>(a, lds, qb, h, b, wl, dma, dq_first_kb(qb, a.window), qb, dq);
+  attn2_dq_store(a, qb, h, b, wl, dq);
+}
+
 // ------------------------------------------------------------ backward dKV
 // A stage holds the query block's Q and dO planes in row orientation only:
 // the products that need them transposed (dV^T = dO^T P, dK^T = Q^T dS) read
 // their fragments with LDS transpose reads.
 constexpr int SROW = 3 * TILE + 512;  // dK/dV stage size in bf16 elements (+1 KB of LSE / Delta)
 
-// The dK / dV accumulation of head h over its query blocks for the 16 keys
-// of slice wl (0..3) of key block kb; lds: NST x [Q | dOh | dOl | LSE,Delta]
-// of this head.  Leaves dK^T / dV^T [16d + 4g + r][key] in dk / dv.
-__device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int kb, int h, int b, int wl,
-                                               f32x4 (&dk)[4], f32x4 (&dv)[4]) {
+// The dK / dV accumulation of head h over query blocks qlo .. qhi (a whole
+// walk is kb .. dkv_end_qb(kb) - 1) for the 16 keys of slice wl (0..3) of
+// key block kb; lds: NST x [Q | dOh | dOl | LSE,Delta] of this head.  Leaves
+// dK^T / dV^T [16d + 4g + r][key] in dk / dv.
+__device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int kb, int h, int b, int wl, int qlo,
+                                               int qhi, f32x4 (&dk)[4], f32x4 (&dv)[4]) {
   const int lane = threadIdx.x & 63, wave = wl;
   const int wave_s = __builtin_amdgcn_readfirstlane(wl);
   const int g = lane >> 4, j = lane & 15;
@@ -596,16 +635,15 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
   };
 #pragma unroll
   for (int d = 0; d < 4; d++) dk[d] = dv[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // last query block that sees a key of this block (window: queries key .. key+window-1)
   const int W = a.window;
-  int nqb = T / QB;
-  if (W > 0 && (kb * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (kb * QB + QB - 1 + W - 1) / QB + 1;
-  wait_vm<0>();
+  const int nqb = qhi + 1;
+  // no wait for the fragment loads above: vector memory operations count
+  // down in issue order, so the first stage's wait covers them too
 #pragma unroll
   for (int s = 0; s < NST - 1; s++)
-    if (kb + s < nqb) issue(kb + s, s);
-  for (int qb = kb; qb < nqb; qb++) {
-    const int it = qb - kb;
+    if (qlo + s < nqb) issue(qlo + s, s);
+  for (int qb = qlo; qb < nqb; qb++) {
+    const int it = qb - qlo;
     if (qb + 1 < nqb) {
       // a stage is 6 DMA instructions per wave (7 on wave 0): leave the
       // NST - 2 later stages in flight
@@ -688,7 +726,7 @@ __device__ __forceinline__ void attn2_dkv_core(const TArgs& a, bf16_t* lds, int 
 __device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, int h, int b) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
   f32x4 dk[4], dv[4];
-  attn2_dkv_core(a, lds, kb, h, b, wave, dk, dv);
+  attn2_dkv_core(a, lds, kb, h, b, wave, kb, dkv_end_qb(kb, a.T, a.window) - 1, dk, dv);
   const int T = a.T, NK = a.HK * DH;
   const int group = a.HQ / a.HK;
   const int kvh = h / group, gi = h % group;
@@ -763,86 +801,215 @@ __global__ __launch_bounds__(256) SJ_BWD_OCC void k_attn2_bwd_dkv(TArgs a) {
   attn2_dkv(a, lds, wm.r, wm.h, wm.b);
 }
 
-// ------------------------------------------ grouped backward (no partials)
-// Both roles per KV head instead of per query head: a workgroup of G x 4
-// waves holds the G query heads of KV head kvh (group gi of four waves:
-// query head kvh * G + gi).  Role 0 (dQ of a query block): each group forms
-// its head's dQ from K | V stages that group 0 alone stages for all G.
-// Role 1 (dK | dV of a key block): each group accumulates its head's share
-// over its own Q / dO stages; the groups then add their shares through LDS
-// in head order, ((0 + h0) + h1) + h2 as the group reduce sums the fp32
-// partials, and group 0 applies the inverse RoPE to dK and writes the hi / lo
-// planes.  No per-head partials leave the workgroup and no reduce pass
-// follows.  G x NST stages of dK/dV operands: G <= 3 fits the LDS.
-template <int G>
-__global__ __launch_bounds__(256 * G) SJ_BWD_OCC void k_attn2_bwd_g(TArgs a) {
-  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
-  const int nb = (int)(gridDim.x >> 1);
-  const WgMap wm = wg_map(2);
-  const int w = threadIdx.x >> 6, gi = w >> 2, wl = w & 3;
-  const int lane = threadIdx.x & 63, g = lane >> 4, j = lane & 15;
-  const int kvh = wm.h, h = kvh * G + gi;
-  if (wm.role == 0) {
-    attn2_dq<NS_DQ>(a, lds, nb - 1 - wm.r, h, wm.b, wl, gi == 0);
-    return;
-  }
-  const int kb = wm.r;
-  f32x4 dk[4], dv[4];
-  attn2_dkv_core(a, lds + gi * NST * SROW, kb, h, wm.b, wl, dk, dv);
-  block_barrier();  // every group is done reading its stages
-  // group q > 0 leaves vector v (dk 0..3, dv 0..3) of lane L of slice wl at
-  // f32x4 index ((q - 1) * 8 + v) * 256 + wl * 64 + L
-  f32x4* sh = (f32x4*)lds;
-  const int slot = wl * 64 + lane;
-  if (gi > 0) {
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-      sh[((gi - 1) * 8 + d) * 256 + slot] = dk[d];
-      sh[((gi - 1) * 8 + 4 + d) * 256 + slot] = dv[d];
-    }
-  }
-  block_barrier();
-  if (gi != 0) return;
-  const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
-  const int kloc = wl * 16 + j, pos = kb * QB + kloc;
-  const long krow = (long)wm.b * T + pos;
-#pragma unroll
-  for (int half = 0; half < 2; half++) {  // dK, then dV
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float s = 0.f;
-        s += half ? dv[d][r] : dk[d][r];
-#pragma unroll
-        for (int q = 1; q < G; q++) s += sh[((q - 1) * 8 + 4 * half + d) * 256 + slot][r];
-        v[r] = s;
-      }
-      if (half == 0 && a.rope) {  // inverse RoPE on dK's pairs (columns 16d + 4g + 2pr, +1)
-#pragma unroll
-        for (int pr = 0; pr < 2; pr++) {
-          const int col = 16 * d + 4 * g + 2 * pr;
-          const float2 cs = *(const float2*)(a.rope + 2 * ((long)pos * (DH / 2) + (col >> 1)));
-          const float x = v[2 * pr], y = v[2 * pr + 1];
-          v[2 * pr] = x * cs.x + y * cs.y;
-          v[2 * pr + 1] = y * cs.x - x * cs.y;
-        }
-      }
-      bf16_t hv[4], lv[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
-      const long col = NQ + half * NK + kvh * DH + 16 * d + 4 * g;
-      *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
-      *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
-    }
-  }
-}
 constexpr int GROUPED_G = 3;  // query heads per KV head of the grouped launch
 constexpr size_t LDS_BWD_G = (size_t)GROUPED_G * NST * SROW * 2 > (size_t)NS_DQ * 2 * TBYTES
                                  ? (size_t)GROUPED_G * NST * SROW * 2
                                  : (size_t)NS_DQ * 2 * TBYTES;
-static_assert(LDS_BWD_G <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 * 16 <= LDS_BWD_G, "grouped LDS budget");
+static_assert(LDS_BWD_G + 16 <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 * 16 <= LDS_BWD_G,
+              "grouped LDS budget (+ the meeting's count)");
+
+
+// ------------------------------------------ grouped backward (no partials)
+// Both roles per KV head instead of per query head: a workgroup of G x 4
+// waves holds the G query heads of KV head kvh (group gi of four waves:
+// query head kvh * G + gi).  A dQ walk (query block qb): each group forms
+// its head's dQ from K | V stages that group 0 alone stages for all G.  A
+// dK | dV walk (key block kb): each group accumulates its head's share over
+// its own Q / dO stages; the groups then add their shares through LDS in
+// head order, ((0 + h0) + h1) + h2 as the group reduce sums the fp32
+// partials, and group 0 applies the inverse RoPE to dK and writes the hi /
+// lo planes.  No per-head partials leave the workgroup and no reduce pass
+// follows.  G x NST stages of dK/dV operands: G <= 3 fits the LDS.
+//
+// Balanced pieces.  The causal walks are 1 .. nb blocks long (dQ of query
+// block qb: qb + 1 key blocks; dK | dV of key block kb: nb - kb query
+// blocks), so with one workgroup per walk a launch that fills the chip once
+// lasts as long as its longest walk, about twice the mean.  The host cuts
+// each role's walks longer than a cap into two parts (SplitPlan; a piece is
+// a whole walk or a part, one workgroup each, dispatched costliest first as
+// CUs free up) with the caps that finish a simulated dispatch first.  Each
+// part of a cut walk writes its fp32 sum (the groups' dQ^T, or the dK | dV
+// after the head sum) to its slot of the workspace and counts itself on the
+// walk's counter; the part that counts second adds the other part's sum to
+// its own (a + b: the same bits whichever part comes second), writes the
+// planes and sets the counter back to zero for the next launch.  (One piece
+// per workgroup: a workgroup that ran several pieces in a loop held their
+// addresses and arguments across the loop and ran every walk slower.)
+constexpr int PLAN_PIECES = 128;  // pieces of both roles: at most 4 t/64 (t <= 2048)
+constexpr int PLAN_POOLS = 8;     // counter pools, taken in turn by successive launches
+constexpr int PLAN_COUNTERS = 1024;  // counters per pool: cut walks of one launch
+// piece: bit 31 set, bits 0-5 block, 6-11 / 12-17 the first / last block of
+// the walk it covers, bit 18 the role (0: dQ, 1: dK | dV), 19-28 cut-walk
+// index + 1 (0: a whole walk), bit 29 the part of the cut walk
+struct SplitPlan {
+  int ncut;  // cut walks per (KV head, sequence)
+  int pool;  // counter pool of this launch
+  uint32_t seg[PLAN_PIECES];
+};
+__device__ uint32_t g_cut_count[PLAN_POOLS * PLAN_COUNTERS];  // zero between launches
+
+// A part's sum passes between workgroups (on different XCDs, each with its
+// own L2) through device-scope accesses, relaxed atomics at agent scope:
+// loads and stores coherent across the L2s by themselves, so the meeting
+// needs no device-scope fence (whose L2 write-back and invalidate cover the
+// whole L2 of the XCD: microseconds, and a cold L2 for the kernels beside).
+__device__ __forceinline__ void put4(float* p, f32x4 v) {
+#pragma unroll
+  for (int r = 0; r < 4; r++) __hip_atomic_store(p + r, v[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 get4(const float* p) {
+  f32x4 v;
+#pragma unroll
+  for (int r = 0; r < 4; r++) v[r] = __hip_atomic_load(p + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+
+// The two parts of a cut walk meet (every thread of the workgroup calls it,
+// after put4 of its share of this part's sum): true in the workgroup that
+// counts second, which may then get4 the other part's sum, and which sets
+// the counter back to zero.  The stores have completed (vmcnt 0) before the
+// barrier that precedes the count, and the other part's loads follow the
+// barrier that hands the count out.
+__device__ __forceinline__ bool meet_second(uint32_t* cnt, uint32_t* flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  block_barrier();
+  if (threadIdx.x == 0) *flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  block_barrier();
+  const uint32_t n = __builtin_amdgcn_readfirstlane(*flag);  // the barrier's memory clobber: read after it
+  if (n == 0) return false;
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// where the sums of cut walk `cut` of (sequence b, KV head kvh) meet:
+// this part's and the other part's slot (slot floats each), its counter
+struct Meet {
+  float *mine, *other;
+  uint32_t* cnt;
+};
+__device__ __forceinline__ Meet meet_at(const TArgs& a, const SplitPlan& pl, int b, int kvh, uint32_t sg, long slot) {
+  const int cut = (int)((sg >> 19) & 1023) - 1, part = (int)((sg >> 29) & 1);
+  const long c = ((long)b * a.HK + kvh) * pl.ncut + cut;
+  float* base = a.part + c * 2 * slot;
+  return Meet{base + part * slot, base + (1 - part) * slot, g_cut_count + pl.pool * PLAN_COUNTERS + c};
+}
+
+// One piece: a whole walk, or a part of a cut walk, of one role.
+template <int G, bool DQ>
+__device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& pl, bf16_t* lds, uint32_t sg, int kvh,
+                                              int b) {
+  constexpr int NT = 256 * G;  // threads
+  constexpr long SLOT = 16 * NT;  // floats of one part's sum (dQ^T: 16 per thread; dK | dV: 32 per group-0 thread)
+  static_assert(32 * 256 <= SLOT, "slot size");
+  uint32_t* s_count = (uint32_t*)((char*)lds + LDS_BWD_G);  // the meeting's count, past the stages
+  {
+    const int tid = (int)threadIdx.x;
+    const int w = tid >> 6, gi = __builtin_amdgcn_readfirstlane(w >> 2), wl = w & 3;
+    const int lane = tid & 63, g = lane >> 4, j = lane & 15;
+    const int h = kvh * G + gi;
+    const int blk = (int)(sg & 63), lo = (int)((sg >> 6) & 63), hi = (int)((sg >> 12) & 63);
+    const bool cut = ((sg >> 19) & 1023) != 0;
+    if constexpr (DQ) {
+      f32x4 dq[4];
+      attn2_dq_walk<NS_DQ>(a, lds, blk, h, b, wl, gi == 0, lo, hi, dq);
+      if (cut) {
+        const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
+#pragma unroll
+        for (int d = 0; d < 4; d++) put4(m.mine + 4 * (d * NT + tid), dq[d]);
+        if (!meet_second(m.cnt, s_count)) return;
+#pragma unroll
+        for (int d = 0; d < 4; d++) dq[d] = dq[d] + get4(m.other + 4 * (d * NT + tid));
+      }
+      attn2_dq_store(a, blk, h, b, wl, dq);
+    } else {
+      const int kb = blk;
+      f32x4 dk[4], dv[4];
+      attn2_dkv_core(a, lds + gi * NST * SROW, kb, h, b, wl, lo, hi, dk, dv);
+      const int pos = kb * QB + wl * 16 + j;
+      float2 cs[8];  // group 0: the inverse-RoPE (cos, sin) of dK columns 16d + 4g + 2pr, +1 (loaded before the exchange)
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        cs[i] = gi == 0 && a.rope
+                    ? *(const float2*)(a.rope + 2 * ((long)pos * (DH / 2) + ((16 * (i >> 1) + 4 * g + 2 * (i & 1)) >> 1)))
+                    : float2{0.f, 0.f};
+      block_barrier();  // every group is done reading its stages
+      // group q > 0 leaves vector v (dk 0..3, dv 0..3) of lane L of slice wl
+      // at f32x4 index ((q - 1) * 8 + v) * 256 + wl * 64 + L
+      f32x4* sh = (f32x4*)lds;
+      const int slot = wl * 64 + lane;
+      if (gi > 0) {
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          sh[((gi - 1) * 8 + d) * 256 + slot] = dk[d];
+          sh[((gi - 1) * 8 + 4 + d) * 256 + slot] = dv[d];
+        }
+      }
+      block_barrier();
+      f32x4 acc[8];  // group 0: dK^T (0..3), dV^T (4..7) summed over the heads
+      if (gi == 0) {
+#pragma unroll
+        for (int v = 0; v < 8; v++) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float s = 0.f;
+            s += v < 4 ? dk[v][r] : dv[v - 4][r];
+#pragma unroll
+            for (int q = 1; q < G; q++) s += sh[((q - 1) * 8 + v) * 256 + slot][r];
+            acc[v][r] = s;
+          }
+        }
+      }
+      if (cut) {
+        const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
+        if (gi == 0) {
+#pragma unroll
+          for (int v = 0; v < 8; v++) put4(m.mine + 4 * (v * 256 + slot), acc[v]);
+        }
+        if (!meet_second(m.cnt, s_count)) return;
+        if (gi == 0) {
+#pragma unroll
+          for (int v = 0; v < 8; v++) acc[v] = acc[v] + get4(m.other + 4 * (v * 256 + slot));
+        }
+      }
+      if (gi != 0) return;
+      const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
+      const long krow = (long)b * T + pos;
+#pragma unroll
+      for (int half = 0; half < 2; half++) {  // dK, then dV
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          float v[4] = {acc[4 * half + d][0], acc[4 * half + d][1], acc[4 * half + d][2], acc[4 * half + d][3]};
+          if (half == 0 && a.rope) {  // inverse RoPE on dK's pairs (columns 16d + 4g + 2pr, +1)
+#pragma unroll
+            for (int pr = 0; pr < 2; pr++) {
+              const float2 c = cs[2 * d + pr];
+              const float x = v[2 * pr], y = v[2 * pr + 1];
+              v[2 * pr] = x * c.x + y * c.y;
+              v[2 * pr + 1] = y * c.x - x * c.y;
+            }
+          }
+          bf16_t hv[4], lv[4];
+#pragma unroll
+          for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
+          const long col = NQ + half * NK + kvh * DH + 16 * d + 4 * g;
+          *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
+          *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
+        }
+      }
+    }
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(256 * G) SJ_BWD_OCC void k_attn2_bwd_g(TArgs a, SplitPlan pl) {
+  extern __shared__ __attribute__((aligned(16))) bf16_t lds[];
+  const WgMap wm = wg_map(1);
+  const uint32_t sg = pl.seg[wm.r];
+  if (!((sg >> 18) & 1))
+    grouped_piece<G, true>(a, pl, lds, sg, wm.h, wm.b);
+  else
+    grouped_piece<G, false>(a, pl, lds, sg, wm.h, wm.b);
+}
 
 constexpr long SEPARATE_ROLES = 2048;  // workgroups per role from which the roles launch separately
 
@@ -869,7 +1036,171 @@ static bool grouped_on() {
 }
 
 bool sjh::attention_bwd_grouped(long batch, long t, long hq, long hk, bool transposed) {
-  return hq == GROUPED_G * hk && !transposed && (t / QB) * hq * batch < SEPARATE_ROLES && grouped_on();
+  return hq == GROUPED_G * hk && !transposed && (t / QB) * hq * batch < SEPARATE_ROLES && 4 * (t / QB) <= PLAN_PIECES &&
+         grouped_on();
+}
+
+// ----------------------------------------------- pieces of the grouped backward
+namespace {
+struct Walk {  // one role's walk for block `block`: blocks first .. last of the other operand
+  int block, first, last;
+  int len() const { return last - first + 1; }
+};
+struct Piece {
+  int block, first, last, role, cut, part;  // cut -1: a whole walk
+  double cost;
+};
+
+// cost of a piece, microseconds per workgroup at the cfg2 shape on MI355X
+// (stamped workgroup start and end times): a dQ walk 5.0 + 1.85 per key
+// block, a dK | dV walk 6.6 + 2.9 per query block, a cut part's meeting 5
+// more (its sum written, counted and read at device scope)
+constexpr double DQ_START = 5.0, DQ_STEP = 1.85, KV_START = 6.6, KV_STEP = 2.9, PIECE_MEET = 5.0;
+
+// the walks of both roles for nb blocks and window W (0: causal)
+void role_walks(int nb, int W, std::vector<Walk>& wq, std::vector<Walk>& wk) {
+  for (int i = 0; i < nb; i++) {
+    const int kb0 = W > 0 && i * QB - W + 1 > 0 ? (i * QB - W + 1) / QB : 0;
+    int nqb = nb;
+    if (W > 0 && (i * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (i * QB + QB - 1 + W - 1) / QB + 1;
+    wq.push_back(Walk{i, kb0, i});
+    wk.push_back(Walk{i, i, nqb - 1});
+  }
+}
+
+// a role's walks as pieces: longer than cap -> cap | the rest (cut indices
+// from *ncut on); false if a walk is longer than 2 cap
+bool cut_walks(const std::vector<Walk>& ws, int role, int cap, std::vector<Piece>& out, int* ncut) {
+  const double start = role == 0 ? DQ_START : KV_START, step = role == 0 ? DQ_STEP : KV_STEP;
+  for (const Walk& w : ws) {
+    if (w.len() > cap) {
+      if (w.len() > 2 * cap) return false;
+      const int c = (*ncut)++;
+      out.push_back(Piece{w.block, w.first, w.first + cap - 1, role, c, 0, start + cap * step + PIECE_MEET});
+      out.push_back(Piece{w.block, w.first + cap, w.last, role, c, 1, start + (w.len() - cap) * step + PIECE_MEET});
+    } else {
+      out.push_back(Piece{w.block, w.first, w.last, role, -1, 0, start + w.len() * step});
+    }
+  }
+  return true;
+}
+
+// finish time of `pairs` copies of the pieces (costliest first, each copy
+// of a piece before the next piece: the launch's dispatch order) taken in
+// turn by the CU free first
+double simulate(std::vector<Piece>& ps, long pairs, int cus) {
+  std::stable_sort(ps.begin(), ps.end(), [](const Piece& x, const Piece& y) { return x.cost > y.cost; });
+  std::vector<double> cu((size_t)cus, 0.0);  // min-heap of free times
+  double end = 0;
+  for (const Piece& p : ps)
+    for (long i = 0; i < pairs; i++) {
+      std::pop_heap(cu.begin(), cu.end(), std::greater<double>());
+      cu.back() += p.cost;
+      end = std::max(end, cu.back());
+      std::push_heap(cu.begin(), cu.end(), std::greater<double>());
+    }
+  return end;
+}
+
+// The pieces of the launch: over every pair of caps (dQ, dK | dV), the one
+// whose simulated dispatch finishes first (ties: the longer caps, fewer
+// cuts), with at most nb cut walks per (KV head, sequence) -- their sums
+// fit the workspace of the per-head partials -- and at most PLAN_COUNTERS
+// for the launch.  cut = false: one piece per walk (the former launch).
+// caps_q / caps_k > 0 fix the caps.
+double plan_pieces(int nb, int W, long pairs, int cus, bool cut, int caps_q, int caps_k, std::vector<Piece>& best,
+                   int& ncut) {
+  std::vector<Walk> wq, wk;
+  role_walks(nb, W, wq, wk);
+  int maxq = 0, maxk = 0;
+  for (const Walk& w : wq) maxq = std::max(maxq, w.len());
+  for (const Walk& w : wk) maxk = std::max(maxk, w.len());
+  double best_t = -1;
+  for (int cq = maxq; cq >= 1; cq--)
+    for (int ck = maxk; ck >= 1; ck--) {
+      if (!cut && (cq != maxq || ck != maxk)) continue;
+      if (caps_q > 0 && cq != std::min(caps_q, maxq)) continue;
+      if (caps_k > 0 && ck != std::min(caps_k, maxk)) continue;
+      std::vector<Piece> ps;
+      int nc = 0;
+      if (!cut_walks(wq, 0, cq, ps, &nc) || !cut_walks(wk, 1, ck, ps, &nc)) continue;
+      if (nc > nb || (long)nc * pairs > PLAN_COUNTERS) continue;
+      const double t = simulate(ps, pairs, cus);
+      if (best_t < 0 || t < best_t - 1e-9) {
+        best_t = t;
+        best = ps;
+        ncut = nc;
+      }
+    }
+  if (best_t < 0) return plan_pieces(nb, W, pairs, cus, false, 0, 0, best, ncut);
+  return best_t;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e ? atoi(e) : dflt;
+}
+
+int device_cus() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0, cu = 0;
+    n = hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cu > 0
+            ? cu
+            : 256;
+  }
+  return n;
+}
+
+// The launch's plan for `pairs` (KV head, sequence) pairs on `cus` CUs,
+// searched once per shape (the search simulates every pair of caps) and
+// kept; each launch takes the next counter pool.  SJ_ATTN_CUT=0: one piece
+// per walk (A/B comparisons); SJ_ATTN_CAPS_Q / SJ_ATTN_CAPS_K fix the caps.
+int make_plan(long t, long window, long pairs, int cus, SplitPlan& pl, int& npieces) {
+  static const int cut_on = env_int("SJ_ATTN_CUT", 1), cq = env_int("SJ_ATTN_CAPS_Q", 0),
+                   ck = env_int("SJ_ATTN_CAPS_K", 0);
+  static std::atomic<unsigned> next_pool{0};
+  static std::mutex mu;
+  static std::map<std::tuple<long, long, long, int>, std::pair<SplitPlan, int>> cache;
+  const int nb = (int)(t / QB);
+  if (4 * nb > PLAN_PIECES) return sjh::fail(SJ_ERR_INVALID, "grouped attention backward: t = %ld beyond the plan", t);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_tuple(t, window, pairs, cus);
+    auto it = cache.find(key);
+    if (it == cache.end()) {
+      std::vector<Piece> ps;
+      int ncut = 0;
+      plan_pieces(nb, (int)window, pairs, cus, cut_on != 0, cq, ck, ps, ncut);  // ps: costliest first
+      SplitPlan p;
+      memset(&p, 0, sizeof(p));
+      for (size_t i = 0; i < ps.size(); i++) {
+        const Piece& x = ps[i];
+        p.seg[i] = (1u << 31) | (uint32_t)x.block | ((uint32_t)x.first << 6) | ((uint32_t)x.last << 12) |
+                   ((uint32_t)x.role << 18) | ((uint32_t)(x.cut + 1) << 19) | ((uint32_t)x.part << 29);
+      }
+      p.ncut = ncut;
+      it = cache.emplace(key, std::make_pair(p, (int)ps.size())).first;
+    }
+    pl = it->second.first;
+    npieces = it->second.second;
+  }
+  pl.pool = (int)(next_pool.fetch_add(1) % PLAN_POOLS);
+  return SJ_OK;
+}
+}  // namespace
+
+extern "C" int sj_attention_bwd_plan(long t, long window, long pairs, int cus, uint32_t* seg, long cap, int* ncut) {
+  if (!(t > 0 && t % QB == 0 && window >= 0 && pairs > 0 && cus > 0 && seg && ncut))
+    return -sjh::fail(SJ_ERR_INVALID, "attention backward plan: arguments");
+  SplitPlan pl;
+  int n = 0;
+  if (int st = make_plan(t, window < t ? window : 0, pairs, cus, pl, n)) return -st;
+  if (cap < n) return -sjh::fail(SJ_ERR_INVALID, "attention backward plan: capacity %ld < %d pieces", cap, n);
+  for (int i = 0; i < n; i++) seg[i] = pl.seg[i];
+  *ncut = pl.ncut;
+  return n;
 }
 
 int sjh::attention_t_prepare() {
@@ -888,7 +1219,7 @@ int sjh::attention_t_prepare() {
     e = hipFuncSetAttribute((const void*)k_attn2_bwd_dkv, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_DKV);
   if (e == hipSuccess)
     e = hipFuncSetAttribute((const void*)k_attn2_bwd_g<GROUPED_G>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)LDS_BWD_G);
+                            (int)(LDS_BWD_G + 16));
   status = e == hipSuccess ? SJ_OK : sjh::hip_check(e, "attention: LDS attribute");
   return status;
 }
@@ -906,14 +1237,14 @@ static int check_t(const void* qkv, long ldqkv, long ldt, long batch, long t, lo
 // One-kernel launch that, while an op is being profiled with kernel events
 // (sjh::ProfHook), records events at the kernel's own start and end, so the
 // kernel's time excludes any wait for CUs held by another stream's work
-template <typename K>
-void launch_timed(K kern, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, const TArgs& a) {
+template <typename K, typename... A>
+void launch_timed(K kern, const char* name, dim3 grid, dim3 block, size_t lds, hipStream_t s, const A&... args) {
   sjh::ProfHook& h = sjh::prof_hook();
   if (h.on && h.k0) {
-    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, h.k0, h.k1, 0u, a);
+    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, h.k0, h.k1, 0u, args...);
     h.used = true;
   } else {
-    hipLaunchKernelGGL(kern, grid, block, lds, s, a);
+    hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
   }
   if (h.on) snprintf(h.kernel, sizeof(h.kernel), "%s", name);
 }
@@ -997,8 +1328,11 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   const long nb = t / QB;
   const bool grouped = sjh::attention_bwd_grouped(batch, t, hq, hk, g_t_hi != nullptr);
   if ((parts & 2) && grouped) {
-    launch_timed(k_attn2_bwd_g<GROUPED_G>, "k_attn2_bwd_g<3>", dim3((unsigned)(2 * nb), (unsigned)hk, (unsigned)batch),
-                 dim3(256 * GROUPED_G), LDS_BWD_G, s, a);
+    SplitPlan pl;
+    int npieces = 0;
+    if (int st = make_plan(t, a.window, batch * hk, device_cus(), pl, npieces)) return st;
+    launch_timed(k_attn2_bwd_g<GROUPED_G>, "k_attn2_bwd_g<3>", dim3((unsigned)npieces, (unsigned)hk, (unsigned)batch),
+                 dim3(256 * GROUPED_G), LDS_BWD_G + 16, s, a, pl);
     SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv (grouped)");
     return SJ_OK;  // dK | dV planes written: nothing for the reduce part
   }

@@ -130,3 +130,98 @@ def test_noalloc_rejects_oversize_before_any_device_call():
     st = lib.sj_rmsnorm_bwd_p_noalloc(None, None, None, None, None, None, None, None, None, None, None, 0,
                                       16 * 1025, 1024, ctypes.c_float(1e-6))
     assert st == 2 and b"SJ_RMSNORM_BWD_NOALLOC_MAX_BYTES" in lib.sj_last_error()
+
+
+def _attention_plan(lib, t, window, pairs=16, cus=256):
+    import ctypes
+    seg = np.zeros(256, np.uint32)
+    ncut = ctypes.c_int(-1)
+    n = lib.sj_attention_bwd_plan(t, window, pairs, cus, seg.ctypes.data, seg.size, ctypes.byref(ncut))
+    pieces = []
+    for x in (int(v) for v in seg[:max(n, 0)]):
+        assert x >> 31
+        pieces.append(dict(block=x & 63, first=(x >> 6) & 63, last=(x >> 12) & 63, role=(x >> 18) & 1,
+                           cut=((x >> 19) & 1023) - 1, part=(x >> 29) & 1))
+    return n, ncut.value, pieces
+
+
+def _piece_us(p):
+    """Modelled workgroup time of a piece (the planner's per-walk start and
+    per-block costs, microseconds, and a cut part's meeting)."""
+    n = p["last"] - p["first"] + 1
+    return (5.0 + 1.85 * n if p["role"] == 0 else 6.6 + 2.9 * n) + (5.0 if p["cut"] >= 0 else 0.0)
+
+
+def _dispatch_finish(pieces, pairs, cus):
+    """Finish time of the launch's dispatch: pieces in order, each for every
+    pair, to the CU free first (the planner's model, restated)."""
+    import heapq
+    free = [0.0] * cus
+    end = 0.0
+    for p in pieces:
+        c = _piece_us(p)
+        for _ in range(pairs):
+            t = heapq.heappop(free) + c
+            end = max(end, t)
+            heapq.heappush(free, t)
+    return end
+
+
+@pytest.mark.parametrize("t,window,pairs", [(64, 0, 16), (128, 0, 16), (256, 0, 4), (320, 100, 1), (256, 128, 4),
+                                            (512, 0, 16), (512, 300, 16), (512, 64, 16), (1024, 0, 3),
+                                            (1024, 200, 8), (2048, 0, 2), (2048, 1000, 2), (512, 0, 64)])
+def test_attention_backward_pieces_cover_every_walk_once(t, window, pairs):
+    """The grouped attention backward's pieces (sj_attention_bwd_plan): every
+    causal walk of both roles (dQ of query block qb over its visible key
+    blocks, dK | dV of key block kb over the query blocks that see it, the
+    walks of the per-block kernels) is covered exactly once, by a whole piece
+    or by two parts that meet end to end, with distinct cut indices below
+    ncut <= t/64 (the workspace holds that many pairs of sums); pieces come
+    costliest first; and the chosen cuts finish the modelled dispatch no
+    later than no cuts at all (earlier at the cfg2 shape, where the longest
+    dK | dV walks are cut)."""
+    from sejong_amd import _native as N
+    lib = N.load()
+    nb_blocks = t // 64
+    W = window if window < t else 0
+    n, ncut, pieces = _attention_plan(lib, t, window, pairs)
+    assert 2 * nb_blocks <= n <= 4 * nb_blocks and 0 <= ncut <= nb_blocks
+    walks = {}
+    for i in range(nb_blocks):
+        kb0 = (i * 64 - W + 1) // 64 if W > 0 and i * 64 - W + 1 > 0 else 0
+        nqb = min(nb_blocks, (i * 64 + 63 + W - 1) // 64 + 1) if W > 0 else nb_blocks
+        walks[(0, i)] = (kb0, i)
+        walks[(1, i)] = (i, nqb - 1)
+    # brute-force check of the walk bounds: the blocks holding a visible pair
+    for (role, i), (lo, hi) in walks.items():
+        vis = []
+        for o in range(nb_blocks):
+            qb, kb = (i, o) if role == 0 else (o, i)
+            pairs_ = [(q, k) for q in range(qb * 64, qb * 64 + 64) for k in range(kb * 64, kb * 64 + 64, 7)]
+            pairs_ += [(q, kb * 64 + 63) for q in range(qb * 64, qb * 64 + 64)]
+            if any(k <= q and (W == 0 or k > q - W) for q, k in pairs_):
+                vis.append(o)
+        assert vis == list(range(lo, hi + 1)), (role, i, vis, lo, hi)
+    covered = {k: [] for k in walks}
+    cuts = {}
+    for p in pieces:
+        covered[(p["role"], p["block"])].append((p["first"], p["last"]))
+        if p["cut"] >= 0:
+            assert p["cut"] < ncut
+            cuts.setdefault(p["cut"], []).append((p["role"], p["block"], p["part"]))
+    for k, (lo, hi) in walks.items():
+        parts = sorted(covered[k])
+        assert parts[0][0] == lo and parts[-1][1] == hi and len(parts) <= 2, (k, parts)
+        for (a0, a1), (b0, b1) in zip(parts, parts[1:]):
+            assert b0 == a1 + 1, (k, parts)
+        assert all(a0 <= a1 for a0, a1 in parts)
+    assert sorted(cuts) == list(range(ncut))
+    for c, ps in cuts.items():
+        assert len(ps) == 2 and ps[0][:2] == ps[1][:2] and {p[2] for p in ps} == {0, 1}, (c, ps)
+    assert all(_piece_us(x) >= _piece_us(y) - 1e-12 for x, y in zip(pieces, pieces[1:]))
+    whole = sorted(({"role": r, "block": b, "first": lo, "last": hi, "cut": -1} for (r, b), (lo, hi) in walks.items()),
+                   key=lambda p: -_piece_us(p))
+    assert _dispatch_finish(pieces, pairs, 256) <= _dispatch_finish(whole, pairs, 256) + 1e-9
+    if (t, window, pairs) == (512, 0, 16):  # cfg2: the dK | dV walks of key blocks 0-3 cut, none of dQ
+        assert ncut == 4 and all(p["role"] == 1 for p in pieces if p["cut"] >= 0)
+        assert _dispatch_finish(pieces, pairs, 256) < 0.85 * _dispatch_finish(whole, pairs, 256)
