@@ -853,14 +853,17 @@ __device__ uint32_t g_cut_count[PLAN_POOLS * PLAN_COUNTERS];  // zero between la
 // loads and stores coherent across the L2s by themselves, so the meeting
 // needs no device-scope fence (whose L2 write-back and invalidate cover the
 // whole L2 of the XCD: microseconds, and a cold L2 for the kernels beside).
-__device__ __forceinline__ void put4(float* p, f32x4 v) {
+// Element r of a thread's vector sits at p[r * stride]: with p the thread's
+// index and stride the thread count, each store or load instruction of a
+// wave covers 256 consecutive bytes (whole cache lines, one request each).
+__device__ __forceinline__ void put4(float* p, long stride, f32x4 v) {
 #pragma unroll
-  for (int r = 0; r < 4; r++) __hip_atomic_store(p + r, v[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int r = 0; r < 4; r++) __hip_atomic_store(p + r * stride, v[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ f32x4 get4(const float* p) {
+__device__ __forceinline__ f32x4 get4(const float* p, long stride) {
   f32x4 v;
 #pragma unroll
-  for (int r = 0; r < 4; r++) v[r] = __hip_atomic_load(p + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int r = 0; r < 4; r++) v[r] = __hip_atomic_load(p + r * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return v;
 }
 
@@ -915,10 +918,10 @@ __device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& p
       if (cut) {
         const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
 #pragma unroll
-        for (int d = 0; d < 4; d++) put4(m.mine + 4 * (d * NT + tid), dq[d]);
+        for (int d = 0; d < 4; d++) put4(m.mine + 4 * d * NT + tid, NT, dq[d]);
         if (!meet_second(m.cnt, s_count)) return;
 #pragma unroll
-        for (int d = 0; d < 4; d++) dq[d] = dq[d] + get4(m.other + 4 * (d * NT + tid));
+        for (int d = 0; d < 4; d++) dq[d] = dq[d] + get4(m.other + 4 * d * NT + tid, NT);
       }
       attn2_dq_store(a, blk, h, b, wl, dq);
     } else {
@@ -963,12 +966,12 @@ __device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& p
         const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
         if (gi == 0) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) put4(m.mine + 4 * (v * 256 + slot), acc[v]);
+          for (int v = 0; v < 8; v++) put4(m.mine + 4 * v * 256 + slot, 256, acc[v]);
         }
         if (!meet_second(m.cnt, s_count)) return;
         if (gi == 0) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) acc[v] = acc[v] + get4(m.other + 4 * (v * 256 + slot));
+          for (int v = 0; v < 8; v++) acc[v] = acc[v] + get4(m.other + 4 * v * 256 + slot, 256);
         }
       }
       if (gi != 0) return;
