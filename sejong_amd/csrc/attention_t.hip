@@ -432,11 +432,11 @@ __global__ __launch_bounds__(256) void k_attn2_fwd_cached(TArgs a) {
 // takes part in staging K | V (the grouped launch shares one copy among the
 // query heads of a KV head)
 // first key block a query of block qb sees (window: keys pos - W + 1 .. pos)
-__device__ __forceinline__ int dq_first_kb(int qb, int W) {
+__host__ __device__ inline int dq_first_kb(int qb, int W) {
   return W > 0 && qb * QB - W + 1 > 0 ? (qb * QB - W + 1) / QB : 0;
 }
 // one past the last query block that sees a key of block kb
-__device__ __forceinline__ int dkv_end_qb(int kb, int T, int W) {
+__host__ __device__ inline int dkv_end_qb(int kb, int T, int W) {
   int nqb = T / QB;
   if (W > 0 && (kb * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (kb * QB + QB - 1 + W - 1) / QB + 1;
   return nqb;
@@ -1060,14 +1060,12 @@ struct Piece {
 // more (its sum written, counted and read at device scope)
 constexpr double DQ_START = 5.0, DQ_STEP = 1.85, KV_START = 6.6, KV_STEP = 2.9, PIECE_MEET = 5.0;
 
-// the walks of both roles for nb blocks and window W (0: causal)
+// the walks of both roles for nb blocks and window W (0: causal), with the
+// bounds the kernels' whole walks use
 void role_walks(int nb, int W, std::vector<Walk>& wq, std::vector<Walk>& wk) {
   for (int i = 0; i < nb; i++) {
-    const int kb0 = W > 0 && i * QB - W + 1 > 0 ? (i * QB - W + 1) / QB : 0;
-    int nqb = nb;
-    if (W > 0 && (i * QB + QB - 1 + W - 1) / QB + 1 < nqb) nqb = (i * QB + QB - 1 + W - 1) / QB + 1;
-    wq.push_back(Walk{i, kb0, i});
-    wk.push_back(Walk{i, i, nqb - 1});
+    wq.push_back(Walk{i, dq_first_kb(i, W), i});
+    wk.push_back(Walk{i, i, dkv_end_qb(i, nb * QB, W) - 1});
   }
 }
 
