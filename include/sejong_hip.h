@@ -367,14 +367,15 @@ int sj_attention_bwd_tt(void *stream, const uint16_t *qkv, long ldqkv, long ldt,
  * KV head (no counterpart in the reference: the split is this library's
  * scheduling, exposed for its tests).  The causal walks (dQ of query block
  * qb over key blocks ..qb, dK | dV of key block kb over query blocks kb..)
- * longer than a cap per role are cut in two parts; every piece (whole walk
- * or part) is one workgroup per (KV head, sequence) pair, dispatched
- * costliest first; the caps are those whose simulated dispatch of `pairs`
- * pairs on `cus` CUs finishes first.  Writes one word per piece into seg
- * (cap words at least): bit 31 set, bits 0-5 block, 6-11 / 12-17 first /
- * last block of the walk it covers, bit 18 role (0 dQ, 1 dK | dV), 19-28
- * cut-walk index + 1 (0: whole walk), bit 29 part; *ncut = cut walks per
- * pair.  Returns the number of pieces, or a negative status. */
+ * longer than a cap per role are cut into parts of at most the cap (up to
+ * four); every piece (whole walk or part) is one workgroup per (KV head,
+ * sequence) pair, dispatched costliest first; the caps are those whose
+ * simulated dispatch of `pairs` pairs on `cus` CUs finishes first.  Writes
+ * one word per piece into seg (cap words at least): bit 31 set, bits 0-5
+ * block, 6-11 / 12-17 first / last block of the walk it covers, bit 18 role
+ * (0 dQ, 1 dK | dV), 19-26 cut-walk index + 1 (0: whole walk), 27-28 part,
+ * 29-30 the walk's parts - 1; *ncut = cut walks per pair.  Returns the
+ * number of pieces, or a negative status. */
 int sj_attention_bwd_plan(long t, long window, long pairs, int cus, uint32_t *seg, long cap, int *ncut);
 
 /* ---------------------------------------------------- Mixture of experts

@@ -825,25 +825,30 @@ static_assert(LDS_BWD_G + 16 <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 
 // block qb: qb + 1 key blocks; dK | dV of key block kb: nb - kb query
 // blocks), so with one workgroup per walk a launch that fills the chip once
 // lasts as long as its longest walk, about twice the mean.  The host cuts
-// each role's walks longer than a cap into two parts (SplitPlan; a piece is
-// a whole walk or a part, one workgroup each, dispatched costliest first as
-// CUs free up) with the caps that finish a simulated dispatch first.  Each
-// part of a cut walk writes its fp32 sum (the groups' dQ^T, or the dK | dV
-// after the head sum) to its slot of the workspace and counts itself on the
-// walk's counter; the part that counts second adds the other part's sum to
-// its own (a + b: the same bits whichever part comes second), writes the
-// planes and sets the counter back to zero for the next launch.  (One piece
-// per workgroup: a workgroup that ran several pieces in a loop held their
-// addresses and arguments across the loop and ran every walk slower.)
-constexpr int PLAN_PIECES = 128;  // pieces of both roles: at most 4 t/64 (t <= 2048)
+// each role's walks longer than a cap into parts of at most the cap (up to
+// PLAN_PARTS; SplitPlan: a piece is a whole walk or a part, one workgroup
+// each, dispatched costliest first as CUs free up) with the caps that finish
+// a simulated dispatch first.  Each part of a cut walk writes its fp32 sum
+// (the groups' dQ^T, or the dK | dV after the head sum) to its slot of the
+// workspace and counts itself on the walk's counter; the part that counts
+// last adds the parts' sums in part order (its own from registers: the same
+// bits whichever part comes last), writes the planes and sets the counter
+// back to zero for the next launch.  (One piece per workgroup: a workgroup
+// that ran several pieces in a loop held their addresses and arguments
+// across the loop and ran every walk slower.)
+constexpr int PLAN_PIECES = 128;  // pieces of both roles
+constexpr int PLAN_CUTS = 64;     // cut walks per (KV head, sequence)
+constexpr int PLAN_PARTS = 4;     // parts of a cut walk
 constexpr int PLAN_POOLS = 8;     // counter pools, taken in turn by successive launches
 constexpr int PLAN_COUNTERS = 1024;  // counters per pool: cut walks of one launch
 // piece: bit 31 set, bits 0-5 block, 6-11 / 12-17 the first / last block of
-// the walk it covers, bit 18 the role (0: dQ, 1: dK | dV), 19-28 cut-walk
-// index + 1 (0: a whole walk), bit 29 the part of the cut walk
+// the walk it covers, bit 18 the role (0: dQ, 1: dK | dV), 19-26 cut-walk
+// index + 1 (0: a whole walk), 27-28 the part, 29-30 the walk's parts - 1
 struct SplitPlan {
-  int ncut;  // cut walks per (KV head, sequence)
-  int pool;  // counter pool of this launch
+  int ncut;    // cut walks per (KV head, sequence)
+  int nslots;  // part sums per (KV head, sequence)
+  int pool;    // counter pool of this launch
+  uint16_t slot0[PLAN_CUTS];  // first part-sum slot of each cut walk
   uint32_t seg[PLAN_PIECES];
 };
 __device__ uint32_t g_cut_count[PLAN_POOLS * PLAN_COUNTERS];  // zero between launches
@@ -867,34 +872,46 @@ __device__ __forceinline__ f32x4 get4(const float* p, long stride) {
   return v;
 }
 
-// The two parts of a cut walk meet (every thread of the workgroup calls it,
+// The parts of a cut walk meet (every thread of the workgroup calls it,
 // after put4 of its share of this part's sum): true in the workgroup that
-// counts second, which may then get4 the other part's sum, and which sets
+// counts last, which may then get4 the other parts' sums, and which sets
 // the counter back to zero.  The stores have completed (vmcnt 0) before the
-// barrier that precedes the count, and the other part's loads follow the
+// barrier that precedes the count, and the other parts' loads follow the
 // barrier that hands the count out.
-__device__ __forceinline__ bool meet_second(uint32_t* cnt, uint32_t* flag) {
+__device__ __forceinline__ bool meet_last(uint32_t* cnt, uint32_t* flag, int nparts) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   block_barrier();
   if (threadIdx.x == 0) *flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   block_barrier();
   const uint32_t n = __builtin_amdgcn_readfirstlane(*flag);  // the barrier's memory clobber: read after it
-  if (n == 0) return false;
+  if (n != (uint32_t)(nparts - 1)) return false;
   if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return true;
 }
 
-// where the sums of cut walk `cut` of (sequence b, KV head kvh) meet:
-// this part's and the other part's slot (slot floats each), its counter
+// where the sums of cut walk `cut` of (sequence b, KV head kvh) meet: the
+// walk's first slot (part p at base + p * slot floats), this part, the
+// walk's parts, its counter
 struct Meet {
-  float *mine, *other;
+  float* base;
+  int part, nparts;
   uint32_t* cnt;
 };
 __device__ __forceinline__ Meet meet_at(const TArgs& a, const SplitPlan& pl, int b, int kvh, uint32_t sg, long slot) {
-  const int cut = (int)((sg >> 19) & 1023) - 1, part = (int)((sg >> 29) & 1);
-  const long c = ((long)b * a.HK + kvh) * pl.ncut + cut;
-  float* base = a.part + c * 2 * slot;
-  return Meet{base + part * slot, base + (1 - part) * slot, g_cut_count + pl.pool * PLAN_COUNTERS + c};
+  const int cut = (int)((sg >> 19) & 255) - 1, part = (int)((sg >> 27) & 3), nparts = (int)((sg >> 29) & 3) + 1;
+  const long pair = (long)b * a.HK + kvh;
+  float* base = a.part + (pair * pl.nslots + pl.slot0[cut]) * slot;
+  return Meet{base, part, nparts, g_cut_count + pl.pool * PLAN_COUNTERS + pair * pl.ncut + cut};
+}
+// the walk's total of vector v (element r at off + r * stride of each
+// part's slot), parts in order: ((s0 + s1) + s2) + s3, this part's own from
+// registers
+__device__ __forceinline__ f32x4 parts_total(const Meet& m, long slot, long off, long stride, f32x4 own) {
+  f32x4 t = m.part == 0 ? own : get4(m.base + off, stride);
+#pragma unroll
+  for (int p = 1; p < PLAN_PARTS; p++)
+    if (p < m.nparts) t = t + (p == m.part ? own : get4(m.base + p * slot + off, stride));
+  return t;
 }
 
 // One piece: a whole walk, or a part of a cut walk, of one role.
@@ -911,17 +928,17 @@ __device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& p
     const int lane = tid & 63, g = lane >> 4, j = lane & 15;
     const int h = kvh * G + gi;
     const int blk = (int)(sg & 63), lo = (int)((sg >> 6) & 63), hi = (int)((sg >> 12) & 63);
-    const bool cut = ((sg >> 19) & 1023) != 0;
+    const bool cut = ((sg >> 19) & 255) != 0;
     if constexpr (DQ) {
       f32x4 dq[4];
       attn2_dq_walk<NS_DQ>(a, lds, blk, h, b, wl, gi == 0, lo, hi, dq);
       if (cut) {
         const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
 #pragma unroll
-        for (int d = 0; d < 4; d++) put4(m.mine + 4 * d * NT + tid, NT, dq[d]);
-        if (!meet_second(m.cnt, s_count)) return;
+        for (int d = 0; d < 4; d++) put4(m.base + m.part * SLOT + 4 * d * NT + tid, NT, dq[d]);
+        if (!meet_last(m.cnt, s_count, m.nparts)) return;
 #pragma unroll
-        for (int d = 0; d < 4; d++) dq[d] = dq[d] + get4(m.other + 4 * d * NT + tid, NT);
+        for (int d = 0; d < 4; d++) dq[d] = parts_total(m, SLOT, 4 * d * NT + tid, NT, dq[d]);
       }
       attn2_dq_store(a, blk, h, b, wl, dq);
     } else {
@@ -966,12 +983,12 @@ __device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& p
         const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
         if (gi == 0) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) put4(m.mine + 4 * v * 256 + slot, 256, acc[v]);
+          for (int v = 0; v < 8; v++) put4(m.base + m.part * SLOT + 4 * v * 256 + slot, 256, acc[v]);
         }
-        if (!meet_second(m.cnt, s_count)) return;
+        if (!meet_last(m.cnt, s_count, m.nparts)) return;
         if (gi == 0) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) acc[v] = acc[v] + get4(m.other + 4 * v * 256 + slot, 256);
+          for (int v = 0; v < 8; v++) acc[v] = parts_total(m, SLOT, 4 * v * 256 + slot, 256, acc[v]);
         }
       }
       if (gi != 0) return;
@@ -1050,7 +1067,7 @@ struct Walk {  // one role's walk for block `block`: blocks first .. last of the
   int len() const { return last - first + 1; }
 };
 struct Piece {
-  int block, first, last, role, cut, part;  // cut -1: a whole walk
+  int block, first, last, role, cut, part, nparts;  // cut -1: a whole walk
   double cost;
 };
 
@@ -1069,18 +1086,23 @@ void role_walks(int nb, int W, std::vector<Walk>& wq, std::vector<Walk>& wk) {
   }
 }
 
-// a role's walks as pieces: longer than cap -> cap | the rest (cut indices
-// from *ncut on); false if a walk is longer than 2 cap
-bool cut_walks(const std::vector<Walk>& ws, int role, int cap, std::vector<Piece>& out, int* ncut) {
+// a role's walks as pieces: one longer than cap is cut into parts of cap
+// blocks and a last part of the rest (cut indices from *ncut on, part-sum
+// slots counted in *nslots); false if a walk needs more than PLAN_PARTS
+bool cut_walks(const std::vector<Walk>& ws, int role, int cap, std::vector<Piece>& out, int* ncut, int* nslots) {
   const double start = role == 0 ? DQ_START : KV_START, step = role == 0 ? DQ_STEP : KV_STEP;
   for (const Walk& w : ws) {
     if (w.len() > cap) {
-      if (w.len() > 2 * cap) return false;
+      const int np = (w.len() + cap - 1) / cap;
+      if (np > PLAN_PARTS) return false;
       const int c = (*ncut)++;
-      out.push_back(Piece{w.block, w.first, w.first + cap - 1, role, c, 0, start + cap * step + PIECE_MEET});
-      out.push_back(Piece{w.block, w.first + cap, w.last, role, c, 1, start + (w.len() - cap) * step + PIECE_MEET});
+      *nslots += np;
+      for (int q = 0; q < np; q++) {
+        const int f = w.first + q * cap, l = std::min(w.last, f + cap - 1);
+        out.push_back(Piece{w.block, f, l, role, c, q, np, start + (l - f + 1) * step + PIECE_MEET});
+      }
     } else {
-      out.push_back(Piece{w.block, w.first, w.last, role, -1, 0, start + w.len() * step});
+      out.push_back(Piece{w.block, w.first, w.last, role, -1, 0, 1, start + w.len() * step});
     }
   }
   return true;
@@ -1105,12 +1127,13 @@ double simulate(std::vector<Piece>& ps, long pairs, int cus) {
 
 // The pieces of the launch: over every pair of caps (dQ, dK | dV), the one
 // whose simulated dispatch finishes first (ties: the longer caps, fewer
-// cuts), with at most nb cut walks per (KV head, sequence) -- their sums
-// fit the workspace of the per-head partials -- and at most PLAN_COUNTERS
-// for the launch.  cut = false: one piece per walk (the former launch).
-// caps_q / caps_k > 0 fix the caps.
+// cuts), with at most 2 nb part sums per (KV head, sequence) -- they fit
+// the workspace of the per-head partials --, PLAN_PIECES pieces,
+// PLAN_CUTS cut walks and PLAN_COUNTERS counters for the launch.
+// cut = false: one piece per walk (the former launch).  caps_q / caps_k > 0
+// fix the caps.
 double plan_pieces(int nb, int W, long pairs, int cus, bool cut, int caps_q, int caps_k, std::vector<Piece>& best,
-                   int& ncut) {
+                   int& ncut, int& nslots) {
   std::vector<Walk> wq, wk;
   role_walks(nb, W, wq, wk);
   int maxq = 0, maxk = 0;
@@ -1123,17 +1146,18 @@ double plan_pieces(int nb, int W, long pairs, int cus, bool cut, int caps_q, int
       if (caps_q > 0 && cq != std::min(caps_q, maxq)) continue;
       if (caps_k > 0 && ck != std::min(caps_k, maxk)) continue;
       std::vector<Piece> ps;
-      int nc = 0;
-      if (!cut_walks(wq, 0, cq, ps, &nc) || !cut_walks(wk, 1, ck, ps, &nc)) continue;
-      if (nc > nb || (long)nc * pairs > PLAN_COUNTERS) continue;
+      int nc = 0, ns = 0;
+      if (!cut_walks(wq, 0, cq, ps, &nc, &ns) || !cut_walks(wk, 1, ck, ps, &nc, &ns)) continue;
+      if (ns > 2 * nb || nc > PLAN_CUTS || (int)ps.size() > PLAN_PIECES || (long)nc * pairs > PLAN_COUNTERS) continue;
       const double t = simulate(ps, pairs, cus);
       if (best_t < 0 || t < best_t - 1e-9) {
         best_t = t;
         best = ps;
         ncut = nc;
+        nslots = ns;
       }
     }
-  if (best_t < 0) return plan_pieces(nb, W, pairs, cus, false, 0, 0, best, ncut);
+  if (best_t < 0) return plan_pieces(nb, W, pairs, cus, false, 0, 0, best, ncut, nslots);
   return best_t;
 }
 
@@ -1172,16 +1196,28 @@ int make_plan(long t, long window, long pairs, int cus, SplitPlan& pl, int& npie
     auto it = cache.find(key);
     if (it == cache.end()) {
       std::vector<Piece> ps;
-      int ncut = 0;
-      plan_pieces(nb, (int)window, pairs, cus, cut_on != 0, cq, ck, ps, ncut);  // ps: costliest first
+      int ncut = 0, nslots = 0;
+      plan_pieces(nb, (int)window, pairs, cus, cut_on != 0, cq, ck, ps, ncut, nslots);  // ps: costliest first
       SplitPlan p;
       memset(&p, 0, sizeof(p));
       for (size_t i = 0; i < ps.size(); i++) {
         const Piece& x = ps[i];
         p.seg[i] = (1u << 31) | (uint32_t)x.block | ((uint32_t)x.first << 6) | ((uint32_t)x.last << 12) |
-                   ((uint32_t)x.role << 18) | ((uint32_t)(x.cut + 1) << 19) | ((uint32_t)x.part << 29);
+                   ((uint32_t)x.role << 18) | ((uint32_t)(x.cut + 1) << 19) | ((uint32_t)x.part << 27) |
+                   ((uint32_t)(x.nparts - 1) << 29);
+      }
+      {  // part-sum slots of each cut walk, in cut order
+        std::vector<int> np((size_t)ncut, 0);
+        for (const Piece& x : ps)
+          if (x.cut >= 0) np[(size_t)x.cut] = x.nparts;
+        int at = 0;
+        for (int c = 0; c < ncut; c++) {
+          p.slot0[c] = (uint16_t)at;
+          at += np[(size_t)c];
+        }
       }
       p.ncut = ncut;
+      p.nslots = nslots;
       it = cache.emplace(key, std::make_pair(p, (int)ps.size())).first;
     }
     pl = it->second.first;

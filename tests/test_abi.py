@@ -141,7 +141,7 @@ def _attention_plan(lib, t, window, pairs=16, cus=256):
     for x in (int(v) for v in seg[:max(n, 0)]):
         assert x >> 31
         pieces.append(dict(block=x & 63, first=(x >> 6) & 63, last=(x >> 12) & 63, role=(x >> 18) & 1,
-                           cut=((x >> 19) & 1023) - 1, part=(x >> 29) & 1))
+                           cut=((x >> 19) & 255) - 1, part=(x >> 27) & 3, nparts=((x >> 29) & 3) + 1))
     return n, ncut.value, pieces
 
 
@@ -205,23 +205,30 @@ def test_attention_backward_pieces_cover_every_walk_once(t, window, pairs):
     covered = {k: [] for k in walks}
     cuts = {}
     for p in pieces:
-        covered[(p["role"], p["block"])].append((p["first"], p["last"]))
+        covered[(p["role"], p["block"])].append((p["first"], p["last"], p["part"]))
         if p["cut"] >= 0:
             assert p["cut"] < ncut
-            cuts.setdefault(p["cut"], []).append((p["role"], p["block"], p["part"]))
+            cuts.setdefault(p["cut"], []).append((p["role"], p["block"], p["part"], p["nparts"]))
+        else:
+            assert p["part"] == 0 and p["nparts"] == 1
     for k, (lo, hi) in walks.items():
         parts = sorted(covered[k])
-        assert parts[0][0] == lo and parts[-1][1] == hi and len(parts) <= 2, (k, parts)
-        for (a0, a1), (b0, b1) in zip(parts, parts[1:]):
-            assert b0 == a1 + 1, (k, parts)
-        assert all(a0 <= a1 for a0, a1 in parts)
+        assert parts[0][0] == lo and parts[-1][1] == hi and len(parts) <= 4, (k, parts)
+        for (a0, a1, ap), (b0, b1, bp) in zip(parts, parts[1:]):
+            assert b0 == a1 + 1 and bp == ap + 1, (k, parts)  # parts in walk order
+        assert all(a0 <= a1 for a0, a1, _ in parts)
     assert sorted(cuts) == list(range(ncut))
+    slots = 0
     for c, ps in cuts.items():
-        assert len(ps) == 2 and ps[0][:2] == ps[1][:2] and {p[2] for p in ps} == {0, 1}, (c, ps)
+        n = ps[0][3]
+        assert 2 <= n <= 4 and len(ps) == n and len({p[:2] for p in ps}) == 1, (c, ps)
+        assert sorted(p[2] for p in ps) == list(range(n)) and all(p[3] == n for p in ps), (c, ps)
+        slots += n
+    assert slots <= 2 * nb_blocks  # the part sums fit the workspace
     assert all(_piece_us(x) >= _piece_us(y) - 1e-12 for x, y in zip(pieces, pieces[1:]))
     whole = sorted(({"role": r, "block": b, "first": lo, "last": hi, "cut": -1} for (r, b), (lo, hi) in walks.items()),
                    key=lambda p: -_piece_us(p))
     assert _dispatch_finish(pieces, pairs, 256) <= _dispatch_finish(whole, pairs, 256) + 1e-9
-    if (t, window, pairs) == (512, 0, 16):  # cfg2: the dK | dV walks of key blocks 0-3 cut, none of dQ
-        assert ncut == 4 and all(p["role"] == 1 for p in pieces if p["cut"] >= 0)
+    if (t, window, pairs) == (512, 0, 16):  # cfg2: the longest dK | dV walks cut, none of dQ
+        assert ncut >= 4 and all(p["role"] == 1 for p in pieces if p["cut"] >= 0)
         assert _dispatch_finish(pieces, pairs, 256) < 0.85 * _dispatch_finish(whole, pairs, 256)

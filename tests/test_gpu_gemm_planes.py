@@ -362,7 +362,8 @@ def test_attention_t_and_planes(api, lib, B, T, HQ, HK):
 
 @pytest.mark.parametrize("B,T,HQ,HK,W", [(2, 256, 6, 2, 0), (1, 512, 4, 4, 0), (2, 128, 8, 1, 0), (2, 256, 4, 2, 128),
                                          (1, 320, 4, 1, 100), (2, 192, 4, 4, 32), (2, 256, 6, 2, 128),
-                                         (1, 320, 3, 1, 100), (2, 512, 6, 2, 0), (1, 1024, 3, 1, 300)])
+                                         (1, 320, 3, 1, 100), (2, 512, 6, 2, 0), (1, 1024, 3, 1, 300),
+                                         (1, 1024, 3, 1, 0)])
 def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     """The step's MFMA-layout attention (q|k|v and dO planes in row
     orientation, transposed fragments by LDS transpose reads) against the
@@ -428,8 +429,9 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
     # transposed outputs are optional (the row-layout dW step): same planes bit
     # for bit; with three query heads per KV head this is the grouped launch
     # (dK | dV summed inside the workgroup, no partials, no reduce pass), whose
-    # walks longer than a bin are cut in two parts added at the end: the same
-    # sums up to fp32 association, and the same bits launch after launch
+    # walks longer than a cap are cut into parts added at the end (T 1024:
+    # three-part walks): the same sums up to fp32 association, and the same
+    # bits launch after launch
     G2h, G2l = empty(M * NG, "bf16"), empty(M * NG, "bf16")
     api.sj_attention_bwd_tt(None, QKV.p, ldq, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DT.p, B, T, HQ, HK, Dh, W, tab.p,
                             G2h.p, G2l.p, NG, None, None, 0, ws.p, ws.nbytes)
