@@ -953,68 +953,67 @@ __device__ __forceinline__ void grouped_piece(const TArgs& a, const SplitPlan& p
                     ? *(const float2*)(a.rope + 2 * ((long)pos * (DH / 2) + ((16 * (i >> 1) + 4 * g + 2 * (i & 1)) >> 1)))
                     : float2{0.f, 0.f};
       block_barrier();  // every group is done reading its stages
-      // group q > 0 leaves vector v (dk 0..3, dv 0..3) of lane L of slice wl
-      // at f32x4 index ((q - 1) * 8 + v) * 256 + wl * 64 + L
+      // dK is summed and stored by group 0, dV by group 1, side by side:
+      // group q leaves vector d of half hf (0 dK, 1 dV) that it does not own
+      // for lane L of slice wl at f32x4 index ((hf * G + q) * 4 + d) * 256 +
+      // wl * 64 + L; the owner adds the heads in head order, ((0 + h0) + h1)
+      // + h2 as the group reduce sums the fp32 partials
+      static_assert(G >= 2 && (size_t)2 * G * 4 * 256 * 16 <= LDS_BWD_G, "grouped exchange");
       f32x4* sh = (f32x4*)lds;
       const int slot = wl * 64 + lane;
-      if (gi > 0) {
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-          sh[((gi - 1) * 8 + d) * 256 + slot] = dk[d];
-          sh[((gi - 1) * 8 + 4 + d) * 256 + slot] = dv[d];
-        }
+      for (int d = 0; d < 4; d++) {
+        if (gi != 0) sh[((0 * G + gi) * 4 + d) * 256 + slot] = dk[d];
+        if (gi != 1) sh[((1 * G + gi) * 4 + d) * 256 + slot] = dv[d];
       }
       block_barrier();
-      f32x4 acc[8];  // group 0: dK^T (0..3), dV^T (4..7) summed over the heads
-      if (gi == 0) {
+      const int hf = gi;  // the half this group owns (groups 0 and 1)
+      f32x4 acc[4];
+      if (hf < 2) {
 #pragma unroll
-        for (int v = 0; v < 8; v++) {
+        for (int d = 0; d < 4; d++) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             float s = 0.f;
-            s += v < 4 ? dk[v][r] : dv[v - 4][r];
 #pragma unroll
-            for (int q = 1; q < G; q++) s += sh[((q - 1) * 8 + v) * 256 + slot][r];
-            acc[v][r] = s;
+            for (int q = 0; q < G; q++) s += q == gi ? (hf ? dv[d][r] : dk[d][r]) : sh[((hf * G + q) * 4 + d) * 256 + slot][r];
+            acc[d][r] = s;
           }
         }
       }
       if (cut) {
         const Meet m = meet_at(a, pl, b, kvh, sg, SLOT);
-        if (gi == 0) {
+        if (hf < 2) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) put4(m.base + m.part * SLOT + 4 * v * 256 + slot, 256, acc[v]);
+          for (int d = 0; d < 4; d++) put4(m.base + m.part * SLOT + 4 * (4 * hf + d) * 256 + slot, 256, acc[d]);
         }
         if (!meet_last(m.cnt, s_count, m.nparts)) return;
-        if (gi == 0) {
+        if (hf < 2) {
 #pragma unroll
-          for (int v = 0; v < 8; v++) acc[v] = parts_total(m, SLOT, 4 * v * 256 + slot, 256, acc[v]);
+          for (int d = 0; d < 4; d++) acc[d] = parts_total(m, SLOT, 4 * (4 * hf + d) * 256 + slot, 256, acc[d]);
         }
       }
-      if (gi != 0) return;
+      if (hf >= 2) return;
       const int T = a.T, NQ = a.HQ * DH, NK = a.HK * DH;
       const long krow = (long)b * T + pos;
 #pragma unroll
-      for (int half = 0; half < 2; half++) {  // dK, then dV
+      for (int d = 0; d < 4; d++) {
+        float v[4] = {acc[d][0], acc[d][1], acc[d][2], acc[d][3]};
+        if (hf == 0 && a.rope) {  // inverse RoPE on dK's pairs (columns 16d + 4g + 2pr, +1)
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-          float v[4] = {acc[4 * half + d][0], acc[4 * half + d][1], acc[4 * half + d][2], acc[4 * half + d][3]};
-          if (half == 0 && a.rope) {  // inverse RoPE on dK's pairs (columns 16d + 4g + 2pr, +1)
-#pragma unroll
-            for (int pr = 0; pr < 2; pr++) {
-              const float2 c = cs[2 * d + pr];
-              const float x = v[2 * pr], y = v[2 * pr + 1];
-              v[2 * pr] = x * c.x + y * c.y;
-              v[2 * pr + 1] = y * c.x - x * c.y;
-            }
+          for (int pr = 0; pr < 2; pr++) {
+            const float2 c = cs[2 * d + pr];
+            const float x = v[2 * pr], y = v[2 * pr + 1];
+            v[2 * pr] = x * c.x + y * c.y;
+            v[2 * pr + 1] = y * c.x - x * c.y;
           }
-          bf16_t hv[4], lv[4];
-#pragma unroll
-          for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
-          const long col = NQ + half * NK + kvh * DH + 16 * d + 4 * g;
-          *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
-          *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
         }
+        bf16_t hv[4], lv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
+        const long col = NQ + hf * NK + kvh * DH + 16 * d + 4 * g;
+        *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
+        *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
       }
     }
   }
