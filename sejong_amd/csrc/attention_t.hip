@@ -817,9 +817,10 @@ static_assert(LDS_BWD_G + 16 <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 
 // dK | dV walk (key block kb): each group accumulates its head's share over
 // its own Q / dO stages; the groups then add their shares through LDS in
 // head order, ((0 + h0) + h1) + h2 as the group reduce sums the fp32
-// partials, and group 0 applies the inverse RoPE to dK and writes the hi /
-// lo planes.  No per-head partials leave the workgroup and no reduce pass
-// follows.  G x NST stages of dK/dV operands: G <= 3 fits the LDS.
+// partials (group 0 for dK, which it rotates back by the inverse RoPE,
+// group 1 for dV, side by side), and each writes its hi / lo planes.  No
+// per-head partials leave the workgroup and no reduce pass follows.  G x NST
+// stages of dK/dV operands: G <= 3 fits the LDS.
 //
 // Balanced pieces.  The causal walks are 1 .. nb blocks long (dQ of query
 // block qb: qb + 1 key blocks; dK | dV of key block kb: nb - kb query
