@@ -68,6 +68,10 @@ def _hier_ops(mc, tc):
               (mc.layers, mc.width, mc.heads, mc.kv, mc.ffn_width, Tg, 0),
               (h.decoder_layers, h.decoder_width, h.decoder_heads, h.decoder_heads, h.decoder_ffn_width, T,
                h.local_window)]
+    # the library's row-layout dW rule: every stage on the transposed-operand
+    # attention (T a multiple of 64) and no parameter-VJP groups
+    rowdw = (planes and os.environ.get("SJ_ATTN_TT", "1") != "0" and all(s[5] % 64 == 0 for s in stages)
+             and getattr(tc, "parameter_vjp", None) is None)
     tot = {}
 
     def add(op, kind, w, n=1):
@@ -88,10 +92,11 @@ def _hier_ops(mc, tc):
                             ("down_residual", "flop", 2 * M * F * d), ("down_dx_swiglu", "flop", 2 * M * F * d),
                             ("down_dw", "flop", 2 * M * F * d)):
             add(op, kind, w, L)
-        add("rmsnorm", "byte", (3 if planes else 2) * M * d * es + d * es, 2 * L)
+        tr = 0 if rowdw else 1  # transposed copies (y^T, dx planes^T) unless row-layout dW
+        add("rmsnorm", "byte", (2 + (tr if planes else 0)) * M * d * es + d * es, 2 * L)
         add("rmsnorm", "byte", 2 * M * d * es + d * es)                       # closing norm
-        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es, 2 * L)
-        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es)
+        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (4 + 4 * tr if planes else 0)) + d * es, 2 * L)
+        add("rmsnorm_bwd", "byte", M * d * (es + 4 + 4 + 4 + (4 + 4 * tr if planes else 0)) + d * es)
     de, dg, dd = h.encoder_width, mc.width, h.decoder_width
     Ml, Mg, V = B * T, B * Tg, 257
     for op, kind, w in (("patch_pool", "byte", Ml * de * es + Mg * de * es),
@@ -134,6 +139,10 @@ def op_work(op: str, mc, tc):
     J = mc.head_dim * mc.kv
     es = 2 if mc.precision == "bf16" else 4
     planes = mc.precision == "bf16" and mc.head_dim == 64 and os.environ.get("SJ_PLANES", "1") != "0"
+    # the library's row-layout dW rule (planes, transposed-operand attention,
+    # no parameter-VJP groups): no transposed copies of the norm outputs
+    rowdw = (planes and os.environ.get("SJ_ATTN_TT", "1") != "0" and tc.sequence % 64 == 0
+             and getattr(tc, "parameter_vjp", None) is None)
     attn_fwd = tc.batch * mc.heads * 4 * mc.head_dim * tc.sequence * (tc.sequence + 1) / 2
     P = sum(math.prod(s) for _, s, _ in __import__("sejong_amd.model", fromlist=["layout"]).layout(mc))
     table = {
@@ -166,10 +175,11 @@ def op_work(op: str, mc, tc):
         "head_fwd": ("flop", 2 * M * d * V),
         "head_dx": ("flop", 2 * M * d * V),
         "head_dw": ("flop", 2 * M * d * V),
-        # plane path: y and y^T written; backward also writes hi/lo planes
-        # in both orientations (4 bf16 copies of dx)
-        "rmsnorm": ("byte", (3 if planes else 2) * M * d * es + d * es),
-        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4 + (8 if planes else 0)) + d * es),
+        # plane path: y (and y^T unless the dW products read row layouts)
+        # written; the backward also writes dx as hi/lo planes (and their
+        # transposes unless row-layout dW)
+        "rmsnorm": ("byte", (2 + (1 if planes and not rowdw else 0)) * M * d * es + d * es),
+        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4 + ((4 if rowdw else 8) if planes else 0)) + d * es),
         "cross_entropy": ("byte", 2 * M * V * 4 + M * 8),
         "loss_summary": ("byte", M * 4),
         "embedding": ("byte", M * 4 + 2 * M * d * es),
