@@ -63,6 +63,9 @@ int sj_device_info(char *arch, size_t arch_len, int *compute_units);
  * Transfers are synchronous; sj_event_elapsed waits for `end`. */
 int sj_alloc(size_t bytes, void **ptr);
 int sj_free(void *ptr);
+/* Engine::available_memory_bytes (crates/sejong-gpu/src/lib.rs:243-245,
+ * hip.rs:154): free and total device memory of the current device. */
+int sj_memory_info(size_t *free_bytes, size_t *total_bytes);
 int sj_upload(void *dst, const void *src, size_t bytes);
 int sj_download(void *dst, const void *src, size_t bytes);
 int sj_synchronize(void *stream);
@@ -358,6 +361,15 @@ int sj_attention_fwd_tt(void *stream, const uint16_t *qkv, long ldqkv, long ldt,
                         long hk, long head_dim, long window, uint16_t *o, long ldo, float *lse, float *lse_t,
                         uint16_t *o_t, long ldot);
 size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long hq, long hk, long head_dim);
+/* The workspace ends with the meeting counters of the grouped launch's cut
+ * walks (the last sj_attention_bwd_tt_counter_bytes(batch, hk) bytes of the
+ * size above; no counterpart in the reference, whose backward does not cut
+ * walks): they must be zero before the first call on a workspace (clear them
+ * when it is allocated) and nothing else may write them between calls;
+ * every call leaves them zero.  Calls that share a workspace must not
+ * overlap (as for any workspace); calls on different workspaces never share
+ * counters. */
+size_t sj_attention_bwd_tt_counter_bytes(long batch, long hk);
 int sj_attention_bwd_tt(void *stream, const uint16_t *qkv, long ldqkv, long ldt, const uint16_t *o, long ldo,
                         const float *lse_t, const uint16_t *do_hi, const uint16_t *do_lo, long lddo, float *delta_t,
                         long batch, long t, long hq, long hk, long head_dim, long window, const float *rope_table,
@@ -866,6 +878,17 @@ int sj_checkpoint_save(const char *directory, const char *manifest_json, long n_
                        const char *const *weight_names, const long *weight_ranks, const long *weight_dims,
                        const float *const *weight_data, long n_optimizer, const char *const *optimizer_names,
                        const long *optimizer_ranks, const long *optimizer_dims, const float *const *optimizer_data);
+
+/* Corpus::open's fingerprint hash (crates/sejong-train/src/lib.rs:32-56:
+ * blake3::Hasher::new / update / finalize of the `blake3` crate 1.8.7):
+ * BLAKE3 in its default hash mode, 32-byte output.  The caller owns the
+ * state (sj_blake3_state_bytes bytes, 8-byte aligned); init, then any
+ * number of updates, then finalize (which leaves the state usable for more
+ * updates).  Host code: no device is touched. */
+size_t sj_blake3_state_bytes(void);
+int sj_blake3_init(void *state);
+int sj_blake3_update(void *state, const void *data, size_t bytes);
+int sj_blake3_finalize(const void *state, uint8_t *out32);
 
 #ifdef __cplusplus
 }

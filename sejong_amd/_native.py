@@ -79,6 +79,7 @@ SIGNATURES = {
     "sj_device_info": (_I, [ctypes.c_char_p, _S, ctypes.POINTER(_I)]),
     "sj_alloc": (_I, [_S, ctypes.POINTER(_P)]),
     "sj_free": (_I, [_P]),
+    "sj_memory_info": (_I, [ctypes.POINTER(_S), ctypes.POINTER(_S)]),
     "sj_upload": (_I, [_P, _P, _S]),
     "sj_download": (_I, [_P, _P, _S]),
     "sj_synchronize": (_I, [_P]),
@@ -147,6 +148,7 @@ SIGNATURES = {
     "sj_gemm_planes": (_I, [_P, _L, _L, _L, _P, _P, _L, _P, _P, _L, _P, _I, _L, _I, _P, _S]),
     "sj_attention_fwd_tt": (_I, [_P, _P, _L, _L, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _L]),
     "sj_attention_bwd_tt_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
+    "sj_attention_bwd_tt_counter_bytes": (_S, [_L, _L]),
     "sj_attention_bwd_tt": (_I, [_P, _P, _L, _L, _P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _L, _P,
                                  _P, _P, _L, _P, _P, _L, _P, _S]),
     "sj_attention_bwd_plan": (_I, [_L, _L, _L, _I, _P, _L, _P]),
@@ -179,6 +181,10 @@ SIGNATURES = {
     "sj_safetensors_header": (_I, [ctypes.c_char_p, _P, _S, ctypes.POINTER(_S)]),
     "sj_safetensors_read": (_I, [ctypes.c_char_p, ctypes.c_char_p, _P, _L]),
     "sj_checkpoint_save": (_I, [ctypes.c_char_p, ctypes.c_char_p, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P]),
+    "sj_blake3_state_bytes": (_S, []),
+    "sj_blake3_init": (_I, [_P]),
+    "sj_blake3_update": (_I, [_P, _P, _S]),
+    "sj_blake3_finalize": (_I, [_P, _P]),
     "sj_model_create_experts": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(ExpertConfig),
                                      ctypes.POINTER(AdamConfig), _P, ctypes.POINTER(_P)]),
     "sj_model_create_hierarchy": (_I, [ctypes.POINTER(ModelConfig), ctypes.POINTER(HierarchyConfig),

@@ -6,8 +6,9 @@ evaluate: bits per byte-token, the mean next-token cross entropy over
 ln 2.  cached_measurement: one held-out sequence, its full-sequence logits,
 then a prefill of all but the last `decode` tokens through a fresh KV cache
 and teacher-forced decoding of the rest one token at a time (one warm-up
-pass, the second pass timed with a synchronisation after each call), and
-the largest |cached - full| over the last token's logits.
+pass, the second pass timed with a synchronisation after each call and the
+logits read back after the timed loop), and the largest |cached - full|
+over the last token's logits.
 """
 from __future__ import annotations
 
@@ -74,15 +75,18 @@ def cached_measurement(model: Model, corpus: Corpus, decode: int, seed: int | No
         try:
             model.synchronize()
             t0 = time.perf_counter()
-            model.forward_cached(ids[:prefix], cache)
+            model.forward_cached(ids[:prefix], cache, read=False)
+            model.synchronize()
             if pass_ == 1:
                 prefill_seconds = time.perf_counter() - t0
             for token in ids[prefix:]:
                 t0 = time.perf_counter()
-                out = model.forward_cached(np.array([token]), cache)  # synchronises
+                model.forward_cached(np.array([token]), cache, read=False)
+                model.synchronize()
                 if pass_ == 1:
                     decode_seconds.append(time.perf_counter() - t0)
-                last = out
+            # the logits are read back after the timed loop (benchmark.rs:150)
+            last = cache.logits()
         finally:
             cache.close()
     if not np.all(np.isfinite(last)):

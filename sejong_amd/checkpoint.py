@@ -182,11 +182,18 @@ def optimizer_tensors(model: Model) -> list:
 
 
 def save(model: Model, directory: str, optimizer: bool = True, training: dict | None = None,
-         data_fingerprint: str | None = None, rng_state: int | None = None, half_as_bf16: bool = False):
+         data_fingerprint: str | None = None, rng_state: int | None = None, half_as_bf16: bool = False,
+         corpus=None):
     """Model::save of a live model at its current step (the Adam / SGD step
-    count), with its optimizer state unless optimizer=False."""
+    count), with its optimizer state unless optimizer=False.  With a corpus,
+    the manifest's data_fingerprint is the corpus's fingerprint, as
+    save_training writes it (train lib.rs:472-491)."""
     if model.values:
         raise ValueError("checkpoints cover the byte language model (not the NativeValue head)")
+    if corpus is not None:
+        if data_fingerprint is not None and data_fingerprint != corpus.fingerprint:
+            raise ValueError("data_fingerprint differs from the corpus's fingerprint")
+        data_fingerprint = corpus.fingerprint
     save_arrays(directory, model.mc, model.get_params(), N.api.sj_model_steps(model.h),
                 optimizer_tensors(model) if optimizer else None, training, data_fingerprint, rng_state,
                 half_as_bf16=half_as_bf16)
@@ -245,14 +252,25 @@ def load_arrays(directory: str, half_as_bf16: bool = False):
     return mc, params, m, opt
 
 
-def load_into(model: Model, directory: str, half_as_bf16: bool = False) -> dict:
+def check_resume_corpus(manifest: dict, corpus) -> None:
+    """The resume check of train_configured (train lib.rs:338-341; the SGD
+    driver's control_variate.rs:452): the checkpoint must record this
+    corpus's fingerprint."""
+    if manifest.get("data_fingerprint") != corpus.fingerprint:
+        raise ValueError("resume corpus differs from checkpoint")
+
+
+def load_into(model: Model, directory: str, half_as_bf16: bool = False, corpus=None) -> dict:
     """Resume a live model from a checkpoint of the same configuration:
     parameters, and the optimizer state (Adam::load_parameters, train
     lib.rs:148-175 with the manifest's step; or the SGD state's parameter
-    RNG, control_variate.rs:125-150).  Returns the manifest."""
+    RNG, control_variate.rs:125-150).  With a corpus, the checkpoint must
+    record its fingerprint (check_resume_corpus).  Returns the manifest."""
     mc, params, m, opt = load_arrays(directory, half_as_bf16)
     if layout(mc) != layout(model.mc):
         raise ValueError("checkpoint model configuration differs from the live model")
+    if corpus is not None:
+        check_resume_corpus(m, corpus)
     model.set_params(params)
     if opt is None:
         return m

@@ -7,21 +7,49 @@ document i occupies the positions (ends[i-1], ends[i]) after its leading EOS
 at ends[i-1], and the final position tokens - 1 is the closing EOS.
 `batch` draws, per sequence, start = rng.index(tokens - sequence) and takes
 inputs start .. start+sequence-1 and targets one position later.  Files are
-memory-mapped; token lookup is vectorised over the batch.
+memory-mapped; token lookup is vectorised over the batch.  `fingerprint` is
+the corpus's BLAKE3 hash as Corpus::open forms it (lib.rs:32-56), hashed by
+the library's host code; checkpoints record it as data_fingerprint and a
+resume refuses a different corpus (lib.rs:338-341, 478-483).
 """
 from __future__ import annotations
 
+import ctypes
 import os
 
 import numpy as np
 
+from . import _native as N
 from .model import EOS
 from .rng import Rng
 
+FINGERPRINT_DOMAIN = b"Sejong byte corpus v1: EOS + document bytes + EOS"
+
+
+def fingerprint(documents) -> str:
+    """Corpus::open's hash (lib.rs:32-44): BLAKE3 of the domain string, then
+    per non-empty document its u64 little-endian length and its bytes."""
+    N.load()
+    state = ctypes.create_string_buffer(N.api.sj_blake3_state_bytes() + 8)
+    st = ctypes.c_void_p((ctypes.addressof(state) + 7) // 8 * 8)
+    N.api.sj_blake3_init(st)
+    N.api.sj_blake3_update(st, FINGERPRINT_DOMAIN, len(FINGERPRINT_DOMAIN))
+    for d in documents:
+        a = np.ascontiguousarray(d, dtype=np.uint8)
+        if a.size == 0:
+            continue
+        n = np.array([a.size], dtype="<u8")
+        N.api.sj_blake3_update(st, ctypes.c_void_p(n.ctypes.data), 8)
+        N.api.sj_blake3_update(st, ctypes.c_void_p(a.ctypes.data), a.size)
+    out = (ctypes.c_uint8 * 32)()
+    N.api.sj_blake3_finalize(st, out)
+    return bytes(out).hex()
+
 
 def _collect_text(path: str, files: list):
-    """collect_text (lib.rs:89-102): a file path is taken as it is; a
-    directory contributes its *.txt files, recursively."""
+    """collect_text (lib.rs:89-109): a file path is taken as it is; a
+    directory contributes its *.txt files, recursively; anything else is an
+    error."""
     if os.path.isfile(path):
         files.append(path)
     elif os.path.isdir(path):
@@ -31,6 +59,8 @@ def _collect_text(path: str, files: list):
                 _collect_text(p, files)
             elif os.path.splitext(entry)[1] == ".txt":
                 files.append(p)
+    else:
+        raise ValueError(f"corpus path does not exist: {path}")
 
 
 def _path_key(p: str):
@@ -52,6 +82,7 @@ class Corpus:
         self._flat = np.concatenate(self.documents) if self.documents else np.zeros(0, np.uint8)
         # start of each document's bytes in the concatenation of all documents
         self._flat_start = np.concatenate([[0], np.cumsum([d.size for d in self.documents])])[:-1]
+        self.fingerprint = fingerprint(self.documents)
 
     @classmethod
     def open(cls, path: str) -> "Corpus":

@@ -183,6 +183,7 @@ struct TArgs {
   bf16_t *gq[2], *gqt[2];  // dQ planes: normal [M][ldg] at columns h*64, transposed [.][ldgt] at rows h*64
   long ldg, ldgt;
   float* part;  // [group][M][2*HK*64] per-head dK | dV
+  uint32_t* cnt;  // grouped backward: the cut walks' meeting counters, PLAN_CUTS per (KV head, sequence)
   int B;        // batch (rows M = B * T)
   // cached forward (one sequence): queries at positions pos0 .. pos0+nq-1
   // in qc [nq][ldqc]; keys and values of positions 0 .. pos0+nq-1 in kc / vc
@@ -834,25 +835,25 @@ static_assert(LDS_BWD_G + 16 <= 160 * 1024 && (size_t)(GROUPED_G - 1) * 8 * 256 
 // workspace and counts itself on the walk's counter; the part that counts
 // last adds the parts' sums in part order (its own from registers: the same
 // bits whichever part comes last), writes the planes and sets the counter
-// back to zero for the next launch.  (One piece per workgroup: a workgroup
+// back to zero for the next launch.  The counters are the caller's: a
+// region of its workspace (PLAN_CUTS words per (KV head, sequence)) that is
+// zero before the first launch and that every launch leaves zero, so
+// launches on different workspaces (two models, a graph replay beside an
+// eager call) never count on each other's counters.  (One piece per workgroup: a workgroup
 // that ran several pieces in a loop held their addresses and arguments
 // across the loop and ran every walk slower.)
 constexpr int PLAN_PIECES = 128;  // pieces of both roles
 constexpr int PLAN_CUTS = 64;     // cut walks per (KV head, sequence)
 constexpr int PLAN_PARTS = 4;     // parts of a cut walk
-constexpr int PLAN_POOLS = 8;     // counter pools, taken in turn by successive launches
-constexpr int PLAN_COUNTERS = 1024;  // counters per pool: cut walks of one launch
 // piece: bit 31 set, bits 0-5 block, 6-11 / 12-17 the first / last block of
 // the walk it covers, bit 18 the role (0: dQ, 1: dK | dV), 19-26 cut-walk
 // index + 1 (0: a whole walk), 27-28 the part, 29-30 the walk's parts - 1
 struct SplitPlan {
   int ncut;    // cut walks per (KV head, sequence)
   int nslots;  // part sums per (KV head, sequence)
-  int pool;    // counter pool of this launch
   uint16_t slot0[PLAN_CUTS];  // first part-sum slot of each cut walk
   uint32_t seg[PLAN_PIECES];
 };
-__device__ uint32_t g_cut_count[PLAN_POOLS * PLAN_COUNTERS];  // zero between launches
 
 // A part's sum passes between workgroups (on different XCDs, each with its
 // own L2) through device-scope accesses, relaxed atomics at agent scope:
@@ -902,7 +903,7 @@ __device__ __forceinline__ Meet meet_at(const TArgs& a, const SplitPlan& pl, int
   const int cut = (int)((sg >> 19) & 255) - 1, part = (int)((sg >> 27) & 3), nparts = (int)((sg >> 29) & 3) + 1;
   const long pair = (long)b * a.HK + kvh;
   float* base = a.part + (pair * pl.nslots + pl.slot0[cut]) * slot;
-  return Meet{base, part, nparts, g_cut_count + pl.pool * PLAN_COUNTERS + pair * pl.ncut + cut};
+  return Meet{base, part, nparts, a.cnt + pair * PLAN_CUTS + cut};
 }
 // the walk's total of vector v (element r at off + r * stride of each
 // part's slot), parts in order: ((s0 + s1) + s2) + s3, this part's own from
@@ -1129,7 +1130,7 @@ double simulate(std::vector<Piece>& ps, long pairs, int cus) {
 // whose simulated dispatch finishes first (ties: the longer caps, fewer
 // cuts), with at most 2 nb part sums per (KV head, sequence) -- they fit
 // the workspace of the per-head partials --, PLAN_PIECES pieces,
-// PLAN_CUTS cut walks and PLAN_COUNTERS counters for the launch.
+// PLAN_CUTS cut walks per (KV head, sequence).
 // cut = false: one piece per walk (the former launch).  caps_q / caps_k > 0
 // fix the caps.
 double plan_pieces(int nb, int W, long pairs, int cus, bool cut, int caps_q, int caps_k, std::vector<Piece>& best,
@@ -1148,7 +1149,7 @@ double plan_pieces(int nb, int W, long pairs, int cus, bool cut, int caps_q, int
       std::vector<Piece> ps;
       int nc = 0, ns = 0;
       if (!cut_walks(wq, 0, cq, ps, &nc, &ns) || !cut_walks(wk, 1, ck, ps, &nc, &ns)) continue;
-      if (ns > 2 * nb || nc > PLAN_CUTS || (int)ps.size() > PLAN_PIECES || (long)nc * pairs > PLAN_COUNTERS) continue;
+      if (ns > 2 * nb || nc > PLAN_CUTS || (int)ps.size() > PLAN_PIECES) continue;
       const double t = simulate(ps, pairs, cus);
       if (best_t < 0 || t < best_t - 1e-9) {
         best_t = t;
@@ -1180,12 +1181,11 @@ int device_cus() {
 
 // The launch's plan for `pairs` (KV head, sequence) pairs on `cus` CUs,
 // searched once per shape (the search simulates every pair of caps) and
-// kept; each launch takes the next counter pool.  SJ_ATTN_CUT=0: one piece
+// kept.  SJ_ATTN_CUT=0: one piece
 // per walk (A/B comparisons); SJ_ATTN_CAPS_Q / SJ_ATTN_CAPS_K fix the caps.
 int make_plan(long t, long window, long pairs, int cus, SplitPlan& pl, int& npieces) {
   static const int cut_on = env_int("SJ_ATTN_CUT", 1), cq = env_int("SJ_ATTN_CAPS_Q", 0),
                    ck = env_int("SJ_ATTN_CAPS_K", 0);
-  static std::atomic<unsigned> next_pool{0};
   static std::mutex mu;
   static std::map<std::tuple<long, long, long, int>, std::pair<SplitPlan, int>> cache;
   const int nb = (int)(t / QB);
@@ -1223,7 +1223,6 @@ int make_plan(long t, long window, long pairs, int cus, SplitPlan& pl, int& npie
     pl = it->second.first;
     npieces = it->second.second;
   }
-  pl.pool = (int)(next_pool.fetch_add(1) % PLAN_POOLS);
   return SJ_OK;
 }
 }  // namespace
@@ -1324,22 +1323,35 @@ int sjh::attention_fwd_cached_t(void* stream, const uint16_t* q, long ldq, const
   return SJ_OK;
 }
 
+// the workspace: the per-head dK | dV partials (or the cut walks' part
+// sums), then, 256-byte aligned, the grouped launch's meeting counters
+static size_t attention_bwd_tt_partial_bytes(long batch, long t, long hq, long hk, long head_dim) {
+  const size_t b = sizeof(float) * (size_t)(hq / (hk > 0 ? hk : 1)) * (size_t)(batch * t) * (size_t)(2 * hk * head_dim);
+  return (b + 255) / 256 * 256;
+}
+
+extern "C" size_t sj_attention_bwd_tt_counter_bytes(long batch, long hk) {
+  return sizeof(uint32_t) * (size_t)PLAN_CUTS * (size_t)(batch > 0 ? batch : 0) * (size_t)(hk > 0 ? hk : 0);
+}
+
 extern "C" size_t sj_attention_bwd_tt_workspace_bytes(long batch, long t, long hq, long hk, long head_dim) {
-  return sizeof(float) * (size_t)(hq / (hk > 0 ? hk : 1)) * (size_t)(batch * t) * (size_t)(2 * hk * head_dim);
+  return attention_bwd_tt_partial_bytes(batch, t, hq, hk, head_dim) + sj_attention_bwd_tt_counter_bytes(batch, hk);
 }
 
 int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, long ldt, const uint16_t* o,
                                 long ldo, const float* lse_t, const uint16_t* do_hi, const uint16_t* do_lo, long lddo,
                                 float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
                                 const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
-                                uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
+                                uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes,
+                                uint32_t* counters) {
   if (int st = check_t(qkv, ldqkv, ldt, batch, t, hq, hk, head_dim, window)) return st;
   SJ_REQUIRE(o && lse_t && do_hi && do_lo && delta_t && g_hi && g_lo && !g_t_hi == !g_t_lo && lddo >= hq * DH &&
                  lddo % 8 == 0 && ldo % 8 == 0 && ldg >= (hq + 2 * hk) * DH && (!g_t_hi || ldgt >= batch * t) &&
                  ((uintptr_t)do_hi & 15) == 0 && ((uintptr_t)do_lo & 15) == 0 && ((uintptr_t)o & 15) == 0 &&
                  ldg % 4 == 0,
              "grouped attention backward (transposed operands): buffers");
-  const size_t need = sj_attention_bwd_tt_workspace_bytes(batch, t, hq, hk, head_dim);
+  const size_t need = counters ? attention_bwd_tt_partial_bytes(batch, t, hq, hk, head_dim)
+                               : sj_attention_bwd_tt_workspace_bytes(batch, t, hq, hk, head_dim);
   if (!workspace || workspace_bytes < need)
     return sjh::fail(SJ_ERR_CAPACITY, "attention backward: required %zu bytes, available %zu bytes", need,
                      workspace_bytes);
@@ -1354,6 +1366,8 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
   a.gq[0] = (bf16_t*)g_hi; a.gq[1] = (bf16_t*)g_lo; a.gqt[0] = (bf16_t*)g_t_hi; a.gqt[1] = (bf16_t*)g_t_lo;
   a.ldg = ldg; a.ldgt = ldgt;
   a.part = (float*)workspace;
+  a.cnt = counters ? counters
+                   : (uint32_t*)((char*)workspace + attention_bwd_tt_partial_bytes(batch, t, hq, hk, head_dim));
   a.B = (int)batch;
   if (parts & 1) {  // Delta
     const long threads = 4 * batch * t * hq;
@@ -1401,5 +1415,5 @@ extern "C" int sj_attention_bwd_tt(void* stream, const uint16_t* qkv, long ldqkv
                                    uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes) {
   return sjh::attention_bwd_tt_parts(7, stream, qkv, ldqkv, ldt, o, ldo, lse_t, do_hi, do_lo, lddo, delta_t, batch, t,
                                      hq, hk, head_dim, window, rope_table, g_hi, g_lo, ldg, g_t_hi, g_t_lo, ldgt,
-                                     workspace, workspace_bytes);
+                                     workspace, workspace_bytes, nullptr);
 }

@@ -80,6 +80,12 @@ extern "C" int sj_free(void* ptr) {
   return SJ_OK;
 }
 
+extern "C" int sj_memory_info(size_t* free_bytes, size_t* total_bytes) {
+  SJ_REQUIRE(free_bytes && total_bytes, "memory info: null");
+  SJ_HIP(hipMemGetInfo(free_bytes, total_bytes));
+  return SJ_OK;
+}
+
 extern "C" int sj_upload(void* dst, const void* src, size_t bytes) {
   SJ_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
   return SJ_OK;

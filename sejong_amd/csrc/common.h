@@ -134,11 +134,15 @@ int attention_fwd_cached_t(void* stream, const uint16_t* q, long ldq, const uint
 int attention_kv_reduce(hipStream_t s, const float* part, long group, long M, long T, long N, long KV,
                         const float* rope, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* gt_hi, uint16_t* gt_lo,
                         long ldgt);
+// parts: 1 Delta, 2 dQ | dK dV, 4 the group reduce; counters: the grouped
+// launch's meeting counters (sj_attention_bwd_tt_counter_bytes, zero before
+// the first call and left zero by each), null for the workspace's own tail
 int attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, long ldqkv, long ldt, const uint16_t* o,
                            long ldo, const float* lse_t, const uint16_t* do_hi, const uint16_t* do_lo, long lddo,
                            float* delta_t, long batch, long t, long hq, long hk, long head_dim, long window,
                            const float* rope_table, uint16_t* g_hi, uint16_t* g_lo, long ldg, uint16_t* g_t_hi,
-                           uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes);
+                           uint16_t* g_t_lo, long ldgt, void* workspace, size_t workspace_bytes,
+                           uint32_t* counters);
 // Profiling hook of the step driver: while one of its ops is timed
 // (sj_model_profile), the op's GEMM launch notes the kernel's name and, in
 // kernel timing mode (k0 set), launches it with hipExtLaunchKernel recording

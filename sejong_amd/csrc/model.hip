@@ -35,6 +35,7 @@
 // normalised activations, O and h also transposed ([cols][rows], the A
 // operands of the dW GEMMs), and carries the fp32 gradients dY that feed
 // GEMMs as hi/lo bf16 planes in both orientations (dX and dW operands).
+#include <algorithm>
 #include <math.h>
 #include <stddef.h>
 #include <stdio.h>
@@ -294,6 +295,10 @@ struct sj_model {
   std::vector<long> slot_close, slot_fn, slot_an;  // per stage / per layer (-1: row kernel)
   std::vector<float*> slot_ptr;
   void* ws2 = nullptr;
+  // the grouped attention backward's meeting counters (zeroed at creation;
+  // every launch leaves them zero): this model's own, not the workspace's,
+  // which the other ops of the stream overwrite between launches
+  uint32_t* attn_cnt = nullptr;
   // activations
   std::vector<void*> x;  // L+1 residual stream tensors
   std::vector<void*> z, qkv, o, x1, z2, gg, uu, hh;
@@ -995,7 +1000,7 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
           OP(nm, sjh::attention_bwd_tt_parts(part, s, qkv, NQ, ldt, (const uint16_t*)m->o[l], d, m->lset[l],
                                              m->dop[0], m->dop[1], d, m->deltat, m->B, S.T, S.HQ, S.HK, S.Dh,
                                              S.window, S.rope, NP(KQ, p)[0], NP(KQ, p)[1], NQ, TP(KQ, p)[0],
-                                             TP(KQ, p)[1], ldt, ws, wsb));
+                                             TP(KQ, p)[1], ldt, ws, wsb, m->attn_cnt));
         else
           OP(nm, sjh::attention_bwd_p_parts(part, s, qkv, NQ, qkv + d, NQ, qkv + d + J, NQ, (const uint16_t*)m->o[l], d,
                                             m->lse[l], m->dO, d, m->delta, m->B, S.T, S.HQ, S.HK, S.Dh, S.rope,
@@ -1863,6 +1868,12 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   m->ws_bytes = ws;
   ALLOC(m->ws, ws);
   if (m->planes) ALLOC(m->ws2, ws);
+  size_t cnt_bytes = 0;
+  for (const Stage& S : m->stages) {
+    const size_t c = sj_attention_bwd_tt_counter_bytes(m->B, S.HK);
+    cnt_bytes = c > cnt_bytes ? c : cnt_bytes;
+  }
+  if (m->planes) ALLOC(m->attn_cnt, cnt_bytes);
 #undef ALLOC
   if (hipHostMalloc((void**)&m->step_host, sizeof(sj_adam_step) * sj_model::RING, 0) != hipSuccess)
     return fail_cleanup(sjh::fail(SJ_ERR_CAPACITY, "model: pinned step buffer"));
@@ -1879,6 +1890,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (e == hipSuccess && p) e = hipMemsetAsync(p, 0, P * 4, s);
   if (e == hipSuccess && m->mirror) e = hipMemsetAsync(m->mirror, 0, P * 2, s);
   if (e == hipSuccess && m->mirror_t) e = hipMemsetAsync(m->mirror_t, 0, P * 2, s);
+  if (e == hipSuccess && m->attn_cnt) e = hipMemsetAsync(m->attn_cnt, 0, cnt_bytes, s);
   // padding columns [M, ldt) of the transposed activations stay zero
   for (long l = 0; l < m->L && m->planes; l++) {
     const Stage& S = m->stages[m->layers[l].stage];
@@ -2363,18 +2375,28 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
 
 // ------------------------------------------------------------ KV cache
 // Model::new_cache / forward_cached (model lib.rs:36-50, 359-394;
-// architecture.rs:428-533, 758-799): per layer the keys and values of one
-// sequence, [capacity][HK * head_dim] in the compute dtype, and scratch for
+// architecture.rs:395-533, 651-799): per layer the keys and values of one
+// sequence, [positions][HK * head_dim] in the compute dtype, and scratch for
 // up to `capacity` new rows.  A call runs the blocks over the new tokens at
-// positions length .. length + n - 1 with the same kernels as the training
-// forward (RoPE rows of a table over the capacity, the cached attention
-// kernels reading the cache), so each row is computed exactly as in the full
+// their positions with the same kernels as the training forward (RoPE rows
+// of a table over the stage's positions, the cached attention kernels
+// reading the cache), so each row is computed exactly as in the full
 // forward; then the final norm and the fp32 head on the last row.
+//
+// The hierarchical model (HierarchyCache, architecture.rs:399-412) keeps
+// one cache per stage: the encoder's and decoder's over the bytes
+// (`capacity` positions), the global stage's over the patches
+// (ceil(capacity / patch) positions), plus the state of the patch being
+// filled: its encoded rows (the reference keeps their fp32 sum, patch_sum,
+// and their count; keeping the rows lets the completed patch be pooled by
+// the full forward's own patch_pool, the same fp32 sum in the same order)
+// and the decoder context of the last completed patch (global_context).
 struct sj_cache {
   sj_model* m = nullptr;
   long capacity = 0, length = 0;
-  std::vector<void*> keys, values;  // [layer] -> [capacity][J]
-  float* rope = nullptr;            // [capacity][Dh/2] (cos, sin)
+  std::vector<void*> keys, values;  // [layer] -> [positions of its stage][J]
+  std::vector<long> scap;           // [stage] positions its cache holds
+  std::vector<float*> rope;         // [stage] RoPE table [scap][Dh/2] (cos, sin)
   void *x[2] = {}, *z = nullptr, *q = nullptr, *o = nullptr, *x1 = nullptr, *z2 = nullptr;
   void *gg = nullptr, *uu = nullptr, *hh = nullptr, *hn = nullptr;
   int32_t* ids = nullptr;
@@ -2384,6 +2406,15 @@ struct sj_cache {
   uint16_t *mlog = nullptr, *mzp = nullptr, *myp = nullptr;
   int32_t *mids = nullptr, *mcnt = nullptr, *moff = nullptr, *mps = nullptr, *mpp = nullptr;
   float* mwts = nullptr;
+  // hierarchical: encoded bytes (encoder_norm output), the filling patch's
+  // encoded rows [patch][de], pooled patches, the global stage's normed
+  // output, decoder contexts of the patches and of the BOS row, the
+  // broadcast contexts, encoder_to_decoder, decoder_norm and
+  // output_projection outputs
+  void *enc = nullptr, *prow = nullptr, *pooled = nullptr, *gout = nullptr, *ctxs = nullptr, *bosd = nullptr;
+  void *gctx = nullptr, *zb = nullptr, *bytes = nullptr, *dec = nullptr, *opo = nullptr;
+  long pcount = 0;       // bytes of the filling patch (patch_count)
+  bool has_ctx = false;  // gctx holds global_context
   std::vector<void*> allocations;
 };
 
@@ -2400,16 +2431,18 @@ int calloc_(sj_cache* c, void** p, size_t bytes) {
   return hipMemset(*p, 0, bytes) == hipSuccess ? SJ_OK : sjh::fail(SJ_ERR_HIP, "cache allocation: clear");
 }
 
-// the blocks of the dense (or MoE) stage over n new rows at offset L; `top`
-// receives the index of the stage output in c->x
-int cached_blocks(sj_model* m, sj_cache* c, long n, long L, int& top) {
-  const Stage& S = m->stages[0];
+// cached_blocks (architecture.rs:474-533): the blocks of stage si over n
+// new rows in c->x[0] at positions L .. L + n - 1 of the stage's cache;
+// then the stage's closing norm into `out` (the encoder, global or decoder
+// norm, or the final norm of a one-stage model)
+int cached_blocks(sj_model* m, sj_cache* c, int si, long n, long L, void* out) {
+  const Stage& S = m->stages[si];
   hipStream_t s = m->stream;
-  const long d = S.d, J = S.J, F = S.F, cap = c->capacity;
+  const long d = S.d, J = S.J, F = S.F, cap = c->scap[si];
   const int dt = m->dt;
   const size_t es = m->esz;
   const float eps = m->c.norm_epsilon;
-  const float* rope = c->rope + L * S.Dh;  // row r of this view is position L + r
+  const float* rope = c->rope[si] + L * S.Dh;  // row r of this view is position L + r
   const long rope_t = cap - L;
   int cur = 0;
   for (long l = S.first; l < S.first + S.count; l++) {
@@ -2460,37 +2493,145 @@ int cached_blocks(sj_model* m, sj_cache* c, long n, long L, int& top) {
     }
     cur ^= 1;
   }
-  top = cur;
+  TRY(sj_rmsnorm_fwd(s, c->x[cur], dt, wc(m, S.norm), dt, out, n, d, eps));
+  return SJ_OK;
+}
+
+// the embedding of n tokens (c->ids from row `at`) into c->x[0]
+int cached_embed(sj_model* m, sj_cache* c, long at, long n) {
+  return sj_embedding_fwd(m->stream, wc(m, m->emb), m->dt, c->ids + at, c->x[0], m->dt, n, m->stages[0].d);
+}
+
+// the decoder side of hidden_from_encoded for n bytes at position L whose
+// encoded rows are in c->enc and whose broadcast contexts are in c->zb:
+// encoder_to_decoder + contexts, the decoder stage, output_projection and
+// the final norm into c->hn (architecture.rs:601-626, 690-725)
+int cached_decoder(sj_model* m, sj_cache* c, long n, long L) {
+  hipStream_t s = m->stream;
+  const int dt = m->dt;
+  const Stage &E = m->stages[0], &D = m->stages[2];
+  const long de = E.d, dd = D.d, dg = m->stages[1].d;
+  TRY(sj_gemm(s, 0, 0, n, dd, de, c->enc, dt, de, wc(m, m->h_e2d), dt, dd, c->bytes, dt, dd, 0, nullptr, 0));
+  TRY(sj_add(s, c->bytes, dt, c->zb, dt, c->x[0], dt, n * dd, 1.f));
+  TRY(cached_blocks(m, c, 2, n, L, c->dec));
+  TRY(sj_gemm(s, 0, 0, n, dg, dd, c->dec, dt, dd, wc(m, m->h_op), dt, dg, c->opo, dt, dg, 0, nullptr, 0));
+  return sj_rmsnorm_fwd(s, c->opo, dt, wc(m, m->final_norm), dt, c->hn, n, dg, m->c.norm_epsilon);
+}
+
+// hierarchical_prefill (architecture.rs:534-650): a fresh cache and at least
+// one patch of bytes: the whole stack over the n bytes as the full forward
+// runs it (the partial last patch pooled over its own bytes and run
+// through the global stage at its slot, which its completion rewrites);
+// then global_context = the last completed patch's context (or the BOS
+// row's) and the filling patch's encoded rows
+int hierarchical_prefill(sj_model* m, sj_cache* c, long n, long& last) {
+  hipStream_t s = m->stream;
+  const int dt = m->dt;
+  const size_t es = m->esz;
+  const long P = m->P, de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d;
+  const long np = (n + P - 1) / P, done = n / P;
+  TRY(cached_embed(m, c, 0, n));
+  TRY(cached_blocks(m, c, 0, n, 0, c->enc));
+  TRY(sj_patch_pool(s, c->enc, dt, 1, n, de, P, c->pooled));
+  TRY(sj_gemm(s, 0, 0, np, dg, de, c->pooled, dt, de, wc(m, m->h_e2g), dt, dg, c->x[0], dt, dg, 0, nullptr, 0));
+  TRY(cached_blocks(m, c, 1, np, 0, c->gout));
+  TRY(sj_gemm(s, 0, 0, np, dd, dg, c->gout, dt, dg, wc(m, m->h_g2d), dt, dd, c->ctxs, dt, dd, 0, nullptr, 0));
+  TRY(sj_gemm(s, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, c->bosd, dt, dd, 0, nullptr, 0));
+  TRY(sj_patch_broadcast(s, c->ctxs, c->bosd, dt, 1, n, dd, P, c->zb));
+  TRY(cached_decoder(m, c, n, 0));
+  last = n - 1;
+  const void* ctx = done == 0 ? c->bosd : (const char*)c->ctxs + (done - 1) * dd * es;
+  SJ_HIP(hipMemcpyAsync(c->gctx, ctx, (size_t)dd * es, hipMemcpyDeviceToDevice, s));
+  c->has_ctx = true;
+  c->pcount = n % P;
+  if (c->pcount)
+    SJ_HIP(hipMemcpyAsync(c->prow, (const char*)c->enc + done * P * de * es, (size_t)c->pcount * de * es,
+                          hipMemcpyDeviceToDevice, s));
+  return SJ_OK;
+}
+
+// hidden_cached's hierarchical loop (architecture.rs:667-783): the bytes in
+// chunks that end at patch boundaries; each chunk through the encoder at
+// its positions, the decoder with the filling patch's context (the last
+// completed patch's, or the BOS row's), and its encoded rows appended to
+// the filling patch; a completed patch is pooled, run through the global
+// stage at its patch position and gives the next context.  `last`: the
+// row of c->hn that holds the last byte's output (the last chunk's)
+int hierarchical_cached(sj_model* m, sj_cache* c, long n, long& last) {
+  hipStream_t s = m->stream;
+  const int dt = m->dt;
+  const size_t es = m->esz;
+  const long P = m->P, de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d;
+  if (c->length == 0 && n >= P) return hierarchical_prefill(m, c, n, last);
+  if (!c->has_ctx) {
+    TRY(sj_gemm(s, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, c->gctx, dt, dd, 0, nullptr, 0));
+    c->has_ctx = true;
+  }
+  long i = 0;
+  while (i < n) {
+    const long count = std::min(P - c->pcount, n - i), pos = c->length + i;
+    TRY(cached_embed(m, c, i, count));
+    TRY(cached_blocks(m, c, 0, count, pos, c->enc));
+    // every row of the chunk lies in one patch: its broadcast row is the
+    // context (the broadcast's first-patch rows take the BOS argument)
+    TRY(sj_patch_broadcast(s, c->gctx, c->gctx, dt, 1, count, dd, P, c->zb));
+    TRY(cached_decoder(m, c, count, pos));
+    last = count - 1;
+    SJ_HIP(hipMemcpyAsync((char*)c->prow + c->pcount * de * es, c->enc, (size_t)count * de * es,
+                          hipMemcpyDeviceToDevice, s));
+    c->pcount += count;
+    if (c->pcount == P) {
+      TRY(sj_patch_pool(s, c->prow, dt, 1, P, de, P, c->pooled));
+      TRY(sj_gemm(s, 0, 0, 1, dg, de, c->pooled, dt, de, wc(m, m->h_e2g), dt, dg, c->x[0], dt, dg, 0, nullptr, 0));
+      TRY(cached_blocks(m, c, 1, 1, pos / P, c->gout));
+      TRY(sj_gemm(s, 0, 0, 1, dd, dg, c->gout, dt, dg, wc(m, m->h_g2d), dt, dd, c->gctx, dt, dd, 0, nullptr, 0));
+      c->pcount = 0;
+    }
+    i += count;
+  }
   return SJ_OK;
 }
 }  // namespace
 
 extern "C" int sj_cache_create(sj_model* m, long capacity, sj_cache** out) {
   SJ_REQUIRE(m && out && capacity > 0, "new_cache: arguments");
-  SJ_REQUIRE(!m->hier && !m->value_n, "new_cache: the cached forward covers the byte language models (dense, MoE)");
-  const Stage& S = m->stages[0];
-  SJ_REQUIRE(m->planes ? S.attn_tt : m->dt == SJ_F32,
-             "new_cache: the cached forward needs the MFMA-layout attention (bf16) or fp32 storage");
+  SJ_REQUIRE(!m->value_n, "new_cache: the cached forward covers the byte language models (dense, MoE, hierarchical)");
+  for (const Stage& S : m->stages)
+    SJ_REQUIRE(m->planes ? S.attn_tt : m->dt == SJ_F32,
+               "new_cache: the cached forward needs the MFMA-layout attention (bf16) or fp32 storage");
   sj_cache* c = new sj_cache();
   c->m = m;
   c->capacity = capacity;
   const size_t es = m->esz;
-  const long d = S.d, J = S.J, F = S.F;
+  long dmax = m->d, fmax = 0;
+  for (const Stage& S : m->stages) {
+    dmax = std::max(dmax, S.d);
+    fmax = std::max(fmax, S.F);
+  }
   int st = SJ_OK;
   auto A = [&](void** p, size_t bytes) {
     if (!st) st = calloc_(c, p, bytes);
   };
+  // positions per stage: the bytes, or the patches for the global stage
+  c->scap.assign(m->stages.size(), capacity);
+  if (m->hier) c->scap[1] = (capacity + m->P - 1) / m->P;
+  c->rope.assign(m->stages.size(), nullptr);
   c->keys.assign(m->L, nullptr);
   c->values.assign(m->L, nullptr);
-  for (long l = 0; l < m->L; l++) {
-    A(&c->keys[l], (size_t)capacity * J * es);
-    A(&c->values[l], (size_t)capacity * J * es);
+  for (size_t si = 0; si < m->stages.size(); si++) {
+    const Stage& S = m->stages[si];
+    for (long l = S.first; l < S.first + S.count; l++) {
+      A(&c->keys[l], (size_t)c->scap[si] * S.J * es);
+      A(&c->values[l], (size_t)c->scap[si] * S.J * es);
+    }
+    A((void**)&c->rope[si], (size_t)c->scap[si] * S.Dh * 4);
   }
-  A((void**)&c->rope, (size_t)capacity * S.Dh * 4);
-  for (void** p : {&c->x[0], &c->x[1], &c->z, &c->q, &c->o, &c->x1, &c->z2, &c->hn}) A(p, (size_t)capacity * d * es);
+  for (void** p : {&c->x[0], &c->x[1], &c->z, &c->q, &c->o, &c->x1, &c->z2, &c->hn})
+    A(p, (size_t)capacity * dmax * es);
   if (m->E) {
+    const Stage& S = m->stages[0];
     c->mcap = sj_route_pack_capacity(capacity * m->K, m->E);
-    const long E = m->E, K = m->K, mc = c->mcap;
+    const long E = m->E, K = m->K, mc = c->mcap, d = S.d, F = S.F;
     A((void**)&c->mlog, (size_t)capacity * E * 2);
     A((void**)&c->mids, (size_t)capacity * K * 4);
     A((void**)&c->mwts, (size_t)capacity * K * 4);
@@ -2502,11 +2643,26 @@ extern "C" int sj_cache_create(sj_model* m, long capacity, sj_cache** out) {
     A((void**)&c->myp, (size_t)mc * d * 2);
     for (void** p : {&c->gg, &c->uu, &c->hh}) A(p, (size_t)mc * F * es);
   } else {
-    for (void** p : {&c->gg, &c->uu, &c->hh}) A(p, (size_t)capacity * F * es);
+    for (void** p : {&c->gg, &c->uu, &c->hh}) A(p, (size_t)capacity * fmax * es);
+  }
+  if (m->hier) {
+    const long de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d, np = c->scap[1];
+    A(&c->enc, (size_t)capacity * de * es);
+    A(&c->prow, (size_t)m->P * de * es);
+    A(&c->pooled, (size_t)np * de * es);
+    A(&c->gout, (size_t)np * dg * es);
+    A(&c->ctxs, (size_t)np * dd * es);
+    A(&c->bosd, (size_t)dd * es);
+    A(&c->gctx, (size_t)dd * es);
+    A(&c->zb, (size_t)capacity * dd * es);
+    A(&c->bytes, (size_t)capacity * dd * es);
+    A(&c->dec, (size_t)capacity * dd * es);
+    A(&c->opo, (size_t)capacity * dg * es);
   }
   A((void**)&c->ids, (size_t)capacity * 4);
   A((void**)&c->logits, (size_t)m->Vp * 4);
-  if (!st) st = sj_rope_table(m->stream, c->rope, capacity, S.Dh, m->c.rope_theta);
+  for (size_t si = 0; si < m->stages.size() && !st; si++)
+    st = sj_rope_table(m->stream, c->rope[si], c->scap[si], m->stages[si].Dh, m->c.rope_theta);
   if (!st && hipStreamSynchronize(m->stream) != hipSuccess) st = sjh::fail(SJ_ERR_HIP, "new_cache: sync");
   if (st) {
     sj_cache_destroy(c);
@@ -2524,9 +2680,12 @@ extern "C" int sj_cache_destroy(sj_cache* c) {
   return SJ_OK;
 }
 
+// HierarchyCache::reset (architecture.rs:406-412) with the length
 extern "C" int sj_cache_reset(sj_cache* c) {
   SJ_REQUIRE(c, "cache reset: null");
   c->length = 0;
+  c->pcount = 0;
+  c->has_ctx = false;
   return SJ_OK;
 }
 
@@ -2538,17 +2697,19 @@ extern "C" int sj_model_forward_cached(sj_model* m, sj_cache* c, const int32_t* 
     SJ_REQUIRE(tokens[i] >= 0 && tokens[i] <= 256 && tokens[i] < m->V, "input tokens must be bytes or EOS");
   SJ_REQUIRE(c->length + n <= c->capacity, "KV cache context limit reached");
   hipStream_t s = m->stream;
-  const Stage& S = m->stages[0];
-  const long d = S.d, L = c->length;
+  const long d = m->d;
   const int dt = m->dt;
   if (m->mt_stale) TRY(transpose_mirror(m));  // weights updated since the last forward
   SJ_HIP(hipMemcpyAsync(c->ids, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
-  TRY(sj_embedding_fwd(s, wc(m, m->emb), dt, c->ids, c->x[0], dt, n, d));
-  int top = 0;
-  TRY(cached_blocks(m, c, n, L, top));
-  TRY(sj_rmsnorm_fwd(s, c->x[top], dt, wc(m, S.norm), dt, c->hn, n, d, m->c.norm_epsilon));
+  long row = n - 1;  // the row of c->hn that holds the last token's output
+  if (m->hier) {
+    TRY(hierarchical_cached(m, c, n, row));
+  } else {
+    TRY(cached_embed(m, c, 0, n));
+    TRY(cached_blocks(m, c, 0, n, c->length, c->hn));
+  }
   // the last row, cast to F32, times the fp32 output matrix (model lib.rs:370-371)
-  const char* last = (const char*)c->hn + (n - 1) * d * m->esz;
+  const char* last = (const char*)c->hn + row * d * m->esz;
   if (m->lm_planes)
     TRY(sj_gemm_planes(s, 1, m->Vp, d, (const uint16_t*)last, nullptr, d, m->hp[2], m->hp[3], d, c->logits, SJ_F32,
                        m->Vp, 0, nullptr, 0));

@@ -293,6 +293,13 @@ class Cache:
     def reset(self):
         N.api.sj_cache_reset(self.h)
 
+    def logits(self) -> np.ndarray:
+        """The fp32 logits the last forward_cached left (synchronises)."""
+        self.model.synchronize()
+        out = np.empty(VOCAB, np.float32)
+        N.api.sj_download(_np_ptr(out), ctypes.c_void_p(self.dev), out.nbytes)
+        return out
+
     def close(self):
         if self.h:
             N.api.sj_cache_destroy(self.h)
@@ -481,15 +488,14 @@ class Model:
         """Model::new_cache (model lib.rs:359-361): capacity = context."""
         return Cache(self, self.mc.context if capacity is None else capacity)
 
-    def forward_cached(self, tokens, cache: "Cache") -> np.ndarray:
+    def forward_cached(self, tokens, cache: "Cache", read: bool = True) -> np.ndarray | None:
         """Model::forward_cached (model lib.rs:362-372): the fp32 logits of
-        the last of `tokens` after running them at the cache's positions."""
+        the last of `tokens` after running them at the cache's positions.
+        read=False only enqueues the call (no synchronisation): the logits
+        stay on the device until cache.logits()."""
         t = np.ascontiguousarray(tokens, dtype=np.int32).ravel()
         N.api.sj_model_forward_cached(self.h, cache.h, _np_ptr(t), t.size, ctypes.c_void_p(cache.dev))
-        self.synchronize()
-        out = np.empty(VOCAB, np.float32)
-        N.api.sj_download(_np_ptr(out), ctypes.c_void_p(cache.dev), out.nbytes)
-        return out
+        return cache.logits() if read else None
 
     def read_loss(self) -> tuple[float, float]:
         loss, norm = ctypes.c_double(), ctypes.c_double()

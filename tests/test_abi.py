@@ -232,3 +232,28 @@ def test_attention_backward_pieces_cover_every_walk_once(t, window, pairs):
     if (t, window, pairs) == (512, 0, 16):  # cfg2: the longest dK | dV walks cut, none of dQ
         assert ncut >= 4 and all(p["role"] == 1 for p in pieces if p["cut"] >= 0)
         assert _dispatch_finish(pieces, pairs, 256) < 0.85 * _dispatch_finish(whole, pairs, 256)
+
+
+@pytest.mark.parametrize("B,T,HQ,HK", [(8, 512, 6, 2), (1, 1024, 3, 1), (2, 256, 6, 2), (16, 1024, 12, 4)])
+def test_attention_backward_workspace_accounting(B, T, HQ, HK):
+    """The grouped attention backward's workspace (no device needed): the
+    part sums of every cut walk of every (KV head, sequence) pair fit the
+    partial region (12288 floats per part: 16 per thread of the 768-thread
+    workgroup), and the meeting counters (64 words per pair, cut index
+    pair * 64 + cut) sit past it, 256-byte aligned, in the last
+    sj_attention_bwd_tt_counter_bytes bytes, which grow with the pairs so
+    that no two pairs, and no two workspaces, share a counter."""
+    from sejong_amd import _native as N
+    lib = N.load()
+    Dh = 64
+    pairs = B * HK
+    cnt = lib.sj_attention_bwd_tt_counter_bytes(B, HK)
+    total = lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh)
+    assert cnt == 4 * 64 * pairs
+    partial = 4 * (HQ // HK) * B * T * 2 * HK * Dh
+    assert total == (partial + 255) // 256 * 256 + cnt
+    n, ncut, pieces = _attention_plan(lib, T, 0, pairs)
+    assert n > 0 and 0 <= ncut <= 64
+    slots = sum(p["nparts"] for p in pieces if p["cut"] >= 0 and p["part"] == 0)
+    if HQ == 3 * HK:  # the grouped launch: part sums of 12288 floats
+        assert pairs * slots * 12288 * 4 <= partial

@@ -186,3 +186,26 @@ def test_half_precision_mapping_is_reported(tmp_path):
         mc.precision = "f32"
         C.save_arrays(tmp_path / "b", mc, params, 1)
         assert C.load_arrays(tmp_path / "b")[0].precision == "f32"
+
+
+def test_data_fingerprint_written_and_checked_on_resume(tmp_path):
+    """save_training writes the corpus fingerprint as data_fingerprint
+    (train lib.rs:472-491) and a resume refuses a checkpoint of another
+    corpus (lib.rs:338-341): the manifest carries Corpus.fingerprint, the
+    same corpus passes check_resume_corpus and a different one fails."""
+    from sejong_amd.corpus import Corpus
+    rng = np.random.default_rng(5)
+    (tmp_path / "a").mkdir()
+    (tmp_path / "a" / "x.txt").write_bytes(rng.integers(0, 256, 3000, dtype=np.uint8).tobytes())
+    (tmp_path / "b").mkdir()
+    (tmp_path / "b" / "x.txt").write_bytes(rng.integers(0, 256, 3000, dtype=np.uint8).tobytes())
+    ca, cb = Corpus.open(tmp_path / "a"), Corpus.open(tmp_path / "b")
+    assert ca.fingerprint != cb.fingerprint and len(ca.fingerprint) == 64
+    mc, _ = _small_cfgs()
+    d = tmp_path / "ck"
+    C.save_arrays(d, mc, init_params(mc, std=0.02), 3, data_fingerprint=ca.fingerprint)
+    m = C.load_manifest(d)
+    assert m["data_fingerprint"] == ca.fingerprint
+    C.check_resume_corpus(m, ca)
+    with pytest.raises(ValueError, match="resume corpus differs from checkpoint"):
+        C.check_resume_corpus(m, cb)

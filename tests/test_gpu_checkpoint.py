@@ -21,16 +21,23 @@ def _pair(mc, tc, seed=0):
 
 
 def test_adamw_resume_is_bit_exact(tmp_path):
+    """... with the training corpus's fingerprint in the manifest and the
+    resume's corpus check (train lib.rs:338-341, 478-483)."""
+    from sejong_amd.corpus import Corpus
     from sejong_amd.model import ModelConfig, TrainConfig
     mc = ModelConfig(width=128, layers=2, heads=2, kv_heads=1, ffn_width=256, context=128, precision="bf16")
     tc = TrainConfig(sequence=128, batch=2, learning_rate=1e-3, weight_decay=0.1)
+    (tmp_path / "data").mkdir()
+    (tmp_path / "data" / "d.txt").write_bytes(np.random.default_rng(1).integers(0, 256, 4000, np.uint8).tobytes())
+    corpus = Corpus.open(tmp_path / "data")
     a, b = _pair(mc, tc)
     try:
         for _ in range(2):
             a.train_step()
-        a.save(tmp_path / "ck", rng_state=77, half_as_bf16=True)
-        man = b.load(tmp_path / "ck", half_as_bf16=True)
+        a.save(tmp_path / "ck", rng_state=77, half_as_bf16=True, corpus=corpus)
+        man = b.load(tmp_path / "ck", half_as_bf16=True, corpus=corpus)
         assert man["step"] == 2 and man["rng_state"] == 77 and b.steps() == 2
+        assert man["data_fingerprint"] == corpus.fingerprint
         ma, va, sa = a.get_adam_state()
         mb, vb, sb = b.get_adam_state()
         np.testing.assert_array_equal(ma, mb); np.testing.assert_array_equal(va, vb); assert sa == sb == 2

@@ -413,7 +413,10 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
                          dK.p, KV, dV.p, KV, De.p, BF, B, T, HQ, HK, Dh, W, tab.p)
     Gh, Gl, Th, Tl = empty(M * NG, "bf16"), empty(M * NG, "bf16"), zeros(NG * ldt, "bf16"), zeros(NG * ldt, "bf16")
     DT = zeros(HQ * ldt)
-    ws = empty(max(lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
+    # the workspace ends with the cut walks' meeting counters: zero before
+    # the first call, and left zero by every call
+    ws = zeros(max(lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh), 256), "u8")
+    ncnt = lib.sj_attention_bwd_tt_counter_bytes(B, HK)
     api.sj_attention_bwd_tt(None, QKV.p, ldq, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DT.p,
                             B, T, HQ, HK, Dh, W, tab.p, Gh.p, Gl.p, NG, Th.p, Tl.p, ldt, ws.p, ws.nbytes)
     sync()
@@ -449,6 +452,7 @@ def test_attention_tt_against_row_path_and_oracle(api, lib, B, T, HQ, HK, W):
             sync()
             np.testing.assert_array_equal(G3h.host(), G2h.host())
             np.testing.assert_array_equal(G3l.host(), G2l.host())
+        assert not ws.host()[ws.nbytes - ncnt:].any(), "meeting counters not back at zero"
         hi, lo = G2h.host().reshape(M, NG), G2l.host().reshape(M, NG)
         got = hi + lo
     else:
@@ -504,3 +508,60 @@ def test_gemm_planes_split_out(api):
     got = Dl.host().reshape(N // 64, ldd)
     assert np.abs(got[:, :M] - want).max() <= 1e-5 * np.abs(want).max()
     assert np.all(got[:, M:] == 0)
+
+
+def _raw(api, buf):
+    """The buffer's bytes, without conversion."""
+    out = np.empty(buf.nbytes, np.uint8)
+    api.sj_download(ctypes.c_void_p(out.ctypes.data), buf.p, buf.nbytes)
+    return out
+
+
+def test_attention_tt_cut_walks_repeat_bits(api, lib):
+    """The grouped backward at the bench's shape (cfg2: B 8, T 512, GQA 6/2),
+    whose plan cuts the longest dK | dV walks into parts that meet through
+    device-scope sums and a counter: 200 launches, alternating between two
+    workspaces (each with its own counters), give the same bits every time,
+    and both workspaces' counters are zero afterwards.  A stale read of a
+    part's sum, or a counter shared between launches, would change the
+    planes of a cut walk."""
+    B, T, HQ, HK, W, Dh = 8, 512, 6, 2, 0, 64
+    rng = np.random.default_rng(2024)
+    M = B * T; N = HQ * Dh; KV = HK * Dh; NG = N + 2 * KV
+    ldq, ldt = NG, M
+    segs = (ctypes.c_uint32 * 128)()
+    ncut = ctypes.c_int()
+    n = lib.sj_attention_bwd_plan(T, W, B * HK, 256, segs, 128, ctypes.byref(ncut))
+    assert n > 0 and ncut.value > 0, "the bench shape's plan must cut walks for this test to mean anything"
+    qkv = rnd((M, NG), "bf16", rng)
+    QKV = dev(qkv, "bf16")
+    O2, L2, LT = empty(M * N, "bf16"), empty(M * HQ), zeros(HQ * ldt)
+    api.sj_attention_fwd_tt(None, QKV.p, ldq, ldt, B, T, HQ, HK, Dh, W, O2.p, N, L2.p, LT.p, None, 0)
+    do = rng.normal(0, 1e-4, (M, N)).astype(np.float32).astype(np.float64)
+    dh = O.round_to(do, "bf16"); dl = O.round_to(do - dh, "bf16")
+    DH_, DL_ = dev(dh, "bf16"), dev(dl, "bf16")
+    tab = empty(T * Dh)
+    api.sj_rope_table(None, tab.p, T, Dh, cf(10000.0))
+    DT = zeros(HQ * ldt)
+    wsb = lib.sj_attention_bwd_tt_workspace_bytes(B, T, HQ, HK, Dh)
+    ncnt = lib.sj_attention_bwd_tt_counter_bytes(B, HK)
+    wss = [zeros(wsb, "u8"), zeros(wsb, "u8")]
+    Gh, Gl = empty(M * NG, "bf16"), empty(M * NG, "bf16")
+    first = None
+    print(f"[attention_tt repeat] B={B} T={T} HQ={HQ} HK={HK}: {n} pieces, {ncut.value} cut walks per pair",
+          flush=True)
+    for it in range(200):
+        ws = wss[it & 1]
+        api.sj_attention_bwd_tt(None, QKV.p, ldq, ldt, O2.p, N, LT.p, DH_.p, DL_.p, N, DT.p, B, T, HQ, HK, Dh, W,
+                                tab.p, Gh.p, Gl.p, NG, None, None, 0, ws.p, ws.nbytes)
+        sync()
+        got = (_raw(api, Gh), _raw(api, Gl))
+        if first is None:
+            first = got
+            assert np.any(got[0]), "planes written"
+        else:
+            assert np.array_equal(got[0], first[0]) and np.array_equal(got[1], first[1]), f"bits differ at launch {it}"
+        if it % 50 == 49:
+            print(f"[attention_tt repeat] {it + 1} launches identical", flush=True)
+    for ws in wss:
+        assert not _raw(api, ws)[wsb - ncnt:].any(), "meeting counters not back at zero"

@@ -148,7 +148,8 @@ def test_cfg3_full_configuration_against_oracle():
     4 heads, FFN 768, window 128; T = 1024 bytes; weights N(0, 0.02)) with
     the batch cut from 8 to 2 sequences to bound the FP64 oracle's time:
     the backward recomputed in FP64 from the device's stored activations,
-    loss and every gradient within 1e-3 relative."""
+    loss and every gradient within 1e-3 relative; and the loss within 1e-3
+    of the oracle's loss from its own bf16 forward (no device values)."""
     from sejong_amd.model import Model, byte_batch, config, init_params
     from sejong_amd.rng import Rng
     mc, tc = config("cfg3")
@@ -172,6 +173,11 @@ def test_cfg3_full_configuration_against_oracle():
         ref_acts = H.model_forward(cfg, p64, ids, "bf16")
         for k in ref_acts:
             assert rel(dev[k], ref_acts[k]) < 3e-2, (k, rel(dev[k], ref_acts[k]))
+        # the loss gate unconditioned: the oracle's loss from its own forward
+        rows, _ = O.cross_entropy(ref_acts["logits"].reshape(-1, O.VOCAB), tg, 1.0)
+        lu = float(np.mean(rows))
+        print(f"[cfg3] loss {loss:.6f} vs the oracle's own forward {lu:.6f}", flush=True)
+        assert abs(loss - lu) <= 1e-3 * abs(lu), (loss, lu)
         print("[cfg3] oracle backward", flush=True)
         lref, gref = H.model_backward(cfg, p64, dev, ids, tg, "bf16")
         assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)

@@ -271,3 +271,104 @@ def test_inference_after_training_uses_updated_weights(graph):
         ca.close(); cb.close()
     finally:
         a.close(); b.close()
+
+
+def _hier_model(precision, P, T, seed=5):
+    """A cfg3-family hierarchical model (encoder, global stack over patches,
+    decoder; local window 96) with a non-zero global_bos row, so the first
+    patch's context is not zero."""
+    from sejong_amd.model import HierarchyConfig, Model, ModelConfig, TrainConfig, init_params
+    mc = ModelConfig(width=512, layers=2, heads=8, kv_heads=2, ffn_width=1376, context=T, precision=precision,
+                     hierarchy=HierarchyConfig(patch_size=P, encoder_width=256, encoder_layers=1, encoder_heads=4,
+                                               encoder_ffn_width=768, decoder_width=256, decoder_layers=2,
+                                               decoder_heads=4, decoder_ffn_width=768, local_window=96))
+    tc = TrainConfig(sequence=T, batch=1)
+    params = init_params(mc, std=0.02, seed=seed)
+    m = Model(mc, tc)
+    for name, (r, c), off in m.param_info():
+        if name == "global_bos":
+            params[off:off + r * c] = np.random.default_rng(seed).normal(0, 0.5, r * c).astype(np.float32)
+    m.set_params(params)
+    return m
+
+
+def _chunk_plans(T, P):
+    """Call sequences over one sequence of T bytes: token by token from an
+    empty cache (every position; the first call is shorter than a patch);
+    a first call shorter than a patch, then uneven chunks that end inside
+    patches and cross several; a prefill with a partial last patch, then
+    single bytes through several patches and longer chunks; the whole
+    sequence at once."""
+    def fill(plan):
+        plan = list(plan)
+        rest = T - sum(plan)
+        while rest > 0:
+            n = min(rest, 1 + (len(plan) * 7) % 23)
+            plan.append(n)
+            rest -= n
+        return plan
+    return [[1] * T,
+            fill([P - 1, 1, 1, P + 2, 2 * P + 1, 1, 64 // P * P - 1, 2, 1]),
+            fill([2 * P + 2] + [1] * (3 * P + 1) + [P + 3, 5 * P, 1]),
+            [T]]
+
+
+@pytest.mark.parametrize("precision,P,T", [("bf16", 4, 256), ("f32", 3, 128)])
+def test_hierarchical_cached_vs_full(precision, P, T):
+    """The hierarchical cached forward (HierarchyCache, hierarchical_prefill
+    and the patch loop of hidden_cached, architecture.rs:395-452, 534-799)
+    against the full forward's logits at the last byte of every call, for
+    prefills shorter and longer than a patch, uneven chunks and decoding
+    through several patches (the fp32 case with patch 3 ends on a partial
+    patch); the cache reset between plans (HierarchyCache::reset) clears the
+    patch state.  The reference's gate is 1e-4 (system_check.rs:48-51);
+    the cached path pools a completed patch with the full forward's own
+    kernel and runs every row through the same kernels, so the logits come
+    out bit-identical."""
+    from sejong_amd.benchmark import full_logits
+    m = _hier_model(precision, P, T)
+    try:
+        ids = np.random.default_rng(T + P).integers(0, 256, T).astype(np.int32)
+        full = full_logits(m, ids)
+        cache = m.new_cache()
+        for k, plan in enumerate(_chunk_plans(T, P)):
+            cache.reset()
+            pos, worst = 0, 0.0
+            print(f"[infer] hierarchical {precision} P={P} T={T} plan {k}: {len(plan)} calls", flush=True)
+            for n in plan:
+                got = m.forward_cached(ids[pos:pos + n], cache)
+                pos += n
+                err = float(np.max(np.abs(got.astype(np.float64) - full[pos - 1])))
+                assert err <= TOL, (k, pos, n, err)
+                worst = max(worst, err)
+            assert pos == T == cache.length
+            print(f"[infer] hierarchical plan {k}: max abs error {worst:.3e}", flush=True)
+        from sejong_amd import _native as N
+        with pytest.raises(N.SejongError, match="context limit"):
+            m.forward_cached(ids[:1], cache)
+        cache.close()
+    finally:
+        m.close()
+
+
+def test_cached_measurement_report_cfg3(tmp_path):
+    """cached_measurement (benchmark.rs:113-171) on the cfg3 hierarchical
+    model (1024 bytes, patches of 4): prefill of 1008 bytes (252 patches),
+    then 16 bytes decoded one at a time through four patches; the error of
+    the last byte's logits within the 1e-4 gate."""
+    from sejong_amd.benchmark import cached_measurement
+    from sejong_amd.corpus import Corpus
+    from sejong_amd.model import config
+    rng = np.random.default_rng(3)
+    (tmp_path / "v.txt").write_bytes(rng.integers(0, 256, 5000, dtype=np.uint8).tobytes())
+    mc, tc = config("cfg3")
+    tc.batch = 1
+    m, _ = _model(mc, tc)
+    try:
+        rep = cached_measurement(m, Corpus.open(tmp_path), 16)
+        print(f"[infer] cfg3 {rep}", flush=True)
+        assert rep["prefill_tokens"] == 1008 and rep["decode_tokens"] == 16
+        assert rep["cached_vs_full_last_logits_max_abs_error"] <= TOL
+        assert rep["decode_tokens_per_second"] > 0
+    finally:
+        m.close()

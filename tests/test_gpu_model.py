@@ -249,6 +249,39 @@ def test_graph_replay_equals_eager_and_is_deterministic():
     assert out[0][1][-1] < out[0][1][0]  # the loss moves down on a fixed batch
 
 
+def test_graph_replay_equals_eager_at_bench_configuration():
+    """The step bench.py times, at its configuration (full cfg2: 6 layers,
+    B 8 x T 512, the dW products on the second stream, the gradient planes
+    reused by layer parity, the attention backward's plan with cut walks):
+    two AdamW steps replayed from the captured graph leave the parameters,
+    gradients, Adam moments and losses bit-identical to two eager steps."""
+    from sejong_amd.model import Model, byte_batch, config, init_params
+    from sejong_amd.rng import Rng
+    mc, tc = config("cfg2")
+    params = init_params(mc, std=0.02)
+    ids, tg = byte_batch(Rng(123), tc.batch, tc.sequence)
+    out = []
+    for graph in (False, True):
+        model = Model(mc, tc)
+        try:
+            model.set_params(params)
+            model.set_batch(ids, tg)
+            model.use_graph(graph)
+            losses = []
+            for _ in range(2):
+                model.train_step(tc.learning_rate)
+                losses.append(model.read_loss())
+            m, v, step = model.get_adam_state()
+            out.append((model.get_params(), model.get_grads(), m, v, step, losses))
+            print(f"[graph] cfg2 graph={graph}: losses {losses}", flush=True)
+        finally:
+            model.close()
+    for name, a, b in zip(("params", "grads", "m", "v"), out[0][:4], out[1][:4]):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+    assert out[0][4] == out[1][4] == 2
+    assert out[0][5] == out[1][5]
+
+
 def test_profiled_steps_equal_plain_steps_and_time_their_gemm_kernels():
     """Per-op profiling in kernel-timing mode (sj_model_profile 3) runs the
     step on one stream and launches each GEMM op's kernel with events at its

@@ -138,7 +138,9 @@ def test_cfg4_full_configuration_against_oracle():
     N(0, 0.02), router N(0, 1/d) so the logits are N(0, 1)) with the batch
     cut from 8 to 2 sequences for the oracle's time: routing of every layer
     bit-exact against the rule on the stored logits, loss and every
-    gradient within 1e-3 of the FP64 backward from the stored activations."""
+    gradient within 1e-3 of the FP64 backward from the stored activations;
+    and the loss within 1e-3 of the oracle's loss from its own bf16
+    forward (no device values)."""
     from sejong_amd.model import Model, byte_batch, config, init_params
     from sejong_amd.rng import Rng
     mc, tc = config("cfg4")
@@ -163,6 +165,11 @@ def test_cfg4_full_configuration_against_oracle():
         ref_acts = OM.model_forward(cfg, p64, ids, "bf16")
         for k in ref_acts:
             assert rel(dev[k], ref_acts[k]) < 3e-2, (k, rel(dev[k], ref_acts[k]))
+        # the loss gate unconditioned: the oracle's loss from its own forward
+        rows, _ = O.cross_entropy(ref_acts[("logits", -1)].reshape(-1, O.VOCAB), tg, 1.0)
+        lu = float(np.mean(rows))
+        print(f"[cfg4] loss {loss:.6f} vs the oracle's own forward {lu:.6f}", flush=True)
+        assert abs(loss - lu) <= 1e-3 * abs(lu), (loss, lu)
         print("[cfg4] oracle backward", flush=True)
         lref, gref, routing = OM.model_backward(cfg, p64, dev, ids, tg, "bf16")
         assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)

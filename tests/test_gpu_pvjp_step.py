@@ -81,7 +81,25 @@ def _oracle_selection(mc, tc, draw):
 
 
 def test_vjp_step_gradients_against_oracle():
-    mc, tc = _cfgs()
+    _vjp_step_parity(*_cfgs())
+
+
+def test_vjp_step_gradients_at_cfg5_widths():
+    """The same parity at cfg5's widths and depth (12 layers, d 1024, GQA
+    16/4, FFN 2752, T 1024, rank 16, residual 0.1 over 32-row blocks, lr
+    1e-2, no clip, no weight decay) with the batch cut from 16 sequences to
+    1 for the FP64 oracle's time: q|k|v and gate|up still compress at 1024
+    tokens (the cost model's decisions at this shape), 60 compressed and 25
+    dense matrices."""
+    from sejong_amd.model import config
+    mc, tc = config("cfg5")
+    tc.batch = 1
+    print(f"[parity] vjp step at cfg5 widths: d={mc.width} L={mc.layers} F={mc.ffn_width} "
+          f"T={tc.sequence} B={tc.batch}", flush=True)
+    _vjp_step_parity(mc, tc)
+
+
+def _vjp_step_parity(mc, tc):
     model, params, ids, tg = _model(mc, tc)
     try:
         L, d, F = mc.layers, mc.width, mc.ffn_width

@@ -829,3 +829,24 @@ def test_pvjp_basis_tolerance_hand_values():
     assert pvjp.basis_tolerance(1 << 20, 4) == np.float32(f32max)
     # one operation short of 1: the largest finite tolerance, 2^24 - 1
     assert pvjp.basis_tolerance(2 ** 24 - 1, 0) == np.float32(16777215.0)
+
+
+def test_blake3_published_digests_and_reference_fingerprints():
+    """oracle/blake3.py against the BLAKE3 specification's digests of the
+    empty input and "abc" (one block, one chunk), and, where the reference
+    checkout is present, against the corpus fingerprints its measurement
+    recorded (multi-chunk trees: docs/measurements/2026-11-01/
+    rx6600-learning-window.json:2111,2119).  A wrong rotation, message
+    permutation, flag or tree split fails one of them."""
+    import os
+    from oracle import blake3 as B3
+    assert B3.blake3(b"").hex() == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+    assert B3.blake3(b"abc").hex() == "6437b3ac38465133ffb63b75273a8db548c558465d79db03fd359c6cd5bd9d85"
+    d = "/root/reference/docs/measurements/2026-11-01/"
+    if os.path.exists(d + "train.txt"):
+        with open(d + "train.txt", "rb") as f:
+            assert B3.corpus_fingerprint([f.read()]) == \
+                "b96cc76f31fa0a61e840635e05d1ceea137d68329cbe2d20504b8f34d371943f"
+        with open(d + "validation.txt", "rb") as f:
+            assert B3.corpus_fingerprint([f.read()]) == \
+                "9a1409d8fd61e18c2ca1fef712488fbe776e90f3c10fd9a9b88d9eb11503d16e"

@@ -59,6 +59,34 @@ def test_noalloc_matches_workspace_entry_twice(api, lib):
             np.testing.assert_array_equal(a, b, err_msg=f"{name} rows {R} d {D}")
 
 
+def test_noalloc_allocates_no_device_memory(api, lib):
+    """After a warm-up call (the module's code object loaded, the shared
+    array's address resolved), further calls leave the device's free memory
+    unchanged: the entry point allocates nothing."""
+    R, D, ldt = 4096, 384, 4096
+    rng = np.random.default_rng(3)
+    X, W = dev(rnd((R, D), "bf16", rng), "bf16"), dev(rnd(D, "bf16", rng), "bf16")
+    DY, ACC = dev(rng.normal(0, 1e-3, (R, D)).astype(np.float32)), dev(np.zeros((R, D), np.float32))
+    DX, DW = empty(R * D), empty(D)
+    Hn, Ln, Ht, Lt = empty(R * D, "bf16"), empty(R * D, "bf16"), empty(D * ldt, "bf16"), empty(D * ldt, "bf16")
+
+    def call(rows):  # the wrapped entry point raises on a non-zero status
+        api.sj_rmsnorm_bwd_p_noalloc(None, X.p, W.p, DY.p, ACC.p, DX.p, DW.p, Hn.p, Ln.p, Ht.p, Lt.p, ldt, rows, D,
+                                     cf(1e-6))
+        sync()
+
+    def free():
+        f, t = ctypes.c_size_t(), ctypes.c_size_t()
+        api.sj_memory_info(ctypes.byref(f), ctypes.byref(t))
+        return f.value
+
+    call(R)
+    before = free()
+    for rows in (R, 1000, R):
+        call(rows)
+    assert free() == before
+
+
 def test_noalloc_rejects_beyond_maximum(lib):
     from sejong_amd import _native as N
     cap = N.load().sj_rmsnorm_bwd_p_workspace_bytes(16 * 1025, 1024)
