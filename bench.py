@@ -122,7 +122,10 @@ def _hier_ops(mc, tc):
     Pn = sum(math.prod(sh) for _, sh, _ in SM.layout(mc))
     mt = sum(L * (d * (d + 2 * (d // hq * hk)) + d * d + 3 * d * F) for L, d, hq, hk, F, _, _ in stages)
     add("grad_norm", "byte", Pn * 4)
-    add("adamw", "byte", 30 * Pn)
+    # a bf16 planes model's AdamW also writes the transposed mirror (and the
+    # head's planes in both orientations when the head runs on them)
+    fused = planes and os.environ.get("SJ_FUSED_ADAMW", "1") != "0"
+    add("adamw", "byte", 30 * Pn + (2 * mt + (8 * dg * ((V + 7) // 8 * 8) if planes else 0) if fused else 0))
     add("mirror_transpose", "byte", 2 * 2 * mt)
     return tot
 
@@ -188,6 +191,15 @@ def op_work(op: str, mc, tc):
         "grad_norm": ("byte", 8 * GRAD_SQ_SLOTS if GRAD_SQ_SLOTS else P * 4),
         "adamw": ("byte", 30 * P),
     }
+    # the bf16 planes step's AdamW also writes the transposed bf16 mirror of
+    # the projection matrices and the output head's hi/lo planes in both
+    # orientations (the update that feeds the forward GEMMs directly)
+    if (planes and getattr(tc, "optimizer", "adamw") == "adamw" and os.environ.get("SJ_FUSED_ADAMW", "1") != "0"):
+        ex_ = getattr(mc, "experts", None)
+        ffn = 3 * d * (ex_.count * ex_.ffn_width if ex_ is not None else F)
+        mt = mc.layers * (d * (d + 2 * J) + d * d + ffn)
+        Vp = (V + 7) // 8 * 8
+        table["adamw"] = ("byte", 30 * P + 2 * mt + 8 * d * Vp)
     ex = getattr(mc, "experts", None)
     if ex is not None:
         # MoE FFN (cfg4): S = M * top_k routed rows; the grouped expert

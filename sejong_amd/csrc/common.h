@@ -47,6 +47,35 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
 
 __device__ __forceinline__ uint32_t pack2(bf16_t a, bf16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
+// The scalars of one multi-tensor AdamW step (Adam::update, crates/sejong-
+// train/src/lib.rs:199-238; kernel adamw, kernels.py:193-202): the clip
+// factor formed on the device from the FP64 squared gradient norm.
+struct AdamCoef {
+  float scale, lr, b1, b2, eps, ib1, ib2, keep;
+};
+// false (and no update) when the norm is not finite
+__device__ __forceinline__ bool adam_coef(const sj_adam_step* st, const double* sumsq, AdamCoef& c) {
+  const double norm = sqrt(sumsq[0]) / (double)st->loss_scale;
+  if (!isfinite(norm)) return false;
+  const double clipping = (st->clip_enabled && norm > (double)st->clip_norm) ? (double)st->clip_norm / norm : 1.0;
+  c.scale = (float)clipping / st->loss_scale;
+  c.lr = st->lr; c.b1 = st->beta1; c.b2 = st->beta2; c.eps = st->eps; c.ib1 = st->inv_b1; c.ib2 = st->inv_b2;
+  c.keep = 1.f - st->lr * st->weight_decay;
+  return true;
+}
+// one parameter: m, v and w updated in place (decay: the parameter is a
+// matrix, p.value.shape.len() > 1).  The fused multiply-adds are written
+// out, so every kernel that updates parameters rounds them alike whatever
+// the compiler would contract in its context.
+__device__ __forceinline__ void adam_elem(float& w, float g, float& m, float& v, const AdamCoef& c, bool decay) {
+  const float gi = g * c.scale;
+  m = fmaf(c.b1, m, (1.f - c.b1) * gi);
+  v = fmaf(c.b2, v, ((1.f - c.b2) * gi) * gi);
+  const float den = sqrtf(v * c.ib2) + c.eps;
+  const float stp = den > 0.f ? (m * c.ib1) / den : 0.f;
+  w = fmaf(w, decay ? c.keep : 1.f, -(c.lr * stp));
+}
+
 // Load a value of dtype `dt` (SJ_F32 or SJ_BF16) at index i as float.
 __device__ __forceinline__ float load_as_f32(const void* p, int dt, long i) {
   return dt == SJ_BF16 ? bf2f(((const bf16_t*)p)[i]) : ((const float*)p)[i];

@@ -275,15 +275,11 @@ __global__ __launch_bounds__(256) void k_adamw_multi(float* __restrict__ w, cons
                                                       bf16_t* __restrict__ mirror, long n, long n_nodecay,
                                                       const sj_adam_step* __restrict__ st,
                                                       const double* __restrict__ sumsq, int32_t* status) {
-  const double norm = sqrt(sumsq[0]) / (double)st->loss_scale;
-  if (!isfinite(norm)) {
+  AdamCoef c;
+  if (!adam_coef(st, sumsq, c)) {
     if (blockIdx.x == 0 && threadIdx.x == 0) status[0] = 1;
     return;
   }
-  double clipping = (st->clip_enabled && norm > (double)st->clip_norm) ? (double)st->clip_norm / norm : 1.0;
-  const float scale = (float)clipping / st->loss_scale;
-  const float lr = st->lr, b1 = st->beta1, b2 = st->beta2, eps = st->eps, ib1 = st->inv_b1, ib2 = st->inv_b2;
-  const float keep = 1.f - lr * st->weight_decay;
   for (long q = blockIdx.x * (long)blockDim.x + threadIdx.x; q * 4 < n; q += (long)gridDim.x * blockDim.x) {
     long i0 = q * 4;
     if (i0 + 4 <= n) {
@@ -292,15 +288,7 @@ __global__ __launch_bounds__(256) void k_adamw_multi(float* __restrict__ w, cons
       float ws[4] = {wv.x, wv.y, wv.z, wv.w}, gs[4] = {gv.x, gv.y, gv.z, gv.w};
       float ms[4] = {mv.x, mv.y, mv.z, mv.w}, vs[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        float gi = gs[j] * scale;
-        ms[j] = b1 * ms[j] + (1.f - b1) * gi;
-        vs[j] = b2 * vs[j] + (1.f - b2) * gi * gi;
-        float den = sqrtf(vs[j] * ib2) + eps;
-        float stp = den > 0.f ? (ms[j] * ib1) / den : 0.f;
-        float k = (i0 + j) < n_nodecay ? 1.f : keep;
-        ws[j] = ws[j] * k - lr * stp;
-      }
+      for (int j = 0; j < 4; j++) adam_elem(ws[j], gs[j], ms[j], vs[j], c, (i0 + j) >= n_nodecay);
       *(float4*)(w + i0) = make_float4(ws[0], ws[1], ws[2], ws[3]);
       *(float4*)(m + i0) = make_float4(ms[0], ms[1], ms[2], ms[3]);
       *(float4*)(v + i0) = make_float4(vs[0], vs[1], vs[2], vs[3]);
@@ -312,13 +300,8 @@ __global__ __launch_bounds__(256) void k_adamw_multi(float* __restrict__ w, cons
       }
     } else {
       for (long i = i0; i < n; i++) {
-        float gi = g[i] * scale;
-        float mi = b1 * m[i] + (1.f - b1) * gi;
-        float vi = b2 * v[i] + (1.f - b2) * gi * gi;
-        float den = sqrtf(vi * ib2) + eps;
-        float stp = den > 0.f ? (mi * ib1) / den : 0.f;
-        float k = i < n_nodecay ? 1.f : keep;
-        float wi = w[i] * k - lr * stp;
+        float wi = w[i], mi = m[i], vi = v[i];
+        adam_elem(wi, g[i], mi, vi, c, i >= n_nodecay);
         w[i] = wi;
         m[i] = mi;
         v[i] = vi;

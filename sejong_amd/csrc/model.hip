@@ -196,6 +196,132 @@ __global__ __launch_bounds__(256) void k_transpose_jobs(const uint16_t* __restri
   }
 }
 
+// A run of parameters outside the transpose table, updated elementwise
+struct FlatChunk {
+  long begin, end;
+};
+
+// The AdamW update of the bf16 planes models with the mirrors it feeds
+// written in the same pass (Adam::update, crates/sejong-train/src/lib.rs:
+// 199-238, with Model::bind's cast, model lib.rs:206-250, fused).  Workgroup
+// b < tiles takes tile b of the transpose table: it updates the tile's
+// masters and moments row by row, writes the bf16 mirror, and from an LDS
+// copy of the new values the transposed mirror the forward GEMMs read
+// (kind 1, the output head: its hi/lo planes, normal and transposed).  The
+// workgroups past the tiles update the flat chunks (everything else, 1024
+// parameters each).  The per-parameter arithmetic is adam_elem, as in
+// k_adamw_multi: the same bits, and the forward no longer waits for a
+// transpose pass.
+__global__ __launch_bounds__(256) void k_adamw_tiles(float* __restrict__ w, const float* __restrict__ g,
+                                                     float* __restrict__ m, float* __restrict__ v,
+                                                     uint16_t* __restrict__ mirror, uint16_t* __restrict__ mirror_t,
+                                                     long n_nodecay, const sj_adam_step* __restrict__ st,
+                                                     const double* __restrict__ sumsq, int32_t* status,
+                                                     const TJob* __restrict__ jobs, int njobs, long tiles,
+                                                     const FlatChunk* __restrict__ chunks, TPlanes hp) {
+  sj::AdamCoef c;
+  if (!sj::adam_coef(st, sumsq, c)) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) status[0] = 1;
+    return;
+  }
+  const int t = threadIdx.x;
+  const long b = blockIdx.x;
+  // four parameters from i0 (vector path when they are whole and aligned)
+  auto quad = [&](long i0, long end, float* out) {
+    if (i0 + 4 <= end && (i0 & 3) == 0) {
+      const float4 wv = *(const float4*)(w + i0), gv = *(const float4*)(g + i0);
+      const float4 mv = *(const float4*)(m + i0), vv = *(const float4*)(v + i0);
+      float ws[4] = {wv.x, wv.y, wv.z, wv.w}, gs[4] = {gv.x, gv.y, gv.z, gv.w};
+      float ms[4] = {mv.x, mv.y, mv.z, mv.w}, vs[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) sj::adam_elem(ws[j], gs[j], ms[j], vs[j], c, (i0 + j) >= n_nodecay);
+      *(float4*)(w + i0) = make_float4(ws[0], ws[1], ws[2], ws[3]);
+      *(float4*)(m + i0) = make_float4(ms[0], ms[1], ms[2], ms[3]);
+      *(float4*)(v + i0) = make_float4(vs[0], vs[1], vs[2], vs[3]);
+      *(uint2*)(mirror + i0) = uint2{sj::pack2(sj::f2bf(ws[0]), sj::f2bf(ws[1])), sj::pack2(sj::f2bf(ws[2]), sj::f2bf(ws[3]))};
+#pragma unroll
+      for (int j = 0; j < 4; j++) out[j] = ws[j];
+    } else {
+      for (int j = 0; j < 4; j++) {
+        const long i = i0 + j;
+        if (i >= end) break;
+        float wi = w[i], mi = m[i], vi = v[i];
+        sj::adam_elem(wi, g[i], mi, vi, c, i >= n_nodecay);
+        w[i] = wi;
+        m[i] = mi;
+        v[i] = vi;
+        mirror[i] = sj::f2bf(wi);
+        out[j] = wi;
+      }
+    }
+  };
+  if (b >= tiles) {  // a flat chunk: one quad per thread
+    const FlatChunk ch = chunks[b - tiles];
+    float tmp[4];
+    const long i0 = ch.begin + 4L * t;
+    if (i0 < ch.end) quad(i0, ch.end, tmp);
+    return;
+  }
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 72];
+  __shared__ __attribute__((aligned(16))) uint16_t tile_lo[64 * 72];
+  int ji = 0;
+  while (ji + 1 < njobs && b >= jobs[ji + 1].tile0) ji++;
+  const long off = jobs[ji].off, rows = jobs[ji].rows, cols = jobs[ji].cols;
+  const bool k1 = jobs[ji].kind == 1;
+  const long lt = b - jobs[ji].tile0;
+  const long r0 = (lt / jobs[ji].tiles_c) * 64, c0 = (lt % jobs[ji].tiles_c) * 64;
+  // 16 rows per pass, 16 threads per 64-column row: 256-byte row segments
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const int r = (t >> 4) + 16 * p, cc = 4 * (t & 15);
+    const long gr = r0 + r, gc = c0 + cc;
+    float nw[4] = {0.f, 0.f, 0.f, 0.f};
+    if (gr < rows && gc < cols) {
+      const long i0 = off + gr * cols + gc;
+      quad(i0, i0 + (cols - gc < 4 ? cols - gc : 4), nw);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const bool in = gr < rows && gc + j < cols;
+      if (k1) {
+        sj::bf16_t h = 0, l = 0;
+        if (in) sj::split_bf(nw[j], h, l);
+        tile[r * 72 + cc + j] = h;
+        tile_lo[r * 72 + cc + j] = l;
+        if (in) {
+          hp.hi[gr * cols + gc + j] = h;
+          hp.lo[gr * cols + gc + j] = l;
+        }
+      } else {
+        tile[r * 72 + cc + j] = in ? sj::f2bf(nw[j]) : (uint16_t)0;
+      }
+    }
+  }
+  __syncthreads();
+  const bool vec = !k1 && (rows & 7) == 0 && r0 + 64 <= rows && c0 + 64 <= cols;
+  uint16_t* D = mirror_t + off;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int oc = (t >> 3) + 32 * p, orr = (t & 7) * 8;  // source column oc, source rows orr..+7
+    uint16_t u[8];
+    for (int i = 0; i < 8; i++) u[i] = tile[(orr + i) * 72 + oc];
+    if (k1) {
+      if (c0 + oc < cols)
+        for (int i = 0; i < 8; i++)
+          if (r0 + orr + i < rows) {
+            hp.hit[(c0 + oc) * rows + r0 + orr + i] = u[i];
+            hp.lot[(c0 + oc) * rows + r0 + orr + i] = tile_lo[(orr + i) * 72 + oc];
+          }
+    } else if (vec) {
+      *(sj::u32x4*)(D + (c0 + oc) * rows + r0 + orr) =
+          sj::u32x4{sj::pack2(u[0], u[1]), sj::pack2(u[2], u[3]), sj::pack2(u[4], u[5]), sj::pack2(u[6], u[7])};
+    } else if (c0 + oc < cols) {
+      for (int i = 0; i < 8; i++)
+        if (r0 + orr + i < rows) D[(c0 + oc) * rows + r0 + orr + i] = u[i];
+    }
+  }
+}
+
 }  // namespace
 
 struct sj_model {
@@ -258,6 +384,11 @@ struct sj_model {
   TJob* tjobs = nullptr;
   int tjob_n = 0;
   long tjob_tiles = 0;
+  // the AdamW update writes the mirrors itself (k_adamw_tiles): the
+  // parameters outside the transpose table as flat chunks
+  bool fused_update = false;
+  FlatChunk* fchunks = nullptr;
+  long nfchunks = 0;
   // the table in groups for the overlapped refresh: group 0 the output head
   // (absent without head planes), group 1 + l layer l; job start, job count,
   // first tile, tile count
@@ -736,10 +867,11 @@ bool gsq_eligible(const sj_model* m) {
   return m->planes && m->lm_planes && !m->E && !m->hier && !m->value_n && m->optimizer == 0 && !m->vjp;
 }
 // the step's forward: the loss sum waits for the backward's second stream,
-// and the transposed mirror is rebuilt beside the forward
+// and the transposed mirror, unless the last update wrote it, is rebuilt
+// beside the forward
 int forward_deferred(sj_model* m) {
   m->defer_loss = !m->value_n && two_streams(m);
-  m->tr_overlap = two_streams(m) && !m->tgroups.empty();
+  m->tr_overlap = !m->fused_update && two_streams(m) && !m->tgroups.empty();
   const int st = forward(m);
   m->tr_overlap = false;
   if (st) m->defer_loss = false;
@@ -1207,6 +1339,16 @@ int backward_body(sj_model* m) {
   return SJ_OK;
 }
 
+int fused_adamw(sj_model* m) {
+  const long blocks = m->tjob_tiles + m->nfchunks;
+  if (blocks == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_adamw_tiles, dim3((unsigned)blocks), dim3(256), 0, m->stream, m->w, m->g, m->m, m->v,
+                     m->mirror, m->mirror_t, m->n_nodecay, m->step_dev, m->sumsq, m->status, m->tjobs, m->tjob_n,
+                     m->tjob_tiles, m->fchunks, TPlanes{m->hp[0], m->hp[1], m->hp[2], m->hp[3]});
+  SJ_LAUNCH_CHECK("adamw (fused mirrors)");
+  return SJ_OK;
+}
+
 int update(sj_model* m) {
   if (m->optimizer == 1) {
     // compact SGD (control_variate.rs:720-775): FP64 norm of the compact
@@ -1225,6 +1367,11 @@ int update(sj_model* m) {
     OP("grad_norm", sjh::sum_slots(m->stream, m->gsq, m->gsq_count, m->sumsq));
   else
     OP("grad_norm", sj_sum_squares(m->stream, m->g, m->n_params, m->sumsq, m->ws, m->ws_bytes));
+  if (m->fused_update) {  // masters, moments and both mirrors in one pass
+    OP("adamw", fused_adamw(m));
+    m->mt_stale = false;
+    return SJ_OK;
+  }
   OP("adamw", sj_adamw_multi(m->stream, m->w, m->g, m->m, m->v, m->dt == SJ_BF16 ? m->mirror : nullptr, m->n_params,
                      m->n_nodecay, m->step_dev, m->sumsq, m->status));
   m->mt_stale = m->planes;  // the next forward rebuilds the transposed mirror
@@ -1628,6 +1775,35 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     ALLOC(m->tjobs, sizeof(TJob) * jobs.size());
     if (hipMemcpy(m->tjobs, jobs.data(), sizeof(TJob) * jobs.size(), hipMemcpyHostToDevice) != hipSuccess)
       return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: transpose job table"));
+    // the fused update: the rest of the arena (norms, embedding, routers,
+    // glue, padding) in chunks of at most 1024 parameters (a quad per thread)
+    static const int fused_env = [] {
+      const char* e = getenv("SJ_FUSED_ADAMW");  // 0: AdamW, then the transpose pass (A/B)
+      return e ? atoi(e) : 1;
+    }();
+    if (m->optimizer == 0 && m->dt == SJ_BF16 && fused_env) {
+      std::vector<std::pair<long, long>> spans;
+      for (const TJob& j : jobs) spans.push_back({j.off, j.off + j.rows * j.cols});
+      std::sort(spans.begin(), spans.end());
+      std::vector<FlatChunk> ch;
+      long at = 0;
+      auto flat = [&](long a, long e) {
+        for (long x = a; x < e; x += 1024) ch.push_back(FlatChunk{x, x + 1024 < e ? x + 1024 : e});
+      };
+      for (const auto& sp : spans) {
+        if (sp.first < at) return fail_cleanup(sjh::fail(SJ_ERR_INVALID, "model: overlapping transpose jobs"));
+        flat(at, sp.first);
+        at = sp.second;
+      }
+      flat(at, (long)P);
+      m->nfchunks = (long)ch.size();
+      if (!ch.empty()) {
+        ALLOC(m->fchunks, sizeof(FlatChunk) * ch.size());
+        if (hipMemcpy(m->fchunks, ch.data(), sizeof(FlatChunk) * ch.size(), hipMemcpyHostToDevice) != hipSuccess)
+          return fail_cleanup(sjh::fail(SJ_ERR_HIP, "model: flat update chunks"));
+      }
+      m->fused_update = true;
+    }
   }
   const size_t es = m->esz;
   // largest per-stage extents (shared scratch) and the head's
@@ -2153,7 +2329,7 @@ static int run_step(sj_model* m) {
     SJ_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
   }
   SJ_HIP(hipGraphLaunch(m->exec, m->stream));
-  m->mt_stale = m->planes;  // the replayed update left the transposed mirror behind
+  m->mt_stale = m->planes && !m->fused_update;  // a replayed AdamW update rewrote the transposed mirror
   return SJ_OK;
 }
 
