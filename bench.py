@@ -122,10 +122,7 @@ def _hier_ops(mc, tc):
     Pn = sum(math.prod(sh) for _, sh, _ in SM.layout(mc))
     mt = sum(L * (d * (d + 2 * (d // hq * hk)) + d * d + 3 * d * F) for L, d, hq, hk, F, _, _ in stages)
     add("grad_norm", "byte", Pn * 4)
-    # a bf16 planes model's AdamW also writes the transposed mirror (and the
-    # head's planes in both orientations when the head runs on them)
-    fused = planes and os.environ.get("SJ_FUSED_ADAMW", "1") != "0"
-    add("adamw", "byte", 30 * Pn + (2 * mt + (8 * dg * ((V + 7) // 8 * 8) if planes else 0) if fused else 0))
+    add("adamw", "byte", 30 * Pn)
     add("mirror_transpose", "byte", 2 * 2 * mt)
     return tot
 
@@ -182,7 +179,10 @@ def op_work(op: str, mc, tc):
         # written; the backward also writes dx as hi/lo planes (and their
         # transposes unless row-layout dW)
         "rmsnorm": ("byte", (2 + (1 if planes and not rowdw else 0)) * M * d * es + d * es),
-        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4 + ((4 if rowdw else 8) if planes else 0)) + d * es),
+        # algorithmic (the dtypes used): x read, dy (fp32) read,
+        # dx (fp32) written, plus the fused residual-gradient add's fp32 read;
+        # the gradient planes it also writes are issued bytes (op_issued_bytes)
+        "rmsnorm_bwd": ("byte", M * d * (es + 4 + 4 + 4) + d * es),
         "cross_entropy": ("byte", 2 * M * V * 4 + M * 8),
         "loss_summary": ("byte", M * 4),
         "embedding": ("byte", M * 4 + 2 * M * d * es),
@@ -191,15 +191,7 @@ def op_work(op: str, mc, tc):
         "grad_norm": ("byte", 8 * GRAD_SQ_SLOTS if GRAD_SQ_SLOTS else P * 4),
         "adamw": ("byte", 30 * P),
     }
-    # the bf16 planes step's AdamW also writes the transposed bf16 mirror of
-    # the projection matrices and the output head's hi/lo planes in both
-    # orientations (the update that feeds the forward GEMMs directly)
-    if (planes and getattr(tc, "optimizer", "adamw") == "adamw" and os.environ.get("SJ_FUSED_ADAMW", "1") != "0"):
-        ex_ = getattr(mc, "experts", None)
-        ffn = 3 * d * (ex_.count * ex_.ffn_width if ex_ is not None else F)
-        mt = mc.layers * (d * (d + 2 * J) + d * d + ffn)
-        Vp = (V + 7) // 8 * 8
-        table["adamw"] = ("byte", 30 * P + 2 * mt + 8 * d * Vp)
+
     ex = getattr(mc, "experts", None)
     if ex is not None:
         # MoE FFN (cfg4): S = M * top_k routed rows; the grouped expert
@@ -253,6 +245,31 @@ def op_work(op: str, mc, tc):
     return table.get(op, ("flop", 0.0))
 
 
+def op_issued_bytes(op: str, mc, tc):
+    """HBM bytes one launch of a bandwidth-bound op moves beyond its
+    algorithmic bytes (op_work), or None: the RMSNorm backward's hi/lo
+    gradient planes (and their transposes where the dW products read
+    transposed copies); the AdamW update's transposed bf16 mirror of the
+    projection matrices and the output head's hi/lo planes in both
+    orientations (the bf16 planes models' update writes them itself)."""
+    if getattr(mc, "hierarchy", None) is not None:
+        return None
+    M = tc.batch * tc.sequence
+    d, F, V = mc.width, mc.ffn_width, 257
+    J = mc.head_dim * mc.kv
+    planes = mc.precision == "bf16" and mc.head_dim == 64 and os.environ.get("SJ_PLANES", "1") != "0"
+    rowdw = (planes and os.environ.get("SJ_ATTN_TT", "1") != "0" and tc.sequence % 64 == 0
+             and getattr(tc, "parameter_vjp", None) is None)
+    if op == "rmsnorm_bwd" and planes:
+        return M * d * (4 if rowdw else 8)
+    if (op == "adamw" and planes and getattr(tc, "optimizer", "adamw") == "adamw"
+            and os.environ.get("SJ_FUSED_ADAMW", "1") != "0"):
+        ex = getattr(mc, "experts", None)
+        ffn = 3 * d * (ex.count * ex.ffn_width if ex is not None else F)
+        return 2 * mc.layers * (d * (d + 2 * J) + d * d + ffn) + 8 * d * ((V + 7) // 8 * 8)
+    return None
+
+
 # issued MFMA work of a kernel per unit of its algorithmic work: the GEMM
 # kernels multiply hi/lo bf16 planes (PA x PB products, lo x lo skipped); the
 # MFMA-layout attention kernels recompute S and dP and multiply the hi/lo
@@ -268,7 +285,7 @@ def issued_factor(kernel: str) -> float:
     return {"k_attn2_fwd<3>": 1.5, "k_attn2_bwd": 6.5 / 2.5, "k_attn2_bwd_g<3>": 6.5 / 2.5}.get(kernel, 1.0)
 
 
-def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config):
+def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config, kern_instep=None):
     """Roofline of the kernel with the largest share of the profiled step.
 
     Every op is charged to the kernel it launches: a GEMM op to the GEMM
@@ -313,6 +330,18 @@ def kernel_roofline(prof, kern_only, op_kernel, mc, tc, config):
     if flop:
         f = issued_factor(kern)
         out["issued"] = {"work_per_launch": wpl * f, "achieved": round(rate * f, 2), "frac": round(rate * f / peak, 4)}
+    # the same kernel timed in the two-stream step (sharing the chip with the
+    # other stream's kernels, as in the graph replay), beside the isolated time
+    if kern_instep:
+        ims = sum(kern_instep[op][0] for op in e["ops"] if op in kern_instep)
+        icalls = sum(kern_instep[op][1] for op in e["ops"] if op in kern_instep)
+        if icalls == e["calls"] and ims > 0:
+            ius = ims * 1e3 / icalls
+            irate = wpl / (ius * 1e-6) / (1e12 if flop else 1e9)
+            out["in_step"] = {"avg_launch_us": round(ius, 3), "achieved": round(irate, 2),
+                              "frac": round(irate / peak, 4)}
+            log(f"  dominant kernel in the two-stream step: {ius:.2f} us per launch, {irate:.2f} "
+                f"{'TFLOP/s' if flop else 'GB/s'}")
     return out
 
 
@@ -385,13 +414,27 @@ def cpu_baseline(mc, tc, sample_batch: int):
 
 
 def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its family / model /
+    stepping numbers (a virtualised host may report only a generic name) and
+    the logical CPUs this process may run on."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping", "cpu MHz") and k not in info:
+                info[k] = v.strip()
+            if k == "processor" and info:
+                break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        ncpu = os.cpu_count() or 0
+    return (f"{name} (family {info.get('cpu family', '?')} model {info.get('model', '?')} stepping "
+            f"{info.get('stepping', '?')}, {info.get('cpu MHz', '?')} MHz, {ncpu} logical CPUs available)")
 
 
 def cpu_extras(mc, tc) -> dict:
@@ -862,6 +905,15 @@ def main():
     model.profile(False)
     kern_only = {op[:-len("#kernel")]: (ms / nprof, calls // nprof) for op, (ms, calls) in kprof.items()
                  if op.endswith("#kernel")}
+    # and once more with the second stream running beside, as in the step:
+    # each kernel's time while it shares the chip (the graph replay's case)
+    model.profile(True, instep=True)
+    for _ in range(nprof):
+        model.train_step(tc.learning_rate)
+    iprof = model.profile_collect()
+    model.profile(False)
+    kern_instep = {op[:-len("#kernel")]: (ms / nprof, calls // nprof) for op, (ms, calls) in iprof.items()
+                   if op.endswith("#kernel")}
     # cold-cache pass: a 512 MiB buffer is written before every op, so the
     # bandwidth-bound ops read their operands from HBM rather than from the
     # 256 MB Infinity Cache
@@ -896,12 +948,19 @@ def main():
                          "hot_gbs": round(work / (hot_us * 1e-6) / 1e9, 1),
                          "cold_gbs": round(work / (cold_us * 1e-6) / 1e9, 1),
                          "cold_frac": round(work / (cold_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+        extra = op_issued_bytes(op, mc, tc)
+        if extra:  # what the kernel moves in all, beside the algorithmic bytes
+            iss = work + extra
+            cold_rows[op]["issued"] = {"bytes": int(iss), "cold_gbs": round(iss / (cold_us * 1e-6) / 1e9, 1),
+                                       "cold_frac": round(iss / (cold_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
     if cold_rows:
         log("  bandwidth-bound ops, hot vs cold cache (512 MiB written before each op):")
         for op, r in sorted(cold_rows.items(), key=lambda kv: -kv[1]["bytes"]):
             log(f"  {op:24s} {r['bytes'] / 1e6:8.2f} MB  hot {r['hot_us']:8.2f} us {r['hot_gbs']:8.1f} GB/s  "
-                f"cold {r['cold_us']:8.2f} us {r['cold_gbs']:8.1f} GB/s ({100 * r['cold_frac']:.1f}% of HBM)")
-    roofline = kernel_roofline(prof, kern_only, op_kernel, mc, tc, args.config)
+                f"cold {r['cold_us']:8.2f} us {r['cold_gbs']:8.1f} GB/s ({100 * r['cold_frac']:.1f}% of HBM)" +
+                (f"; issued {r['issued']['bytes'] / 1e6:.2f} MB, {100 * r['issued']['cold_frac']:.1f}% cold"
+                 if "issued" in r else ""))
+    roofline = kernel_roofline(prof, kern_only, op_kernel, mc, tc, args.config, kern_instep)
     # whole-step MFMA fraction (algorithmic GEMM + attention flops / step time)
     step_flops = sum(op_work(op, mc, tc)[1] * calls for op, (_, calls) in prof.items()
                      if op_work(op, mc, tc)[0] == "flop")

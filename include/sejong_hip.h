@@ -828,7 +828,10 @@ int sj_model_forward_cached(sj_model *m, sj_cache *c, const int32_t *tokens, lon
  * times each GEMM op's kernel alone, by events the launch records at the
  * kernel's own start and end (hipExtLaunchKernel: no launch gaps, no split-K
  * reduce), as an aggregate "<op>#kernel" (the extra packets lengthen the
- * op's own pair, so op times come from on = 1).  sj_model_profile_kernel
+ * op's own pair, so op times come from on = 1).  on = 4 records only those
+ * kernel-own pairs (the "#kernel" aggregates) and keeps the step's second
+ * stream: each kernel's time as it shares the chip in the step (no
+ * counterpart in the reference).  sj_model_profile_kernel
  * names the GEMM kernel an aggregate's
  * op launched, as rocprofv3 lists it ("k_gemm_fast<BM, BN, PA, PB, EPI, NS,
  * TM>"; "" for ops without one); it has no counterpart in the reference. */

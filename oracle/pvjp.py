@@ -13,6 +13,7 @@ integers; floating-point parts are float64 numpy.
   vjp coefficients (E dY)                      parameter_vjp.rs:308-320
   factored gradient / update / norm            parameter.py:193-291,
                                                parameter_vjp.rs:329-530
+  graph_statistics (grouping, donor, retain)   graph.rs:551-566, 915-1005
 
 Pinning (tests/test_oracle.py): the reference check program's own index
 generator (crates/sejong-gpu/examples/parameter_vjp_check.rs:74-100,
@@ -20,7 +21,9 @@ restated as text) on its default shape; the cfg5 budget and compression
 decisions; orthonormality and the span of the basis (projector of a QR of
 the same columns) and the drop rule on a duplicated column; the factored
 gradient equal to X^T D when every block is selected (for any orthonormal
-Q); the update and norm closed forms.
+Q); the update and norm closed forms; graph_statistics against the
+statistics the reference recorded for its production configuration
+(docs/measurements/2026-11-01-architecture-fit/applied.json).
 """
 from __future__ import annotations
 
@@ -166,3 +169,55 @@ def factored_update(W, G, lr, clipping, weight_decay, decays):
     LR = float(np.float32(np.float32(lr) * np.float32(clipping)))
     DECAY = float(np.float32(np.float32(lr) * np.float32(weight_decay)))
     return np.asarray(W, np.float64) * ((1.0 - DECAY) if decays else 1.0) - LR * G
+
+
+def graph_statistics(matmuls, rank, residual_fraction, block_rows):
+    """VjpStatistics of one backward (Graph::propagate's grouping, graph.rs:
+    551-566, and compressed_parameter_vjp, graph.rs:915-1005).
+
+    matmuls: the Matmul nodes with a parameter weight, in graph order, as
+    (input id, rows n, input width a, output width b).  Nodes whose input has
+    n >= a are grouped by input; a group's donor is its widest member (the
+    last such member on ties: Rust's max_by_key); the members are retained
+    while selects_compression holds for them with the current member count,
+    until the set stops shrinking.  A node with n < a, or outside its group's
+    retained set, is dense.  A group with retained members is a projection
+    group; it creates a basis group when its (n, rank) has none yet."""
+    members = {}
+    for idx, (inp, n, a, b) in enumerate(matmuls):
+        if n >= a:
+            members.setdefault(inp, []).append(idx)
+    stats = dict(compressed_matrices=0, dense_matrices=0, basis_groups=0, projection_groups=0)
+    groups, bases = {}, set()
+    for idx in reversed(range(len(matmuls))):  # the backward visits the nodes last first
+        inp, n, a, b = matmuls[idx]
+        if n < a:
+            stats["dense_matrices"] += 1
+            continue
+        if inp not in groups:
+            mem = members[inp]
+            donor = mem[0]
+            for i in mem:
+                if matmuls[i][3] >= matmuls[donor][3]:
+                    donor = i
+            donor_width = matmuls[donor][3]
+            active = set(mem)
+            while active:
+                count = len(active)
+                active = {i for i in active
+                          if selects_compression(rank, residual_fraction, block_rows, n, a, matmuls[i][3],
+                                                 donor_width, count)}
+                if len(active) == count:
+                    break
+            if active:
+                r = budget(rank, residual_fraction, block_rows, n, a, donor_width)[0]
+                if (n, r) not in bases:
+                    bases.add((n, r))
+                    stats["basis_groups"] += 1
+                stats["projection_groups"] += 1
+            groups[inp] = active
+        if idx in groups[inp]:
+            stats["compressed_matrices"] += 1
+        else:
+            stats["dense_matrices"] += 1
+    return stats

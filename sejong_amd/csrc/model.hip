@@ -469,6 +469,7 @@ struct sj_model {
   // kernel timing: each GEMM op's kernel records events at its own start and
   // end (hipExtLaunchKernel; its extra packets lengthen the op's own pair)
   bool kernel_events = false;
+  bool instep = false;  // profile mode 4: kernel events only, both streams as in the step
   float* flush = nullptr;
   std::vector<hipEvent_t> prof_events;  // start, end, GEMM kernel start, end per recorded op
   std::vector<const char*> prof_names;  // one per recorded op
@@ -543,7 +544,7 @@ int prof_mark(sj_model* m, const char* name) {
   }
   m->prof_names.push_back(name);
   if (m->cold && m->flush) TRY(sj_fill(m->stream, m->flush, SJ_F32, FLUSH_FLOATS, 0.f));
-  SJ_HIP(hipEventRecord(m->prof_events[4 * k], m->stream));
+  if (!m->instep) SJ_HIP(hipEventRecord(m->prof_events[4 * k], m->stream));
   sjh::ProfHook& h = sjh::prof_hook();
   h.on = true;
   h.k0 = m->kernel_events ? m->prof_events[4 * k + 2] : nullptr;
@@ -559,7 +560,7 @@ int prof_end(sj_model* m) {
   m->prof_kernel.emplace_back(h.kernel);
   h.on = false;
   h.k0 = h.k1 = nullptr;
-  SJ_HIP(hipEventRecord(m->prof_events[4 * k + 1], m->stream));
+  if (!m->instep) SJ_HIP(hipEventRecord(m->prof_events[4 * k + 1], m->stream));
   return SJ_OK;
 }
 #define OP(name, call)                         \
@@ -959,7 +960,7 @@ int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb
 // The dW products (and parameter-VJP groups) run on a second stream beside
 // the dX chain (planes path, graph and plain eager steps; per-op profiling
 // keeps one stream).
-bool two_streams(const sj_model* m) { return m->planes && !m->profiling; }
+bool two_streams(const sj_model* m) { return m->planes && (!m->profiling || m->instep); }
 
 // Backward of stage si from dzin = d(closing norm output) [M][d] (fp32):
 // the closing norm, then per layer from the top down / SwiGLU / gate+up /
@@ -2334,11 +2335,12 @@ static int run_step(sj_model* m) {
 }
 
 extern "C" int sj_model_profile(sj_model* m, int on) {
-  SJ_REQUIRE(m && on >= 0 && on <= 3, "profile: mode");
+  SJ_REQUIRE(m && on >= 0 && on <= 4, "profile: mode");
   if (on == 2 && !m->flush) TRY(dalloc(m, (void**)&m->flush, (size_t)FLUSH_FLOATS * 4));
   m->profiling = on != 0;
   m->cold = on == 2;
-  m->kernel_events = on == 3;
+  m->kernel_events = on == 3 || on == 4;
+  m->instep = on == 4;
   return SJ_OK;
 }
 
@@ -2365,9 +2367,11 @@ extern "C" long sj_model_profile_collect(sj_model* m) {
   if (m->prof_kused.size() != m->prof_names.size()) return -1;  // an op was left open
   for (size_t k = 0; k < m->prof_names.size(); k++) {
     float ms = 0.f;
-    if (hipEventElapsedTime(&ms, m->prof_events[4 * k], m->prof_events[4 * k + 1]) != hipSuccess) return -1;
     const std::string nm(m->prof_names[k]);
-    add(nm, ms, m->prof_kernel[k]);
+    if (!m->instep) {  // (in-step mode times the kernels only)
+      if (hipEventElapsedTime(&ms, m->prof_events[4 * k], m->prof_events[4 * k + 1]) != hipSuccess) return -1;
+      add(nm, ms, m->prof_kernel[k]);
+    }
     if (m->prof_kused[k]) {  // the GEMM kernel alone, from its own start to its end
       if (hipEventElapsedTime(&ms, m->prof_events[4 * k + 2], m->prof_events[4 * k + 3]) != hipSuccess) return -1;
       add(nm + "#kernel", ms, m->prof_kernel[k]);

@@ -529,11 +529,13 @@ class Model:
     def synchronize(self):
         N.api.sj_synchronize(ctypes.c_void_p(self.stream))
 
-    def profile(self, on: bool = True, cold: bool = False, kernels: bool = False):
+    def profile(self, on: bool = True, cold: bool = False, kernels: bool = False, instep: bool = False):
         """Per-op HIP-event timing of eager steps; cold: a 512 MiB buffer is
         written before each op so its operands come from HBM; kernels: each
-        GEMM op's kernel is also timed alone ("<op>#kernel" aggregates)."""
-        N.api.sj_model_profile(self.h, 0 if not on else 2 if cold else 3 if kernels else 1)
+        GEMM op's kernel is also timed alone ("<op>#kernel" aggregates);
+        instep: only those kernel times, with the step's second stream
+        running beside (the kernels share the chip as in the step)."""
+        N.api.sj_model_profile(self.h, 0 if not on else 4 if instep else 2 if cold else 3 if kernels else 1)
 
     def profile_collect(self) -> dict[str, tuple[float, int]]:
         """{op name: (total ms, calls)} for the ops run since the last collect

@@ -257,3 +257,25 @@ def test_attention_backward_workspace_accounting(B, T, HQ, HK):
     slots = sum(p["nparts"] for p in pieces if p["cut"] >= 0 and p["part"] == 0)
     if HQ == 3 * HK:  # the grouped launch: part sums of 12288 floats
         assert pairs * slots * 12288 * 4 <= partial
+
+
+def test_pvjp_library_decisions_on_reference_production_shapes():
+    """The library's host decision function (sj_pvjp_selects_compression)
+    on every group the reference's production configuration forms (its
+    recorded 44 compressed / 126 dense matrices: tests/test_oracle.py), with
+    the retain loop's member counts: the same verdict as the oracle for the
+    global q|k|v (512 patches x 512), the local q|k|v and gate|up (4096 bytes
+    x 128) and the single-use and expert products (rank 16, residual 0.25,
+    32-row blocks)."""
+    from oracle import pvjp
+    from sejong_amd import _native as N
+    lib = N.load()
+    cases = [  # n, a, b, donor, uses
+        (512, 512, 512, 512, 3), (512, 512, 256, 512, 3),                 # global q, k / v
+        (4096, 128, 128, 128, 3), (4096, 128, 384, 384, 2),               # local q|k|v, gate|up
+        (4096, 128, 128, 128, 1), (4096, 384, 128, 128, 1),               # attention_output, down
+        (512, 512, 4, 4, 1), (512, 128, 512, 512, 1), (4096, 512, 257, 257, 1),  # router, glue, head
+        (256, 512, 384, 384, 2), (512, 512, 384, 384, 2)]                 # an expert's gate|up
+    for n, a, b, donor, uses in cases:
+        want = pvjp.selects_compression(16, 0.25, 32, n, a, b, donor, uses)
+        assert bool(lib.sj_pvjp_selects_compression(16, 0.25, 32, n, a, b, donor, uses)) == want, (n, a, b, uses)

@@ -850,3 +850,82 @@ def test_blake3_published_digests_and_reference_fingerprints():
         with open(d + "validation.txt", "rb") as f:
             assert B3.corpus_fingerprint([f.read()]) == \
                 "9a1409d8fd61e18c2ca1fef712488fbe776e90f3c10fd9a9b88d9eb11503d16e"
+
+
+def _production_matmuls(expert_rows=256):
+    """The parameter products of one training step of the reference's
+    production model (configs/sejong.toml: hierarchical with 8-byte patches;
+    encoder and decoder 2 x d128 with 2 heads and FFN 384, window
+    128; global 8 x d512, 8 query / 4 KV heads, 4 SwiGLU experts of 384 with
+    top-2 routing; batch 8 x 512 bytes), in graph order, as (input id, rows,
+    input width, output width): architecture.rs:200-247 (Block::apply) and
+    368-393 (hidden_from_encoded).  Every expert sees `expert_rows` of the 512
+    patches (top-2 of 4: 256 on average; never all 512)."""
+    Ml, Mg = 8 * 512, 8 * 512 // 8
+    out, nid = [], [0]
+
+    def new():
+        nid[0] += 1
+        return nid[0]
+
+    def local():
+        for _ in range(2):
+            z, o, z2, h = new(), new(), new(), new()
+            out.extend([(z, Ml, 128, 128)] * 3)                       # q, k, v (2 heads = 2 KV heads)
+            out.append((o, Ml, 128, 128))                             # attention_output
+            out.extend([(z2, Ml, 128, 384)] * 2)                      # gate, up
+            out.append((h, Ml, 384, 128))                             # down
+
+    local()                                                           # encoder
+    out.append((new(), Mg, 128, 512))                                 # encoder_to_global (pooled)
+    for _ in range(8):                                                # global stage over the patches
+        z, o, z2 = new(), new(), new()
+        out.extend([(z, Mg, 512, 512), (z, Mg, 512, 256), (z, Mg, 512, 256)])
+        out.append((o, Mg, 512, 512))
+        out.append((z2, Mg, 512, 4))                                  # router
+        for _ in range(4):
+            xe, he = new(), new()
+            out.extend([(xe, expert_rows, 512, 384)] * 2)             # expert gate, up (gathered rows)
+            out.append((he, expert_rows, 384, 512))                   # expert down
+    out.append((new(), Mg, 512, 128))                                 # global_to_decoder (latent)
+    out.append((new(), 1, 512, 128))                                  # global_to_decoder (BOS row)
+    out.append((new(), Ml, 128, 128))                                 # encoder_to_decoder
+    local()                                                           # decoder
+    out.append((new(), Ml, 128, 512))                                 # output_projection
+    out.append((new(), Ml, 512, 257))                                 # output head (fp32 master)
+    return out
+
+
+def test_pvjp_graph_statistics_match_reference_production_record():
+    """The compression decisions and grouping (graph.rs:551-566, 915-1005,
+    with selects_compression and budget of parameter_vjp.rs:85-130) on the
+    reference's production configuration give the statistics its measurement
+    recorded for every one of its 64 steps: 44 compressed and 126 dense
+    matrices, 2 basis groups and 16 projection groups
+    (docs/measurements/2026-11-01-architecture-fit/applied.json,
+    parameter_vjp_statistics; rank 16, residual_fraction 0.25, block_rows
+    32).  The 16 groups are the 8 global q|k|v groups (512 patches) and the
+    encoder's and decoder's 2 q|k|v and 2 gate|up groups (4096 bytes: a
+    second token basis); single-use products and the expert products (fewer
+    routed rows than input columns) stay dense.  Also at the routing
+    extremes an expert can reach (any count below 512 rows)."""
+    import os
+    from oracle import pvjp
+    want = dict(compressed_matrices=44, dense_matrices=126, basis_groups=2, projection_groups=16)
+    for rows in (256, 1, 511):
+        mm = _production_matmuls(rows)
+        assert len(mm) == 170
+        assert pvjp.graph_statistics(mm, 16, 0.25, 32) == want, rows
+    rec = "/root/reference/docs/measurements/2026-11-01-architecture-fit/applied.json"
+    if os.path.exists(rec):
+        import json
+        steps = json.load(open(rec))["runs"][0]["measured_step_records"]
+        assert len(steps) == 64 and all(s["parameter_vjp_statistics"] == want for s in steps)
+    # the record constrains the inputs: other settings give other counts
+    # (all blocks selected: nothing compresses; 128-row blocks: the local
+    # stages' 128 features form one block, fully selected; every expert
+    # reaching 512 rows: its gate|up group forms too)
+    mm = _production_matmuls(256)
+    assert pvjp.graph_statistics(mm, 16, 1.0, 32)["compressed_matrices"] == 0
+    assert pvjp.graph_statistics(mm, 16, 0.25, 128)["compressed_matrices"] == 24
+    assert pvjp.graph_statistics(_production_matmuls(512), 16, 0.25, 32)["projection_groups"] > 16
