@@ -536,6 +536,12 @@ size_t sj_pvjp_prepare_workspace_bytes(long a, long n, long rank);
 int sj_pvjp_prepare(void *stream, const uint16_t *x_t, long ldxt, long a, long n, const float *q, long rank,
                     const int32_t *rows, long k, float inverse, float *left, float *e, uint16_t *e_hi,
                     uint16_t *e_lo, long lde, void *workspace, size_t workspace_bytes);
+/* The same with X in row layout, x [n][ldx] (the stored activation itself,
+ * no transposed copy): n, a and the leading dimensions multiples of 8.
+ * Workspace: sj_pvjp_prepare_workspace_bytes. */
+int sj_pvjp_prepare_rows(void *stream, const uint16_t *x, long ldx, long a, long n, const float *q, long rank,
+                         const int32_t *rows, long k, float inverse, float *left, float *e, uint16_t *e_hi,
+                         uint16_t *e_lo, long lde, void *workspace, size_t workspace_bytes);
 /* Engine::parameter_vjp, parameter_vjp.rs:308-320: coefficients = E dY
  * [rows][b] (right = rows 0..rank-1, tail = the rest) from the E planes and
  * dY^T planes [b][lddy] (columns past n zero).  Workspace:
@@ -544,6 +550,12 @@ size_t sj_pvjp_vjp_workspace_bytes(long rows, long b, long n);
 int sj_pvjp_vjp(void *stream, const uint16_t *e_hi, const uint16_t *e_lo, long lde, long rows, long n,
                 const uint16_t *dy_t_hi, const uint16_t *dy_t_lo, long lddy, long b, float *coefficients,
                 long ldc, void *workspace, size_t workspace_bytes);
+/* The same with dY in row layout, hi/lo planes [n][lddy] (the gradient
+ * planes the dX products read): n and b multiples of 8.  Workspace:
+ * sj_pvjp_vjp_workspace_bytes. */
+int sj_pvjp_vjp_rows(void *stream, const uint16_t *e_hi, const uint16_t *e_lo, long lde, long rows, long n,
+                     const uint16_t *dy_hi, const uint16_t *dy_lo, long lddy, long b, float *coefficients,
+                     long ldc, void *workspace, size_t workspace_bytes);
 /* GradientPlan (parameter_vjp.rs:329-530; kernels parameter.py:193-291):
  * per parameter W [rows][cols] fp32, G = dense (nullable) + sum over its
  * terms of scale * (left right + tail rows placed by row_map).  Terms of a

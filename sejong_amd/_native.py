@@ -127,8 +127,10 @@ SIGNATURES = {
     "sj_pvjp_basis": (_I, [_P, _P, _I, _L, _L, _P, _L, _F, _P, _P, _S]),
     "sj_pvjp_prepare_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_pvjp_prepare": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _F, _P, _P, _P, _P, _L, _P, _S]),
+    "sj_pvjp_prepare_rows": (_I, [_P, _P, _L, _L, _L, _P, _L, _P, _L, _F, _P, _P, _P, _P, _L, _P, _S]),
     "sj_pvjp_vjp_workspace_bytes": (_S, [_L, _L, _L]),
     "sj_pvjp_vjp": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _L, _P, _S]),
+    "sj_pvjp_vjp_rows": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _L, _L, _P, _L, _P, _S]),
     "sj_factored_meta_bytes": (_S, [_P, _L, _L]),
     "sj_factored_pack": (_I, [_P, _L, _P, _L, _P, _S, _P]),
     "sj_factored_apply": (_I, [_P, _P, _L, _I, _F, _F, _P]),

@@ -217,6 +217,15 @@ int rmsnorm_bwd_p_deferred(void* stream, const uint16_t* x, const uint16_t* w, c
                            float* dx, uint16_t* dx_hi, uint16_t* dx_lo, uint16_t* dx_t_hi, uint16_t* dx_t_lo,
                            long ldt, long rows, long d, float eps, float* partial);
 int rmsnorm_reduce_multi(void* stream, const sj::RmsReduceJob* jobs, long njobs, long max_d);
+// the parameter VJP's token-contracted products with one operand in row
+// layout (gemm_fast.hip): C = X^T B^T (X [K][ldx] one plane, B [N][K] hi/lo)
+// and C = A Y (A [M][K] hi/lo, Y [K][ldy] hi/lo); fp32 C, K % 8 == 0;
+// workspace as sj_gemm_planes_workspace_bytes(M, N, K)
+int gemm_planes_rows_a(void* stream, long M, long N, long K, const uint16_t* x, long ldx, const uint16_t* b_hi,
+                       const uint16_t* b_lo, long ldb, float* c, long ldc, void* workspace, size_t workspace_bytes);
+int gemm_planes_rows_b(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo, long lda,
+                       const uint16_t* y_hi, const uint16_t* y_lo, long ldy, float* c, long ldc, void* workspace,
+                       size_t workspace_bytes);
 // out[0] = FP64 sum of slots[0 .. count) in a fixed order (one workgroup)
 int sum_slots(hipStream_t stream, const double* slots, long count, double* out);
 // one-time kernel attribute setup (dynamic LDS limits), outside capture

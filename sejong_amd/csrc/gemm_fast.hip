@@ -1420,6 +1420,17 @@ int launch_planes(hipStream_t s, const FParams& p, int pa, int pb, int bm, int b
   return sjh::fail(SJ_ERR_UNSUPPORTED, "gemm: planes %d/%d for this epilogue", pa, pb);
 }
 
+// One operand in row layout, the other k-contiguous (the parameter VJP's
+// token-contracted products): TM 1, A = X [K][M] as one plane and B as two;
+// TM 2, A as two planes and B = Y [K][N] as two.
+template <int EPI, int TM>
+int launch_planes_one(hipStream_t s, const FParams& p, int pa, int pb, int bm, int bn, int splits) {
+  static_assert(TM == 1 || TM == 2, "one row-layout operand");
+  constexpr int PA = TM == 1 ? 1 : 2, PB = 2;
+  if (pa != PA || pb != PB) return sjh::fail(SJ_ERR_UNSUPPORTED, "gemm: planes %d/%d with row-layout operand %d", pa, pb, TM);
+  return launch_tile<EPI, PA, PB, TM>(s, p, bm, bn, splits);
+}
+
 bool ok16(const void* q) { return ((uintptr_t)q & 15) == 0; }
 
 // The row-plane SwiGLU epilogue moves G, U and the four planes in whole
@@ -1494,6 +1505,10 @@ int gemm_fast_prepare() {
   if (!status) status = set_attrs_planes<E_PLANES>();
   if (!status) status = set_attrs_planes<E_STORE, 3>();
   if (!status) status = set_attrs_planes<E_PARTIAL, 3>();
+  if (!status) status = set_attrs_tiles<E_STORE, 1, 2, 1>();
+  if (!status) status = set_attrs_tiles<E_PARTIAL, 1, 2, 1>();
+  if (!status) status = set_attrs_tiles<E_STORE, 2, 2, 2>();
+  if (!status) status = set_attrs_tiles<E_PARTIAL, 2, 2, 2>();
   if (!status) status = set_attrs_kw<E_STORE>();
   if (!status) status = set_attrs_kw<E_PARTIAL>();
   return status;
@@ -1581,11 +1596,19 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
     splits = (int)((K + kchunk - 1) / kchunk);
     p.kchunk = kchunk;
     p.partial = (float*)workspace;
-    int st = launch_planes<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
+    int st;
+    if constexpr (TM == 1 || TM == 2)
+      st = launch_planes_one<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
+    else
+      st = launch_planes<E_PARTIAL, TM>(s, p, pa, pb, bm, bn, splits);
     if (st) return st;
     reduce_partials(s, p, splits, workspace);
   } else {
-    int st = launch_planes<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
+    int st;
+    if constexpr (TM == 1 || TM == 2)
+      st = launch_planes_one<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
+    else
+      st = launch_planes<E_STORE, TM>(s, p, pa, pb, bm, bn, 1);
     if (st) return st;
     if (sjh::grad_sq().base && sjh::grad_sq().on) sjh::grad_sq().missed = true;
   }
@@ -1593,6 +1616,36 @@ int gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, cons
   return SJ_OK;
 }
 }  // namespace
+
+// The parameter VJP's two token-contracted products with one operand in row
+// layout (K = tokens, a multiple of 8; fp32 C):
+//   rows_a: C [M][N] = X^T B^T, X [K][ldx] one bf16 plane (row layout), B
+//           [N][K] hi/lo planes (k-contiguous);
+//   rows_b: C [M][N] = A Y, A [M][K] hi/lo planes (k-contiguous), Y [K][ldy]
+//           hi/lo planes (row layout).
+int sjh::gemm_planes_rows_a(void* stream, long M, long N, long K, const uint16_t* x, long ldx, const uint16_t* b_hi,
+                            const uint16_t* b_lo, long ldb, float* c, long ldc, void* workspace,
+                            size_t workspace_bytes) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M > 0 && N > 0 && K > 0 && M % 8 == 0 && K % 8 == 0 && ldx % 8 == 0 && ldb % 8 == 0 && ldx >= M &&
+                 ldb >= K && ldc >= N && x && b_hi && b_lo && ok16(x) && ok16(b_hi) && ok16(b_lo),
+             "matmul planes (row-layout A): M %ld N %ld K %ld ldx %ld ldb %ld (M, K and ld multiples of 8)", M, N, K,
+             ldx, ldb);
+  return gemm_planes<1>(stream, M, N, K, x, nullptr, ldx, b_hi, b_lo, ldb, c, SJ_F32, ldc, 0, workspace,
+                        workspace_bytes);
+}
+int sjh::gemm_planes_rows_b(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
+                            long lda, const uint16_t* y_hi, const uint16_t* y_lo, long ldy, float* c, long ldc,
+                            void* workspace, size_t workspace_bytes) {
+  if (int st0 = sjh::gemm_fast_prepare()) return st0;
+  SJ_REQUIRE(M > 0 && N > 0 && K > 0 && N % 8 == 0 && K % 8 == 0 && lda % 8 == 0 && ldy % 8 == 0 && lda >= K &&
+                 ldy >= N && ldc >= N && a_hi && a_lo && y_hi && y_lo && ok16(a_hi) && ok16(a_lo) && ok16(y_hi) &&
+                 ok16(y_lo),
+             "matmul planes (row-layout B): M %ld N %ld K %ld lda %ld ldy %ld (N, K and ld multiples of 8)", M, N, K,
+             lda, ldy);
+  return gemm_planes<2>(stream, M, N, K, a_hi, a_lo, lda, y_hi, y_lo, ldy, c, SJ_F32, ldc, 0, workspace,
+                        workspace_bytes);
+}
 
 extern "C" int sj_gemm_planes(void* stream, long M, long N, long K, const uint16_t* a_hi, const uint16_t* a_lo,
                               long lda, const uint16_t* b_hi, const uint16_t* b_lo, long ldb, void* c, int c_dtype,

@@ -938,8 +938,10 @@ int forward(sj_model* m) {
 // the forward basis from the up projection's output (its widest member,
 // the last one on ties: graph.rs:931-934); every later group reuses both
 // (one basis per (tokens, rank), one selection per width, graph.rs:
-// 957-982), so one seed is consumed per step.
-int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb, uint16_t* const* dyt) {
+// 957-982), so one seed is consumed per step.  Row-layout dW (rowdw): the
+// group's stored input and the dX chain's gradient planes are read as they
+// are; otherwise their transposed copies (x^T, dY^T).
+int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb, uint16_t* const* dy) {
   const long M = m->M, d = m->d, F = m->F, R = m->vjp_R, k = m->vjp_k, ldt = m->ldt;
   const long width = kind == 0 ? m->NQKV : 2 * F;
   if (l == m->L - 1 && kind == 1) {
@@ -948,10 +950,18 @@ int vjp_group(sj_model* m, long l, int kind, hipStream_t s, void* ws, size_t wsb
                                              m->vjp_scratch, m->vjp_cols, m->vjp_rows, m->vjp_map));
     OP("pvjp_basis", sj_pvjp_basis(s, m->uu[m->L - 1], SJ_BF16, F, M, m->vjp_cols, R, m->vjp_eps, m->vjp_q, ws, wsb));
   }
+  if (m->rowdw) {
+    const uint16_t* x = (const uint16_t*)(kind == 0 ? m->z[l] : m->z2[l]);
+    OP("pvjp_prepare", sj_pvjp_prepare_rows(s, x, d, d, M, m->vjp_q, R, m->vjp_rows, k, m->vjp_inverse,
+                                            m->vjp_left[kind][l], nullptr, m->vjp_eh, m->vjp_el, ldt, ws, wsb));
+    OP("pvjp_coefficients", sj_pvjp_vjp_rows(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dy[0], dy[1], width, width,
+                                             m->vjp_coeff[kind][l], width, ws, wsb));
+    return SJ_OK;
+  }
   const uint16_t* xt = kind == 0 ? m->zt[l] : m->z2t[l];
   OP("pvjp_prepare", sj_pvjp_prepare(s, xt, ldt, d, M, m->vjp_q, R, m->vjp_rows, k, m->vjp_inverse,
                                      m->vjp_left[kind][l], nullptr, m->vjp_eh, m->vjp_el, ldt, ws, wsb));
-  OP("pvjp_coefficients", sj_pvjp_vjp(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dyt[0], dyt[1], ldt, width,
+  OP("pvjp_coefficients", sj_pvjp_vjp(s, m->vjp_eh, m->vjp_el, ldt, R + k, M, dy[0], dy[1], ldt, width,
                                       m->vjp_coeff[kind][l], width, ws, wsb));
   return SJ_OK;
 }
@@ -1092,8 +1102,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       if (!early_dw) TRY(down_dw());
       OP("gate_up_dx", sj_gemm_planes(s, M, d, 2 * F, NP(KG, p)[0], NP(KG, p)[1], 2 * F, W + y.gu, nullptr, 2 * F,
                                       m->dz, SJ_F32, d, 0, ws, wsb));
-      if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, T(KG, p)));
-      if (rdw)
+      if (m->group_on[1]) TRY(vjp_group(m, l, 1, s2, ws2, wsb, rdw ? NP(KG, p) : T(KG, p)));
+      if (rdw && !m->group_all[1])
         GOP("gate_up_dw", sj_gemm_planes_tn(s2, d, 2 * F, M, (const uint16_t*)m->z2[l], nullptr, d, NP(KG, p)[0],
                                            NP(KG, p)[1], 2 * F, G + y.gu, SJ_F32, 2 * F, 0, ws2, wsb));
       else if (!m->group_all[1])
@@ -1142,8 +1152,8 @@ int stage_backward(sj_model* m, int si, const float* dzin, int& cur) {
       TRY(written(KQ, p));
       OP("qkv_dx", sj_gemm_planes(s, M, d, NQ, NP(KQ, p)[0], NP(KQ, p)[1], NQ, W + y.qkv, nullptr, NQ, m->dz, SJ_F32, d,
                                   0, ws, wsb));
-      if (m->group_on[0]) TRY(vjp_group(m, l, 0, s2, ws2, wsb, T(KQ, p)));
-      if (rdw)
+      if (m->group_on[0]) TRY(vjp_group(m, l, 0, s2, ws2, wsb, rdw ? NP(KQ, p) : T(KQ, p)));
+      if (rdw && !m->group_all[0])
         GOP("qkv_dw", sj_gemm_planes_tn(s2, d, NQ, M, (const uint16_t*)m->z[l], nullptr, d, NP(KQ, p)[0], NP(KQ, p)[1],
                                        NQ, G + y.qkv, SJ_F32, NQ, 0, ws2, wsb));
       else if (!m->group_all[0])
@@ -1722,7 +1732,10 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     st = vjp_decide(m);
     if (st) return fail_cleanup(st);
   }
-  m->rowdw = m->planes && !m->vjp;
+  // row-layout dW products (no transposed copies of activations or gradient
+  // planes; the parameter VJP reads the row layout too): cfg5 34.5 -> 36.9
+  // ms/step with the transposed copies written, dense SGD on one box
+  m->rowdw = m->planes;
   for (const Stage& S : m->stages) m->rowdw = m->rowdw && S.attn_tt;
 #define ALLOC(ptr, bytes)                                    \
   do {                                                       \

@@ -264,8 +264,9 @@ __global__ __launch_bounds__(256) void k_pvjp_qt(const float* __restrict__ q, in
 // E[R+i][tok] = (X^T[row_i][tok] - sum_r Q[tok][r] A[row_i][r]) * inverse,
 // zero for row_i = -1 (parameter.py:167-190); fp32 and planes.  Thread per
 // token: its Q row is read once, the block's RROWS selected rows of A sit
-// in LDS.
+// in LDS.  XROWS: X given in row layout, x [tok][ldxt] (else X^T [row][ldxt]).
 constexpr int RROWS = 16;
+template <bool XROWS>
 __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict__ xt, long ldxt,
                                                        const float* __restrict__ q, int R, long n,
                                                        const float* __restrict__ left, const int32_t* __restrict__ rows,
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
 #pragma unroll
       for (int r = 0; r < RMAX; r++)
         if (r < R) acc += qr[r] * sa[ii][r];
-      v = (bf2f(xt[row * ldxt + tok]) - acc) * inverse;
+      v = (bf2f(xt[XROWS ? tok * ldxt + row : row * ldxt + tok]) - acc) * inverse;
     }
     const long o = (R + i) * lde + tok;
     if (e) e[o] = v;
@@ -634,9 +635,38 @@ extern "C" int sj_pvjp_prepare(void* stream, const uint16_t* x_t, long ldxt, lon
                               workspace, workspace_bytes))
     return st;
   if (k > 0) {
-    hipLaunchKernelGGL(k_pvjp_residual, dim3((unsigned)((n8 + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
+    hipLaunchKernelGGL(k_pvjp_residual<false>, dim3((unsigned)((n8 + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
                        dim3(256), 0, s, (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, k, inverse, e,
                        (bf16_t*)e_hi, (bf16_t*)e_lo, lde, n8);
+    SJ_LAUNCH_CHECK("parameter_residual");
+  }
+  return SJ_OK;
+}
+
+// sj_pvjp_prepare with X in row layout (x [n][ldx], the stored activation
+// itself): left = X^T Q on the row-layout product, the residual rows read
+// X[tok][row].  n % 8 == 0 (the token rows are the products' K).
+extern "C" int sj_pvjp_prepare_rows(void* stream, const uint16_t* x, long ldx, long a, long n, const float* q,
+                                    long rank, const int32_t* rows, long k, float inverse, float* left, float* e,
+                                    uint16_t* e_hi, uint16_t* e_lo, long lde, void* workspace,
+                                    size_t workspace_bytes) {
+  SJ_REQUIRE(a > 0 && n > 0 && n % 8 == 0 && a % 8 == 0 && rank > 0 && k >= 0 && ldx >= a && ldx % 8 == 0 &&
+                 lde >= n && lde % 8 == 0 && ((uintptr_t)e_hi & 15) == 0 && ((uintptr_t)e_lo & 15) == 0 &&
+                 ((uintptr_t)x & 15) == 0,
+             "parameter_prepare (row-layout X): a %ld n %ld ldx %ld lde %ld (a, n and leading dimensions multiples "
+             "of 8)", a, n, ldx, lde);
+  hipStream_t s = (hipStream_t)stream;
+  const long qn = rank * n;
+  hipLaunchKernelGGL(k_pvjp_qt, dim3((unsigned)((qn + 255) / 256)), dim3(256), 0, s, q, (int)rank, n, n, e,
+                     (bf16_t*)e_hi, (bf16_t*)e_lo, lde);
+  SJ_LAUNCH_CHECK("parameter_prepare");
+  if (int st = sjh::gemm_planes_rows_a(stream, a, rank, n, x, ldx, e_hi, e_lo, lde, left, rank, workspace,
+                                       workspace_bytes))
+    return st;
+  if (k > 0) {
+    hipLaunchKernelGGL(k_pvjp_residual<true>, dim3((unsigned)((n + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
+                       dim3(256), 0, s, (const bf16_t*)x, ldx, q, (int)rank, n, left, rows, k, inverse, e,
+                       (bf16_t*)e_hi, (bf16_t*)e_lo, lde, n);
     SJ_LAUNCH_CHECK("parameter_residual");
   }
   return SJ_OK;
@@ -654,6 +684,18 @@ extern "C" int sj_pvjp_vjp(void* stream, const uint16_t* e_hi, const uint16_t* e
              "parameter_vjp: dimensions (leading dimensions >= n rounded up to 8, zero padded)");
   return sj_gemm_planes(stream, rows, b, n8, e_hi, e_lo, lde, dy_t_hi, dy_t_lo, lddy, coefficients, SJ_F32, ldc, 0,
                         workspace, workspace_bytes);
+}
+
+// sj_pvjp_vjp with dY in row layout (planes [n][lddy], the dX chain's own
+// gradient planes): coefficients = E dY on the row-layout product.
+// n % 8 == 0.
+extern "C" int sj_pvjp_vjp_rows(void* stream, const uint16_t* e_hi, const uint16_t* e_lo, long lde, long rows, long n,
+                                const uint16_t* dy_hi, const uint16_t* dy_lo, long lddy, long b, float* coefficients,
+                                long ldc, void* workspace, size_t workspace_bytes) {
+  SJ_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && b > 0 && b % 8 == 0 && ldc >= b && lde >= n && lddy >= b,
+             "parameter_vjp (row-layout dY): rows %ld n %ld b %ld (n and b multiples of 8)", rows, n, b);
+  return sjh::gemm_planes_rows_b(stream, rows, b, n, e_hi, e_lo, lde, dy_hi, dy_lo, lddy, coefficients, ldc,
+                                 workspace, workspace_bytes);
 }
 
 // tiles of a parameter list (the owners table's length)

@@ -64,7 +64,7 @@ def _prepare(N, X, Y, rank, frac, block_rows, seed, ydtype="f32"):
     return dict(R=R, blocks=blocks, S=S, k=k, n8=n8, eps=eps, cols=COL.host(), rows=ROWS.host(), map=MAP.host(),
                 q=Q.host().reshape(n, R), left=LEFT.host().reshape(a, R), e=E.host().reshape(R + k, n8),
                 eh=EH.host().reshape(R + k, n8), el=EL.host().reshape(R + k, n8), EH=EH, EL=EL, LEFT=LEFT, MAP=MAP,
-                inverse=inverse)
+                inverse=inverse, Q=Q, ROWS=ROWS)
 
 
 def _coefficients(N, P, D):
@@ -237,3 +237,35 @@ def test_cfg5_projection_group(N):
     assert rel(P["left"], A_ref) < 1e-5 and rel(P["e"], E_ref) < 1e-5
     C = _coefficients(N, P, D)
     assert rel(C.host().reshape(R + k, b), (P["eh"] + P["el"]) @ D) < 1e-5
+
+
+@pytest.mark.parametrize("n,a,b", [(1024, 256, 640), (8192, 1024, 512)])
+def test_row_layout_prepare_and_coefficients_match_transposed(N, n, a, b):
+    """sj_pvjp_prepare_rows / sj_pvjp_vjp_rows (X and dY in row layout, as the
+    step stores them) give the bits of the transposed-operand entry points."""
+    api, lib = N.api, N.load()
+    rng = np.random.default_rng(n + a)
+    X = O.round_to(rng.normal(0, 1, (n, a)), "bf16")
+    Y = O.round_to(rng.normal(0, 1, (n, 2 * b)), "bf16")
+    D = (rng.normal(0, 1, (n, b)) / n).astype(np.float32).astype(np.float64)
+    P = _prepare(N, X, Y, 16, 0.1, 32, 7, ydtype="bf16")
+    R, k, n8 = P["R"], P["k"], P["n8"]
+    XR = dev(X, "bf16")
+    LEFT, E = empty(a * R), empty((R + k) * n8)
+    EH, EL = empty((R + k) * n8, "bf16"), empty((R + k) * n8, "bf16")
+    ws = empty(max(lib.sj_pvjp_prepare_workspace_bytes(a, n, R), 256), "u8")
+    api.sj_pvjp_prepare_rows(None, XR.p, a, a, n, P["Q"].p, R, P["ROWS"].p, k, cf(P["inverse"]), LEFT.p, E.p, EH.p,
+                             EL.p, n8, ws.p, ws.nbytes)
+    sync()
+    np.testing.assert_array_equal(LEFT.host().reshape(a, R), P["left"])
+    np.testing.assert_array_equal(E.host().reshape(R + k, n8), P["e"])
+    np.testing.assert_array_equal(EH.host().reshape(R + k, n8), P["eh"])
+    np.testing.assert_array_equal(EL.host().reshape(R + k, n8), P["el"])
+    C = _coefficients(N, P, D)
+    dh, dl = _planes(D)
+    DH, DL = dev(dh, "bf16"), dev(dl, "bf16")
+    C2 = empty((R + k) * b)
+    wsv = empty(max(lib.sj_pvjp_vjp_workspace_bytes(R + k, b, n), 256), "u8")
+    api.sj_pvjp_vjp_rows(None, P["EH"].p, P["EL"].p, n8, R + k, n, DH.p, DL.p, b, b, C2.p, b, wsv.p, wsv.nbytes)
+    sync()
+    np.testing.assert_array_equal(C2.host(), C.host())
