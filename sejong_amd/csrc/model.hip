@@ -1877,8 +1877,11 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     ALLOC(m->mdzp, cap * d * 4);
   }
   if (m->planes) {
-    m->zt.resize(m->L); m->ot.resize(m->L); m->z2t.resize(m->L); m->ht.resize(m->L);
-    for (long l = 0; l < m->L; l++) {
+    // transposed copies of the retained activations: only the transposed-
+    // operand dW products read them (row-layout dW reads the rows)
+    m->zt.assign(m->L, nullptr); m->ot.assign(m->L, nullptr); m->z2t.assign(m->L, nullptr);
+    m->ht.assign(m->L, nullptr);
+    for (long l = 0; l < m->L && !m->rowdw; l++) {
       const Stage& S = m->stages[m->layers[l].stage];
       const size_t MT = (size_t)S.ldt, d = (size_t)S.d;
       ALLOC(m->zt[l], d * MT * 2);
@@ -2082,7 +2085,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   if (e == hipSuccess && m->mirror_t) e = hipMemsetAsync(m->mirror_t, 0, P * 2, s);
   if (e == hipSuccess && m->attn_cnt) e = hipMemsetAsync(m->attn_cnt, 0, cnt_bytes, s);
   // padding columns [M, ldt) of the transposed activations stay zero
-  for (long l = 0; l < m->L && m->planes; l++) {
+  for (long l = 0; l < m->L && m->planes && !m->rowdw; l++) {
     const Stage& S = m->stages[m->layers[l].stage];
     const size_t MT = (size_t)S.ldt;
     for (uint16_t* q : {m->zt[l], m->ot[l], m->z2t[l]})
