@@ -710,8 +710,10 @@ def workload_moe(args):
 def workload_pvjp(args):
     """cfg5 parameter-VJP pieces of one step: 16384
     tokens, d 1024, 12 layers, FFN 2752, rank 16, 10% of 32-row blocks.  One
-    index draw and one CGS2 basis (shared by all groups: same n, rank and
-    width), a prepare per projection group (QKV and gate/up of 12 layers),
+    index draw and one basis (shared by all groups: same n, rank and width),
+    a prepare per projection group (QKV and gate/up of 12 layers) on the
+    stored input rows and a coefficient GEMM per group on the row-layout dY
+    planes (the forms the training step runs),
     the coefficient GEMM of every compressed member (q, k, v, gate, up), and
     the factored SGD update over all 133.5M parameters (dense gradients for
     the single-use projections, embedding, norms and head).  The dense
@@ -732,7 +734,7 @@ def workload_pvjp(args):
     # donor: the up projection's output u [n][F] (widest member of the gate/up
     # group, the last one on ties)
     donor = B(n * F * 2).upload(_bf16(rng.normal(0, 1, (n, F))))
-    xt = B(d * n * 2).upload(_bf16(rng.normal(0, 1, (d, n))))
+    x = B(n * d * 2).upload(_bf16(rng.normal(0, 1, (n, d))))
     scr, cols, rows_, fmap = B((F + blocks) * 4), B(R * 4), B(k * 4), B(d * 4)
     q = B(n * R * 4)
     wsb = B(lib.sj_pvjp_basis_workspace_bytes(n, R))
@@ -740,10 +742,10 @@ def workload_pvjp(args):
     groups = []
     for g in range(2 * L):
         groups.append(dict(left=B(d * R * 4), e=B((R + k) * n * 4), eh=B((R + k) * n * 2), el=B((R + k) * n * 2)))
-    # dY^T planes of a group's members, concatenated as the step keeps them
-    # ([q|k|v] and [gate|up] rows): one coefficient GEMM per group
+    # dY planes of a group's members, concatenated as the step keeps them
+    # ([tokens][q|k|v] and [tokens][gate|up]): one coefficient GEMM per group
     W2 = 2 * F
-    dyh = B(W2 * n * 2).upload(_bf16(rng.normal(0, 1e-4, (W2, n))))
+    dyh = B(W2 * n * 2).upload(_bf16(rng.normal(0, 1e-4, (n, W2))))
     dyl = B(W2 * n * 2).upload(np.zeros(W2 * n, np.uint16))
     wsp = B(max(lib.sj_pvjp_prepare_workspace_bytes(d, n, R), lib.sj_pvjp_vjp_workspace_bytes(R + k, W2, n), 256))
     # parameters (reference layout shapes) and their gradients
@@ -790,10 +792,10 @@ def workload_pvjp(args):
         run("pvjp_indices", lambda: api.sj_pvjp_indices(None, seed, d, F, blocks, S, R, 32, scr.p(), cols.p(), rows_.p(), fmap.p()))
         run("pvjp_basis", lambda: api.sj_pvjp_basis(None, donor.p(), 4, F, n, cols.p(), R, cf(eps), q.p(), wsb.p(), wsb.nbytes))
         for g in groups:
-            run("pvjp_prepare", lambda: api.sj_pvjp_prepare(None, xt.p(), n, d, n, q.p(), R, rows_.p(), k, cf(blocks / S), g["left"].p(), g["e"].p(), g["eh"].p(), g["el"].p(), n, wsp.p(), wsp.nbytes))
+            run("pvjp_prepare", lambda: api.sj_pvjp_prepare_rows(None, x.p(), d, d, n, q.p(), R, rows_.p(), k, cf(blocks / S), g["left"].p(), g["e"].p(), g["eh"].p(), g["el"].p(), n, wsp.p(), wsp.nbytes))
         for gi, co, c in coeffs:
             g = groups[gi]
-            run("pvjp_coefficients", lambda: api.sj_pvjp_vjp(None, g["eh"].p(), g["el"].p(), n, R + k, n, dyh.p(), dyl.p(), n, c, co.p(), c, wsp.p(), wsp.nbytes))
+            run("pvjp_coefficients", lambda: api.sj_pvjp_vjp_rows(None, g["eh"].p(), g["el"].p(), n, R + k, n, dyh.p(), dyl.p(), W2, c, co.p(), c, wsp.p(), wsp.nbytes))
         run("factored_norm", lambda: api.sj_factored_apply(None, meta.p(), tiles.value, 2, cf(0), cf(0), part.p()))
         run("norm_sum", lambda: api.sj_sum_f64(None, part.p(), tiles.value, norm.p()))
         run("factored_sgd_update", lambda: api.sj_factored_apply(None, meta.p(), tiles.value, 1, cf(1e-2), cf(0.0), None))

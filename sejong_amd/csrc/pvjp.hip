@@ -265,8 +265,11 @@ __global__ __launch_bounds__(256) void k_pvjp_qt(const float* __restrict__ q, in
 // zero for row_i = -1 (parameter.py:167-190); fp32 and planes.  Thread per
 // token: its Q row is read once, the block's RROWS selected rows of A sit
 // in LDS.  XROWS: X given in row layout, x [tok][ldxt] (else X^T [row][ldxt]).
+// RB: a compile-time bound on the rank R (16, 32 or 64): the per-row sum
+// runs over RB terms, the ones past R predicated off, in the same order
+// whatever RB is.
 constexpr int RROWS = 16;
-template <bool XROWS>
+template <bool XROWS, int RB>
 __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict__ xt, long ldxt,
                                                        const float* __restrict__ q, int R, long n,
                                                        const float* __restrict__ left, const int32_t* __restrict__ rows,
@@ -285,9 +288,9 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
   __syncthreads();
   const long tok = blockIdx.x * 256L + threadIdx.x;
   if (tok >= n8) return;
-  float qr[RMAX];
+  float qr[RB];
 #pragma unroll
-  for (int r = 0; r < RMAX; r++)
+  for (int r = 0; r < RB; r++)
     if (r < R) qr[r] = tok < n ? q[tok * R + r] : 0.f;
   for (int ii = 0; ii < RROWS; ii++) {
     const long i = i0 + ii;
@@ -297,7 +300,7 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
     if (row >= 0 && tok < n) {
       float acc = 0.f;
 #pragma unroll
-      for (int r = 0; r < RMAX; r++)
+      for (int r = 0; r < RB; r++)
         if (r < R) acc += qr[r] * sa[ii][r];
       v = (bf2f(xt[XROWS ? tok * ldxt + row : row * ldxt + tok]) - acc) * inverse;
     }
@@ -308,6 +311,21 @@ __global__ __launch_bounds__(256) void k_pvjp_residual(const bf16_t* __restrict_
     eh[o] = h;
     el[o] = l;
   }
+}
+
+template <bool XROWS>
+void launch_residual(hipStream_t s, dim3 grid, const bf16_t* x, long ldx, const float* q, int R, long n,
+                     const float* left, const int32_t* rows, long k, float inverse, float* e, bf16_t* eh,
+                     bf16_t* el, long lde, long n8) {
+  if (R <= 16)
+    hipLaunchKernelGGL((k_pvjp_residual<XROWS, 16>), grid, dim3(256), 0, s, x, ldx, q, R, n, left, rows, k, inverse,
+                       e, eh, el, lde, n8);
+  else if (R <= 32)
+    hipLaunchKernelGGL((k_pvjp_residual<XROWS, 32>), grid, dim3(256), 0, s, x, ldx, q, R, n, left, rows, k, inverse,
+                       e, eh, el, lde, n8);
+  else
+    hipLaunchKernelGGL((k_pvjp_residual<XROWS, RMAX>), grid, dim3(256), 0, s, x, ldx, q, R, n, left, rows, k,
+                       inverse, e, eh, el, lde, n8);
 }
 
 // ------------------------------------------------------------------- apply
@@ -621,9 +639,10 @@ extern "C" int sj_pvjp_prepare(void* stream, const uint16_t* x_t, long ldxt, lon
                                const int32_t* rows, long k, float inverse, float* left, float* e, uint16_t* e_hi,
                                uint16_t* e_lo, long lde, void* workspace, size_t workspace_bytes) {
   const long n8 = (n + 7) / 8 * 8;
-  SJ_REQUIRE(a > 0 && n > 0 && rank > 0 && k >= 0 && ldxt >= n8 && ldxt % 8 == 0 && lde >= n8 && lde % 8 == 0 &&
+  SJ_REQUIRE(a > 0 && n > 0 && rank > 0 && rank <= RMAX && k >= 0 && ldxt >= n8 && ldxt % 8 == 0 && lde >= n8 &&
+                 lde % 8 == 0 &&
                  ((uintptr_t)e_hi & 15) == 0 && ((uintptr_t)e_lo & 15) == 0 && ((uintptr_t)x_t & 15) == 0,
-             "parameter_prepare: dimensions (leading dimensions multiples of 8, >= n rounded up to 8)");
+             "parameter_prepare: dimensions (rank <= 64, leading dimensions multiples of 8, >= n rounded up to 8)");
   hipStream_t s = (hipStream_t)stream;
   const long qn = rank * n8;
   hipLaunchKernelGGL(k_pvjp_qt, dim3((unsigned)((qn + 255) / 256)), dim3(256), 0, s, q, (int)rank, n, n8, e,
@@ -635,9 +654,9 @@ extern "C" int sj_pvjp_prepare(void* stream, const uint16_t* x_t, long ldxt, lon
                               workspace, workspace_bytes))
     return st;
   if (k > 0) {
-    hipLaunchKernelGGL(k_pvjp_residual<false>, dim3((unsigned)((n8 + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
-                       dim3(256), 0, s, (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, k, inverse, e,
-                       (bf16_t*)e_hi, (bf16_t*)e_lo, lde, n8);
+    launch_residual<false>(s, dim3((unsigned)((n8 + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
+                           (const bf16_t*)x_t, ldxt, q, (int)rank, n, left, rows, k, inverse, e, (bf16_t*)e_hi,
+                           (bf16_t*)e_lo, lde, n8);
     SJ_LAUNCH_CHECK("parameter_residual");
   }
   return SJ_OK;
@@ -650,11 +669,12 @@ extern "C" int sj_pvjp_prepare_rows(void* stream, const uint16_t* x, long ldx, l
                                     long rank, const int32_t* rows, long k, float inverse, float* left, float* e,
                                     uint16_t* e_hi, uint16_t* e_lo, long lde, void* workspace,
                                     size_t workspace_bytes) {
-  SJ_REQUIRE(a > 0 && n > 0 && n % 8 == 0 && a % 8 == 0 && rank > 0 && k >= 0 && ldx >= a && ldx % 8 == 0 &&
+  SJ_REQUIRE(a > 0 && n > 0 && n % 8 == 0 && a % 8 == 0 && rank > 0 && rank <= RMAX && k >= 0 && ldx >= a &&
+                 ldx % 8 == 0 &&
                  lde >= n && lde % 8 == 0 && ((uintptr_t)e_hi & 15) == 0 && ((uintptr_t)e_lo & 15) == 0 &&
                  ((uintptr_t)x & 15) == 0,
-             "parameter_prepare (row-layout X): a %ld n %ld ldx %ld lde %ld (a, n and leading dimensions multiples "
-             "of 8)", a, n, ldx, lde);
+             "parameter_prepare (row-layout X): a %ld n %ld ldx %ld lde %ld (rank <= 64; a, n and leading "
+             "dimensions multiples of 8)", a, n, ldx, lde);
   hipStream_t s = (hipStream_t)stream;
   const long qn = rank * n;
   hipLaunchKernelGGL(k_pvjp_qt, dim3((unsigned)((qn + 255) / 256)), dim3(256), 0, s, q, (int)rank, n, n, e,
@@ -664,9 +684,9 @@ extern "C" int sj_pvjp_prepare_rows(void* stream, const uint16_t* x, long ldx, l
                                        workspace_bytes))
     return st;
   if (k > 0) {
-    hipLaunchKernelGGL(k_pvjp_residual<true>, dim3((unsigned)((n + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
-                       dim3(256), 0, s, (const bf16_t*)x, ldx, q, (int)rank, n, left, rows, k, inverse, e,
-                       (bf16_t*)e_hi, (bf16_t*)e_lo, lde, n);
+    launch_residual<true>(s, dim3((unsigned)((n + 255) / 256), (unsigned)((k + RROWS - 1) / RROWS)),
+                          (const bf16_t*)x, ldx, q, (int)rank, n, left, rows, k, inverse, e, (bf16_t*)e_hi,
+                          (bf16_t*)e_lo, lde, n);
     SJ_LAUNCH_CHECK("parameter_residual");
   }
   return SJ_OK;
