@@ -793,6 +793,18 @@ int sj_model_set_adam_state(sj_model *m, const float *m_host, const float *v_hos
 /* Batch input: host arrays (synchronous copy) or device arrays (async D2D
  * on the model stream).  ids/targets int32 [batch*sequence]. */
 int sj_model_set_batch(sj_model *m, const int32_t *ids, const int32_t *targets, int on_device);
+/* Gradient accumulation (TrainConfig::accumulation; train lib.rs:390-415
+ * with Adam::accumulate, lib.rs:179-198): `observations` batches stacked
+ * ([observations][batch*sequence], host arrays).  Each following
+ * sj_model_train_step runs every observation's forward and backward on its
+ * batch (objective seed loss_scale / observations, loss summary weighted
+ * 1 / observations into its own slot), keeps the first observation's
+ * gradients and adds the later ones in order, then takes one FP64 norm and
+ * one AdamW update; sj_model_forward_backward leaves the summed gradients in
+ * the gradient arena, and sj_model_read_loss returns the sum of the slots.
+ * AdamW byte language models only; 1 <= observations <= 256.
+ * sj_model_set_batch returns to one observation per update. */
+int sj_model_set_batches(sj_model *m, const int32_t *ids, const int32_t *targets, long observations);
 /* Forward + backward only (gradients left in the model's gradient arena). */
 int sj_model_forward_backward(sj_model *m);
 /* One full training step: forward, backward, FP64 grad norm, clip, AdamW

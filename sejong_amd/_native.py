@@ -211,6 +211,7 @@ SIGNATURES = {
     "sj_model_get_adam_state": (_I, [_P, _P, _P, ctypes.POINTER(_L)]),
     "sj_model_set_adam_state": (_I, [_P, _P, _P, _L]),
     "sj_model_set_batch": (_I, [_P, _P, _P, _I]),
+    "sj_model_set_batches": (_I, [_P, _P, _P, _L]),
     "sj_model_forward_backward": (_I, [_P]),
     "sj_model_train_step": (_I, [_P, _F]),
     "sj_model_use_graph": (_I, [_P, _I]),

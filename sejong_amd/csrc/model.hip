@@ -379,6 +379,14 @@ struct sj_model {
   // hi/lo planes [M][Vp] written by the cross entropy
   bool lm_planes = false;
   bool defer_loss = false;  // set inside a training step: loss_summary runs after the backward's fork
+  // gradient accumulation (train lib.rs:390-415): observations per update,
+  // the observation being run, its batches stacked on the device, and the
+  // accumulator arena (Adam::accumulate)
+  static constexpr long OBS_MAX = 256;  // loss summary slots
+  long obs = 1, obs_slot = 0;
+  int32_t *obs_ids = nullptr, *obs_targets = nullptr;
+  long obs_cap = 0;
+  float* g_acc = nullptr;
   uint16_t* hp[4] = {};
   uint16_t* dlp[2] = {};
   TJob* tjobs = nullptr;
@@ -901,14 +909,18 @@ int forward(sj_model* m) {
     OP("value_bias", sj_bias_add(s, m->logits, m->Vp, m->w + m->bias, m->logits, m->Vp, R, n));
     OP("cross_entropy", sj_cross_entropy(s, m->logits, m->Vp, m->labels, m->loss_rows, m->dlogits, m->Vp, R, n,
                                          nullptr, 1.0f / (float)R));
-    OP("loss_summary", sj_loss_summary(s, m->loss_rows, R, m->loss, 0, 1.0f));
+    OP("loss_summary", sj_loss_summary(s, m->loss_rows, R, m->loss, m->obs_slot, 1.0f / (float)m->obs));
     return SJ_OK;
   }
   // fp32 head on the fp32 master (architecture.rs:160-167); hn's values are
   // exact in fp32 (Graph::cast to F32), so it is read in its storage dtype.
   // On the planes path the master enters as hi + lo bf16 planes (2^-17
   // relative) and the cross entropy leaves dlogits as hi/lo planes.
-  const float seed = 1.0f / (float)M;  // scale / count, graph.rs:546
+  // scale / count (graph.rs:546) with the objective's seed scale =
+  // loss_scale / accumulation (train lib.rs:409) for AdamW; the SGD driver's
+  // update takes its gradients unscaled (loss_scale 1 with the VJP)
+  const float scale = m->optimizer == 1 ? 1.0f : m->adam.loss_scale / (float)m->obs;
+  const float seed = scale / (float)M;
   if (m->lm_planes) {
     // no split-K (no workspace): a row's sum order does not depend on M,
     // so the cached forward's one-row product gives the same logits
@@ -925,7 +937,8 @@ int forward(sj_model* m) {
   }
   // the loss sum is read only by read_loss: in a training step it runs on
   // the second stream after the backward's fork, off the dX chain
-  if (!m->defer_loss) OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, 0, 1.0f));
+  if (!m->defer_loss)
+    OP("loss_summary", sj_loss_summary(s, m->loss_rows, M, m->loss, m->obs_slot, 1.0f / (float)m->obs));
   return SJ_OK;
 }
 
@@ -1315,7 +1328,7 @@ int backward_body(sj_model* m) {
     void* wsw = two ? m->ws2 : m->ws;
     if (m->defer_loss) {
       m->defer_loss = false;
-      OP("loss_summary", sj_loss_summary(sw, m->loss_rows, M, m->loss, 0, 1.0f));
+      OP("loss_summary", sj_loss_summary(sw, m->loss_rows, M, m->loss, m->obs_slot, 1.0f / (float)m->obs));
     }
     if (m->value_n)
       OP("head_dw", sj_gemm(sw, 1, 0, d, m->HV, m->HR, m->hsel, SJ_F32, d, m->dlogits, SJ_F32, m->Vp, G + m->out, SJ_F32,
@@ -1389,11 +1402,57 @@ int update(sj_model* m) {
   return SJ_OK;
 }
 
+int accumulate_observations(sj_model* m, bool deferred);
 int whole_step(sj_model* m) {
-  TRY(forward_deferred(m));
-  TRY(backward(m));
-  TRY(update(m));
-  return SJ_OK;
+  if (m->obs <= 1) {
+    TRY(forward_deferred(m));
+    TRY(backward(m));
+    TRY(update(m));
+    return SJ_OK;
+  }
+  // gradient accumulation (train lib.rs:390-415): each observation runs on
+  // its own batch, its loss summary lands in its slot with weight
+  // 1/accumulation and its backward is seeded with loss_scale/accumulation;
+  // Adam::accumulate keeps the first observation's gradients and adds the
+  // later ones in order (current + incoming, lib.rs:179-198); the update
+  // reads the accumulator.  The producers' FP64 norm slots hold only the last
+  // observation's gradients, so the norm sums the accumulated arena.
+  float* const g0 = m->g;
+  int st = accumulate_observations(m, true);
+  if (st) return st;
+  m->gsq_ok = false;
+  m->g = m->g_acc;
+  st = update(m);
+  m->g = g0;
+  return st;
+}
+
+// the observations' forward and backward passes with their gradients summed
+// into m->g_acc (deferred: the training step's two-stream form)
+int accumulate_observations(sj_model* m, bool deferred) {
+  float* const g0 = m->g;
+  int32_t* const ids0 = m->ids;
+  int32_t* const tg0 = m->targets;
+  const size_t gbytes = sizeof(float) * (size_t)m->n_params;
+  int st = SJ_OK;
+  for (long o = 0; o < m->obs && !st; o++) {
+    m->obs_slot = o;
+    m->ids = m->obs_ids + o * m->M;
+    m->targets = m->obs_targets + o * m->M;
+    st = deferred ? forward_deferred(m) : forward(m);
+    if (!st) st = backward(m);
+    if (st) break;
+    if (o == 0) {
+      const hipError_t e = hipMemcpyAsync(m->g_acc, g0, gbytes, hipMemcpyDeviceToDevice, m->stream);
+      if (e != hipSuccess) st = sjh::hip_check(e, "accumulate");
+    } else {
+      st = sj_add(m->stream, m->g_acc, SJ_F32, g0, SJ_F32, m->g_acc, SJ_F32, m->n_params, 1.0f);
+    }
+  }
+  m->obs_slot = 0;
+  m->ids = ids0;
+  m->targets = tg0;
+  return st;
 }
 
 // Rng::next_u64 (SplitMix64, crates/sejong-core/src/lib.rs:591-609) on the host
@@ -1985,7 +2044,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
   m->rope = m->stages[0].rope;
   ALLOC(m->ids, (size_t)m->M * 4);
   ALLOC(m->targets, (size_t)m->M * 4);
-  ALLOC(m->loss, 64);
+  ALLOC(m->loss, sizeof(double) * sj_model::OBS_MAX);
   ALLOC(m->sumsq, 64);
   if (gsq_eligible(m)) ALLOC(m->gsq, sizeof(double) * (size_t)sj_model::GSQ_CAP);
   ALLOC(m->status, 64);
@@ -2132,7 +2191,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (ps) return fail_cleanup(ps);
   }
   if (e == hipSuccess) e = hipMemsetAsync(m->status, 0, 64, s);
-  if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, 64, s);
+  if (e == hipSuccess) e = hipMemsetAsync(m->loss, 0, sizeof(double) * sj_model::OBS_MAX, s);
   if (e == hipSuccess) e = hipMemsetAsync(m->sumsq, 0, 64, s);
   if (e != hipSuccess) return fail_cleanup(sjh::hip_check(e, "model: clear arenas"));
   for (const Stage& S : m->stages) {
@@ -2247,9 +2306,57 @@ extern "C" int sj_model_set_adam_state(sj_model* m, const float* mh, const float
   return SJ_OK;
 }
 
+// a change of the step's structure (the observation count) needs a new capture
+static void drop_graph(sj_model* m) {
+  if (m->exec) hipGraphExecDestroy(m->exec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  m->exec = nullptr;
+  m->graph = nullptr;
+}
+
+extern "C" int sj_model_set_batches(sj_model* m, const int32_t* ids, const int32_t* targets, long observations) {
+  SJ_REQUIRE(m && ids && targets, "set_batches: null");
+  SJ_REQUIRE(!m->value_n && m->optimizer == 0,
+             "set_batches: gradient accumulation covers the byte language models trained with AdamW");
+  SJ_REQUIRE(observations >= 1 && observations <= sj_model::OBS_MAX, "set_batches: observations %ld (1 .. %ld)",
+             observations, sj_model::OBS_MAX);
+  const long n = observations * m->M;
+  for (long i = 0; i < n; i++)
+    SJ_REQUIRE(ids[i] >= 0 && ids[i] < m->V && targets[i] >= 0 && targets[i] < m->V,
+               "batch token %ld out of vocabulary", i);
+  SJ_HIP(hipStreamSynchronize(m->stream));
+  if (observations > m->obs_cap) {
+    void *pi = nullptr, *pt = nullptr;
+    TRY(dalloc(m, &pi, sizeof(int32_t) * (size_t)n));
+    TRY(dalloc(m, &pt, sizeof(int32_t) * (size_t)n));
+    m->obs_ids = (int32_t*)pi;
+    m->obs_targets = (int32_t*)pt;
+    m->obs_cap = observations;
+  }
+  if (observations > 1 && !m->g_acc) {
+    void* pg = nullptr;
+    TRY(dalloc(m, &pg, sizeof(float) * (size_t)m->n_params));
+    m->g_acc = (float*)pg;
+  }
+  SJ_HIP(hipMemcpy(m->obs_ids, ids, sizeof(int32_t) * (size_t)n, hipMemcpyHostToDevice));
+  SJ_HIP(hipMemcpy(m->obs_targets, targets, sizeof(int32_t) * (size_t)n, hipMemcpyHostToDevice));
+  if (observations == 1) {  // one observation: the ordinary batch buffers
+    SJ_HIP(hipMemcpy(m->ids, ids, sizeof(int32_t) * (size_t)m->M, hipMemcpyHostToDevice));
+    SJ_HIP(hipMemcpy(m->targets, targets, sizeof(int32_t) * (size_t)m->M, hipMemcpyHostToDevice));
+  }
+  if (observations != m->obs) drop_graph(m);
+  m->obs = observations;
+  return SJ_OK;
+}
+
 extern "C" int sj_model_set_batch(sj_model* m, const int32_t* ids, const int32_t* targets, int on_device) {
   SJ_REQUIRE(m && ids && targets, "set_batch: null");
   SJ_REQUIRE(!m->value_n, "set_batch: a native value model takes sj_model_set_value_batch");
+  if (m->obs != 1) {  // back to one observation per update
+    SJ_HIP(hipStreamSynchronize(m->stream));
+    drop_graph(m);
+    m->obs = 1;
+  }
   size_t bytes = sizeof(int32_t) * (size_t)m->M;
   if (on_device) {
     SJ_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyDeviceToDevice, m->stream));
@@ -2282,6 +2389,11 @@ extern "C" int sj_model_set_value_batch(sj_model* m, const int32_t* ids, const i
 extern "C" int sj_model_forward_backward(sj_model* m) {
   SJ_REQUIRE(m, "forward_backward: null");
   if (m->optimizer == 1) TRY(stage_sgd(m, 0.f));  // the backward's parameter-VJP seed
+  if (m->obs > 1) {  // the accumulated gradients of every observation, left in the gradient arena
+    TRY(accumulate_observations(m, false));
+    SJ_HIP(hipMemcpyAsync(m->g, m->g_acc, sizeof(float) * (size_t)m->n_params, hipMemcpyDeviceToDevice, m->stream));
+    return SJ_OK;
+  }
   TRY(forward(m));
   TRY(backward(m));
   return SJ_OK;
@@ -2418,7 +2530,11 @@ extern "C" int sj_model_read_loss(sj_model* m, double* loss, double* grad_norm) 
   SJ_HIP(hipStreamSynchronize(m->stream));
   double l = 0, ss = 0;
   int32_t flag = 0;
-  SJ_HIP(hipMemcpy(&l, m->loss, sizeof(double), hipMemcpyDeviceToHost));
+  {  // the step's loss: the observations' summaries (each weighted 1/accumulation), in order
+    double slots[sj_model::OBS_MAX];
+    SJ_HIP(hipMemcpy(slots, m->loss, sizeof(double) * (size_t)m->obs, hipMemcpyDeviceToHost));
+    for (long o = 0; o < m->obs; o++) l += slots[o];
+  }
   SJ_HIP(hipMemcpy(&ss, m->sumsq, sizeof(double), hipMemcpyDeviceToHost));
   SJ_HIP(hipMemcpy(&flag, m->status, sizeof(int32_t), hipMemcpyDeviceToHost));
   if (loss) *loss = l;

@@ -451,6 +451,18 @@ class Model:
         assert ids.size == self.tc.batch * self.tc.sequence == tg.size
         N.api.sj_model_set_batch(self.h, _np_ptr(ids), _np_ptr(tg), 0)
 
+    def set_batches(self, ids: np.ndarray, targets: np.ndarray):
+        """Gradient accumulation (train lib.rs:390-415): ids / targets hold
+        `observations` batches ([observations][batch * sequence]); each
+        following train_step runs every observation's forward and backward
+        (its own batch, seed loss_scale / observations, loss summary weighted
+        1 / observations) and one AdamW update on the summed gradients.
+        set_batch returns to one observation per update."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32); tg = np.ascontiguousarray(targets, dtype=np.int32)
+        n = self.tc.batch * self.tc.sequence
+        assert ids.size == tg.size and ids.size % n == 0
+        N.api.sj_model_set_batches(self.h, _np_ptr(ids), _np_ptr(tg), ids.size // n)
+
     def set_value_batch(self, ids: np.ndarray, positions: np.ndarray, labels: np.ndarray):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         pos = np.ascontiguousarray(positions, dtype=np.int32); lab = np.ascontiguousarray(labels, dtype=np.int32)
