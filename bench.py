@@ -38,7 +38,7 @@ GRAD_SQ_SLOTS = 0
 # plane-path kernels (bf16, head_dim 64, T a multiple of 64)
 OP_KERNEL = {"attention_bwd": "k_attn2_bwd", "attention_bwd_dq_dkv": "k_attn2_bwd_g<3>", "attention_bwd_delta": "k_attn_delta",
              "attention_bwd_kv_reduce": "k_attn_kv_reduce_rows", "attention_fwd": "k_attn2_fwd<3>",
-             "adamw": "k_adamw_multi", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd4",
+             "adamw": "k_adamw_tiles", "mirror_transpose": "k_transpose_jobs", "embedding_bwd": "k_embedding_bwd4",
              "embedding": "k_embedding_fwd", "cross_entropy": "k_cross_entropy_planes", "rmsnorm": "k_rms_fwd_t<3>",
              "rmsnorm_bwd": "k_rms_bwd_p<3>", "rmsnorm_dw_reduce": "k_rms_reduce_multi", "loss_summary": "k_loss_summary"}
 
