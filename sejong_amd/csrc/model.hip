@@ -425,6 +425,9 @@ struct sj_model {
   hipStream_t stream2 = nullptr;
   uint16_t* pt[4][2][2] = {};
   hipEvent_t ev_w[4][2] = {}, ev_r[4][2] = {}, ev_fork = nullptr, ev_join = nullptr, ev_norm = nullptr;
+  // the hierarchy's glue gradients on the second stream: written events
+  // (the dX chain produced a glue product's dY)
+  hipEvent_t ev_glue[2] = {};
   // norm-weight gradients of the planes path: every RMSNorm backward leaves
   // its per-row-block partial sums in a slot of its own, and one batched
   // reduce at the end of the backward (second stream) forms all dw
@@ -1233,25 +1236,42 @@ int hierarchy_backward(sj_model* m, int& cur) {
   void* ws = m->ws;
   const size_t wsb = m->ws_bytes;
   float** hg = m->hg;
+  // The glue products' weight gradients (and the BOS row's) whose dY the
+  // dX chain never overwrites (hg[0], hg[3], hg[4]) go on the second stream
+  // after a written event, beside the chain.  The two that read a stage's
+  // d(input) (m->dres[cur], overwritten by the next stage's backward) stay
+  // on the chain: a wait for the second stream, which queues the stages' dW
+  // products too, cost more than they take (cfg3 3.51 against 3.45 ms).
+  const bool two = two_streams(m);
+  hipStream_t s2 = two ? m->stream2 : s;
+  void* ws2 = two ? m->ws2 : ws;
+  auto to_s2 = [&](int k) -> int {  // s2 may read what the chain wrote so far
+    if (!two) return SJ_OK;
+    SJ_HIP(hipEventRecord(m->ev_glue[k], s));
+    SJ_HIP(hipStreamWaitEvent(s2, m->ev_glue[k], 0));
+    return SJ_OK;
+  };
   OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->dz, nullptr, hg[0], G + m->final_norm,
                                    Ml, dg, eps, ws, wsb));
+  TRY(to_s2(0));
+  OP("output_projection_dw", sj_gemm(s2, 1, 0, dd, dg, Ml, D.out, dt, dd, hg[0], SJ_F32, dg, G + m->h_op, SJ_F32, dg,
+                                     0, ws2, wsb));
   OP("output_projection_dx", sj_gemm(s, 0, 1, Ml, dd, dg, hg[0], SJ_F32, dg, wc(m, m->h_op), dt, dg, hg[1], SJ_F32, dd,
                                      0, ws, wsb));
-  OP("output_projection_dw", sj_gemm(s, 1, 0, dd, dg, Ml, D.out, dt, dd, hg[0], SJ_F32, dg, G + m->h_op, SJ_F32, dg, 0,
-                                     ws, wsb));
   TRY(stage_backward(m, 2, hg[1], cur));
   const float* dxd = m->dres[cur];  // d(decoder input) = d(bytes) = d(broadcast output)
   OP("encoder_to_decoder_dx", sj_gemm(s, 0, 1, Ml, de, dd, dxd, SJ_F32, dd, wc(m, m->h_e2d), dt, dd, hg[2], SJ_F32, de,
                                       0, ws, wsb));
+  OP("patch_broadcast_bwd", sj_patch_broadcast_bwd(s, dxd, B, E.T, dd, P, hg[3], hg[4]));
   OP("encoder_to_decoder_dw", sj_gemm(s, 1, 0, de, dd, Ml, E.out, dt, de, dxd, SJ_F32, dd, G + m->h_e2d, SJ_F32, dd, 0,
                                       ws, wsb));
-  OP("patch_broadcast_bwd", sj_patch_broadcast_bwd(s, dxd, B, E.T, dd, P, hg[3], hg[4]));
-  OP("global_to_decoder_dw", sj_gemm(s, 1, 0, dg, dd, Mg, Gs.out, dt, dg, hg[3], SJ_F32, dd, G + m->h_g2d, SJ_F32, dd, 0,
-                                     ws, wsb));
-  OP("bos_to_decoder_dw", sj_gemm(s, 1, 0, dg, dd, 1, wc(m, m->h_bos), dt, dg, hg[4], SJ_F32, dd, G + m->h_g2d, SJ_F32,
-                                  dd, 1, ws, wsb));
-  OP("bos_to_decoder_dx", sj_gemm(s, 0, 1, 1, dg, dd, hg[4], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, G + m->h_bos, SJ_F32,
-                                  dg, 0, ws, wsb));
+  TRY(to_s2(1));
+  OP("global_to_decoder_dw", sj_gemm(s2, 1, 0, dg, dd, Mg, Gs.out, dt, dg, hg[3], SJ_F32, dd, G + m->h_g2d, SJ_F32, dd,
+                                     0, ws2, wsb));
+  OP("bos_to_decoder_dw", sj_gemm(s2, 1, 0, dg, dd, 1, wc(m, m->h_bos), dt, dg, hg[4], SJ_F32, dd, G + m->h_g2d, SJ_F32,
+                                  dd, 1, ws2, wsb));
+  OP("bos_to_decoder_dx", sj_gemm(s2, 0, 1, 1, dg, dd, hg[4], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, G + m->h_bos, SJ_F32,
+                                  dg, 0, ws2, wsb));
   OP("global_to_decoder_dx", sj_gemm(s, 0, 1, Mg, dg, dd, hg[3], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, hg[5], SJ_F32, dg,
                                      0, ws, wsb));
   TRY(stage_backward(m, 1, hg[5], cur));
@@ -2167,6 +2187,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_norm, hipEventDisableTiming);
+    for (int k = 0; k < 2 && e == hipSuccess && m->hier; k++) e = hipEventCreateWithFlags(&m->ev_glue[k], hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_tr_fork, hipEventDisableTiming);
     m->ev_tr.assign(m->tgroups.size(), nullptr);
     for (size_t g = 0; g < m->ev_tr.size() && e == hipSuccess; g++)
@@ -2232,6 +2253,8 @@ extern "C" int sj_model_destroy(sj_model* m) {
   if (m->ev_fork) hipEventDestroy(m->ev_fork);
   if (m->ev_join) hipEventDestroy(m->ev_join);
   if (m->ev_norm) hipEventDestroy(m->ev_norm);
+  for (hipEvent_t ev : m->ev_glue)
+    if (ev) hipEventDestroy(ev);
   if (m->ev_tr_fork) hipEventDestroy(m->ev_tr_fork);
   for (hipEvent_t ev : m->ev_tr)
     if (ev) hipEventDestroy(ev);
