@@ -425,9 +425,10 @@ struct sj_model {
   hipStream_t stream2 = nullptr;
   uint16_t* pt[4][2][2] = {};
   hipEvent_t ev_w[4][2] = {}, ev_r[4][2] = {}, ev_fork = nullptr, ev_join = nullptr, ev_norm = nullptr;
-  // the hierarchy's glue gradients on the second stream: written events
-  // (the dX chain produced a glue product's dY)
-  hipEvent_t ev_glue[2] = {};
+  // the hierarchy's glue on the second stream: [0, 1] backward written
+  // events (the dX chain produced a glue product's dY), [2, 3] the forward's
+  // fork and join around the decoder-side products of the encoder output
+  hipEvent_t ev_glue[4] = {};
   // norm-weight gradients of the planes path: every RMSNorm backward leaves
   // its per-row-block partial sums in a slot of its own, and one batched
   // reduce at the end of the backward (second stream) forms all dw
@@ -845,6 +846,7 @@ int stage_forward(sj_model* m, int si) {
 // broadcast added to encoder_to_decoder of the encoded bytes, the decoder
 // stage, output_projection and the final norm (into hn).  Every product
 // stores in the compute dtype (Graph::matmul, graph.rs:212-221).
+bool two_streams(const sj_model* m);
 int hierarchy_forward(sj_model* m) {
   hipStream_t s = m->stream;
   const int dt = m->dt;
@@ -853,16 +855,30 @@ int hierarchy_forward(sj_model* m) {
   const long B = m->B, P = m->P, de = E.d, dg = G.d, dd = D.d, Ml = E.M, Mg = G.M;
   void* ws = m->ws;
   const size_t wsb = m->ws_bytes;
+  // the BOS row's projection (parameters only) and encoder_to_decoder (the
+  // encoder output only) run on the second stream beside the pool, the
+  // global stage and global_to_decoder; the broadcast waits for both
+  const bool two = two_streams(m);
+  hipStream_t s2 = two ? m->stream2 : s;
+  void* ws2 = two ? m->ws2 : ws;
+  if (two) {
+    SJ_HIP(hipEventRecord(m->ev_glue[2], s));
+    SJ_HIP(hipStreamWaitEvent(s2, m->ev_glue[2], 0));
+  }
+  OP("bos_to_decoder", sj_gemm(s2, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, m->bosd, dt, dd, 0,
+                               ws2, wsb));
+  OP("encoder_to_decoder", sj_gemm(s2, 0, 0, Ml, dd, de, E.out, dt, de, wc(m, m->h_e2d), dt, dd, m->bytes, dt, dd, 0,
+                                   ws2, wsb));
   OP("patch_pool", sj_patch_pool(s, E.out, dt, B, E.T, de, P, m->pooled));
   OP("encoder_to_global", sj_gemm(s, 0, 0, Mg, dg, de, m->pooled, dt, de, wc(m, m->h_e2g), dt, dg, xin(m, G.first), dt,
                                   dg, 0, ws, wsb));
   TRY(stage_forward(m, 1));
   OP("global_to_decoder", sj_gemm(s, 0, 0, Mg, dd, dg, G.out, dt, dg, wc(m, m->h_g2d), dt, dd, m->gd, dt, dd, 0, ws, wsb));
-  OP("bos_to_decoder", sj_gemm(s, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, m->bosd, dt, dd, 0,
-                               ws, wsb));
+  if (two) {
+    SJ_HIP(hipEventRecord(m->ev_glue[3], s2));
+    SJ_HIP(hipStreamWaitEvent(s, m->ev_glue[3], 0));
+  }
   OP("patch_broadcast", sj_patch_broadcast(s, m->gd, m->bosd, dt, B, E.T, dd, P, m->zb));
-  OP("encoder_to_decoder", sj_gemm(s, 0, 0, Ml, dd, de, E.out, dt, de, wc(m, m->h_e2d), dt, dd, m->bytes, dt, dd, 0, ws,
-                                   wsb));
   OP("decoder_input", sj_add(s, m->bytes, dt, m->zb, dt, xin(m, D.first), dt, Ml * dd, 1.f));
   TRY(stage_forward(m, 2));
   OP("output_projection", sj_gemm(s, 0, 0, Ml, dg, dd, D.out, dt, dd, wc(m, m->h_op), dt, dg, m->opo, dt, dg, 0, ws, wsb));
@@ -2187,7 +2203,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_norm, hipEventDisableTiming);
-    for (int k = 0; k < 2 && e == hipSuccess && m->hier; k++) e = hipEventCreateWithFlags(&m->ev_glue[k], hipEventDisableTiming);
+    for (int k = 0; k < 4 && e == hipSuccess && m->hier; k++) e = hipEventCreateWithFlags(&m->ev_glue[k], hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&m->ev_tr_fork, hipEventDisableTiming);
     m->ev_tr.assign(m->tgroups.size(), nullptr);
     for (size_t g = 0; g < m->ev_tr.size() && e == hipSuccess; g++)
