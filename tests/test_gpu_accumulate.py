@@ -107,6 +107,68 @@ def test_accumulated_step_graph_equals_eager_and_set_batch_returns_to_one():
     assert out[0][5] == out[1][5]
 
 
+def _family(kind):
+    from sejong_amd.model import ExpertConfig, HierarchyConfig, ModelConfig, TrainConfig, init_params
+    if kind == "moe":
+        mc = ModelConfig(width=256, layers=2, heads=4, kv_heads=2, ffn_width=512, context=128, precision="bf16",
+                         experts=ExpertConfig(count=4, top_k=2, ffn_width=256))
+        tc = TrainConfig(sequence=128, batch=2, learning_rate=1e-3, weight_decay=0.1)
+    else:
+        mc = ModelConfig(width=256, layers=2, heads=4, kv_heads=2, ffn_width=512, context=256, precision="bf16",
+                         hierarchy=HierarchyConfig(patch_size=4, encoder_width=128, encoder_layers=1, encoder_heads=2,
+                                                   encoder_ffn_width=256, decoder_width=128, decoder_layers=2,
+                                                   decoder_heads=2, decoder_ffn_width=384, local_window=96))
+        tc = TrainConfig(sequence=256, batch=2, learning_rate=1e-3, weight_decay=0.1)
+    return mc, tc, init_params(mc, std=0.02)
+
+
+@pytest.mark.parametrize("kind", ["moe", "hier"])
+def test_accumulation_across_model_families(kind):
+    """The MoE and the hierarchical byte models accumulate the same way as
+    the dense one: two observations give fp32(gA / 2 + gB / 2) bit for bit
+    (routing, patch pooling and the glue products are linear in the seed,
+    which halves exactly) and the loss (lossA + lossB) / 2; two accumulated
+    steps replayed from the graph equal two eager ones bit for bit."""
+    from sejong_amd.model import Model, byte_batch
+    from sejong_amd.rng import Rng
+    mc, tc, params = _family(kind)
+    rng = Rng(19)
+    ia, ta = byte_batch(rng, tc.batch, tc.sequence)
+    ib, tb = byte_batch(rng, tc.batch, tc.sequence)
+    ids, tg = np.stack([ia, ib]), np.stack([ta, tb])
+    model = Model(mc, tc)
+    try:
+        model.set_params(params)
+        model.set_batch(ia, ta); model.forward_backward(); ga = model.get_grads(); la = model.read_loss()[0]
+        model.set_batch(ib, tb); model.forward_backward(); gb = model.get_grads(); lb = model.read_loss()[0]
+        model.set_batches(ids, tg)
+        model.forward_backward()
+        gab, lab = model.get_grads(), model.read_loss()[0]
+    finally:
+        model.close()
+    half = np.float32(0.5)
+    np.testing.assert_array_equal(gab, (ga * half).astype(np.float32) + (gb * half).astype(np.float32))
+    assert abs(lab - (la + lb) / 2) <= 1e-12 * abs(lab), (lab, la, lb)
+    out = []
+    for graph in (False, True):
+        model = Model(mc, tc)
+        try:
+            model.set_params(params)
+            model.set_batches(ids, tg)
+            model.use_graph(graph)
+            losses = []
+            for _ in range(2):
+                model.train_step(tc.learning_rate)
+                losses.append(model.read_loss())
+            out.append((model.get_params(), model.get_grads(), losses))
+        finally:
+            model.close()
+    np.testing.assert_array_equal(out[0][0], out[1][0])
+    np.testing.assert_array_equal(out[0][1], out[1][1])
+    assert out[0][2] == out[1][2]
+    assert np.all(np.isfinite(out[0][0]))
+
+
 def test_set_batches_rejects_bad_arguments():
     from sejong_amd import _native as N
     from sejong_amd.model import Model, byte_batch
