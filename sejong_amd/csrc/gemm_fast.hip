@@ -1272,8 +1272,11 @@ int splits_for(long M, long N, long K, int bm, int bn);
 // Tile and split-K plan of sj_gemm_planes (measured on the cfg2 and cfg5
 // step shapes with the occupancy-chosen pipeline depth):
 //   very long K (>= 8192) with a short output (M <= 512 or N <= 64: the
-//   token-contracted products of the parameter VJP): 64x128 tiles (64x64
-//   for N < 128) and 4..16 K slices of >= 512;
+//   token-contracted products of the parameter VJP): 64x64 tiles and
+//   floor(4 x CUs / tiles) K slices, clamped to 8..16 and to slices of
+//   >= 512 (cfg5 coefficients 144 x 1536 x 16384: 14 slices, 66 -> 51 us;
+//   144 x 5504 x 16384: 8 slices, 175 -> 158 us; 64x128 tiles lose at every
+//   slice count);
 //   dW-shaped products (K >= 2048, at most one 64x64 tile per CU): one K
 //   slice up to K = 4096, else 4, and the largest tile giving min(2 per CU,
 //   slices x the 64x64 tiles) workgroups (cfg5 attention-output dW: 128x64
@@ -1287,12 +1290,21 @@ void plan(long M, long N, long K, int pa, int& bm, int& bn, int& splits, bool ro
   const char* es = getenv("SJ_GEMM_SPLITS");
   if (!et && !es) {
     if (K >= 8192 && (M <= 512 || N <= 64)) {
+      static int lkn = -1, lks = 0;
+      if (lkn < 0) {  // sweeps: SJ_GEMM_LK_TILE=64x<bn>, SJ_GEMM_LK_SPLITS=<n>
+        lkn = 0;
+        const char* e = getenv("SJ_GEMM_LK_TILE");
+        int a = 0, b = 0;
+        if (e && sscanf(e, "%dx%d", &a, &b) == 2 && a == 64 && (b == 64 || b == 128)) lkn = b;
+        if (const char* s = getenv("SJ_GEMM_LK_SPLITS")) lks = atoi(s);
+      }
       bm = 64;
-      bn = N >= 128 ? 128 : 64;
+      bn = lkn && N >= 128 ? lkn : 64;
       const long t = tiles(M, N, bm, bn);
-      long sp = (4 * cu + t - 1) / t;
-      sp = sp < 4 ? 4 : sp;
+      long sp = 4 * cu / t;
+      sp = sp < 8 ? 8 : sp;
       sp = sp > 16 ? 16 : sp;
+      if (lks > 0) sp = lks;
       sp = sp > K / 512 ? K / 512 : sp;
       splits = (int)sp;
       return;
