@@ -509,6 +509,50 @@ def copy_probe(mib: int):
           flush=True)
 
 
+def copy_reference(byte_counts, reps: int = 9):
+    """The practical ceiling of a bandwidth-bound op of a given size: the
+    library's plain copy (k_cast, fp32 -> fp32) moving the same bytes, half
+    read and half written, timed hot and with the cold-cache pass's 512 MiB
+    write in front of it.  That write leaves dirty lines in the 256 MB
+    Infinity Cache whose write-back the next kernel pays for, so a cold copy
+    runs well below a hot one.  Returns {bytes: (hot_us, cold_us)}, medians."""
+    import ctypes
+    import statistics
+    from sejong_amd import _native as N
+    api = N.api
+    keep = []
+    top = max(byte_counts)
+    half = (top // 2 + 15) // 16 * 16
+    src, dst = _Buf(api, half, keep), _Buf(api, half, keep)
+    flush_n = 512 * (1 << 20) // 4
+    flush = _Buf(api, flush_n * 4, keep)
+    api.sj_fill(None, src.p(), 0, half // 4, ctypes.c_float(1.0))
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    api.sj_event_create(ctypes.byref(a)); api.sj_event_create(ctypes.byref(b))
+    ms = ctypes.c_float()
+    out = {}
+    try:
+        for nbytes in byte_counts:
+            n = max(nbytes // 8, 1)  # fp32 elements read (and written)
+            times = {False: [], True: []}
+            for cold in (False, True):
+                for i in range(reps + 2):
+                    if cold:
+                        api.sj_fill(None, flush.p(), 0, flush_n, ctypes.c_float(0.0))
+                    api.sj_event_record(a, None)
+                    api.sj_cast(None, src.p(), 0, dst.p(), 0, n)
+                    api.sj_event_record(b, None)
+                    api.sj_event_elapsed(a, b, ctypes.byref(ms))
+                    if i >= 2:
+                        times[cold].append(ms.value * 1e3)
+            out[nbytes] = (statistics.median(times[False]), statistics.median(times[True]))
+    finally:
+        api.sj_event_destroy(a); api.sj_event_destroy(b)
+        for buf in keep:
+            api.sj_free(buf.p())
+    return out
+
+
 # ------------------------------------------------------------ workloads
 class _Buf:
     """A device buffer from the library allocator (torch is not loaded:
@@ -956,12 +1000,26 @@ def main():
             cold_rows[op]["issued"] = {"bytes": int(iss), "cold_gbs": round(iss / (cold_us * 1e-6) / 1e9, 1),
                                        "cold_frac": round(iss / (cold_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
     if cold_rows:
-        log("  bandwidth-bound ops, hot vs cold cache (512 MiB written before each op):")
+        # each op beside a plain copy of its own (issued) byte count under the
+        # same protocol: the fraction of the copy's rate the op reaches
+        sizes = {op: r.get("issued", r)["bytes"] for op, r in cold_rows.items()}
+        ref = copy_reference(sorted(set(sizes.values())))
+        for op, r in cold_rows.items():
+            chot, ccold = ref[sizes[op]]
+            r["copy_same_bytes"] = {"bytes": sizes[op], "hot_us": round(chot, 3), "cold_us": round(ccold, 3),
+                                    "cold_gbs": round(sizes[op] / (ccold * 1e-6) / 1e9, 1)}
+            r["hot_vs_copy"] = round(chot / r["hot_us"], 4)
+            r["cold_vs_copy"] = round(ccold / r["cold_us"], 4)
+        log("  bandwidth-bound ops, hot vs cold cache (512 MiB written before each op), "
+            "and a plain copy of the op's issued bytes under the same protocol:")
         for op, r in sorted(cold_rows.items(), key=lambda kv: -kv[1]["bytes"]):
+            c = r["copy_same_bytes"]
             log(f"  {op:24s} {r['bytes'] / 1e6:8.2f} MB  hot {r['hot_us']:8.2f} us {r['hot_gbs']:8.1f} GB/s  "
                 f"cold {r['cold_us']:8.2f} us {r['cold_gbs']:8.1f} GB/s ({100 * r['cold_frac']:.1f}% of HBM)" +
                 (f"; issued {r['issued']['bytes'] / 1e6:.2f} MB, {100 * r['issued']['cold_frac']:.1f}% cold"
-                 if "issued" in r else ""))
+                 if "issued" in r else "") +
+                f"; copy hot {c['hot_us']:.2f} cold {c['cold_us']:.2f} us -> op at "
+                f"{100 * r['hot_vs_copy']:.0f}% / {100 * r['cold_vs_copy']:.0f}% of the copy's rate")
     roofline = kernel_roofline(prof, kern_only, op_kernel, mc, tc, args.config, kern_instep)
     # whole-step MFMA fraction (algorithmic GEMM + attention flops / step time)
     step_flops = sum(op_work(op, mc, tc)[1] * calls for op, (_, calls) in prof.items()

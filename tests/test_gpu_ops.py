@@ -233,6 +233,51 @@ def test_cross_entropy_and_loss_summary(api):
     assert abs(s - L.host().sum() * 0.5 / R) < 1e-9 * abs(s)
 
 
+def _bf16_rne(x32):
+    """fp32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = np.asarray(x32, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("xd,yd", [("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16"), ("bf16", "f32")])
+def test_cast_copy_bits_offsets_and_tails(api, xd, yd):
+    """Engine::cast / copy_into (kernels.py:11-14): the same-dtype copy moves
+    the bits (NaN payloads, signed zeros, denormals included), through the
+    16-byte vector path when both pointers are aligned and the element loop
+    for the rest; f32 -> bf16 rounds to nearest even; nothing outside
+    y[0, n) is written."""
+    rng = np.random.default_rng(8)
+    item = {"f32": 4, "bf16": 2}
+    for n in (1, 3, 4, 5, 8, 9, 1000, 4099, 300001):
+        for xo, yo in ((0, 0), (item[xd], 0), (0, item[yd]), (16, 16)):
+            if xd == "f32" and yd == "f32":  # any bits: a NaN payload, -0, the smallest denormal
+                xbits = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+                xbits[:3] = np.array([0x7FC01234, 0x80000000, 0x00000001], np.uint32)[:min(n, 3)]
+            elif xd == "f32":  # finite values for the rounding check
+                xbits = rng.normal(0, 3, n).astype(np.float32).view(np.uint32)
+            else:
+                xbits = _bf16_rne(rng.normal(0, 3, n).astype(np.float32))
+                if yd == "bf16":
+                    xbits[:2] = np.array([0x7FC1, 0x8000], np.uint16)[:min(n, 2)]
+            xraw = xbits.view(np.uint8)
+            X = dev(np.concatenate([np.zeros(xo, np.uint8), xraw]), "u8")
+            guard = np.full(yo + n * item[yd] + 64, 0xA5, np.uint8)
+            Y = dev(guard, "u8")
+            print(f"[cast] {xd}->{yd} n {n} offsets {xo}/{yo}", flush=True)
+            api.sj_cast(None, ctypes.c_void_p(X.ptr + xo), DT[xd], ctypes.c_void_p(Y.ptr + yo), DT[yd], n)
+            sync()
+            got = Y.host()
+            assert np.all(got[:yo] == 0xA5) and np.all(got[yo + n * item[yd]:] == 0xA5), (n, xo, yo)
+            body = got[yo:yo + n * item[yd]]
+            if xd == yd:
+                want = xraw
+            elif yd == "bf16":
+                want = _bf16_rne(xbits.view(np.float32)).view(np.uint8)
+            else:
+                want = (xbits.astype(np.uint32) << 16).view(np.uint8)
+            np.testing.assert_array_equal(body, want, err_msg=f"{xd}->{yd} n {n} offsets {xo}/{yo}")
+
+
 def test_embedding_forward_backward(api):
     rng = np.random.default_rng(8)
     V, D, Nn = 257, 384, 3000
