@@ -663,7 +663,9 @@ def workload_moe(args):
     grouped gate/up and down, combine + residual; the backward (combine,
     grouped down dX + SwiGLU, grouped dW, grouped gate/up dX, gather +
     routing backward + router dW); AdamW on the fp32 expert masters and
-    the bf16 mirror cast.  Attention is not part of this measurement."""
+    the bf16 mirror cast.  The forms the training step runs: the grouped dW
+    on the row-layout operands (packed rows and the dX chain's planes), no
+    transposed copies.  Attention is not part of this measurement."""
     import ctypes
     import numpy as np
     from sejong_amd import _native as N
@@ -692,13 +694,13 @@ def workload_moe(args):
     out = B(M * d * 2)
     logits, ids, wts = B(M * E * 2), B(S * 4), B(S * 4)
     tok, slt, cnt, off, ps, pp = B(E * S * 4), B(E * S * 4), B(E * 4), B((E + 1) * 4), B(cap * 4), B(S * 4)
-    zp, zpt = B(cap * d * 2), B(d * cap * 2)
-    g_, u_, h_, ht = B(cap * F * 2), B(cap * F * 2), B(cap * F * 2), B(F * cap * 2)
+    zp = B(cap * d * 2)
+    g_, u_, h_ = B(cap * F * 2), B(cap * F * 2), B(cap * F * 2)
     yp = B(cap * d * 2)
     dres = B(M * d * 4).upload(rng.normal(0, 1e-3, (M, d)).astype(np.float32))
-    dxh, dxl, dxth, dxtl = (B(cap * d * 2) for _ in range(4))
+    dxh, dxl = (B(cap * d * 2) for _ in range(2))
     dwts = B(S * 4)
-    dgh, dgl, dgth, dgtl = (B(cap * 2 * F * 2) for _ in range(4))
+    dgh, dgl = (B(cap * 2 * F * 2) for _ in range(2))
     dzp, dz, dlog, dwr = B(cap * d * 4), B(M * d * 4), B(M * E * 4), B(d * E * 4)
     ws = B(max(lib.sj_gemm_workspace_bytes(d, E, M), 256))
     api.sj_synchronize(None)
@@ -708,17 +710,17 @@ def workload_moe(args):
         for y in layers:
             run("router_topk", lambda: api.sj_router_topk(None, z.p(), d, y["wr"].p(), d, M, E, K, logits.p(), ids.p(), wts.p()))
             run("route_pack", lambda: api.sj_route_pack(None, ids.p(), M, K, E, tok.p(), slt.p(), cnt.p(), off.p(), ps.p(), pp.p(), cap))
-            run("moe_gather", lambda: api.sj_moe_gather(None, z.p(), d, d, ps.p(), K, cap, zp.p(), zpt.p(), cap))
-            run("expert_gate_up", lambda: api.sj_moe_gate_up_fwd(None, off.p(), E, cap, zp.p(), d, d, y["gu_t"].p(), y["gu_t"].p(F * d * 2), d, 2 * F * d, F, g_.p(), u_.p(), h_.p(), F, ht.p(), cap))
+            run("moe_gather", lambda: api.sj_moe_gather(None, z.p(), d, d, ps.p(), K, cap, zp.p(), None, cap))
+            run("expert_gate_up", lambda: api.sj_moe_gate_up_fwd(None, off.p(), E, cap, zp.p(), d, d, y["gu_t"].p(), y["gu_t"].p(F * d * 2), d, 2 * F * d, F, g_.p(), u_.p(), h_.p(), F, None, cap))
             run("expert_down", lambda: api.sj_moe_down_fwd(None, off.p(), E, cap, h_.p(), F, F, y["d_t"].p(), F, d * F, d, yp.p(), d))
             run("combine_residual", lambda: api.sj_moe_combine(None, yp.p(), d, d, ids.p(), pp.p(), wts.p(), M, K, x1.p(), d, out.p(), d))
         for y in reversed(layers):
             gu_off = E * d * 2 * F
-            run("combine_bwd", lambda: api.sj_moe_combine_bwd(None, yp.p(), d, d, ps.p(), wts.p(), K, cap, dres.p(), d, dxh.p(), dxl.p(), dxth.p(), dxtl.p(), cap, dwts.p()))
-            run("expert_down_dx_swiglu", lambda: api.sj_moe_down_bwd_swiglu_p(None, off.p(), E, cap, dxh.p(), dxl.p(), d, d, y["mirror"].p(gu_off * 2), d, F * d, F, g_.p(), u_.p(), F, dgh.p(), dgl.p(), 2 * F, dgth.p(), dgtl.p(), cap))
-            run("expert_down_dw", lambda: api.sj_moe_gemm_dw(None, off.p(), E, cap, F, d, ht.p(), cap, dxth.p(), dxtl.p(), cap, y["g"].p(gu_off * 4), d, F * d))
+            run("combine_bwd", lambda: api.sj_moe_combine_bwd(None, yp.p(), d, d, ps.p(), wts.p(), K, cap, dres.p(), d, dxh.p(), dxl.p(), None, None, cap, dwts.p()))
+            run("expert_down_dx_swiglu", lambda: api.sj_moe_down_bwd_swiglu_p(None, off.p(), E, cap, dxh.p(), dxl.p(), d, d, y["mirror"].p(gu_off * 2), d, F * d, F, g_.p(), u_.p(), F, dgh.p(), dgl.p(), 2 * F, None, None, cap))
+            run("expert_down_dw", lambda: api.sj_moe_gemm_dw_tn(None, off.p(), E, cap, F, d, h_.p(), F, dxh.p(), dxl.p(), d, y["g"].p(gu_off * 4), d, F * d))
             run("expert_gate_up_dx", lambda: api.sj_moe_gemm_rows(None, off.p(), E, cap, d, 2 * F, dgh.p(), dgl.p(), 2 * F, y["mirror"].p(), 2 * F, d * 2 * F, dzp.p(), d, 0))
-            run("expert_gate_up_dw", lambda: api.sj_moe_gemm_dw(None, off.p(), E, cap, d, 2 * F, zpt.p(), cap, dgth.p(), dgtl.p(), cap, y["g"].p(), 2 * F, d * 2 * F))
+            run("expert_gate_up_dw", lambda: api.sj_moe_gemm_dw_tn(None, off.p(), E, cap, d, 2 * F, zp.p(), d, dgh.p(), dgl.p(), 2 * F, y["g"].p(), 2 * F, d * 2 * F))
             run("gather_route_bwd", lambda: api.sj_moe_gather_bwd(None, dzp.p(), d, d, ids.p(), pp.p(), wts.p(), logits.p(), dwts.p(), y["wr"].p(), M, K, E, dres.p(), d, dz.p(), d, dlog.p()))
             run("router_dw", lambda: api.sj_gemm(None, 1, 0, d, E, M, z.p(), 4, d, dlog.p(), 0, E, dwr.p(), 0, E, 0, ws.p(), ws.nbytes))
         for y in layers:
