@@ -464,6 +464,21 @@ __global__ __launch_bounds__(NT) void k_moe_gather(const bf16_t* __restrict__ x,
   }
 }
 
+// the gather without the transposed copy (row-layout dW): one thread per
+// 16-byte chunk of a packed row
+__global__ __launch_bounds__(NT) void k_moe_gather16(const bf16_t* __restrict__ x, long ldx, long d,
+                                                     const int32_t* __restrict__ pslot, int K, long cap,
+                                                     bf16_t* __restrict__ y) {
+  const long cpr = d / 8, total = cap * cpr;
+  for (long q = blockIdx.x * (long)NT + threadIdx.x; q < total; q += (long)gridDim.x * NT) {
+    const long p = q / cpr, c = (q - p * cpr) * 8;
+    const int s = pslot[p];
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (s >= 0) v = *(const u32x4*)(x + (long)(s / K) * ldx + c);
+    *(u32x4*)(y + p * d + c) = v;
+  }
+}
+
 // a token's K (expert, packed position, weight) in ascending expert order
 // (unrolled compare-exchange over KMAX entries; unused entries sort last)
 __device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, const int32_t* ppos, const float* w,
@@ -494,6 +509,7 @@ __device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, c
 // Block::apply (architecture.rs:245): u = bf16(sum_e w*y_e) with each
 // product rounded before its add (the reference's atomic_add of weight*value,
 // launches in expert order), out = bf16(residual + u).  One wave per token.
+template <bool V8>
 __global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ yp, long ldy, long d,
                                                     const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
                                                     const float* __restrict__ weights, long R, int K,
@@ -505,6 +521,38 @@ __global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ y
   int pos[KMAX];
   float wk[KMAX];
   const int n = token_routes(t, K, ids, ppos, weights, pos, wk);
+  if constexpr (V8) {  // 8 columns per lane, 16-byte accesses; the same arithmetic per column
+    for (long c = 8 * lane; c < d; c += 512) {
+      float a[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) a[i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < KMAX; j++) {
+        if (j >= n) break;
+        const u32x4 v = *(const u32x4*)(yp + pos[j] * ldy + c);
+        const uint32_t vv[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          a[2 * i] = a[2 * i] + mul_rn(wk[j], bf2f((bf16_t)(vv[i] & 0xffffu)));
+          a[2 * i + 1] = a[2 * i + 1] + mul_rn(wk[j], bf2f((bf16_t)(vv[i] >> 16)));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) a[i] = round_bf(a[i]);
+      if (residual) {
+        const u32x4 r = *(const u32x4*)(residual + t * ldr + c);
+        const uint32_t rr[4] = {r[0], r[1], r[2], r[3]};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          a[2 * i] = bf2f((bf16_t)(rr[i] & 0xffffu)) + a[2 * i];
+          a[2 * i + 1] = bf2f((bf16_t)(rr[i] >> 16)) + a[2 * i + 1];
+        }
+      }
+      *(u32x4*)(out + t * ldo + c) = u32x4{pack2(f2bf(a[0]), f2bf(a[1])), pack2(f2bf(a[2]), f2bf(a[3])),
+                                           pack2(f2bf(a[4]), f2bf(a[5])), pack2(f2bf(a[6]), f2bf(a[7]))};
+    }
+    return;
+  }
   for (long c = 2 * lane; c < d; c += 128) {
     float a = 0.f, b = 0.f;
 #pragma unroll
@@ -808,6 +856,13 @@ extern "C" int sj_moe_gather(void* stream, const uint16_t* x, long ldx, long d, 
                  (!y_t || (ldt >= capacity && ldt % 8 == 0 && ((uintptr_t)y_t & 15) == 0)),
              "gather (experts): d %ld (<= 1024, multiple of 8), capacity %ld", d, capacity);
   if (capacity == 0) return SJ_OK;
+  if (!y_t && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0) {
+    const long chunks = capacity * (d / 8), blocks = (chunks + NT - 1) / NT;
+    hipLaunchKernelGGL(k_moe_gather16, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(NT), 0,
+                       (hipStream_t)stream, (const bf16_t*)x, ldx, d, pslot, (int)top_k, capacity, (bf16_t*)y);
+    SJ_LAUNCH_CHECK("gather");
+    return SJ_OK;
+  }
   const size_t lds = sizeof(bf16_t) * TR * (size_t)d;
   hipLaunchKernelGGL(k_moe_gather, dim3((unsigned)(capacity / TR)), dim3(NT), lds, (hipStream_t)stream,
                      (const bf16_t*)x, ldx, d, pslot, (int)top_k, capacity, (bf16_t*)y, (bf16_t*)y_t, ldt);
@@ -822,9 +877,11 @@ extern "C" int sj_moe_combine(void* stream, const uint16_t* yp, long ldy, long d
                  top_k > 0 && top_k <= KMAX,
              "expert combine dimensions");
   if (rows == 0) return SJ_OK;
-  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream,
-                     (const bf16_t*)yp, ldy, d, ids, ppos, weights, rows, (int)top_k, (const bf16_t*)residual, ldr,
-                     (bf16_t*)out, ldo);
+  const bool v8 = d % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && (!residual || (ldr % 8 == 0 && ((uintptr_t)residual & 15) == 0)) &&
+                  ((uintptr_t)yp & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  auto kern = v8 ? k_moe_combine<true> : k_moe_combine<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream, (const bf16_t*)yp, ldy, d, ids, ppos, weights, rows, (int)top_k,
+                     (const bf16_t*)residual, ldr, (bf16_t*)out, ldo);
   SJ_LAUNCH_CHECK("hierarchy_expert_combine");
   return SJ_OK;
 }

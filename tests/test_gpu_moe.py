@@ -82,7 +82,16 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     api.sj_moe_down_fwd(None, OFF.p, E, cap, H.p, F, F, WDT.p, F, d * F, d, YP.p, d)
     OUT = empty(M * d, "bf16")
     api.sj_moe_combine(None, YP.p, d, d, IDS.p, PP.p, WTS.p, M, K, X1.p, d, OUT.p, d)
+    # the row-only gather (16-byte chunks) and the combine through its
+    # 2-column path (an output stride that is not a multiple of 8) give the
+    # same bits as the forms above
+    ZP2 = zeros(cap * d, "bf16")
+    api.sj_moe_gather(None, Z.p, d, d, PS.p, K, cap, ZP2.p, None, cap)
+    OUT2 = zeros(M * (d + 2), "bf16")
+    api.sj_moe_combine(None, YP.p, d, d, IDS.p, PP.p, WTS.p, M, K, X1.p, d, OUT2.p, d + 2)
     sync()
+    np.testing.assert_array_equal(ZP2.host(), ZP.host())
+    np.testing.assert_array_equal(OUT2.host().reshape(M, d + 2)[:, :d], OUT.host().reshape(M, d))
 
     logits = LOG.host().reshape(M, E)
     assert_stored_close(logits, z @ wr, "bf16", "logits", terms=np.abs(z) @ np.abs(wr))
