@@ -636,6 +636,46 @@ __global__ __launch_bounds__(NT) void k_moe_combine_bwd(const bf16_t* __restrict
   }
 }
 
+// The combine backward without transposed planes (row-layout dW): one wave
+// per packed row, 8 columns per lane in 16- and 32-byte accesses; dx and its
+// planes as above, dw summed per lane over its columns in order, then across
+// the wave.
+__global__ __launch_bounds__(NT) void k_moe_combine_bwd8(const bf16_t* __restrict__ yp, long ldy, long d,
+                                                         const int32_t* __restrict__ pslot,
+                                                         const float* __restrict__ weights, int K, long cap,
+                                                         const float* __restrict__ dy, long lddy,
+                                                         bf16_t* __restrict__ hi, bf16_t* __restrict__ lo,
+                                                         float* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const long p = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (p >= cap) return;
+  const int s = pslot[p];
+  const long tok = s >= 0 ? s / K : -1;
+  const float w = s >= 0 ? weights[s] : 0.f;
+  float dot = 0.f;
+  for (long c = 8 * lane; c < d; c += 512) {
+    u32x4 ph = u32x4{0u, 0u, 0u, 0u}, pl = u32x4{0u, 0u, 0u, 0u};
+    if (tok >= 0) {
+      const float4 g0 = *(const float4*)(dy + tok * lddy + c), g1 = *(const float4*)(dy + tok * lddy + c + 4);
+      const u32x4 yv = *(const u32x4*)(yp + p * ldy + c);
+      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      bf16_t h[8], l[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t word = yv[i >> 1];
+        dot += bf2f((bf16_t)((i & 1) ? word >> 16 : word & 0xffffu)) * g[i];
+        split_bf(mul_rn(g[i], w), h[i], l[i]);
+      }
+      ph = u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
+      pl = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
+    }
+    *(u32x4*)(hi + p * d + c) = ph;
+    *(u32x4*)(lo + p * d + c) = pl;
+  }
+  dot = wave_sum(dot);
+  if (lane == 0 && s >= 0) dw[s] = dot;
+}
+
 // Per token: route_topk backward (dlogits), router dX (dlogits W_r^T,
 // W_r [d][E] bf16), the gather's scatter-add (sum of the token's expert
 // input gradients in ascending expert order) and the tape's accumulation
@@ -895,6 +935,14 @@ extern "C" int sj_moe_combine_bwd(void* stream, const uint16_t* yp, long ldy, lo
                  ((uintptr_t)dx_t_hi & 15) == 0 && ((uintptr_t)dx_t_lo & 15) == 0,
              "expert combine backward dimensions (transposed planes both or neither)");
   if (capacity == 0) return SJ_OK;
+  if (!dx_t_hi && ldy % 8 == 0 && lddy % 8 == 0 && ((uintptr_t)yp & 15) == 0 && ((uintptr_t)dy & 15) == 0 &&
+      ((uintptr_t)dx_hi & 15) == 0 && ((uintptr_t)dx_lo & 15) == 0) {
+    hipLaunchKernelGGL(k_moe_combine_bwd8, dim3((unsigned)(capacity / 4)), dim3(NT), 0, (hipStream_t)stream,
+                       (const bf16_t*)yp, ldy, d, pslot, weights, (int)top_k, capacity, dy, lddy, (bf16_t*)dx_hi,
+                       (bf16_t*)dx_lo, dweights);
+    SJ_LAUNCH_CHECK("hierarchy_expert_backward");
+    return SJ_OK;
+  }
   const size_t lds = 2 * sizeof(bf16_t) * TRB * (size_t)d;
   hipLaunchKernelGGL(k_moe_combine_bwd, dim3((unsigned)(capacity / TRB)), dim3(NT), lds, (hipStream_t)stream,
                      (const bf16_t*)yp, ldy, d, pslot, weights, (int)top_k, capacity, dy, lddy, (bf16_t*)dx_hi,

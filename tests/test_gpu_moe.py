@@ -148,6 +148,10 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     DXH, DXL, DXTH, DXTL = (zeros(cap * d, "bf16") for _ in range(4))
     DWT = empty(M * K)
     api.sj_moe_combine_bwd(None, YP.p, d, d, PS.p, WTS.p, K, cap, DUP.p, d, DXH.p, DXL.p, DXTH.p, DXTL.p, cap, DWT.p)
+    # the rows-only form (one wave per packed row, 8 columns per lane): the
+    # same planes bit for bit; its dw sums in another order (checked below)
+    DXH8, DXL8, DWT8 = zeros(cap * d, "bf16"), zeros(cap * d, "bf16"), empty(M * K)
+    api.sj_moe_combine_bwd(None, YP.p, d, d, PS.p, WTS.p, K, cap, DUP.p, d, DXH8.p, DXL8.p, None, None, cap, DWT8.p)
     DGH, DGL, DGTH, DGTL = (zeros(cap * 2 * F, "bf16") for _ in range(4))
     api.sj_moe_down_bwd_swiglu_p(None, OFF.p, E, cap, DXH.p, DXL.p, d, d, WD.p, d, F * d, F, G.p, U.p, F, DGH.p,
                                  DGL.p, 2 * F, DGTH.p, DGTL.p, cap)
@@ -196,6 +200,9 @@ def test_moe_ffn_forward_backward(api, lib, M, d, E, F, K):
     acts = dict(logits=logits, ids=ids, w=w, per=per)
     dz_ref, dwr_ref, grads_ref, dwts_ref, dlog_ref = moe.moe_backward(z, wr, experts, acts, dup)
     assert rel(DWT.host(), dwts_ref) < 1e-5
+    assert rel(DWT8.host(), dwts_ref) < 1e-5
+    np.testing.assert_array_equal(DXH8.host(), DXH.host())
+    np.testing.assert_array_equal(DXL8.host(), DXL.host())
     assert rel(DLOG.host(), dlog_ref) < 1e-4
     dwd = DWD.host().reshape(E, F, d)
     dwgu = DWGU.host().reshape(E, d, 2 * F)
