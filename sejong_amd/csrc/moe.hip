@@ -19,6 +19,7 @@
 // k_moe_gather_bwd (route_topk backward + router dX + the gather's
 // scatter-add, summed per token without atomics).
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -104,6 +105,75 @@ __global__ __launch_bounds__(NT) void k_router_topk(const bf16_t* __restrict__ z
         weights[r * K + k] = w[k];
       }
   }
+}
+
+// The same with LPT lanes per token (64 / LPT tokens per wave; d a multiple
+// of 8 LPT, E of 8, aligned rows): lane j of a token accumulates columns
+// 8j .. 8j+7 (+ 8 LPT i) for every expert from 16-byte chunks of z and
+// W_r, an xor tree over the token's lanes adds the sums (the same bits on
+// every lane: each add is commutative), and the token's first lane rounds
+// the logits, stores them and runs the top-k.  Against one wave per token,
+// the reduction takes log2(LPT) steps instead of 6 and the serial top-k
+// runs for 64 / LPT tokens per wave at once.
+template <int EW, int LPT>
+__global__ __launch_bounds__(NT) void k_router_topk_lanes(const bf16_t* __restrict__ z, long ldz,
+                                                          const bf16_t* __restrict__ wr, long d, long R, int E, int K,
+                                                          bf16_t* __restrict__ logits, int32_t* __restrict__ ids,
+                                                          float* __restrict__ weights) {
+  constexpr int EE = 8 * EW;
+  const int j = threadIdx.x % LPT;
+  const long r = (blockIdx.x * (long)NT + threadIdx.x) / LPT;
+  const bool live = r < R;
+  float acc[EE];
+#pragma unroll
+  for (int e = 0; e < EE; e++) acc[e] = 0.f;
+  if (live) {
+    for (long c8 = 8L * j; c8 < d; c8 += 8 * LPT) {
+      const u32x4 zv = *(const u32x4*)(z + r * ldz + c8);
+      float zf[8];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        zf[2 * i] = __uint_as_float(zv[i] << 16);
+        zf[2 * i + 1] = __uint_as_float(zv[i] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const bf16_t* wrow = wr + (c8 + i) * E;
+#pragma unroll
+        for (int e8 = 0; e8 < EE; e8 += 8) {
+          if (e8 >= E) break;
+          const u32x4 wv = *(const u32x4*)(wrow + e8);
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            acc[e8 + 2 * q] += zf[i] * __uint_as_float(wv[q] << 16);
+            acc[e8 + 2 * q + 1] += zf[i] * __uint_as_float(wv[q] & 0xffff0000u);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < LPT; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < EE; e++) acc[e] += __shfl_xor(acc[e], o, WAVE);
+  if (!live || j != 0) return;
+  float sc[EMAX];
+#pragma unroll
+  for (int e = 0; e < EMAX; e++) sc[e] = e < EE && e < E ? round_bf(acc[e < EE ? e : 0]) : 0.f;
+#pragma unroll
+  for (int e8 = 0; e8 < EE; e8 += 8)
+    if (e8 < E)
+      *(u32x4*)(logits + r * E + e8) = u32x4{pack2(f2bf(sc[e8]), f2bf(sc[e8 + 1])), pack2(f2bf(sc[e8 + 2]), f2bf(sc[e8 + 3])),
+                                             pack2(f2bf(sc[e8 + 4]), f2bf(sc[e8 + 5])), pack2(f2bf(sc[e8 + 6]), f2bf(sc[e8 + 7]))};
+  int32_t id[KMAX];
+  float w[KMAX];
+  topk_rows(sc, E, K, id, w);
+#pragma unroll
+  for (int k = 0; k < KMAX; k++)
+    if (k < K) {
+      ids[r * K + k] = id[k];
+      weights[r * K + k] = w[k];
+    }
 }
 
 // The same with 16-byte loads (d % 8 == 0, E % 8 == 0, aligned rows): lane
@@ -830,7 +900,24 @@ extern "C" int sj_router_topk(void* stream, const uint16_t* z, long ldz, const u
              "router top-k dimensions (experts <= %d, top_k <= %d)", EMAX, KMAX);
   if (rows == 0) return SJ_OK;
   const bool vec = d % 8 == 0 && ldz % 8 == 0 && experts % 8 == 0 && ((uintptr_t)z & 15) == 0 &&
-                   ((uintptr_t)w_router & 15) == 0;
+                   ((uintptr_t)w_router & 15) == 0 && ((uintptr_t)logits & 15) == 0;
+  static int lpt = -1;
+  if (lpt < 0) {
+    const char* e = getenv("SJ_ROUTER_LANES");  // sweeps: 8, 16, or 64 (one wave per token)
+    lpt = e ? atoi(e) : 16;
+  }
+  if (vec && (lpt == 8 || lpt == 16) && d % (8 * lpt) == 0) {
+    const long threads = rows * lpt;
+    const dim3 grid((unsigned)((threads + NT - 1) / NT));
+    auto kern = lpt == 8 ? (experts <= 8 ? k_router_topk_lanes<1, 8> : experts <= 16 ? k_router_topk_lanes<2, 8>
+                                                                                     : k_router_topk_lanes<4, 8>)
+                         : (experts <= 8 ? k_router_topk_lanes<1, 16> : experts <= 16 ? k_router_topk_lanes<2, 16>
+                                                                                      : k_router_topk_lanes<4, 16>);
+    hipLaunchKernelGGL(kern, grid, dim3(NT), 0, (hipStream_t)stream, (const bf16_t*)z, ldz,
+                       (const bf16_t*)w_router, d, rows, (int)experts, (int)top_k, (bf16_t*)logits, ids, weights);
+    SJ_LAUNCH_CHECK("router_topk");
+    return SJ_OK;
+  }
   hipLaunchKernelGGL(vec ? k_router_topk8 : k_router_topk, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
                      (hipStream_t)stream, (const bf16_t*)z, ldz, (const bf16_t*)w_router, d, rows, (int)experts,
                      (int)top_k, (bf16_t*)logits, ids, weights);
