@@ -117,7 +117,10 @@ def _hier_ops(mc, tc):
                         ("embedding_bwd", "byte", Ml * de * 4 + V * de * 4 + Ml * 4)):
         add(op, kind, w)
     add("rmsnorm", "byte", 2 * Ml * dg * es + dg * es)                            # final norm
-    add("rmsnorm_bwd", "byte", Ml * dg * (es + 4 + 4 + 4) + dg * es)
+    add("rmsnorm_bwd", "byte", Ml * dg * (es + 4 + 4 + 4 + (4 if planes else 0)) + dg * es)
+    if planes:  # the glue products' dY as hi/lo planes: one split pass each (fp32 in, two bf16 planes out)
+        for n in (Ml * dd, Mg * dd, Mg * dg):
+            add("glue_split", "byte", 8 * n)
     import sejong_amd.model as SM
     Pn = sum(math.prod(sh) for _, sh, _ in SM.layout(mc))
     mt = sum(L * (d * (d + 2 * (d // hq * hk)) + d * d + 3 * d * F) for L, d, hq, hk, F, _, _ in stages)

@@ -150,6 +150,9 @@ int attention_t_prepare();
 // whether attention_bwd_tt_parts runs the grouped launch for these sizes
 // (dK | dV planes written by part 2, part 4 does nothing)
 bool attention_bwd_grouped(long batch, long t, long hq, long hk, bool transposed);
+// fp32 -> hi/lo bf16 planes of n contiguous values (hi = RNE(x), lo =
+// RNE(x - hi)); n a multiple of 8, all three pointers 16-byte aligned
+int split_planes(hipStream_t s, const float* x, long n, uint16_t* hi, uint16_t* lo);
 // cross entropy with dX as hi/lo bf16 planes [rows][ldp] (columns past vocab zero)
 int cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss, uint16_t* dx_hi,
                          uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar);

@@ -38,6 +38,20 @@ __global__ __launch_bounds__(EW_THREADS) void k_copy16(const uint4* __restrict__
   for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n16; i += (long)gridDim.x * blockDim.x) y[i] = x[i];
 }
 
+// fp32 values as hi/lo bf16 planes, 8 per thread (32-byte loads, 16-byte stores)
+__global__ __launch_bounds__(EW_THREADS) void k_split_planes(const float* __restrict__ x, long n8,
+                                                             uint16_t* __restrict__ hi, uint16_t* __restrict__ lo) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n8; i += (long)gridDim.x * blockDim.x) {
+    const float4 a = ((const float4*)x)[2 * i], b = ((const float4*)x)[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    bf16_t h[8], l[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) split_bf(v[k], h[k], l[k]);
+    ((u32x4*)hi)[i] = u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
+    ((u32x4*)lo)[i] = u32x4{pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7])};
+  }
+}
+
 // kernels.py:16-21: y = x + alpha*z in fp32
 __global__ void k_add(const void* x, int xd, const void* z, int zd, void* y, int yd, long n, float alpha) {
   for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
@@ -363,6 +377,15 @@ __global__ void k_bias_reduce(const float* x, long ldx, float* y, long rows, lon
 }  // namespace
 
 // ---------------------------------------------------------------- C ABI
+
+int sjh::split_planes(hipStream_t s, const float* x, long n, uint16_t* hi, uint16_t* lo) {
+  SJ_REQUIRE(n >= 0 && n % 8 == 0 && (((uintptr_t)x | (uintptr_t)hi | (uintptr_t)lo) & 15) == 0,
+             "split planes: n %ld (multiple of 8, 16-byte aligned buffers)", n);
+  if (n == 0) return SJ_OK;
+  hipLaunchKernelGGL(k_split_planes, dim3(ew_blocks(n / 8)), dim3(EW_THREADS), 0, s, x, n / 8, hi, lo);
+  SJ_LAUNCH_CHECK("split planes");
+  return SJ_OK;
+}
 
 extern "C" int sj_fill(void* stream, void* y, int dtype, long n, float value) {
   SJ_REQUIRE(dtype_ok(dtype) && n >= 0, "fill: dtype %d / n %ld", dtype, n);

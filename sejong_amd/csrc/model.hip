@@ -337,6 +337,10 @@ struct sj_model {
   long h_inproj = 0, h_e2g = 0, h_e2d = 0, h_g2d = 0, h_bos = 0, h_op = 0;  // glue parameters
   void *pooled = nullptr, *gd = nullptr, *bosd = nullptr, *zb = nullptr, *bytes = nullptr, *opo = nullptr;
   float* hg[8] = {};                            // glue backward scratch
+  // bf16 models: hi/lo planes of the glue products' dY (the final norm's
+  // dX, d(decoder input), the broadcast's patch gradient, d(global input)),
+  // each read by that glue pair's dX and row-layout dW products
+  uint16_t* glue_p[4][2] = {};
   // mixture of experts (every block; F is the expert width): routing, the
   // packed expert rows and, per layer, the backward planes the dW stream reads
   long E = 0, K = 0, cap = 0;
@@ -1267,35 +1271,83 @@ int hierarchy_backward(sj_model* m, int& cur) {
     SJ_HIP(hipStreamWaitEvent(s2, m->ev_glue[k], 0));
     return SJ_OK;
   };
-  OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->dz, nullptr, hg[0], G + m->final_norm,
-                                   Ml, dg, eps, ws, wsb));
+  // bf16: each glue pair's dY as hi/lo planes (the final norm writes its
+  // own; the other three take one split pass), read by the pair's dX
+  // product (the weight's bf16 mirror is already the [N][K] operand) and
+  // its row-layout dW product, as the stages' own products are
+  const bool pl = dt == SJ_BF16 && m->glue_p[0][0];
+  auto& gp = m->glue_p;
+  const uint16_t* W16 = (const uint16_t*)m->mirror;
+  if (pl) {
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd_p(s, (const uint16_t*)m->opo, W16 + m->final_norm, m->dz, nullptr, hg[0],
+                                       G + m->final_norm, gp[0][0], gp[0][1], nullptr, nullptr, 0, Ml, dg, eps, ws,
+                                       wsb));
+  } else {
+    OP("rmsnorm_bwd", sj_rmsnorm_bwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->dz, nullptr, hg[0],
+                                     G + m->final_norm, Ml, dg, eps, ws, wsb));
+  }
   TRY(to_s2(0));
-  OP("output_projection_dw", sj_gemm(s2, 1, 0, dd, dg, Ml, D.out, dt, dd, hg[0], SJ_F32, dg, G + m->h_op, SJ_F32, dg,
-                                     0, ws2, wsb));
-  OP("output_projection_dx", sj_gemm(s, 0, 1, Ml, dd, dg, hg[0], SJ_F32, dg, wc(m, m->h_op), dt, dg, hg[1], SJ_F32, dd,
-                                     0, ws, wsb));
+  if (pl) {
+    OP("output_projection_dw", sj_gemm_planes_tn(s2, dd, dg, Ml, (const uint16_t*)D.out, nullptr, dd, gp[0][0],
+                                                 gp[0][1], dg, G + m->h_op, SJ_F32, dg, 0, ws2, wsb));
+    OP("output_projection_dx", sj_gemm_planes(s, Ml, dd, dg, gp[0][0], gp[0][1], dg, W16 + m->h_op, nullptr, dg,
+                                              hg[1], SJ_F32, dd, 0, ws, wsb));
+  } else {
+    OP("output_projection_dw", sj_gemm(s2, 1, 0, dd, dg, Ml, D.out, dt, dd, hg[0], SJ_F32, dg, G + m->h_op, SJ_F32,
+                                       dg, 0, ws2, wsb));
+    OP("output_projection_dx", sj_gemm(s, 0, 1, Ml, dd, dg, hg[0], SJ_F32, dg, wc(m, m->h_op), dt, dg, hg[1], SJ_F32,
+                                       dd, 0, ws, wsb));
+  }
   TRY(stage_backward(m, 2, hg[1], cur));
   const float* dxd = m->dres[cur];  // d(decoder input) = d(bytes) = d(broadcast output)
-  OP("encoder_to_decoder_dx", sj_gemm(s, 0, 1, Ml, de, dd, dxd, SJ_F32, dd, wc(m, m->h_e2d), dt, dd, hg[2], SJ_F32, de,
-                                      0, ws, wsb));
+  if (pl) {
+    OP("glue_split", sjh::split_planes(s, dxd, Ml * dd, gp[1][0], gp[1][1]));
+    OP("encoder_to_decoder_dx", sj_gemm_planes(s, Ml, de, dd, gp[1][0], gp[1][1], dd, W16 + m->h_e2d, nullptr, dd,
+                                               hg[2], SJ_F32, de, 0, ws, wsb));
+  } else {
+    OP("encoder_to_decoder_dx", sj_gemm(s, 0, 1, Ml, de, dd, dxd, SJ_F32, dd, wc(m, m->h_e2d), dt, dd, hg[2], SJ_F32,
+                                        de, 0, ws, wsb));
+  }
   OP("patch_broadcast_bwd", sj_patch_broadcast_bwd(s, dxd, B, E.T, dd, P, hg[3], hg[4]));
-  OP("encoder_to_decoder_dw", sj_gemm(s, 1, 0, de, dd, Ml, E.out, dt, de, dxd, SJ_F32, dd, G + m->h_e2d, SJ_F32, dd, 0,
-                                      ws, wsb));
+  if (pl) {
+    OP("encoder_to_decoder_dw", sj_gemm_planes_tn(s, de, dd, Ml, (const uint16_t*)E.out, nullptr, de, gp[1][0],
+                                                  gp[1][1], dd, G + m->h_e2d, SJ_F32, dd, 0, ws, wsb));
+    OP("glue_split", sjh::split_planes(s, hg[3], Mg * dd, gp[2][0], gp[2][1]));
+  } else {
+    OP("encoder_to_decoder_dw", sj_gemm(s, 1, 0, de, dd, Ml, E.out, dt, de, dxd, SJ_F32, dd, G + m->h_e2d, SJ_F32, dd,
+                                        0, ws, wsb));
+  }
   TRY(to_s2(1));
-  OP("global_to_decoder_dw", sj_gemm(s2, 1, 0, dg, dd, Mg, Gs.out, dt, dg, hg[3], SJ_F32, dd, G + m->h_g2d, SJ_F32, dd,
-                                     0, ws2, wsb));
+  if (pl)
+    OP("global_to_decoder_dw", sj_gemm_planes_tn(s2, dg, dd, Mg, (const uint16_t*)Gs.out, nullptr, dg, gp[2][0],
+                                                 gp[2][1], dd, G + m->h_g2d, SJ_F32, dd, 0, ws2, wsb));
+  else
+    OP("global_to_decoder_dw", sj_gemm(s2, 1, 0, dg, dd, Mg, Gs.out, dt, dg, hg[3], SJ_F32, dd, G + m->h_g2d, SJ_F32,
+                                       dd, 0, ws2, wsb));
   OP("bos_to_decoder_dw", sj_gemm(s2, 1, 0, dg, dd, 1, wc(m, m->h_bos), dt, dg, hg[4], SJ_F32, dd, G + m->h_g2d, SJ_F32,
                                   dd, 1, ws2, wsb));
   OP("bos_to_decoder_dx", sj_gemm(s2, 0, 1, 1, dg, dd, hg[4], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, G + m->h_bos, SJ_F32,
                                   dg, 0, ws2, wsb));
-  OP("global_to_decoder_dx", sj_gemm(s, 0, 1, Mg, dg, dd, hg[3], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, hg[5], SJ_F32, dg,
-                                     0, ws, wsb));
+  if (pl)
+    OP("global_to_decoder_dx", sj_gemm_planes(s, Mg, dg, dd, gp[2][0], gp[2][1], dd, W16 + m->h_g2d, nullptr, dd,
+                                              hg[5], SJ_F32, dg, 0, ws, wsb));
+  else
+    OP("global_to_decoder_dx", sj_gemm(s, 0, 1, Mg, dg, dd, hg[3], SJ_F32, dd, wc(m, m->h_g2d), dt, dd, hg[5], SJ_F32,
+                                       dg, 0, ws, wsb));
   TRY(stage_backward(m, 1, hg[5], cur));
   const float* dxg = m->dres[cur];  // d(global input)
-  OP("encoder_to_global_dx", sj_gemm(s, 0, 1, Mg, de, dg, dxg, SJ_F32, dg, wc(m, m->h_e2g), dt, dg, hg[6], SJ_F32, de,
-                                     0, ws, wsb));
-  OP("encoder_to_global_dw", sj_gemm(s, 1, 0, de, dg, Mg, m->pooled, dt, de, dxg, SJ_F32, dg, G + m->h_e2g, SJ_F32, dg,
-                                     0, ws, wsb));
+  if (pl) {
+    OP("glue_split", sjh::split_planes(s, dxg, Mg * dg, gp[3][0], gp[3][1]));
+    OP("encoder_to_global_dx", sj_gemm_planes(s, Mg, de, dg, gp[3][0], gp[3][1], dg, W16 + m->h_e2g, nullptr, dg,
+                                              hg[6], SJ_F32, de, 0, ws, wsb));
+    OP("encoder_to_global_dw", sj_gemm_planes_tn(s, de, dg, Mg, (const uint16_t*)m->pooled, nullptr, de, gp[3][0],
+                                                 gp[3][1], dg, G + m->h_e2g, SJ_F32, dg, 0, ws, wsb));
+  } else {
+    OP("encoder_to_global_dx", sj_gemm(s, 0, 1, Mg, de, dg, dxg, SJ_F32, dg, wc(m, m->h_e2g), dt, dg, hg[6], SJ_F32,
+                                       de, 0, ws, wsb));
+    OP("encoder_to_global_dw", sj_gemm(s, 1, 0, de, dg, Mg, m->pooled, dt, de, dxg, SJ_F32, dg, G + m->h_e2g, SJ_F32,
+                                       dg, 0, ws, wsb));
+  }
   OP("patch_pool_bwd", sj_patch_pool_bwd(s, hg[6], B, E.T, de, P, hg[7]));
   OP("encoded_grad_sum", sj_add(s, hg[2], SJ_F32, hg[7], SJ_F32, hg[7], SJ_F32, Ml * de, 1.f));
   return stage_backward(m, 0, hg[7], cur);
@@ -2056,6 +2108,11 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     const size_t hsz[8] = {(size_t)(E.M * Gs.d), (size_t)(E.M * D.d), (size_t)(E.M * E.d), (size_t)(Gs.M * D.d),
                            (size_t)D.d, (size_t)(Gs.M * Gs.d), (size_t)(Gs.M * E.d), (size_t)(E.M * E.d)};
     for (int i = 0; i < 8; i++) ALLOC(m->hg[i], hsz[i] * 4);
+    if (m->dt == SJ_BF16) {
+      const size_t psz[4] = {(size_t)(E.M * Gs.d), (size_t)(E.M * D.d), (size_t)(Gs.M * D.d), (size_t)(Gs.M * Gs.d)};
+      for (int i = 0; i < 4; i++)
+        for (int h = 0; h < 2; h++) ALLOC(m->glue_p[i][h], psz[i] * 2);
+    }
   } else {
     m->stages[0].out = m->hn;
   }
@@ -2145,6 +2202,12 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
                               {Ml, dd, dg}, {dd, dg, Ml}, {Ml, de, dd}, {de, dd, Ml}, {dg, dd, Mg},
                               {dg, dd, 1},  {1, dg, dd},  {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}};
     for (const auto& sh : shapes) upd(sj_gemm_workspace_bytes(sh[0], sh[1], sh[2]));
+    if (m->dt == SJ_BF16) {  // the glue products on planes and the final norm's planes
+      const long pshapes[][3] = {{dd, dg, Ml}, {Ml, dd, dg}, {Ml, de, dd}, {de, dd, Ml},
+                                 {dg, dd, Mg}, {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}};
+      for (const auto& sh : pshapes) upd(sj_gemm_planes_workspace_bytes(sh[0], sh[1], sh[2]));
+      upd(sj_rmsnorm_bwd_p_workspace_bytes(Ml, dg));
+    }
   }
   if (m->vjp) {
     const long rows = m->vjp_R + m->vjp_k;
