@@ -410,6 +410,7 @@ struct sj_model {
   };
   std::vector<TGroup> tgroups;
   std::vector<hipEvent_t> ev_tr;   // group g's transposes done (second stream)
+  size_t tr_glue = (size_t)-1;     // the hierarchical glue matrices' transpose group (bf16)
   hipEvent_t ev_tr_fork = nullptr;
   bool mt_stale = false;           // the transposed mirror lags the last update
   bool tr_overlap = false;         // this forward refreshes it on the second stream
@@ -871,13 +872,32 @@ int hierarchy_forward(sj_model* m) {
   }
   OP("bos_to_decoder", sj_gemm(s2, 0, 0, 1, dd, dg, wc(m, m->h_bos), dt, dg, wc(m, m->h_g2d), dt, dd, m->bosd, dt, dd, 0,
                                ws2, wsb));
-  OP("encoder_to_decoder", sj_gemm(s2, 0, 0, Ml, dd, de, E.out, dt, de, wc(m, m->h_e2d), dt, dd, m->bytes, dt, dd, 0,
-                                   ws2, wsb));
+  // bf16: the glue products on the MFMA layout, each weight's transposed
+  // mirror the [N][K] operand (the second stream runs any transposes first)
+  const bool pl = dt == SJ_BF16 && m->mirror_t && m->tr_glue != (size_t)-1;
+  const uint16_t* WT = m->mirror_t;
+  if (pl)
+    OP("encoder_to_decoder", sj_gemm_planes(s2, Ml, dd, de, (const uint16_t*)E.out, nullptr, de, WT + m->h_e2d, nullptr,
+                                            de, m->bytes, SJ_BF16, dd, 0, ws2, wsb));
+  else
+    OP("encoder_to_decoder", sj_gemm(s2, 0, 0, Ml, dd, de, E.out, dt, de, wc(m, m->h_e2d), dt, dd, m->bytes, dt, dd, 0,
+                                     ws2, wsb));
   OP("patch_pool", sj_patch_pool(s, E.out, dt, B, E.T, de, P, m->pooled));
-  OP("encoder_to_global", sj_gemm(s, 0, 0, Mg, dg, de, m->pooled, dt, de, wc(m, m->h_e2g), dt, dg, xin(m, G.first), dt,
-                                  dg, 0, ws, wsb));
+  if (pl) {
+    TRY(await_transposed(m, s, m->tr_glue));
+    OP("encoder_to_global", sj_gemm_planes(s, Mg, dg, de, (const uint16_t*)m->pooled, nullptr, de, WT + m->h_e2g,
+                                           nullptr, de, xin(m, G.first), SJ_BF16, dg, 0, ws, wsb));
+  } else {
+    OP("encoder_to_global", sj_gemm(s, 0, 0, Mg, dg, de, m->pooled, dt, de, wc(m, m->h_e2g), dt, dg, xin(m, G.first),
+                                    dt, dg, 0, ws, wsb));
+  }
   TRY(stage_forward(m, 1));
-  OP("global_to_decoder", sj_gemm(s, 0, 0, Mg, dd, dg, G.out, dt, dg, wc(m, m->h_g2d), dt, dd, m->gd, dt, dd, 0, ws, wsb));
+  if (pl)
+    OP("global_to_decoder", sj_gemm_planes(s, Mg, dd, dg, (const uint16_t*)G.out, nullptr, dg, WT + m->h_g2d, nullptr,
+                                           dg, m->gd, SJ_BF16, dd, 0, ws, wsb));
+  else
+    OP("global_to_decoder", sj_gemm(s, 0, 0, Mg, dd, dg, G.out, dt, dg, wc(m, m->h_g2d), dt, dd, m->gd, dt, dd, 0, ws,
+                                    wsb));
   if (two) {
     SJ_HIP(hipEventRecord(m->ev_glue[3], s2));
     SJ_HIP(hipStreamWaitEvent(s, m->ev_glue[3], 0));
@@ -885,7 +905,12 @@ int hierarchy_forward(sj_model* m) {
   OP("patch_broadcast", sj_patch_broadcast(s, m->gd, m->bosd, dt, B, E.T, dd, P, m->zb));
   OP("decoder_input", sj_add(s, m->bytes, dt, m->zb, dt, xin(m, D.first), dt, Ml * dd, 1.f));
   TRY(stage_forward(m, 2));
-  OP("output_projection", sj_gemm(s, 0, 0, Ml, dg, dd, D.out, dt, dd, wc(m, m->h_op), dt, dg, m->opo, dt, dg, 0, ws, wsb));
+  if (pl)
+    OP("output_projection", sj_gemm_planes(s, Ml, dg, dd, (const uint16_t*)D.out, nullptr, dd, WT + m->h_op, nullptr,
+                                           dd, m->opo, SJ_BF16, dg, 0, ws, wsb));
+  else
+    OP("output_projection", sj_gemm(s, 0, 0, Ml, dg, dd, D.out, dt, dd, wc(m, m->h_op), dt, dg, m->opo, dt, dg, 0, ws,
+                                    wsb));
   OP("rmsnorm", sj_rmsnorm_fwd(s, m->opo, dt, wc(m, m->final_norm), dt, m->hn, Ml, dg, eps));
   return SJ_OK;
 }
@@ -1931,6 +1956,17 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
       }
       group(j0, t0);  // group 1 + l: layer l
     }
+    if (m->hier) {  // group 1 + L: the glue projections' [N][K] operands of the forward
+      const long de = m->stages[0].d, dg = m->stages[1].d, dd = m->stages[2].d;
+      const int j0 = (int)jobs.size();
+      const long t0 = tiles;
+      job(m->h_e2g, de, dg);
+      job(m->h_e2d, de, dd);
+      job(m->h_g2d, dg, dd);
+      job(m->h_op, dd, dg);
+      m->tr_glue = m->tgroups.size();
+      group(j0, t0);
+    }
     m->tjob_n = (int)jobs.size();
     m->tjob_tiles = tiles;
     ALLOC(m->tjobs, sizeof(TJob) * jobs.size());
@@ -2203,8 +2239,9 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
                               {dg, dd, 1},  {1, dg, dd},  {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}};
     for (const auto& sh : shapes) upd(sj_gemm_workspace_bytes(sh[0], sh[1], sh[2]));
     if (m->dt == SJ_BF16) {  // the glue products on planes and the final norm's planes
-      const long pshapes[][3] = {{dd, dg, Ml}, {Ml, dd, dg}, {Ml, de, dd}, {de, dd, Ml},
-                                 {dg, dd, Mg}, {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}};
+      const long pshapes[][3] = {{dd, dg, Ml}, {Ml, dd, dg}, {Ml, de, dd}, {de, dd, Ml}, {dg, dd, Mg},
+                                 {Mg, dg, dd}, {Mg, de, dg}, {de, dg, Mg}, {Ml, dd, de}, {Mg, dg, de},
+                                 {Mg, dd, dg}, {Ml, dg, dd}};
       for (const auto& sh : pshapes) upd(sj_gemm_planes_workspace_bytes(sh[0], sh[1], sh[2]));
       upd(sj_rmsnorm_bwd_p_workspace_bytes(Ml, dg));
     }
