@@ -1844,7 +1844,21 @@ extern "C" int sj_down_bwd_swiglu_p(void* stream, const uint16_t* dy_hi, const u
 // capacity and workgroups past the last segment leave at once.
 
 namespace {
-int grouped_bn(long cap, long N) { return tiles(cap, N, 64, 128) >= cus() ? 128 : 64; }
+// Column tile of the grouped expert products (rows: 64, the segment
+// alignment).  `narrow`: the dual gate/up forward and the products with a
+// split A (gate/up dX, down dX + SwiGLU) take 64 (cfg4: 52.5 -> 47.4,
+// 67.1 -> 63.4, 57.5 -> 52.9 us against 128); the expert down forward keeps
+// 128 once it gives a tile per CU (25.4 against 31.7 us at 64).
+int grouped_bn(long cap, long N, bool narrow = false) {
+  static int ov = -1;
+  if (ov < 0) {
+    const char* e = getenv("SJ_MOE_BN");  // sweeps: 64 or 128
+    ov = e ? atoi(e) : 0;
+  }
+  if (ov == 64 || ov == 128) return ov;
+  if (narrow) return 64;
+  return tiles(cap, N, 64, 128) >= cus() ? 128 : 64;
+}
 bool grouped_ok(const int32_t* off, long experts, long cap) {
   return off && experts > 0 && experts <= 1024 && cap > 0 && cap % 64 == 0;
 }
@@ -1866,7 +1880,7 @@ extern "C" int sj_moe_gate_up_fwd(void* stream, const int32_t* offsets, long exp
   p.c[0] = g; p.c[1] = u; p.c[2] = h; p.c[3] = h_t; p.ldc[0] = ldo; p.ldc[3] = ldht;
   p.M = capacity; p.N = F; p.K = D; p.c_bf16 = 1;
   p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
-  int st = launch_planes<E_GATEUP>((hipStream_t)stream, p, 1, 1, 64, grouped_bn(capacity, F), 1);
+  int st = launch_planes<E_GATEUP>((hipStream_t)stream, p, 1, 1, 64, grouped_bn(capacity, F, true), 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("expert gate_up");
   return SJ_OK;
@@ -1909,7 +1923,7 @@ extern "C" int sj_moe_down_bwd_swiglu_p(void* stream, const int32_t* offsets, lo
   p.gin = (const bf16_t*)g; p.uin = (const bf16_t*)u; p.ldgu = ldgu; p.F = F;
   p.M = capacity; p.N = F; p.K = D;
   p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = w_stride;
-  const int bn = grouped_bn(capacity, F);
+  const int bn = grouped_bn(capacity, F, true);
   int st = swiglu_rows_ok(p) ? launch_planes<E_SWIGLU_ROWS>((hipStream_t)stream, p, 2, 1, 64, bn, 1)
                              : launch_planes<E_SWIGLU_BWD>((hipStream_t)stream, p, 2, 1, 64, bn, 1);
   if (st) return st;
@@ -1931,7 +1945,7 @@ extern "C" int sj_moe_gemm_rows(void* stream, const int32_t* offsets, long exper
   p.c[0] = c; p.ldc[0] = ldc; p.accumulate = accumulate;
   p.M = capacity; p.N = N; p.K = K;
   p.goff = offsets; p.gE = (int)experts; p.gmode = 1; p.gstride_b = b_stride;
-  int st = launch_planes<E_STORE>((hipStream_t)stream, p, a_lo ? 2 : 1, 1, 64, grouped_bn(capacity, N), 1);
+  int st = launch_planes<E_STORE>((hipStream_t)stream, p, a_lo ? 2 : 1, 1, 64, grouped_bn(capacity, N, a_lo != nullptr), 1);
   if (st) return st;
   SJ_LAUNCH_CHECK("expert matmul (rows)");
   return SJ_OK;
