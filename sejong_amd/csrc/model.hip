@@ -874,7 +874,7 @@ int hierarchy_forward(sj_model* m) {
                                ws2, wsb));
   // bf16: the glue products on the MFMA layout, each weight's transposed
   // mirror the [N][K] operand (the second stream runs any transposes first)
-  const bool pl = dt == SJ_BF16 && m->mirror_t && m->tr_glue != (size_t)-1;
+  const bool pl = dt == SJ_BF16 && m->mirror_t && m->tr_glue != (size_t)-1 && (de | dg | dd) % 8 == 0;
   const uint16_t* WT = m->mirror_t;
   if (pl)
     OP("encoder_to_decoder", sj_gemm_planes(s2, Ml, dd, de, (const uint16_t*)E.out, nullptr, de, WT + m->h_e2d, nullptr,
@@ -1300,7 +1300,7 @@ int hierarchy_backward(sj_model* m, int& cur) {
   // own; the other three take one split pass), read by the pair's dX
   // product (the weight's bf16 mirror is already the [N][K] operand) and
   // its row-layout dW product, as the stages' own products are
-  const bool pl = dt == SJ_BF16 && m->glue_p[0][0];
+  const bool pl = dt == SJ_BF16 && m->glue_p[0][0] && (de | dg | dd) % 8 == 0 && dg <= 1024;
   auto& gp = m->glue_p;
   const uint16_t* W16 = (const uint16_t*)m->mirror;
   if (pl) {
