@@ -79,7 +79,9 @@ int sj_event_elapsed(void *start, void *end, float *ms);
 /* Engine::full, crates/sejong-gpu/src/lib.rs:544-553 (kernel `fill`,
  * python/sejong_kernels/ops/kernels.py:6-9). */
 int sj_fill(void *stream, void *y, int dtype, long n, float value);
-/* Engine::cast / copy_into, lib.rs:554-571 (kernel `copy`, kernels.py:11-14). */
+/* Engine::cast / copy_into, lib.rs:554-571 (kernel `copy`, kernels.py:11-14).
+ * Same dtype: a bit copy (16-byte vectors when both pointers are aligned);
+ * fp32 -> bf16 rounds to nearest even. */
 int sj_cast(void *stream, const void *x, int x_dtype, void *y, int y_dtype, long n);
 /* Engine::add / add_into, lib.rs:572-593 (kernel `add`, kernels.py:16-21):
  * y = x + alpha*z computed in fp32, stored in y_dtype. */
