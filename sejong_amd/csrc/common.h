@@ -153,6 +153,10 @@ bool attention_bwd_grouped(long batch, long t, long hq, long hk, bool transposed
 // fp32 -> hi/lo bf16 planes of n contiguous values (hi = RNE(x), lo =
 // RNE(x - hi)); n a multiple of 8, all three pointers 16-byte aligned
 int split_planes(hipStream_t s, const float* x, long n, uint16_t* hi, uint16_t* lo);
+// sj_rmsnorm_fwd_t with the embedding lookup fused in: row r of the input is
+// row ids[r] of the bf16 table, also written to x0 [rows][d]
+int rmsnorm_fwd_t_embed(void* stream, const uint16_t* table, const int32_t* ids, uint16_t* x0, const uint16_t* w,
+                        uint16_t* y, uint16_t* y_t, long ldt, long rows, long d, float eps);
 // cross entropy with dX as hi/lo bf16 planes [rows][ldp] (columns past vocab zero)
 int cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss, uint16_t* dx_hi,
                          uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar);

@@ -799,7 +799,11 @@ int stage_forward(sj_model* m, int si) {
     const uint16_t *x = (const uint16_t*)xin(m, l), *x1 = (const uint16_t*)m->x1[l];
     uint16_t *z = (uint16_t*)m->z[l], *z2 = (uint16_t*)m->z2[l], *o = (uint16_t*)m->o[l];
     uint16_t *gg = (uint16_t*)m->gg[l], *uu = (uint16_t*)m->uu[l], *hh = (uint16_t*)m->hh[l];
-    OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->rowdw ? nullptr : m->zt[l], ldt, M, d, eps));
+    if (l == 0)  // the embedding lookup fused in (forward() leaves it to this norm)
+      OP("rmsnorm", sjh::rmsnorm_fwd_t_embed(s, W + m->emb, m->ids, (uint16_t*)m->x[0], W + y.an, z,
+                                             m->rowdw ? nullptr : m->zt[l], ldt, M, d, eps));
+    else
+      OP("rmsnorm", sj_rmsnorm_fwd_t(s, x, W + y.an, z, m->rowdw ? nullptr : m->zt[l], ldt, M, d, eps));
     OP("qkv_rope", sj_qkv_fwd_t(s, z, d, M, d, WT + y.qkv, d, d, J, qkv, NQ, S.rope, S.T, S.Dh, nullptr, ldt));
     if (S.attn_tt)
       OP("attention_fwd", sj_attention_fwd_tt(s, qkv, NQ, ldt, m->B, S.T, S.HQ, S.HK, S.Dh, S.window, o, d,
@@ -943,7 +947,9 @@ int forward(sj_model* m) {
     OP("mirror_transpose", transpose_mirror_overlapped(m));
   else if (m->mt_stale)
     OP("mirror_transpose", transpose_mirror(m));
-  OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, m->stages[0].M, m->stages[0].d));
+  // the MFMA-layout blocks fold the lookup into the first block's norm
+  if (!(m->planes && m->L > 0 && m->stages[0].count > 0))
+    OP("embedding", sj_embedding_fwd(s, wc(m, m->emb), dt, m->ids, m->x[0], dt, m->stages[0].M, m->stages[0].d));
   TRY(stage_forward(m, 0));
   if (m->hier) TRY(hierarchy_forward(m));
   if (m->value_n) {

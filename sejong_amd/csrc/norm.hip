@@ -234,11 +234,14 @@ __device__ __forceinline__ void store_col8(bf16_t* dst, const bf16_t* src, long 
   }
 }
 
-// y = rmsnorm(x) (bf16 x, w) -> y [rows][d] and y_t [d][ldt]
+// y = rmsnorm(x) (bf16 x, w) -> y [rows][d] and y_t [d][ldt].  With ids,
+// row r of x is row ids[r] of the table x (the embedding lookup), and xout
+// receives the looked-up rows (the residual stream's input).
 template <int NP>
 __global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x, const bf16_t* __restrict__ w,
                                                    bf16_t* __restrict__ y, bf16_t* __restrict__ yt, long rows,
-                                                   long d, long ldt, float eps) {
+                                                   long d, long ldt, float eps, const int32_t* __restrict__ ids,
+                                                   bf16_t* __restrict__ xout) {
   extern __shared__ __attribute__((aligned(16))) bf16_t stage[];  // [TR][d]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const long r0 = xcd_block(blockIdx.x, gridDim.x) * TR;
@@ -248,14 +251,22 @@ __global__ __launch_bounds__(NTT) void k_rms_fwd_t(const bf16_t* __restrict__ x,
   // latency follows the row reduction
   float2 xv[NP], wt[NP];
   float s = 0.f;
+  const long src = r < rows ? (ids ? (long)ids[r] : r) * d : 0;
 #pragma unroll
   for (int j = 0; j < NP; j++) {
     const long p = lane + 64L * j;
     xv[j] = wt[j] = make_float2(0.f, 0.f);
     if (p < pairs) wt[j] = ld2<SJ_BF16>(w, 2 * p);
     if (p < pairs && r < rows) {
-      xv[j] = ld2<SJ_BF16>(x, r * d + 2 * p);
+      xv[j] = ld2<SJ_BF16>(x, src + 2 * p);
       s += xv[j].x * xv[j].x + xv[j].y * xv[j].y;
+    }
+  }
+  if (xout && r < rows) {
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+      const long p = lane + 64L * j;
+      if (p < pairs) *(uint32_t*)(xout + r * d + 2 * p) = pack2(f2bf(xv[j].x), f2bf(xv[j].y));
     }
   }
   s = wave_sum(s);
@@ -459,9 +470,10 @@ int norm_prepare() {
 namespace {
 template <int NP>
 void launch_fwd_t(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x, const uint16_t* w, uint16_t* y,
-                  uint16_t* y_t, long rows, long d, long ldt, float eps) {
+                  uint16_t* y_t, long rows, long d, long ldt, float eps, const int32_t* ids = nullptr,
+                  uint16_t* xout = nullptr) {
   hipLaunchKernelGGL(k_rms_fwd_t<NP>, dim3(blocks), dim3(NTT), lds, s, (const bf16_t*)x, (const bf16_t*)w, (bf16_t*)y,
-                     (bf16_t*)y_t, rows, d, ldt, eps);
+                     (bf16_t*)y_t, rows, d, ldt, eps, ids, (bf16_t*)xout);
 }
 template <int NP>
 void launch_bwd_p(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x, const uint16_t* w, const float* dy,
@@ -472,8 +484,8 @@ void launch_bwd_p(hipStream_t s, unsigned blocks, size_t lds, const uint16_t* x,
 }
 }  // namespace
 
-extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t* w, uint16_t* y, uint16_t* y_t,
-                                long ldt, long rows, long d, float eps) {
+static int rmsnorm_fwd_t_any(void* stream, const uint16_t* x, const uint16_t* w, uint16_t* y, uint16_t* y_t, long ldt,
+                             long rows, long d, float eps, const int32_t* ids, uint16_t* xout) {
   SJ_REQUIRE(rows >= 0 && d > 0 && d % 8 == 0 && d <= 1024 && (!y_t || (ldt >= rows && ldt % 8 == 0)) &&
                  ((uintptr_t)y_t & 15) == 0,
              "RMSNorm (transposed output): rows %ld d %ld ldt %ld (d <= 1024)", rows, d, ldt);
@@ -483,17 +495,30 @@ extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t*
   const unsigned blocks = (unsigned)((rows + TR - 1) / TR);
   hipStream_t s = (hipStream_t)stream;
   switch ((d / 2 + 63) / 64) {
-    case 1: launch_fwd_t<1>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 2: launch_fwd_t<2>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 3: launch_fwd_t<3>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 4: launch_fwd_t<4>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 5: launch_fwd_t<5>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 6: launch_fwd_t<6>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    case 7: launch_fwd_t<7>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
-    default: launch_fwd_t<8>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps); break;
+    case 1: launch_fwd_t<1>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 2: launch_fwd_t<2>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 3: launch_fwd_t<3>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 4: launch_fwd_t<4>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 5: launch_fwd_t<5>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 6: launch_fwd_t<6>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    case 7: launch_fwd_t<7>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
+    default: launch_fwd_t<8>(s, blocks, lds, x, w, y, y_t, rows, d, ldt, eps, ids, xout); break;
   }
   SJ_LAUNCH_CHECK("rmsnorm_t");
   return SJ_OK;
+}
+
+extern "C" int sj_rmsnorm_fwd_t(void* stream, const uint16_t* x, const uint16_t* w, uint16_t* y, uint16_t* y_t,
+                                long ldt, long rows, long d, float eps) {
+  return rmsnorm_fwd_t_any(stream, x, w, y, y_t, ldt, rows, d, eps, nullptr, nullptr);
+}
+
+// the embedding lookup (Engine::embedding) fused into the first block's
+// norm: row r of the input is row ids[r] of the bf16 table, written to x0
+int sjh::rmsnorm_fwd_t_embed(void* stream, const uint16_t* table, const int32_t* ids, uint16_t* x0,
+                             const uint16_t* w, uint16_t* y, uint16_t* y_t, long ldt, long rows, long d, float eps) {
+  SJ_REQUIRE(table && ids && x0, "RMSNorm with the embedding lookup: table, ids and x0 required");
+  return rmsnorm_fwd_t_any(stream, table, w, y, y_t, ldt, rows, d, eps, ids, x0);
 }
 
 // sj_rmsnorm_bwd_p without its dw reduce: the partial sums [groups][d]
