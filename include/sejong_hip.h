@@ -881,7 +881,9 @@ int sj_model_export_activations(sj_model *m, float *host);
  * parameter-VJP models "vjp_columns", "vjp_rows", "vjp_map" (int32) and
  * "vjp_basis" (fp32 [tokens][rank]); for MoE models, per layer l,
  * "route_ids.<l>" (int32 [rows][top_k]), "route_weights.<l>" (fp32),
- * "route_counts.<l>" and "route_offsets.<l>" (int32)). */
+ * "route_counts.<l>", "route_offsets.<l>", "route_pslot.<l>" (the packed
+ * slot per position, -1 for padding) and "route_ppos.<l>" (each slot's
+ * packed position) (int32)). */
 int sj_model_buffer(sj_model *m, const char *what, void **ptr, long *elements);
 
 /* ----------------------------------------------------------- Checkpoints

@@ -157,6 +157,16 @@ int split_planes(hipStream_t s, const float* x, long n, uint16_t* hi, uint16_t* 
 // row ids[r] of the bf16 table, also written to x0 [rows][d]
 int rmsnorm_fwd_t_embed(void* stream, const uint16_t* table, const int32_t* ids, uint16_t* x0, const uint16_t* w,
                         uint16_t* y, uint16_t* y_t, long ldt, long rows, long d, float eps);
+// router top-k (16 lanes per token, 16 tokens per workgroup) that also
+// writes each workgroup's routed-slot count per expert into hist
+// [router_hist_blocks(rows)][E], and the pack that reads those counts
+// (the same counts, offsets, pslot and ppos as sj_route_pack); E == 8, K <= 4
+bool router_pack_ok(long d, long ldz, long E, long K, const void* z, const void* wr, const void* logits);
+long router_hist_blocks(long rows);
+int router_topk_hist(hipStream_t s, const uint16_t* z, long ldz, const uint16_t* wr, long d, long rows, long E, long K,
+                     uint16_t* logits, int32_t* ids, float* weights, int32_t* hist);
+int route_pack_hist(hipStream_t s, const int32_t* ids, long rows, long K, long E, const int32_t* hist, int32_t* counts,
+                    int32_t* offsets, int32_t* pslot, int32_t* ppos, long cap);
 // cross entropy with dX as hi/lo bf16 planes [rows][ldp] (columns past vocab zero)
 int cross_entropy_planes(void* stream, const float* x, long ldx, const int32_t* targets, float* loss, uint16_t* dx_hi,
                          uint16_t* dx_lo, long ldp, long rows, long vocab, float dy_scalar);

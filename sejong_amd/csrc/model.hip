@@ -341,6 +341,7 @@ struct sj_model {
   // dX, d(decoder input), the broadcast's patch gradient, d(global input)),
   // each read by that glue pair's dX and row-layout dW products
   uint16_t* glue_p[4][2] = {};
+  int32_t* mhist = nullptr;  // mixture of experts: the router top-k's per-workgroup counts (E == 8)
   // mixture of experts (every block; F is the expert width): routing, the
   // packed expert rows and, per layer, the backward planes the dW stream reads
   long E = 0, K = 0, cap = 0;
@@ -815,9 +816,18 @@ int stage_forward(sj_model* m, int si) {
     OP("rmsnorm", sj_rmsnorm_fwd_t(s, x1, W + y.fn, z2, m->rowdw ? nullptr : m->z2t[l], ldt, M, d, eps));
     if (m->E) {  // Block::apply's MoE branch (architecture.rs:229-242), packed by expert on the device
       const long E = m->E, K = m->K, cap = m->cap;
-      OP("router_topk", sj_router_topk(s, z2, d, W + y.router, d, M, E, K, m->mlog[l], m->mids[l], m->mwts[l]));
-      OP("route_pack", sj_route_pack(s, m->mids[l], M, K, E, nullptr, nullptr, m->mcnt[l], m->moff[l], m->mps[l],
-                                     m->mpp[l], cap));
+      if (m->mhist && sjh::router_pack_ok(d, d, E, K, z2, W + y.router, m->mlog[l])) {
+        // the top-k also counts each workgroup's routed slots; the pack
+        // places them from those counts in parallel
+        OP("router_topk", sjh::router_topk_hist(s, z2, d, W + y.router, d, M, E, K, (uint16_t*)m->mlog[l],
+                                                m->mids[l], m->mwts[l], m->mhist));
+        OP("route_pack", sjh::route_pack_hist(s, m->mids[l], M, K, E, m->mhist, m->mcnt[l], m->moff[l], m->mps[l],
+                                              m->mpp[l], cap));
+      } else {
+        OP("router_topk", sj_router_topk(s, z2, d, W + y.router, d, M, E, K, m->mlog[l], m->mids[l], m->mwts[l]));
+        OP("route_pack", sj_route_pack(s, m->mids[l], M, K, E, nullptr, nullptr, m->mcnt[l], m->moff[l], m->mps[l],
+                                       m->mpp[l], cap));
+      }
       OP("moe_gather", sj_moe_gather(s, z2, d, d, m->mps[l], K, cap, m->mzp[l], m->rowdw ? nullptr : m->mzpt[l], cap));
       OP("expert_gate_up", sj_moe_gate_up_fwd(s, m->moff[l], E, cap, m->mzp[l], d, d, WT + y.gu, WT + y.gu + F * d, d,
                                               2 * F * d, F, gg, uu, hh, F, m->rowdw ? nullptr : m->ht[l], cap));
@@ -2045,6 +2055,7 @@ int create_model(const sj_model_config* cfg, const sj_hierarchy_config* hc, cons
     for (auto* v : {&m->mids, &m->mcnt, &m->moff, &m->mps, &m->mpp}) v->assign(m->L, nullptr);
     for (auto* v : {&m->mwts, &m->mdwts, &m->mdlog}) v->assign(m->L, nullptr);
     for (int i = 0; i < 4; i++) { m->mdx[i].assign(m->L, nullptr); m->mdg[i].assign(m->L, nullptr); }
+    if (E == 8) ALLOC(m->mhist, (size_t)sjh::router_hist_blocks((long)M) * E * 4);
     for (long l = 0; l < m->L; l++) {
       ALLOC(m->mlog[l], M * E * 2);
       ALLOC(m->mids[l], S * 4);
@@ -2823,6 +2834,8 @@ extern "C" int sj_model_buffer(sj_model* m, const char* what, void** ptr, long* 
     else if (kind == "route_weights") { *ptr = m->mwts[l]; n = m->M * m->K; }
     else if (kind == "route_counts") { *ptr = m->mcnt[l]; n = m->E; }
     else if (kind == "route_offsets") { *ptr = m->moff[l]; n = m->E + 1; }
+    else if (kind == "route_pslot") { *ptr = m->mps[l]; n = m->cap; }
+    else if (kind == "route_ppos") { *ptr = m->mpp[l]; n = m->M * m->K; }
     else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);
   }
   else return sjh::fail(SJ_ERR_INVALID, "buffer: unknown name %s", what);

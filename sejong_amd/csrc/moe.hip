@@ -119,7 +119,7 @@ template <int EW, int LPT>
 __global__ __launch_bounds__(NT) void k_router_topk_lanes(const bf16_t* __restrict__ z, long ldz,
                                                           const bf16_t* __restrict__ wr, long d, long R, int E, int K,
                                                           bf16_t* __restrict__ logits, int32_t* __restrict__ ids,
-                                                          float* __restrict__ weights) {
+                                                          float* __restrict__ weights, int32_t* __restrict__ hist) {
   constexpr int EE = 8 * EW;
   const int j = threadIdx.x % LPT;
   const long r = (blockIdx.x * (long)NT + threadIdx.x) / LPT;
@@ -156,7 +156,14 @@ __global__ __launch_bounds__(NT) void k_router_topk_lanes(const bf16_t* __restri
   for (int o = 1; o < LPT; o <<= 1)
 #pragma unroll
     for (int e = 0; e < EE; e++) acc[e] += __shfl_xor(acc[e], o, WAVE);
-  if (!live || j != 0) return;
+  // hist (uniform): this workgroup's routed-slot count per expert, for the
+  // pack that follows (integer adds, so their order does not matter)
+  __shared__ int hcnt[EMAX];
+  if (hist) {
+    if (threadIdx.x < EMAX) hcnt[threadIdx.x] = 0;
+    __syncthreads();
+  }
+  if (live && j == 0) {
   float sc[EMAX];
 #pragma unroll
   for (int e = 0; e < EMAX; e++) sc[e] = e < EE && e < E ? round_bf(acc[e < EE ? e : 0]) : 0.f;
@@ -173,7 +180,82 @@ __global__ __launch_bounds__(NT) void k_router_topk_lanes(const bf16_t* __restri
     if (k < K) {
       ids[r * K + k] = id[k];
       weights[r * K + k] = w[k];
+      if (hist) atomicAdd(&hcnt[id[k]], 1);
     }
+  }
+  if (hist) {
+    __syncthreads();
+    if (threadIdx.x < E) hist[blockIdx.x * (long)E + threadIdx.x] = hcnt[threadIdx.x];
+  }
+}
+
+// The pack (k_route_pack_wide's result) from the top-k workgroups' counts:
+// workgroup b places the K-slots of top-k workgroup b's tokens (slots
+// b * per .. b * per + per - 1, per <= 64, one per lane).  Its base in
+// expert e's segment is the count of e in workgroups 0 .. b - 1, and the
+// rank among its own slots of expert e is that of the lanes below with the
+// same expert (a ballot per expert): every segment lists its slots in slot
+// order, as the single-workgroup scan does.  Workgroup 0 also writes the
+// counts and offsets and marks the segments' padding and the tail empty.
+__global__ __launch_bounds__(64) void k_route_pack_hist(const int32_t* __restrict__ ids, long S, int E, long cap,
+                                                        const int32_t* __restrict__ hist, int nblk, int per,
+                                                        int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ pslot, int32_t* __restrict__ ppos) {
+  constexpr int EP = 8;  // experts covered (E <= 8)
+  const int lane = threadIdx.x, b = blockIdx.x;
+  int tot[EP], base[EP];
+#pragma unroll
+  for (int e = 0; e < EP; e++) tot[e] = base[e] = 0;
+  for (int r = lane; r < nblk; r += 64)
+#pragma unroll
+    for (int e = 0; e < EP; e++)
+      if (e < E) {
+        const int v = hist[(long)r * E + e];
+        tot[e] += v;
+        if (r < b) base[e] += v;
+      }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int e = 0; e < EP; e++) {
+      tot[e] += __shfl_xor(tot[e], o, WAVE);
+      base[e] += __shfl_xor(base[e], o, WAVE);
+    }
+  int off[EP + 1];
+  int o = 0;
+#pragma unroll
+  for (int e = 0; e < EP; e++) {
+    off[e] = o;
+    if (e < E) o += (tot[e] + SEG - 1) / SEG * SEG;
+  }
+  off[EP] = o;  // == off[E]
+  const long s = (long)b * per + lane;
+  const bool has = lane < per && s < S;
+  const int ex = has ? ids[s] : -1;
+  int pos = 0;
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int e = 0; e < EP; e++) {
+    if (e >= E) break;
+    const uint64_t m = __ballot(ex == e);
+    if (ex == e) pos = off[e] + base[e] + __popcll(m & below);
+  }
+  if (has) {
+    pslot[pos] = (int32_t)s;
+    ppos[s] = pos;
+  }
+  if (b != 0) return;
+#pragma unroll
+  for (int e = 0; e < EP; e++) {
+    if (e >= E) break;
+    if (lane == 0) {
+      offsets[e] = off[e];
+      if (counts) counts[e] = tot[e];
+    }
+    for (long i = off[e] + tot[e] + lane; i < off[e + 1 < EP ? e + 1 : EP]; i += 64) pslot[i] = -1;
+  }
+  if (lane == 0) offsets[E] = off[EP];
+  for (long i = off[EP] + lane; i < cap; i += 64) pslot[i] = -1;
 }
 
 // The same with 16-byte loads (d % 8 == 0, E % 8 == 0, aligned rows): lane
@@ -893,6 +975,35 @@ extern "C" long sj_route_pack_capacity(long slots, long experts) {
   return pack_capacity(slots, experts);
 }
 
+bool sjh::router_pack_ok(long d, long ldz, long E, long K, const void* z, const void* wr, const void* logits) {
+  return E == 8 && K > 0 && K <= 4 && d % 128 == 0 && ldz >= d && ldz % 8 == 0 &&
+         (((uintptr_t)z | (uintptr_t)wr | (uintptr_t)logits) & 15) == 0;
+}
+
+long sjh::router_hist_blocks(long rows) { return (rows * 16 + NT - 1) / NT; }
+
+int sjh::router_topk_hist(hipStream_t s, const uint16_t* z, long ldz, const uint16_t* wr, long d, long rows, long E,
+                          long K, uint16_t* logits, int32_t* ids, float* weights, int32_t* hist) {
+  SJ_REQUIRE(router_pack_ok(d, ldz, E, K, z, wr, logits) && rows > 0 && hist, "router top-k with counts: shapes");
+  hipLaunchKernelGGL((k_router_topk_lanes<1, 16>), dim3((unsigned)router_hist_blocks(rows)), dim3(NT), 0, s,
+                     (const bf16_t*)z, ldz, (const bf16_t*)wr, d, rows, (int)E, (int)K, (bf16_t*)logits, ids, weights,
+                     hist);
+  SJ_LAUNCH_CHECK("router_topk");
+  return SJ_OK;
+}
+
+int sjh::route_pack_hist(hipStream_t s, const int32_t* ids, long rows, long K, long E, const int32_t* hist,
+                         int32_t* counts, int32_t* offsets, int32_t* pslot, int32_t* ppos, long cap) {
+  SJ_REQUIRE(E == 8 && K > 0 && K <= 4 && rows > 0 && hist && offsets && pslot && ppos &&
+                 cap >= pack_capacity(rows * K, E),
+             "route pack from counts: shapes (capacity %ld)", cap);
+  const long nblk = router_hist_blocks(rows);
+  hipLaunchKernelGGL(k_route_pack_hist, dim3((unsigned)nblk), dim3(64), 0, s, ids, rows * K, (int)E, cap, hist,
+                     (int)nblk, (int)(NT / 16 * K), counts, offsets, pslot, ppos);
+  SJ_LAUNCH_CHECK("hierarchy_route_pack");
+  return SJ_OK;
+}
+
 extern "C" int sj_router_topk(void* stream, const uint16_t* z, long ldz, const uint16_t* w_router, long d, long rows,
                               long experts, long top_k, uint16_t* logits, int32_t* ids, float* weights) {
   SJ_REQUIRE(rows >= 0 && d > 0 && ldz >= d && experts > 0 && experts <= EMAX && top_k > 0 && top_k <= KMAX &&
@@ -914,7 +1025,8 @@ extern "C" int sj_router_topk(void* stream, const uint16_t* z, long ldz, const u
                          : (experts <= 8 ? k_router_topk_lanes<1, 16> : experts <= 16 ? k_router_topk_lanes<2, 16>
                                                                                       : k_router_topk_lanes<4, 16>);
     hipLaunchKernelGGL(kern, grid, dim3(NT), 0, (hipStream_t)stream, (const bf16_t*)z, ldz,
-                       (const bf16_t*)w_router, d, rows, (int)experts, (int)top_k, (bf16_t*)logits, ids, weights);
+                       (const bf16_t*)w_router, d, rows, (int)experts, (int)top_k, (bf16_t*)logits, ids, weights,
+                       (int32_t*)nullptr);
     SJ_LAUNCH_CHECK("router_topk");
     return SJ_OK;
   }

@@ -58,6 +58,30 @@ def _download(ptr, n, dtype):
     return out
 
 
+def _check_pack(model, l, M, K, E):
+    """The step's pack of layer l (for 8 experts, placed from the top-k
+    workgroups' counts) against sj_route_pack on the same routing ids: the
+    offsets, the packed slot per position and each slot's position, bit for
+    bit."""
+    from sejong_amd import _native as N
+    ids_ptr, n_ids = model.buffer(f"route_ids.{l}")
+    ps_ptr, cap = model.buffer(f"route_pslot.{l}")
+    pp_ptr, _ = model.buffer(f"route_ppos.{l}")
+    off_ptr, _ = model.buffer(f"route_offsets.{l}")
+    bufs = [ctypes.c_void_p() for _ in range(4)]
+    for b, nb in zip(bufs, (E * 4, (E + 1) * 4, cap * 4, n_ids * 4)):
+        N.api.sj_alloc(nb, ctypes.byref(b))
+    try:
+        N.api.sj_route_pack(None, ctypes.c_void_p(ids_ptr), M, K, E, None, None, bufs[0], bufs[1], bufs[2], bufs[3],
+                            cap)
+        N.api.sj_synchronize(None)
+        for got, ref, nel in ((off_ptr, bufs[1], E + 1), (ps_ptr, bufs[2], cap), (pp_ptr, bufs[3], n_ids)):
+            np.testing.assert_array_equal(_download(got, nel, np.int32), _download(ref.value, nel, np.int32))
+    finally:
+        for b in bufs:
+            N.api.sj_free(b)
+
+
 def test_moe_model_layout_matches_oracle():
     from sejong_amd.model import Model
     mc, tc = _configs()
@@ -93,6 +117,7 @@ def test_moe_model_step_against_oracle():
         assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)
         # routing of every layer: bit-exact against the rule on the stored logits
         for l, (rid, rw, counts, _, _) in enumerate(routing):
+            _check_pack(model, l, M, K, E)
             d_ids = _download(model.buffer(f"route_ids.{l}")[0], M * K, np.int32).reshape(M, K)
             d_w = _download(model.buffer(f"route_weights.{l}")[0], M * K, np.float32).reshape(M, K)
             d_cnt = _download(model.buffer(f"route_counts.{l}")[0], E, np.int32)
@@ -174,6 +199,7 @@ def test_cfg4_full_configuration_against_oracle():
         lref, gref, routing = OM.model_backward(cfg, p64, dev, ids, tg, "bf16")
         assert abs(loss - lref) <= 1e-6 * abs(lref), (loss, lref)
         for l, (rid, rw, counts, _, _) in enumerate(routing):
+            _check_pack(model, l, M, K, E)
             d_ids = _download(model.buffer(f"route_ids.{l}")[0], M * K, np.int32).reshape(M, K)
             d_w = _download(model.buffer(f"route_weights.{l}")[0], M * K, np.float32).reshape(M, K)
             d_cnt = _download(model.buffer(f"route_counts.{l}")[0], E, np.int32)
