@@ -336,31 +336,32 @@ __global__ __launch_bounds__(NT) void k_route_topk(const void* __restrict__ x, i
 }
 
 // Engine::route_topk_backward (hierarchy.py:194-209): dx = p (dy_sel - sum_k w_k dy_k)
+template <int EM = EMAX>  // EM: the arrays' bound (E <= EM)
 __device__ __forceinline__ void route_bwd_row(const float* lg, int E, int K, const int32_t* id, const float* w,
                                               const float* dy, float* dx) {
   float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < EMAX; e++)
+  for (int e = 0; e < EM; e++)
     if (e < E) mx = fmaxf(mx, lg[e]);
-  float den = 0.f, ex[EMAX];
+  float den = 0.f, ex[EM];
 #pragma unroll
-  for (int e = 0; e < EMAX; e++) {
+  for (int e = 0; e < EM; e++) {
     ex[e] = e < E ? expf(lg[e] - mx) : 0.f;
     den += ex[e];
   }
-  float total = 0.f, sel[EMAX];
+  float total = 0.f, sel[EM];
 #pragma unroll
-  for (int e = 0; e < EMAX; e++) sel[e] = 0.f;
+  for (int e = 0; e < EM; e++) sel[e] = 0.f;
 #pragma unroll
   for (int k = 0; k < KMAX; k++) {
     if (k >= K) break;
     total += w[k] * dy[k];
 #pragma unroll
-    for (int e = 0; e < EMAX; e++)
+    for (int e = 0; e < EM; e++)
       if (e == id[k]) sel[e] += dy[k];
   }
 #pragma unroll
-  for (int e = 0; e < EMAX; e++)
+  for (int e = 0; e < EM; e++)
     if (e < E) dx[e] = ex[e] / den * (sel[e] - total);
 }
 
@@ -888,6 +889,7 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd(const float* __restrict__
 // k_moe_gather_bwd with 8 consecutive columns per lane per step (16-byte
 // loads and stores; d % 8 == 0, E % 8 == 0, row strides multiples of 4):
 // every column's arithmetic is the same as above, in the same order.
+template <int EM>  // the expert arrays' bound (E <= EM): 8 keeps the registers of an 8-expert layer small
 __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict__ dxp, long lddx, long d,
                                                         const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
                                                         const float* __restrict__ weights,
@@ -900,25 +902,25 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict_
   const int lane = threadIdx.x & 63;
   const long t = blockIdx.x * 4L + (threadIdx.x >> 6);
   if (t >= R) return;
-  float dl[EMAX];
+  float dl[EM];
 #pragma unroll
-  for (int e = 0; e < EMAX; e++) dl[e] = 0.f;
+  for (int e = 0; e < EM; e++) dl[e] = 0.f;
   if (logits) {
-    float lg[EMAX], w[KMAX], g[KMAX];
+    float lg[EM], w[KMAX], g[KMAX];
     int32_t id[KMAX];
 #pragma unroll
-    for (int e = 0; e < EMAX; e++) lg[e] = e < E ? bf2f(logits[t * E + e]) : 0.f;
+    for (int e = 0; e < EM; e++) lg[e] = e < E ? bf2f(logits[t * E + e]) : 0.f;
 #pragma unroll
     for (int k = 0; k < KMAX; k++) {
       id[k] = k < K ? ids[t * K + k] : -1;
       w[k] = k < K ? weights[t * K + k] : 0.f;
       g[k] = k < K ? dweights[t * K + k] : 0.f;
     }
-    route_bwd_row(lg, E, K, id, w, g, dl);
+    route_bwd_row<EM>(lg, E, K, id, w, g, dl);
     if (lane < E) {
       float v = 0.f;
 #pragma unroll
-      for (int e = 0; e < EMAX; e++)
+      for (int e = 0; e < EM; e++)
         if (e == lane) v = dl[e];
       dlogits[t * E + lane] = v;
     }
@@ -949,7 +951,7 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict_
         const bf16_t* wrow = wr + (c8 + i) * E;
         float r = 0.f;
 #pragma unroll
-        for (int e8 = 0; e8 < EMAX; e8 += 8) {
+        for (int e8 = 0; e8 < EM; e8 += 8) {
           if (e8 >= E) break;
           const u32x4 wv = *(const u32x4*)(wrow + e8);
 #pragma unroll
@@ -1161,7 +1163,8 @@ extern "C" int sj_moe_gather_bwd(void* stream, const float* dxp, long lddx, long
   const bool vec = d % 8 == 0 && experts % 8 == 0 && lddx % 4 == 0 && lddz % 4 == 0 && (!dz_acc || ldacc % 4 == 0) &&
                    ((uintptr_t)dxp & 15) == 0 && ((uintptr_t)dz & 15) == 0 && ((uintptr_t)dz_acc & 15) == 0 &&
                    ((uintptr_t)w_router & 15) == 0;
-  hipLaunchKernelGGL(vec ? k_moe_gather_bwd8 : k_moe_gather_bwd, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
+  auto kern = vec ? (experts <= 8 ? k_moe_gather_bwd8<8> : k_moe_gather_bwd8<EMAX>) : k_moe_gather_bwd;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
                      (hipStream_t)stream, dxp, lddx, d, ids, ppos, weights, (const bf16_t*)logits, dweights,
                      (const bf16_t*)w_router, rows, (int)top_k, (int)experts, dz_acc, ldacc, dz, lddz, dlogits);
   SJ_LAUNCH_CHECK("gather_backward");
