@@ -37,17 +37,18 @@ long pack_capacity(long S, long E) { return (S + (SEG - 1) * E + SEG - 1) / SEG 
 // top-k of E scores (registers, unrolled over EMAX): softmax over all E,
 // K rounds of argmax with the lowest index on ties, weight = full-softmax
 // probability (hierarchy.py:175-191)
+template <int EM = EMAX>  // the score arrays' bound (E <= EM)
 __device__ __forceinline__ void topk_rows(const float* sc_in, int E, int K, int32_t* ids, float* wout) {
-  float sc[EMAX];
+  float sc[EM];
   float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < EMAX; e++) {
+  for (int e = 0; e < EM; e++) {
     sc[e] = e < E ? sc_in[e] : -INFINITY;
     mx = fmaxf(mx, sc[e]);
   }
   float den = 0.f;
 #pragma unroll
-  for (int e = 0; e < EMAX; e++)
+  for (int e = 0; e < EM; e++)
     if (e < E) den += expf(sc[e] - mx);
 #pragma unroll
   for (int k = 0; k < KMAX; k++) {
@@ -55,7 +56,7 @@ __device__ __forceinline__ void topk_rows(const float* sc_in, int E, int K, int3
     float best = -INFINITY;
     int idx = E;
 #pragma unroll
-    for (int e = 0; e < EMAX; e++)
+    for (int e = 0; e < EM; e++)
       if (e < E && (sc[e] > best || (idx == E && sc[e] == best))) {
         best = sc[e];
         idx = e;
@@ -63,7 +64,7 @@ __device__ __forceinline__ void topk_rows(const float* sc_in, int E, int K, int3
     ids[k] = idx;
     wout[k] = expf(best - mx) / den;
 #pragma unroll
-    for (int e = 0; e < EMAX; e++)
+    for (int e = 0; e < EM; e++)
       if (e == idx) sc[e] = -INFINITY;
   }
 }
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(NT) void k_router_topk_lanes(const bf16_t* __restri
                                              pack2(f2bf(sc[e8 + 4]), f2bf(sc[e8 + 5])), pack2(f2bf(sc[e8 + 6]), f2bf(sc[e8 + 7]))};
   int32_t id[KMAX];
   float w[KMAX];
-  topk_rows(sc, E, K, id, w);
+  topk_rows<EE>(sc, E, K, id, w);
 #pragma unroll
   for (int k = 0; k < KMAX; k++)
     if (k < K) {
