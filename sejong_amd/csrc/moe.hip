@@ -635,11 +635,12 @@ __global__ __launch_bounds__(NT) void k_moe_gather16(const bf16_t* __restrict__ 
 
 // a token's K (expert, packed position, weight) in ascending expert order
 // (unrolled compare-exchange over KMAX entries; unused entries sort last)
+template <int KM = KMAX>  // the route arrays' bound (K <= KM)
 __device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, const int32_t* ppos, const float* w,
                                             int* pos, float* wk) {
-  int e[KMAX], n = 0;
+  int e[KM], n = 0;
 #pragma unroll
-  for (int k = 0; k < KMAX; k++) {
+  for (int k = 0; k < KM; k++) {
     const int pk = k < K ? ppos[t * K + k] : -1;
     e[k] = pk >= 0 ? ids[t * K + k] : 0x7fffffff;
     pos[k] = pk;
@@ -647,9 +648,9 @@ __device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, c
     n += pk >= 0;
   }
 #pragma unroll
-  for (int i = 0; i < KMAX; i++)
+  for (int i = 0; i < KM; i++)
 #pragma unroll
-    for (int j = 0; j + 1 < KMAX - i; j++)
+    for (int j = 0; j + 1 < KM - i; j++)
       if (e[j] > e[j + 1]) {
         const int te = e[j], tp = pos[j];
         const float tw = wk[j];
@@ -663,7 +664,7 @@ __device__ __forceinline__ int token_routes(long t, int K, const int32_t* ids, c
 // Block::apply (architecture.rs:245): u = bf16(sum_e w*y_e) with each
 // product rounded before its add (the reference's atomic_add of weight*value,
 // launches in expert order), out = bf16(residual + u).  One wave per token.
-template <bool V8>
+template <bool V8, int KM = KMAX>
 __global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ yp, long ldy, long d,
                                                     const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
                                                     const float* __restrict__ weights, long R, int K,
@@ -672,16 +673,16 @@ __global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ y
   const int lane = threadIdx.x & 63;
   const long t = blockIdx.x * 4L + (threadIdx.x >> 6);
   if (t >= R) return;
-  int pos[KMAX];
-  float wk[KMAX];
-  const int n = token_routes(t, K, ids, ppos, weights, pos, wk);
+  int pos[KM];
+  float wk[KM];
+  const int n = token_routes<KM>(t, K, ids, ppos, weights, pos, wk);
   if constexpr (V8) {  // 8 columns per lane, 16-byte accesses; the same arithmetic per column
     for (long c = 8 * lane; c < d; c += 512) {
       float a[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) a[i] = 0.f;
 #pragma unroll
-      for (int j = 0; j < KMAX; j++) {
+      for (int j = 0; j < KM; j++) {
         if (j >= n) break;
         const u32x4 v = *(const u32x4*)(yp + pos[j] * ldy + c);
         const uint32_t vv[4] = {v[0], v[1], v[2], v[3]};
@@ -710,7 +711,7 @@ __global__ __launch_bounds__(NT) void k_moe_combine(const bf16_t* __restrict__ y
   for (long c = 2 * lane; c < d; c += 128) {
     float a = 0.f, b = 0.f;
 #pragma unroll
-    for (int j = 0; j < KMAX; j++) {
+    for (int j = 0; j < KM; j++) {
       if (j >= n) break;
       const uint32_t v = *(const uint32_t*)(yp + pos[j] * ldy + c);
       a = a + mul_rn(wk[j], bf2f((bf16_t)(v & 0xffffu)));
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd(const float* __restrict__
 // k_moe_gather_bwd with 8 consecutive columns per lane per step (16-byte
 // loads and stores; d % 8 == 0, E % 8 == 0, row strides multiples of 4):
 // every column's arithmetic is the same as above, in the same order.
-template <int EM>  // the expert arrays' bound (E <= EM): 8 keeps the registers of an 8-expert layer small
+template <int EM, int KM = KMAX>  // the expert and route arrays' bounds (E <= EM, K <= KM)
 __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict__ dxp, long lddx, long d,
                                                         const int32_t* __restrict__ ids, const int32_t* __restrict__ ppos,
                                                         const float* __restrict__ weights,
@@ -926,9 +927,9 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict_
       dlogits[t * E + lane] = v;
     }
   }
-  int pos[KMAX];
-  float unused[KMAX];
-  const int n = token_routes(t, K, ids, ppos, nullptr, pos, unused);
+  int pos[KM];
+  float unused[KM];
+  const int n = token_routes<KM>(t, K, ids, ppos, nullptr, pos, unused);
   for (long c8 = 8L * lane; c8 < d; c8 += 512) {
     float s[8], ex[8];
 #pragma unroll
@@ -938,7 +939,7 @@ __global__ __launch_bounds__(NT) void k_moe_gather_bwd8(const float* __restrict_
       s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
     }
 #pragma unroll
-    for (int j = 0; j < KMAX; j++)
+    for (int j = 0; j < KM; j++)
       if (j < n) {
         const float4 x0 = *(const float4*)(dxp + pos[j] * lddx + c8), x1 = *(const float4*)(dxp + pos[j] * lddx + c8 + 4);
         ex[0] += x0.x; ex[1] += x0.y; ex[2] += x0.z; ex[3] += x0.w;
@@ -1121,7 +1122,7 @@ extern "C" int sj_moe_combine(void* stream, const uint16_t* yp, long ldy, long d
   if (rows == 0) return SJ_OK;
   const bool v8 = d % 8 == 0 && ldy % 8 == 0 && ldo % 8 == 0 && (!residual || (ldr % 8 == 0 && ((uintptr_t)residual & 15) == 0)) &&
                   ((uintptr_t)yp & 15) == 0 && ((uintptr_t)out & 15) == 0;
-  auto kern = v8 ? k_moe_combine<true> : k_moe_combine<false>;
+  auto kern = v8 ? (top_k <= 2 ? k_moe_combine<true, 2> : k_moe_combine<true>) : k_moe_combine<false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0, (hipStream_t)stream, (const bf16_t*)yp, ldy, d, ids, ppos, weights, rows, (int)top_k,
                      (const bf16_t*)residual, ldr, (bf16_t*)out, ldo);
   SJ_LAUNCH_CHECK("hierarchy_expert_combine");
@@ -1164,7 +1165,9 @@ extern "C" int sj_moe_gather_bwd(void* stream, const float* dxp, long lddx, long
   const bool vec = d % 8 == 0 && experts % 8 == 0 && lddx % 4 == 0 && lddz % 4 == 0 && (!dz_acc || ldacc % 4 == 0) &&
                    ((uintptr_t)dxp & 15) == 0 && ((uintptr_t)dz & 15) == 0 && ((uintptr_t)dz_acc & 15) == 0 &&
                    ((uintptr_t)w_router & 15) == 0;
-  auto kern = vec ? (experts <= 8 ? k_moe_gather_bwd8<8> : k_moe_gather_bwd8<EMAX>) : k_moe_gather_bwd;
+  auto kern = vec ? (experts <= 8 ? (top_k <= 2 ? k_moe_gather_bwd8<8, 2> : k_moe_gather_bwd8<8>)
+                                   : k_moe_gather_bwd8<EMAX>)
+                   : k_moe_gather_bwd;
   hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(NT), 0,
                      (hipStream_t)stream, dxp, lddx, d, ids, ppos, weights, (const bf16_t*)logits, dweights,
                      (const bf16_t*)w_router, rows, (int)top_k, (int)experts, dz_acc, ldacc, dz, lddz, dlogits);
