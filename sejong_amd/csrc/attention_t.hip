@@ -733,6 +733,37 @@ __device__ __forceinline__ void attn2_dkv(const TArgs& a, bf16_t* lds, int kb, i
   const int kvh = h / group, gi = h % group;
   const long krow = (long)b * T + kb * QB + wave * 16 + j;
   // lane holds dK^T / dV^T [16d + 4g + r][key]: 4 consecutive columns of the partial row
+  if (group == 1 && !a.gqt[0]) {
+    // one query head per KV head, row planes only: the head's share is the
+    // whole gradient, so it goes straight to the dK | dV planes (dK rotated
+    // back by the inverse RoPE, as the group reduce does) and no partials
+    // or reduce pass follow
+    const int pos = kb * QB + wave * 16 + j, NQ = a.HQ * DH;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        float v[4] = {hf ? dv[d][0] : dk[d][0], hf ? dv[d][1] : dk[d][1], hf ? dv[d][2] : dk[d][2],
+                      hf ? dv[d][3] : dk[d][3]};
+        if (hf == 0 && a.rope) {
+#pragma unroll
+          for (int pr = 0; pr < 2; pr++) {
+            const float2 c = *(const float2*)(a.rope + 2 * ((long)pos * (DH / 2) + ((16 * d + 4 * g + 2 * pr) >> 1)));
+            const float x = v[2 * pr], y = v[2 * pr + 1];
+            v[2 * pr] = x * c.x + y * c.y;
+            v[2 * pr + 1] = y * c.x - x * c.y;
+          }
+        }
+        bf16_t hv[4], lv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) split_bf(v[r], hv[r], lv[r]);
+        const long col = NQ + hf * NK + kvh * DH + 16 * d + 4 * g;
+        *(u32x2*)(a.gq[0] + krow * a.ldg + col) = u32x2{pack2(hv[0], hv[1]), pack2(hv[2], hv[3])};
+        *(u32x2*)(a.gq[1] + krow * a.ldg + col) = u32x2{pack2(lv[0], lv[1]), pack2(lv[2], lv[3])};
+      }
+    }
+    return;
+  }
   const long M = (long)T * a.B;
   float* prow_ = a.part + ((long)gi * M + krow) * 2 * NK + kvh * DH;
 #pragma unroll
@@ -1399,7 +1430,7 @@ int sjh::attention_bwd_tt_parts(int parts, void* stream, const uint16_t* qkv, lo
     }
     SJ_LAUNCH_CHECK("hierarchy_attention_dq_dkv");
   }
-  if (parts & 4) {
+  if ((parts & 4) && !(hq == hk && !g_t_hi)) {  // one head per KV head: the dK | dV kernel wrote the planes
     const long M = batch * t;
     if (int st = sjh::attention_kv_reduce(s, a.part, hq / hk, M, t, hq * DH, hk * DH, rope_table, g_hi, g_lo, ldg,
                                           g_t_hi, g_t_lo, ldgt))
